@@ -1,0 +1,54 @@
+// Shared helpers for the gfx950 kernels of the QLoRA training step.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#define QLORA_API extern "C" __attribute__((visibility("default")))
+
+// Error convention of every entry point: 0 on success, a hipError_t otherwise. Arguments that a
+// kernel cannot take are rejected before anything is launched.
+#define QLORA_CHECK_ARG(cond)                          \
+  do {                                                 \
+    if (!(cond)) return (int)hipErrorInvalidValue;     \
+  } while (0)
+
+static inline int qlora_launch_status() { return (int)hipGetLastError(); }
+
+static inline int64_t qlora_cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+namespace qlora {
+
+constexpr int kWave = 64;
+
+// ---- fp16 <-> fp32 (round to nearest even, as the reference's `.to(tl.float16)`) -------------
+__device__ __forceinline__ float h2f(__half h) { return __half2float(h); }
+__device__ __forceinline__ __half f2h(float f) { return __float2half_rn(f); }
+
+__device__ __forceinline__ float h2f_bits(uint16_t b) {
+  return __half2float(__ushort_as_half(b));
+}
+__device__ __forceinline__ uint16_t f2h_bits(float f) {
+  return __half_as_ushort(__float2half_rn(f));
+}
+// two fp32 -> packed pair of fp16 bits (low half = a)
+__device__ __forceinline__ uint32_t pack2h(float a, float b) {
+  return (uint32_t)f2h_bits(a) | ((uint32_t)f2h_bits(b) << 16);
+}
+__device__ __forceinline__ float lo_h(uint32_t w) { return h2f_bits((uint16_t)(w & 0xFFFFu)); }
+__device__ __forceinline__ float hi_h(uint32_t w) { return h2f_bits((uint16_t)(w >> 16)); }
+
+// ---- wavefront reductions (64 lanes) ----------------------------------------------------------
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+  return v;
+}
+
+}  // namespace qlora

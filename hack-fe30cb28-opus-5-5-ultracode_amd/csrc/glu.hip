@@ -1,0 +1,118 @@
+// SwiGLU over the fused [gate | up] projection output, and its backward written in place.
+// Reference: glu_fwd_kernel kernels.py:312-321 (_glu_fwd engine.py:1012-1017) and
+// glu_bwd_kernel kernels.py:324-336 (_glu_bwd engine.py:1020-1023).
+//   m  = fp16( g * sigmoid(g) * u )                               g, u = gu[:, :I], gu[:, I:]
+//   gu <- [ fp16(dm * u * s * (1 + g (1 - s))) | fp16(dm * g * s) ]   s = sigmoid(g)
+// HBM-bound elementwise: 8 columns per thread (16-byte loads and stores) when I % 8 == 0.
+#include "common.h"
+
+namespace qlora {
+
+template <int W>
+struct VecH;
+template <>
+struct VecH<8> {
+  using T = uint4;
+  static __device__ __forceinline__ void unpack(const T w, float (&v)[8]) {
+    v[0] = lo_h(w.x); v[1] = hi_h(w.x); v[2] = lo_h(w.y); v[3] = hi_h(w.y);
+    v[4] = lo_h(w.z); v[5] = hi_h(w.z); v[6] = lo_h(w.w); v[7] = hi_h(w.w);
+  }
+  static __device__ __forceinline__ T pack(const float (&v)[8]) {
+    return make_uint4(pack2h(v[0], v[1]), pack2h(v[2], v[3]), pack2h(v[4], v[5]),
+                      pack2h(v[6], v[7]));
+  }
+};
+template <>
+struct VecH<1> {
+  using T = uint16_t;
+  static __device__ __forceinline__ void unpack(const T w, float (&v)[1]) { v[0] = h2f_bits(w); }
+  static __device__ __forceinline__ T pack(const float (&v)[1]) { return f2h_bits(v[0]); }
+};
+
+__device__ __forceinline__ float sigmoidf(float g) { return 1.0f / (1.0f + expf(-g)); }
+
+template <int W>
+__global__ __launch_bounds__(256) void glu_fwd_kernel(const uint16_t* gu, uint16_t* m,
+                                                      int64_t n, int64_t I) {
+  using V = VecH<W>;
+  using T = typename V::T;
+  const int64_t per_row = I / W;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= n * per_row) return;
+  const int64_t row = gid / per_row;
+  const int64_t col = (gid - row * per_row) * W;
+  const uint16_t* src = gu + row * 2 * I + col;
+  float g[W], u[W], o[W];
+  V::unpack(*reinterpret_cast<const T*>(src), g);
+  V::unpack(*reinterpret_cast<const T*>(src + I), u);
+#pragma unroll
+  for (int i = 0; i < W; ++i) o[i] = g[i] / (1.0f + expf(-g[i])) * u[i];
+  *reinterpret_cast<T*>(m + row * I + col) = V::pack(o);
+}
+
+template <int W>
+__global__ __launch_bounds__(256) void glu_bwd_kernel(const uint16_t* dm, uint16_t* gu,
+                                                      int64_t n, int64_t I) {
+  using V = VecH<W>;
+  using T = typename V::T;
+  const int64_t per_row = I / W;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= n * per_row) return;
+  const int64_t row = gid / per_row;
+  const int64_t col = (gid - row * per_row) * W;
+  uint16_t* src = gu + row * 2 * I + col;
+  float g[W], u[W], d[W], og[W], ou[W];
+  V::unpack(*reinterpret_cast<const T*>(src), g);
+  V::unpack(*reinterpret_cast<const T*>(src + I), u);
+  V::unpack(*reinterpret_cast<const T*>(dm + row * I + col), d);
+#pragma unroll
+  for (int i = 0; i < W; ++i) {
+    const float s = sigmoidf(g[i]);
+    og[i] = d[i] * u[i] * s * (1.0f + g[i] * (1.0f - s));
+    ou[i] = d[i] * g[i] * s;
+  }
+  *reinterpret_cast<T*>(src) = V::pack(og);
+  *reinterpret_cast<T*>(src + I) = V::pack(ou);
+}
+
+}  // namespace qlora
+
+using namespace qlora;
+
+namespace {
+bool al(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+}
+
+QLORA_API int qlora_glu_fwd(const void* gu, void* m, int64_t n, int64_t I, void* stream) {
+  QLORA_CHECK_ARG(n >= 0 && I > 0);
+  if (n == 0) return 0;
+  QLORA_CHECK_ARG(gu && m);
+  const bool v8 = I % 8 == 0 && al(gu, 16) && al(m, 16);
+  const int W = v8 ? 8 : 1;
+  const int64_t total = n * (I / W);
+  const dim3 grid((unsigned)qlora_cdiv(total, 256));
+  if (v8)
+    hipLaunchKernelGGL(glu_fwd_kernel<8>, grid, dim3(256), 0, (hipStream_t)stream,
+                       static_cast<const uint16_t*>(gu), static_cast<uint16_t*>(m), n, I);
+  else
+    hipLaunchKernelGGL(glu_fwd_kernel<1>, grid, dim3(256), 0, (hipStream_t)stream,
+                       static_cast<const uint16_t*>(gu), static_cast<uint16_t*>(m), n, I);
+  return qlora_launch_status();
+}
+
+QLORA_API int qlora_glu_bwd(const void* dm, void* gu, int64_t n, int64_t I, void* stream) {
+  QLORA_CHECK_ARG(n >= 0 && I > 0);
+  if (n == 0) return 0;
+  QLORA_CHECK_ARG(gu && dm);
+  const bool v8 = I % 8 == 0 && al(gu, 16) && al(dm, 16);
+  const int W = v8 ? 8 : 1;
+  const int64_t total = n * (I / W);
+  const dim3 grid((unsigned)qlora_cdiv(total, 256));
+  if (v8)
+    hipLaunchKernelGGL(glu_bwd_kernel<8>, grid, dim3(256), 0, (hipStream_t)stream,
+                       static_cast<const uint16_t*>(dm), static_cast<uint16_t*>(gu), n, I);
+  else
+    hipLaunchKernelGGL(glu_bwd_kernel<1>, grid, dim3(256), 0, (hipStream_t)stream,
+                       static_cast<const uint16_t*>(dm), static_cast<uint16_t*>(gu), n, I);
+  return qlora_launch_status();
+}

@@ -1,0 +1,60 @@
+// NF4 (bitsandbytes 4-bit NormalFloat) decode shared by the standalone dequant kernel and the
+// fused dequant-GEMM B-operand loaders (reference: kernels.py:34-105, engine.py:74-157).
+//
+// Element i of a row-major [N, K] weight is nibble (i & 1 ? low : high) of byte i / 2. Its scale
+// is that of block b = i / BS1:
+//   nested:  fp32(fp32(code2[absmax_q[b]] * absmax2[b / BS2]) + offset[segment(b)])
+//   plain:   absmax_f32[b]
+// and its value fp16_rne(fp32(level[code] * scale)). The multiply and the add are separate IEEE
+// operations (never fused): bitsandbytes rounds the product before adding the offset.
+#pragma once
+
+#include "common.h"
+
+namespace qlora {
+
+struct NF4Ref {
+  const uint8_t* packed;    // numel / 2 bytes
+  const void* absmax;       // uint8 [blocks] (nested) or fp32 [blocks]
+  const float* code2;       // fp32 [256] (nested)
+  const float* absmax2;     // fp32 [ceil(blocks / bs2)] (nested)
+  const float* offsets;     // fp32 [segments] (nested)
+  const float* code;        // fp32 [16] levels (used when !standard)
+  int64_t seg1, seg2;       // first block of the 2nd / 3rd stacked weight
+  int bs1, bs2;
+  int nested, standard;
+};
+
+// The 16 NF4 levels (QLoRA's NormalFloat4 code; kernels.py:38-41), fp32.
+__device__ __constant__ static const float kNF4Levels[16] = {
+    -1.0f, -0.6961928009986877f, -0.5250730514526367f, -0.39491748809814453f,
+    -0.28444138169288635f, -0.18477343022823334f, -0.09105003625154495f, 0.0f,
+    0.07958029955625534f, 0.16093020141124725f, 0.24611230194568634f, 0.33791524171829224f,
+    0.44070982933044434f, 0.5626170039176941f, 0.7229568362236023f, 1.0f};
+
+// fp32 scale of quantization block b (no FMA contraction: explicit IEEE mul, then add).
+__device__ __forceinline__ float nf4_block_scale(const NF4Ref& w, int64_t b) {
+  if (w.nested) {
+    const uint8_t q = static_cast<const uint8_t*>(w.absmax)[b];
+    const float prod = __fmul_rn(w.code2[q], w.absmax2[b / w.bs2]);
+    const int seg = (int)(b >= w.seg1) + (int)(b >= w.seg2);
+    return __fadd_rn(prod, w.offsets[seg]);
+  }
+  return static_cast<const float*>(w.absmax)[b];
+}
+
+// Eight fp16 values (as four packed fp16 pairs) from one 32-bit word of packed nibbles (bytes
+// in memory order: element 2k is the high nibble of byte k). `lut` holds the 16 levels.
+__device__ __forceinline__ uint4 nf4_decode_word(uint32_t word, float scale, const float* lut) {
+  uint32_t out[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t byte = (word >> (8 * k)) & 0xFFu;
+    const float a = __fmul_rn(lut[byte >> 4], scale);
+    const float b = __fmul_rn(lut[byte & 15u], scale);
+    out[k] = pack2h(a, b);
+  }
+  return make_uint4(out[0], out[1], out[2], out[3]);
+}
+
+}  // namespace qlora

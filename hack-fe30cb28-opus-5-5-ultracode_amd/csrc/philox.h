@@ -1,0 +1,78 @@
+// LoRA-dropout keep masks: the mask PyTorch-ROCm's vectorized dropout kernel draws, computed
+// from the generator's (seed, offset) instead of stored (reference: kernels.py:108-126,
+// engine.py:767-805).
+//
+// Element e of a dropout call over a contiguous tensor is handled by thread (e / VEC) mod G of
+// the G-thread launch; that thread's j-th uniform4 draw, j = ((e / VEC) div G) * VEC/4 +
+// (e mod VEC) / 4, is Philox4x32-10 (Random123) with key = seed and counter
+// (ctr + j, thread) -- the layout rocrand_init(seed, subsequence = thread, offset = 4 ctr) gives
+// -- and the element takes output word e mod 4, mapped to (0, 1] as 2^-32 + r * 2^-32 in fp32.
+// Kept iff that value < 1 - p.
+#pragma once
+
+#include "common.h"
+
+namespace qlora {
+
+struct DropParams {
+  uint64_t seed;    // generator seed (int64 bits as uint64)
+  uint64_t ctr;     // generator offset / 4
+  uint64_t G;       // threads of the dropout launch
+  float p_keep;     // 1 - p
+  int vec;          // elements per vector load (4 or 8)
+};
+
+__device__ __forceinline__ uint4 philox4x32_10(uint4 c, uint32_t k0, uint32_t k1) {
+  constexpr uint32_t M0 = 0xD2511F53u, M1 = 0xCD9E8D57u;
+  constexpr uint32_t W0 = 0x9E3779B9u, W1 = 0xBB67AE85u;
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    const uint32_t hi0 = __umulhi(M0, c.x), lo0 = M0 * c.x;
+    const uint32_t hi1 = __umulhi(M1, c.z), lo1 = M1 * c.z;
+    c = make_uint4(hi1 ^ c.y ^ k0, lo1, hi0 ^ c.w ^ k1, lo0);
+    k0 += W0;
+    k1 += W1;
+  }
+  return c;
+}
+
+__device__ __forceinline__ bool keep_word(uint32_t r, float p_keep) {
+  const float inv = 2.3283064365386963e-10f;  // 2^-32, exact
+  const float u = inv + (float)r * inv;       // exact product: FMA or not, same value
+  return u < p_keep;
+}
+
+// The Philox words of the aligned group of four elements that holds element e (4 | e0).
+__device__ __forceinline__ uint4 drop_words(const DropParams& d, uint64_t e0) {
+  uint64_t g = e0 / (uint64_t)d.vec;
+  uint64_t thread, it;
+  if ((g >> 32) == 0 && (d.G >> 32) == 0) {
+    const uint32_t g32 = (uint32_t)g, G32 = (uint32_t)d.G;
+    it = g32 / G32;
+    thread = g32 - (uint32_t)it * G32;
+  } else {
+    it = g / d.G;
+    thread = g - it * d.G;
+  }
+  const uint64_t j = it * (uint64_t)(d.vec >> 2) + (e0 % (uint64_t)d.vec) / 4;
+  const uint64_t c = d.ctr + j;
+  return philox4x32_10(make_uint4((uint32_t)c, (uint32_t)(c >> 32), (uint32_t)thread,
+                                  (uint32_t)(thread >> 32)),
+                       (uint32_t)d.seed, (uint32_t)(d.seed >> 32));
+}
+
+__device__ __forceinline__ bool drop_keep(const DropParams& d, uint64_t e) {
+  const uint4 w = drop_words(d, e & ~(uint64_t)3);
+  const uint32_t comp = (uint32_t)(e & 3);
+  const uint32_t r = comp == 0 ? w.x : comp == 1 ? w.y : comp == 2 ? w.z : w.w;
+  return keep_word(r, d.p_keep);
+}
+
+// Keep bits (bit i = element e0 + i) of four consecutive elements starting at e0, 4 | e0.
+__device__ __forceinline__ uint32_t drop_keep4(const DropParams& d, uint64_t e0) {
+  const uint4 w = drop_words(d, e0);
+  return (uint32_t)keep_word(w.x, d.p_keep) | ((uint32_t)keep_word(w.y, d.p_keep) << 1) |
+         ((uint32_t)keep_word(w.z, d.p_keep) << 2) | ((uint32_t)keep_word(w.w, d.p_keep) << 3);
+}
+
+}  // namespace qlora

@@ -1,0 +1,525 @@
+"""The kernel-call layer: the reference engine's op wrappers, same names, signatures and argument
+meaning (solution/engine.py:683-1045), each launching one gfx950 kernel of libqlora_amd.so on
+torch's current HIP stream.
+
+Ownership as in the reference: wrappers allocate their outputs with torch.empty on the input's
+device; `_glu_bwd` overwrites `gu`, `_ce` the logits, `_ce_piece` the logits rows below n_sup and
+its state tensors. Inputs are checked (device, dtype, shape, contiguity) before any launch, and a
+CPU tensor is refused: there is no CPU path.
+"""
+
+import torch
+
+from . import _lib
+
+# launch-shape constants of the reference that are part of the interface (engine.py:42-47)
+CE_BLOCK = 4096  # (the reference's vocabulary block; pieces must start on a multiple of it)
+HEAD_CHUNK = 256
+PIECE = 8192  # vocabulary rows per piece of the chunked head (engine.py:1414)
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device):
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _need(t, name, dtype=None, device=None, contiguous=True):
+    if t is None:
+        raise ValueError(f"{name} is required")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be a GPU tensor (got {t.device}); there is no CPU path")
+    if device is not None and t.device != device:
+        raise ValueError(f"{name} is on {t.device}, expected {device}")
+    if dtype is not None and t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype} (got {t.dtype})")
+    if contiguous and not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    return t
+
+
+def _rows_view(t, name, dtype, rows, cols, device):
+    """A [rows, cols] tensor with unit column stride; returns its row stride."""
+    _need(t, name, dtype, device, contiguous=False)
+    if t.dim() != 2 or t.shape[0] != rows or t.shape[1] != cols or t.stride(1) != 1:
+        raise ValueError(f"{name} must be [{rows}, {cols}] with unit column stride")
+    return t.stride(0)
+
+
+# ---------------------------------------------------------------------------------------------
+# NF4 weights (engine.py:74-157, 683-694)
+# ---------------------------------------------------------------------------------------------
+NF4_LEVELS = (-1.0, -0.6961928009986877, -0.5250730514526367, -0.39491748809814453,
+              -0.28444138169288635, -0.18477343022823334, -0.09105003625154495, 0.0,
+              0.07958029955625534, 0.16093020141124725, 0.24611230194568634,
+              0.33791524171829224, 0.44070982933044434, 0.5626170039176941,
+              0.7229568362236023, 1.0)
+_NO_SEG = 2**63 - 1
+
+
+class NF4Weight:
+    """The packed bytes and quant state of one bitsandbytes-format Linear4bit weight (reads a
+    Params4bit's `.data` and `.quant_state`, engine.py:74-101)."""
+
+    def __init__(self, param):
+        qs = param.quant_state
+        self.param = param
+        self.packed = param.data
+        self.group = None
+        self.shape = tuple(int(s) for s in qs.shape)
+        self.numel = self.shape[0] * self.shape[1]
+        self.code = qs.code.float().contiguous()
+        self.bs1 = int(qs.blocksize)
+        if self.numel % self.bs1:
+            raise ValueError("weight size is not a whole number of quantization blocks")
+        levels = torch.tensor(NF4_LEVELS, dtype=torch.float32, device=self.code.device)
+        self.standard = bool(torch.equal(self.code, levels))
+        self.nested = bool(qs.nested)
+        if self.nested:
+            self.absmax = qs.absmax
+            self.code2 = qs.state2.code.float().contiguous()
+            self.absmax2 = qs.state2.absmax.float().contiguous()
+            self.offset = torch.as_tensor(qs.offset, device=self.code.device,
+                                          dtype=torch.float32).reshape(1)
+            self.bs2 = int(qs.state2.blocksize)
+        else:
+            self.absmax = qs.absmax.float().contiguous()
+            self.code2 = self.absmax2 = self.offset = self.absmax
+            self.bs2 = 1
+
+    @property
+    def blocks(self):
+        return self.numel // self.bs1
+
+    def dequant_into(self, out):
+        _launch_dequant(self.packed, self.absmax, self.code2, self.absmax2, self.offset,
+                        self.code, out, self.blocks, self.nested, self.standard, self.bs1,
+                        self.bs2, _NO_SEG, _NO_SEG, self.numel)
+        return out
+
+
+class NF4Group:
+    """Weights stored back to back and dequantized in one launch (engine.py:112-157): only the
+    double-quantization offset differs per segment; their absmax2 are concatenated, which needs
+    every weight but the last to end on a whole block of absmax2."""
+
+    @classmethod
+    def of(cls, weights):
+        if not 2 <= len(weights) <= 3:
+            return None
+        w0 = weights[0]
+        for w in weights:
+            if (w.shape[1] != w0.shape[1] or w.bs1 != w0.bs1 or w.bs2 != w0.bs2
+                    or w.nested != w0.nested or w.standard != w0.standard
+                    or not torch.equal(w.code, w0.code)
+                    or (w.nested and not torch.equal(w.code2, w0.code2))):
+                return None
+        if any((w.numel // w.bs1) % w.bs2 for w in weights[:-1]):
+            return None
+        return cls(weights)
+
+    def __init__(self, weights):
+        w0 = weights[0]
+        self.weights = weights
+        self.nested, self.standard, self.bs1, self.bs2 = w0.nested, w0.standard, w0.bs1, w0.bs2
+        self.code, self.code2 = w0.code, w0.code2
+        self.numel = sum(w.numel for w in weights)
+        self.blocks = self.numel // self.bs1
+        bounds = []
+        for w in weights[:-1]:
+            bounds.append((bounds[-1] if bounds else 0) + w.numel // self.bs1)
+        self.seg1, self.seg2 = (bounds + [_NO_SEG, _NO_SEG])[:2]
+        # one resident copy of the packed bytes and absmax, back to back (the reference keeps
+        # them in a WeightStream slot; on MI355X everything stays in HBM)
+        self.packed = torch.cat([w.packed.reshape(-1) for w in weights])
+        self.absmax = torch.cat([w.absmax.reshape(-1) for w in weights])
+        if self.nested:
+            self.absmax2 = torch.cat([w.absmax2 for w in weights])
+            self.offsets = torch.cat([w.offset for w in weights])
+        else:
+            self.absmax2 = self.offsets = self.absmax
+        for w in weights:
+            w.group = self
+
+    def dequant_into(self, out):
+        _launch_dequant(self.packed, self.absmax, self.code2, self.absmax2, self.offsets,
+                        self.code, out, self.blocks, self.nested, self.standard, self.bs1,
+                        self.bs2, self.seg1, self.seg2, self.numel)
+        return out
+
+
+def _launch_dequant(packed, absmax, code2, absmax2, offsets, code, out, blocks, nested,
+                    standard, bs1, bs2, seg1, seg2, numel):
+    dev = out.device
+    _need(out, "out", torch.float16, contiguous=True)
+    if out.numel() != numel:
+        raise ValueError(f"out has {out.numel()} elements, the weight {numel}")
+    _need(packed, "packed", torch.uint8, dev, contiguous=False)
+    if packed.numel() * 2 != numel or not packed.is_contiguous():
+        raise ValueError("packed must hold numel / 2 contiguous bytes")
+    _need(absmax, "absmax", torch.uint8 if nested else torch.float32, dev)
+    if absmax.numel() != blocks:
+        raise ValueError("absmax must have one entry per block")
+    if nested:
+        _need(code2, "code2", torch.float32, dev)
+        _need(absmax2, "absmax2", torch.float32, dev)
+        _need(offsets, "offsets", torch.float32, dev)
+        if code2.numel() != 256 or absmax2.numel() < (blocks + bs2 - 1) // bs2:
+            raise ValueError("code2 must have 256 entries and absmax2 one per block of absmax")
+    if not standard:
+        _need(code, "code", torch.float32, dev)
+        if code.numel() != 16:
+            raise ValueError("code must have 16 entries")
+    if blocks == 0:
+        return
+    _lib.call("qlora_nf4_dequant", _ptr(packed), _ptr(absmax),
+              _ptr(code2) if nested else None, _ptr(absmax2) if nested else None,
+              _ptr(offsets) if nested else None, _ptr(code), _ptr(out), blocks, int(nested),
+              int(standard), bs1, bs2, seg1, seg2, _stream(dev))
+
+
+def dequant(weights, device):
+    """Dequantize one or more [n_i, K] weights stacked into one fp16 [sum n_i, K] buffer
+    (engine.py:683-694): one launch when they form an NF4Group."""
+    rows = sum(w.shape[0] for w in weights)
+    out = torch.empty((rows, weights[0].shape[1]), device=device, dtype=torch.float16)
+    group = weights[0].group
+    if group is not None and group.weights == weights:
+        return group.dequant_into(out)
+    start = 0
+    for w in weights:
+        w.dequant_into(out[start:start + w.shape[0]])
+        start += w.shape[0]
+    return out
+
+
+# ---------------------------------------------------------------------------------------------
+# LoRA dropout masks (engine.py:767-828)
+# ---------------------------------------------------------------------------------------------
+class TorchDropout:
+    """The LoRA dropout masks of the base, bit for bit: `draw` takes the default generator's
+    Philox state (seed, offset) for the next nn.Dropout call on nelem elements and advances the
+    generator as PyTorch's dropout launch does (engine.py:767-805); the kernels compute the mask
+    from it."""
+
+    BLOCK, UNROLL = 256, 4
+
+    CHECK_SEED = 20261031
+    CHECK_TOKENS = 64
+
+    def __init__(self, device, dtype):
+        self.device, self.dtype = torch.device(device), dtype
+        self.ok = None
+        props = torch.cuda.get_device_properties(self.device)
+        self.max_blocks = props.multi_processor_count \
+            * (props.max_threads_per_multi_processor // self.BLOCK)
+        idx = self.device.index if self.device.index is not None else torch.cuda.current_device()
+        self.gen = torch.cuda.default_generators[idx]
+        self.vec = 16 // torch.empty((), dtype=dtype).element_size()
+        assert self.vec in (4, 8), dtype
+
+    def draw(self, nelem):
+        """(seed, counter, threads) of a dropout call on nelem elements; advances the generator."""
+        assert nelem % self.vec == 0, nelem
+        blocks = min(self.max_blocks, (nelem + self.BLOCK - 1) // self.BLOCK)
+        increment = ((nelem - 1) // (self.BLOCK * blocks * self.UNROLL) + 1) * self.UNROLL
+        seed, offset = self.gen.initial_seed(), self.gen.get_offset()
+        self.gen.set_offset(offset + increment)
+        if seed >= 2**63:
+            seed -= 2**64
+        return seed, offset // 4, blocks * self.BLOCK
+
+    def check(self, B, T, H, p):
+        """Whether the rms kernel's mask equals PyTorch's dropout kernel on this GPU and build:
+        dropout of ones over [B, T, H] on a private generator (engine.py:807-828)."""
+        gen = torch.Generator(device=self.device)
+        gen.manual_seed(self.CHECK_SEED)
+        ones = torch.ones((B, T, H), device=self.device, dtype=self.dtype)
+        _, ref = torch._fused_dropout(ones, 1.0 - p, gen)
+        nelem = B * T * H
+        blocks = min(self.max_blocks, (nelem + self.BLOCK - 1) // self.BLOCK)
+
+        class _Check:
+            dropout_p, drop_seed, drop_threads, drop_vec = p, self.CHECK_SEED, \
+                blocks * self.BLOCK, self.vec
+            tok = torch.arange(B * T, device=self.device)
+            eps = 1e-6
+
+        x = ones.view(B * T, H).float()
+        _, _, yq, _, _ = _rms_fwd(_Check, x, torch.ones(H, device=self.device), _Check,
+                                  write_y=False, seeds=(0, 0), drop_q=True)
+        return bool(torch.equal((yq != 0).view(B, T, H), ref.bool()))
+
+
+def keep_mask(nelem, seed, ctr, threads, p, vec, device):
+    """Keep mask (bool [nelem]) of one dropout call (the test hook, kernels.py:129-135)."""
+    out = torch.empty(nelem, device=device, dtype=torch.int8)
+    _lib.call("qlora_dropout_keep", _ptr(out), nelem, int(seed), int(ctr), int(threads),
+              1.0 - p, int(vec), _stream(out.device))
+    return out.bool()
+
+
+# ---------------------------------------------------------------------------------------------
+# RMSNorm + LoRA dropout (engine.py:933-981)
+# ---------------------------------------------------------------------------------------------
+_DUMMIES = {}
+
+
+def _dropout_args(packed, x, seeds):
+    """The rms kernels' dropout arguments (engine.py:933-941): the tokens' indices in the padded
+    batch, the keep probability and scale, the generator's seed, the q and v counters, threads."""
+    tok = getattr(packed, "tok", None)
+    p = getattr(packed, "dropout_p", 0.0) or 0.0
+    return (tok, 1.0 - p, 1.0 / (1.0 - p), getattr(packed, "drop_seed", None) or 0, seeds[0],
+            seeds[1], getattr(packed, "drop_threads", None) or 1)
+
+
+def _weight_arg(weight, H, device):
+    _need(weight, "weight", None, device)
+    if weight.dtype not in (torch.float32, torch.float16) or weight.numel() != H:
+        raise ValueError("norm weight must be fp32 or fp16 with H entries")
+    return int(weight.dtype == torch.float16)
+
+
+def _rms_fwd(spec, x, weight, packed, *, delta=None, write_y=True, seeds=(0, 0),
+             drop_q=False, drop_v=False):
+    """[x += delta] + RMSNorm -> (xsum, y fp16, yq, yv, rstd) (engine.py:947-966)."""
+    _need(x, "x", torch.float32)
+    n, H = x.shape
+    dev = x.device
+    w_half = _weight_arg(weight, H, dev)
+    if delta is not None:
+        _need(delta, "delta", torch.float16, dev)
+        if delta.shape != x.shape:
+            raise ValueError("delta must match x")
+    xsum = torch.empty_like(x) if delta is not None else x
+    y = torch.empty((n, H), device=dev, dtype=torch.float16) if write_y else None
+    yq = torch.empty((n, H), device=dev, dtype=torch.float16) if drop_q else None
+    yv = torch.empty((n, H), device=dev, dtype=torch.float16) if drop_v else None
+    rstd = torch.empty((n,), device=dev, dtype=torch.float32)
+    if n:
+        tok, p_keep, keep_scale, seed, ctr_q, ctr_v, threads = _dropout_args(packed, x, seeds)
+        vec = getattr(packed, "drop_vec", 4)
+        if drop_q or drop_v:
+            _need(tok, "packed.tok", torch.int64, dev)
+            if tok.numel() != n:
+                raise ValueError("packed.tok must have one entry per row")
+        _lib.call("qlora_rms_fwd", _ptr(x), _ptr(delta), _ptr(weight), w_half,
+                  _ptr(xsum) if delta is not None else None, _ptr(y), _ptr(yq), _ptr(yv),
+                  _ptr(rstd), _ptr(tok) if (drop_q or drop_v) else None, n, H,
+                  float(spec.eps), p_keep, keep_scale, int(seed), int(ctr_q), int(ctr_v),
+                  int(threads), int(delta is not None), int(write_y), int(drop_q), int(drop_v),
+                  int(vec), _stream(dev))
+    return xsum, y, yq, yv, rstd
+
+
+def _rms_bwd(spec, dy, x, rstd, weight, packed, *, dres=None, tq=None, tv=None, seeds=(0, 0),
+             grad_scale=1.0, out=None):
+    """RMSNorm backward with the LoRA-dropout gradients merged (engine.py:969-981)."""
+    _need(x, "x", torch.float32)
+    n, H = x.shape
+    dev = x.device
+    w_half = _weight_arg(weight, H, dev)
+    dy_stride = _rows_view(dy, "dy", torch.float16, n, H, dev) if n else H
+    _need(rstd, "rstd", torch.float32, dev)
+    for t, name in ((tq, "tq"), (tv, "tv")):
+        if t is not None:
+            _need(t, name, torch.float16, dev)
+            if t.shape != x.shape:
+                raise ValueError(f"{name} must match x")
+    if dres is not None:
+        _need(dres, "dres", torch.float32, dev)
+        if dres.shape != x.shape:
+            raise ValueError("dres must match x")
+    dx = out if out is not None else torch.empty_like(x)
+    _need(dx, "out", torch.float32, dev)
+    if n:
+        tok, p_keep, keep_scale, seed, ctr_q, ctr_v, threads = _dropout_args(packed, x, seeds)
+        vec = getattr(packed, "drop_vec", 4)
+        if tq is not None or tv is not None:
+            _need(tok, "packed.tok", torch.int64, dev)
+        _lib.call("qlora_rms_bwd", _ptr(dy), _ptr(tq), _ptr(tv), _ptr(x), _ptr(rstd),
+                  _ptr(weight), w_half, _ptr(dres), _ptr(dx),
+                  _ptr(tok) if (tq is not None or tv is not None) else None, n, H, dy_stride,
+                  p_keep, keep_scale, int(seed), int(ctr_q), int(ctr_v), int(threads),
+                  float(grad_scale), int(tq is not None), int(tv is not None),
+                  int(dres is not None), int(vec), _stream(dev))
+    return dx
+
+
+# ---------------------------------------------------------------------------------------------
+# qkv + RoPE (engine.py:984-1009)
+# ---------------------------------------------------------------------------------------------
+def _rope_fwd(spec, qkv, lq, lv, packed, lora_scale, kv_heads=None):
+    """(q, k, v) fp16 [n, heads, D] from the fused qkv GEMM output and the LoRA deltas
+    (engine.py:984-997). k and v come out repeated for the GQA groups ([n, HQ, D]) as in the
+    reference, or with kv_heads=spec.HKV in grouped layout."""
+    HQ, HKV, D = spec.HQ, spec.HKV, spec.D
+    C = (HQ + 2 * HKV) * D
+    _need(qkv, "qkv", torch.float16)
+    n = qkv.shape[0]
+    dev = qkv.device
+    if qkv.shape != (n, C):
+        raise ValueError(f"qkv must be [n, {C}]")
+    if lq is not None:
+        _need(lq, "lq", torch.float16, dev)
+        if lq.shape != (n, HQ * D):
+            raise ValueError("lq must be [n, HQ*D]")
+    if lv is not None:
+        _need(lv, "lv", torch.float16, dev)
+        if lv.shape != (n, HKV * D):
+            raise ValueError("lv must be [n, HKV*D]")
+    kh = HQ if kv_heads is None else int(kv_heads)
+    q = torch.empty((n, HQ, D), device=dev, dtype=torch.float16)
+    k = torch.empty((n, kh, D), device=dev, dtype=torch.float16)
+    v = torch.empty((n, kh, D), device=dev, dtype=torch.float16)
+    if n:
+        cos, sin, pos = _rope_tables(packed, D, n, dev)
+        _lib.call("qlora_rope_fwd", _ptr(qkv), _ptr(lq), _ptr(lv), _ptr(cos), _ptr(sin),
+                  cos.shape[0], _ptr(pos), _ptr(q), _ptr(k), _ptr(v), n, HQ, HKV, D, kh,
+                  float(lora_scale), _stream(dev))
+    return q, k, v
+
+
+def _rope_bwd(spec, dq, dk, dv, packed):
+    """[dq | dk | dv] pre-rotary gradient of the fused qkv output (engine.py:1000-1009)."""
+    HQ, HKV, D = spec.HQ, spec.HKV, spec.D
+    n = dq.shape[0]
+    dev = dq.device
+    dq, dk, dv = dq.contiguous(), dk.contiguous(), dv.contiguous()
+    _need(dq, "dq", torch.float16)
+    kh = dk.shape[1]
+    for t, name in ((dk, "dk"), (dv, "dv")):
+        _need(t, name, torch.float16, dev)
+        if t.shape != (n, kh, D):
+            raise ValueError(f"{name} must be [n, heads, D]")
+    if dq.shape != (n, HQ, D):
+        raise ValueError("dq must be [n, HQ, D]")
+    C = (HQ + 2 * HKV) * D
+    dqkv = torch.empty((n, C), device=dev, dtype=torch.float16)
+    if n:
+        cos, sin, pos = _rope_tables(packed, D, n, dev)
+        _lib.call("qlora_rope_bwd", _ptr(dq), _ptr(dk), _ptr(dv), _ptr(cos), _ptr(sin),
+                  cos.shape[0], _ptr(pos), _ptr(dqkv), n, HQ, HKV, D, kh, _stream(dev))
+    return dqkv
+
+
+def _rope_tables(packed, D, n, dev):
+    cos, sin, pos = packed.cos, packed.sin, packed.pos
+    _need(cos, "packed.cos", torch.float32, dev)
+    _need(sin, "packed.sin", torch.float32, dev)
+    _need(pos, "packed.pos", torch.int32, dev)
+    if cos.dim() != 2 or cos.shape[1] != D // 2 or sin.shape != cos.shape or pos.numel() != n:
+        raise ValueError("packed.cos/sin must be [positions, D/2] and packed.pos [n]")
+    return cos, sin, pos
+
+
+# ---------------------------------------------------------------------------------------------
+# SwiGLU (engine.py:1012-1023)
+# ---------------------------------------------------------------------------------------------
+def _glu_fwd(gu, I, out=None):
+    """m = silu(g) * u over the fused [g | u] (engine.py:1012-1017)."""
+    _need(gu, "gu", torch.float16)
+    n = gu.shape[0]
+    if gu.shape != (n, 2 * I):
+        raise ValueError("gu must be [n, 2I]")
+    m = out if out is not None else torch.empty((n, I), device=gu.device, dtype=torch.float16)
+    _need(m, "out", torch.float16, gu.device)
+    if m.shape != (n, I):
+        raise ValueError("out must be [n, I]")
+    if n:
+        _lib.call("qlora_glu_fwd", _ptr(gu), _ptr(m), n, I, _stream(gu.device))
+    return m
+
+
+def _glu_bwd(dm, gu, I):
+    """In place: gu <- [dL/dg | dL/du] (engine.py:1020-1023)."""
+    _need(gu, "gu", torch.float16)
+    n = gu.shape[0]
+    _need(dm, "dm", torch.float16, gu.device)
+    if gu.shape != (n, 2 * I) or dm.shape != (n, I):
+        raise ValueError("gu must be [n, 2I] and dm [n, I]")
+    if n:
+        _lib.call("qlora_glu_bwd", _ptr(dm), _ptr(gu), n, I, _stream(gu.device))
+
+
+# ---------------------------------------------------------------------------------------------
+# Cross-entropy head (engine.py:1026-1045)
+# ---------------------------------------------------------------------------------------------
+def _ce_outputs(rows, dev, tok_loss, entropy, correct, targets):
+    _need(targets, "targets", torch.int64, dev)
+    _need(tok_loss, "tok_loss", torch.float32, dev)
+    _need(entropy, "entropy", torch.float32, dev)
+    _need(correct, "correct", torch.int32, dev)
+    for t, name in ((targets, "targets"), (tok_loss, "tok_loss"), (entropy, "entropy"),
+                    (correct, "correct")):
+        if t.numel() != rows:
+            raise ValueError(f"{name} must have one entry per row")
+
+
+def _ce(logits, targets, tok_loss, entropy, correct, zero_unsupervised=True):
+    """Loss, entropy, accuracy of whole rows; logits overwritten with softmax - onehot
+    (engine.py:1026-1030)."""
+    _need(logits, "logits", torch.float16, contiguous=False)
+    rows, V = logits.shape
+    if rows == 0:
+        return
+    ld = _rows_view(logits, "logits", torch.float16, rows, V, logits.device)
+    _ce_outputs(rows, logits.device, tok_loss, entropy, correct, targets)
+    _lib.call("qlora_ce", _ptr(logits), ld, _ptr(targets), _ptr(tok_loss), _ptr(entropy),
+              _ptr(correct), rows, V, int(zero_unsupervised), _stream(logits.device))
+
+
+def _ce_piece(logits, w, targets, state, best_idx, xt, alpha, wt, v0, n_sup):
+    """One vocabulary piece of the online cross-entropy (engine.py:1033-1038)."""
+    _need(logits, "logits", torch.float16, contiguous=False)
+    rows, width = logits.shape
+    if rows == 0:
+        return
+    dev = logits.device
+    ld = _rows_view(logits, "logits", torch.float16, rows, width, dev)
+    _need(w, "w", torch.float16, dev)
+    H = w.shape[1]
+    if w.shape[0] != width:
+        raise ValueError("w must be [width, H]")
+    _need(targets, "targets", torch.int64, dev)
+    _need(state, "state", torch.float32, dev)
+    _need(best_idx, "best_idx", torch.int32, dev)
+    _need(xt, "xt", torch.float32, dev)
+    if state.shape != (rows, 4) or best_idx.numel() != rows or xt.numel() != rows \
+            or targets.numel() != rows:
+        raise ValueError("state must be [rows, 4]; best_idx, xt, targets [rows]")
+    if n_sup:
+        _need(alpha, "alpha", torch.float32, dev)
+        _need(wt, "wt", torch.float16, dev)
+        if alpha.numel() < n_sup or wt.shape[0] < n_sup or wt.shape[1] != H:
+            raise ValueError("alpha must hold n_sup entries and wt [n_sup, H]")
+    _lib.call("qlora_ce_piece", _ptr(logits), ld, _ptr(w), _ptr(targets), _ptr(state),
+              _ptr(best_idx), _ptr(xt), _ptr(alpha), _ptr(wt), int(v0), rows, width,
+              int(n_sup), H, _stream(dev))
+
+
+def _ce_finish(state, best_idx, xt, targets, tok_loss, entropy, correct, acc, wt, dh, n_sup):
+    """Loss, entropy, accuracy and dh = acc/s - W[target] after the last piece
+    (engine.py:1041-1045)."""
+    _need(state, "state", torch.float32)
+    rows = state.shape[0]
+    if rows == 0:
+        return
+    dev = state.device
+    H = acc.shape[1]
+    _ce_outputs(rows, dev, tok_loss, entropy, correct, targets)
+    _need(best_idx, "best_idx", torch.int32, dev)
+    _need(xt, "xt", torch.float32, dev)
+    if n_sup:
+        _need(acc, "acc", torch.float32, dev)
+        _need(wt, "wt", torch.float16, dev)
+        _need(dh, "dh", torch.float16, dev)
+        if acc.shape[0] < n_sup or wt.shape != acc.shape or dh.shape[1] != H \
+                or dh.shape[0] < n_sup:
+            raise ValueError("acc, wt, dh must be [n_sup, H]")
+    _lib.call("qlora_ce_finish", _ptr(state), _ptr(best_idx), _ptr(xt), _ptr(targets),
+              _ptr(tok_loss), _ptr(entropy), _ptr(correct), _ptr(acc), _ptr(wt), _ptr(dh),
+              rows, int(n_sup), H, _stream(dev))

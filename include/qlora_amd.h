@@ -1,0 +1,157 @@
+/*
+ * C-ABI of the MI355X (gfx950) QLoRA training-step kernels: libqlora_amd.so.
+ *
+ * Every entry point takes raw device pointers, sizes and scalars, launches on the given HIP
+ * stream (hipStream_t passed as void*; NULL = the default stream) and returns 0 on success or a
+ * hipError_t (hipErrorInvalidValue = 1 for arguments a kernel cannot take; checked before any
+ * launch). Nothing is allocated or freed; no global mutable state; callable from any thread.
+ * n == 0 (rows, tokens, blocks) is a no-op that returns 0, as the reference skips such launches.
+ *
+ * Dtypes: "f16" = IEEE half as 16-bit words, "f32" = float, "i64"/"i32" = int64_t/int32_t.
+ * All tensors are contiguous row-major unless a leading dimension is given.
+ *
+ * Each entry point replaces one Triton kernel launch of the reference (Magurin/hack-fe30cb28 -
+ * solution/kernels.py), called through the Python wrappers of solution/engine.py; the citation
+ * is given as kernel (file:line) <- wrapper (file:line).
+ */
+#ifndef QLORA_AMD_H
+#define QLORA_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Library version of this ABI (1). */
+int qlora_abi_version(void);
+/* hipGetErrorString of a returned code. */
+const char* qlora_error_string(int code);
+
+/*
+ * NF4 -> fp16 dequantisation, bit-exact with bitsandbytes' dequantize_4bit.
+ * Replaces nf4_dequant_kernel (kernels.py:68-105) <- NF4Weight.dequant_into
+ * (engine.py:103-109), NF4Group.dequant_into (engine.py:148-157), dequant (engine.py:683-694).
+ *   packed   u8 [n_blocks*bs1/2], element i = high nibble of byte i/2 for even i, low for odd
+ *   absmax   nested: u8 [n_blocks] codes into code2; else f32 [n_blocks]
+ *   code2    f32 [256]; absmax2 f32 [ceil(n_blocks/bs2)]; offsets f32 [1..3] (nested only)
+ *   code     f32 [16] levels, read only when standard == 0 (else the NF4 table)
+ *   out      f16 [n_blocks*bs1]
+ *   seg1/2   first block of the 2nd/3rd weight stacked back to back (INT64_MAX if none): they
+ *            select offsets[1] / offsets[2]
+ * Requires bs1 % 8 == 0, packed 4-byte and out 16-byte aligned.
+ */
+int qlora_nf4_dequant(const void* packed, const void* absmax, const float* code2,
+                      const float* absmax2, const float* offsets, const float* code, void* out,
+                      int64_t n_blocks, int32_t nested, int32_t standard, int32_t bs1,
+                      int32_t bs2, int64_t seg1, int64_t seg2, void* stream);
+
+/*
+ * Keep mask (i8 0/1) of elements 0..nelem of one PyTorch dropout call whose Philox state is
+ * (seed, offset = 4*ctr) over G threads, vec elements per thread load (4 fp32, 8 fp16).
+ * Replaces torch_dropout_keep_kernel (kernels.py:129-135), the test hook of
+ * test_kernels.py:52-60.
+ */
+int qlora_dropout_keep(int8_t* out, int64_t nelem, int64_t seed, int64_t ctr, int64_t G,
+                       float p_keep, int32_t vec, void* stream);
+
+/*
+ * RMSNorm forward over n rows of H: [x += f32(delta); xsum = x], rstd = 1/sqrt(mean(x^2)+eps),
+ * y = w * (x * rstd) -> f16, and the LoRA inputs yq / yv = f16(keep ? y * keep_scale : 0) with
+ * the keep masks of two dropout calls (counters ctr_q, ctr_v) at padded-batch elements
+ * tok[row]*H + col. Replaces rms_fwd_kernel (kernels.py:145-175) <- _rms_fwd
+ * (engine.py:947-966).
+ *   x f32 [n,H]; delta f16 [n,H]; w [H] (f32, or f16 if w_half); xsum f32 [n,H];
+ *   y, yq, yv f16 [n,H]; rstd f32 [n]; tok i64 [n]
+ */
+int qlora_rms_fwd(const float* x, const void* delta, const void* w, int32_t w_half, float* xsum,
+                  void* y, void* yq, void* yv, float* rstd, const int64_t* tok, int64_t n,
+                  int64_t H, float eps, float p_keep, float keep_scale, int64_t seed,
+                  int64_t ctr_q, int64_t ctr_v, int64_t G, int32_t has_delta, int32_t write_y,
+                  int32_t drop_q, int32_t drop_v, int32_t vec, void* stream);
+
+/*
+ * RMSNorm backward: g = w * (dy + keep_q * tq * keep_scale + keep_v * tv * keep_scale),
+ * dx = [dres +] grad_scale * rstd * (g - xhat * mean(g * xhat)), xhat = x * rstd.
+ * Replaces rms_bwd_kernel (kernels.py:178-205) <- _rms_bwd (engine.py:969-981).
+ *   dy f16 [n, dy_stride]; tq, tv f16 [n,H]; x f32 [n,H]; rstd f32 [n]; dres, dx f32 [n,H]
+ */
+int qlora_rms_bwd(const void* dy, const void* tq, const void* tv, const float* x,
+                  const float* rstd, const void* w, int32_t w_half, const float* dres, float* dx,
+                  const int64_t* tok, int64_t n, int64_t H, int64_t dy_stride, float p_keep,
+                  float keep_scale, int64_t seed, int64_t ctr_q, int64_t ctr_v, int64_t G,
+                  float grad_scale, int32_t drop_q, int32_t drop_v, int32_t has_res,
+                  int32_t vec, void* stream);
+
+/*
+ * qkv split + LoRA deltas + rotate-half RoPE. q = f16(rope(qkv_q + s*lq)),
+ * k = f16(rope(qkv_k)), v = f16(qkv_v + s*lv); cos/sin f32 [positions, D/2] at pos[t].
+ * k, v are written with kv_heads_out heads: HKV, or HQ (each kv head repeated HQ/HKV times).
+ * A position outside [0, positions) yields NaN for that token (no out-of-bounds table read).
+ * Replaces qkv_rope_fwd_kernel (kernels.py:212-264) <- _rope_fwd (engine.py:984-997).
+ *   qkv f16 [n,(HQ+2HKV)*D]; lq f16 [n,HQ*D] or NULL; lv f16 [n,HKV*D] or NULL; pos i32 [n]
+ *   q f16 [n,HQ,D]; k, v f16 [n,kv_heads_out,D]. Requires D % 16 == 0, 16-byte alignment.
+ */
+int qlora_rope_fwd(const void* qkv, const void* lq, const void* lv, const float* cos,
+                   const float* sin, int64_t positions, const int32_t* pos, void* q, void* k,
+                   void* v, int64_t n, int32_t HQ, int32_t HKV, int32_t D, int32_t kv_heads_out,
+                   float lora_scale, void* stream);
+
+/*
+ * Inverse: dqkv = [rope^-1(dq) | rope^-1(sum_g dk) | sum_g dv] f16 [n,(HQ+2HKV)*D], where
+ * dk, dv have kv_heads_in heads (HQ: summed over each kv head's replicas in fp32).
+ * Replaces qkv_rope_bwd_kernel (kernels.py:267-306) <- _rope_bwd (engine.py:1000-1009).
+ */
+int qlora_rope_bwd(const void* dq, const void* dk, const void* dv, const float* cos,
+                   const float* sin, int64_t positions, const int32_t* pos, void* dqkv,
+                   int64_t n, int32_t HQ, int32_t HKV, int32_t D, int32_t kv_heads_in,
+                   void* stream);
+
+/*
+ * SwiGLU: m = f16(silu(g) * u), gu = [g | u] f16 [n, 2I], m f16 [n, I].
+ * Replaces glu_fwd_kernel (kernels.py:312-321) <- _glu_fwd (engine.py:1012-1017).
+ */
+int qlora_glu_fwd(const void* gu, void* m, int64_t n, int64_t I, void* stream);
+
+/*
+ * SwiGLU backward in place: gu <- [dm*u*s*(1+g(1-s)) | dm*g*s], s = sigmoid(g).
+ * Replaces glu_bwd_kernel (kernels.py:324-336) <- _glu_bwd (engine.py:1020-1023).
+ */
+int qlora_glu_bwd(const void* dm, void* gu, int64_t n, int64_t I, void* stream);
+
+/*
+ * Cross-entropy over whole rows of f16 logits [rows, V] (leading dimension ld), in place:
+ * loss (f32, 0 if target < 0), entropy (f32), correct (i32, argmax == target, first max wins);
+ * rows with a target get f16(softmax - onehot) written over their logits, the others zeros if
+ * zero_unsupervised. Replaces lm_head_ce_kernel (kernels.py:344-388) <- _ce
+ * (engine.py:1026-1030).
+ */
+int qlora_ce(void* logits, int64_t ld, const int64_t* target, float* loss, float* entropy,
+             int32_t* correct, int64_t rows, int64_t V, int32_t zero_unsupervised,
+             void* stream);
+
+/*
+ * One vocabulary piece [v0, v0+width) of the online cross-entropy: updates state f32 [rows,4]
+ * (max, sum exp, sum exp*x, best), best_idx i32 [rows], xt f32 [rows] (target logit if in the
+ * piece); for rows < n_sup writes alpha f32 [n_sup] = exp(m_old - m_new) and overwrites their
+ * logits with f16(exp(x - m_new)); copies w[target - v0] (f16 [width, H]) into wt f16 [n_sup,H].
+ * Replaces lm_head_piece_kernel (kernels.py:401-450) <- _ce_piece (engine.py:1033-1038).
+ */
+int qlora_ce_piece(void* logits, int64_t ld, const void* w, const int64_t* target, float* state,
+                   int32_t* best_idx, float* xt, float* alpha, void* wt, int64_t v0,
+                   int64_t rows, int64_t width, int64_t n_sup, int64_t H, void* stream);
+
+/*
+ * After the last piece: loss, entropy, correct as qlora_ce; dh f16 [n_sup,H] = acc/s - wt.
+ * Replaces lm_head_finish_kernel (kernels.py:458-479) <- _ce_finish (engine.py:1041-1045).
+ */
+int qlora_ce_finish(const float* state, const int32_t* best_idx, const float* xt,
+                    const int64_t* target, float* loss, float* entropy, int32_t* correct,
+                    const float* acc, const void* wt, void* dh, int64_t rows, int64_t n_sup,
+                    int64_t H, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QLORA_AMD_H */

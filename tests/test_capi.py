@@ -1,0 +1,91 @@
+"""The C-ABI library: loads, exports every entry point include/qlora_amd.h declares, and the
+Python binding covers the same set with the same arity. No device call is made here."""
+
+import os
+import re
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared():
+    decls = {}
+    for name in os.listdir(os.path.join(ROOT, "include")):
+        if not name.endswith(".h"):
+            continue
+        text = open(os.path.join(ROOT, "include", name)).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        for m in re.finditer(r"\b(?:int|const char\*)\s+(qlora_\w+)\s*\(([^;]*?)\)\s*;", text,
+                             flags=re.S):
+            args = m.group(2).strip()
+            decls[m.group(1)] = 0 if args in ("", "void") else args.count(",") + 1
+    return decls
+
+
+def test_header_declares_entry_points():
+    decls = _declared()
+    assert len(decls) >= 13
+    assert "qlora_nf4_dequant" in decls and "qlora_ce_piece" in decls
+
+
+def test_library_exports_every_declared_symbol(pkg):
+    lib = pkg._lib.load()
+    for name in _declared():
+        assert hasattr(lib, name), name
+    assert lib.qlora_abi_version() == 1
+
+
+def test_binding_matches_header(pkg):
+    decls = _declared()
+    sigs = pkg._lib.SIGNATURES
+    for name, nargs in decls.items():
+        if name in ("qlora_error_string", "qlora_abi_version"):
+            continue
+        assert name in sigs, name
+        assert len(sigs[name]) == nargs, (name, len(sigs[name]), nargs)
+    assert set(sigs) <= set(decls)
+
+
+def test_error_string(pkg):
+    lib = pkg._lib.load()
+    assert lib.qlora_error_string(1)  # hipErrorInvalidValue has a message
+
+
+class _Spec:
+    eps = 1e-6
+    HQ, HKV, D = 12, 2, 128
+
+
+def test_ops_refuse_cpu_tensors(pkg):
+    """No CPU path: host tensors are rejected before any launch."""
+    x = torch.zeros(4, 64)
+    w = torch.ones(64)
+    with pytest.raises(ValueError, match="GPU"):
+        pkg.ops._rms_fwd(_Spec, x, w, None)
+    with pytest.raises(ValueError, match="GPU"):
+        pkg.ops._glu_fwd(torch.zeros(2, 16, dtype=torch.float16), 8)
+    with pytest.raises(ValueError, match="GPU"):
+        pkg.ops._ce(torch.zeros(2, 16, dtype=torch.float16), torch.zeros(2, dtype=torch.long),
+                    torch.zeros(2), torch.zeros(2), torch.zeros(2, dtype=torch.int32))
+
+
+def test_zero_rows_is_noop_without_launch(pkg):
+    """n == 0 returns 0 from the C-ABI without touching the device (reference: launches are
+    skipped for empty inputs, engine.py:958, 973, 991)."""
+    lib = pkg._lib.load()
+    assert lib.qlora_glu_fwd(None, None, 0, 8960, None) == 0
+    assert lib.qlora_nf4_dequant(None, None, None, None, None, None, None, 0, 1, 1, 64, 256,
+                                 0, 0, None) == 0
+    assert lib.qlora_ce(None, 16, None, None, None, None, 0, 16, 1, None) == 0
+
+
+def test_invalid_arguments_rejected_before_launch(pkg):
+    lib = pkg._lib.load()
+    # D not a multiple of 16, negative sizes, bad block size: hipErrorInvalidValue (1)
+    assert lib.qlora_rope_fwd(None, None, None, None, None, 512, None, None, None, None, 5, 12,
+                              2, 100, 12, 1.0, None) == 1
+    assert lib.qlora_glu_fwd(None, None, -1, 8, None) == 1
+    assert lib.qlora_nf4_dequant(None, None, None, None, None, None, None, 4, 0, 1, 6, 256,
+                                 0, 0, None) == 1
