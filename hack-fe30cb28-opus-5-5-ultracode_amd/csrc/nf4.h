@@ -21,7 +21,7 @@ struct NF4Ref {
   const float* offsets;     // fp32 [segments] (nested)
   const float* code;        // fp32 [16] levels (used when !standard)
   int64_t seg1, seg2;       // first block of the 2nd / 3rd stacked weight
-  int bs1, bs2;
+  int bs1_shift, bs2_shift;  // log2 of the block sizes (powers of two, as in bitsandbytes)
   int nested, standard;
 };
 
@@ -32,13 +32,19 @@ __device__ __constant__ static const float kNF4Levels[16] = {
     0.07958029955625534f, 0.16093020141124725f, 0.24611230194568634f, 0.33791524171829224f,
     0.44070982933044434f, 0.5626170039176941f, 0.7229568362236023f, 1.0f};
 
-// fp32 scale of quantization block b (no FMA contraction: explicit IEEE mul, then add).
+// Pins an fp32 value in a register: the compiler may otherwise fold a rounded fp32 product into
+// the following add (FMA) or into the fp16 conversion (v_fma_mix*_f16, one rounding instead of
+// two). Emits no instruction.
+__device__ __forceinline__ void fp32_barrier(float& v) { __asm__ volatile("" : "+v"(v)); }
+
+// fp32 scale of quantization block b: the product rounded to fp32, then the add.
 __device__ __forceinline__ float nf4_block_scale(const NF4Ref& w, int64_t b) {
   if (w.nested) {
     const uint8_t q = static_cast<const uint8_t*>(w.absmax)[b];
-    const float prod = __fmul_rn(w.code2[q], w.absmax2[b / w.bs2]);
+    float prod = w.code2[q] * w.absmax2[b >> w.bs2_shift];
+    fp32_barrier(prod);
     const int seg = (int)(b >= w.seg1) + (int)(b >= w.seg2);
-    return __fadd_rn(prod, w.offsets[seg]);
+    return prod + w.offsets[seg];
   }
   return static_cast<const float*>(w.absmax)[b];
 }
@@ -50,8 +56,10 @@ __device__ __forceinline__ uint4 nf4_decode_word(uint32_t word, float scale, con
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const uint32_t byte = (word >> (8 * k)) & 0xFFu;
-    const float a = __fmul_rn(lut[byte >> 4], scale);
-    const float b = __fmul_rn(lut[byte & 15u], scale);
+    float a = lut[byte >> 4] * scale;
+    float b = lut[byte & 15u] * scale;
+    fp32_barrier(a);  // fp16(fp32(level * scale)): two roundings, as the reference
+    fp32_barrier(b);
     out[k] = pack2h(a, b);
   }
   return make_uint4(out[0], out[1], out[2], out[3]);

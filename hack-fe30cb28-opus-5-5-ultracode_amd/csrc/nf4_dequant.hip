@@ -20,7 +20,6 @@ __global__ __launch_bounds__(kDequantThreads) void nf4_dequant_kernel(NF4Ref w, 
   __syncthreads();
   const uint32_t* words = reinterpret_cast<const uint32_t*>(w.packed);
   const int64_t base = (int64_t)blockIdx.x * (kDequantThreads * kDequantWPT) + threadIdx.x;
-  const int words_per_block = w.bs1 / 8;
   uint32_t v[kDequantWPT];
 #pragma unroll
   for (int i = 0; i < kDequantWPT; ++i) {
@@ -31,7 +30,7 @@ __global__ __launch_bounds__(kDequantThreads) void nf4_dequant_kernel(NF4Ref w, 
   for (int i = 0; i < kDequantWPT; ++i) {
     const int64_t idx = base + i * kDequantThreads;
     if (idx < n_words) {
-      const float scale = nf4_block_scale(w, idx / words_per_block);
+      const float scale = nf4_block_scale(w, idx >> (w.bs1_shift - 3));
       out[idx] = nf4_decode_word(v[i], scale, lut);
     }
   }
@@ -49,12 +48,12 @@ QLORA_API int qlora_nf4_dequant(const void* packed, const void* absmax, const fl
   QLORA_CHECK_ARG(n_blocks >= 0);
   if (n_blocks == 0) return 0;
   QLORA_CHECK_ARG(packed && absmax && out);
-  QLORA_CHECK_ARG(bs1 >= 8 && bs1 % 8 == 0);
-  QLORA_CHECK_ARG(!nested || (code2 && absmax2 && offsets && bs2 > 0));
+  QLORA_CHECK_ARG(bs1 >= 8 && (bs1 & (bs1 - 1)) == 0);
+  QLORA_CHECK_ARG(!nested || (code2 && absmax2 && offsets && bs2 > 0 && (bs2 & (bs2 - 1)) == 0));
   QLORA_CHECK_ARG(standard || code);
   QLORA_CHECK_ARG(((uintptr_t)packed & 3) == 0 && ((uintptr_t)out & 15) == 0);
   NF4Ref w{static_cast<const uint8_t*>(packed), absmax, code2, absmax2, offsets, code,
-           seg1, seg2, bs1, nested ? bs2 : 1, nested, standard};
+           seg1, seg2, __builtin_ctz(bs1), nested ? __builtin_ctz(bs2) : 0, nested, standard};
   const int64_t n_words = n_blocks * (bs1 / 8);
   const int64_t grid = qlora_cdiv(n_words, (int64_t)kDequantThreads * kDequantWPT);
   QLORA_CHECK_ARG(grid < (1ll << 31));

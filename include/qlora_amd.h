@@ -39,7 +39,7 @@ const char* qlora_error_string(int code);
  *   out      f16 [n_blocks*bs1]
  *   seg1/2   first block of the 2nd/3rd weight stacked back to back (INT64_MAX if none): they
  *            select offsets[1] / offsets[2]
- * Requires bs1 % 8 == 0, packed 4-byte and out 16-byte aligned.
+ * Requires bs1 >= 8 and bs1, bs2 powers of two; packed 4-byte and out 16-byte aligned.
  */
 int qlora_nf4_dequant(const void* packed, const void* absmax, const float* code2,
                       const float* absmax2, const float* offsets, const float* code, void* out,
