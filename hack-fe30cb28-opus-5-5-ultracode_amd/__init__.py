@@ -5,6 +5,8 @@ through solution/engine.py's op wrappers): the same Python call signatures, each
 hand-written HIP kernel of libqlora_amd.so (C-ABI: include/qlora_amd.h) on torch's current HIP
 stream. There is no Triton and no CPU fallback: without the built library every op raises.
 
+  engine   the training step: Packed, _Layer, _Head, FusedQwen2, random_qwen2
+  linear   the step's GEMMs (NF4 projections forward/backward, lm_head)
   ops      the engine's op wrappers (_rms_fwd, _rms_bwd, _rope_fwd, _rope_bwd, _glu_fwd,
            _glu_bwd, _ce, _ce_piece, _ce_finish, dequant, NF4Weight, NF4Group, TorchDropout)
   quant    bitsandbytes-format NF4 double quantisation (builds the frozen weights)
@@ -12,6 +14,6 @@ stream. There is no Triton and no CPU fallback: without the built library every 
   build    hipcc build of the library
 """
 
-from . import _lib, ops, quant  # noqa: F401
+from . import _lib, ops, quant, linear, engine, profiling  # noqa: F401
 from .ops import (NF4Group, NF4Weight, TorchDropout, _ce, _ce_finish, _ce_piece,  # noqa: F401
                   _glu_bwd, _glu_fwd, _rms_bwd, _rms_fwd, _rope_bwd, _rope_fwd, dequant)

@@ -34,6 +34,7 @@ SIGNATURES = {
 }
 
 _lib = None
+HOOKS = {}  # entry point -> object with .call(fn, args) (profiling.LaunchTimer)
 
 
 class LibraryMissing(RuntimeError):
@@ -64,7 +65,9 @@ def load():
 def call(name, *args):
     """Call entry point `name`; raise RuntimeError on a non-zero return code."""
     lib = load()
-    rc = getattr(lib, name)(*args)
+    hook = HOOKS.get(name)
+    fn = getattr(lib, name)
+    rc = hook.call(fn, args) if hook is not None else fn(*args)
     if rc != 0:
         msg = lib.qlora_error_string(rc).decode(errors="replace")
         raise RuntimeError(f"{name} failed: hipError {rc} ({msg})")

@@ -1,0 +1,463 @@
+"""One Qwen2 + NF4 + LoRA training step around the gfx950 kernels (the counterpart of the
+reference's solution/engine.py, FusedQwen2 and its layer/head autograd functions).
+
+The math and rounding points are the reference's (engine.py:27-31, 1054-1400): fp32 residual
+stream, norms, RoPE, softmax and loss; fp16 at the projection outputs, the attention inputs and
+the MLP product. Pad tokens are dropped (Packed, varlen attention over cu_seqlens); every decoder
+layer is one autograd.Function that recomputes its forward in backward from its fp32 input
+(per-layer recompute), or keeps its intermediates (`keep=True`: with 288 GB of HBM the whole
+step's activations fit); the head runs final norm + lm_head + cross-entropy + dh in chunks of rows
+with the logits gradient formed in place. The LoRA-dropout masks are the ones PyTorch's
+nn.Dropout would draw, in PEFT's call order (layer 0 q, layer 0 v, layer 1 q, ...), computed by
+the kernels from the generator state, in backward again.
+
+Everything stays resident in HBM: the reference's host-offload machinery (WeightStream,
+InputStream, GuStream, AttnStream, HostHead, memory-cap planning) has no counterpart here.
+"""
+
+import math
+
+import torch
+
+from . import linear as L
+from .ops import (NF4Group, NF4Weight, TorchDropout, _ce, _glu_bwd, _glu_fwd, _rms_bwd,
+                  _rms_fwd, _rope_bwd, _rope_fwd)
+from .quant import quantize_nf4
+
+
+class UnsupportedBatch(ValueError):
+    """The step does not take this batch; raised before anything changes (engine.py:700-702)."""
+
+
+# ---------------------------------------------------------------------------------------------
+# Model description
+# ---------------------------------------------------------------------------------------------
+class Qwen2Config:
+    """Qwen2.5-1.5B by default (hidden 1536, intermediate 8960, 28 layers, 12/2 heads)."""
+
+    def __init__(self, hidden_size=1536, intermediate_size=8960, num_hidden_layers=28,
+                 num_attention_heads=12, num_key_value_heads=2, head_dim=128,
+                 vocab_size=151936, rope_theta=1e6, rms_norm_eps=1e-6, lora_r=16,
+                 lora_alpha=32, lora_dropout=0.05):
+        self.hidden_size = hidden_size
+        self.intermediate_size = intermediate_size
+        self.num_hidden_layers = num_hidden_layers
+        self.num_attention_heads = num_attention_heads
+        self.num_key_value_heads = num_key_value_heads
+        self.head_dim = head_dim
+        self.vocab_size = vocab_size
+        self.rope_theta = rope_theta
+        self.rms_norm_eps = rms_norm_eps
+        self.lora_r = lora_r
+        self.lora_alpha = lora_alpha
+        self.lora_dropout = lora_dropout
+
+
+class LayerSpec:
+    """One decoder layer's frozen weights and LoRA parameters (engine.py:875-921)."""
+
+    def __init__(self, index, cfg, ln1, ln2, nf4, bias_qkv, lora):
+        self.index = index
+        self.H = cfg.hidden_size
+        self.D = cfg.head_dim
+        self.HQ = cfg.num_attention_heads
+        self.HKV = cfg.num_key_value_heads
+        self.I = cfg.intermediate_size
+        self.eps = cfg.rms_norm_eps
+        self.ln1, self.ln2 = ln1, ln2
+        self.scale = self.D ** -0.5
+        self.w = {name: NF4Weight(p) for name, p in nf4.items()}
+        self.qkv = NF4Group.of([self.w["q_proj"], self.w["k_proj"], self.w["v_proj"]])
+        self.gu = NF4Group.of([self.w["gate_proj"], self.w["up_proj"]])
+        self.bias_qkv = bias_qkv
+        self.lora = lora  # {"q": (A, B, scaling), "v": (A, B, scaling)}
+
+    def lora_params(self):
+        out = []
+        for short in ("q", "v"):
+            a, b, _ = self.lora[short]
+            out += [a, b]
+        return out
+
+
+def _lora_scale(spec):
+    scales = {v[2] for v in spec.lora.values()}
+    assert len(scales) <= 1
+    return scales.pop() if scales else 1.0
+
+
+@torch.no_grad()
+def random_qwen2(cfg, device, seed=0, norm_dtype=torch.float32):
+    """A random-init Qwen2 with NF4 (double-quant, blocksize 64) frozen linears, fp16 tied
+    embedding, fp32 RMSNorm weights ~ 1 + N(0, 0.02), fp16 qkv bias ~ N(0, 0.02), LoRA r/alpha on
+    q and v (A kaiming-uniform fp32, B ~ N(0, 0.01) fp32). Weights ~ N(0, 0.02)."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    H, I, D = cfg.hidden_size, cfg.intermediate_size, cfg.head_dim
+    HQ, HKV, r = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.lora_r
+    shapes = {"q_proj": (HQ * D, H), "k_proj": (HKV * D, H), "v_proj": (HKV * D, H),
+              "o_proj": (H, HQ * D), "gate_proj": (I, H), "up_proj": (I, H),
+              "down_proj": (H, I)}
+
+    def randn(*shape, std=1.0, dtype=torch.float32):
+        return (torch.randn(shape, generator=g, device=device) * std).to(dtype)
+
+    layers = []
+    bound = 1.0 / math.sqrt(H)  # kaiming_uniform_(a=sqrt(5)) on a [r, H] matrix
+    scaling = cfg.lora_alpha / r
+    for i in range(cfg.num_hidden_layers):
+        nf4 = {name: quantize_nf4(randn(*shape, std=0.02, dtype=torch.float16))
+               for name, shape in shapes.items()}
+        ln1 = (1.0 + randn(H, std=0.02)).to(norm_dtype)
+        ln2 = (1.0 + randn(H, std=0.02)).to(norm_dtype)
+        bias = randn((HQ + 2 * HKV) * D, std=0.02, dtype=torch.float16)
+        lora = {}
+        for short, out_dim in (("q", HQ * D), ("v", HKV * D)):
+            a = ((torch.rand((r, H), generator=g, device=device) * 2 - 1) * bound)
+            b = randn(out_dim, r, std=0.01)
+            lora[short] = (a.requires_grad_(), b.requires_grad_(), scaling)
+        layers.append(LayerSpec(i, cfg, ln1, ln2, nf4, bias, lora))
+    embed = randn(cfg.vocab_size, H, std=0.02, dtype=torch.float16)
+    norm_w = (1.0 + randn(H, std=0.02)).to(norm_dtype)
+    return FusedQwen2(cfg, layers, embed, norm_w, device)
+
+
+# ---------------------------------------------------------------------------------------------
+# Per-step packing (engine.py:705-764)
+# ---------------------------------------------------------------------------------------------
+class RopeTable:
+    """cos / sin [positions, D/2] fp32 of the rotary embedding (rotate-half, Qwen2):
+    inv_freq_k = theta^(-2k/D), angle = pos * inv_freq in fp32 (engine.py:831-851)."""
+
+    def __init__(self, theta, head_dim, device):
+        self.theta, self.half, self.device = theta, head_dim // 2, device
+        self.cos = self.sin = None
+
+    def table(self, length):
+        if self.cos is None or self.cos.shape[0] < length:
+            size = max(1024, 1 << max(0, (length - 1).bit_length()))
+            inv = 1.0 / (self.theta ** (torch.arange(0, 2 * self.half, 2, device=self.device,
+                                                     dtype=torch.int64).float()
+                                        / (2 * self.half)))
+            freqs = torch.arange(size, device=self.device).float()[:, None] * inv[None, :]
+            self.cos = freqs.cos().contiguous()
+            self.sin = freqs.sin().contiguous()
+        return self.cos, self.sin
+
+
+class Packed:
+    """One micro-batch without its padding: real tokens of every row, back to back."""
+
+    def __init__(self, input_ids, attention_mask, labels, rope, dropout, dropout_p):
+        if input_ids.dim() != 2 or attention_mask.shape != input_ids.shape \
+                or labels.shape != input_ids.shape:
+            raise UnsupportedBatch("inputs are not [rows, tokens]")
+        B, T = input_ids.shape
+        lengths = attention_mask.sum(dim=1)
+        lengths_cpu = lengths.tolist()
+        expected = torch.arange(T, device=input_ids.device)[None, :] < lengths[:, None]
+        if not bool(torch.equal(attention_mask.bool(), expected)):
+            raise UnsupportedBatch("attention_mask is not right-padded")
+        flat = expected.reshape(-1).nonzero().squeeze(1)
+        self.n = int(flat.numel())
+        self.tok = flat  # each packed token's index in the padded [B, T] batch (int64)
+        self.T = T
+        self.rows = B
+        self.lengths = [int(x) for x in lengths_cpu]
+        self.max_len = max(self.lengths) if self.lengths else 0
+        self.ids = input_ids.reshape(-1)[flat]
+        self.pos = (flat % T).to(torch.int32)
+        shifted = torch.full_like(labels, -100)
+        shifted[:, :-1] = labels[:, 1:]
+        self.targets = shifted.reshape(-1)[flat].contiguous()
+        supervised = self.targets >= 0
+        self.head_order = torch.argsort((~supervised).to(torch.int8), stable=True)
+        self.n_supervised = int(supervised.sum())
+        cu = [0]
+        for length in self.lengths:
+            cu.append(cu[-1] + length)
+        self.cu_seqlens_host = cu
+        self.cu_seqlens = torch.tensor(cu, device=input_ids.device, dtype=torch.int32)
+        self.cos, self.sin = rope.table(max(self.max_len, 1))
+        self.dropout_p = dropout_p
+        self.dropout = dropout
+        self.drop_seed = self.drop_threads = None
+        self.drop_vec = dropout.vec if dropout is not None else 4
+        self.lora16_views = None
+
+    def lora16(self, index, weights):
+        if self.lora16_views is not None:
+            return self.lora16_views[index]
+        return tuple(None if t is None else t.detach().to(torch.float16) for t in weights)
+
+    def draw(self, H):
+        """The counter of the next LoRA dropout mask of this step (the next nn.Dropout call on
+        the padded [B, T, H] LoRA input), engine.py:758-764."""
+        seed, ctr, threads = self.dropout.draw(self.rows * self.T * H)
+        assert self.drop_seed in (None, seed) and self.drop_threads in (None, threads)
+        self.drop_seed, self.drop_threads = seed, threads
+        return ctr
+
+
+# ---------------------------------------------------------------------------------------------
+# Attention (engine.py:857-869): causal attention within each packed sequence
+# ---------------------------------------------------------------------------------------------
+# PyTorch-ROCm's varlen entry points (aten._efficient_attention_* with cu_seqlens) gave NaN
+# gradients on MI355X for multi-sequence batches, so each sequence runs through the dense causal
+# scaled_dot_product_attention ([1, heads, L, D]); the backward recomputes the sequence's
+# attention under autograd. k and v arrive repeated to HQ heads (rope kernel, kv_heads = HQ).
+def _seq_slices(packed):
+    cu = packed.cu_seqlens_host
+    return [slice(cu[i], cu[i + 1]) for i in range(len(cu) - 1) if cu[i + 1] > cu[i]]
+
+
+def _heads_first(t):
+    return t.transpose(0, 1).contiguous()[None]
+
+
+def _attn_fwd(q, k, v, packed, scale):
+    out = torch.empty_like(q)
+    with torch.no_grad():
+        for sl in _seq_slices(packed):
+            o = torch.nn.functional.scaled_dot_product_attention(
+                _heads_first(q[sl]), _heads_first(k[sl]), _heads_first(v[sl]), is_causal=True,
+                scale=scale)
+            out[sl] = o[0].transpose(0, 1)
+    return out, None, None, None
+
+
+def _attn_bwd(dout, q, k, v, out, lse, seed, offset, packed, scale):
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    with torch.enable_grad():
+        for sl in _seq_slices(packed):
+            qs = _heads_first(q[sl]).requires_grad_()
+            ks = _heads_first(k[sl]).requires_grad_()
+            vs = _heads_first(v[sl]).requires_grad_()
+            o = torch.nn.functional.scaled_dot_product_attention(qs, ks, vs, is_causal=True,
+                                                                 scale=scale)
+            g = torch.autograd.grad(o, (qs, ks, vs), _heads_first(dout[sl]))
+            dq[sl] = g[0][0].transpose(0, 1)
+            dk[sl] = g[1][0].transpose(0, 1)
+            dv[sl] = g[2][0].transpose(0, 1)
+    return dq, dk, dv
+
+
+# ---------------------------------------------------------------------------------------------
+# One decoder layer (engine.py:1054-1340)
+# ---------------------------------------------------------------------------------------------
+def _layer_forward(spec, h, packed, lora16, seeds, keep):
+    """The layer's forward; with keep=True returns (None, everything the backward reads)."""
+    n, H = h.shape
+    D, HQ = spec.D, spec.HQ
+    aq_w, bq_w, av_w, bv_w = lora16
+    s = _lora_scale(spec)
+    _, a, aq, av, rstd1 = _rms_fwd(spec, h, spec.ln1, packed, seeds=seeds,
+                                   drop_q=aq_w is not None, drop_v=av_w is not None)
+    qkv = L.nf4_linear(a, spec.qkv, bias=spec.bias_qkv)
+    del a
+    xq = aq @ aq_w.t()
+    lq = xq @ bq_w.t()
+    xv = av @ av_w.t()
+    lv = xv @ bv_w.t()
+    q, k, v = _rope_fwd(spec, qkv, lq, lv, packed, s)
+    del qkv, lq, lv
+    out, lse, aseed, aoffset = _attn_fwd(q, k, v, packed, spec.scale)
+    o = L.nf4_linear(out.reshape(n, HQ * D), spec.w["o_proj"])
+    h2, b, _, _, rstd2 = _rms_fwd(spec, h, spec.ln2, packed, delta=o)
+    del o
+    gu = L.nf4_linear(b, spec.gu)
+    del b
+    if keep:
+        return None, dict(rstd1=rstd1, aq=aq, av=av, xq=xq, xv=xv, q=q, k=k, v=v, out=out,
+                          lse=lse, aseed=aseed, aoffset=aoffset, h2=h2, rstd2=rstd2, gu=gu)
+    m = _glu_fwd(gu, spec.I)
+    del gu
+    d = L.nf4_linear(m, spec.w["down_proj"])
+    return torch.add(h2, d), None
+
+
+class _Layer(torch.autograd.Function):
+    """One decoder layer: input (fp32 residual) kept; the backward recomputes the forward with
+    the same dropout counters (or reads the kept intermediates) and goes back through it. The
+    LoRA weights are inputs, so autograd hands their gradients to the optimizer."""
+
+    @staticmethod
+    def forward(ctx, h, spec, packed, keep_all, aq_w, bq_w, av_w, bv_w):
+        drop = packed.dropout is not None
+        seeds = (packed.draw(spec.H) if drop else 0, packed.draw(spec.H) if drop else 0)
+        lora16 = packed.lora16(spec.index, (aq_w, bq_w, av_w, bv_w))
+        if keep_all:
+            _, f = _layer_forward(spec, h, packed, lora16, seeds, keep=True)
+            m = _glu_fwd(f["gu"], spec.I)
+            h3 = torch.add(f["h2"], L.nf4_linear(m, spec.w["down_proj"]))
+            del m
+            ctx.kept = f
+        else:
+            h3, _ = _layer_forward(spec, h, packed, lora16, seeds, keep=False)
+            ctx.kept = None
+        ctx.save_for_backward(h, aq_w, bq_w, av_w, bv_w)
+        ctx.spec, ctx.packed, ctx.seeds = spec, packed, seeds
+        return h3
+
+    @staticmethod
+    def backward(ctx, dh3):
+        h, aq_w, bq_w, av_w, bv_w = ctx.saved_tensors
+        spec, packed, seeds = ctx.spec, ctx.packed, ctx.seeds
+        s = _lora_scale(spec)
+        n, H = h.shape
+        D, HQ, HKV = spec.D, spec.HQ, spec.HKV
+        C = (HQ + 2 * HKV) * D
+        dh3 = dh3.contiguous()
+        lora16 = packed.lora16(spec.index, (aq_w, bq_w, av_w, bv_w))
+        dm = L.nf4_linear_t(dh3.to(torch.float16), spec.w["down_proj"])
+        if ctx.kept is not None:
+            f, ctx.kept = ctx.kept, None
+        else:
+            with torch.no_grad():
+                _, f = _layer_forward(spec, h, packed, lora16, seeds, keep=True)
+        gu = f.pop("gu")
+        _glu_bwd(dm, gu, spec.I)
+        del dm
+        db = L.nf4_linear_t(gu, spec.gu)
+        del gu
+        dh2 = _rms_bwd(spec, db, f.pop("h2"), f.pop("rstd2"), spec.ln2, packed, dres=dh3)
+        del db, dh3
+        dout = L.nf4_linear_t(dh2.to(torch.float16), spec.w["o_proj"]).view(n, HQ, D)
+        dq, dk, dv = _attn_bwd(dout, f.pop("q"), f.pop("k"), f.pop("v"), f.pop("out"),
+                               f.pop("lse"), f.pop("aseed"), f.pop("aoffset"), packed,
+                               spec.scale)
+        del dout
+        dqkv = _rope_bwd(spec, dq, dk, dv, packed)
+        del dq, dk, dv
+        need_dh = ctx.needs_input_grad[0]
+        da = L.nf4_linear_t(dqkv, spec.qkv) if need_dh else None
+        # LoRA (engine.py:1319-1331): dB = s g^T x, dx = s g B, dA = dx^T drop(a), t = dx A
+        grads = {}
+        for short, a_w, b_w, cols in (("q", lora16[0], lora16[1], slice(0, HQ * D)),
+                                      ("v", lora16[2], lora16[3], slice((HQ + HKV) * D, C))):
+            x_lo, a_in = f.pop("x" + short), f.pop("a" + short)
+            g = dqkv[:, cols]
+            db_w = (g.t() @ x_lo).float() * s
+            dx_lo = (g @ b_w) * s
+            da_w = (dx_lo.t() @ a_in).float()
+            grads[short] = (da_w, db_w, dx_lo @ a_w if need_dh else None)
+        del dqkv
+        dh = None
+        if need_dh:
+            dh = _rms_bwd(spec, da, h, f["rstd1"], spec.ln1, packed, dres=dh2,
+                          tq=grads["q"][2], tv=grads["v"][2], seeds=seeds)
+        return (dh, None, None, None, grads["q"][0], grads["q"][1], grads["v"][0],
+                grads["v"][1])
+
+
+# ---------------------------------------------------------------------------------------------
+# Final norm + lm_head + cross-entropy (engine.py:1352-1400)
+# ---------------------------------------------------------------------------------------------
+class HeadStats:
+    """Row order, per-token loss, entropy and correct of the head (the logged metrics)."""
+
+
+class _Head(torch.autograd.Function):
+    """Final RMSNorm + lm_head + cross-entropy, rows supervised-first in chunks: logits of a
+    chunk, the CE kernel writes softmax - onehot over them, dhn = G W, then the norm's backward
+    with grad_scale = 1/denom. The loss is sum(tok_loss)/denom; the backward scales the saved
+    dh."""
+
+    @staticmethod
+    def forward(ctx, h, norm_w, eps, lm_w, packed, denom, stats, chunk):
+        n, H = h.shape
+        dev = h.device
+        spec = HeadStats()
+        spec.eps = eps
+        order = packed.head_order
+        n_sup = packed.n_supervised
+        hp = h.index_select(0, order)
+        targets = packed.targets.index_select(0, order)
+        _, hn, _, _, rstd = _rms_fwd(spec, hp, norm_w, packed)
+        dhp = torch.empty_like(hp)
+        tok_loss = torch.empty((n,), device=dev, dtype=torch.float32)
+        entropy = torch.empty((n,), device=dev, dtype=torch.float32)
+        correct = torch.empty((n,), device=dev, dtype=torch.int32)
+        inv = 1.0 / float(denom) if float(denom) else float("nan")
+        for c0 in range(0, n, chunk):
+            c1 = min(n, c0 + chunk)
+            logits = L.linear(hn[c0:c1], lm_w)
+            needs_grad = c0 < n_sup
+            _ce(logits, targets[c0:c1], tok_loss[c0:c1], entropy[c0:c1], correct[c0:c1],
+                zero_unsupervised=needs_grad)
+            if needs_grad:
+                dhn = L.linear_t(logits, lm_w)
+                del logits
+                _rms_bwd(spec, dhn, hp[c0:c1], rstd[c0:c1], norm_w, packed, grad_scale=inv,
+                         out=dhp[c0:c1])
+                del dhn
+            else:
+                del logits
+                dhp[c0:c1].zero_()
+        dh = torch.empty_like(h)
+        dh.index_copy_(0, order, dhp)
+        ctx.save_for_backward(dh)
+        stats.order, stats.tok_loss = order, tok_loss
+        stats.entropy, stats.correct = entropy, correct
+        return tok_loss.sum() * inv
+
+    @staticmethod
+    def backward(ctx, grad):
+        (dh,) = ctx.saved_tensors
+        return dh * grad, None, None, None, None, None, None, None
+
+
+# ---------------------------------------------------------------------------------------------
+# The model
+# ---------------------------------------------------------------------------------------------
+class FusedQwen2:
+    """The step of a Qwen2 NF4 + LoRA model (engine.py:1568-1922 without the offload planner)."""
+
+    HEAD_CHUNK = 4096  # rows of logits alive at a time (4096 x 151936 fp16 = 1.2 GB)
+
+    def __init__(self, cfg, layers, embed, norm_w, device, keep_all=False):
+        self.cfg = cfg
+        self.layers = layers
+        self.embed = embed
+        self.lm_w = embed  # tied
+        self.norm_w = norm_w
+        self.eps = cfg.rms_norm_eps
+        self.device = torch.device(device)
+        self.keep_all = keep_all
+        self.dropout_p = cfg.lora_dropout
+        self.rope = RopeTable(cfg.rope_theta, cfg.head_dim, self.device)
+        self.dropout = TorchDropout(self.device, torch.float32) if self.dropout_p > 0 else None
+        # one fp16 buffer for every LoRA weight, refreshed by a single foreach copy per step
+        # (engine.py:1599-1624)
+        self.lora_fp32 = [t for spec in layers for t in spec.lora_params()]
+        total = sum(t.numel() for t in self.lora_fp32)
+        self.lora_buf = torch.empty((total,), device=self.device, dtype=torch.float16)
+        views, start = [], 0
+        for t in self.lora_fp32:
+            views.append(self.lora_buf[start:start + t.numel()].view(t.shape))
+            start += t.numel()
+        self.lora_views = views
+        self.lora16_by_layer = [tuple(views[4 * i:4 * i + 4]) for i in range(len(layers))]
+
+    def parameters(self):
+        return list(self.lora_fp32)
+
+    def step(self, input_ids, attention_mask, labels, denom):
+        """The step's forward: (loss, packed, stats); autograd runs the backward."""
+        packed = Packed(input_ids, attention_mask, labels, self.rope, self.dropout,
+                        self.dropout_p)
+        if self.dropout is not None and self.dropout.ok is None:
+            self.dropout.ok = self.dropout.check(packed.rows,
+                                                 min(packed.T, TorchDropout.CHECK_TOKENS),
+                                                 self.cfg.hidden_size, self.dropout_p)
+        if self.dropout is not None and not self.dropout.ok:
+            raise UnsupportedBatch("LoRA dropout masks differ from PyTorch's on this GPU")
+        with torch.no_grad():
+            torch._foreach_copy_(self.lora_views, [t.detach() for t in self.lora_fp32])
+        packed.lora16_views = self.lora16_by_layer
+        h = torch.nn.functional.embedding(packed.ids, self.embed).float()
+        for spec in self.layers:
+            h = _Layer.apply(h, spec, packed, self.keep_all, *spec.lora_params())
+        stats = HeadStats()
+        loss = _Head.apply(h, self.norm_w, self.eps, self.lm_w, packed, denom, stats,
+                           self.HEAD_CHUNK)
+        return loss, packed, stats

@@ -1,0 +1,82 @@
+"""Per-launch timing of one C-ABI entry point with HIP events, and its algorithmic work.
+
+`LaunchTimer(entry)` records a pair of events on torch's current stream (the stream every entry
+point is launched on) around each launch of `entry` while active, and reports the average launch
+duration and achieved bandwidth or FLOP rate against the MI355X peak (HBM 8 TB/s, dense fp16
+MFMA 2.5 PFLOP/s).
+"""
+
+import torch
+
+from . import _lib
+
+HBM_PEAK_GBS = 8000.0
+FP16_PEAK_TFLOPS = 2500.0
+
+# the kernel reported as the step's roofline entry
+DOMINANT = "qlora_nf4_dequant"
+
+
+def _dequant_bytes(args):
+    """Algorithmic HBM bytes of one qlora_nf4_dequant launch: packed nibbles, absmax, the
+    double-quantisation tables, and the fp16 output."""
+    n_blocks, nested, bs1, bs2, seg1, seg2 = args[7], args[8], args[10], args[11], args[12], \
+        args[13]
+    numel = n_blocks * bs1
+    b = numel // 2 + 2 * numel
+    if nested:
+        segs = 1 + (seg1 < n_blocks) + (seg2 < n_blocks)
+        b += n_blocks + 4 * ((n_blocks + bs2 - 1) // bs2) + 4 * 256 + 4 * segs
+    else:
+        b += 4 * n_blocks
+    return b
+
+
+WORK = {
+    "qlora_nf4_dequant": ("hbm", _dequant_bytes),
+}
+
+
+class LaunchTimer:
+    def __init__(self, entry):
+        if entry not in WORK:
+            raise ValueError(f"no work model for {entry}")
+        self.entry = entry
+        self.bound, self.work = WORK[entry]
+        self.records = []
+
+    def __enter__(self):
+        _lib.HOOKS[self.entry] = self
+        return self
+
+    def __exit__(self, *exc):
+        _lib.HOOKS.pop(self.entry, None)
+        return False
+
+    def call(self, fn, args):
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        rc = fn(*args)
+        end.record()
+        self.records.append((start, end, self.work(args)))
+        return rc
+
+    def summary(self):
+        torch.cuda.synchronize()
+        if not self.records:
+            return None
+        ms = [s.elapsed_time(e) for s, e, _ in self.records]
+        work = sum(w for _, _, w in self.records)
+        total_s = sum(ms) * 1e-3
+        avg_us = 1e3 * sum(ms) / len(ms)
+        if self.bound == "hbm":
+            achieved = work / total_s / 1e9
+            peak, unit = HBM_PEAK_GBS, "GB/s"
+        else:
+            achieved = work / total_s / 1e12
+            peak, unit = FP16_PEAK_TFLOPS, "TFLOP/s"
+        return {"bound": self.bound, "achieved": achieved, "peak": peak, "unit": unit,
+                "frac": achieved / peak, "traffic": None, "kernel": self.entry,
+                "launches": len(ms), "avg_us": avg_us,
+                "work_per_launch": work / len(ms)}

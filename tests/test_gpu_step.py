@@ -1,0 +1,118 @@
+"""The whole step on the GPU against the CPU oracle step (autograd), and the varlen attention it
+relies on against per-sequence SDPA (test_kernels.py:245-281, 314-400)."""
+
+import pytest
+import torch
+
+from oracle import step as OS
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def close(a, b, tol):
+    torch.testing.assert_close(a.detach().cpu().float(), b.detach().cpu().float(), rtol=tol,
+                               atol=tol)
+
+
+def test_varlen_attention_matches_sdpa(pkg):
+    torch.manual_seed(0)
+    lengths = [7, 130, 1, 64]
+    HQ, D = 12, 128
+
+    class P:
+        pass
+
+    packed = P()
+    packed.cu_seqlens_host = [0, *torch.tensor(lengths).cumsum(0).tolist()]
+    packed.cu_seqlens = torch.tensor(packed.cu_seqlens_host, device=DEV, dtype=torch.int32)
+    packed.max_len = max(lengths)
+    n = sum(lengths)
+    q = torch.randn(n, HQ, D, device=DEV, dtype=torch.float16)
+    k = torch.randn(n, HQ, D, device=DEV, dtype=torch.float16)
+    v = torch.randn(n, HQ, D, device=DEV, dtype=torch.float16)
+    scale = D ** -0.5
+    out, lse, s, o = pkg.engine._attn_fwd(q, k, v, packed, scale)
+    dout = torch.randn_like(q)
+    dq, dk, dv = pkg.engine._attn_bwd(dout, q, k, v, out, lse, s, o, packed, scale)
+    start = 0
+    for length in lengths:
+        sl = slice(start, start + length)
+        qr = q[sl].float().cpu().transpose(0, 1).requires_grad_()
+        kr = k[sl].float().cpu().transpose(0, 1).requires_grad_()
+        vr = v[sl].float().cpu().transpose(0, 1).requires_grad_()
+        ref = torch.nn.functional.scaled_dot_product_attention(qr, kr, vr, is_causal=True)
+        g = torch.autograd.grad(ref, (qr, kr, vr), dout[sl].float().cpu().transpose(0, 1))
+        close(out[sl], ref.transpose(0, 1), 2e-3)
+        close(dq[sl], g[0].transpose(0, 1), 1e-2)
+        close(dk[sl], g[1].transpose(0, 1), 1e-2)
+        close(dv[sl], g[2].transpose(0, 1), 1e-2)
+        start += length
+
+
+def _tiny(pkg, layers=2, dropout=0.05):
+    cfg = pkg.engine.Qwen2Config(hidden_size=256, intermediate_size=640, num_hidden_layers=layers,
+                                 num_attention_heads=4, num_key_value_heads=2, head_dim=64,
+                                 vocab_size=3000, lora_dropout=dropout)
+    return pkg.engine.random_qwen2(cfg, DEV, seed=3)
+
+
+def _batch(lengths, vocab, prompt=3, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    B, T = len(lengths), max(lengths)
+    ids = torch.randint(0, vocab, (B, T), generator=g)
+    mask = (torch.arange(T)[None] < torch.tensor(lengths)[:, None]).long()
+    ids = torch.where(mask.bool(), ids, 0)
+    labels = torch.where(mask.bool(), ids, -100)
+    labels[:, :prompt] = -100
+    return ids, mask, labels
+
+
+@pytest.mark.parametrize("lengths,keep_all", [([17, 60, 33, 5], False), ([4], False),
+                                              ([40, 40], True)])
+def test_step_matches_oracle(pkg, lengths, keep_all):
+    """Loss and LoRA gradients of one GPU step equal the CPU oracle's (fp32 autograd with the
+    same NF4 bytes and dropout masks) within the reference's whole-step tolerance; the CUDA
+    generator advances exactly as the base's 2 x layers dropout calls would."""
+    model = _tiny(pkg)
+    model.keep_all = keep_all
+    cpu = OS.CpuQwen2(model)
+    ids, mask, labels = _batch(lengths, model.cfg.vocab_size)
+    denom = float((labels[:, 1:] != -100).sum())
+    torch.cuda.manual_seed(1234)
+    gen = model.dropout.gen
+    seed, offset = gen.initial_seed(), gen.get_offset()
+    loss, packed, stats = model.step(ids.to(DEV), mask.to(DEV), labels.to(DEV), denom)
+    loss.backward()
+    torch.cuda.synchronize()
+    ref, _ = OS.forward_loss(cpu, ids, mask, labels, denom, drop_seed=seed, drop_offset=offset,
+                             drop_G=model.dropout.max_blocks * 256, p=model.dropout_p, vec=4)
+    ref.backward()
+    assert abs(loss.item() - ref.item()) <= 2e-3 * abs(ref.item())
+    # the generator moved as the base's dropout calls would (engine.py:796-805)
+    B, T = ids.shape
+    want = offset
+    for _ in range(2 * len(model.layers)):
+        _, _, inc = OS.philox.draw(B * T * model.cfg.hidden_size, want, model.dropout.max_blocks)
+        want += inc
+    assert gen.get_offset() == want
+    for g_gpu, leaf in zip(model.parameters(), cpu.lora_leaves()):
+        ga, gb = g_gpu.grad.detach().cpu().double(), leaf.grad.double()
+        rel = (ga - gb).norm() / gb.norm().clamp_min(1e-30)
+        assert rel < 2e-2, rel.item()
+    # per-token metrics: loss of supervised tokens, entropy finite, order supervised-first
+    assert torch.isfinite(stats.entropy).all()
+    assert int(packed.n_supervised) == int((packed.targets >= 0).sum())
+
+
+def test_unsupported_batch_is_rejected_before_any_change(pkg):
+    """Left padding raises UnsupportedBatch before the generator or anything else moves
+    (engine.py:700-717)."""
+    model = _tiny(pkg, layers=1)
+    ids, mask, labels = _batch([5, 9], model.cfg.vocab_size)
+    mask = mask.flip(1)
+    before = model.dropout.gen.get_offset()
+    with pytest.raises(pkg.engine.UnsupportedBatch):
+        model.step(ids.to(DEV), mask.to(DEV), labels.to(DEV), 1.0)
+    assert model.dropout.gen.get_offset() == before
