@@ -1,0 +1,447 @@
+// NF4 dequantisation fused into fp16 MFMA GEMMs for the frozen projections of the step.
+// Reference: the dequant kernel (kernels.py:68-105) followed by cuBLAS at engine.py:1082
+// (qkv + bias), 1112 (o), 1163 (gate|up), 1179 (down) in forward and 1239, 1293, 1301, 1316
+// (dY W) in backward.
+//
+//   NT (forward):  C[m, n] = sum_k A[m, k] W[n, k]      W = [N, K] NF4, K = reduction
+//   NN (backward): C[m, n] = sum_k A[m, k] W[k, n]      W = [K, N] NF4, N = W's columns
+//
+// The W tile is decoded once per workgroup, straight from the bitsandbytes bytes (4-bit codes,
+// double-quantised absmax) into LDS as fp16, with the same two roundings as the standalone
+// dequant, so the fused product equals dequant-then-GEMM up to the fp32 summation order. The
+// LDS B tile is always [n][k] with k contiguous (the MFMA B-operand layout): in NN each thread
+// decodes an 8-row x CW-column block and packs the values along the rows.
+//
+// Tiles BM x BN x 64 with 256 threads = 4 wavefronts in 2 x 2, each owning a (BM/2) x (BN/2)
+// block of v_mfma_f32_32x32x16_f16 accumulators. A 256-row tile amortises the NF4 decode (VALU)
+// over 256 rows of MFMA work and a 128 x 128 wavefront tile halves the LDS fragment reads per
+// MFMA compared with 64 x 64. LDS rows hold 64 halves (eight 16-byte chunks); chunk c of row r
+// sits at c ^ ((r ^ r >> 3) & 7), so the fragment reads (consecutive rows, same chunk) and the
+// tile writes are free of bank conflicts for 32 or 64 banks. Double-buffered LDS, next tile's
+// global loads issued before the current tile's MFMAs; workgroups ordered so each XCD (blocks
+// are dispatched round-robin over the 8 XCDs) sweeps a contiguous range of W tiles.
+//
+// Split-K: with splits > 1 each z-slice reduces a contiguous range of k-tiles into an fp32
+// workspace [splits, M, N]; a second kernel sums the slices and applies the epilogue.
+//
+// Epilogues: fp16 store; + fp16 bias (qkv); fp32 residual add out = res + f32(fp16(acc))
+// (h3 = h2 + d); SwiGLU m = fp16(silu(fp16 g) * fp16 u) with the gate and up rows of one output
+// column in the same wavefront (gate|up forward without materialising [gate|up]).
+#include "nf4.h"
+
+namespace qlora {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kBK = 64, kGemmThreads = 256;
+
+enum { kEpiStore = 0, kEpiBias = 1, kEpiResid = 2, kEpiSwiglu = 3, kEpiPartial = 4 };
+
+struct GemmArgs {
+  const void* a;         // [M, Kr] fp16, or fp32 (a_f32: rounded to fp16 on load)
+  int64_t lda;
+  NF4Ref w;
+  int64_t Kw;            // W's row length (columns)
+  void* c;               // fp16 [M, ldc]; fp32 for kEpiResid; fp32 [splits, M, N] partials
+  int64_t ldc;
+  const uint16_t* bias;  // fp16 [N] (kEpiBias)
+  const float* resid;    // fp32 [M, ldr] (kEpiResid)
+  int64_t ldr;
+  int64_t M, N, Kr;      // output rows, output columns, reduction length
+  int64_t I;             // SwiGLU: first W row of the up projection
+  int64_t kt_per_split;  // k-tiles per z-slice
+};
+
+__device__ __forceinline__ int swz(int row) { return (row ^ (row >> 3)) & 7; }
+__device__ __forceinline__ int lds_off(int row, int chunk) {
+  return row * kBK + ((chunk ^ swz(row)) << 3);
+}
+
+__device__ __forceinline__ int64_t tile_order(int64_t b, int64_t total) {
+  const int64_t full = total / 8 * 8;
+  return b < full ? (b % 8) * (full / 8) + b / 8 : b;
+}
+
+template <int BM, bool A_F32>
+struct ALoader {
+  static constexpr int kPer = BM * kBK / 8 / kGemmThreads;  // 16-byte chunks per thread
+  uint4 v[kPer];
+  __device__ __forceinline__ void load(const GemmArgs& g, int64_t m0, int64_t k0) {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int id = threadIdx.x + kGemmThreads * i;
+      const int row = id >> 3, col = (id & 7) * 8;
+      const int64_t m = m0 + row;
+      if (m < g.M) {
+        if constexpr (A_F32) {
+          const float* p = static_cast<const float*>(g.a) + m * g.lda + k0 + col;
+          const float4 x = reinterpret_cast<const float4*>(p)[0];
+          const float4 y = reinterpret_cast<const float4*>(p)[1];
+          v[i] = make_uint4(pack2h(x.x, x.y), pack2h(x.z, x.w), pack2h(y.x, y.y),
+                            pack2h(y.z, y.w));
+        } else {
+          v[i] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(g.a) +
+                                                 m * g.lda + k0 + col);
+        }
+      } else {
+        v[i] = make_uint4(0, 0, 0, 0);
+      }
+    }
+  }
+  __device__ __forceinline__ void store(uint16_t* s) const {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int id = threadIdx.x + kGemmThreads * i;
+      *reinterpret_cast<uint4*>(s + lds_off(id >> 3, id & 7)) = v[i];
+    }
+  }
+};
+
+// W row of LDS B row `n` in the NT orientation. SwiGLU: within each wavefront's BN/2 rows, the
+// first half are gate rows and the second half the up rows of the same output columns.
+template <int BN, int EPI>
+__device__ __forceinline__ int64_t nt_wrow(const GemmArgs& g, int64_t tile_n, int n) {
+  if constexpr (EPI == kEpiSwiglu) {
+    constexpr int WN = BN / 2, HALF = WN / 2;
+    const int64_t j = tile_n * (BN / 2) + (n / WN) * HALF + (n % HALF);
+    return (n % WN) >= HALF ? g.I + j : j;
+  } else {
+    return tile_n * BN + n;
+  }
+}
+
+// NT: B tile = W rows (BN) x 64 columns; a run = 32 columns of one row (16 bytes, one scale).
+template <int BN, int EPI>
+struct BLoaderNT {
+  static constexpr int kPer = BN * kBK / 32 / kGemmThreads;
+  uint4 v[kPer];
+  float scale[kPer];
+  __device__ __forceinline__ void load(const GemmArgs& g, int64_t tile_n, int64_t k0) {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int id = threadIdx.x + kGemmThreads * i;
+      const int n = id % BN, part = id / BN;
+      const int64_t e = nt_wrow<BN, EPI>(g, tile_n, n) * g.Kw + k0 + 32 * part;
+      v[i] = *reinterpret_cast<const uint4*>(g.w.packed + (e >> 1));
+      scale[i] = nf4_block_scale(g.w, e >> g.w.bs1_shift);
+    }
+  }
+  __device__ __forceinline__ void store(uint16_t* s, const float* lut) const {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int id = threadIdx.x + kGemmThreads * i;
+      const int n = id % BN, part = id / BN;
+      *reinterpret_cast<uint4*>(s + lds_off(n, 4 * part + 0)) = nf4_decode_word(v[i].x, scale[i], lut);
+      *reinterpret_cast<uint4*>(s + lds_off(n, 4 * part + 1)) = nf4_decode_word(v[i].y, scale[i], lut);
+      *reinterpret_cast<uint4*>(s + lds_off(n, 4 * part + 2)) = nf4_decode_word(v[i].z, scale[i], lut);
+      *reinterpret_cast<uint4*>(s + lds_off(n, 4 * part + 3)) = nf4_decode_word(v[i].w, scale[i], lut);
+    }
+  }
+};
+
+// NN: B tile = W rows k0..k0+63 x columns n0..n0+BN-1; thread t decodes rows 8g..8g+7 of a
+// CW-column chunk (CW = 8 for BN = 256, 4 for BN = 128) and writes each column's 8 values as one
+// 16-byte chunk of the [n][k] tile.
+template <int BN>
+struct BLoaderNN {
+  static constexpr int CW = BN * kBK / 8 / kGemmThreads;  // columns per thread
+  static constexpr int CHUNKS = BN / CW;                  // column chunks per row
+  uint32_t v[8];
+  float scale[8];
+  __device__ __forceinline__ void load(const GemmArgs& g, int64_t n0, int64_t k0) {
+    const int c = threadIdx.x % CHUNKS, gr = threadIdx.x / CHUNKS;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int64_t e = (k0 + 8 * gr + i) * g.Kw + n0 + CW * c;
+      if constexpr (CW == 8) v[i] = *reinterpret_cast<const uint32_t*>(g.w.packed + (e >> 1));
+      else v[i] = *reinterpret_cast<const uint16_t*>(g.w.packed + (e >> 1));
+      scale[i] = nf4_block_scale(g.w, e >> g.w.bs1_shift);
+    }
+  }
+  __device__ __forceinline__ void store(uint16_t* s, const float* lut) const {
+    const int c = threadIdx.x % CHUNKS, gr = threadIdx.x / CHUNKS;
+    float x[8][CW];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+#pragma unroll
+      for (int k = 0; k < CW / 2; ++k) {
+        const uint32_t byte = (v[i] >> (8 * k)) & 0xFFu;
+        float a = lut[byte >> 4] * scale[i];
+        float b = lut[byte & 15u] * scale[i];
+        fp32_barrier(a);  // fp16(fp32(level * scale)): two roundings
+        fp32_barrier(b);
+        x[i][2 * k] = a;
+        x[i][2 * k + 1] = b;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < CW; ++j) {
+      const int n = CW * c + j;
+      *reinterpret_cast<uint4*>(s + lds_off(n, gr)) =
+          make_uint4(pack2h(x[0][j], x[1][j]), pack2h(x[2][j], x[3][j]),
+                     pack2h(x[4][j], x[5][j]), pack2h(x[6][j], x[7][j]));
+    }
+  }
+};
+
+template <int BM, int BN>
+struct GemmSmem {
+  uint16_t a[2][BM * kBK];
+  uint16_t b[2][BN * kBK];
+  float lut[16];
+};
+
+template <int BM, int BN, bool NN, int EPI, bool A_F32>
+__global__ __launch_bounds__(kGemmThreads) void nf4_gemm_kernel(GemmArgs g) {
+  constexpr int WM = BM / 2, WN = BN / 2, FM = WM / 32, FN = WN / 32;
+  __shared__ GemmSmem<BM, BN> sm;
+  if (threadIdx.x < 16)
+    sm.lut[threadIdx.x] = g.w.standard ? kNF4Levels[threadIdx.x] : g.w.code[threadIdx.x];
+
+  const int64_t m_tiles = (g.M + BM - 1) / BM;
+  const int64_t t = tile_order(blockIdx.x, gridDim.x);
+  const int64_t tile_m = t % m_tiles, tile_n = t / m_tiles;
+  const int64_t m0 = tile_m * BM;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  ALoader<BM, A_F32> la;
+  BLoaderNT<BN, EPI> lbt;
+  BLoaderNN<BN> lbn;
+  const int64_t kt0 = (int64_t)blockIdx.z * g.kt_per_split;
+  int64_t kt1 = kt0 + g.kt_per_split;
+  const int64_t ktiles_all = g.Kr / kBK;
+  if (kt1 > ktiles_all) kt1 = ktiles_all;
+
+  auto load_tile = [&](int64_t kt) {
+    la.load(g, m0, kt * kBK);
+    if constexpr (NN) lbn.load(g, tile_n * BN, kt * kBK);
+    else lbt.load(g, tile_n, kt * kBK);
+  };
+  auto store_tile = [&](int buf) {
+    la.store(sm.a[buf]);
+    if constexpr (NN) lbn.store(sm.b[buf], sm.lut);
+    else lbt.store(sm.b[buf], sm.lut);
+  };
+
+  f32x16 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  if (kt0 < kt1) {
+    load_tile(kt0);
+    __syncthreads();  // lut
+    store_tile(0);
+    __syncthreads();
+  }
+
+  const int frow = lane & 31, fchunk = lane >> 5;
+  for (int64_t kt = kt0; kt < kt1; ++kt) {
+    const int buf = (kt - kt0) & 1;
+    if (kt + 1 < kt1) load_tile(kt + 1);
+    const uint16_t* sa = sm.a[buf];
+    const uint16_t* sb = sm.b[buf];
+#pragma unroll
+    for (int ks = 0; ks < kBK / 16; ++ks) {
+      half8_t af[FM], bf[FN];
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+        af[i] = *reinterpret_cast<const half8_t*>(
+            sa + lds_off(wm * WM + i * 32 + frow, 2 * ks + fchunk));
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        bf[j] = *reinterpret_cast<const half8_t*>(
+            sb + lds_off(wn * WN + j * 32 + frow, 2 * ks + fchunk));
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+    if (kt + 1 < kt1) store_tile(buf ^ 1);
+    __syncthreads();
+  }
+
+  // epilogue: register r of lane l in a 32x32 block holds row 8(r/4) + 4(l/32) + r%4, col l%32
+  const int col_in = lane & 31;
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int64_t m = m0 + wm * WM + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+      if (m >= g.M) continue;
+      if constexpr (EPI == kEpiSwiglu) {
+#pragma unroll
+        for (int j = 0; j < FN / 2; ++j) {
+          const int64_t n = tile_n * (BN / 2) + wn * (WN / 2) + j * 32 + col_in;
+          const float gt = h2f(f2h(acc[i][j][r])), up = h2f(f2h(acc[i][j + FN / 2][r]));
+          const float mval = gt / (1.0f + expf(-gt)) * up;
+          static_cast<uint16_t*>(g.c)[m * g.ldc + n] = f2h_bits(mval);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          const int64_t n = tile_n * BN + wn * WN + j * 32 + col_in;
+          float v = acc[i][j][r];
+          if constexpr (EPI == kEpiPartial) {
+            static_cast<float*>(g.c)[((int64_t)blockIdx.z * g.M + m) * g.N + n] = v;
+          } else if constexpr (EPI == kEpiResid) {
+            static_cast<float*>(g.c)[m * g.ldc + n] = g.resid[m * g.ldr + n] + h2f(f2h(v));
+          } else {
+            if constexpr (EPI == kEpiBias) v += h2f_bits(g.bias[n]);
+            static_cast<uint16_t*>(g.c)[m * g.ldc + n] = f2h_bits(v);
+          }
+        }
+      }
+    }
+  }
+}
+
+// Sum of the split-K partials [splits, M, N] and the epilogue (store / bias / residual).
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* ws, int splits,
+                                                            int64_t M, int64_t N, int epi,
+                                                            void* c, int64_t ldc,
+                                                            const uint16_t* bias,
+                                                            const float* resid, int64_t ldr) {
+  const int64_t idx = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (idx >= M * N) return;
+  const int64_t m = idx / N, n = idx - m * N;  // N % 4 == 0: four columns of one row
+  float4 s = reinterpret_cast<const float4*>(ws + idx)[0];
+  for (int k = 1; k < splits; ++k) {
+    const float4 t = reinterpret_cast<const float4*>(ws + (int64_t)k * M * N + idx)[0];
+    s.x += t.x; s.y += t.y; s.z += t.z; s.w += t.w;
+  }
+  float v[4] = {s.x, s.y, s.z, s.w};
+  if (epi == kEpiResid) {
+    float* out = static_cast<float*>(c) + m * ldc + n;
+    const float* r = resid + m * ldr + n;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[i] = r[i] + h2f(f2h(v[i]));
+  } else {
+    uint16_t* out = static_cast<uint16_t*>(c) + m * ldc + n;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (epi == kEpiBias) v[i] += h2f_bits(bias[n + i]);
+      out[i] = f2h_bits(v[i]);
+    }
+  }
+}
+
+}  // namespace qlora
+
+using namespace qlora;
+
+namespace {
+
+template <int BM, int BN, bool NN, int EPI, bool A_F32>
+void launch_gemm(const GemmArgs& g, dim3 grid, hipStream_t s) {
+  hipLaunchKernelGGL((nf4_gemm_kernel<BM, BN, NN, EPI, A_F32>), grid, dim3(kGemmThreads), 0, s,
+                     g);
+}
+
+template <int BM, int BN, bool NN, int EPI>
+void launch_a(const GemmArgs& g, dim3 grid, hipStream_t s, bool a_f32) {
+  if (a_f32) launch_gemm<BM, BN, NN, EPI, true>(g, grid, s);
+  else launch_gemm<BM, BN, NN, EPI, false>(g, grid, s);
+}
+
+template <int BM, int BN, bool NN>
+void launch_epi(const GemmArgs& g, dim3 grid, hipStream_t s, bool a_f32, int epi) {
+  switch (epi) {
+    case kEpiStore: launch_a<BM, BN, NN, kEpiStore>(g, grid, s, a_f32); break;
+    case kEpiBias: launch_a<BM, BN, NN, kEpiBias>(g, grid, s, a_f32); break;
+    case kEpiResid: launch_a<BM, BN, NN, kEpiResid>(g, grid, s, a_f32); break;
+    case kEpiPartial: launch_a<BM, BN, NN, kEpiPartial>(g, grid, s, a_f32); break;
+    default:
+      if constexpr (!NN) launch_a<BM, BN, NN, kEpiSwiglu>(g, grid, s, a_f32);
+      break;
+  }
+}
+
+bool al(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+
+}  // namespace
+
+// mode: 0 = NT (C = A W^T), 1 = NN (C = A W). epi: 0 store fp16, 1 + bias, 2 fp32 residual,
+// 3 SwiGLU (NT only). a_f32: A is fp32 (rounded to fp16 on load). tile: 0 = 256 x 256,
+// 1 = 256 x 128. splits > 1: split-K through `ws` (fp32, splits * M * N elements).
+QLORA_API int qlora_nf4_gemm(const void* a, int64_t lda, int32_t a_f32, const void* packed,
+                             const void* absmax, const float* code2, const float* absmax2,
+                             const float* offsets, const float* code, int32_t nested,
+                             int32_t standard, int32_t bs1, int32_t bs2, int64_t seg1,
+                             int64_t seg2, int64_t w_rows, int64_t w_cols, void* c, int64_t ldc,
+                             const void* bias, const float* resid, int64_t ldr, int64_t M,
+                             int32_t mode, int32_t epi, int64_t swiglu_I, int32_t tile,
+                             int32_t splits, float* ws, int64_t ws_elems, void* stream) {
+  QLORA_CHECK_ARG(M >= 0 && w_rows > 0 && w_cols > 0);
+  if (M == 0) return 0;
+  QLORA_CHECK_ARG(a && packed && absmax && c && (mode == 0 || mode == 1));
+  QLORA_CHECK_ARG(epi >= 0 && epi <= 3 && !(epi == 3 && mode != 0));
+  QLORA_CHECK_ARG(tile == 0 || tile == 1);
+  QLORA_CHECK_ARG(splits >= 1 && splits <= 16 && !(splits > 1 && epi == 3));
+  QLORA_CHECK_ARG(bs1 >= 32 && (bs1 & (bs1 - 1)) == 0);
+  QLORA_CHECK_ARG(!nested || (code2 && absmax2 && offsets && bs2 > 0 && (bs2 & (bs2 - 1)) == 0));
+  QLORA_CHECK_ARG(standard || code);
+  QLORA_CHECK_ARG(epi != 1 || bias);
+  QLORA_CHECK_ARG(epi != 2 || (resid && ldr >= 0));
+  const int BN = tile == 0 ? 256 : 128;
+  int64_t N, Kr;
+  if (mode == 0) {
+    Kr = w_cols;
+    N = epi == 3 ? swiglu_I : w_rows;
+    QLORA_CHECK_ARG(epi != 3 || (swiglu_I % (BN / 2) == 0 && 2 * swiglu_I == w_rows));
+    QLORA_CHECK_ARG(epi == 3 || w_rows % BN == 0);
+    QLORA_CHECK_ARG(w_cols % kBK == 0);
+  } else {
+    Kr = w_rows;
+    N = w_cols;
+    QLORA_CHECK_ARG(w_cols % BN == 0 && w_rows % kBK == 0);
+  }
+  QLORA_CHECK_ARG(lda >= Kr && ldc >= N && (epi != 2 || ldr >= N));
+  QLORA_CHECK_ARG(lda % 8 == 0 && al(a, 16) && al(packed, 16));
+  QLORA_CHECK_ARG(splits == 1 || (ws && ws_elems >= (int64_t)splits * M * N && al(ws, 16)));
+  const int64_t n_tiles = epi == 3 ? N / (BN / 2) : N / BN;
+  const int64_t grid = qlora_cdiv(M, 256) * n_tiles;
+  QLORA_CHECK_ARG(grid < (1ll << 31));
+  const int64_t ktiles = Kr / kBK;
+  GemmArgs g;
+  g.a = a;
+  g.lda = lda;
+  g.w = NF4Ref{static_cast<const uint8_t*>(packed), absmax, code2, absmax2, offsets, code,
+               seg1, seg2, __builtin_ctz(bs1), nested ? __builtin_ctz(bs2) : 0, nested,
+               standard};
+  g.Kw = w_cols;
+  g.c = splits > 1 ? (void*)ws : c;
+  g.ldc = ldc;
+  g.bias = static_cast<const uint16_t*>(bias);
+  g.resid = resid;
+  g.ldr = ldr;
+  g.M = M;
+  g.N = N;
+  g.Kr = Kr;
+  g.I = swiglu_I;
+  g.kt_per_split = qlora_cdiv(ktiles, splits);
+  const int kepi = splits > 1 ? (int)kEpiPartial : epi;
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 gdim((unsigned)grid, 1, (unsigned)splits);
+  if (mode == 0) {
+    if (tile == 0) launch_epi<256, 256, false>(g, gdim, s, a_f32, kepi);
+    else launch_epi<256, 128, false>(g, gdim, s, a_f32, kepi);
+  } else {
+    if (tile == 0) launch_epi<256, 256, true>(g, gdim, s, a_f32, kepi);
+    else launch_epi<256, 128, true>(g, gdim, s, a_f32, kepi);
+  }
+  int rc = qlora_launch_status();
+  if (rc != 0 || splits == 1) return rc;
+  QLORA_CHECK_ARG(N % 4 == 0 && ldc % 4 == 0 && (epi != 2 || ldr % 4 == 0));
+  const int64_t quads = M * N / 4;
+  hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)qlora_cdiv(quads, 256)), dim3(256), 0,
+                     s, ws, splits, M, N, epi, c, ldc, static_cast<const uint16_t*>(bias), resid,
+                     ldr);
+  return qlora_launch_status();
+}

@@ -264,15 +264,15 @@ def _layer_forward(spec, h, packed, lora16, seeds, keep):
     o = L.nf4_linear(out.reshape(n, HQ * D), spec.w["o_proj"])
     h2, b, _, _, rstd2 = _rms_fwd(spec, h, spec.ln2, packed, delta=o)
     del o
-    gu = L.nf4_linear(b, spec.gu)
-    del b
     if keep:
+        gu = L.nf4_linear(b, spec.gu)
         return None, dict(rstd1=rstd1, aq=aq, av=av, xq=xq, xv=xv, q=q, k=k, v=v, out=out,
                           lse=lse, aseed=aseed, aoffset=aoffset, h2=h2, rstd2=rstd2, gu=gu)
-    m = _glu_fwd(gu, spec.I)
-    del gu
-    d = L.nf4_linear(m, spec.w["down_proj"])
-    return torch.add(h2, d), None
+    # gate|up GEMM with the SwiGLU in its epilogue ([gate|up] never stored), then down_proj
+    # with the residual add in its epilogue: h3 = h2 + fp16(m W_d^T)
+    m = L.nf4_linear_swiglu(b, spec.gu, spec.I)
+    del b
+    return L.nf4_linear_resid(m, spec.w["down_proj"], h2), None
 
 
 class _Layer(torch.autograd.Function):
@@ -288,7 +288,7 @@ class _Layer(torch.autograd.Function):
         if keep_all:
             _, f = _layer_forward(spec, h, packed, lora16, seeds, keep=True)
             m = _glu_fwd(f["gu"], spec.I)
-            h3 = torch.add(f["h2"], L.nf4_linear(m, spec.w["down_proj"]))
+            h3 = L.nf4_linear_resid(m, spec.w["down_proj"], f["h2"])
             del m
             ctx.kept = f
         else:
@@ -308,7 +308,7 @@ class _Layer(torch.autograd.Function):
         C = (HQ + 2 * HKV) * D
         dh3 = dh3.contiguous()
         lora16 = packed.lora16(spec.index, (aq_w, bq_w, av_w, bv_w))
-        dm = L.nf4_linear_t(dh3.to(torch.float16), spec.w["down_proj"])
+        dm = L.nf4_linear_t(dh3, spec.w["down_proj"])  # fp32 dh3 rounded to fp16 on load
         if ctx.kept is not None:
             f, ctx.kept = ctx.kept, None
         else:
@@ -321,7 +321,7 @@ class _Layer(torch.autograd.Function):
         del gu
         dh2 = _rms_bwd(spec, db, f.pop("h2"), f.pop("rstd2"), spec.ln2, packed, dres=dh3)
         del db, dh3
-        dout = L.nf4_linear_t(dh2.to(torch.float16), spec.w["o_proj"]).view(n, HQ, D)
+        dout = L.nf4_linear_t(dh2, spec.w["o_proj"]).view(n, HQ, D)
         dq, dk, dv = _attn_bwd(dout, f.pop("q"), f.pop("k"), f.pop("v"), f.pop("out"),
                                f.pop("lse"), f.pop("aseed"), f.pop("aoffset"), packed,
                                spec.scale)

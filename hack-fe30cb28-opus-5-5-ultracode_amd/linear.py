@@ -2,16 +2,20 @@
 (dX = dY W), and the plain fp16 lm_head products (engine.py:1082, 1112, 1163, 1179, 1239, 1293,
 1301, 1316, 1376, 1381).
 
-Backend "dequant": the NF4 weight is dequantised by the HIP kernel into an fp16 buffer (bit-exact
-with bitsandbytes), then multiplied by hipBLASLt through torch (fp16 in, fp32 accumulate, fp16
-out) - the reference's own structure (dequant, then cuBLAS).
+Backend "fused": qlora_nf4_gemm, the NF4 decode inside the MFMA GEMM's B-operand
+loader, with the epilogues the step needs (qkv bias, the SwiGLU of gate|up, the residual add
+after down_proj, fp32 gradients rounded to fp16 on load).
+Backend "dequant" (default while it is the faster one): the standalone dequant kernel into an
+fp16 buffer, then hipBLASLt through torch - the reference's own structure (dequant, then cuBLAS).
 """
 
 import torch
 
-from .ops import NF4Group, dequant
+from . import _lib
+from .ops import NF4Group, _need, _ptr, _stream, dequant
 
 BACKEND = "dequant"
+_NO_SEG = 2**63 - 1
 
 
 def _weights(w):
@@ -24,16 +28,128 @@ def dequantize(w):
     return dequant(ws, ws[0].packed.device)
 
 
+def _shape(w):
+    ws = _weights(w)
+    return sum(x.shape[0] for x in ws), ws[0].shape[1]
+
+
+def _nf4_args(w):
+    """(packed, absmax, code2, absmax2, offsets, code, nested, standard, bs1, bs2, seg1, seg2)
+    of an NF4Weight or NF4Group, as the C-ABI takes them."""
+    if isinstance(w, NF4Group):
+        seg1, seg2, offsets = w.seg1, w.seg2, w.offsets
+    else:
+        seg1 = seg2 = _NO_SEG
+        offsets = w.offset
+    nested = w.nested
+    return (_ptr(w.packed), _ptr(w.absmax), _ptr(w.code2) if nested else None,
+            _ptr(w.absmax2) if nested else None, _ptr(offsets) if nested else None,
+            _ptr(w.code), int(nested), int(w.standard), w.bs1, w.bs2 if nested else 1, seg1,
+            seg2)
+
+
+def _plan(M, N, Kr, mode, epi, w_rows, w_cols, swiglu_I):
+    """(tile, splits): 256 x 256 tiles when they fill the 256 CUs, else 256 x 128, and split-K
+    for long reductions that still leave CUs idle."""
+    def ok(bn):
+        if mode == 0:
+            return swiglu_I % (bn // 2) == 0 if epi == 3 else w_rows % bn == 0
+        return w_cols % bn == 0
+    m_tiles = -(-M // 256)
+    tile = 0 if ok(256) and m_tiles * (N // 256 if epi != 3 else N // 128) >= 256 else 1
+    if not ok(128 if tile == 1 else 256):
+        raise ValueError("W shape not supported by the fused GEMM tiles")
+    n_tiles = (N // (128 if tile == 0 else 64)) if epi == 3 else N // (256 if tile == 0 else 128)
+    tiles = m_tiles * n_tiles
+    splits = 1
+    ktiles = Kr // 64
+    if epi != 3 and tiles < 192:
+        while splits < 4 and tiles * splits * 2 <= 320 and ktiles // (splits * 2) >= 16:
+            splits *= 2
+    return tile, splits
+
+
+def nf4_gemm(a, w, mode, epi=0, bias=None, resid=None, out=None, swiglu_I=0, tile=None,
+             splits=None):
+    """The fused GEMM (qlora_nf4_gemm). mode 0: A [M, K] x W^T; mode 1: A [M, N_w] x W."""
+    dev = a.device
+    _need(a, "a", None, contiguous=False)
+    if a.dtype not in (torch.float16, torch.float32) or a.dim() != 2 or a.stride(1) != 1:
+        raise ValueError("a must be a 2-D fp16/fp32 tensor with unit column stride")
+    M = a.shape[0]
+    w_rows, w_cols = _shape(w)
+    if mode == 0:
+        n_out = swiglu_I if epi == 3 else w_rows
+        kr = w_cols
+        if a.shape[1] != w_cols:
+            raise ValueError(f"a has {a.shape[1]} columns, W {w_cols}")
+    else:
+        n_out = w_cols
+        kr = w_rows
+        if a.shape[1] != w_rows:
+            raise ValueError(f"a has {a.shape[1]} columns, W has {w_rows} rows")
+    odt = torch.float32 if epi == 2 else torch.float16
+    if out is None:
+        out = torch.empty((M, n_out), device=dev, dtype=odt)
+    _need(out, "out", odt, dev, contiguous=False)
+    if out.shape != (M, n_out) or out.stride(1) != 1:
+        raise ValueError("out has the wrong shape")
+    if epi == 1:
+        _need(bias, "bias", torch.float16, dev)
+        if bias.numel() != n_out:
+            raise ValueError("bias must have one entry per output column")
+    ldr = 0
+    if epi == 2:
+        _need(resid, "resid", torch.float32, dev, contiguous=False)
+        if resid.shape != (M, n_out) or resid.stride(1) != 1:
+            raise ValueError("resid must match the output")
+        ldr = resid.stride(0)
+    if M == 0:
+        return out
+    t, sp = _plan(M, n_out, kr, mode, epi, w_rows, w_cols, swiglu_I)
+    tile = t if tile is None else tile
+    splits = sp if splits is None else splits
+    ws = torch.empty((splits * M * n_out,), device=dev, dtype=torch.float32) if splits > 1 \
+        else None
+    _lib.call("qlora_nf4_gemm", _ptr(a), a.stride(0), int(a.dtype == torch.float32),
+              *_nf4_args(w), w_rows, w_cols, _ptr(out), out.stride(0), _ptr(bias),
+              _ptr(resid), ldr, M, mode, epi, swiglu_I, tile, splits, _ptr(ws),
+              0 if ws is None else ws.numel(), _stream(dev))
+    return out
+
+
 def nf4_linear(x, w, bias=None):
     """Y = X W^T [+ bias], fp16 [M, N]."""
+    if BACKEND == "fused":
+        return nf4_gemm(x, w, 0, epi=1 if bias is not None else 0, bias=bias)
     wd = dequantize(w)
     if bias is not None:
         return torch.addmm(bias, x, wd.t())
     return x @ wd.t()
 
 
+def nf4_linear_swiglu(x, w, I):
+    """m = fp16(silu(g) * u) of [g | u] = X W^T for the stacked gate|up weight, fp16 [M, I]."""
+    if BACKEND == "fused":
+        return nf4_gemm(x, w, 0, epi=3, swiglu_I=I)
+    from .ops import _glu_fwd
+    return _glu_fwd(nf4_linear(x, w), I)
+
+
+def nf4_linear_resid(x, w, resid, out=None):
+    """fp32 resid + fp16(X W^T) (the layer output h2 + d)."""
+    if BACKEND == "fused":
+        return nf4_gemm(x, w, 0, epi=2, resid=resid, out=out)
+    return torch.add(resid, nf4_linear(x, w), out=out)
+
+
 def nf4_linear_t(dy, w):
-    """dX = dY W, fp16 [M, K]."""
+    """dX = fp16(dY) W, fp16 [M, K]; dY may be fp32 (rounded to fp16 first, as the reference's
+    dY.to(fp16) @ W)."""
+    if BACKEND == "fused":
+        return nf4_gemm(dy, w, 1)
+    if dy.dtype != torch.float16:
+        dy = dy.to(torch.float16)
     return dy @ dequantize(w)
 
 

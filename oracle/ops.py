@@ -201,3 +201,19 @@ def ce_finish(state, best_idx, xt, targets, acc, wt, n_sup):
     correct = (valid & (best_idx.long() == targets)).to(torch.int32)
     dh = (acc[:n_sup] / s[:n_sup, None] - wt[:n_sup].float()).half()
     return loss, entropy, correct, dh
+
+
+def mlp(x, w_gu, w_d, dy):
+    """The MLP of a layer with the reference's fp16 rounding points (engine.py:1163-1179,
+    1238-1293), fp32 products of fp16 values: gu = fp16(x W_gu^T), h = fp16(silu(g) u),
+    y = fp16(h W_d^T); backward: dh = fp16(fp16(dy) W_d), [dg|du] = glu_bwd(dh, gu),
+    dx = fp16([dg|du] W_gu). Returns (h, y, dx)."""
+    f = lambda t: t.float()  # noqa: E731
+    I = w_gu.shape[0] // 2
+    gu = (f(x) @ f(w_gu).t()).half()
+    h = glu_fwd(gu, I)
+    y = (f(h) @ f(w_d).t()).half()
+    dh = (f(dy.half()) @ f(w_d)).half()
+    dgu = glu_bwd(dh, gu, I)
+    dx = (f(dgu) @ f(w_gu)).half()
+    return h, y, dx

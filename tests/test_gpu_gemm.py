@@ -1,0 +1,149 @@
+"""The fused NF4 dequant + MFMA GEMM (qlora_nf4_gemm): bit-exact decode, both orientations at the
+step's shapes, every epilogue, ragged token counts, and the config-2 MLP forward/backward against
+the oracle (1e-3 relative, fp16)."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import ops as O
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _weight(pkg, shape, seed):
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    w = (torch.randn(shape, generator=g, device=DEV) * 0.02).half()
+    return pkg.ops.NF4Weight(pkg.quant.quantize_nf4(w))
+
+
+def _group(pkg, shapes, seed):
+    return pkg.ops.NF4Group.of([_weight(pkg, s, seed + i) for i, s in enumerate(shapes)])
+
+
+def rel_err(a, ref):
+    a, ref = a.double(), ref.double()
+    return ((a - ref).norm() / ref.norm().clamp_min(1e-30)).item()
+
+
+@pytest.mark.parametrize("shape", [(1536, 1536), (2048, 1536), (1536, 8960)])
+def test_decode_inside_gemm_is_bit_exact(pkg, shape):
+    """With A = identity the product is the decoded weight itself (one exact fp32 term per
+    output): NT gives W^T, NN gives W, both bit-equal to the standalone dequant."""
+    L = pkg.linear
+    w = _weight(pkg, shape, 0)
+    ref = L.dequantize(w)
+    N, K = shape
+    eye_k = torch.eye(K, device=DEV, dtype=torch.float16)
+    nt = L.nf4_gemm(eye_k, w, 0)
+    assert torch.equal(nt.view(torch.int16), ref.t().contiguous().view(torch.int16))
+    eye_n = torch.eye(N, device=DEV, dtype=torch.float16)
+    nn = L.nf4_gemm(eye_n, w, 1)
+    assert torch.equal(nn.view(torch.int16), ref.view(torch.int16))
+
+
+def test_group_decode_bit_exact(pkg):
+    """q|k|v stacked (three double-quant offsets by segment) decode inside the GEMM."""
+    L = pkg.linear
+    grp = _group(pkg, [(1536, 1536), (256, 1536), (256, 1536)], 5)
+    ref = L.dequantize(grp)
+    eye = torch.eye(2048, device=DEV, dtype=torch.float16)
+    assert torch.equal(L.nf4_gemm(eye, grp, 1).view(torch.int16), ref.view(torch.int16))
+
+
+@pytest.mark.parametrize("M", [2048, 2049, 37, 1])
+@pytest.mark.parametrize("wshape", [(17920, 1536), (1536, 8960), (2048, 1536)])
+def test_gemm_nt_nn_against_fp64(pkg, M, wshape):
+    L = pkg.linear
+    w = _weight(pkg, wshape, 1)
+    wd = L.dequantize(w).double()
+    g = torch.Generator(device=DEV).manual_seed(M)
+    x = torch.randn(M, wshape[1], generator=g, device=DEV).half()
+    y = L.nf4_gemm(x, w, 0)
+    ref = x.double() @ wd.t()
+    assert rel_err(y, ref) < 1e-3
+    torch.testing.assert_close(y.double(), ref, rtol=2e-3, atol=2e-3 * ref.abs().max().item())
+    dy = torch.randn(M, wshape[0], generator=g, device=DEV).half()
+    dx = L.nf4_gemm(dy, w, 1)
+    ref = dy.double() @ wd
+    assert rel_err(dx, ref) < 1e-3
+    torch.testing.assert_close(dx.double(), ref, rtol=2e-3, atol=2e-3 * ref.abs().max().item())
+
+
+def test_epilogues(pkg):
+    L = pkg.linear
+    M = 300
+    g = torch.Generator(device=DEV).manual_seed(9)
+    # bias (the qkv projection)
+    grp = _group(pkg, [(1536, 1536), (256, 1536), (256, 1536)], 7)
+    wq = L.dequantize(grp).double()
+    x = torch.randn(M, 1536, generator=g, device=DEV).half()
+    bias = (torch.randn(2048, generator=g, device=DEV) * 0.1).half()
+    y = L.nf4_gemm(x, grp, 0, epi=1, bias=bias)
+    assert rel_err(y, x.double() @ wq.t() + bias.double()) < 1e-3
+    # residual add in fp32 of the fp16-rounded product (h3 = h2 + d)
+    wd = _weight(pkg, (1536, 8960), 8)
+    m = torch.randn(M, 8960, generator=g, device=DEV).half()
+    h2 = torch.randn(M, 1536, generator=g, device=DEV)
+    d = L.nf4_gemm(m, wd, 0)
+    h3 = L.nf4_gemm(m, wd, 0, epi=2, resid=h2)
+    assert h3.dtype == torch.float32
+    assert torch.equal(h3, h2 + d.float())
+    # SwiGLU over gate|up without materialising it
+    gu_w = _group(pkg, [(8960, 1536), (8960, 1536)], 10)
+    mm = L.nf4_gemm(x, gu_w, 0, epi=3, swiglu_I=8960)
+    gu = L.nf4_gemm(x, gu_w, 0)
+    assert torch.equal(mm, pkg.ops._glu_fwd(gu, 8960))
+    # fp32 A rounded to fp16 on load
+    a32 = torch.randn(M, 1536, generator=g, device=DEV)
+    assert torch.equal(L.nf4_gemm(a32, wd, 1), L.nf4_gemm(a32.half(), wd, 1))
+
+
+def test_mlp_up_path_config2(pkg):
+    """x [2048, 1536] ~ N(0,1), NF4 [gate|up] [17920, 1536] and down
+    [1536, 8960] from N(0, 0.02); h = silu(gate) * up, y = h W_d^T; backward w.r.t. x with
+    dy ~ N(0,1). Fused GEMMs against the oracle's fp32 products of the same fp16 values."""
+    L = pkg.linear
+    gu_w = _group(pkg, [(8960, 1536), (8960, 1536)], 20)
+    wd = _weight(pkg, (1536, 8960), 22)
+    g = torch.Generator().manual_seed(2)
+    x = torch.randn(2048, 1536, generator=g).half()
+    dy = torch.randn(2048, 1536, generator=g).half()
+    h_o, y_o, dx_o = O.mlp(x, L.dequantize(gu_w).cpu(), L.dequantize(wd).cpu(), dy)
+    xg, dyg = x.to(DEV), dy.to(DEV)
+    h = L.nf4_linear_swiglu(xg, gu_w, 8960)
+    y = L.nf4_linear(h, wd)
+    dh = L.nf4_linear_t(dyg, wd)
+    gu = L.nf4_linear(xg, gu_w)
+    pkg.ops._glu_bwd(dh, gu, 8960)
+    dx = L.nf4_linear_t(gu, gu_w)
+    for got, want in ((h, h_o), (y, y_o), (dx, dx_o)):
+        assert rel_err(got.cpu(), want) < 1e-3
+
+
+@pytest.mark.parametrize("tile,splits", [(0, 1), (1, 1), (0, 3), (1, 2)])
+@pytest.mark.parametrize("mode", [0, 1])
+def test_every_tile_and_split(pkg, tile, splits, mode):
+    """Each compiled tile shape and split-K setting (forced) against fp64, with the residual and
+    bias epilogues through the split-K reduce."""
+    L = pkg.linear
+    w = _weight(pkg, (1536, 2048), 31)
+    wd = L.dequantize(w).double()
+    g = torch.Generator(device=DEV).manual_seed(tile * 7 + splits)
+    M = 531
+    if mode == 0:
+        x = torch.randn(M, 2048, generator=g, device=DEV).half()
+        ref = x.double() @ wd.t()
+        bias = (torch.randn(1536, generator=g, device=DEV) * 0.1).half()
+        y = L.nf4_gemm(x, w, 0, epi=1, bias=bias, tile=tile, splits=splits)
+        assert rel_err(y, ref + bias.double()) < 1e-3
+        res = torch.randn(M, 1536, generator=g, device=DEV)
+        h = L.nf4_gemm(x, w, 0, epi=2, resid=res, tile=tile, splits=splits)
+        assert rel_err(h - res, ref) < 1e-3
+    else:
+        dy = torch.randn(M, 1536, generator=g, device=DEV)  # fp32 A, rounded on load
+        ref = dy.half().double() @ wd
+        y = L.nf4_gemm(dy, w, 1, tile=tile, splits=splits)
+        assert rel_err(y, ref) < 1e-3
