@@ -20,8 +20,8 @@ import math
 import torch
 
 from . import linear as L
-from .ops import (NF4Group, NF4Weight, TorchDropout, _ce, _glu_bwd, _glu_fwd, _rms_bwd,
-                  _rms_fwd, _rope_bwd, _rope_fwd)
+from .ops import (NF4Group, NF4Weight, TorchDropout, _attn_bwd, _attn_fwd, _ce, _glu_bwd,
+                  _glu_fwd, _rms_bwd, _rms_fwd, _rope_bwd, _rope_fwd)
 from .quant import quantize_nf4
 
 
@@ -199,48 +199,10 @@ class Packed:
 
 
 # ---------------------------------------------------------------------------------------------
-# Attention (engine.py:857-869): causal attention within each packed sequence
+# Attention (engine.py:857-869): the HIP varlen causal kernels of ops (_attn_fwd/_attn_bwd) read
+# k and v in their grouped layout [n, HKV, D]; dk/dv come back per q head and the RoPE backward
+# sums each group, as the reference's backward through the repeated k/v does.
 # ---------------------------------------------------------------------------------------------
-# PyTorch-ROCm's varlen entry points (aten._efficient_attention_* with cu_seqlens) gave NaN
-# gradients on MI355X for multi-sequence batches, so each sequence runs through the dense causal
-# scaled_dot_product_attention ([1, heads, L, D]); the backward recomputes the sequence's
-# attention under autograd. k and v arrive repeated to HQ heads (rope kernel, kv_heads = HQ).
-def _seq_slices(packed):
-    cu = packed.cu_seqlens_host
-    return [slice(cu[i], cu[i + 1]) for i in range(len(cu) - 1) if cu[i + 1] > cu[i]]
-
-
-def _heads_first(t):
-    return t.transpose(0, 1).contiguous()[None]
-
-
-def _attn_fwd(q, k, v, packed, scale):
-    out = torch.empty_like(q)
-    with torch.no_grad():
-        for sl in _seq_slices(packed):
-            o = torch.nn.functional.scaled_dot_product_attention(
-                _heads_first(q[sl]), _heads_first(k[sl]), _heads_first(v[sl]), is_causal=True,
-                scale=scale)
-            out[sl] = o[0].transpose(0, 1)
-    return out, None, None, None
-
-
-def _attn_bwd(dout, q, k, v, out, lse, seed, offset, packed, scale):
-    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
-    with torch.enable_grad():
-        for sl in _seq_slices(packed):
-            qs = _heads_first(q[sl]).requires_grad_()
-            ks = _heads_first(k[sl]).requires_grad_()
-            vs = _heads_first(v[sl]).requires_grad_()
-            o = torch.nn.functional.scaled_dot_product_attention(qs, ks, vs, is_causal=True,
-                                                                 scale=scale)
-            g = torch.autograd.grad(o, (qs, ks, vs), _heads_first(dout[sl]))
-            dq[sl] = g[0][0].transpose(0, 1)
-            dk[sl] = g[1][0].transpose(0, 1)
-            dv[sl] = g[2][0].transpose(0, 1)
-    return dq, dk, dv
-
-
 # ---------------------------------------------------------------------------------------------
 # One decoder layer (engine.py:1054-1340)
 # ---------------------------------------------------------------------------------------------
@@ -258,7 +220,7 @@ def _layer_forward(spec, h, packed, lora16, seeds, keep):
     lq = xq @ bq_w.t()
     xv = av @ av_w.t()
     lv = xv @ bv_w.t()
-    q, k, v = _rope_fwd(spec, qkv, lq, lv, packed, s)
+    q, k, v = _rope_fwd(spec, qkv, lq, lv, packed, s, kv_heads=spec.HKV)
     del qkv, lq, lv
     out, lse, aseed, aoffset = _attn_fwd(q, k, v, packed, spec.scale)
     o = L.nf4_linear(out.reshape(n, HQ * D), spec.w["o_proj"])

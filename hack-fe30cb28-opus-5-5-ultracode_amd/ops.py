@@ -406,6 +406,58 @@ def _rope_bwd(spec, dq, dk, dv, packed):
     return dqkv
 
 
+# ---------------------------------------------------------------------------------------------
+# Varlen causal attention (engine.py:857-869)
+# ---------------------------------------------------------------------------------------------
+def _attn_shapes(q, k, v, packed):
+    _need(q, "q", torch.float16)
+    dev = q.device
+    _need(k, "k", torch.float16, dev)
+    _need(v, "v", torch.float16, dev)
+    if q.dim() != 3 or k.dim() != 3 or k.shape != v.shape or k.shape[0] != q.shape[0] \
+            or k.shape[2] != q.shape[2] or q.shape[1] % k.shape[1]:
+        raise ValueError("q must be [n, HQ, D] and k, v [n, KH, D] with KH dividing HQ")
+    cu = _need(packed.cu_seqlens, "packed.cu_seqlens", torch.int32, dev)
+    if cu.dim() != 1 or cu.numel() < 1:
+        raise ValueError("packed.cu_seqlens must be [sequences + 1]")
+    return q.shape[0], q.shape[1], k.shape[1], q.shape[2], cu, dev
+
+
+def _attn_fwd(q, k, v, packed, scale):
+    """(out [n, HQ, D] fp16, lse [HQ, n] fp32, None, None): causal attention within each
+    sequence of cu_seqlens (engine.py:857-862; no dropout, so no Philox seed/offset). k and v
+    may be in grouped layout [n, KH, D] (q head h reads kv head h // (HQ // KH))."""
+    n, HQ, KH, D, cu, dev = _attn_shapes(q, k, v, packed)
+    out = torch.empty_like(q)
+    lse = torch.empty((HQ, n), device=dev, dtype=torch.float32)
+    if n:
+        _lib.call("qlora_attn_fwd", _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(lse), _ptr(cu),
+                  cu.numel() - 1, int(packed.max_len), n, HQ, KH, D, float(scale), _stream(dev))
+    return out, lse, None, None
+
+
+def _attn_bwd(dout, q, k, v, out, lse, seed, offset, packed, scale):
+    """(dq, dk, dv) of _attn_fwd (engine.py:865-869); dk and dv are per q head [n, HQ, D], the
+    gradient of the repeated k/v the reference's kernel sees (the RoPE backward sums each
+    group)."""
+    n, HQ, KH, D, cu, dev = _attn_shapes(q, k, v, packed)
+    dout = dout.contiguous()
+    _need(dout, "dout", torch.float16, dev)
+    _need(out, "out", torch.float16, dev)
+    _need(lse, "lse", torch.float32, dev)
+    if dout.shape != q.shape or out.shape != q.shape or lse.shape != (HQ, n):
+        raise ValueError("dout/out must match q and lse be [HQ, n]")
+    dq = torch.empty_like(q)
+    dk = torch.empty_like(q)
+    dv = torch.empty_like(q)
+    if n:
+        delta = torch.empty((HQ, n), device=dev, dtype=torch.float32)
+        _lib.call("qlora_attn_bwd", _ptr(dout), _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(lse),
+                  _ptr(delta), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(cu), cu.numel() - 1,
+                  int(packed.max_len), n, HQ, KH, D, float(scale), _stream(dev))
+    return dq, dk, dv
+
+
 def _rope_tables(packed, D, n, dev):
     cos, sin, pos = packed.cos, packed.sin, packed.pos
     _need(cos, "packed.cos", torch.float32, dev)

@@ -179,6 +179,32 @@ int qlora_nf4_gemm(const void* a, int64_t lda, int32_t a_f32, const void* packed
                    int64_t ldr, int64_t M, int32_t mode, int32_t epi, int64_t swiglu_I,
                    int32_t tile, int32_t splits, float* ws, int64_t ws_elems, void* stream);
 
+/*
+ * Causal attention within each packed sequence (flash attention, online softmax), grouped-query
+ * heads, fp16 operands and fp32 accumulation/softmax.
+ *   q [n, HQ, D], k/v [n, KH, D] (q head h reads kv head h / (HQ/KH)), out [n, HQ, D] fp16,
+ *   lse fp32 [HQ, n] (natural-log log-sum-exp of each query's scaled scores),
+ *   cu_seqlens int32 [nseq + 1] on the device (0 = cu[0] <= ... <= cu[nseq] = n, every
+ *   length <= max_len), scale = softmax scale (D^-1/2).
+ * Replaces _attn_fwd engine.py:857-862 (aten._efficient_attention_forward with cu_seqlens,
+ * causal) and the k/v repeat of _expand_kv engine.py:655-660.
+ * Requires D in {64, 128}, HQ % KH == 0, HQ / KH <= 6, 16-byte aligned tensors.
+ */
+int qlora_attn_fwd(const void* q, const void* k, const void* v, void* out, float* lse,
+                   const int32_t* cu_seqlens, int32_t nseq, int32_t max_len, int64_t n,
+                   int32_t HQ, int32_t KH, int32_t D, float scale, void* stream);
+
+/*
+ * Its backward: dq [n, HQ, D]; dk, dv [n, HQ, D] per q head (the caller sums the HQ/KH heads
+ * of each kv head, as the reference's backward through the repeated k/v does); delta is an
+ * fp32 [HQ, n] workspace (rowsum(dout * out)). Replaces _attn_bwd engine.py:865-869
+ * (aten._efficient_attention_backward).
+ */
+int qlora_attn_bwd(const void* dout, const void* q, const void* k, const void* v,
+                   const void* out, const float* lse, float* delta, void* dq, void* dk, void* dv,
+                   const int32_t* cu_seqlens, int32_t nseq, int32_t max_len, int64_t n,
+                   int32_t HQ, int32_t KH, int32_t D, float scale, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
