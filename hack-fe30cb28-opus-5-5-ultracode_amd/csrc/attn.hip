@@ -25,7 +25,9 @@
 // and the staging writes are spread over the banks.
 //
 // One workgroup = the q heads that share a kv head (forward, dQ), which share the staged K/V
-// tiles; dK/dV: one wavefront per (32-key block, q head). dK/dV come out per q head
+// tiles; dK/dV: four wavefronts on 128 consecutive keys of one q head, sharing the staged Q/dO.
+// Global loads of the next tile are issued before the current tile's MFMAs (register
+// prefetch), so their latency overlaps the arithmetic. dK/dV come out per q head
 // ([n, HQ, D]); the caller sums each group (the RoPE backward does, as the reference sums the
 // repeated kv heads). The log-sum-exp of the forward (natural log, fp32 [HQ, n]) and
 // delta = rowsum(dO * O) (fp32 [HQ, n], written by the dQ kernel) feed the dK/dV kernel.
@@ -39,7 +41,6 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kTok = 32;   // queries (forward, dQ) or keys (dK/dV) per wavefront
 constexpr int kKB = 64;    // keys per staged block (forward, dQ)
-constexpr int kMaxGroup = 6;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 
@@ -93,49 +94,80 @@ __device__ __forceinline__ half8_t ld_g(const uint16_t* p) {
   return *reinterpret_cast<const half8_t*>(p);
 }
 
-// rows [0, rows) of a token-major matrix (row stride `stride` elements) into a [rows][D] tile;
-// rows >= valid are zero.
-template <int D>
-__device__ __forceinline__ void stage_rows(uint16_t* tile, const uint16_t* base, int64_t stride,
-                                           int rows, int valid, int tid, int nthr) {
-  constexpr int CPR = D / 8;
-  for (int id = tid; id < rows * CPR; id += nthr) {
-    const int r = id / CPR, c = id % CPR;
-    uint4 x = make_uint4(0, 0, 0, 0);
-    if (r < valid) x = *reinterpret_cast<const uint4*>(base + (int64_t)r * stride + c * 8);
-    *reinterpret_cast<uint4*>(tile + rm_off<D>(r, c)) = x;
-  }
-}
-
-__device__ __forceinline__ uint32_t half_of(const uint4& x, int i) {
-  const uint32_t w = i < 2 ? (i == 0 ? x.x : x.y) : (i == 2 ? x.z : x.w);
-  return w;
-}
-
-// rows [0, S) of a token-major matrix into the transposed [D][S] tile, token t at slot
-// (t & ~15) | perm16(t & 15); rows >= valid are zero. A work item is a pair of rows x 8 columns.
-template <int D, int S>
-__device__ __forceinline__ void stage_tr(uint16_t* tile, const uint16_t* base, int64_t stride,
-                                         int valid, int tid, int nthr) {
-  constexpr int CPR = D / 8;
-  for (int id = tid; id < (S / 2) * CPR; id += nthr) {
-    const int c = id % CPR, j = id / CPR;
-    const int r0 = 2 * j;
-    uint4 a = make_uint4(0, 0, 0, 0), b = make_uint4(0, 0, 0, 0);
-    if (r0 < valid) a = *reinterpret_cast<const uint4*>(base + (int64_t)r0 * stride + c * 8);
-    if (r0 + 1 < valid)
-      b = *reinterpret_cast<const uint4*>(base + (int64_t)(r0 + 1) * stride + c * 8);
-    const int slot = (r0 & ~15) | perm16(r0 & 15);
+// Staging of token-major global rows into LDS tiles, split into a load phase (all of a thread's
+// global loads issued back to back into registers, so their latencies overlap, and early enough
+// to hide behind the previous tile's MFMAs) and a store phase into the tile.
+//
+// RowStage: rows [0, ROWS) of a token-major matrix (row stride `stride` elements) into a
+// [ROWS][D] tile; rows >= valid are zero.
+template <int D, int ROWS, int NT>
+struct RowStage {
+  static constexpr int CPR = D / 8, TOTAL = ROWS * CPR, CNT = (TOTAL + NT - 1) / NT;
+  uint4 r[CNT];
+  __device__ __forceinline__ void load(const uint16_t* base, int64_t stride, int valid,
+                                       int tid) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t wa = half_of(a, i), wb = half_of(b, i);
-      *reinterpret_cast<uint32_t*>(tile + tr_off<S>(8 * c + 2 * i, slot)) =
-          (wa & 0xFFFFu) | (wb << 16);
-      *reinterpret_cast<uint32_t*>(tile + tr_off<S>(8 * c + 2 * i + 1, slot)) =
-          (wa >> 16) | (wb & 0xFFFF0000u);
+    for (int i = 0; i < CNT; ++i) {
+      const int id = tid + i * NT, row = id / CPR, c = id % CPR;
+      r[i] = make_uint4(0, 0, 0, 0);
+      if (id < TOTAL && row < valid)
+        r[i] = *reinterpret_cast<const uint4*>(base + (int64_t)row * stride + c * 8);
     }
   }
+  __device__ __forceinline__ void store(uint16_t* tile, int tid) const {
+#pragma unroll
+    for (int i = 0; i < CNT; ++i) {
+      const int id = tid + i * NT;
+      if (id < TOTAL) *reinterpret_cast<uint4*>(tile + rm_off<D>(id / CPR, id % CPR)) = r[i];
+    }
+  }
+};
+
+__device__ __forceinline__ uint32_t word_of(const uint4& x, int i) {
+  return i < 2 ? (i == 0 ? x.x : x.y) : (i == 2 ? x.z : x.w);
 }
+
+// PairStage: rows [0, S) into the transposed [D][S] tile, token t at slot
+// (t & ~15) | perm16(t & 15), and optionally also into the [S][D] row tile. A work item is a
+// pair of rows x 8 columns (consecutive threads take consecutive column chunks of a row pair).
+template <int D, int S, int NT>
+struct PairStage {
+  static constexpr int CPR = D / 8, TOTAL = (S / 2) * CPR, CNT = (TOTAL + NT - 1) / NT;
+  uint4 x[CNT], y[CNT];
+  __device__ __forceinline__ void load(const uint16_t* base, int64_t stride, int valid,
+                                       int tid) {
+#pragma unroll
+    for (int i = 0; i < CNT; ++i) {
+      const int id = tid + i * NT, c = id % CPR, r0 = 2 * (id / CPR);
+      x[i] = y[i] = make_uint4(0, 0, 0, 0);
+      if (id < TOTAL) {
+        if (r0 < valid) x[i] = *reinterpret_cast<const uint4*>(base + (int64_t)r0 * stride + c * 8);
+        if (r0 + 1 < valid)
+          y[i] = *reinterpret_cast<const uint4*>(base + (int64_t)(r0 + 1) * stride + c * 8);
+      }
+    }
+  }
+  __device__ __forceinline__ void store(uint16_t* tr, uint16_t* rows, int tid) const {
+#pragma unroll
+    for (int i = 0; i < CNT; ++i) {
+      const int id = tid + i * NT, c = id % CPR, r0 = 2 * (id / CPR);
+      if (id >= TOTAL) continue;
+      const int slot = (r0 & ~15) | perm16(r0 & 15);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const uint32_t wa = word_of(x[i], w), wb = word_of(y[i], w);
+        *reinterpret_cast<uint32_t*>(tr + tr_off<S>(8 * c + 2 * w, slot)) =
+            (wa & 0xFFFFu) | (wb << 16);
+        *reinterpret_cast<uint32_t*>(tr + tr_off<S>(8 * c + 2 * w + 1, slot)) =
+            (wa >> 16) | (wb & 0xFFFF0000u);
+      }
+      if (rows != nullptr) {
+        *reinterpret_cast<uint4*>(rows + rm_off<D>(r0, c)) = x[i];
+        *reinterpret_cast<uint4*>(rows + rm_off<D>(r0 + 1, c)) = y[i];
+      }
+    }
+  }
+};
 
 // 8 accumulator values (registers 8 * half .. + 7 of acc) as an fp16 B operand.
 __device__ __forceinline__ half8_t to_b(const f32x16& acc, int half) {
@@ -167,14 +199,14 @@ __device__ __forceinline__ void store_token_row(uint16_t* row, const f32x16 (&ac
 
 // ------------------------------------------------------------------------------------------------
 // Forward: O = softmax(scale Q K^T + causal mask) V per sequence, and the log-sum-exp.
-// grid (nseq * KH, ceil(max_len / 32)), block 64 * (HQ / KH).
+// grid (nseq * KH, ceil(max_len / 32)), block 64 * G (G = HQ / KH q heads, one per wavefront).
+// Key blocks of 64 keys: block kb + 1 is loaded into registers while block kb is multiplied.
 // ------------------------------------------------------------------------------------------------
-template <int D>
-__global__ __launch_bounds__(64 * kMaxGroup) void attn_fwd_kernel(Args a) {
-  constexpr int KC = D / 16, DT = D / 32;
+template <int D, int G>
+__global__ __launch_bounds__(64 * G) void attn_fwd_kernel(Args a) {
+  constexpr int KC = D / 16, DT = D / 32, NT = 64 * G;
   __shared__ __align__(16) uint16_t ks[kKB * D];
   __shared__ __align__(16) uint16_t vt[D * kKB];
-  const int G = blockDim.x / 64;
   const int seq = blockIdx.x / a.KH, kvh = blockIdx.x % a.KH;
   const int q0 = (gridDim.y - 1 - blockIdx.y) * kTok;  // longest rows first
   const int start = a.cu[seq], L = a.cu[seq + 1] - start;
@@ -184,6 +216,15 @@ __global__ __launch_bounds__(64 * kMaxGroup) void attn_fwd_kernel(Args a) {
   const int qi = q0 + (lane & 31);
   const bool qok = qi < L;
   const int64_t qs = (int64_t)a.HQ * D, kvs = (int64_t)a.KH * D;
+  const int kend = min(q0 + kTok, L);
+  const int nkb = (kend + kKB - 1) / kKB;
+  const uint16_t* kbase = a.k + (int64_t)start * kvs + kvh * D;
+  const uint16_t* vbase = a.v + (int64_t)start * kvs + kvh * D;
+
+  RowStage<D, kKB, NT> sk;
+  PairStage<D, kKB, NT> sv;
+  sk.load(kbase, kvs, min(kKB, L), tid);
+  sv.load(vbase, kvs, min(kKB, L), tid);
 
   half8_t qr[KC];
 #pragma unroll
@@ -198,18 +239,18 @@ __global__ __launch_bounds__(64 * kMaxGroup) void attn_fwd_kernel(Args a) {
   for (int u = 0; u < DT; ++u) o[u] = f32x16{};
   float m = -__builtin_inff(), lsum = 0.f;
   const float c = a.scale * kLog2e;
-  const int kend = min(q0 + kTok, L);
-  const int nkb = (kend + kKB - 1) / kKB;
-  const uint16_t* kbase = a.k + (int64_t)start * kvs + kvh * D;
-  const uint16_t* vbase = a.v + (int64_t)start * kvs + kvh * D;
 
   for (int kb = 0; kb < nkb; ++kb) {
     const int k0 = kb * kKB;
-    const int valid = min(kKB, L - k0);
     __syncthreads();
-    stage_rows<D>(ks, kbase + (int64_t)k0 * kvs, kvs, kKB, valid, tid, blockDim.x);
-    stage_tr<D, kKB>(vt, vbase + (int64_t)k0 * kvs, kvs, valid, tid, blockDim.x);
+    sk.store(ks, tid);
+    sv.store(vt, nullptr, tid);
     __syncthreads();
+    if (kb + 1 < nkb) {
+      const int nvalid = min(kKB, L - k0 - kKB);
+      sk.load(kbase + (int64_t)(k0 + kKB) * kvs, kvs, nvalid, tid);
+      sv.load(vbase + (int64_t)(k0 + kKB) * kvs, kvs, nvalid, tid);
+    }
     f32x16 s[2];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
@@ -267,17 +308,16 @@ __global__ __launch_bounds__(64 * kMaxGroup) void attn_fwd_kernel(Args a) {
 }
 
 // ------------------------------------------------------------------------------------------------
-// Backward, dQ (and delta = rowsum(dO * O)): per 32 queries of a q head, over the key blocks
-// up to the diagonal: S^T = K Q^T, P = exp(S - lse), dP^T = V dO^T, dS = P (dP - delta),
-// dQ^T += K^T dS^T. grid and block as the forward.
+// Backward, dQ (and delta = rowsum(dO * O)): per 32 queries of a q head, over 32-key blocks up
+// to the diagonal: S^T = K Q^T, P = exp(S - lse), dP^T = V dO^T, dS = P (dP - delta),
+// dQ^T += K^T dS^T. grid and block as the forward; block kb + 1 prefetched during block kb.
 // ------------------------------------------------------------------------------------------------
-template <int D>
-__global__ __launch_bounds__(64 * kMaxGroup) void attn_dq_kernel(Args a) {
-  constexpr int KC = D / 16, DT = D / 32;
-  __shared__ __align__(16) uint16_t ks[kKB * D];
-  __shared__ __align__(16) uint16_t vs[kKB * D];
-  __shared__ __align__(16) uint16_t kt[D * kKB];
-  const int G = blockDim.x / 64;
+template <int D, int G>
+__global__ __launch_bounds__(64 * G) void attn_dq_kernel(Args a) {
+  constexpr int KC = D / 16, DT = D / 32, NT = 64 * G, KB = kTok;
+  __shared__ __align__(16) uint16_t ks[KB * D];
+  __shared__ __align__(16) uint16_t vs[KB * D];
+  __shared__ __align__(16) uint16_t kt[D * KB];
   const int seq = blockIdx.x / a.KH, kvh = blockIdx.x % a.KH;
   const int q0 = (gridDim.y - 1 - blockIdx.y) * kTok;
   const int start = a.cu[seq], L = a.cu[seq + 1] - start;
@@ -287,6 +327,15 @@ __global__ __launch_bounds__(64 * kMaxGroup) void attn_dq_kernel(Args a) {
   const int qi = q0 + (lane & 31);
   const bool qok = qi < L;
   const int64_t qs = (int64_t)a.HQ * D, kvs = (int64_t)a.KH * D;
+  const int kend = min(q0 + kTok, L);
+  const int nkb = (kend + KB - 1) / KB;
+  const uint16_t* kbase = a.k + (int64_t)start * kvs + kvh * D;
+  const uint16_t* vbase = a.v + (int64_t)start * kvs + kvh * D;
+
+  PairStage<D, KB, NT> sk;  // K into both the row tile and the transposed tile
+  RowStage<D, KB, NT> sv;
+  sk.load(kbase, kvs, min(KB, L), tid);
+  sv.load(vbase, kvs, min(KB, L), tid);
 
   half8_t qr[KC], dr[KC];
 #pragma unroll
@@ -311,76 +360,92 @@ __global__ __launch_bounds__(64 * kMaxGroup) void attn_dq_kernel(Args a) {
 #pragma unroll
   for (int u = 0; u < DT; ++u) dq[u] = f32x16{};
   const float c = a.scale * kLog2e;
-  const int kend = min(q0 + kTok, L);
-  const int nkb = (kend + kKB - 1) / kKB;
-  const uint16_t* kbase = a.k + (int64_t)start * kvs + kvh * D;
-  const uint16_t* vbase = a.v + (int64_t)start * kvs + kvh * D;
 
   for (int kb = 0; kb < nkb; ++kb) {
-    const int k0 = kb * kKB;
-    const int valid = min(kKB, L - k0);
+    const int k0 = kb * KB;
     __syncthreads();
-    stage_rows<D>(ks, kbase + (int64_t)k0 * kvs, kvs, kKB, valid, tid, blockDim.x);
-    stage_rows<D>(vs, vbase + (int64_t)k0 * kvs, kvs, kKB, valid, tid, blockDim.x);
-    stage_tr<D, kKB>(kt, kbase + (int64_t)k0 * kvs, kvs, valid, tid, blockDim.x);
+    sk.store(kt, ks, tid);
+    sv.store(vs, tid);
     __syncthreads();
-    f32x16 s[2], dp[2];
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      s[t] = f32x16{};
-      dp[t] = f32x16{};
-#pragma unroll
-      for (int kk = 0; kk < KC; ++kk) {
-        const int row = 32 * t + (lane & 31), ch = 2 * kk + (lane >> 5);
-        s[t] = mfma(ld_rm<D>(ks, row, ch), qr[kk], s[t]);
-        dp[t] = mfma(ld_rm<D>(vs, row, ch), dr[kk], dp[t]);
-      }
+    if (kb + 1 < nkb) {
+      const int nvalid = min(KB, L - k0 - KB);
+      sk.load(kbase + (int64_t)(k0 + KB) * kvs, kvs, nvalid, tid);
+      sv.load(vbase + (int64_t)(k0 + KB) * kvs, kvs, nvalid, tid);
     }
-    const bool mask = k0 + kKB - 1 > q0 || k0 + kKB > L;
+    f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int kk = 0; kk < KC; ++kk) {
+      const int row = lane & 31, ch = 2 * kk + (lane >> 5);
+      s = mfma(ld_rm<D>(ks, row, ch), qr[kk], s);
+      dp = mfma(ld_rm<D>(vs, row, ch), dr[kk], dp);
+    }
+    const bool mask = k0 + KB - 1 > q0 || k0 + KB > L;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float p = exp2f(s[t][r] * c - lse2);
-        if (mask) {
-          const int key = k0 + 32 * t + acc_row(r, lane);
-          if (key > qi || key >= L) p = 0.f;
-        }
-        s[t][r] = p * (dp[t][r] - delta);
+    for (int r = 0; r < 16; ++r) {
+      float p = exp2f(s[r] * c - lse2);
+      if (mask) {
+        const int key = k0 + acc_row(r, lane);
+        if (key > qi || key >= L) p = 0.f;
       }
-    half8_t sb[4];
+      s[r] = p * (dp[r] - delta);
+    }
+    half8_t sb[2];
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) sb[kk] = to_b(s[kk >> 1], kk & 1);
+    for (int kk = 0; kk < 2; ++kk) sb[kk] = to_b(s, kk);
 #pragma unroll
     for (int u = 0; u < DT; ++u)
 #pragma unroll
-      for (int kk = 0; kk < 4; ++kk)
-        dq[u] = mfma(ld_tr<kKB>(kt, 32 * u + (lane & 31), 2 * kk + (lane >> 5)), sb[kk], dq[u]);
+      for (int kk = 0; kk < 2; ++kk)
+        dq[u] = mfma(ld_tr<KB>(kt, 32 * u + (lane & 31), 2 * kk + (lane >> 5)), sb[kk], dq[u]);
   }
   if (qok) store_token_row<D>(a.out + (int64_t)(start + qi) * qs + h * D, dq, a.scale, lane);
 }
 
 // ------------------------------------------------------------------------------------------------
-// Backward, dK and dV of one q head: per 32 keys, over the query blocks from the diagonal to the
-// end of the sequence: S = Q K^T, P = exp(S - lse), dP = dO V^T, dS = P (dP - delta),
-// dV^T += dO^T P, dK^T += Q^T dS. grid (nseq * HQ, ceil(max_len / 32)), block 64.
+// Backward, dK and dV of one q head: a workgroup of 4 wavefronts owns 128 consecutive keys (32
+// per wavefront) and walks the 32-query blocks from its first key to the end of the sequence,
+// staging each block's Q and dO (rows and transposed, plus lse and delta) once for the four
+// wavefronts: S = Q K^T, P = exp(S - lse), dP = dO V^T, dS = P (dP - delta), dV^T += dO^T P,
+// dK^T += Q^T dS. A wavefront skips query blocks that lie wholly before its keys.
+// grid (nseq * HQ, ceil(max_len / 128)), block 256.
 // ------------------------------------------------------------------------------------------------
+constexpr int kKeyWaves = 4;
+
 template <int D>
-__global__ __launch_bounds__(64) void attn_dkdv_kernel(Args a) {
-  constexpr int KC = D / 16, DT = D / 32;
+__global__ __launch_bounds__(64 * kKeyWaves) void attn_dkdv_kernel(Args a) {
+  constexpr int KC = D / 16, DT = D / 32, NT = 64 * kKeyWaves;
   __shared__ __align__(16) uint16_t qsm[kTok * D];
   __shared__ __align__(16) uint16_t qt[D * kTok];
   __shared__ __align__(16) uint16_t dsm[kTok * D];
   __shared__ __align__(16) uint16_t dt[D * kTok];
+  __shared__ __align__(16) float lse_s[kTok];
+  __shared__ __align__(16) float dl_s[kTok];
   const int seq = blockIdx.x / a.HQ, h = blockIdx.x % a.HQ;
   const int kvh = h / (a.HQ / a.KH);
-  const int k0 = blockIdx.y * kTok;
+  const int kw0 = blockIdx.y * kTok * kKeyWaves;
   const int start = a.cu[seq], L = a.cu[seq + 1] - start;
-  if (k0 >= L) return;
-  const int lane = threadIdx.x;
+  if (kw0 >= L) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int k0 = kw0 + kTok * wave;
   const int kj = k0 + (lane & 31);
   const bool kok = kj < L;
   const int64_t qs = (int64_t)a.HQ * D, kvs = (int64_t)a.KH * D;
+  const uint16_t* qbase = a.q + (int64_t)start * qs + h * D;
+  const uint16_t* dbase = a.dout + (int64_t)start * qs + h * D;
+  const float* lse = a.lse + (int64_t)h * a.n + start;
+  const float* dl = a.delta + (int64_t)h * a.n + start;
+
+  PairStage<D, kTok, NT> sq, sd;
+  float lv = 0.f;  // threads 0..31: lse of query q0 + tid; 32..63: delta of q0 + tid - 32
+  auto load = [&](int q0) {
+    const int valid = min(kTok, L - q0);
+    sq.load(qbase + (int64_t)q0 * qs, qs, valid, tid);
+    sd.load(dbase + (int64_t)q0 * qs, qs, valid, tid);
+    lv = 0.f;
+    if (tid < 2 * kTok && (tid & (kTok - 1)) < valid)
+      lv = tid < kTok ? lse[q0 + tid] * kLog2e : dl[q0 + tid - kTok];
+  };
+  load(kw0);
 
   half8_t kr[KC], vr[KC];
 #pragma unroll
@@ -397,19 +462,15 @@ __global__ __launch_bounds__(64) void attn_dkdv_kernel(Args a) {
 #pragma unroll
   for (int u = 0; u < DT; ++u) dk[u] = dv[u] = f32x16{};
   const float c = a.scale * kLog2e;
-  const uint16_t* qbase = a.q + (int64_t)start * qs + h * D;
-  const uint16_t* dbase = a.dout + (int64_t)start * qs + h * D;
-  const float* lse = a.lse + (int64_t)h * a.n + start;
-  const float* dl = a.delta + (int64_t)h * a.n + start;
 
-  for (int q0 = k0; q0 < L; q0 += kTok) {
-    const int valid = min(kTok, L - q0);
+  for (int q0 = kw0; q0 < L; q0 += kTok) {
     __syncthreads();
-    stage_rows<D>(qsm, qbase + (int64_t)q0 * qs, qs, kTok, valid, lane, 64);
-    stage_tr<D, kTok>(qt, qbase + (int64_t)q0 * qs, qs, valid, lane, 64);
-    stage_rows<D>(dsm, dbase + (int64_t)q0 * qs, qs, kTok, valid, lane, 64);
-    stage_tr<D, kTok>(dt, dbase + (int64_t)q0 * qs, qs, valid, lane, 64);
+    sq.store(qt, qsm, tid);
+    sd.store(dt, dsm, tid);
+    if (tid < 2 * kTok) (tid < kTok ? lse_s : dl_s)[tid & (kTok - 1)] = lv;
     __syncthreads();
+    if (q0 + kTok < L) load(q0 + kTok);
+    if (q0 + kTok <= k0 || k0 >= L) continue;  // every query of the block precedes these keys
     f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
     for (int kk = 0; kk < KC; ++kk) {
@@ -418,15 +479,19 @@ __global__ __launch_bounds__(64) void attn_dkdv_kernel(Args a) {
       dp = mfma(ld_rm<D>(dsm, row, ch), vr[kk], dp);
     }
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int qq = q0 + acc_row(r, lane);
-      float p = 0.f, d = 0.f;
-      if (qq < L && kj <= qq) {
-        p = exp2f(s[r] * c - lse[qq] * kLog2e);
-        d = dl[qq];
+    for (int j = 0; j < 4; ++j) {
+      const int qr0 = 8 * j + 4 * (lane >> 5);
+      const float4 l4 = *reinterpret_cast<const float4*>(lse_s + qr0);
+      const float4 d4 = *reinterpret_cast<const float4*>(dl_s + qr0);
+      const float lq[4] = {l4.x, l4.y, l4.z, l4.w}, dq4[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 4 * j + i, qq = q0 + qr0 + i;
+        float p = 0.f;
+        if (qq < L && kj <= qq) p = exp2f(s[r] * c - lq[i]);
+        s[r] = p;
+        dp[r] = p * (dp[r] - dq4[i]);
       }
-      s[r] = p;
-      dp[r] = p * (dp[r] - d);
     }
     half8_t pb[2], sb[2];
 #pragma unroll
@@ -462,9 +527,36 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 int check_common(int32_t nseq, int32_t max_len, int64_t n, int32_t HQ, int32_t KH, int32_t D) {
   QLORA_CHECK_ARG(nseq >= 0 && max_len >= 0 && n >= 0);
   QLORA_CHECK_ARG(D == 64 || D == 128);
-  QLORA_CHECK_ARG(HQ > 0 && KH > 0 && HQ % KH == 0 && HQ / KH <= kMaxGroup);
+  QLORA_CHECK_ARG(HQ > 0 && KH > 0 && HQ % KH == 0);
+  const int G = HQ / KH;
+  QLORA_CHECK_ARG(G == 1 || G == 2 || G == 4 || G == 6);
   QLORA_CHECK_ARG((int64_t)nseq * HQ < (1ll << 31));
   return 0;
+}
+
+template <int D, int G, bool DQ>
+void launch_q(const Args& a, dim3 grid, hipStream_t s) {
+  if constexpr (DQ) hipLaunchKernelGGL((attn_dq_kernel<D, G>), grid, dim3(64 * G), 0, s, a);
+  else hipLaunchKernelGGL((attn_fwd_kernel<D, G>), grid, dim3(64 * G), 0, s, a);
+}
+
+template <bool DQ>
+void launch_q_any(const Args& a, int D, int G, dim3 grid, hipStream_t s) {
+  if (D == 128) {
+    switch (G) {
+      case 1: launch_q<128, 1, DQ>(a, grid, s); break;
+      case 2: launch_q<128, 2, DQ>(a, grid, s); break;
+      case 4: launch_q<128, 4, DQ>(a, grid, s); break;
+      default: launch_q<128, 6, DQ>(a, grid, s); break;
+    }
+  } else {
+    switch (G) {
+      case 1: launch_q<64, 1, DQ>(a, grid, s); break;
+      case 2: launch_q<64, 2, DQ>(a, grid, s); break;
+      case 4: launch_q<64, 4, DQ>(a, grid, s); break;
+      default: launch_q<64, 6, DQ>(a, grid, s); break;
+    }
+  }
 }
 
 }  // namespace
@@ -491,10 +583,7 @@ QLORA_API int qlora_attn_fwd(const void* q, const void* k, const void* v, void* 
   a.KH = KH;
   a.scale = scale;
   const dim3 grid((unsigned)(nseq * KH), (unsigned)qlora_cdiv(max_len, kTok));
-  const dim3 block(64 * (HQ / KH));
-  hipStream_t s = (hipStream_t)stream;
-  if (D == 128) hipLaunchKernelGGL(attn_fwd_kernel<128>, grid, block, 0, s, a);
-  else hipLaunchKernelGGL(attn_fwd_kernel<64>, grid, block, 0, s, a);
+  launch_q_any<false>(a, D, HQ / KH, grid, (hipStream_t)stream);
   return qlora_launch_status();
 }
 
@@ -528,13 +617,11 @@ QLORA_API int qlora_attn_bwd(const void* dout, const void* q, const void* k, con
   a.KH = KH;
   a.scale = scale;
   hipStream_t s = (hipStream_t)stream;
-  const unsigned blocks = (unsigned)qlora_cdiv(max_len, kTok);
-  const dim3 g1((unsigned)(nseq * KH), blocks), b1(64 * (HQ / KH));
-  if (D == 128) hipLaunchKernelGGL(attn_dq_kernel<128>, g1, b1, 0, s, a);
-  else hipLaunchKernelGGL(attn_dq_kernel<64>, g1, b1, 0, s, a);
+  const dim3 g1((unsigned)(nseq * KH), (unsigned)qlora_cdiv(max_len, kTok));
+  launch_q_any<true>(a, D, HQ / KH, g1, s);
   if (int rc = qlora_launch_status()) return rc;
-  const dim3 g2((unsigned)(nseq * HQ), blocks), b2(64);
-  if (D == 128) hipLaunchKernelGGL(attn_dkdv_kernel<128>, g2, b2, 0, s, a);
-  else hipLaunchKernelGGL(attn_dkdv_kernel<64>, g2, b2, 0, s, a);
+  const dim3 g2((unsigned)(nseq * HQ), (unsigned)qlora_cdiv(max_len, kTok * kKeyWaves));
+  if (D == 128) hipLaunchKernelGGL(attn_dkdv_kernel<128>, g2, dim3(64 * kKeyWaves), 0, s, a);
+  else hipLaunchKernelGGL(attn_dkdv_kernel<64>, g2, dim3(64 * kKeyWaves), 0, s, a);
   return qlora_launch_status();
 }
