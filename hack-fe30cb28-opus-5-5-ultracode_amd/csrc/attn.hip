@@ -96,7 +96,9 @@ __device__ __forceinline__ half8_t ld_g(const uint16_t* p) {
 
 // Staging of token-major global rows into LDS tiles, split into a load phase (all of a thread's
 // global loads issued back to back into registers, so their latencies overlap, and early enough
-// to hide behind the previous tile's MFMAs) and a store phase into the tile.
+// to hide behind the previous tile's MFMAs) and a store phase into the tile. The loads are
+// unconditional (rows past `valid` read row 0 of the block, then are zeroed): a load under a
+// branch is fenced by a wait for every load before it.
 //
 // RowStage: rows [0, ROWS) of a token-major matrix (row stride `stride` elements) into a
 // [ROWS][D] tile; rows >= valid are zero.
@@ -109,9 +111,10 @@ struct RowStage {
 #pragma unroll
     for (int i = 0; i < CNT; ++i) {
       const int id = tid + i * NT, row = id / CPR, c = id % CPR;
-      r[i] = make_uint4(0, 0, 0, 0);
-      if (id < TOTAL && row < valid)
-        r[i] = *reinterpret_cast<const uint4*>(base + (int64_t)row * stride + c * 8);
+      const bool ok = id < TOTAL && row < valid;
+      const uint4 x =
+          *reinterpret_cast<const uint4*>(base + (int64_t)(ok ? row : 0) * stride + c * 8);
+      r[i] = ok ? x : make_uint4(0, 0, 0, 0);
     }
   }
   __device__ __forceinline__ void store(uint16_t* tile, int tid) const {
@@ -139,12 +142,13 @@ struct PairStage {
 #pragma unroll
     for (int i = 0; i < CNT; ++i) {
       const int id = tid + i * NT, c = id % CPR, r0 = 2 * (id / CPR);
-      x[i] = y[i] = make_uint4(0, 0, 0, 0);
-      if (id < TOTAL) {
-        if (r0 < valid) x[i] = *reinterpret_cast<const uint4*>(base + (int64_t)r0 * stride + c * 8);
-        if (r0 + 1 < valid)
-          y[i] = *reinterpret_cast<const uint4*>(base + (int64_t)(r0 + 1) * stride + c * 8);
-      }
+      const bool ok0 = id < TOTAL && r0 < valid, ok1 = id < TOTAL && r0 + 1 < valid;
+      const uint4 a =
+          *reinterpret_cast<const uint4*>(base + (int64_t)(ok0 ? r0 : 0) * stride + c * 8);
+      const uint4 b =
+          *reinterpret_cast<const uint4*>(base + (int64_t)(ok1 ? r0 + 1 : 0) * stride + c * 8);
+      x[i] = ok0 ? a : make_uint4(0, 0, 0, 0);
+      y[i] = ok1 ? b : make_uint4(0, 0, 0, 0);
     }
   }
   __device__ __forceinline__ void store(uint16_t* tr, uint16_t* rows, int tid) const {
@@ -227,12 +231,13 @@ __global__ __launch_bounds__(64 * G) void attn_fwd_kernel(Args a) {
   sv.load(vbase, kvs, min(kKB, L), tid);
 
   half8_t qr[KC];
+  {
+    const uint16_t* p = a.q + (int64_t)(start + (qok ? qi : 0)) * qs + h * D + 8 * (lane >> 5);
 #pragma unroll
-  for (int kk = 0; kk < KC; ++kk) qr[kk] = half8_t{};
-  if (qok) {
-    const uint16_t* p = a.q + (int64_t)(start + qi) * qs + h * D + 8 * (lane >> 5);
-#pragma unroll
-    for (int kk = 0; kk < KC; ++kk) qr[kk] = ld_g(p + 16 * kk);
+    for (int kk = 0; kk < KC; ++kk) {
+      const half8_t x = ld_g(p + 16 * kk);
+      qr[kk] = qok ? x : half8_t{};
+    }
   }
   f32x16 o[DT];
 #pragma unroll
@@ -338,21 +343,23 @@ __global__ __launch_bounds__(64 * G) void attn_dq_kernel(Args a) {
   sv.load(vbase, kvs, min(KB, L), tid);
 
   half8_t qr[KC], dr[KC];
-#pragma unroll
-  for (int kk = 0; kk < KC; ++kk) qr[kk] = dr[kk] = half8_t{};
-  float dpart = 0.f, lse2 = __builtin_inff();  // out-of-range queries: P = 0
-  if (qok) {
-    const int64_t off = (int64_t)(start + qi) * qs + h * D + 8 * (lane >> 5);
+  float dpart = 0.f;
+  const int qc = qok ? qi : 0;
+  {
+    const int64_t off = (int64_t)(start + qc) * qs + h * D + 8 * (lane >> 5);
 #pragma unroll
     for (int kk = 0; kk < KC; ++kk) {
-      qr[kk] = ld_g(a.q + off + 16 * kk);
-      dr[kk] = ld_g(a.dout + off + 16 * kk);
+      const half8_t x = ld_g(a.q + off + 16 * kk), y = ld_g(a.dout + off + 16 * kk);
+      qr[kk] = qok ? x : half8_t{};
+      dr[kk] = qok ? y : half8_t{};
       const half8_t ov = ld_g(a.o + off + 16 * kk);
 #pragma unroll
       for (int i = 0; i < 8; ++i) dpart += (float)dr[kk][i] * (float)ov[i];
     }
-    lse2 = a.lse[(int64_t)h * a.n + start + qi] * kLog2e;
   }
+  // out-of-range queries: lse2 = inf makes P = 0
+  const float lse_q = a.lse[(int64_t)h * a.n + start + qc];
+  const float lse2 = qok ? lse_q * kLog2e : __builtin_inff();
   const float delta = dpart + __shfl_xor(dpart, 32, 64);
   if (qok && lane < 32) a.delta[(int64_t)h * a.n + start + qi] = delta;
 
@@ -441,21 +448,21 @@ __global__ __launch_bounds__(64 * kKeyWaves) void attn_dkdv_kernel(Args a) {
     const int valid = min(kTok, L - q0);
     sq.load(qbase + (int64_t)q0 * qs, qs, valid, tid);
     sd.load(dbase + (int64_t)q0 * qs, qs, valid, tid);
-    lv = 0.f;
-    if (tid < 2 * kTok && (tid & (kTok - 1)) < valid)
-      lv = tid < kTok ? lse[q0 + tid] * kLog2e : dl[q0 + tid - kTok];
+    const int j = tid & (kTok - 1);
+    const bool ok = tid < 2 * kTok && j < valid;
+    const float x = (tid < kTok ? lse : dl)[q0 + (ok ? j : 0)];
+    lv = ok ? (tid < kTok ? x * kLog2e : x) : 0.f;
   };
   load(kw0);
 
   half8_t kr[KC], vr[KC];
-#pragma unroll
-  for (int kk = 0; kk < KC; ++kk) kr[kk] = vr[kk] = half8_t{};
-  if (kok) {
-    const int64_t off = (int64_t)(start + kj) * kvs + kvh * D + 8 * (lane >> 5);
+  {
+    const int64_t off = (int64_t)(start + (kok ? kj : 0)) * kvs + kvh * D + 8 * (lane >> 5);
 #pragma unroll
     for (int kk = 0; kk < KC; ++kk) {
-      kr[kk] = ld_g(a.k + off + 16 * kk);
-      vr[kk] = ld_g(a.v + off + 16 * kk);
+      const half8_t x = ld_g(a.k + off + 16 * kk), y = ld_g(a.v + off + 16 * kk);
+      kr[kk] = kok ? x : half8_t{};
+      vr[kk] = kok ? y : half8_t{};
     }
   }
   f32x16 dk[DT], dv[DT];

@@ -49,22 +49,26 @@ def _nf4_args(w):
 
 
 def _plan(M, N, Kr, mode, epi, w_rows, w_cols, swiglu_I):
-    """(tile, splits): 256 x 256 tiles when they fill the 256 CUs, else 256 x 128, and split-K
-    for long reductions that still leave CUs idle."""
+    """(tile, splits): 256 x 256 tiles (tile 0) when they alone give at least one workgroup per
+    CU (256), else 128 x 128 (tile 1); split-K when even those leave CUs idle on a long
+    reduction."""
     def ok(bn):
         if mode == 0:
             return swiglu_I % (bn // 2) == 0 if epi == 3 else w_rows % bn == 0
         return w_cols % bn == 0
-    m_tiles = -(-M // 256)
-    tile = 0 if ok(256) and m_tiles * (N // 256 if epi != 3 else N // 128) >= 256 else 1
-    if not ok(128 if tile == 1 else 256):
+
+    def tiles(bm):
+        return -(-M // bm) * (N // (bm // 2) if epi == 3 else N // bm)
+
+    # NN 256 x 256 runs out of registers (spills), so the backward products use 128 x 128
+    tile = 0 if mode == 0 and ok(256) and tiles(256) >= 256 else 1
+    if not ok(256 if tile == 0 else 128):
         raise ValueError("W shape not supported by the fused GEMM tiles")
-    n_tiles = (N // (128 if tile == 0 else 64)) if epi == 3 else N // (256 if tile == 0 else 128)
-    tiles = m_tiles * n_tiles
+    n = tiles(256 if tile == 0 else 128)
     splits = 1
     ktiles = Kr // 64
-    if epi != 3 and tiles < 192:
-        while splits < 4 and tiles * splits * 2 <= 320 and ktiles // (splits * 2) >= 16:
+    if epi != 3:
+        while splits < 8 and n * splits < 192 and ktiles // (splits * 2) >= 8:
             splits *= 2
     return tile, splits
 

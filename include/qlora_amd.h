@@ -160,7 +160,7 @@ int qlora_ce_finish(const float* state, const int32_t* best_idx, const float* xt
  *   epi 3 (mode 0, SwiGLU): W = [gate; up] with gate rows [0, I) and up rows [I, 2I);
  *          C f16 [M, I] = f16(silu(f16 g) * f16 u), I = swiglu_I.
  *   a_f32: A is f32 and is rounded to f16 as it is loaded.
- *   tile: 0 = 256x256 output tiles, 1 = 256x128. splits > 1: split-K, the partial sums go
+ *   tile: 0 = 256x256 output tiles (8 wavefronts), 1 = 128x128 (4 wavefronts). splits > 1: split-K, the partial sums go
  *         through the caller's fp32 workspace ws (>= splits*M*N elements) and a reduce kernel
  *         applies the epilogue (not with epi 3).
  * The decoded weight values are bit-identical to qlora_nf4_dequant's.

@@ -96,6 +96,10 @@ def test_epilogues(pkg):
     mm = L.nf4_gemm(x, gu_w, 0, epi=3, swiglu_I=8960)
     gu = L.nf4_gemm(x, gu_w, 0)
     assert torch.equal(mm, pkg.ops._glu_fwd(gu, 8960))
+    for tile in (0, 1):  # both tile shapes (gate and up rows are placed per wavefront)
+        mm = L.nf4_gemm(x, gu_w, 0, epi=3, swiglu_I=8960, tile=tile, splits=1)
+        gu = L.nf4_gemm(x, gu_w, 0, tile=tile, splits=1)
+        assert torch.equal(mm, pkg.ops._glu_fwd(gu, 8960))
     # fp32 A rounded to fp16 on load
     a32 = torch.randn(M, 1536, generator=g, device=DEV)
     assert torch.equal(L.nf4_gemm(a32, wd, 1), L.nf4_gemm(a32.half(), wd, 1))
