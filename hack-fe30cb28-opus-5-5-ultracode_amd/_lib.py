@@ -22,8 +22,8 @@ SIGNATURES = {
     "qlora_dropout_keep": [P, I64, I64, I64, I64, F32, I32, P],
     "qlora_rms_fwd": [P, P, P, I32, P, P, P, P, P, P, I64, I64, F32, F32, F32, I64, I64, I64,
                       I64, I32, I32, I32, I32, I32, P],
-    "qlora_rms_bwd": [P, P, P, P, P, P, I32, P, P, P, I64, I64, I64, F32, F32, I64, I64, I64,
-                      I64, F32, I32, I32, I32, I32, P],
+    "qlora_rms_bwd": [P, P, P, P, P, P, I32, P, P, P, P, I64, I64, I64, F32, F32, I64, I64,
+                      I64, I64, F32, I32, I32, I32, I32, P],
     "qlora_rope_fwd": [P, P, P, P, P, I64, P, P, P, P, I64, I32, I32, I32, I32, F32, P],
     "qlora_rope_bwd": [P, P, P, P, P, I64, P, P, I64, I32, I32, I32, I32, P],
     "qlora_glu_fwd": [P, P, I64, I64, P],
@@ -33,6 +33,7 @@ SIGNATURES = {
     "qlora_ce_finish": [P, P, P, P, P, P, P, P, P, P, I64, I64, I64, P],
     "qlora_nf4_gemm": [P, I64, I32, P, P, P, P, P, P, I32, I32, I32, I32, I64, I64, I64, I64,
                        P, I64, P, P, I64, I64, I32, I32, I64, I32, I32, P, I64, P],
+    "qlora_resid_add": [P, P, P, I64, P],
     "qlora_attn_fwd": [P, P, P, P, P, P, I32, I32, I64, I32, I32, I32, F32, P],
     "qlora_attn_bwd": [P, P, P, P, P, P, P, P, P, P, P, I32, I32, I64, I32, I32, I32, F32, P],
 }

@@ -116,3 +116,28 @@ QLORA_API int qlora_glu_bwd(const void* dm, void* gu, int64_t n, int64_t I, void
                        static_cast<const uint16_t*>(dm), static_cast<uint16_t*>(gu), n, I);
   return qlora_launch_status();
 }
+
+// out = a + fp32(d): the residual add after a projection whose fp16 output d is added to the fp32
+// residual stream (engine.py:1048-1051, h3 = h2 + d). 4 elements per thread.
+__global__ __launch_bounds__(256) void resid_add_kernel(const float* a, const uint16_t* d,
+                                                        float* out, int64_t n4) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n4) return;
+  const float4 x = reinterpret_cast<const float4*>(a)[i];
+  const uint2 y = reinterpret_cast<const uint2*>(d)[i];
+  reinterpret_cast<float4*>(out)[i] =
+      make_float4(x.x + lo_h(y.x), x.y + hi_h(y.x), x.z + lo_h(y.y), x.w + hi_h(y.y));
+}
+
+QLORA_API int qlora_resid_add(const float* a, const void* d, float* out, int64_t numel,
+                              void* stream) {
+  QLORA_CHECK_ARG(numel >= 0);
+  if (numel == 0) return 0;
+  QLORA_CHECK_ARG(a && d && out && numel % 4 == 0);
+  QLORA_CHECK_ARG(((uintptr_t)a & 15) == 0 && ((uintptr_t)out & 15) == 0 &&
+                  ((uintptr_t)d & 7) == 0);
+  const int64_t n4 = numel / 4;
+  hipLaunchKernelGGL(resid_add_kernel, dim3((unsigned)qlora_cdiv(n4, 256)), dim3(256), 0,
+                     (hipStream_t)stream, a, static_cast<const uint16_t*>(d), out, n4);
+  return qlora_launch_status();
+}

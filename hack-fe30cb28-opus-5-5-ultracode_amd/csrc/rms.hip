@@ -40,6 +40,7 @@ struct RmsBwdArgs {
   const void* w;
   const float* dres;  // fp32 [n, H] or null
   float* dx;
+  uint16_t* dx16;     // fp16 copy of dx [n, H] or null (the next product's fp16 operand)
   const int64_t* tok;
   int64_t n, H, dy_stride;
   float keep_scale, grad_scale;
@@ -222,6 +223,10 @@ __global__ __launch_bounds__(kWave* kRowsPerBlock) void rms_bwd_kernel(RmsBwdArg
       for (int k = 0; k < W; ++k) dx[k] += r[k];
     }
     store_f32<W>(a.dx + base + c * W, dx);
+    if (a.dx16) {
+#pragma unroll
+      for (int k = 0; k < W; ++k) a.dx16[base + c * W + k] = f2h_bits(dx[k]);
+    }
   }
 }
 
@@ -327,7 +332,7 @@ QLORA_API int qlora_rms_fwd(const float* x, const void* delta, const void* w, in
 
 QLORA_API int qlora_rms_bwd(const void* dy, const void* tq, const void* tv, const float* x,
                             const float* rstd, const void* w, int32_t w_half, const float* dres,
-                            float* dx, const int64_t* tok, int64_t n, int64_t H,
+                            float* dx, void* dx16, const int64_t* tok, int64_t n, int64_t H,
                             int64_t dy_stride, float p_keep, float keep_scale, int64_t seed,
                             int64_t ctr_q, int64_t ctr_v, int64_t G, float grad_scale,
                             int32_t drop_q, int32_t drop_v, int32_t has_res, int32_t vec,
@@ -342,7 +347,8 @@ QLORA_API int qlora_rms_bwd(const void* dy, const void* tq, const void* tv, cons
   RmsBwdArgs a{static_cast<const uint16_t*>(dy), drop_q ? static_cast<const uint16_t*>(tq)
                                                         : nullptr,
                drop_v ? static_cast<const uint16_t*>(tv) : nullptr, x, rstd, w,
-               has_res ? dres : nullptr, dx, (drop_q || drop_v) ? tok : nullptr, n, H,
+               has_res ? dres : nullptr, dx, static_cast<uint16_t*>(dx16),
+               (drop_q || drop_v) ? tok : nullptr, n, H,
                dy_stride, keep_scale, grad_scale, (uint64_t)ctr_q, (uint64_t)ctr_v,
                make_drop(seed, G, p_keep, vec), w_half};
   const bool v4 = H % 4 == 0 && dy_stride % 4 == 0 && aligned(dy, 8) && aligned(x, 16) &&

@@ -183,6 +183,7 @@ class Packed:
         self.drop_seed = self.drop_threads = None
         self.drop_vec = dropout.vec if dropout is not None else 4
         self.lora16_views = None
+        self.grad16 = None  # (dh, fp16(dh)) handed from a layer's backward to the one below
 
     def lora16(self, index, weights):
         if self.lora16_views is not None:
@@ -264,13 +265,24 @@ class _Layer(torch.autograd.Function):
     def backward(ctx, dh3):
         h, aq_w, bq_w, av_w, bv_w = ctx.saved_tensors
         spec, packed, seeds = ctx.spec, ctx.packed, ctx.seeds
+        with L.reuse_dequant():  # qkv, o, gate|up: one dequant for the recompute and dY W
+            return _Layer._backward(ctx, dh3, h, aq_w, bq_w, av_w, bv_w, spec, packed, seeds)
+
+    @staticmethod
+    def _backward(ctx, dh3, h, aq_w, bq_w, av_w, bv_w, spec, packed, seeds):
         s = _lora_scale(spec)
         n, H = h.shape
         D, HQ, HKV = spec.D, spec.HQ, spec.HKV
         C = (HQ + 2 * HKV) * D
         dh3 = dh3.contiguous()
+        # the fp16 copy of this gradient written by the layer above's norm backward, when the
+        # gradient is that very tensor; else it is rounded on load (dY.to(fp16) W)
+        g16 = packed.grad16
+        dh3_16 = g16[1] if g16 is not None and g16[0] is dh3 else dh3
+        packed.grad16 = None
         lora16 = packed.lora16(spec.index, (aq_w, bq_w, av_w, bv_w))
-        dm = L.nf4_linear_t(dh3, spec.w["down_proj"])  # fp32 dh3 rounded to fp16 on load
+        dm = L.nf4_linear_t(dh3_16, spec.w["down_proj"])
+        del dh3_16
         if ctx.kept is not None:
             f, ctx.kept = ctx.kept, None
         else:
@@ -281,9 +293,12 @@ class _Layer(torch.autograd.Function):
         del dm
         db = L.nf4_linear_t(gu, spec.gu)
         del gu
-        dh2 = _rms_bwd(spec, db, f.pop("h2"), f.pop("rstd2"), spec.ln2, packed, dres=dh3)
+        dh2_16 = torch.empty((n, H), device=h.device, dtype=torch.float16)
+        dh2 = _rms_bwd(spec, db, f.pop("h2"), f.pop("rstd2"), spec.ln2, packed, dres=dh3,
+                       out16=dh2_16)
         del db, dh3
-        dout = L.nf4_linear_t(dh2, spec.w["o_proj"]).view(n, HQ, D)
+        dout = L.nf4_linear_t(dh2_16, spec.w["o_proj"]).view(n, HQ, D)
+        del dh2_16
         dq, dk, dv = _attn_bwd(dout, f.pop("q"), f.pop("k"), f.pop("v"), f.pop("out"),
                                f.pop("lse"), f.pop("aseed"), f.pop("aoffset"), packed,
                                spec.scale)
@@ -305,8 +320,10 @@ class _Layer(torch.autograd.Function):
         del dqkv
         dh = None
         if need_dh:
+            dh16 = torch.empty((n, H), device=h.device, dtype=torch.float16)
             dh = _rms_bwd(spec, da, h, f["rstd1"], spec.ln1, packed, dres=dh2,
-                          tq=grads["q"][2], tv=grads["v"][2], seeds=seeds)
+                          tq=grads["q"][2], tv=grads["v"][2], seeds=seeds, out16=dh16)
+            packed.grad16 = (dh, dh16)
         return (dh, None, None, None, grads["q"][0], grads["q"][1], grads["v"][0],
                 grads["v"][1])
 

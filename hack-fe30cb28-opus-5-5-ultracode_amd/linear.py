@@ -12,7 +12,7 @@ fp16 buffer, then hipBLASLt through torch - the reference's own structure (dequa
 import torch
 
 from . import _lib
-from .ops import NF4Group, _need, _ptr, _stream, dequant
+from .ops import NF4Group, _need, _ptr, _resid_add, _stream, dequant
 
 BACKEND = "dequant"
 _NO_SEG = 2**63 - 1
@@ -22,10 +22,34 @@ def _weights(w):
     return w.weights if isinstance(w, NF4Group) else [w]
 
 
+_REUSE = None
+
+
+class reuse_dequant:
+    """Within this context each NF4 weight is dequantized once and its fp16 copy reused (a
+    layer's backward multiplies by the same weights in its recompute and in its dY W products);
+    the copies are dropped on exit."""
+
+    def __enter__(self):
+        global _REUSE
+        self.prev, _REUSE = _REUSE, {}
+        return self
+
+    def __exit__(self, *exc):
+        global _REUSE
+        _REUSE = self.prev
+        return False
+
+
 def dequantize(w):
     """fp16 [N, K] of an NF4Weight or NF4Group (one launch for a group)."""
+    if _REUSE is not None and w in _REUSE:
+        return _REUSE[w]
     ws = _weights(w)
-    return dequant(ws, ws[0].packed.device)
+    out = dequant(ws, ws[0].packed.device)
+    if _REUSE is not None:
+        _REUSE[w] = out
+    return out
 
 
 def _shape(w):
@@ -144,7 +168,7 @@ def nf4_linear_resid(x, w, resid, out=None):
     """fp32 resid + fp16(X W^T) (the layer output h2 + d)."""
     if BACKEND == "fused":
         return nf4_gemm(x, w, 0, epi=2, resid=resid, out=out)
-    return torch.add(resid, nf4_linear(x, w), out=out)
+    return _resid_add(resid, nf4_linear(x, w), out=out)
 
 
 def nf4_linear_t(dy, w):

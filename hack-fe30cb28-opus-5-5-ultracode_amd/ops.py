@@ -316,8 +316,10 @@ def _rms_fwd(spec, x, weight, packed, *, delta=None, write_y=True, seeds=(0, 0),
 
 
 def _rms_bwd(spec, dy, x, rstd, weight, packed, *, dres=None, tq=None, tv=None, seeds=(0, 0),
-             grad_scale=1.0, out=None):
-    """RMSNorm backward with the LoRA-dropout gradients merged (engine.py:969-981)."""
+             grad_scale=1.0, out=None, out16=None):
+    """RMSNorm backward with the LoRA-dropout gradients merged (engine.py:969-981). With out16
+    (fp16 [n, H]) the kernel also writes fp16(dx) there, the operand the next backward product
+    rounds the gradient to."""
     _need(x, "x", torch.float32)
     n, H = x.shape
     dev = x.device
@@ -335,13 +337,17 @@ def _rms_bwd(spec, dy, x, rstd, weight, packed, *, dres=None, tq=None, tv=None, 
             raise ValueError("dres must match x")
     dx = out if out is not None else torch.empty_like(x)
     _need(dx, "out", torch.float32, dev)
+    if out16 is not None:
+        _need(out16, "out16", torch.float16, dev)
+        if out16.shape != x.shape:
+            raise ValueError("out16 must match x")
     if n:
         tok, p_keep, keep_scale, seed, ctr_q, ctr_v, threads = _dropout_args(packed, x, seeds)
         vec = getattr(packed, "drop_vec", 4)
         if tq is not None or tv is not None:
             _need(tok, "packed.tok", torch.int64, dev)
         _lib.call("qlora_rms_bwd", _ptr(dy), _ptr(tq), _ptr(tv), _ptr(x), _ptr(rstd),
-                  _ptr(weight), w_half, _ptr(dres), _ptr(dx),
+                  _ptr(weight), w_half, _ptr(dres), _ptr(dx), _ptr(out16),
                   _ptr(tok) if (tq is not None or tv is not None) else None, n, H, dy_stride,
                   p_keep, keep_scale, int(seed), int(ctr_q), int(ctr_v), int(threads),
                   float(grad_scale), int(tq is not None), int(tv is not None),
@@ -404,6 +410,24 @@ def _rope_bwd(spec, dq, dk, dv, packed):
         _lib.call("qlora_rope_bwd", _ptr(dq), _ptr(dk), _ptr(dv), _ptr(cos), _ptr(sin),
                   cos.shape[0], _ptr(pos), _ptr(dqkv), n, HQ, HKV, D, kh, _stream(dev))
     return dqkv
+
+
+def _resid_add(a, d, out=None):
+    """a + fp32(d) (fp32 residual stream plus an fp16 projection output; engine.py:1048-1051)."""
+    _need(a, "a", torch.float32)
+    _need(d, "d", torch.float16, a.device)
+    if d.shape != a.shape:
+        raise ValueError("d must match a")
+    out = torch.empty_like(a) if out is None else out
+    _need(out, "out", torch.float32, a.device)
+    if out.shape != a.shape:
+        raise ValueError("out must match a")
+    n = a.numel()
+    if n % 4:
+        raise ValueError("numel must be a multiple of 4")
+    if n:
+        _lib.call("qlora_resid_add", _ptr(a), _ptr(d), _ptr(out), n, _stream(a.device))
+    return out
 
 
 # ---------------------------------------------------------------------------------------------

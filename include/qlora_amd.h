@@ -74,11 +74,13 @@ int qlora_rms_fwd(const float* x, const void* delta, const void* w, int32_t w_ha
  * RMSNorm backward: g = w * (dy + keep_q * tq * keep_scale + keep_v * tv * keep_scale),
  * dx = [dres +] grad_scale * rstd * (g - xhat * mean(g * xhat)), xhat = x * rstd.
  * Replaces rms_bwd_kernel (kernels.py:178-205) <- _rms_bwd (engine.py:969-981).
- *   dy f16 [n, dy_stride]; tq, tv f16 [n,H]; x f32 [n,H]; rstd f32 [n]; dres, dx f32 [n,H]
+ *   dy f16 [n, dy_stride]; tq, tv f16 [n,H]; x f32 [n,H]; rstd f32 [n]; dres, dx f32 [n,H];
+ *   dx16 (optional, may be null) f16 [n,H] = fp16(dx), the operand of the next dY W product
+ *   (engine.py:1238 and 1301 round the gradient to fp16 before it).
  */
 int qlora_rms_bwd(const void* dy, const void* tq, const void* tv, const float* x,
                   const float* rstd, const void* w, int32_t w_half, const float* dres, float* dx,
-                  const int64_t* tok, int64_t n, int64_t H, int64_t dy_stride, float p_keep,
+                  void* dx16, const int64_t* tok, int64_t n, int64_t H, int64_t dy_stride, float p_keep,
                   float keep_scale, int64_t seed, int64_t ctr_q, int64_t ctr_v, int64_t G,
                   float grad_scale, int32_t drop_q, int32_t drop_v, int32_t has_res,
                   int32_t vec, void* stream);
@@ -178,6 +180,12 @@ int qlora_nf4_gemm(const void* a, int64_t lda, int32_t a_f32, const void* packed
                    int64_t w_cols, void* c, int64_t ldc, const void* bias, const float* resid,
                    int64_t ldr, int64_t M, int32_t mode, int32_t epi, int64_t swiglu_I,
                    int32_t tile, int32_t splits, float* ws, int64_t ws_elems, void* stream);
+
+/*
+ * out = a + fp32(d) over numel elements (a, out f32; d f16; numel % 4 == 0; out may alias a):
+ * the residual add after the down projection, h3 = h2 + d (engine.py:1048-1051, 1179).
+ */
+int qlora_resid_add(const float* a, const void* d, float* out, int64_t numel, void* stream);
 
 /*
  * Causal attention within each packed sequence (flash attention, online softmax), grouped-query

@@ -202,6 +202,25 @@ def test_rms_forward_backward(pkg, n, H, wdtype):
     dx2 = pkg.ops._rms_bwd(_Spec, wide[:, :H], xsum, rstd, w.to(DEV), packed, dres=dres.to(DEV),
                            tq=tq.to(DEV), tv=tv.to(DEV), seeds=ctrs, grad_scale=0.5)
     assert torch.equal(dx, dx2) or (dx - dx2).abs().max() < 1e-6
+    # the optional fp16 copy is exactly fp16(dx) (RNE), dx itself unchanged
+    dx16 = torch.empty(n, H, dtype=torch.float16, device=DEV)
+    dx3 = pkg.ops._rms_bwd(_Spec, dy.to(DEV), xsum, rstd, w.to(DEV), packed, dres=dres.to(DEV),
+                           tq=tq.to(DEV), tv=tv.to(DEV), seeds=ctrs, grad_scale=0.5, out16=dx16)
+    assert torch.equal(dx3, dx)
+    assert torch.equal(dx16.view(torch.int16), dx.half().view(torch.int16))
+
+
+@pytest.mark.parametrize("numel", [4, 1536 * 37, 2560 * 1536])
+def test_resid_add(pkg, numel):
+    """h3 = h2 + fp32(d) bit-exact (engine.py:1048-1051); in place too."""
+    g = torch.Generator(device=DEV).manual_seed(numel)
+    a = torch.randn(numel, generator=g, device=DEV)
+    d = torch.randn(numel, generator=g, device=DEV).half()
+    out = pkg.ops._resid_add(a, d)
+    assert torch.equal(out, a + d.float())
+    b = a.clone()
+    pkg.ops._resid_add(b, d, out=b)
+    assert torch.equal(b, out)
 
 
 @pytest.mark.parametrize("kv_heads", [None, 2])
