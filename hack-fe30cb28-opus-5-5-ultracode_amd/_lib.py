@@ -67,14 +67,18 @@ def load():
     return lib
 
 
+_FNS = {}
+
+
 def call(name, *args):
     """Call entry point `name`; raise RuntimeError on a non-zero return code."""
-    lib = load()
-    hook = HOOKS.get(name)
-    fn = getattr(lib, name)
+    fn = _FNS.get(name)
+    if fn is None:
+        fn = _FNS[name] = getattr(load(), name)
+    hook = HOOKS.get(name) if HOOKS else None
     rc = hook.call(fn, args) if hook is not None else fn(*args)
     if rc != 0:
-        msg = lib.qlora_error_string(rc).decode(errors="replace")
+        msg = load().qlora_error_string(rc).decode(errors="replace")
         raise RuntimeError(f"{name} failed: hipError {rc} ({msg})")
     return rc
 

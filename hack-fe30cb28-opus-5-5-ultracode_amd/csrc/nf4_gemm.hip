@@ -180,10 +180,11 @@ struct BLoaderNT {
 // register budget per SIMD.
 template <int BN, int NT>
 struct BLoaderNN {
-  static constexpr int CW = 4;
-  static constexpr int CHUNKS = BN / CW;  // column groups per row
-  static_assert(CHUNKS * 8 == NT, "one 8 x 4 block per thread");
-  uint32_t v[4];   // row i's two bytes in half i & 1 of v[i / 2]
+  static constexpr int CW = 8 * BN / NT;   // columns per thread: 4 or 8
+  static constexpr int CHUNKS = BN / CW;   // column groups per row
+  static_assert(CW == 4 || CW == 8, "8 rows x 4 or 8 columns per thread");
+  static constexpr int VR = CW == 8 ? 8 : 4;  // registers of packed bytes
+  uint32_t v[VR];  // CW == 4: row i's two bytes in half i & 1 of v[i / 2]; CW == 8: row i
   uint32_t q[2];   // nested: absmax code of row i in byte i & 3 of q[i / 4]
   float a2[8];     // nested: absmax2; plain: the fp32 absmax
   uint32_t seg;    // 2 bits per row
@@ -194,14 +195,15 @@ struct BLoaderNN {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int64_t e = (k0 + 8 * gr + i) * g.Kw + n0 + CW * c;
-      vv[i] = *reinterpret_cast<const uint16_t*>(g.w.packed + (e >> 1));
+      if constexpr (CW == 8) vv[i] = *reinterpret_cast<const uint32_t*>(g.w.packed + (e >> 1));
+      else vv[i] = *reinterpret_cast<const uint16_t*>(g.w.packed + (e >> 1));
       const ScaleIn si = scale_load(g.w, e >> g.w.bs1_shift);
       qq[i] = si.q;
       a2[i] = si.a2;
       seg |= si.seg << (2 * i);
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = vv[2 * i] | (vv[2 * i + 1] << 16);
+    for (int i = 0; i < VR; ++i) v[i] = CW == 8 ? vv[i] : (vv[2 * i] | (vv[2 * i + 1] << 16));
 #pragma unroll
     for (int i = 0; i < 2; ++i)
       q[i] = qq[4 * i] | (qq[4 * i + 1] << 8) | (qq[4 * i + 2] << 16) | (qq[4 * i + 3] << 24);
@@ -219,7 +221,7 @@ struct BLoaderNN {
         const float scale = scale_of(
             ScaleIn{(q[i >> 2] >> (8 * (i & 3))) & 0xFFu, a2[i], (seg >> (2 * i)) & 3u},
             g.w.nested, c2, offs);
-        const uint32_t row = (v[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
+        const uint32_t row = CW == 8 ? v[i] : ((v[i >> 1] >> (16 * (i & 1))) & 0xFFFFu);
 #pragma unroll
         for (int k = 0; k < CW / 2; ++k) {
           const uint32_t byte = (row >> (8 * k)) & 0xFFu;
@@ -402,28 +404,28 @@ using namespace qlora;
 
 namespace {
 
-template <int BM, int BN, bool NN, int EPI, bool A_F32>
+template <int BM, int BN, int WGN, bool NN, int EPI, bool A_F32>
 void launch_gemm(const GemmArgs& g, dim3 grid, hipStream_t s) {
-  constexpr int WGM = 2, WGN = BM == 256 ? 4 : 2;
+  constexpr int WGM = 2;
   hipLaunchKernelGGL((nf4_gemm_kernel<BM, BN, WGM, WGN, NN, EPI, A_F32>), grid,
                      dim3(WGM * WGN * 64), 0, s, g);
 }
 
-template <int BM, int BN, bool NN, int EPI>
+template <int BM, int BN, int WGN, bool NN, int EPI>
 void launch_a(const GemmArgs& g, dim3 grid, hipStream_t s, bool a_f32) {
-  if (a_f32) launch_gemm<BM, BN, NN, EPI, true>(g, grid, s);
-  else launch_gemm<BM, BN, NN, EPI, false>(g, grid, s);
+  if (a_f32) launch_gemm<BM, BN, WGN, NN, EPI, true>(g, grid, s);
+  else launch_gemm<BM, BN, WGN, NN, EPI, false>(g, grid, s);
 }
 
-template <int BM, int BN, bool NN>
+template <int BM, int BN, int WGN, bool NN>
 void launch_epi(const GemmArgs& g, dim3 grid, hipStream_t s, bool a_f32, int epi) {
   switch (epi) {
-    case kEpiStore: launch_a<BM, BN, NN, kEpiStore>(g, grid, s, a_f32); break;
-    case kEpiBias: launch_a<BM, BN, NN, kEpiBias>(g, grid, s, a_f32); break;
-    case kEpiResid: launch_a<BM, BN, NN, kEpiResid>(g, grid, s, a_f32); break;
-    case kEpiPartial: launch_a<BM, BN, NN, kEpiPartial>(g, grid, s, a_f32); break;
+    case kEpiStore: launch_a<BM, BN, WGN, NN, kEpiStore>(g, grid, s, a_f32); break;
+    case kEpiBias: launch_a<BM, BN, WGN, NN, kEpiBias>(g, grid, s, a_f32); break;
+    case kEpiResid: launch_a<BM, BN, WGN, NN, kEpiResid>(g, grid, s, a_f32); break;
+    case kEpiPartial: launch_a<BM, BN, WGN, NN, kEpiPartial>(g, grid, s, a_f32); break;
     default:
-      if constexpr (!NN) launch_a<BM, BN, NN, kEpiSwiglu>(g, grid, s, a_f32);
+      if constexpr (!NN) launch_a<BM, BN, WGN, NN, kEpiSwiglu>(g, grid, s, a_f32);
       break;
   }
 }
@@ -434,7 +436,7 @@ bool al(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 
 // mode: 0 = NT (C = A W^T), 1 = NN (C = A W). epi: 0 store fp16, 1 + bias, 2 fp32 residual,
 // 3 SwiGLU (NT only). a_f32: A is fp32 (rounded to fp16 on load). tile: 0 = 256 x 256
-// (8 wavefronts), 1 = 128 x 128 (4 wavefronts). splits > 1: split-K through `ws` (fp32, splits * M * N elements).
+// (8 wavefronts), 1 = 128 x 128 (4 wavefronts), 2 = 256 x 256 (4 wavefronts of 128 x 128). splits > 1: split-K through `ws` (fp32, splits * M * N elements).
 QLORA_API int qlora_nf4_gemm(const void* a, int64_t lda, int32_t a_f32, const void* packed,
                              const void* absmax, const float* code2, const float* absmax2,
                              const float* offsets, const float* code, int32_t nested,
@@ -447,14 +449,14 @@ QLORA_API int qlora_nf4_gemm(const void* a, int64_t lda, int32_t a_f32, const vo
   if (M == 0) return 0;
   QLORA_CHECK_ARG(a && packed && absmax && c && (mode == 0 || mode == 1));
   QLORA_CHECK_ARG(epi >= 0 && epi <= 3 && !(epi == 3 && mode != 0));
-  QLORA_CHECK_ARG(tile == 0 || tile == 1);
+  QLORA_CHECK_ARG(tile >= 0 && tile <= 2);
   QLORA_CHECK_ARG(splits >= 1 && splits <= 16 && !(splits > 1 && epi == 3));
   QLORA_CHECK_ARG(bs1 >= 32 && (bs1 & (bs1 - 1)) == 0);
   QLORA_CHECK_ARG(!nested || (code2 && absmax2 && offsets && bs2 > 0 && (bs2 & (bs2 - 1)) == 0));
   QLORA_CHECK_ARG(standard || code);
   QLORA_CHECK_ARG(epi != 1 || bias);
   QLORA_CHECK_ARG(epi != 2 || (resid && ldr >= 0));
-  const int BM = tile == 0 ? 256 : 128, BN = BM;
+  const int BM = tile == 1 ? 128 : 256, BN = BM;
   int64_t N, Kr;
   if (mode == 0) {
     Kr = w_cols;
@@ -495,11 +497,13 @@ QLORA_API int qlora_nf4_gemm(const void* a, int64_t lda, int32_t a_f32, const vo
   hipStream_t s = (hipStream_t)stream;
   const dim3 gdim((unsigned)grid, 1, (unsigned)splits);
   if (mode == 0) {
-    if (tile == 0) launch_epi<256, 256, false>(g, gdim, s, a_f32, kepi);
-    else launch_epi<128, 128, false>(g, gdim, s, a_f32, kepi);
+    if (tile == 0) launch_epi<256, 256, 4, false>(g, gdim, s, a_f32, kepi);
+    else if (tile == 1) launch_epi<128, 128, 2, false>(g, gdim, s, a_f32, kepi);
+    else launch_epi<256, 256, 2, false>(g, gdim, s, a_f32, kepi);
   } else {
-    if (tile == 0) launch_epi<256, 256, true>(g, gdim, s, a_f32, kepi);
-    else launch_epi<128, 128, true>(g, gdim, s, a_f32, kepi);
+    if (tile == 0) launch_epi<256, 256, 4, true>(g, gdim, s, a_f32, kepi);
+    else if (tile == 1) launch_epi<128, 128, 2, true>(g, gdim, s, a_f32, kepi);
+    else launch_epi<256, 256, 2, true>(g, gdim, s, a_f32, kepi);
   }
   int rc = qlora_launch_status();
   if (rc != 0 || splits == 1) return rc;

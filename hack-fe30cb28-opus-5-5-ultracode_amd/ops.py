@@ -23,7 +23,9 @@ def _ptr(t):
 
 
 def _stream(device):
-    return torch.cuda.current_stream(device).cuda_stream
+    """torch's current HIP stream on `device` (raw handle, as the C-ABI takes it)."""
+    return torch._C._cuda_getCurrentRawStream(
+        device.index if device.index is not None else torch.cuda.current_device())
 
 
 def _need(t, name, dtype=None, device=None, contiguous=True):
@@ -88,15 +90,18 @@ class NF4Weight:
             self.absmax = qs.absmax.float().contiguous()
             self.code2 = self.absmax2 = self.offset = self.absmax
             self.bs2 = 1
+        self._args = _dequant_args(self.packed, self.absmax, self.code2, self.absmax2,
+                                   self.offset, self.code, self.blocks, self.nested,
+                                   self.standard, self.bs1, self.bs2, _NO_SEG, _NO_SEG,
+                                   self.numel)
 
     @property
     def blocks(self):
         return self.numel // self.bs1
 
     def dequant_into(self, out):
-        _launch_dequant(self.packed, self.absmax, self.code2, self.absmax2, self.offset,
-                        self.code, out, self.blocks, self.nested, self.standard, self.bs1,
-                        self.bs2, _NO_SEG, _NO_SEG, self.numel)
+        _launch_dequant(self._args, out, self.blocks, self.nested, self.standard, self.bs1,
+                        self.bs2, _NO_SEG, _NO_SEG, self.numel, self.packed.device)
         return out
 
 
@@ -142,20 +147,22 @@ class NF4Group:
             self.absmax2 = self.offsets = self.absmax
         for w in weights:
             w.group = self
+        self._args = _dequant_args(self.packed, self.absmax, self.code2, self.absmax2,
+                                   self.offsets, self.code, self.blocks, self.nested,
+                                   self.standard, self.bs1, self.bs2, self.seg1, self.seg2,
+                                   self.numel)
 
     def dequant_into(self, out):
-        _launch_dequant(self.packed, self.absmax, self.code2, self.absmax2, self.offsets,
-                        self.code, out, self.blocks, self.nested, self.standard, self.bs1,
-                        self.bs2, self.seg1, self.seg2, self.numel)
+        _launch_dequant(self._args, out, self.blocks, self.nested, self.standard, self.bs1,
+                        self.bs2, self.seg1, self.seg2, self.numel, self.packed.device)
         return out
 
 
-def _launch_dequant(packed, absmax, code2, absmax2, offsets, code, out, blocks, nested,
-                    standard, bs1, bs2, seg1, seg2, numel):
-    dev = out.device
-    _need(out, "out", torch.float16, contiguous=True)
-    if out.numel() != numel:
-        raise ValueError(f"out has {out.numel()} elements, the weight {numel}")
+def _dequant_args(packed, absmax, code2, absmax2, offsets, code, blocks, nested, standard, bs1,
+                  bs2, seg1, seg2, numel):
+    """Checks a weight's quantization state once and returns the qlora_nf4_dequant arguments
+    that do not change between launches (everything but the output and the stream)."""
+    dev = packed.device
     _need(packed, "packed", torch.uint8, dev, contiguous=False)
     if packed.numel() * 2 != numel or not packed.is_contiguous():
         raise ValueError("packed must hold numel / 2 contiguous bytes")
@@ -172,12 +179,18 @@ def _launch_dequant(packed, absmax, code2, absmax2, offsets, code, out, blocks, 
         _need(code, "code", torch.float32, dev)
         if code.numel() != 16:
             raise ValueError("code must have 16 entries")
+    return (_ptr(packed), _ptr(absmax), _ptr(code2) if nested else None,
+            _ptr(absmax2) if nested else None, _ptr(offsets) if nested else None, _ptr(code))
+
+
+def _launch_dequant(args, out, blocks, nested, standard, bs1, bs2, seg1, seg2, numel, dev):
+    if out.dtype != torch.float16 or out.device != dev or not out.is_contiguous() \
+            or out.numel() != numel:
+        raise ValueError(f"out must be a contiguous fp16 tensor of {numel} elements on {dev}")
     if blocks == 0:
         return
-    _lib.call("qlora_nf4_dequant", _ptr(packed), _ptr(absmax),
-              _ptr(code2) if nested else None, _ptr(absmax2) if nested else None,
-              _ptr(offsets) if nested else None, _ptr(code), _ptr(out), blocks, int(nested),
-              int(standard), bs1, bs2, seg1, seg2, _stream(dev))
+    _lib.call("qlora_nf4_dequant", *args, _ptr(out), blocks, int(nested), int(standard), bs1,
+              bs2, seg1, seg2, _stream(dev))
 
 
 def dequant(weights, device):

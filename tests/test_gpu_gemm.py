@@ -96,7 +96,7 @@ def test_epilogues(pkg):
     mm = L.nf4_gemm(x, gu_w, 0, epi=3, swiglu_I=8960)
     gu = L.nf4_gemm(x, gu_w, 0)
     assert torch.equal(mm, pkg.ops._glu_fwd(gu, 8960))
-    for tile in (0, 1):  # both tile shapes (gate and up rows are placed per wavefront)
+    for tile in (0, 1, 2):  # every tile shape (gate and up rows are placed per wavefront)
         mm = L.nf4_gemm(x, gu_w, 0, epi=3, swiglu_I=8960, tile=tile, splits=1)
         gu = L.nf4_gemm(x, gu_w, 0, tile=tile, splits=1)
         assert torch.equal(mm, pkg.ops._glu_fwd(gu, 8960))
@@ -127,7 +127,7 @@ def test_mlp_up_path_config2(pkg):
         assert rel_err(got.cpu(), want) < 1e-3
 
 
-@pytest.mark.parametrize("tile,splits", [(0, 1), (1, 1), (0, 3), (1, 2)])
+@pytest.mark.parametrize("tile,splits", [(0, 1), (1, 1), (2, 1), (0, 3), (1, 2), (2, 2)])
 @pytest.mark.parametrize("mode", [0, 1])
 def test_every_tile_and_split(pkg, tile, splits, mode):
     """Each compiled tile shape and split-K setting (forced) against fp64, with the residual and
