@@ -131,8 +131,12 @@ def main():
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--keep-all", action="store_true",
-                    help="keep every layer's intermediates instead of recomputing")
+    ap.add_argument("--policy", choices=("plan", "recompute", "keep"), default="plan",
+                    help="which layers keep their intermediates for the backward: the "
+                         "reference's memory-cap plan under this GPU's memory (default; every "
+                         "layer keeps them on 288 GB), none (full per-layer recompute) or all")
+    ap.add_argument("--recompute-steps", type=int, default=10,
+                    help="also time this many steps with full per-layer recompute (0: skip)")
     ap.add_argument("--layers", type=int, default=28)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -146,7 +150,7 @@ def main():
     torch.cuda.manual_seed(0)
     cfg = pkg.engine.Qwen2Config(num_hidden_layers=args.layers)
     model = pkg.engine.random_qwen2(cfg, dev, seed=0)
-    model.keep_all = args.keep_all
+    model.keep_all = {"plan": None, "recompute": False, "keep": True}[args.policy]
     trainer = Trainer(model)
     batches = make_batches(args.warmup + args.steps + 1, cfg.vocab_size, device=dev)
     print(f"[bench] model built; warmup {args.warmup}", file=sys.stderr, flush=True)
@@ -166,6 +170,26 @@ def main():
     value = tokens / elapsed
     print(f"[bench] {args.steps} steps {elapsed:.3f} s, {value:.0f} tokens/s", file=sys.stderr,
           flush=True)
+    kept = model.keep_plan(batches[-1][4])
+    recompute = None
+    if args.recompute_steps > 0 and model.keep_all is not False:
+        # the same step with every layer recomputing its forward in backward
+        saved, model.keep_all = model.keep_all, False
+        for i in range(2):
+            trainer.step(batches[i])
+        torch.cuda.synchronize()
+        rtok, t1 = 0, time.perf_counter()
+        for i in range(args.recompute_steps):
+            b = batches[(args.warmup + i) % (len(batches) - 1)]
+            trainer.step(b)
+            rtok += b[4]
+        torch.cuda.synchronize()
+        rel = time.perf_counter() - t1
+        recompute = {"value": rtok / rel, "ms_per_step": 1000.0 * rel / args.recompute_steps,
+                     "steps": args.recompute_steps}
+        model.keep_all = saved
+        print(f"[bench] full recompute: {recompute['value']:.0f} tokens/s", file=sys.stderr,
+              flush=True)
     roof = measure_kernel(pkg, trainer, batches[-1], pkg.profiling.DOMINANT)
     result = {
         "metric": "train tokens/s (1.5B NF4 QLoRA step, 1 GPU); NF4 dequant HBM GB/s",
@@ -175,8 +199,12 @@ def main():
         "data": "synthetic (random token ids, random-init Qwen2.5-1.5B NF4 weights)",
         "config": {"workload": "config 5: full Qwen2.5-1.5B NF4+LoRA training step",
                    "batch": "4 packed sequences, lengths U[256,1024]",
-                   "tokens": tokens, "recompute": not args.keep_all,
-                   "layers": args.layers, "parallelism": "single GPU"},
+                   "tokens": tokens, "layers": args.layers, "parallelism": "single GPU",
+                   "activations": (f"kept for the backward by {kept} of {args.layers} layers "
+                                   "(the reference's memory-cap plan, engine.py:1626-1640, "
+                                   "under this GPU's memory); the others recompute their "
+                                   "forward")},
+        "full_recompute": recompute,
         "loss_first_last": [losses[0], losses[-1]],
         "roofline": roof,
     }

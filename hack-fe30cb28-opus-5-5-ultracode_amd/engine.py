@@ -389,11 +389,18 @@ class _Head(torch.autograd.Function):
 # The model
 # ---------------------------------------------------------------------------------------------
 class FusedQwen2:
-    """The step of a Qwen2 NF4 + LoRA model (engine.py:1568-1922 without the offload planner)."""
+    """The step of a Qwen2 NF4 + LoRA model (engine.py:1568-1922 without the host offload).
+
+    Which layers keep their intermediates for the backward instead of recomputing their forward
+    follows the reference's memory-cap plan (keep_plan, engine.py:1626-1640): the last layers
+    keep everything as long as the step's predicted peak stays under the cap. The default cap is
+    the GPU's memory (less a margin), under which every layer of a 1.5B step keeps its
+    intermediates; `keep_all` True/False forces one policy for every layer."""
 
     HEAD_CHUNK = 4096  # rows of logits alive at a time (4096 x 151936 fp16 = 1.2 GB)
+    CAP_MARGIN = 8 * 2**30  # bytes of device memory the default cap leaves free
 
-    def __init__(self, cfg, layers, embed, norm_w, device, keep_all=False):
+    def __init__(self, cfg, layers, embed, norm_w, device, keep_all=None):
         self.cfg = cfg
         self.layers = layers
         self.embed = embed
@@ -402,6 +409,7 @@ class FusedQwen2:
         self.eps = cfg.rms_norm_eps
         self.device = torch.device(device)
         self.keep_all = keep_all
+        self.memory_cap = None
         self.dropout_p = cfg.lora_dropout
         self.rope = RopeTable(cfg.rope_theta, cfg.head_dim, self.device)
         self.dropout = TorchDropout(self.device, torch.float32) if self.dropout_p > 0 else None
@@ -420,6 +428,37 @@ class FusedQwen2:
     def parameters(self):
         return list(self.lora_fp32)
 
+    def set_memory_cap(self, cap_bytes):
+        """The step may keep activations as long as its predicted peak stays under this
+        (engine.py:1626-1628); None = the device's memory less CAP_MARGIN."""
+        self.memory_cap = cap_bytes
+
+    def kept_bytes_per_layer(self, n):
+        """Device bytes one layer's kept intermediates take for n tokens: the fp16 LoRA inputs
+        (2 H), q/k/v and the attention output ((2 HQ + 2 HKV) D), the fp32 residual after
+        attention (H), [gate | up] (2 I), the log-sum-exp and the two rstd."""
+        spec = self.layers[0]
+        per_token = (2 * spec.H * 2 + (2 * spec.HQ + 2 * spec.HKV) * spec.D * 2 + spec.H * 4
+                     + 2 * spec.I * 2 + spec.HQ * 4 + 2 * 4 + 2 * 16 * 2)
+        return n * per_token
+
+    def keep_plan(self, n):
+        """The number of last layers that keep every intermediate for a step of n tokens: as
+        many as fit under the memory cap above what is allocated now plus one recomputing
+        layer's working set (its dequantized weights and per-token buffers)."""
+        if self.keep_all is not None:
+            return len(self.layers) if self.keep_all else 0
+        cap = self.memory_cap
+        if cap is None:
+            cap = torch.cuda.get_device_properties(self.device).total_memory - self.CAP_MARGIN
+        spec = self.layers[0]
+        weights = 2 * spec.H * ((spec.HQ + 2 * spec.HKV) * spec.D + spec.HQ * spec.D
+                                + 3 * spec.I)
+        work = weights + 64 * 2**20 + n * 96 * 1024 + n * self.cfg.vocab_size * 2
+        free = cap - torch.cuda.memory_allocated(self.device) - work
+        per_layer = max(1, self.kept_bytes_per_layer(n))
+        return int(max(0, min(len(self.layers), free // per_layer)))
+
     def step(self, input_ids, attention_mask, labels, denom):
         """The step's forward: (loss, packed, stats); autograd runs the backward."""
         packed = Packed(input_ids, attention_mask, labels, self.rope, self.dropout,
@@ -434,8 +473,10 @@ class FusedQwen2:
             torch._foreach_copy_(self.lora_views, [t.detach() for t in self.lora_fp32])
         packed.lora16_views = self.lora16_by_layer
         h = torch.nn.functional.embedding(packed.ids, self.embed).float()
-        for spec in self.layers:
-            h = _Layer.apply(h, spec, packed, self.keep_all, *spec.lora_params())
+        keep_from = len(self.layers) - self.keep_plan(packed.n)
+        packed.keep_all_from = keep_from
+        for i, spec in enumerate(self.layers):
+            h = _Layer.apply(h, spec, packed, i >= keep_from, *spec.lora_params())
         stats = HeadStats()
         loss = _Head.apply(h, self.norm_w, self.eps, self.lm_w, packed, denom, stats,
                            self.HEAD_CHUNK)

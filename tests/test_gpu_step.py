@@ -70,13 +70,29 @@ def _batch(lengths, vocab, prompt=3, seed=0):
 
 
 @pytest.mark.parametrize("lengths,keep_all", [([17, 60, 33, 5], False), ([4], False),
-                                              ([40, 40], True)])
+                                              ([40, 40], True), ([17, 60, 33, 5], None),
+                                              ([17, 60, 33, 5], "mixed")])
 def test_step_matches_oracle(pkg, lengths, keep_all):
     """Loss and LoRA gradients of one GPU step equal the CPU oracle's (fp32 autograd with the
     same NF4 bytes and dropout masks) within the reference's whole-step tolerance; the CUDA
-    generator advances exactly as the base's 2 x layers dropout calls would."""
+    generator advances exactly as the base's 2 x layers dropout calls would. keep_all: every
+    layer recomputes (False), keeps (True), the memory-cap plan (None: all keep), or a cap that
+    admits exactly one kept layer ("mixed": layer 0 recomputes, layer 1 keeps)."""
     model = _tiny(pkg)
-    model.keep_all = keep_all
+    if keep_all == "mixed":
+        model.keep_all = None
+        n = sum(lengths)
+        spec = model.layers[0]
+        weights = 2 * spec.H * ((spec.HQ + 2 * spec.HKV) * spec.D + spec.HQ * spec.D
+                                + 3 * spec.I)
+        work = weights + 64 * 2**20 + n * 96 * 1024 + n * model.cfg.vocab_size * 2
+        model.set_memory_cap(torch.cuda.memory_allocated() + work
+                             + int(1.5 * model.kept_bytes_per_layer(n)))
+        assert model.keep_plan(n) == 1
+    else:
+        model.keep_all = keep_all
+        if keep_all is None:
+            assert model.keep_plan(sum(lengths)) == len(model.layers)
     cpu = OS.CpuQwen2(model)
     ids, mask, labels = _batch(lengths, model.cfg.vocab_size)
     denom = float((labels[:, 1:] != -100).sum())
