@@ -1,38 +1,88 @@
 // Standalone NF4 -> fp16 dequantisation (reference: nf4_dequant_kernel, kernels.py:68-105;
-// launched by NF4Weight.dequant_into / NF4Group.dequant_into, engine.py:103-157).
+// launched by NF4Weight.dequant_into / NF4Group.dequant_into, engine.py:103-157, and by
+// dequant(), engine.py:683-694, for several weights at once).
 //
 // HBM-bound: per 8 output values one 32-bit word of nibbles is read and 16 bytes are written.
-// Each thread handles WPT words spaced a workgroup apart, so every load and every 16-byte store
-// instruction of a wavefront covers one contiguous span (256 B in, 1 KiB out). The 16 levels
-// sit in LDS; the per-block scale comes from the (L1/L2-resident) absmax tables.
+// One launch covers up to kMaxJobs weights (a layer's qkv, o, gate|up and down: 23 MB read and
+// 94 MB written per launch), so the launch cost and the tail of one weight overlap the next.
+// Each thread handles kWPT words spaced a workgroup apart: every load and every 16-byte store instruction of a wavefront covers one contiguous
+// span (256 B in, 1 KiB out). All loads are unconditional (indices clamped, results masked), so
+// a thread's loads issue back to back. The 16 levels and the 256-entry double-quant code sit in
+// LDS; the per-block absmax byte and absmax2 are shared by the 8 consecutive lanes of a block.
 #include "nf4.h"
 
 namespace qlora {
 
 constexpr int kDequantThreads = 256;
-constexpr int kDequantWPT = 4;
+constexpr int kWPT = 8;  // words per thread
+constexpr int kTileWords = kDequantThreads * kWPT;
+constexpr int kMaxJobs = 4;
 
-__global__ __launch_bounds__(kDequantThreads) void nf4_dequant_kernel(NF4Ref w, uint4* out,
-                                                                       int64_t n_words) {
+struct DequantJob {
+  NF4Ref w;
+  uint4* out;
+  int64_t n_words;
+};
+
+struct DequantBatch {
+  DequantJob job[kMaxJobs];
+  int64_t first_tile[kMaxJobs + 1];  // workgroup ranges of the jobs
+  int count;
+};
+
+__global__ __launch_bounds__(kDequantThreads) void nf4_dequant_kernel(DequantBatch b) {
   __shared__ float lut[16];
-  if (threadIdx.x < 16)
-    lut[threadIdx.x] = w.standard ? kNF4Levels[threadIdx.x] : w.code[threadIdx.x];
-  __syncthreads();
-  const uint32_t* words = reinterpret_cast<const uint32_t*>(w.packed);
-  const int64_t base = (int64_t)blockIdx.x * (kDequantThreads * kDequantWPT) + threadIdx.x;
-  uint32_t v[kDequantWPT];
+  __shared__ float c2[256];
+  __shared__ float offs[3];
+  int j = 0;
 #pragma unroll
-  for (int i = 0; i < kDequantWPT; ++i) {
-    const int64_t idx = base + i * kDequantThreads;
-    v[i] = idx < n_words ? __builtin_nontemporal_load(words + idx) : 0u;
+  for (int k = 1; k < kMaxJobs; ++k)
+    j += (k < b.count && (int64_t)blockIdx.x >= b.first_tile[k]);
+  const DequantJob& job = b.job[j];
+  const NF4Ref& w = job.w;
+  const int t = threadIdx.x;
+  if (t < 16) lut[t] = w.standard ? kNF4Levels[t] : w.code[t];
+  if (w.nested) {
+    c2[t] = w.code2[t];  // 256 threads, 256 entries
+    if (t < 3) {
+      const int nseg = 1 + (int)(w.seg1 != INT64_MAX) + (int)(w.seg2 != INT64_MAX);
+      offs[t] = w.offsets[t < nseg ? t : 0];
+    }
+  }
+  __syncthreads();
+
+  const uint32_t* words = reinterpret_cast<const uint32_t*>(w.packed);
+  const int64_t base = ((int64_t)blockIdx.x - b.first_tile[j]) * kTileWords + t;
+  const int64_t last = job.n_words - 1;
+  const int wshift = w.bs1_shift - 3;  // words per block = bs1 / 8
+  uint32_t v[kWPT], q[kWPT];
+  float a2[kWPT];
+#pragma unroll
+  for (int i = 0; i < kWPT; ++i) {
+    int64_t idx = base + i * kDequantThreads;
+    idx = idx < last ? idx : last;
+    v[i] = __builtin_nontemporal_load(words + idx);
+    const int64_t blk = idx >> wshift;
+    if (w.nested) {
+      q[i] = static_cast<const uint8_t*>(w.absmax)[blk];
+      a2[i] = w.absmax2[blk >> w.bs2_shift];
+    } else {
+      q[i] = 0;
+      a2[i] = static_cast<const float*>(w.absmax)[blk];
+    }
   }
 #pragma unroll
-  for (int i = 0; i < kDequantWPT; ++i) {
+  for (int i = 0; i < kWPT; ++i) {
     const int64_t idx = base + i * kDequantThreads;
-    if (idx < n_words) {
-      const float scale = nf4_block_scale(w, idx >> (w.bs1_shift - 3));
-      out[idx] = nf4_decode_word(v[i], scale, lut);
+    float scale = a2[i];
+    if (w.nested) {
+      const int64_t blk = idx >> wshift;
+      float prod = c2[q[i]] * a2[i];  // rounded before the offset is added (bitsandbytes)
+      fp32_barrier(prod);
+      scale = prod + offs[(int)(blk >= w.seg1) + (int)(blk >= w.seg2)];
     }
+    const uint4 r = nf4_decode_word(v[i], scale, lut);
+    if (idx <= last) job.out[idx] = r;
   }
 }
 
@@ -40,24 +90,82 @@ __global__ __launch_bounds__(kDequantThreads) void nf4_dequant_kernel(NF4Ref w, 
 
 using namespace qlora;
 
-QLORA_API int qlora_nf4_dequant(const void* packed, const void* absmax, const float* code2,
-                                const float* absmax2, const float* offsets, const float* code,
-                                void* out, int64_t n_blocks, int32_t nested, int32_t standard,
-                                int32_t bs1, int32_t bs2, int64_t seg1, int64_t seg2,
-                                void* stream) {
+namespace {
+
+int make_job(DequantJob& job, const void* packed, const void* absmax, const float* code2,
+             const float* absmax2, const float* offsets, const float* code, void* out,
+             int64_t n_blocks, int32_t nested, int32_t standard, int32_t bs1, int32_t bs2,
+             int64_t seg1, int64_t seg2) {
   QLORA_CHECK_ARG(n_blocks >= 0);
-  if (n_blocks == 0) return 0;
+  job = DequantJob{};
+  if (n_blocks == 0) return 0;  // nothing to read or write: no other argument is looked at
   QLORA_CHECK_ARG(packed && absmax && out);
   QLORA_CHECK_ARG(bs1 >= 8 && (bs1 & (bs1 - 1)) == 0);
   QLORA_CHECK_ARG(!nested || (code2 && absmax2 && offsets && bs2 > 0 && (bs2 & (bs2 - 1)) == 0));
   QLORA_CHECK_ARG(standard || code);
   QLORA_CHECK_ARG(((uintptr_t)packed & 3) == 0 && ((uintptr_t)out & 15) == 0);
-  NF4Ref w{static_cast<const uint8_t*>(packed), absmax, code2, absmax2, offsets, code,
-           seg1, seg2, __builtin_ctz(bs1), nested ? __builtin_ctz(bs2) : 0, nested, standard};
-  const int64_t n_words = n_blocks * (bs1 / 8);
-  const int64_t grid = qlora_cdiv(n_words, (int64_t)kDequantThreads * kDequantWPT);
-  QLORA_CHECK_ARG(grid < (1ll << 31));
-  hipLaunchKernelGGL(nf4_dequant_kernel, dim3((unsigned)grid), dim3(kDequantThreads), 0,
-                     (hipStream_t)stream, w, static_cast<uint4*>(out), n_words);
+  job.w = NF4Ref{static_cast<const uint8_t*>(packed), absmax, code2, absmax2, offsets, code,
+                 seg1, seg2, __builtin_ctz(bs1), nested ? __builtin_ctz(bs2) : 0, nested,
+                 standard};
+  job.out = static_cast<uint4*>(out);
+  job.n_words = n_blocks * (bs1 / 8);
+  return 0;
+}
+
+int launch(DequantBatch& b, hipStream_t stream) {
+  // drop empty jobs, then lay the workgroups of the rest end to end
+  int k = 0;
+  for (int i = 0; i < b.count; ++i)
+    if (b.job[i].n_words > 0) b.job[k++] = b.job[i];
+  b.count = k;
+  if (k == 0) return 0;
+  int64_t tiles = 0;
+  for (int i = 0; i < k; ++i) {
+    b.first_tile[i] = tiles;
+    tiles += qlora_cdiv(b.job[i].n_words, kTileWords);
+  }
+  for (int i = k; i <= kMaxJobs; ++i) b.first_tile[i] = tiles;
+  QLORA_CHECK_ARG(tiles < (1ll << 31));
+  hipLaunchKernelGGL(nf4_dequant_kernel, dim3((unsigned)tiles), dim3(kDequantThreads), 0,
+                     stream, b);
   return qlora_launch_status();
+}
+
+}  // namespace
+
+QLORA_API int qlora_nf4_dequant(const void* packed, const void* absmax, const float* code2,
+                                const float* absmax2, const float* offsets, const float* code,
+                                void* out, int64_t n_blocks, int32_t nested, int32_t standard,
+                                int32_t bs1, int32_t bs2, int64_t seg1, int64_t seg2,
+                                void* stream) {
+  DequantBatch b{};
+  b.count = 1;
+  if (int rc = make_job(b.job[0], packed, absmax, code2, absmax2, offsets, code, out, n_blocks,
+                        nested, standard, bs1, bs2, seg1, seg2))
+    return rc;
+  return launch(b, (hipStream_t)stream);
+}
+
+// Up to four weights in one launch: argument arrays of length `count`, entry i as in
+// qlora_nf4_dequant.
+QLORA_API int qlora_nf4_dequant_many(int32_t count, const void* const* packed,
+                                     const void* const* absmax, const float* const* code2,
+                                     const float* const* absmax2, const float* const* offsets,
+                                     const float* const* code, void* const* out,
+                                     const int64_t* n_blocks, const int32_t* nested,
+                                     const int32_t* standard, const int32_t* bs1,
+                                     const int32_t* bs2, const int64_t* seg1,
+                                     const int64_t* seg2, void* stream) {
+  QLORA_CHECK_ARG(count >= 0 && count <= kMaxJobs);
+  QLORA_CHECK_ARG(count == 0 || (packed && absmax && code2 && absmax2 && offsets && code &&
+                                 out && n_blocks && nested && standard && bs1 && bs2 && seg1 &&
+                                 seg2));
+  DequantBatch b{};
+  b.count = count;
+  for (int i = 0; i < count; ++i)
+    if (int rc = make_job(b.job[i], packed[i], absmax[i], code2[i], absmax2[i], offsets[i],
+                          code[i], out[i], n_blocks[i], nested[i], standard[i], bs1[i], bs2[i],
+                          seg1[i], seg2[i]))
+      return rc;
+  return launch(b, (hipStream_t)stream);
 }

@@ -69,6 +69,7 @@ class LayerSpec:
         self.w = {name: NF4Weight(p) for name, p in nf4.items()}
         self.qkv = NF4Group.of([self.w["q_proj"], self.w["k_proj"], self.w["v_proj"]])
         self.gu = NF4Group.of([self.w["gate_proj"], self.w["up_proj"]])
+        self.nf4_all = [self.qkv, self.w["o_proj"], self.gu, self.w["down_proj"]]
         self.bias_qkv = bias_qkv
         self.lora = lora  # {"q": (A, B, scaling), "v": (A, B, scaling)}
 
@@ -245,6 +246,12 @@ class _Layer(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, h, spec, packed, keep_all, aq_w, bq_w, av_w, bv_w):
+        with L.reuse_dequant():  # the layer's four weights in one dequant launch
+            L.dequant_layer(spec.nf4_all)
+            return _Layer._forward(ctx, h, spec, packed, keep_all, aq_w, bq_w, av_w, bv_w)
+
+    @staticmethod
+    def _forward(ctx, h, spec, packed, keep_all, aq_w, bq_w, av_w, bv_w):
         drop = packed.dropout is not None
         seeds = (packed.draw(spec.H) if drop else 0, packed.draw(spec.H) if drop else 0)
         lora16 = packed.lora16(spec.index, (aq_w, bq_w, av_w, bv_w))
@@ -265,7 +272,8 @@ class _Layer(torch.autograd.Function):
     def backward(ctx, dh3):
         h, aq_w, bq_w, av_w, bv_w = ctx.saved_tensors
         spec, packed, seeds = ctx.spec, ctx.packed, ctx.seeds
-        with L.reuse_dequant():  # qkv, o, gate|up: one dequant for the recompute and dY W
+        with L.reuse_dequant():  # one dequant launch for the recompute and the dY W products
+            L.dequant_layer(spec.nf4_all)
             return _Layer._backward(ctx, dh3, h, aq_w, bq_w, av_w, bv_w, spec, packed, seeds)
 
     @staticmethod

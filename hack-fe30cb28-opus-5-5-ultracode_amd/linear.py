@@ -12,7 +12,7 @@ fp16 buffer, then hipBLASLt through torch - the reference's own structure (dequa
 import torch
 
 from . import _lib
-from .ops import NF4Group, _need, _ptr, _resid_add, _stream, dequant
+from .ops import NF4Group, _need, _ptr, _resid_add, _stream, dequant, dequant_many
 
 BACKEND = "dequant"
 _NO_SEG = 2**63 - 1
@@ -39,6 +39,17 @@ class reuse_dequant:
         global _REUSE
         _REUSE = self.prev
         return False
+
+
+def dequant_layer(weights):
+    """Dequantize the given weights (at most four: a layer's qkv, o, gate|up, down) in one
+    launch into the active reuse_dequant context, where the layer's products then find them."""
+    if _REUSE is None or BACKEND != "dequant":
+        return
+    todo = [w for w in weights if w not in _REUSE]
+    if todo:
+        for w, out in zip(todo, dequant_many(todo, todo[0].packed.device)):
+            _REUSE[w] = out
 
 
 def dequantize(w):

@@ -193,6 +193,42 @@ def _launch_dequant(args, out, blocks, nested, standard, bs1, bs2, seg1, seg2, n
               bs2, seg1, seg2, _stream(dev))
 
 
+def _dq_segs(w):
+    return (w.seg1, w.seg2) if isinstance(w, NF4Group) else (_NO_SEG, _NO_SEG)
+
+
+def _dq_shape(w):
+    if isinstance(w, NF4Group):
+        return sum(x.shape[0] for x in w.weights), w.weights[0].shape[1]
+    return w.shape
+
+
+def dequant_many(items, device):
+    """fp16 [N_i, K_i] of each NF4Weight / NF4Group of `items` (at most 4), all in one launch
+    (a layer's qkv, o, gate|up and down)."""
+    import ctypes
+    if not 1 <= len(items) <= 4:
+        raise ValueError("dequant_many takes 1 to 4 weights")
+    outs = [torch.empty(_dq_shape(w), device=device, dtype=torch.float16) for w in items]
+    device = outs[0].device  # "cuda" -> "cuda:<current>"
+    for w in items:
+        if w.packed.device != device:
+            raise ValueError(f"weight on {w.packed.device}, expected {device}")
+    k = len(items)
+    P = ctypes.c_void_p * k
+    args = [P(*[w._args[i] for w in items]) for i in range(6)]
+    segs = [_dq_segs(w) for w in items]
+    _lib.call("qlora_nf4_dequant_many", k, *args, P(*[o.data_ptr() for o in outs]),
+              (ctypes.c_int64 * k)(*[w.blocks for w in items]),
+              (ctypes.c_int32 * k)(*[int(w.nested) for w in items]),
+              (ctypes.c_int32 * k)(*[int(w.standard) for w in items]),
+              (ctypes.c_int32 * k)(*[w.bs1 for w in items]),
+              (ctypes.c_int32 * k)(*[w.bs2 for w in items]),
+              (ctypes.c_int64 * k)(*[s[0] for s in segs]),
+              (ctypes.c_int64 * k)(*[s[1] for s in segs]), _stream(device))
+    return outs
+
+
 def dequant(weights, device):
     """Dequantize one or more [n_i, K] weights stacked into one fp16 [sum n_i, K] buffer
     (engine.py:683-694): one launch when they form an NF4Group."""

@@ -14,7 +14,7 @@ HBM_PEAK_GBS = 8000.0
 FP16_PEAK_TFLOPS = 2500.0
 
 # the kernel reported as the step's roofline entry
-DOMINANT = "qlora_nf4_dequant"
+DOMINANT = "qlora_nf4_dequant_many"
 
 
 def _dequant_bytes(args):
@@ -32,8 +32,20 @@ def _dequant_bytes(args):
     return b
 
 
+def _dequant_many_bytes(args):
+    """The same, summed over the weights of one qlora_nf4_dequant_many launch."""
+    k = args[0]
+    total = 0
+    for i in range(k):
+        n_blocks, nested, bs1, bs2 = args[8][i], args[9][i], args[11][i], args[12][i]
+        seg1, seg2 = args[13][i], args[14][i]
+        total += _dequant_bytes([None] * 7 + [n_blocks, nested, None, bs1, bs2, seg1, seg2])
+    return total
+
+
 WORK = {
     "qlora_nf4_dequant": ("hbm", _dequant_bytes),
+    "qlora_nf4_dequant_many": ("hbm", _dequant_many_bytes),
 }
 
 

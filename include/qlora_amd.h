@@ -153,6 +153,19 @@ int qlora_ce_finish(const float* state, const int32_t* best_idx, const float* xt
                     int64_t H, void* stream);
 
 /*
+ * Up to four weights in one launch (a layer's qkv, o, gate|up and down): arrays of `count`
+ * entries, entry i exactly the arguments of one qlora_nf4_dequant call (pointer arrays and
+ * value arrays live in host memory; the pointers they hold are device pointers).
+ * Replaces the per-weight launches of dequant() (engine.py:683-694) for a whole layer.
+ */
+int qlora_nf4_dequant_many(int32_t count, const void* const* packed, const void* const* absmax,
+                           const float* const* code2, const float* const* absmax2,
+                           const float* const* offsets, const float* const* code,
+                           void* const* out, const int64_t* n_blocks, const int32_t* nested,
+                           const int32_t* standard, const int32_t* bs1, const int32_t* bs2,
+                           const int64_t* seg1, const int64_t* seg2, void* stream);
+
+/*
  * NF4 dequantisation fused into an fp16 MFMA GEMM (fp32 accumulation) with a frozen NF4 weight
  * W [w_rows, w_cols] in the layout of qlora_nf4_dequant (same absmax/code2/absmax2/offsets/
  * segment arguments):

@@ -88,6 +88,41 @@ def test_nf4_group_dequant_equals_separate(pkg):
     assert torch.equal(bits16(out), bits16(want))
 
 
+@pytest.mark.parametrize("mix", ["layer", "ragged"])
+def test_nf4_dequant_many_equals_oracle(pkg, mix):
+    """One qlora_nf4_dequant_many launch over several weights (a layer's q|k|v group, o,
+    gate|up group and down; or ragged sizes, plain absmax and a non-standard code mixed in)
+    equals the oracle bit for bit for every weight."""
+    rng = np.random.default_rng(7)
+
+    def make(shape, nested=True, code=None):
+        w = (rng.standard_normal(shape) * 0.02).astype(np.float16)
+        if code is None:
+            packed, st = ON.quantize_nf4(w, compress_statistics=nested)
+            return packed, st, ON.dequantize_nf4(packed, st)
+        packed = rng.integers(0, 256, shape[0] * shape[1] // 2, dtype=np.uint8)
+        st = ON.QuantState(rng.random(shape[0] * shape[1] // 64).astype(np.float32), shape,
+                           code, 64)
+        return packed, st, ON.dequantize_nf4(packed, st, levels=code)
+
+    if mix == "layer":
+        parts = [[make((1536, 1536)), make((256, 1536)), make((256, 1536))], [make((1536, 1536))],
+                 [make((8960, 1536)), make((8960, 1536))], [make((1536, 8960))]]
+    else:
+        code = np.sort(rng.standard_normal(16).astype(np.float32))
+        parts = [[make((64, 64))], [make((300, 512), nested=False)], [make((8, 64), code=code)],
+                 [make((64, 1536)), make((256, 1536))]]
+    items, wants = [], []
+    for grp in parts:
+        ws = [pkg.ops.NF4Weight(_device_state(p, st)) for p, st, _ in grp]
+        items.append(ws[0] if len(ws) == 1 else pkg.ops.NF4Group.of(ws))
+        assert items[-1] is not None
+        wants.append(torch.from_numpy(np.concatenate([d for _, _, d in grp])))
+    outs = pkg.ops.dequant_many(items, torch.device(DEV))
+    for out, want in zip(outs, wants):
+        assert torch.equal(bits16(out), bits16(want))
+
+
 def test_quantizer_bytes_dequantize_like_oracle(pkg):
     """The package's torch quantiser (GPU) produces bitsandbytes-layout bytes that the HIP
     dequant and the oracle dequant read identically."""
