@@ -81,6 +81,56 @@ def measure_kernel(pkg, trainer, batch, which):
     return timer.summary()
 
 
+def config1(pkg, copies=64, reps=20):
+    """BASELINE config 1 on the GPU: NF4 double-quant dequant of one Qwen2.5-1.5B q_proj weight
+    [1536, 1536] (N(0, 0.02) from seed 1, bitsandbytes layout), rotating over `copies`
+    independent copies (> 256 MB of Infinity Cache per pass), and the same for the four weights
+    of a layer in one launch (qkv | o | gate-up | down, the step's dequant). Beside them a plain
+    device copy of the q_proj output size: the calibration kernel for the FETCH_SIZE /
+    WRITE_SIZE counter runs. Returns a dict of achieved GB/s (algorithmic bytes / event time)."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(1)
+
+    def weight(shape):
+        w = (torch.randn(shape, generator=g, device=dev) * 0.02).half()
+        return pkg.ops.NF4Weight(pkg.quant.quantize_nf4(w))
+
+    qs = [weight((1536, 1536)) for _ in range(copies)]
+    outs = [torch.empty((1536, 1536), device=dev, dtype=torch.float16) for _ in range(copies)]
+    per_q = pkg.profiling._dequant_bytes([None] * 7 + [qs[0].blocks, 1, None, 64, 256,
+                                                       2**63 - 1, 2**63 - 1])
+
+    def timed(fn, n):
+        for i in range(min(n, 4)):
+            fn(i)
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for i in range(n):
+            fn(i)
+        e.record()
+        torch.cuda.synchronize()
+        return s.elapsed_time(e) * 1e-3 / n
+
+    t_q = timed(lambda i: qs[i % copies].dequant_into(outs[i % copies]), copies * reps)
+    layers = []
+    for i in range(8):
+        grp = lambda shapes: pkg.ops.NF4Group.of([weight(sh) for sh in shapes])  # noqa: E731
+        layers.append([grp([(1536, 1536), (256, 1536), (256, 1536)]), weight((1536, 1536)),
+                       grp([(8960, 1536), (8960, 1536)]), weight((1536, 8960))])
+    per_layer = sum(pkg.profiling._dequant_bytes(
+        [None] * 7 + [w.blocks, 1, None, 64, 256, getattr(w, "seg1", 2**63 - 1),
+                      getattr(w, "seg2", 2**63 - 1)]) for w in layers[0])
+    t_l = timed(lambda i: pkg.ops.dequant_many(layers[i % 8], dev), 8 * reps)
+    src = torch.empty(1536 * 1536, device=dev, dtype=torch.float16).normal_()
+    dst = torch.empty_like(src)
+    t_c = timed(lambda i: dst.copy_(src), copies * reps)
+    return {"q_proj_dequant_GBs": per_q / t_q / 1e9, "q_proj_bytes": per_q,
+            "q_proj_us": t_q * 1e6, "layer_dequant_GBs": per_layer / t_l / 1e9,
+            "layer_bytes": per_layer, "layer_us": t_l * 1e6,
+            "copy_GBs": 2 * src.numel() * 2 / t_c / 1e9, "copies": copies}
+
+
 def cpu_baseline(pkg, model, batch):
     """The CPU oracle step on a bounded sample: forward + autograd backward of embedding +
     2 layers + head, and of the head alone; a 28-layer step is head + 28 x layer."""
@@ -138,6 +188,8 @@ def main():
     ap.add_argument("--recompute-steps", type=int, default=10,
                     help="also time this many steps with full per-layer recompute (0: skip)")
     ap.add_argument("--layers", type=int, default=28)
+    ap.add_argument("--config1", action="store_true",
+                    help="only the config-1 dequant measurement (and its copy calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus}: this build measures one GPU only (the path is "
@@ -146,6 +198,9 @@ def main():
     pkg = importlib.import_module(PKG_NAME)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.config1:
+        print(json.dumps({"config1": config1(pkg)}), flush=True)
+        return
     torch.manual_seed(0)
     torch.cuda.manual_seed(0)
     cfg = pkg.engine.Qwen2Config(num_hidden_layers=args.layers)
@@ -207,6 +262,7 @@ def main():
         "full_recompute": recompute,
         "loss_first_last": [losses[0], losses[-1]],
         "roofline": roof,
+        "config1": config1(pkg),
     }
     if not args.no_cpu:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)

@@ -14,8 +14,6 @@
 namespace qlora {
 
 constexpr int kDequantThreads = 256;
-constexpr int kWPT = 8;  // words per thread
-constexpr int kTileWords = kDequantThreads * kWPT;
 constexpr int kMaxJobs = 4;
 
 struct DequantJob {
@@ -30,7 +28,10 @@ struct DequantBatch {
   int count;
 };
 
+// kWPT words per thread: 8 for large launches, fewer when that would leave CUs without work.
+template <int kWPT>
 __global__ __launch_bounds__(kDequantThreads) void nf4_dequant_kernel(DequantBatch b) {
+  constexpr int kTileWords = kDequantThreads * kWPT;
   __shared__ float lut[16];
   __shared__ float c2[256];
   __shared__ float offs[3];
@@ -41,16 +42,7 @@ __global__ __launch_bounds__(kDequantThreads) void nf4_dequant_kernel(DequantBat
   const DequantJob& job = b.job[j];
   const NF4Ref& w = job.w;
   const int t = threadIdx.x;
-  if (t < 16) lut[t] = w.standard ? kNF4Levels[t] : w.code[t];
-  if (w.nested) {
-    c2[t] = w.code2[t];  // 256 threads, 256 entries
-    if (t < 3) {
-      const int nseg = 1 + (int)(w.seg1 != INT64_MAX) + (int)(w.seg2 != INT64_MAX);
-      offs[t] = w.offsets[t < nseg ? t : 0];
-    }
-  }
-  __syncthreads();
-
+  // the words and their block scales' inputs first (their latency then overlaps the table fill)
   const uint32_t* words = reinterpret_cast<const uint32_t*>(w.packed);
   const int64_t base = ((int64_t)blockIdx.x - b.first_tile[j]) * kTileWords + t;
   const int64_t last = job.n_words - 1;
@@ -71,6 +63,15 @@ __global__ __launch_bounds__(kDequantThreads) void nf4_dequant_kernel(DequantBat
       a2[i] = static_cast<const float*>(w.absmax)[blk];
     }
   }
+  if (t < 16) lut[t] = w.standard ? kNF4Levels[t] : w.code[t];
+  if (w.nested) {
+    c2[t] = w.code2[t];  // 256 threads, 256 entries
+    if (t < 3) {
+      const int nseg = 1 + (int)(w.seg1 != INT64_MAX) + (int)(w.seg2 != INT64_MAX);
+      offs[t] = w.offsets[t < nseg ? t : 0];
+    }
+  }
+  __syncthreads();
 #pragma unroll
   for (int i = 0; i < kWPT; ++i) {
     const int64_t idx = base + i * kDequantThreads;
@@ -112,23 +113,38 @@ int make_job(DequantJob& job, const void* packed, const void* absmax, const floa
   return 0;
 }
 
-int launch(DequantBatch& b, hipStream_t stream) {
-  // drop empty jobs, then lay the workgroups of the rest end to end
-  int k = 0;
-  for (int i = 0; i < b.count; ++i)
-    if (b.job[i].n_words > 0) b.job[k++] = b.job[i];
-  b.count = k;
-  if (k == 0) return 0;
+template <int kWPT>
+int launch_wpt(DequantBatch& b, hipStream_t stream) {
+  constexpr int64_t kTileWords = kDequantThreads * kWPT;
   int64_t tiles = 0;
-  for (int i = 0; i < k; ++i) {
+  for (int i = 0; i < b.count; ++i) {
     b.first_tile[i] = tiles;
     tiles += qlora_cdiv(b.job[i].n_words, kTileWords);
   }
-  for (int i = k; i <= kMaxJobs; ++i) b.first_tile[i] = tiles;
+  for (int i = b.count; i <= kMaxJobs; ++i) b.first_tile[i] = tiles;
   QLORA_CHECK_ARG(tiles < (1ll << 31));
-  hipLaunchKernelGGL(nf4_dequant_kernel, dim3((unsigned)tiles), dim3(kDequantThreads), 0,
+  hipLaunchKernelGGL(nf4_dequant_kernel<kWPT>, dim3((unsigned)tiles), dim3(kDequantThreads), 0,
                      stream, b);
   return qlora_launch_status();
+}
+
+int launch(DequantBatch& b, hipStream_t stream) {
+  // drop empty jobs, then lay the workgroups of the rest end to end
+  int k = 0;
+  int64_t words = 0;
+  for (int i = 0; i < b.count; ++i)
+    if (b.job[i].n_words > 0) {
+      words += b.job[i].n_words;
+      b.job[k++] = b.job[i];
+    }
+  b.count = k;
+  if (k == 0) return 0;
+  // at least ~2048 workgroups (8 per CU) when the launch is big enough for that
+  constexpr int64_t kTarget = 2048 * kDequantThreads;
+  if (words >= 8 * kTarget) return launch_wpt<8>(b, stream);
+  if (words >= 4 * kTarget) return launch_wpt<4>(b, stream);
+  if (words >= 2 * kTarget) return launch_wpt<2>(b, stream);
+  return launch_wpt<1>(b, stream);
 }
 
 }  // namespace
