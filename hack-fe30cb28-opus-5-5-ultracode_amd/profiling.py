@@ -16,6 +16,13 @@ FP16_PEAK_TFLOPS = 2500.0
 # the kernel reported as the step's roofline entry
 DOMINANT = "qlora_nf4_dequant_many"
 
+# Measured HBM bytes per launch over algorithmic bytes per launch: rocprofv3 FETCH_SIZE and
+# WRITE_SIZE of the layer-wide dequant launch (the same kernel and byte count as each of the
+# step's launches), each divided by what the counter reads for a plain 4.5 MiB device copy
+# (FETCH 0.5025, WRITE 1.000 of the bytes moved): (11,903.5 / 0.5025 + 91,392) KiB per launch
+# = 1.001 x the algorithmic 117,728,444 B.
+TRAFFIC_RATIO = {"qlora_nf4_dequant_many": 1.001}
+
 
 def _dequant_bytes(args):
     """Algorithmic HBM bytes of one qlora_nf4_dequant launch: packed nibbles, absmax, the
@@ -88,7 +95,9 @@ class LaunchTimer:
         else:
             achieved = work / total_s / 1e12
             peak, unit = FP16_PEAK_TFLOPS, "TFLOP/s"
+        ratio = TRAFFIC_RATIO.get(self.entry)
+        traffic = work / len(ms) * ratio if ratio is not None else None
         return {"bound": self.bound, "achieved": achieved, "peak": peak, "unit": unit,
-                "frac": achieved / peak, "traffic": None, "kernel": self.entry,
+                "frac": achieved / peak, "traffic": traffic, "kernel": self.entry,
                 "launches": len(ms), "avg_us": avg_us,
                 "work_per_launch": work / len(ms)}
