@@ -131,6 +131,35 @@ def config1(pkg, copies=64, reps=20):
             "copy_GBs": 2 * src.numel() * 2 / t_c / 1e9, "copies": copies}
 
 
+def config4(pkg, reps=3):
+    """BASELINE config 4 on the GPU: LM head loss over hidden [2048, 1536] (N(0, 1)) and the
+    tied embedding [151936, 1536] (N(0, 0.02)), ~25 % of the labels ignored, with the hidden and
+    embedding gradients: vocabulary pieces of 8192 (online softmax, head.chunked_head: logits,
+    the dh accumulation, recomputed logits, dE; 4 products of 2 T V H flops) and whole rows
+    (head.full_head: logits, G E, G^T h; 3 products)."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(4)
+    T, V, H = 2048, 151936, 1536
+    hn = torch.randn(T, H, generator=g, device=dev).half()
+    E = (torch.randn(V, H, generator=g, device=dev) * 0.02).half()
+    targets = torch.randint(0, V, (T,), generator=g, device=dev)
+    targets[torch.rand(T, generator=g, device=dev) < 0.25] = -100
+    denom = float((targets >= 0).sum())
+    out = {}
+    for name, fn, products in (("pieces", pkg.head.chunked_head, 4),
+                               ("whole_rows", pkg.head.full_head, 3)):
+        fn(hn, E, targets, denom)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            r = fn(hn, E, targets, denom)
+        torch.cuda.synchronize()
+        dt = (time.perf_counter() - t0) / reps
+        flops = products * 2.0 * T * V * H
+        out[name] = {"ms": dt * 1e3, "TFLOPs": flops / dt / 1e12, "loss": float(r.loss)}
+    return out
+
+
 def cpu_baseline(pkg, model, batch):
     """The CPU oracle step on a bounded sample: forward + autograd backward of embedding +
     2 layers + head, and of the head alone; a 28-layer step is head + 28 x layer."""
@@ -263,6 +292,7 @@ def main():
         "loss_first_last": [losses[0], losses[-1]],
         "roofline": roof,
         "config1": config1(pkg),
+        "config4": config4(pkg),
     }
     if not args.no_cpu:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)

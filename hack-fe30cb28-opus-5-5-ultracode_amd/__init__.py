@@ -7,13 +7,16 @@ stream. There is no Triton and no CPU fallback: without the built library every 
 
   engine   the training step: Packed, _Layer, _Head, FusedQwen2, random_qwen2
   linear   the step's GEMMs (NF4 projections forward/backward, lm_head)
+  head     the LM head over vocabulary pieces with the hidden and embedding gradients
   ops      the engine's op wrappers (_rms_fwd, _rms_bwd, _rope_fwd, _rope_bwd, _glu_fwd,
-           _glu_bwd, _ce, _ce_piece, _ce_finish, dequant, NF4Weight, NF4Group, TorchDropout)
+           _glu_bwd, _attn_fwd, _attn_bwd, _ce, _ce_piece, _ce_finish, _ce_grad, dequant,
+           dequant_many, NF4Weight, NF4Group, TorchDropout)
   quant    bitsandbytes-format NF4 double quantisation (builds the frozen weights)
   _lib     the ctypes binding of the C-ABI
   build    hipcc build of the library
 """
 
-from . import _lib, ops, quant, linear, engine, profiling  # noqa: F401
-from .ops import (NF4Group, NF4Weight, TorchDropout, _ce, _ce_finish, _ce_piece,  # noqa: F401
-                  _glu_bwd, _glu_fwd, _rms_bwd, _rms_fwd, _rope_bwd, _rope_fwd, dequant)
+from . import _lib, ops, quant, linear, engine, head, profiling  # noqa: F401
+from .ops import (NF4Group, NF4Weight, TorchDropout, _attn_bwd, _attn_fwd, _ce,  # noqa: F401
+                  _ce_finish, _ce_grad, _ce_piece, _glu_bwd, _glu_fwd, _rms_bwd, _rms_fwd,
+                  _rope_bwd, _rope_fwd, dequant, dequant_many)

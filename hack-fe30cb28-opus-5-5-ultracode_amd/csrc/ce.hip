@@ -269,6 +269,24 @@ __global__ __launch_bounds__(kCeThreads) void ce_piece_kernel(
   }
 }
 
+// After the last piece: the logits of one piece (rows < n_sup, recomputed) overwritten with
+// fp16(e^(x - lse) - onehot), lse from the finished row state. The expression is the whole-row
+// kernel's, and a row's state after all pieces equals the whole-row state bit for bit, so the
+// piece's gradient rows equal the columns [v0, v0 + width) of the whole-row gradient.
+template <bool VEC>
+__global__ __launch_bounds__(kCeThreads) void ce_grad_kernel(uint16_t* logits, int64_t ld,
+                                                             const int64_t* target,
+                                                             const float* state, int64_t v0,
+                                                             int64_t width) {
+  const int64_t r = blockIdx.x;
+  uint16_t* row = logits + r * ld;
+  const float lse = state[r * 4 + 0] + logf(state[r * 4 + 1]);
+  const int64_t local = target[r] >= 0 ? target[r] - v0 : -1;
+  rewrite<VEC>(row, width, [&](float x, int64_t c) {
+    return __expf(x - lse) - (c == local ? 1.f : 0.f);
+  });
+}
+
 __global__ __launch_bounds__(kCeThreads) void ce_finish_kernel(
     const float* state, const int32_t* best_idx, const float* xt, const int64_t* target,
     float* loss, float* entropy, int32_t* correct, const float* acc, const uint16_t* wt,
@@ -350,5 +368,23 @@ QLORA_API int qlora_ce_finish(const float* state, const int32_t* best_idx, const
   hipLaunchKernelGGL(ce_finish_kernel, dim3((unsigned)rows), dim3(kCeThreads), 0,
                      (hipStream_t)stream, state, best_idx, xt, target, loss, entropy, correct,
                      acc, static_cast<const uint16_t*>(wt), static_cast<uint16_t*>(dh), n_sup, H);
+  return qlora_launch_status();
+}
+
+// Gradient rows of one recomputed piece after the finish step (for the embedding gradient).
+QLORA_API int qlora_ce_grad(void* logits, int64_t ld, const int64_t* target, const float* state,
+                            int64_t v0, int64_t n_sup, int64_t width, void* stream) {
+  QLORA_CHECK_ARG(n_sup >= 0 && width >= 0 && ld >= width && v0 >= 0);
+  if (n_sup == 0 || width == 0) return 0;
+  QLORA_CHECK_ARG(logits && target && state);
+  const bool vec = ld % kCeVec == 0 && al16(logits);
+  if (vec)
+    hipLaunchKernelGGL(ce_grad_kernel<true>, dim3((unsigned)n_sup), dim3(kCeThreads), 0,
+                       (hipStream_t)stream, static_cast<uint16_t*>(logits), ld, target, state,
+                       v0, width);
+  else
+    hipLaunchKernelGGL(ce_grad_kernel<false>, dim3((unsigned)n_sup), dim3(kCeThreads), 0,
+                       (hipStream_t)stream, static_cast<uint16_t*>(logits), ld, target, state,
+                       v0, width);
   return qlora_launch_status();
 }

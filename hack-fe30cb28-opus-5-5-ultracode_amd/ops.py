@@ -648,3 +648,21 @@ def _ce_finish(state, best_idx, xt, targets, tok_loss, entropy, correct, acc, wt
     _lib.call("qlora_ce_finish", _ptr(state), _ptr(best_idx), _ptr(xt), _ptr(targets),
               _ptr(tok_loss), _ptr(entropy), _ptr(correct), _ptr(acc), _ptr(wt), _ptr(dh),
               rows, int(n_sup), H, _stream(dev))
+
+
+def _ce_grad(logits, targets, state, v0, n_sup):
+    """The gradient rows (< n_sup) of one recomputed vocabulary piece after _ce_finish, in place:
+    fp16(e^(x - lse) - onehot) (for the embedding gradient; the reference freezes the
+    embedding and has no such pass)."""
+    _need(logits, "logits", torch.float16, contiguous=False)
+    rows, width = logits.shape
+    if n_sup == 0 or width == 0:
+        return
+    dev = logits.device
+    ld = _rows_view(logits, "logits", torch.float16, rows, width, dev)
+    _need(targets, "targets", torch.int64, dev)
+    _need(state, "state", torch.float32, dev)
+    if n_sup > rows or targets.numel() < n_sup or state.shape[0] < n_sup or state.shape[1] != 4:
+        raise ValueError("targets and state must cover the n_sup rows")
+    _lib.call("qlora_ce_grad", _ptr(logits), ld, _ptr(targets), _ptr(state), int(v0),
+              int(n_sup), width, _stream(dev))

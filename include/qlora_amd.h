@@ -153,6 +153,17 @@ int qlora_ce_finish(const float* state, const int32_t* best_idx, const float* xt
                     int64_t H, void* stream);
 
 /*
+ * Embedding-gradient pass of the chunked head (no reference counterpart: the reference's
+ * embedding is frozen; BASELINE config 4 asks for dE): after qlora_ce_finish, the recomputed
+ * logits of one piece, rows < n_sup (f16, row stride ld, columns [v0, v0 + width) of the
+ * vocabulary) are overwritten in place with f16(e^(x - lse) - onehot(target)), lse = m + log s
+ * from the finished state f32 [rows, 4]. Equal bit for bit to the same columns of qlora_ce's
+ * in-place gradient.
+ */
+int qlora_ce_grad(void* logits, int64_t ld, const int64_t* target, const float* state,
+                  int64_t v0, int64_t n_sup, int64_t width, void* stream);
+
+/*
  * Up to four weights in one launch (a layer's qkv, o, gate|up and down): arrays of `count`
  * entries, entry i exactly the arguments of one qlora_nf4_dequant call (pointer arrays and
  * value arrays live in host memory; the pointers they hold are device pointers).
