@@ -21,7 +21,8 @@ import torch
 
 from . import linear as L
 from .ops import (NF4Group, NF4Weight, TorchDropout, _attn_bwd, _attn_fwd, _ce, _glu_bwd,
-                  _glu_fwd, _rms_bwd, _rms_fwd, _rope_bwd, _rope_fwd)
+                  _glu_fwd, _lora_bwd_rows, _lora_fwd_rows, _rms_bwd, _rms_fwd, _rope_bwd,
+                  _rope_fwd)
 from .quant import quantize_nf4
 
 
@@ -184,12 +185,19 @@ class Packed:
         self.drop_seed = self.drop_threads = None
         self.drop_vec = dropout.vec if dropout is not None else 4
         self.lora16_views = None
+        self.lora16t_views = None
         self.grad16 = None  # (dh, fp16(dh)) handed from a layer's backward to the one below
 
     def lora16(self, index, weights):
         if self.lora16_views is not None:
             return self.lora16_views[index]
         return tuple(None if t is None else t.detach().to(torch.float16) for t in weights)
+
+    def lora16t(self, index, lora16):
+        """(A_q^T, B_q^T, A_v^T, B_v^T) fp16 contiguous: the backward's operand layout."""
+        if self.lora16t_views is not None:
+            return self.lora16t_views[index]
+        return tuple(None if t is None else t.t().contiguous() for t in lora16)
 
     def draw(self, H):
         """The counter of the next LoRA dropout mask of this step (the next nn.Dropout call on
@@ -218,10 +226,7 @@ def _layer_forward(spec, h, packed, lora16, seeds, keep):
                                    drop_q=aq_w is not None, drop_v=av_w is not None)
     qkv = L.nf4_linear(a, spec.qkv, bias=spec.bias_qkv)
     del a
-    xq = aq @ aq_w.t()
-    lq = xq @ bq_w.t()
-    xv = av @ av_w.t()
-    lv = xv @ bv_w.t()
+    xq, xv, lq, lv = _lora_fwd_rows(aq, av, aq_w, bq_w, av_w, bv_w)
     q, k, v = _rope_fwd(spec, qkv, lq, lv, packed, s, kv_heads=spec.HKV)
     del qkv, lq, lv
     out, lse, aseed, aoffset = _attn_fwd(q, k, v, packed, spec.scale)
@@ -315,16 +320,23 @@ class _Layer(torch.autograd.Function):
         del dq, dk, dv
         need_dh = ctx.needs_input_grad[0]
         da = L.nf4_linear_t(dqkv, spec.qkv) if need_dh else None
-        # LoRA (engine.py:1319-1331): dB = s g^T x, dx = s g B, dA = dx^T drop(a), t = dx A
+        # LoRA (engine.py:1319-1331): dx = s g B and t = dx A per token in one kernel for both
+        # adapters; the token reductions dB = s g^T x and dA = dx^T drop(a) as fp32 products
+        qc, vc = slice(0, HQ * D), slice((HQ + HKV) * D, C)
+        lt = packed.lora16t(spec.index, lora16)
+        dxq, dxv, tq, tv = _lora_bwd_rows(dqkv, qc, vc, lt[0], lt[1], lt[2], lt[3], s,
+                                          need_t=need_dh)
         grads = {}
-        for short, a_w, b_w, cols in (("q", lora16[0], lora16[1], slice(0, HQ * D)),
-                                      ("v", lora16[2], lora16[3], slice((HQ + HKV) * D, C))):
+        for short, cols, dx in (("q", qc, dxq), ("v", vc, dxv)):
             x_lo, a_in = f.pop("x" + short), f.pop("a" + short)
             g = dqkv[:, cols]
-            db_w = (g.t() @ x_lo).float() * s
-            dx_lo = (g @ b_w) * s
-            da_w = (dx_lo.t() @ a_in).float()
-            grads[short] = (da_w, db_w, dx_lo @ a_w if need_dh else None)
+            db_w = torch.addmm(torch.empty((g.shape[1], x_lo.shape[1]), device=g.device,
+                                           dtype=torch.float32), g.t(), x_lo, beta=0.0,
+                               alpha=s, out_dtype=torch.float32)
+            da_w = torch.mm(dx.t(), a_in, out_dtype=torch.float32)
+            grads[short] = (da_w, db_w)
+        grads["q"] += (tq,)
+        grads["v"] += (tv,)
         del dqkv
         dh = None
         if need_dh:
@@ -432,6 +444,23 @@ class FusedQwen2:
             start += t.numel()
         self.lora_views = views
         self.lora16_by_layer = [tuple(views[4 * i:4 * i + 4]) for i in range(len(layers))]
+        # the same fp16 weights transposed (A^T [H, r], B^T [r, N]), for the backward: per kind
+        # one [L, ...] tensor refreshed by one strided copy from lora_buf
+        nl = len(layers)
+        shapes = [tuple(t.shape) for t in self.lora_fp32]
+        per_layer = total // nl
+        self.lora_t_src, self.lora_t = [], []
+        if all(shapes[4 * i:4 * i + 4] == shapes[:4] for i in range(nl)):
+            off = 0
+            for d0, d1 in shapes[:4]:
+                self.lora_t_src.append(self.lora_buf.as_strided((nl, d1, d0),
+                                                                (per_layer, 1, d1), off))
+                self.lora_t.append(torch.empty((nl, d1, d0), device=self.device,
+                                               dtype=torch.float16))
+                off += d0 * d1
+            self.lora16t_by_layer = [tuple(t[i] for t in self.lora_t) for i in range(nl)]
+        else:
+            self.lora16t_by_layer = None
 
     def parameters(self):
         return list(self.lora_fp32)
@@ -479,7 +508,10 @@ class FusedQwen2:
             raise UnsupportedBatch("LoRA dropout masks differ from PyTorch's on this GPU")
         with torch.no_grad():
             torch._foreach_copy_(self.lora_views, [t.detach() for t in self.lora_fp32])
+            for dst, src in zip(self.lora_t, self.lora_t_src):
+                dst.copy_(src)
         packed.lora16_views = self.lora16_by_layer
+        packed.lora16t_views = self.lora16t_by_layer
         h = torch.nn.functional.embedding(packed.ids, self.embed).float()
         keep_from = len(self.layers) - self.keep_plan(packed.n)
         packed.keep_all_from = keep_from

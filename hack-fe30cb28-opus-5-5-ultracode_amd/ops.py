@@ -480,6 +480,64 @@ def _resid_add(a, d, out=None):
 
 
 # ---------------------------------------------------------------------------------------------
+# LoRA per-token products (engine.py:1088-1093, 1319-1331)
+# ---------------------------------------------------------------------------------------------
+def _lora_fwd_rows(a_q, a_v, A_q, B_q, A_v, B_v):
+    """(x_q, x_v, l_q, l_v): x = fp16(a A^T) [n, r], l = fp16(x B^T) [n, N] for the q and v
+    adapters (engine.py:1088-1093); a [n, H], A [r, H], B [N, r] fp16."""
+    _need(a_q, "a_q", torch.float16)
+    n, H = a_q.shape
+    dev = a_q.device
+    _need(a_v, "a_v", torch.float16, dev)
+    for t, name in ((A_q, "A_q"), (B_q, "B_q"), (A_v, "A_v"), (B_v, "B_v")):
+        _need(t, name, torch.float16, dev)
+    r = A_q.shape[0]
+    if a_v.shape != (n, H) or A_q.shape != (r, H) or A_v.shape != (r, H) \
+            or B_q.shape[1] != r or B_v.shape[1] != r:
+        raise ValueError("a [n, H], A [r, H] and B [N, r] for both adapters")
+    Nq, Nv = B_q.shape[0], B_v.shape[0]
+    x_q = torch.empty((n, r), device=dev, dtype=torch.float16)
+    x_v = torch.empty((n, r), device=dev, dtype=torch.float16)
+    l_q = torch.empty((n, Nq), device=dev, dtype=torch.float16)
+    l_v = torch.empty((n, Nv), device=dev, dtype=torch.float16)
+    if n:
+        _lib.call("qlora_lora_fwd_rows", _ptr(a_q), _ptr(a_v), _ptr(A_q), _ptr(A_v), _ptr(B_q),
+                  _ptr(B_v), _ptr(x_q), _ptr(x_v), _ptr(l_q), _ptr(l_v), n, Nq, Nv, H, r,
+                  _stream(dev))
+    return x_q, x_v, l_q, l_v
+
+
+def _lora_bwd_rows(dqkv, q_cols, v_cols, at_q, bt_q, at_v, bt_v, scale, need_t=True):
+    """(dx_q, dx_v, t_q, t_v) of the q and v adapters from the fused [dq|dk|dv] gradient:
+    dx = fp16(fp16(g B) * s) [n, r], t = fp16(dx A) [n, H] (None without need_t); g = the
+    adapter's columns (slices q_cols / v_cols of dqkv's columns). The adapter weights come
+    transposed: at = A^T [H, r], bt = B^T [r, N] fp16 (contiguous)."""
+    _need(dqkv, "dqkv", torch.float16, contiguous=False)
+    n, C = dqkv.shape
+    dev = dqkv.device
+    if dqkv.stride(1) != 1:
+        raise ValueError("dqkv must have unit column stride")
+    for t, name in ((at_q, "at_q"), (bt_q, "bt_q"), (at_v, "at_v"), (bt_v, "bt_v")):
+        _need(t, name, torch.float16, dev)
+    H, r = at_q.shape
+    Nq, Nv = q_cols.stop - q_cols.start, v_cols.stop - v_cols.start
+    if at_v.shape != (H, r) or bt_q.shape != (r, Nq) or bt_v.shape != (r, Nv):
+        raise ValueError("A^T must be [H, r] and B^T [r, N] for both adapters")
+    if (2 * q_cols.start) % 16 or (2 * v_cols.start) % 16:
+        raise ValueError("the adapters' columns must start on 16-byte boundaries")
+    dx_q = torch.empty((n, r), device=dev, dtype=torch.float16)
+    dx_v = torch.empty((n, r), device=dev, dtype=torch.float16)
+    t_q = torch.empty((n, H), device=dev, dtype=torch.float16) if need_t else None
+    t_v = torch.empty((n, H), device=dev, dtype=torch.float16) if need_t else None
+    if n:
+        base = dqkv.data_ptr()
+        _lib.call("qlora_lora_bwd_rows", base + 2 * q_cols.start, base + 2 * v_cols.start,
+                  dqkv.stride(0), _ptr(bt_q), _ptr(bt_v), _ptr(at_q), _ptr(at_v), _ptr(dx_q),
+                  _ptr(dx_v), _ptr(t_q), _ptr(t_v), n, Nq, Nv, H, r, float(scale), _stream(dev))
+    return dx_q, dx_v, t_q, t_v
+
+
+# ---------------------------------------------------------------------------------------------
 # Varlen causal attention (engine.py:857-869)
 # ---------------------------------------------------------------------------------------------
 def _attn_shapes(q, k, v, packed):

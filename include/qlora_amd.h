@@ -212,6 +212,34 @@ int qlora_nf4_gemm(const void* a, int64_t lda, int32_t a_f32, const void* packed
 int qlora_resid_add(const float* a, const void* d, float* out, int64_t numel, void* stream);
 
 /*
+ * The LoRA forward of a layer's q and v adapters in one launch (engine.py:1088-1093):
+ *   x_a = f16(a_a A_a^T)   f16 [n, 16] (kept for the backward)
+ *   l_a = f16(x_a B_a^T)   f16 [n, N_a] (added to the projection output by qlora_rope_fwd)
+ * a_a f16 [n, H] (the dropped LoRA inputs of qlora_rms_fwd); A_a f16 [16, H]; B_a f16 [N_a, 16].
+ * Requires r == 16, H % 16 == 0, N_a % 32 == 0; a_a, A_a, B_a 16-byte and l_a 8-byte aligned.
+ * No reference counterpart as one launch: the reference makes four fp16 products.
+ */
+int qlora_lora_fwd_rows(const void* a_q, const void* a_v, const void* A_q, const void* A_v,
+                        const void* B_q, const void* B_v, void* x_q, void* x_v, void* l_q,
+                        void* l_v, int64_t n, int32_t N_q, int32_t N_v, int32_t H, int32_t r,
+                        void* stream);
+
+/*
+ * Per-token part of the LoRA backward of a layer's q and v adapters in one launch:
+ *   dx_a = f16(f16(g_a B_a) * s)   f16 [n, 16]        t_a = f16(dx_a A_a)   f16 [n, H]
+ * g_q / g_v: the adapters' columns of the fused d[q|k|v] gradient (f16, row stride ldg);
+ * Bt_a = B_a^T f16 [16, N_a]; At_a = A_a^T f16 [H, 16] (the transposed adapter weights);
+ * t_q/t_v may both be null (then not computed). Replaces `dx_lo = (g @ b_w) * s` and
+ * `dx_lo @ a_w` (engine.py:1326-1330) for both adapters; the token reductions dB and dA stay
+ * products. Requires r == 16, N_a % 16 == 0, H % 32 == 0, ldg % 8 == 0; g_a, Bt_a, At_a 16-byte
+ * and t_a 8-byte aligned.
+ */
+int qlora_lora_bwd_rows(const void* g_q, const void* g_v, int64_t ldg, const void* Bt_q,
+                        const void* Bt_v, const void* At_q, const void* At_v, void* dx_q,
+                        void* dx_v, void* t_q, void* t_v, int64_t n, int32_t N_q, int32_t N_v,
+                        int32_t H, int32_t r, float s, void* stream);
+
+/*
  * Causal attention within each packed sequence (flash attention, online softmax), grouped-query
  * heads, fp16 operands and fp32 accumulation/softmax.
  *   q [n, HQ, D], k/v [n, KH, D] (q head h reads kv head h / (HQ/KH)), out [n, HQ, D] fp16,

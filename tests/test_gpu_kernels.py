@@ -402,3 +402,54 @@ def test_ce_kernels_take_the_target_logit_before_the_row_is_overwritten(pkg):
         cor = torch.empty(n, device=DEV, dtype=torch.int32)
         pkg.ops._ce(logits.clone(), targets, loss, ent, cor)
         assert (loss - exact).abs().max() < 1e-3
+
+
+@pytest.mark.parametrize("n,H,Nq,Nv", [(300, 1536, 1536, 256), (1, 1536, 1536, 256),
+                                       (77, 256, 256, 128), (4100, 896, 896, 128),
+                                       (33, 3584, 3584, 512)])
+def test_lora_bwd_rows(pkg, n, H, Nq, Nv):
+    """dx = fp16(fp16(g B) s), t = fp16(dx A) for both adapters against fp64 of the same
+    roundings (engine.py:1326-1330); g are column slices of one fused gradient (row stride C)."""
+    g = torch.Generator().manual_seed(n)
+    C = Nq + 2 * Nv
+    dqkv = torch.randn(n, C, generator=g).half()
+    aq = (torch.randn(16, H, generator=g) * 0.05).half()
+    av = (torch.randn(16, H, generator=g) * 0.05).half()
+    bq = (torch.randn(Nq, 16, generator=g) * 0.05).half()
+    bv = (torch.randn(Nv, 16, generator=g) * 0.05).half()
+    s = 2.0
+    qc, vc = slice(0, Nq), slice(Nq + Nv, C)
+    tr = [w.t().contiguous().to(DEV) for w in (aq, bq, av, bv)]
+    dxq, dxv, tq, tv = pkg.ops._lora_bwd_rows(dqkv.to(DEV), qc, vc, *tr, s)
+    for cols, b, a, dx, t in ((qc, bq, aq, dxq, tq), (vc, bv, av, dxv, tv)):
+        gd = dqkv[:, cols].double()
+        want = ((gd @ b.double()).half().double() * s).half()
+        # fp16 GEMM outputs may differ from fp64 in the last bit (summation order)
+        close(dx, want, 2e-3 * want.abs().max().item())
+        tw = (dx.cpu().double() @ a.double()).half()
+        close(t, tw, 2e-3 * tw.abs().max().item())
+    dq2, dv2, t0, t1 = pkg.ops._lora_bwd_rows(dqkv.to(DEV), qc, vc, *tr, s, need_t=False)
+    assert t0 is None and t1 is None
+    assert torch.equal(dq2, dxq) and torch.equal(dv2, dxv)
+
+
+@pytest.mark.parametrize("n,H,Nq,Nv", [(300, 1536, 1536, 256), (1, 1536, 1536, 256),
+                                       (77, 256, 256, 128), (4100, 896, 896, 128),
+                                       (33, 3584, 3584, 512)])
+def test_lora_fwd_rows(pkg, n, H, Nq, Nv):
+    """x = fp16(a A^T), l = fp16(x B^T) for both adapters (engine.py:1088-1093) against fp64 of
+    the same roundings."""
+    g = torch.Generator().manual_seed(n + 1)
+    aq = torch.randn(n, H, generator=g).half()
+    av = torch.randn(n, H, generator=g).half()
+    Aq = (torch.randn(16, H, generator=g) * 0.05).half()
+    Av = (torch.randn(16, H, generator=g) * 0.05).half()
+    Bq = (torch.randn(Nq, 16, generator=g) * 0.05).half()
+    Bv = (torch.randn(Nv, 16, generator=g) * 0.05).half()
+    xq, xv, lq, lv = pkg.ops._lora_fwd_rows(aq.to(DEV), av.to(DEV), Aq.to(DEV), Bq.to(DEV),
+                                            Av.to(DEV), Bv.to(DEV))
+    for a, A, B, x, l in ((aq, Aq, Bq, xq, lq), (av, Av, Bv, xv, lv)):
+        want = (a.double() @ A.double().t()).half()
+        close(x, want, 2e-3 * want.abs().max().item())
+        lw = (x.cpu().double() @ B.double().t()).half()
+        close(l, lw, 2e-3 * lw.abs().max().item())
