@@ -1,7 +1,7 @@
 """Benchmark: full Qwen2.5-1.5B NF4 + LoRA training steps on one MI355X.
 
-A step = forward + backward (per-layer recompute) + fp16 loss scaling (GradScaler) + AdamW on
-the LoRA parameters, over one synthetic batch of 4 packed sequences with lengths ~ U[256, 1024]
+A step = forward + backward (intermediates kept per the reference's memory-cap plan, or
+recomputed) + fp16 loss scaling (GradScaler) + fused AdamW on the LoRA parameters, over one synthetic batch of 4 packed sequences with lengths ~ U[256, 1024]
 and random token ids (first 25% of each sequence unsupervised). Random-init weights of the
 Qwen2.5-1.5B architecture, all linears NF4 double-quant (blocksize 64), tied fp16 embedding.
 
@@ -12,7 +12,7 @@ Prints ONE JSON line: value = tokens/s over the K timed steps (inputs resident i
                 cores, on a bounded sample (embedding + 2 layers + head, and the head alone),
                 scaled to a 28-layer step
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--keep-all]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--policy plan|recompute|keep]
 """
 
 import argparse
@@ -52,13 +52,14 @@ def make_batches(count, vocab, seed=0, rows=4, lo=256, hi=1024, device="cuda"):
 
 class Trainer:
     """fp16 loss scaling (torch GradScaler, as HF Trainer with fp16) + AdamW on the LoRA
-    parameters."""
+    parameters: the fused AdamW, HF TrainingArguments' default optimizer ("adamw_torch_fused")
+    with torch >= 2.8, which takes the scaler's inf check on the device (no host sync)."""
 
     def __init__(self, model, lr=2e-4):
         self.model = model
         self.params = model.parameters()
         self.opt = torch.optim.AdamW(self.params, lr=lr, betas=(0.9, 0.999), eps=1e-8,
-                                     weight_decay=0.0)
+                                     weight_decay=0.0, fused=True)
         self.scaler = torch.amp.GradScaler("cuda", init_scale=2.0**16)
 
     def step(self, batch):
@@ -237,7 +238,12 @@ def main():
     model.keep_all = {"plan": None, "recompute": False, "keep": True}[args.policy]
     trainer = Trainer(model)
     batches = make_batches(args.warmup + args.steps + 1, cfg.vocab_size, device=dev)
-    print(f"[bench] model built; warmup {args.warmup}", file=sys.stderr, flush=True)
+    print("[bench] model built; timing the projection GEMM solutions", file=sys.stderr,
+          flush=True)
+    # every step size config 5 can produce (4 rows of 256..1024 tokens), before any timing
+    tune_s = model.tune_gemms(range(4 * 256, 4 * 1024 + 1, pkg.gemm.BUCKET))
+    print(f"[bench] GEMM tuning {tune_s:.1f} s; warmup {args.warmup}", file=sys.stderr,
+          flush=True)
     for i in range(args.warmup):
         trainer.step(batches[i])
     torch.cuda.synchronize()
@@ -288,6 +294,7 @@ def main():
                                    "(the reference's memory-cap plan, engine.py:1626-1640, "
                                    "under this GPU's memory); the others recompute their "
                                    "forward")},
+        "gemm_tuning_s": tune_s,
         "full_recompute": recompute,
         "loss_first_last": [losses[0], losses[-1]],
         "roofline": roof,

@@ -5,6 +5,7 @@ Compiled in-tree, next to this file, so the library travels with the source tree
   -ffp-contract=off          no implicit FMA: the NF4 dequant must round the product
                              code2 * absmax2 before adding the offset, as bitsandbytes does
   -target-feature -packed-fp32-ops   no packed fp32 VALU instructions
+Linked against rocBLAS (the plain projection GEMMs, csrc/blas.hip).
 Usage: python -m <package>.build  (or build() from __graft_entry__)
 """
 
@@ -54,7 +55,8 @@ def build(verbose=False, jobs=None):
         msg = "\n".join(f"--- {s}\n{o}" for s, o in failed)
         raise RuntimeError(f"hipcc failed:\n{msg}")
     tmp = LIB + ".tmp"
-    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
+    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp,
+           "-L/opt/rocm/lib", "-lrocblas"]
     subprocess.run(cmd, check=True)
     os.replace(tmp, LIB)
     return LIB

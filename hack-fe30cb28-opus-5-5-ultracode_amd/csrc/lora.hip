@@ -7,7 +7,7 @@
 //              l  = f16(x B^T)            [n, N]    (added to the projection by the RoPE kernel)
 //   backward:  dx = f16(f16(g B) * s)     [n, 16]   (g: the adapter's columns of d[q|k|v])
 //              t  = f16(dx A)             [n, H]    (the gradient reaching the LoRA input)
-// The token reductions of the backward (dB = s g^T x, dA = dx^T a) stay GEMMs.
+// The token reductions of the backward (dB = s g^T x, dA = dx^T a) are qlora_lora_grad, below.
 //
 // Generic form: phase 1 P = X W (X [n, K1] rows, W given as Wt [16, K1]), phase 2 Y = P V (V
 // given as Vt [M2, 16]). Every MFMA operand is then a 16-byte run along the contraction. The
@@ -157,6 +157,158 @@ int launch(Args& a, hipStream_t stream) {
   return qlora_launch_status();
 }
 
+// ------------------------------------------------------------------------------------------------
+// Token reductions of the LoRA backward (engine.py:1327, 1329), all four in one pair of launches:
+//   dB_a = s * sum_t g_a[t]^T x_a[t]     fp32 [N_a, 16]
+//   dA_a =     sum_t dx_a[t]^T a_a[t]    fp32 [16, H]
+// Generic job: out[c][k] = scale * sum_t W[t][c] Z[t][k] with W token-major (a wide fp16 matrix
+// read along its rows, coalesced) and Z fp16 [n, 16]. Pass 1: a workgroup takes 128 columns of
+// one job and a chunk of kGradChunk tokens, split in four quarters (one per wavefront). A thread
+// owns two adjacent columns of its quarter: it issues the loads of all its token pairs at once
+// (enough bytes in flight to cover the memory latency), then accumulates the 2 x 16 sums with
+// v_dot2_f32_f16 (the pair (W[t][c], W[t+1][c]) against (Z[t][k], Z[t+1][k]), the latter
+// staged in LDS and read as a broadcast). The quarters are added in LDS and the chunk's fp32
+// partial sums go to a workspace [chunks][columns][16]. Pass 2 adds the chunks in a fixed order
+// (the result does not depend on scheduling) and writes the outputs, transposed for dA.
+// Products are exact in fp32; sums are fp32, as the reference's GEMMs accumulate.
+// ------------------------------------------------------------------------------------------------
+constexpr int kGradThreads = 256;
+constexpr int kGradPairs = 64;                     // column pairs per workgroup (one wavefront)
+constexpr int kGradCols = 2 * kGradPairs;          // columns per workgroup
+constexpr int kGradQuarter = 64;                   // tokens per wavefront
+constexpr int kGradChunk = 4 * kGradQuarter;       // tokens per workgroup
+constexpr int kGradJobs = 4;
+
+struct GradJob {
+  const uint16_t* W;  // fp16, column c of token t at W[t * ldw + c]
+  const uint16_t* Z;  // fp16 [n, 16]
+  float* out;         // trans 0: out[c * 16 + k]; trans 1: out[k * ncols + c]
+  int64_t ldw;
+  int ncols, trans, col0;  // col0: the job's first column in the workspace (multiple of 128)
+  float scale;
+};
+
+struct GradArgs {
+  GradJob job[kGradJobs];
+  float* part;
+  int64_t n;
+  int total_cols, nchunks;
+};
+
+__device__ __forceinline__ int grad_job(const GradArgs& a, int col) {
+  int j = 0;
+#pragma unroll
+  for (int i = 1; i < kGradJobs; ++i) j = col >= a.job[i].col0 ? i : j;
+  return j;
+}
+
+__device__ __forceinline__ float dot2u(uint32_t a, uint32_t b, float c) {
+  typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, a), __builtin_bit_cast(half2_t, b),
+                                c, false);
+}
+
+__global__ __launch_bounds__(kGradThreads) void lora_grad_part_kernel(GradArgs a) {
+  constexpr int kQP = kGradQuarter / 2;  // token pairs per thread
+  constexpr int kRow = 2 * kRank + 4;    // floats per column pair in the LDS sum (padded)
+  __shared__ __align__(16) uint32_t zp[kGradChunk / 2][kRank];
+  __shared__ __align__(16) float red[4][kGradPairs][kRow];
+  const int tid = threadIdx.x, quarter = tid >> 6, cp = tid & 63;
+  const int wg_col = blockIdx.x * kGradCols;
+  const GradJob& jb = a.job[grad_job(a, wg_col)];
+  const int64_t t0 = (int64_t)blockIdx.y * kGradChunk;
+  const int nt = (int)min((int64_t)kGradChunk, a.n - t0);  // >= 1
+  // this thread's loads first: its quarter's token pairs of columns c, c + 1 (rows past the
+  // chunk read its last row and meet a zero Z below)
+  const int c = wg_col - jb.col0 + 2 * cp;
+  const bool col_ok = c < jb.ncols;
+  const uint16_t* wp = jb.W + (col_ok ? c : 0);
+  uint32_t w0[kQP], w1[kQP];
+#pragma unroll
+  for (int i = 0; i < kQP; ++i) {
+    const int64_t ta = t0 + min(kGradQuarter * quarter + 2 * i, nt - 1);
+    const int64_t tb = t0 + min(kGradQuarter * quarter + 2 * i + 1, nt - 1);
+    w0[i] = *reinterpret_cast<const uint32_t*>(wp + ta * jb.ldw);
+    w1[i] = *reinterpret_cast<const uint32_t*>(wp + tb * jb.ldw);
+  }
+  for (int i = tid; i < (kGradChunk / 2) * kRank; i += kGradThreads) {
+    const int p = i / kRank, k = i % kRank;
+    const int64_t ta = t0 + min(2 * p, nt - 1), tb = t0 + min(2 * p + 1, nt - 1);
+    const uint32_t za = jb.Z[ta * kRank + k], zb = jb.Z[tb * kRank + k];
+    zp[p][k] = (2 * p < nt ? za : 0u) | ((2 * p + 1 < nt ? zb : 0u) << 16);
+  }
+  __syncthreads();
+  float acc0[kRank], acc1[kRank];
+#pragma unroll
+  for (int k = 0; k < kRank; ++k) acc0[k] = acc1[k] = 0.f;
+#pragma unroll
+  for (int i = 0; i < kQP; ++i) {
+    const uint32_t pc0 = (w0[i] & 0xFFFFu) | (w1[i] << 16);  // column c, tokens t, t + 1
+    const uint32_t pc1 = (w0[i] >> 16) | (w1[i] & 0xFFFF0000u);  // column c + 1
+    const uint4* zq = reinterpret_cast<const uint4*>(zp[kQP * quarter + i]);
+#pragma unroll
+    for (int q = 0; q < kRank / 4; ++q) {
+      const uint4 z = zq[q];
+      acc0[4 * q + 0] = dot2u(pc0, z.x, acc0[4 * q + 0]);
+      acc0[4 * q + 1] = dot2u(pc0, z.y, acc0[4 * q + 1]);
+      acc0[4 * q + 2] = dot2u(pc0, z.z, acc0[4 * q + 2]);
+      acc0[4 * q + 3] = dot2u(pc0, z.w, acc0[4 * q + 3]);
+      acc1[4 * q + 0] = dot2u(pc1, z.x, acc1[4 * q + 0]);
+      acc1[4 * q + 1] = dot2u(pc1, z.y, acc1[4 * q + 1]);
+      acc1[4 * q + 2] = dot2u(pc1, z.z, acc1[4 * q + 2]);
+      acc1[4 * q + 3] = dot2u(pc1, z.w, acc1[4 * q + 3]);
+    }
+  }
+  float4* mine = reinterpret_cast<float4*>(red[quarter][cp]);
+#pragma unroll
+  for (int q = 0; q < kRank / 4; ++q) {
+    mine[q] = make_float4(acc0[4 * q], acc0[4 * q + 1], acc0[4 * q + 2], acc0[4 * q + 3]);
+    mine[kRank / 4 + q] =
+        make_float4(acc1[4 * q], acc1[4 * q + 1], acc1[4 * q + 2], acc1[4 * q + 3]);
+  }
+  __syncthreads();
+  // the chunk's sums: 64 column pairs x 32 values, 8 per thread (two float4 of one pair)
+  const int pair = tid >> 2, part4 = (tid & 3) * 2;
+  if (wg_col - jb.col0 + 2 * pair >= jb.ncols) return;  // no barrier follows
+  float4* dst = reinterpret_cast<float4*>(
+      a.part + ((int64_t)blockIdx.y * a.total_cols + wg_col + 2 * pair) * kRank);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int f = part4 + h;  // float4 index within the pair's 32 values
+    float4 v = reinterpret_cast<const float4*>(red[0][pair])[f];
+#pragma unroll
+    for (int qq = 1; qq < 4; ++qq) {
+      const float4 u = reinterpret_cast<const float4*>(red[qq][pair])[f];
+      v.x += u.x;
+      v.y += u.y;
+      v.z += u.z;
+      v.w += u.w;
+    }
+    dst[f] = v;
+  }
+}
+
+__global__ __launch_bounds__(256) void lora_grad_reduce_kernel(GradArgs a) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)a.total_cols * kRank) return;
+  const int col = (int)(i / kRank), k = (int)(i % kRank);
+  const GradJob& jb = a.job[grad_job(a, col)];
+  const int c = col - jb.col0;
+  if (c >= jb.ncols) return;
+  float v = 0.f;
+#pragma unroll 8
+  for (int ch = 0; ch < a.nchunks; ++ch) v += a.part[(int64_t)ch * a.total_cols * kRank + i];
+  v *= jb.scale;
+  jb.out[jb.trans ? (int64_t)k * jb.ncols + c : (int64_t)c * kRank + k] = v;
+}
+
+int64_t grad_pad(int64_t c) { return qlora_cdiv(c, kGradCols) * kGradCols; }
+
+int64_t grad_workspace(int64_t n, int N_q, int N_v, int H) {
+  const int64_t cols = grad_pad(N_q) + grad_pad(N_v) + 2 * grad_pad(H);
+  return qlora_cdiv(n, kGradChunk) * cols * kRank;
+}
+
 }  // namespace lora
 }  // namespace qlora
 
@@ -201,4 +353,54 @@ QLORA_API int qlora_lora_bwd_rows(const void* g_q, const void* g_v, int64_t ldg,
   a.s = s;
   a.scale = 1;
   return launch(a, (hipStream_t)stream);
+}
+
+// Workspace (fp32 elements) qlora_lora_grad needs for these sizes.
+QLORA_API int qlora_lora_grad_workspace(int64_t n, int32_t N_q, int32_t N_v, int32_t H,
+                                        int64_t* elems) {
+  QLORA_CHECK_ARG(n >= 0 && N_q > 0 && N_v > 0 && H > 0 && elems);
+  *elems = grad_workspace(n, N_q, N_v, H);
+  return 0;
+}
+
+// dB_a = s g_a^T x_a fp32 [N_a, 16], dA_a = dx_a^T a_a fp32 [16, H] for a = q, v (zeros for n = 0).
+QLORA_API int qlora_lora_grad(const void* g_q, const void* g_v, int64_t ldg, const void* x_q,
+                              const void* x_v, const void* a_q, const void* a_v,
+                              const void* dx_q, const void* dx_v, float* dB_q, float* dB_v,
+                              float* dA_q, float* dA_v, int64_t n, int32_t N_q, int32_t N_v,
+                              int32_t H, int32_t r, float s, float* work, int64_t work_elems,
+                              void* stream) {
+  QLORA_CHECK_ARG(n >= 0 && N_q > 0 && N_v > 0 && H > 0 && r == kRank);
+  QLORA_CHECK_ARG(N_q % 2 == 0 && N_v % 2 == 0 && H % 2 == 0 && ldg % 2 == 0);
+  QLORA_CHECK_ARG(ldg >= N_q && ldg >= N_v);
+  QLORA_CHECK_ARG(dB_q && dB_v && dA_q && dA_v);
+  QLORA_CHECK_ARG(work_elems >= grad_workspace(n, N_q, N_v, H) && (n == 0 || work));
+  if (n > 0) {
+    QLORA_CHECK_ARG(g_q && g_v && x_q && x_v && a_q && a_v && dx_q && dx_v);
+    QLORA_CHECK_ARG(aligned(g_q, 4) && aligned(g_v, 4) && aligned(a_q, 4) && aligned(a_v, 4));
+    QLORA_CHECK_ARG(aligned(work, 16));
+  }
+  GradArgs a{};
+  int col = 0;
+  const void* W[4] = {g_q, g_v, a_q, a_v};
+  const void* Z[4] = {x_q, x_v, dx_q, dx_v};
+  float* out[4] = {dB_q, dB_v, dA_q, dA_v};
+  const int64_t ldw[4] = {ldg, ldg, H, H};
+  const int nc[4] = {N_q, N_v, H, H};
+  for (int j = 0; j < 4; ++j) {
+    a.job[j] = GradJob{static_cast<const uint16_t*>(W[j]), static_cast<const uint16_t*>(Z[j]),
+                       out[j], ldw[j], nc[j], j >= 2, col, j < 2 ? s : 1.f};
+    col += (int)grad_pad(nc[j]);
+  }
+  a.part = work;
+  a.n = n;
+  a.total_cols = col;
+  a.nchunks = (int)qlora_cdiv(n, kGradChunk);
+  hipStream_t st = (hipStream_t)stream;
+  if (n > 0)
+    hipLaunchKernelGGL(lora_grad_part_kernel, dim3(col / kGradCols, a.nchunks),
+                       dim3(kGradThreads), 0, st, a);
+  hipLaunchKernelGGL(lora_grad_reduce_kernel, dim3((unsigned)qlora_cdiv((int64_t)col * kRank, 256)),
+                     dim3(256), 0, st, a);
+  return qlora_launch_status();
 }

@@ -19,10 +19,11 @@ import math
 
 import torch
 
+from . import gemm as G
 from . import linear as L
 from .ops import (NF4Group, NF4Weight, TorchDropout, _attn_bwd, _attn_fwd, _ce, _glu_bwd,
-                  _glu_fwd, _lora_bwd_rows, _lora_fwd_rows, _rms_bwd, _rms_fwd, _rope_bwd,
-                  _rope_fwd)
+                  _glu_fwd, _lora_bwd_rows, _lora_fwd_rows, _lora_grad, _rms_bwd, _rms_fwd,
+                  _rope_bwd, _rope_fwd)
 from .quant import quantize_nf4
 
 
@@ -321,22 +322,14 @@ class _Layer(torch.autograd.Function):
         need_dh = ctx.needs_input_grad[0]
         da = L.nf4_linear_t(dqkv, spec.qkv) if need_dh else None
         # LoRA (engine.py:1319-1331): dx = s g B and t = dx A per token in one kernel for both
-        # adapters; the token reductions dB = s g^T x and dA = dx^T drop(a) as fp32 products
+        # adapters; the token reductions dB = s g^T x and dA = dx^T drop(a) of both in another
         qc, vc = slice(0, HQ * D), slice((HQ + HKV) * D, C)
         lt = packed.lora16t(spec.index, lora16)
         dxq, dxv, tq, tv = _lora_bwd_rows(dqkv, qc, vc, lt[0], lt[1], lt[2], lt[3], s,
                                           need_t=need_dh)
-        grads = {}
-        for short, cols, dx in (("q", qc, dxq), ("v", vc, dxv)):
-            x_lo, a_in = f.pop("x" + short), f.pop("a" + short)
-            g = dqkv[:, cols]
-            db_w = torch.addmm(torch.empty((g.shape[1], x_lo.shape[1]), device=g.device,
-                                           dtype=torch.float32), g.t(), x_lo, beta=0.0,
-                               alpha=s, out_dtype=torch.float32)
-            da_w = torch.mm(dx.t(), a_in, out_dtype=torch.float32)
-            grads[short] = (da_w, db_w)
-        grads["q"] += (tq,)
-        grads["v"] += (tv,)
+        dA_q, dB_q, dA_v, dB_v = _lora_grad(dqkv, qc, vc, f.pop("xq"), f.pop("xv"),
+                                            f.pop("aq"), f.pop("av"), dxq, dxv, s)
+        grads = {"q": (dA_q, dB_q, tq), "v": (dA_v, dB_v, tv)}
         del dqkv
         dh = None
         if need_dh:
@@ -430,6 +423,7 @@ class FusedQwen2:
         self.device = torch.device(device)
         self.keep_all = keep_all
         self.memory_cap = None
+        self.autotune = True  # time the projections' GEMM solutions for each new token bucket
         self.dropout_p = cfg.lora_dropout
         self.rope = RopeTable(cfg.rope_theta, cfg.head_dim, self.device)
         self.dropout = TorchDropout(self.device, torch.float32) if self.dropout_p > 0 else None
@@ -496,10 +490,26 @@ class FusedQwen2:
         per_layer = max(1, self.kept_bytes_per_layer(n))
         return int(max(0, min(len(self.layers), free // per_layer)))
 
+    def gemm_shapes(self):
+        """(op, N, K) of the projections' GEMMs: y = x W^T for qkv, o, gate|up, down and
+        dX = dY W for the same four weights."""
+        spec = self.layers[0]
+        H, I, qkv, o = spec.H, spec.I, (spec.HQ + 2 * spec.HKV) * spec.D, spec.HQ * spec.D
+        fwd = [(qkv, H), (H, o), (2 * I, H), (H, I)]
+        return ([(G.NT, n, k) for n, k in fwd] +
+                [(G.NN, k, n) for n, k in fwd])
+
+    def tune_gemms(self, token_counts, log=None):
+        """Measure the projections' GEMM solutions for the buckets of these step sizes (tokens);
+        returns the seconds spent."""
+        return G.tune(self.gemm_shapes(), list(token_counts), self.device, log=log)
+
     def step(self, input_ids, attention_mask, labels, denom):
         """The step's forward: (loss, packed, stats); autograd runs the backward."""
         packed = Packed(input_ids, attention_mask, labels, self.rope, self.dropout,
                         self.dropout_p)
+        if self.autotune:
+            self.tune_gemms([packed.n])
         if self.dropout is not None and self.dropout.ok is None:
             self.dropout.ok = self.dropout.check(packed.rows,
                                                  min(packed.T, TorchDropout.CHECK_TOKENS),

@@ -6,12 +6,14 @@ Backend "fused": qlora_nf4_gemm, the NF4 decode inside the MFMA GEMM's B-operand
 loader, with the epilogues the step needs (qkv bias, the SwiGLU of gate|up, the residual add
 after down_proj, fp32 gradients rounded to fp16 on load).
 Backend "dequant" (default while it is the faster one): the standalone dequant kernel into an
-fp16 buffer, then hipBLASLt through torch - the reference's own structure (dequant, then cuBLAS).
+fp16 buffer, then a plain GEMM (gemm.mm: rocBLAS with a measured solution per shape and token
+bucket, or torch's matmul where that is the faster) - the reference's own structure (dequant,
+then cuBLAS).
 """
 
 import torch
 
-from . import _lib
+from . import _lib, gemm
 from .ops import NF4Group, _need, _ptr, _resid_add, _stream, dequant, dequant_many
 
 BACKEND = "dequant"
@@ -161,10 +163,7 @@ def nf4_linear(x, w, bias=None):
     """Y = X W^T [+ bias], fp16 [M, N]."""
     if BACKEND == "fused":
         return nf4_gemm(x, w, 0, epi=1 if bias is not None else 0, bias=bias)
-    wd = dequantize(w)
-    if bias is not None:
-        return torch.addmm(bias, x, wd.t())
-    return x @ wd.t()
+    return gemm.mm(x, dequantize(w), gemm.NT, bias=bias)
 
 
 def nf4_linear_swiglu(x, w, I):
@@ -189,7 +188,7 @@ def nf4_linear_t(dy, w):
         return nf4_gemm(dy, w, 1)
     if dy.dtype != torch.float16:
         dy = dy.to(torch.float16)
-    return dy @ dequantize(w)
+    return gemm.mm(dy, dequantize(w), gemm.NN)
 
 
 def linear(x, w):

@@ -8,6 +8,8 @@ its state tensors. Inputs are checked (device, dtype, shape, contiguity) before 
 CPU tensor is refused: there is no CPU path.
 """
 
+import ctypes
+
 import torch
 
 from . import _lib
@@ -535,6 +537,41 @@ def _lora_bwd_rows(dqkv, q_cols, v_cols, at_q, bt_q, at_v, bt_v, scale, need_t=T
                   dqkv.stride(0), _ptr(bt_q), _ptr(bt_v), _ptr(at_q), _ptr(at_v), _ptr(dx_q),
                   _ptr(dx_v), _ptr(t_q), _ptr(t_v), n, Nq, Nv, H, r, float(scale), _stream(dev))
     return dx_q, dx_v, t_q, t_v
+
+
+def _lora_grad(dqkv, q_cols, v_cols, x_q, x_v, a_q, a_v, dx_q, dx_v, scale):
+    """(dA_q, dB_q, dA_v, dB_v) fp32 of the q and v adapters: dB = s g^T x [N, r] and
+    dA = dx^T a [r, H], g the adapter's columns of dqkv (engine.py:1327, 1329), in two launches
+    for all four (fp32 sums of exact products, no fp16 rounding of the results)."""
+    _need(dqkv, "dqkv", torch.float16, contiguous=False)
+    n, C = dqkv.shape
+    dev = dqkv.device
+    if dqkv.stride(1) != 1:
+        raise ValueError("dqkv must have unit column stride")
+    for t, name in ((x_q, "x_q"), (x_v, "x_v"), (a_q, "a_q"), (a_v, "a_v"), (dx_q, "dx_q"),
+                    (dx_v, "dx_v")):
+        _need(t, name, torch.float16, dev)
+    r = x_q.shape[1]
+    H = a_q.shape[1]
+    Nq, Nv = q_cols.stop - q_cols.start, v_cols.stop - v_cols.start
+    for t, shape in ((x_q, (n, r)), (x_v, (n, r)), (dx_q, (n, r)), (dx_v, (n, r)),
+                     (a_q, (n, H)), (a_v, (n, H))):
+        if t.shape != shape:
+            raise ValueError(f"expected {shape}, got {tuple(t.shape)}")
+    f32 = torch.float32
+    dB_q, dB_v = torch.empty((Nq, r), device=dev, dtype=f32), torch.empty((Nv, r), device=dev,
+                                                                             dtype=f32)
+    dA_q, dA_v = torch.empty((r, H), device=dev, dtype=f32), torch.empty((r, H), device=dev,
+                                                                           dtype=f32)
+    elems = ctypes.c_int64(0)
+    _lib.call("qlora_lora_grad_workspace", n, Nq, Nv, H, ctypes.byref(elems))
+    work = torch.empty((max(elems.value, 1),), device=dev, dtype=f32)
+    base = dqkv.data_ptr()
+    _lib.call("qlora_lora_grad", base + 2 * q_cols.start, base + 2 * v_cols.start,
+              dqkv.stride(0), _ptr(x_q), _ptr(x_v), _ptr(a_q), _ptr(a_v), _ptr(dx_q), _ptr(dx_v),
+              _ptr(dB_q), _ptr(dB_v), _ptr(dA_q), _ptr(dA_v), n, Nq, Nv, H, r, float(scale),
+              _ptr(work), work.numel(), _stream(dev))
+    return dA_q, dB_q, dA_v, dB_v
 
 
 # ---------------------------------------------------------------------------------------------

@@ -212,6 +212,27 @@ int qlora_nf4_gemm(const void* a, int64_t lda, int32_t a_f32, const void* packed
 int qlora_resid_add(const float* a, const void* d, float* out, int64_t numel, void* stream);
 
 /*
+ * Row-major fp16 GEMM, fp32 accumulation, through rocBLAS with an explicit Tensile solution:
+ *   C[M, N] = alpha * A[M, K] op(B) + beta * C,  op = 0: B [N, K] (C = A B^T), op = 1: B [K, N].
+ * Leading dimensions in elements; solution 0 = rocBLAS's own choice, > 0 an index returned by
+ * qlora_gemm_solutions for the same problem. Replaces the frozen projections' torch matmuls:
+ * y = x W^T (engine.py:1082, 1112, 1135, 1156) and dX = dY W (engine.py:1239, 1293, 1301, 1316).
+ * Returns 100000 + rocblas_status on a rocBLAS error.
+ */
+int qlora_gemm(int32_t op, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
+               const void* B, int64_t ldb, void* C, int64_t ldc, float alpha, float beta,
+               int32_t solution, void* stream);
+
+/*
+ * The rocBLAS solution indices that can run the qlora_gemm problem with these sizes: up to cap of
+ * them into list, their total number into *count (no kernel is launched; the pointers are the
+ * problem's buffers). No reference counterpart: the tuning step of the projections above.
+ */
+int qlora_gemm_solutions(int32_t op, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
+                         const void* B, int64_t ldb, void* C, int64_t ldc, int32_t* list,
+                         int32_t cap, int32_t* count);
+
+/*
  * The LoRA forward of a layer's q and v adapters in one launch (engine.py:1088-1093):
  *   x_a = f16(a_a A_a^T)   f16 [n, 16] (kept for the backward)
  *   l_a = f16(x_a B_a^T)   f16 [n, N_a] (added to the projection output by qlora_rope_fwd)
@@ -230,14 +251,30 @@ int qlora_lora_fwd_rows(const void* a_q, const void* a_v, const void* A_q, const
  * g_q / g_v: the adapters' columns of the fused d[q|k|v] gradient (f16, row stride ldg);
  * Bt_a = B_a^T f16 [16, N_a]; At_a = A_a^T f16 [H, 16] (the transposed adapter weights);
  * t_q/t_v may both be null (then not computed). Replaces `dx_lo = (g @ b_w) * s` and
- * `dx_lo @ a_w` (engine.py:1326-1330) for both adapters; the token reductions dB and dA stay
- * products. Requires r == 16, N_a % 16 == 0, H % 32 == 0, ldg % 8 == 0; g_a, Bt_a, At_a 16-byte
- * and t_a 8-byte aligned.
+ * `dx_lo @ a_w` (engine.py:1326-1330) for both adapters; the token reductions dB and dA are
+ * qlora_lora_grad. Requires r == 16, N_a % 16 == 0, H % 32 == 0, ldg % 8 == 0; g_a, Bt_a,
+ * At_a 16-byte and t_a 8-byte aligned.
  */
 int qlora_lora_bwd_rows(const void* g_q, const void* g_v, int64_t ldg, const void* Bt_q,
                         const void* Bt_v, const void* At_q, const void* At_v, void* dx_q,
                         void* dx_v, void* t_q, void* t_v, int64_t n, int32_t N_q, int32_t N_v,
                         int32_t H, int32_t r, float s, void* stream);
+
+/*
+ * Token reductions of the LoRA backward of a layer's q and v adapters (engine.py:1327, 1329):
+ *   dB_a = s * g_a^T x_a   fp32 [N_a, 16]        dA_a = dx_a^T a_a   fp32 [16, H]
+ * g_q / g_v as in qlora_lora_bwd_rows (row stride ldg); x_a f16 [n, 16] (qlora_lora_fwd_rows);
+ * a_a f16 [n, H] (the dropped LoRA inputs); dx_a f16 [n, 16] (qlora_lora_bwd_rows). fp32 sums
+ * of exact products, reduced in a fixed order (deterministic); the reference rounds dB and dA
+ * to fp16 before its `.float()`, these keep fp32. work: fp32 workspace of at least the
+ * qlora_lora_grad_workspace size. n = 0 writes zeros. Requires r == 16; N_a, H, ldg even.
+ */
+int qlora_lora_grad_workspace(int64_t n, int32_t N_q, int32_t N_v, int32_t H, int64_t* elems);
+int qlora_lora_grad(const void* g_q, const void* g_v, int64_t ldg, const void* x_q,
+                    const void* x_v, const void* a_q, const void* a_v, const void* dx_q,
+                    const void* dx_v, float* dB_q, float* dB_v, float* dA_q, float* dA_v,
+                    int64_t n, int32_t N_q, int32_t N_v, int32_t H, int32_t r, float s,
+                    float* work, int64_t work_elems, void* stream);
 
 /*
  * Causal attention within each packed sequence (flash attention, online softmax), grouped-query

@@ -89,3 +89,15 @@ def test_invalid_arguments_rejected_before_launch(pkg):
     assert lib.qlora_glu_fwd(None, None, -1, 8, None) == 1
     assert lib.qlora_nf4_dequant(None, None, None, None, None, None, None, 4, 0, 1, 6, 256,
                                  0, 0, None) == 1
+
+
+def test_gemm_rejects_bad_problems_before_any_device_call(pkg):
+    """qlora_gemm / qlora_gemm_solutions check op, sizes and leading dimensions on the host."""
+    import ctypes
+    lib = pkg._lib.load()
+    cnt = ctypes.c_int32(0)
+    for op, M, N, K, lda in ((2, 4, 4, 4, 4), (0, 0, 4, 4, 4), (0, 4, 4, -1, 4), (0, 4, 4, 8, 4)):
+        assert lib.qlora_gemm_solutions(op, M, N, K, 8, lda, 8, max(K, N), 8, N, None, 0,
+                                        ctypes.byref(cnt)) == 1
+        assert lib.qlora_gemm(op, M, N, K, 8, lda, 8, max(K, N), 8, N, 1.0, 0.0, 0, None) == 1
+    assert lib.qlora_error_string(100000 + 3) != lib.qlora_error_string(3)

@@ -1,0 +1,85 @@
+"""The projections' plain GEMMs through qlora_gemm (rocBLAS with an explicit solution) against an
+fp64 product of the same fp16 operands: every solution computes fp16(sum in fp32), so results
+agree with fp64 to fp16 rounding plus fp32 summation-order noise."""
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def ref(a, b, op, bias=None):
+    bd = b.double()
+    r = a.double() @ (bd.t() if op == 0 else bd)
+    if bias is not None:
+        r = r + bias.double()
+    return r
+
+
+def check(out, want):
+    # one fp16 rounding of the fp32 sum: |err| <= 2^-11 |x| + accumulation noise
+    err = (out.double() - want).abs()
+    tol = want.abs() * 2.0**-10 + 1e-3 * want.abs().max()
+    assert bool((err <= tol).all()), float((err - tol).max())
+
+
+@pytest.mark.parametrize("op", [0, 1])
+@pytest.mark.parametrize("M,N,K", [(1, 256, 128), (37, 384, 200), (600, 1536, 1536),
+                                   (2537, 2048, 1536)])
+def test_gemm_default_and_listed_solutions(pkg, op, M, N, K):
+    g = torch.Generator(device=DEV).manual_seed(M + N + K + op)
+    a = torch.randn((M, K), device=DEV, generator=g).half()
+    b = (torch.randn((N, K) if op == 0 else (K, N), device=DEV, generator=g) * 0.05).half()
+    want = ref(a, b, op)
+    sols = pkg.gemm.solutions(op, a, b, torch.empty((M, N), device=DEV, dtype=torch.float16))
+    assert len(sols) > 0
+    for sol in [0] + sols[:: max(1, len(sols) // 6)]:
+        out = torch.full((M, N), float("nan"), device=DEV, dtype=torch.float16)
+        pkg.gemm._run(sol, op, a, b, out, 1.0, 0.0, M, N, K, K, b.stride(0), N, a.device)
+        check(out, want)
+
+
+def test_gemm_strided_views_alpha_beta(pkg):
+    """Row strides larger than the width (column slices of wider buffers), alpha and beta."""
+    g = torch.Generator(device=DEV).manual_seed(5)
+    M, N, K = 300, 256, 320
+    abuf = torch.randn((M, K + 64), device=DEV, generator=g).half()
+    bbuf = (torch.randn((N, K + 32), device=DEV, generator=g) * 0.05).half()
+    cbuf = torch.randn((M, N + 128), device=DEV, generator=g).half()
+    a, b, c = abuf[:, 16:16 + K], bbuf[:, :K], cbuf[:, 64:64 + N]
+    c0, outside = c.clone(), cbuf[:, :64].clone()
+    pkg._lib.call("qlora_gemm", 0, M, N, K, a.data_ptr(), a.stride(0), b.data_ptr(), b.stride(0),
+                  c.data_ptr(), c.stride(0), 0.5, 2.0, 0, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    check(c, 0.5 * ref(a, b, 0) + 2.0 * c0.double())
+    assert torch.equal(cbuf[:, :64], outside)  # columns outside the view are not written
+
+
+def test_mm_bias_and_tuned_choice(pkg):
+    """gemm.mm with a tuned bucket (a rocBLAS solution or torch's matmul), with and without the
+    bias (one rounding of acc + bias), and at sizes of neighbouring buckets."""
+    G = pkg.gemm
+    G.reset()
+    try:
+        N, K = 512, 256
+        G.tune([(G.NT, N, K), (G.NN, K, N)], [700], DEV)
+        assert (0, G.NT, N, K, G._bucket(700)) in G._CHOICE
+        g = torch.Generator(device=DEV).manual_seed(9)
+        w = (torch.randn((N, K), device=DEV, generator=g) * 0.05).half()
+        bias = (torch.randn((N,), device=DEV, generator=g) * 0.1).half()
+        for M in (700, 650, 1, 1500):
+            x = torch.randn((M, K), device=DEV, generator=g).half()
+            check(G.mm(x, w, G.NT), ref(x, w, 0))
+            check(G.mm(x, w, G.NT, bias=bias), ref(x, w, 0, bias))
+            dy = torch.randn((M, N), device=DEV, generator=g).half()
+            check(G.mm(dy, w, G.NN), ref(dy, w, 1))
+        # force a rocBLAS solution for the bucket and check the bias path through it
+        sols = G.solutions(G.NT, x, w, torch.empty((x.shape[0], N), device=DEV,
+                                                   dtype=torch.float16))
+        G._CHOICE[(0, G.NT, N, K, G._bucket(x.shape[0]))] = sols[0]
+        check(G.mm(x, w, G.NT, bias=bias), ref(x, w, 0, bias))
+    finally:
+        G.reset()
+

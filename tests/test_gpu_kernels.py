@@ -453,3 +453,29 @@ def test_lora_fwd_rows(pkg, n, H, Nq, Nv):
         close(x, want, 2e-3 * want.abs().max().item())
         lw = (x.cpu().double() @ B.double().t()).half()
         close(l, lw, 2e-3 * lw.abs().max().item())
+
+
+@pytest.mark.parametrize("n,H,Nq,Nv", [(300, 1536, 1536, 256), (1, 1536, 1536, 256),
+                                       (129, 256, 256, 128), (4100, 896, 896, 128),
+                                       (0, 256, 256, 128)])
+def test_lora_grad(pkg, n, H, Nq, Nv):
+    """dB = s g^T x and dA = dx^T a of both adapters (engine.py:1327, 1329) against fp64 sums of
+    the same fp16 operands (fp32 accumulation: relative error ~ 1e-6 of the magnitudes)."""
+    g = torch.Generator().manual_seed(n + 7)
+    C = Nq + 2 * Nv
+    dqkv = torch.randn(n, C, generator=g).half()
+    xs = [torch.randn(n, 16, generator=g).half() for _ in range(4)]  # x_q, x_v, dx_q, dx_v
+    aq = torch.randn(n, H, generator=g).half()
+    av = torch.randn(n, H, generator=g).half()
+    s = 2.0
+    qc, vc = slice(0, Nq), slice(Nq + Nv, C)
+    d = [t.to(DEV) for t in (dqkv, *xs, aq, av)]
+    dA_q, dB_q, dA_v, dB_v = pkg.ops._lora_grad(d[0], qc, vc, d[1], d[2], d[5], d[6], d[3],
+                                                d[4], s)
+    for got, want in ((dB_q, s * dqkv[:, qc].double().t() @ xs[0].double()),
+                      (dB_v, s * dqkv[:, vc].double().t() @ xs[1].double()),
+                      (dA_q, xs[2].double().t() @ aq.double()),
+                      (dA_v, xs[3].double().t() @ av.double())):
+        assert got.dtype == torch.float32 and got.shape == want.shape
+        scale = max(1.0, math.sqrt(max(n, 1))) * 8
+        close(got, want, 1e-5 * scale)
