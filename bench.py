@@ -241,7 +241,8 @@ def main():
     print("[bench] model built; timing the projection GEMM solutions", file=sys.stderr,
           flush=True)
     # every step size config 5 can produce (4 rows of 256..1024 tokens), before any timing
-    tune_s = model.tune_gemms(range(4 * 256, 4 * 1024 + 1, pkg.gemm.BUCKET))
+    tune_s = model.tune_gemms(range(4 * 256, 4 * 1024 + pkg.gemm.BUCKET, pkg.gemm.BUCKET),
+                              log=lambda m: print("[bench] " + m, file=sys.stderr, flush=True))
     print(f"[bench] GEMM tuning {tune_s:.1f} s; warmup {args.warmup}", file=sys.stderr,
           flush=True)
     for i in range(args.warmup):

@@ -97,24 +97,22 @@ __device__ __forceinline__ half8_t ld_g(const uint16_t* p) {
 // Staging of token-major global rows into LDS tiles, split into a load phase (all of a thread's
 // global loads issued back to back into registers, so their latencies overlap, and early enough
 // to hide behind the previous tile's MFMAs) and a store phase into the tile. The loads are
-// unconditional (rows past `valid` read row 0 of the block, then are zeroed): a load under a
-// branch is fenced by a wait for every load before it.
+// buffer loads over the sequence's rows of one head: rows past the sequence read zeros, so
+// there is neither a clamp nor a select on the loaded value (which the compiler may turn into a
+// branch around the load, whose join then waits for every load in flight).
 //
-// RowStage: rows [0, ROWS) of a token-major matrix (row stride `stride` elements) into a
-// [ROWS][D] tile; rows >= valid are zero.
+// Offsets are bytes from the resource base: row r at r * stride_b, chunk c (8 halves) at 16 c.
+//
+// RowStage: rows [row0, row0 + ROWS) into a [ROWS][D] tile.
 template <int D, int ROWS, int NT>
 struct RowStage {
   static constexpr int CPR = D / 8, TOTAL = ROWS * CPR, CNT = (TOTAL + NT - 1) / NT;
   uint4 r[CNT];
-  __device__ __forceinline__ void load(const uint16_t* base, int64_t stride, int valid,
-                                       int tid) {
+  __device__ __forceinline__ void load(rsrc_t src, int row0, int stride_b, int tid) {
 #pragma unroll
     for (int i = 0; i < CNT; ++i) {
-      const int id = tid + i * NT, row = id / CPR, c = id % CPR;
-      const bool ok = id < TOTAL && row < valid;
-      const uint4 x =
-          *reinterpret_cast<const uint4*>(base + (int64_t)(ok ? row : 0) * stride + c * 8);
-      r[i] = ok ? x : make_uint4(0, 0, 0, 0);
+      const int id = tid + i * NT, row = id / CPR, c = id % CPR;  // id >= TOTAL: not stored
+      r[i] = buf_load16(src, (uint32_t)((row0 + row) * stride_b + c * 16));
     }
   }
   __device__ __forceinline__ void store(uint16_t* tile, int tid) const {
@@ -130,25 +128,19 @@ __device__ __forceinline__ uint32_t word_of(const uint4& x, int i) {
   return i < 2 ? (i == 0 ? x.x : x.y) : (i == 2 ? x.z : x.w);
 }
 
-// PairStage: rows [0, S) into the transposed [D][S] tile, token t at slot
+// PairStage: rows [row0, row0 + S) into the transposed [D][S] tile, token t at slot
 // (t & ~15) | perm16(t & 15), and optionally also into the [S][D] row tile. A work item is a
 // pair of rows x 8 columns (consecutive threads take consecutive column chunks of a row pair).
 template <int D, int S, int NT>
 struct PairStage {
   static constexpr int CPR = D / 8, TOTAL = (S / 2) * CPR, CNT = (TOTAL + NT - 1) / NT;
   uint4 x[CNT], y[CNT];
-  __device__ __forceinline__ void load(const uint16_t* base, int64_t stride, int valid,
-                                       int tid) {
+  __device__ __forceinline__ void load(rsrc_t src, int row0, int stride_b, int tid) {
 #pragma unroll
     for (int i = 0; i < CNT; ++i) {
-      const int id = tid + i * NT, c = id % CPR, r0 = 2 * (id / CPR);
-      const bool ok0 = id < TOTAL && r0 < valid, ok1 = id < TOTAL && r0 + 1 < valid;
-      const uint4 a =
-          *reinterpret_cast<const uint4*>(base + (int64_t)(ok0 ? r0 : 0) * stride + c * 8);
-      const uint4 b =
-          *reinterpret_cast<const uint4*>(base + (int64_t)(ok1 ? r0 + 1 : 0) * stride + c * 8);
-      x[i] = ok0 ? a : make_uint4(0, 0, 0, 0);
-      y[i] = ok1 ? b : make_uint4(0, 0, 0, 0);
+      const int id = tid + i * NT, c = id % CPR, r0 = row0 + 2 * (id / CPR);
+      x[i] = buf_load16(src, (uint32_t)(r0 * stride_b + c * 16));
+      y[i] = buf_load16(src, (uint32_t)((r0 + 1) * stride_b + c * 16));
     }
   }
   __device__ __forceinline__ void store(uint16_t* tr, uint16_t* rows, int tid) const {
@@ -172,6 +164,22 @@ struct PairStage {
     }
   }
 };
+
+// A resource over rows [0, L) of one head of a token-major [*, stride] fp16 matrix starting at
+// `base` (the sequence's first row, this head's first column).
+__device__ __forceinline__ rsrc_t rows_rsrc(const uint16_t* base, int L, int64_t stride, int D) {
+  return make_rsrc(base, L > 0 ? (uint32_t)(((int64_t)(L - 1) * stride + D) * 2) : 0u);
+}
+
+// One token's D/16 MFMA operands (chunks 2 kk + l/32 of row `row`) from a row resource.
+template <int D>
+__device__ __forceinline__ void load_token(rsrc_t src, int row, int stride_b, int lane,
+                                           half8_t (&out)[D / 16]) {
+#pragma unroll
+  for (int kk = 0; kk < D / 16; ++kk)
+    out[kk] = __builtin_bit_cast(
+        half8_t, buf_load16(src, (uint32_t)(row * stride_b + (2 * kk + (lane >> 5)) * 16)));
+}
 
 // 8 accumulator values (registers 8 * half .. + 7 of acc) as an fp16 B operand.
 __device__ __forceinline__ half8_t to_b(const f32x16& acc, int half) {
@@ -216,34 +224,29 @@ __global__ __launch_bounds__(64 * G) void attn_fwd_kernel(Args a) {
   const int start = a.cu[seq], L = a.cu[seq + 1] - start;
   if (q0 >= L) return;
   const int tid = threadIdx.x, lane = tid & 63;
-  const int h = kvh * G + (tid >> 6);
+  const int h = kvh * G + __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int qi = q0 + (lane & 31);
-  const bool qok = qi < L;
   const int64_t qs = (int64_t)a.HQ * D, kvs = (int64_t)a.KH * D;
+  const int kvs_b = (int)(kvs * 2);
   const int kend = min(q0 + kTok, L);
   const int nkb = (kend + kKB - 1) / kKB;
-  const uint16_t* kbase = a.k + (int64_t)start * kvs + kvh * D;
-  const uint16_t* vbase = a.v + (int64_t)start * kvs + kvh * D;
+  const rsrc_t ksrc = rows_rsrc(a.k + (int64_t)start * kvs + kvh * D, L, kvs, D);
+  const rsrc_t vsrc = rows_rsrc(a.v + (int64_t)start * kvs + kvh * D, L, kvs, D);
 
   RowStage<D, kKB, NT> sk;
   PairStage<D, kKB, NT> sv;
-  sk.load(kbase, kvs, min(kKB, L), tid);
-  sv.load(vbase, kvs, min(kKB, L), tid);
+  sk.load(ksrc, 0, kvs_b, tid);
+  sv.load(vsrc, 0, kvs_b, tid);
 
-  half8_t qr[KC];
-  {
-    const uint16_t* p = a.q + (int64_t)(start + (qok ? qi : 0)) * qs + h * D + 8 * (lane >> 5);
-#pragma unroll
-    for (int kk = 0; kk < KC; ++kk) {
-      const half8_t x = ld_g(p + 16 * kk);
-      qr[kk] = qok ? x : half8_t{};
-    }
-  }
+  half8_t qr[KC];  // queries past the sequence read zeros (their rows are not stored)
+  load_token<D>(rows_rsrc(a.q + (int64_t)start * qs + h * D, L, qs, D), qi, (int)(qs * 2), lane,
+                qr);
   f32x16 o[DT];
 #pragma unroll
   for (int u = 0; u < DT; ++u) o[u] = f32x16{};
   float m = -__builtin_inff(), lsum = 0.f;
   const float c = a.scale * kLog2e;
+  const int lim = min(qi, L - 1);  // the last key this query attends to
 
   for (int kb = 0; kb < nkb; ++kb) {
     const int k0 = kb * kKB;
@@ -251,30 +254,25 @@ __global__ __launch_bounds__(64 * G) void attn_fwd_kernel(Args a) {
     sk.store(ks, tid);
     sv.store(vt, nullptr, tid);
     __syncthreads();
-    if (kb + 1 < nkb) {
-      const int nvalid = min(kKB, L - k0 - kKB);
-      sk.load(kbase + (int64_t)(k0 + kKB) * kvs, kvs, nvalid, tid);
-      sv.load(vbase + (int64_t)(k0 + kKB) * kvs, kvs, nvalid, tid);
-    }
+    // the next block (past the sequence: zeros, not used)
+    sk.load(ksrc, k0 + kKB, kvs_b, tid);
+    sv.load(vsrc, k0 + kKB, kvs_b, tid);
     f32x16 s[2];
+    s[0] = s[1] = f32x16{};
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      s[t] = f32x16{};
-#pragma unroll
-      for (int kk = 0; kk < KC; ++kk)
-        s[t] = mfma(ld_rm<D>(ks, 32 * t + (lane & 31), 2 * kk + (lane >> 5)), qr[kk], s[t]);
+    for (int kk = 0; kk < KC; ++kk) {
+      const half8_t k0op = ld_rm<D>(ks, lane & 31, 2 * kk + (lane >> 5));
+      const half8_t k1op = ld_rm<D>(ks, 32 + (lane & 31), 2 * kk + (lane >> 5));
+      s[0] = mfma(k0op, qr[kk], s[0]);
+      s[1] = mfma(k1op, qr[kk], s[1]);
     }
-    const bool mask = k0 + kKB - 1 > q0 || k0 + kKB > L;
     float mx = -__builtin_inff();
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        float x = s[t][r] * c;
-        if (mask) {
-          const int key = k0 + 32 * t + acc_row(r, lane);
-          if (key > qi || key >= L) x = -__builtin_inff();
-        }
+        const int key = k0 + 32 * t + acc_row(r, lane);
+        const float x = key > lim ? -__builtin_inff() : s[t][r] * c;
         s[t][r] = x;
         mx = fmaxf(mx, x);
       }
@@ -300,13 +298,17 @@ __global__ __launch_bounds__(64 * G) void attn_fwd_kernel(Args a) {
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) pb[kk] = to_b(s[kk >> 1], kk & 1);
 #pragma unroll
-    for (int u = 0; u < DT; ++u)
+    for (int u = 0; u < DT; ++u) {
+      half8_t vop[4];
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk)
-        o[u] = mfma(ld_tr<kKB>(vt, 32 * u + (lane & 31), 2 * kk + (lane >> 5)), pb[kk], o[u]);
+        vop[kk] = ld_tr<kKB>(vt, 32 * u + (lane & 31), 2 * kk + (lane >> 5));
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) o[u] = mfma(vop[kk], pb[kk], o[u]);
+    }
   }
   const float ltot = lsum + __shfl_xor(lsum, 32, 64);
-  if (qok) {
+  if (qi < L) {
     store_token_row<D>(a.out + (int64_t)(start + qi) * qs + h * D, o, 1.0f / ltot, lane);
     if (lane < 32) a.lse[(int64_t)h * a.n + start + qi] = (m + log2f(ltot)) * kLn2;
   }
@@ -328,45 +330,42 @@ __global__ __launch_bounds__(64 * G) void attn_dq_kernel(Args a) {
   const int start = a.cu[seq], L = a.cu[seq + 1] - start;
   if (q0 >= L) return;
   const int tid = threadIdx.x, lane = tid & 63;
-  const int h = kvh * G + (tid >> 6);
+  const int h = kvh * G + __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int qi = q0 + (lane & 31);
-  const bool qok = qi < L;
   const int64_t qs = (int64_t)a.HQ * D, kvs = (int64_t)a.KH * D;
+  const int qs_b = (int)(qs * 2), kvs_b = (int)(kvs * 2);
   const int kend = min(q0 + kTok, L);
   const int nkb = (kend + KB - 1) / KB;
-  const uint16_t* kbase = a.k + (int64_t)start * kvs + kvh * D;
-  const uint16_t* vbase = a.v + (int64_t)start * kvs + kvh * D;
+  const rsrc_t ksrc = rows_rsrc(a.k + (int64_t)start * kvs + kvh * D, L, kvs, D);
+  const rsrc_t vsrc = rows_rsrc(a.v + (int64_t)start * kvs + kvh * D, L, kvs, D);
 
   PairStage<D, KB, NT> sk;  // K into both the row tile and the transposed tile
   RowStage<D, KB, NT> sv;
-  sk.load(kbase, kvs, min(KB, L), tid);
-  sv.load(vbase, kvs, min(KB, L), tid);
+  sk.load(ksrc, 0, kvs_b, tid);
+  sv.load(vsrc, 0, kvs_b, tid);
 
-  half8_t qr[KC], dr[KC];
+  // this query's q, dO and O (queries past the sequence read zeros; their dq is not stored)
+  const int64_t hoff = (int64_t)start * qs + h * D;
+  half8_t qr[KC], dr[KC], orow[KC];
+  load_token<D>(rows_rsrc(a.q + hoff, L, qs, D), qi, qs_b, lane, qr);
+  load_token<D>(rows_rsrc(a.dout + hoff, L, qs, D), qi, qs_b, lane, dr);
+  load_token<D>(rows_rsrc(a.o + hoff, L, qs, D), qi, qs_b, lane, orow);
+  const float lse2 =
+      buf_load_f32(make_rsrc(a.lse + (int64_t)h * a.n + start, (uint32_t)L * 4), qi * 4) *
+      kLog2e;
   float dpart = 0.f;
-  const int qc = qok ? qi : 0;
-  {
-    const int64_t off = (int64_t)(start + qc) * qs + h * D + 8 * (lane >> 5);
 #pragma unroll
-    for (int kk = 0; kk < KC; ++kk) {
-      const half8_t x = ld_g(a.q + off + 16 * kk), y = ld_g(a.dout + off + 16 * kk);
-      qr[kk] = qok ? x : half8_t{};
-      dr[kk] = qok ? y : half8_t{};
-      const half8_t ov = ld_g(a.o + off + 16 * kk);
+  for (int kk = 0; kk < KC; ++kk)
 #pragma unroll
-      for (int i = 0; i < 8; ++i) dpart += (float)dr[kk][i] * (float)ov[i];
-    }
-  }
-  // out-of-range queries: lse2 = inf makes P = 0
-  const float lse_q = a.lse[(int64_t)h * a.n + start + qc];
-  const float lse2 = qok ? lse_q * kLog2e : __builtin_inff();
+    for (int i = 0; i < 8; ++i) dpart += (float)dr[kk][i] * (float)orow[kk][i];
   const float delta = dpart + __shfl_xor(dpart, 32, 64);
-  if (qok && lane < 32) a.delta[(int64_t)h * a.n + start + qi] = delta;
+  if (qi < L && lane < 32) a.delta[(int64_t)h * a.n + start + qi] = delta;
 
   f32x16 dq[DT];
 #pragma unroll
   for (int u = 0; u < DT; ++u) dq[u] = f32x16{};
   const float c = a.scale * kLog2e;
+  const int lim = min(qi, L - 1);
 
   for (int kb = 0; kb < nkb; ++kb) {
     const int k0 = kb * KB;
@@ -374,38 +373,34 @@ __global__ __launch_bounds__(64 * G) void attn_dq_kernel(Args a) {
     sk.store(kt, ks, tid);
     sv.store(vs, tid);
     __syncthreads();
-    if (kb + 1 < nkb) {
-      const int nvalid = min(KB, L - k0 - KB);
-      sk.load(kbase + (int64_t)(k0 + KB) * kvs, kvs, nvalid, tid);
-      sv.load(vbase + (int64_t)(k0 + KB) * kvs, kvs, nvalid, tid);
-    }
+    sk.load(ksrc, k0 + KB, kvs_b, tid);
+    sv.load(vsrc, k0 + KB, kvs_b, tid);
     f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
     for (int kk = 0; kk < KC; ++kk) {
       const int row = lane & 31, ch = 2 * kk + (lane >> 5);
-      s = mfma(ld_rm<D>(ks, row, ch), qr[kk], s);
-      dp = mfma(ld_rm<D>(vs, row, ch), dr[kk], dp);
+      const half8_t kop = ld_rm<D>(ks, row, ch), vop = ld_rm<D>(vs, row, ch);
+      s = mfma(kop, qr[kk], s);
+      dp = mfma(vop, dr[kk], dp);
     }
-    const bool mask = k0 + KB - 1 > q0 || k0 + KB > L;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      float p = exp2f(s[r] * c - lse2);
-      if (mask) {
-        const int key = k0 + acc_row(r, lane);
-        if (key > qi || key >= L) p = 0.f;
-      }
+      const float e = exp2f(s[r] * c - lse2);
+      const float p = k0 + acc_row(r, lane) > lim ? 0.f : e;
       s[r] = p * (dp[r] - delta);
     }
     half8_t sb[2];
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) sb[kk] = to_b(s, kk);
 #pragma unroll
-    for (int u = 0; u < DT; ++u)
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-        dq[u] = mfma(ld_tr<KB>(kt, 32 * u + (lane & 31), 2 * kk + (lane >> 5)), sb[kk], dq[u]);
+    for (int u = 0; u < DT; ++u) {
+      const half8_t t0 = ld_tr<KB>(kt, 32 * u + (lane & 31), lane >> 5);
+      const half8_t t1 = ld_tr<KB>(kt, 32 * u + (lane & 31), 2 + (lane >> 5));
+      dq[u] = mfma(t0, sb[0], dq[u]);
+      dq[u] = mfma(t1, sb[1], dq[u]);
+    }
   }
-  if (qok) store_token_row<D>(a.out + (int64_t)(start + qi) * qs + h * D, dq, a.scale, lane);
+  if (qi < L) store_token_row<D>(a.out + (int64_t)(start + qi) * qs + h * D, dq, a.scale, lane);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -432,38 +427,35 @@ __global__ __launch_bounds__(64 * kKeyWaves) void attn_dkdv_kernel(Args a) {
   const int kw0 = blockIdx.y * kTok * kKeyWaves;
   const int start = a.cu[seq], L = a.cu[seq + 1] - start;
   if (kw0 >= L) return;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int k0 = kw0 + kTok * wave;
   const int kj = k0 + (lane & 31);
-  const bool kok = kj < L;
   const int64_t qs = (int64_t)a.HQ * D, kvs = (int64_t)a.KH * D;
-  const uint16_t* qbase = a.q + (int64_t)start * qs + h * D;
-  const uint16_t* dbase = a.dout + (int64_t)start * qs + h * D;
-  const float* lse = a.lse + (int64_t)h * a.n + start;
-  const float* dl = a.delta + (int64_t)h * a.n + start;
+  const int qs_b = (int)(qs * 2), kvs_b = (int)(kvs * 2);
+  const int64_t hoff = (int64_t)start * qs + h * D;
+  const rsrc_t qsrc = rows_rsrc(a.q + hoff, L, qs, D);
+  const rsrc_t dsrc = rows_rsrc(a.dout + hoff, L, qs, D);
+  const rsrc_t lsrc = make_rsrc(a.lse + (int64_t)h * a.n + start, (uint32_t)L * 4);
+  const rsrc_t dlsrc = make_rsrc(a.delta + (int64_t)h * a.n + start, (uint32_t)L * 4);
 
   PairStage<D, kTok, NT> sq, sd;
-  float lv = 0.f;  // threads 0..31: lse of query q0 + tid; 32..63: delta of q0 + tid - 32
+  float lv = 0.f;  // threads 0..31: lse (log2) of query q0 + tid; 32..63: delta of q0 + tid - 32
+  const float first = tid < kTok ? 1.f : 0.f;
   auto load = [&](int q0) {
-    const int valid = min(kTok, L - q0);
-    sq.load(qbase + (int64_t)q0 * qs, qs, valid, tid);
-    sd.load(dbase + (int64_t)q0 * qs, qs, valid, tid);
-    const int j = tid & (kTok - 1);
-    const bool ok = tid < 2 * kTok && j < valid;
-    const float x = (tid < kTok ? lse : dl)[q0 + (ok ? j : 0)];
-    lv = ok ? (tid < kTok ? x * kLog2e : x) : 0.f;
+    sq.load(qsrc, q0, qs_b, tid);
+    sd.load(dsrc, q0, qs_b, tid);
+    const uint32_t off = (uint32_t)(q0 + (tid & (kTok - 1))) * 4;
+    const float xl = buf_load_f32(lsrc, off), xd = buf_load_f32(dlsrc, off);
+    lv = fmaf(first, xl * kLog2e, (1.f - first) * xd);  // a blend, not a select of loads
   };
   load(kw0);
 
-  half8_t kr[KC], vr[KC];
+  half8_t kr[KC], vr[KC];  // keys past the sequence read zeros (their rows are not stored)
   {
-    const int64_t off = (int64_t)(start + (kok ? kj : 0)) * kvs + kvh * D + 8 * (lane >> 5);
-#pragma unroll
-    for (int kk = 0; kk < KC; ++kk) {
-      const half8_t x = ld_g(a.k + off + 16 * kk), y = ld_g(a.v + off + 16 * kk);
-      kr[kk] = kok ? x : half8_t{};
-      vr[kk] = kok ? y : half8_t{};
-    }
+    const int64_t koff = (int64_t)start * kvs + kvh * D;
+    load_token<D>(rows_rsrc(a.k + koff, L, kvs, D), kj, kvs_b, lane, kr);
+    load_token<D>(rows_rsrc(a.v + koff, L, kvs, D), kj, kvs_b, lane, vr);
   }
   f32x16 dk[DT], dv[DT];
 #pragma unroll
@@ -476,14 +468,15 @@ __global__ __launch_bounds__(64 * kKeyWaves) void attn_dkdv_kernel(Args a) {
     sd.store(dt, dsm, tid);
     if (tid < 2 * kTok) (tid < kTok ? lse_s : dl_s)[tid & (kTok - 1)] = lv;
     __syncthreads();
-    if (q0 + kTok < L) load(q0 + kTok);
+    load(q0 + kTok);  // the next block (past the sequence: zeros, not used)
     if (q0 + kTok <= k0 || k0 >= L) continue;  // every query of the block precedes these keys
     f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
     for (int kk = 0; kk < KC; ++kk) {
       const int row = lane & 31, ch = 2 * kk + (lane >> 5);
-      s = mfma(ld_rm<D>(qsm, row, ch), kr[kk], s);
-      dp = mfma(ld_rm<D>(dsm, row, ch), vr[kk], dp);
+      const half8_t qop = ld_rm<D>(qsm, row, ch), dop = ld_rm<D>(dsm, row, ch);
+      s = mfma(qop, kr[kk], s);
+      dp = mfma(dop, vr[kk], dp);
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -494,8 +487,8 @@ __global__ __launch_bounds__(64 * kKeyWaves) void attn_dkdv_kernel(Args a) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int r = 4 * j + i, qq = q0 + qr0 + i;
-        float p = 0.f;
-        if (qq < L && kj <= qq) p = exp2f(s[r] * c - lq[i]);
+        const float e = exp2f(s[r] * c - lq[i]);
+        const float p = (qq < L && kj <= qq) ? e : 0.f;
         s[r] = p;
         dp[r] = p * (dp[r] - dq4[i]);
       }
@@ -507,15 +500,18 @@ __global__ __launch_bounds__(64 * kKeyWaves) void attn_dkdv_kernel(Args a) {
       sb[kk] = to_b(dp, kk);
     }
 #pragma unroll
-    for (int u = 0; u < DT; ++u)
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        const int d = 32 * u + (lane & 31), ch = 2 * kk + (lane >> 5);
-        dv[u] = mfma(ld_tr<kTok>(dt, d, ch), pb[kk], dv[u]);
-        dk[u] = mfma(ld_tr<kTok>(qt, d, ch), sb[kk], dk[u]);
-      }
+    for (int u = 0; u < DT; ++u) {
+      const int d = 32 * u + (lane & 31);
+      const half8_t d0 = ld_tr<kTok>(dt, d, lane >> 5), d1 = ld_tr<kTok>(dt, d, 2 + (lane >> 5));
+      const half8_t q0op = ld_tr<kTok>(qt, d, lane >> 5);
+      const half8_t q1op = ld_tr<kTok>(qt, d, 2 + (lane >> 5));
+      dv[u] = mfma(d0, pb[0], dv[u]);
+      dk[u] = mfma(q0op, sb[0], dk[u]);
+      dv[u] = mfma(d1, pb[1], dv[u]);
+      dk[u] = mfma(q1op, sb[1], dk[u]);
+    }
   }
-  if (kok) {
+  if (kj < L) {
     const int64_t off = (int64_t)(start + kj) * qs + h * D;
     store_token_row<D>(a.dk + off, dk, a.scale, lane);
     store_token_row<D>(a.dv + off, dv, 1.0f, lane);
@@ -538,6 +534,8 @@ int check_common(int32_t nseq, int32_t max_len, int64_t n, int32_t HQ, int32_t K
   const int G = HQ / KH;
   QLORA_CHECK_ARG(G == 1 || G == 2 || G == 4 || G == 6);
   QLORA_CHECK_ARG((int64_t)nseq * HQ < (1ll << 31));
+  // buffer offsets within one sequence's rows (plus the prefetch past its end) fit 32 bits
+  QLORA_CHECK_ARG(((int64_t)max_len + 4 * kKB) * HQ * D * 2 < (1ll << 31));
   return 0;
 }
 

@@ -12,6 +12,12 @@
 // rocBLAS is column-major: the row-major C is the column-major C^T = op(B)^T A^T, so the call
 // is m = N, n = M, k = K with B as its first operand.
 //
+// Split-K (qlora_gemm_splitk): the reduction is cut into `splits` equal slices computed as one
+// strided-batched GEMM with fp32 outputs [splits][M][N] (a workspace), then summed in a fixed
+// order and rounded once to fp16 (plus an optional bias) by splitk_reduce_kernel - for the
+// products whose output is too small to fill the GPU with tiles (long K, narrow N: the
+// gate|up input gradient, the lm_head's).
+//
 // rocBLAS status codes are returned as kStatusBase + status, so they do not collide with HIP
 // error codes; qlora_error_string names both.
 #include "common.h"
@@ -126,4 +132,130 @@ QLORA_API int qlora_gemm_solutions(int32_t op, int64_t M, int64_t N, int64_t K, 
       rocblas_gemm_flags_none, list, &n));
 #pragma clang diagnostic pop
   return rc;
+}
+
+namespace qlora {
+namespace blas {
+
+// out[m][n] = fp16(sum_j work[j][m][n] (+ bias[n])), four columns per thread (N % 4 == 0).
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ work,
+                                                            int splits, int64_t M, int64_t N,
+                                                            uint16_t* out, int64_t ldc,
+                                                            const uint16_t* bias) {
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i >= M * N) return;
+  const int64_t m = i / N, n = i % N;
+  float4 acc = *reinterpret_cast<const float4*>(work + i);
+  for (int j = 1; j < splits; ++j) {
+    const float4 w = *reinterpret_cast<const float4*>(work + (int64_t)j * M * N + i);
+    acc.x += w.x;
+    acc.y += w.y;
+    acc.z += w.z;
+    acc.w += w.w;
+  }
+  if (bias != nullptr) {
+    acc.x += h2f_bits(bias[n]);
+    acc.y += h2f_bits(bias[n + 1]);
+    acc.z += h2f_bits(bias[n + 2]);
+    acc.w += h2f_bits(bias[n + 3]);
+  }
+  uint2 r;
+  r.x = pack2h(acc.x, acc.y);
+  r.y = pack2h(acc.z, acc.w);
+  *reinterpret_cast<uint2*>(out + m * ldc + n) = r;
+}
+
+struct Split {
+  Problem p;
+  rocblas_int kc;                 // K per slice
+  rocblas_stride sa, sb, sc;      // rocBLAS strides of its A (our B), B (our A) and C
+};
+
+int make_split(int32_t op, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
+               int32_t splits, Split* sp) {
+  int rc = make_problem(op, M, N, K, lda, ldb, N, &sp->p);
+  if (rc != 0) return rc;
+  QLORA_CHECK_ARG(splits >= 2 && splits <= 64 && K % (8 * splits) == 0 && N % 4 == 0);
+  QLORA_CHECK_ARG(M * N * (int64_t)splits < (1ll << 40));
+  const int64_t kc = K / splits;
+  sp->kc = (rocblas_int)kc;
+  sp->p.k = (rocblas_int)kc;
+  sp->sa = op == 0 ? kc : kc * ldb;  // B [N, K]: column slices; B [K, N]: row slices
+  sp->sb = kc;                       // A [M, K]: column slices
+  sp->sc = M * N;                    // fp32 [M, N] per slice, ld N
+  return 0;
+}
+
+}  // namespace blas
+}  // namespace qlora
+
+// fp16 C[M, N] (ld ldc) = fp16(A op(B) (+ bias)) with the reduction cut into `splits` slices:
+// fp32 partial products into work [splits][M][N] (one strided-batched rocBLAS call, solution as
+// in qlora_gemm but of the batched fp32-output problem), then one fixed-order sum and rounding.
+// Requires K % (8 splits) == 0, N % 4 == 0, work_elems >= splits M N.
+QLORA_API int qlora_gemm_splitk(int32_t op, int64_t M, int64_t N, int64_t K, const void* A,
+                                int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc,
+                                const void* bias, int32_t splits, float* work,
+                                int64_t work_elems, int32_t solution, void* stream) {
+  Split sp;
+  int rc = make_split(op, M, N, K, lda, ldb, splits, &sp);
+  if (rc != 0) return rc;
+  QLORA_CHECK_ARG(A && B && C && work && solution >= 0 && ldc >= N);
+  QLORA_CHECK_ARG(work_elems >= M * N * (int64_t)splits);
+  QLORA_CHECK_ARG(((uintptr_t)C & 7) == 0 && ldc % 4 == 0 && ((uintptr_t)work & 15) == 0);
+  rocblas_handle h;
+  if ((rc = handle_for(&h)) != 0) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  if ((rc = status(rocblas_set_stream(h, st))) != 0) return rc;
+  const float alpha = 1.f, beta = 0.f;
+  const Problem& p = sp.p;
+  rc = status(rocblas_gemm_strided_batched_ex(
+      h, p.ta, rocblas_operation_none, p.m, p.n, p.k, &alpha, B, rocblas_datatype_f16_r, p.lda,
+      sp.sa, A, rocblas_datatype_f16_r, p.ldb, sp.sb, &beta, work, rocblas_datatype_f32_r,
+      (rocblas_int)N, sp.sc, work, rocblas_datatype_f32_r, (rocblas_int)N, sp.sc, splits,
+      rocblas_datatype_f32_r,
+      solution > 0 ? rocblas_gemm_algo_solution_index : rocblas_gemm_algo_standard, solution,
+      rocblas_gemm_flags_none));
+  if (rc != 0) return rc;
+  const int64_t quads = M * N / 4;
+  hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)qlora_cdiv(quads, 256)), dim3(256), 0,
+                     st, work, splits, M, N, static_cast<uint16_t*>(C), ldc,
+                     static_cast<const uint16_t*>(bias));
+  return qlora_launch_status();
+}
+
+// The solution indices of the strided-batched fp32-output problem of qlora_gemm_splitk.
+QLORA_API int qlora_gemm_splitk_solutions(int32_t op, int64_t M, int64_t N, int64_t K,
+                                          const void* A, int64_t lda, const void* B, int64_t ldb,
+                                          float* work, int32_t splits, int32_t* list, int32_t cap,
+                                          int32_t* count) {
+  Split sp;
+  int rc = make_split(op, M, N, K, lda, ldb, splits, &sp);
+  if (rc != 0) return rc;
+  QLORA_CHECK_ARG(A && B && work && count && cap >= 0 && (cap == 0 || list));
+  rocblas_handle h;
+  if ((rc = handle_for(&h)) != 0) return rc;
+  const float alpha = 1.f, beta = 0.f;
+  const Problem& p = sp.p;
+  rocblas_int size = 0;
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Wdeprecated-declarations"
+  for (int pass = 0; pass < 2; ++pass) {
+    rocblas_int* arr = pass == 0 ? nullptr : list;
+    rocblas_int n = pass == 0 ? 0 : (size < cap ? size : cap);
+    rocblas_int* sz = pass == 0 ? &size : &n;
+    rc = status(rocblas_gemm_strided_batched_ex_get_solutions(
+        h, p.ta, rocblas_operation_none, p.m, p.n, p.k, &alpha, B, rocblas_datatype_f16_r,
+        p.lda, sp.sa, A, rocblas_datatype_f16_r, p.ldb, sp.sb, &beta, work,
+        rocblas_datatype_f32_r, (rocblas_int)N, sp.sc, work, rocblas_datatype_f32_r,
+        (rocblas_int)N, sp.sc, splits, rocblas_datatype_f32_r, rocblas_gemm_algo_solution_index,
+        rocblas_gemm_flags_none, arr, sz));
+    if (rc != 0) return rc;
+    if (pass == 0) {
+      *count = size;
+      if (cap == 0 || size == 0) return 0;
+    }
+  }
+#pragma clang diagnostic pop
+  return 0;
 }

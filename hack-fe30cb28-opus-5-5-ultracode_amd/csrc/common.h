@@ -51,4 +51,22 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// ---- buffer loads ------------------------------------------------------------------------------
+// A wave-uniform resource over [base, base + bytes): loads at offsets past the end return zeros
+// (the hardware range check), so tile loads need neither clamped indices nor selects - and a
+// select of a loaded value is what the compiler may turn into a branch around the load, whose
+// join then waits for every load in flight.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+__device__ __forceinline__ uint4 buf_load16(rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ float buf_load_f32(rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+
 }  // namespace qlora

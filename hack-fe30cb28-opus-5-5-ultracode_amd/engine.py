@@ -377,10 +377,14 @@ class _Head(torch.autograd.Function):
             _ce(logits, targets[c0:c1], tok_loss[c0:c1], entropy[c0:c1], correct[c0:c1],
                 zero_unsupervised=needs_grad)
             if needs_grad:
-                dhn = L.linear_t(logits, lm_w)
+                # rows past n_sup have all-zero logits gradients (zero_unsupervised), hence
+                # zero dhn and zero dh: only the supervised rows go through the products
+                s1 = min(c1, n_sup)
+                dhn = L.linear_t(logits[:s1 - c0], lm_w)
                 del logits
-                _rms_bwd(spec, dhn, hp[c0:c1], rstd[c0:c1], norm_w, packed, grad_scale=inv,
-                         out=dhp[c0:c1])
+                _rms_bwd(spec, dhn, hp[c0:s1], rstd[c0:s1], norm_w, packed, grad_scale=inv,
+                         out=dhp[c0:s1])
+                dhp[s1:c1].zero_()
                 del dhn
             else:
                 del logits
@@ -491,25 +495,32 @@ class FusedQwen2:
         return int(max(0, min(len(self.layers), free // per_layer)))
 
     def gemm_shapes(self):
-        """(op, N, K) of the projections' GEMMs: y = x W^T for qkv, o, gate|up, down and
-        dX = dY W for the same four weights."""
+        """(op, N, K) of the step's GEMMs: y = x W^T for qkv, o, gate|up, down and the lm_head,
+        and dX = dY W for the same five weights."""
         spec = self.layers[0]
         H, I, qkv, o = spec.H, spec.I, (spec.HQ + 2 * spec.HKV) * spec.D, spec.HQ * spec.D
-        fwd = [(qkv, H), (H, o), (2 * I, H), (H, I)]
+        fwd = [(qkv, H), (H, o), (2 * I, H), (H, I), (self.cfg.vocab_size, H)]
         return ([(G.NT, n, k) for n, k in fwd] +
                 [(G.NN, k, n) for n, k in fwd])
 
     def tune_gemms(self, token_counts, log=None):
-        """Measure the projections' GEMM solutions for the buckets of these step sizes (tokens);
-        returns the seconds spent."""
-        return G.tune(self.gemm_shapes(), list(token_counts), self.device, log=log)
+        """Measure the GEMM solutions for the buckets of these step sizes (tokens); the head's
+        dX product runs over the supervised rows only, so it is also measured at 3/4 and 1/2 of
+        each size. Returns the seconds spent."""
+        counts = list(token_counts)
+        shapes = self.gemm_shapes()
+        t = G.tune(shapes, counts, self.device, log=log)
+        sup = sorted({max(1, (c * f) // 4) for c in counts for f in (2, 3)})
+        return t + G.tune(shapes[-1:], sup, self.device, log=log)
 
     def step(self, input_ids, attention_mask, labels, denom):
         """The step's forward: (loss, packed, stats); autograd runs the backward."""
         packed = Packed(input_ids, attention_mask, labels, self.rope, self.dropout,
                         self.dropout_p)
         if self.autotune:
-            self.tune_gemms([packed.n])
+            shapes = self.gemm_shapes()
+            G.tune(shapes, [packed.n], self.device)
+            G.tune(shapes[-1:], [max(1, packed.n_supervised)], self.device)
         if self.dropout is not None and self.dropout.ok is None:
             self.dropout.ok = self.dropout.check(packed.rows,
                                                  min(packed.T, TorchDropout.CHECK_TOKENS),

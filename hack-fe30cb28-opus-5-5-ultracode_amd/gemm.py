@@ -1,13 +1,19 @@
-"""The frozen projections' plain fp16 GEMMs through qlora_gemm (rocBLAS, Tensile kernels) with a
-solution measured per weight shape and token-count bucket.
+"""The step's plain fp16 GEMMs through qlora_gemm / qlora_gemm_splitk (rocBLAS, Tensile kernels)
+with a variant measured per weight shape and token-count bucket.
 
-y = x W^T and dX = dY W (engine.py:1082-1316) are torch matmuls in the reference, i.e. whatever
-kernel the library's size heuristic picks. At this step's sizes (M = a few thousand tokens) the
-heuristic leaves 20-30 % on the table for the widest projections (gate|up: 0.93 -> 1.15 PFLOP/s
-forward, 0.65 -> 0.83 backward on MI355X). The tuner times every solution rocBLAS offers for a
-shape once, keeps the fastest few as candidates, and then, per bucket of BUCKET tokens, the
-fastest candidate (torch's own matmul is one of them). Results are bit-for-bit those of an fp16
-GEMM with fp32 accumulation; only the summation order differs between solutions.
+y = x W^T and dX = dY W (engine.py:1082-1316, 1376-1381) are torch matmuls in the reference,
+i.e. whatever kernel the library's size heuristic picks. At this step's sizes (M = a few
+thousand tokens) the heuristic leaves 20-40 % on the table: for the widest projections
+(gate|up: 0.93 -> 1.15 PFLOP/s forward, 0.65 -> 0.83 backward on MI355X), and most for the
+long-K, narrow-N input gradients (gate|up K = 17920, lm_head K = 151936, N = 1536), whose
+output has too few tiles to fill 256 CUs - there a split of K into slices (fp32 partials, one
+fixed-order sum) wins.
+
+A variant is (solution, splits): solution -1 = torch's matmul, 0 = rocBLAS's own choice, > 0 a
+Tensile solution index; splits 1 = one GEMM, > 1 = qlora_gemm_splitk. The tuner times every
+solution rocBLAS offers for a shape once (for each split count that divides K), keeps the
+fastest few as candidates, and then, per bucket of BUCKET tokens, the fastest candidate. Every
+variant computes fp16(sum of fp16 products in fp32 (+ bias)); only the summation order differs.
 """
 
 import ctypes
@@ -19,12 +25,14 @@ from . import _lib
 from .ops import _need, _ptr, _stream
 
 BUCKET = 256
-TORCH = -1       # candidate: torch's matmul
-DEFAULT = 0      # candidate: rocBLAS's own choice
-NT, NN = 0, 1    # op: C = A B^T (B [N, K]) or C = A B (B [K, N])
+TORCH = (-1, 1)   # torch's matmul
+DEFAULT = (0, 1)  # rocBLAS's own choice
+NT, NN = 0, 1     # op: C = A B^T (B [N, K]) or C = A B (B [K, N])
+SPLITS = (2, 4, 8)
+MIN_SLICE = 1024  # no split leaves less than this much K per slice
 
-_CANDIDATES = {}  # (device index, op, N, K) -> [solution, ...]
-_CHOICE = {}      # (device index, op, N, K, bucket) -> solution
+_CANDIDATES = {}  # (device index, op, N, K) -> [variant, ...]
+_CHOICE = {}      # (device index, op, N, K, bucket) -> variant
 
 
 def _bucket(M):
@@ -49,13 +57,20 @@ def _check(t, name, dev):
     return t.stride(0)
 
 
+def split_counts(N, K):
+    """The split counts qlora_gemm_splitk accepts for this shape and the tuner tries."""
+    if N % 4:
+        return []
+    return [s for s in SPLITS if K % (8 * s) == 0 and K // s >= MIN_SLICE]
+
+
 def choice(dev_index, op, N, K, M):
-    """The solution used for this problem: the tuned one for M's bucket, else the nearest tuned
+    """The variant used for this problem: the tuned one for M's bucket, else the nearest tuned
     bucket's, else torch's matmul."""
     b = _bucket(M)
-    sol = _CHOICE.get((dev_index, op, N, K, b))
-    if sol is not None:
-        return sol
+    v = _CHOICE.get((dev_index, op, N, K, b))
+    if v is not None:
+        return v
     near = [k[4] for k in _CHOICE if k[:4] == (dev_index, op, N, K)]
     if not near:
         return TORCH
@@ -63,9 +78,20 @@ def choice(dev_index, op, N, K, M):
     return _CHOICE[(dev_index, op, N, K, nb)]
 
 
-def _run(sol, op, a, b, out, alpha, beta, M, N, K, lda, ldb, ldc, dev):
-    _lib.call("qlora_gemm", op, M, N, K, _ptr(a), lda, _ptr(b), ldb, _ptr(out), ldc,
-              float(alpha), float(beta), int(sol), _stream(dev))
+def _run(variant, op, a, b, out, bias, M, N, K, lda, ldb, ldc, dev, work=None):
+    sol, splits = variant
+    if splits == 1:
+        beta = 0.0
+        if bias is not None:
+            out.copy_(bias.view(1, N).expand(M, N))
+            beta = 1.0
+        _lib.call("qlora_gemm", op, M, N, K, _ptr(a), lda, _ptr(b), ldb, _ptr(out), ldc, 1.0,
+                  beta, int(sol), _stream(dev))
+        return
+    if work is None:
+        work = torch.empty((splits * M * N,), device=dev, dtype=torch.float32)
+    _lib.call("qlora_gemm_splitk", op, M, N, K, _ptr(a), lda, _ptr(b), ldb, _ptr(out), ldc,
+              _ptr(bias), splits, _ptr(work), work.numel(), int(sol), _stream(dev))
 
 
 def mm(a, b, op, out=None, bias=None):
@@ -86,64 +112,82 @@ def mm(a, b, op, out=None, bias=None):
             raise ValueError("bias must have one entry per output column")
     if M == 0:
         return out
-    sol = choice(dev.index or 0, op, N, K, M)
-    if sol == TORCH:
+    v = choice(dev.index or 0, op, N, K, M)
+    if v == TORCH:
         bt = b.t() if op == NT else b
         if bias is not None:
             return torch.addmm(bias, a, bt, out=out)
         return torch.mm(a, bt, out=out)
-    beta = 0.0
-    if bias is not None:
-        out.copy_(bias.view(1, N).expand(M, N))
-        beta = 1.0
+    if v[1] > 1 and (ldc % 4 or out.data_ptr() % 8):
+        v = DEFAULT
     try:
-        _run(sol, op, a, b, out, 1.0, beta, M, N, K, lda, ldb, ldc, dev)
+        _run(v, op, a, b, out, bias, M, N, K, lda, ldb, ldc, dev)
     except RuntimeError:
-        if sol == DEFAULT:
+        if v == DEFAULT:
             raise
-        # the bucket's solution rejects this exact size (rocBLAS checks before launching)
+        # the bucket's variant rejects this exact size (rocBLAS checks before launching)
         _CHOICE[(dev.index or 0, op, N, K, _bucket(M))] = DEFAULT
-        _run(DEFAULT, op, a, b, out, 1.0, beta, M, N, K, lda, ldb, ldc, dev)
+        _run(DEFAULT, op, a, b, out, bias, M, N, K, lda, ldb, ldc, dev)
     return out
 
 
-def solutions(op, a, b, out):
-    """Every rocBLAS solution index for this problem."""
-    dev = a.device
-    lda, ldb, ldc = _check(a, "a", dev), _check(b, "b", dev), _check(out, "out", dev)
-    M, N, K = _dims(a, b, op)
+def _listed(fn, *args):
     cnt = ctypes.c_int32(0)
-    _lib.call("qlora_gemm_solutions", op, M, N, K, _ptr(a), lda, _ptr(b), ldb, _ptr(out), ldc,
-              None, 0, ctypes.byref(cnt))
+    _lib.call(fn, *args, None, 0, ctypes.byref(cnt))
     if cnt.value == 0:
         return []
     arr = (ctypes.c_int32 * cnt.value)()
-    _lib.call("qlora_gemm_solutions", op, M, N, K, _ptr(a), lda, _ptr(b), ldb, _ptr(out), ldc,
-              arr, cnt.value, ctypes.byref(cnt))
+    _lib.call(fn, *args, arr, cnt.value, ctypes.byref(cnt))
     return list(arr)[:cnt.value]
 
 
+def solutions(op, a, b, out, splits=1, work=None):
+    """Every rocBLAS solution index for this problem (and split count; work: the fp32
+    workspace of the split problem)."""
+    dev = a.device
+    lda, ldb = _check(a, "a", dev), _check(b, "b", dev)
+    M, N, K = _dims(a, b, op)
+    if splits == 1:
+        ldc = _check(out, "out", dev)
+        return _listed("qlora_gemm_solutions", op, M, N, K, _ptr(a), lda, _ptr(b), ldb,
+                       _ptr(out), ldc)
+    return _listed("qlora_gemm_splitk_solutions", op, M, N, K, _ptr(a), lda, _ptr(b), ldb,
+                   _ptr(work), splits)
+
+
+FLUSH_BYTES = 512 * 2**20  # > the 256 MB last-level (Infinity) cache of an MI355X
+_FLUSH = {}
+
+
 def _time(fn, reps):
+    """Mean duration (ms) of fn over reps runs, each after the last-level cache was overwritten:
+    in the step the operands come from HBM, and timing a variant against warm operands favours
+    those that move more bytes (split-K's fp32 partials)."""
     fn()
-    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    s.record()
-    for _ in range(reps):
+    dev = torch.cuda.current_device()
+    buf = _FLUSH.get(dev)
+    if buf is None:
+        buf = _FLUSH[dev] = torch.empty((FLUSH_BYTES // 4,), device=dev, dtype=torch.float32)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(reps)]
+    for s, e in ev:
+        buf.fill_(0.0)
+        s.record()
         fn()
-    e.record()
-    e.synchronize()
-    return s.elapsed_time(e) / reps
+        e.record()
+    ev[-1][1].synchronize()
+    return sum(s.elapsed_time(e) for s, e in ev) / reps
 
 
-def tune(shapes, Ms, device, top=6, reps=3, log=None):
+def tune(shapes, Ms, device, top=6, top_split=2, reps=3, log=None):
     """Measure, for each (op, N, K) in shapes and each token count in Ms, the fastest of: torch's
-    matmul, rocBLAS's default, and the `top` solutions that were fastest at the median token
-    count. Buckets already tuned are skipped. Returns the seconds spent."""
+    matmul, rocBLAS's default, the `top` solutions that were fastest at the median token count
+    and, per split count, rocBLAS's default and the `top_split` fastest. Buckets already tuned
+    are skipped. Returns the seconds spent."""
     t0 = time.perf_counter()
     dev = torch.device(device)
     di = dev.index or 0
     buckets = sorted({_bucket(M) for M in Ms if M > 0})
-    if not buckets:
-        return 0.0
     work = [(op, N, K, [bk for bk in buckets if (di, op, N, K, bk) not in _CHOICE])
             for op, N, K in shapes]
     work = [w for w in work if w[3]]
@@ -156,40 +200,52 @@ def tune(shapes, Ms, device, top=6, reps=3, log=None):
         bshape = (N, K) if op == NT else (K, N)
         b = (torch.randn(bshape, device=dev, generator=g) * 0.02).to(torch.float16)
         c_full = torch.empty((m_max, N), device=dev, dtype=torch.float16)
+        splits_ok = split_counts(N, K)
+        ws = torch.empty((max(splits_ok, default=0) * m_max * N or 1,), device=dev,
+                         dtype=torch.float32)
         ldb = b.stride(0)
 
-        def runner(sol, M):
+        def runner(v, M):
             a, c = a_full[:M], c_full[:M]
-            if sol == TORCH:
+            if v == TORCH:
                 bt = b.t() if op == NT else b
                 return lambda: torch.mm(a, bt, out=c)
-            return lambda: _run(sol, op, a, b, c, 1.0, 0.0, M, N, K, K, ldb, N, dev)
+            return lambda: _run(v, op, a, b, c, None, M, N, K, K, ldb, N, dev, work=ws)
+
+        def listed(M, splits):
+            return solutions(op, a_full[:M], b, c_full[:M], splits, ws)
 
         key = (di, op, N, K)
         if key not in _CANDIDATES:
             m_mid = todo[len(todo) // 2] * BUCKET
-            timed = []
-            for sol in solutions(op, a_full[:m_mid], b, c_full[:m_mid]):
-                try:
-                    timed.append((_time(runner(sol, m_mid), 1), sol))
-                except RuntimeError:
-                    continue  # a solution that rejects the problem is not a candidate
-            timed.sort()
-            _CANDIDATES[key] = [TORCH, DEFAULT] + [s for _, s in timed[:top] if s != DEFAULT]
+            cands = [TORCH, DEFAULT]
+            for splits, keep in [(1, top)] + [(s, top_split) for s in splits_ok]:
+                timed = []
+                for sol in listed(m_mid, splits):
+                    try:
+                        timed.append((_time(runner((sol, splits), m_mid), 1), sol))
+                    except RuntimeError:
+                        continue  # a solution that rejects the problem is not a candidate
+                timed.sort()
+                if splits > 1:
+                    cands.append((0, splits))
+                cands += [(s, splits) for _, s in timed[:keep] if s != 0]
+            _CANDIDATES[key] = cands
         for bk in todo:
             M = bk * BUCKET
-            valid = set(solutions(op, a_full[:M], b, c_full[:M])) | {TORCH, DEFAULT}
-            best = min((_time(runner(sol, M), reps), sol) for sol in _CANDIDATES[key]
-                       if sol in valid)
+            valid = {TORCH, DEFAULT}
+            for splits in [1] + splits_ok:
+                valid |= {(s, splits) for s in [0] + listed(M, splits)}
+            best = min((_time(runner(v, M), reps), v) for v in _CANDIDATES[key] if v in valid)
             _CHOICE[key + (bk,)] = best[1]
             if log is not None:
-                log(f"gemm tune op={op} N={N} K={K} M={M}: solution {best[1]} "
-                    f"{best[0] * 1e3:.1f} us")
-        del a_full, b, c_full
+                log(f"gemm tune op={op} N={N} K={K} M={M}: {best[1]} {best[0] * 1e3:.1f} us")
+        del a_full, b, c_full, ws
     return time.perf_counter() - t0
 
 
 def reset():
-    """Forget every measurement (tests)."""
+    """Forget every measurement and the flush buffers (tests)."""
     _CANDIDATES.clear()
     _CHOICE.clear()
+    _FLUSH.clear()

@@ -193,9 +193,9 @@ def nf4_linear_t(dy, w):
 
 def linear(x, w):
     """x W^T for an fp16 weight [V, H] (the lm_head)."""
-    return x @ w.t()
+    return gemm.mm(x, w, gemm.NT)
 
 
 def linear_t(g, w):
     """g W for an fp16 weight [V, H]."""
-    return g @ w
+    return gemm.mm(g, w, gemm.NN)

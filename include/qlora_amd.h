@@ -233,6 +233,22 @@ int qlora_gemm_solutions(int32_t op, int64_t M, int64_t N, int64_t K, const void
                          int32_t cap, int32_t* count);
 
 /*
+ * qlora_gemm with the reduction cut into `splits` equal slices: one strided-batched rocBLAS call
+ * writes fp32 partial products into work [splits][M][N], a kernel sums them in a fixed order and
+ * rounds once: C = fp16(sum + bias) (bias f16 [N] or null). For long-K, narrow-N products whose
+ * output alone has too few tiles for the GPU (dX of gate|up, engine.py:1293; dX of the lm_head,
+ * engine.py:1381). Requires K % (8 splits) == 0, N % 4 == 0, ldc % 4 == 0, C 8-byte aligned,
+ * work_elems >= splits M N; solution: 0 or an index from qlora_gemm_splitk_solutions.
+ */
+int qlora_gemm_splitk(int32_t op, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
+                      const void* B, int64_t ldb, void* C, int64_t ldc, const void* bias,
+                      int32_t splits, float* work, int64_t work_elems, int32_t solution,
+                      void* stream);
+int qlora_gemm_splitk_solutions(int32_t op, int64_t M, int64_t N, int64_t K, const void* A,
+                                int64_t lda, const void* B, int64_t ldb, float* work,
+                                int32_t splits, int32_t* list, int32_t cap, int32_t* count);
+
+/*
  * The LoRA forward of a layer's q and v adapters in one launch (engine.py:1088-1093):
  *   x_a = f16(a_a A_a^T)   f16 [n, 16] (kept for the backward)
  *   l_a = f16(x_a B_a^T)   f16 [n, N_a] (added to the projection output by qlora_rope_fwd)

@@ -101,3 +101,13 @@ def test_gemm_rejects_bad_problems_before_any_device_call(pkg):
                                         ctypes.byref(cnt)) == 1
         assert lib.qlora_gemm(op, M, N, K, 8, lda, 8, max(K, N), 8, N, 1.0, 0.0, 0, None) == 1
     assert lib.qlora_error_string(100000 + 3) != lib.qlora_error_string(3)
+
+
+def test_gemm_splitk_rejects_bad_problems(pkg):
+    """qlora_gemm_splitk needs K divisible into 8-aligned slices, N % 4 == 0, a workspace."""
+    lib = pkg._lib.load()
+    # K % (8 splits) != 0; N % 4 != 0; splits < 2; workspace too small
+    for M, N, K, splits, work in ((4, 8, 100, 2, 1 << 20), (4, 6, 64, 2, 1 << 20),
+                                  (4, 8, 64, 1, 1 << 20), (4, 8, 64, 2, 10)):
+        assert lib.qlora_gemm_splitk(1, M, N, K, 16, K, 16, N, 16, N, None, splits, 16, work, 0,
+                                     None) == 1

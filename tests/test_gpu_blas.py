@@ -37,7 +37,7 @@ def test_gemm_default_and_listed_solutions(pkg, op, M, N, K):
     assert len(sols) > 0
     for sol in [0] + sols[:: max(1, len(sols) // 6)]:
         out = torch.full((M, N), float("nan"), device=DEV, dtype=torch.float16)
-        pkg.gemm._run(sol, op, a, b, out, 1.0, 0.0, M, N, K, K, b.stride(0), N, a.device)
+        pkg.gemm._run((sol, 1), op, a, b, out, None, M, N, K, K, b.stride(0), N, a.device)
         check(out, want)
 
 
@@ -78,8 +78,49 @@ def test_mm_bias_and_tuned_choice(pkg):
         # force a rocBLAS solution for the bucket and check the bias path through it
         sols = G.solutions(G.NT, x, w, torch.empty((x.shape[0], N), device=DEV,
                                                    dtype=torch.float16))
-        G._CHOICE[(0, G.NT, N, K, G._bucket(x.shape[0]))] = sols[0]
+        G._CHOICE[(0, G.NT, N, K, G._bucket(x.shape[0]))] = (sols[0], 1)
         check(G.mm(x, w, G.NT, bias=bias), ref(x, w, 0, bias))
     finally:
         G.reset()
 
+
+
+@pytest.mark.parametrize("op", [0, 1])
+@pytest.mark.parametrize("splits", [2, 4, 8])
+@pytest.mark.parametrize("M,N,K", [(1, 256, 8192), (300, 1536, 17920), (37, 512, 4096)])
+def test_gemm_splitk(pkg, op, splits, M, N, K):
+    """qlora_gemm_splitk: fp32 partial products over K slices, one fixed-order sum, one rounding
+    (with and without bias), for rocBLAS's default and listed solutions of the batched problem;
+    the output's row stride may exceed its width."""
+    G = pkg.gemm
+    g = torch.Generator(device=DEV).manual_seed(M * splits + N + op)
+    a = torch.randn((M, K), device=DEV, generator=g).half()
+    b = (torch.randn((N, K) if op == 0 else (K, N), device=DEV, generator=g) * 0.05).half()
+    bias = (torch.randn((N,), device=DEV, generator=g) * 0.1).half()
+    want = ref(a, b, op)
+    work = torch.empty((splits * M * N,), device=DEV, dtype=torch.float32)
+    sols = G.solutions(op, a, b, None, splits, work)
+    assert len(sols) > 0
+    cbuf = torch.full((M, N + 8), float("nan"), device=DEV, dtype=torch.float16)
+    out = cbuf[:, :N]
+    for sol in [0] + sols[:: max(1, len(sols) // 3)]:
+        G._run((sol, splits), op, a, b, out, None, M, N, K, K, b.stride(0), out.stride(0),
+               a.device, work=work)
+        check(out, want)
+    G._run((0, splits), op, a, b, out, bias, M, N, K, K, b.stride(0), out.stride(0), a.device)
+    check(out, want + bias.double())
+    assert torch.isnan(cbuf[:, N:].float()).all()  # columns past the view are not written
+
+
+def test_mm_uses_a_tuned_split_variant(pkg):
+    G = pkg.gemm
+    G.reset()
+    try:
+        N, K, M = 512, 16384, 600
+        G._CHOICE[(0, G.NN, N, K, G._bucket(M))] = (0, 4)
+        g = torch.Generator(device=DEV).manual_seed(3)
+        dy = torch.randn((M, K), device=DEV, generator=g).half()
+        w = (torch.randn((K, N), device=DEV, generator=g) * 0.05).half()
+        check(G.mm(dy, w, G.NN), ref(dy, w, 1))
+    finally:
+        G.reset()
