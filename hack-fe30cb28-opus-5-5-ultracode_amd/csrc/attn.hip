@@ -61,6 +61,10 @@ struct Args {
   float scale;
 };
 
+// 2^x by the hardware instruction (v_exp_f32): no denormal-range fix-up (results below 2^-126
+// flush to zero, which a probability that small does not miss).
+__device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
+
 __device__ __forceinline__ f32x16 mfma(half8_t a, half8_t b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
@@ -248,15 +252,8 @@ __global__ __launch_bounds__(64 * G) void attn_fwd_kernel(Args a) {
   const float c = a.scale * kLog2e;
   const int lim = min(qi, L - 1);  // the last key this query attends to
 
-  for (int kb = 0; kb < nkb; ++kb) {
-    const int k0 = kb * kKB;
-    __syncthreads();
-    sk.store(ks, tid);
-    sv.store(vt, nullptr, tid);
-    __syncthreads();
-    // the next block (past the sequence: zeros, not used)
-    sk.load(ksrc, k0 + kKB, kvs_b, tid);
-    sv.load(vsrc, k0 + kKB, kvs_b, tid);
+  // one key block from the staged tiles (ks, vt)
+  auto block = [&](int k0) {
     f32x16 s[2];
     s[0] = s[1] = f32x16{};
 #pragma unroll
@@ -266,34 +263,39 @@ __global__ __launch_bounds__(64 * G) void attn_fwd_kernel(Args a) {
       s[0] = mfma(k0op, qr[kk], s[0]);
       s[1] = mfma(k1op, qr[kk], s[1]);
     }
+    if (k0 + kKB - 1 > q0) {  // a block on the diagonal (uniform): mask keys past the query
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          s[t][r] = k0 + 32 * t + acc_row(r, lane) > lim ? -__builtin_inff() : s[t][r];
+    }
+    // the state is in log2 units of the scaled scores: m = max(c s), p = 2^(c s - m)
     float mx = -__builtin_inff();
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = k0 + 32 * t + acc_row(r, lane);
-        const float x = key > lim ? -__builtin_inff() : s[t][r] * c;
-        s[t][r] = x;
-        mx = fmaxf(mx, x);
-      }
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[t][r]);
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float mnew = fmaxf(m, mx);
-    const float alpha = exp2f(m - mnew);
+    const float mnew = fmaxf(m, mx * c);
+    const float alpha = ex2(m - mnew);
     m = mnew;
     float ps = 0.f;
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float p = exp2f(s[t][r] - mnew);
+        const float p = ex2(fmaf(s[t][r], c, -mnew));
         s[t][r] = p;
         ps += p;
       }
     lsum = lsum * alpha + ps;
+    if (__any(alpha != 1.f)) {  // once the running maxima settle, most blocks skip this
 #pragma unroll
-    for (int u = 0; u < DT; ++u)
+      for (int u = 0; u < DT; ++u)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) o[u][r] *= alpha;
+        for (int r = 0; r < 16; ++r) o[u][r] *= alpha;
+    }
     half8_t pb[4];
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) pb[kk] = to_b(s[kk >> 1], kk & 1);
@@ -306,6 +308,17 @@ __global__ __launch_bounds__(64 * G) void attn_fwd_kernel(Args a) {
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) o[u] = mfma(vop[kk], pb[kk], o[u]);
     }
+  };
+
+  for (int kb = 0; kb < nkb; ++kb) {
+    __syncthreads();
+    sk.store(ks, tid);
+    sv.store(vt, nullptr, tid);
+    __syncthreads();
+    // the next block (past the sequence: zeros, not used)
+    sk.load(ksrc, (kb + 1) * kKB, kvs_b, tid);
+    sv.load(vsrc, (kb + 1) * kKB, kvs_b, tid);
+    block(kb * kKB);
   }
   const float ltot = lsum + __shfl_xor(lsum, 32, 64);
   if (qi < L) {
@@ -384,11 +397,13 @@ __global__ __launch_bounds__(64 * G) void attn_dq_kernel(Args a) {
       dp = mfma(vop, dr[kk], dp);
     }
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const float e = exp2f(s[r] * c - lse2);
-      const float p = k0 + acc_row(r, lane) > lim ? 0.f : e;
-      s[r] = p * (dp[r] - delta);
+    for (int r = 0; r < 16; ++r) s[r] = ex2(fmaf(s[r], c, -lse2));
+    if (k0 + KB - 1 > q0) {  // a block on the diagonal (uniform)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[r] = k0 + acc_row(r, lane) > lim ? 0.f : s[r];
     }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[r] *= dp[r] - delta;
     half8_t sb[2];
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) sb[kk] = to_b(s, kk);
@@ -478,6 +493,8 @@ __global__ __launch_bounds__(64 * kKeyWaves) void attn_dkdv_kernel(Args a) {
       s = mfma(qop, kr[kk], s);
       dp = mfma(dop, vr[kk], dp);
     }
+    // masks only where the block reaches the diagonal or the end of the sequence (uniform)
+    const bool edge = q0 < k0 + kTok || q0 + kTok > L;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int qr0 = 8 * j + 4 * (lane >> 5);
@@ -486,11 +503,13 @@ __global__ __launch_bounds__(64 * kKeyWaves) void attn_dkdv_kernel(Args a) {
       const float lq[4] = {l4.x, l4.y, l4.z, l4.w}, dq4[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int r = 4 * j + i, qq = q0 + qr0 + i;
-        const float e = exp2f(s[r] * c - lq[i]);
-        const float p = (qq < L && kj <= qq) ? e : 0.f;
-        s[r] = p;
-        dp[r] = p * (dp[r] - dq4[i]);
+        const int r = 4 * j + i;
+        s[r] = ex2(fmaf(s[r], c, -lq[i]));
+        if (edge) {
+          const int qq = q0 + qr0 + i;
+          s[r] = (qq < L && kj <= qq) ? s[r] : 0.f;
+        }
+        dp[r] = s[r] * (dp[r] - dq4[i]);
       }
     }
     half8_t pb[2], sb[2];
