@@ -45,8 +45,11 @@ def make_batches(count, vocab, seed=0, rows=4, lo=256, hi=1024, device="cuda"):
         for r in range(rows):
             labels[r, :int(lengths[r]) // 4] = -100
         denom = float((labels[:, 1:] != -100).sum())
+        # host-side metadata a collator has: row lengths and the supervised-token count (here
+        # equal to denom: every label of a real token after the first is supervised or -100)
+        meta = {"lengths": lengths.tolist(), "n_supervised": int(denom)}
         out.append((ids.to(device), mask.to(device), labels.to(device), denom,
-                    int(lengths.sum())))
+                    int(lengths.sum()), meta))
     return out
 
 
@@ -63,8 +66,8 @@ class Trainer:
         self.scaler = torch.amp.GradScaler("cuda", init_scale=2.0**16)
 
     def step(self, batch):
-        ids, mask, labels, denom, _ = batch
-        loss, packed, stats = self.model.step(ids, mask, labels, denom)
+        ids, mask, labels, denom, _, meta = batch
+        loss, packed, stats = self.model.step(ids, mask, labels, denom, **meta)
         self.scaler.scale(loss).backward()
         self.scaler.step(self.opt)
         self.scaler.update()
@@ -166,7 +169,7 @@ def cpu_baseline(pkg, model, batch):
     2 layers + head, and of the head alone; a 28-layer step is head + 28 x layer."""
     from oracle import step as OS
 
-    ids, mask, labels, denom, ntok = batch
+    ids, mask, labels, denom, ntok, _ = batch
     threads = torch.get_num_threads()
     L = len(model.layers)
     gen = model.dropout.gen

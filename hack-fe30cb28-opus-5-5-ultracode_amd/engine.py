@@ -147,25 +147,48 @@ class RopeTable:
         return self.cos, self.sin
 
 
+def _to_device(host, dev):
+    """A small host tensor on the device through pinned memory, queued on the current stream
+    (the host does not wait)."""
+    if dev.type != "cuda":
+        return host.to(dev)
+    return host.pin_memory().to(dev, non_blocking=True)
+
+
 class Packed:
     """One micro-batch without its padding: real tokens of every row, back to back."""
 
-    def __init__(self, input_ids, attention_mask, labels, rope, dropout, dropout_p):
+    def __init__(self, input_ids, attention_mask, labels, rope, dropout, dropout_p, lengths=None,
+                 n_supervised=None):
+        """`lengths` (tokens of each row) and `n_supervised` (tokens with a label), when the
+        caller knows them on the host (a collator does), spare the step its reads of device
+        values: each such read waits for all the work queued before it (the previous step's
+        backward), and the GPU then idles while this step's first launches are being queued.
+        Given lengths, the mask is trusted to be right-padded to them."""
         if input_ids.dim() != 2 or attention_mask.shape != input_ids.shape \
                 or labels.shape != input_ids.shape:
             raise UnsupportedBatch("inputs are not [rows, tokens]")
         B, T = input_ids.shape
-        lengths = attention_mask.sum(dim=1)
-        lengths_cpu = lengths.tolist()
-        expected = torch.arange(T, device=input_ids.device)[None, :] < lengths[:, None]
-        if not bool(torch.equal(attention_mask.bool(), expected)):
-            raise UnsupportedBatch("attention_mask is not right-padded")
-        flat = expected.reshape(-1).nonzero().squeeze(1)
-        self.n = int(flat.numel())
+        dev = input_ids.device
+        if lengths is None:
+            lengths_t = attention_mask.sum(dim=1)
+            lengths = lengths_t.tolist()
+            expected = torch.arange(T, device=dev)[None, :] < lengths_t[:, None]
+            if not bool(torch.equal(attention_mask.bool(), expected)):
+                raise UnsupportedBatch("attention_mask is not right-padded")
+        lengths = [int(x) for x in lengths]
+        if len(lengths) != B or any(x < 0 or x > T for x in lengths):
+            raise UnsupportedBatch("lengths do not fit the batch")
+        # packed token -> its index in the padded [B, T] batch, built on the host and copied
+        # without waiting for the device
+        parts = [torch.arange(b * T, b * T + x, dtype=torch.int64) for b, x in enumerate(lengths)]
+        flat_host = torch.cat(parts) if parts else torch.zeros((0,), dtype=torch.int64)
+        flat = _to_device(flat_host, dev)
+        self.n = int(flat_host.numel())
         self.tok = flat  # each packed token's index in the padded [B, T] batch (int64)
         self.T = T
         self.rows = B
-        self.lengths = [int(x) for x in lengths_cpu]
+        self.lengths = lengths
         self.max_len = max(self.lengths) if self.lengths else 0
         self.ids = input_ids.reshape(-1)[flat]
         self.pos = (flat % T).to(torch.int32)
@@ -174,12 +197,12 @@ class Packed:
         self.targets = shifted.reshape(-1)[flat].contiguous()
         supervised = self.targets >= 0
         self.head_order = torch.argsort((~supervised).to(torch.int8), stable=True)
-        self.n_supervised = int(supervised.sum())
+        self.n_supervised = int(supervised.sum()) if n_supervised is None else int(n_supervised)
         cu = [0]
         for length in self.lengths:
             cu.append(cu[-1] + length)
         self.cu_seqlens_host = cu
-        self.cu_seqlens = torch.tensor(cu, device=input_ids.device, dtype=torch.int32)
+        self.cu_seqlens = _to_device(torch.tensor(cu, dtype=torch.int32), dev)
         self.cos, self.sin = rope.table(max(self.max_len, 1))
         self.dropout_p = dropout_p
         self.dropout = dropout
@@ -513,10 +536,12 @@ class FusedQwen2:
         sup = sorted({max(1, (c * f) // 4) for c in counts for f in (2, 3)})
         return t + G.tune(shapes[-1:], sup, self.device, log=log)
 
-    def step(self, input_ids, attention_mask, labels, denom):
-        """The step's forward: (loss, packed, stats); autograd runs the backward."""
+    def step(self, input_ids, attention_mask, labels, denom, lengths=None, n_supervised=None):
+        """The step's forward: (loss, packed, stats); autograd runs the backward. `lengths`
+        and `n_supervised`: the batch's row lengths and supervised-token count when the caller
+        has them on the host (then the step reads nothing back from the device)."""
         packed = Packed(input_ids, attention_mask, labels, self.rope, self.dropout,
-                        self.dropout_p)
+                        self.dropout_p, lengths=lengths, n_supervised=n_supervised)
         if self.autotune:
             shapes = self.gemm_shapes()
             G.tune(shapes, [packed.n], self.device)

@@ -132,3 +132,25 @@ def test_unsupported_batch_is_rejected_before_any_change(pkg):
     with pytest.raises(pkg.engine.UnsupportedBatch):
         model.step(ids.to(DEV), mask.to(DEV), labels.to(DEV), 1.0)
     assert model.dropout.gen.get_offset() == before
+
+
+def test_host_metadata_gives_the_same_step(pkg):
+    """A step given the row lengths and the supervised count on the host (no device reads)
+    equals the step that reads them back: same loss, same LoRA gradients, same packing."""
+    lengths = [17, 60, 33, 5]
+    ids, mask, labels = _batch(lengths, 3000)
+    denom = float((labels[:, 1:] != -100).sum())
+    out = []
+    for meta in ({}, {"lengths": lengths, "n_supervised": int(denom)}):
+        model = _tiny(pkg)
+        torch.cuda.manual_seed(99)
+        loss, packed, _ = model.step(ids.to(DEV), mask.to(DEV), labels.to(DEV), denom, **meta)
+        loss.backward()
+        torch.cuda.synchronize()
+        out.append((loss.item(), [p.grad.clone() for p in model.parameters()],
+                    packed.tok.cpu(), packed.cu_seqlens.cpu(), packed.n_supervised))
+    (l0, g0, t0, c0, n0), (l1, g1, t1, c1, n1) = out
+    assert l0 == l1 and n0 == n1 == int(denom)
+    assert torch.equal(t0, t1) and torch.equal(c0, c1)
+    for a, b in zip(g0, g1):
+        assert torch.equal(a, b)
