@@ -75,4 +75,19 @@ __device__ __forceinline__ uint32_t drop_keep4(const DropParams& d, uint64_t e0)
          ((uint32_t)keep_word(w.z, d.p_keep) << 2) | ((uint32_t)keep_word(w.w, d.p_keep) << 3);
 }
 
+// drop_keep4 for element indices below 2^32 with vec = 1 << vec_shift: 32-bit index arithmetic
+// (a shift and one 32-bit division instead of the 64-bit divisions of drop_words).
+__device__ __forceinline__ uint32_t drop_keep4_u32(const DropParams& d, uint32_t e0,
+                                                   uint32_t G32, int vec_shift) {
+  const uint32_t g = e0 >> vec_shift;
+  const uint32_t it = g / G32, thread = g - it * G32;
+  const uint64_t j = (uint64_t)it * (uint32_t)(1 << (vec_shift - 2)) +
+                     ((e0 & ((1u << vec_shift) - 1)) >> 2);
+  const uint64_t c = d.ctr + j;
+  const uint4 w = philox4x32_10(make_uint4((uint32_t)c, (uint32_t)(c >> 32), thread, 0u),
+                                (uint32_t)d.seed, (uint32_t)(d.seed >> 32));
+  return (uint32_t)keep_word(w.x, d.p_keep) | ((uint32_t)keep_word(w.y, d.p_keep) << 1) |
+         ((uint32_t)keep_word(w.z, d.p_keep) << 2) | ((uint32_t)keep_word(w.w, d.p_keep) << 3);
+}
+
 }  // namespace qlora

@@ -10,6 +10,8 @@
 // + 4H (dx). The masks are regenerated from (seed, counter) in both directions, never stored.
 #include "philox.h"
 
+#include <type_traits>
+
 namespace qlora {
 
 constexpr int kRowsPerBlock = 4;
@@ -230,6 +232,175 @@ __global__ __launch_bounds__(kWave* kRowsPerBlock) void rms_bwd_kernel(RmsBwdArg
   }
 }
 
+// ---- rows of H = 256 NV columns: every lane holds NV chunks of 4 (no bounds tests), and all
+// of a row's loads are issued before the first use of any of them (a load whose result feeds
+// the next instruction, or one behind a per-lane branch, makes the wavefront wait for it
+// before issuing the next: the generic kernels above pay a full memory round trip per chunk).
+// Dropout element indices (token * H + column) are below 2^32 (checked on the host).
+__device__ __forceinline__ float4 h4(uint2 t) {
+  return make_float4(lo_h(t.x), hi_h(t.x), lo_h(t.y), hi_h(t.y));
+}
+__device__ __forceinline__ uint2 pack4(float a, float b, float c, float d) {
+  return make_uint2(pack2h(a, b), pack2h(c, d));
+}
+__device__ __forceinline__ float comp(const float4& v, int k) {
+  return k == 0 ? v.x : k == 1 ? v.y : k == 2 ? v.z : v.w;
+}
+
+// weights of the lane's NV chunks as fp32 (fp32 or fp16 storage)
+template <int NV>
+__device__ __forceinline__ void load_w4(const void* w, int w_half, int lane, float4 (&wv)[NV]) {
+  if (w_half) {
+    uint2 t[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+      t[i] = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(w) + 4 * (lane + 64 * i));
+#pragma unroll
+    for (int i = 0; i < NV; ++i) wv[i] = h4(t[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+      wv[i] = *reinterpret_cast<const float4*>(static_cast<const float*>(w) + 4 * (lane + 64 * i));
+  }
+}
+
+template <int NV, bool DELTA, bool DROP>
+__global__ __launch_bounds__(kWave* kRowsPerBlock) void rms_fwd4_kernel(RmsFwdArgs a) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= a.n) return;
+  const int64_t base = row * a.H;
+  float4 x[NV];
+  uint2 dr[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t off = base + 4 * (lane + 64 * i);
+    x[i] = *reinterpret_cast<const float4*>(a.x + off);
+    if constexpr (DELTA) dr[i] = *reinterpret_cast<const uint2*>(a.delta + off);
+  }
+  float4 wv[NV];
+  load_w4<NV>(a.w, a.w_half, lane, wv);
+  const uint32_t tok_e = DROP ? (uint32_t)a.tok[row] * (uint32_t)a.H : 0u;
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    if constexpr (DELTA) {
+      const float4 d = h4(dr[i]);
+      x[i].x += d.x;
+      x[i].y += d.y;
+      x[i].z += d.z;
+      x[i].w += d.w;
+      *reinterpret_cast<float4*>(a.xsum + base + 4 * (lane + 64 * i)) = x[i];
+    }
+    ss += x[i].x * x[i].x;  // the generic kernel's order of additions
+    ss += x[i].y * x[i].y;
+    ss += x[i].z * x[i].z;
+    ss += x[i].w * x[i].w;
+  }
+  ss = wave_sum(ss);
+  const float rstd = 1.0f / sqrtf(ss / (float)a.H + a.eps);
+  if (lane == 0) a.rstd[row] = rstd;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t off = base + 4 * (lane + 64 * i);
+    const float4 y = make_float4(wv[i].x * (x[i].x * rstd), wv[i].y * (x[i].y * rstd),
+                                 wv[i].z * (x[i].z * rstd), wv[i].w * (x[i].w * rstd));
+    if (a.y) *reinterpret_cast<uint2*>(a.y + off) = pack4(y.x, y.y, y.z, y.w);
+    if constexpr (DROP) {
+      const uint32_t e0 = tok_e + 4u * (uint32_t)(lane + 64 * i);
+      const uint32_t G32 = (uint32_t)a.drop.G;
+      const int vs = a.drop.vec == 8 ? 3 : 2;
+      uint16_t* outs[2] = {a.yq, a.yv};
+      const uint64_t ctrs[2] = {a.ctr_q, a.ctr_v};
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        if (outs[t] == nullptr) continue;
+        DropParams d = a.drop;
+        d.ctr = ctrs[t];
+        const uint32_t keep = drop_keep4_u32(d, e0, G32, vs);
+        float o[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) o[k] = (keep >> k) & 1 ? comp(y, k) * a.keep_scale : 0.f;
+        *reinterpret_cast<uint2*>(outs[t] + off) = pack4(o[0], o[1], o[2], o[3]);
+      }
+    }
+  }
+}
+
+template <int NV, bool DROP, bool RES>
+__global__ __launch_bounds__(kWave* kRowsPerBlock) void rms_bwd4_kernel(RmsBwdArgs a) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= a.n) return;
+  const int64_t base = row * a.H;
+  uint2 dyr[NV], tqr[NV], tvr[NV];
+  float4 x[NV], r[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t col = 4 * (lane + 64 * i);
+    dyr[i] = *reinterpret_cast<const uint2*>(a.dy + row * a.dy_stride + col);
+    x[i] = *reinterpret_cast<const float4*>(a.x + base + col);
+    if constexpr (DROP) {
+      tqr[i] = *reinterpret_cast<const uint2*>(a.tq + base + col);
+      tvr[i] = *reinterpret_cast<const uint2*>(a.tv + base + col);
+    }
+    if constexpr (RES) r[i] = *reinterpret_cast<const float4*>(a.dres + base + col);
+  }
+  float4 wv[NV];
+  load_w4<NV>(a.w, a.w_half, lane, wv);
+  const float rstd = a.rstd[row];
+  uint32_t kq[NV], kv[NV];
+  if constexpr (DROP) {  // the masks, while the loads are in flight
+    const uint32_t tok_e = (uint32_t)a.tok[row] * (uint32_t)a.H;
+    const uint32_t G32 = (uint32_t)a.drop.G;
+    const int vs = a.drop.vec == 8 ? 3 : 2;
+    DropParams dq = a.drop, dv = a.drop;
+    dq.ctr = a.ctr_q;
+    dv.ctr = a.ctr_v;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const uint32_t e0 = tok_e + 4u * (uint32_t)(lane + 64 * i);
+      kq[i] = drop_keep4_u32(dq, e0, G32, vs);
+      kv[i] = drop_keep4_u32(dv, e0, G32, vs);
+    }
+  }
+  float g[NV][4], xh[NV][4];
+  float dot = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const float4 dy = h4(dyr[i]);
+    float d[4] = {dy.x, dy.y, dy.z, dy.w};
+    if constexpr (DROP) {
+      const float4 q = h4(tqr[i]), v = h4(tvr[i]);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        d[k] += (kq[i] >> k) & 1 ? comp(q, k) * a.keep_scale : 0.f;
+        d[k] += (kv[i] >> k) & 1 ? comp(v, k) * a.keep_scale : 0.f;
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      g[i][k] = d[k] * comp(wv[i], k);
+      xh[i][k] = comp(x[i], k) * rstd;
+      dot += g[i][k] * xh[i][k];
+    }
+  }
+  dot = wave_sum(dot);
+  const float mean = dot / (float)a.H;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t off = base + 4 * (lane + 64 * i);
+    float dx[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      dx[k] = rstd * (g[i][k] - xh[i][k] * mean) * a.grad_scale;
+      if constexpr (RES) dx[k] += comp(r[i], k);
+    }
+    *reinterpret_cast<float4*>(a.dx + off) = make_float4(dx[0], dx[1], dx[2], dx[3]);
+    if (a.dx16) *reinterpret_cast<uint2*>(a.dx16 + off) = pack4(dx[0], dx[1], dx[2], dx[3]);
+  }
+}
+
 __global__ void dropout_keep_kernel(int8_t* out, int64_t nelem, DropParams d) {
   const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // group of 4 elements
   const int64_t e0 = q * 4;
@@ -265,6 +436,47 @@ int pick_nv(int64_t need) {
   for (int v : kNV)
     if (v >= need) return v;
   return 0;
+}
+
+// The fast kernels' NV (H = 256 NV); 0: use the generic kernels.
+int fast_nv(int64_t H) {
+  if (H % 256) return 0;
+  const int64_t nv = H / 256;
+  return (nv <= 8 || nv == 12 || nv == 14 || nv == 16) ? (int)nv : 0;
+}
+
+template <int NV>
+void fwd4_launch(dim3 g, hipStream_t s, const RmsFwdArgs& a, bool delta, bool drop) {
+  const dim3 b(kWave * kRowsPerBlock);
+  if (delta && drop) hipLaunchKernelGGL((rms_fwd4_kernel<NV, true, true>), g, b, 0, s, a);
+  else if (delta) hipLaunchKernelGGL((rms_fwd4_kernel<NV, true, false>), g, b, 0, s, a);
+  else if (drop) hipLaunchKernelGGL((rms_fwd4_kernel<NV, false, true>), g, b, 0, s, a);
+  else hipLaunchKernelGGL((rms_fwd4_kernel<NV, false, false>), g, b, 0, s, a);
+}
+template <int NV>
+void bwd4_launch(dim3 g, hipStream_t s, const RmsBwdArgs& a, bool drop, bool res) {
+  const dim3 b(kWave * kRowsPerBlock);
+  if (drop && res) hipLaunchKernelGGL((rms_bwd4_kernel<NV, true, true>), g, b, 0, s, a);
+  else if (drop) hipLaunchKernelGGL((rms_bwd4_kernel<NV, true, false>), g, b, 0, s, a);
+  else if (res) hipLaunchKernelGGL((rms_bwd4_kernel<NV, false, true>), g, b, 0, s, a);
+  else hipLaunchKernelGGL((rms_bwd4_kernel<NV, false, false>), g, b, 0, s, a);
+}
+
+template <class F>
+void by_nv(int nv, F&& f) {
+  switch (nv) {
+    case 1: f(std::integral_constant<int, 1>()); break;
+    case 2: f(std::integral_constant<int, 2>()); break;
+    case 3: f(std::integral_constant<int, 3>()); break;
+    case 4: f(std::integral_constant<int, 4>()); break;
+    case 5: f(std::integral_constant<int, 5>()); break;
+    case 6: f(std::integral_constant<int, 6>()); break;
+    case 7: f(std::integral_constant<int, 7>()); break;
+    case 8: f(std::integral_constant<int, 8>()); break;
+    case 12: f(std::integral_constant<int, 12>()); break;
+    case 14: f(std::integral_constant<int, 14>()); break;
+    default: f(std::integral_constant<int, 16>()); break;
+  }
 }
 
 template <template <int, int> class K, int W, class Args>
@@ -325,8 +537,16 @@ QLORA_API int qlora_rms_fwd(const float* x, const void* delta, const void* w, in
   const int nv = pick_nv(qlora_cdiv(H / W, kWave));
   QLORA_CHECK_ARG(nv > 0);
   const dim3 grid((unsigned)qlora_cdiv(n, kRowsPerBlock));
-  if (v4) launch_nv<FwdK, 4>(nv, grid, (hipStream_t)stream, a);
-  else launch_nv<FwdK, 1>(nv, grid, (hipStream_t)stream, a);
+  const int fnv = v4 ? fast_nv(H) : 0;
+  if (fnv > 0) {
+    const bool delta = a.delta != nullptr, drop = a.yq != nullptr || a.yv != nullptr;
+    by_nv(fnv, [&](auto k) { fwd4_launch<decltype(k)::value>(grid, (hipStream_t)stream, a,
+                                                                delta, drop); });
+  } else if (v4) {
+    launch_nv<FwdK, 4>(nv, grid, (hipStream_t)stream, a);
+  } else {
+    launch_nv<FwdK, 1>(nv, grid, (hipStream_t)stream, a);
+  }
   return qlora_launch_status();
 }
 
@@ -359,8 +579,17 @@ QLORA_API int qlora_rms_bwd(const void* dy, const void* tq, const void* tv, cons
   const int nv = pick_nv(qlora_cdiv(H / W, kWave));
   QLORA_CHECK_ARG(nv > 0);
   const dim3 grid((unsigned)qlora_cdiv(n, kRowsPerBlock));
-  if (v4) launch_nv<BwdK, 4>(nv, grid, (hipStream_t)stream, a);
-  else launch_nv<BwdK, 1>(nv, grid, (hipStream_t)stream, a);
+  // the fast kernel takes both LoRA inputs or neither (the step's two cases)
+  const int fnv = v4 && (a.tq != nullptr) == (a.tv != nullptr) ? fast_nv(H) : 0;
+  if (fnv > 0) {
+    const bool drop = a.tq != nullptr, res = a.dres != nullptr;
+    by_nv(fnv, [&](auto k) { bwd4_launch<decltype(k)::value>(grid, (hipStream_t)stream, a,
+                                                                drop, res); });
+  } else if (v4) {
+    launch_nv<BwdK, 4>(nv, grid, (hipStream_t)stream, a);
+  } else {
+    launch_nv<BwdK, 1>(nv, grid, (hipStream_t)stream, a);
+  }
   return qlora_launch_status();
 }
 

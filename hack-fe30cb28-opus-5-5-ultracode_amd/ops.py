@@ -323,6 +323,9 @@ def _dropout_args(packed, x, seeds):
     batch, the keep probability and scale, the generator's seed, the q and v counters, threads."""
     tok = getattr(packed, "tok", None)
     p = getattr(packed, "dropout_p", 0.0) or 0.0
+    rows, T = getattr(packed, "rows", 0), getattr(packed, "T", 0)
+    if rows * T * x.shape[1] >= 2**32:
+        raise ValueError("the dropout element index (token * H + column) must stay below 2^32")
     return (tok, 1.0 - p, 1.0 / (1.0 - p), getattr(packed, "drop_seed", None) or 0, seeds[0],
             seeds[1], getattr(packed, "drop_threads", None) or 1)
 

@@ -59,7 +59,7 @@ int qlora_dropout_keep(int8_t* out, int64_t nelem, int64_t seed, int64_t ctr, in
  * RMSNorm forward over n rows of H: [x += f32(delta); xsum = x], rstd = 1/sqrt(mean(x^2)+eps),
  * y = w * (x * rstd) -> f16, and the LoRA inputs yq / yv = f16(keep ? y * keep_scale : 0) with
  * the keep masks of two dropout calls (counters ctr_q, ctr_v) at padded-batch elements
- * tok[row]*H + col. Replaces rms_fwd_kernel (kernels.py:145-175) <- _rms_fwd
+ * tok[row]*H + col (below 2^32). Replaces rms_fwd_kernel (kernels.py:145-175) <- _rms_fwd
  * (engine.py:947-966).
  *   x f32 [n,H]; delta f16 [n,H]; w [H] (f32, or f16 if w_half); xsum f32 [n,H];
  *   y, yq, yv f16 [n,H]; rstd f32 [n]; tok i64 [n]

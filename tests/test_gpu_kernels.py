@@ -194,7 +194,9 @@ class _Packed:
 
 
 @pytest.mark.parametrize("n,H,wdtype", [(37, 1536, torch.float32), (5, 100, torch.float32),
-                                        (2304, 1536, torch.float16), (3, 50, torch.float16)])
+                                        (2304, 1536, torch.float16), (3, 50, torch.float16),
+                                        (7, 3584, torch.float32), (9, 896, torch.float32),
+                                        (4, 256, torch.float16)])
 def test_rms_forward_backward(pkg, n, H, wdtype):
     g = torch.Generator().manual_seed(0)
     x = torch.randn(n, H, generator=g) * 3
