@@ -9,6 +9,7 @@ stream. There is no Triton and no CPU fallback: without the built library every 
   linear   the step's GEMMs (NF4 projections forward/backward, lm_head)
   gemm     plain fp16 GEMMs through rocBLAS with a measured solution per shape and token bucket
   head     the LM head over vocabulary pieces with the hidden and embedding gradients
+  trainer  the HF / TRL Trainer drop-in: compute_loss replaced by the fused step (install)
   ops      the engine's op wrappers (_rms_fwd, _rms_bwd, _rope_fwd, _rope_bwd, _glu_fwd,
            _glu_bwd, _attn_fwd, _attn_bwd, _ce, _ce_piece, _ce_finish, _ce_grad, dequant,
            dequant_many, NF4Weight, NF4Group, TorchDropout)
@@ -17,7 +18,7 @@ stream. There is no Triton and no CPU fallback: without the built library every 
   build    hipcc build of the library
 """
 
-from . import _lib, ops, quant, gemm, linear, engine, head, profiling  # noqa: F401
+from . import _lib, ops, quant, gemm, linear, engine, head, profiling, trainer  # noqa: F401
 from .ops import (NF4Group, NF4Weight, TorchDropout, _attn_bwd, _attn_fwd, _ce,  # noqa: F401
                   _ce_finish, _ce_grad, _ce_piece, _glu_bwd, _glu_fwd, _rms_bwd, _rms_fwd,
                   _rope_bwd, _rope_fwd, dequant, dequant_many)

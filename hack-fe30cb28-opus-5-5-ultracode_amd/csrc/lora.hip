@@ -30,7 +30,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr int kRank = 16;
 constexpr int kTok = 32;
 constexpr int kWaves = 8;
-constexpr int kChunk1 = 6;  // phase-1 k-steps per wavefront per chunk
+constexpr int kChunk1 = 12;  // phase-1 k-steps per wavefront per chunk
 constexpr int kChunk2 = 6;  // phase-2 column tiles per wavefront per chunk
 
 struct Job {

@@ -124,6 +124,93 @@ def random_qwen2(cfg, device, seed=0, norm_dtype=torch.float32):
     return FusedQwen2(cfg, layers, embed, norm_w, device)
 
 
+class UnsupportedModel(ValueError):
+    """The model is not a PEFT-wrapped 4-bit Qwen2 the step supports (patch.py:_is_supported)."""
+
+
+def _lora_targets(layer):
+    """The adapter name of each LoRA-wrapped projection of a decoder layer, {"q": name, ...}."""
+    out = {}
+    projs = {"q": layer.self_attn.q_proj, "k": layer.self_attn.k_proj,
+             "v": layer.self_attn.v_proj, "o": layer.self_attn.o_proj,
+             "gate": layer.mlp.gate_proj, "up": layer.mlp.up_proj,
+             "down": layer.mlp.down_proj}
+    for short, module in projs.items():
+        lora_a = getattr(module, "lora_A", None)
+        if lora_a is None or len(lora_a) == 0:
+            continue
+        active = getattr(module, "active_adapter", None)
+        if isinstance(active, (list, tuple)):
+            active = active[0] if active else None
+        out[short] = active if active in lora_a else next(iter(lora_a.keys()))
+    return out
+
+
+@torch.no_grad()
+def from_peft(peft_model, keep_all=None):
+    """The step over a PEFT-wrapped, bitsandbytes-4bit Qwen2ForCausalLM (engine.py:1571-1600,
+    875-921): the NF4 weights and norms are borrowed (Params4bit `.data` / `.quant_state`), the
+    LoRA A/B parameters are the PEFT modules' own (the optimizer's), the embedding is the tied
+    lm_head. Supported: LoRA on q and v only, one dropout probability, one scaling."""
+    causal = peft_model.get_base_model() if hasattr(peft_model, "get_base_model") else peft_model
+    inner = causal.model
+    hf = causal.config
+    layers_hf = list(inner.layers)
+    if not layers_hf:
+        raise UnsupportedModel("no decoder layers")
+    names = _lora_targets(layers_hf[0])
+    if set(names) != {"q", "v"}:
+        raise UnsupportedModel(f"LoRA on {sorted(names)}; the step takes LoRA on q and v only")
+    H, HQ = hf.hidden_size, hf.num_attention_heads
+    D = getattr(hf, "head_dim", None) or H // HQ
+    rope = getattr(hf, "rope_parameters", None) or {}
+    theta = getattr(hf, "rope_theta", None) or rope.get("rope_theta", 10000.0)
+    q0 = layers_hf[0].self_attn.q_proj
+    qname = names["q"]
+    r = int(q0.lora_A[qname].weight.shape[0])
+    scaling = float(q0.scaling[qname])
+    drop = q0.lora_dropout[qname] if hasattr(q0, "lora_dropout") else None
+    p = float(getattr(drop, "p", 0.0))
+    cfg = Qwen2Config(hidden_size=H, intermediate_size=hf.intermediate_size,
+                      num_hidden_layers=len(layers_hf), num_attention_heads=HQ,
+                      num_key_value_heads=hf.num_key_value_heads, head_dim=D,
+                      vocab_size=hf.vocab_size, rope_theta=float(theta),
+                      rms_norm_eps=float(layers_hf[0].input_layernorm.variance_epsilon),
+                      lora_r=r, lora_alpha=scaling * r, lora_dropout=p)
+
+    def base_of(module):
+        return getattr(module, "base_layer", module)
+
+    specs = []
+    for i, layer in enumerate(layers_hf):
+        attn, mlp = layer.self_attn, layer.mlp
+        projs = {name: getattr(attn, name) for name in ("q_proj", "k_proj", "v_proj", "o_proj")}
+        projs.update({name: getattr(mlp, name) for name in ("gate_proj", "up_proj", "down_proj")})
+        nf4 = {name: base_of(m).weight for name, m in projs.items()}
+        biases = [base_of(projs[n]).bias for n in ("q_proj", "k_proj", "v_proj")]
+        if any(b is None for b in biases):
+            raise UnsupportedModel("q/k/v projections without bias (not Qwen2)")
+        bias = torch.cat([b.detach().to(torch.float16) for b in biases]).contiguous()
+        lora = {}
+        for short in ("q", "v"):
+            module, name = projs[f"{short}_proj"], names[short]
+            if float(module.scaling[name]) != scaling:
+                raise UnsupportedModel("LoRA scalings differ between adapters")
+            lora[short] = (module.lora_A[name].weight, module.lora_B[name].weight, scaling)
+        specs.append(LayerSpec(i, cfg, layer.input_layernorm.weight,
+                               layer.post_attention_layernorm.weight, nf4, bias, lora))
+    embed = inner.embed_tokens.weight
+    lm = causal.lm_head.weight
+    if lm.data_ptr() != embed.data_ptr():
+        raise UnsupportedModel("lm_head is not tied to the embedding")
+    if embed.dtype != torch.float16:
+        raise UnsupportedModel("the tied embedding must be fp16")
+    model = FusedQwen2(cfg, specs, embed.detach(), inner.norm.weight.detach(), embed.device,
+                       keep_all=keep_all)
+    model.eps = float(inner.norm.variance_epsilon)
+    return model
+
+
 # ---------------------------------------------------------------------------------------------
 # Per-step packing (engine.py:705-764)
 # ---------------------------------------------------------------------------------------------
@@ -211,6 +298,11 @@ class Packed:
         self.lora16_views = None
         self.lora16t_views = None
         self.grad16 = None  # (dh, fp16(dh)) handed from a layer's backward to the one below
+
+    @property
+    def row_of_token(self):
+        """Each packed token's row of the batch (int64 [n], on the device)."""
+        return self.tok // self.T
 
     def lora16(self, index, weights):
         if self.lora16_views is not None:

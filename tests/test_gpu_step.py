@@ -154,3 +154,96 @@ def test_host_metadata_gives_the_same_step(pkg):
     assert torch.equal(t0, t1) and torch.equal(c0, c1)
     for a, b in zip(g0, g1):
         assert torch.equal(a, b)
+
+
+def _peft_tree(model):
+    """A stand-in for a PEFT-wrapped bitsandbytes 4-bit Qwen2ForCausalLM over the same weights:
+    the attribute paths engine.from_peft reads (engine.py:875-906, 1571-1600)."""
+    from types import SimpleNamespace as NS
+    cfg = model.cfg
+    layers = []
+    for spec in model.layers:
+        D = spec.D
+        nq, nk = spec.HQ * D, spec.HKV * D
+        b = spec.bias_qkv
+        biases = {"q_proj": b[:nq], "k_proj": b[nq:nq + nk], "v_proj": b[nq + nk:]}
+
+        def proj(name, short=None):
+            base = NS(weight=spec.w[name].param, bias=biases.get(name))
+            m = NS(base_layer=base)
+            if short is not None:
+                A, B, s = spec.lora[short]
+                m.lora_A = {"default": NS(weight=A)}
+                m.lora_B = {"default": NS(weight=B)}
+                m.scaling = {"default": s}
+                m.lora_dropout = {"default": NS(p=cfg.lora_dropout)}
+                m.active_adapter = ["default"]
+            return m
+
+        attn = NS(q_proj=proj("q_proj", "q"), k_proj=proj("k_proj"), v_proj=proj("v_proj", "v"),
+                  o_proj=proj("o_proj"))
+        mlp = NS(gate_proj=proj("gate_proj"), up_proj=proj("up_proj"),
+                 down_proj=proj("down_proj"))
+        layers.append(NS(self_attn=attn, mlp=mlp,
+                         input_layernorm=NS(weight=spec.ln1, variance_epsilon=spec.eps),
+                         post_attention_layernorm=NS(weight=spec.ln2,
+                                                     variance_epsilon=spec.eps)))
+    embed = NS(weight=model.embed)
+    inner = NS(layers=layers, embed_tokens=embed,
+               norm=NS(weight=model.norm_w, variance_epsilon=model.eps))
+    config = NS(hidden_size=cfg.hidden_size, intermediate_size=cfg.intermediate_size,
+                num_attention_heads=cfg.num_attention_heads,
+                num_key_value_heads=cfg.num_key_value_heads, head_dim=cfg.head_dim,
+                vocab_size=cfg.vocab_size, rope_theta=cfg.rope_theta)
+    causal = NS(model=inner, lm_head=NS(weight=model.embed), config=config)
+    return NS(get_base_model=lambda: causal)
+
+
+def test_from_peft_and_trainer_drop_in(pkg):
+    """engine.from_peft over a PEFT-shaped module tree of the same weights gives the same step
+    (loss and LoRA gradients bit for bit), and trainer.install + compute_loss runs it."""
+    import types
+    model = _tiny(pkg)
+    twin = pkg.engine.from_peft(_peft_tree(model))
+    assert twin.dropout_p == model.dropout_p and len(twin.layers) == len(model.layers)
+    lengths = [17, 60, 33, 5]
+    ids, mask, labels = _batch(lengths, 3000)
+    denom = float((labels[:, 1:] != -100).sum())
+    out = []
+    for m in (model, twin):
+        for p in m.parameters():
+            p.grad = None
+        torch.cuda.manual_seed(5)
+        loss, _, _ = m.step(ids.to(DEV), mask.to(DEV), labels.to(DEV), denom)
+        loss.backward()
+        torch.cuda.synchronize()
+        out.append((loss.item(), [p.grad.clone() for p in m.parameters()]))
+    assert out[0][0] == out[1][0]
+    for a, b in zip(out[0][1], out[1][1]):
+        assert torch.equal(a, b)
+
+    class Tr:
+        compute_loss_func = label_smoother = None
+        model_accepts_loss_kwargs = False
+        args = types.SimpleNamespace(average_tokens_across_devices=False, n_gpu=1)
+
+        def __init__(self):
+            self._metrics = {"train": {"entropy": [], "mean_token_accuracy": []}}
+            self.cbs = []
+
+        def compute_loss(self, model, inputs, return_outputs=False, num_items_in_batch=None):
+            raise AssertionError("the fused step should run")
+
+        def add_callback(self, cb):
+            self.cbs.append(cb)
+
+    tr = Tr()
+    assert pkg.trainer.install(tr, engine=twin)
+    torch.cuda.manual_seed(5)
+    batch = {"input_ids": ids.to(DEV), "attention_mask": mask.to(DEV), "labels": labels.to(DEV)}
+    loss = tr.compute_loss(types.SimpleNamespace(training=True), batch)
+    assert loss.item() == out[0][0]
+    tr.cbs[0].on_pre_optimizer_step(None, None, None)
+    assert len(tr._metrics["train"]["entropy"]) == 1
+    assert tr._metrics["train"]["num_tokens"] == [sum(lengths)]
+    assert 0.0 <= tr._metrics["train"]["mean_token_accuracy"][0] <= 1.0

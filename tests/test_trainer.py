@@ -1,0 +1,150 @@
+"""The trainer drop-in's host logic (the reference's patch.py:268-398) against a stand-in engine
+on the CPU: when the fused step runs and when the original compute_loss does, the loss
+normaliser, the UnsupportedBatch fallback, the metrics and their deferred recording."""
+
+import types
+
+import pytest
+import torch
+
+
+class _Packed:
+    def __init__(self, n, targets, rows, T):
+        self.n, self.targets, self.rows, self.T = n, targets, rows, T
+        self.tok = torch.arange(n)
+
+    @property
+    def row_of_token(self):
+        return self.tok // self.T
+
+
+class _Stats:
+    pass
+
+
+class _Engine:
+    """Returns a loss that records the denominator it was given; raises UnsupportedBatch on
+    request."""
+
+    def __init__(self, pkg, fail=False):
+        self.pkg, self.fail, self.calls = pkg, fail, []
+
+    def step(self, ids, mask, labels, denom):
+        if self.fail:
+            raise self.pkg.engine.UnsupportedBatch("left padding")
+        self.calls.append(denom)
+        B, T = ids.shape
+        n = int(mask.sum())
+        targets = torch.tensor([1, -100, 2, 3][:n] + [5] * max(0, n - 4))
+        packed = _Packed(n, targets, B, T)
+        stats = _Stats()
+        stats.entropy = torch.full((n,), 2.0)
+        stats.correct = torch.tensor([1, 0, 1, 0][:n] + [1] * max(0, n - 4), dtype=torch.int32)
+        stats.tok_loss = torch.ones(n)
+        stats.order = torch.arange(n)
+        loss = torch.tensor(3.0, requires_grad=True) * 1.0
+        return loss, packed, stats
+
+
+class _Trainer:
+    def __init__(self):
+        self.compute_loss_func = None
+        self.label_smoother = None
+        self.model_accepts_loss_kwargs = False
+        self.args = types.SimpleNamespace(average_tokens_across_devices=False, n_gpu=1)
+        self._metrics = {"train": {"entropy": [], "mean_token_accuracy": []}}
+        self.callbacks = []
+        self.original_calls = 0
+
+    def compute_loss(self, model, inputs, return_outputs=False, num_items_in_batch=None):
+        self.original_calls += 1
+        return torch.tensor(-1.0)
+
+    def add_callback(self, cb):
+        self.callbacks.append(cb)
+
+
+def _batch():
+    ids = torch.tensor([[5, 6, 7, 8], [9, 10, 0, 0]])
+    mask = torch.tensor([[1, 1, 1, 1], [1, 1, 0, 0]])
+    labels = torch.tensor([[-100, 6, 7, 8], [-100, 10, -100, -100]])
+    return {"input_ids": ids, "attention_mask": mask, "labels": labels}
+
+
+def _install(pkg, engine):
+    tr = _Trainer()
+    assert pkg.trainer.install(tr, engine=engine)
+    assert pkg.trainer.install(tr, engine=engine)  # idempotent
+    assert len(tr.callbacks) == 1
+    return tr
+
+
+def test_fused_step_runs_and_normalises_like_hf(pkg):
+    eng = _Engine(pkg)
+    tr = _install(pkg, eng)
+    model = types.SimpleNamespace(training=True)
+    loss = tr.compute_loss(model, _batch())
+    assert float(loss) == 3.0 and tr.original_calls == 0
+    assert eng.calls == [4.0]  # supervised shifted labels: 6, 7, 8 and 10
+    tr.model_accepts_loss_kwargs = True
+    tr.compute_loss(model, _batch(), num_items_in_batch=torch.tensor(11))
+    assert eng.calls[-1] == 11.0
+    tr.compute_loss(model, _batch(), num_items_in_batch=None)
+    assert eng.calls[-1] == 4.0
+
+
+def test_original_compute_loss_when_not_usable(pkg):
+    eng = _Engine(pkg)
+    tr = _install(pkg, eng)
+    train = types.SimpleNamespace(training=True)
+    b = _batch()
+    b["pixel_values"] = torch.zeros(1)
+    assert float(tr.compute_loss(train, b)) == -1.0
+    assert float(tr.compute_loss(types.SimpleNamespace(training=False), _batch())) == -1.0
+    tr.compute_loss_func = lambda *a, **k: None
+    assert float(tr.compute_loss(train, _batch())) == -1.0
+    assert tr.original_calls == 3 and eng.calls == []
+
+
+def test_unsupported_batch_falls_back_with_inputs_intact(pkg):
+    tr = _install(pkg, _Engine(pkg, fail=True))
+    b = _batch()
+    b["_prediction_loss_only"] = True
+    assert float(tr.compute_loss(types.SimpleNamespace(training=True), b)) == -1.0
+    assert tr.original_calls == 1 and "_prediction_loss_only" in b
+
+
+def test_metrics_recorded_after_backward_is_queued(pkg):
+    tr = _install(pkg, _Engine(pkg))
+    model = types.SimpleNamespace(training=True)
+    tr.compute_loss(model, _batch())
+    m = tr._metrics["train"]
+    assert m["num_tokens"] == [6] and m["entropy"] == []  # deferred
+    tr.callbacks[0].on_pre_optimizer_step(None, None, None)
+    assert m["entropy"] == [2.0]
+    # correct 1,0,1,0,1,1 over the supervised 1,-,2,3,5,5: 4 right out of 5 supervised
+    assert m["mean_token_accuracy"] == [pytest.approx(4 / 5)]
+    tr.compute_loss(model, _batch())  # the next micro-batch flushes nothing new by itself
+    assert m["num_tokens"] == [12] and len(m["entropy"]) == 1
+    tr.callbacks[0].on_step_end(None, None, None)
+    assert len(m["entropy"]) == 2
+    tr.callbacks[0].on_step_end(None, None, None)  # nothing pending: no new entry
+    assert len(m["entropy"]) == 2
+
+
+def test_average_tokens_across_devices_scales_the_loss(pkg):
+    tr = _install(pkg, _Engine(pkg))
+    tr.model_accepts_loss_kwargs = True
+    tr.args.average_tokens_across_devices = True
+    tr.accelerator = types.SimpleNamespace(num_processes=4, parallelism_config=None)
+    loss = tr.compute_loss(types.SimpleNamespace(training=True), _batch(), num_items_in_batch=8)
+    assert float(loss) == 12.0
+
+
+def test_row_losses(pkg):
+    eng = _Engine(pkg)
+    b = _batch()
+    loss, packed, stats = eng.step(b["input_ids"], b["attention_mask"], b["labels"], 1.0)
+    means, counts = pkg.trainer.row_losses(packed, stats, b["labels"])
+    assert counts == [3, 1]
+    assert means == pytest.approx([4 / 3, 2.0])  # row 0 holds tokens 0-3, row 1 4-5 (T = 4)
