@@ -5,7 +5,7 @@ Compiled in-tree, next to this file, so the library travels with the source tree
   -ffp-contract=off          no implicit FMA: the NF4 dequant must round the product
                              code2 * absmax2 before adding the offset, as bitsandbytes does
   -target-feature -packed-fp32-ops   no packed fp32 VALU instructions
-Linked against rocBLAS (the plain projection GEMMs, csrc/blas.hip).
+Linked against rocBLAS and hipBLASLt (the plain projection GEMMs, csrc/blas.hip, csrc/blaslt.hip).
 Usage: python -m <package>.build  (or build() from __graft_entry__)
 """
 
@@ -56,7 +56,7 @@ def build(verbose=False, jobs=None):
         raise RuntimeError(f"hipcc failed:\n{msg}")
     tmp = LIB + ".tmp"
     cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp,
-           "-L/opt/rocm/lib", "-lrocblas"]
+           "-L/opt/rocm/lib", "-lrocblas", "-lhipblaslt"]
     subprocess.run(cmd, check=True)
     os.replace(tmp, LIB)
     return LIB

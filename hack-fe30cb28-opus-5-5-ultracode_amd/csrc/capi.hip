@@ -3,8 +3,22 @@
 
 #include <rocblas/rocblas.h>
 
-// Codes from 100000 up are rocBLAS statuses (qlora_gemm*), below are hipError_t values.
+// Codes from 200000 up are hipBLASLt statuses (qlora_gemmlt*), from 100000 up rocBLAS statuses
+// (qlora_gemm*), below are hipError_t values.
 QLORA_API const char* qlora_error_string(int code) {
+  if (code >= 200000) {
+    switch (code - 200000) {
+      case 1: return "hipBLASLt: not initialized";
+      case 2: return "hipBLASLt: allocation failed";
+      case 3: return "hipBLASLt: invalid value";
+      case 4: return "hipBLASLt: mapping error";
+      case 5: return "hipBLASLt: execution failed";
+      case 6: return "hipBLASLt: internal error";
+      case 7: return "hipBLASLt: not supported";
+      case 8: return "hipBLASLt: architecture mismatch";
+      default: return "hipBLASLt: error";
+    }
+  }
   if (code >= 100000) return rocblas_status_to_string((rocblas_status)(code - 100000));
   return hipGetErrorString((hipError_t)code);
 }

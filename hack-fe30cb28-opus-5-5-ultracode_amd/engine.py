@@ -610,13 +610,13 @@ class FusedQwen2:
         return int(max(0, min(len(self.layers), free // per_layer)))
 
     def gemm_shapes(self):
-        """(op, N, K) of the step's GEMMs: y = x W^T for qkv, o, gate|up, down and the lm_head,
-        and dX = dY W for the same five weights."""
+        """(op, N, K, bias) of the step's GEMMs: y = x W^T (+ b for qkv) for qkv, o, gate|up,
+        down and the lm_head, and dX = dY W for the same five weights (the lm_head last)."""
         spec = self.layers[0]
         H, I, qkv, o = spec.H, spec.I, (spec.HQ + 2 * spec.HKV) * spec.D, spec.HQ * spec.D
         fwd = [(qkv, H), (H, o), (2 * I, H), (H, I), (self.cfg.vocab_size, H)]
-        return ([(G.NT, n, k) for n, k in fwd] +
-                [(G.NN, k, n) for n, k in fwd])
+        return ([(G.NT, n, k, i == 0) for i, (n, k) in enumerate(fwd)] +
+                [(G.NN, k, n, False) for n, k in fwd])
 
     def tune_gemms(self, token_counts, log=None):
         """Measure the GEMM solutions for the buckets of these step sizes (tokens); the head's

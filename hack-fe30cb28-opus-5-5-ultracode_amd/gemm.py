@@ -1,5 +1,5 @@
 """The step's plain fp16 GEMMs through qlora_gemm / qlora_gemm_splitk (rocBLAS, Tensile kernels)
-with a variant measured per weight shape and token-count bucket.
+and qlora_gemmlt (hipBLASLt) with a variant measured per weight shape and token-count bucket.
 
 y = x W^T and dX = dY W (engine.py:1082-1316, 1376-1381) are torch matmuls in the reference,
 i.e. whatever kernel the library's size heuristic picks. At this step's sizes (M = a few
@@ -10,10 +10,19 @@ output has too few tiles to fill 256 CUs - there a split of K into slices (fp32 
 fixed-order sum) wins.
 
 A variant is (solution, splits): solution -1 = torch's matmul, 0 = rocBLAS's own choice, > 0 a
-Tensile solution index; splits 1 = one GEMM, > 1 = qlora_gemm_splitk. The tuner times every
-solution rocBLAS offers for a shape once (for each split count that divides K), keeps the
-fastest few as candidates, and then, per bucket of BUCKET tokens, the fastest candidate. Every
-variant computes fp16(sum of fp16 products in fp32 (+ bias)); only the summation order differs.
+Tensile solution index; splits 1 = one GEMM, > 1 = qlora_gemm_splitk; splits LT (0) =
+qlora_gemmlt with hipBLASLt's first choice for the exact problem, whose epilogue adds a bias
+before the one rounding (rocBLAS has no bias: the output is first filled with it, an extra
+write and read of the output, +30 % on the qkv projection). The tuner times every solution
+rocBLAS offers for a shape once (for each split count that divides K), keeps the fastest few as
+candidates, and then, per bucket of BUCKET tokens, the fastest candidate, with the bias when the
+shape has one. Every variant computes fp16(sum of fp16 products in fp32 (+ bias)); only the
+summation order differs.
+
+hipBLASLt's listed solutions are not candidates: they are mostly rocBLAS's own (rocBLAS runs
+the same Tensile library on this GPU), none was faster than rocBLAS's best by more than 4 % at
+the step's shapes with cold caches, and listing them costs ~30 ms of host time per new token
+count and shape, against ~10 us for the first choice.
 """
 
 import ctypes
@@ -28,11 +37,14 @@ BUCKET = 256
 TORCH = (-1, 1)   # torch's matmul
 DEFAULT = (0, 1)  # rocBLAS's own choice
 NT, NN = 0, 1     # op: C = A B^T (B [N, K]) or C = A B (B [K, N])
+LT = 0           # splits value of the hipBLASLt variant
+LT_DEFAULT = (0, LT)
+LT_WORKSPACE = 32 * 2**20  # bytes of workspace offered to hipBLASLt
 SPLITS = (2, 4, 8)
 MIN_SLICE = 1024  # no split leaves less than this much K per slice
 
-_CANDIDATES = {}  # (device index, op, N, K) -> [variant, ...]
-_CHOICE = {}      # (device index, op, N, K, bucket) -> variant
+_CANDIDATES = {}  # (device index, op, N, K, bias) -> [variant, ...]
+_CHOICE = {}      # (device index, op, N, K, bias, bucket) -> variant
 
 
 def _bucket(M):
@@ -64,22 +76,29 @@ def split_counts(N, K):
     return [s for s in SPLITS if K % (8 * s) == 0 and K // s >= MIN_SLICE]
 
 
-def choice(dev_index, op, N, K, M):
+def choice(dev_index, op, N, K, M, bias=False):
     """The variant used for this problem: the tuned one for M's bucket, else the nearest tuned
     bucket's, else torch's matmul."""
     b = _bucket(M)
-    v = _CHOICE.get((dev_index, op, N, K, b))
+    shape = (dev_index, op, N, K, bool(bias))
+    v = _CHOICE.get(shape + (b,))
     if v is not None:
         return v
-    near = [k[4] for k in _CHOICE if k[:4] == (dev_index, op, N, K)]
+    near = [k[5] for k in _CHOICE if k[:5] == shape]
     if not near:
         return TORCH
     nb = min(near, key=lambda x: (abs(x - b), x))
-    return _CHOICE[(dev_index, op, N, K, nb)]
+    return _CHOICE[shape + (nb,)]
 
 
 def _run(variant, op, a, b, out, bias, M, N, K, lda, ldb, ldc, dev, work=None):
     sol, splits = variant
+    if splits == LT:
+        if work is None or work.numel() * work.element_size() < LT_WORKSPACE:
+            work = torch.empty((LT_WORKSPACE,), device=dev, dtype=torch.uint8)
+        _lib.call("qlora_gemmlt", op, M, N, K, _ptr(a), lda, _ptr(b), ldb, _ptr(out), ldc,
+                  _ptr(bias), 1.0, 0.0, int(sol), _ptr(work), LT_WORKSPACE, _stream(dev))
+        return
     if splits == 1:
         beta = 0.0
         if bias is not None:
@@ -112,7 +131,7 @@ def mm(a, b, op, out=None, bias=None):
             raise ValueError("bias must have one entry per output column")
     if M == 0:
         return out
-    v = choice(dev.index or 0, op, N, K, M)
+    v = choice(dev.index or 0, op, N, K, M, bias is not None)
     if v == TORCH:
         bt = b.t() if op == NT else b
         if bias is not None:
@@ -125,8 +144,8 @@ def mm(a, b, op, out=None, bias=None):
     except RuntimeError:
         if v == DEFAULT:
             raise
-        # the bucket's variant rejects this exact size (rocBLAS checks before launching)
-        _CHOICE[(dev.index or 0, op, N, K, _bucket(M))] = DEFAULT
+        # the bucket's variant rejects this exact size (the libraries check before launching)
+        _CHOICE[(dev.index or 0, op, N, K, bias is not None, _bucket(M))] = DEFAULT
         _run(DEFAULT, op, a, b, out, bias, M, N, K, lda, ldb, ldc, dev)
     return out
 
@@ -180,45 +199,56 @@ def _time(fn, reps):
 
 
 def tune(shapes, Ms, device, top=6, top_split=2, reps=3, log=None):
-    """Measure, for each (op, N, K) in shapes and each token count in Ms, the fastest of: torch's
-    matmul, rocBLAS's default, the `top` solutions that were fastest at the median token count
-    and, per split count, rocBLAS's default and the `top_split` fastest. Buckets already tuned
-    are skipped. Returns the seconds spent."""
+    """Measure, for each (op, N, K[, bias]) in shapes and each token count in Ms, the fastest of:
+    torch's matmul, rocBLAS's default, hipBLASLt's first choice, the `top` rocBLAS solutions that
+    were fastest at the median token count and, per split count, rocBLAS's default and the
+    `top_split` fastest; with a bias added when the shape has one. Buckets already tuned are
+    skipped. Returns the seconds spent."""
     t0 = time.perf_counter()
     dev = torch.device(device)
     di = dev.index or 0
     buckets = sorted({_bucket(M) for M in Ms if M > 0})
-    work = [(op, N, K, [bk for bk in buckets if (di, op, N, K, bk) not in _CHOICE])
-            for op, N, K in shapes]
-    work = [w for w in work if w[3]]
+    work = []
+    for shape in shapes:
+        op, N, K = shape[:3]
+        has_bias = bool(shape[3]) if len(shape) > 3 else False
+        todo = [bk for bk in buckets if (di, op, N, K, has_bias, bk) not in _CHOICE]
+        if todo:
+            work.append((op, N, K, has_bias, todo))
     if not work:
         return 0.0
     m_max = buckets[-1] * BUCKET
     g = torch.Generator(device=dev).manual_seed(0)
-    for op, N, K, todo in work:
+    for op, N, K, has_bias, todo in work:
         a_full = torch.randn((m_max, K), device=dev, generator=g).to(torch.float16)
         bshape = (N, K) if op == NT else (K, N)
         b = (torch.randn(bshape, device=dev, generator=g) * 0.02).to(torch.float16)
+        bias = (torch.randn((N,), device=dev, generator=g) * 0.02).to(torch.float16) \
+            if has_bias else None
         c_full = torch.empty((m_max, N), device=dev, dtype=torch.float16)
         splits_ok = split_counts(N, K)
         ws = torch.empty((max(splits_ok, default=0) * m_max * N or 1,), device=dev,
                          dtype=torch.float32)
+        lt_ws = torch.empty((LT_WORKSPACE,), device=dev, dtype=torch.uint8)
         ldb = b.stride(0)
 
         def runner(v, M):
             a, c = a_full[:M], c_full[:M]
             if v == TORCH:
                 bt = b.t() if op == NT else b
+                if bias is not None:
+                    return lambda: torch.addmm(bias, a, bt, out=c)
                 return lambda: torch.mm(a, bt, out=c)
-            return lambda: _run(v, op, a, b, c, None, M, N, K, K, ldb, N, dev, work=ws)
+            w = lt_ws if v[1] == LT else ws
+            return lambda: _run(v, op, a, b, c, bias, M, N, K, K, ldb, N, dev, work=w)
 
         def listed(M, splits):
             return solutions(op, a_full[:M], b, c_full[:M], splits, ws)
 
-        key = (di, op, N, K)
+        key = (di, op, N, K, has_bias)
         if key not in _CANDIDATES:
             m_mid = todo[len(todo) // 2] * BUCKET
-            cands = [TORCH, DEFAULT]
+            cands = [TORCH, DEFAULT, LT_DEFAULT]
             for splits, keep in [(1, top)] + [(s, top_split) for s in splits_ok]:
                 timed = []
                 for sol in listed(m_mid, splits):
@@ -233,14 +263,23 @@ def tune(shapes, Ms, device, top=6, top_split=2, reps=3, log=None):
             _CANDIDATES[key] = cands
         for bk in todo:
             M = bk * BUCKET
-            valid = {TORCH, DEFAULT}
+            valid = {TORCH, DEFAULT, LT_DEFAULT}
             for splits in [1] + splits_ok:
                 valid |= {(s, splits) for s in [0] + listed(M, splits)}
-            best = min((_time(runner(v, M), reps), v) for v in _CANDIDATES[key] if v in valid)
+            timed = []
+            for v in _CANDIDATES[key]:
+                if v not in valid:
+                    continue
+                try:
+                    timed.append((_time(runner(v, M), reps), v))
+                except RuntimeError:
+                    continue  # e.g. hipBLASLt has no solution for this problem
+            best = min(timed)
             _CHOICE[key + (bk,)] = best[1]
             if log is not None:
-                log(f"gemm tune op={op} N={N} K={K} M={M}: {best[1]} {best[0] * 1e3:.1f} us")
-        del a_full, b, c_full, ws
+                log(f"gemm tune op={op} N={N} K={K} bias={int(has_bias)} M={M}: {best[1]} "
+                    f"{best[0] * 1e3:.1f} us")
+        del a_full, b, c_full, ws, lt_ws, bias
     return time.perf_counter() - t0
 
 

@@ -249,6 +249,25 @@ int qlora_gemm_splitk_solutions(int32_t op, int64_t M, int64_t N, int64_t K, con
                                 int32_t splits, int32_t* list, int32_t cap, int32_t* count);
 
 /*
+ * The qlora_gemm problem through hipBLASLt: C = alpha A op(B) (+ bias[N], f16, in the epilogue
+ * before the one rounding) + beta C. solution: an index that qlora_gemmlt_solutions lists for the
+ * same (op, sizes, leading dimensions, bias or not, ws_bytes); any other is rejected
+ * (hipErrorInvalidValue, nothing launched). workspace: device memory of ws_bytes (may be 0).
+ * Same reference call sites as qlora_gemm (engine.py:1082-1316); returns 200000 +
+ * hipblasStatus_t on a hipBLASLt error.
+ */
+int qlora_gemmlt(int32_t op, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
+                 const void* B, int64_t ldb, void* C, int64_t ldc, const void* bias, float alpha,
+                 float beta, int32_t solution, void* workspace, int64_t ws_bytes, void* stream);
+/*
+ * The solution indices hipBLASLt's heuristic returns for that problem (bias != 0: with the bias
+ * epilogue), in its order: up to cap into list, the number into *count. No kernel is launched.
+ */
+int qlora_gemmlt_solutions(int32_t op, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
+                           int64_t ldc, int32_t bias, int64_t ws_bytes, int32_t* list,
+                           int32_t cap, int32_t* count);
+
+/*
  * The LoRA forward of a layer's q and v adapters in one launch (engine.py:1088-1093):
  *   x_a = f16(a_a A_a^T)   f16 [n, 16] (kept for the backward)
  *   l_a = f16(x_a B_a^T)   f16 [n, N_a] (added to the projection output by qlora_rope_fwd)

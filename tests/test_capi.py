@@ -100,7 +100,16 @@ def test_gemm_rejects_bad_problems_before_any_device_call(pkg):
         assert lib.qlora_gemm_solutions(op, M, N, K, 8, lda, 8, max(K, N), 8, N, None, 0,
                                         ctypes.byref(cnt)) == 1
         assert lib.qlora_gemm(op, M, N, K, 8, lda, 8, max(K, N), 8, N, 1.0, 0.0, 0, None) == 1
+        assert lib.qlora_gemmlt_solutions(op, M, N, K, lda, max(K, N), N, 0, 0, None, 0,
+                                          ctypes.byref(cnt)) == 1
+        assert lib.qlora_gemmlt(op, M, N, K, 8, lda, 8, max(K, N), 8, N, None, 1.0, 0.0, 0,
+                                None, 0, None) == 1
+    # a workspace size without a workspace, a negative workspace size
+    assert lib.qlora_gemmlt(0, 4, 4, 4, 8, 4, 8, 4, 8, 4, None, 1.0, 0.0, 0, None, 64, None) == 1
+    assert lib.qlora_gemmlt_solutions(0, 4, 4, 4, 4, 4, 4, 0, -1, None, 0,
+                                      ctypes.byref(cnt)) == 1
     assert lib.qlora_error_string(100000 + 3) != lib.qlora_error_string(3)
+    assert lib.qlora_error_string(200000 + 3) != lib.qlora_error_string(100000 + 3)
 
 
 def test_gemm_splitk_rejects_bad_problems(pkg):

@@ -1,6 +1,9 @@
-"""The projections' plain GEMMs through qlora_gemm (rocBLAS with an explicit solution) against an
-fp64 product of the same fp16 operands: every solution computes fp16(sum in fp32), so results
-agree with fp64 to fp16 rounding plus fp32 summation-order noise."""
+"""The projections' plain GEMMs through qlora_gemm (rocBLAS with an explicit solution) and
+qlora_gemmlt (hipBLASLt) against an fp64 product of the same fp16 operands: every solution
+computes fp16(sum in fp32 (+ bias)), so results agree with fp64 to fp16 rounding plus fp32
+summation-order noise."""
+
+import ctypes
 
 import pytest
 import torch
@@ -64,8 +67,9 @@ def test_mm_bias_and_tuned_choice(pkg):
     G.reset()
     try:
         N, K = 512, 256
-        G.tune([(G.NT, N, K), (G.NN, K, N)], [700], DEV)
-        assert (0, G.NT, N, K, G._bucket(700)) in G._CHOICE
+        G.tune([(G.NT, N, K), (G.NT, N, K, True), (G.NN, K, N)], [700], DEV)
+        assert (0, G.NT, N, K, False, G._bucket(700)) in G._CHOICE
+        assert (0, G.NT, N, K, True, G._bucket(700)) in G._CHOICE
         g = torch.Generator(device=DEV).manual_seed(9)
         w = (torch.randn((N, K), device=DEV, generator=g) * 0.05).half()
         bias = (torch.randn((N,), device=DEV, generator=g) * 0.1).half()
@@ -78,7 +82,10 @@ def test_mm_bias_and_tuned_choice(pkg):
         # force a rocBLAS solution for the bucket and check the bias path through it
         sols = G.solutions(G.NT, x, w, torch.empty((x.shape[0], N), device=DEV,
                                                    dtype=torch.float16))
-        G._CHOICE[(0, G.NT, N, K, G._bucket(x.shape[0]))] = (sols[0], 1)
+        G._CHOICE[(0, G.NT, N, K, True, G._bucket(x.shape[0]))] = (sols[0], 1)
+        check(G.mm(x, w, G.NT, bias=bias), ref(x, w, 0, bias))
+        # and hipBLASLt's first choice, bias in its epilogue
+        G._CHOICE[(0, G.NT, N, K, True, G._bucket(x.shape[0]))] = G.LT_DEFAULT
         check(G.mm(x, w, G.NT, bias=bias), ref(x, w, 0, bias))
     finally:
         G.reset()
@@ -117,10 +124,70 @@ def test_mm_uses_a_tuned_split_variant(pkg):
     G.reset()
     try:
         N, K, M = 512, 16384, 600
-        G._CHOICE[(0, G.NN, N, K, G._bucket(M))] = (0, 4)
+        G._CHOICE[(0, G.NN, N, K, False, G._bucket(M))] = (0, 4)
         g = torch.Generator(device=DEV).manual_seed(3)
         dy = torch.randn((M, K), device=DEV, generator=g).half()
         w = (torch.randn((K, N), device=DEV, generator=g) * 0.05).half()
         check(G.mm(dy, w, G.NN), ref(dy, w, 1))
     finally:
         G.reset()
+
+
+def _lt_listed(pkg, op, M, N, K, lda, ldb, ldc, bias, ws_bytes):
+    cnt = ctypes.c_int32(0)
+    arr = (ctypes.c_int32 * 512)()
+    pkg._lib.call("qlora_gemmlt_solutions", op, M, N, K, lda, ldb, ldc, int(bias), ws_bytes, arr,
+                  512, ctypes.byref(cnt))
+    return list(arr)[:min(cnt.value, 512)]
+
+
+@pytest.mark.parametrize("op", [0, 1])
+@pytest.mark.parametrize("with_bias", [False, True])
+@pytest.mark.parametrize("M,N,K", [(1, 256, 128), (37, 384, 200), (2537, 2048, 1536)])
+def test_gemmlt_first_choice_and_listed_solutions(pkg, op, with_bias, M, N, K):
+    """qlora_gemmlt: hipBLASLt's first choice and a spread of its listed solutions for the exact
+    problem, with the bias added in the epilogue (one rounding), on strided views; columns
+    outside the output view stay untouched."""
+    g = torch.Generator(device=DEV).manual_seed(M + N + K + op + 7 * with_bias)
+    abuf = torch.randn((M, K + 8), device=DEV, generator=g).half()
+    b = (torch.randn((N, K) if op == 0 else (K, N), device=DEV, generator=g) * 0.05).half()
+    bias = (torch.randn((N,), device=DEV, generator=g) * 0.1).half() if with_bias else None
+    a = abuf[:, 8:]
+    want = ref(a, b, op, bias)
+    ws_bytes = pkg.gemm.LT_WORKSPACE
+    ws = torch.empty((ws_bytes,), device=DEV, dtype=torch.uint8)
+    cbuf = torch.full((M, N + 16), float("nan"), device=DEV, dtype=torch.float16)
+    out = cbuf[:, :N]
+    sols = _lt_listed(pkg, op, M, N, K, a.stride(0), b.stride(0), out.stride(0), with_bias,
+                      ws_bytes)
+    assert len(sols) > 0
+    for sol in [0] + sols[:: max(1, len(sols) // 5)]:
+        out.fill_(float("nan"))
+        pkg._lib.call("qlora_gemmlt", op, M, N, K, a.data_ptr(), a.stride(0), b.data_ptr(),
+                      b.stride(0), out.data_ptr(), out.stride(0),
+                      bias.data_ptr() if bias is not None else None, 1.0, 0.0, sol,
+                      ws.data_ptr(), ws_bytes, torch.cuda.current_stream().cuda_stream)
+        check(out, want)
+    assert torch.isnan(cbuf[:, N:].float()).all()
+
+
+def test_gemmlt_alpha_beta_and_unlisted_solution(pkg):
+    g = torch.Generator(device=DEV).manual_seed(11)
+    M, N, K = 300, 256, 320
+    a = torch.randn((M, K), device=DEV, generator=g).half()
+    b = (torch.randn((N, K), device=DEV, generator=g) * 0.05).half()
+    c = torch.randn((M, N), device=DEV, generator=g).half()
+    c0 = c.clone()
+    stream = torch.cuda.current_stream().cuda_stream
+    pkg._lib.call("qlora_gemmlt", 0, M, N, K, a.data_ptr(), K, b.data_ptr(), K, c.data_ptr(), N,
+                  None, 0.5, 2.0, 0, None, 0, stream)
+    torch.cuda.synchronize()
+    check(c, 0.5 * ref(a, b, 0) + 2.0 * c0.double())
+    listed = set(_lt_listed(pkg, 0, M, N, K, K, K, N, False, 0))
+    bogus = max(listed) + 1000
+    c1 = c.clone()
+    with pytest.raises(RuntimeError):
+        pkg._lib.call("qlora_gemmlt", 0, M, N, K, a.data_ptr(), K, b.data_ptr(), K,
+                      c.data_ptr(), N, None, 1.0, 0.0, bogus, None, 0, stream)
+    torch.cuda.synchronize()
+    assert torch.equal(c, c1)  # nothing ran
