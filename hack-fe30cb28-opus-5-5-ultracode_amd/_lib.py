@@ -49,6 +49,10 @@ SIGNATURES = {
     "qlora_gemmlt_solutions": [I32, I64, I64, I64, I64, I64, I64, I32, I64, P, I32, P],
     "qlora_attn_fwd": [P, P, P, P, P, P, I32, I32, I64, I32, I32, I32, F32, P],
     "qlora_attn_bwd": [P, P, P, P, P, P, P, P, P, P, P, I32, I32, I64, I32, I32, I32, F32, P],
+    "qlora_attn_split_workspace": [I32, I64, I32, I32, I32, P],
+    "qlora_attn_fwd_split": [P, P, P, P, P, P, I32, I32, I64, I32, I32, I32, F32, I32, P, I64, P],
+    "qlora_attn_bwd_split": [P, P, P, P, P, P, P, P, P, P, P, I32, I32, I64, I32, I32, I32, F32,
+                             I32, P, I64, P],
 }
 
 _lib = None

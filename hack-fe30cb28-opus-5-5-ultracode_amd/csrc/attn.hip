@@ -56,10 +56,23 @@ struct Args {
   float* lse;            // fp32 [HQ, n] natural-log log-sum-exp of each query's scores
   float* delta;          // fp32 [HQ, n]
   const int32_t* cu;     // int32 [nseq + 1]
+  float* part;           // split key range: fp32 partial O / dQ [nch][n][HQ][D]
+  float2* part_ml;       // forward split: (running max (log2 units), sum) [nch][HQ][n]
   int64_t n;
   int HQ, KH;
+  int chunk;             // key blocks per workgroup (0: the whole range in one workgroup)
+  int ntiles;            // query (forward, dQ) or key (dK/dV) tiles per sequence and head
   float scale;
 };
+
+// The key range of a query tile with nkb key blocks may be cut into chunks of a.chunk blocks, one
+// workgroup each (blockIdx.z = chunk), when a batch of few long sequences would otherwise leave
+// most of the GPU idle while its longest tiles walk their keys. With one chunk the workgroup
+// writes the result itself; otherwise each writes fp32 partials and attn_merge_kernel merges them
+// in chunk order.
+__device__ __forceinline__ int num_chunks(int nkb, int chunk) {
+  return chunk > 0 ? (nkb + chunk - 1) / chunk : 1;
+}
 
 // 2^x by the hardware instruction (v_exp_f32): no denormal-range fix-up (results below 2^-126
 // flush to zero, which a probability that small does not miss).
@@ -213,18 +226,40 @@ __device__ __forceinline__ void store_token_row(uint16_t* row, const f32x16 (&ac
     }
 }
 
+// Stores 32 x D fp32 values of one token (lane & 31) held as D/32 accumulators (d in the rows).
+template <int D>
+__device__ __forceinline__ void store_token_row_f32(float* row, const f32x16 (&acc)[D / 32],
+                                                    int lane) {
+#pragma unroll
+  for (int u = 0; u < D / 32; ++u)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int d = 32 * u + 8 * j + 4 * (lane >> 5);
+      *reinterpret_cast<float4*>(row + d) =
+          make_float4(acc[u][4 * j], acc[u][4 * j + 1], acc[u][4 * j + 2], acc[u][4 * j + 3]);
+    }
+}
+
 // ------------------------------------------------------------------------------------------------
 // Forward: O = softmax(scale Q K^T + causal mask) V per sequence, and the log-sum-exp.
-// grid (nseq * KH, ceil(max_len / 32)), block 64 * G (G = HQ / KH q heads, one per wavefront).
-// Key blocks of 64 keys: block kb + 1 is loaded into registers while block kb is multiplied.
+// grid (ceil(max_len / 32) * nseq * KH, 1, chunks), block 64 * G (G = HQ / KH q heads, one per
+// wavefront). Key blocks of 64 keys: block kb + 1 is loaded into registers while block kb is
+// multiplied. The longest query tiles' key ranges set the kernel's time when the batch has few
+// sequences (the rest of the GPU idles): cutting the range into chunks spreads one tile over
+// several workgroups.
 // ------------------------------------------------------------------------------------------------
 template <int D, int G>
 __global__ __launch_bounds__(64 * G) void attn_fwd_kernel(Args a) {
   constexpr int KC = D / 16, DT = D / 32, NT = 64 * G;
   __shared__ __align__(16) uint16_t ks[kKB * D];
   __shared__ __align__(16) uint16_t vt[D * kKB];
-  const int seq = blockIdx.x / a.KH, kvh = blockIdx.x % a.KH;
-  const int q0 = (gridDim.y - 1 - blockIdx.y) * kTok;  // longest rows first
+  // blockIdx.x = tile + ntiles (seq KH + kvh), the tile fastest: consecutive workgroups (which
+  // the dispatcher deals to the 8 XCDs in turn) take tiles of the same sequence, so every XCD
+  // gets a share of each; the longest rows first
+  const int sh = blockIdx.x / a.ntiles;
+  const int tile = a.ntiles - 1 - (int)(blockIdx.x - sh * a.ntiles);
+  const int seq = sh / a.KH, kvh = sh % a.KH;
+  const int q0 = tile * kTok;
   const int start = a.cu[seq], L = a.cu[seq + 1] - start;
   if (q0 >= L) return;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -234,13 +269,16 @@ __global__ __launch_bounds__(64 * G) void attn_fwd_kernel(Args a) {
   const int kvs_b = (int)(kvs * 2);
   const int kend = min(q0 + kTok, L);
   const int nkb = (kend + kKB - 1) / kKB;
+  const int nch = num_chunks(nkb, a.chunk), ch = blockIdx.z;
+  if (ch >= nch) return;
+  const int kb0 = ch * a.chunk, kb1 = nch == 1 ? nkb : min(nkb, kb0 + a.chunk);
   const rsrc_t ksrc = rows_rsrc(a.k + (int64_t)start * kvs + kvh * D, L, kvs, D);
   const rsrc_t vsrc = rows_rsrc(a.v + (int64_t)start * kvs + kvh * D, L, kvs, D);
 
   RowStage<D, kKB, NT> sk;
   PairStage<D, kKB, NT> sv;
-  sk.load(ksrc, 0, kvs_b, tid);
-  sv.load(vsrc, 0, kvs_b, tid);
+  sk.load(ksrc, kb0 * kKB, kvs_b, tid);
+  sv.load(vsrc, kb0 * kKB, kvs_b, tid);
 
   half8_t qr[KC];  // queries past the sequence read zeros (their rows are not stored)
   load_token<D>(rows_rsrc(a.q + (int64_t)start * qs + h * D, L, qs, D), qi, (int)(qs * 2), lane,
@@ -310,7 +348,7 @@ __global__ __launch_bounds__(64 * G) void attn_fwd_kernel(Args a) {
     }
   };
 
-  for (int kb = 0; kb < nkb; ++kb) {
+  for (int kb = kb0; kb < kb1; ++kb) {
     __syncthreads();
     sk.store(ks, tid);
     sv.store(vt, nullptr, tid);
@@ -321,9 +359,20 @@ __global__ __launch_bounds__(64 * G) void attn_fwd_kernel(Args a) {
     block(kb * kKB);
   }
   const float ltot = lsum + __shfl_xor(lsum, 32, 64);
+  if (nch == 1) {
+    if (qi < L) {
+      store_token_row<D>(a.out + (int64_t)(start + qi) * qs + h * D, o, 1.0f / ltot, lane);
+      if (lane < 32) a.lse[(int64_t)h * a.n + start + qi] = (m + log2f(ltot)) * kLn2;
+    }
+    return;
+  }
+  // Several chunks: this one's unnormalised partial and (m, l). Every chunk holds at least one
+  // unmasked key of each query (the last one starts at or before the tile's first query: q0 is
+  // a multiple of 32, blocks are 64 keys; the others precede it), so m is finite.
   if (qi < L) {
-    store_token_row<D>(a.out + (int64_t)(start + qi) * qs + h * D, o, 1.0f / ltot, lane);
-    if (lane < 32) a.lse[(int64_t)h * a.n + start + qi] = (m + log2f(ltot)) * kLn2;
+    store_token_row_f32<D>(a.part + (((int64_t)ch * a.n + start + qi) * a.HQ + h) * D, o, lane);
+    if (lane < 32)
+      a.part_ml[((int64_t)ch * a.HQ + h) * a.n + start + qi] = make_float2(m, ltot);
   }
 }
 
@@ -338,8 +387,10 @@ __global__ __launch_bounds__(64 * G) void attn_dq_kernel(Args a) {
   __shared__ __align__(16) uint16_t ks[KB * D];
   __shared__ __align__(16) uint16_t vs[KB * D];
   __shared__ __align__(16) uint16_t kt[D * KB];
-  const int seq = blockIdx.x / a.KH, kvh = blockIdx.x % a.KH;
-  const int q0 = (gridDim.y - 1 - blockIdx.y) * kTok;
+  const int sh = blockIdx.x / a.ntiles;  // as the forward
+  const int tile = a.ntiles - 1 - (int)(blockIdx.x - sh * a.ntiles);
+  const int seq = sh / a.KH, kvh = sh % a.KH;
+  const int q0 = tile * kTok;
   const int start = a.cu[seq], L = a.cu[seq + 1] - start;
   if (q0 >= L) return;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -349,13 +400,16 @@ __global__ __launch_bounds__(64 * G) void attn_dq_kernel(Args a) {
   const int qs_b = (int)(qs * 2), kvs_b = (int)(kvs * 2);
   const int kend = min(q0 + kTok, L);
   const int nkb = (kend + KB - 1) / KB;
+  const int nch = num_chunks(nkb, a.chunk), ch = blockIdx.z;
+  if (ch >= nch) return;
+  const int kb0 = ch * a.chunk, kb1 = nch == 1 ? nkb : min(nkb, kb0 + a.chunk);
   const rsrc_t ksrc = rows_rsrc(a.k + (int64_t)start * kvs + kvh * D, L, kvs, D);
   const rsrc_t vsrc = rows_rsrc(a.v + (int64_t)start * kvs + kvh * D, L, kvs, D);
 
   PairStage<D, KB, NT> sk;  // K into both the row tile and the transposed tile
   RowStage<D, KB, NT> sv;
-  sk.load(ksrc, 0, kvs_b, tid);
-  sv.load(vsrc, 0, kvs_b, tid);
+  sk.load(ksrc, kb0 * KB, kvs_b, tid);
+  sv.load(vsrc, kb0 * KB, kvs_b, tid);
 
   // this query's q, dO and O (queries past the sequence read zeros; their dq is not stored)
   const int64_t hoff = (int64_t)start * qs + h * D;
@@ -372,7 +426,7 @@ __global__ __launch_bounds__(64 * G) void attn_dq_kernel(Args a) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) dpart += (float)dr[kk][i] * (float)orow[kk][i];
   const float delta = dpart + __shfl_xor(dpart, 32, 64);
-  if (qi < L && lane < 32) a.delta[(int64_t)h * a.n + start + qi] = delta;
+  if (ch == 0 && qi < L && lane < 32) a.delta[(int64_t)h * a.n + start + qi] = delta;
 
   f32x16 dq[DT];
 #pragma unroll
@@ -380,7 +434,7 @@ __global__ __launch_bounds__(64 * G) void attn_dq_kernel(Args a) {
   const float c = a.scale * kLog2e;
   const int lim = min(qi, L - 1);
 
-  for (int kb = 0; kb < nkb; ++kb) {
+  for (int kb = kb0; kb < kb1; ++kb) {
     const int k0 = kb * KB;
     __syncthreads();
     sk.store(kt, ks, tid);
@@ -415,7 +469,75 @@ __global__ __launch_bounds__(64 * G) void attn_dq_kernel(Args a) {
       dq[u] = mfma(t1, sb[1], dq[u]);
     }
   }
-  if (qi < L) store_token_row<D>(a.out + (int64_t)(start + qi) * qs + h * D, dq, a.scale, lane);
+  if (nch == 1) {
+    if (qi < L) store_token_row<D>(a.out + (int64_t)(start + qi) * qs + h * D, dq, a.scale, lane);
+    return;
+  }
+  // several chunks: this one's unscaled partial
+  if (qi < L)
+    store_token_row_f32<D>(a.part + (((int64_t)ch * a.n + start + qi) * a.HQ + h) * D, dq, lane);
+}
+
+// ------------------------------------------------------------------------------------------------
+// Merge of the chunks' partials, in chunk order. Forward: M = max m_c, l = sum l_c 2^(m_c - M),
+// O = sum o_c 2^(m_c - M) / l, lse = (M + log2 l) ln 2; dQ: dq = scale sum dq_c. One thread per
+// 4 columns of a query row: all C chunk loads are issued before any use (chunks past the tile's
+// count read the last one again and weigh 0). blockIdx.x = tile + ntiles (q head of the group +
+// G (seq KH + kvh)), block 32 D/4; tiles of one chunk were written directly and are skipped.
+// ------------------------------------------------------------------------------------------------
+template <int D, int C, bool FWD>
+__global__ __launch_bounds__(32 * D / 4) void attn_merge_kernel(Args a) {
+  constexpr int D4 = D / 4, KBLK = FWD ? kKB : kTok;
+  const int G = a.HQ / a.KH;
+  const int rest = blockIdx.x / a.ntiles;
+  const int tile = (int)(blockIdx.x - rest * a.ntiles);
+  const int g = rest % G, sh = rest / G;
+  const int seq = sh / a.KH, h = (sh % a.KH) * G + g;
+  const int q0 = tile * kTok;
+  const int start = a.cu[seq], L = a.cu[seq + 1] - start;
+  if (q0 >= L) return;
+  const int kend = min(q0 + kTok, L);
+  const int nch = num_chunks((kend + KBLK - 1) / KBLK, a.chunk);
+  const int qi = q0 + (int)(threadIdx.x / D4), d4 = (int)(threadIdx.x % D4);
+  if (nch == 1 || qi >= L) return;
+  const int64_t cstride = a.n * a.HQ * D, mstride = (int64_t)a.HQ * a.n;
+  const float* src = a.part + ((int64_t)(start + qi) * a.HQ + h) * D + 4 * d4;
+  float4 x[C];
+  float w[C];
+#pragma unroll
+  for (int c = 0; c < C; ++c) x[c] = *reinterpret_cast<const float4*>(src + min(c, nch - 1) * cstride);
+  float M = 0.f, l = 0.f;
+  if constexpr (FWD) {
+    const float2* ml = a.part_ml + (int64_t)h * a.n + start + qi;
+    float2 y[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) y[c] = ml[min(c, nch - 1) * mstride];
+    M = -__builtin_inff();
+#pragma unroll
+    for (int c = 0; c < C; ++c) M = fmaxf(M, y[c].x);  // repeats of the last chunk change nothing
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      w[c] = c < nch ? ex2(y[c].x - M) : 0.f;
+      l += y[c].y * w[c];
+    }
+    const float inv = 1.0f / l;
+#pragma unroll
+    for (int c = 0; c < C; ++c) w[c] *= inv;
+  } else {
+#pragma unroll
+    for (int c = 0; c < C; ++c) w[c] = c < nch ? a.scale : 0.f;
+  }
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    acc.x += w[c] * x[c].x;
+    acc.y += w[c] * x[c].y;
+    acc.z += w[c] * x[c].z;
+    acc.w += w[c] * x[c].w;
+  }
+  *reinterpret_cast<uint2*>(a.out + ((int64_t)(start + qi) * a.HQ + h) * D + 4 * d4) =
+      make_uint2(pack2h(acc.x, acc.y), pack2h(acc.z, acc.w));
+  if (FWD && d4 == 0) a.lse[(int64_t)h * a.n + start + qi] = (M + log2f(l)) * kLn2;
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -424,7 +546,7 @@ __global__ __launch_bounds__(64 * G) void attn_dq_kernel(Args a) {
 // staging each block's Q and dO (rows and transposed, plus lse and delta) once for the four
 // wavefronts: S = Q K^T, P = exp(S - lse), dP = dO V^T, dS = P (dP - delta), dV^T += dO^T P,
 // dK^T += Q^T dS. A wavefront skips query blocks that lie wholly before its keys.
-// grid (nseq * HQ, ceil(max_len / 128)), block 256.
+// grid (nseq * HQ * ceil(max_len / 128)), block 256.
 // ------------------------------------------------------------------------------------------------
 constexpr int kKeyWaves = 4;
 
@@ -437,9 +559,14 @@ __global__ __launch_bounds__(64 * kKeyWaves) void attn_dkdv_kernel(Args a) {
   __shared__ __align__(16) uint16_t dt[D * kTok];
   __shared__ __align__(16) float lse_s[kTok];
   __shared__ __align__(16) float dl_s[kTok];
-  const int seq = blockIdx.x / a.HQ, h = blockIdx.x % a.HQ;
+  // blockIdx.x = (seq HQ + h) + pairs key tile: the first key tiles of every sequence and head,
+  // which walk the most queries, are dispatched first (with more workgroups than CUs, the
+  // heaviest then do not wait for a free CU)
+  const int pairs = (int)(gridDim.x / a.ntiles);
+  const int kt = blockIdx.x / pairs, sh = (int)(blockIdx.x - kt * pairs);
+  const int seq = sh / a.HQ, h = sh % a.HQ;
   const int kvh = h / (a.HQ / a.KH);
-  const int kw0 = blockIdx.y * kTok * kKeyWaves;
+  const int kw0 = kt * kTok * kKeyWaves;
   const int start = a.cu[seq], L = a.cu[seq + 1] - start;
   if (kw0 >= L) return;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -583,7 +710,134 @@ void launch_q_any(const Args& a, int D, int G, dim3 grid, hipStream_t s) {
   }
 }
 
+// Chunks of the split forms: chunk_keys a positive multiple of 64, at most kMaxChunks chunks.
+constexpr int kMaxChunks = 16;
+int split_chunks(int32_t max_len, int32_t chunk_keys, int64_t* nch) {
+  QLORA_CHECK_ARG(chunk_keys >= kKB && chunk_keys % kKB == 0);
+  *nch = qlora_cdiv(max_len, chunk_keys);
+  QLORA_CHECK_ARG(*nch >= 1 && *nch <= kMaxChunks);
+  return 0;
+}
+
+// Workgroups of one launch: tiles x (sequence, head) pairs, within the 32-bit grid.
+int grid_of(int64_t tiles, int64_t pairs, unsigned* x) {
+  QLORA_CHECK_ARG(tiles * pairs < (1ll << 31));
+  *x = (unsigned)(tiles * pairs);
+  return 0;
+}
+
+// The merge kernel for nch chunks (C: the next supported count at or above it).
+template <bool FWD>
+int launch_merge(const Args& a, int D, int64_t nseq, int64_t nch, hipStream_t s) {
+  unsigned gx;
+  if (int rc = grid_of(a.ntiles, nseq * a.HQ, &gx)) return rc;
+#define QLORA_MERGE(DD, CC) \
+  hipLaunchKernelGGL((attn_merge_kernel<DD, CC, FWD>), dim3(gx), dim3(32 * DD / 4), 0, s, a)
+  if (D == 128) {
+    if (nch <= 2) QLORA_MERGE(128, 2);
+    else if (nch <= 4) QLORA_MERGE(128, 4);
+    else if (nch <= 8) QLORA_MERGE(128, 8);
+    else QLORA_MERGE(128, 16);
+  } else {
+    if (nch <= 2) QLORA_MERGE(64, 2);
+    else if (nch <= 4) QLORA_MERGE(64, 4);
+    else if (nch <= 8) QLORA_MERGE(64, 8);
+    else QLORA_MERGE(64, 16);
+  }
+#undef QLORA_MERGE
+  return qlora_launch_status();
+}
+
+int run_fwd(Args a, int32_t nseq, int32_t max_len, int D, int64_t nch, hipStream_t s) {
+  a.ntiles = (int)qlora_cdiv(max_len, kTok);
+  unsigned gx;
+  if (int rc = grid_of(a.ntiles, (int64_t)nseq * a.KH, &gx)) return rc;
+  launch_q_any<false>(a, D, a.HQ / a.KH, dim3(gx, 1, (unsigned)nch), s);
+  if (int rc = qlora_launch_status()) return rc;
+  return nch > 1 ? launch_merge<true>(a, D, nseq, nch, s) : 0;
+}
+
+int run_bwd(Args a, int32_t nseq, int32_t max_len, int D, int64_t nch, hipStream_t s) {
+  a.ntiles = (int)qlora_cdiv(max_len, kTok);
+  unsigned gx;
+  if (int rc = grid_of(a.ntiles, (int64_t)nseq * a.KH, &gx)) return rc;
+  launch_q_any<true>(a, D, a.HQ / a.KH, dim3(gx, 1, (unsigned)nch), s);
+  if (int rc = qlora_launch_status()) return rc;
+  if (nch > 1) {
+    if (int rc = launch_merge<false>(a, D, nseq, nch, s)) return rc;
+  }
+  a.ntiles = (int)qlora_cdiv(max_len, kTok * kKeyWaves);
+  if (int rc = grid_of(a.ntiles, (int64_t)nseq * a.HQ, &gx)) return rc;
+  if (D == 128) hipLaunchKernelGGL(attn_dkdv_kernel<128>, dim3(gx), dim3(64 * kKeyWaves), 0, s, a);
+  else hipLaunchKernelGGL(attn_dkdv_kernel<64>, dim3(gx), dim3(64 * kKeyWaves), 0, s, a);
+  return qlora_launch_status();
+}
+
+Args make_args(const void* q, const void* k, const void* v, int64_t n, int32_t HQ, int32_t KH,
+               float scale, const int32_t* cu) {
+  Args a{};
+  a.q = static_cast<const uint16_t*>(q);
+  a.k = static_cast<const uint16_t*>(k);
+  a.v = static_cast<const uint16_t*>(v);
+  a.cu = cu;
+  a.n = n;
+  a.HQ = HQ;
+  a.KH = KH;
+  a.scale = scale;
+  return a;
+}
+
+// The split's chunk count and fp32 workspace for these sizes (none when max_len fits one chunk).
+int split_sizes(int32_t max_len, int64_t n, int32_t HQ, int32_t D, int32_t chunk_keys,
+                int64_t* nch, int64_t* work) {
+  if (int rc = split_chunks(max_len, chunk_keys, nch)) return rc;
+  *work = *nch == 1 ? 0 : *nch * n * HQ * (int64_t)(D + 2);
+  return 0;
+}
+
 }  // namespace
+
+// fp32 workspace elements of qlora_attn_fwd_split / qlora_attn_bwd_split for these sizes and
+// chunk_keys (keys per workgroup: a positive multiple of 64 with ceil(max_len / chunk_keys)
+// <= 16); 0 when max_len fits one chunk. No reference counterpart: a work split of the same
+// attention.
+QLORA_API int qlora_attn_split_workspace(int32_t max_len, int64_t n, int32_t HQ, int32_t D,
+                                         int32_t chunk_keys, int64_t* work_elems) {
+  QLORA_CHECK_ARG(work_elems && max_len >= 0 && n >= 0 && HQ > 0 && (D == 64 || D == 128));
+  *work_elems = 0;
+  if (max_len == 0 || n == 0) return 0;
+  int64_t nch;
+  return split_sizes(max_len, n, HQ, D, chunk_keys, &nch, work_elems);
+}
+
+// qlora_attn_fwd with each query tile's key range cut into chunks of chunk_keys keys (0: not
+// cut), one workgroup each, and a second kernel that merges the fp32 partials in chunk order.
+// work: fp32, 16-byte aligned, of qlora_attn_split_workspace elements. Same reference call site
+// as qlora_attn_fwd (engine.py:857-862).
+QLORA_API int qlora_attn_fwd_split(const void* q, const void* k, const void* v, void* out,
+                                   float* lse, const int32_t* cu_seqlens, int32_t nseq,
+                                   int32_t max_len, int64_t n, int32_t HQ, int32_t KH, int32_t D,
+                                   float scale, int32_t chunk_keys, float* work,
+                                   int64_t work_elems, void* stream) {
+  if (int rc = check_common(nseq, max_len, n, HQ, KH, D)) return rc;
+  if (n == 0 || nseq == 0 || max_len == 0) return 0;
+  int64_t nch = 1, need = 0;
+  if (chunk_keys != 0) {
+    if (int rc = split_sizes(max_len, n, HQ, D, chunk_keys, &nch, &need)) return rc;
+  }
+  QLORA_CHECK_ARG(q && k && v && out && lse && cu_seqlens);
+  QLORA_CHECK_ARG(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out));
+  QLORA_CHECK_ARG(work_elems >= need && (nch == 1 || (work && aligned16(work))));
+  Args a = make_args(q, k, v, n, HQ, KH, scale, cu_seqlens);
+  a.out = static_cast<uint16_t*>(out);
+  a.lse = lse;
+  if (nch > 1) {
+    a.chunk = chunk_keys / kKB;
+    a.part = work;
+    a.part_ml = reinterpret_cast<float2*>(work + nch * n * HQ * D);
+  }
+  return run_fwd(a, nseq, max_len, D, nch, (hipStream_t)stream);
+}
 
 // Forward. q [n, HQ, D], k/v [n, KH, D], out [n, HQ, D] fp16 contiguous; lse fp32 [HQ, n];
 // cu_seqlens int32 [nseq + 1] on the device, non-decreasing from 0 to n, every length
@@ -591,24 +845,42 @@ void launch_q_any(const Args& a, int D, int G, dim3 grid, hipStream_t s) {
 QLORA_API int qlora_attn_fwd(const void* q, const void* k, const void* v, void* out, float* lse,
                              const int32_t* cu_seqlens, int32_t nseq, int32_t max_len, int64_t n,
                              int32_t HQ, int32_t KH, int32_t D, float scale, void* stream) {
+  return qlora_attn_fwd_split(q, k, v, out, lse, cu_seqlens, nseq, max_len, n, HQ, KH, D, scale,
+                              0, nullptr, 0, stream);
+}
+
+// qlora_attn_bwd with the dQ kernel's key range cut into chunks of chunk_keys keys (0: not cut),
+// one workgroup each, summed in chunk order by a second kernel; dK/dV as in qlora_attn_bwd. work
+// as for qlora_attn_fwd_split. Same reference call site (engine.py:865-869).
+QLORA_API int qlora_attn_bwd_split(const void* dout, const void* q, const void* k, const void* v,
+                                   const void* out, const float* lse, float* delta, void* dq,
+                                   void* dk, void* dv, const int32_t* cu_seqlens, int32_t nseq,
+                                   int32_t max_len, int64_t n, int32_t HQ, int32_t KH, int32_t D,
+                                   float scale, int32_t chunk_keys, float* work,
+                                   int64_t work_elems, void* stream) {
   if (int rc = check_common(nseq, max_len, n, HQ, KH, D)) return rc;
   if (n == 0 || nseq == 0 || max_len == 0) return 0;
-  QLORA_CHECK_ARG(q && k && v && out && lse && cu_seqlens);
-  QLORA_CHECK_ARG(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out));
-  Args a{};
-  a.q = static_cast<const uint16_t*>(q);
-  a.k = static_cast<const uint16_t*>(k);
-  a.v = static_cast<const uint16_t*>(v);
-  a.out = static_cast<uint16_t*>(out);
-  a.lse = lse;
-  a.cu = cu_seqlens;
-  a.n = n;
-  a.HQ = HQ;
-  a.KH = KH;
-  a.scale = scale;
-  const dim3 grid((unsigned)(nseq * KH), (unsigned)qlora_cdiv(max_len, kTok));
-  launch_q_any<false>(a, D, HQ / KH, grid, (hipStream_t)stream);
-  return qlora_launch_status();
+  int64_t nch = 1, need = 0;
+  if (chunk_keys != 0) {
+    if (int rc = split_sizes(max_len, n, HQ, D, chunk_keys, &nch, &need)) return rc;
+  }
+  QLORA_CHECK_ARG(dout && q && k && v && out && lse && delta && dq && dk && dv && cu_seqlens);
+  QLORA_CHECK_ARG(aligned16(dout) && aligned16(q) && aligned16(k) && aligned16(v) &&
+                  aligned16(out) && aligned16(dq) && aligned16(dk) && aligned16(dv));
+  QLORA_CHECK_ARG(work_elems >= need && (nch == 1 || (work && aligned16(work))));
+  Args a = make_args(q, k, v, n, HQ, KH, scale, cu_seqlens);
+  a.o = static_cast<const uint16_t*>(out);
+  a.dout = static_cast<const uint16_t*>(dout);
+  a.out = static_cast<uint16_t*>(dq);
+  a.dk = static_cast<uint16_t*>(dk);
+  a.dv = static_cast<uint16_t*>(dv);
+  a.lse = const_cast<float*>(lse);
+  a.delta = delta;
+  if (nch > 1) {
+    a.chunk = chunk_keys / kTok;
+    a.part = work;
+  }
+  return run_bwd(a, nseq, max_len, D, nch, (hipStream_t)stream);
 }
 
 // Backward. dout/out/q [n, HQ, D], k/v [n, KH, D] as in the forward, lse from it; delta: fp32
@@ -619,33 +891,6 @@ QLORA_API int qlora_attn_bwd(const void* dout, const void* q, const void* k, con
                              void* dv, const int32_t* cu_seqlens, int32_t nseq, int32_t max_len,
                              int64_t n, int32_t HQ, int32_t KH, int32_t D, float scale,
                              void* stream) {
-  if (int rc = check_common(nseq, max_len, n, HQ, KH, D)) return rc;
-  if (n == 0 || nseq == 0 || max_len == 0) return 0;
-  QLORA_CHECK_ARG(dout && q && k && v && out && lse && delta && dq && dk && dv && cu_seqlens);
-  QLORA_CHECK_ARG(aligned16(dout) && aligned16(q) && aligned16(k) && aligned16(v) &&
-                  aligned16(out) && aligned16(dq) && aligned16(dk) && aligned16(dv));
-  Args a{};
-  a.q = static_cast<const uint16_t*>(q);
-  a.k = static_cast<const uint16_t*>(k);
-  a.v = static_cast<const uint16_t*>(v);
-  a.o = static_cast<const uint16_t*>(out);
-  a.dout = static_cast<const uint16_t*>(dout);
-  a.out = static_cast<uint16_t*>(dq);
-  a.dk = static_cast<uint16_t*>(dk);
-  a.dv = static_cast<uint16_t*>(dv);
-  a.lse = const_cast<float*>(lse);
-  a.delta = delta;
-  a.cu = cu_seqlens;
-  a.n = n;
-  a.HQ = HQ;
-  a.KH = KH;
-  a.scale = scale;
-  hipStream_t s = (hipStream_t)stream;
-  const dim3 g1((unsigned)(nseq * KH), (unsigned)qlora_cdiv(max_len, kTok));
-  launch_q_any<true>(a, D, HQ / KH, g1, s);
-  if (int rc = qlora_launch_status()) return rc;
-  const dim3 g2((unsigned)(nseq * HQ), (unsigned)qlora_cdiv(max_len, kTok * kKeyWaves));
-  if (D == 128) hipLaunchKernelGGL(attn_dkdv_kernel<128>, g2, dim3(64 * kKeyWaves), 0, s, a);
-  else hipLaunchKernelGGL(attn_dkdv_kernel<64>, g2, dim3(64 * kKeyWaves), 0, s, a);
-  return qlora_launch_status();
+  return qlora_attn_bwd_split(dout, q, k, v, out, lse, delta, dq, dk, dv, cu_seqlens, nseq,
+                              max_len, n, HQ, KH, D, scale, 0, nullptr, 0, stream);
 }

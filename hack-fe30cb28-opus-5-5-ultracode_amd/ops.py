@@ -594,16 +594,94 @@ def _attn_shapes(q, k, v, packed):
     return q.shape[0], q.shape[1], k.shape[1], q.shape[2], cu, dev
 
 
+# Split of the attention's key ranges (qlora_attn_fwd_split / qlora_attn_bwd_split). Resident
+# workgroups of the forward and dQ kernels: one per CU (their registers), 256 on an MI355X. A
+# workgroup costs about two key blocks of fixed work (loads of its queries, the first block, the
+# stores) plus one per block it walks (5.2 us for one 64-key block, +1.75 us per block, with few
+# workgroups running). Measured on MI355X: with a sequence of 1024 (64 workgroups) chunks of 256
+# keys take the forward from 35.7 to 25.8 us and dQ + dK/dV from 115 to 92 us, with one of 2048
+# chunks of 512 keys 65.6 -> 53.3 and 212 -> 191 us; once the unsplit launch fills half the GPU
+# (four sequences of up to 1024 tokens: 166 workgroups) every split was slower (each workgroup's
+# key blocks take longer when more run at once, and the merge costs 8-12 us), so none is made.
+ATTN_SLOTS = 256
+ATTN_WG_BLOCKS = 2.0
+ATTN_MAX_CHUNKS = 16
+ATTN_MIN_CHUNK = 256
+
+
+def attn_chunk(lengths, heads, block):
+    """Keys per workgroup (a multiple of 64) for the split kernels, or 0 for no split: none when
+    the unsplit launch already has half as many workgroups as the GPU holds, else the chunk of
+    at least ATTN_MIN_CHUNK keys that minimises max(longest workgroup, total work / resident
+    workgroups), over a batch of sequence `lengths`, `heads` (sequence, head) workgroup rows per
+    tile, key blocks of `block` keys (64: forward, 32: dQ)."""
+    lengths = [int(x) for x in lengths if x > 0]
+    if not lengths:
+        return 0
+    max_len = max(lengths)
+    nkb = []
+    for L in lengths:  # tile t of 32 queries walks ceil(min(32 (t + 1), L) / block) blocks
+        nkb += [-(-min(32 * (t + 1), L) // block) for t in range(-(-L // 32))]
+    if len(nkb) * heads > ATTN_SLOTS // 2:
+        return 0
+    nkb = torch.tensor(nkb, dtype=torch.float64)
+    best, best_cost = 0, None
+    cands = [0] + [c for c in (256, 384, 512, 768, 1024, 1536, 2048, 3072, 4096, 6144, 8192)
+                   if c >= ATTN_MIN_CHUNK and c < max_len and -(-max_len // c) <= ATTN_MAX_CHUNKS]
+    for c in cands:
+        per = c // block if c else int(nkb.max())
+        nch = torch.ceil(nkb / per)
+        total = float((nch * ATTN_WG_BLOCKS + nkb).sum()) * heads
+        longest = ATTN_WG_BLOCKS + min(per, float(nkb.max())) + (0.3 * float(nch.max()) if c else 0)
+        cost = max(longest, total / ATTN_SLOTS)
+        if best_cost is None or cost < best_cost * 0.97:  # prefer fewer chunks on a near tie
+            best, best_cost = c, cost
+    return best
+
+
+def _attn_plan(packed, kind, HQ, KH):
+    """Chunk keys for `kind` ("fwd", "dq") of this batch, computed once per packed batch from the
+    host-side lengths (0 when there are none)."""
+    plans = getattr(packed, "_attn_plans", None)
+    if plans is None:
+        plans = {}
+        try:
+            packed._attn_plans = plans
+        except AttributeError:
+            pass
+    key = (kind, HQ, KH)
+    if key not in plans:
+        cu = getattr(packed, "cu_seqlens_host", None)
+        if cu is None:
+            plans[key] = 0
+        else:
+            lengths = [b - a for a, b in zip(cu[:-1], cu[1:])]
+            plans[key] = attn_chunk(lengths, KH, 64 if kind == "fwd" else 32)
+    return plans[key]
+
+
+def _attn_work(n, max_len, HQ, D, chunk, dev):
+    """fp32 workspace of a split launch (partials of every chunk)."""
+    we = ctypes.c_int64(0)
+    _lib.call("qlora_attn_split_workspace", max_len, n, HQ, D, chunk, ctypes.byref(we))
+    return torch.empty((max(we.value, 4),), device=dev, dtype=torch.float32)
+
+
 def _attn_fwd(q, k, v, packed, scale):
     """(out [n, HQ, D] fp16, lse [HQ, n] fp32, None, None): causal attention within each
     sequence of cu_seqlens (engine.py:857-862; no dropout, so no Philox seed/offset). k and v
-    may be in grouped layout [n, KH, D] (q head h reads kv head h // (HQ // KH))."""
+    may be in grouped layout [n, KH, D] (q head h reads kv head h // (HQ // KH)). With the
+    lengths on the host, the key ranges of long tiles are split over several workgroups."""
     n, HQ, KH, D, cu, dev = _attn_shapes(q, k, v, packed)
     out = torch.empty_like(q)
     lse = torch.empty((HQ, n), device=dev, dtype=torch.float32)
     if n:
-        _lib.call("qlora_attn_fwd", _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(lse), _ptr(cu),
-                  cu.numel() - 1, int(packed.max_len), n, HQ, KH, D, float(scale), _stream(dev))
+        nseq, max_len = cu.numel() - 1, int(packed.max_len)
+        chunk = _attn_plan(packed, "fwd", HQ, KH)
+        work = _attn_work(n, max_len, HQ, D, chunk, dev) if chunk else None
+        _lib.call("qlora_attn_fwd_split", _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(lse),
+                  _ptr(cu), nseq, max_len, n, HQ, KH, D, float(scale), chunk, _ptr(work),
+                  work.numel() if work is not None else 0, _stream(dev))
     return out, lse, None, None
 
 
@@ -622,10 +700,14 @@ def _attn_bwd(dout, q, k, v, out, lse, seed, offset, packed, scale):
     dk = torch.empty_like(q)
     dv = torch.empty_like(q)
     if n:
+        nseq, max_len = cu.numel() - 1, int(packed.max_len)
         delta = torch.empty((HQ, n), device=dev, dtype=torch.float32)
-        _lib.call("qlora_attn_bwd", _ptr(dout), _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(lse),
-                  _ptr(delta), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(cu), cu.numel() - 1,
-                  int(packed.max_len), n, HQ, KH, D, float(scale), _stream(dev))
+        chunk = _attn_plan(packed, "dq", HQ, KH)
+        work = _attn_work(n, max_len, HQ, D, chunk, dev) if chunk else None
+        _lib.call("qlora_attn_bwd_split", _ptr(dout), _ptr(q), _ptr(k), _ptr(v), _ptr(out),
+                  _ptr(lse), _ptr(delta), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(cu), nseq, max_len,
+                  n, HQ, KH, D, float(scale), chunk, _ptr(work),
+                  work.numel() if work is not None else 0, _stream(dev))
     return dq, dk, dv
 
 

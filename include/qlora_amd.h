@@ -337,6 +337,27 @@ int qlora_attn_bwd(const void* dout, const void* q, const void* k, const void* v
                    const int32_t* cu_seqlens, int32_t nseq, int32_t max_len, int64_t n,
                    int32_t HQ, int32_t KH, int32_t D, float scale, void* stream);
 
+/*
+ * Work-split forms of the two calls above (same results up to fp32 summation order): the key
+ * range of each 32-query tile (forward, dQ) is cut into chunks of chunk_keys keys (a positive
+ * multiple of 64, at most 16 chunks for max_len; 0: not cut), one workgroup each, and a second
+ * kernel merges the fp32 partials in chunk order. A batch of few long sequences otherwise leaves
+ * most of the GPU idle while its longest tiles walk their keys. work: fp32, 16-byte aligned, of
+ * the elements qlora_attn_split_workspace returns (0 when max_len fits one chunk). Same
+ * reference call sites (engine.py:857-869).
+ */
+int qlora_attn_split_workspace(int32_t max_len, int64_t n, int32_t HQ, int32_t D,
+                               int32_t chunk_keys, int64_t* work_elems);
+int qlora_attn_fwd_split(const void* q, const void* k, const void* v, void* out, float* lse,
+                         const int32_t* cu_seqlens, int32_t nseq, int32_t max_len, int64_t n,
+                         int32_t HQ, int32_t KH, int32_t D, float scale, int32_t chunk_keys,
+                         float* work, int64_t work_elems, void* stream);
+int qlora_attn_bwd_split(const void* dout, const void* q, const void* k, const void* v,
+                         const void* out, const float* lse, float* delta, void* dq, void* dk,
+                         void* dv, const int32_t* cu_seqlens, int32_t nseq, int32_t max_len,
+                         int64_t n, int32_t HQ, int32_t KH, int32_t D, float scale,
+                         int32_t chunk_keys, float* work, int64_t work_elems, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -2,7 +2,8 @@
 scaled_dot_product_attention per sequence on the CPU, at the reference's tolerances
 (test_kernels.py:244-281: out 2e-3, dq/dk/dv 1e-2), including the reference's own case
 (lengths 7, 130, 1, 64; 12 q heads over 2 kv heads; D 128), the config-3/5 shapes (lengths up to
-1024), k/v in grouped and in repeated layout, and head_dim 64."""
+1024), k/v in grouped and in repeated layout, head_dim 64, and the split of long key ranges over
+several workgroups (qlora_attn_fwd_split / qlora_attn_bwd_split) at forced chunk sizes."""
 
 import pytest
 import torch
@@ -55,7 +56,7 @@ def _reference(q, k, v, dout, lengths):
             torch.cat(dvs))
 
 
-def _run(pkg, lengths, HQ, KH, D, seed=0, expand=False):
+def _run(pkg, lengths, HQ, KH, D, seed=0, expand=False, chunk=None):
     torch.manual_seed(seed)
     n = sum(lengths)
     q = torch.randn(n, HQ, D, device=DEV, dtype=torch.float16)
@@ -63,9 +64,12 @@ def _run(pkg, lengths, HQ, KH, D, seed=0, expand=False):
     v = torch.randn(n, KH, D, device=DEV, dtype=torch.float16)
     dout = torch.randn(n, HQ, D, device=DEV, dtype=torch.float16)
     packed = _Packed(lengths)
+    if chunk is not None:  # force the split (0: none) instead of the cost model's choice
+        packed._attn_plans = {("fwd", HQ, KH): chunk, ("dq", HQ, KH): chunk}
     kk, vv = (_expand(k, HQ // KH).contiguous(), _expand(v, HQ // KH).contiguous()) if expand \
         else (k, v)
-    print(f"attn lengths={lengths} HQ={HQ} KH={KH} D={D} expand={expand}", flush=True)
+    print(f"attn lengths={lengths} HQ={HQ} KH={KH} D={D} expand={expand} chunk={chunk}",
+          flush=True)
     out, lse, _, _ = pkg.ops._attn_fwd(q, kk, vv, packed, D ** -0.5)
     dq, dk, dv = pkg.ops._attn_bwd(dout, q, kk, vv, out, lse, None, None, packed, D ** -0.5)
     torch.cuda.synchronize()
@@ -75,6 +79,7 @@ def _run(pkg, lengths, HQ, KH, D, seed=0, expand=False):
     close(dq, rdq, 1e-2)
     close(dk, rdk, 1e-2)
     close(dv, rdv, 1e-2)
+    return out, lse, dq, dk, dv
 
 
 def test_reference_case(pkg):
@@ -109,3 +114,25 @@ def test_empty_sequences(pkg):
     k = torch.empty(0, 2, 128, device=DEV, dtype=torch.float16)
     out, lse, _, _ = pkg.ops._attn_fwd(q, k, k, packed, 128 ** -0.5)
     assert out.shape == (0, 12, 128) and lse.shape == (12, 0)
+
+
+@pytest.mark.parametrize("chunk", [64, 128, 192, 512])
+def test_split_key_ranges(pkg, chunk):
+    """Key ranges cut into chunks of `chunk` keys (several workgroups per query tile and a merge
+    kernel), incl. tiles of one chunk, a sequence of 1 and the longest row."""
+    _run(pkg, [1024, 301, 777, 1, 128, 65], 12, 2, 128, seed=chunk, chunk=chunk)
+
+
+def test_split_head_dim_64(pkg):
+    _run(pkg, [300, 17, 129], 4, 2, 64, seed=3, chunk=64)
+
+
+def test_split_is_deterministic_and_matches_unsplit(pkg):
+    """The merge order is fixed: two split runs agree bit for bit, and with the unsplit kernels
+    to fp32 summation order."""
+    a = _run(pkg, [700, 300, 40], 12, 2, 128, seed=11, chunk=128)
+    b = _run(pkg, [700, 300, 40], 12, 2, 128, seed=11, chunk=128)
+    c = _run(pkg, [700, 300, 40], 12, 2, 128, seed=11, chunk=0)
+    for x, y, z in zip(a, b, c):
+        assert torch.equal(x, y)
+        close(x, z, 2e-3)
