@@ -296,8 +296,9 @@ def main():
                    "tokens": tokens, "layers": args.layers, "parallelism": "single GPU",
                    "activations": (f"kept for the backward by {kept} of {args.layers} layers "
                                    "(the reference's memory-cap plan, engine.py:1626-1640, "
-                                   "under this GPU's memory); the others recompute their "
-                                   "forward")},
+                                   "under this GPU's memory), with their dequantized weights "
+                                   "(each NF4 weight dequantized once per step); the others "
+                                   "recompute their forward")},
         "gemm_tuning_s": tune_s,
         "full_recompute": recompute,
         "loss_first_last": [losses[0], losses[-1]],

@@ -367,9 +367,13 @@ class _Layer(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, h, spec, packed, keep_all, aq_w, bq_w, av_w, bv_w):
-        with L.reuse_dequant():  # the layer's four weights in one dequant launch
+        with L.reuse_dequant() as weights:  # the layer's four weights in one dequant launch
             L.dequant_layer(spec.nf4_all)
-            return _Layer._forward(ctx, h, spec, packed, keep_all, aq_w, bq_w, av_w, bv_w)
+            h3 = _Layer._forward(ctx, h, spec, packed, keep_all, aq_w, bq_w, av_w, bv_w)
+        # a layer that keeps its intermediates may keep its dequantized weights as well, so
+        # that its backward does not dequantize the same NF4 weights a second time
+        ctx.weights = weights.copies if keep_all and getattr(packed, "keep_weights", False) else None
+        return h3
 
     @staticmethod
     def _forward(ctx, h, spec, packed, keep_all, aq_w, bq_w, av_w, bv_w):
@@ -393,7 +397,9 @@ class _Layer(torch.autograd.Function):
     def backward(ctx, dh3):
         h, aq_w, bq_w, av_w, bv_w = ctx.saved_tensors
         spec, packed, seeds = ctx.spec, ctx.packed, ctx.seeds
-        with L.reuse_dequant():  # one dequant launch for the recompute and the dY W products
+        kept, ctx.weights = ctx.weights, None
+        # one dequant launch for the recompute and the dY W products (none with kept weights)
+        with L.reuse_dequant(kept):
             L.dequant_layer(spec.nf4_all)
             return _Layer._backward(ctx, dh3, h, aq_w, bq_w, av_w, bv_w, spec, packed, seeds)
 
@@ -543,6 +549,9 @@ class FusedQwen2:
         self.keep_all = keep_all
         self.memory_cap = None
         self.autotune = True  # time the projections' GEMM solutions for each new token bucket
+        # layers that keep their intermediates also keep their dequantized weights for the
+        # backward (one dequant per layer and step instead of two; 94 MB per 1.5B layer)
+        self.keep_weights = True
         self.dropout_p = cfg.lora_dropout
         self.rope = RopeTable(cfg.rope_theta, cfg.head_dim, self.device)
         self.dropout = TorchDropout(self.device, torch.float32) if self.dropout_p > 0 else None
@@ -592,21 +601,26 @@ class FusedQwen2:
                      + 2 * spec.I * 2 + spec.HQ * 4 + 2 * 4 + 2 * 16 * 2)
         return n * per_token
 
+    def weight_bytes_per_layer(self):
+        """Device bytes of one layer's dequantized fp16 weights (qkv, o, gate|up, down)."""
+        spec = self.layers[0]
+        return 2 * spec.H * ((spec.HQ + 2 * spec.HKV) * spec.D + spec.HQ * spec.D + 3 * spec.I)
+
     def keep_plan(self, n):
         """The number of last layers that keep every intermediate for a step of n tokens: as
         many as fit under the memory cap above what is allocated now plus one recomputing
-        layer's working set (its dequantized weights and per-token buffers)."""
+        layer's working set (its dequantized weights and per-token buffers). With keep_weights
+        a keeping layer also holds its dequantized weights from the forward to its backward
+        (weight_bytes_per_layer more per layer)."""
         if self.keep_all is not None:
             return len(self.layers) if self.keep_all else 0
         cap = self.memory_cap
         if cap is None:
             cap = torch.cuda.get_device_properties(self.device).total_memory - self.CAP_MARGIN
-        spec = self.layers[0]
-        weights = 2 * spec.H * ((spec.HQ + 2 * spec.HKV) * spec.D + spec.HQ * spec.D
-                                + 3 * spec.I)
+        weights = self.weight_bytes_per_layer()
         work = weights + 64 * 2**20 + n * 96 * 1024 + n * self.cfg.vocab_size * 2
         free = cap - torch.cuda.memory_allocated(self.device) - work
-        per_layer = max(1, self.kept_bytes_per_layer(n))
+        per_layer = max(1, self.kept_bytes_per_layer(n) + (weights if self.keep_weights else 0))
         return int(max(0, min(len(self.layers), free // per_layer)))
 
     def gemm_shapes(self):
@@ -653,6 +667,7 @@ class FusedQwen2:
         h = torch.nn.functional.embedding(packed.ids, self.embed).float()
         keep_from = len(self.layers) - self.keep_plan(packed.n)
         packed.keep_all_from = keep_from
+        packed.keep_weights = self.keep_weights
         for i, spec in enumerate(self.layers):
             h = _Layer.apply(h, spec, packed, i >= keep_from, *spec.lora_params())
         stats = HeadStats()

@@ -30,11 +30,16 @@ _REUSE = None
 class reuse_dequant:
     """Within this context each NF4 weight is dequantized once and its fp16 copy reused (a
     layer's backward multiplies by the same weights in its recompute and in its dY W products);
-    the copies are dropped on exit."""
+    `copies`: fp16 copies made earlier (a forward's, kept for its backward), used instead of
+    dequantizing again. On exit the context's copies stay in `self.copies` for the caller to
+    keep or drop."""
+
+    def __init__(self, copies=None):
+        self.copies = {} if copies is None else copies
 
     def __enter__(self):
         global _REUSE
-        self.prev, _REUSE = _REUSE, {}
+        self.prev, _REUSE = _REUSE, self.copies
         return self
 
     def __exit__(self, *exc):

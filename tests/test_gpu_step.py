@@ -71,24 +71,28 @@ def _batch(lengths, vocab, prompt=3, seed=0):
 
 @pytest.mark.parametrize("lengths,keep_all", [([17, 60, 33, 5], False), ([4], False),
                                               ([40, 40], True), ([17, 60, 33, 5], None),
-                                              ([17, 60, 33, 5], "mixed")])
+                                              ([17, 60, 33, 5], "mixed"),
+                                              ([40, 40], "no_weights")])
 def test_step_matches_oracle(pkg, lengths, keep_all):
     """Loss and LoRA gradients of one GPU step equal the CPU oracle's (fp32 autograd with the
     same NF4 bytes and dropout masks) within the reference's whole-step tolerance; the CUDA
     generator advances exactly as the base's 2 x layers dropout calls would. keep_all: every
-    layer recomputes (False), keeps (True), the memory-cap plan (None: all keep), or a cap that
-    admits exactly one kept layer ("mixed": layer 0 recomputes, layer 1 keeps)."""
+    layer recomputes (False), keeps (True; with its dequantized weights), the memory-cap plan
+    (None: all keep), a cap that admits exactly one kept layer ("mixed": layer 0 recomputes,
+    layer 1 keeps), or every layer keeps its intermediates but dequantizes again in its
+    backward ("no_weights")."""
     model = _tiny(pkg)
     if keep_all == "mixed":
         model.keep_all = None
         n = sum(lengths)
-        spec = model.layers[0]
-        weights = 2 * spec.H * ((spec.HQ + 2 * spec.HKV) * spec.D + spec.HQ * spec.D
-                                + 3 * spec.I)
+        weights = model.weight_bytes_per_layer()
         work = weights + 64 * 2**20 + n * 96 * 1024 + n * model.cfg.vocab_size * 2
         model.set_memory_cap(torch.cuda.memory_allocated() + work
-                             + int(1.5 * model.kept_bytes_per_layer(n)))
+                             + int(1.5 * (model.kept_bytes_per_layer(n) + weights)))
         assert model.keep_plan(n) == 1
+    elif keep_all == "no_weights":
+        model.keep_all = True
+        model.keep_weights = False
     else:
         model.keep_all = keep_all
         if keep_all is None:
