@@ -92,12 +92,14 @@ __device__ __forceinline__ void load_block(const uint16_t* row, int64_t b0, int6
       x[h * kCeVec + i] = c + i < width ? h2f_bits(row[c + i]) : kNegInf;
   }
 }
-__device__ __forceinline__ int64_t col_of(int64_t b0, int j) {
-  return b0 + (j / kCeVec) * (kCeBlock / 2) + (int64_t)threadIdx.x * kCeVec + (j % kCeVec);
+// Column of value j of thread t's 16 in the block starting at b0.
+__device__ __forceinline__ int64_t col_of(int64_t b0, int j, int t = threadIdx.x) {
+  return b0 + (j / kCeVec) * (kCeBlock / 2) + (int64_t)t * kCeVec + (j % kCeVec);
 }
 
-// Fold a thread's 16 values (fresh state), in increasing column order.
-__device__ __forceinline__ Online fold16(const float (&x)[kCePerThread], int64_t b0) {
+// Fold thread t's 16 values (fresh state), in increasing column order.
+__device__ __forceinline__ Online fold16(const float (&x)[kCePerThread], int64_t b0,
+                                        int t = threadIdx.x) {
   float mx = x[0];
   int j_best = 0;
 #pragma unroll
@@ -106,7 +108,7 @@ __device__ __forceinline__ Online fold16(const float (&x)[kCePerThread], int64_t
   Online st;
   st.m = mx;
   st.best = mx;
-  st.idx = mx == kNegInf ? 0x7fffffff : (int32_t)col_of(b0, j_best);
+  st.idx = mx == kNegInf ? 0x7fffffff : (int32_t)col_of(b0, j_best, t);
   float se = 0.f, te = 0.f;
   if (mx != kNegInf) {
 #pragma unroll
@@ -228,6 +230,121 @@ __global__ __launch_bounds__(kCeThreads) void ce_full_kernel(uint16_t* logits, i
     rewrite<VEC>(row, V, [](float, int64_t) { return 0.f; });
 }
 
+// Whole rows with the row held in registers: one 1024-thread workgroup per row, four groups of
+// 256 threads; group g holds blocks g, g + 4, ... of the row (NB blocks at most, 16 columns per
+// thread each, the same columns a thread of ce_full_kernel reads in that block), so the row is
+// read from memory once and written once (ce_full_kernel reads it twice). The arithmetic is
+// ce_full_kernel's, in its order: each block's state from the same per-thread folds and the
+// same wavefront butterfly and four-wave merge, then the blocks advanced in column order; the
+// results are equal bit for bit. Requires V % 8 == 0, 16-byte aligned rows, V <= NB 4 kCeBlock.
+constexpr int kRowGroups = 4;
+constexpr int kRowThreads = kCeThreads * kRowGroups;
+
+template <int NB>
+__global__ __launch_bounds__(kRowThreads) void ce_rows_kernel(uint16_t* logits, int64_t ld,
+                                                              const int64_t* target, float* loss,
+                                                              float* entropy, int32_t* correct,
+                                                              int64_t V, int zero_unsupervised) {
+  __shared__ Online wpart[NB * kRowGroups][kCeThreads / kWave];
+  __shared__ Online blk[NB * kRowGroups];
+  __shared__ Online fin;
+  __shared__ float xt_part[kRowThreads / kWave];
+  const int64_t r = blockIdx.x;
+  uint16_t* row = logits + r * ld;
+  const rsrc_t src = make_rsrc(row, (uint32_t)(V * 2));
+  const int tid = threadIdx.x, grp = tid / kCeThreads, t = tid % kCeThreads;
+  const int nblocks = (int)((V + kCeBlock - 1) / kCeBlock);
+  const int64_t tgt = target[r];
+  // every load issued before any use; blocks past the row read zeros (masked below)
+  uint4 raw[NB][2];
+#pragma unroll
+  for (int j = 0; j < NB; ++j)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int64_t c = (int64_t)(grp + kRowGroups * j) * kCeBlock + h * (kCeBlock / 2) + t * kCeVec;
+      raw[j][h] = buf_load16(src, (uint32_t)(c * 2));
+    }
+  float mine = 0.f;
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    const int b = grp + kRowGroups * j;
+    if (b >= nblocks) break;  // uniform over the wavefront
+    const int64_t b0 = (int64_t)b * kCeBlock;
+    float x[kCePerThread];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      unpack8(raw[j][h], x + h * kCeVec);
+      const int64_t c = b0 + h * (kCeBlock / 2) + t * kCeVec;
+      if (c >= V) {  // V % 8 == 0: a run is wholly inside or outside the row
+#pragma unroll
+        for (int i = 0; i < kCeVec; ++i) x[h * kCeVec + i] = kNegInf;
+      }
+      if (tgt >= c && tgt < c + kCeVec) {
+#pragma unroll
+        for (int i = 0; i < kCeVec; ++i)
+          if (c + i == tgt) mine = x[h * kCeVec + i];
+      }
+    }
+    // the block's state as block_state forms it: wavefront butterfly, then the four waves
+    Online st = fold16(x, b0, t);
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+      const Online o = shfl_online(st, off);
+      st = ((t & off) == 0) ? merge(st, o) : merge(o, st);
+    }
+    if ((t & (kWave - 1)) == 0) wpart[b][t / kWave] = st;
+  }
+  mine = wave_sum(mine);
+  if ((tid & (kWave - 1)) == 0) xt_part[tid / kWave] = mine;
+  __syncthreads();
+  if (tid < nblocks) {
+    Online bs = wpart[tid][0];
+#pragma unroll
+    for (int i = 1; i < kCeThreads / kWave; ++i) bs = merge(bs, wpart[tid][i]);
+    blk[tid] = bs;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    Online st = online_empty();
+    for (int b = 0; b < nblocks; ++b) st = advance(st, blk[b]);
+    fin = st;
+  }
+  __syncthreads();
+  const Online st = fin;
+  float xt = 0.f;
+#pragma unroll
+  for (int i = 0; i < kRowThreads / kWave; ++i) xt += xt_part[i];
+  const float lse = st.m + logf(st.s);
+  const bool valid = tgt >= 0;
+  if (tid == 0) {
+    entropy[r] = lse - st.t / st.s;
+    loss[r] = valid ? lse - xt : 0.f;
+    correct[r] = (int32_t)(valid && (int64_t)st.idx == tgt);
+  }
+  if (!valid && !zero_unsupervised) return;
+  // in place: fp16(e^(x - lse) - onehot), or zeros; stores past the row are dropped
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    const int b = grp + kRowGroups * j;
+    if (b >= nblocks) break;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int64_t c = (int64_t)b * kCeBlock + h * (kCeBlock / 2) + t * kCeVec;
+      float x[kCeVec];
+      unpack8(raw[j][h], x);
+      uint32_t o[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float g0 = valid ? __expf(x[2 * i] - lse) - (c + 2 * i == tgt ? 1.f : 0.f) : 0.f;
+        const float g1 =
+            valid ? __expf(x[2 * i + 1] - lse) - (c + 2 * i + 1 == tgt ? 1.f : 0.f) : 0.f;
+        o[i] = pack2h(g0, g1);
+      }
+      buf_store16(src, (uint32_t)(c * 2), make_uint4(o[0], o[1], o[2], o[3]));
+    }
+  }
+}
+
 template <bool VEC>
 __global__ __launch_bounds__(kCeThreads) void ce_piece_kernel(
     uint16_t* logits, int64_t ld, const uint16_t* w, const int64_t* target, float* state,
@@ -323,7 +440,22 @@ QLORA_API int qlora_ce(void* logits, int64_t ld, const int64_t* target, float* l
   QLORA_CHECK_ARG(logits && target && loss && entropy && correct);
   QLORA_CHECK_ARG(V < (1ll << 31) - kCeBlock && rows < (1ll << 31));
   const bool vec = ld % 8 == 0 && al16(logits);
-  if (vec)
+  const int64_t nb = (qlora_cdiv(V, kCeBlock) + kRowGroups - 1) / kRowGroups;
+  if (vec && V % 8 == 0 && nb <= 12) {
+    hipStream_t s = (hipStream_t)stream;
+    uint16_t* lg = static_cast<uint16_t*>(logits);
+    const dim3 g((unsigned)rows), b(kRowThreads);
+#define QLORA_CE_ROWS(NB)                                                                        \
+  hipLaunchKernelGGL(ce_rows_kernel<NB>, g, b, 0, s, lg, ld, target, loss, entropy, correct, V, \
+                     zero_unsupervised)
+    if (nb <= 2) QLORA_CE_ROWS(2);
+    else if (nb <= 4) QLORA_CE_ROWS(4);
+    else if (nb <= 6) QLORA_CE_ROWS(6);
+    else if (nb <= 8) QLORA_CE_ROWS(8);
+    else if (nb <= 10) QLORA_CE_ROWS(10);
+    else QLORA_CE_ROWS(12);
+#undef QLORA_CE_ROWS
+  } else if (vec)
     hipLaunchKernelGGL(ce_full_kernel<true>, dim3((unsigned)rows), dim3(kCeThreads), 0,
                        (hipStream_t)stream, static_cast<uint16_t*>(logits), ld, target, loss,
                        entropy, correct, V, zero_unsupervised);
