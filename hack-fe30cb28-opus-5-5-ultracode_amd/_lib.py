@@ -47,6 +47,9 @@ SIGNATURES = {
     "qlora_gemm_splitk_solutions": [I32, I64, I64, I64, P, I64, P, I64, P, I32, P, I32, P],
     "qlora_gemmlt": [I32, I64, I64, I64, P, I64, P, I64, P, I64, P, F32, F32, I32, P, I64, P],
     "qlora_gemmlt_solutions": [I32, I64, I64, I64, I64, I64, I64, I32, I64, P, I32, P],
+    "qlora_nf4_quantize": [P, I32, I64, P, P, P],
+    "qlora_nf4_quantize_stats_workspace": [I64, P],
+    "qlora_nf4_quantize_stats": [P, I64, P, P, I64, P, P, P, P],
     "qlora_attn_fwd": [P, P, P, P, P, P, I32, I32, I64, I32, I32, I32, F32, P],
     "qlora_attn_bwd": [P, P, P, P, P, P, P, P, P, P, P, I32, I32, I64, I32, I32, I32, F32, P],
     "qlora_attn_split_workspace": [I32, I64, I32, I32, I32, P],

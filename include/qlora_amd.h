@@ -47,6 +47,26 @@ int qlora_nf4_dequant(const void* packed, const void* absmax, const float* code2
                       int32_t bs2, int64_t seg1, int64_t seg2, void* stream);
 
 /*
+ * NF4 quantisation on the GPU in bitsandbytes' Params4bit layout (the load-time step before the
+ * path: the bytes engine.py:77-101 reads; restates bitsandbytes 0.50.2 quantize_4bit): per block
+ * of 64 elements of w (fp16, or fp32 if w_f32; n_blocks x 64, row-major flat) absmax f32 =
+ * max |w| and code = the NF4 decision tree on fp32 midpoints of w * (1 / absmax), two codes a byte
+ * (even element high) in packed u8 [n_blocks * 32]. w 4-byte (fp16) / 8-byte (fp32) aligned.
+ */
+int qlora_nf4_quantize(const void* w, int32_t w_f32, int64_t n_blocks, void* packed,
+                       float* absmax, void* stream);
+/*
+ * Its double quantisation (compress_statistics): offset = fp32(fp64 tree sum of the n absmax /
+ * n), then per 256 values absmax2 = max |a - offset| and q u8 = bitsandbytes' dQuantize of
+ * (a - offset) / absmax2 over code2 (its signed dynamic map, f32 [256], sorted). work: fp64 of
+ * qlora_nf4_quantize_stats_workspace elements; absmax2 f32 [ceil(n / 256)], offset f32 [1].
+ */
+int qlora_nf4_quantize_stats_workspace(int64_t n, int64_t* elems);
+int qlora_nf4_quantize_stats(const float* absmax, int64_t n, const float* code2, double* work,
+                             int64_t work_elems, uint8_t* q, float* absmax2, float* offset,
+                             void* stream);
+
+/*
  * Keep mask (i8 0/1) of elements 0..nelem of one PyTorch dropout call whose Philox state is
  * (seed, offset = 4*ctr) over G threads, vec elements per thread load (4 fp32, 8 fp16).
  * Replaces torch_dropout_keep_kernel (kernels.py:129-135), the test hook of

@@ -20,10 +20,17 @@ Pins:
   * NF4_LEVELS: the table held by the reference (kernels.py:38-41), which is also the published
     QLoRA NF4 code (Dettmers et al. 2023) - checked for symmetry/ordering properties in tests.
   * quantize_*: restates bitsandbytes' published quantiser (bitsandbytes 0.50.2,
-    functional.quantize_4bit / quantize_blockwise / create_dynamic_map; not vendored in the
-    reference and not installable here). It only generates inputs: both the HIP kernels and
-    this oracle dequantise the same bytes, so dequant parity does not depend on it. Byte
-    equality with bitsandbytes' own quantiser: parity unpinned.
+    functional.quantize_4bit / quantize_blockwise / create_dynamic_map and its CUDA
+    dQuantizeNF4 / dQuantize; not vendored in the reference and not installable here): the
+    NF4 decision tree on fp32 midpoints, the 8-bit binary search with its midpoint rule. It is
+    the checker of the HIP quantiser (csrc/nf4_quant.hip, bit for bit) and generates the other
+    tests' inputs (both the HIP kernels and this oracle dequantise the same bytes, so dequant
+    parity does not depend on it). Pinned by: the tie rules at every threshold, exact levels
+    and code entries mapping to themselves, the nearest-entry property away from midpoints,
+    round-trip error bounds (tests/test_oracle_nf4.py). Byte equality with bitsandbytes' own
+    output: parity unpinned; the mean of the absmax is defined here as an fp64 sum over a
+    binary tree of adjacent pairs (bitsandbytes takes torch's fp32 mean, whose summation order
+    is the device library's), so the offset can differ from bitsandbytes' in its last bit.
 """
 
 import numpy as np
@@ -66,15 +73,63 @@ def create_dynamic_map(signed=True, max_exponent_bits=7, total_bits=8):
     return np.array(data, dtype=np.float32)
 
 
-def _nearest_code(x, code):
-    """Index of the nearest entry of the sorted `code` for each x (ties to the lower entry)."""
-    mids = (code[:-1].astype(np.float64) + code[1:].astype(np.float64)) / 2.0
-    return np.searchsorted(mids, x.astype(np.float64), side="left").astype(np.uint8)
+# midpoints of neighbouring NF4 levels rounded to fp32: bitsandbytes' dQuantizeNF4 thresholds
+NF4_MIDS = ((NF4_LEVELS[:-1].astype(np.float64) + NF4_LEVELS[1:].astype(np.float64))
+            / 2.0).astype(np.float32)
+
+
+def nf4_codes(x):
+    """dQuantizeNF4: the NF4 code of each fp32 x, the number of fp32 midpoints strictly below x
+    (its decision tree compares x > threshold at every node; ties go to the lower level)."""
+    return np.searchsorted(NF4_MIDS, np.asarray(x, np.float32), side="left").astype(np.uint8)
+
+
+def dquantize(code, x):
+    """bitsandbytes' dQuantize (deterministic) over a sorted 256-entry fp32 code: seven halving
+    steps of a binary search from pivot 127, then the nearer of the last pivot and the pivot
+    bracketing it on x's side, by an fp32 midpoint (x == midpoint keeps the last pivot)."""
+    code = np.asarray(code, np.float32)
+    x = np.asarray(x, np.float32)
+    pivot = np.full(x.shape, 127, np.int64)
+    upper_p = np.full(x.shape, 255, np.int64)
+    lower_p = np.zeros(x.shape, np.int64)
+    lower = np.full(x.shape, -1.0, np.float32)
+    upper = np.full(x.shape, 1.0, np.float32)
+    val = code[pivot]
+    i = 64
+    while i > 0:
+        gt = x > val
+        lower_p, lower = np.where(gt, pivot, lower_p), np.where(gt, val, lower)
+        upper_p, upper = np.where(gt, upper_p, pivot), np.where(gt, upper, val)
+        pivot = np.where(gt, pivot + i, pivot - i)
+        val = code[pivot]
+        i >>= 1
+    upper = np.where(upper_p == 255, code[255], upper).astype(np.float32)
+    lower = np.where(lower_p == 0, code[0], lower).astype(np.float32)
+    mid_u = ((upper + val) * np.float32(0.5)).astype(np.float32)
+    mid_l = ((lower + val) * np.float32(0.5)).astype(np.float32)
+    out = np.where(x > val, np.where(x > mid_u, upper_p, pivot),
+                   np.where(x < mid_l, lower_p, pivot))
+    return out.astype(np.uint8)
+
+
+def tree_sum(values, chunk=1024):
+    """fp64 sum over a binary tree of adjacent pairs, the values zero-padded to a power of
+    `chunk` (summed `chunk` at a time, level by level)."""
+    x = np.asarray(values, np.float64).reshape(-1)
+    levels = int(np.log2(chunk))
+    while True:
+        x = np.concatenate([x, np.zeros((-x.size) % chunk)]).reshape(-1, chunk)
+        for _ in range(levels):
+            x = x[:, 0::2] + x[:, 1::2]
+        x = x.reshape(-1)
+        if x.size == 1:
+            return x[0]
 
 
 def quantize_blockwise(a, blocksize=256, code=None):
-    """8-bit blockwise quantisation of fp32 values: absmax per block, nearest code entry of
-    a / absmax. Returns (uint8 codes, fp32 absmax per block, code)."""
+    """8-bit blockwise quantisation of fp32 values: absmax per block (zero-padded), the code
+    index of a * (1 / absmax) by dQuantize. Returns (uint8 codes, fp32 absmax per block, code)."""
     if code is None:
         code = create_dynamic_map(signed=True)
     a = np.asarray(a, dtype=np.float32).reshape(-1)
@@ -86,7 +141,7 @@ def quantize_blockwise(a, blocksize=256, code=None):
     absmax = np.abs(blocks).max(axis=1).astype(np.float32)
     inv = np.where(absmax > 0, np.float32(1.0) / np.where(absmax > 0, absmax, 1), 0)
     normed = (blocks * inv.astype(np.float32)[:, None]).astype(np.float32)
-    q = _nearest_code(normed.reshape(-1), code)[:n]
+    q = dquantize(code, normed.reshape(-1))[:n]
     return q, absmax, code
 
 
@@ -115,10 +170,10 @@ class QuantState2:
 def quantize_nf4(w, blocksize=64, compress_statistics=True, blocksize2=256):
     """bitsandbytes-style NF4 quantisation of a [N, K] weight (numpy, any float dtype).
 
-    Per block of `blocksize` consecutive elements: absmax = max |w|; code = nearest NF4 level of
-    w * (1 / absmax). With compress_statistics the fp32 absmax are double-quantised:
-    offset = mean(absmax), then 8-bit blockwise quantisation of (absmax - offset) in blocks of
-    `blocksize2`. Returns (packed uint8 [numel/2], QuantState with numpy arrays)."""
+    Per block of `blocksize` consecutive elements: absmax = max |w|; code = nf4_codes of
+    w * (1 / absmax) (0 for an all-zero block). With compress_statistics the fp32 absmax are
+    double-quantised: offset = fp32(tree_sum(absmax) / count), then 8-bit blockwise
+    quantisation of (absmax - offset) in blocks of `blocksize2`. Returns (packed uint8 [numel/2], QuantState with numpy arrays)."""
     w = np.asarray(w)
     shape = w.shape
     flat = w.astype(np.float32).reshape(-1)
@@ -130,10 +185,10 @@ def quantize_nf4(w, blocksize=64, compress_statistics=True, blocksize2=256):
     inv = np.where(absmax > 0, np.float32(1.0) / np.where(absmax > 0, absmax, 1),
                    np.float32(0)).astype(np.float32)
     normed = (blocks * inv[:, None]).astype(np.float32).reshape(-1)
-    codes = _nearest_code(normed, NF4_LEVELS)
+    codes = nf4_codes(normed)
     packed = ((codes[0::2] << 4) | codes[1::2]).astype(np.uint8)
     if compress_statistics:
-        offset = np.float32(absmax.astype(np.float32).mean(dtype=np.float32))
+        offset = np.float32(tree_sum(absmax) / np.float64(absmax.size))
         q, absmax2, code2 = quantize_blockwise(absmax - offset, blocksize=blocksize2)
         state = QuantState(q, shape, NF4_LEVELS.copy(), blocksize, offset=offset,
                            state2=QuantState2(absmax2, code2, blocksize2))

@@ -123,19 +123,53 @@ def test_nf4_dequant_many_equals_oracle(pkg, mix):
         assert torch.equal(bits16(out), bits16(want))
 
 
+def _oracle_state(qs):
+    return ON.QuantState(qs.absmax.cpu().numpy(), tuple(qs.shape), qs.code.cpu().numpy(), 64,
+                         offset=np.float32(qs.offset.item()),
+                         state2=ON.QuantState2(qs.state2.absmax.cpu().numpy(),
+                                               qs.state2.code.cpu().numpy(), 256))
+
+
+@pytest.mark.parametrize("shape", [(3, 64), (64, 64), (1536, 1536), (1536, 8960)])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("nested", [True, False])
+def test_gpu_quantizer_matches_oracle(pkg, shape, dtype, nested):
+    """qlora_nf4_quantize(_stats) against the oracle's restatement of bitsandbytes' quantiser,
+    bit for bit: packed codes, absmax (or its 8-bit codes, absmax2 and the offset), over block
+    counts below one workgroup, with partial 256-blocks and with a two-level offset sum; the
+    first block all zeros, the second holding every NF4 threshold exactly."""
+    g = torch.Generator().manual_seed(shape[0] + shape[1])
+    w = (torch.randn(shape, generator=g) * 0.03).to(dtype)
+    flat = w.view(-1)
+    flat[:64] = 0
+    if flat.numel() >= 128:
+        flat[64] = 1.0
+        flat[65:80] = torch.from_numpy(ON.NF4_MIDS.astype(np.float32)).to(dtype)
+    print(f"quantize shape={shape} dtype={dtype} nested={nested}", flush=True)
+    param = pkg.quant.quantize_nf4(w.to(DEV), compress_statistics=nested)
+    torch.cuda.synchronize()
+    packed, st = ON.quantize_nf4(w.numpy() if dtype == torch.float32 else w.numpy(),
+                                 compress_statistics=nested)
+    assert np.array_equal(param.data.view(-1).cpu().numpy(), packed)
+    qs = param.quant_state
+    if nested:
+        assert np.array_equal(qs.absmax.cpu().numpy(), st.absmax)
+        assert np.array_equal(qs.state2.absmax.cpu().numpy(), st.state2.absmax)
+        assert np.float32(qs.offset.item()) == st.offset
+        assert np.array_equal(qs.state2.code.cpu().numpy(), st.state2.code)
+    else:
+        assert np.array_equal(qs.absmax.cpu().numpy(), st.absmax)
+
+
 def test_quantizer_bytes_dequantize_like_oracle(pkg):
-    """The package's torch quantiser (GPU) produces bitsandbytes-layout bytes that the HIP
-    dequant and the oracle dequant read identically."""
+    """The package's GPU quantiser produces bitsandbytes-layout bytes that the HIP dequant and
+    the oracle dequant read identically."""
     torch.manual_seed(0)
     w = (torch.randn(512, 1536, device=DEV) * 0.02).half()
     param = pkg.quant.quantize_nf4(w)
     out = torch.empty_like(w)
     pkg.ops.NF4Weight(param).dequant_into(out)
-    qs = param.quant_state
-    st = ON.QuantState(qs.absmax.cpu().numpy(), tuple(qs.shape), qs.code.cpu().numpy(), 64,
-                       offset=np.float32(qs.offset.item()),
-                       state2=ON.QuantState2(qs.state2.absmax.cpu().numpy(),
-                                             qs.state2.code.cpu().numpy(), 256))
+    st = _oracle_state(param.quant_state)
     want = torch.from_numpy(ON.dequantize_nf4(param.data.cpu().numpy(), st))
     assert torch.equal(bits16(out), bits16(want))
     assert (out.float() - w.float()).abs().max() < 0.02

@@ -114,3 +114,54 @@ def test_dynamic_map_shape():
     assert np.all(np.diff(code) >= 0)
     assert code[-1] == 1.0 and 0.0 in code
     assert np.sum(code > 0) == 128 and np.sum(code < 0) == 127
+
+
+def test_nf4_tree_thresholds_and_ties():
+    """dQuantizeNF4's thresholds are the fp32 midpoints of neighbouring levels (the published
+    tree's root and right-spine constants), a midpoint itself goes to the lower level, the next
+    float above it to the upper; every level maps to its own code."""
+    mids = N.NF4_MIDS
+    assert mids.dtype == np.float32 and np.all(np.diff(mids) > 0)
+    for i, c in ((7, 0.03979014977812767), (11, 0.3893125355243683), (13, 0.6427869200706482),
+                 (14, 0.8614784181118011)):
+        assert mids[i] == np.float32(c)
+    for i, m in enumerate(mids):
+        assert N.nf4_codes(m) == i
+        assert N.nf4_codes(np.nextafter(m, np.float32(np.inf))) == i + 1
+    assert np.array_equal(N.nf4_codes(N.NF4_LEVELS), np.arange(16))
+    assert N.nf4_codes(np.float32(-2.0)) == 0 and N.nf4_codes(np.float32(2.0)) == 15
+
+
+def test_dquantize_binary_search():
+    """Every entry of the dynamic map maps to its own index; away from the midpoints the result
+    is the nearest entry (brute force); at a midpoint it is one of its two entries."""
+    code = N.create_dynamic_map()
+    assert np.array_equal(N.dquantize(code, code), np.arange(256))
+    rng = np.random.default_rng(3)
+    x = rng.uniform(-1.0, 1.0, 200000).astype(np.float32)
+    x = np.concatenate([x, (rng.standard_normal(50000) * 1e-3).astype(np.float32)])
+    mids = (code[:-1].astype(np.float64) + code[1:].astype(np.float64)) / 2
+    gaps = np.diff(code.astype(np.float64))
+    near = np.abs(x.astype(np.float64)[:, None] - mids[None, :]) < 1e-3 * gaps[None, :]
+    keep = ~near.any(axis=1)
+    want = np.abs(x[keep, None].astype(np.float64) - code[None, :].astype(np.float64)).argmin(1)
+    assert np.array_equal(N.dquantize(code, x[keep]), want)
+    m32 = ((code[:-1] + code[1:]) * np.float32(0.5)).astype(np.float32)
+    got = N.dquantize(code, m32).astype(np.int64)
+    assert np.all((got == np.arange(255)) | (got == np.arange(1, 256)))
+
+
+@pytest.mark.parametrize("n", [1, 5, 1024, 1025, 70000])
+def test_tree_sum(n):
+    """Exact on small integers (any order is exact there), and within fp64 rounding of fsum."""
+    import math
+    ints = np.arange(n, dtype=np.float64) % 97
+    assert N.tree_sum(ints) == ints.sum()
+    rng = np.random.default_rng(n)
+    v = rng.uniform(0.0, 1.0, n)
+    assert abs(N.tree_sum(v) - math.fsum(v)) <= 1e-13 * max(1.0, math.fsum(v))
+
+
+def test_product_dynamic_map_equals_oracle(pkg):
+    """The code the GPU quantiser is handed is the oracle's create_dynamic_map, bit for bit."""
+    assert np.array_equal(pkg.quant._dynamic_map().numpy(), N.create_dynamic_map())
