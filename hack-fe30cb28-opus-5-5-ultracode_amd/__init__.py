@@ -7,13 +7,14 @@ stream. There is no Triton and no CPU fallback: without the built library every 
 
   engine   the training step: Packed, _Layer, _Head, FusedQwen2, random_qwen2
   linear   the step's GEMMs (NF4 projections forward/backward, lm_head)
-  gemm     plain fp16 GEMMs through rocBLAS with a measured solution per shape and token bucket
+  gemm     plain fp16 GEMMs through rocBLAS / hipBLASLt with a measured variant per shape and
+           token bucket
   head     the LM head over vocabulary pieces with the hidden and embedding gradients
   trainer  the HF / TRL Trainer drop-in: compute_loss replaced by the fused step (install)
   ops      the engine's op wrappers (_rms_fwd, _rms_bwd, _rope_fwd, _rope_bwd, _glu_fwd,
            _glu_bwd, _attn_fwd, _attn_bwd, _ce, _ce_piece, _ce_finish, _ce_grad, dequant,
            dequant_many, NF4Weight, NF4Group, TorchDropout)
-  quant    bitsandbytes-format NF4 double quantisation (builds the frozen weights)
+  quant    bitsandbytes-format NF4 double quantisation on the GPU (builds the frozen weights)
   _lib     the ctypes binding of the C-ABI
   build    hipcc build of the library
 """
