@@ -38,7 +38,7 @@ SIGNATURES = {
     "qlora_resid_add": [P, P, P, I64, P],
     "qlora_lora_fwd_rows": [P, P, P, P, P, P, P, P, P, P, I64, I32, I32, I32, I32, P],
     "qlora_lora_bwd_rows": [P, P, I64, P, P, P, P, P, P, P, P, I64, I32, I32, I32, I32, F32, P],
-    "qlora_lora_grad_workspace": [I64, I32, I32, I32, P],
+    "qlora_lora_grad_workspace": [I64, I32, I32, I32, I32, P],
     "qlora_lora_grad": [P, P, I64, P, P, P, P, P, P, P, P, P, P, I64, I32, I32, I32, I32, F32, P,
                         I64, P],
     "qlora_gemm": [I32, I64, I64, I64, P, I64, P, I64, P, I64, F32, F32, I32, P],

@@ -678,7 +678,7 @@ int check_common(int32_t nseq, int32_t max_len, int64_t n, int32_t HQ, int32_t K
   QLORA_CHECK_ARG(D == 64 || D == 128);
   QLORA_CHECK_ARG(HQ > 0 && KH > 0 && HQ % KH == 0);
   const int G = HQ / KH;
-  QLORA_CHECK_ARG(G == 1 || G == 2 || G == 4 || G == 6);
+  QLORA_CHECK_ARG(G >= 1 && G <= 8);  // every Qwen2 size: 14/2, 12/2, 16/2, 28/4, 40/8, 64/8
   QLORA_CHECK_ARG((int64_t)nseq * HQ < (1ll << 31));
   // buffer offsets within one sequence's rows (plus the prefetch past its end) fit 32 bits
   QLORA_CHECK_ARG(((int64_t)max_len + 4 * kKB) * HQ * D * 2 < (1ll << 31));
@@ -691,23 +691,24 @@ void launch_q(const Args& a, dim3 grid, hipStream_t s) {
   else hipLaunchKernelGGL((attn_fwd_kernel<D, G>), grid, dim3(64 * G), 0, s, a);
 }
 
+template <bool DQ, int D>
+void launch_q_g(const Args& a, int G, dim3 grid, hipStream_t s) {
+  switch (G) {
+    case 1: launch_q<D, 1, DQ>(a, grid, s); break;
+    case 2: launch_q<D, 2, DQ>(a, grid, s); break;
+    case 3: launch_q<D, 3, DQ>(a, grid, s); break;
+    case 4: launch_q<D, 4, DQ>(a, grid, s); break;
+    case 5: launch_q<D, 5, DQ>(a, grid, s); break;
+    case 6: launch_q<D, 6, DQ>(a, grid, s); break;
+    case 7: launch_q<D, 7, DQ>(a, grid, s); break;
+    default: launch_q<D, 8, DQ>(a, grid, s); break;
+  }
+}
+
 template <bool DQ>
 void launch_q_any(const Args& a, int D, int G, dim3 grid, hipStream_t s) {
-  if (D == 128) {
-    switch (G) {
-      case 1: launch_q<128, 1, DQ>(a, grid, s); break;
-      case 2: launch_q<128, 2, DQ>(a, grid, s); break;
-      case 4: launch_q<128, 4, DQ>(a, grid, s); break;
-      default: launch_q<128, 6, DQ>(a, grid, s); break;
-    }
-  } else {
-    switch (G) {
-      case 1: launch_q<64, 1, DQ>(a, grid, s); break;
-      case 2: launch_q<64, 2, DQ>(a, grid, s); break;
-      case 4: launch_q<64, 4, DQ>(a, grid, s); break;
-      default: launch_q<64, 6, DQ>(a, grid, s); break;
-    }
-  }
+  if (D == 128) launch_q_g<DQ, 128>(a, G, grid, s);
+  else launch_q_g<DQ, 64>(a, G, grid, s);
 }
 
 // Chunks of the split forms: chunk_keys a positive multiple of 64, at most kMaxChunks chunks.

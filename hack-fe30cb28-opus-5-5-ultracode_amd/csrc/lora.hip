@@ -1,24 +1,24 @@
 // Per-token parts of the LoRA forward and backward for the q and v adapters of a layer, one
-// launch each, on gfx950 MFMA (v_mfma_f32_32x32x16_f16).
+// launch each, on gfx950 MFMA (v_mfma_f32_32x32x16_f16), for LoRA ranks r = 8, 16, 32, 64.
 // Reference: engine.py:1088-1093 (forward: lora_A then lora_B on the dropped LoRA input) and
-// engine.py:1319-1331 (backward). Both are two chained fp16 products through the rank-16
+// engine.py:1319-1331 (backward). Both are two chained fp16 products through the rank-r
 // bottleneck, each accumulated in fp32 and rounded once, as the reference's GEMMs:
-//   forward:   x  = f16(a A^T)            [n, 16]   (kept for the backward)
+//   forward:   x  = f16(a A^T)            [n, r]    (kept for the backward)
 //              l  = f16(x B^T)            [n, N]    (added to the projection by the RoPE kernel)
-//   backward:  dx = f16(f16(g B) * s)     [n, 16]   (g: the adapter's columns of d[q|k|v])
+//   backward:  dx = f16(f16(g B) * s)     [n, r]    (g: the adapter's columns of d[q|k|v])
 //              t  = f16(dx A)             [n, H]    (the gradient reaching the LoRA input)
 // The token reductions of the backward (dB = s g^T x, dA = dx^T a) are qlora_lora_grad, below.
 //
-// Generic form: phase 1 P = X W (X [n, K1] rows, W given as Wt [16, K1]), phase 2 Y = P V (V
-// given as Vt [M2, 16]). Every MFMA operand is then a 16-byte run along the contraction. The
+// Generic form: phase 1 P = X W (X [n, K1] rows, W given as Wt [r, K1]), phase 2 Y = P V (V
+// given as Vt [M2, r]). Every MFMA operand is then a 16-byte run along the contraction. The
 // backward's Wt = B^T and Vt = A^T are the fp16 copies the caller keeps transposed.
 //
 // A workgroup owns 32 tokens of one adapter (blockIdx.y: 0 = q, 1 = v), eight wavefronts.
-// Phase 1: a 32 x 32 MFMA tile (rank columns 16..31 ignored), the 16-wide k-steps dealt
-// round-robin to the wavefronts in chunks whose loads are all issued before the chunk's MFMAs;
-// the eight partial tiles are summed in LDS and rounded. Phase 2 computes Y^T = Vt P^T, one
-// MFMA per 32 output columns, so that a lane holds four consecutive columns of one token and
-// writes 8-byte runs; the first chunk of Vt operands is loaded before phase 1.
+// Phase 1: 32 x 32 MFMA tiles over the rank columns, the 16-wide k-steps dealt round-robin to the
+// wavefronts in chunks whose loads are all issued before the chunk's MFMAs; the eight partial
+// tiles are summed in LDS and rounded. Phase 2 computes Y^T = Vt P^T, one MFMA per 32 output
+// columns and 16 ranks, so that a lane holds four consecutive columns of one token and writes
+// 8-byte runs; the first chunk of Vt operands is loaded before phase 1.
 #include "common.h"
 
 namespace qlora {
@@ -27,17 +27,18 @@ namespace lora {
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kRank = 16;
 constexpr int kTok = 32;
 constexpr int kWaves = 8;
 constexpr int kChunk1 = 12;  // phase-1 k-steps per wavefront per chunk
-constexpr int kChunk2 = 6;  // phase-2 column tiles per wavefront per chunk
+
+// The LoRA ranks the kernels take (template parameter R).
+__host__ __device__ constexpr bool rank_ok(int r) { return r == 8 || r == 16 || r == 32 || r == 64; }
 
 struct Job {
   const uint16_t* X;   // fp16 [n, ldx] (phase-1 rows)
-  const uint16_t* Wt;  // fp16 [16, K1]
-  uint16_t* P;         // fp16 [n, 16]
-  const uint16_t* Vt;  // fp16 [M2, 16]
+  const uint16_t* Wt;  // fp16 [R, K1]
+  uint16_t* P;         // fp16 [n, R]
+  const uint16_t* Vt;  // fp16 [M2, R]
   uint16_t* Y;         // fp16 [n, M2] or null (no phase 2)
   int64_t ldx;
   int K1, M2;
@@ -58,9 +59,17 @@ __device__ __forceinline__ half8_t ld8(const uint16_t* p) {
   return *reinterpret_cast<const half8_t*>(p);
 }
 
+// Rank R: phase 1 uses ceil(R / 32) MFMA column tiles (rank columns past R read duplicated rows
+// of Wt and are dropped); phase 2 contracts over ceil(R / 16) k-steps of 16, the rank-R
+// intermediate zero-padded to a multiple of 16 in LDS (the matching Vt columns then read
+// duplicated, finite weights: 0 x finite adds exactly 0).
+template <int R>
 __global__ __launch_bounds__(64 * kWaves) void lora_rows_kernel(Args a) {
-  __shared__ float red[kWaves][kTok][kRank];
-  __shared__ __align__(16) uint16_t ps[kTok][kRank];
+  constexpr int NT1 = (R + 31) / 32, KS2 = (R + 15) / 16, RP = 16 * KS2;
+  constexpr int CH1 = NT1 == 1 ? kChunk1 : kChunk1 / 2;
+  constexpr int CH2 = KS2 == 1 ? 6 : (KS2 == 2 ? 3 : 2);  // phase-2 column tiles per chunk
+  __shared__ float red[kWaves][kTok][R];
+  __shared__ __align__(16) uint16_t ps[kTok][RP];
   const Job& jb = a.job[blockIdx.y];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int row = lane & 31, half = lane >> 5;
@@ -68,65 +77,93 @@ __global__ __launch_bounds__(64 * kWaves) void lora_rows_kernel(Args a) {
   const int64_t tok = t0 + row < a.n ? t0 + row : a.n - 1;  // rows past n: computed, not stored
   const bool two = jb.Y != nullptr;
   const int tiles = two ? jb.M2 / 32 : 0;
-  // phase-2 operands of the first chunk: Vt rows 32 c + l%32, ranks 8(l/32)..+7
-  half8_t vop[kChunk2];
+  // phase-2 operands of the first chunk: Vt rows 32 c + l%32, ranks 16 kk + 8(l/32)..+7 (past R:
+  // the row's first ranks again)
+  half8_t vop[CH2][KS2];
 #pragma unroll
-  for (int i = 0; i < kChunk2; ++i) {
+  for (int i = 0; i < CH2; ++i) {
     const int c = min(wave + kWaves * i, max(tiles - 1, 0));
-    vop[i] = two ? ld8(jb.Vt + (int64_t)(32 * c + row) * kRank + 8 * half) : half8_t{};
-  }
-  // phase 1: P[32 x 16] = X[32 x K1] W[K1 x 16]
-  const uint16_t* xrow = jb.X + tok * jb.ldx + 8 * half;
-  const uint16_t* wrow = jb.Wt + (int64_t)(row & (kRank - 1)) * jb.K1 + 8 * half;
-  const int steps = jb.K1 / 16;
-  f32x16 acc = f32x16{};
-  for (int k0 = wave; k0 < steps; k0 += kWaves * kChunk1) {
-    half8_t xa[kChunk1], wb[kChunk1];
 #pragma unroll
-    for (int i = 0; i < kChunk1; ++i) {
+    for (int kk = 0; kk < KS2; ++kk) {
+      const int r0 = min(16 * kk + 8 * half, R - 8);
+      vop[i][kk] = two ? ld8(jb.Vt + (int64_t)(32 * c + row) * R + r0) : half8_t{};
+    }
+  }
+  // phase 1: P[32 x R] = X[32 x K1] W[K1 x R]
+  const uint16_t* xrow = jb.X + tok * jb.ldx + 8 * half;
+  const uint16_t* wrow[NT1];
+#pragma unroll
+  for (int t = 0; t < NT1; ++t)
+    wrow[t] = jb.Wt + (int64_t)((32 * t + row) & (R - 1)) * jb.K1 + 8 * half;
+  const int steps = jb.K1 / 16;
+  f32x16 acc[NT1];
+#pragma unroll
+  for (int t = 0; t < NT1; ++t) acc[t] = f32x16{};
+  for (int k0 = wave; k0 < steps; k0 += kWaves * CH1) {
+    half8_t xa[CH1], wb[CH1][NT1];
+#pragma unroll
+    for (int i = 0; i < CH1; ++i) {
       const int ks = min(k0 + kWaves * i, steps - 1);
       xa[i] = ld8(xrow + 16 * ks);
-      wb[i] = ld8(wrow + 16 * ks);
+#pragma unroll
+      for (int t = 0; t < NT1; ++t) wb[i][t] = ld8(wrow[t] + 16 * ks);
     }
 #pragma unroll
-    for (int i = 0; i < kChunk1; ++i)
-      acc = mfma(xa[i], k0 + kWaves * i < steps ? wb[i] : half8_t{}, acc);
-  }
-  // register r of lane l holds P[8(r/4) + 4(l/32) + r%4][l%32]
-  if (row < kRank) {
+    for (int i = 0; i < CH1; ++i)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) red[wave][8 * (r >> 2) + 4 * half + (r & 3)][row] = acc[r];
+      for (int t = 0; t < NT1; ++t)
+        acc[t] = mfma(xa[i], k0 + kWaves * i < steps ? wb[i][t] : half8_t{}, acc[t]);
+  }
+  // register r of lane l holds P[8(r/4) + 4(l/32) + r%4][32 t + l%32]
+#pragma unroll
+  for (int t = 0; t < NT1; ++t) {
+    if (32 * t + row < R) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        red[wave][8 * (r >> 2) + 4 * half + (r & 3)][32 * t + row] = acc[t][r];
+    }
   }
   __syncthreads();
-  {
-    const int t = tid / kRank, k = tid % kRank;  // 512 threads = 32 tokens x 16 ranks
-    float v = 0.f;
+  for (int idx = tid; idx < kTok * RP; idx += 64 * kWaves) {
+    const int t = idx / RP, k = idx % RP;
+    uint16_t b = 0;
+    if (k < R) {
+      float v = 0.f;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) v += red[w][t][k];
-    v = h2f(f2h(v));
-    if (a.scale) v = h2f(f2h(v * a.s));
-    const uint16_t b = f2h_bits(v);
+      for (int w = 0; w < kWaves; ++w) v += red[w][t][k];
+      v = h2f(f2h(v));
+      if (a.scale) v = h2f(f2h(v * a.s));
+      b = f2h_bits(v);
+      if (t0 + t < a.n) jb.P[(t0 + t) * R + k] = b;
+    }
     ps[t][k] = b;
-    if (t0 + t < a.n) jb.P[(t0 + t) * kRank + k] = b;
   }
   if (!two) return;  // uniform over the workgroup
   __syncthreads();
-  // phase 2: Y^T[32 cols x 32 tok] = Vt[32 x 16] P^T[16 x 32]; B operand P[l%32][8(l/32)..+7]
-  const half8_t pb = ld8(&ps[row][8 * half]);
+  // phase 2: Y^T[32 cols x 32 tok] = Vt[32 x R] P^T[R x 32]; B operand P[l%32][16 kk + 8(l/32)..]
+  half8_t pb[KS2];
+#pragma unroll
+  for (int kk = 0; kk < KS2; ++kk) pb[kk] = ld8(&ps[row][16 * kk + 8 * half]);
   const bool store = t0 + row < a.n;
   uint16_t* yrow = jb.Y + (t0 + row) * jb.M2 + 4 * half;
-  for (int c0 = wave; c0 < tiles; c0 += kWaves * kChunk2) {
+  for (int c0 = wave; c0 < tiles; c0 += kWaves * CH2) {
     if (c0 != wave) {
 #pragma unroll
-      for (int i = 0; i < kChunk2; ++i) {
+      for (int i = 0; i < CH2; ++i) {
         const int c = min(c0 + kWaves * i, tiles - 1);
-        vop[i] = ld8(jb.Vt + (int64_t)(32 * c + row) * kRank + 8 * half);
+#pragma unroll
+        for (int kk = 0; kk < KS2; ++kk) {
+          const int r0 = min(16 * kk + 8 * half, R - 8);
+          vop[i][kk] = ld8(jb.Vt + (int64_t)(32 * c + row) * R + r0);
+        }
       }
     }
 #pragma unroll
-    for (int i = 0; i < kChunk2; ++i) {
+    for (int i = 0; i < CH2; ++i) {
       const int c = c0 + kWaves * i;
-      const f32x16 y = mfma(vop[i], pb, f32x16{});
+      f32x16 y = f32x16{};
+#pragma unroll
+      for (int kk = 0; kk < KS2; ++kk) y = mfma(vop[i][kk], pb[kk], y);
       // register r: Y[t0 + l%32][32 c + 8(r/4) + 4(l/32) + r%4]
       if (store && c < tiles) {
 #pragma unroll
@@ -143,7 +180,8 @@ __global__ __launch_bounds__(64 * kWaves) void lora_rows_kernel(Args a) {
 
 bool aligned(const void* p, uintptr_t b) { return ((uintptr_t)p & (b - 1)) == 0; }
 
-int launch(Args& a, hipStream_t stream) {
+int launch(Args& a, int r, hipStream_t stream) {
+  QLORA_CHECK_ARG(rank_ok(r));
   for (int i = 0; i < 2; ++i) {
     const Job& j = a.job[i];
     QLORA_CHECK_ARG(j.X && j.Wt && j.P && j.K1 > 0 && j.K1 % 16 == 0 && j.ldx >= j.K1);
@@ -152,8 +190,13 @@ int launch(Args& a, hipStream_t stream) {
                     (j.Vt && j.M2 > 0 && j.M2 % 32 == 0 && aligned(j.Vt, 16) && aligned(j.Y, 8)));
   }
   QLORA_CHECK_ARG(a.n < (1ll << 31) * kTok);
-  hipLaunchKernelGGL(lora_rows_kernel, dim3((unsigned)qlora_cdiv(a.n, kTok), 2),
-                     dim3(64 * kWaves), 0, stream, a);
+  const dim3 grid((unsigned)qlora_cdiv(a.n, kTok), 2), block(64 * kWaves);
+  switch (r) {
+    case 8: hipLaunchKernelGGL(lora_rows_kernel<8>, grid, block, 0, stream, a); break;
+    case 16: hipLaunchKernelGGL(lora_rows_kernel<16>, grid, block, 0, stream, a); break;
+    case 32: hipLaunchKernelGGL(lora_rows_kernel<32>, grid, block, 0, stream, a); break;
+    default: hipLaunchKernelGGL(lora_rows_kernel<64>, grid, block, 0, stream, a); break;
+  }
   return qlora_launch_status();
 }
 
@@ -208,10 +251,14 @@ __device__ __forceinline__ float dot2u(uint32_t a, uint32_t b, float c) {
                                 c, false);
 }
 
+// Rank R: every thread accumulates all R sums of its two columns (2 R fp32 registers); they are
+// merged over the quarters in LDS in slices of S = min(R, 16) ranks.
+template <int R>
 __global__ __launch_bounds__(kGradThreads) void lora_grad_part_kernel(GradArgs a) {
+  constexpr int S = R < 16 ? R : 16;
   constexpr int kQP = kGradQuarter / 2;  // token pairs per thread
-  constexpr int kRow = 2 * kRank + 4;    // floats per column pair in the LDS sum (padded)
-  __shared__ __align__(16) uint32_t zp[kGradChunk / 2][kRank];
+  constexpr int kRow = 2 * S + 4;        // floats per column pair in the LDS sum (padded)
+  __shared__ __align__(16) uint32_t zp[kGradChunk / 2][R];
   __shared__ __align__(16) float red[4][kGradPairs][kRow];
   const int tid = threadIdx.x, quarter = tid >> 6, cp = tid & 63;
   const int wg_col = blockIdx.x * kGradCols;
@@ -231,23 +278,23 @@ __global__ __launch_bounds__(kGradThreads) void lora_grad_part_kernel(GradArgs a
     w0[i] = *reinterpret_cast<const uint32_t*>(wp + ta * jb.ldw);
     w1[i] = *reinterpret_cast<const uint32_t*>(wp + tb * jb.ldw);
   }
-  for (int i = tid; i < (kGradChunk / 2) * kRank; i += kGradThreads) {
-    const int p = i / kRank, k = i % kRank;
+  for (int i = tid; i < (kGradChunk / 2) * R; i += kGradThreads) {
+    const int p = i / R, k = i % R;
     const int64_t ta = t0 + min(2 * p, nt - 1), tb = t0 + min(2 * p + 1, nt - 1);
-    const uint32_t za = jb.Z[ta * kRank + k], zb = jb.Z[tb * kRank + k];
+    const uint32_t za = jb.Z[ta * R + k], zb = jb.Z[tb * R + k];
     zp[p][k] = (2 * p < nt ? za : 0u) | ((2 * p + 1 < nt ? zb : 0u) << 16);
   }
   __syncthreads();
-  float acc0[kRank], acc1[kRank];
+  float acc0[R], acc1[R];
 #pragma unroll
-  for (int k = 0; k < kRank; ++k) acc0[k] = acc1[k] = 0.f;
+  for (int k = 0; k < R; ++k) acc0[k] = acc1[k] = 0.f;
 #pragma unroll
   for (int i = 0; i < kQP; ++i) {
     const uint32_t pc0 = (w0[i] & 0xFFFFu) | (w1[i] << 16);  // column c, tokens t, t + 1
     const uint32_t pc1 = (w0[i] >> 16) | (w1[i] & 0xFFFF0000u);  // column c + 1
     const uint4* zq = reinterpret_cast<const uint4*>(zp[kQP * quarter + i]);
 #pragma unroll
-    for (int q = 0; q < kRank / 4; ++q) {
+    for (int q = 0; q < R / 4; ++q) {
       const uint4 z = zq[q];
       acc0[4 * q + 0] = dot2u(pc0, z.x, acc0[4 * q + 0]);
       acc0[4 * q + 1] = dot2u(pc0, z.y, acc0[4 * q + 1]);
@@ -259,54 +306,60 @@ __global__ __launch_bounds__(kGradThreads) void lora_grad_part_kernel(GradArgs a
       acc1[4 * q + 3] = dot2u(pc1, z.w, acc1[4 * q + 3]);
     }
   }
-  float4* mine = reinterpret_cast<float4*>(red[quarter][cp]);
+  const int pair = tid >> 2, sub = tid & 3;  // the final sums: 4 threads per column pair
+  const bool pair_ok = wg_col - jb.col0 + 2 * pair < jb.ncols;
 #pragma unroll
-  for (int q = 0; q < kRank / 4; ++q) {
-    mine[q] = make_float4(acc0[4 * q], acc0[4 * q + 1], acc0[4 * q + 2], acc0[4 * q + 3]);
-    mine[kRank / 4 + q] =
-        make_float4(acc1[4 * q], acc1[4 * q + 1], acc1[4 * q + 2], acc1[4 * q + 3]);
-  }
-  __syncthreads();
-  // the chunk's sums: 64 column pairs x 32 values, 8 per thread (two float4 of one pair)
-  const int pair = tid >> 2, part4 = (tid & 3) * 2;
-  if (wg_col - jb.col0 + 2 * pair >= jb.ncols) return;  // no barrier follows
-  float4* dst = reinterpret_cast<float4*>(
-      a.part + ((int64_t)blockIdx.y * a.total_cols + wg_col + 2 * pair) * kRank);
+  for (int rs = 0; rs < R / S; ++rs) {
+    if (rs > 0) __syncthreads();  // the previous slice's sums have been read
+    float4* mine = reinterpret_cast<float4*>(red[quarter][cp]);
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int f = part4 + h;  // float4 index within the pair's 32 values
-    float4 v = reinterpret_cast<const float4*>(red[0][pair])[f];
-#pragma unroll
-    for (int qq = 1; qq < 4; ++qq) {
-      const float4 u = reinterpret_cast<const float4*>(red[qq][pair])[f];
-      v.x += u.x;
-      v.y += u.y;
-      v.z += u.z;
-      v.w += u.w;
+    for (int q = 0; q < S / 4; ++q) {
+      const int k = rs * S + 4 * q;
+      mine[q] = make_float4(acc0[k], acc0[k + 1], acc0[k + 2], acc0[k + 3]);
+      mine[S / 4 + q] = make_float4(acc1[k], acc1[k + 1], acc1[k + 2], acc1[k + 3]);
     }
-    dst[f] = v;
+    __syncthreads();
+    // the pair's 2 S sums as S / 2 float4: the first S / 4 of column c, the rest of c + 1
+    if (pair_ok) {
+      for (int f = sub; f < S / 2; f += 4) {
+        float4 v = reinterpret_cast<const float4*>(red[0][pair])[f];
+#pragma unroll
+        for (int qq = 1; qq < 4; ++qq) {
+          const float4 u = reinterpret_cast<const float4*>(red[qq][pair])[f];
+          v.x += u.x;
+          v.y += u.y;
+          v.z += u.z;
+          v.w += u.w;
+        }
+        const int col = wg_col + 2 * pair + (f >= S / 4 ? 1 : 0);
+        const int k = rs * S + 4 * (f % (S / 4));
+        *reinterpret_cast<float4*>(a.part + ((int64_t)blockIdx.y * a.total_cols + col) * R + k) =
+            v;
+      }
+    }
   }
 }
 
+template <int R>
 __global__ __launch_bounds__(256) void lora_grad_reduce_kernel(GradArgs a) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= (int64_t)a.total_cols * kRank) return;
-  const int col = (int)(i / kRank), k = (int)(i % kRank);
+  if (i >= (int64_t)a.total_cols * R) return;
+  const int col = (int)(i / R), k = (int)(i % R);
   const GradJob& jb = a.job[grad_job(a, col)];
   const int c = col - jb.col0;
   if (c >= jb.ncols) return;
   float v = 0.f;
 #pragma unroll 8
-  for (int ch = 0; ch < a.nchunks; ++ch) v += a.part[(int64_t)ch * a.total_cols * kRank + i];
+  for (int ch = 0; ch < a.nchunks; ++ch) v += a.part[(int64_t)ch * a.total_cols * R + i];
   v *= jb.scale;
-  jb.out[jb.trans ? (int64_t)k * jb.ncols + c : (int64_t)c * kRank + k] = v;
+  jb.out[jb.trans ? (int64_t)k * jb.ncols + c : (int64_t)c * R + k] = v;
 }
 
 int64_t grad_pad(int64_t c) { return qlora_cdiv(c, kGradCols) * kGradCols; }
 
-int64_t grad_workspace(int64_t n, int N_q, int N_v, int H) {
+int64_t grad_workspace(int64_t n, int N_q, int N_v, int H, int r) {
   const int64_t cols = grad_pad(N_q) + grad_pad(N_v) + 2 * grad_pad(H);
-  return qlora_cdiv(n, kGradChunk) * cols * kRank;
+  return qlora_cdiv(n, kGradChunk) * cols * r;
 }
 
 }  // namespace lora
@@ -320,7 +373,7 @@ QLORA_API int qlora_lora_fwd_rows(const void* a_q, const void* a_v, const void* 
                                   int32_t N_v, int32_t H, int32_t r, void* stream) {
   QLORA_CHECK_ARG(n >= 0 && N_q > 0 && N_v > 0 && H > 0);
   if (n == 0) return 0;
-  QLORA_CHECK_ARG(r == kRank && l_q && l_v);
+  QLORA_CHECK_ARG(rank_ok(r) && l_q && l_v);
   Args a{};
   a.job[0] = Job{static_cast<const uint16_t*>(a_q), static_cast<const uint16_t*>(A_q),
                  static_cast<uint16_t*>(x_q), static_cast<const uint16_t*>(B_q),
@@ -331,7 +384,7 @@ QLORA_API int qlora_lora_fwd_rows(const void* a_q, const void* a_v, const void* 
   a.n = n;
   a.s = 1.f;
   a.scale = 0;
-  return launch(a, (hipStream_t)stream);
+  return launch(a, r, (hipStream_t)stream);
 }
 
 QLORA_API int qlora_lora_bwd_rows(const void* g_q, const void* g_v, int64_t ldg,
@@ -341,7 +394,7 @@ QLORA_API int qlora_lora_bwd_rows(const void* g_q, const void* g_v, int64_t ldg,
                                   float s, void* stream) {
   QLORA_CHECK_ARG(n >= 0 && N_q > 0 && N_v > 0 && H > 0);
   if (n == 0) return 0;
-  QLORA_CHECK_ARG(r == kRank && (t_q == nullptr) == (t_v == nullptr));
+  QLORA_CHECK_ARG(rank_ok(r) && (t_q == nullptr) == (t_v == nullptr));
   Args a{};
   a.job[0] = Job{static_cast<const uint16_t*>(g_q), static_cast<const uint16_t*>(Bt_q),
                  static_cast<uint16_t*>(dx_q), static_cast<const uint16_t*>(At_q),
@@ -352,29 +405,29 @@ QLORA_API int qlora_lora_bwd_rows(const void* g_q, const void* g_v, int64_t ldg,
   a.n = n;
   a.s = s;
   a.scale = 1;
-  return launch(a, (hipStream_t)stream);
+  return launch(a, r, (hipStream_t)stream);
 }
 
 // Workspace (fp32 elements) qlora_lora_grad needs for these sizes.
 QLORA_API int qlora_lora_grad_workspace(int64_t n, int32_t N_q, int32_t N_v, int32_t H,
-                                        int64_t* elems) {
-  QLORA_CHECK_ARG(n >= 0 && N_q > 0 && N_v > 0 && H > 0 && elems);
-  *elems = grad_workspace(n, N_q, N_v, H);
+                                        int32_t r, int64_t* elems) {
+  QLORA_CHECK_ARG(n >= 0 && N_q > 0 && N_v > 0 && H > 0 && rank_ok(r) && elems);
+  *elems = grad_workspace(n, N_q, N_v, H, r);
   return 0;
 }
 
-// dB_a = s g_a^T x_a fp32 [N_a, 16], dA_a = dx_a^T a_a fp32 [16, H] for a = q, v (zeros for n = 0).
+// dB_a = s g_a^T x_a fp32 [N_a, r], dA_a = dx_a^T a_a fp32 [r, H] for a = q, v (zeros for n = 0).
 QLORA_API int qlora_lora_grad(const void* g_q, const void* g_v, int64_t ldg, const void* x_q,
                               const void* x_v, const void* a_q, const void* a_v,
                               const void* dx_q, const void* dx_v, float* dB_q, float* dB_v,
                               float* dA_q, float* dA_v, int64_t n, int32_t N_q, int32_t N_v,
                               int32_t H, int32_t r, float s, float* work, int64_t work_elems,
                               void* stream) {
-  QLORA_CHECK_ARG(n >= 0 && N_q > 0 && N_v > 0 && H > 0 && r == kRank);
+  QLORA_CHECK_ARG(n >= 0 && N_q > 0 && N_v > 0 && H > 0 && rank_ok(r));
   QLORA_CHECK_ARG(N_q % 2 == 0 && N_v % 2 == 0 && H % 2 == 0 && ldg % 2 == 0);
   QLORA_CHECK_ARG(ldg >= N_q && ldg >= N_v);
   QLORA_CHECK_ARG(dB_q && dB_v && dA_q && dA_v);
-  QLORA_CHECK_ARG(work_elems >= grad_workspace(n, N_q, N_v, H) && (n == 0 || work));
+  QLORA_CHECK_ARG(work_elems >= grad_workspace(n, N_q, N_v, H, r) && (n == 0 || work));
   if (n > 0) {
     QLORA_CHECK_ARG(g_q && g_v && x_q && x_v && a_q && a_v && dx_q && dx_v);
     QLORA_CHECK_ARG(aligned(g_q, 4) && aligned(g_v, 4) && aligned(a_q, 4) && aligned(a_v, 4));
@@ -397,10 +450,19 @@ QLORA_API int qlora_lora_grad(const void* g_q, const void* g_v, int64_t ldg, con
   a.total_cols = col;
   a.nchunks = (int)qlora_cdiv(n, kGradChunk);
   hipStream_t st = (hipStream_t)stream;
-  if (n > 0)
-    hipLaunchKernelGGL(lora_grad_part_kernel, dim3(col / kGradCols, a.nchunks),
-                       dim3(kGradThreads), 0, st, a);
-  hipLaunchKernelGGL(lora_grad_reduce_kernel, dim3((unsigned)qlora_cdiv((int64_t)col * kRank, 256)),
-                     dim3(256), 0, st, a);
+  const dim3 g1(col / kGradCols, a.nchunks), g2((unsigned)qlora_cdiv((int64_t)col * r, 256));
+#define QLORA_GRAD(RR)                                                                   \
+  do {                                                                                   \
+    if (n > 0)                                                                           \
+      hipLaunchKernelGGL(lora_grad_part_kernel<RR>, g1, dim3(kGradThreads), 0, st, a);   \
+    hipLaunchKernelGGL(lora_grad_reduce_kernel<RR>, g2, dim3(256), 0, st, a);            \
+  } while (0)
+  switch (r) {
+    case 8: QLORA_GRAD(8); break;
+    case 16: QLORA_GRAD(16); break;
+    case 32: QLORA_GRAD(32); break;
+    default: QLORA_GRAD(64); break;
+  }
+#undef QLORA_GRAD
   return qlora_launch_status();
 }

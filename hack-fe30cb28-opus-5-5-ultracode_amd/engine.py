@@ -124,6 +124,9 @@ def random_qwen2(cfg, device, seed=0, norm_dtype=torch.float32):
     return FusedQwen2(cfg, layers, embed, norm_w, device)
 
 
+SUPPORTED_RANKS = (8, 16, 32, 64)  # LoRA ranks of the HIP kernels
+
+
 class UnsupportedModel(ValueError):
     """The model is not a PEFT-wrapped 4-bit Qwen2 the step supports (patch.py:_is_supported)."""
 
@@ -168,6 +171,13 @@ def from_peft(peft_model, keep_all=None):
     q0 = layers_hf[0].self_attn.q_proj
     qname = names["q"]
     r = int(q0.lora_A[qname].weight.shape[0])
+    HKV = hf.num_key_value_heads
+    if r not in SUPPORTED_RANKS:
+        raise UnsupportedModel(f"LoRA rank {r}; the kernels take {SUPPORTED_RANKS}")
+    if HQ % HKV or not 1 <= HQ // HKV <= 8 or D not in (64, 128) or H % 32:
+        raise UnsupportedModel(f"attention heads {HQ}/{HKV} x {D}, hidden {H}: the kernels "
+                               "take up to 8 q heads per kv head, head_dim 64 or 128, hidden "
+                               "size a multiple of 32")
     scaling = float(q0.scaling[qname])
     drop = q0.lora_dropout[qname] if hasattr(q0, "lora_dropout") else None
     p = float(getattr(drop, "p", 0.0))

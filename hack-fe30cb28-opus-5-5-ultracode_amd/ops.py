@@ -567,7 +567,7 @@ def _lora_grad(dqkv, q_cols, v_cols, x_q, x_v, a_q, a_v, dx_q, dx_v, scale):
     dA_q, dA_v = torch.empty((r, H), device=dev, dtype=f32), torch.empty((r, H), device=dev,
                                                                            dtype=f32)
     elems = ctypes.c_int64(0)
-    _lib.call("qlora_lora_grad_workspace", n, Nq, Nv, H, ctypes.byref(elems))
+    _lib.call("qlora_lora_grad_workspace", n, Nq, Nv, H, r, ctypes.byref(elems))
     work = torch.empty((max(elems.value, 1),), device=dev, dtype=f32)
     base = dqkv.data_ptr()
     _lib.call("qlora_lora_grad", base + 2 * q_cols.start, base + 2 * v_cols.start,

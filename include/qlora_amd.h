@@ -289,10 +289,11 @@ int qlora_gemmlt_solutions(int32_t op, int64_t M, int64_t N, int64_t K, int64_t 
 
 /*
  * The LoRA forward of a layer's q and v adapters in one launch (engine.py:1088-1093):
- *   x_a = f16(a_a A_a^T)   f16 [n, 16] (kept for the backward)
+ *   x_a = f16(a_a A_a^T)   f16 [n, r] (kept for the backward)
  *   l_a = f16(x_a B_a^T)   f16 [n, N_a] (added to the projection output by qlora_rope_fwd)
- * a_a f16 [n, H] (the dropped LoRA inputs of qlora_rms_fwd); A_a f16 [16, H]; B_a f16 [N_a, 16].
- * Requires r == 16, H % 16 == 0, N_a % 32 == 0; a_a, A_a, B_a 16-byte and l_a 8-byte aligned.
+ * a_a f16 [n, H] (the dropped LoRA inputs of qlora_rms_fwd); A_a f16 [r, H]; B_a f16 [N_a, r].
+ * Requires r in {8, 16, 32, 64}, H % 16 == 0, N_a % 32 == 0; a_a, A_a, B_a 16-byte and l_a
+ * 8-byte aligned.
  * No reference counterpart as one launch: the reference makes four fp16 products.
  */
 int qlora_lora_fwd_rows(const void* a_q, const void* a_v, const void* A_q, const void* A_v,
@@ -302,13 +303,13 @@ int qlora_lora_fwd_rows(const void* a_q, const void* a_v, const void* A_q, const
 
 /*
  * Per-token part of the LoRA backward of a layer's q and v adapters in one launch:
- *   dx_a = f16(f16(g_a B_a) * s)   f16 [n, 16]        t_a = f16(dx_a A_a)   f16 [n, H]
+ *   dx_a = f16(f16(g_a B_a) * s)   f16 [n, r]        t_a = f16(dx_a A_a)   f16 [n, H]
  * g_q / g_v: the adapters' columns of the fused d[q|k|v] gradient (f16, row stride ldg);
- * Bt_a = B_a^T f16 [16, N_a]; At_a = A_a^T f16 [H, 16] (the transposed adapter weights);
+ * Bt_a = B_a^T f16 [r, N_a]; At_a = A_a^T f16 [H, r] (the transposed adapter weights);
  * t_q/t_v may both be null (then not computed). Replaces `dx_lo = (g @ b_w) * s` and
  * `dx_lo @ a_w` (engine.py:1326-1330) for both adapters; the token reductions dB and dA are
- * qlora_lora_grad. Requires r == 16, N_a % 16 == 0, H % 32 == 0, ldg % 8 == 0; g_a, Bt_a,
- * At_a 16-byte and t_a 8-byte aligned.
+ * qlora_lora_grad. Requires r in {8, 16, 32, 64}, N_a % 16 == 0, H % 32 == 0, ldg % 8 == 0;
+ * g_a, Bt_a, At_a 16-byte and t_a 8-byte aligned.
  */
 int qlora_lora_bwd_rows(const void* g_q, const void* g_v, int64_t ldg, const void* Bt_q,
                         const void* Bt_v, const void* At_q, const void* At_v, void* dx_q,
@@ -317,14 +318,16 @@ int qlora_lora_bwd_rows(const void* g_q, const void* g_v, int64_t ldg, const voi
 
 /*
  * Token reductions of the LoRA backward of a layer's q and v adapters (engine.py:1327, 1329):
- *   dB_a = s * g_a^T x_a   fp32 [N_a, 16]        dA_a = dx_a^T a_a   fp32 [16, H]
- * g_q / g_v as in qlora_lora_bwd_rows (row stride ldg); x_a f16 [n, 16] (qlora_lora_fwd_rows);
- * a_a f16 [n, H] (the dropped LoRA inputs); dx_a f16 [n, 16] (qlora_lora_bwd_rows). fp32 sums
+ *   dB_a = s * g_a^T x_a   fp32 [N_a, r]        dA_a = dx_a^T a_a   fp32 [r, H]
+ * g_q / g_v as in qlora_lora_bwd_rows (row stride ldg); x_a f16 [n, r] (qlora_lora_fwd_rows);
+ * a_a f16 [n, H] (the dropped LoRA inputs); dx_a f16 [n, r] (qlora_lora_bwd_rows). fp32 sums
  * of exact products, reduced in a fixed order (deterministic); the reference rounds dB and dA
  * to fp16 before its `.float()`, these keep fp32. work: fp32 workspace of at least the
- * qlora_lora_grad_workspace size. n = 0 writes zeros. Requires r == 16; N_a, H, ldg even.
+ * qlora_lora_grad_workspace size. n = 0 writes zeros. Requires r in {8, 16, 32, 64}; N_a, H,
+ * ldg even.
  */
-int qlora_lora_grad_workspace(int64_t n, int32_t N_q, int32_t N_v, int32_t H, int64_t* elems);
+int qlora_lora_grad_workspace(int64_t n, int32_t N_q, int32_t N_v, int32_t H, int32_t r,
+                              int64_t* elems);
 int qlora_lora_grad(const void* g_q, const void* g_v, int64_t ldg, const void* x_q,
                     const void* x_v, const void* a_q, const void* a_v, const void* dx_q,
                     const void* dx_v, float* dB_q, float* dB_v, float* dA_q, float* dA_v,

@@ -443,16 +443,16 @@ def test_ce_kernels_take_the_target_logit_before_the_row_is_overwritten(pkg):
 @pytest.mark.parametrize("n,H,Nq,Nv", [(300, 1536, 1536, 256), (1, 1536, 1536, 256),
                                        (77, 256, 256, 128), (4100, 896, 896, 128),
                                        (33, 3584, 3584, 512)])
-def test_lora_bwd_rows(pkg, n, H, Nq, Nv):
+def test_lora_bwd_rows(pkg, n, H, Nq, Nv, r=16):
     """dx = fp16(fp16(g B) s), t = fp16(dx A) for both adapters against fp64 of the same
     roundings (engine.py:1326-1330); g are column slices of one fused gradient (row stride C)."""
-    g = torch.Generator().manual_seed(n)
+    g = torch.Generator().manual_seed(n + r)
     C = Nq + 2 * Nv
     dqkv = torch.randn(n, C, generator=g).half()
-    aq = (torch.randn(16, H, generator=g) * 0.05).half()
-    av = (torch.randn(16, H, generator=g) * 0.05).half()
-    bq = (torch.randn(Nq, 16, generator=g) * 0.05).half()
-    bv = (torch.randn(Nv, 16, generator=g) * 0.05).half()
+    aq = (torch.randn(r, H, generator=g) * 0.05).half()
+    av = (torch.randn(r, H, generator=g) * 0.05).half()
+    bq = (torch.randn(Nq, r, generator=g) * 0.05).half()
+    bv = (torch.randn(Nv, r, generator=g) * 0.05).half()
     s = 2.0
     qc, vc = slice(0, Nq), slice(Nq + Nv, C)
     tr = [w.t().contiguous().to(DEV) for w in (aq, bq, av, bv)]
@@ -472,16 +472,16 @@ def test_lora_bwd_rows(pkg, n, H, Nq, Nv):
 @pytest.mark.parametrize("n,H,Nq,Nv", [(300, 1536, 1536, 256), (1, 1536, 1536, 256),
                                        (77, 256, 256, 128), (4100, 896, 896, 128),
                                        (33, 3584, 3584, 512)])
-def test_lora_fwd_rows(pkg, n, H, Nq, Nv):
+def test_lora_fwd_rows(pkg, n, H, Nq, Nv, r=16):
     """x = fp16(a A^T), l = fp16(x B^T) for both adapters (engine.py:1088-1093) against fp64 of
     the same roundings."""
-    g = torch.Generator().manual_seed(n + 1)
+    g = torch.Generator().manual_seed(n + 1 + r)
     aq = torch.randn(n, H, generator=g).half()
     av = torch.randn(n, H, generator=g).half()
-    Aq = (torch.randn(16, H, generator=g) * 0.05).half()
-    Av = (torch.randn(16, H, generator=g) * 0.05).half()
-    Bq = (torch.randn(Nq, 16, generator=g) * 0.05).half()
-    Bv = (torch.randn(Nv, 16, generator=g) * 0.05).half()
+    Aq = (torch.randn(r, H, generator=g) * 0.05).half()
+    Av = (torch.randn(r, H, generator=g) * 0.05).half()
+    Bq = (torch.randn(Nq, r, generator=g) * 0.05).half()
+    Bv = (torch.randn(Nv, r, generator=g) * 0.05).half()
     xq, xv, lq, lv = pkg.ops._lora_fwd_rows(aq.to(DEV), av.to(DEV), Aq.to(DEV), Bq.to(DEV),
                                             Av.to(DEV), Bv.to(DEV))
     for a, A, B, x, l in ((aq, Aq, Bq, xq, lq), (av, Av, Bv, xv, lv)):
@@ -494,13 +494,13 @@ def test_lora_fwd_rows(pkg, n, H, Nq, Nv):
 @pytest.mark.parametrize("n,H,Nq,Nv", [(300, 1536, 1536, 256), (1, 1536, 1536, 256),
                                        (129, 256, 256, 128), (4100, 896, 896, 128),
                                        (0, 256, 256, 128)])
-def test_lora_grad(pkg, n, H, Nq, Nv):
+def test_lora_grad(pkg, n, H, Nq, Nv, r=16):
     """dB = s g^T x and dA = dx^T a of both adapters (engine.py:1327, 1329) against fp64 sums of
     the same fp16 operands (fp32 accumulation: relative error ~ 1e-6 of the magnitudes)."""
-    g = torch.Generator().manual_seed(n + 7)
+    g = torch.Generator().manual_seed(n + 7 + r)
     C = Nq + 2 * Nv
     dqkv = torch.randn(n, C, generator=g).half()
-    xs = [torch.randn(n, 16, generator=g).half() for _ in range(4)]  # x_q, x_v, dx_q, dx_v
+    xs = [torch.randn(n, r, generator=g).half() for _ in range(4)]  # x_q, x_v, dx_q, dx_v
     aq = torch.randn(n, H, generator=g).half()
     av = torch.randn(n, H, generator=g).half()
     s = 2.0
@@ -515,3 +515,15 @@ def test_lora_grad(pkg, n, H, Nq, Nv):
         assert got.dtype == torch.float32 and got.shape == want.shape
         scale = max(1.0, math.sqrt(max(n, 1))) * 8
         close(got, want, 1e-5 * scale)
+
+
+
+@pytest.mark.parametrize("r", [8, 32, 64])
+@pytest.mark.parametrize("n,H,Nq,Nv", [(300, 1536, 1536, 256), (33, 896, 896, 128)])
+def test_lora_other_ranks(pkg, n, H, Nq, Nv, r):
+    """The three LoRA kernels at ranks 8, 32 and 64 (PEFT's other common choices): the same
+    fp64 checks as at rank 16."""
+    print(f"lora rank {r} n={n} H={H}", flush=True)
+    test_lora_fwd_rows(pkg, n, H, Nq, Nv, r)
+    test_lora_bwd_rows(pkg, n, H, Nq, Nv, r)
+    test_lora_grad(pkg, n, H, Nq, Nv, r)

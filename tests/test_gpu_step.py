@@ -51,10 +51,11 @@ def test_varlen_attention_matches_sdpa(pkg):
         start += length
 
 
-def _tiny(pkg, layers=2, dropout=0.05):
-    cfg = pkg.engine.Qwen2Config(hidden_size=256, intermediate_size=640, num_hidden_layers=layers,
-                                 num_attention_heads=4, num_key_value_heads=2, head_dim=64,
-                                 vocab_size=3000, lora_dropout=dropout)
+def _tiny(pkg, layers=2, dropout=0.05, H=256, HQ=4, HKV=2, D=64, r=16):
+    cfg = pkg.engine.Qwen2Config(hidden_size=H, intermediate_size=640, num_hidden_layers=layers,
+                                 num_attention_heads=HQ, num_key_value_heads=HKV, head_dim=D,
+                                 vocab_size=3000, lora_dropout=dropout, lora_r=r,
+                                 lora_alpha=2 * r)
     return pkg.engine.random_qwen2(cfg, DEV, seed=3)
 
 
@@ -67,6 +68,35 @@ def _batch(lengths, vocab, prompt=3, seed=0):
     labels = torch.where(mask.bool(), ids, -100)
     labels[:, :prompt] = -100
     return ids, mask, labels
+
+
+@pytest.mark.parametrize("H,HQ,HKV,D,r", [(896, 14, 2, 64, 8), (512, 8, 1, 64, 32),
+                                          (640, 10, 2, 64, 16), (512, 4, 1, 128, 64)])
+def test_step_other_model_shapes(pkg, H, HQ, HKV, D, r):
+    """Other Qwen2 family shapes through the whole step against the CPU oracle: 7 q heads per kv
+    head with D 64 (Qwen2.5-0.5B: 14/2), 8 (3B, 72B), 5 (14B, 32B), D 128 with 4, and LoRA ranks
+    8, 32, 64 beside 16."""
+    print(f"step H={H} HQ={HQ} HKV={HKV} D={D} r={r}", flush=True)
+    model = _tiny(pkg, H=H, HQ=HQ, HKV=HKV, D=D, r=r)
+    model.keep_all = None
+    cpu = OS.CpuQwen2(model)
+    lengths = [17, 60, 33, 5]
+    ids, mask, labels = _batch(lengths, model.cfg.vocab_size)
+    denom = float((labels[:, 1:] != -100).sum())
+    torch.cuda.manual_seed(99)
+    gen = model.dropout.gen
+    seed, offset = gen.initial_seed(), gen.get_offset()
+    loss, _, _ = model.step(ids.to(DEV), mask.to(DEV), labels.to(DEV), denom)
+    loss.backward()
+    torch.cuda.synchronize()
+    ref, _ = OS.forward_loss(cpu, ids, mask, labels, denom, drop_seed=seed, drop_offset=offset,
+                             drop_G=model.dropout.max_blocks * 256, p=model.dropout_p, vec=4)
+    ref.backward()
+    assert abs(loss.item() - ref.item()) <= 2e-3 * abs(ref.item())
+    for g_gpu, leaf in zip(model.parameters(), cpu.lora_leaves()):
+        ga, gb = g_gpu.grad.detach().cpu().double(), leaf.grad.double()
+        rel = (ga - gb).norm() / gb.norm().clamp_min(1e-30)
+        assert rel < 2e-2, rel.item()
 
 
 @pytest.mark.parametrize("lengths,keep_all", [([17, 60, 33, 5], False), ([4], False),

@@ -148,3 +148,38 @@ def test_row_losses(pkg):
     means, counts = pkg.trainer.row_losses(packed, stats, b["labels"])
     assert counts == [3, 1]
     assert means == pytest.approx([4 / 3, 2.0])  # row 0 holds tokens 0-3, row 1 4-5 (T = 4)
+
+
+def _fake_peft(r=16, HQ=12, HKV=2, D=128, H=1536):
+    """The attribute paths engine.from_peft reads before it touches any weight (CPU tensors)."""
+    NS = types.SimpleNamespace
+
+    def proj(lora):
+        m = NS(base_layer=NS(weight=None, bias=None))
+        if lora:
+            m.lora_A = {"default": NS(weight=torch.zeros(r, H))}
+            m.lora_B = {"default": NS(weight=torch.zeros(HQ * D, r))}
+            m.scaling = {"default": 2.0}
+            m.lora_dropout = {"default": NS(p=0.05)}
+            m.active_adapter = ["default"]
+        return m
+
+    layer = NS(self_attn=NS(q_proj=proj(True), k_proj=proj(False), v_proj=proj(True),
+                            o_proj=proj(False)),
+               mlp=NS(gate_proj=proj(False), up_proj=proj(False), down_proj=proj(False)),
+               input_layernorm=NS(weight=None, variance_epsilon=1e-6),
+               post_attention_layernorm=NS(weight=None, variance_epsilon=1e-6))
+    config = NS(hidden_size=H, intermediate_size=4 * H, num_attention_heads=HQ,
+                num_key_value_heads=HKV, head_dim=D, vocab_size=1000, rope_theta=1e6)
+    causal = NS(model=NS(layers=[layer]), config=config)
+    return NS(get_base_model=lambda: causal)
+
+
+@pytest.mark.parametrize("kw", [{"r": 12}, {"r": 128}, {"HQ": 18, "HKV": 2},
+                                {"HQ": 12, "HKV": 5}, {"D": 96}])
+def test_from_peft_rejects_what_the_kernels_do_not_take(pkg, kw):
+    """A LoRA rank outside 8/16/32/64, more than 8 q heads per kv head, head counts that do not
+    divide, head_dim other than 64/128: UnsupportedModel (install then leaves the trainer on
+    its own compute_loss) before any weight is read."""
+    with pytest.raises(pkg.engine.UnsupportedModel):
+        pkg.engine.from_peft(_fake_peft(**kw))
