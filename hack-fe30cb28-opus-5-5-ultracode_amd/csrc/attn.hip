@@ -15,8 +15,9 @@
 //    and l ^ 32 share a query and combine their maxima with one shuffle), and O^T = V^T P^T
 //    keeps the lane <-> query ownership, so rescaling O is a per-lane multiply.
 //  * dK/dV compute S = Q K^T (lane <-> key), dV^T = dO^T P and dK^T = Q^T dS.
-// A product that contracts over tokens needs a token-contiguous operand: V^T (forward), K^T
-// (dQ), Q^T and dO^T (dK/dV) are transposed while being staged into LDS. The P/dS operand comes
+// A product that contracts over tokens needs a token-contiguous operand: the forward stages V
+// row-major and reads V^T with ds_read_b64_tr_b16 (tr_operand); K^T (dQ), Q^T and dO^T (dK/dV)
+// are transposed while being staged into LDS. The P/dS operand comes
 // straight from the accumulator registers, whose rows within each 16-row group are in the
 // order 0-3, 8-11, 4-7, 12-15 for the lower/upper half-wave; the transposed tiles store their
 // tokens in that same slot order (perm16: swap rows 4-7 with 8-11), so no register shuffles
@@ -30,8 +31,11 @@
 // prefetch), so their latency overlaps the arithmetic. dK/dV come out per q head
 // ([n, HQ, D]); the caller sums each group (the RoPE backward does, as the reference sums the
 // repeated kv heads). The log-sum-exp of the forward (natural log, fp32 [HQ, n]) and
-// delta = rowsum(dO * O) (fp32 [HQ, n], written by the dQ kernel) feed the dK/dV kernel.
+// delta = rowsum(dO * O) (fp32 [HQ, n], written by attn_delta_kernel) feed the dQ and the dK/dV
+// kernels, which run at the same time on two streams.
 #include "common.h"
+
+#include <mutex>
 
 namespace qlora {
 namespace attn {
@@ -99,6 +103,36 @@ __device__ __forceinline__ int tr_off(int d, int slot) {
   return d * S + (((slot >> 3) ^ sw) << 3) + (slot & 7);
 }
 
+// [rows][D] tile read transposed by ds_read_b64_tr_b16 (tr_operand): a half-wave reads 4
+// consecutive rows (the first a multiple of 4) x 4 aligned chunks, which this swizzle spreads
+// over distinct banks; 16-byte row stores (16 threads a row) stay conflict-free too.
+template <int D>
+__device__ __forceinline__ int tt_off(int row, int chunk) {
+  const int j = D == 128 ? row : row >> 1;  // rows sharing the 64 banks: 1 (D = 128) or 2
+  const int sw = D == 128 ? (((j & 3) << 2) | ((j >> 2) & 3)) : (((j & 1) << 2) | ((j >> 1) & 3));
+  return row * D + ((chunk ^ sw) << 3);
+}
+
+typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) short4_t lds_short4_t;
+
+// The MFMA A operand T[d][8 token slots] of a tt_off tile (T = the tile transposed): lane l
+// supplies d = d0 + l % 32 and tokens k0 + 4 (l / 32) + {0..3, 8..11}, the slot order of an
+// accumulator's rows (acc_row). ds_read_b64_tr_b16 gives lane i of each 16-lane group element
+// i % 4 of the 4 halves read by lane 4 j + i / 4 of the group, as its element j; so lane p of the
+// group reads row (first token) + p / 4, columns (group's first d) + 4 (p % 4) .. + 3.
+template <int D>
+__device__ __forceinline__ half8_t tr_operand(const uint16_t* t, int k0, int d0, int lane) {
+  const int p = lane & 15;
+  const int row = k0 + 4 * (lane >> 5) + (p >> 2);
+  const int col = d0 + 16 * ((lane >> 4) & 1) + 4 * (p & 3);
+  const int o0 = tt_off<D>(row, col >> 3) + (col & 7);
+  const int o1 = tt_off<D>(row + 8, col >> 3) + (col & 7);
+  const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)(t + o0));
+  const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)(t + o1));
+  return __builtin_bit_cast(half8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
 template <int D>
 __device__ __forceinline__ half8_t ld_rm(const uint16_t* t, int row, int chunk) {
   return *reinterpret_cast<const half8_t*>(t + rm_off<D>(row, chunk));
@@ -120,8 +154,9 @@ __device__ __forceinline__ half8_t ld_g(const uint16_t* p) {
 //
 // Offsets are bytes from the resource base: row r at r * stride_b, chunk c (8 halves) at 16 c.
 //
-// RowStage: rows [row0, row0 + ROWS) into a [ROWS][D] tile.
-template <int D, int ROWS, int NT>
+// RowStage: rows [row0, row0 + ROWS) into a [ROWS][D] tile (swizzle rm_off, or tt_off for a
+// tile read by tr_operand).
+template <int D, int ROWS, int NT, bool TT = false>
 struct RowStage {
   static constexpr int CPR = D / 8, TOTAL = ROWS * CPR, CNT = (TOTAL + NT - 1) / NT;
   uint4 r[CNT];
@@ -136,7 +171,9 @@ struct RowStage {
 #pragma unroll
     for (int i = 0; i < CNT; ++i) {
       const int id = tid + i * NT;
-      if (id < TOTAL) *reinterpret_cast<uint4*>(tile + rm_off<D>(id / CPR, id % CPR)) = r[i];
+      if (id < TOTAL)
+        *reinterpret_cast<uint4*>(tile + (TT ? tt_off<D>(id / CPR, id % CPR)
+                                             : rm_off<D>(id / CPR, id % CPR))) = r[i];
     }
   }
 };
@@ -252,7 +289,7 @@ template <int D, int G>
 __global__ __launch_bounds__(64 * G) void attn_fwd_kernel(Args a) {
   constexpr int KC = D / 16, DT = D / 32, NT = 64 * G;
   __shared__ __align__(16) uint16_t ks[kKB * D];
-  __shared__ __align__(16) uint16_t vt[D * kKB];
+  __shared__ __align__(16) uint16_t vs[kKB * D];
   // blockIdx.x = tile + ntiles (seq KH + kvh), the tile fastest: consecutive workgroups (which
   // the dispatcher deals to the 8 XCDs in turn) take tiles of the same sequence, so every XCD
   // gets a share of each; the longest rows first
@@ -276,7 +313,7 @@ __global__ __launch_bounds__(64 * G) void attn_fwd_kernel(Args a) {
   const rsrc_t vsrc = rows_rsrc(a.v + (int64_t)start * kvs + kvh * D, L, kvs, D);
 
   RowStage<D, kKB, NT> sk;
-  PairStage<D, kKB, NT> sv;
+  RowStage<D, kKB, NT, true> sv;
   sk.load(ksrc, kb0 * kKB, kvs_b, tid);
   sv.load(vsrc, kb0 * kKB, kvs_b, tid);
 
@@ -290,7 +327,7 @@ __global__ __launch_bounds__(64 * G) void attn_fwd_kernel(Args a) {
   const float c = a.scale * kLog2e;
   const int lim = min(qi, L - 1);  // the last key this query attends to
 
-  // one key block from the staged tiles (ks, vt)
+  // one key block from the staged tiles (ks, vs)
   auto block = [&](int k0) {
     f32x16 s[2];
     s[0] = s[1] = f32x16{};
@@ -341,8 +378,7 @@ __global__ __launch_bounds__(64 * G) void attn_fwd_kernel(Args a) {
     for (int u = 0; u < DT; ++u) {
       half8_t vop[4];
 #pragma unroll
-      for (int kk = 0; kk < 4; ++kk)
-        vop[kk] = ld_tr<kKB>(vt, 32 * u + (lane & 31), 2 * kk + (lane >> 5));
+      for (int kk = 0; kk < 4; ++kk) vop[kk] = tr_operand<D>(vs, 16 * kk, 32 * u, lane);
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) o[u] = mfma(vop[kk], pb[kk], o[u]);
     }
@@ -351,7 +387,7 @@ __global__ __launch_bounds__(64 * G) void attn_fwd_kernel(Args a) {
   for (int kb = kb0; kb < kb1; ++kb) {
     __syncthreads();
     sk.store(ks, tid);
-    sv.store(vt, nullptr, tid);
+    sv.store(vs, tid);
     __syncthreads();
     // the next block (past the sequence: zeros, not used)
     sk.load(ksrc, (kb + 1) * kKB, kvs_b, tid);
@@ -377,11 +413,50 @@ __global__ __launch_bounds__(64 * G) void attn_fwd_kernel(Args a) {
 }
 
 // ------------------------------------------------------------------------------------------------
-// Backward, dQ (and delta = rowsum(dO * O)): per 32 queries of a q head, over 32-key blocks up
-// to the diagonal: S^T = K Q^T, P = exp(S - lse), dP^T = V dO^T, dS = P (dP - delta),
-// dQ^T += K^T dS^T. grid and block as the forward; block kb + 1 prefetched during block kb.
+// Backward, delta = rowsum(dO * O) per (q head, token), fp32 [HQ, n], read by both the dQ and the
+// dK/dV kernel (which may then run at the same time). Two threads per row: thread `half` sums
+// the products of the 16-byte chunks 2 kk + half (kk = 0 .. D/16 - 1) in order, then the pair's
+// two sums are added.
 // ------------------------------------------------------------------------------------------------
-template <int D, int G>
+template <int D>
+__global__ __launch_bounds__(256) void attn_delta_kernel(const uint16_t* dout, const uint16_t* o,
+                                                         float* delta, int64_t n, int HQ) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t p = t >> 1;  // h n + token
+  const int half = (int)(t & 1);
+  const bool ok = p < n * HQ;
+  float s = 0.f;
+  if (ok) {
+    const int64_t h = p / n, tok = p - h * n;
+    const uint4* dr = reinterpret_cast<const uint4*>(dout + (tok * HQ + h) * D);
+    const uint4* orow = reinterpret_cast<const uint4*>(o + (tok * HQ + h) * D);
+    uint4 x[D / 16], y[D / 16];
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk) {
+      x[kk] = dr[2 * kk + half];
+      y[kk] = orow[2 * kk + half];
+    }
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk)
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const uint32_t xa = word_of(x[kk], w), ya = word_of(y[kk], w);
+        s += lo_h(xa) * lo_h(ya);
+        s += hi_h(xa) * hi_h(ya);
+      }
+  }
+  const float tot = s + __shfl_xor(s, 1, 64);
+  if (ok && half == 0) delta[p] = tot;
+}
+
+// ------------------------------------------------------------------------------------------------
+// Backward, dQ: per 32 queries of a q head, over 32-key blocks up to the diagonal: S^T = K Q^T,
+// P = exp(S - lse), dP^T = V dO^T, dS = P (dP - delta), dQ^T += K^T dS^T. grid and block as the
+// forward; block kb + 1 prefetched during block kb. OWN_DELTA: the kernel forms delta itself
+// (lanes l and l ^ 32 sum the chunks of attn_delta_kernel's two threads, in its order) and the
+// first chunk writes it for the dK/dV kernel that follows; else it reads attn_delta_kernel's.
+// ------------------------------------------------------------------------------------------------
+template <int D, int G, bool OWN_DELTA>
 __global__ __launch_bounds__(64 * G) void attn_dq_kernel(Args a) {
   constexpr int KC = D / 16, DT = D / 32, NT = 64 * G, KB = kTok;
   __shared__ __align__(16) uint16_t ks[KB * D];
@@ -411,22 +486,29 @@ __global__ __launch_bounds__(64 * G) void attn_dq_kernel(Args a) {
   sk.load(ksrc, kb0 * KB, kvs_b, tid);
   sv.load(vsrc, kb0 * KB, kvs_b, tid);
 
-  // this query's q, dO and O (queries past the sequence read zeros; their dq is not stored)
+  // this query's q and dO (queries past the sequence read zeros; their dq is not stored), its
+  // log-sum-exp and delta (attn_delta_kernel)
   const int64_t hoff = (int64_t)start * qs + h * D;
-  half8_t qr[KC], dr[KC], orow[KC];
+  half8_t qr[KC], dr[KC];
   load_token<D>(rows_rsrc(a.q + hoff, L, qs, D), qi, qs_b, lane, qr);
   load_token<D>(rows_rsrc(a.dout + hoff, L, qs, D), qi, qs_b, lane, dr);
-  load_token<D>(rows_rsrc(a.o + hoff, L, qs, D), qi, qs_b, lane, orow);
   const float lse2 =
       buf_load_f32(make_rsrc(a.lse + (int64_t)h * a.n + start, (uint32_t)L * 4), qi * 4) *
       kLog2e;
-  float dpart = 0.f;
+  float delta;
+  if constexpr (OWN_DELTA) {
+    half8_t orow[KC];
+    load_token<D>(rows_rsrc(a.o + hoff, L, qs, D), qi, qs_b, lane, orow);
+    float dpart = 0.f;
 #pragma unroll
-  for (int kk = 0; kk < KC; ++kk)
+    for (int kk = 0; kk < KC; ++kk)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) dpart += (float)dr[kk][i] * (float)orow[kk][i];
-  const float delta = dpart + __shfl_xor(dpart, 32, 64);
-  if (ch == 0 && qi < L && lane < 32) a.delta[(int64_t)h * a.n + start + qi] = delta;
+      for (int i = 0; i < 8; ++i) dpart += (float)dr[kk][i] * (float)orow[kk][i];
+    delta = dpart + __shfl_xor(dpart, 32, 64);
+    if (ch == 0 && qi < L && lane < 32) a.delta[(int64_t)h * a.n + start + qi] = delta;
+  } else {
+    delta = buf_load_f32(make_rsrc(a.delta + (int64_t)h * a.n + start, (uint32_t)L * 4), qi * 4);
+  }
 
   f32x16 dq[DT];
 #pragma unroll
@@ -685,30 +767,34 @@ int check_common(int32_t nseq, int32_t max_len, int64_t n, int32_t HQ, int32_t K
   return 0;
 }
 
-template <int D, int G, bool DQ>
+// MODE: 0 forward, 1 dQ reading delta, 2 dQ forming delta
+template <int D, int G, int MODE>
 void launch_q(const Args& a, dim3 grid, hipStream_t s) {
-  if constexpr (DQ) hipLaunchKernelGGL((attn_dq_kernel<D, G>), grid, dim3(64 * G), 0, s, a);
+  if constexpr (MODE == 1)
+    hipLaunchKernelGGL((attn_dq_kernel<D, G, false>), grid, dim3(64 * G), 0, s, a);
+  else if constexpr (MODE == 2)
+    hipLaunchKernelGGL((attn_dq_kernel<D, G, true>), grid, dim3(64 * G), 0, s, a);
   else hipLaunchKernelGGL((attn_fwd_kernel<D, G>), grid, dim3(64 * G), 0, s, a);
 }
 
-template <bool DQ, int D>
+template <int MODE, int D>
 void launch_q_g(const Args& a, int G, dim3 grid, hipStream_t s) {
   switch (G) {
-    case 1: launch_q<D, 1, DQ>(a, grid, s); break;
-    case 2: launch_q<D, 2, DQ>(a, grid, s); break;
-    case 3: launch_q<D, 3, DQ>(a, grid, s); break;
-    case 4: launch_q<D, 4, DQ>(a, grid, s); break;
-    case 5: launch_q<D, 5, DQ>(a, grid, s); break;
-    case 6: launch_q<D, 6, DQ>(a, grid, s); break;
-    case 7: launch_q<D, 7, DQ>(a, grid, s); break;
-    default: launch_q<D, 8, DQ>(a, grid, s); break;
+    case 1: launch_q<D, 1, MODE>(a, grid, s); break;
+    case 2: launch_q<D, 2, MODE>(a, grid, s); break;
+    case 3: launch_q<D, 3, MODE>(a, grid, s); break;
+    case 4: launch_q<D, 4, MODE>(a, grid, s); break;
+    case 5: launch_q<D, 5, MODE>(a, grid, s); break;
+    case 6: launch_q<D, 6, MODE>(a, grid, s); break;
+    case 7: launch_q<D, 7, MODE>(a, grid, s); break;
+    default: launch_q<D, 8, MODE>(a, grid, s); break;
   }
 }
 
-template <bool DQ>
+template <int MODE>
 void launch_q_any(const Args& a, int D, int G, dim3 grid, hipStream_t s) {
-  if (D == 128) launch_q_g<DQ, 128>(a, G, grid, s);
-  else launch_q_g<DQ, 64>(a, G, grid, s);
+  if (D == 128) launch_q_g<MODE, 128>(a, G, grid, s);
+  else launch_q_g<MODE, 64>(a, G, grid, s);
 }
 
 // Chunks of the split forms: chunk_keys a positive multiple of 64, at most kMaxChunks chunks.
@@ -753,25 +839,96 @@ int run_fwd(Args a, int32_t nseq, int32_t max_len, int D, int64_t nch, hipStream
   a.ntiles = (int)qlora_cdiv(max_len, kTok);
   unsigned gx;
   if (int rc = grid_of(a.ntiles, (int64_t)nseq * a.KH, &gx)) return rc;
-  launch_q_any<false>(a, D, a.HQ / a.KH, dim3(gx, 1, (unsigned)nch), s);
+  launch_q_any<0>(a, D, a.HQ / a.KH, dim3(gx, 1, (unsigned)nch), s);
   if (int rc = qlora_launch_status()) return rc;
   return nch > 1 ? launch_merge<true>(a, D, nseq, nch, s) : 0;
 }
 
+// The second stream of each device on which the dK/dV kernel runs while the dQ kernel runs on
+// the caller's stream (both only read what the delta kernel and the forward wrote): neither
+// launch alone fills the GPU when the batch holds few sequences. Fork and join are event
+// waits, so the caller's stream orders everything after the backward as before. Created on
+// first use (default priority), kept for the process.
+struct SideStream {
+  hipStream_t stream = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+};
+std::mutex g_side_mu;
+SideStream g_side[64];
+
+int side_stream(SideStream** out) {
+  int dev = 0;
+  if (hipError_t e = hipGetDevice(&dev)) return (int)e;
+  if (dev < 0 || dev >= 64) return (int)hipErrorInvalidDevice;
+  SideStream& ss = g_side[dev];
+  if (ss.stream == nullptr) {
+    if (hipError_t e = hipStreamCreateWithFlags(&ss.stream, hipStreamNonBlocking)) return (int)e;
+    if (hipError_t e = hipEventCreateWithFlags(&ss.fork, hipEventDisableTiming)) return (int)e;
+    if (hipError_t e = hipEventCreateWithFlags(&ss.join, hipEventDisableTiming)) return (int)e;
+  }
+  *out = &ss;
+  return 0;
+}
+
+// Concurrent dQ and dK/dV pay when the dQ launch is long but leaves most of the GPU idle (few
+// long sequences: at most ~1.25 workgroups per CU of 256, key ranges of 512 and more); a full
+// launch gains nothing from the second stream and pays the delta kernel and the fork.
+bool bwd_concurrent(int32_t max_len, unsigned dq_groups) {
+  return max_len >= 512 && dq_groups <= 320;
+}
+
+void launch_dkdv(const Args& b, int D, unsigned gkv, hipStream_t s) {
+  if (D == 128)
+    hipLaunchKernelGGL(attn_dkdv_kernel<128>, dim3(gkv), dim3(64 * kKeyWaves), 0, s, b);
+  else
+    hipLaunchKernelGGL(attn_dkdv_kernel<64>, dim3(gkv), dim3(64 * kKeyWaves), 0, s, b);
+}
+
 int run_bwd(Args a, int32_t nseq, int32_t max_len, int D, int64_t nch, hipStream_t s) {
+  Args b = a;  // dK/dV
+  b.ntiles = (int)qlora_cdiv(max_len, kTok * kKeyWaves);
+  unsigned gkv;
+  if (int rc = grid_of(b.ntiles, (int64_t)nseq * a.HQ, &gkv)) return rc;
   a.ntiles = (int)qlora_cdiv(max_len, kTok);
+  const int W = a.HQ / a.KH;
   unsigned gx;
   if (int rc = grid_of(a.ntiles, (int64_t)nseq * a.KH, &gx)) return rc;
-  launch_q_any<true>(a, D, a.HQ / a.KH, dim3(gx, 1, (unsigned)nch), s);
-  if (int rc = qlora_launch_status()) return rc;
-  if (nch > 1) {
-    if (int rc = launch_merge<false>(a, D, nseq, nch, s)) return rc;
+  if (!bwd_concurrent(max_len, gx * (unsigned)nch)) {  // dQ (writing delta), then dK/dV
+    launch_q_any<2>(a, D, W, dim3(gx, 1, (unsigned)nch), s);
+    if (int rc = qlora_launch_status()) return rc;
+    if (nch > 1) {
+      if (int rc = launch_merge<false>(a, D, nseq, nch, s)) return rc;
+    }
+    launch_dkdv(b, D, gkv, s);
+    return qlora_launch_status();
   }
-  a.ntiles = (int)qlora_cdiv(max_len, kTok * kKeyWaves);
-  if (int rc = grid_of(a.ntiles, (int64_t)nseq * a.HQ, &gx)) return rc;
-  if (D == 128) hipLaunchKernelGGL(attn_dkdv_kernel<128>, dim3(gx), dim3(64 * kKeyWaves), 0, s, a);
-  else hipLaunchKernelGGL(attn_dkdv_kernel<64>, dim3(gx), dim3(64 * kKeyWaves), 0, s, a);
-  return qlora_launch_status();
+  const int64_t rows = a.n * a.HQ;
+  QLORA_CHECK_ARG(qlora_cdiv(2 * rows, 256) < (1ll << 31));
+  const dim3 dgrid((unsigned)qlora_cdiv(2 * rows, 256));
+  if (D == 128)
+    hipLaunchKernelGGL(attn_delta_kernel<128>, dgrid, dim3(256), 0, s, a.dout, a.o, a.delta,
+                       a.n, a.HQ);
+  else
+    hipLaunchKernelGGL(attn_delta_kernel<64>, dgrid, dim3(256), 0, s, a.dout, a.o, a.delta, a.n,
+                       a.HQ);
+  if (int rc = qlora_launch_status()) return rc;
+
+  std::lock_guard<std::mutex> lock(g_side_mu);
+  SideStream* ss;
+  if (int rc = side_stream(&ss)) return rc;
+  if (hipError_t e = hipEventRecord(ss->fork, s)) return (int)e;
+  if (hipError_t e = hipStreamWaitEvent(ss->stream, ss->fork, 0)) return (int)e;
+  launch_dkdv(b, D, gkv, ss->stream);
+  int rc = qlora_launch_status();
+  if (rc == 0) {
+    launch_q_any<1>(a, D, W, dim3(gx, 1, (unsigned)nch), s);
+    rc = qlora_launch_status();
+  }
+  if (rc == 0 && nch > 1) rc = launch_merge<false>(a, D, nseq, nch, s);
+  // join whatever was launched, also after an error
+  if (hipError_t e = hipEventRecord(ss->join, ss->stream)) return rc ? rc : (int)e;
+  if (hipError_t e = hipStreamWaitEvent(s, ss->join, 0)) return rc ? rc : (int)e;
+  return rc;
 }
 
 Args make_args(const void* q, const void* k, const void* v, int64_t n, int32_t HQ, int32_t KH,

@@ -25,21 +25,24 @@ struct DropParams {
 __device__ __forceinline__ uint4 philox4x32_10(uint4 c, uint32_t k0, uint32_t k1) {
   constexpr uint32_t M0 = 0xD2511F53u, M1 = 0xCD9E8D57u;
   constexpr uint32_t W0 = 0x9E3779B9u, W1 = 0xBB67AE85u;
+  // each round's two 32 x 32 -> 64-bit products as one v_mad_u64_u32 apiece (high and low
+  // words together), not a mul_hi and a mul_lo
 #pragma unroll
   for (int r = 0; r < 10; ++r) {
-    const uint32_t hi0 = __umulhi(M0, c.x), lo0 = M0 * c.x;
-    const uint32_t hi1 = __umulhi(M1, c.z), lo1 = M1 * c.z;
-    c = make_uint4(hi1 ^ c.y ^ k0, lo1, hi0 ^ c.w ^ k1, lo0);
+    const uint64_t p0 = (uint64_t)M0 * c.x, p1 = (uint64_t)M1 * c.z;
+    c = make_uint4((uint32_t)(p1 >> 32) ^ c.y ^ k0, (uint32_t)p1,
+                   (uint32_t)(p0 >> 32) ^ c.w ^ k1, (uint32_t)p0);
     k0 += W0;
     k1 += W1;
   }
   return c;
 }
 
+// p_keep >= 1 (p = 0) keeps everything: PyTorch's dropout returns its input unchanged then.
 __device__ __forceinline__ bool keep_word(uint32_t r, float p_keep) {
   const float inv = 2.3283064365386963e-10f;  // 2^-32, exact
   const float u = inv + (float)r * inv;       // exact product: FMA or not, same value
-  return u < p_keep;
+  return u < p_keep || p_keep >= 1.0f;
 }
 
 // The Philox words of the aligned group of four elements that holds element e (4 | e0).

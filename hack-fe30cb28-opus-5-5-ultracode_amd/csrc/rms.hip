@@ -7,7 +7,9 @@
 // holds NV chunks of W consecutive columns), the sums are wavefront reductions (no LDS, no
 // barrier). HBM-bound: per row of H columns the forward moves 4H (x) [+2H delta +4H xsum] + 2H
 // (y) + 2H (yq) + 2H (yv) bytes and the backward 2H (dy) + 2H (tq) + 2H (tv) + 4H (x) [+4H dres]
-// + 4H (dx). The masks are regenerated from (seed, counter) in both directions, never stored.
+// + 4H (dx). The masks come from (seed, counter); the forward may also store them as bits
+// (keep: u8 [n][2][ceil(H / 4)], bit k of byte j of mask m = element 4 j + k kept, m = 0 for
+// q, 1 for v) for the backward to read instead of drawing them again.
 #include "philox.h"
 
 #include <type_traits>
@@ -31,6 +33,7 @@ struct RmsFwdArgs {
   uint64_t ctr_q, ctr_v;
   DropParams drop;
   int w_half;
+  uint8_t* keep;          // u8 [n][2][ceil(H / 4)] keep bits (written when dropping) or null
 };
 
 struct RmsBwdArgs {
@@ -49,7 +52,11 @@ struct RmsBwdArgs {
   uint64_t ctr_q, ctr_v;
   DropParams drop;
   int w_half;
+  const uint8_t* keep;  // keep bits stored by the forward, or null: draw them again
 };
+
+// Bytes of one mask of one row in the keep-bit layout.
+__host__ __device__ __forceinline__ int64_t keep_row_bytes(int64_t H) { return (H + 3) / 4; }
 
 template <int W>
 __device__ __forceinline__ void load_f32(const float* p, float (&v)[W]) {
@@ -140,6 +147,7 @@ __global__ __launch_bounds__(kWave* kRowsPerBlock) void rms_fwd_kernel(RmsFwdArg
     for (int k = 0; k < W; ++k) y[k] = wv[k] * (x[i][k] * rstd);
     if (a.y) store_h<W>(a.y + base + c * W, y);
     const uint64_t e0 = tok_e + (uint64_t)(c * W);
+    uint8_t* kr = W == 4 && a.keep ? a.keep + row * 2 * keep_row_bytes(a.H) + c : nullptr;
     if (a.yq) {
       DropParams d = a.drop;
       d.ctr = a.ctr_q;
@@ -148,6 +156,7 @@ __global__ __launch_bounds__(kWave* kRowsPerBlock) void rms_fwd_kernel(RmsFwdArg
 #pragma unroll
       for (int k = 0; k < W; ++k) o[k] = (keep >> k) & 1 ? y[k] * a.keep_scale : 0.f;
       store_h<W>(a.yq + base + c * W, o);
+      if (kr) kr[0] = (uint8_t)keep;
     }
     if (a.yv) {
       DropParams d = a.drop;
@@ -157,6 +166,7 @@ __global__ __launch_bounds__(kWave* kRowsPerBlock) void rms_fwd_kernel(RmsFwdArg
 #pragma unroll
       for (int k = 0; k < W; ++k) o[k] = (keep >> k) & 1 ? y[k] * a.keep_scale : 0.f;
       store_h<W>(a.yv + base + c * W, o);
+      if (kr) kr[keep_row_bytes(a.H)] = (uint8_t)keep;
     }
   }
 }
@@ -181,10 +191,11 @@ __global__ __launch_bounds__(kWave* kRowsPerBlock) void rms_bwd_kernel(RmsBwdArg
     float dy[W];
     load_h<W>(a.dy + row * a.dy_stride + c * W, dy);
     const uint64_t e0 = tok_e + (uint64_t)(c * W);
+    const uint8_t* kr = W == 4 && a.keep ? a.keep + row * 2 * keep_row_bytes(a.H) + c : nullptr;
     if (a.tq) {
       DropParams d = a.drop;
       d.ctr = a.ctr_q;
-      const uint32_t keep = keep_bits<W>(d, e0);
+      const uint32_t keep = kr ? kr[0] : keep_bits<W>(d, e0);
       float t[W];
       load_h<W>(a.tq + base + c * W, t);
 #pragma unroll
@@ -193,7 +204,7 @@ __global__ __launch_bounds__(kWave* kRowsPerBlock) void rms_bwd_kernel(RmsBwdArg
     if (a.tv) {
       DropParams d = a.drop;
       d.ctr = a.ctr_v;
-      const uint32_t keep = keep_bits<W>(d, e0);
+      const uint32_t keep = kr ? kr[keep_row_bytes(a.H)] : keep_bits<W>(d, e0);
       float t[W];
       load_h<W>(a.tv + base + c * W, t);
 #pragma unroll
@@ -267,9 +278,13 @@ __device__ __forceinline__ void load_w4(const void* w, int w_half, int lane, flo
 template <int NV, bool DELTA, bool DROP>
 __global__ __launch_bounds__(kWave* kRowsPerBlock) void rms_fwd4_kernel(RmsFwdArgs a) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  // wave-uniform row: its token index and rstd go through scalar loads, which the vector
+  // loads' counter does not hold up
+  const int64_t row =
+      (int64_t)blockIdx.x * kRowsPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (row >= a.n) return;
   const int64_t base = row * a.H;
+  const uint32_t tok_e = DROP ? (uint32_t)a.tok[row] * (uint32_t)a.H : 0u;
   float4 x[NV];
   uint2 dr[NV];
 #pragma unroll
@@ -280,7 +295,30 @@ __global__ __launch_bounds__(kWave* kRowsPerBlock) void rms_fwd4_kernel(RmsFwdAr
   }
   float4 wv[NV];
   load_w4<NV>(a.w, a.w_half, lane, wv);
-  const uint32_t tok_e = DROP ? (uint32_t)a.tok[row] * (uint32_t)a.H : 0u;
+  uint32_t kq[NV], kv[NV];
+  if constexpr (DROP) {  // the masks, while the loads are in flight (p = 0: all kept)
+    const uint32_t G32 = (uint32_t)a.drop.G;
+    const int vs = a.drop.vec == 8 ? 3 : 2;
+    const bool all = a.drop.p_keep >= 1.0f;
+    DropParams dq = a.drop, dv = a.drop;
+    dq.ctr = a.ctr_q;
+    dv.ctr = a.ctr_v;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const uint32_t e0 = tok_e + 4u * (uint32_t)(lane + 64 * i);
+      kq[i] = !a.yq ? 0u : all ? 0xFu : drop_keep4_u32(dq, e0, G32, vs);
+      kv[i] = !a.yv ? 0u : all ? 0xFu : drop_keep4_u32(dv, e0, G32, vs);
+    }
+    if (a.keep) {
+      const int64_t kb = a.H / 4;
+      uint8_t* kr = a.keep + row * 2 * kb;
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        if (a.yq) kr[lane + 64 * i] = (uint8_t)kq[i];
+        if (a.yv) kr[kb + lane + 64 * i] = (uint8_t)kv[i];
+      }
+    }
+  }
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
@@ -307,17 +345,12 @@ __global__ __launch_bounds__(kWave* kRowsPerBlock) void rms_fwd4_kernel(RmsFwdAr
                                  wv[i].z * (x[i].z * rstd), wv[i].w * (x[i].w * rstd));
     if (a.y) *reinterpret_cast<uint2*>(a.y + off) = pack4(y.x, y.y, y.z, y.w);
     if constexpr (DROP) {
-      const uint32_t e0 = tok_e + 4u * (uint32_t)(lane + 64 * i);
-      const uint32_t G32 = (uint32_t)a.drop.G;
-      const int vs = a.drop.vec == 8 ? 3 : 2;
       uint16_t* outs[2] = {a.yq, a.yv};
-      const uint64_t ctrs[2] = {a.ctr_q, a.ctr_v};
+      const uint32_t keeps[2] = {kq[i], kv[i]};
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         if (outs[t] == nullptr) continue;
-        DropParams d = a.drop;
-        d.ctr = ctrs[t];
-        const uint32_t keep = drop_keep4_u32(d, e0, G32, vs);
+        const uint32_t keep = keeps[t];
         float o[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) o[k] = (keep >> k) & 1 ? comp(y, k) * a.keep_scale : 0.f;
@@ -330,9 +363,11 @@ __global__ __launch_bounds__(kWave* kRowsPerBlock) void rms_fwd4_kernel(RmsFwdAr
 template <int NV, bool DROP, bool RES>
 __global__ __launch_bounds__(kWave* kRowsPerBlock) void rms_bwd4_kernel(RmsBwdArgs a) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  const int64_t row =  // wave-uniform, as the forward
+      (int64_t)blockIdx.x * kRowsPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (row >= a.n) return;
   const int64_t base = row * a.H;
+  const uint32_t tok_e = DROP && !a.keep ? (uint32_t)a.tok[row] * (uint32_t)a.H : 0u;
   uint2 dyr[NV], tqr[NV], tvr[NV];
   float4 x[NV], r[NV];
 #pragma unroll
@@ -350,18 +385,26 @@ __global__ __launch_bounds__(kWave* kRowsPerBlock) void rms_bwd4_kernel(RmsBwdAr
   load_w4<NV>(a.w, a.w_half, lane, wv);
   const float rstd = a.rstd[row];
   uint32_t kq[NV], kv[NV];
-  if constexpr (DROP) {  // the masks, while the loads are in flight
-    const uint32_t tok_e = (uint32_t)a.tok[row] * (uint32_t)a.H;
+  if (DROP && a.keep) {  // the forward's masks
+    const int64_t kb = a.H / 4;
+    const uint8_t* kr = a.keep + row * 2 * kb;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      kq[i] = kr[lane + 64 * i];
+      kv[i] = kr[kb + lane + 64 * i];
+    }
+  } else if constexpr (DROP) {  // the masks, while the loads are in flight (p = 0: all kept)
     const uint32_t G32 = (uint32_t)a.drop.G;
     const int vs = a.drop.vec == 8 ? 3 : 2;
+    const bool all = a.drop.p_keep >= 1.0f;
     DropParams dq = a.drop, dv = a.drop;
     dq.ctr = a.ctr_q;
     dv.ctr = a.ctr_v;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const uint32_t e0 = tok_e + 4u * (uint32_t)(lane + 64 * i);
-      kq[i] = drop_keep4_u32(dq, e0, G32, vs);
-      kv[i] = drop_keep4_u32(dv, e0, G32, vs);
+      kq[i] = all ? 0xFu : drop_keep4_u32(dq, e0, G32, vs);
+      kv[i] = all ? 0xFu : drop_keep4_u32(dv, e0, G32, vs);
     }
   }
   float g[NV][4], xh[NV][4];
@@ -399,6 +442,23 @@ __global__ __launch_bounds__(kWave* kRowsPerBlock) void rms_bwd4_kernel(RmsBwdAr
     *reinterpret_cast<float4*>(a.dx + off) = make_float4(dx[0], dx[1], dx[2], dx[3]);
     if (a.dx16) *reinterpret_cast<uint2*>(a.dx16 + off) = pack4(dx[0], dx[1], dx[2], dx[3]);
   }
+}
+
+// Keep bits of the rows [n, H] in the keep-bit layout, element by element (the forward's
+// one-column path, which holds single elements per lane). One thread per byte of each mask.
+__global__ void rms_keep_bits_kernel(uint8_t* keep, const int64_t* tok, int64_t n, int64_t H,
+                                     DropParams d, uint64_t ctr_q, uint64_t ctr_v, int has_q,
+                                     int has_v) {
+  const int64_t kb = keep_row_bytes(H);
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // (row, mask, byte)
+  if (i >= n * 2 * kb) return;
+  const int64_t row = i / (2 * kb), m = (i / kb) % 2, j = i % kb;
+  if (!(m == 0 ? has_q : has_v)) return;
+  d.ctr = m == 0 ? ctr_q : ctr_v;
+  const uint64_t e = (uint64_t)tok[row] * (uint64_t)H + 4 * j;
+  uint32_t bits = 0;
+  for (int k = 0; k < 4 && 4 * j + k < H; ++k) bits |= (uint32_t)drop_keep(d, e + k) << k;
+  keep[i] = (uint8_t)bits;
 }
 
 __global__ void dropout_keep_kernel(int8_t* out, int64_t nelem, DropParams d) {
@@ -514,7 +574,7 @@ QLORA_API int qlora_rms_fwd(const float* x, const void* delta, const void* w, in
                             const int64_t* tok, int64_t n, int64_t H, float eps, float p_keep,
                             float keep_scale, int64_t seed, int64_t ctr_q, int64_t ctr_v,
                             int64_t G, int32_t has_delta, int32_t write_y, int32_t drop_q,
-                            int32_t drop_v, int32_t vec, void* stream) {
+                            int32_t drop_v, int32_t vec, uint8_t* keep, void* stream) {
   QLORA_CHECK_ARG(n >= 0 && H > 0);
   if (n == 0) return 0;
   QLORA_CHECK_ARG(x && w && rstd);
@@ -529,6 +589,7 @@ QLORA_API int qlora_rms_fwd(const float* x, const void* delta, const void* w, in
                drop_v ? static_cast<uint16_t*>(yv) : nullptr, rstd,
                (drop_q || drop_v) ? tok : nullptr, n, H, eps, keep_scale, (uint64_t)ctr_q,
                (uint64_t)ctr_v, make_drop(seed, G, p_keep, vec), w_half};
+  a.keep = drop_q || drop_v ? keep : nullptr;
   const bool v4 = H % 4 == 0 && aligned(x, 16) && aligned(w, w_half ? 8 : 16) &&
                   (!a.delta || aligned(delta, 8)) && (!a.xsum || aligned(xsum, 16)) &&
                   (!a.y || aligned(y, 8)) && (!a.yq || aligned(yq, 8)) &&
@@ -546,6 +607,14 @@ QLORA_API int qlora_rms_fwd(const float* x, const void* delta, const void* w, in
     launch_nv<FwdK, 4>(nv, grid, (hipStream_t)stream, a);
   } else {
     launch_nv<FwdK, 1>(nv, grid, (hipStream_t)stream, a);
+    if (a.keep) {  // the one-column kernel holds single elements: the bits in a pass of their own
+      if (int rc = qlora_launch_status()) return rc;
+      const int64_t total = n * 2 * keep_row_bytes(H);
+      QLORA_CHECK_ARG(qlora_cdiv(total, 256) < (1ll << 31));
+      hipLaunchKernelGGL(rms_keep_bits_kernel, dim3((unsigned)qlora_cdiv(total, 256)), dim3(256),
+                         0, (hipStream_t)stream, a.keep, tok, n, H, a.drop, a.ctr_q, a.ctr_v,
+                         drop_q ? 1 : 0, drop_v ? 1 : 0);
+    }
   }
   return qlora_launch_status();
 }
@@ -556,7 +625,7 @@ QLORA_API int qlora_rms_bwd(const void* dy, const void* tq, const void* tv, cons
                             int64_t dy_stride, float p_keep, float keep_scale, int64_t seed,
                             int64_t ctr_q, int64_t ctr_v, int64_t G, float grad_scale,
                             int32_t drop_q, int32_t drop_v, int32_t has_res, int32_t vec,
-                            void* stream) {
+                            const uint8_t* keep, void* stream) {
   QLORA_CHECK_ARG(n >= 0 && H > 0);
   if (n == 0) return 0;
   QLORA_CHECK_ARG(dy && x && rstd && w && dx && dy_stride >= H);
@@ -571,6 +640,7 @@ QLORA_API int qlora_rms_bwd(const void* dy, const void* tq, const void* tv, cons
                (drop_q || drop_v) ? tok : nullptr, n, H,
                dy_stride, keep_scale, grad_scale, (uint64_t)ctr_q, (uint64_t)ctr_v,
                make_drop(seed, G, p_keep, vec), w_half};
+  a.keep = drop_q || drop_v ? keep : nullptr;  // the one-column kernel draws the masks again
   const bool v4 = H % 4 == 0 && dy_stride % 4 == 0 && aligned(dy, 8) && aligned(x, 16) &&
                   aligned(w, w_half ? 8 : 16) && aligned(dx, 16) &&
                   (!a.tq || aligned(tq, 8)) && (!a.tv || aligned(tv, 8)) &&

@@ -23,7 +23,7 @@ from . import gemm as G
 from . import linear as L
 from .ops import (NF4Group, NF4Weight, TorchDropout, _attn_bwd, _attn_fwd, _ce, _glu_bwd,
                   _glu_fwd, _lora_bwd_rows, _lora_fwd_rows, _lora_grad, _rms_bwd, _rms_fwd,
-                  _rope_bwd, _rope_fwd)
+                  _rope_bwd, _rope_fwd, keep_bits_shape)
 from .quant import quantize_nf4
 
 
@@ -348,8 +348,17 @@ def _layer_forward(spec, h, packed, lora16, seeds, keep):
     D, HQ = spec.D, spec.HQ
     aq_w, bq_w, av_w, bv_w = lora16
     s = _lora_scale(spec)
-    _, a, aq, av, rstd1 = _rms_fwd(spec, h, spec.ln1, packed, seeds=seeds,
-                                   drop_q=aq_w is not None, drop_v=av_w is not None)
+    # LoRA dropout (engine.py:767-805); p = 0 is the identity (nn.Identity in PEFT), so both
+    # adapters read the normed rows themselves. A kept layer stores the masks as bits for its
+    # backward.
+    drop = packed.dropout is not None
+    drop_q, drop_v = drop and aq_w is not None, drop and av_w is not None
+    kbits = (torch.empty(keep_bits_shape(n, H), device=h.device, dtype=torch.uint8)
+             if keep and (drop_q or drop_v) else None)
+    _, a, aq, av, rstd1 = _rms_fwd(spec, h, spec.ln1, packed, seeds=seeds, drop_q=drop_q,
+                                   drop_v=drop_v, keep=kbits)
+    if not drop:
+        aq, av = (a if aq_w is not None else None), (a if av_w is not None else None)
     qkv = L.nf4_linear(a, spec.qkv, bias=spec.bias_qkv)
     del a
     xq, xv, lq, lv = _lora_fwd_rows(aq, av, aq_w, bq_w, av_w, bv_w)
@@ -362,7 +371,8 @@ def _layer_forward(spec, h, packed, lora16, seeds, keep):
     if keep:
         gu = L.nf4_linear(b, spec.gu)
         return None, dict(rstd1=rstd1, aq=aq, av=av, xq=xq, xv=xv, q=q, k=k, v=v, out=out,
-                          lse=lse, aseed=aseed, aoffset=aoffset, h2=h2, rstd2=rstd2, gu=gu)
+                          lse=lse, aseed=aseed, aoffset=aoffset, h2=h2, rstd2=rstd2, gu=gu,
+                          keep=kbits)
     # gate|up GEMM with the SwiGLU in its epilogue ([gate|up] never stored), then down_proj
     # with the residual add in its epilogue: h3 = h2 + fp16(m W_d^T)
     m = L.nf4_linear_swiglu(b, spec.gu, spec.I)
@@ -466,7 +476,8 @@ class _Layer(torch.autograd.Function):
         if need_dh:
             dh16 = torch.empty((n, H), device=h.device, dtype=torch.float16)
             dh = _rms_bwd(spec, da, h, f["rstd1"], spec.ln1, packed, dres=dh2,
-                          tq=grads["q"][2], tv=grads["v"][2], seeds=seeds, out16=dh16)
+                          tq=grads["q"][2], tv=grads["v"][2], seeds=seeds, out16=dh16,
+                          keep=f["keep"])
             packed.grad16 = (dh, dh16)
         return (dh, None, None, None, grads["q"][0], grads["q"][1], grads["v"][0],
                 grads["v"][1])
@@ -605,10 +616,11 @@ class FusedQwen2:
     def kept_bytes_per_layer(self, n):
         """Device bytes one layer's kept intermediates take for n tokens: the fp16 LoRA inputs
         (2 H), q/k/v and the attention output ((2 HQ + 2 HKV) D), the fp32 residual after
-        attention (H), [gate | up] (2 I), the log-sum-exp and the two rstd."""
+        attention (H), [gate | up] (2 I), the log-sum-exp, the two rstd and the dropout keep
+        bits (2 ceil(H / 4) bytes)."""
         spec = self.layers[0]
         per_token = (2 * spec.H * 2 + (2 * spec.HQ + 2 * spec.HKV) * spec.D * 2 + spec.H * 4
-                     + 2 * spec.I * 2 + spec.HQ * 4 + 2 * 4 + 2 * 16 * 2)
+                     + 2 * spec.I * 2 + spec.HQ * 4 + 2 * 4 + 2 * 16 * 2 + 2 * ((spec.H + 3) // 4))
         return n * per_token
 
     def weight_bytes_per_layer(self):

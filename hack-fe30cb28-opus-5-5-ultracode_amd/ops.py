@@ -337,9 +337,26 @@ def _weight_arg(weight, H, device):
     return int(weight.dtype == torch.float16)
 
 
+def keep_bits_shape(n, H):
+    """Shape of the keep-bit buffer of _rms_fwd / _rms_bwd (uint8): two masks (q, v) per row,
+    bit k of byte j = element 4 j + k kept."""
+    return (n, 2, (H + 3) // 4)
+
+
+def _keep_arg(keep, n, H, dev):
+    if keep is None:
+        return None
+    _need(keep, "keep", torch.uint8, dev)
+    if tuple(keep.shape) != keep_bits_shape(n, H):
+        raise ValueError(f"keep must be uint8 {keep_bits_shape(n, H)}")
+    return _ptr(keep)
+
+
 def _rms_fwd(spec, x, weight, packed, *, delta=None, write_y=True, seeds=(0, 0),
-             drop_q=False, drop_v=False):
-    """[x += delta] + RMSNorm -> (xsum, y fp16, yq, yv, rstd) (engine.py:947-966)."""
+             drop_q=False, drop_v=False, keep=None):
+    """[x += delta] + RMSNorm -> (xsum, y fp16, yq, yv, rstd) (engine.py:947-966). With keep
+    (uint8 keep_bits_shape(n, H)) the dropout masks are also stored there as bits, for
+    _rms_bwd to read instead of drawing them again."""
     _need(x, "x", torch.float32)
     n, H = x.shape
     dev = x.device
@@ -353,6 +370,7 @@ def _rms_fwd(spec, x, weight, packed, *, delta=None, write_y=True, seeds=(0, 0),
     yq = torch.empty((n, H), device=dev, dtype=torch.float16) if drop_q else None
     yv = torch.empty((n, H), device=dev, dtype=torch.float16) if drop_v else None
     rstd = torch.empty((n,), device=dev, dtype=torch.float32)
+    keep_p = _keep_arg(keep, n, H, dev)
     if n:
         tok, p_keep, keep_scale, seed, ctr_q, ctr_v, threads = _dropout_args(packed, x, seeds)
         vec = getattr(packed, "drop_vec", 4)
@@ -365,15 +383,16 @@ def _rms_fwd(spec, x, weight, packed, *, delta=None, write_y=True, seeds=(0, 0),
                   _ptr(rstd), _ptr(tok) if (drop_q or drop_v) else None, n, H,
                   float(spec.eps), p_keep, keep_scale, int(seed), int(ctr_q), int(ctr_v),
                   int(threads), int(delta is not None), int(write_y), int(drop_q), int(drop_v),
-                  int(vec), _stream(dev))
+                  int(vec), keep_p, _stream(dev))
     return xsum, y, yq, yv, rstd
 
 
 def _rms_bwd(spec, dy, x, rstd, weight, packed, *, dres=None, tq=None, tv=None, seeds=(0, 0),
-             grad_scale=1.0, out=None, out16=None):
+             grad_scale=1.0, out=None, out16=None, keep=None):
     """RMSNorm backward with the LoRA-dropout gradients merged (engine.py:969-981). With out16
     (fp16 [n, H]) the kernel also writes fp16(dx) there, the operand the next backward product
-    rounds the gradient to."""
+    rounds the gradient to. keep: the masks _rms_fwd stored for these rows (same packed and
+    seeds), or None to draw them again."""
     _need(x, "x", torch.float32)
     n, H = x.shape
     dev = x.device
@@ -395,6 +414,7 @@ def _rms_bwd(spec, dy, x, rstd, weight, packed, *, dres=None, tq=None, tv=None, 
         _need(out16, "out16", torch.float16, dev)
         if out16.shape != x.shape:
             raise ValueError("out16 must match x")
+    keep_p = _keep_arg(keep, n, H, dev)
     if n:
         tok, p_keep, keep_scale, seed, ctr_q, ctr_v, threads = _dropout_args(packed, x, seeds)
         vec = getattr(packed, "drop_vec", 4)
@@ -405,7 +425,7 @@ def _rms_bwd(spec, dy, x, rstd, weight, packed, *, dres=None, tq=None, tv=None, 
                   _ptr(tok) if (tq is not None or tv is not None) else None, n, H, dy_stride,
                   p_keep, keep_scale, int(seed), int(ctr_q), int(ctr_v), int(threads),
                   float(grad_scale), int(tq is not None), int(tv is not None),
-                  int(dres is not None), int(vec), _stream(dev))
+                  int(dres is not None), int(vec), keep_p, _stream(dev))
     return dx
 
 

@@ -83,12 +83,15 @@ int qlora_dropout_keep(int8_t* out, int64_t nelem, int64_t seed, int64_t ctr, in
  * (engine.py:947-966).
  *   x f32 [n,H]; delta f16 [n,H]; w [H] (f32, or f16 if w_half); xsum f32 [n,H];
  *   y, yq, yv f16 [n,H]; rstd f32 [n]; tok i64 [n]
+ *   keep (may be null) u8 [n][2][ceil(H/4)]: with dropout, the masks stored as bits (bit k of
+ *   byte j of mask m = element 4j+k kept; m = 0 for yq, 1 for yv) for qlora_rms_bwd to read
+ *   instead of drawing them again (no reference counterpart: the reference draws them twice).
  */
 int qlora_rms_fwd(const float* x, const void* delta, const void* w, int32_t w_half, float* xsum,
                   void* y, void* yq, void* yv, float* rstd, const int64_t* tok, int64_t n,
                   int64_t H, float eps, float p_keep, float keep_scale, int64_t seed,
                   int64_t ctr_q, int64_t ctr_v, int64_t G, int32_t has_delta, int32_t write_y,
-                  int32_t drop_q, int32_t drop_v, int32_t vec, void* stream);
+                  int32_t drop_q, int32_t drop_v, int32_t vec, uint8_t* keep, void* stream);
 
 /*
  * RMSNorm backward: g = w * (dy + keep_q * tq * keep_scale + keep_v * tv * keep_scale),
@@ -97,13 +100,15 @@ int qlora_rms_fwd(const float* x, const void* delta, const void* w, int32_t w_ha
  *   dy f16 [n, dy_stride]; tq, tv f16 [n,H]; x f32 [n,H]; rstd f32 [n]; dres, dx f32 [n,H];
  *   dx16 (optional, may be null) f16 [n,H] = fp16(dx), the operand of the next dY W product
  *   (engine.py:1238 and 1301 round the gradient to fp16 before it).
+ *   keep (may be null) u8 [n][2][ceil(H/4)]: the masks qlora_rms_fwd stored for these rows
+ *   (same tok, seed and counters); null: drawn again from (seed, ctr_q, ctr_v).
  */
 int qlora_rms_bwd(const void* dy, const void* tq, const void* tv, const float* x,
                   const float* rstd, const void* w, int32_t w_half, const float* dres, float* dx,
                   void* dx16, const int64_t* tok, int64_t n, int64_t H, int64_t dy_stride, float p_keep,
                   float keep_scale, int64_t seed, int64_t ctr_q, int64_t ctr_v, int64_t G,
                   float grad_scale, int32_t drop_q, int32_t drop_v, int32_t has_res,
-                  int32_t vec, void* stream);
+                  int32_t vec, const uint8_t* keep, void* stream);
 
 /*
  * qkv split + LoRA deltas + rotate-half RoPE. q = f16(rope(qkv_q + s*lq)),
@@ -353,7 +358,9 @@ int qlora_attn_fwd(const void* q, const void* k, const void* v, void* out, float
  * Its backward: dq [n, HQ, D]; dk, dv [n, HQ, D] per q head (the caller sums the HQ/KH heads
  * of each kv head, as the reference's backward through the repeated k/v does); delta is an
  * fp32 [HQ, n] workspace (rowsum(dout * out)). Replaces _attn_bwd engine.py:865-869
- * (aten._efficient_attention_backward).
+ * (aten._efficient_attention_backward). When the dQ launch would leave most of the GPU idle (few
+ * long sequences) the dK/dV kernel runs on a second stream of the library's, forked from and
+ * joined back into `stream` by events: work queued on `stream` afterwards sees every result.
  */
 int qlora_attn_bwd(const void* dout, const void* q, const void* k, const void* v,
                    const void* out, const float* lse, float* delta, void* dq, void* dk, void* dv,

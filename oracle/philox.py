@@ -72,10 +72,14 @@ def _seed_words(seed):
 
 
 def keep_mask(elems, seed, ctr, G, p_keep, vec):
-    """Keep mask (bool) of the given element indices of one dropout call."""
+    """Keep mask (bool) of the given element indices of one dropout call. p_keep >= 1 (p = 0)
+    keeps everything: PyTorch's dropout returns its input unchanged for p = 0 (ATen
+    Dropout.cpp, _dropout_impl), PEFT puts nn.Identity there."""
     e = np.asarray(elems, dtype=np.int64)
     if vec not in (4, 8):
         raise ValueError("vec must be 4 or 8")
+    if np.float32(p_keep) >= np.float32(1.0):
+        return np.ones(e.shape, dtype=bool)
     g = e // vec
     thread = (g % G).astype(np.uint64)
     j = (g // G) * (vec // 4) + (e % vec) // 4

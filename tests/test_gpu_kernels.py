@@ -279,6 +279,53 @@ def test_rms_forward_backward(pkg, n, H, wdtype):
                            tq=tq.to(DEV), tv=tv.to(DEV), seeds=ctrs, grad_scale=0.5, out16=dx16)
     assert torch.equal(dx3, dx)
     assert torch.equal(dx16.view(torch.int16), dx.half().view(torch.int16))
+    # the masks stored as bits by the forward: the oracle's masks, the same outputs, and a
+    # backward that reads them equals the one that draws them again, bit for bit
+    kb = torch.full(pkg.ops.keep_bits_shape(n, H), 0xAA, dtype=torch.uint8, device=DEV)
+    _, y4, yq4, yv4, _ = pkg.ops._rms_fwd(_Spec, x.to(DEV), w.to(DEV), packed,
+                                          delta=delta.to(DEV), seeds=ctrs, drop_q=True,
+                                          drop_v=True, keep=kb)
+    assert torch.equal(y4, y) and torch.equal(yq4, yq) and torch.equal(yv4, yv)
+    masks = [O._keep(tok, H, n, seed, c, G, np.float32(1 - p), 4) for c in ctrs]
+    assert torch.equal(kb.cpu(), _pack_keep(masks, n, H))
+    dx5 = pkg.ops._rms_bwd(_Spec, dy.to(DEV), xsum, rstd, w.to(DEV), packed, dres=dres.to(DEV),
+                           tq=tq.to(DEV), tv=tv.to(DEV), seeds=ctrs, grad_scale=0.5, keep=kb)
+    assert torch.equal(dx5, dx)
+
+
+def _pack_keep(masks, n, H):
+    """bool masks [n, H] (q, v) -> the keep-bit layout u8 [n, 2, ceil(H / 4)]."""
+    kb = (H + 3) // 4
+    out = torch.zeros(n, 2, kb, dtype=torch.int32)
+    for m, mask in enumerate(masks):
+        padded = torch.zeros(n, 4 * kb, dtype=torch.int32)
+        padded[:, :H] = mask.to(torch.int32)
+        q = padded.view(n, kb, 4)
+        out[:, m] = q[..., 0] | (q[..., 1] << 1) | (q[..., 2] << 2) | (q[..., 3] << 3)
+    return out.to(torch.uint8)
+
+
+@pytest.mark.parametrize("n,H", [(37, 1536), (5, 100), (3, 50)])
+def test_rms_dropout_p0_is_identity(pkg, n, H):
+    """p = 0 keeps every element (PyTorch's dropout returns its input; PEFT: nn.Identity), in
+    both directions and in the stored bits."""
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(n, H, generator=g)
+    w = torch.rand(H, generator=g) + 0.5
+    packed = _Packed(0.0)
+    packed.tok = (torch.arange(n) * 5).to(DEV)
+    packed.drop_seed, packed.drop_threads, packed.drop_vec = 3, 4096, 4
+    kb = torch.zeros(pkg.ops.keep_bits_shape(n, H), dtype=torch.uint8, device=DEV)
+    _, y, yq, yv, rstd = pkg.ops._rms_fwd(_Spec, x.to(DEV), w.to(DEV), packed, seeds=(1, 2),
+                                          drop_q=True, drop_v=True, keep=kb)
+    assert torch.equal(yq, y) and torch.equal(yv, y)
+    assert torch.equal(kb.cpu(), _pack_keep([torch.ones(n, H, dtype=torch.bool)] * 2, n, H))
+    dy, tq, tv = (torch.randn(n, H, generator=g).half() for _ in range(3))
+    dx = pkg.ops._rms_bwd(_Spec, dy.to(DEV), x.to(DEV), rstd, w.to(DEV), packed, tq=tq.to(DEV),
+                          tv=tv.to(DEV), seeds=(1, 2))
+    want = O.rms_bwd(dy, x, rstd.cpu(), w, tq=tq, tv=tv, tok=packed.tok.cpu(), p=0.0, seed=3,
+                     ctrs=(1, 2), G=4096, vec=4)
+    close(dx, want, 1e-4)
 
 
 @pytest.mark.parametrize("numel", [4, 1536 * 37, 2560 * 1536])

@@ -87,3 +87,16 @@ def test_generator_offsets_of_reference_run():
         assert adv % 56 == 0
         inc = adv // 56
         assert inc % 4 == 0 and inc in reachable, (adv, inc)
+
+
+def test_p0_keeps_everything():
+    """p = 0: every element kept, whatever the draw (PyTorch's dropout is the identity then);
+    the oracle's normed LoRA inputs equal the normed rows."""
+    assert P.keep_mask(np.arange(1 << 16), 5, 7, 4096, np.float32(1.0), 4).all()
+    import torch
+    from oracle import ops as O
+    x = torch.randn(6, 40, generator=torch.Generator().manual_seed(0))
+    w = torch.rand(40, generator=torch.Generator().manual_seed(1)) + 0.5
+    o = O.rms_fwd(x, w, 1e-6, tok=torch.arange(6), p=0.0, seed=9, ctrs=(3, 4), G=64,
+                  drop_q=True, drop_v=True)
+    assert torch.equal(o[2], o[1]) and torch.equal(o[3], o[1])
