@@ -4,7 +4,8 @@
 //
 // HBM-bound: per 8 output values one 32-bit word of nibbles is read and 16 bytes are written.
 // One launch covers up to kMaxJobs weights (a layer's qkv, o, gate|up and down: 23 MB read and
-// 94 MB written per launch), so the launch cost and the tail of one weight overlap the next.
+// 94 MB written; or the weights of eight layers at once), so the launch cost and the tail of one
+// weight overlap the next.
 // Each thread handles kWPT words spaced a workgroup apart: every load and every 16-byte store instruction of a wavefront covers one contiguous
 // span (256 B in, 1 KiB out). All loads are unconditional (indices clamped, results masked), so
 // a thread's loads issue back to back. The 16 levels and the 256-entry double-quant code sit in
@@ -14,7 +15,7 @@
 namespace qlora {
 
 constexpr int kDequantThreads = 256;
-constexpr int kMaxJobs = 4;
+constexpr int kMaxJobs = 32;  // the batch stays within the 4 KiB of kernel arguments
 
 struct DequantJob {
   NF4Ref w;
@@ -27,6 +28,7 @@ struct DequantBatch {
   int64_t first_tile[kMaxJobs + 1];  // workgroup ranges of the jobs
   int count;
 };
+static_assert(sizeof(DequantBatch) <= 4096, "kernel arguments");
 
 // kWPT words per thread: 8 for large launches, fewer when that would leave CUs without work.
 template <int kWPT>
@@ -35,10 +37,12 @@ __global__ __launch_bounds__(kDequantThreads) void nf4_dequant_kernel(DequantBat
   __shared__ float lut[16];
   __shared__ float c2[256];
   __shared__ float offs[3];
+  // the job of this workgroup: the last one whose first tile is at or before it (binary search
+  // over the ascending first_tile; tiles past count repeat the total)
   int j = 0;
 #pragma unroll
-  for (int k = 1; k < kMaxJobs; ++k)
-    j += (k < b.count && (int64_t)blockIdx.x >= b.first_tile[k]);
+  for (int step = kMaxJobs / 2; step > 0; step >>= 1)
+    if (j + step < b.count && (int64_t)blockIdx.x >= b.first_tile[j + step]) j += step;
   const DequantJob& job = b.job[j];
   const NF4Ref& w = job.w;
   const int t = threadIdx.x;
@@ -162,8 +166,8 @@ QLORA_API int qlora_nf4_dequant(const void* packed, const void* absmax, const fl
   return launch(b, (hipStream_t)stream);
 }
 
-// Up to four weights in one launch: argument arrays of length `count`, entry i as in
-// qlora_nf4_dequant.
+// Up to 32 weights in one launch (a layer's four, or those of eight layers): argument arrays of
+// length `count`, entry i as in qlora_nf4_dequant.
 QLORA_API int qlora_nf4_dequant_many(int32_t count, const void* const* packed,
                                      const void* const* absmax, const float* const* code2,
                                      const float* const* absmax2, const float* const* offsets,

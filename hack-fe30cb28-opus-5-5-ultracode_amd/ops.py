@@ -205,12 +205,15 @@ def _dq_shape(w):
     return w.shape
 
 
+DEQUANT_MANY_MAX = 32  # weights per qlora_nf4_dequant_many launch
+
+
 def dequant_many(items, device):
-    """fp16 [N_i, K_i] of each NF4Weight / NF4Group of `items` (at most 4), all in one launch
-    (a layer's qkv, o, gate|up and down)."""
+    """fp16 [N_i, K_i] of each NF4Weight / NF4Group of `items` (at most DEQUANT_MANY_MAX), all
+    in one launch (a layer's qkv, o, gate|up and down, or those of several layers)."""
     import ctypes
-    if not 1 <= len(items) <= 4:
-        raise ValueError("dequant_many takes 1 to 4 weights")
+    if not 1 <= len(items) <= DEQUANT_MANY_MAX:
+        raise ValueError(f"dequant_many takes 1 to {DEQUANT_MANY_MAX} weights")
     outs = [torch.empty(_dq_shape(w), device=device, dtype=torch.float16) for w in items]
     device = outs[0].device  # "cuda" -> "cuda:<current>"
     for w in items:

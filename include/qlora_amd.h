@@ -189,10 +189,10 @@ int qlora_ce_grad(void* logits, int64_t ld, const int64_t* target, const float* 
                   int64_t v0, int64_t n_sup, int64_t width, void* stream);
 
 /*
- * Up to four weights in one launch (a layer's qkv, o, gate|up and down): arrays of `count`
- * entries, entry i exactly the arguments of one qlora_nf4_dequant call (pointer arrays and
- * value arrays live in host memory; the pointers they hold are device pointers).
- * Replaces the per-weight launches of dequant() (engine.py:683-694) for a whole layer.
+ * Up to 32 weights in one launch (a layer's qkv, o, gate|up and down, or the weights of eight
+ * layers): arrays of `count` entries, entry i exactly the arguments of one qlora_nf4_dequant
+ * call (pointer arrays and value arrays live in host memory; the pointers they hold are device
+ * pointers). Replaces the per-weight launches of dequant() (engine.py:683-694) for whole layers.
  */
 int qlora_nf4_dequant_many(int32_t count, const void* const* packed, const void* const* absmax,
                            const float* const* code2, const float* const* absmax2,

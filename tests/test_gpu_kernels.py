@@ -88,7 +88,7 @@ def test_nf4_group_dequant_equals_separate(pkg):
     assert torch.equal(bits16(out), bits16(want))
 
 
-@pytest.mark.parametrize("mix", ["layer", "ragged"])
+@pytest.mark.parametrize("mix", ["layer", "ragged", "32"])
 def test_nf4_dequant_many_equals_oracle(pkg, mix):
     """One qlora_nf4_dequant_many launch over several weights (a layer's q|k|v group, o,
     gate|up group and down; or ragged sizes, plain absmax and a non-standard code mixed in)
@@ -108,10 +108,18 @@ def test_nf4_dequant_many_equals_oracle(pkg, mix):
     if mix == "layer":
         parts = [[make((1536, 1536)), make((256, 1536)), make((256, 1536))], [make((1536, 1536))],
                  [make((8960, 1536)), make((8960, 1536))], [make((1536, 8960))]]
-    else:
+    elif mix == "ragged":
         code = np.sort(rng.standard_normal(16).astype(np.float32))
         parts = [[make((64, 64))], [make((300, 512), nested=False)], [make((8, 64), code=code)],
                  [make((64, 1536)), make((256, 1536))]]
+    else:  # the most one launch takes (eight layers' weights), sizes and formats mixed
+        code = np.sort(rng.standard_normal(16).astype(np.float32))
+        parts = []
+        for i in range(32):
+            rows = int(rng.integers(1, 40)) * 8
+            kind = i % 4
+            parts.append([make((rows, 512), nested=kind != 1, code=code if kind == 2 else None)]
+                         if kind != 3 else [make((64 * (1 + i % 3), 256)), make((64, 256))])
     items, wants = [], []
     for grp in parts:
         ws = [pkg.ops.NF4Weight(_device_state(p, st)) for p, st, _ in grp]
@@ -119,6 +127,10 @@ def test_nf4_dequant_many_equals_oracle(pkg, mix):
         assert items[-1] is not None
         wants.append(torch.from_numpy(np.concatenate([d for _, _, d in grp])))
     outs = pkg.ops.dequant_many(items, torch.device(DEV))
+    assert len(outs) == len(items)
+    if mix == "32":
+        with pytest.raises(ValueError):
+            pkg.ops.dequant_many(items + items[:1], torch.device(DEV))
     for out, want in zip(outs, wants):
         assert torch.equal(bits16(out), bits16(want))
 
