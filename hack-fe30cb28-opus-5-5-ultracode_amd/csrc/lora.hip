@@ -17,8 +17,16 @@
 // Phase 1: 32 x 32 MFMA tiles over the rank columns, the 16-wide k-steps dealt round-robin to the
 // wavefronts in chunks whose loads are all issued before the chunk's MFMAs; the eight partial
 // tiles are summed in LDS and rounded. Phase 2 computes Y^T = Vt P^T, one MFMA per 32 output
-// columns and 16 ranks, so that a lane holds four consecutive columns of one token and writes
-// 8-byte runs; the first chunk of Vt operands is loaded before phase 1.
+// columns and 16 ranks (a lane holds columns of one token), over chunks of kChunkCols output
+// columns: the wavefronts put their tiles into an LDS copy of the chunk's 32 rows, then the
+// workgroup writes the rows with 16-byte stores, a wavefront per 1 KiB of a row (the MFMA layout
+// itself would store 16-byte pieces of 32 different rows per instruction, which ran phase 2 at
+// a third of the bandwidth). A workgroup takes a.cpw consecutive chunks (blockIdx.z: which
+// group; each group's workgroup forms P itself, the first writes it): a workgroup's time is a
+// chain of dependent steps, so a launch that would not fill the GPU gives each chunk its own
+// workgroup (more, shorter chains), a full one keeps a row's chunks together (no second phase
+// 1). The first chunk's Vt operands are loaded before phase 1, the next chunk's before the
+// current one is stored.
 #include "common.h"
 
 namespace qlora {
@@ -30,6 +38,11 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr int kTok = 32;
 constexpr int kWaves = 8;
 constexpr int kChunk1 = 12;  // phase-1 k-steps per wavefront per chunk
+constexpr int kChunkCols = 512;  // phase-2 output columns staged in LDS at a time
+constexpr int kCUs = 256;        // compute units of an MI355X
+constexpr int kTilesPerWave = kChunkCols / 32 / kWaves;  // phase-2 tiles per wavefront per chunk
+constexpr int kStageLd = kChunkCols + 4;  // LDS row stride (halves): 8-byte writes of the 32
+                                          // rows of a tile land on distinct banks
 
 // The LoRA ranks the kernels take (template parameter R).
 __host__ __device__ constexpr bool rank_ok(int r) { return r == 8 || r == 16 || r == 32 || r == 64; }
@@ -49,6 +62,7 @@ struct Args {
   int64_t n;
   float s;
   int scale;  // 1: P = f16(f16(acc) * s), 0: P = f16(acc)
+  int cpw;    // phase-2 column chunks per workgroup
 };
 
 __device__ __forceinline__ f32x16 mfma(half8_t a, half8_t b, f32x16 c) {
@@ -67,9 +81,9 @@ template <int R>
 __global__ __launch_bounds__(64 * kWaves) void lora_rows_kernel(Args a) {
   constexpr int NT1 = (R + 31) / 32, KS2 = (R + 15) / 16, RP = 16 * KS2;
   constexpr int CH1 = NT1 == 1 ? kChunk1 : kChunk1 / 2;
-  constexpr int CH2 = KS2 == 1 ? 6 : (KS2 == 2 ? 3 : 2);  // phase-2 column tiles per chunk
   __shared__ float red[kWaves][kTok][R];
   __shared__ __align__(16) uint16_t ps[kTok][RP];
+  __shared__ __align__(16) uint16_t stage[kTok][kStageLd];
   const Job& jb = a.job[blockIdx.y];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int row = lane & 31, half = lane >> 5;
@@ -77,18 +91,25 @@ __global__ __launch_bounds__(64 * kWaves) void lora_rows_kernel(Args a) {
   const int64_t tok = t0 + row < a.n ? t0 + row : a.n - 1;  // rows past n: computed, not stored
   const bool two = jb.Y != nullptr;
   const int tiles = two ? jb.M2 / 32 : 0;
-  // phase-2 operands of the first chunk: Vt rows 32 c + l%32, ranks 16 kk + 8(l/32)..+7 (past R:
-  // the row's first ranks again)
-  half8_t vop[CH2][KS2];
+  constexpr int kTilesPerChunk = kChunkCols / 32;
+  const int group = blockIdx.z, c_first = group * a.cpw * kTilesPerChunk;
+  const int c_end = min(tiles, c_first + a.cpw * kTilesPerChunk);
+  if (group > 0 && c_first >= tiles) return;  // uniform: this job has fewer chunks
+  // phase-2 operands of this wavefront's tiles of the first chunk: Vt rows 32 c + l%32, ranks
+  // 16 kk + 8(l/32)..+7 (past R: the row's first ranks again; tiles past the end: the last one)
+  half8_t vop[kTilesPerWave][KS2];
+  auto load_vop = [&](int c0) {
 #pragma unroll
-  for (int i = 0; i < CH2; ++i) {
-    const int c = min(wave + kWaves * i, max(tiles - 1, 0));
+    for (int i = 0; i < kTilesPerWave; ++i) {
+      const int c = min(c0 + kTilesPerWave * wave + i, max(tiles - 1, 0));
 #pragma unroll
-    for (int kk = 0; kk < KS2; ++kk) {
-      const int r0 = min(16 * kk + 8 * half, R - 8);
-      vop[i][kk] = two ? ld8(jb.Vt + (int64_t)(32 * c + row) * R + r0) : half8_t{};
+      for (int kk = 0; kk < KS2; ++kk) {
+        const int r0 = min(16 * kk + 8 * half, R - 8);
+        vop[i][kk] = two ? ld8(jb.Vt + (int64_t)(32 * c + row) * R + r0) : half8_t{};
+      }
     }
-  }
+  };
+  load_vop(c_first);
   // phase 1: P[32 x R] = X[32 x K1] W[K1 x R]
   const uint16_t* xrow = jb.X + tok * jb.ldx + 8 * half;
   const uint16_t* wrow[NT1];
@@ -134,7 +155,7 @@ __global__ __launch_bounds__(64 * kWaves) void lora_rows_kernel(Args a) {
       v = h2f(f2h(v));
       if (a.scale) v = h2f(f2h(v * a.s));
       b = f2h_bits(v);
-      if (t0 + t < a.n) jb.P[(t0 + t) * R + k] = b;
+      if (group == 0 && t0 + t < a.n) jb.P[(t0 + t) * R + k] = b;
     }
     ps[t][k] = b;
   }
@@ -144,36 +165,42 @@ __global__ __launch_bounds__(64 * kWaves) void lora_rows_kernel(Args a) {
   half8_t pb[KS2];
 #pragma unroll
   for (int kk = 0; kk < KS2; ++kk) pb[kk] = ld8(&ps[row][16 * kk + 8 * half]);
-  const bool store = t0 + row < a.n;
-  uint16_t* yrow = jb.Y + (t0 + row) * jb.M2 + 4 * half;
-  for (int c0 = wave; c0 < tiles; c0 += kWaves * CH2) {
-    if (c0 != wave) {
+  for (int c0 = c_first; c0 < c_end; c0 += kTilesPerChunk) {
+    f32x16 ys[kTilesPerWave];
 #pragma unroll
-      for (int i = 0; i < CH2; ++i) {
-        const int c = min(c0 + kWaves * i, tiles - 1);
+    for (int i = 0; i < kTilesPerWave; ++i) {
+      ys[i] = f32x16{};
 #pragma unroll
-        for (int kk = 0; kk < KS2; ++kk) {
-          const int r0 = min(16 * kk + 8 * half, R - 8);
-          vop[i][kk] = ld8(jb.Vt + (int64_t)(32 * c + row) * R + r0);
-        }
-      }
+      for (int kk = 0; kk < KS2; ++kk) ys[i] = mfma(vop[i][kk], pb[kk], ys[i]);
     }
+    if (c0 + kTilesPerChunk < c_end) load_vop(c0 + kTilesPerChunk);  // the next chunk's
+    if (c0 != c_first) __syncthreads();  // the previous chunk's rows are out of the stage
 #pragma unroll
-    for (int i = 0; i < CH2; ++i) {
-      const int c = c0 + kWaves * i;
-      f32x16 y = f32x16{};
-#pragma unroll
-      for (int kk = 0; kk < KS2; ++kk) y = mfma(vop[i][kk], pb[kk], y);
+    for (int i = 0; i < kTilesPerWave; ++i) {
+      const int lt = kTilesPerWave * wave + i;  // tile within the chunk
+      const f32x16& y = ys[i];
       // register r: Y[t0 + l%32][32 c + 8(r/4) + 4(l/32) + r%4]
-      if (store && c < tiles) {
+      if (c0 + lt < tiles) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           uint2 w;
           w.x = pack2h(y[4 * j + 0], y[4 * j + 1]);
           w.y = pack2h(y[4 * j + 2], y[4 * j + 3]);
-          *reinterpret_cast<uint2*>(yrow + 32 * c + 8 * j) = w;
+          *reinterpret_cast<uint2*>(&stage[row][32 * lt + 8 * j + 4 * half]) = w;
         }
       }
+    }
+    __syncthreads();
+    // the chunk's rows: 16-byte units, consecutive threads along a row
+    const int ccols = min(kChunkCols, 32 * (tiles - c0));
+    const int units = ccols / 8;  // per row
+    for (int u = tid; u < kTok * units; u += 64 * kWaves) {
+      const int tr = u / units, cu = u - tr * units;
+      if (t0 + tr >= a.n) continue;
+      const uint2 lo = *reinterpret_cast<const uint2*>(&stage[tr][8 * cu]);
+      const uint2 hi = *reinterpret_cast<const uint2*>(&stage[tr][8 * cu + 4]);
+      *reinterpret_cast<uint4*>(jb.Y + (t0 + tr) * jb.M2 + 32 * c0 + 8 * cu) =
+          make_uint4(lo.x, lo.y, hi.x, hi.y);
     }
   }
 }
@@ -187,10 +214,21 @@ int launch(Args& a, int r, hipStream_t stream) {
     QLORA_CHECK_ARG(j.X && j.Wt && j.P && j.K1 > 0 && j.K1 % 16 == 0 && j.ldx >= j.K1);
     QLORA_CHECK_ARG(j.ldx % 8 == 0 && aligned(j.X, 16) && aligned(j.Wt, 16) && aligned(j.P, 2));
     QLORA_CHECK_ARG(j.Y == nullptr ||
-                    (j.Vt && j.M2 > 0 && j.M2 % 32 == 0 && aligned(j.Vt, 16) && aligned(j.Y, 8)));
+                    (j.Vt && j.M2 > 0 && j.M2 % 32 == 0 && aligned(j.Vt, 16) && aligned(j.Y, 16)));
   }
   QLORA_CHECK_ARG(a.n < (1ll << 31) * kTok);
-  const dim3 grid((unsigned)qlora_cdiv(a.n, kTok), 2), block(64 * kWaves);
+  int chunks = 1;  // phase-2 column chunks of the job with the most
+  for (int i = 0; i < 2; ++i)
+    if (a.job[i].Y != nullptr)
+      chunks = (int)std::max<int64_t>(chunks, qlora_cdiv(a.job[i].M2, kChunkCols));
+  // the chunks of a row go to separate workgroups while the launch stays within one workgroup
+  // per CU (256 on MI355X); a fuller launch keeps them together
+  const int64_t rows = qlora_cdiv(a.n, kTok);
+  int groups = chunks;
+  while (groups > 1 && rows * 2 * groups > kCUs) --groups;
+  a.cpw = (int)qlora_cdiv(chunks, groups);
+  groups = (int)qlora_cdiv(chunks, a.cpw);
+  const dim3 grid((unsigned)rows, 2, (unsigned)groups), block(64 * kWaves);
   switch (r) {
     case 8: hipLaunchKernelGGL(lora_rows_kernel<8>, grid, block, 0, stream, a); break;
     case 16: hipLaunchKernelGGL(lora_rows_kernel<16>, grid, block, 0, stream, a); break;

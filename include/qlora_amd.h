@@ -297,8 +297,8 @@ int qlora_gemmlt_solutions(int32_t op, int64_t M, int64_t N, int64_t K, int64_t 
  *   x_a = f16(a_a A_a^T)   f16 [n, r] (kept for the backward)
  *   l_a = f16(x_a B_a^T)   f16 [n, N_a] (added to the projection output by qlora_rope_fwd)
  * a_a f16 [n, H] (the dropped LoRA inputs of qlora_rms_fwd); A_a f16 [r, H]; B_a f16 [N_a, r].
- * Requires r in {8, 16, 32, 64}, H % 16 == 0, N_a % 32 == 0; a_a, A_a, B_a 16-byte and l_a
- * 8-byte aligned.
+ * Requires r in {8, 16, 32, 64}, H % 16 == 0, N_a % 32 == 0; a_a, A_a, B_a, l_a 16-byte
+ * aligned.
  * No reference counterpart as one launch: the reference makes four fp16 products.
  */
 int qlora_lora_fwd_rows(const void* a_q, const void* a_v, const void* A_q, const void* A_v,
@@ -314,7 +314,7 @@ int qlora_lora_fwd_rows(const void* a_q, const void* a_v, const void* A_q, const
  * t_q/t_v may both be null (then not computed). Replaces `dx_lo = (g @ b_w) * s` and
  * `dx_lo @ a_w` (engine.py:1326-1330) for both adapters; the token reductions dB and dA are
  * qlora_lora_grad. Requires r in {8, 16, 32, 64}, N_a % 16 == 0, H % 32 == 0, ldg % 8 == 0;
- * g_a, Bt_a, At_a 16-byte and t_a 8-byte aligned.
+ * g_a, Bt_a, At_a, t_a 16-byte aligned.
  */
 int qlora_lora_bwd_rows(const void* g_q, const void* g_v, int64_t ldg, const void* Bt_q,
                         const void* Bt_v, const void* At_q, const void* At_v, void* dx_q,
