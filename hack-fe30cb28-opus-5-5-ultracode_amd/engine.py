@@ -258,21 +258,30 @@ class Packed:
     def __init__(self, input_ids, attention_mask, labels, rope, dropout, dropout_p, lengths=None,
                  n_supervised=None):
         """`lengths` (tokens of each row) and `n_supervised` (tokens with a label), when the
-        caller knows them on the host (a collator does), spare the step its reads of device
-        values: each such read waits for all the work queued before it (the previous step's
-        backward), and the GPU then idles while this step's first launches are being queued.
-        Given lengths, the mask is trusted to be right-padded to them."""
+        caller knows them on the host (a collator does), spare the step its one read of device
+        values (lengths, the padding check and the supervised count together): a read waits for
+        all the work queued before it (the previous step's backward), and the GPU then idles
+        while this step's first launches are being queued. Given lengths, the mask is trusted to
+        be right-padded to them."""
         if input_ids.dim() != 2 or attention_mask.shape != input_ids.shape \
                 or labels.shape != input_ids.shape:
             raise UnsupportedBatch("inputs are not [rows, tokens]")
         B, T = input_ids.shape
         dev = input_ids.device
         if lengths is None:
-            lengths_t = attention_mask.sum(dim=1)
-            lengths = lengths_t.tolist()
+            # one read of the device: the row lengths, whether the mask is right-padded to them,
+            # and the supervised count (a token whose next label is not -100)
+            mask = attention_mask.bool()
+            lengths_t = mask.sum(dim=1)
             expected = torch.arange(T, device=dev)[None, :] < lengths_t[:, None]
-            if not bool(torch.equal(attention_mask.bool(), expected)):
+            padded_ok = (mask == expected).all().view(1).to(torch.int64)
+            sup = ((labels[:, 1:] >= 0) & mask[:, :-1]).sum().view(1).to(torch.int64)
+            host = torch.cat([lengths_t.to(torch.int64), padded_ok, sup]).tolist()
+            lengths = host[:B]
+            if not host[B]:
                 raise UnsupportedBatch("attention_mask is not right-padded")
+            if n_supervised is None:
+                n_supervised = host[B + 1]
         lengths = [int(x) for x in lengths]
         if len(lengths) != B or any(x < 0 or x > T for x in lengths):
             raise UnsupportedBatch("lengths do not fit the batch")
