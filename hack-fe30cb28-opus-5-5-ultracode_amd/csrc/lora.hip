@@ -283,6 +283,10 @@ __device__ __forceinline__ int grad_job(const GradArgs& a, int col) {
   return j;
 }
 
+__device__ __forceinline__ uint32_t word_of4(const uint4& x, int i) {
+  return i < 2 ? (i == 0 ? x.x : x.y) : (i == 2 ? x.z : x.w);
+}
+
 __device__ __forceinline__ float dot2u(uint32_t a, uint32_t b, float c) {
   typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
   return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, a), __builtin_bit_cast(half2_t, b),
@@ -374,6 +378,102 @@ __global__ __launch_bounds__(kGradThreads) void lora_grad_part_kernel(GradArgs a
         *reinterpret_cast<float4*>(a.part + ((int64_t)blockIdx.y * a.total_cols + col) * R + k) =
             v;
       }
+    }
+  }
+}
+
+// MFMA form of the same pass (the same partial sums up to fp32 summation order), for jobs whose
+// rows hold whole 16-byte chunks: the workgroup stages its 256 tokens x 128 columns of W in LDS
+// with 16-byte row loads (16 chunks a row, chunk c of row t at c ^ 4 (t mod 4)) and Z^T
+// [R][256] (rows padded by 16 bytes); wavefront w then forms out[32 w .. + 31][0 .. R) over the
+// 16 token steps of 16 with v_mfma_f32_32x32x16_f16: A = W^T through ds_read_b64_tr_b16 (8
+// consecutive tokens of one column per lane), B = Z from Z^T. The v_dot2 form spends most of its
+// time in the 256 products per token pair and thread; this one in the loads.
+constexpr int kZLd = kGradChunk + 8;  // Z^T row stride (halves)
+
+__device__ __forceinline__ int wt_off(int row, int col) {
+  return row * kGradCols + (((col >> 3) ^ ((row & 3) << 2)) << 3) + (col & 7);
+}
+
+// The MFMA A operand W^T[32 columns][8 tokens] of a wt_off tile: lane l supplies column
+// c0 + l % 32 and tokens k0 + 8 (l / 32) .. + 7. ds_read_b64_tr_b16 gives lane i of each
+// 16-lane group element i % 4 of the 4 halves read by lane 4 j + i / 4 of the group as its
+// element j; so lane p of a group reads row (first token) + p / 4, columns (group's first) +
+// 4 (p % 4) .. + 3, and two reads cover the 8 tokens.
+__device__ __forceinline__ half8_t tr_cols(const uint16_t* t, int k0, int c0, int lane) {
+  typedef short short4_t __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) short4_t lds_short4_t;
+  const int p = lane & 15;
+  const int row = k0 + 8 * (lane >> 5) + (p >> 2);
+  const int col = c0 + 16 * ((lane >> 4) & 1) + 4 * (p & 3);
+  const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)(t + wt_off(row, col)));
+  const short4_t hi =
+      __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)(t + wt_off(row + 4, col)));
+  return __builtin_bit_cast(half8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+template <int R>
+__global__ __launch_bounds__(kGradThreads) void lora_grad_mfma_kernel(GradArgs a) {
+  constexpr int NTR = (R + 31) / 32;  // 32-rank tiles of the MFMA output
+  constexpr int kLoads = kGradChunk * (kGradCols / 8) / kGradThreads;
+  __shared__ __align__(16) uint16_t wt[kGradChunk * kGradCols];
+  __shared__ __align__(16) uint16_t zt[R][kZLd];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wg_col = blockIdx.x * kGradCols;
+  const GradJob& jb = a.job[grad_job(a, wg_col)];
+  const int64_t t0 = (int64_t)blockIdx.y * kGradChunk;
+  const int nt = (int)min((int64_t)kGradChunk, a.n - t0);  // >= 1
+  const int cbase = wg_col - jb.col0;  // the tile's first column within the job
+  // W: every load issued first (rows past the chunk read its last row and meet a zero Z^T;
+  // columns past the job read its last chunk and are not written)
+  uint4 wv[kLoads];
+#pragma unroll
+  for (int i = 0; i < kLoads; ++i) {
+    const int id = tid + i * kGradThreads, row = id >> 4, ch = id & 15;
+    const int c = min(cbase + 8 * ch, jb.ncols - 8);
+    wv[i] = *reinterpret_cast<const uint4*>(jb.W + (t0 + min(row, nt - 1)) * jb.ldw + c);
+  }
+  for (int i = tid; i < kGradChunk * (R / 8); i += kGradThreads) {
+    const int t = i / (R / 8), kq = i % (R / 8);
+    uint4 z = *reinterpret_cast<const uint4*>(jb.Z + (t0 + min(t, nt - 1)) * R + 8 * kq);
+    if (t >= nt) z = make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t w = word_of4(z, j);
+      zt[8 * kq + 2 * j][t] = (uint16_t)(w & 0xFFFFu);
+      zt[8 * kq + 2 * j + 1][t] = (uint16_t)(w >> 16);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kLoads; ++i) {
+    const int id = tid + i * kGradThreads, row = id >> 4, ch = id & 15;
+    *reinterpret_cast<uint4*>(wt + wt_off(row, 8 * ch)) = wv[i];
+  }
+  __syncthreads();
+  f32x16 acc[NTR];
+#pragma unroll
+  for (int u = 0; u < NTR; ++u) acc[u] = f32x16{};
+#pragma unroll 4
+  for (int kk = 0; kk < kGradChunk / 16; ++kk) {
+    const half8_t aop = tr_cols(wt, 16 * kk, 32 * wave, lane);
+#pragma unroll
+    for (int u = 0; u < NTR; ++u) {
+      const int rank = 32 * u + (lane & 31);
+      const half8_t bop = rank < R ? ld8(&zt[rank < R ? rank : 0][16 * kk + 8 * (lane >> 5)])
+                                   : half8_t{};
+      acc[u] = mfma(aop, bop, acc[u]);
+    }
+  }
+  // register r of lane l: out[column 32 w + 8(r/4) + 4(l/32) + r%4][rank 32 u + l%32]
+#pragma unroll
+  for (int u = 0; u < NTR; ++u) {
+    const int rank = 32 * u + (lane & 31);
+    if (rank >= R) continue;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int m = 32 * wave + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+      if (cbase + m < jb.ncols)
+        a.part[((int64_t)blockIdx.y * a.total_cols + wg_col + m) * R + rank] = acc[u][r];
     }
   }
 }
@@ -489,11 +589,18 @@ QLORA_API int qlora_lora_grad(const void* g_q, const void* g_v, int64_t ldg, con
   a.nchunks = (int)qlora_cdiv(n, kGradChunk);
   hipStream_t st = (hipStream_t)stream;
   const dim3 g1(col / kGradCols, a.nchunks), g2((unsigned)qlora_cdiv((int64_t)col * r, 256));
-#define QLORA_GRAD(RR)                                                                   \
-  do {                                                                                   \
-    if (n > 0)                                                                           \
-      hipLaunchKernelGGL(lora_grad_part_kernel<RR>, g1, dim3(kGradThreads), 0, st, a);   \
-    hipLaunchKernelGGL(lora_grad_reduce_kernel<RR>, g2, dim3(256), 0, st, a);            \
+  // the MFMA pass needs whole 16-byte chunks in every row of every job
+  bool mfma_ok = true;
+  for (int j = 0; j < 4; ++j)
+    mfma_ok = mfma_ok && aligned(W[j], 16) && aligned(Z[j], 16) && ldw[j] % 8 == 0 &&
+              nc[j] % 8 == 0;
+#define QLORA_GRAD(RR)                                                                     \
+  do {                                                                                     \
+    if (n > 0 && mfma_ok)                                                                  \
+      hipLaunchKernelGGL(lora_grad_mfma_kernel<RR>, g1, dim3(kGradThreads), 0, st, a);     \
+    else if (n > 0)                                                                        \
+      hipLaunchKernelGGL(lora_grad_part_kernel<RR>, g1, dim3(kGradThreads), 0, st, a);     \
+    hipLaunchKernelGGL(lora_grad_reduce_kernel<RR>, g2, dim3(256), 0, st, a);              \
   } while (0)
   switch (r) {
     case 8: QLORA_GRAD(8); break;
