@@ -3,7 +3,11 @@
 // glu_bwd_kernel kernels.py:324-336 (_glu_bwd engine.py:1020-1023).
 //   m  = fp16( g * sigmoid(g) * u )                               g, u = gu[:, :I], gu[:, I:]
 //   gu <- [ fp16(dm * u * s * (1 + g (1 - s))) | fp16(dm * g * s) ]   s = sigmoid(g)
-// HBM-bound elementwise: 8 columns per thread (16-byte loads and stores) when I % 8 == 0.
+// HBM-bound elementwise: 8 columns per thread (16-byte loads and stores) when I % 8 == 0. The
+// sigmoid is 1 / (1 + 2^(-g log2 e)) with the hardware exp2 and reciprocal (v_exp_f32,
+// v_rcp_f32, about 1 ulp each in fp32, ahead of the fp16 rounding); with the correctly rounded
+// expf and an IEEE division per element, and a 64-bit division for each thread's row, the
+// forward issued about 280 instructions per 48 bytes and was bound by them, not by HBM.
 #include "common.h"
 
 namespace qlora {
@@ -29,9 +33,26 @@ struct VecH<1> {
   static __device__ __forceinline__ T pack(const float (&v)[1]) { return f2h_bits(v[0]); }
 };
 
-__device__ __forceinline__ float sigmoidf(float g) { return 1.0f / (1.0f + expf(-g)); }
+// 1 / (1 + e^-g): g -> -inf gives 1 / inf = 0, g -> +inf gives 1 / 1, NaN stays NaN
+__device__ __forceinline__ float sigmoidf(float g) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.4426950408889634f));
+}
 
-template <int W>
+// The thread's row and first column: 32-bit division while the thread count fits (SMALL).
+template <bool SMALL>
+__device__ __forceinline__ void row_col(int64_t gid, int64_t per_row, int W, int64_t& row,
+                                        int64_t& col) {
+  if constexpr (SMALL) {
+    const uint32_t g = (uint32_t)gid, pr = (uint32_t)per_row, r = g / pr;
+    row = r;
+    col = (int64_t)(g - r * pr) * W;
+  } else {
+    row = gid / per_row;
+    col = (gid - row * per_row) * W;
+  }
+}
+
+template <int W, bool SMALL>
 __global__ __launch_bounds__(256) void glu_fwd_kernel(const uint16_t* gu, uint16_t* m,
                                                       int64_t n, int64_t I) {
   using V = VecH<W>;
@@ -39,18 +60,18 @@ __global__ __launch_bounds__(256) void glu_fwd_kernel(const uint16_t* gu, uint16
   const int64_t per_row = I / W;
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (gid >= n * per_row) return;
-  const int64_t row = gid / per_row;
-  const int64_t col = (gid - row * per_row) * W;
+  int64_t row, col;
+  row_col<SMALL>(gid, per_row, W, row, col);
   const uint16_t* src = gu + row * 2 * I + col;
   float g[W], u[W], o[W];
   V::unpack(*reinterpret_cast<const T*>(src), g);
   V::unpack(*reinterpret_cast<const T*>(src + I), u);
 #pragma unroll
-  for (int i = 0; i < W; ++i) o[i] = g[i] / (1.0f + expf(-g[i])) * u[i];
+  for (int i = 0; i < W; ++i) o[i] = g[i] * sigmoidf(g[i]) * u[i];
   *reinterpret_cast<T*>(m + row * I + col) = V::pack(o);
 }
 
-template <int W>
+template <int W, bool SMALL>
 __global__ __launch_bounds__(256) void glu_bwd_kernel(const uint16_t* dm, uint16_t* gu,
                                                       int64_t n, int64_t I) {
   using V = VecH<W>;
@@ -58,8 +79,8 @@ __global__ __launch_bounds__(256) void glu_bwd_kernel(const uint16_t* dm, uint16
   const int64_t per_row = I / W;
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (gid >= n * per_row) return;
-  const int64_t row = gid / per_row;
-  const int64_t col = (gid - row * per_row) * W;
+  int64_t row, col;
+  row_col<SMALL>(gid, per_row, W, row, col);
   uint16_t* src = gu + row * 2 * I + col;
   float g[W], u[W], d[W], og[W], ou[W];
   V::unpack(*reinterpret_cast<const T*>(src), g);
@@ -90,13 +111,16 @@ QLORA_API int qlora_glu_fwd(const void* gu, void* m, int64_t n, int64_t I, void*
   const bool v8 = I % 8 == 0 && al(gu, 16) && al(m, 16);
   const int W = v8 ? 8 : 1;
   const int64_t total = n * (I / W);
+  QLORA_CHECK_ARG(qlora_cdiv(total, 256) < (1ll << 32));
   const dim3 grid((unsigned)qlora_cdiv(total, 256));
-  if (v8)
-    hipLaunchKernelGGL(glu_fwd_kernel<8>, grid, dim3(256), 0, (hipStream_t)stream,
-                       static_cast<const uint16_t*>(gu), static_cast<uint16_t*>(m), n, I);
-  else
-    hipLaunchKernelGGL(glu_fwd_kernel<1>, grid, dim3(256), 0, (hipStream_t)stream,
-                       static_cast<const uint16_t*>(gu), static_cast<uint16_t*>(m), n, I);
+  const bool small = qlora_cdiv(total, 256) * 256 <= (int64_t)UINT32_MAX;
+  const uint16_t* src = static_cast<const uint16_t*>(gu);
+  uint16_t* dst = static_cast<uint16_t*>(m);
+  hipStream_t s = (hipStream_t)stream;
+  if (v8 && small) hipLaunchKernelGGL((glu_fwd_kernel<8, true>), grid, dim3(256), 0, s, src, dst, n, I);
+  else if (v8) hipLaunchKernelGGL((glu_fwd_kernel<8, false>), grid, dim3(256), 0, s, src, dst, n, I);
+  else if (small) hipLaunchKernelGGL((glu_fwd_kernel<1, true>), grid, dim3(256), 0, s, src, dst, n, I);
+  else hipLaunchKernelGGL((glu_fwd_kernel<1, false>), grid, dim3(256), 0, s, src, dst, n, I);
   return qlora_launch_status();
 }
 
@@ -107,13 +131,16 @@ QLORA_API int qlora_glu_bwd(const void* dm, void* gu, int64_t n, int64_t I, void
   const bool v8 = I % 8 == 0 && al(gu, 16) && al(dm, 16);
   const int W = v8 ? 8 : 1;
   const int64_t total = n * (I / W);
+  QLORA_CHECK_ARG(qlora_cdiv(total, 256) < (1ll << 32));
   const dim3 grid((unsigned)qlora_cdiv(total, 256));
-  if (v8)
-    hipLaunchKernelGGL(glu_bwd_kernel<8>, grid, dim3(256), 0, (hipStream_t)stream,
-                       static_cast<const uint16_t*>(dm), static_cast<uint16_t*>(gu), n, I);
-  else
-    hipLaunchKernelGGL(glu_bwd_kernel<1>, grid, dim3(256), 0, (hipStream_t)stream,
-                       static_cast<const uint16_t*>(dm), static_cast<uint16_t*>(gu), n, I);
+  const bool small = qlora_cdiv(total, 256) * 256 <= (int64_t)UINT32_MAX;
+  const uint16_t* d = static_cast<const uint16_t*>(dm);
+  uint16_t* x = static_cast<uint16_t*>(gu);
+  hipStream_t s = (hipStream_t)stream;
+  if (v8 && small) hipLaunchKernelGGL((glu_bwd_kernel<8, true>), grid, dim3(256), 0, s, d, x, n, I);
+  else if (v8) hipLaunchKernelGGL((glu_bwd_kernel<8, false>), grid, dim3(256), 0, s, d, x, n, I);
+  else if (small) hipLaunchKernelGGL((glu_bwd_kernel<1, true>), grid, dim3(256), 0, s, d, x, n, I);
+  else hipLaunchKernelGGL((glu_bwd_kernel<1, false>), grid, dim3(256), 0, s, d, x, n, I);
   return qlora_launch_status();
 }
 
