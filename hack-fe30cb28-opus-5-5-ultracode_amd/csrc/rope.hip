@@ -5,8 +5,7 @@
 // Rotate-half RoPE over the two halves of each head (Qwen2):
 //   out[:D/2] = x1 cos - x2 sin,  out[D/2:] = x2 cos + x1 sin,   cos/sin = table[pos, 0:D/2]
 // with pos restarting at every sequence of the packed batch. One work item is 8 columns of
-// one half-head pair (two 16-byte loads, two 16-byte stores per output copy); consecutive threads
-// take consecutive items, so each wavefront reads and writes contiguous spans.
+// one half-head pair (two 16-byte loads, two 16-byte stores per output copy).
 //
 // k and v come out with `kv_heads_out` heads: HKV (grouped-query layout) or HQ (each kv head
 // repeated HQ/HKV times, as repeat_kv does: kv head j at heads j*G .. j*G+G-1).
@@ -52,43 +51,67 @@ __device__ __forceinline__ uint4 pack8(const float (&v)[8]) {
 __device__ __forceinline__ uint4 ld16(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
 __device__ __forceinline__ void st16(uint16_t* p, uint4 v) { *reinterpret_cast<uint4*>(p) = v; }
 // cos/sin of position p (8 columns from d0); a position outside the table gives NaN instead of
-// an out-of-bounds read.
+// an out-of-bounds read (the address is clamped, the values replaced after the load).
 __device__ __forceinline__ void ld_table(const float* tab, int64_t p, int64_t positions,
                                          int half, int d0, float (&v)[8]) {
-  if (p < 0 || p >= positions) {
+  const bool ok = p >= 0 && p < positions;
+  const int64_t pc = ok ? p : 0;
+  const float4 a = reinterpret_cast<const float4*>(tab + pc * half + d0)[0];
+  const float4 b = reinterpret_cast<const float4*>(tab + pc * half + d0)[1];
+  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  if (!ok) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) v[i] = __builtin_nanf("");
-    return;
   }
-  const float4 a = reinterpret_cast<const float4*>(tab + p * half + d0)[0];
-  const float4 b = reinterpret_cast<const float4*>(tab + p * half + d0)[1];
-  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
+// Work items are head-major: item = (head n + token) * per_head + chunk, so a wavefront's items
+// are one head of consecutive tokens (the q / k / v branches are uniform but at head
+// boundaries) and each token-head's 8-column chunks are consecutive threads (128 contiguous
+// bytes per half-head). The position is loaded first and the data right after it, so the table
+// loads that need the position wait for that one load only: two memory round trips per item.
+__device__ __forceinline__ void item_of(uint32_t gid, uint32_t n, int per_head, int& head,
+                                        int64_t& tok, int& d0) {
+  const uint32_t per = n * (uint32_t)per_head, h = gid / per, rem = gid - h * per;
+  head = (int)h;
+  tok = rem / (uint32_t)per_head;
+  d0 = (int)(rem - (uint32_t)tok * (uint32_t)per_head) * 8;
 }
 
 __global__ __launch_bounds__(256) void rope_fwd_kernel(RopeFwdArgs a) {
   const int half = a.D / 2, per_head = half / 8;
-  const int items = (a.HQ + 2 * a.HKV) * per_head;
-  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (gid >= a.n * items) return;
-  const int64_t tok = gid / items;
-  const int it = (int)(gid - tok * items);
-  const int head = it / per_head;  // 0..HQ-1 q, HQ..HQ+HKV-1 k, then v
-  const int d0 = (it - head * per_head) * 8;
-  const int C = (a.HQ + 2 * a.HKV) * a.D;
+  const int heads = a.HQ + 2 * a.HKV;
+  const uint32_t gid = blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= (uint32_t)a.n * (uint32_t)(heads * per_head)) return;
+  int head, d0;
+  int64_t tok;
+  item_of(gid, (uint32_t)a.n, per_head, head, tok, d0);
+  const int p = a.pos[tok];
+  const int C = heads * a.D;
   const uint16_t* src = a.qkv + tok * C + (int64_t)head * a.D + d0;
+  const uint4 w1 = ld16(src), w2 = ld16(src + half);
+  const bool is_q = head < a.HQ, is_v = head >= a.HQ + a.HKV;
+  const int hv = head - a.HQ - a.HKV;
+  // the LoRA delta of a q or v head (a k head, or an absent delta: none)
+  const uint16_t* l = is_q ? a.lq : is_v ? a.lv : nullptr;
+  uint4 m1 = make_uint4(0u, 0u, 0u, 0u), m2 = m1;
+  if (l != nullptr) {
+    l += is_q ? tok * ((int64_t)a.HQ * a.D) + (int64_t)head * a.D + d0
+              : tok * ((int64_t)a.HKV * a.D) + (int64_t)hv * a.D + d0;
+    m1 = ld16(l);
+    m2 = ld16(l + half);
+  }
   float x1[8], x2[8];
-  unpack8(ld16(src), x1);
-  unpack8(ld16(src + half), x2);
-  if (head >= a.HQ + a.HKV) {  // v: no rotation
-    const int hv = head - a.HQ - a.HKV;
-    if (a.lv) {
-      float l1[8], l2[8];
-      const uint16_t* l = a.lv + tok * ((int64_t)a.HKV * a.D) + (int64_t)hv * a.D + d0;
-      unpack8(ld16(l), l1);
-      unpack8(ld16(l + half), l2);
+  unpack8(w1, x1);
+  unpack8(w2, x2);
+  if (l != nullptr) {
+    float l1[8], l2[8];
+    unpack8(m1, l1);
+    unpack8(m2, l2);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) { x1[i] += l1[i] * a.lora_scale; x2[i] += l2[i] * a.lora_scale; }
-    }
+    for (int i = 0; i < 8; ++i) { x1[i] += l1[i] * a.lora_scale; x2[i] += l2[i] * a.lora_scale; }
+  }
+  if (is_v) {  // v: no rotation
     const uint4 o1 = pack8(x1), o2 = pack8(x2);
     const int rep = a.KH / a.HKV;
     for (int r = 0; r < rep; ++r) {
@@ -98,15 +121,6 @@ __global__ __launch_bounds__(256) void rope_fwd_kernel(RopeFwdArgs a) {
     }
     return;
   }
-  if (head < a.HQ && a.lq) {
-    float l1[8], l2[8];
-    const uint16_t* l = a.lq + tok * ((int64_t)a.HQ * a.D) + (int64_t)head * a.D + d0;
-    unpack8(ld16(l), l1);
-    unpack8(ld16(l + half), l2);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) { x1[i] += l1[i] * a.lora_scale; x2[i] += l2[i] * a.lora_scale; }
-  }
-  const int p = a.pos[tok];
   float c[8], s[8], o1[8], o2[8];
   ld_table(a.cos, p, a.positions, half, d0, c);
   ld_table(a.sin, p, a.positions, half, d0, s);
@@ -116,7 +130,7 @@ __global__ __launch_bounds__(256) void rope_fwd_kernel(RopeFwdArgs a) {
     o2[i] = x2[i] * c[i] + x1[i] * s[i];
   }
   const uint4 p1 = pack8(o1), p2 = pack8(o2);
-  if (head < a.HQ) {
+  if (is_q) {
     uint16_t* dst = a.q + tok * ((int64_t)a.HQ * a.D) + (int64_t)head * a.D + d0;
     st16(dst, p1);
     st16(dst + half, p2);
@@ -133,28 +147,49 @@ __global__ __launch_bounds__(256) void rope_fwd_kernel(RopeFwdArgs a) {
 
 __global__ __launch_bounds__(256) void rope_bwd_kernel(RopeBwdArgs a) {
   const int half = a.D / 2, per_head = half / 8;
-  const int items = (a.HQ + 2 * a.HKV) * per_head;
-  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (gid >= a.n * items) return;
-  const int64_t tok = gid / items;
-  const int it = (int)(gid - tok * items);
-  const int head = it / per_head;
-  const int d0 = (it - head * per_head) * 8;
-  const int C = (a.HQ + 2 * a.HKV) * a.D;
+  const int heads = a.HQ + 2 * a.HKV;
+  const uint32_t gid = blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= (uint32_t)a.n * (uint32_t)(heads * per_head)) return;
+  int head, d0;
+  int64_t tok;
+  item_of(gid, (uint32_t)a.n, per_head, head, tok, d0);
+  const int p = a.pos[tok];
+  const int C = heads * a.D;
   uint16_t* out = a.dqkv + tok * C + (int64_t)head * a.D + d0;
   float g1[8], g2[8];
-  if (head < a.HQ) {
+  const bool is_q = head < a.HQ, is_v = head >= a.HQ + a.HKV;
+  if (is_q) {
     const uint16_t* src = a.dq + tok * ((int64_t)a.HQ * a.D) + (int64_t)head * a.D + d0;
-    unpack8(ld16(src), g1);
-    unpack8(ld16(src + half), g2);
+    const uint4 w1 = ld16(src), w2 = ld16(src + half);
+    unpack8(w1, g1);
+    unpack8(w2, g2);
   } else {
-    const bool is_v = head >= a.HQ + a.HKV;
     const int hk = is_v ? head - a.HQ - a.HKV : head - a.HQ;
     const uint16_t* base = (is_v ? a.dv : a.dk) + tok * ((int64_t)a.KH * a.D);
     const int rep = a.KH / a.HKV;
 #pragma unroll
     for (int i = 0; i < 8; ++i) g1[i] = g2[i] = 0.f;
-    for (int r = 0; r < rep; ++r) {  // sum of the grouped-query replicas, fp32
+    // sum of the grouped-query replicas, fp32, in order; up to 8 replicas' loads are issued
+    // before the first sum (one round trip, not one per replica)
+    constexpr int kMaxRep = 8;
+    uint4 w[kMaxRep][2];
+#pragma unroll
+    for (int r = 0; r < kMaxRep; ++r)
+      if (r < rep) {
+        const uint16_t* src = base + (int64_t)(hk * rep + r) * a.D + d0;
+        w[r][0] = ld16(src);
+        w[r][1] = ld16(src + half);
+      }
+#pragma unroll
+    for (int r = 0; r < kMaxRep; ++r)
+      if (r < rep) {
+        float t1[8], t2[8];
+        unpack8(w[r][0], t1);
+        unpack8(w[r][1], t2);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) { g1[i] += t1[i]; g2[i] += t2[i]; }
+      }
+    for (int r = kMaxRep; r < rep; ++r) {
       const uint16_t* src = base + (int64_t)(hk * rep + r) * a.D + d0;
       float t1[8], t2[8];
       unpack8(ld16(src), t1);
@@ -168,7 +203,6 @@ __global__ __launch_bounds__(256) void rope_bwd_kernel(RopeBwdArgs a) {
       return;
     }
   }
-  const int p = a.pos[tok];
   float c[8], s[8], o1[8], o2[8];
   ld_table(a.cos, p, a.positions, half, d0, c);
   ld_table(a.sin, p, a.positions, half, d0, s);
@@ -205,6 +239,7 @@ QLORA_API int qlora_rope_fwd(const void* qkv, const void* lq, const void* lv, co
                 static_cast<uint16_t*>(k), static_cast<uint16_t*>(v), n, positions, HQ, HKV,
                 D, kv_heads_out, lora_scale};
   const int64_t total = n * (int64_t)(HQ + 2 * HKV) * (D / 16);
+  QLORA_CHECK_ARG(qlora_cdiv(total, 256) * 256 <= (int64_t)UINT32_MAX);  // 32-bit item index
   hipLaunchKernelGGL(rope_fwd_kernel, dim3((unsigned)qlora_cdiv(total, 256)), dim3(256), 0,
                      (hipStream_t)stream, a);
   return qlora_launch_status();
@@ -225,6 +260,7 @@ QLORA_API int qlora_rope_bwd(const void* dq, const void* dk, const void* dv, con
                 static_cast<const uint16_t*>(dv), cos, sin, pos, static_cast<uint16_t*>(dqkv),
                 n, positions, HQ, HKV, D, kv_heads_in};
   const int64_t total = n * (int64_t)(HQ + 2 * HKV) * (D / 16);
+  QLORA_CHECK_ARG(qlora_cdiv(total, 256) * 256 <= (int64_t)UINT32_MAX);  // 32-bit item index
   hipLaunchKernelGGL(rope_bwd_kernel, dim3((unsigned)qlora_cdiv(total, 256)), dim3(256), 0,
                      (hipStream_t)stream, a);
   return qlora_launch_status();
