@@ -36,6 +36,13 @@ __device__ __forceinline__ uint16_t f2h_bits(float f) {
 __device__ __forceinline__ uint32_t pack2h(float a, float b) {
   return (uint32_t)f2h_bits(a) | ((uint32_t)f2h_bits(b) << 16);
 }
+// SwiGLU's sigmoid, 1 / (1 + 2^(-g log2 e)) with the hardware exp2 and reciprocal (v_exp_f32,
+// v_rcp_f32, about 1 ulp each in fp32): g -> -inf gives 1 / inf = 0, g -> +inf gives 1, NaN stays
+// NaN. Every kernel that forms silu(g) uses this one, so their fp16 results agree bit for bit.
+__device__ __forceinline__ float sigmoid_fast(float g) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.4426950408889634f));
+}
+
 __device__ __forceinline__ float lo_h(uint32_t w) { return h2f_bits((uint16_t)(w & 0xFFFFu)); }
 __device__ __forceinline__ float hi_h(uint32_t w) { return h2f_bits((uint16_t)(w >> 16)); }
 

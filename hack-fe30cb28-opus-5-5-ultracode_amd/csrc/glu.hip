@@ -33,11 +33,6 @@ struct VecH<1> {
   static __device__ __forceinline__ T pack(const float (&v)[1]) { return f2h_bits(v[0]); }
 };
 
-// 1 / (1 + e^-g): g -> -inf gives 1 / inf = 0, g -> +inf gives 1 / 1, NaN stays NaN
-__device__ __forceinline__ float sigmoidf(float g) {
-  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.4426950408889634f));
-}
-
 // The thread's row and first column: 32-bit division while the thread count fits (SMALL).
 template <bool SMALL>
 __device__ __forceinline__ void row_col(int64_t gid, int64_t per_row, int W, int64_t& row,
@@ -67,7 +62,7 @@ __global__ __launch_bounds__(256) void glu_fwd_kernel(const uint16_t* gu, uint16
   V::unpack(*reinterpret_cast<const T*>(src), g);
   V::unpack(*reinterpret_cast<const T*>(src + I), u);
 #pragma unroll
-  for (int i = 0; i < W; ++i) o[i] = g[i] * sigmoidf(g[i]) * u[i];
+  for (int i = 0; i < W; ++i) o[i] = g[i] * sigmoid_fast(g[i]) * u[i];
   *reinterpret_cast<T*>(m + row * I + col) = V::pack(o);
 }
 
@@ -88,7 +83,7 @@ __global__ __launch_bounds__(256) void glu_bwd_kernel(const uint16_t* dm, uint16
   V::unpack(*reinterpret_cast<const T*>(dm + row * I + col), d);
 #pragma unroll
   for (int i = 0; i < W; ++i) {
-    const float s = sigmoidf(g[i]);
+    const float s = sigmoid_fast(g[i]);
     og[i] = d[i] * u[i] * s * (1.0f + g[i] * (1.0f - s));
     ou[i] = d[i] * g[i] * s;
   }
