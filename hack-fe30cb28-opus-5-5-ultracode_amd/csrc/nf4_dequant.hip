@@ -12,6 +12,8 @@
 // LDS; the per-block absmax byte and absmax2 are shared by the 8 consecutive lanes of a block.
 #include "nf4.h"
 
+#include <hip/hip_ext.h>
+
 namespace qlora {
 
 constexpr int kDequantThreads = 256;
@@ -117,8 +119,10 @@ int make_job(DequantJob& job, const void* packed, const void* absmax, const floa
   return 0;
 }
 
+// start/stop (may be null): events recorded by the dispatch itself at the kernel's start and end
+// (hipExtLaunchKernelGGL), i.e. the kernel's own duration without the launch gap.
 template <int kWPT>
-int launch_wpt(DequantBatch& b, hipStream_t stream) {
+int launch_wpt(DequantBatch& b, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
   constexpr int64_t kTileWords = kDequantThreads * kWPT;
   int64_t tiles = 0;
   for (int i = 0; i < b.count; ++i) {
@@ -127,12 +131,17 @@ int launch_wpt(DequantBatch& b, hipStream_t stream) {
   }
   for (int i = b.count; i <= kMaxJobs; ++i) b.first_tile[i] = tiles;
   QLORA_CHECK_ARG(tiles < (1ll << 31));
-  hipLaunchKernelGGL(nf4_dequant_kernel<kWPT>, dim3((unsigned)tiles), dim3(kDequantThreads), 0,
-                     stream, b);
+  if (start != nullptr || stop != nullptr)
+    hipExtLaunchKernelGGL(nf4_dequant_kernel<kWPT>, dim3((unsigned)tiles),
+                          dim3(kDequantThreads), 0, stream, start, stop, 0, b);
+  else
+    hipLaunchKernelGGL(nf4_dequant_kernel<kWPT>, dim3((unsigned)tiles), dim3(kDequantThreads),
+                       0, stream, b);
   return qlora_launch_status();
 }
 
-int launch(DequantBatch& b, hipStream_t stream) {
+int launch(DequantBatch& b, hipStream_t stream, hipEvent_t start = nullptr,
+           hipEvent_t stop = nullptr) {
   // drop empty jobs, then lay the workgroups of the rest end to end
   int k = 0;
   int64_t words = 0;
@@ -145,10 +154,10 @@ int launch(DequantBatch& b, hipStream_t stream) {
   if (k == 0) return 0;
   // at least ~2048 workgroups (8 per CU) when the launch is big enough for that
   constexpr int64_t kTarget = 2048 * kDequantThreads;
-  if (words >= 8 * kTarget) return launch_wpt<8>(b, stream);
-  if (words >= 4 * kTarget) return launch_wpt<4>(b, stream);
-  if (words >= 2 * kTarget) return launch_wpt<2>(b, stream);
-  return launch_wpt<1>(b, stream);
+  if (words >= 8 * kTarget) return launch_wpt<8>(b, stream, start, stop);
+  if (words >= 4 * kTarget) return launch_wpt<4>(b, stream, start, stop);
+  if (words >= 2 * kTarget) return launch_wpt<2>(b, stream, start, stop);
+  return launch_wpt<1>(b, stream, start, stop);
 }
 
 }  // namespace
@@ -168,6 +177,19 @@ QLORA_API int qlora_nf4_dequant(const void* packed, const void* absmax, const fl
 
 // Up to 32 weights in one launch (a layer's four, or those of eight layers): argument arrays of
 // length `count`, entry i as in qlora_nf4_dequant.
+// qlora_nf4_dequant_many that also records two events at the kernel's own start and end (the
+// dispatch timestamps rocprof reads), for callers that time the kernel without its launch gap.
+// start/stop: hipEvent_t created with timing, or null. No reference counterpart (measurement).
+QLORA_API int qlora_nf4_dequant_many_timed(int32_t count, const void* const* packed,
+                                           const void* const* absmax, const float* const* code2,
+                                           const float* const* absmax2,
+                                           const float* const* offsets, const float* const* code,
+                                           void* const* out, const int64_t* n_blocks,
+                                           const int32_t* nested, const int32_t* standard,
+                                           const int32_t* bs1, const int32_t* bs2,
+                                           const int64_t* seg1, const int64_t* seg2,
+                                           void* stream, void* start, void* stop);
+
 QLORA_API int qlora_nf4_dequant_many(int32_t count, const void* const* packed,
                                      const void* const* absmax, const float* const* code2,
                                      const float* const* absmax2, const float* const* offsets,
@@ -176,6 +198,20 @@ QLORA_API int qlora_nf4_dequant_many(int32_t count, const void* const* packed,
                                      const int32_t* standard, const int32_t* bs1,
                                      const int32_t* bs2, const int64_t* seg1,
                                      const int64_t* seg2, void* stream) {
+  return qlora_nf4_dequant_many_timed(count, packed, absmax, code2, absmax2, offsets, code, out,
+                                      n_blocks, nested, standard, bs1, bs2, seg1, seg2, stream,
+                                      nullptr, nullptr);
+}
+
+QLORA_API int qlora_nf4_dequant_many_timed(int32_t count, const void* const* packed,
+                                           const void* const* absmax, const float* const* code2,
+                                           const float* const* absmax2,
+                                           const float* const* offsets, const float* const* code,
+                                           void* const* out, const int64_t* n_blocks,
+                                           const int32_t* nested, const int32_t* standard,
+                                           const int32_t* bs1, const int32_t* bs2,
+                                           const int64_t* seg1, const int64_t* seg2,
+                                           void* stream, void* start, void* stop) {
   QLORA_CHECK_ARG(count >= 0 && count <= kMaxJobs);
   QLORA_CHECK_ARG(count == 0 || (packed && absmax && code2 && absmax2 && offsets && code &&
                                  out && n_blocks && nested && standard && bs1 && bs2 && seg1 &&
@@ -187,5 +223,6 @@ QLORA_API int qlora_nf4_dequant_many(int32_t count, const void* const* packed,
                           code[i], out[i], n_blocks[i], nested[i], standard[i], bs1[i], bs2[i],
                           seg1[i], seg2[i]))
       return rc;
-  return launch(b, (hipStream_t)stream);
+  return launch(b, (hipStream_t)stream, static_cast<hipEvent_t>(start),
+                static_cast<hipEvent_t>(stop));
 }

@@ -202,6 +202,21 @@ int qlora_nf4_dequant_many(int32_t count, const void* const* packed, const void*
                            const int64_t* seg1, const int64_t* seg2, void* stream);
 
 /*
+ * qlora_nf4_dequant_many that also records start/stop (hipEvent_t created with timing, or null)
+ * at the kernel's own start and end (the dispatch's timestamps, as a profiler reads them, without
+ * the launch gap an event pair around the call also measures). No reference counterpart: the
+ * bench's per-launch timing of the step's dequant.
+ */
+int qlora_nf4_dequant_many_timed(int32_t count, const void* const* packed,
+                                 const void* const* absmax, const float* const* code2,
+                                 const float* const* absmax2, const float* const* offsets,
+                                 const float* const* code, void* const* out,
+                                 const int64_t* n_blocks, const int32_t* nested,
+                                 const int32_t* standard, const int32_t* bs1, const int32_t* bs2,
+                                 const int64_t* seg1, const int64_t* seg2, void* stream,
+                                 void* start, void* stop);
+
+/*
  * NF4 dequantisation fused into an fp16 MFMA GEMM (fp32 accumulation) with a frozen NF4 weight
  * W [w_rows, w_cols] in the layout of qlora_nf4_dequant (same absmax/code2/absmax2/offsets/
  * segment arguments):

@@ -586,3 +586,24 @@ def test_lora_other_ranks(pkg, n, H, Nq, Nv, r):
     test_lora_fwd_rows(pkg, n, H, Nq, Nv, r)
     test_lora_bwd_rows(pkg, n, H, Nq, Nv, r)
     test_lora_grad(pkg, n, H, Nq, Nv, r)
+
+
+def test_dequant_timed_form(pkg):
+    """The timed form writes what the plain launch writes, and its events (recorded by the
+    dispatch at the kernel's start and end) lie inside a pair recorded around the call."""
+    import ctypes
+    rng = np.random.default_rng(3)
+    w = (rng.standard_normal((1536, 1536)) * 0.02).astype(np.float16)
+    packed, st = ON.quantize_nf4(w)
+    item = pkg.ops.NF4Weight(_device_state(packed, st))
+    want = pkg.ops.dequant_many([item], torch.device(DEV))[0]
+    timer = pkg.profiling.LaunchTimer("qlora_nf4_dequant_many")
+    outer0, outer1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with timer:
+        outer0.record()
+        got = pkg.ops.dequant_many([item], torch.device(DEV))[0]
+        outer1.record()
+    torch.cuda.synchronize()
+    assert torch.equal(bits16(got), bits16(want))
+    s = timer.summary()
+    assert s["launches"] == 1 and 0 < s["avg_us"] <= outer0.elapsed_time(outer1) * 1e3
