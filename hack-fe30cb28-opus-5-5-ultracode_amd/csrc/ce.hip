@@ -123,25 +123,36 @@ __device__ __forceinline__ Online fold16(const float (&x)[kCePerThread], int64_t
   return st;
 }
 
-__device__ __forceinline__ Online shfl_online(const Online& a, int off) {
-  Online b;
-  b.m = __shfl_xor(a.m, off, kWave);
-  b.s = __shfl_xor(a.s, off, kWave);
-  b.t = __shfl_xor(a.t, off, kWave);
-  b.best = __shfl_xor(a.best, off, kWave);
-  b.idx = __shfl_xor(a.idx, off, kWave);
-  return b;
+// The wavefront's state from its lanes' states, identical in every lane: the maximum first (a
+// butterfly of fmaxf, exact), each lane's sums rescaled to it once, then butterflies of fp32 adds
+// (a + b and b + a are the same float, so both lanes of a pair, and in the end all 64, hold the
+// same bits) and of the best logit with its first column. One exponential per lane, where
+// merging the full states level by level takes two per level.
+__device__ __forceinline__ Online wave_state(const Online& st) {
+  float m = st.m;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, kWave));
+  const float f = rescale(st.m, m);
+  float s = st.s * f, t = st.t * f, best = st.best;
+  int32_t idx = st.idx;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    s += __shfl_xor(s, off, kWave);
+    t += __shfl_xor(t, off, kWave);
+    const float ob = __shfl_xor(best, off, kWave);
+    const int32_t oi = __shfl_xor(idx, off, kWave);
+    const bool take = ob > best || (ob == best && oi < idx);
+    best = take ? ob : best;
+    idx = take ? oi : idx;
+  }
+  return {m, s, t, best, idx};
 }
 
 // The block's state, identical in every thread. `buf` alternates between two LDS slots so one
 // barrier per block suffices.
 __device__ __forceinline__ Online block_state(Online st, Online (*part)[kCeThreads / kWave],
                                               int buf) {
-#pragma unroll
-  for (int off = 1; off < kWave; off <<= 1) {
-    const Online o = shfl_online(st, off);
-    st = ((threadIdx.x & off) == 0) ? merge(st, o) : merge(o, st);
-  }
+  st = wave_state(st);
   if ((threadIdx.x & (kWave - 1)) == 0) part[buf][threadIdx.x / kWave] = st;
   __syncthreads();
   Online r = part[buf][0];
@@ -286,12 +297,7 @@ __global__ __launch_bounds__(kRowThreads) void ce_rows_kernel(uint16_t* logits, 
       }
     }
     // the block's state as block_state forms it: wavefront butterfly, then the four waves
-    Online st = fold16(x, b0, t);
-#pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-      const Online o = shfl_online(st, off);
-      st = ((t & off) == 0) ? merge(st, o) : merge(o, st);
-    }
+    const Online st = wave_state(fold16(x, b0, t));
     if ((t & (kWave - 1)) == 0) wpart[b][t / kWave] = st;
   }
   mine = wave_sum(mine);

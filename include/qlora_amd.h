@@ -101,7 +101,7 @@ int qlora_rms_fwd(const float* x, const void* delta, const void* w, int32_t w_ha
  *   dx16 (optional, may be null) f16 [n,H] = fp16(dx), the operand of the next dY W product
  *   (engine.py:1238 and 1301 round the gradient to fp16 before it).
  *   keep (may be null) u8 [n][2][ceil(H/4)]: the masks qlora_rms_fwd stored for these rows
- *   (same tok, seed and counters); null: drawn again from (seed, ctr_q, ctr_v).
+ *   (same tok, seed, counters and drop_q/drop_v); null: drawn again from (seed, ctr_q, ctr_v).
  */
 int qlora_rms_bwd(const void* dy, const void* tq, const void* tv, const float* x,
                   const float* rstd, const void* w, int32_t w_half, const float* dres, float* dx,
