@@ -552,10 +552,12 @@ def test_lora_fwd_rows(pkg, n, H, Nq, Nv, r=16):
 
 @pytest.mark.parametrize("n,H,Nq,Nv", [(300, 1536, 1536, 256), (1, 1536, 1536, 256),
                                        (129, 256, 256, 128), (4100, 896, 896, 128),
-                                       (0, 256, 256, 128)])
+                                       (0, 256, 256, 128), (70, 250, 250, 66)])
 def test_lora_grad(pkg, n, H, Nq, Nv, r=16):
     """dB = s g^T x and dA = dx^T a of both adapters (engine.py:1327, 1329) against fp64 sums of
-    the same fp16 operands (fp32 accumulation: relative error ~ 1e-6 of the magnitudes)."""
+    the same fp16 operands (fp32 accumulation: relative error ~ 1e-6 of the magnitudes). Widths
+    that are multiples of 8 take the MFMA pass; (70, 250, 250, 66) has rows without whole
+    16-byte chunks and takes the v_dot2 pass."""
     g = torch.Generator().manual_seed(n + 7 + r)
     C = Nq + 2 * Nv
     dqkv = torch.randn(n, C, generator=g).half()
