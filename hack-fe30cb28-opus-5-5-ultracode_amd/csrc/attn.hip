@@ -16,8 +16,8 @@
 //    keeps the lane <-> query ownership, so rescaling O is a per-lane multiply.
 //  * dK/dV compute S = Q K^T (lane <-> key), dV^T = dO^T P and dK^T = Q^T dS.
 // A product that contracts over tokens needs a token-contiguous operand: the forward stages V
-// row-major and reads V^T with ds_read_b64_tr_b16 (tr_operand); K^T (dQ), Q^T and dO^T (dK/dV)
-// are transposed while being staged into LDS. The P/dS operand comes
+// and dQ stages K row-major and read V^T / K^T with ds_read_b64_tr_b16 (tr_operand); Q^T and
+// dO^T (dK/dV) are transposed while being staged into LDS. The P/dS operand comes
 // straight from the accumulator registers, whose rows within each 16-row group are in the
 // order 0-3, 8-11, 4-7, 12-15 for the lower/upper half-wave; the transposed tiles store their
 // tokens in that same slot order (perm16: swap rows 4-7 with 8-11), so no register shuffles
@@ -131,6 +131,13 @@ __device__ __forceinline__ half8_t tr_operand(const uint16_t* t, int k0, int d0,
   const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)(t + o0));
   const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)(t + o1));
   return __builtin_bit_cast(half8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+// A row operand (as ld_rm) of a tt_off tile: the swizzle maps 16 consecutive rows of one chunk
+// to distinct banks too.
+template <int D>
+__device__ __forceinline__ half8_t ld_tt(const uint16_t* t, int row, int chunk) {
+  return *reinterpret_cast<const half8_t*>(t + tt_off<D>(row, chunk));
 }
 
 template <int D>
@@ -459,9 +466,8 @@ __global__ __launch_bounds__(256) void attn_delta_kernel(const uint16_t* dout, c
 template <int D, int G, bool OWN_DELTA>
 __global__ __launch_bounds__(64 * G) void attn_dq_kernel(Args a) {
   constexpr int KC = D / 16, DT = D / 32, NT = 64 * G, KB = kTok;
-  __shared__ __align__(16) uint16_t ks[KB * D];
+  __shared__ __align__(16) uint16_t ks[KB * D];  // tt_off: read by rows and transposed
   __shared__ __align__(16) uint16_t vs[KB * D];
-  __shared__ __align__(16) uint16_t kt[D * KB];
   const int sh = blockIdx.x / a.ntiles;  // as the forward
   const int tile = a.ntiles - 1 - (int)(blockIdx.x - sh * a.ntiles);
   const int seq = sh / a.KH, kvh = sh % a.KH;
@@ -481,7 +487,7 @@ __global__ __launch_bounds__(64 * G) void attn_dq_kernel(Args a) {
   const rsrc_t ksrc = rows_rsrc(a.k + (int64_t)start * kvs + kvh * D, L, kvs, D);
   const rsrc_t vsrc = rows_rsrc(a.v + (int64_t)start * kvs + kvh * D, L, kvs, D);
 
-  PairStage<D, KB, NT> sk;  // K into both the row tile and the transposed tile
+  RowStage<D, KB, NT, true> sk;  // K: one tile for S^T = K Q^T and K^T (tr_operand)
   RowStage<D, KB, NT> sv;
   sk.load(ksrc, kb0 * KB, kvs_b, tid);
   sv.load(vsrc, kb0 * KB, kvs_b, tid);
@@ -519,7 +525,7 @@ __global__ __launch_bounds__(64 * G) void attn_dq_kernel(Args a) {
   for (int kb = kb0; kb < kb1; ++kb) {
     const int k0 = kb * KB;
     __syncthreads();
-    sk.store(kt, ks, tid);
+    sk.store(ks, tid);
     sv.store(vs, tid);
     __syncthreads();
     sk.load(ksrc, k0 + KB, kvs_b, tid);
@@ -528,7 +534,7 @@ __global__ __launch_bounds__(64 * G) void attn_dq_kernel(Args a) {
 #pragma unroll
     for (int kk = 0; kk < KC; ++kk) {
       const int row = lane & 31, ch = 2 * kk + (lane >> 5);
-      const half8_t kop = ld_rm<D>(ks, row, ch), vop = ld_rm<D>(vs, row, ch);
+      const half8_t kop = ld_tt<D>(ks, row, ch), vop = ld_rm<D>(vs, row, ch);
       s = mfma(kop, qr[kk], s);
       dp = mfma(vop, dr[kk], dp);
     }
@@ -545,8 +551,8 @@ __global__ __launch_bounds__(64 * G) void attn_dq_kernel(Args a) {
     for (int kk = 0; kk < 2; ++kk) sb[kk] = to_b(s, kk);
 #pragma unroll
     for (int u = 0; u < DT; ++u) {
-      const half8_t t0 = ld_tr<KB>(kt, 32 * u + (lane & 31), lane >> 5);
-      const half8_t t1 = ld_tr<KB>(kt, 32 * u + (lane & 31), 2 + (lane >> 5));
+      const half8_t t0 = tr_operand<D>(ks, 0, 32 * u, lane);
+      const half8_t t1 = tr_operand<D>(ks, 16, 32 * u, lane);
       dq[u] = mfma(t0, sb[0], dq[u]);
       dq[u] = mfma(t1, sb[1], dq[u]);
     }
