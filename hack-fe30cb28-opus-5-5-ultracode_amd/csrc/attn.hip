@@ -15,13 +15,12 @@
 //    and l ^ 32 share a query and combine their maxima with one shuffle), and O^T = V^T P^T
 //    keeps the lane <-> query ownership, so rescaling O is a per-lane multiply.
 //  * dK/dV compute S = Q K^T (lane <-> key), dV^T = dO^T P and dK^T = Q^T dS.
-// A product that contracts over tokens needs a token-contiguous operand: the forward stages V
-// and dQ stages K row-major and read V^T / K^T with ds_read_b64_tr_b16 (tr_operand); Q^T and
-// dO^T (dK/dV) are transposed while being staged into LDS. The P/dS operand comes
-// straight from the accumulator registers, whose rows within each 16-row group are in the
-// order 0-3, 8-11, 4-7, 12-15 for the lower/upper half-wave; the transposed tiles store their
-// tokens in that same slot order (perm16: swap rows 4-7 with 8-11), so no register shuffles
-// are needed.
+// A product that contracts over tokens needs a token-contiguous operand (V^T forward, K^T dQ,
+// Q^T and dO^T dK/dV): the tiles are staged row-major with 16-byte stores and read transposed
+// with ds_read_b64_tr_b16 (tr_operand). The P/dS operand comes straight from the accumulator
+// registers, whose rows within each 16-row group are in the order 0-3, 8-11, 4-7, 12-15 for the
+// lower/upper half-wave; tr_operand hands out the tokens in that same order, so no register
+// shuffles are needed.
 // LDS tiles are XOR-swizzled by 16-byte chunk so that the operand reads (32 rows, same chunk)
 // and the staging writes are spread over the banks.
 //
@@ -86,21 +85,10 @@ __device__ __forceinline__ f32x16 mfma(half8_t a, half8_t b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
-// Token order of the transposed tiles within each aligned group of 16 (self-inverse).
-__device__ __forceinline__ int perm16(int s) {
-  return s ^ ((((s >> 2) ^ (s >> 3)) & 1) * 12);
-}
-
 // [rows][D] tile, 16-byte chunk c of row r at chunk c ^ (r mod D/8).
 template <int D>
 __device__ __forceinline__ int rm_off(int row, int chunk) {
   return row * D + ((chunk ^ (row & (D / 8 - 1))) << 3);
-}
-// [D][S] transposed tile (S = 64 or 32 token slots).
-template <int S>
-__device__ __forceinline__ int tr_off(int d, int slot) {
-  const int sw = S == 64 ? ((d ^ (d >> 3)) & 7) : ((d >> 2) & 3);
-  return d * S + (((slot >> 3) ^ sw) << 3) + (slot & 7);
 }
 
 // [rows][D] tile read transposed by ds_read_b64_tr_b16 (tr_operand): a half-wave reads 4
@@ -144,10 +132,6 @@ template <int D>
 __device__ __forceinline__ half8_t ld_rm(const uint16_t* t, int row, int chunk) {
   return *reinterpret_cast<const half8_t*>(t + rm_off<D>(row, chunk));
 }
-template <int S>
-__device__ __forceinline__ half8_t ld_tr(const uint16_t* t, int d, int chunk) {
-  return *reinterpret_cast<const half8_t*>(t + tr_off<S>(d, 8 * chunk));
-}
 __device__ __forceinline__ half8_t ld_g(const uint16_t* p) {
   return *reinterpret_cast<const half8_t*>(p);
 }
@@ -188,43 +172,6 @@ struct RowStage {
 __device__ __forceinline__ uint32_t word_of(const uint4& x, int i) {
   return i < 2 ? (i == 0 ? x.x : x.y) : (i == 2 ? x.z : x.w);
 }
-
-// PairStage: rows [row0, row0 + S) into the transposed [D][S] tile, token t at slot
-// (t & ~15) | perm16(t & 15), and optionally also into the [S][D] row tile. A work item is a
-// pair of rows x 8 columns (consecutive threads take consecutive column chunks of a row pair).
-template <int D, int S, int NT>
-struct PairStage {
-  static constexpr int CPR = D / 8, TOTAL = (S / 2) * CPR, CNT = (TOTAL + NT - 1) / NT;
-  uint4 x[CNT], y[CNT];
-  __device__ __forceinline__ void load(rsrc_t src, int row0, int stride_b, int tid) {
-#pragma unroll
-    for (int i = 0; i < CNT; ++i) {
-      const int id = tid + i * NT, c = id % CPR, r0 = row0 + 2 * (id / CPR);
-      x[i] = buf_load16(src, (uint32_t)(r0 * stride_b + c * 16));
-      y[i] = buf_load16(src, (uint32_t)((r0 + 1) * stride_b + c * 16));
-    }
-  }
-  __device__ __forceinline__ void store(uint16_t* tr, uint16_t* rows, int tid) const {
-#pragma unroll
-    for (int i = 0; i < CNT; ++i) {
-      const int id = tid + i * NT, c = id % CPR, r0 = 2 * (id / CPR);
-      if (id >= TOTAL) continue;
-      const int slot = (r0 & ~15) | perm16(r0 & 15);
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const uint32_t wa = word_of(x[i], w), wb = word_of(y[i], w);
-        *reinterpret_cast<uint32_t*>(tr + tr_off<S>(8 * c + 2 * w, slot)) =
-            (wa & 0xFFFFu) | (wb << 16);
-        *reinterpret_cast<uint32_t*>(tr + tr_off<S>(8 * c + 2 * w + 1, slot)) =
-            (wa >> 16) | (wb & 0xFFFF0000u);
-      }
-      if (rows != nullptr) {
-        *reinterpret_cast<uint4*>(rows + rm_off<D>(r0, c)) = x[i];
-        *reinterpret_cast<uint4*>(rows + rm_off<D>(r0 + 1, c)) = y[i];
-      }
-    }
-  }
-};
 
 // A resource over rows [0, L) of one head of a token-major [*, stride] fp16 matrix starting at
 // `base` (the sequence's first row, this head's first column).
@@ -641,10 +588,8 @@ constexpr int kKeyWaves = 4;
 template <int D>
 __global__ __launch_bounds__(64 * kKeyWaves) void attn_dkdv_kernel(Args a) {
   constexpr int KC = D / 16, DT = D / 32, NT = 64 * kKeyWaves;
-  __shared__ __align__(16) uint16_t qsm[kTok * D];
-  __shared__ __align__(16) uint16_t qt[D * kTok];
+  __shared__ __align__(16) uint16_t qsm[kTok * D];  // tt_off: read by rows and transposed
   __shared__ __align__(16) uint16_t dsm[kTok * D];
-  __shared__ __align__(16) uint16_t dt[D * kTok];
   __shared__ __align__(16) float lse_s[kTok];
   __shared__ __align__(16) float dl_s[kTok];
   // blockIdx.x = (seq HQ + h) + pairs key tile: the first key tiles of every sequence and head,
@@ -669,7 +614,7 @@ __global__ __launch_bounds__(64 * kKeyWaves) void attn_dkdv_kernel(Args a) {
   const rsrc_t lsrc = make_rsrc(a.lse + (int64_t)h * a.n + start, (uint32_t)L * 4);
   const rsrc_t dlsrc = make_rsrc(a.delta + (int64_t)h * a.n + start, (uint32_t)L * 4);
 
-  PairStage<D, kTok, NT> sq, sd;
+  RowStage<D, kTok, NT, true> sq, sd;
   float lv = 0.f;  // threads 0..31: lse (log2) of query q0 + tid; 32..63: delta of q0 + tid - 32
   const float first = tid < kTok ? 1.f : 0.f;
   auto load = [&](int q0) {
@@ -694,8 +639,8 @@ __global__ __launch_bounds__(64 * kKeyWaves) void attn_dkdv_kernel(Args a) {
 
   for (int q0 = kw0; q0 < L; q0 += kTok) {
     __syncthreads();
-    sq.store(qt, qsm, tid);
-    sd.store(dt, dsm, tid);
+    sq.store(qsm, tid);
+    sd.store(dsm, tid);
     if (tid < 2 * kTok) (tid < kTok ? lse_s : dl_s)[tid & (kTok - 1)] = lv;
     __syncthreads();
     load(q0 + kTok);  // the next block (past the sequence: zeros, not used)
@@ -704,7 +649,7 @@ __global__ __launch_bounds__(64 * kKeyWaves) void attn_dkdv_kernel(Args a) {
 #pragma unroll
     for (int kk = 0; kk < KC; ++kk) {
       const int row = lane & 31, ch = 2 * kk + (lane >> 5);
-      const half8_t qop = ld_rm<D>(qsm, row, ch), dop = ld_rm<D>(dsm, row, ch);
+      const half8_t qop = ld_tt<D>(qsm, row, ch), dop = ld_tt<D>(dsm, row, ch);
       s = mfma(qop, kr[kk], s);
       dp = mfma(dop, vr[kk], dp);
     }
@@ -735,10 +680,10 @@ __global__ __launch_bounds__(64 * kKeyWaves) void attn_dkdv_kernel(Args a) {
     }
 #pragma unroll
     for (int u = 0; u < DT; ++u) {
-      const int d = 32 * u + (lane & 31);
-      const half8_t d0 = ld_tr<kTok>(dt, d, lane >> 5), d1 = ld_tr<kTok>(dt, d, 2 + (lane >> 5));
-      const half8_t q0op = ld_tr<kTok>(qt, d, lane >> 5);
-      const half8_t q1op = ld_tr<kTok>(qt, d, 2 + (lane >> 5));
+      const half8_t d0 = tr_operand<D>(dsm, 0, 32 * u, lane);
+      const half8_t d1 = tr_operand<D>(dsm, 16, 32 * u, lane);
+      const half8_t q0op = tr_operand<D>(qsm, 0, 32 * u, lane);
+      const half8_t q1op = tr_operand<D>(qsm, 16, 32 * u, lane);
       dv[u] = mfma(d0, pb[0], dv[u]);
       dk[u] = mfma(q0op, sb[0], dk[u]);
       dv[u] = mfma(d1, pb[1], dv[u]);
