@@ -160,3 +160,11 @@ def test_concurrent_backward_matches_sequential(pkg):
         res.append((out[:n_few], lse[:, :n_few], dq[:n_few], dk[:n_few], dv[:n_few]))
     for x, y in zip(*res):
         assert torch.equal(x, y)
+
+
+@pytest.mark.parametrize("HQ,KH,D", [(14, 2, 64), (16, 2, 128), (28, 4, 128), (8, 8, 64)])
+def test_concurrent_backward_other_shapes(pkg, HQ, KH, D):
+    """The concurrent backward (few sequences, max_len >= 512: dK/dV beside dQ, delta from its
+    own kernel) at other head sizes and group counts (Qwen2 0.5B 14/2 x 64, 3B 16/2, 7B 28/4,
+    and one q head per kv head) against fp32 SDPA, key ranges unsplit."""
+    _run(pkg, [600, 300], HQ, KH, D, seed=HQ + D, chunk=0)
