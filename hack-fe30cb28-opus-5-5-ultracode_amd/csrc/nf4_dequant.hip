@@ -27,7 +27,7 @@ struct DequantJob {
 
 struct DequantBatch {
   DequantJob job[kMaxJobs];
-  int64_t first_tile[kMaxJobs + 1];  // workgroup ranges of the jobs
+  int32_t first_tile[kMaxJobs + 1];  // workgroup ranges of the jobs (< 2^31)
   int count;
 };
 static_assert(sizeof(DequantBatch) <= 4096, "kernel arguments");
@@ -39,13 +39,13 @@ __global__ __launch_bounds__(kDequantThreads) void nf4_dequant_kernel(DequantBat
   __shared__ float lut[16];
   __shared__ float c2[256];
   __shared__ float offs[3];
-  // the job of this workgroup: the last one whose first tile is at or before it (binary search
-  // over the ascending first_tile; tiles past count repeat the total)
+  // the job of this workgroup: the number of later jobs' first tiles at or before it. A count
+  // over fixed offsets: its scalar loads issue together (a search would chain one round trip per
+  // step before the first data load). Entries past count hold the total, which no tile reaches;
   int j = 0;
 #pragma unroll
-  for (int step = kMaxJobs / 2; step > 0; step >>= 1)
-    if (j + step < b.count && (int64_t)blockIdx.x >= b.first_tile[j + step]) j += step;
-  const DequantJob& job = b.job[j];
+  for (int i = 1; i < kMaxJobs; ++i) j += (int)blockIdx.x >= b.first_tile[i] ? 1 : 0;
+  const DequantJob job = b.job[j];  // by value: its fields are loaded once
   const NF4Ref& w = job.w;
   const int t = threadIdx.x;
   // the words and their block scales' inputs first (their latency then overlaps the table fill)
@@ -125,12 +125,14 @@ template <int kWPT>
 int launch_wpt(DequantBatch& b, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
   constexpr int64_t kTileWords = kDequantThreads * kWPT;
   int64_t tiles = 0;
+  for (int i = 0; i < b.count; ++i) tiles += qlora_cdiv(b.job[i].n_words, kTileWords);
+  QLORA_CHECK_ARG(tiles < (1ll << 31));
+  tiles = 0;
   for (int i = 0; i < b.count; ++i) {
-    b.first_tile[i] = tiles;
+    b.first_tile[i] = (int32_t)tiles;
     tiles += qlora_cdiv(b.job[i].n_words, kTileWords);
   }
-  for (int i = b.count; i <= kMaxJobs; ++i) b.first_tile[i] = tiles;
-  QLORA_CHECK_ARG(tiles < (1ll << 31));
+  for (int i = b.count; i <= kMaxJobs; ++i) b.first_tile[i] = (int32_t)tiles;
   if (start != nullptr || stop != nullptr)
     hipExtLaunchKernelGGL(nf4_dequant_kernel<kWPT>, dim3((unsigned)tiles),
                           dim3(kDequantThreads), 0, stream, start, stop, 0, b);
