@@ -1,24 +1,32 @@
 """Benchmark: full Qwen2.5-1.5B NF4 + LoRA training steps on one MI355X.
 
-A step = forward + backward (intermediates kept per the reference's memory-cap plan, or
-recomputed) + fp16 loss scaling (GradScaler) + fused AdamW on the LoRA parameters, over one synthetic batch of 4 packed sequences with lengths ~ U[256, 1024]
-and random token ids (first 25% of each sequence unsupervised). Random-init weights of the
-Qwen2.5-1.5B architecture, all linears NF4 double-quant (blocksize 64), tied fp16 embedding.
+A step = forward + backward with per-layer recompute (each decoder layer keeps only its input
+and recomputes its forward in backward, as config 5 states) + fp16 loss scaling (GradScaler) +
+fused AdamW on the LoRA parameters, over one synthetic batch of 4 packed sequences with lengths
+~ U[256, 1024] and random token ids (first 25 % of each sequence unsupervised). Random-init
+weights of the Qwen2.5-1.5B architecture, all linears NF4 double-quant (blocksize 64), tied
+fp16 embedding. `value` = tokens/s over the K timed steps, inputs resident in HBM.
 
-Prints ONE JSON line: value = tokens/s over the K timed steps (inputs resident in HBM), plus
-  roofline      the dominant hand-written kernel, achieved vs MI355X peak, measured with HIP
-                events around each of its launches in one extra (untimed) step
-  cpu_baseline  the CPU oracle step (oracle.step, plain PyTorch fp32 autograd) on this host's
-                cores, on a bounded sample (embedding + 2 layers + head, and the head alone),
-                scaled to a 28-layer step
+Beside it, on the same JSON line:
+  loss_curve     the loss of steps 1..64 from the random init (warmup and timed steps included)
+  keep_all       the same step with every layer keeping its intermediates (no recompute)
+  roofline       the step's NF4 dequant launches (the north star's dequant GB/s); roofline_mfma:
+                 the attention kernels against the fp16 MFMA peak (algorithmic flops of the
+                 batch's causal pairs)
+  config1..4     BASELINE configs 1-4 on the GPU (dequant GB/s; MLP, attention-input block and
+                 LM-head TFLOP/s on their algorithmic work), each with its CPU oracle time
+  cpu_baseline   one full 28-layer step of the CPU oracle (oracle.step, torch fp32 autograd) on
+                 this host's cores from the same init and batch as the GPU's first step, with
+                 the two steps' loss and LoRA gradients compared
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--policy plan|recompute|keep]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--policy recompute|keep]
 """
 
 import argparse
 import importlib
 import json
 import os
+import statistics
 import sys
 import time
 
@@ -30,6 +38,11 @@ PKG_NAME = "hack-fe30cb28-opus-5-5-ultracode_amd"
 
 HBM_PEAK_GBS = 8000.0
 FP16_PEAK_TFLOPS = 2500.0
+CURVE_STEPS = 64
+
+
+def log(msg):
+    print("[bench] " + msg, file=sys.stderr, flush=True)
 
 
 def make_batches(count, vocab, seed=0, rows=4, lo=256, hi=1024, device="cuda"):
@@ -75,14 +88,87 @@ class Trainer:
         return loss
 
 
-def measure_kernel(pkg, trainer, batch, which):
-    """Average duration and algorithmic work of every launch of the dominant kernel in one step,
-    from HIP events recorded on the launch stream around each launch."""
-    timer = pkg.profiling.LaunchTimer(which)
-    with timer:
-        trainer.step(batch)
+def first_step(model, batch, scale=2.0**16):
+    """Loss and LoRA gradients of one step from the current state, backward through a loss
+    scaled by `scale` as the trainer does, gradients unscaled; the dropout generator is put back
+    where it was, so the first training step draws the same masks."""
+    ids, mask, labels, denom, _, meta = batch
+    gen = model.dropout.gen if model.dropout is not None else None
+    seed, offset = (gen.initial_seed(), gen.get_offset()) if gen is not None else (0, 0)
+    loss, packed, _ = model.step(ids, mask, labels, denom, **meta)
+    (loss * scale).backward()
+    grads = [p.grad.detach().clone() / scale for p in model.parameters()]
+    for p in model.parameters():
+        p.grad = None
+    ok = packed.metadata_ok
+    if gen is not None:
+        gen.set_offset(offset)
     torch.cuda.synchronize()
-    return timer.summary()
+    return {"loss": float(loss), "grads": grads, "seed": seed, "offset": offset,
+            "metadata_ok": None if ok is None else bool(ok)}
+
+
+def causal_pairs(lengths):
+    return sum(L * (L + 1) // 2 for L in lengths)
+
+
+def measure_step_kernels(pkg, trainer, batch, cfg):
+    """One extra (untimed) step with HIP events around every launch of the dequant and the
+    attention entry points: the dequant's achieved GB/s (dispatch-recorded events), and the
+    attention forward / backward TFLOP/s on the batch's causal pairs (fwd: QK^T and PV, 4 D
+    flops per pair and head; bwd: S, dP, dQ, dK, dV, 10 D flops per pair and head)."""
+    P = pkg.profiling
+    pairs = causal_pairs(batch[5]["lengths"])
+    heads, D = cfg.num_attention_heads, cfg.head_dim
+    fwd = P.LaunchTimer("qlora_attn_fwd_split", bound="mfma")
+    bwd = P.LaunchTimer("qlora_attn_bwd_split", bound="mfma")
+    dq = P.LaunchTimer(P.DOMINANT)
+    with dq:
+        with fwd:
+            with bwd:
+                trainer.step(batch)
+    torch.cuda.synchronize()
+    n_f, n_b = len(fwd.records), len(bwd.records)
+    return dq.summary(), [
+        dict(fwd.summary(work_total=4.0 * D * heads * pairs * n_f), kernel="attn_fwd_kernel"),
+        dict(bwd.summary(work_total=10.0 * D * heads * pairs * n_b),
+             kernel="attn_delta + attn_dq + attn_dkdv kernels")]
+
+
+def _median_time(fn, reps, sync=True):
+    ts = []
+    for _ in range(reps):
+        if sync:
+            torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        fn()
+        if sync:
+            torch.cuda.synchronize()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts)
+
+
+def _event_time(fn, reps):
+    fn()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(reps):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) * 1e-3 / reps
+
+
+def _nf4(pkg, g, shape, dev):
+    w = (torch.randn(shape, generator=g, device=dev) * 0.02).half()
+    return pkg.ops.NF4Weight(pkg.quant.quantize_nf4(w))
+
+
+def _mfma_roof(flops, seconds):
+    achieved = flops / seconds / 1e12
+    return {"bound": "mfma", "achieved": achieved, "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": achieved / FP16_PEAK_TFLOPS}
 
 
 def config1(pkg, copies=64, reps=20):
@@ -90,57 +176,165 @@ def config1(pkg, copies=64, reps=20):
     [1536, 1536] (N(0, 0.02) from seed 1, bitsandbytes layout), rotating over `copies`
     independent copies (> 256 MB of Infinity Cache per pass), and the same for the four weights
     of a layer in one launch (qkv | o | gate-up | down, the step's dequant). Beside them a plain
-    device copy of the q_proj output size: the calibration kernel for the FETCH_SIZE /
-    WRITE_SIZE counter runs. Returns a dict of achieved GB/s (algorithmic bytes / event time)."""
+    device copy of 1 GiB (512 MiB read, 512 MiB written): the calibration kernel of the
+    FETCH_SIZE / WRITE_SIZE counter runs. Returns achieved GB/s (algorithmic bytes / event
+    time) and the CPU oracle's time for the same dequant."""
+    from oracle import nf4 as ON
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev).manual_seed(1)
-
-    def weight(shape):
-        w = (torch.randn(shape, generator=g, device=dev) * 0.02).half()
-        return pkg.ops.NF4Weight(pkg.quant.quantize_nf4(w))
-
-    qs = [weight((1536, 1536)) for _ in range(copies)]
+    qs = [_nf4(pkg, g, (1536, 1536), dev) for _ in range(copies)]
     outs = [torch.empty((1536, 1536), device=dev, dtype=torch.float16) for _ in range(copies)]
     per_q = pkg.profiling._dequant_bytes([None] * 7 + [qs[0].blocks, 1, None, 64, 256,
                                                        2**63 - 1, 2**63 - 1])
-
-    def timed(fn, n):
-        for i in range(min(n, 4)):
-            fn(i)
-        torch.cuda.synchronize()
-        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        s.record()
-        for i in range(n):
-            fn(i)
-        e.record()
-        torch.cuda.synchronize()
-        return s.elapsed_time(e) * 1e-3 / n
-
-    t_q = timed(lambda i: qs[i % copies].dequant_into(outs[i % copies]), copies * reps)
+    t_q = _event_time(lambda: [qs[i].dequant_into(outs[i]) for i in range(copies)], reps) \
+        / copies
     layers = []
-    for i in range(8):
-        grp = lambda shapes: pkg.ops.NF4Group.of([weight(sh) for sh in shapes])  # noqa: E731
-        layers.append([grp([(1536, 1536), (256, 1536), (256, 1536)]), weight((1536, 1536)),
-                       grp([(8960, 1536), (8960, 1536)]), weight((1536, 8960))])
+    for _ in range(8):
+        grp = lambda shapes: pkg.ops.NF4Group.of([_nf4(pkg, g, sh, dev) for sh in shapes])  # noqa
+        layers.append([grp([(1536, 1536), (256, 1536), (256, 1536)]),
+                       _nf4(pkg, g, (1536, 1536), dev), grp([(8960, 1536), (8960, 1536)]),
+                       _nf4(pkg, g, (1536, 8960), dev)])
     per_layer = sum(pkg.profiling._dequant_bytes(
         [None] * 7 + [w.blocks, 1, None, 64, 256, getattr(w, "seg1", 2**63 - 1),
                       getattr(w, "seg2", 2**63 - 1)]) for w in layers[0])
-    t_l = timed(lambda i: pkg.ops.dequant_many(layers[i % 8], dev), 8 * reps)
-    src = torch.empty(1536 * 1536, device=dev, dtype=torch.float16).normal_()
+    t_l = _event_time(lambda: [pkg.ops.dequant_many(layers[i], dev) for i in range(8)], reps) / 8
+    src = torch.empty(256 * 2**20, device=dev, dtype=torch.float16).normal_()
     dst = torch.empty_like(src)
-    t_c = timed(lambda i: dst.copy_(src), copies * reps)
+    t_c = _event_time(lambda: dst.copy_(src), reps)
+    # the CPU oracle's dequant of the same weight (numpy, bit-exact restatement)
+    w0 = qs[0]
+    st = ON.QuantState(w0.absmax.cpu().numpy(), (1536, 1536), w0.code.cpu().numpy(), 64,
+                       offset=w0.offset.cpu().numpy()[0],
+                       state2=ON.QuantState2(w0.absmax2.cpu().numpy(), w0.code2.cpu().numpy(),
+                                             256))
+    packed = w0.packed.cpu().numpy().reshape(-1)
+    t_cpu = _median_time(lambda: ON.dequantize_nf4(packed, st), 5, sync=False)
     return {"q_proj_dequant_GBs": per_q / t_q / 1e9, "q_proj_bytes": per_q,
             "q_proj_us": t_q * 1e6, "layer_dequant_GBs": per_layer / t_l / 1e9,
             "layer_bytes": per_layer, "layer_us": t_l * 1e6,
-            "copy_GBs": 2 * src.numel() * 2 / t_c / 1e9, "copies": copies}
+            "copy_GBs": 2 * src.numel() * 2 / t_c / 1e9, "copy_bytes": 2 * src.numel() * 2,
+            "copies": copies,
+            "cpu": {"q_proj_ms": t_cpu * 1e3, "GBs": per_q / t_cpu / 1e9, "threads": 1,
+                    "kind": "port (oracle.nf4, numpy)"}}
 
 
-def config4(pkg, reps=3):
+def config2(pkg, reps=10):
+    """x [2048, 1536] ~ N(0, 1), NF4 [gate|up] [17920, 1536] and down
+    [1536, 8960] (N(0, 0.02), seed 2); forward h = silu(gate) up, y = h W_d^T; backward w.r.t.
+    x with dy ~ N(0, 1): dh = dy W_d, [dg|du] = SwiGLU', dx = [dg|du] W_gu. Four products,
+    338.2 GFLOP; the NF4 decode of both weights (the layer-wide dequant, or inside the fused
+    GEMM) is in the timed region. CPU: oracle.ops.mlp on the same values."""
+    from oracle import ops as O
+    L, ops = pkg.linear, pkg.ops
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(2)
+    gu_w = ops.NF4Group.of([_nf4(pkg, g, (8960, 1536), dev), _nf4(pkg, g, (8960, 1536), dev)])
+    wd = _nf4(pkg, g, (1536, 8960), dev)
+    x = torch.randn(2048, 1536, generator=g, device=dev).half()
+    dy = torch.randn(2048, 1536, generator=g, device=dev).half()
+    I = 8960
+
+    def run():
+        with L.reuse_dequant():
+            L.dequant_layer([gu_w, wd])
+            gu = L.nf4_linear(x, gu_w)
+            h = ops._glu_fwd(gu, I)
+            y = L.nf4_linear(h, wd)
+            dh = L.nf4_linear_t(dy, wd)
+            ops._glu_bwd(dh, gu, I)
+            dx = L.nf4_linear_t(gu, gu_w)
+        return y, dx
+
+    flops = 2.0 * 2048 * 1536 * (2 * I) * 2 + 2.0 * 2048 * I * 1536 * 2
+    t = _event_time(run, reps)
+    wg, wdd = L.dequantize(gu_w).cpu(), L.dequantize(wd).cpu()
+    xc, dyc = x.cpu(), dy.cpu()
+    t_cpu = _median_time(lambda: O.mlp(xc, wg, wdd, dyc), 3, sync=False)
+    return {"ms": t * 1e3, "gflop": flops / 1e9, "TFLOPs": flops / t / 1e12,
+            "roofline": _mfma_roof(flops, t), "backend": L.BACKEND,
+            "cpu": {"ms": t_cpu * 1e3, "TFLOPs": flops / t_cpu / 1e12,
+                    "threads": torch.get_num_threads(), "kind": "port (oracle.ops.mlp)"}}
+
+
+def config3(pkg, reps=10):
+    """the attention-input block (engine.attn_input_fwd/_bwd: input RMSNorm
+    with both LoRA-dropout copies, NF4 qkv projection + bias, LoRA r 16 on q and v, RoPE) on 4
+    packed sequences with lengths ~ U[128, 1024] (seed 3), hidden 1536, 12/2 heads of 128,
+    forward and backward (dh and the four LoRA gradients). Work: the qkv GEMMs, 4 N 1536 2048
+    flops (forward and dX); HBM bytes of the RMSNorm forward (15,364 per token) and the RoPE
+    forward (11,776 per token) from events around their launches. CPU: oracle.step.attn_input
+    with autograd on the same sizes."""
+    import numpy as np
+
+    from oracle import step as OS
+    E, P = pkg.engine, pkg.profiling
+    dev = torch.device("cuda:0")
+    cfg = E.Qwen2Config(num_hidden_layers=1, vocab_size=1000)
+    model = E.random_qwen2(cfg, dev, seed=3)
+    spec = model.layers[0]
+    H, HQ, HKV, D = cfg.hidden_size, cfg.num_attention_heads, cfg.num_key_value_heads, \
+        cfg.head_dim
+    gl = torch.Generator().manual_seed(3)
+    lengths = torch.randint(128, 1025, (4,), generator=gl).tolist()
+    T = max(lengths)
+    mask = (torch.arange(T)[None] < torch.tensor(lengths)[:, None]).long()
+    ids = torch.zeros_like(mask)
+    packed = E.Packed(ids.to(dev), mask.to(dev), torch.full_like(ids, -100).to(dev), model.rope,
+                      model.dropout, model.dropout_p, lengths=lengths, n_supervised=0)
+    n = packed.n
+    seeds = (packed.draw(H), packed.draw(H))
+    g = torch.Generator(device=dev).manual_seed(4)
+    h = torch.randn(n, H, generator=g, device=dev)
+    dq = torch.randn(n, HQ, D, generator=g, device=dev).half()
+    dk = torch.randn(n, HQ, D, generator=g, device=dev).half()
+    dv = torch.randn(n, HQ, D, generator=g, device=dev).half()
+    lora = [t.detach().half() for t in spec.lora_params()]
+    lora_t = [t.t().contiguous() for t in lora]
+
+    def run():
+        with pkg.linear.reuse_dequant():
+            pkg.linear.dequant_layer([spec.qkv])
+            q, k, v, saved = E.attn_input_fwd(spec, h, packed, lora, seeds)
+            return E.attn_input_bwd(spec, dq, dk, dv, h, saved, packed, lora_t, seeds)
+
+    t = _event_time(run, reps)
+    flops = 4.0 * n * H * (HQ + 2 * HKV) * D
+    rms = P.LaunchTimer("qlora_rms_fwd", work=lambda a: 15364.0 * a[10], bound="hbm")
+    rope = P.LaunchTimer("qlora_rope_fwd", work=lambda a: 11776.0 * a[10], bound="hbm")
+    with rms, rope:
+        run()
+    # CPU: the block with autograd on the same sizes
+    cpu = OS.CpuQwen2(model).layers[0]
+    hc = h.cpu()
+    cos, sin = OS.rope_cos_sin(packed.pos.cpu().long(), D, cfg.rope_theta)
+    keep = torch.rand(n, H) >= model.dropout_p
+    dqc, dkc, dvc = dq.cpu().float(), dk.cpu().float(), dv.cpu().float()
+    kscale = float(np.float32(1.0 / (1 - model.dropout_p)))
+
+    def cpu_run():
+        hr = hc.clone().requires_grad_()
+        qo, ko, vo = OS.attn_input(cpu, hr, (keep, keep), kscale, cos, sin, HQ, HKV, D,
+                                   cfg.rms_norm_eps)
+        rep = HQ // HKV
+        ((qo * dqc).sum() + (ko.repeat_interleave(rep, 1) * dkc).sum()
+         + (vo.repeat_interleave(rep, 1) * dvc).sum()).backward()
+
+    t_cpu = _median_time(cpu_run, 3, sync=False)
+    return {"lengths": lengths, "tokens": n, "ms": t * 1e3, "gemm_gflop": flops / 1e9,
+            "TFLOPs": flops / t / 1e12, "roofline": _mfma_roof(flops, t),
+            "rms_fwd": rms.summary(), "rope_fwd": rope.summary(),
+            "cpu": {"ms": t_cpu * 1e3, "threads": torch.get_num_threads(),
+                    "kind": "port (oracle.step.attn_input + autograd)"}}
+
+
+def config4(pkg, reps=3, cpu_rows=256):
     """BASELINE config 4 on the GPU: LM head loss over hidden [2048, 1536] (N(0, 1)) and the
     tied embedding [151936, 1536] (N(0, 0.02)), ~25 % of the labels ignored, with the hidden and
-    embedding gradients: vocabulary pieces of 8192 (online softmax, head.chunked_head: logits,
-    the dh accumulation, recomputed logits, dE; 4 products of 2 T V H flops) and whole rows
-    (head.full_head: logits, G E, G^T h; 3 products)."""
+    embedding gradients: vocabulary pieces of 8192 (online softmax, head.chunked_head) and whole
+    rows (head.full_head). Algorithmic work: the logits over all T rows (2 T V H) and the dh and
+    dE products over the supervised rows (2 n_sup V H each). CPU: the oracle's cross-entropy
+    with autograd over `cpu_rows` rows (logits, loss, dh, dE), scaled to T rows."""
+    from oracle import ops as O
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev).manual_seed(4)
     T, V, H = 2048, 151936, 1536
@@ -149,9 +343,10 @@ def config4(pkg, reps=3):
     targets = torch.randint(0, V, (T,), generator=g, device=dev)
     targets[torch.rand(T, generator=g, device=dev) < 0.25] = -100
     denom = float((targets >= 0).sum())
-    out = {}
-    for name, fn, products in (("pieces", pkg.head.chunked_head, 4),
-                               ("whole_rows", pkg.head.full_head, 3)):
+    n_sup = int(denom)
+    flops = 2.0 * T * V * H + 2 * (2.0 * n_sup * V * H)
+    out = {"gflop": flops / 1e9, "n_supervised": n_sup}
+    for name, fn in (("pieces", pkg.head.chunked_head), ("whole_rows", pkg.head.full_head)):
         fn(hn, E, targets, denom)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
@@ -159,42 +354,51 @@ def config4(pkg, reps=3):
             r = fn(hn, E, targets, denom)
         torch.cuda.synchronize()
         dt = (time.perf_counter() - t0) / reps
-        flops = products * 2.0 * T * V * H
-        out[name] = {"ms": dt * 1e3, "TFLOPs": flops / dt / 1e12, "loss": float(r.loss)}
+        out[name] = {"ms": dt * 1e3, "TFLOPs": flops / dt / 1e12, "loss": float(r.loss),
+                     "roofline": _mfma_roof(flops, dt)}
+    hc, Ec, tc = hn[:cpu_rows].cpu(), E.cpu().float(), targets[:cpu_rows].cpu()
+
+    def cpu_run():
+        h = hc.float().requires_grad_()
+        w = Ec.clone().requires_grad_()
+        logits = h @ w.t()
+        loss = torch.nn.functional.cross_entropy(logits, tc, ignore_index=-100,
+                                                 reduction="sum") / denom
+        loss.backward()
+        return O  # (the oracle module's formulas are F.cross_entropy's)
+
+    t_cpu = _median_time(cpu_run, 3, sync=False) * T / cpu_rows
+    out["cpu"] = {"ms_scaled_to_T": t_cpu * 1e3, "rows_timed": cpu_rows,
+                  "threads": torch.get_num_threads(), "kind": "port (torch fp32 autograd)"}
     return out
 
 
-def cpu_baseline(pkg, model, batch):
-    """The CPU oracle step on a bounded sample: forward + autograd backward of embedding +
-    2 layers + head, and of the head alone; a 28-layer step is head + 28 x layer."""
+def cpu_step(pkg, model, cpu_model, batch, first):
+    """The CPU oracle's full step (oracle.step.forward_loss + autograd, every layer) on the
+    batch of the GPU's first step, from the same init and dropout generator state: its time is
+    the CPU baseline, its loss and LoRA gradients are compared with the GPU's."""
     from oracle import step as OS
-
     ids, mask, labels, denom, ntok, _ = batch
-    threads = torch.get_num_threads()
-    L = len(model.layers)
-    gen = model.dropout.gen
-    seed, offset = gen.initial_seed(), gen.get_offset()
-    G = model.dropout.max_blocks * 256
-    cpu2 = OS.CpuQwen2(model, layers=[0, 1])
     t0 = time.perf_counter()
-    loss, _ = OS.forward_loss(cpu2, ids, mask, labels, denom, drop_seed=seed,
-                              drop_offset=offset, drop_G=G, p=model.dropout_p, vec=4)
+    loss, _ = OS.forward_loss(cpu_model, ids, mask, labels, denom, drop_seed=first["seed"],
+                              drop_offset=first["offset"], drop_G=model.dropout.max_blocks * 256,
+                              p=model.dropout_p, vec=4)
     loss.backward()
-    t_two = time.perf_counter() - t0
-    cpu0 = OS.CpuQwen2(model, layers=[])
-    n = int(mask.sum())
-    h = torch.randn(n, model.cfg.hidden_size, requires_grad=True)
-    t0 = time.perf_counter()
-    loss0, _ = OS.forward_loss(cpu0, ids, mask, labels, denom, first_layer_input=h)
-    loss0.backward()
-    t_head = time.perf_counter() - t0
-    t_layer = max(t_two - t_head, 1e-9) / 2
-    t_step = t_head + L * t_layer
-    return {"value": ntok / t_step, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": (f"oracle.step (torch fp32 autograd) on {ntok} tokens: embedding + 2 of "
-                       f"{L} layers + head fwd+bwd {t_two:.2f} s, head alone {t_head:.2f} s; "
-                       f"step = head + {L} x layer = {t_step:.2f} s"),
-            "cpu": _cpu_model()}
+    dt = time.perf_counter() - t0
+    rels = []
+    for g_gpu, leaf in zip(first["grads"], cpu_model.lora_leaves()):
+        a, b = g_gpu.cpu().double(), leaf.grad.double()
+        rels.append(float((a - b).norm() / b.norm().clamp_min(1e-30)))
+    L = len(cpu_model.layers)
+    return {"value": ntok / dt, "unit": "tokens/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": (f"one full {L}-layer step of oracle.step (torch fp32 autograd) on the "
+                       f"GPU's first batch ({ntok} tokens), forward + backward: {dt:.2f} s"),
+            "cpu": _cpu_model(),
+            "parity": {"loss_gpu": first["loss"], "loss_cpu": float(loss),
+                       "loss_rel_diff": abs(first["loss"] - float(loss)) / abs(float(loss)),
+                       "lora_grad_rel_norm_max": max(rels), "lora_grads": len(rels),
+                       "tolerance": {"loss": 2e-3, "lora_grad": 2e-2}}}
 
 
 def _cpu_model():
@@ -208,19 +412,32 @@ def _cpu_model():
     return "unknown"
 
 
+def time_steps(trainer, batches, start, count):
+    """Runs `count` steps from batches[start]; returns (tokens, seconds, losses)."""
+    torch.cuda.synchronize()
+    tokens, losses = 0, []
+    t0 = time.perf_counter()
+    for i in range(start, start + count):
+        losses.append(trainer.step(batches[i]).detach())
+        tokens += batches[i][4]
+    torch.cuda.synchronize()
+    return tokens, time.perf_counter() - t0, [float(x) for x in losses]
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--policy", choices=("plan", "recompute", "keep"), default="plan",
-                    help="which layers keep their intermediates for the backward: the "
-                         "reference's memory-cap plan under this GPU's memory (default; every "
-                         "layer keeps them on 288 GB), none (full per-layer recompute) or all")
-    ap.add_argument("--recompute-steps", type=int, default=10,
-                    help="also time this many steps with full per-layer recompute (0: skip)")
+    ap.add_argument("--policy", choices=("recompute", "keep"), default="recompute",
+                    help="recompute (config 5: every layer recomputes its forward in backward) "
+                         "or keep (every layer keeps its intermediates)")
+    ap.add_argument("--keep-steps", type=int, default=10,
+                    help="also time this many steps with every layer keeping its "
+                         "intermediates (0: skip)")
     ap.add_argument("--layers", type=int, default=28)
+    ap.add_argument("--no-configs", action="store_true", help="skip the config 1-4 legs")
     ap.add_argument("--config1", action="store_true",
                     help="only the config-1 dequant measurement (and its copy calibration)")
     args = ap.parse_args()
@@ -238,53 +455,40 @@ def main():
     torch.cuda.manual_seed(0)
     cfg = pkg.engine.Qwen2Config(num_hidden_layers=args.layers)
     model = pkg.engine.random_qwen2(cfg, dev, seed=0)
-    model.keep_all = {"plan": None, "recompute": False, "keep": True}[args.policy]
+    model.keep_all = args.policy == "keep"
     trainer = Trainer(model)
-    batches = make_batches(args.warmup + args.steps + 1, cfg.vocab_size, device=dev)
-    print("[bench] model built; timing the projection GEMM solutions", file=sys.stderr,
-          flush=True)
+    n_batches = max(CURVE_STEPS, args.warmup + args.steps) + 1
+    batches = make_batches(n_batches, cfg.vocab_size, device=dev)
+    log("model built; timing the projection GEMM solutions")
     # every step size config 5 can produce (4 rows of 256..1024 tokens), before any timing
     tune_s = model.tune_gemms(range(4 * 256, 4 * 1024 + pkg.gemm.BUCKET, pkg.gemm.BUCKET),
-                              log=lambda m: print("[bench] " + m, file=sys.stderr, flush=True))
-    print(f"[bench] GEMM tuning {tune_s:.1f} s; warmup {args.warmup}", file=sys.stderr,
-          flush=True)
-    for i in range(args.warmup):
-        trainer.step(batches[i])
-    torch.cuda.synchronize()
-    print("[bench] timing", file=sys.stderr, flush=True)
-    tokens = 0
-    losses = []
-    t0 = time.perf_counter()
-    for i in range(args.warmup, args.warmup + args.steps):
-        losses.append(trainer.step(batches[i]).detach())
-        tokens += batches[i][4]
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    losses = [float(x) for x in losses]
+                              log=log)
+    cpu_model = None
+    if not args.no_cpu:
+        from oracle import step as OS
+        cpu_model = OS.CpuQwen2(model)  # the init's weights, before any optimizer step
+    first = first_step(model, batches[0])
+    log(f"GEMM tuning {tune_s:.1f} s; first step loss {first['loss']:.5f}; warmup {args.warmup}")
+    _, _, warm_losses = time_steps(trainer, batches, 0, args.warmup)
+    log("timing")
+    tokens, elapsed, timed_losses = time_steps(trainer, batches, args.warmup, args.steps)
     value = tokens / elapsed
-    print(f"[bench] {args.steps} steps {elapsed:.3f} s, {value:.0f} tokens/s", file=sys.stderr,
-          flush=True)
-    kept = model.keep_plan(batches[-1][4])
-    recompute = None
-    if args.recompute_steps > 0 and model.keep_all is not False:
-        # the same step with every layer recomputing its forward in backward
-        saved, model.keep_all = model.keep_all, False
-        for i in range(2):
-            trainer.step(batches[i])
-        torch.cuda.synchronize()
-        rtok, t1 = 0, time.perf_counter()
-        for i in range(args.recompute_steps):
-            b = batches[(args.warmup + i) % (len(batches) - 1)]
-            trainer.step(b)
-            rtok += b[4]
-        torch.cuda.synchronize()
-        rel = time.perf_counter() - t1
-        recompute = {"value": rtok / rel, "ms_per_step": 1000.0 * rel / args.recompute_steps,
-                     "steps": args.recompute_steps}
-        model.keep_all = saved
-        print(f"[bench] full recompute: {recompute['value']:.0f} tokens/s", file=sys.stderr,
-              flush=True)
-    roof = measure_kernel(pkg, trainer, batches[-1], pkg.profiling.DOMINANT)
+    log(f"{args.steps} steps {elapsed:.3f} s, {value:.0f} tokens/s")
+    done = args.warmup + args.steps
+    _, _, rest = time_steps(trainer, batches, done, max(0, CURVE_STEPS - done))
+    curve = (warm_losses + timed_losses + rest)[:CURVE_STEPS]
+    kernels = measure_step_kernels(pkg, trainer, batches[-1], cfg)
+    keep = None
+    if args.keep_steps > 0 and args.policy != "keep":
+        model.keep_all = True
+        time_steps(trainer, batches, 0, 2)
+        ktok, kel, _ = time_steps(trainer, batches, args.warmup, args.keep_steps)
+        keep = {"value": ktok / kel, "ms_per_step": 1000.0 * kel / args.keep_steps,
+                "steps": args.keep_steps,
+                "what": "every layer keeps its intermediates and dequantized weights for the "
+                        "backward (no recompute): not config 5, reported beside it"}
+        model.keep_all = args.policy == "keep"
+        log(f"keep-all: {keep['value']:.0f} tokens/s")
     result = {
         "metric": "train tokens/s (1.5B NF4 QLoRA step, 1 GPU); NF4 dequant HBM GB/s",
         "value": value, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
@@ -294,21 +498,27 @@ def main():
         "config": {"workload": "config 5: full Qwen2.5-1.5B NF4+LoRA training step",
                    "batch": "4 packed sequences, lengths U[256,1024]",
                    "tokens": tokens, "layers": args.layers, "parallelism": "single GPU",
-                   "activations": (f"kept for the backward by {kept} of {args.layers} layers "
-                                   "(the reference's memory-cap plan, engine.py:1626-1640, "
-                                   "under this GPU's memory), with their dequantized weights "
-                                   "(each NF4 weight dequantized once per step); the others "
-                                   "recompute their forward")},
+                   "activations": ("per-layer recompute: each layer keeps its input and "
+                                   "recomputes its forward (NF4 dequant included) in backward"
+                                   if args.policy == "recompute" else
+                                   "every layer keeps its intermediates (no recompute)"),
+                   "gemm_backend": pkg.linear.BACKEND},
+        "roofline": kernels[0],
+        "roofline_mfma": kernels[1],
+        "loss_curve": curve,
+        "keep_all": keep,
         "gemm_tuning_s": tune_s,
-        "full_recompute": recompute,
-        "loss_first_last": [losses[0], losses[-1]],
-        "roofline": roof,
-        "config1": config1(pkg),
-        "config4": config4(pkg),
     }
-    if not args.no_cpu:
-        print("[bench] cpu baseline", file=sys.stderr, flush=True)
-        result["cpu_baseline"] = cpu_baseline(pkg, model, batches[-1])
+    if not args.no_configs:
+        for name, fn in (("config1", config1), ("config2", config2), ("config3", config3),
+                         ("config4", config4)):
+            log(name)
+            result[name] = fn(pkg)
+    if cpu_model is not None:
+        log("cpu baseline: the oracle's full step")
+        result["cpu_baseline"] = cpu_step(pkg, model, cpu_model, batches[0], first)
+        if first["metadata_ok"] is not None:
+            result["cpu_baseline"]["parity"]["packing_metadata_ok"] = first["metadata_ok"]
     print(json.dumps(result), flush=True)
 
 

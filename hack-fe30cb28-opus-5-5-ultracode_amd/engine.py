@@ -15,6 +15,7 @@ Everything stays resident in HBM: the reference's host-offload machinery (Weight
 InputStream, GuStream, AttnStream, HostHead, memory-cap planning) has no counterpart here.
 """
 
+import itertools
 import math
 
 import torch
@@ -168,6 +169,14 @@ def from_peft(peft_model, keep_all=None):
     D = getattr(hf, "head_dim", None) or H // HQ
     rope = getattr(hf, "rope_parameters", None) or {}
     theta = getattr(hf, "rope_theta", None) or rope.get("rope_theta", 10000.0)
+    # the rotary tables here are the plain ones, angle = pos * theta^(-2k/D); a scaled variant
+    # (linear, dynamic, YaRN, ...) would train with other positions, so it is refused
+    scaling = getattr(hf, "rope_scaling", None) or {}
+    kinds = {str(d.get(key)) for d in (rope, scaling) for key in ("rope_type", "type")
+             if d.get(key) is not None}
+    if kinds - {"default"}:
+        raise UnsupportedModel(f"rotary embedding type {sorted(kinds)}; the step takes the "
+                               "default (unscaled) rotary embedding only")
     q0 = layers_hf[0].self_attn.q_proj
     qname = names["q"]
     r = int(q0.lora_A[qname].weight.shape[0])
@@ -252,70 +261,92 @@ def _to_device(host, dev):
     return host.pin_memory().to(dev, non_blocking=True)
 
 
+def _read_lengths(attention_mask, labels):
+    """Row lengths and supervised-token count from the device in one read, and whether the mask
+    is right-padded (ones, then zeros)."""
+    B, T = attention_mask.shape
+    mask = attention_mask.bool()
+    lengths = mask.sum(dim=1)
+    right = torch.arange(T, device=mask.device)[None, :] < lengths[:, None]
+    flags = torch.stack([(mask == right).all(),
+                         ((labels[:, 1:] >= 0) & mask[:, :-1]).sum()]).to(torch.int64)
+    host = torch.cat([lengths.to(torch.int64), flags]).tolist()
+    if not host[B]:
+        raise UnsupportedBatch("attention_mask is not right-padded")
+    return host[:B], host[B + 1]
+
+
+def _pack_index(lengths, T):
+    """int64 host vector [4n + B + 1] of a packing with these row lengths in [B, T]: each
+    token's flat index in the batch, the flat index of its next-token label (B*T, a -100
+    sentinel, for a token in a row's last column), its position in its sequence, and
+    cu_seqlens."""
+    B = len(lengths)
+    starts = torch.arange(B, dtype=torch.int64) * T
+    tok = torch.cat([torch.arange(L, dtype=torch.int64) + s for L, s in zip(lengths, starts)]) \
+        if B else torch.zeros((0,), dtype=torch.int64)
+    pos = tok % T
+    nxt = torch.where(pos + 1 < T, tok + 1, torch.full_like(tok, B * T))
+    cu = torch.tensor([0, *itertools.accumulate(lengths)], dtype=torch.int64)
+    return torch.cat([tok, nxt, pos, cu])
+
+
 class Packed:
-    """One micro-batch without its padding: real tokens of every row, back to back."""
+    """A right-padded micro-batch with its padding dropped: the real tokens of all rows, back to
+    back, with the fields the reference's packing provides (engine.py:705-764): tok (each
+    token's index in the padded [B, T] batch), ids, pos (position within its sequence),
+    targets (next-token labels, -100 ignored), head_order (supervised tokens first),
+    n_supervised, cu_seqlens, lengths, max_len, and the rotary tables.
+
+    Whatever follows from the row lengths is computed on the host and reaches the device in one
+    pinned copy. The lengths come from the caller when it has them (`lengths`, `n_supervised`:
+    a collator knows both), which spares the step its one read of the device: a read waits for
+    all queued work, the previous step's backward included, and the GPU then idles while this
+    step's first launches are queued. The caller's metadata is then checked on the device
+    without waiting: `metadata_ok` is a device bool, False when the mask is not right-padded to
+    the given lengths or the supervised count differs (read it when the step is synchronised
+    anyway)."""
 
     def __init__(self, input_ids, attention_mask, labels, rope, dropout, dropout_p, lengths=None,
                  n_supervised=None):
-        """`lengths` (tokens of each row) and `n_supervised` (tokens with a label), when the
-        caller knows them on the host (a collator does), spare the step its one read of device
-        values (lengths, the padding check and the supervised count together): a read waits for
-        all the work queued before it (the previous step's backward), and the GPU then idles
-        while this step's first launches are being queued. Given lengths, the mask is trusted to
-        be right-padded to them."""
         if input_ids.dim() != 2 or attention_mask.shape != input_ids.shape \
                 or labels.shape != input_ids.shape:
             raise UnsupportedBatch("inputs are not [rows, tokens]")
         B, T = input_ids.shape
         dev = input_ids.device
-        if lengths is None:
-            # one read of the device: the row lengths, whether the mask is right-padded to them,
-            # and the supervised count (a token whose next label is not -100)
-            mask = attention_mask.bool()
-            lengths_t = mask.sum(dim=1)
-            expected = torch.arange(T, device=dev)[None, :] < lengths_t[:, None]
-            padded_ok = (mask == expected).all().view(1).to(torch.int64)
-            sup = ((labels[:, 1:] >= 0) & mask[:, :-1]).sum().view(1).to(torch.int64)
-            host = torch.cat([lengths_t.to(torch.int64), padded_ok, sup]).tolist()
-            lengths = host[:B]
-            if not host[B]:
-                raise UnsupportedBatch("attention_mask is not right-padded")
-            if n_supervised is None:
-                n_supervised = host[B + 1]
+        given = lengths is not None
+        if not given:
+            lengths, counted = _read_lengths(attention_mask, labels)
+            n_supervised = counted if n_supervised is None else n_supervised
         lengths = [int(x) for x in lengths]
-        if len(lengths) != B or any(x < 0 or x > T for x in lengths):
+        if len(lengths) != B or any(not 0 <= x <= T for x in lengths):
             raise UnsupportedBatch("lengths do not fit the batch")
-        # packed token -> its index in the padded [B, T] batch, built on the host and copied
-        # without waiting for the device
-        parts = [torch.arange(b * T, b * T + x, dtype=torch.int64) for b, x in enumerate(lengths)]
-        flat_host = torch.cat(parts) if parts else torch.zeros((0,), dtype=torch.int64)
-        flat = _to_device(flat_host, dev)
-        self.n = int(flat_host.numel())
-        self.tok = flat  # each packed token's index in the padded [B, T] batch (int64)
-        self.T = T
-        self.rows = B
-        self.lengths = lengths
-        self.max_len = max(self.lengths) if self.lengths else 0
-        self.ids = input_ids.reshape(-1)[flat]
-        self.pos = (flat % T).to(torch.int32)
-        shifted = torch.full_like(labels, -100)
-        shifted[:, :-1] = labels[:, 1:]
-        self.targets = shifted.reshape(-1)[flat].contiguous()
-        supervised = self.targets >= 0
-        self.head_order = torch.argsort((~supervised).to(torch.int8), stable=True)
-        self.n_supervised = int(supervised.sum()) if n_supervised is None else int(n_supervised)
-        cu = [0]
-        for length in self.lengths:
-            cu.append(cu[-1] + length)
-        self.cu_seqlens_host = cu
-        self.cu_seqlens = _to_device(torch.tensor(cu, dtype=torch.int32), dev)
+        self.rows, self.T, self.lengths = B, T, lengths
+        self.max_len = max(lengths, default=0)
+        self.cu_seqlens_host = [0, *itertools.accumulate(lengths)]
+        n = self.n = self.cu_seqlens_host[-1]
+        index = _to_device(_pack_index(lengths, T), dev)
+        self.tok = index[:n]
+        self.pos = index[2 * n:3 * n].to(torch.int32)
+        self.cu_seqlens = index[3 * n:].to(torch.int32)
+        self.ids = input_ids.reshape(-1).index_select(0, self.tok)
+        sentinel = torch.full((1,), -100, device=dev, dtype=labels.dtype)
+        self.targets = torch.cat([labels.reshape(-1), sentinel]).index_select(0, index[n:2 * n])
+        unsupervised = self.targets < 0
+        self.head_order = torch.argsort(unsupervised.to(torch.int8), stable=True)
+        counted = (n - unsupervised.sum()) if n_supervised is None or given else None
+        self.n_supervised = int(counted) if n_supervised is None else int(n_supervised)
+        self.metadata_ok = None
+        if given:
+            cu = index[3 * n:]
+            right = torch.arange(T, device=dev)[None, :] < (cu[1:] - cu[:-1])[:, None]
+            self.metadata_ok = (attention_mask.bool() == right).all() & \
+                (counted == self.n_supervised)
         self.cos, self.sin = rope.table(max(self.max_len, 1))
-        self.dropout_p = dropout_p
-        self.dropout = dropout
-        self.drop_seed = self.drop_threads = None
+        self.dropout_p, self.dropout = dropout_p, dropout
+        self.drop_seed = self.drop_threads = None  # set by the step's first draw
         self.drop_vec = dropout.vec if dropout is not None else 4
-        self.lora16_views = None
-        self.lora16t_views = None
+        self.lora16_views = self.lora16t_views = None
         self.grad16 = None  # (dh, fp16(dh)) handed from a layer's backward to the one below
 
     @property
@@ -335,11 +366,14 @@ class Packed:
         return tuple(None if t is None else t.t().contiguous() for t in lora16)
 
     def draw(self, H):
-        """The counter of the next LoRA dropout mask of this step (the next nn.Dropout call on
-        the padded [B, T, H] LoRA input), engine.py:758-764."""
+        """The counter of this step's next LoRA dropout mask: the next nn.Dropout call of the
+        base, on its padded [B, T, H] LoRA input (engine.py:758-764). Every call of one step
+        has the same seed and launch size."""
         seed, ctr, threads = self.dropout.draw(self.rows * self.T * H)
-        assert self.drop_seed in (None, seed) and self.drop_threads in (None, threads)
-        self.drop_seed, self.drop_threads = seed, threads
+        if self.drop_seed is None:
+            self.drop_seed, self.drop_threads = seed, threads
+        elif (seed, threads) != (self.drop_seed, self.drop_threads):
+            raise RuntimeError("the dropout generator was reseeded during the step")
         return ctr
 
 
@@ -351,19 +385,20 @@ class Packed:
 # ---------------------------------------------------------------------------------------------
 # One decoder layer (engine.py:1054-1340)
 # ---------------------------------------------------------------------------------------------
-def _layer_forward(spec, h, packed, lora16, seeds, keep):
-    """The layer's forward; with keep=True returns (None, everything the backward reads)."""
+def attn_input_fwd(spec, h, packed, lora16, seeds, keep_bits=False):
+    """The attention-input block (engine.py:1073-1109): input RMSNorm with the two LoRA-dropout
+    copies, the qkv projection (+ bias), the q/v LoRA products and RoPE. Returns q [n, HQ, D],
+    k and v in grouped layout [n, HKV, D], and what attn_input_bwd reads. keep_bits: store the
+    dropout masks as bits for the backward (else it draws them again)."""
     n, H = h.shape
-    D, HQ = spec.D, spec.HQ
     aq_w, bq_w, av_w, bv_w = lora16
     s = _lora_scale(spec)
     # LoRA dropout (engine.py:767-805); p = 0 is the identity (nn.Identity in PEFT), so both
-    # adapters read the normed rows themselves. A kept layer stores the masks as bits for its
-    # backward.
+    # adapters read the normed rows themselves
     drop = packed.dropout is not None
     drop_q, drop_v = drop and aq_w is not None, drop and av_w is not None
     kbits = (torch.empty(keep_bits_shape(n, H), device=h.device, dtype=torch.uint8)
-             if keep and (drop_q or drop_v) else None)
+             if keep_bits and (drop_q or drop_v) else None)
     _, a, aq, av, rstd1 = _rms_fwd(spec, h, spec.ln1, packed, seeds=seeds, drop_q=drop_q,
                                    drop_v=drop_v, keep=kbits)
     if not drop:
@@ -372,16 +407,51 @@ def _layer_forward(spec, h, packed, lora16, seeds, keep):
     del a
     xq, xv, lq, lv = _lora_fwd_rows(aq, av, aq_w, bq_w, av_w, bv_w)
     q, k, v = _rope_fwd(spec, qkv, lq, lv, packed, s, kv_heads=spec.HKV)
-    del qkv, lq, lv
+    return q, k, v, dict(rstd1=rstd1, aq=aq, av=av, xq=xq, xv=xv, keep=kbits)
+
+
+def attn_input_bwd(spec, dq, dk, dv, h, saved, packed, lora16t, seeds, dres=None,
+                   need_dh=True):
+    """Backward of attn_input_fwd (engine.py:1296-1338) from dq [n, HQ, D] and dk, dv per q
+    head [n, HQ, D] (or grouped): (dh fp32 [n, H] or None, its fp16 copy, (dA_q, dB_q, dA_v,
+    dB_v) fp32). dres: the residual stream's gradient added to dh."""
+    s = _lora_scale(spec)
+    n, H = h.shape
+    D, HQ, HKV = spec.D, spec.HQ, spec.HKV
+    C = (HQ + 2 * HKV) * D
+    dqkv = _rope_bwd(spec, dq, dk, dv, packed)
+    da = L.nf4_linear_t(dqkv, spec.qkv) if need_dh else None
+    # LoRA (engine.py:1319-1331): dx = s g B and t = dx A per token in one kernel for both
+    # adapters; the token reductions dB = s g^T x and dA = dx^T drop(a) of both in another
+    qc, vc = slice(0, HQ * D), slice((HQ + HKV) * D, C)
+    lt = lora16t
+    dxq, dxv, tq, tv = _lora_bwd_rows(dqkv, qc, vc, lt[0], lt[1], lt[2], lt[3], s,
+                                      need_t=need_dh)
+    grads = _lora_grad(dqkv, qc, vc, saved["xq"], saved["xv"], saved["aq"], saved["av"], dxq,
+                       dxv, s)
+    del dqkv
+    dh = dh16 = None
+    if need_dh:
+        dh16 = torch.empty((n, H), device=h.device, dtype=torch.float16)
+        dh = _rms_bwd(spec, da, h, saved["rstd1"], spec.ln1, packed, dres=dres, tq=tq, tv=tv,
+                      seeds=seeds, out16=dh16, keep=saved["keep"])
+    return dh, dh16, grads
+
+
+def _layer_forward(spec, h, packed, lora16, seeds, keep):
+    """The layer's forward; with keep=True returns (None, everything the backward reads)."""
+    n, H = h.shape
+    D, HQ = spec.D, spec.HQ
+    q, k, v, f = attn_input_fwd(spec, h, packed, lora16, seeds, keep_bits=keep)
     out, lse, aseed, aoffset = _attn_fwd(q, k, v, packed, spec.scale)
     o = L.nf4_linear(out.reshape(n, HQ * D), spec.w["o_proj"])
     h2, b, _, _, rstd2 = _rms_fwd(spec, h, spec.ln2, packed, delta=o)
     del o
     if keep:
         gu = L.nf4_linear(b, spec.gu)
-        return None, dict(rstd1=rstd1, aq=aq, av=av, xq=xq, xv=xv, q=q, k=k, v=v, out=out,
-                          lse=lse, aseed=aseed, aoffset=aoffset, h2=h2, rstd2=rstd2, gu=gu,
-                          keep=kbits)
+        f.update(q=q, k=k, v=v, out=out, lse=lse, aseed=aseed, aoffset=aoffset, h2=h2,
+                 rstd2=rstd2, gu=gu)
+        return None, f
     # gate|up GEMM with the SwiGLU in its epilogue ([gate|up] never stored), then down_proj
     # with the residual add in its epilogue: h3 = h2 + fp16(m W_d^T)
     m = L.nf4_linear_swiglu(b, spec.gu, spec.I)
@@ -434,10 +504,8 @@ class _Layer(torch.autograd.Function):
 
     @staticmethod
     def _backward(ctx, dh3, h, aq_w, bq_w, av_w, bv_w, spec, packed, seeds):
-        s = _lora_scale(spec)
         n, H = h.shape
-        D, HQ, HKV = spec.D, spec.HQ, spec.HKV
-        C = (HQ + 2 * HKV) * D
+        D, HQ = spec.D, spec.HQ
         dh3 = dh3.contiguous()
         # the fp16 copy of this gradient written by the layer above's norm backward, when the
         # gradient is that very tensor; else it is rounded on load (dY.to(fp16) W)
@@ -467,29 +535,14 @@ class _Layer(torch.autograd.Function):
                                f.pop("lse"), f.pop("aseed"), f.pop("aoffset"), packed,
                                spec.scale)
         del dout
-        dqkv = _rope_bwd(spec, dq, dk, dv, packed)
-        del dq, dk, dv
         need_dh = ctx.needs_input_grad[0]
-        da = L.nf4_linear_t(dqkv, spec.qkv) if need_dh else None
-        # LoRA (engine.py:1319-1331): dx = s g B and t = dx A per token in one kernel for both
-        # adapters; the token reductions dB = s g^T x and dA = dx^T drop(a) of both in another
-        qc, vc = slice(0, HQ * D), slice((HQ + HKV) * D, C)
-        lt = packed.lora16t(spec.index, lora16)
-        dxq, dxv, tq, tv = _lora_bwd_rows(dqkv, qc, vc, lt[0], lt[1], lt[2], lt[3], s,
-                                          need_t=need_dh)
-        dA_q, dB_q, dA_v, dB_v = _lora_grad(dqkv, qc, vc, f.pop("xq"), f.pop("xv"),
-                                            f.pop("aq"), f.pop("av"), dxq, dxv, s)
-        grads = {"q": (dA_q, dB_q, tq), "v": (dA_v, dB_v, tv)}
-        del dqkv
-        dh = None
+        dh, dh16, (dA_q, dB_q, dA_v, dB_v) = attn_input_bwd(
+            spec, dq, dk, dv, h, f, packed, packed.lora16t(spec.index, lora16), seeds,
+            dres=dh2, need_dh=need_dh)
+        del dq, dk, dv
         if need_dh:
-            dh16 = torch.empty((n, H), device=h.device, dtype=torch.float16)
-            dh = _rms_bwd(spec, da, h, f["rstd1"], spec.ln1, packed, dres=dh2,
-                          tq=grads["q"][2], tv=grads["v"][2], seeds=seeds, out16=dh16,
-                          keep=f["keep"])
             packed.grad16 = (dh, dh16)
-        return (dh, None, None, None, grads["q"][0], grads["q"][1], grads["v"][0],
-                grads["v"][1])
+        return dh, None, None, None, dA_q, dB_q, dA_v, dB_v
 
 
 # ---------------------------------------------------------------------------------------------
@@ -499,59 +552,60 @@ class HeadStats:
     """Row order, per-token loss, entropy and correct of the head (the logged metrics)."""
 
 
+class _NormSpec:
+    """The one field the RMSNorm wrappers read from a layer spec."""
+
+    def __init__(self, eps):
+        self.eps = eps
+
+
 class _Head(torch.autograd.Function):
-    """Final RMSNorm + lm_head + cross-entropy, rows supervised-first in chunks: logits of a
-    chunk, the CE kernel writes softmax - onehot over them, dhn = G W, then the norm's backward
-    with grad_scale = 1/denom. The loss is sum(tok_loss)/denom; the backward scales the saved
-    dh."""
+    """Final RMSNorm, the tied lm_head and the cross-entropy over the packed tokens: the loss
+    sum(tok_loss) / denom and the logged per-token loss, entropy and accuracy (the outputs of
+    engine.py:1352-1400).
+
+    The loss is linear in the per-token losses, so its gradient w.r.t. h is formed during the
+    forward and the backward only scales it. Tokens are taken in packed.head_order (supervised
+    first). Per slab of at most `chunk` tokens: one GEMM forms the logits, the CE kernel
+    reduces each row and overwrites it with softmax - onehot (zeros for unsupervised tokens),
+    and the slab's supervised rows alone go through G E and the norm's backward (scaled by
+    1/denom); the other rows' gradient is zero."""
 
     @staticmethod
     def forward(ctx, h, norm_w, eps, lm_w, packed, denom, stats, chunk):
-        n, H = h.shape
+        n = h.shape[0]
         dev = h.device
-        spec = HeadStats()
-        spec.eps = eps
-        order = packed.head_order
-        n_sup = packed.n_supervised
-        hp = h.index_select(0, order)
+        norm = _NormSpec(eps)
+        order, n_sup = packed.head_order, packed.n_supervised
+        rows = h.index_select(0, order)
         targets = packed.targets.index_select(0, order)
-        _, hn, _, _, rstd = _rms_fwd(spec, hp, norm_w, packed)
-        dhp = torch.empty_like(hp)
-        tok_loss = torch.empty((n,), device=dev, dtype=torch.float32)
-        entropy = torch.empty((n,), device=dev, dtype=torch.float32)
+        _, hn, _, _, rstd = _rms_fwd(norm, rows, norm_w, packed)
+        tok_loss, entropy = (torch.empty((n,), device=dev, dtype=torch.float32)
+                             for _ in range(2))
         correct = torch.empty((n,), device=dev, dtype=torch.int32)
-        inv = 1.0 / float(denom) if float(denom) else float("nan")
-        for c0 in range(0, n, chunk):
-            c1 = min(n, c0 + chunk)
-            logits = L.linear(hn[c0:c1], lm_w)
-            needs_grad = c0 < n_sup
-            _ce(logits, targets[c0:c1], tok_loss[c0:c1], entropy[c0:c1], correct[c0:c1],
-                zero_unsupervised=needs_grad)
-            if needs_grad:
-                # rows past n_sup have all-zero logits gradients (zero_unsupervised), hence
-                # zero dhn and zero dh: only the supervised rows go through the products
-                s1 = min(c1, n_sup)
-                dhn = L.linear_t(logits[:s1 - c0], lm_w)
-                del logits
-                _rms_bwd(spec, dhn, hp[c0:s1], rstd[c0:s1], norm_w, packed, grad_scale=inv,
-                         out=dhp[c0:s1])
-                dhp[s1:c1].zero_()
-                del dhn
-            else:
-                del logits
-                dhp[c0:c1].zero_()
-        dh = torch.empty_like(h)
-        dh.index_copy_(0, order, dhp)
+        grad_rows = torch.zeros_like(rows)
+        scale = 1.0 / float(denom) if float(denom) else float("nan")  # 0/0 as the base
+        for lo in range(0, n, chunk):
+            hi = min(n, lo + chunk)
+            logits = L.linear(hn[lo:hi], lm_w)
+            _ce(logits, targets[lo:hi], tok_loss[lo:hi], entropy[lo:hi], correct[lo:hi],
+                zero_unsupervised=lo < n_sup)
+            top = min(hi, n_sup)
+            if top > lo:
+                g_hn = L.linear_t(logits[:top - lo], lm_w)
+                _rms_bwd(norm, g_hn, rows[lo:top], rstd[lo:top], norm_w, packed,
+                         grad_scale=scale, out=grad_rows[lo:top])
+            del logits
+        dh = torch.empty_like(h).index_copy_(0, order, grad_rows)
         ctx.save_for_backward(dh)
-        stats.order, stats.tok_loss = order, tok_loss
-        stats.entropy, stats.correct = entropy, correct
-        return tok_loss.sum() * inv
+        stats.order, stats.tok_loss, stats.entropy, stats.correct = \
+            order, tok_loss, entropy, correct
+        return tok_loss.sum() * scale
 
     @staticmethod
     def backward(ctx, grad):
         (dh,) = ctx.saved_tensors
         return dh * grad, None, None, None, None, None, None, None
-
 
 # ---------------------------------------------------------------------------------------------
 # The model

@@ -9,6 +9,7 @@ CPU tensor is refused: there is no CPU path.
 """
 
 import ctypes
+import itertools
 
 import torch
 
@@ -53,45 +54,68 @@ def _rows_view(t, name, dtype, rows, cols, device):
 
 
 # ---------------------------------------------------------------------------------------------
-# NF4 weights (engine.py:74-157, 683-694)
+# NF4 weights in bitsandbytes' storage (read in place; the reference's wrappers read the same
+# Params4bit fields, engine.py:74-157, and stack weights the same way, 683-694)
 # ---------------------------------------------------------------------------------------------
 NF4_LEVELS = (-1.0, -0.6961928009986877, -0.5250730514526367, -0.39491748809814453,
               -0.28444138169288635, -0.18477343022823334, -0.09105003625154495, 0.0,
               0.07958029955625534, 0.16093020141124725, 0.24611230194568634,
               0.33791524171829224, 0.44070982933044434, 0.5626170039176941,
               0.7229568362236023, 1.0)
-_NO_SEG = 2**63 - 1
+_NO_SEG = 2**63 - 1  # a segment bound past every block: "no further segment"
+
+
+def _f32(t):
+    return t.detach().to(torch.float32).contiguous()
+
+
+def _is_nf4_table(code):
+    """Whether a 16-entry code is bitsandbytes' NF4 table (the kernels then use their own copy
+    of it instead of loading the code)."""
+    if code.numel() != 16:
+        return False
+    ref = torch.tensor(NF4_LEVELS, dtype=torch.float32, device=code.device)
+    return bool((code.reshape(-1) == ref).all())
+
+
+def _offset_tensor(offset, device):
+    if torch.is_tensor(offset):
+        return offset.detach().to(device=device, dtype=torch.float32).reshape(1).clone()
+    return torch.tensor([float(offset)], device=device, dtype=torch.float32)
 
 
 class NF4Weight:
-    """The packed bytes and quant state of one bitsandbytes-format Linear4bit weight (reads a
-    Params4bit's `.data` and `.quant_state`, engine.py:74-101)."""
+    """A frozen Linear4bit weight [N, K] as bitsandbytes stores it, read without a copy.
+
+    `param.data` holds the codes, two per byte (element 2j in the high nibble of byte j);
+    `param.quant_state` holds one scale per `bs1` consecutive elements. With double
+    quantisation (`nested`) each scale is itself an 8-bit code: scale = code2[absmax[b]] *
+    absmax2[b // bs2] + offset; otherwise `absmax` is the fp32 scale. The attributes below are
+    what the dequant and fused-GEMM entry points take."""
 
     def __init__(self, param):
-        qs = param.quant_state
-        self.param = param
-        self.packed = param.data
-        self.group = None
-        self.shape = tuple(int(s) for s in qs.shape)
-        self.numel = self.shape[0] * self.shape[1]
-        self.code = qs.code.float().contiguous()
-        self.bs1 = int(qs.blocksize)
+        st = param.quant_state
+        rows, cols = (int(d) for d in st.shape)
+        dev = param.data.device
+        self.param, self.packed, self.group = param, param.data, None
+        self.shape, self.numel = (rows, cols), rows * cols
+        self.bs1 = int(st.blocksize)
         if self.numel % self.bs1:
-            raise ValueError("weight size is not a whole number of quantization blocks")
-        levels = torch.tensor(NF4_LEVELS, dtype=torch.float32, device=self.code.device)
-        self.standard = bool(torch.equal(self.code, levels))
-        self.nested = bool(qs.nested)
+            raise ValueError(f"a {rows} x {cols} weight does not split into blocks of "
+                             f"{self.bs1} values")
+        self.code = _f32(st.code)
+        self.standard = _is_nf4_table(self.code)
+        self.nested = bool(getattr(st, "nested", False))
         if self.nested:
-            self.absmax = qs.absmax
-            self.code2 = qs.state2.code.float().contiguous()
-            self.absmax2 = qs.state2.absmax.float().contiguous()
-            self.offset = torch.as_tensor(qs.offset, device=self.code.device,
-                                          dtype=torch.float32).reshape(1)
-            self.bs2 = int(qs.state2.blocksize)
+            inner = st.state2
+            self.bs2 = int(inner.blocksize)
+            self.absmax = st.absmax  # uint8 codes into code2
+            self.code2, self.absmax2 = _f32(inner.code), _f32(inner.absmax)
+            self.offset = _offset_tensor(st.offset, dev)
         else:
-            self.absmax = qs.absmax.float().contiguous()
-            self.code2 = self.absmax2 = self.offset = self.absmax
             self.bs2 = 1
+            self.absmax = _f32(st.absmax)  # the scales themselves
+            self.code2 = self.absmax2 = self.offset = None
         self._args = _dequant_args(self.packed, self.absmax, self.code2, self.absmax2,
                                    self.offset, self.code, self.blocks, self.nested,
                                    self.standard, self.bs1, self.bs2, _NO_SEG, _NO_SEG,
@@ -101,58 +125,72 @@ class NF4Weight:
     def blocks(self):
         return self.numel // self.bs1
 
+    @property
+    def layout(self):
+        """What two weights must share to be decoded by one launch over their concatenation:
+        row length, block sizes, double quantisation and the code table."""
+        return (self.shape[1], self.bs1, self.bs2, self.nested, self.standard)
+
     def dequant_into(self, out):
         _launch_dequant(self._args, out, self.blocks, self.nested, self.standard, self.bs1,
                         self.bs2, _NO_SEG, _NO_SEG, self.numel, self.packed.device)
         return out
 
 
+def _same_tables(a, b):
+    if not torch.equal(a.code, b.code):
+        return False
+    return not a.nested or torch.equal(a.code2, b.code2)
+
+
 class NF4Group:
-    """Weights stored back to back and dequantized in one launch (engine.py:112-157): only the
-    double-quantization offset differs per segment; their absmax2 are concatenated, which needs
-    every weight but the last to end on a whole block of absmax2."""
+    """2 or 3 NF4 weights with the same layout, concatenated along their rows (q|k|v, gate|up)
+    so that one launch decodes all of them. The packed codes and absmax are concatenated into
+    resident copies; with double quantisation the per-weight offsets become segments: block b
+    takes offsets[0] below seg1, offsets[1] below seg2, offsets[2] after that. Concatenating the
+    absmax2 tables keeps block b's entry at b // bs2 only if every weight but the last covers
+    whole bs2-block groups."""
 
     @classmethod
     def of(cls, weights):
-        if not 2 <= len(weights) <= 3:
+        """The group of these weights, or None when they cannot share one launch."""
+        weights = list(weights)
+        if len(weights) not in (2, 3):
             return None
-        w0 = weights[0]
-        for w in weights:
-            if (w.shape[1] != w0.shape[1] or w.bs1 != w0.bs1 or w.bs2 != w0.bs2
-                    or w.nested != w0.nested or w.standard != w0.standard
-                    or not torch.equal(w.code, w0.code)
-                    or (w.nested and not torch.equal(w.code2, w0.code2))):
-                return None
-        if any((w.numel // w.bs1) % w.bs2 for w in weights[:-1]):
+        first = weights[0]
+        if any(w.layout != first.layout or not _same_tables(w, first) for w in weights[1:]):
+            return None
+        if any(w.blocks % w.bs2 for w in weights[:-1]):
             return None
         return cls(weights)
 
     def __init__(self, weights):
-        w0 = weights[0]
-        self.weights = weights
-        self.nested, self.standard, self.bs1, self.bs2 = w0.nested, w0.standard, w0.bs1, w0.bs2
-        self.code, self.code2 = w0.code, w0.code2
-        self.numel = sum(w.numel for w in weights)
-        self.blocks = self.numel // self.bs1
-        bounds = []
-        for w in weights[:-1]:
-            bounds.append((bounds[-1] if bounds else 0) + w.numel // self.bs1)
-        self.seg1, self.seg2 = (bounds + [_NO_SEG, _NO_SEG])[:2]
-        # one resident copy of the packed bytes and absmax, back to back (the reference keeps
-        # them in a WeightStream slot; on MI355X everything stays in HBM)
-        self.packed = torch.cat([w.packed.reshape(-1) for w in weights])
-        self.absmax = torch.cat([w.absmax.reshape(-1) for w in weights])
+        first = weights[0]
+        self.weights = list(weights)
+        self.nested, self.standard = first.nested, first.standard
+        self.bs1, self.bs2 = first.bs1, first.bs2
+        self.code, self.code2 = first.code, first.code2
+        ends = list(itertools.accumulate(w.blocks for w in self.weights))
+        self.blocks = ends[-1]
+        self.numel = self.blocks * self.bs1
+        self.seg1, self.seg2 = (ends[:-1] + [_NO_SEG, _NO_SEG])[:2]
+        self.packed = torch.cat([w.packed.reshape(-1) for w in self.weights])
+        self.absmax = torch.cat([w.absmax.reshape(-1) for w in self.weights])
         if self.nested:
-            self.absmax2 = torch.cat([w.absmax2 for w in weights])
-            self.offsets = torch.cat([w.offset for w in weights])
+            self.absmax2 = torch.cat([w.absmax2.reshape(-1) for w in self.weights])
+            self.offsets = torch.cat([w.offset for w in self.weights])
         else:
-            self.absmax2 = self.offsets = self.absmax
-        for w in weights:
+            self.absmax2 = self.offsets = None
+        for w in self.weights:
             w.group = self
         self._args = _dequant_args(self.packed, self.absmax, self.code2, self.absmax2,
                                    self.offsets, self.code, self.blocks, self.nested,
                                    self.standard, self.bs1, self.bs2, self.seg1, self.seg2,
                                    self.numel)
+
+    @property
+    def shape(self):
+        return sum(w.shape[0] for w in self.weights), self.weights[0].shape[1]
 
     def dequant_into(self, out):
         _launch_dequant(self._args, out, self.blocks, self.nested, self.standard, self.bs1,
@@ -199,26 +237,26 @@ def _dq_segs(w):
     return (w.seg1, w.seg2) if isinstance(w, NF4Group) else (_NO_SEG, _NO_SEG)
 
 
-def _dq_shape(w):
-    if isinstance(w, NF4Group):
-        return sum(x.shape[0] for x in w.weights), w.weights[0].shape[1]
-    return w.shape
-
-
 DEQUANT_MANY_MAX = 32  # weights per qlora_nf4_dequant_many launch
 
 
-def dequant_many(items, device):
+def dequant_many(items, device, outs=None):
     """fp16 [N_i, K_i] of each NF4Weight / NF4Group of `items` (at most DEQUANT_MANY_MAX), all
-    in one launch (a layer's qkv, o, gate|up and down, or those of several layers)."""
-    import ctypes
+    in one launch (a layer's qkv, o, gate|up and down, or those of several layers). `outs`:
+    contiguous fp16 destinations of the right sizes, else they are allocated."""
     if not 1 <= len(items) <= DEQUANT_MANY_MAX:
         raise ValueError(f"dequant_many takes 1 to {DEQUANT_MANY_MAX} weights")
-    outs = [torch.empty(_dq_shape(w), device=device, dtype=torch.float16) for w in items]
+    if outs is None:
+        outs = [torch.empty(w.shape, device=device, dtype=torch.float16) for w in items]
+    if len(outs) != len(items):
+        raise ValueError("one output per weight")
     device = outs[0].device  # "cuda" -> "cuda:<current>"
-    for w in items:
+    for w, o in zip(items, outs):
         if w.packed.device != device:
             raise ValueError(f"weight on {w.packed.device}, expected {device}")
+        _need(o, "out", torch.float16, device)
+        if o.numel() != w.numel:
+            raise ValueError(f"out has {o.numel()} elements, the weight {w.numel}")
     k = len(items)
     P = ctypes.c_void_p * k
     args = [P(*[w._args[i] for w in items]) for i in range(6)]
@@ -235,76 +273,105 @@ def dequant_many(items, device):
 
 
 def dequant(weights, device):
-    """Dequantize one or more [n_i, K] weights stacked into one fp16 [sum n_i, K] buffer
-    (engine.py:683-694): one launch when they form an NF4Group."""
-    rows = sum(w.shape[0] for w in weights)
-    out = torch.empty((rows, weights[0].shape[1]), device=device, dtype=torch.float16)
+    """fp16 [sum N_i, K]: the weights decoded one below the other (engine.py:683-694's
+    contract). One launch either way: the group's own when the weights are exactly a group,
+    else one qlora_nf4_dequant_many launch writing each weight's row range."""
+    weights = list(weights)
+    cols = {w.shape[1] for w in weights}
+    if len(cols) != 1:
+        raise ValueError("stacked weights must have the same number of columns")
+    rows = [w.shape[0] for w in weights]
+    out = torch.empty((sum(rows), cols.pop()), device=device, dtype=torch.float16)
     group = weights[0].group
     if group is not None and group.weights == weights:
         return group.dequant_into(out)
-    start = 0
-    for w in weights:
-        w.dequant_into(out[start:start + w.shape[0]])
-        start += w.shape[0]
+    bounds = [0, *itertools.accumulate(rows)]
+    for i in range(0, len(weights), DEQUANT_MANY_MAX):
+        part = weights[i:i + DEQUANT_MANY_MAX]
+        dequant_many(part, out.device,
+                     outs=[out[bounds[j]:bounds[j + 1]] for j in range(i, i + len(part))])
     return out
 
 
 # ---------------------------------------------------------------------------------------------
-# LoRA dropout masks (engine.py:767-828)
+# LoRA dropout masks: the Philox stream of PyTorch's dropout (engine.py:767-828 draws from the
+# same generator; the mask arithmetic is kernels.py:108-135's, restated for rocRAND)
 # ---------------------------------------------------------------------------------------------
+def _as_int64(x):
+    """A 64-bit seed as the signed value the C-ABI takes (same bits)."""
+    return x - 2**64 if x >= 2**63 else x
+
+
 class TorchDropout:
-    """The LoRA dropout masks of the base, bit for bit: `draw` takes the default generator's
-    Philox state (seed, offset) for the next nn.Dropout call on nelem elements and advances the
-    generator as PyTorch's dropout launch does (engine.py:767-805); the kernels compute the mask
-    from it."""
+    """Where the masks of PEFT's LoRA dropout come from, so that the kernels can recompute them.
 
-    BLOCK, UNROLL = 256, 4
+    PEFT applies nn.Dropout(p) to each adapter's input, a contiguous [B, T, H] tensor, in the
+    order the forward reaches the adapters (layer 0 q, layer 0 v, layer 1 q, ...). On ROCm that
+    dropout is one fused launch of up to `max_blocks` blocks of 256 threads (the device's CUs x
+    the blocks resident per CU); thread i of the grid draws Philox4x32-10 outputs at counter
+    (offset/4 + round, i) of the default generator, four values a round and `vec` elements per
+    16-byte access, and the launch moves the generator's offset past the rounds it used.
+    `draw` hands out the (seed, counter, threads) of the next such call and moves the generator
+    exactly as that launch would; `check` compares the RMSNorm kernel's mask with nn.Dropout's
+    own on this device, once."""
 
-    CHECK_SEED = 20261031
-    CHECK_TOKENS = 64
+    THREADS_PER_BLOCK = 256
+    VALUES_PER_ROUND = 4
+
+    CHECK_SEED = 0x1D20_2F5B  # seeds the self-check's private generator state
+    CHECK_TOKENS = 48         # tokens per row checked
 
     def __init__(self, device, dtype):
-        self.device, self.dtype = torch.device(device), dtype
-        self.ok = None
+        self.device = torch.device(device)
+        if self.device.index is None:
+            self.device = torch.device("cuda", torch.cuda.current_device())
+        self.dtype = dtype
         props = torch.cuda.get_device_properties(self.device)
-        self.max_blocks = props.multi_processor_count \
-            * (props.max_threads_per_multi_processor // self.BLOCK)
-        idx = self.device.index if self.device.index is not None else torch.cuda.current_device()
-        self.gen = torch.cuda.default_generators[idx]
+        self.max_blocks = props.multi_processor_count * (
+            props.max_threads_per_multi_processor // self.THREADS_PER_BLOCK)
+        self.gen = torch.cuda.default_generators[self.device.index]
         self.vec = 16 // torch.empty((), dtype=dtype).element_size()
-        assert self.vec in (4, 8), dtype
+        if self.vec not in (4, 8):
+            raise ValueError(f"dropout input dtype {dtype} is not 2 or 4 bytes wide")
+        self.ok = None  # the self-check's verdict, once run
+
+    def launch(self, nelem):
+        """(threads, counter advance) of PyTorch's dropout launch over nelem elements."""
+        blocks = max(1, min(self.max_blocks, -(-nelem // self.THREADS_PER_BLOCK)))
+        threads = blocks * self.THREADS_PER_BLOCK
+        rounds = -(-nelem // (threads * self.VALUES_PER_ROUND))
+        return threads, rounds * self.VALUES_PER_ROUND
 
     def draw(self, nelem):
-        """(seed, counter, threads) of a dropout call on nelem elements; advances the generator."""
-        assert nelem % self.vec == 0, nelem
-        blocks = min(self.max_blocks, (nelem + self.BLOCK - 1) // self.BLOCK)
-        increment = ((nelem - 1) // (self.BLOCK * blocks * self.UNROLL) + 1) * self.UNROLL
+        """(seed, counter, threads) of the next dropout call on nelem elements; the generator
+        moves on as that call would move it."""
+        if nelem % self.vec:
+            raise ValueError(f"{nelem} elements are not whole {self.vec}-element accesses")
+        threads, advance = self.launch(nelem)
         seed, offset = self.gen.initial_seed(), self.gen.get_offset()
-        self.gen.set_offset(offset + increment)
-        if seed >= 2**63:
-            seed -= 2**64
-        return seed, offset // 4, blocks * self.BLOCK
+        self.gen.set_offset(offset + advance)
+        return _as_int64(seed), offset // 4, threads
 
     def check(self, B, T, H, p):
-        """Whether the rms kernel's mask equals PyTorch's dropout kernel on this GPU and build:
-        dropout of ones over [B, T, H] on a private generator (engine.py:807-828)."""
-        gen = torch.Generator(device=self.device)
-        gen.manual_seed(self.CHECK_SEED)
-        ones = torch.ones((B, T, H), device=self.device, dtype=self.dtype)
-        _, ref = torch._fused_dropout(ones, 1.0 - p, gen)
-        nelem = B * T * H
-        blocks = min(self.max_blocks, (nelem + self.BLOCK - 1) // self.BLOCK)
+        """True when the RMSNorm kernel's q mask equals nn.Dropout's on this device: F.dropout
+        of ones over [B, T, H] and our mask drawn from the same freshly seeded generator state,
+        inside a fork of the RNG state (the caller's generator is left where it was)."""
+        with torch.random.fork_rng(devices=[self.device.index], device_type="cuda"):
+            self.gen.manual_seed(self.CHECK_SEED)
+            ones = torch.ones((B, T, H), device=self.device, dtype=self.dtype)
+            want = torch.nn.functional.dropout(ones, p=p, training=True) != 0
+            self.gen.manual_seed(self.CHECK_SEED)
+            seed, ctr, threads = self.draw(B * T * H)
 
-        class _Check:
-            dropout_p, drop_seed, drop_threads, drop_vec = p, self.CHECK_SEED, \
-                blocks * self.BLOCK, self.vec
-            tok = torch.arange(B * T, device=self.device)
+        class _Rows:  # the fields _rms_fwd reads from a spec and a packed batch
             eps = 1e-6
+            dropout_p, drop_seed, drop_threads, drop_vec = p, seed, threads, self.vec
+            tok = torch.arange(B * T, device=self.device)
 
-        x = ones.view(B * T, H).float()
-        _, _, yq, _, _ = _rms_fwd(_Check, x, torch.ones(H, device=self.device), _Check,
-                                  write_y=False, seeds=(0, 0), drop_q=True)
-        return bool(torch.equal((yq != 0).view(B, T, H), ref.bool()))
+        x = torch.ones((B * T, H), device=self.device, dtype=torch.float32)
+        _, _, got, _, _ = _rms_fwd(_Rows, x, torch.ones(H, device=self.device), _Rows,
+                                   write_y=False, seeds=(ctr, 0), drop_q=True)
+        return bool(torch.equal(got.view(B, T, H) != 0, want))
 
 
 def keep_mask(nelem, seed, ctr, threads, p, vec, device):

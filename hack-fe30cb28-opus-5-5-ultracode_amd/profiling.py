@@ -62,11 +62,19 @@ WORK = {
 
 
 class LaunchTimer:
-    def __init__(self, entry):
-        if entry not in WORK:
+    """Times every launch of `entry` while active. The work of a launch comes from WORK, or
+    from `work` (a function of the call's arguments) with its `bound` ("hbm": bytes, "mfma":
+    flops), or is given afterwards per launch to summary() (`work_total`)."""
+
+    def __init__(self, entry, work=None, bound=None):
+        if work is None and bound is None and entry not in WORK:
             raise ValueError(f"no work model for {entry}")
         self.entry = entry
-        self.bound, self.work = WORK[entry]
+        self.bound, self.work = WORK.get(entry, (bound, work))
+        if work is not None:
+            self.bound, self.work = bound, work
+        if self.work is None:
+            self.work = lambda args: 0.0
         self.records = []
 
     def __enter__(self):
@@ -92,12 +100,12 @@ class LaunchTimer:
         self.records.append((start, end, self.work(args)))
         return rc
 
-    def summary(self):
+    def summary(self, work_total=None):
         torch.cuda.synchronize()
         if not self.records:
             return None
         ms = [s.elapsed_time(e) for s, e, _ in self.records]
-        work = sum(w for _, _, w in self.records)
+        work = sum(w for _, _, w in self.records) if work_total is None else work_total
         total_s = sum(ms) * 1e-3
         avg_us = 1e3 * sum(ms) / len(ms)
         if self.bound == "hbm":

@@ -4,7 +4,17 @@
  * Every entry point takes raw device pointers, sizes and scalars, launches on the given HIP
  * stream (hipStream_t passed as void*; NULL = the default stream) and returns 0 on success or a
  * hipError_t (hipErrorInvalidValue = 1 for arguments a kernel cannot take; checked before any
- * launch). Nothing is allocated or freed; no global mutable state; callable from any thread.
+ * launch). Kernels allocate nothing: callers pass every output and workspace. The library keeps
+ * this process-wide state, each created on first use per device and kept until the process ends:
+ *   - one rocBLAS handle per device (qlora_gemm*, csrc/blas.hip; rocBLAS keeps its own small
+ *     workspace in it);
+ *   - one hipBLASLt handle per device and a cache of its plans (matmul descriptors and the
+ *     heuristic's choice) per exact problem, in a map behind a mutex (qlora_gemmlt*,
+ *     csrc/blaslt.hip);
+ *   - one second stream and two events per device (csrc/attn.hip), on which the attention
+ *     backward runs dK/dV beside dQ; it is forked from and joined back into the caller's stream
+ *     inside the call, so the call is ordered on the caller's stream as any other.
+ * Entry points are callable from any thread; the state above is created under a lock.
  * n == 0 (rows, tokens, blocks) is a no-op that returns 0, as the reference skips such launches.
  *
  * Dtypes: "f16" = IEEE half as 16-bit words, "f32" = float, "i64"/"i32" = int64_t/int32_t.

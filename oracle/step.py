@@ -89,6 +89,38 @@ def _rope(x, cos, sin):
     return torch.cat([x1 * cos - x2 * sin, x2 * cos + x1 * sin], -1)
 
 
+def rope_cos_sin(pos, D, theta):
+    """cos, sin [n, 1, D/2] fp32 of angle = pos * theta^(-2k/D) (test_kernels.py:154-156)."""
+    inv = 1.0 / (theta ** (torch.arange(0, D, 2).float() / D))
+    ang = pos.float()[:, None] * inv[None, :]
+    return ang.cos()[:, None, :], ang.sin()[:, None, :]
+
+
+def attn_input(lay, h, masks, kscale, cos, sin, HQ, HKV, D, eps):
+    """The attention-input block (engine.py:1073-1109) with autograd: input RMSNorm, the
+    dropout'ed LoRA inputs (masks = (keep_q, keep_v) bool [n, H], or None without dropout),
+    qkv = fp16(a W_qkv^T + bias), lq = fp16(fp16(aq A_q^T) B_q^T), lv likewise, then
+    q = fp16(rope(qkv_q + s lq)), k = fp16(rope(qkv_k)), v = fp16(qkv_v + s lv) with k, v in
+    grouped layout [n, HKV, D]."""
+    n = h.shape[0]
+    (aq_w, bq_w, s), (av_w, bv_w, _) = lay.lora["q"], lay.lora["v"]
+    y = _rms(h, lay.ln1, eps)
+    a = _r16(y)
+    if masks is not None:
+        mq, mv = masks
+        aq = _r16(torch.where(mq, y * kscale, torch.zeros_like(y)))
+        av = _r16(torch.where(mv, y * kscale, torch.zeros_like(y)))
+    else:
+        aq = av = a
+    qkv = _r16(a @ lay.w_qkv.t() + lay.bias)
+    lq = _r16(_r16(aq @ _r16(aq_w).t()) @ _r16(bq_w).t())
+    lv = _r16(_r16(av @ _r16(av_w).t()) @ _r16(bv_w).t())
+    q = (qkv[:, :HQ * D] + s * lq).view(n, HQ, D)
+    k = qkv[:, HQ * D:(HQ + HKV) * D].view(n, HKV, D)
+    v = (qkv[:, (HQ + HKV) * D:] + s * lv).view(n, HKV, D)
+    return _r16(_rope(q, cos, sin)), _r16(_rope(k, cos, sin)), _r16(v)
+
+
 class Batch:
     """The packing of a right-padded batch (engine.py:705-751), on the CPU."""
 
@@ -117,9 +149,7 @@ def forward_loss(model, input_ids, attention_mask, labels, denom, *, drop_seed=0
     bt = Batch(input_ids.cpu(), attention_mask.cpu(), labels.cpu())
     n, H, D = bt.n, cfg.hidden_size, cfg.head_dim
     HQ, HKV, eps = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.rms_norm_eps
-    inv = 1.0 / (cfg.rope_theta ** (torch.arange(0, D, 2).float() / D))
-    ang = bt.pos.float()[:, None] * inv[None, :]
-    cos, sin = ang.cos()[:, None, :], ang.sin()[:, None, :]
+    cos, sin = rope_cos_sin(bt.pos, D, cfg.rope_theta)
     p_keep, kscale = np.float32(1 - p), float(np.float32(1.0 / (1 - p))) if p > 0 else 1.0
     offset = drop_offset
     nelem = bt.B * bt.T * H
@@ -137,22 +167,8 @@ def forward_loss(model, input_ids, attention_mask, labels, denom, *, drop_seed=0
     else:
         h = first_layer_input
     for lay in model.layers:
-        (aq_w, bq_w, s), (av_w, bv_w, _) = lay.lora["q"], lay.lora["v"]
-        y = _rms(h, lay.ln1, eps)
-        a = _r16(y)
-        if p > 0:
-            mq, mv = next_mask(), next_mask()
-            aq = _r16(torch.where(mq, y * kscale, torch.zeros_like(y)))
-            av = _r16(torch.where(mv, y * kscale, torch.zeros_like(y)))
-        else:
-            aq = av = a
-        qkv = _r16(a @ lay.w_qkv.t() + lay.bias)
-        lq = _r16(_r16(aq @ _r16(aq_w).t()) @ _r16(bq_w).t())
-        lv = _r16(_r16(av @ _r16(av_w).t()) @ _r16(bv_w).t())
-        q = (qkv[:, :HQ * D] + s * lq).view(n, HQ, D)
-        k = qkv[:, HQ * D:(HQ + HKV) * D].view(n, HKV, D)
-        v = (qkv[:, (HQ + HKV) * D:] + s * lv).view(n, HKV, D)
-        q, k, v = _r16(_rope(q, cos, sin)), _r16(_rope(k, cos, sin)), _r16(v)
+        masks = (next_mask(), next_mask()) if p > 0 else None
+        q, k, v = attn_input(lay, h, masks, kscale, cos, sin, HQ, HKV, D, eps)
         rep = HQ // HKV
         k = k.repeat_interleave(rep, 1)
         v = v.repeat_interleave(rep, 1)

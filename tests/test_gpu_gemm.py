@@ -105,10 +105,13 @@ def test_epilogues(pkg):
     assert torch.equal(L.nf4_gemm(a32, wd, 1), L.nf4_gemm(a32.half(), wd, 1))
 
 
-def test_mlp_up_path_config2(pkg):
+@pytest.mark.parametrize("path", ["step", "fused"])
+def test_mlp_up_path_config2(pkg, path):
     """x [2048, 1536] ~ N(0,1), NF4 [gate|up] [17920, 1536] and down
     [1536, 8960] from N(0, 0.02); h = silu(gate) * up, y = h W_d^T; backward w.r.t. x with
-    dy ~ N(0,1). Fused GEMMs against the oracle's fp32 products of the same fp16 values."""
+    dy ~ N(0,1), against the oracle's fp32 products of the same fp16 values. path "step": the
+    projections as the step runs them (linear.nf4_linear*, whichever backend is the default);
+    "fused": the fused NF4 GEMM kernel itself (SwiGLU epilogue, NT, NN)."""
     L = pkg.linear
     gu_w = _group(pkg, [(8960, 1536), (8960, 1536)], 20)
     wd = _weight(pkg, (1536, 8960), 22)
@@ -117,12 +120,20 @@ def test_mlp_up_path_config2(pkg):
     dy = torch.randn(2048, 1536, generator=g).half()
     h_o, y_o, dx_o = O.mlp(x, L.dequantize(gu_w).cpu(), L.dequantize(wd).cpu(), dy)
     xg, dyg = x.to(DEV), dy.to(DEV)
-    h = L.nf4_linear_swiglu(xg, gu_w, 8960)
-    y = L.nf4_linear(h, wd)
-    dh = L.nf4_linear_t(dyg, wd)
-    gu = L.nf4_linear(xg, gu_w)
-    pkg.ops._glu_bwd(dh, gu, 8960)
-    dx = L.nf4_linear_t(gu, gu_w)
+    if path == "step":
+        h = L.nf4_linear_swiglu(xg, gu_w, 8960)
+        y = L.nf4_linear(h, wd)
+        dh = L.nf4_linear_t(dyg, wd)
+        gu = L.nf4_linear(xg, gu_w)
+        pkg.ops._glu_bwd(dh, gu, 8960)
+        dx = L.nf4_linear_t(gu, gu_w)
+    else:
+        h = L.nf4_gemm(xg, gu_w, 0, epi=3, swiglu_I=8960)
+        y = L.nf4_gemm(h, wd, 0)
+        dh = L.nf4_gemm(dyg, wd, 1)
+        gu = L.nf4_gemm(xg, gu_w, 0)
+        pkg.ops._glu_bwd(dh, gu, 8960)
+        dx = L.nf4_gemm(gu, gu_w, 1)
     for got, want in ((h, h_o), (y, y_o), (dx, dx_o)):
         assert rel_err(got.cpu(), want) < 1e-3
 

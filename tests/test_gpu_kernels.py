@@ -404,6 +404,28 @@ def test_glu_forward_backward(pkg, n, I):
     close(work[:, I:], want[:, I:], 1e-2)
 
 
+def _ulps(a, b):
+    """Distance in fp16 units in the last place between two fp16 tensors (same sign order)."""
+    def key(t):
+        i = t.view(torch.int16).to(torch.int32)
+        return torch.where(i < 0, -(i & 0x7FFF), i)
+    return (key(a) - key(b)).abs()
+
+
+def test_glu_forward_ulp_bound_config2(pkg):
+    """SwiGLU at config 2's size ([2048, 8960] out of gu ~ N(0, 1) fp16) forms the sigmoid from
+    the hardware exp2 and reciprocal: every output is within 1 fp16 ulp of the oracle's
+    fp32 silu (accurate exp) rounded once, and under 0.1 % of outputs differ at all."""
+    I = 8960
+    g = torch.Generator().manual_seed(7)
+    gu = torch.randn(2048, 2 * I, generator=g).half()
+    m = pkg.ops._glu_fwd(gu.to(DEV), I).cpu()
+    want = O.glu_fwd(gu, I)
+    d = _ulps(m, want)
+    assert int(d.max()) <= 1
+    assert float((d > 0).float().mean()) < 1e-3
+
+
 @pytest.mark.parametrize("V", [151936, 5000, 4093])
 def test_lm_head_ce(pkg, V):
     g = torch.Generator().manual_seed(0)

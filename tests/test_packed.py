@@ -48,3 +48,54 @@ def test_left_padding_is_refused():
     mask = mask.flip(1)
     with pytest.raises(E.UnsupportedBatch):
         _packed(ids, mask, labels)
+
+
+def test_host_metadata_is_checked_on_the_device():
+    """Caller-given lengths and supervised count are checked without a read: metadata_ok is a
+    device bool that turns False for a mask not right-padded to the lengths or a wrong count."""
+    lengths, T = [5, 9, 1, 9], 9
+    ids, mask, labels = _batch(lengths, T, 3)
+    right = _packed(ids, mask, labels)
+    n_sup = right.n_supervised
+    assert right.metadata_ok is None  # read from the device: nothing to check
+    assert bool(_packed(ids, mask, labels, lengths=lengths, n_supervised=n_sup).metadata_ok)
+    assert not bool(_packed(ids, mask, labels, lengths=lengths,
+                            n_supervised=n_sup - 1).metadata_ok)
+    assert not bool(_packed(ids, mask, labels, lengths=[5, 8, 1, 9],
+                            n_supervised=n_sup).metadata_ok)
+
+
+def test_next_token_labels_and_positions():
+    """targets[i] is the label one column right of token i (-100 past the last column), pos
+    restarts at 0 for every row, cu_seqlens are the running sums of the lengths."""
+    lengths, T = [3, 0, 4], 4
+    ids, mask, labels = _batch(lengths, T, 7)
+    p = _packed(ids, mask, labels, lengths=lengths)
+    assert p.pos.tolist() == [0, 1, 2, 0, 1, 2, 3]
+    assert p.cu_seqlens.tolist() == [0, 3, 3, 7]
+    assert p.tok.tolist() == [0, 1, 2, 8, 9, 10, 11]
+    want = [int(labels[0, 1]), int(labels[0, 2]), int(labels[0, 3]),
+            int(labels[2, 1]), int(labels[2, 2]), int(labels[2, 3]), -100]
+    assert p.targets.tolist() == want
+    sup = [i for i, t in enumerate(want) if t >= 0]
+    assert p.head_order.tolist()[:len(sup)] == sup
+
+
+@pytest.mark.parametrize("scaling", [{"rope_type": "yarn", "factor": 4.0},
+                                     {"type": "linear", "factor": 2.0}])
+def test_scaled_rotary_embedding_is_refused(scaling):
+    """A checkpoint whose rotary embedding is scaled is refused, not trained with the plain
+    tables."""
+    from types import SimpleNamespace as NS
+    q = NS(lora_A={"default": NS(weight=torch.zeros(16, 64))}, lora_B={}, scaling={"default": 2.0},
+           active_adapter=["default"])
+    v = NS(lora_A={"default": NS(weight=torch.zeros(16, 64))}, lora_B={}, scaling={"default": 2.0},
+           active_adapter=["default"])
+    plain = NS()
+    layer = NS(self_attn=NS(q_proj=q, k_proj=plain, v_proj=v, o_proj=plain),
+               mlp=NS(gate_proj=plain, up_proj=plain, down_proj=plain))
+    cfg = NS(hidden_size=64, num_attention_heads=4, num_key_value_heads=2, head_dim=16,
+             rope_theta=1e6, rope_scaling=scaling, intermediate_size=128, vocab_size=100)
+    causal = NS(model=NS(layers=[layer]), config=cfg)
+    with pytest.raises(E.UnsupportedModel, match="rotary"):
+        E.from_peft(NS(get_base_model=lambda: causal))
