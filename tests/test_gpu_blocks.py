@@ -112,7 +112,11 @@ def test_config5_full_width_step(pkg):
     seed, offset = gen.initial_seed(), gen.get_offset()
     loss, packed, _ = model.step(ids.to(DEV), mask.to(DEV), labels.to(DEV), denom,
                                  lengths=lengths, n_supervised=int(denom))
-    loss.backward()
+    # fp16 training scales the loss (GradScaler's 2^16, as the trainer): unscaled, the
+    # per-token gradients of a 151,936-way softmax over ~2,000 tokens sit in fp16's subnormal
+    # range inside the layers' fp16 products
+    scale = 2.0**16
+    (loss * scale).backward()
     torch.cuda.synchronize()
     assert bool(packed.metadata_ok)
     print(f"gpu loss {loss.item():.6f}; oracle...", flush=True)
@@ -122,6 +126,6 @@ def test_config5_full_width_step(pkg):
     ref.backward()
     print(f"oracle loss {ref.item():.6f}", flush=True)
     assert abs(loss.item() - ref.item()) <= 2e-3 * abs(ref.item())
-    for g_gpu, leaf in zip(model.parameters(), cpu.lora_leaves()):
-        r = rel(g_gpu.grad, leaf.grad)
-        assert r < 2e-2, r
+    for i, (g_gpu, leaf) in enumerate(zip(model.parameters(), cpu.lora_leaves())):
+        r = rel(g_gpu.grad / scale, leaf.grad)
+        assert r < 2e-2, (i, r)
