@@ -34,8 +34,10 @@ SIGNATURES = {
     "qlora_ce_piece": [P, I64, P, P, P, P, P, P, P, I64, I64, I64, I64, I64, P],
     "qlora_ce_finish": [P, P, P, P, P, P, P, P, P, P, I64, I64, I64, P],
     "qlora_ce_grad": [P, I64, P, P, I64, I64, I64, P],
-    "qlora_nf4_gemm": [P, I64, I32, P, P, P, P, P, P, I32, I32, I32, I32, I64, I64, I64, I64,
-                       P, I64, P, P, I64, I64, I32, I32, I64, I32, I32, P, I64, P],
+    "qlora_nf4_gemm": [P, I64, P, P, P, P, P, P, I32, I32, I32, I32, I64, I64, I64, I64,
+                       P, I64, P, P, I64, I64, I32, I32, I64, I32, P, I64, P],
+    "qlora_hgemm": [P, I64, P, I64, I64, I64, I64, I32, P, I64, P, P, I64, I32, I64, I32, P, I64,
+                    P],
     "qlora_resid_add": [P, P, P, I64, P],
     "qlora_lora_fwd_rows": [P, P, P, P, P, P, P, P, P, P, I64, I32, I32, I32, I32, P],
     "qlora_lora_bwd_rows": [P, P, I64, P, P, P, P, P, P, P, P, I64, I32, I32, I32, I32, F32, P],

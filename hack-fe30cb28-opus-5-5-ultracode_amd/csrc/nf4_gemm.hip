@@ -1,51 +1,70 @@
-// NF4 dequantisation fused into fp16 MFMA GEMMs for the frozen projections of the step.
-// Reference: the dequant kernel (kernels.py:68-105) followed by cuBLAS at engine.py:1082
+// fp16 MFMA GEMMs of the step, with the B operand either fp16 in memory or NF4 decoded inside the
+// kernel. Reference: the dequant kernel (kernels.py:68-105) followed by cuBLAS at engine.py:1082
 // (qkv + bias), 1112 (o), 1163 (gate|up), 1179 (down) in forward and 1239, 1293, 1301, 1316
-// (dY W) in backward.
+// (dY W) in backward, and the lm_head products (engine.py:1376-1381).
 //
-//   NT (forward):  C[m, n] = sum_k A[m, k] W[n, k]      W = [N, K] NF4, K = reduction
-//   NN (backward): C[m, n] = sum_k A[m, k] W[k, n]      W = [K, N] NF4, N = W's columns
+//   NT (forward):  C[m, n] = sum_k A[m, k] B[n, k]      B = W [N, K], K = reduction
+//   NN (backward): C[m, n] = sum_k A[m, k] B[k, n]      B = W [K, N], N = W's columns
 //
-// The W tile is decoded once per workgroup, straight from the bitsandbytes bytes (4-bit codes,
-// double-quantised absmax) into LDS as fp16, with the same two roundings as the standalone
-// dequant, so the fused product equals dequant-then-GEMM up to the fp32 summation order. The
-// LDS B tile is always [n][k] with k contiguous (the MFMA B-operand layout): in NN each thread
-// decodes an 8-row x 4-column block and packs each column's 8 values along the rows.
+// One workgroup = 4 wavefronts on a 256 x 256 output tile, k-tiles of 64; each wavefront owns a
+// 128 x 128 block as 4 x 4 v_mfma_f32_32x32x16_f16 accumulators (256 accumulation registers, one
+// wavefront per SIMD). On gfx950 a 128 x 128 wavefront block is what keeps the operand reads
+// below the MFMA time: per k-tile a wavefront reads 2 x 128 x 64 fp16 from LDS for 64 MFMAs
+// (half of LDS's 128 B/clk against 2.5 PFLOP/s); smaller blocks make the kernel LDS-bound.
 //
-// Two tile shapes: 256 x 256 x 64 with 8 wavefronts (2 x 4, each a 128 x 64 block of
-// v_mfma_f32_32x32x16_f16 accumulators; two wavefronts per SIMD, so one's NF4 decode (VALU)
-// overlaps the other's MFMAs) for the wide projections, and 128 x 128 x 64 with 4 wavefronts
-// (2 x 2 of 64 x 64) for the 1536/2048-wide ones, where 256-wide tiles would leave most of the
-// 256 CUs idle. The 256-entry double-quant code and the 16 NF4 levels live in LDS; a thread's
-// global loads for k-tile t + 1 (activations, packed nibbles, absmax bytes) are issued before
-// the MFMAs of tile t and decoded into the other LDS buffer after them (double buffering, one
-// barrier per k-tile). LDS rows hold 64 halves (eight 16-byte chunks); chunk c of row r sits
-// at c ^ ((r ^ r >> 3) & 7), so the fragment reads (consecutive rows, same chunk) and the tile
-// writes are free of bank conflicts. Workgroups are ordered so each XCD (blocks are dispatched
-// round-robin over the 8 XCDs) sweeps a contiguous range of W tiles.
+// Operand staging. The A tile (and an fp16 B tile) goes from global memory straight into LDS
+// (global_load_lds_dwordx4: a wavefront instruction writes 1 KB of consecutive LDS, lane l at
+// 16 l), two stages, the next k-tile's loads issued at the top of the current one. The LDS
+// layout is swizzled through the choice of which global 16-byte chunk a lane fetches: in a
+// K-contiguous tile [rows][64] (A; B in NT) chunk c of row r sits in slot c ^ ((r >> 1) & 7), so
+// a fragment read (16 consecutive rows, one chunk, per 16-lane pass) covers all 64 banks; in an
+// N-contiguous tile [64][256] (B in NN) chunk c of row k sits in slot c ^ ((k & 3) << 2), the
+// pattern under which ds_read_b64_tr_b16 (4 rows x 16 columns per 16 lanes) is conflict-free.
+// Every stage is its own __shared__ array and the loop is unrolled by two, so the compiler can
+// tell which buffer a read touches (an LDS read is otherwise held behind every outstanding LDS
+// DMA); the waits are explicit: vmcnt(0) + lgkmcnt(0) and one s_barrier per k-tile.
 //
-// Split-K: with splits > 1 each z-slice reduces a contiguous range of k-tiles into an fp32
-// workspace [splits, M, N]; a second kernel sums the slices and applies the epilogue.
+// NF4 B. A thread decodes one 64-value block per k-tile (NT: one W row of the tile; NN: a
+// quarter of one W row): its packed bytes (32) and the block's scale inputs are loaded two
+// k-tiles ahead into registers, and the block is decoded while the MFMAs of the current k-tile
+// run, into the other B stage. Decode: the block's 16 possible values fp16(fp32(level * scale))
+// (16 products, 8 v_cvt_pk_f16_f32: the standalone dequant's two roundings) are split into a
+// low-byte and a high-byte plane of 16 bytes each; each value is then looked up by its code
+// with v_perm_b32 (two 8-byte halves of a plane, merged by the code's bit 3): about 4 VALU
+// instructions per value and no LDS lookup table (LDS bandwidth is the scarce resource here).
+// The result equals dequant-then-GEMM bit for bit in the B operand.
 //
-// Epilogues: fp16 store; + fp16 bias (qkv); fp32 residual add out = res + f32(fp16(acc))
-// (h3 = h2 + d); SwiGLU m = fp16(silu(fp16 g) * fp16 u) with the gate and up rows of one output
-// column in the same wavefront (gate|up forward without materialising [gate|up]).
+// Epilogues: fp16 store; + fp16 bias (qkv); fp32 residual out = res + f32(fp16(acc)) (down);
+// SwiGLU m = fp16(silu(fp16 g) * fp16 u) (gate|up: each wavefront's first two 32-column blocks
+// are gate rows, the last two the up rows of the same output columns); fp32 partial sums for
+// split-K ([splits, M, N], summed in a fixed order by splitk_reduce_kernel).
+//
+// Work order: workgroup ids are dealt to the 8 XCDs in turn; tile_order gives each XCD a
+// contiguous range of tiles (the M tiles of a few N tiles), so an XCD's L2 holds the B tiles it
+// reads and the A tiles are shared through the MALL.
 #include "nf4.h"
 
 namespace qlora {
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) short4_t lds_short4_t;
+typedef __attribute__((address_space(3))) void lds_void_t;
 
-constexpr int kBK = 64;
+constexpr int kBM = 256, kBN = 256, kBK = 32, kStages = 4, kThreads = 256;
+constexpr int kTile = 256 * kBK;  // halves per operand stage (16 KB)
 
 enum { kEpiStore = 0, kEpiBias = 1, kEpiResid = 2, kEpiSwiglu = 3, kEpiPartial = 4 };
+enum { kBHalf = 0, kBNF4 = 1 };
 
 struct GemmArgs {
-  const void* a;         // [M, Kr] fp16, or fp32 (a_f32: rounded to fp16 on load)
+  const uint16_t* a;     // A [M, Kr] fp16
   int64_t lda;
-  NF4Ref w;
-  int64_t Kw;            // W's row length (columns)
+  const uint16_t* b;     // fp16 B: NT [N rows, Kr], NN [Kr rows, N]
+  int64_t ldb;
+  NF4Ref w;              // NF4 B: W [rows, Kw] (NT: rows = N, Kw = Kr; NN: rows = Kr, Kw = N)
+  int64_t Kw;
   void* c;               // fp16 [M, ldc]; fp32 for kEpiResid; fp32 [splits, M, N] partials
   int64_t ldc;
   const uint16_t* bias;  // fp16 [N] (kEpiBias)
@@ -53,314 +72,481 @@ struct GemmArgs {
   int64_t ldr;
   int64_t M, N, Kr;      // output rows, output columns, reduction length
   int64_t I;             // SwiGLU: first W row of the up projection
-  int64_t kt_per_split;  // k-tiles per z-slice
+  int kt_per_split;      // k-tiles per z-slice
+  int m_tiles;
 };
 
-__device__ __forceinline__ int swz(int row) { return (row ^ (row >> 3)) & 7; }
-__device__ __forceinline__ int lds_off(int row, int chunk) {
-  return row * kBK + ((chunk ^ swz(row)) << 3);
+// ---- swizzled LDS offsets (in halves) ---------------------------------------------------------
+__device__ __forceinline__ int kmaj_off(int row, int chunk) {  // [rows][32]
+  return row * 32 + ((chunk ^ ((row >> 2) & 3)) << 3);
+}
+__device__ __forceinline__ int nmaj_off(int row, int chunk) {  // [32][256]
+  return row * 256 + ((chunk ^ ((row & 3) << 2)) << 3);
 }
 
+// Workgroup b of `total` -> tile index: XCD x (= b % 8) takes the contiguous range
+// [x total/8, (x+1) total/8) of tiles.
 __device__ __forceinline__ int64_t tile_order(int64_t b, int64_t total) {
   const int64_t full = total / 8 * 8;
   return b < full ? (b % 8) * (full / 8) + b / 8 : b;
 }
 
-// The raw inputs of one block scale, loaded with the tile; the scale itself is formed when the
-// tile is decoded (the code2 lookup and the segment offset come from LDS, after the absmax byte
-// has arrived). Every load is unconditional (pointers selected instead of branches), so the
-// loads of a tile issue back to back instead of each waiting for the one before.
-struct ScaleIn {
-  uint32_t q;    // nested: absmax code
-  float a2;      // nested: absmax2 of the block's group; plain: the fp32 absmax
-  uint32_t seg;  // nested: segment of the block (stacked weights)
+// ---- global -> LDS (DMA) ----------------------------------------------------------------------
+// Lane byte offsets of a tile's DMA relative to a wave-uniform base (the tile's first element),
+// computed once: the loads then take the scalar-base + 32-bit vector-offset form and advance by
+// moving the base.
+//
+// K-contiguous tile (256 rows x 32 halves): wavefront w loads rows 64w .. 64w+63, sixteen rows
+// per instruction.
+struct DmaK {
+  uint32_t off[4];
+  // row_of(r): the row (relative to the base) that tile row r holds
+  template <typename RowOf>
+  __device__ __forceinline__ void init(int64_t ld, RowOf row_of, int wave, int lane) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int r = 64 * wave + 16 * j + (lane >> 2);
+      const int c = (lane & 3) ^ ((r >> 2) & 3);
+      off[j] = (uint32_t)((row_of(r) * ld + 8 * c) * 2);
+    }
+  }
+  // base: the tile's element (row0, k0)
+  __device__ __forceinline__ void issue(const uint16_t* base, uint16_t* dst, int wave) const {
+    const char* b = reinterpret_cast<const char*>(base);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      __builtin_amdgcn_global_load_lds(b + off[j], (lds_void_t*)(dst + (64 * wave + 16 * j) * 32),
+                                       16, 0, 0);
+  }
 };
 
-__device__ __forceinline__ ScaleIn scale_load(const NF4Ref& w, int64_t b) {
-  ScaleIn s;
+// N-contiguous tile (32 rows x 256 halves): wavefront w loads rows 8w .. 8w+7, two rows per
+// instruction.
+struct DmaN {
+  uint32_t off[4];
+  __device__ __forceinline__ void init(int64_t ld, int wave, int lane) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int r = 8 * wave + 2 * j + (lane >> 5);
+      const int c = (lane & 31) ^ ((r & 3) << 2);
+      off[j] = (uint32_t)((r * ld + 8 * c) * 2);
+    }
+  }
+  __device__ __forceinline__ void issue(const uint16_t* base, uint16_t* dst, int wave) const {
+    const char* b = reinterpret_cast<const char*>(base);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      __builtin_amdgcn_global_load_lds(b + off[j], (lds_void_t*)(dst + (8 * wave + 2 * j) * 256),
+                                       16, 0, 0);
+  }
+};
+
+// ---- NF4 block decode -------------------------------------------------------------------------
+struct NF4Raw {      // 32 values (half a 64-value block): codes and the inputs of the scale
+  uint4 v;           // 16 bytes of codes
+  uint32_t q;        // nested: absmax code
+  float a2;          // nested: absmax2 of the block's group; plain: the fp32 absmax
+  uint32_t seg;      // nested: segment of the block (stacked weights)
+};
+
+// Three vector-memory loads (the codes, the absmax byte, absmax2 or the fp32 absmax).
+__device__ __forceinline__ void nf4_load(NF4Raw& r, const NF4Ref& w, int64_t e) {
+  r.v = *reinterpret_cast<const uint4*>(w.packed + (e >> 1));
+  const int64_t b = e >> 6;
   const bool nested = w.nested;
-  s.q = static_cast<const uint8_t*>(w.absmax)[nested ? b : 0];
-  s.a2 = nested ? w.absmax2[b >> w.bs2_shift] : static_cast<const float*>(w.absmax)[b];
-  s.seg = (uint32_t)((int)(b >= w.seg1) + (int)(b >= w.seg2));
-  return s;
+  r.q = static_cast<const uint8_t*>(w.absmax)[nested ? b : 0];
+  r.a2 = nested ? w.absmax2[b >> w.bs2_shift] : static_cast<const float*>(w.absmax)[b];
+  r.seg = (uint32_t)((int)(b >= w.seg1) + (int)(b >= w.seg2));
 }
 
-// fp32(fp32(code2[q] * absmax2) + offset), the product rounded before the add (bitsandbytes).
-__device__ __forceinline__ float scale_of(const ScaleIn& s, int nested, const float* c2,
-                                          const float* offs) {
-  if (!nested) return s.a2;
-  float prod = c2[s.q] * s.a2;
-  fp32_barrier(prod);
-  return prod + offs[s.seg];
-}
-
-template <int BM, int NT, bool A_F32>
-struct ALoader {
-  static constexpr int kPer = BM * kBK / 8 / NT;  // 16-byte chunks per thread
-  uint4 v[kPer];
-  __device__ __forceinline__ void load(const GemmArgs& g, int64_t m0, int64_t k0) {
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const int id = threadIdx.x + NT * i;
-      const int row = id >> 3, col = (id & 7) * 8;
-      const int64_t m = m0 + row;
-      const bool ok = m < g.M;
-      const int64_t mc = ok ? m : g.M - 1;  // rows past M: load a valid row, then zero it
-      uint4 x;
-      if constexpr (A_F32) {
-        const float* p = static_cast<const float*>(g.a) + mc * g.lda + k0 + col;
-        const float4 lo = reinterpret_cast<const float4*>(p)[0];
-        const float4 hi = reinterpret_cast<const float4*>(p)[1];
-        x = make_uint4(pack2h(lo.x, lo.y), pack2h(lo.z, lo.w), pack2h(hi.x, hi.y),
-                       pack2h(hi.z, hi.w));
-      } else {
-        x = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(g.a) + mc * g.lda +
-                                            k0 + col);
-      }
-      v[i] = ok ? x : make_uint4(0, 0, 0, 0);
-    }
-  }
-  __device__ __forceinline__ void store(uint16_t* s) const {
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const int id = threadIdx.x + NT * i;
-      *reinterpret_cast<uint4*>(s + lds_off(id >> 3, id & 7)) = v[i];
-    }
-  }
+// The block's 16 values fp16(fp32(level[c] * scale)) as byte planes: lo[p] holds the low bytes
+// of values 4p .. 4p+3, hi[p] their high bytes.
+struct NF4Planes {
+  uint32_t lo[4], hi[4];
 };
 
-// W row of LDS B row `n` in the NT orientation. SwiGLU: within each wavefront's WN rows, the
-// first half are gate rows and the second half the up rows of the same output columns.
-template <int BN, int WN, int EPI>
+__device__ __forceinline__ NF4Planes nf4_planes(float scale, const float* lv) {
+  uint32_t d[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float p0 = lv[2 * i] * scale, p1 = lv[2 * i + 1] * scale;
+    fp32_barrier(p0);  // the fp32 product, then one RNE rounding to fp16 (never an FMA-mix)
+    fp32_barrier(p1);
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    d[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){p0, p1}, h2));
+  }
+  NF4Planes t;
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    t.lo[p] = __builtin_amdgcn_perm(d[2 * p + 1], d[2 * p], 0x06040200u);
+    t.hi[p] = __builtin_amdgcn_perm(d[2 * p + 1], d[2 * p], 0x07050301u);
+  }
+  return t;
+}
+
+// Four values from four codes (one per byte of `n`, 0..15): two packed fp16 pairs.
+__device__ __forceinline__ uint2 nf4_lookup4(const NF4Planes& t, uint32_t n) {
+  const uint32_t s = n & 0x07070707u;
+  const uint32_t sel = ((n >> 1) & 0x04040404u) | 0x03020100u;  // byte i: i, or 4 + i if >= 8
+  const uint32_t lo = __builtin_amdgcn_perm(__builtin_amdgcn_perm(t.lo[3], t.lo[2], s),
+                                            __builtin_amdgcn_perm(t.lo[1], t.lo[0], s), sel);
+  const uint32_t hi = __builtin_amdgcn_perm(__builtin_amdgcn_perm(t.hi[3], t.hi[2], s),
+                                            __builtin_amdgcn_perm(t.hi[1], t.hi[0], s), sel);
+  return make_uint2(__builtin_amdgcn_perm(hi, lo, 0x05010400u),
+                    __builtin_amdgcn_perm(hi, lo, 0x07030602u));
+}
+
+// Eight values (16 bytes, memory order) from one 32-bit word of codes: element 2k is the high
+// nibble of byte k.
+__device__ __forceinline__ uint4 nf4_decode8(const NF4Planes& t, uint32_t wd) {
+  const uint32_t lo4 = wd & 0x0F0F0F0Fu, hi4 = (wd >> 4) & 0x0F0F0F0Fu;
+  const uint2 a = nf4_lookup4(t, __builtin_amdgcn_perm(hi4, lo4, 0x01050004u));
+  const uint2 b = nf4_lookup4(t, __builtin_amdgcn_perm(hi4, lo4, 0x03070206u));
+  return make_uint4(a.x, a.y, b.x, b.y);
+}
+
+// Branch-free (a branch would split the main loop's scheduling region): without double
+// quantisation the code2 lookup reads a harmless table entry and its result is not selected.
+__device__ __forceinline__ float nf4_scale(const NF4Raw& r, int nested, const float* c2,
+                                           const float* offs) {
+  float prod = c2[r.q] * r.a2;
+  fp32_barrier(prod);  // bitsandbytes rounds the product before adding the offset
+  float sc = prod + offs[r.seg];
+  fp32_barrier(sc);  // (also keeps the table reads out of a branch on `nested`)
+  return nested ? sc : r.a2;
+}
+
+// W row of LDS B row `n` (NT). SwiGLU: within each wavefront's 128 rows the first 64 are gate
+// rows and the last 64 the up rows of the same 64 output columns.
+template <int EPI>
 __device__ __forceinline__ int64_t nt_wrow(const GemmArgs& g, int64_t tile_n, int n) {
   if constexpr (EPI == kEpiSwiglu) {
-    constexpr int HALF = WN / 2;
-    const int64_t j = tile_n * (BN / 2) + (n / WN) * HALF + (n % HALF);
-    return (n % WN) >= HALF ? g.I + j : j;
+    const int64_t j = tile_n * 128 + (n >> 7) * 64 + (n & 63);
+    return (n & 64) ? g.I + j : j;
   } else {
-    return tile_n * BN + n;
+    return tile_n * kBN + n;
   }
 }
 
-// NT: B tile = W rows (BN) x 64 columns; a run = 32 columns of one row (16 bytes, one scale).
-template <int BN, int WN, int NT, int EPI>
-struct BLoaderNT {
-  static constexpr int kPer = BN * kBK / 32 / NT;
-  uint4 v[kPer];
-  ScaleIn sc[kPer];
-  __device__ __forceinline__ void load(const GemmArgs& g, int64_t tile_n, int64_t k0) {
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const int id = threadIdx.x + NT * i;
-      const int n = id % BN, part = id / BN;
-      const int64_t e = nt_wrow<BN, WN, EPI>(g, tile_n, n) * g.Kw + k0 + 32 * part;
-      v[i] = *reinterpret_cast<const uint4*>(g.w.packed + (e >> 1));
-      sc[i] = scale_load(g.w, e >> g.w.bs1_shift);
-    }
-  }
-  __device__ __forceinline__ void store(uint16_t* s, const GemmArgs& g, const float* lut,
-                                        const float* c2, const float* offs) const {
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const int id = threadIdx.x + NT * i;
-      const int n = id % BN, part = id / BN;
-      const float scale = scale_of(sc[i], g.w.nested, c2, offs);
-      *reinterpret_cast<uint4*>(s + lds_off(n, 4 * part + 0)) = nf4_decode_word(v[i].x, scale, lut);
-      *reinterpret_cast<uint4*>(s + lds_off(n, 4 * part + 1)) = nf4_decode_word(v[i].y, scale, lut);
-      *reinterpret_cast<uint4*>(s + lds_off(n, 4 * part + 2)) = nf4_decode_word(v[i].z, scale, lut);
-      *reinterpret_cast<uint4*>(s + lds_off(n, 4 * part + 3)) = nf4_decode_word(v[i].w, scale, lut);
-    }
-  }
+// ---- the kernel -------------------------------------------------------------------------------
+// The operand fragments of one 16-wide k-step: 4 A blocks (rows) and 4 B blocks (columns) of
+// 32, 8 halves a lane.
+struct Frags {
+  half8_t a[4], b[4];
 };
 
-// NN: B tile = W rows k0..k0+63 x columns n0..n0+BN-1; thread t decodes rows 8g..8g+7 of a
-// 4-column group (2 bytes per row, one scale per row) and writes each column's 8 values as one
-// 16-byte chunk of the [n][k] tile. The eight scales' inputs are kept compact (absmax codes
-// packed four to a register, segment numbers as 2-bit fields) to stay within two wavefronts'
-// register budget per SIMD.
-template <int BN, int NT>
-struct BLoaderNN {
-  static constexpr int CW = 8 * BN / NT;   // columns per thread: 4 or 8
-  static constexpr int CHUNKS = BN / CW;   // column groups per row
-  static_assert(CW == 4 || CW == 8, "8 rows x 4 or 8 columns per thread");
-  static constexpr int VR = CW == 8 ? 8 : 4;  // registers of packed bytes
-  uint32_t v[VR];  // CW == 4: row i's two bytes in half i & 1 of v[i / 2]; CW == 8: row i
-  uint32_t q[2];   // nested: absmax code of row i in byte i & 3 of q[i / 4]
-  float a2[8];     // nested: absmax2; plain: the fp32 absmax
-  uint32_t seg;    // 2 bits per row
-  __device__ __forceinline__ void load(const GemmArgs& g, int64_t n0, int64_t k0) {
-    const int c = threadIdx.x % CHUNKS, gr = threadIdx.x / CHUNKS;
-    seg = 0;
-    uint32_t vv[8], qq[8];
+template <bool NN>
+__device__ __forceinline__ void read_frags(Frags& f, const uint16_t* sa, const uint16_t* sb,
+                                           int s, int wm, int wn, int lane) {
+  const int frow = lane & 31, fhalf = lane >> 5;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int64_t e = (k0 + 8 * gr + i) * g.Kw + n0 + CW * c;
-      if constexpr (CW == 8) vv[i] = *reinterpret_cast<const uint32_t*>(g.w.packed + (e >> 1));
-      else vv[i] = *reinterpret_cast<const uint16_t*>(g.w.packed + (e >> 1));
-      const ScaleIn si = scale_load(g.w, e >> g.w.bs1_shift);
-      qq[i] = si.q;
-      a2[i] = si.a2;
-      seg |= si.seg << (2 * i);
-    }
+  for (int i = 0; i < 4; ++i)
+    f.a[i] = *reinterpret_cast<const half8_t*>(
+        sa + kmaj_off(wm * 128 + 32 * i + frow, 2 * s + fhalf));
 #pragma unroll
-    for (int i = 0; i < VR; ++i) v[i] = CW == 8 ? vv[i] : (vv[2 * i] | (vv[2 * i + 1] << 16));
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-      q[i] = qq[4 * i] | (qq[4 * i + 1] << 8) | (qq[4 * i + 2] << 16) | (qq[4 * i + 3] << 24);
-  }
-  __device__ __forceinline__ void store(uint16_t* s, const GemmArgs& g, const float* lut,
-                                        const float* c2, const float* offs) const {
-    const int c = threadIdx.x % CHUNKS, gr = threadIdx.x / CHUNKS;
-    uint32_t out[CW][4];  // column j, row pair p: fp16 pair (row 2p, row 2p + 1)
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      float x[2][CW];
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int i = 2 * p + h;
-        const float scale = scale_of(
-            ScaleIn{(q[i >> 2] >> (8 * (i & 3))) & 0xFFu, a2[i], (seg >> (2 * i)) & 3u},
-            g.w.nested, c2, offs);
-        const uint32_t row = CW == 8 ? v[i] : ((v[i >> 1] >> (16 * (i & 1))) & 0xFFFFu);
-#pragma unroll
-        for (int k = 0; k < CW / 2; ++k) {
-          const uint32_t byte = (row >> (8 * k)) & 0xFFu;
-          float a = lut[byte >> 4] * scale;
-          float b = lut[byte & 15u] * scale;
-          fp32_barrier(a);  // fp16(fp32(level * scale)): two roundings
-          fp32_barrier(b);
-          x[h][2 * k] = a;
-          x[h][2 * k + 1] = b;
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < CW; ++j) out[j][p] = pack2h(x[0][j], x[1][j]);
-    }
-#pragma unroll
-    for (int j = 0; j < CW; ++j)
-      *reinterpret_cast<uint4*>(s + lds_off(CW * c + j, gr)) =
-          make_uint4(out[j][0], out[j][1], out[j][2], out[j][3]);
-  }
-};
-
-template <int BM, int BN>
-struct GemmSmem {
-  uint16_t a[2][BM * kBK];
-  uint16_t b[2][BN * kBK];
-  float lut[16];
-  float c2[256];
-  float offs[4];
-};
-
-template <int BM, int BN, int WGM, int WGN, bool NN, int EPI, bool A_F32>
-__global__ __launch_bounds__(WGM * WGN * 64) void nf4_gemm_kernel(GemmArgs g) {
-  constexpr int NT = WGM * WGN * 64;
-  constexpr int WM = BM / WGM, WN = BN / WGN, FM = WM / 32, FN = WN / 32;
-  __shared__ GemmSmem<BM, BN> sm;
-  const int tid = threadIdx.x;
-  if (tid < 16) sm.lut[tid] = g.w.standard ? kNF4Levels[tid] : g.w.code[tid];
-  if (g.w.nested) {
-    for (int i = tid; i < 256; i += NT) sm.c2[i] = g.w.code2[i];
-    // segment offsets: one per stacked weight; an absent segment bound is INT64_MAX
-    if (tid < 3) {
-      const int nseg = 1 + (int)(g.w.seg1 != INT64_MAX) + (int)(g.w.seg2 != INT64_MAX);
-      sm.offs[tid] = g.w.offsets[tid < nseg ? tid : 0];
+  for (int j = 0; j < 4; ++j) {
+    if constexpr (!NN) {
+      f.b[j] = *reinterpret_cast<const half8_t*>(
+          sb + kmaj_off(wn * 128 + 32 * j + frow, 2 * s + fhalf));
+    } else {
+      // ds_read_b64_tr_b16: lane p of a 16-lane group reads row k + p / 4, columns
+      // c0 + 4 (p % 4) .. + 3; lane i of the group receives column c0 + i of rows k .. k+3
+      const int p = lane & 15;
+      const int col = wn * 128 + 32 * j + 16 * ((lane >> 4) & 1) + 4 * (p & 3);
+      const int k = 16 * s + 8 * fhalf + (p >> 2);
+      const int o0 = nmaj_off(k, col >> 3) + (col & 7);
+      const int o1 = nmaj_off(k + 4, col >> 3) + (col & 7);
+      const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)(sb + o0));
+      const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)(sb + o1));
+      f.b[j] = __builtin_bit_cast(half8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
     }
   }
+}
 
-  const int64_t m_tiles = (g.M + BM - 1) / BM;
-  const int64_t t = tile_order(blockIdx.x, gridDim.x);
-  const int64_t tile_m = t % m_tiles, tile_n = t / m_tiles;
-  const int64_t m0 = tile_m * BM;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int wm = wave / WGN, wn = wave % WGN;
+__device__ __forceinline__ void mfma_step(f32x16 (&acc)[4][4], const Frags& f) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
+}
 
-  ALoader<BM, NT, A_F32> la;
-  BLoaderNT<BN, WN, NT, EPI> lbt;
-  BLoaderNN<BN, NT> lbn;
+// Scheduling of one k-step: the reads of the next k-step's fragments between this k-step's 16
+// MFMAs (one read per MFMA), `VMEM` global loads (the prefetch DMA) one per MFMA from the
+// first, and `VALU` VALU instructions (the NF4 decode, the DMA addresses) after each MFMA.
+template <bool NN, int VALU, int VMEM>
+__device__ __forceinline__ void sched_step() {
+  constexpr int reads = NN ? 12 : 8;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+    if (i < reads) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+    if (i < VMEM) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
+    if constexpr (VALU > 0) __builtin_amdgcn_sched_group_barrier(0x002, VALU, 0);  // VALU
+  }
+}
+
+// Half `part` (0, 1) of the decode of one raw half-block (32 values) with scale `sc` into the
+// B stage: part 0 forms the byte planes and words 0-1, part 1 words 2-3. NT: LDS row `row`,
+// chunks 0-3; NN: row `row`, chunks chunk0 .. chunk0+3.
+template <bool NN>
+__device__ __forceinline__ void nf4_decode_part(const NF4Raw& r, float sc, NF4Planes& t,
+                                                uint16_t* sb, int row, int chunk0,
+                                                const float* lv, int part) {
+  const uint32_t wds[4] = {r.v.x, r.v.y, r.v.z, r.v.w};
+  if (part == 0) t = nf4_planes(sc, lv);
+#pragma unroll
+  for (int c = 2 * part; c < 2 * part + 2; ++c) {
+    const int off = NN ? nmaj_off(row, chunk0 + c) : kmaj_off(row, c);
+    *reinterpret_cast<uint4*>(sb + off) = nf4_decode8(t, wds[c]);
+  }
+}
+
+// s_waitcnt with vmcnt(VM) and lgkmcnt(0), then s_barrier: this thread's LDS stores and all
+// but its VM most recent vector-memory loads are done, and so are every other thread's.
+template <int VM>
+__device__ __forceinline__ void sync_tile() {
+  static_assert(VM >= 0 && VM < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((VM & 15) | ((VM >> 4) << 14) | (7 << 4));
+  __builtin_amdgcn_s_barrier();
+}
+
+template <bool NN, int BSRC, int EPI>
+__global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
+  __shared__ __attribute__((aligned(1024))) uint16_t sA0[kTile];
+  __shared__ __attribute__((aligned(1024))) uint16_t sA1[kTile];
+  __shared__ __attribute__((aligned(1024))) uint16_t sA2[kTile];
+  __shared__ __attribute__((aligned(1024))) uint16_t sA3[kTile];
+  __shared__ __attribute__((aligned(1024))) uint16_t sB0[kTile];
+  __shared__ __attribute__((aligned(1024))) uint16_t sB1[kTile];
+  __shared__ __attribute__((aligned(1024))) uint16_t sB2[kTile];
+  __shared__ __attribute__((aligned(1024))) uint16_t sB3[kTile];
+  __shared__ float s_c2[256];
+  __shared__ float s_offs[4];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+
+  const int64_t t_lin = tile_order(blockIdx.x, gridDim.x);
+  const int64_t tile_m = t_lin % g.m_tiles, tile_n = t_lin / g.m_tiles;
+  const int64_t m0 = tile_m * kBM;
   const int64_t kt0 = (int64_t)blockIdx.z * g.kt_per_split;
   int64_t kt1 = kt0 + g.kt_per_split;
-  const int64_t ktiles_all = g.Kr / kBK;
-  if (kt1 > ktiles_all) kt1 = ktiles_all;
+  if (kt1 > g.Kr / kBK) kt1 = g.Kr / kBK;  // k-tile counts are multiples of 4 (host check)
+  const int64_t kt_last = kt1 - 1;
 
-  auto load_tile = [&](int64_t kt) {
-    la.load(g, m0, kt * kBK);
-    if constexpr (NN) lbn.load(g, tile_n * BN, kt * kBK);
-    else lbt.load(g, tile_n, kt * kBK);
-  };
-  auto store_tile = [&](int buf) {
-    la.store(sm.a[buf]);
-    if constexpr (NN) lbn.store(sm.b[buf], g, sm.lut, sm.c2, sm.offs);
-    else lbt.store(sm.b[buf], g, sm.lut, sm.c2, sm.offs);
-  };
-
-  f32x16 acc[FM][FN];
-#pragma unroll
-  for (int i = 0; i < FM; ++i)
-#pragma unroll
-    for (int j = 0; j < FN; ++j) acc[i][j] = f32x16{};
-
-  if (kt0 < kt1) load_tile(kt0);
-  __syncthreads();  // lut, c2, offs
-  if (kt0 < kt1) store_tile(0);
-  __syncthreads();
-
-  const int frow = lane & 31, fchunk = lane >> 5;
-  for (int64_t kt = kt0; kt < kt1; ++kt) {
-    const int buf = (kt - kt0) & 1;
-    const bool more = kt + 1 < kt1;
-    if (more) load_tile(kt + 1);
-    const uint16_t* sa = sm.a[buf];
-    const uint16_t* sb = sm.b[buf];
-#pragma unroll
-    for (int ks = 0; ks < kBK / 16; ++ks) {
-      half8_t af[FM], bf[FN];
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-        af[i] = *reinterpret_cast<const half8_t*>(
-            sa + lds_off(wm * WM + i * 32 + frow, 2 * ks + fchunk));
-#pragma unroll
-      for (int j = 0; j < FN; ++j)
-        bf[j] = *reinterpret_cast<const half8_t*>(
-            sb + lds_off(wn * WN + j * 32 + frow, 2 * ks + fchunk));
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+  DmaK dma_a;
+  const int64_t a_rows = g.M - m0;  // rows past M re-read the last row
+  dma_a.init(g.lda, [&](int r) -> int64_t { return r < a_rows ? r : a_rows - 1; }, wave, lane);
+  const uint16_t* a_base = g.a + m0 * g.lda;  // + k0 per k-tile
+  DmaK dma_bk;
+  DmaN dma_bn;
+  const uint16_t* b_base = nullptr;
+  int64_t b_step = 0;
+  if constexpr (BSRC == kBHalf) {
+    if constexpr (NN) {
+      dma_bn.init(g.ldb, wave, lane);
+      b_base = g.b + tile_n * kBN;
+      b_step = (int64_t)kBK * g.ldb;
+    } else {
+      // rows past N (a last, partial tile: the lm_head's 151,936) re-read row N - 1
+      dma_bk.init(g.ldb, [&](int r) -> int64_t {
+        const int64_t row = nt_wrow<EPI>(g, tile_n, r);
+        return (EPI == kEpiSwiglu || row < g.N) ? row : g.N - 1;
+      }, wave, lane);
+      b_base = g.b;
+      b_step = kBK;
     }
-    if (more) store_tile(buf ^ 1);
-    __syncthreads();
   }
+
+  // NF4: levels in registers, the double-quant code and the segment offsets in LDS; this
+  // thread's half-block at k-tile kt is element e_base + kt * e_step, decoded into row b_row
+  // from chunk b_chunk0 (NT: row tid; NN: row tid / 8, chunks 4 (tid % 8) ..)
+  float lv[16];
+  NF4Raw raw0, raw1, raw2, raw3;  // half-block of k-tile kt in raw[kt % 4]
+  int64_t e_base = 0, e_step = 0;
+  int b_row = 0, b_chunk0 = 0;
+  if constexpr (BSRC == kBNF4) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) lv[i] = g.w.standard ? kNF4Levels[i] : g.w.code[i];
+    if (g.w.nested) {
+      s_c2[tid] = g.w.code2[tid];
+      if (tid < 3) {
+        const int nseg = 1 + (int)(g.w.seg1 != INT64_MAX) + (int)(g.w.seg2 != INT64_MAX);
+        s_offs[tid] = g.w.offsets[tid < nseg ? tid : 0];
+      }
+    }
+    if constexpr (!NN) {
+      b_row = tid;
+      e_base = nt_wrow<EPI>(g, tile_n, tid) * g.Kw;
+      e_step = kBK;
+    } else {
+      b_row = tid >> 3;
+      b_chunk0 = 4 * (tid & 7);
+      e_base = (int64_t)b_row * g.Kw + tile_n * kBN + 32 * (tid & 7);
+      e_step = (int64_t)kBK * g.Kw;
+    }
+  }
+  // vector-memory instructions one k-tile issues (its DMA, or the A DMA and a raw half-block)
+  constexpr int kVmPerTile = 4 + (BSRC == kBHalf ? 4 : 3);
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+
+  auto clamp_kt = [&](int64_t kt) { return kt < kt1 ? kt : kt_last; };
+  auto issue_tile = [&](int64_t kt, uint16_t* sa, uint16_t* sb) {
+    kt = clamp_kt(kt);
+    dma_a.issue(a_base + kt * kBK, sa, wave);
+    if constexpr (BSRC == kBHalf) {
+      if constexpr (NN) dma_bn.issue(b_base + kt * b_step, sb, wave);
+      else dma_bk.issue(b_base + kt * b_step, sb, wave);
+    }
+  };
+
+  // prologue: k-tiles kt0 .. kt0+2 into stages 0-2; NF4: the raw half-blocks of kt0 .. kt0+3,
+  // the first two decoded into B stages 0 and 1
+  issue_tile(kt0, sA0, sB0);
+  issue_tile(kt0 + 1, sA1, sB1);
+  issue_tile(kt0 + 2, sA2, sB2);
+  NF4Planes planes;
+  if constexpr (BSRC == kBNF4) {
+    NF4Raw r0, r1;
+    nf4_load(r0, g.w, e_base + kt0 * e_step);
+    nf4_load(r1, g.w, e_base + (kt0 + 1) * e_step);
+    nf4_load(raw2, g.w, e_base + clamp_kt(kt0 + 2) * e_step);
+    nf4_load(raw3, g.w, e_base + clamp_kt(kt0 + 3) * e_step);
+    nf4_load(raw0, g.w, e_base + clamp_kt(kt0 + 4) * e_step);
+    __syncthreads();  // s_c2, s_offs
+    const float sc0 = nf4_scale(r0, g.w.nested, s_c2, s_offs);
+    nf4_decode_part<NN>(r0, sc0, planes, sB0, b_row, b_chunk0, lv, 0);
+    nf4_decode_part<NN>(r0, sc0, planes, sB0, b_row, b_chunk0, lv, 1);
+    const float sc1 = nf4_scale(r1, g.w.nested, s_c2, s_offs);
+    nf4_decode_part<NN>(r1, sc1, planes, sB1, b_row, b_chunk0, lv, 0);
+    nf4_decode_part<NN>(r1, sc1, planes, sB1, b_row, b_chunk0, lv, 1);
+  }
+  sync_tile<0>();
+
+  // Software pipeline over four LDS stages, unrolled by four so every buffer is static (k-tile
+  // t on stage t % 4). At the top of k-tile t the DMA of t + 3 goes into the stage k-tile t - 1
+  // used (free since the last barrier); NF4: the raw half-block of t + 5 is loaded into the
+  // registers of t + 1 (decoded at t - 1), and t + 2 is decoded into its B stage across both
+  // k-steps (done by the barrier that ends t + 1); its raw loads were issued three k-tiles
+  // earlier, so the barrier waits already cover them. Each k-step's 16 MFMAs run while the next k-step's fragments are
+  // read; the second k-step reads the first fragments of t + 1 after the barrier that makes
+  // t + 1 visible (the wait leaves the loads of t + 2 and t + 3 in flight). Past the last
+  // k-tile the prefetches re-read it into stages no longer read: a trip has no branch.
+  constexpr int kValu = BSRC == kBNF4 ? 5 : 0;
+  Frags f0, f1;
+  read_frags<NN>(f0, sA0, sB0, 0, wm, wn, lane);
+  auto k_tile = [&](int64_t t, uint16_t* sa, uint16_t* sb, uint16_t* sa_next, uint16_t* sb_next,
+                    uint16_t* sa_pre, uint16_t* sb_pre, uint16_t* sb_dec, NF4Raw& r_load,
+                    const NF4Raw& r_dec) {
+    float sc = 0.0f;
+    if constexpr (BSRC == kBNF4) sc = nf4_scale(r_dec, g.w.nested, s_c2, s_offs);
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags<NN>(f1, sa, sb, 1, wm, wn, lane);
+    if constexpr (BSRC == kBNF4)
+      nf4_decode_part<NN>(r_dec, sc, planes, sb_dec, b_row, b_chunk0, lv, 0);
+    mfma_step(acc, f0);
+    sched_step<NN, kValu, 0>();
+    __builtin_amdgcn_sched_barrier(0);
+    sync_tile<kVmPerTile>();  // k-tile t + 1 landed; t + 2 may still be in flight
+    // the DMA of t + 3 into the stage t - 1 used, issued while no LDS read is outstanding
+    issue_tile(t + 3, sa_pre, sb_pre);
+    if constexpr (BSRC == kBNF4) nf4_load(r_load, g.w, e_base + clamp_kt(t + 5) * e_step);
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags<NN>(f0, sa_next, sb_next, 0, wm, wn, lane);
+    if constexpr (BSRC == kBNF4)
+      nf4_decode_part<NN>(r_dec, sc, planes, sb_dec, b_row, b_chunk0, lv, 1);
+    mfma_step(acc, f1);
+    sched_step<NN, kValu, 0>();
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  for (int64_t t = kt0; t < kt1; t += 4) {
+    k_tile(t, sA0, sB0, sA1, sB1, sA3, sB3, sB2, raw1, raw2);
+    k_tile(t + 1, sA1, sB1, sA2, sB2, sA0, sB0, sB3, raw2, raw3);
+    k_tile(t + 2, sA2, sB2, sA3, sB3, sA1, sB1, sB0, raw3, raw0);
+    k_tile(t + 3, sA3, sB3, sA0, sB0, sA2, sB2, sB1, raw0, raw1);
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // the prefetches past the end: nothing left in flight
 
   // epilogue: register r of lane l in a 32x32 block holds row 8(r/4) + 4(l/32) + r%4, col l%32
   const int col_in = lane & 31;
+  if constexpr (EPI == kEpiStore || EPI == kEpiBias || EPI == kEpiSwiglu) {
+    // fp16 outputs go through LDS: each wavefront writes its block there as fp16 (2-byte LDS
+    // stores, chunks XOR-swizzled by row so both half-waves hit distinct banks), then stores
+    // whole rows to memory with 16-byte stores. Stages are free once every wavefront is done.
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_s_barrier();
+    uint16_t* lo = wave == 0 ? sA0 : wave == 1 ? sA2 : wave == 2 ? sB0 : sB2;
+    uint16_t* hi = wave == 0 ? sA1 : wave == 1 ? sA3 : wave == 2 ? sB1 : sB3;
+    constexpr int kCols = EPI == kEpiSwiglu ? 64 : 128;   // output columns of a wavefront
+    constexpr int kChunks = kCols / 8;
+    // [128 rows][kCols] fp16: rows 0-63 in `lo`, 64-127 in `hi`
+    auto stage_off = [&](int row, int chunk) {
+      return (row & 63) * kCols + ((chunk ^ (row & (kChunks - 1))) << 3);
+    };
 #pragma unroll
-  for (int i = 0; i < FM; ++i) {
+    for (int i = 0; i < 4; ++i) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int64_t m = m0 + wm * WM + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-      if (m >= g.M) continue;
-      if constexpr (EPI == kEpiSwiglu) {
+      for (int r = 0; r < 16; ++r) {
+        const int row = i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+        uint16_t* base = row < 64 ? lo : hi;
+        if constexpr (EPI == kEpiSwiglu) {
 #pragma unroll
-        for (int j = 0; j < FN / 2; ++j) {
-          const int64_t n = tile_n * (BN / 2) + wn * (WN / 2) + j * 32 + col_in;
-          const float gt = h2f(f2h(acc[i][j][r])), up = h2f(f2h(acc[i][j + FN / 2][r]));
-          const float mval = gt * sigmoid_fast(gt) * up;  // as glu_fwd_kernel
-          static_cast<uint16_t*>(g.c)[m * g.ldc + n] = f2h_bits(mval);
+          for (int j = 0; j < 2; ++j) {
+            const int col = j * 32 + col_in;
+            const float gt = h2f(f2h(acc[i][j][r])), up = h2f(f2h(acc[i][j + 2][r]));
+            const float mval = gt * sigmoid_fast(gt) * up;  // as glu_fwd_kernel
+            base[stage_off(row, col >> 3) + (col & 7)] = f2h_bits(mval);
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int col = j * 32 + col_in;
+            float v = acc[i][j][r];
+            if constexpr (EPI == kEpiBias) {
+              const int64_t n = tile_n * kBN + wn * 128 + col;
+              v += h2f_bits(g.bias[n < g.N ? n : g.N - 1]);
+            }
+            base[stage_off(row, col >> 3) + (col & 7)] = f2h_bits(v);
+          }
         }
-      } else {
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the wavefront's own LDS stores
+    constexpr int kRowsPer = 64 / kChunks;  // rows per 16-byte store instruction
+    const int64_t n_base = EPI == kEpiSwiglu ? tile_n * 128 + wn * 64 : tile_n * kBN + wn * 128;
 #pragma unroll
-        for (int j = 0; j < FN; ++j) {
-          const int64_t n = tile_n * BN + wn * WN + j * 32 + col_in;
-          float v = acc[i][j][r];
+    for (int k = 0; k < 128 / kRowsPer; ++k) {
+      const int row = k * kRowsPer + lane / kChunks, chunk = lane % kChunks;
+      const uint4 v = *reinterpret_cast<const uint4*>((row < 64 ? lo : hi) +
+                                                       stage_off(row, chunk));
+      const int64_t m = m0 + wm * 128 + row, n = n_base + chunk * 8;
+      if (m < g.M && n < g.N)
+        *reinterpret_cast<uint4*>(static_cast<uint16_t*>(g.c) + m * g.ldc + n) = v;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t m = m0 + wm * 128 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+        if (m >= g.M) continue;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int64_t n = tile_n * kBN + wn * 128 + j * 32 + col_in;
+          if (n >= g.N) continue;
+          const float v = acc[i][j][r];
           if constexpr (EPI == kEpiPartial) {
             static_cast<float*>(g.c)[((int64_t)blockIdx.z * g.M + m) * g.N + n] = v;
-          } else if constexpr (EPI == kEpiResid) {
-            static_cast<float*>(g.c)[m * g.ldc + n] = g.resid[m * g.ldr + n] + h2f(f2h(v));
           } else {
-            if constexpr (EPI == kEpiBias) v += h2f_bits(g.bias[n]);
-            static_cast<uint16_t*>(g.c)[m * g.ldc + n] = f2h_bits(v);
+            static_cast<float*>(g.c)[m * g.ldc + n] = g.resid[m * g.ldr + n] + h2f(f2h(v));
           }
         }
       }
@@ -404,86 +590,109 @@ using namespace qlora;
 
 namespace {
 
-template <int BM, int BN, int WGN, bool NN, int EPI, bool A_F32>
-void launch_gemm(const GemmArgs& g, dim3 grid, hipStream_t s) {
-  constexpr int WGM = 2;
-  hipLaunchKernelGGL((nf4_gemm_kernel<BM, BN, WGM, WGN, NN, EPI, A_F32>), grid,
-                     dim3(WGM * WGN * 64), 0, s, g);
-}
-
-template <int BM, int BN, int WGN, bool NN, int EPI>
-void launch_a(const GemmArgs& g, dim3 grid, hipStream_t s, bool a_f32) {
-  if (a_f32) launch_gemm<BM, BN, WGN, NN, EPI, true>(g, grid, s);
-  else launch_gemm<BM, BN, WGN, NN, EPI, false>(g, grid, s);
-}
-
-template <int BM, int BN, int WGN, bool NN>
-void launch_epi(const GemmArgs& g, dim3 grid, hipStream_t s, bool a_f32, int epi) {
+template <bool NN, int BSRC>
+void launch_epi(const GemmArgs& g, dim3 grid, hipStream_t s, int epi) {
+  const dim3 block(kThreads);
   switch (epi) {
-    case kEpiStore: launch_a<BM, BN, WGN, NN, kEpiStore>(g, grid, s, a_f32); break;
-    case kEpiBias: launch_a<BM, BN, WGN, NN, kEpiBias>(g, grid, s, a_f32); break;
-    case kEpiResid: launch_a<BM, BN, WGN, NN, kEpiResid>(g, grid, s, a_f32); break;
-    case kEpiPartial: launch_a<BM, BN, WGN, NN, kEpiPartial>(g, grid, s, a_f32); break;
+    case kEpiStore: hipLaunchKernelGGL((gemm_kernel<NN, BSRC, kEpiStore>), grid, block, 0, s, g); break;
+    case kEpiBias: hipLaunchKernelGGL((gemm_kernel<NN, BSRC, kEpiBias>), grid, block, 0, s, g); break;
+    case kEpiResid: hipLaunchKernelGGL((gemm_kernel<NN, BSRC, kEpiResid>), grid, block, 0, s, g); break;
+    case kEpiPartial: hipLaunchKernelGGL((gemm_kernel<NN, BSRC, kEpiPartial>), grid, block, 0, s, g); break;
     default:
-      if constexpr (!NN) launch_a<BM, BN, WGN, NN, kEpiSwiglu>(g, grid, s, a_f32);
+      if constexpr (!NN) hipLaunchKernelGGL((gemm_kernel<NN, BSRC, kEpiSwiglu>), grid, block, 0, s, g);
       break;
   }
 }
 
 bool al(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 
+// Shared launch path: shapes and workspace checked, then the tile grid (and the split-K reduce).
+int run_gemm(GemmArgs& g, int bsrc, int mode, int epi, int splits, float* ws, int64_t ws_elems,
+             hipStream_t s) {
+  const int64_t n_tiles = epi == kEpiSwiglu ? g.N / 128 : qlora_cdiv(g.N, kBN);
+  g.m_tiles = (int)qlora_cdiv(g.M, kBM);
+  const int64_t grid = (int64_t)g.m_tiles * n_tiles;
+  QLORA_CHECK_ARG(grid < (1ll << 31));
+  // fp16 outputs leave in 16-byte row pieces
+  QLORA_CHECK_ARG(epi == kEpiResid || splits > 1 || (g.ldc % 8 == 0 && al(g.c, 16)));
+  QLORA_CHECK_ARG(splits == 1 || (ws && ws_elems >= (int64_t)splits * g.M * g.N && al(ws, 16)));
+  const int64_t ktiles = g.Kr / kBK;
+  QLORA_CHECK_ARG(ktiles % kStages == 0);  // the main loop takes four k-tiles per trip
+  g.kt_per_split = (int)(qlora_cdiv(qlora_cdiv(ktiles, splits), kStages) * kStages);
+  QLORA_CHECK_ARG((int64_t)g.kt_per_split * (splits - 1) < ktiles);  // no empty slice
+  const int kepi = splits > 1 ? (int)kEpiPartial : epi;
+  void* out = g.c;
+  if (splits > 1) g.c = ws;
+  const dim3 gdim((unsigned)grid, 1, (unsigned)splits);
+  if (mode == 0) {
+    if (bsrc == kBNF4) launch_epi<false, kBNF4>(g, gdim, s, kepi);
+    else launch_epi<false, kBHalf>(g, gdim, s, kepi);
+  } else {
+    if (bsrc == kBNF4) launch_epi<true, kBNF4>(g, gdim, s, kepi);
+    else launch_epi<true, kBHalf>(g, gdim, s, kepi);
+  }
+  int rc = qlora_launch_status();
+  if (rc != 0 || splits == 1) return rc;
+  QLORA_CHECK_ARG(g.N % 4 == 0 && g.ldc % 4 == 0 && (epi != kEpiResid || g.ldr % 4 == 0));
+  const int64_t quads = g.M * g.N / 4;
+  hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)qlora_cdiv(quads, 256)), dim3(256), 0,
+                     s, ws, splits, g.M, g.N, epi, out, g.ldc, g.bias, g.resid, g.ldr);
+  return qlora_launch_status();
+}
+
+// Output columns and reduction length of a problem, from the weight's shape and the mode.
+int shape_of(int mode, int epi, int64_t w_rows, int64_t w_cols, int64_t swiglu_I, int64_t* N,
+             int64_t* Kr) {
+  if (mode == 0) {
+    *Kr = w_cols;
+    *N = epi == kEpiSwiglu ? swiglu_I : w_rows;
+    QLORA_CHECK_ARG(epi != kEpiSwiglu || (swiglu_I % 128 == 0 && 2 * swiglu_I == w_rows));
+    QLORA_CHECK_ARG(epi == kEpiSwiglu || w_rows % kBN == 0);
+  } else {
+    *Kr = w_rows;
+    *N = w_cols;
+    QLORA_CHECK_ARG(w_cols % kBN == 0);
+  }
+  QLORA_CHECK_ARG(*Kr % (kStages * kBK) == 0);
+  return 0;
+}
+
 }  // namespace
 
-// mode: 0 = NT (C = A W^T), 1 = NN (C = A W). epi: 0 store fp16, 1 + bias, 2 fp32 residual,
-// 3 SwiGLU (NT only). a_f32: A is fp32 (rounded to fp16 on load). tile: 0 = 256 x 256
-// (8 wavefronts), 1 = 128 x 128 (4 wavefronts), 2 = 256 x 256 (4 wavefronts of 128 x 128). splits > 1: split-K through `ws` (fp32, splits * M * N elements).
-QLORA_API int qlora_nf4_gemm(const void* a, int64_t lda, int32_t a_f32, const void* packed,
-                             const void* absmax, const float* code2, const float* absmax2,
-                             const float* offsets, const float* code, int32_t nested,
-                             int32_t standard, int32_t bs1, int32_t bs2, int64_t seg1,
-                             int64_t seg2, int64_t w_rows, int64_t w_cols, void* c, int64_t ldc,
-                             const void* bias, const float* resid, int64_t ldr, int64_t M,
-                             int32_t mode, int32_t epi, int64_t swiglu_I, int32_t tile,
-                             int32_t splits, float* ws, int64_t ws_elems, void* stream) {
+// NF4-decode GEMM. mode: 0 = NT (C = A W^T), 1 = NN (C = A W). epi: 0 store fp16, 1 + bias,
+// 2 fp32 residual, 3 SwiGLU (NT only). splits > 1: split-K through `ws` (fp32, splits M N).
+QLORA_API int qlora_nf4_gemm(const void* a, int64_t lda, const void* packed, const void* absmax,
+                             const float* code2, const float* absmax2, const float* offsets,
+                             const float* code, int32_t nested, int32_t standard, int32_t bs1,
+                             int32_t bs2, int64_t seg1, int64_t seg2, int64_t w_rows,
+                             int64_t w_cols, void* c, int64_t ldc, const void* bias,
+                             const float* resid, int64_t ldr, int64_t M, int32_t mode,
+                             int32_t epi, int64_t swiglu_I, int32_t splits, float* ws,
+                             int64_t ws_elems, void* stream) {
   QLORA_CHECK_ARG(M >= 0 && w_rows > 0 && w_cols > 0);
   if (M == 0) return 0;
   QLORA_CHECK_ARG(a && packed && absmax && c && (mode == 0 || mode == 1));
   QLORA_CHECK_ARG(epi >= 0 && epi <= 3 && !(epi == 3 && mode != 0));
-  QLORA_CHECK_ARG(tile >= 0 && tile <= 2);
   QLORA_CHECK_ARG(splits >= 1 && splits <= 16 && !(splits > 1 && epi == 3));
-  QLORA_CHECK_ARG(bs1 >= 32 && (bs1 & (bs1 - 1)) == 0);
+  QLORA_CHECK_ARG(bs1 == 64);  // one quantization block per thread and k-tile
   QLORA_CHECK_ARG(!nested || (code2 && absmax2 && offsets && bs2 > 0 && (bs2 & (bs2 - 1)) == 0));
   QLORA_CHECK_ARG(standard || code);
   QLORA_CHECK_ARG(epi != 1 || bias);
   QLORA_CHECK_ARG(epi != 2 || (resid && ldr >= 0));
-  const int BM = tile == 1 ? 128 : 256, BN = BM;
   int64_t N, Kr;
-  if (mode == 0) {
-    Kr = w_cols;
-    N = epi == 3 ? swiglu_I : w_rows;
-    QLORA_CHECK_ARG(epi != 3 || (swiglu_I % (BN / 2) == 0 && 2 * swiglu_I == w_rows));
-    QLORA_CHECK_ARG(epi == 3 || w_rows % BN == 0);
-    QLORA_CHECK_ARG(w_cols % kBK == 0);
-  } else {
-    Kr = w_rows;
-    N = w_cols;
-    QLORA_CHECK_ARG(w_cols % BN == 0 && w_rows % kBK == 0);
-  }
+  int rc = shape_of(mode, epi, w_rows, w_cols, swiglu_I, &N, &Kr);
+  if (rc) return rc;
   QLORA_CHECK_ARG(lda >= Kr && ldc >= N && (epi != 2 || ldr >= N));
   QLORA_CHECK_ARG(lda % 8 == 0 && al(a, 16) && al(packed, 16));
-  QLORA_CHECK_ARG(splits == 1 || (ws && ws_elems >= (int64_t)splits * M * N && al(ws, 16)));
-  const int64_t n_tiles = epi == 3 ? N / (BN / 2) : N / BN;
-  const int64_t grid = qlora_cdiv(M, BM) * n_tiles;
-  QLORA_CHECK_ARG(grid < (1ll << 31));
-  const int64_t ktiles = Kr / kBK;
-  GemmArgs g;
-  g.a = a;
+  QLORA_CHECK_ARG(256 * lda * 2 < (1ll << 32));  // 32-bit DMA offsets within an A tile
+  GemmArgs g{};
+  g.a = static_cast<const uint16_t*>(a);
   g.lda = lda;
   g.w = NF4Ref{static_cast<const uint8_t*>(packed), absmax, code2, absmax2, offsets, code,
                seg1, seg2, __builtin_ctz(bs1), nested ? __builtin_ctz(bs2) : 0, nested,
                standard};
   g.Kw = w_cols;
-  g.c = splits > 1 ? (void*)ws : c;
+  g.c = c;
   g.ldc = ldc;
   g.bias = static_cast<const uint16_t*>(bias);
   g.resid = resid;
@@ -492,25 +701,44 @@ QLORA_API int qlora_nf4_gemm(const void* a, int64_t lda, int32_t a_f32, const vo
   g.N = N;
   g.Kr = Kr;
   g.I = swiglu_I;
-  g.kt_per_split = qlora_cdiv(ktiles, splits);
-  const int kepi = splits > 1 ? (int)kEpiPartial : epi;
-  hipStream_t s = (hipStream_t)stream;
-  const dim3 gdim((unsigned)grid, 1, (unsigned)splits);
-  if (mode == 0) {
-    if (tile == 0) launch_epi<256, 256, 4, false>(g, gdim, s, a_f32, kepi);
-    else if (tile == 1) launch_epi<128, 128, 2, false>(g, gdim, s, a_f32, kepi);
-    else launch_epi<256, 256, 2, false>(g, gdim, s, a_f32, kepi);
-  } else {
-    if (tile == 0) launch_epi<256, 256, 4, true>(g, gdim, s, a_f32, kepi);
-    else if (tile == 1) launch_epi<128, 128, 2, true>(g, gdim, s, a_f32, kepi);
-    else launch_epi<256, 256, 2, true>(g, gdim, s, a_f32, kepi);
-  }
-  int rc = qlora_launch_status();
-  if (rc != 0 || splits == 1) return rc;
-  QLORA_CHECK_ARG(N % 4 == 0 && ldc % 4 == 0 && (epi != 2 || ldr % 4 == 0));
-  const int64_t quads = M * N / 4;
-  hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)qlora_cdiv(quads, 256)), dim3(256), 0,
-                     s, ws, splits, M, N, epi, c, ldc, static_cast<const uint16_t*>(bias), resid,
-                     ldr);
-  return qlora_launch_status();
+  return run_gemm(g, kBNF4, mode, epi, splits, ws, ws_elems, (hipStream_t)stream);
+}
+
+// The same GEMM with an fp16 B in memory: NT B [N, K] (ldb), NN B [K, N] (ldb).
+QLORA_API int qlora_hgemm(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t M,
+                          int64_t N, int64_t K, int32_t mode, void* c, int64_t ldc,
+                          const void* bias, const float* resid, int64_t ldr, int32_t epi,
+                          int64_t swiglu_I, int32_t splits, float* ws, int64_t ws_elems,
+                          void* stream) {
+  QLORA_CHECK_ARG(M >= 0 && N > 0 && K > 0);
+  if (M == 0) return 0;
+  QLORA_CHECK_ARG(a && b && c && (mode == 0 || mode == 1));
+  QLORA_CHECK_ARG(epi >= 0 && epi <= 3 && !(epi == 3 && mode != 0));
+  QLORA_CHECK_ARG(splits >= 1 && splits <= 16 && !(splits > 1 && epi == 3));
+  QLORA_CHECK_ARG(epi != 1 || bias);
+  QLORA_CHECK_ARG(epi != 2 || (resid && ldr >= N));
+  QLORA_CHECK_ARG(K % (kStages * kBK) == 0);
+  if (epi == kEpiSwiglu) QLORA_CHECK_ARG(N % 128 == 0);  // N = I (output columns)
+  else QLORA_CHECK_ARG(mode == 0 ? N % 8 == 0 : N % kBN == 0);  // NT: a partial last tile
+  QLORA_CHECK_ARG(lda >= K && lda % 8 == 0 && al(a, 16) && al(b, 16) && ldb % 8 == 0);
+  QLORA_CHECK_ARG(mode == 0 ? ldb >= K : ldb >= N);
+  QLORA_CHECK_ARG(ldc >= N);
+  // the DMA addresses rows by 32-bit byte offsets: from B's start (NT), from a tile (A, NN B)
+  if (mode == 0) QLORA_CHECK_ARG((epi == kEpiSwiglu ? 2 * N : N) * ldb * 2 < (1ll << 32));
+  QLORA_CHECK_ARG(256 * lda * 2 < (1ll << 32) && 64 * ldb * 2 < (1ll << 32));
+  GemmArgs g{};
+  g.a = static_cast<const uint16_t*>(a);
+  g.lda = lda;
+  g.b = static_cast<const uint16_t*>(b);
+  g.ldb = ldb;
+  g.c = c;
+  g.ldc = ldc;
+  g.bias = static_cast<const uint16_t*>(bias);
+  g.resid = resid;
+  g.ldr = ldr;
+  g.M = M;
+  g.N = N;
+  g.Kr = K;
+  g.I = swiglu_I;
+  return run_gemm(g, kBHalf, mode, epi, splits, ws, ws_elems, (hipStream_t)stream);
 }

@@ -90,77 +90,112 @@ def _nf4_args(w):
             seg2)
 
 
-def _plan(M, N, Kr, mode, epi, w_rows, w_cols, swiglu_I):
-    """(tile, splits): 256 x 256 tiles (tile 0) when they alone give at least one workgroup per
-    CU (256), else 128 x 128 (tile 1); split-K when even those leave CUs idle on a long
-    reduction."""
-    def ok(bn):
-        if mode == 0:
-            return swiglu_I % (bn // 2) == 0 if epi == 3 else w_rows % bn == 0
-        return w_cols % bn == 0
+TILE = 256  # output tile of the MFMA GEMM kernels (256 x 256; SwiGLU: 256 x 128 outputs)
+SLOTS = 256  # workgroups resident at once (one per CU)
 
-    def tiles(bm):
-        return -(-M // bm) * (N // (bm // 2) if epi == 3 else N // bm)
 
-    # NN 256 x 256 runs out of registers (spills), so the backward products use 128 x 128
-    tile = 0 if mode == 0 and ok(256) and tiles(256) >= 256 else 1
-    if not ok(256 if tile == 0 else 128):
-        raise ValueError("W shape not supported by the fused GEMM tiles")
-    n = tiles(256 if tile == 0 else 128)
-    splits = 1
+def split_k(M, N, Kr, epi):
+    """Slices of the reduction for the MFMA GEMMs: doubled while the tiles alone leave CUs idle
+    and every slice keeps at least 8 k-tiles of 64 (the partial sums cost an fp32 round trip
+    of M N per slice)."""
+    if epi == 3:
+        return 1
+    tiles = -(-M // TILE) * (N // TILE)
     ktiles = Kr // 64
-    if epi != 3:
-        while splits < 8 and n * splits < 192 and ktiles // (splits * 2) >= 8:
-            splits *= 2
-    return tile, splits
+    s = 1
+    while s < 8 and tiles * s < SLOTS and ktiles // (2 * s) >= 8:
+        s *= 2
+    return s
 
 
-def nf4_gemm(a, w, mode, epi=0, bias=None, resid=None, out=None, swiglu_I=0, tile=None,
-             splits=None):
-    """The fused GEMM (qlora_nf4_gemm). mode 0: A [M, K] x W^T; mode 1: A [M, N_w] x W."""
-    dev = a.device
-    _need(a, "a", None, contiguous=False)
-    if a.dtype not in (torch.float16, torch.float32) or a.dim() != 2 or a.stride(1) != 1:
-        raise ValueError("a must be a 2-D fp16/fp32 tensor with unit column stride")
-    M = a.shape[0]
-    w_rows, w_cols = _shape(w)
-    if mode == 0:
-        n_out = swiglu_I if epi == 3 else w_rows
-        kr = w_cols
-        if a.shape[1] != w_cols:
-            raise ValueError(f"a has {a.shape[1]} columns, W {w_cols}")
-    else:
-        n_out = w_cols
-        kr = w_rows
-        if a.shape[1] != w_rows:
-            raise ValueError(f"a has {a.shape[1]} columns, W has {w_rows} rows")
+def _gemm_out(a, M, n_out, epi, resid, out, dev):
     odt = torch.float32 if epi == 2 else torch.float16
     if out is None:
         out = torch.empty((M, n_out), device=dev, dtype=odt)
     _need(out, "out", odt, dev, contiguous=False)
     if out.shape != (M, n_out) or out.stride(1) != 1:
         raise ValueError("out has the wrong shape")
-    if epi == 1:
-        _need(bias, "bias", torch.float16, dev)
-        if bias.numel() != n_out:
-            raise ValueError("bias must have one entry per output column")
     ldr = 0
     if epi == 2:
         _need(resid, "resid", torch.float32, dev, contiguous=False)
         if resid.shape != (M, n_out) or resid.stride(1) != 1:
             raise ValueError("resid must match the output")
         ldr = resid.stride(0)
+    return out, ldr
+
+
+def _a16(a):
+    _need(a, "a", None, contiguous=False)
+    if a.dim() != 2:
+        raise ValueError("a must be 2-D")
+    if a.dtype == torch.float32:
+        a = a.to(torch.float16)  # the reference's dY.to(fp16) before the product
+    if a.dtype != torch.float16:
+        raise ValueError("a must be fp16 or fp32")
+    if a.stride(1) != 1 or a.stride(0) % 8 or a.data_ptr() % 16:
+        a = a.contiguous()
+    return a
+
+
+def nf4_gemm(a, w, mode, epi=0, bias=None, resid=None, out=None, swiglu_I=0, splits=None):
+    """The fused NF4-decode GEMM (qlora_nf4_gemm). mode 0: A [M, K] x W^T; mode 1:
+    A [M, N_w] x W. epi 0 fp16, 1 + bias, 2 fp32 residual (out = resid + fp16(acc)), 3 SwiGLU
+    of [gate | up] (mode 0)."""
+    dev = a.device
+    a = _a16(a)
+    M = a.shape[0]
+    w_rows, w_cols = _shape(w)
+    if mode == 0:
+        n_out, kr = (swiglu_I if epi == 3 else w_rows), w_cols
+    else:
+        n_out, kr = w_cols, w_rows
+    if a.shape[1] != kr:
+        raise ValueError(f"a has {a.shape[1]} columns, the product reduces over {kr}")
+    if epi == 1:
+        _need(bias, "bias", torch.float16, dev)
+        if bias.numel() != n_out:
+            raise ValueError("bias must have one entry per output column")
+    out, ldr = _gemm_out(a, M, n_out, epi, resid, out, dev)
     if M == 0:
         return out
-    t, sp = _plan(M, n_out, kr, mode, epi, w_rows, w_cols, swiglu_I)
-    tile = t if tile is None else tile
-    splits = sp if splits is None else splits
+    splits = split_k(M, n_out, kr, epi) if splits is None else splits
     ws = torch.empty((splits * M * n_out,), device=dev, dtype=torch.float32) if splits > 1 \
         else None
-    _lib.call("qlora_nf4_gemm", _ptr(a), a.stride(0), int(a.dtype == torch.float32),
-              *_nf4_args(w), w_rows, w_cols, _ptr(out), out.stride(0), _ptr(bias),
-              _ptr(resid), ldr, M, mode, epi, swiglu_I, tile, splits, _ptr(ws),
-              0 if ws is None else ws.numel(), _stream(dev))
+    _lib.call("qlora_nf4_gemm", _ptr(a), a.stride(0), *_nf4_args(w), w_rows, w_cols, _ptr(out),
+              out.stride(0), _ptr(bias), _ptr(resid), ldr, M, mode, epi, swiglu_I, splits,
+              _ptr(ws), 0 if ws is None else ws.numel(), _stream(dev))
+    return out
+
+
+def hgemm(a, b, mode, epi=0, bias=None, resid=None, out=None, swiglu_I=0, splits=None):
+    """The MFMA GEMM with an fp16 B (qlora_hgemm): mode 0 C = A B^T (B [N, K]), mode 1 C = A B
+    (B [K, N]); epilogues as nf4_gemm."""
+    dev = a.device
+    a = _a16(a)
+    _need(b, "b", torch.float16, dev, contiguous=False)
+    if b.dim() != 2 or b.stride(1) != 1:
+        raise ValueError("b must be 2-D with unit column stride")
+    M, K = a.shape
+    if mode == 0:
+        rows, kb = b.shape
+        n_out = swiglu_I if epi == 3 else rows
+    else:
+        kb, n_out = b.shape
+    if kb != K:
+        raise ValueError(f"inner dimensions differ: {K} vs {kb}")
+    if epi == 1:
+        _need(bias, "bias", torch.float16, dev)
+        if bias.numel() != n_out:
+            raise ValueError("bias must have one entry per output column")
+    out, ldr = _gemm_out(a, M, n_out, epi, resid, out, dev)
+    if M == 0:
+        return out
+    splits = split_k(M, n_out, K, epi) if splits is None else splits
+    ws = torch.empty((splits * M * n_out,), device=dev, dtype=torch.float32) if splits > 1 \
+        else None
+    _lib.call("qlora_hgemm", _ptr(a), a.stride(0), _ptr(b), b.stride(0), M, n_out, K, mode,
+              _ptr(out), out.stride(0), _ptr(bias), _ptr(resid), ldr, epi, swiglu_I, splits,
+              _ptr(ws), 0 if ws is None else ws.numel(), _stream(dev))
     return out
 
 

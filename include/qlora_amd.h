@@ -229,31 +229,44 @@ int qlora_nf4_dequant_many_timed(int32_t count, const void* const* packed,
 /*
  * NF4 dequantisation fused into an fp16 MFMA GEMM (fp32 accumulation) with a frozen NF4 weight
  * W [w_rows, w_cols] in the layout of qlora_nf4_dequant (same absmax/code2/absmax2/offsets/
- * segment arguments):
+ * segment arguments); 256 x 256 output tiles, the NF4 blocks decoded into LDS inside the kernel:
  *   mode 0 (NT): C[M, w_rows] = A[M, w_cols] W^T      mode 1 (NN): C[M, w_cols] = A[M, w_rows] W
+ *   A f16 [M, lda].
  *   epi 0: C f16 = f16(acc);  epi 1: C f16 = f16(acc + bias[n]) (bias f16);
  *   epi 2: C f32 = resid[m, n] + f32(f16(acc)) (may alias resid);
  *   epi 3 (mode 0, SwiGLU): W = [gate; up] with gate rows [0, I) and up rows [I, 2I);
  *          C f16 [M, I] = f16(silu(f16 g) * f16 u), I = swiglu_I.
- *   a_f32: A is f32 and is rounded to f16 as it is loaded.
- *   tile: 0 = 256x256 output tiles (8 wavefronts), 1 = 128x128 (4 wavefronts). splits > 1: split-K, the partial sums go
- *         through the caller's fp32 workspace ws (>= splits*M*N elements) and a reduce kernel
- *         applies the epilogue (not with epi 3).
+ *   splits > 1: split-K, the partial sums go through the caller's fp32 workspace ws
+ *         (>= splits*M*N elements) and a reduce kernel applies the epilogue (not with epi 3).
  * The decoded weight values are bit-identical to qlora_nf4_dequant's.
  * Replaces dequant (engine.py:683-694) + the cuBLAS products at engine.py:1082 (qkv + bias),
  * 1112 (o), 1135-1165 (gate|up), 1179 (down), 1239, 1293, 1301, 1316 (dY W) and the
  * SwiGLU (kernels.py:312-321) and residual add (engine.py:1048-1051) that follow them.
- * Requires (BN = 256 or 128 by tile): M >= 0; mode 0: w_rows % BN == 0 (epi 3:
- * I % (BN/2) == 0), w_cols % 64 == 0; mode 1: w_cols % BN == 0, w_rows % 64 == 0;
- * lda % 8 == 0; A and packed 16-byte aligned; bs1 >= 32 a power of two; splits <= 16.
+ * Requires: M >= 0; bs1 == 64; mode 0: w_rows % 256 == 0 (epi 3: I % 128 == 0),
+ * w_cols % 128 == 0; mode 1: w_cols % 256 == 0, w_rows % 128 == 0; lda % 8 == 0; A and packed
+ * 16-byte aligned; splits <= 16.
  */
-int qlora_nf4_gemm(const void* a, int64_t lda, int32_t a_f32, const void* packed,
-                   const void* absmax, const float* code2, const float* absmax2,
-                   const float* offsets, const float* code, int32_t nested, int32_t standard,
-                   int32_t bs1, int32_t bs2, int64_t seg1, int64_t seg2, int64_t w_rows,
-                   int64_t w_cols, void* c, int64_t ldc, const void* bias, const float* resid,
-                   int64_t ldr, int64_t M, int32_t mode, int32_t epi, int64_t swiglu_I,
-                   int32_t tile, int32_t splits, float* ws, int64_t ws_elems, void* stream);
+int qlora_nf4_gemm(const void* a, int64_t lda, const void* packed, const void* absmax,
+                   const float* code2, const float* absmax2, const float* offsets,
+                   const float* code, int32_t nested, int32_t standard, int32_t bs1, int32_t bs2,
+                   int64_t seg1, int64_t seg2, int64_t w_rows, int64_t w_cols, void* c,
+                   int64_t ldc, const void* bias, const float* resid, int64_t ldr, int64_t M,
+                   int32_t mode, int32_t epi, int64_t swiglu_I, int32_t splits, float* ws,
+                   int64_t ws_elems, void* stream);
+
+/*
+ * The same GEMM with an fp16 B operand in memory (the dequantized projections; the lm_head):
+ *   mode 0 (NT): C[M, N] = A[M, K] B^T, B [N, K] (ldb);  mode 1 (NN): C = A B, B [K, N] (ldb).
+ * epi, splits, ws as qlora_nf4_gemm (epi 3: B = [gate; up] rows, N = I).
+ * Replaces the cuBLAS products of the frozen projections after dequant (engine.py:1082, 1112,
+ * 1163, 1179, 1239, 1293, 1301, 1316) and of the lm_head (engine.py:1376-1381).
+ * Requires: K % 128 == 0; mode 1: N % 256 == 0; mode 0: N % 8 == 0 (epi 3: N % 128 == 0); lda, ldb % 8 == 0; A, B
+ * 16-byte aligned.
+ */
+int qlora_hgemm(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t M, int64_t N,
+                int64_t K, int32_t mode, void* c, int64_t ldc, const void* bias,
+                const float* resid, int64_t ldr, int32_t epi, int64_t swiglu_I, int32_t splits,
+                float* ws, int64_t ws_elems, void* stream);
 
 /*
  * out = a + fp32(d) over numel elements (a, out f32; d f16; numel % 4 == 0; out may alias a):

@@ -94,12 +94,11 @@ def test_epilogues(pkg):
     # SwiGLU over gate|up without materialising it
     gu_w = _group(pkg, [(8960, 1536), (8960, 1536)], 10)
     mm = L.nf4_gemm(x, gu_w, 0, epi=3, swiglu_I=8960)
-    gu = L.nf4_gemm(x, gu_w, 0)
+    gu = L.nf4_gemm(x, gu_w, 0, splits=1)  # the SwiGLU epilogue sums K in one slice
     assert torch.equal(mm, pkg.ops._glu_fwd(gu, 8960))
-    for tile in (0, 1, 2):  # every tile shape (gate and up rows are placed per wavefront)
-        mm = L.nf4_gemm(x, gu_w, 0, epi=3, swiglu_I=8960, tile=tile, splits=1)
-        gu = L.nf4_gemm(x, gu_w, 0, tile=tile, splits=1)
-        assert torch.equal(mm, pkg.ops._glu_fwd(gu, 8960))
+    # the same from the fp16 B path (gate and up rows placed per wavefront by the B loader)
+    wgu = L.dequantize(gu_w)
+    assert torch.equal(L.hgemm(x, wgu, 0, epi=3, swiglu_I=8960), mm)
     # fp32 A rounded to fp16 on load
     a32 = torch.randn(M, 1536, generator=g, device=DEV)
     assert torch.equal(L.nf4_gemm(a32, wd, 1), L.nf4_gemm(a32.half(), wd, 1))
@@ -138,27 +137,61 @@ def test_mlp_up_path_config2(pkg, path):
         assert rel_err(got.cpu(), want) < 1e-3
 
 
-@pytest.mark.parametrize("tile,splits", [(0, 1), (1, 1), (2, 1), (0, 3), (1, 2), (2, 2)])
+@pytest.mark.parametrize("splits", [1, 2, 3])
 @pytest.mark.parametrize("mode", [0, 1])
-def test_every_tile_and_split(pkg, tile, splits, mode):
-    """Each compiled tile shape and split-K setting (forced) against fp64, with the residual and
-    bias epilogues through the split-K reduce."""
+def test_every_split(pkg, splits, mode):
+    """Split-K settings (forced) against fp64, with the residual and bias epilogues through the
+    split-K reduce, for the NF4 and the fp16-B kernels."""
     L = pkg.linear
     w = _weight(pkg, (1536, 2048), 31)
-    wd = L.dequantize(w).double()
-    g = torch.Generator(device=DEV).manual_seed(tile * 7 + splits)
+    wd16 = L.dequantize(w)
+    wd = wd16.double()
+    g = torch.Generator(device=DEV).manual_seed(splits * 7 + mode)
     M = 531
     if mode == 0:
         x = torch.randn(M, 2048, generator=g, device=DEV).half()
         ref = x.double() @ wd.t()
         bias = (torch.randn(1536, generator=g, device=DEV) * 0.1).half()
-        y = L.nf4_gemm(x, w, 0, epi=1, bias=bias, tile=tile, splits=splits)
+        y = L.nf4_gemm(x, w, 0, epi=1, bias=bias, splits=splits)
         assert rel_err(y, ref + bias.double()) < 1e-3
+        assert torch.equal(L.hgemm(x, wd16, 0, epi=1, bias=bias, splits=splits), y)
         res = torch.randn(M, 1536, generator=g, device=DEV)
-        h = L.nf4_gemm(x, w, 0, epi=2, resid=res, tile=tile, splits=splits)
+        h = L.nf4_gemm(x, w, 0, epi=2, resid=res, splits=splits)
         assert rel_err(h - res, ref) < 1e-3
     else:
-        dy = torch.randn(M, 1536, generator=g, device=DEV)  # fp32 A, rounded on load
+        dy = torch.randn(M, 1536, generator=g, device=DEV)  # fp32 A, rounded to fp16 first
         ref = dy.half().double() @ wd
-        y = L.nf4_gemm(dy, w, 1, tile=tile, splits=splits)
+        y = L.nf4_gemm(dy, w, 1, splits=splits)
         assert rel_err(y, ref) < 1e-3
+        assert torch.equal(L.hgemm(dy, wd16, 1, splits=splits), y)
+
+
+@pytest.mark.parametrize("M", [2560, 1, 300])
+@pytest.mark.parametrize("mode", [0, 1])
+def test_fp16_b_gemm_equals_fused(pkg, M, mode):
+    """qlora_hgemm on the dequantized weight equals qlora_nf4_gemm on the NF4 weight bit for bit
+    (same B values, same summation order) at the step's widest shapes, and both match fp64."""
+    L = pkg.linear
+    gu_w = _group(pkg, [(8960, 1536), (8960, 1536)], 40)
+    wd16 = L.dequantize(gu_w)
+    g = torch.Generator(device=DEV).manual_seed(M + mode)
+    a = torch.randn(M, 1536 if mode == 0 else 17920, generator=g, device=DEV).half()
+    fused = L.nf4_gemm(a, gu_w, mode)
+    plain = L.hgemm(a, wd16, mode)
+    assert torch.equal(fused, plain)
+    ref = a.double() @ (wd16.double().t() if mode == 0 else wd16.double())
+    assert rel_err(plain, ref) < 1e-3
+
+
+def test_lm_head_shapes(pkg):
+    """The lm_head products on the fp16 path: logits = hn E^T (N = 151,936) and G E (K =
+    151,936, split-K) against fp64."""
+    L = pkg.linear
+    g = torch.Generator(device=DEV).manual_seed(11)
+    E = (torch.randn(151936, 1536, generator=g, device=DEV) * 0.02).half()
+    hn = torch.randn(300, 1536, generator=g, device=DEV).half()
+    logits = L.hgemm(hn, E, 0)
+    assert rel_err(logits, hn.double() @ E.double().t()) < 1e-3
+    G = (torch.randn(300, 151936, generator=g, device=DEV) * 1e-3).half()
+    dh = L.hgemm(G, E, 1)
+    assert rel_err(dh, G.double() @ E.double()) < 1e-3
