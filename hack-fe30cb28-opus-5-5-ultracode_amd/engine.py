@@ -691,6 +691,10 @@ class FusedQwen2:
         spec = self.layers[0]
         return 2 * spec.H * ((spec.HQ + 2 * spec.HKV) * spec.D + spec.HQ * spec.D + 3 * spec.I)
 
+    def allocated_bytes(self):
+        """Device memory the plan counts as taken (torch's allocator on this device)."""
+        return torch.cuda.memory_allocated(self.device)
+
     def keep_plan(self, n):
         """The number of last layers that keep every intermediate for a step of n tokens: as
         many as fit under the memory cap above what is allocated now plus one recomputing
@@ -704,7 +708,7 @@ class FusedQwen2:
             cap = torch.cuda.get_device_properties(self.device).total_memory - self.CAP_MARGIN
         weights = self.weight_bytes_per_layer()
         work = weights + 64 * 2**20 + n * 96 * 1024 + n * self.cfg.vocab_size * 2
-        free = cap - torch.cuda.memory_allocated(self.device) - work
+        free = cap - self.allocated_bytes() - work
         per_layer = max(1, self.kept_bytes_per_layer(n) + (weights if self.keep_weights else 0))
         return int(max(0, min(len(self.layers), free // per_layer)))
 
