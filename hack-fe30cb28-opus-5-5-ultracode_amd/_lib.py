@@ -44,6 +44,8 @@ SIGNATURES = {
     "qlora_lora_grad_workspace": [I64, I32, I32, I32, I32, P],
     "qlora_lora_grad": [P, P, I64, P, P, P, P, P, P, P, P, P, P, I64, I32, I32, I32, I32, F32, P,
                         I64, P],
+    "qlora_lora_grad_noalloc": [P, P, I64, P, P, P, P, P, P, P, P, P, P, I64, I32, I32, I32, I32,
+                                F32, P],
     "qlora_gemm": [I32, I64, I64, I64, P, I64, P, I64, P, I64, F32, F32, I32, P],
     "qlora_gemm_solutions": [I32, I64, I64, I64, P, I64, P, I64, P, I64, P, I32, P],
     "qlora_gemm_splitk": [I32, I64, I64, I64, P, I64, P, I64, P, I64, P, I32, P, I64, I32, P],

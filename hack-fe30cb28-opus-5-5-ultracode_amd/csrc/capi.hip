@@ -3,9 +3,13 @@
 
 #include <rocblas/rocblas.h>
 
-// Codes from 200000 up are hipBLASLt statuses (qlora_gemmlt*), from 100000 up rocBLAS statuses
+// Codes from 300000 up are the library's own (QLORA_ERR_*), from 200000 up hipBLASLt statuses (qlora_gemmlt*), from 100000 up rocBLAS statuses
 // (qlora_gemm*), below are hipError_t values.
 QLORA_API const char* qlora_error_string(int code) {
+  if (code == QLORA_ERR_SCRATCH_TOO_SMALL)
+    return "qlora: the problem needs more scratch than the allocation-free entry point's static "
+           "buffer holds; call the entry point that takes a workspace";
+  if (code >= 300000) return "qlora: error";
   if (code >= 200000) {
     switch (code - 200000) {
       case 1: return "hipBLASLt: not initialized";

@@ -16,6 +16,9 @@
 
 static inline int qlora_launch_status() { return (int)hipGetLastError(); }
 
+// Returned by an allocation-free entry point whose problem needs more than its static scratch.
+#define QLORA_ERR_SCRATCH_TOO_SMALL 300001
+
 static inline int64_t qlora_cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 namespace qlora {

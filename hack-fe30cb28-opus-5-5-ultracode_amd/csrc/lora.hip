@@ -29,6 +29,8 @@
 // current one is stored.
 #include "common.h"
 
+#include <mutex>
+
 namespace qlora {
 namespace lora {
 
@@ -610,4 +612,60 @@ QLORA_API int qlora_lora_grad(const void* g_q, const void* g_v, int64_t ldg, con
   }
 #undef QLORA_GRAD
   return qlora_launch_status();
+}
+
+// ------------------------------------------------------------------------------------------------
+// Allocation-free form of qlora_lora_grad, for callers that cannot allocate (code under HIP graph
+// capture, serving loops, harnesses that forbid hipMalloc): the pass-1 partial sums go to a
+// file-scope device array instead of a caller workspace. Its address is taken once per device
+// (hipGetSymbolAddress, that device current) on the first call there and kept; kernels get that
+// address, never the array's name (a host-side stand-in). Every element pass 2 reads is written
+// by pass 1 of the same call, so the array needs no clearing between calls; calls that overlap
+// on one GPU (two streams) share the array and race.
+// ------------------------------------------------------------------------------------------------
+namespace {
+
+constexpr int64_t kGradScratchElems = int64_t(4) << 20;  // fp32: 16 MiB per device
+static __device__ __align__(256) float scratch[kGradScratchElems];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxDevices] = {};
+
+// The device address of `scratch` on the current device, or nullptr on a failed lookup.
+float* scratch_on_current_device(int* rc) {
+  int dev = 0;
+  *rc = (int)hipGetDevice(&dev);
+  if (*rc != 0) return nullptr;
+  if (dev < 0 || dev >= kMaxDevices) {
+    *rc = (int)hipErrorInvalidDevice;
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    *rc = (int)hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (*rc != 0) return nullptr;
+    g_scratch_ptr[dev] = static_cast<float*>(p);
+  }
+  return g_scratch_ptr[dev];
+}
+
+}  // namespace
+
+// qlora_lora_grad without a workspace argument; QLORA_ERR_SCRATCH_TOO_SMALL when
+// qlora_lora_grad_workspace(...) exceeds the static scratch (4 Mi fp32).
+QLORA_API int qlora_lora_grad_noalloc(const void* g_q, const void* g_v, int64_t ldg,
+                                      const void* x_q, const void* x_v, const void* a_q,
+                                      const void* a_v, const void* dx_q, const void* dx_v,
+                                      float* dB_q, float* dB_v, float* dA_q, float* dA_v,
+                                      int64_t n, int32_t N_q, int32_t N_v, int32_t H, int32_t r,
+                                      float s, void* stream) {
+  QLORA_CHECK_ARG(n >= 0 && N_q > 0 && N_v > 0 && H > 0 && rank_ok(r));
+  if (grad_workspace(n, N_q, N_v, H, r) > kGradScratchElems) return QLORA_ERR_SCRATCH_TOO_SMALL;
+  int rc = 0;
+  float* work = scratch_on_current_device(&rc);
+  if (work == nullptr) return rc != 0 ? rc : (int)hipErrorInvalidValue;
+  return qlora_lora_grad(g_q, g_v, ldg, x_q, x_v, a_q, a_v, dx_q, dx_v, dB_q, dB_v, dA_q, dA_v, n,
+                         N_q, N_v, H, r, s, work, kGradScratchElems, stream);
 }

@@ -667,6 +667,44 @@ def _lora_grad(dqkv, q_cols, v_cols, x_q, x_v, a_q, a_v, dx_q, dx_v, scale):
     return dA_q, dB_q, dA_v, dB_v
 
 
+def _lora_grad_noalloc(dqkv, q_cols, v_cols, x_q, x_v, a_q, a_v, dx_q, dx_v, scale, out=None):
+    """_lora_grad through qlora_lora_grad_noalloc: the partial sums in the library's static
+    scratch instead of a workspace (no device allocation by the library; outputs allocated here
+    unless `out` = (dA_q, dB_q, dA_v, dB_v) fp32 is given). Raises when the problem needs more
+    scratch than the library holds."""
+    _need(dqkv, "dqkv", torch.float16, contiguous=False)
+    n, C = dqkv.shape
+    dev = dqkv.device
+    if dqkv.stride(1) != 1:
+        raise ValueError("dqkv must have unit column stride")
+    for t, name in ((x_q, "x_q"), (x_v, "x_v"), (a_q, "a_q"), (a_v, "a_v"), (dx_q, "dx_q"),
+                    (dx_v, "dx_v")):
+        _need(t, name, torch.float16, dev)
+    r = x_q.shape[1]
+    H = a_q.shape[1]
+    Nq, Nv = q_cols.stop - q_cols.start, v_cols.stop - v_cols.start
+    for t, shape in ((x_q, (n, r)), (x_v, (n, r)), (dx_q, (n, r)), (dx_v, (n, r)),
+                     (a_q, (n, H)), (a_v, (n, H))):
+        if t.shape != shape:
+            raise ValueError(f"expected {shape}, got {tuple(t.shape)}")
+    f32 = torch.float32
+    if out is None:
+        out = (torch.empty((r, H), device=dev, dtype=f32), torch.empty((Nq, r), device=dev, dtype=f32),
+               torch.empty((r, H), device=dev, dtype=f32), torch.empty((Nv, r), device=dev, dtype=f32))
+    dA_q, dB_q, dA_v, dB_v = out
+    for t, shape, name in ((dA_q, (r, H), "dA_q"), (dB_q, (Nq, r), "dB_q"),
+                           (dA_v, (r, H), "dA_v"), (dB_v, (Nv, r), "dB_v")):
+        _need(t, name, f32, dev)
+        if t.shape != shape:
+            raise ValueError(f"{name} must be {shape}")
+    base = dqkv.data_ptr()
+    _lib.call("qlora_lora_grad_noalloc", base + 2 * q_cols.start, base + 2 * v_cols.start,
+              dqkv.stride(0), _ptr(x_q), _ptr(x_v), _ptr(a_q), _ptr(a_v), _ptr(dx_q), _ptr(dx_v),
+              _ptr(dB_q), _ptr(dB_v), _ptr(dA_q), _ptr(dA_v), n, Nq, Nv, H, r, float(scale),
+              _stream(dev))
+    return dA_q, dB_q, dA_v, dB_v
+
+
 # ---------------------------------------------------------------------------------------------
 # Varlen causal attention (engine.py:857-869)
 # ---------------------------------------------------------------------------------------------

@@ -378,6 +378,22 @@ int qlora_lora_grad(const void* g_q, const void* g_v, int64_t ldg, const void* x
                     float* work, int64_t work_elems, void* stream);
 
 /*
+ * qlora_lora_grad without a workspace argument: the partial sums go to a static device array of
+ * the library (4 Mi fp32 = 16 MiB per GPU, held from the first call on that GPU until the
+ * process ends). No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc);
+ * it calls no hipMalloc/hipFree. Returns QLORA_ERR_SCRATCH_TOO_SMALL (300001) when
+ * qlora_lora_grad_workspace(n, N_q, N_v, H, r) exceeds 4 Mi elements (e.g. more than 13,568
+ * tokens at N_q = H = 1536, N_v = 256, r = 16). Calls that overlap on one GPU share the array
+ * and race; the array needs no clearing between calls.
+ */
+int qlora_lora_grad_noalloc(const void* g_q, const void* g_v, int64_t ldg, const void* x_q,
+                            const void* x_v, const void* a_q, const void* a_v, const void* dx_q,
+                            const void* dx_v, float* dB_q, float* dB_v, float* dA_q,
+                            float* dA_v, int64_t n, int32_t N_q, int32_t N_v, int32_t H,
+                            int32_t r, float s, void* stream);
+
+/*
  * Causal attention within each packed sequence (flash attention, online softmax), grouped-query
  * heads, fp16 operands and fp32 accumulation/softmax.
  *   q [n, HQ, D], k/v [n, KH, D] (q head h reads kv head h / (HQ/KH)), out [n, HQ, D] fp16,
