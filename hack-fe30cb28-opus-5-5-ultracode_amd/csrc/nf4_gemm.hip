@@ -6,38 +6,44 @@
 //   NT (forward):  C[m, n] = sum_k A[m, k] B[n, k]      B = W [N, K], K = reduction
 //   NN (backward): C[m, n] = sum_k A[m, k] B[k, n]      B = W [K, N], N = W's columns
 //
-// One workgroup = 4 wavefronts on a 256 x 256 output tile, k-tiles of 64; each wavefront owns a
+// One workgroup = 4 wavefronts on a 256 x 256 output tile, k-tiles of 32; each wavefront owns a
 // 128 x 128 block as 4 x 4 v_mfma_f32_32x32x16_f16 accumulators (256 accumulation registers, one
 // wavefront per SIMD). On gfx950 a 128 x 128 wavefront block is what keeps the operand reads
-// below the MFMA time: per k-tile a wavefront reads 2 x 128 x 64 fp16 from LDS for 64 MFMAs
-// (half of LDS's 128 B/clk against 2.5 PFLOP/s); smaller blocks make the kernel LDS-bound.
+// below the MFMA time: per 16-wide k-step a wavefront reads 2 x 128 x 16 fp16 from LDS for 16
+// MFMAs; smaller blocks make the kernel LDS-bound.
 //
 // Operand staging. The A tile (and an fp16 B tile) goes from global memory straight into LDS
 // (global_load_lds_dwordx4: a wavefront instruction writes 1 KB of consecutive LDS, lane l at
-// 16 l), two stages, the next k-tile's loads issued at the top of the current one. The LDS
-// layout is swizzled through the choice of which global 16-byte chunk a lane fetches: in a
-// K-contiguous tile [rows][64] (A; B in NT) chunk c of row r sits in slot c ^ ((r >> 1) & 7), so
-// a fragment read (16 consecutive rows, one chunk, per 16-lane pass) covers all 64 banks; in an
-// N-contiguous tile [64][256] (B in NN) chunk c of row k sits in slot c ^ ((k & 3) << 2), the
-// pattern under which ds_read_b64_tr_b16 (4 rows x 16 columns per 16 lanes) is conflict-free.
-// Every stage is its own __shared__ array and the loop is unrolled by two, so the compiler can
-// tell which buffer a read touches (an LDS read is otherwise held behind every outstanding LDS
-// DMA); the waits are explicit: vmcnt(0) + lgkmcnt(0) and one s_barrier per k-tile.
+// 16 l), four stages, the loads of k-tile t + 3 issued in the middle of k-tile t and spread
+// over its MFMAs. The LDS layout is swizzled through the choice of which global 16-byte chunk a
+// lane fetches: in a K-contiguous tile [rows][32] (A; B in NT) chunk c of row r sits in slot
+// c ^ ((r >> 2) & 3), so a fragment read covers all banks; in an N-contiguous tile [32][256] (B
+// in NN) chunk c of row k sits in slot c ^ ((k & 3) << 2), the pattern under which
+// ds_read_b64_tr_b16 (4 rows x 16 columns per 16 lanes) is conflict-free. Every stage is its own
+// __shared__ array and the loop is unrolled by four, so the compiler can tell which buffer a
+// read touches (an LDS read is otherwise held behind every outstanding LDS DMA); the waits are
+// explicit: one vmcnt + lgkmcnt(0) and one s_barrier per k-tile.
 //
-// NF4 B. A thread decodes one 64-value block per k-tile (NT: one W row of the tile; NN: a
-// quarter of one W row): its packed bytes (32) and the block's scale inputs are loaded two
-// k-tiles ahead into registers, and the block is decoded while the MFMAs of the current k-tile
-// run, into the other B stage. Decode: the block's 16 possible values fp16(fp32(level * scale))
-// (16 products, 8 v_cvt_pk_f16_f32: the standalone dequant's two roundings) are split into a
-// low-byte and a high-byte plane of 16 bytes each; each value is then looked up by its code
-// with v_perm_b32 (two 8-byte halves of a plane, merged by the code's bit 3): about 4 VALU
-// instructions per value and no LDS lookup table (LDS bandwidth is the scarce resource here).
-// The result equals dequant-then-GEMM bit for bit in the B operand.
+// NF4 B. A thread decodes 32 values (half of a 64-value block) per k-tile (NT: one W row of the
+// tile; NN: a quarter of one W row). Their codes (16 bytes) and the block's fp32 scale arrive by
+// DMA too, five k-tiles ahead, into small LDS stages of their own; the scale is formed once per
+// weight by nf4_block_scales_kernel (the double-quant chain code2[q] * absmax2 + offset, as the
+// standalone dequant forms it), since the weights are frozen. With every operand arriving
+// through LDS, no loaded register is live across the loop's back edge, where the compiler
+// would otherwise drain the memory queue. The half-block of k-tile t + 2 is decoded while the
+// MFMAs of k-tile t run, into its B stage. Decode: the block's 16 possible values
+// fp16(fp32(level * scale)) (16 products, 8 v_cvt_pk_f16_f32: the standalone dequant's two
+// roundings) are split into a low-byte and a high-byte plane of 16 bytes each; each value is
+// then looked up by its code with v_perm_b32 (two 8-byte halves of a plane, merged by the code's
+// bit 3): about 4 VALU instructions per value and no LDS lookup table. The result equals
+// dequant-then-GEMM bit for bit in the B operand.
 //
 // Epilogues: fp16 store; + fp16 bias (qkv); fp32 residual out = res + f32(fp16(acc)) (down);
 // SwiGLU m = fp16(silu(fp16 g) * fp16 u) (gate|up: each wavefront's first two 32-column blocks
 // are gate rows, the last two the up rows of the same output columns); fp32 partial sums for
-// split-K ([splits, M, N], summed in a fixed order by splitk_reduce_kernel).
+// split-K ([splits, M, N], summed in a fixed order by splitk_reduce_kernel). The fp16 ones are
+// staged through LDS from transposed accumulators (four consecutive columns per lane) and leave
+// as whole 16-byte row pieces.
 //
 // Work order: workgroup ids are dealt to the 8 XCDs in turn; tile_order gives each XCD a
 // contiguous range of tiles (the M tiles of a few N tiles), so an XCD's L2 holds the B tiles it
@@ -63,7 +69,10 @@ struct GemmArgs {
   int64_t lda;
   const uint16_t* b;     // fp16 B: NT [N rows, Kr], NN [Kr rows, N]
   int64_t ldb;
-  NF4Ref w;              // NF4 B: W [rows, Kw] (NT: rows = N, Kw = Kr; NN: rows = Kr, Kw = N)
+  // NF4 B: W [rows, Kw] (NT: rows = N, Kw = Kr; NN: rows = Kr, Kw = N), 64-value blocks
+  const uint8_t* w_packed;  // codes, two per byte (element 2j in the high nibble of byte j)
+  const float* w_scales;    // fp32 scale of each block
+  const float* w_code;      // the 16 levels, or null for the NF4 table
   int64_t Kw;
   void* c;               // fp16 [M, ldc]; fp32 for kEpiResid; fp32 [splits, M, N] partials
   int64_t ldc;
@@ -142,21 +151,16 @@ struct DmaN {
 };
 
 // ---- NF4 block decode -------------------------------------------------------------------------
-struct NF4Raw {      // 32 values (half a 64-value block): codes and the inputs of the scale
-  uint4 v;           // 16 bytes of codes
-  uint32_t q;        // nested: absmax code
-  float a2;          // nested: absmax2 of the block's group; plain: the fp32 absmax
-  uint32_t seg;      // nested: segment of the block (stacked weights)
-};
-
-// Three vector-memory loads (the codes, the absmax byte, absmax2 or the fp32 absmax).
-__device__ __forceinline__ void nf4_load(NF4Raw& r, const NF4Ref& w, int64_t e) {
-  r.v = *reinterpret_cast<const uint4*>(w.packed + (e >> 1));
-  const int64_t b = e >> 6;
-  const bool nested = w.nested;
-  r.q = static_cast<const uint8_t*>(w.absmax)[nested ? b : 0];
-  r.a2 = nested ? w.absmax2[b >> w.bs2_shift] : static_cast<const float*>(w.absmax)[b];
-  r.seg = (uint32_t)((int)(b >= w.seg1) + (int)(b >= w.seg2));
+// NF4 B by DMA: the codes of a thread's half-block of a k-tile (16 bytes, 32 values) and its
+// block's fp32 scale go into slot `tid` of a codes stage and a scales stage (wavefront w's lanes
+// fill slots 64 w .. 64 w + 63, the same wavefront's threads read them). `e`: the half-block's
+// first element in W.
+__device__ __forceinline__ void nf4_issue(const GemmArgs& g, int64_t e, uint8_t* codes,
+                                          float* scales, int wave) {
+  __builtin_amdgcn_global_load_lds(g.w_packed + (e >> 1), (lds_void_t*)(codes + 1024 * wave), 16,
+                                   0, 0);
+  __builtin_amdgcn_global_load_lds(g.w_scales + (e >> 6), (lds_void_t*)(scales + 64 * wave), 4, 0,
+                                   0);
 }
 
 // The block's 16 values fp16(fp32(level[c] * scale)) as byte planes: lo[p] holds the low bytes
@@ -206,17 +210,6 @@ __device__ __forceinline__ uint4 nf4_decode8(const NF4Planes& t, uint32_t wd) {
   return make_uint4(a.x, a.y, b.x, b.y);
 }
 
-// Branch-free (a branch would split the main loop's scheduling region): without double
-// quantisation the code2 lookup reads a harmless table entry and its result is not selected.
-__device__ __forceinline__ float nf4_scale(const NF4Raw& r, int nested, const float* c2,
-                                           const float* offs) {
-  float prod = c2[r.q] * r.a2;
-  fp32_barrier(prod);  // bitsandbytes rounds the product before adding the offset
-  float sc = prod + offs[r.seg];
-  fp32_barrier(sc);  // (also keeps the table reads out of a branch on `nested`)
-  return nested ? sc : r.a2;
-}
-
 // W row of LDS B row `n` (NT). SwiGLU: within each wavefront's 128 rows the first 64 are gate
 // rows and the last 64 the up rows of the same 64 output columns.
 template <int EPI>
@@ -264,17 +257,26 @@ __device__ __forceinline__ void read_frags(Frags& f, const uint16_t* sa, const u
   }
 }
 
+// T: the accumulators hold the transposed blocks (B fragments as the MFMA's first operand), so
+// register r of lane l in block (i, j) is row 32 i + l % 32, column 32 j + 8 (r / 4) + 4 (l / 32)
+// + r % 4: four consecutive output columns per lane, stored as one 8-byte LDS write. Otherwise
+// register r is row 32 i + 8 (r / 4) + 4 (l / 32) + r % 4, column 32 j + l % 32.
+template <bool T>
 __device__ __forceinline__ void mfma_step(f32x16 (&acc)[4][4], const Frags& f) {
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
+      acc[i][j] = T ? __builtin_amdgcn_mfma_f32_32x32x16_f16(f.b[j], f.a[i], acc[i][j], 0, 0, 0)
+                    : __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
 }
 
 // Scheduling of one k-step: the reads of the next k-step's fragments between this k-step's 16
 // MFMAs (one read per MFMA), `VMEM` global loads (the prefetch DMA) one per MFMA from the
 // first, and `VALU` VALU instructions (the NF4 decode, the DMA addresses) after each MFMA.
+// Spreading the DMA over the MFMAs keeps the four wavefronts, which leave the k-tile's barrier
+// together, from queueing all their loads at the texture unit at once (measured: 6 % of the
+// gate|up GEMM's time).
 template <bool NN, int VALU, int VMEM>
 __device__ __forceinline__ void sched_step() {
   constexpr int reads = NN ? 12 : 8;
@@ -287,14 +289,14 @@ __device__ __forceinline__ void sched_step() {
   }
 }
 
-// Half `part` (0, 1) of the decode of one raw half-block (32 values) with scale `sc` into the
-// B stage: part 0 forms the byte planes and words 0-1, part 1 words 2-3. NT: LDS row `row`,
+// Half `part` (0, 1) of the decode of one half-block (32 values, codes `v`) with scale `sc` into
+// the B stage: part 0 forms the byte planes and words 0-1, part 1 words 2-3. NT: LDS row `row`,
 // chunks 0-3; NN: row `row`, chunks chunk0 .. chunk0+3.
 template <bool NN>
-__device__ __forceinline__ void nf4_decode_part(const NF4Raw& r, float sc, NF4Planes& t,
+__device__ __forceinline__ void nf4_decode_part(const uint4& v, float sc, NF4Planes& t,
                                                 uint16_t* sb, int row, int chunk0,
                                                 const float* lv, int part) {
-  const uint32_t wds[4] = {r.v.x, r.v.y, r.v.z, r.v.w};
+  const uint32_t wds[4] = {v.x, v.y, v.z, v.w};
   if (part == 0) t = nf4_planes(sc, lv);
 #pragma unroll
   for (int c = 2 * part; c < 2 * part + 2; ++c) {
@@ -322,8 +324,15 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
   __shared__ __attribute__((aligned(1024))) uint16_t sB1[kTile];
   __shared__ __attribute__((aligned(1024))) uint16_t sB2[kTile];
   __shared__ __attribute__((aligned(1024))) uint16_t sB3[kTile];
-  __shared__ float s_c2[256];
-  __shared__ float s_offs[4];
+  // NF4 codes and scales, stage u % 4 for k-tile u (unused with an fp16 B)
+  __shared__ __attribute__((aligned(1024))) uint8_t sC0[kThreads * 16];
+  __shared__ __attribute__((aligned(1024))) uint8_t sC1[kThreads * 16];
+  __shared__ __attribute__((aligned(1024))) uint8_t sC2[kThreads * 16];
+  __shared__ __attribute__((aligned(1024))) uint8_t sC3[kThreads * 16];
+  __shared__ __attribute__((aligned(1024))) float sS0[kThreads];
+  __shared__ __attribute__((aligned(1024))) float sS1[kThreads];
+  __shared__ __attribute__((aligned(1024))) float sS2[kThreads];
+  __shared__ __attribute__((aligned(1024))) float sS3[kThreads];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -361,23 +370,15 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
     }
   }
 
-  // NF4: levels in registers, the double-quant code and the segment offsets in LDS; this
-  // thread's half-block at k-tile kt is element e_base + kt * e_step, decoded into row b_row
-  // from chunk b_chunk0 (NT: row tid; NN: row tid / 8, chunks 4 (tid % 8) ..)
+  // NF4: levels in registers; this thread's half-block at k-tile kt is element e_base + kt *
+  // e_step, decoded into row b_row from chunk b_chunk0 (NT: row tid; NN: row tid / 8, chunks
+  // 4 (tid % 8) ..)
   float lv[16];
-  NF4Raw raw0, raw1, raw2, raw3;  // half-block of k-tile kt in raw[kt % 4]
   int64_t e_base = 0, e_step = 0;
   int b_row = 0, b_chunk0 = 0;
   if constexpr (BSRC == kBNF4) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) lv[i] = g.w.standard ? kNF4Levels[i] : g.w.code[i];
-    if (g.w.nested) {
-      s_c2[tid] = g.w.code2[tid];
-      if (tid < 3) {
-        const int nseg = 1 + (int)(g.w.seg1 != INT64_MAX) + (int)(g.w.seg2 != INT64_MAX);
-        s_offs[tid] = g.w.offsets[tid < nseg ? tid : 0];
-      }
-    }
+    for (int i = 0; i < 16; ++i) lv[i] = g.w_code ? g.w_code[i] : kNF4Levels[i];
     if constexpr (!NN) {
       b_row = tid;
       e_base = nt_wrow<EPI>(g, tile_n, tid) * g.Kw;
@@ -389,8 +390,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
       e_step = (int64_t)kBK * g.Kw;
     }
   }
-  // vector-memory instructions one k-tile issues (its DMA, or the A DMA and a raw half-block)
-  constexpr int kVmPerTile = 4 + (BSRC == kBHalf ? 4 : 3);
+  // vector-memory instructions one k-tile issues (its DMA; NF4: the A DMA, codes and scales)
+  constexpr int kVmPerTile = 4 + (BSRC == kBHalf ? 4 : 2);
 
   f32x16 acc[4][4];
 #pragma unroll
@@ -408,79 +409,94 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
     }
   };
 
-  // prologue: k-tiles kt0 .. kt0+2 into stages 0-2; NF4: the raw half-blocks of kt0 .. kt0+3,
-  // the first two decoded into B stages 0 and 1
+  // prologue: k-tiles kt0 .. kt0+2 into stages 0-2. NF4: the codes and scales of kt0 .. kt0+3
+  // into their stages; kt0 and kt0+1 decoded into B stages 0 and 1, kt0+2's read into
+  // registers (decoded during kt0), then kt0+4's DMA into stage 0.
   issue_tile(kt0, sA0, sB0);
   issue_tile(kt0 + 1, sA1, sB1);
   issue_tile(kt0 + 2, sA2, sB2);
   NF4Planes planes;
+  uint4 cx{}, cy{};  // codes of the half-block decoded at the even / odd k-tiles of a trip
+  float sx = 0.0f, sy = 0.0f;
+  auto nf4_at = [&](int64_t kt) { return e_base + clamp_kt(kt) * e_step; };
   if constexpr (BSRC == kBNF4) {
-    NF4Raw r0, r1;
-    nf4_load(r0, g.w, e_base + kt0 * e_step);
-    nf4_load(r1, g.w, e_base + (kt0 + 1) * e_step);
-    nf4_load(raw2, g.w, e_base + clamp_kt(kt0 + 2) * e_step);
-    nf4_load(raw3, g.w, e_base + clamp_kt(kt0 + 3) * e_step);
-    nf4_load(raw0, g.w, e_base + clamp_kt(kt0 + 4) * e_step);
-    __syncthreads();  // s_c2, s_offs
-    const float sc0 = nf4_scale(r0, g.w.nested, s_c2, s_offs);
-    nf4_decode_part<NN>(r0, sc0, planes, sB0, b_row, b_chunk0, lv, 0);
-    nf4_decode_part<NN>(r0, sc0, planes, sB0, b_row, b_chunk0, lv, 1);
-    const float sc1 = nf4_scale(r1, g.w.nested, s_c2, s_offs);
-    nf4_decode_part<NN>(r1, sc1, planes, sB1, b_row, b_chunk0, lv, 0);
-    nf4_decode_part<NN>(r1, sc1, planes, sB1, b_row, b_chunk0, lv, 1);
+    nf4_issue(g, nf4_at(kt0), sC0, sS0, wave);
+    nf4_issue(g, nf4_at(kt0 + 1), sC1, sS1, wave);
+    nf4_issue(g, nf4_at(kt0 + 2), sC2, sS2, wave);
+    nf4_issue(g, nf4_at(kt0 + 3), sC3, sS3, wave);
+    __builtin_amdgcn_s_waitcnt(0);  // (each thread reads the slots its own wavefront filled)
+    const uint4 c0 = *reinterpret_cast<const uint4*>(sC0 + 16 * tid);
+    const uint4 c1 = *reinterpret_cast<const uint4*>(sC1 + 16 * tid);
+    const float s0 = sS0[tid], s1 = sS1[tid];
+    cx = *reinterpret_cast<const uint4*>(sC2 + 16 * tid);
+    sx = sS2[tid];
+    nf4_decode_part<NN>(c0, s0, planes, sB0, b_row, b_chunk0, lv, 0);
+    nf4_decode_part<NN>(c0, s0, planes, sB0, b_row, b_chunk0, lv, 1);
+    nf4_decode_part<NN>(c1, s1, planes, sB1, b_row, b_chunk0, lv, 0);
+    nf4_decode_part<NN>(c1, s1, planes, sB1, b_row, b_chunk0, lv, 1);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): stage 0 read before its next DMA
+    nf4_issue(g, nf4_at(kt0 + 4), sC0, sS0, wave);
   }
   sync_tile<0>();
 
   // Software pipeline over four LDS stages, unrolled by four so every buffer is static (k-tile
-  // t on stage t % 4). At the top of k-tile t the DMA of t + 3 goes into the stage k-tile t - 1
-  // used (free since the last barrier); NF4: the raw half-block of t + 5 is loaded into the
-  // registers of t + 1 (decoded at t - 1), and t + 2 is decoded into its B stage across both
-  // k-steps (done by the barrier that ends t + 1); its raw loads were issued three k-tiles
-  // earlier, so the barrier waits already cover them. Each k-step's 16 MFMAs run while the next k-step's fragments are
-  // read; the second k-step reads the first fragments of t + 1 after the barrier that makes
-  // t + 1 visible (the wait leaves the loads of t + 2 and t + 3 in flight). Past the last
-  // k-tile the prefetches re-read it into stages no longer read: a trip has no branch.
+  // t on stage t % 4). After the barrier in the middle of k-tile t the DMA of t + 3 goes into
+  // the stage k-tile t - 1 used. NF4: k-tile t decodes t + 2 into its B stage across both
+  // k-steps (done by the barrier that ends t + 1) from codes read into registers during t - 1;
+  // after its barrier it issues the DMA of t + 5's codes and scales (stage (t + 1) % 4, read
+  // during t - 2) and reads t + 3's, which that barrier made complete: everything a k-tile
+  // issues has landed by the barrier of the k-tile after next. Every memory operand reaches the
+  // kernel through LDS, so the compiler's waits on loaded registers never drain the queue. Each
+  // k-step's 16 MFMAs run while the next k-step's fragments are read; the second k-step reads
+  // the first fragments of t + 1 after the barrier that makes t + 1 visible (the wait leaves
+  // the loads of t + 2 in flight). Past the last k-tile the prefetches re-read it into stages
+  // no longer read: a trip has no branch.
   constexpr int kValu = BSRC == kBNF4 ? 5 : 0;
+  // fp16 outputs leave through LDS from transposed accumulators (mfma_step)
+  constexpr bool kT = EPI == kEpiStore || EPI == kEpiBias || EPI == kEpiSwiglu;
   Frags f0, f1;
   read_frags<NN>(f0, sA0, sB0, 0, wm, wn, lane);
   auto k_tile = [&](int64_t t, uint16_t* sa, uint16_t* sb, uint16_t* sa_next, uint16_t* sb_next,
-                    uint16_t* sa_pre, uint16_t* sb_pre, uint16_t* sb_dec, NF4Raw& r_load,
-                    const NF4Raw& r_dec) {
-    float sc = 0.0f;
-    if constexpr (BSRC == kBNF4) sc = nf4_scale(r_dec, g.w.nested, s_c2, s_offs);
+                    uint16_t* sa_pre, uint16_t* sb_pre, uint16_t* sb_dec, uint8_t* c_load,
+                    float* s_load, const uint8_t* c_read, const float* s_read,
+                    const uint4& c_dec, const float& s_dec, uint4& c_next, float& s_next) {
     __builtin_amdgcn_sched_barrier(0);
     read_frags<NN>(f1, sa, sb, 1, wm, wn, lane);
     if constexpr (BSRC == kBNF4)
-      nf4_decode_part<NN>(r_dec, sc, planes, sb_dec, b_row, b_chunk0, lv, 0);
-    mfma_step(acc, f0);
+      nf4_decode_part<NN>(c_dec, s_dec, planes, sb_dec, b_row, b_chunk0, lv, 0);
+    mfma_step<kT>(acc, f0);
     sched_step<NN, kValu, 0>();
     __builtin_amdgcn_sched_barrier(0);
     sync_tile<kVmPerTile>();  // k-tile t + 1 landed; t + 2 may still be in flight
-    // the DMA of t + 3 into the stage t - 1 used, issued while no LDS read is outstanding
+    // the DMA of t + 3 into the stage t - 1 used (every wavefront's reads of it ended before
+    // the barrier), spread over this k-step's MFMAs
     issue_tile(t + 3, sa_pre, sb_pre);
-    if constexpr (BSRC == kBNF4) nf4_load(r_load, g.w, e_base + clamp_kt(t + 5) * e_step);
-    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (BSRC == kBNF4) nf4_issue(g, nf4_at(t + 5), c_load, s_load, wave);
     read_frags<NN>(f0, sa_next, sb_next, 0, wm, wn, lane);
-    if constexpr (BSRC == kBNF4)
-      nf4_decode_part<NN>(r_dec, sc, planes, sb_dec, b_row, b_chunk0, lv, 1);
-    mfma_step(acc, f1);
-    sched_step<NN, kValu, 0>();
+    if constexpr (BSRC == kBNF4) {
+      nf4_decode_part<NN>(c_dec, s_dec, planes, sb_dec, b_row, b_chunk0, lv, 1);
+      c_next = *reinterpret_cast<const uint4*>(c_read + 16 * tid);
+      s_next = s_read[tid];
+    }
+    mfma_step<kT>(acc, f1);
+    sched_step<NN, kValu, kVmPerTile>();
     __builtin_amdgcn_sched_barrier(0);
   };
   for (int64_t t = kt0; t < kt1; t += 4) {
-    k_tile(t, sA0, sB0, sA1, sB1, sA3, sB3, sB2, raw1, raw2);
-    k_tile(t + 1, sA1, sB1, sA2, sB2, sA0, sB0, sB3, raw2, raw3);
-    k_tile(t + 2, sA2, sB2, sA3, sB3, sA1, sB1, sB0, raw3, raw0);
-    k_tile(t + 3, sA3, sB3, sA0, sB0, sA2, sB2, sB1, raw0, raw1);
+    k_tile(t, sA0, sB0, sA1, sB1, sA3, sB3, sB2, sC1, sS1, sC3, sS3, cx, sx, cy, sy);
+    k_tile(t + 1, sA1, sB1, sA2, sB2, sA0, sB0, sB3, sC2, sS2, sC0, sS0, cy, sy, cx, sx);
+    k_tile(t + 2, sA2, sB2, sA3, sB3, sA1, sB1, sB0, sC3, sS3, sC1, sS1, cx, sx, cy, sy);
+    k_tile(t + 3, sA3, sB3, sA0, sB0, sA2, sB2, sB1, sC0, sS0, sC2, sS2, cy, sy, cx, sx);
   }
   __builtin_amdgcn_s_waitcnt(0);  // the prefetches past the end: nothing left in flight
 
-  // epilogue: register r of lane l in a 32x32 block holds row 8(r/4) + 4(l/32) + r%4, col l%32
+  // epilogue (register layouts: mfma_step)
   const int col_in = lane & 31;
-  if constexpr (EPI == kEpiStore || EPI == kEpiBias || EPI == kEpiSwiglu) {
-    // fp16 outputs go through LDS: each wavefront writes its block there as fp16 (2-byte LDS
-    // stores, chunks XOR-swizzled by row so both half-waves hit distinct banks), then stores
-    // whole rows to memory with 16-byte stores. Stages are free once every wavefront is done.
+  if constexpr (kT) {
+    // fp16 outputs go through LDS: each wavefront writes its block there as fp16 (8-byte LDS
+    // stores of four columns, 16-byte chunks XOR-swizzled by row so the 32 rows of a store
+    // spread over the banks), then stores whole rows to memory with 16-byte stores. Stages are
+    // free once every wavefront is done.
     __builtin_amdgcn_s_waitcnt(0);
     __builtin_amdgcn_s_barrier();
     uint16_t* lo = wave == 0 ? sA0 : wave == 1 ? sA2 : wave == 2 ? sB0 : sB2;
@@ -491,30 +507,42 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
     auto stage_off = [&](int row, int chunk) {
       return (row & 63) * kCols + ((chunk ^ (row & (kChunks - 1))) << 3);
     };
+    const int c4 = 4 * (lane >> 5);  // first of the lane's four columns in an 8-column group
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
+      const int row = i * 32 + col_in;
+      uint16_t* base = i < 2 ? lo : hi;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-        uint16_t* base = row < 64 ? lo : hi;
+      for (int q = 0; q < 4; ++q) {  // 8-column group q of each 32-column block
         if constexpr (EPI == kEpiSwiglu) {
 #pragma unroll
           for (int j = 0; j < 2; ++j) {
-            const int col = j * 32 + col_in;
-            const float gt = h2f(f2h(acc[i][j][r])), up = h2f(f2h(acc[i][j + 2][r]));
-            const float mval = gt * sigmoid_fast(gt) * up;  // as glu_fwd_kernel
-            base[stage_off(row, col >> 3) + (col & 7)] = f2h_bits(mval);
+            const int col = j * 32 + 8 * q + c4;
+            float m[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float gt = h2f(f2h(acc[i][j][4 * q + e]));
+              const float up = h2f(f2h(acc[i][j + 2][4 * q + e]));
+              m[e] = gt * sigmoid_fast(gt) * up;  // as glu_fwd_kernel
+            }
+            *reinterpret_cast<uint2*>(base + stage_off(row, col >> 3) + c4) =
+                make_uint2(pack2h(m[0], m[1]), pack2h(m[2], m[3]));
           }
         } else {
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            const int col = j * 32 + col_in;
-            float v = acc[i][j][r];
-            if constexpr (EPI == kEpiBias) {
-              const int64_t n = tile_n * kBN + wn * 128 + col;
-              v += h2f_bits(g.bias[n < g.N ? n : g.N - 1]);
+            const int col = j * 32 + 8 * q + c4;
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              v[e] = acc[i][j][4 * q + e];
+              if constexpr (EPI == kEpiBias) {
+                const int64_t n = tile_n * kBN + wn * 128 + col + e;
+                v[e] += h2f_bits(g.bias[n < g.N ? n : g.N - 1]);
+              }
             }
-            base[stage_off(row, col >> 3) + (col & 7)] = f2h_bits(v);
+            *reinterpret_cast<uint2*>(base + stage_off(row, col >> 3) + c4) =
+                make_uint2(pack2h(v[0], v[1]), pack2h(v[2], v[3]));
           }
         }
       }
@@ -659,38 +687,60 @@ int shape_of(int mode, int epi, int64_t w_rows, int64_t w_cols, int64_t swiglu_I
 
 }  // namespace
 
-// NF4-decode GEMM. mode: 0 = NT (C = A W^T), 1 = NN (C = A W). epi: 0 store fp16, 1 + bias,
-// 2 fp32 residual, 3 SwiGLU (NT only). splits > 1: split-K through `ws` (fp32, splits M N).
-QLORA_API int qlora_nf4_gemm(const void* a, int64_t lda, const void* packed, const void* absmax,
-                             const float* code2, const float* absmax2, const float* offsets,
-                             const float* code, int32_t nested, int32_t standard, int32_t bs1,
-                             int32_t bs2, int64_t seg1, int64_t seg2, int64_t w_rows,
-                             int64_t w_cols, void* c, int64_t ldc, const void* bias,
-                             const float* resid, int64_t ldr, int64_t M, int32_t mode,
-                             int32_t epi, int64_t swiglu_I, int32_t splits, float* ws,
-                             int64_t ws_elems, void* stream) {
+// The fp32 scale of each 64-value block of an NF4 weight, as the dequant forms it (nf4.h:
+// nf4_block_scale): the GEMM's B loader reads one word per block instead of the double-quant
+// chain (absmax code -> code2 -> times absmax2 -> plus offset). Weights are frozen, so the host
+// computes these once per weight.
+__global__ __launch_bounds__(256) void nf4_block_scales_kernel(NF4Ref w, int64_t blocks,
+                                                               float* out) {
+  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b < blocks) out[b] = nf4_block_scale(w, b);
+}
+
+QLORA_API int qlora_nf4_block_scales(const void* absmax, const float* code2,
+                                     const float* absmax2, const float* offsets, int32_t nested,
+                                     int32_t bs2, int64_t seg1, int64_t seg2, int64_t blocks,
+                                     float* out, void* stream) {
+  QLORA_CHECK_ARG(blocks >= 0);
+  if (blocks == 0) return 0;
+  QLORA_CHECK_ARG(absmax && out);
+  QLORA_CHECK_ARG(!nested || (code2 && absmax2 && offsets && bs2 > 0 && (bs2 & (bs2 - 1)) == 0));
+  const NF4Ref w{nullptr, absmax, code2, absmax2, offsets, nullptr, seg1, seg2, 6,
+                 nested ? __builtin_ctz(bs2) : 0, nested, 1};
+  hipLaunchKernelGGL(nf4_block_scales_kernel, dim3((unsigned)qlora_cdiv(blocks, 256)), dim3(256),
+                     0, (hipStream_t)stream, w, blocks, out);
+  return qlora_launch_status();
+}
+
+// NF4-decode GEMM. W [w_rows, w_cols]: `packed` codes, `scales` the fp32 scale of each 64-value
+// block (qlora_nf4_block_scales), `code` the 16 levels or null for the NF4 table. mode: 0 = NT
+// (C = A W^T), 1 = NN (C = A W). epi: 0 store fp16, 1 + bias, 2 fp32 residual, 3 SwiGLU (NT
+// only). splits > 1: split-K through `ws` (fp32, splits M N).
+QLORA_API int qlora_nf4_gemm(const void* a, int64_t lda, const void* packed, const float* scales,
+                             const float* code, int32_t bs1, int64_t w_rows, int64_t w_cols,
+                             void* c, int64_t ldc, const void* bias, const float* resid,
+                             int64_t ldr, int64_t M, int32_t mode, int32_t epi, int64_t swiglu_I,
+                             int32_t splits, float* ws, int64_t ws_elems, void* stream) {
   QLORA_CHECK_ARG(M >= 0 && w_rows > 0 && w_cols > 0);
   if (M == 0) return 0;
-  QLORA_CHECK_ARG(a && packed && absmax && c && (mode == 0 || mode == 1));
+  QLORA_CHECK_ARG(a && packed && scales && c && (mode == 0 || mode == 1));
   QLORA_CHECK_ARG(epi >= 0 && epi <= 3 && !(epi == 3 && mode != 0));
   QLORA_CHECK_ARG(splits >= 1 && splits <= 16 && !(splits > 1 && epi == 3));
-  QLORA_CHECK_ARG(bs1 == 64);  // one quantization block per thread and k-tile
-  QLORA_CHECK_ARG(!nested || (code2 && absmax2 && offsets && bs2 > 0 && (bs2 & (bs2 - 1)) == 0));
-  QLORA_CHECK_ARG(standard || code);
+  QLORA_CHECK_ARG(bs1 == 64);  // a thread's 32 values of a k-tile lie in one block
   QLORA_CHECK_ARG(epi != 1 || bias);
   QLORA_CHECK_ARG(epi != 2 || (resid && ldr >= 0));
   int64_t N, Kr;
   int rc = shape_of(mode, epi, w_rows, w_cols, swiglu_I, &N, &Kr);
   if (rc) return rc;
   QLORA_CHECK_ARG(lda >= Kr && ldc >= N && (epi != 2 || ldr >= N));
-  QLORA_CHECK_ARG(lda % 8 == 0 && al(a, 16) && al(packed, 16));
+  QLORA_CHECK_ARG(lda % 8 == 0 && al(a, 16) && al(packed, 16) && al(scales, 4));
   QLORA_CHECK_ARG(256 * lda * 2 < (1ll << 32));  // 32-bit DMA offsets within an A tile
   GemmArgs g{};
   g.a = static_cast<const uint16_t*>(a);
   g.lda = lda;
-  g.w = NF4Ref{static_cast<const uint8_t*>(packed), absmax, code2, absmax2, offsets, code,
-               seg1, seg2, __builtin_ctz(bs1), nested ? __builtin_ctz(bs2) : 0, nested,
-               standard};
+  g.w_packed = static_cast<const uint8_t*>(packed);
+  g.w_scales = scales;
+  g.w_code = code;
   g.Kw = w_cols;
   g.c = c;
   g.ldc = ldc;

@@ -17,7 +17,6 @@ from . import _lib, gemm
 from .ops import NF4Group, _need, _ptr, _resid_add, _stream, dequant, dequant_many
 
 BACKEND = "dequant"
-_NO_SEG = 2**63 - 1
 
 
 def _weights(w):
@@ -76,18 +75,9 @@ def _shape(w):
 
 
 def _nf4_args(w):
-    """(packed, absmax, code2, absmax2, offsets, code, nested, standard, bs1, bs2, seg1, seg2)
-    of an NF4Weight or NF4Group, as the C-ABI takes them."""
-    if isinstance(w, NF4Group):
-        seg1, seg2, offsets = w.seg1, w.seg2, w.offsets
-    else:
-        seg1 = seg2 = _NO_SEG
-        offsets = w.offset
-    nested = w.nested
-    return (_ptr(w.packed), _ptr(w.absmax), _ptr(w.code2) if nested else None,
-            _ptr(w.absmax2) if nested else None, _ptr(offsets) if nested else None,
-            _ptr(w.code), int(nested), int(w.standard), w.bs1, w.bs2 if nested else 1, seg1,
-            seg2)
+    """(packed, scales, code, bs1) of an NF4Weight or NF4Group, as qlora_nf4_gemm takes them
+    (code null for the NF4 table)."""
+    return (_ptr(w.packed), _ptr(w.block_scales()), None if w.standard else _ptr(w.code), w.bs1)
 
 
 TILE = 256  # output tile of the MFMA GEMM kernels (256 x 256; SwiGLU: 256 x 128 outputs)

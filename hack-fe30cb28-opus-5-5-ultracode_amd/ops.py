@@ -120,6 +120,13 @@ class NF4Weight:
                                    self.offset, self.code, self.blocks, self.nested,
                                    self.standard, self.bs1, self.bs2, _NO_SEG, _NO_SEG,
                                    self.numel)
+        self._scales = None
+
+    def block_scales(self):
+        """fp32 [blocks]: each block's scale, the operand of the fused NF4 GEMM."""
+        if self._scales is None:
+            self._scales = _block_scales(self, self.offset, _NO_SEG, _NO_SEG)
+        return self._scales
 
     @property
     def blocks(self):
@@ -187,6 +194,13 @@ class NF4Group:
                                    self.offsets, self.code, self.blocks, self.nested,
                                    self.standard, self.bs1, self.bs2, self.seg1, self.seg2,
                                    self.numel)
+        self._scales = None
+
+    def block_scales(self):
+        """fp32 [blocks]: each block's scale (its weight's offset by segment)."""
+        if self._scales is None:
+            self._scales = _block_scales(self, self.offsets, self.seg1, self.seg2)
+        return self._scales
 
     @property
     def shape(self):
@@ -231,6 +245,19 @@ def _launch_dequant(args, out, blocks, nested, standard, bs1, bs2, seg1, seg2, n
         return
     _lib.call("qlora_nf4_dequant", *args, _ptr(out), blocks, int(nested), int(standard), bs1,
               bs2, seg1, seg2, _stream(dev))
+
+
+def _block_scales(w, offsets, seg1, seg2):
+    """The fp32 scale of each block of an NF4Weight / NF4Group (qlora_nf4_block_scales): the
+    absmax itself without double quantisation, else decoded once - the weights are frozen, so
+    the fused GEMM reads one word per block for the whole run."""
+    if not w.nested:
+        return w.absmax
+    out = torch.empty(w.blocks, device=w.packed.device, dtype=torch.float32)
+    _lib.call("qlora_nf4_block_scales", _ptr(w.absmax), _ptr(w.code2), _ptr(w.absmax2),
+              _ptr(offsets), 1, w.bs2, seg1, seg2, w.blocks, _ptr(out),
+              _stream(w.packed.device))
+    return out
 
 
 def _dq_segs(w):

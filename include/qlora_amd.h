@@ -227,9 +227,22 @@ int qlora_nf4_dequant_many_timed(int32_t count, const void* const* packed,
                                  void* start, void* stop);
 
 /*
+ * The fp32 scale of each of `blocks` 64-value NF4 blocks (nested: fp32(fp32(code2[absmax[b]] *
+ * absmax2[b / bs2]) + offsets[segment(b)]), the segments as qlora_nf4_dequant's; plain: the fp32
+ * absmax copied) into out [blocks]: the scale operand of qlora_nf4_gemm, bit-identical to the
+ * scale qlora_nf4_dequant applies. The weights are frozen, so a caller forms it once per weight.
+ * Replaces the absmax dequantisation of the reference's dequant (kernels.py:68-105,
+ * engine.py:74-157), done once instead of per use.
+ */
+int qlora_nf4_block_scales(const void* absmax, const float* code2, const float* absmax2,
+                           const float* offsets, int32_t nested, int32_t bs2, int64_t seg1,
+                           int64_t seg2, int64_t blocks, float* out, void* stream);
+
+/*
  * NF4 dequantisation fused into an fp16 MFMA GEMM (fp32 accumulation) with a frozen NF4 weight
- * W [w_rows, w_cols] in the layout of qlora_nf4_dequant (same absmax/code2/absmax2/offsets/
- * segment arguments); 256 x 256 output tiles, the NF4 blocks decoded into LDS inside the kernel:
+ * W [w_rows, w_cols]: `packed` codes as qlora_nf4_dequant's, `scales` fp32 [w_rows*w_cols/64]
+ * (qlora_nf4_block_scales), `code` the 16 levels (null: the NF4 table); 256 x 256 output tiles,
+ * the NF4 blocks decoded into LDS inside the kernel:
  *   mode 0 (NT): C[M, w_rows] = A[M, w_cols] W^T      mode 1 (NN): C[M, w_cols] = A[M, w_rows] W
  *   A f16 [M, lda].
  *   epi 0: C f16 = f16(acc);  epi 1: C f16 = f16(acc + bias[n]) (bias f16);
@@ -244,12 +257,10 @@ int qlora_nf4_dequant_many_timed(int32_t count, const void* const* packed,
  * SwiGLU (kernels.py:312-321) and residual add (engine.py:1048-1051) that follow them.
  * Requires: M >= 0; bs1 == 64; mode 0: w_rows % 256 == 0 (epi 3: I % 128 == 0),
  * w_cols % 128 == 0; mode 1: w_cols % 256 == 0, w_rows % 128 == 0; lda % 8 == 0; A and packed
- * 16-byte aligned; splits <= 16.
+ * 16-byte aligned, scales 4-byte aligned; splits <= 16.
  */
-int qlora_nf4_gemm(const void* a, int64_t lda, const void* packed, const void* absmax,
-                   const float* code2, const float* absmax2, const float* offsets,
-                   const float* code, int32_t nested, int32_t standard, int32_t bs1, int32_t bs2,
-                   int64_t seg1, int64_t seg2, int64_t w_rows, int64_t w_cols, void* c,
+int qlora_nf4_gemm(const void* a, int64_t lda, const void* packed, const float* scales,
+                   const float* code, int32_t bs1, int64_t w_rows, int64_t w_cols, void* c,
                    int64_t ldc, const void* bias, const float* resid, int64_t ldr, int64_t M,
                    int32_t mode, int32_t epi, int64_t swiglu_I, int32_t splits, float* ws,
                    int64_t ws_elems, void* stream);
@@ -260,8 +271,8 @@ int qlora_nf4_gemm(const void* a, int64_t lda, const void* packed, const void* a
  * epi, splits, ws as qlora_nf4_gemm (epi 3: B = [gate; up] rows, N = I).
  * Replaces the cuBLAS products of the frozen projections after dequant (engine.py:1082, 1112,
  * 1163, 1179, 1239, 1293, 1301, 1316) and of the lm_head (engine.py:1376-1381).
- * Requires: K % 128 == 0; mode 1: N % 256 == 0; mode 0: N % 8 == 0 (epi 3: N % 128 == 0); lda, ldb % 8 == 0; A, B
- * 16-byte aligned.
+ * Requires: K % 128 == 0; mode 1: N % 256 == 0; mode 0: N % 8 == 0 (epi 3: N % 128 == 0);
+ * lda, ldb % 8 == 0; A, B 16-byte aligned.
  */
 int qlora_hgemm(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t M, int64_t N,
                 int64_t K, int32_t mode, void* c, int64_t ldc, const void* bias,

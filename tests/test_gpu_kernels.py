@@ -88,6 +88,29 @@ def test_nf4_group_dequant_equals_separate(pkg):
     assert torch.equal(bits16(out), bits16(want))
 
 
+def test_nf4_block_scales_equal_oracle(pkg):
+    """qlora_nf4_block_scales (the fused GEMM's scale operand) equals the oracle's per-block
+    scale bit for bit: a q|k|v group with three double-quant offsets by segment, a single
+    nested weight, and a plain fp32 absmax (returned as is)."""
+    rng = np.random.default_rng(11)
+    ws = []
+    for shape in ((1536, 1536), (256, 1536), (256, 1536)):
+        w = (rng.standard_normal(shape) * 0.02).astype(np.float16)
+        packed, st = ON.quantize_nf4(w)
+        ws.append((packed, st, pkg.ops.NF4Weight(_device_state(packed, st))))
+    group = pkg.ops.NF4Group.of([w for _, _, w in ws])
+    want = np.concatenate([ON.block_scales(st) for _, st, _ in ws])
+    got = group.block_scales().cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert group.block_scales() is group.block_scales()  # formed once
+    single = ws[1][2].block_scales().cpu().numpy()
+    assert np.array_equal(single.view(np.uint32), ON.block_scales(ws[1][1]).view(np.uint32))
+    w = (rng.standard_normal((256, 512)) * 0.02).astype(np.float16)
+    packed, st = ON.quantize_nf4(w, compress_statistics=False)
+    plain = pkg.ops.NF4Weight(_device_state(packed, st))
+    assert plain.block_scales() is plain.absmax
+
+
 @pytest.mark.parametrize("mix", ["layer", "ragged", "32"])
 def test_nf4_dequant_many_equals_oracle(pkg, mix):
     """One qlora_nf4_dequant_many launch over several weights (a layer's q|k|v group, o,
