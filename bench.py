@@ -23,6 +23,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--policy 
 """
 
 import argparse
+import contextlib
 import importlib
 import json
 import os
@@ -113,26 +114,38 @@ def causal_pairs(lengths):
 
 
 def measure_step_kernels(pkg, trainer, batch, cfg):
-    """One extra (untimed) step with HIP events around every launch of the dequant and the
-    attention entry points: the dequant's achieved GB/s (dispatch-recorded events), and the
-    attention forward / backward TFLOP/s on the batch's causal pairs (fwd: QK^T and PV, 4 D
-    flops per pair and head; bwd: S, dP, dQ, dK, dV, 10 D flops per pair and head)."""
+    """One extra (untimed) step with HIP events around every launch of the dequant, the
+    attention and the GEMM entry points: the dequant's achieved GB/s (dispatch-recorded events),
+    the attention forward / backward TFLOP/s on the batch's causal pairs (fwd: QK^T and PV, 4 D
+    flops per pair and head; bwd: S, dP, dQ, dK, dV, 10 D flops per pair and head), and the
+    library GEMMs' TFLOP/s (2 M N K a product): all of the step's projection and lm_head
+    products, and the gate|up forward alone (the largest MFMA kernel of the step)."""
     P = pkg.profiling
     pairs = causal_pairs(batch[5]["lengths"])
     heads, D = cfg.num_attention_heads, cfg.head_dim
     fwd = P.LaunchTimer("qlora_attn_fwd_split", bound="mfma")
     bwd = P.LaunchTimer("qlora_attn_bwd_split", bound="mfma")
     dq = P.LaunchTimer(P.DOMINANT)
-    with dq:
-        with fwd:
-            with bwd:
-                trainer.step(batch)
+    flops = lambda a: 2.0 * a[1] * a[2] * a[3]  # noqa: E731  (op, M, N, K, ...)
+    gemms = [P.LaunchTimer(e, work=flops, bound="mfma")
+             for e in ("qlora_gemm", "qlora_gemm_splitk", "qlora_gemmlt")]
+    with contextlib.ExitStack() as stack:
+        for t in (dq, fwd, bwd, *gemms):
+            stack.enter_context(t)
+        trainer.step(batch)
     torch.cuda.synchronize()
     n_f, n_b = len(fwd.records), len(bwd.records)
-    return dq.summary(), [
-        dict(fwd.summary(work_total=4.0 * D * heads * pairs * n_f), kernel="attn_fwd_kernel"),
-        dict(bwd.summary(work_total=10.0 * D * heads * pairs * n_b),
-             kernel="attn_delta + attn_dq + attn_dkdv kernels")]
+    gate_up = 2 * cfg.intermediate_size
+    out = [dict(fwd.summary(work_total=4.0 * D * heads * pairs * n_f), kernel="attn_fwd_kernel"),
+           dict(bwd.summary(work_total=10.0 * D * heads * pairs * n_b),
+                kernel="attn_delta + attn_dq + attn_dkdv kernels")]
+    every = gemms[0].summary(also=gemms[1:])
+    if every is not None:
+        out.append(dict(every, kernel="every library GEMM of the step (projections, lm_head)"))
+    gu = gemms[0].summary(also=gemms[1:], select=lambda a: a[0] == 0 and a[2] == gate_up)
+    if gu is not None:
+        out.append(dict(gu, kernel="gate|up forward GEMM (y = x W^T, N = 2 I)"))
+    return dq.summary(), out
 
 
 def _median_time(fn, reps, sync=True):
@@ -440,6 +453,10 @@ def main():
     ap.add_argument("--no-configs", action="store_true", help="skip the config 1-4 legs")
     ap.add_argument("--config1", action="store_true",
                     help="only the config-1 dequant measurement (and its copy calibration)")
+    ap.add_argument("--profile", action="store_true",
+                    help="a run to profile: GEMM solutions timed only for the token counts of "
+                         "the batches it runs; no loss curve past the timed steps, no keep-all "
+                         "extra, no config legs, no CPU baseline")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus}: this build measures one GPU only (the path is "
@@ -461,8 +478,12 @@ def main():
     batches = make_batches(n_batches, cfg.vocab_size, device=dev)
     log("model built; timing the projection GEMM solutions")
     # every step size config 5 can produce (4 rows of 256..1024 tokens), before any timing
-    tune_s = model.tune_gemms(range(4 * 256, 4 * 1024 + pkg.gemm.BUCKET, pkg.gemm.BUCKET),
-                              log=log)
+    sizes = range(4 * 256, 4 * 1024 + pkg.gemm.BUCKET, pkg.gemm.BUCKET)
+    if args.profile:
+        sizes = sorted({int(b[4]) for b in batches[:args.warmup + args.steps]} |
+                       {int(batches[-1][4])})
+        args.no_cpu, args.no_configs, args.keep_steps = True, True, 0
+    tune_s = model.tune_gemms(sizes, log=log)
     cpu_model = None
     if not args.no_cpu:
         from oracle import step as OS
@@ -475,7 +496,9 @@ def main():
     value = tokens / elapsed
     log(f"{args.steps} steps {elapsed:.3f} s, {value:.0f} tokens/s")
     done = args.warmup + args.steps
-    _, _, rest = time_steps(trainer, batches, done, max(0, CURVE_STEPS - done))
+    rest = []
+    if not args.profile:
+        _, _, rest = time_steps(trainer, batches, done, max(0, CURVE_STEPS - done))
     curve = (warm_losses + timed_losses + rest)[:CURVE_STEPS]
     kernels = measure_step_kernels(pkg, trainer, batches[-1], cfg)
     keep = None

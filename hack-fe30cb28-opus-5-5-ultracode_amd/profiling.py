@@ -20,10 +20,10 @@ DOMINANT = "qlora_nf4_dequant_many"
 
 # Measured HBM bytes per launch over algorithmic bytes per launch: rocprofv3 FETCH_SIZE and
 # WRITE_SIZE of the layer-wide dequant launch (the same kernel and byte count as each of the
-# step's launches), each divided by what the counter reads for a plain 4.5 MiB device copy
-# (FETCH 0.5025, WRITE 1.000 of the bytes moved): (11,903.5 / 0.5025 + 91,392) KiB per launch
-# = 1.001 x the algorithmic 117,728,444 B.
-TRAFFIC_RATIO = {"qlora_nf4_dequant_many": 1.001}
+# step's launches), each divided by what the counter reads for a plain device copy of 1 GiB
+# (512 MiB each way; FETCH 0.50004, WRITE 1.000 of the bytes moved):
+# (11,892.4 / 0.50004 + 91,392) KiB per launch = 1.0018 x the algorithmic 117,728,444 B.
+TRAFFIC_RATIO = {"qlora_nf4_dequant_many": 1.0018}
 
 
 def _dequant_bytes(args):
@@ -97,15 +97,18 @@ class LaunchTimer:
         else:
             rc = fn(*args)
             end.record()
-        self.records.append((start, end, self.work(args)))
+        self.records.append((start, end, self.work(args), args))
         return rc
 
-    def summary(self, work_total=None):
+    def summary(self, work_total=None, select=None, also=()):
+        """Average duration and achieved rate over the launches (`select`: a predicate on a
+        launch's arguments; `also`: more timers of the same bound whose launches count too)."""
         torch.cuda.synchronize()
-        if not self.records:
+        recs = [r for t in (self, *also) for r in t.records if select is None or select(r[3])]
+        if not recs:
             return None
-        ms = [s.elapsed_time(e) for s, e, _ in self.records]
-        work = sum(w for _, _, w in self.records) if work_total is None else work_total
+        ms = [s.elapsed_time(e) for s, e, _, _ in recs]
+        work = sum(w for _, _, w, _ in recs) if work_total is None else work_total
         total_s = sum(ms) * 1e-3
         avg_us = 1e3 * sum(ms) / len(ms)
         if self.bound == "hbm":
