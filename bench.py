@@ -109,6 +109,64 @@ def first_step(model, batch, scale=2.0**16):
             "metadata_ok": None if ok is None else bool(ok)}
 
 
+GRAPH_T = 256  # a captured step's columns: the batch's longest row rounded up to a multiple
+
+
+def graph_leg(pkg, trainer, batches, count=8):
+    """Device-only packing and the step captured as a HIP graph (engine.StepGraph) on config-5
+    batches: each batch padded to the next multiple of GRAPH_T columns, one graph per padded
+    shape (the capture's time reported apart), replayed with the trainer's GradScaler scale (a
+    device scalar) and followed by its AdamW step; beside it the same padded steps run eagerly.
+    Tokens/s count the real tokens; the padded steps compute over rows x columns tokens."""
+    model = trainer.model
+    scaler, opt = trainer.scaler, trainer.opt
+    padded = []
+    for ids, mask, labels, denom, ntok, _ in batches[:count]:
+        T = ids.shape[1]
+        Tp = -(-T // GRAPH_T) * GRAPH_T
+
+        def pad(t, v):
+            return torch.nn.functional.pad(t, (0, Tp - T), value=v)
+        padded.append((pad(ids, 0), pad(mask, 0), pad(labels, -100), denom, ntok))
+    t0 = time.perf_counter()
+    graphs = {}
+    for ids, *_ in padded:
+        if tuple(ids.shape) not in graphs:
+            graphs[tuple(ids.shape)] = pkg.engine.StepGraph(model, *ids.shape)
+    torch.cuda.synchronize()
+    capture_s = time.perf_counter() - t0
+
+    def run(replay):
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        tokens, rows = 0, 0
+        for ids, mask, labels, denom, ntok in padded:
+            if replay:
+                graphs[tuple(ids.shape)].replay(ids, mask, labels, denom, scaler._scale)
+            else:
+                loss, _, _ = model.step(ids, mask, labels, denom, padded=True)
+                scaler.scale(loss).backward()
+            scaler.step(opt)
+            scaler.update()
+            opt.zero_grad(set_to_none=True)
+            tokens += ntok
+            rows += ids.numel()
+        torch.cuda.synchronize()
+        return tokens, rows, time.perf_counter() - t
+
+    run(True)  # the first replay of each graph uploads it
+    tok, rows, t_graph = run(True)
+    _, _, t_eager = run(False)
+    n = len(padded)
+    return {"tokens_per_s_graph": tok / t_graph, "ms_per_step_graph": 1e3 * t_graph / n,
+            "tokens_per_s_eager_padded": tok / t_eager, "ms_per_step_eager_padded":
+                1e3 * t_eager / n, "steps": n, "real_tokens": tok, "padded_tokens": rows,
+            "shapes": sorted(graphs), "capture_s": capture_s,
+            "what": "device-only packing: padded [rows, T] batches (T rounded up to "
+                    f"{GRAPH_T}), forward + backward replayed from a HIP graph, GradScaler + "
+                    "AdamW after each; eager padded steps on the same batches beside it"}
+
+
 def causal_pairs(lengths):
     return sum(L * (L + 1) // 2 for L in lengths)
 
@@ -512,6 +570,11 @@ def main():
                         "backward (no recompute): not config 5, reported beside it"}
         model.keep_all = args.policy == "keep"
         log(f"keep-all: {keep['value']:.0f} tokens/s")
+    graph = None
+    if not args.profile:
+        graph = graph_leg(pkg, trainer, batches[args.warmup:])
+        log(f"graph: {graph['tokens_per_s_graph']:.0f} tokens/s replayed, "
+            f"{graph['tokens_per_s_eager_padded']:.0f} eager padded")
     result = {
         "metric": "train tokens/s (1.5B NF4 QLoRA step, 1 GPU); NF4 dequant HBM GB/s",
         "value": value, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
@@ -530,6 +593,7 @@ def main():
         "roofline_mfma": kernels[1],
         "loss_curve": curve,
         "keep_all": keep,
+        "graph": graph,
         "gemm_tuning_s": tune_s,
     }
     if not args.no_configs:

@@ -34,6 +34,7 @@ struct RmsFwdArgs {
   DropParams drop;
   int w_half;
   uint8_t* keep;          // u8 [n][2][ceil(H / 4)] keep bits (written when dropping) or null
+  const int64_t* ctr_base = nullptr;  // device int64 added to ctr_q / ctr_v, or null
 };
 
 struct RmsBwdArgs {
@@ -53,7 +54,14 @@ struct RmsBwdArgs {
   DropParams drop;
   int w_half;
   const uint8_t* keep;  // keep bits stored by the forward, or null: draw them again
+  const int64_t* ctr_base = nullptr;  // device int64 added to ctr_q / ctr_v, or null
 };
+
+// The counter of a mask: the launch's argument plus, when the caller keeps the step's first
+// counter on the device (a captured step replayed with fresh masks), that base.
+__device__ __forceinline__ uint64_t mask_ctr(uint64_t ctr, const int64_t* base) {
+  return base ? ctr + (uint64_t)*base : ctr;
+}
 
 // Bytes of one mask of one row in the keep-bit layout.
 __host__ __device__ __forceinline__ int64_t keep_row_bytes(int64_t H) { return (H + 3) / 4; }
@@ -150,7 +158,7 @@ __global__ __launch_bounds__(kWave* kRowsPerBlock) void rms_fwd_kernel(RmsFwdArg
     uint8_t* kr = W == 4 && a.keep ? a.keep + row * 2 * keep_row_bytes(a.H) + c : nullptr;
     if (a.yq) {
       DropParams d = a.drop;
-      d.ctr = a.ctr_q;
+      d.ctr = mask_ctr(a.ctr_q, a.ctr_base);
       const uint32_t keep = keep_bits<W>(d, e0);
       float o[W];
 #pragma unroll
@@ -160,7 +168,7 @@ __global__ __launch_bounds__(kWave* kRowsPerBlock) void rms_fwd_kernel(RmsFwdArg
     }
     if (a.yv) {
       DropParams d = a.drop;
-      d.ctr = a.ctr_v;
+      d.ctr = mask_ctr(a.ctr_v, a.ctr_base);
       const uint32_t keep = keep_bits<W>(d, e0);
       float o[W];
 #pragma unroll
@@ -194,7 +202,7 @@ __global__ __launch_bounds__(kWave* kRowsPerBlock) void rms_bwd_kernel(RmsBwdArg
     const uint8_t* kr = W == 4 && a.keep ? a.keep + row * 2 * keep_row_bytes(a.H) + c : nullptr;
     if (a.tq) {
       DropParams d = a.drop;
-      d.ctr = a.ctr_q;
+      d.ctr = mask_ctr(a.ctr_q, a.ctr_base);
       const uint32_t keep = kr ? kr[0] : keep_bits<W>(d, e0);
       float t[W];
       load_h<W>(a.tq + base + c * W, t);
@@ -203,7 +211,7 @@ __global__ __launch_bounds__(kWave* kRowsPerBlock) void rms_bwd_kernel(RmsBwdArg
     }
     if (a.tv) {
       DropParams d = a.drop;
-      d.ctr = a.ctr_v;
+      d.ctr = mask_ctr(a.ctr_v, a.ctr_base);
       const uint32_t keep = kr ? kr[keep_row_bytes(a.H)] : keep_bits<W>(d, e0);
       float t[W];
       load_h<W>(a.tv + base + c * W, t);
@@ -301,8 +309,8 @@ __global__ __launch_bounds__(kWave* kRowsPerBlock) void rms_fwd4_kernel(RmsFwdAr
     const int vs = a.drop.vec == 8 ? 3 : 2;
     const bool all = a.drop.p_keep >= 1.0f;
     DropParams dq = a.drop, dv = a.drop;
-    dq.ctr = a.ctr_q;
-    dv.ctr = a.ctr_v;
+    dq.ctr = mask_ctr(a.ctr_q, a.ctr_base);
+    dv.ctr = mask_ctr(a.ctr_v, a.ctr_base);
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const uint32_t e0 = tok_e + 4u * (uint32_t)(lane + 64 * i);
@@ -398,8 +406,8 @@ __global__ __launch_bounds__(kWave* kRowsPerBlock) void rms_bwd4_kernel(RmsBwdAr
     const int vs = a.drop.vec == 8 ? 3 : 2;
     const bool all = a.drop.p_keep >= 1.0f;
     DropParams dq = a.drop, dv = a.drop;
-    dq.ctr = a.ctr_q;
-    dv.ctr = a.ctr_v;
+    dq.ctr = mask_ctr(a.ctr_q, a.ctr_base);
+    dv.ctr = mask_ctr(a.ctr_v, a.ctr_base);
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const uint32_t e0 = tok_e + 4u * (uint32_t)(lane + 64 * i);
@@ -447,14 +455,14 @@ __global__ __launch_bounds__(kWave* kRowsPerBlock) void rms_bwd4_kernel(RmsBwdAr
 // Keep bits of the rows [n, H] in the keep-bit layout, element by element (the forward's
 // one-column path, which holds single elements per lane). One thread per byte of each mask.
 __global__ void rms_keep_bits_kernel(uint8_t* keep, const int64_t* tok, int64_t n, int64_t H,
-                                     DropParams d, uint64_t ctr_q, uint64_t ctr_v, int has_q,
-                                     int has_v) {
+                                     DropParams d, uint64_t ctr_q, uint64_t ctr_v,
+                                     const int64_t* ctr_base, int has_q, int has_v) {
   const int64_t kb = keep_row_bytes(H);
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // (row, mask, byte)
   if (i >= n * 2 * kb) return;
   const int64_t row = i / (2 * kb), m = (i / kb) % 2, j = i % kb;
   if (!(m == 0 ? has_q : has_v)) return;
-  d.ctr = m == 0 ? ctr_q : ctr_v;
+  d.ctr = mask_ctr(m == 0 ? ctr_q : ctr_v, ctr_base);
   const uint64_t e = (uint64_t)tok[row] * (uint64_t)H + 4 * j;
   uint32_t bits = 0;
   for (int k = 0; k < 4 && 4 * j + k < H; ++k) bits |= (uint32_t)drop_keep(d, e + k) << k;
@@ -574,7 +582,8 @@ QLORA_API int qlora_rms_fwd(const float* x, const void* delta, const void* w, in
                             const int64_t* tok, int64_t n, int64_t H, float eps, float p_keep,
                             float keep_scale, int64_t seed, int64_t ctr_q, int64_t ctr_v,
                             int64_t G, int32_t has_delta, int32_t write_y, int32_t drop_q,
-                            int32_t drop_v, int32_t vec, uint8_t* keep, void* stream) {
+                            int32_t drop_v, int32_t vec, uint8_t* keep,
+                            const int64_t* ctr_base, void* stream) {
   QLORA_CHECK_ARG(n >= 0 && H > 0);
   if (n == 0) return 0;
   QLORA_CHECK_ARG(x && w && rstd);
@@ -590,6 +599,7 @@ QLORA_API int qlora_rms_fwd(const float* x, const void* delta, const void* w, in
                (drop_q || drop_v) ? tok : nullptr, n, H, eps, keep_scale, (uint64_t)ctr_q,
                (uint64_t)ctr_v, make_drop(seed, G, p_keep, vec), w_half};
   a.keep = drop_q || drop_v ? keep : nullptr;
+  a.ctr_base = ctr_base;
   const bool v4 = H % 4 == 0 && aligned(x, 16) && aligned(w, w_half ? 8 : 16) &&
                   (!a.delta || aligned(delta, 8)) && (!a.xsum || aligned(xsum, 16)) &&
                   (!a.y || aligned(y, 8)) && (!a.yq || aligned(yq, 8)) &&
@@ -613,7 +623,7 @@ QLORA_API int qlora_rms_fwd(const float* x, const void* delta, const void* w, in
       QLORA_CHECK_ARG(qlora_cdiv(total, 256) < (1ll << 31));
       hipLaunchKernelGGL(rms_keep_bits_kernel, dim3((unsigned)qlora_cdiv(total, 256)), dim3(256),
                          0, (hipStream_t)stream, a.keep, tok, n, H, a.drop, a.ctr_q, a.ctr_v,
-                         drop_q ? 1 : 0, drop_v ? 1 : 0);
+                         a.ctr_base, drop_q ? 1 : 0, drop_v ? 1 : 0);
     }
   }
   return qlora_launch_status();
@@ -625,7 +635,7 @@ QLORA_API int qlora_rms_bwd(const void* dy, const void* tq, const void* tv, cons
                             int64_t dy_stride, float p_keep, float keep_scale, int64_t seed,
                             int64_t ctr_q, int64_t ctr_v, int64_t G, float grad_scale,
                             int32_t drop_q, int32_t drop_v, int32_t has_res, int32_t vec,
-                            const uint8_t* keep, void* stream) {
+                            const uint8_t* keep, const int64_t* ctr_base, void* stream) {
   QLORA_CHECK_ARG(n >= 0 && H > 0);
   if (n == 0) return 0;
   QLORA_CHECK_ARG(dy && x && rstd && w && dx && dy_stride >= H);
@@ -641,6 +651,7 @@ QLORA_API int qlora_rms_bwd(const void* dy, const void* tq, const void* tv, cons
                dy_stride, keep_scale, grad_scale, (uint64_t)ctr_q, (uint64_t)ctr_v,
                make_drop(seed, G, p_keep, vec), w_half};
   a.keep = drop_q || drop_v ? keep : nullptr;  // the one-column kernel draws the masks again
+  a.ctr_base = ctr_base;
   const bool v4 = H % 4 == 0 && dy_stride % 4 == 0 && aligned(dy, 8) && aligned(x, 16) &&
                   aligned(w, w_half ? 8 : 16) && aligned(dx, 16) &&
                   (!a.tq || aligned(tq, 8)) && (!a.tv || aligned(tv, 8)) &&

@@ -24,7 +24,7 @@ from . import gemm as G
 from . import linear as L
 from .ops import (NF4Group, NF4Weight, TorchDropout, _attn_bwd, _attn_fwd, _ce, _glu_bwd,
                   _glu_fwd, _lora_bwd_rows, _lora_fwd_rows, _lora_grad, _rms_bwd, _rms_fwd,
-                  _rope_bwd, _rope_fwd, keep_bits_shape)
+                  _rope_bwd, _rope_fwd, _as_int64, keep_bits_shape)
 from .quant import quantize_nf4
 
 
@@ -305,13 +305,62 @@ class Packed:
     step's first launches are queued. The caller's metadata is then checked on the device
     without waiting: `metadata_ok` is a device bool, False when the mask is not right-padded to
     the given lengths or the supervised count differs (read it when the step is synchronised
-    anyway)."""
+    anyway).
+
+    `padded=True` keeps the padding in place instead (device-only packing): every row is one
+    sequence of T tokens, its padding after its real tokens, so causal attention keeps the
+    padding out of every real token's result, and the padding tokens take no label. Nothing is
+    read from the device and no host lengths are needed: every shape follows from [B, T], so
+    the step can be captured in a HIP graph (StepGraph). The step then computes over B*T rows;
+    n_supervised is B*T, an upper bound (the head's unsupervised rows take a zero gradient);
+    metadata_ok reports on the device whether the mask was right-padded. `ctr_base`: a device
+    int64 holding the step's first dropout counter; the masks' counters are then relative to
+    it (padded batches only)."""
 
     def __init__(self, input_ids, attention_mask, labels, rope, dropout, dropout_p, lengths=None,
-                 n_supervised=None):
+                 n_supervised=None, padded=False, ctr_base=None):
         if input_ids.dim() != 2 or attention_mask.shape != input_ids.shape \
                 or labels.shape != input_ids.shape:
             raise UnsupportedBatch("inputs are not [rows, tokens]")
+        self.ctr_base, self.drawn = None, 0
+        if padded:
+            self._pack_padded(input_ids, attention_mask, labels, ctr_base)
+        else:
+            if ctr_base is not None:
+                raise ValueError("a device counter base needs padded=True")
+            self._pack(input_ids, attention_mask, labels, lengths, n_supervised)
+        self.cos, self.sin = rope.table(max(self.max_len, 1))
+        self.dropout_p, self.dropout = dropout_p, dropout
+        self.drop_seed = self.drop_threads = None  # set by the step's first draw
+        self.drop_vec = dropout.vec if dropout is not None else 4
+        self.lora16_views = self.lora16t_views = None
+        self.grad16 = None  # (dh, fp16(dh)) handed from a layer's backward to the one below
+
+    def _pack_padded(self, input_ids, attention_mask, labels, ctr_base):
+        B, T = input_ids.shape
+        dev = input_ids.device
+        self.rows, self.T, self.lengths = B, T, [T] * B
+        self.max_len = T
+        self.cu_seqlens_host = [T * r for r in range(B + 1)]
+        n = self.n = B * T
+        self.tok = torch.arange(n, device=dev)
+        self.pos = (self.tok % max(T, 1)).to(torch.int32)
+        self.cu_seqlens = torch.arange(0, n + 1, max(T, 1), device=dev, dtype=torch.int32)
+        self.ids = input_ids.reshape(-1)
+        real = attention_mask.bool()
+        nxt = torch.cat([labels[:, 1:], torch.full_like(labels[:, :1], -100)], dim=1)
+        self.targets = torch.where(real, nxt, torch.full_like(nxt, -100)).reshape(-1)
+        self.head_order = torch.argsort((self.targets < 0).to(torch.int8), stable=True)
+        self.n_supervised = n
+        right = torch.arange(T, device=dev)[None, :] < real.sum(dim=1, keepdim=True)
+        self.metadata_ok = (real == right).all()
+        if ctr_base is not None:
+            if ctr_base.dtype != torch.int64 or ctr_base.numel() != 1 or \
+                    ctr_base.device != dev:
+                raise ValueError("ctr_base must be one int64 on the batch's device")
+            self.ctr_base = ctr_base
+
+    def _pack(self, input_ids, attention_mask, labels, lengths, n_supervised):
         B, T = input_ids.shape
         dev = input_ids.device
         given = lengths is not None
@@ -342,12 +391,6 @@ class Packed:
             right = torch.arange(T, device=dev)[None, :] < (cu[1:] - cu[:-1])[:, None]
             self.metadata_ok = (attention_mask.bool() == right).all() & \
                 (counted == self.n_supervised)
-        self.cos, self.sin = rope.table(max(self.max_len, 1))
-        self.dropout_p, self.dropout = dropout_p, dropout
-        self.drop_seed = self.drop_threads = None  # set by the step's first draw
-        self.drop_vec = dropout.vec if dropout is not None else 4
-        self.lora16_views = self.lora16t_views = None
-        self.grad16 = None  # (dh, fp16(dh)) handed from a layer's backward to the one below
 
     @property
     def row_of_token(self):
@@ -368,8 +411,17 @@ class Packed:
     def draw(self, H):
         """The counter of this step's next LoRA dropout mask: the next nn.Dropout call of the
         base, on its padded [B, T, H] LoRA input (engine.py:758-764). Every call of one step
-        has the same seed and launch size."""
-        seed, ctr, threads = self.dropout.draw(self.rows * self.T * H)
+        has the same seed and launch size. With a device counter base the counter is relative
+        to the step's first and the generator is left alone: `drawn` counts the offset the
+        step's draws cover, by which the caller moves the generator."""
+        if self.ctr_base is not None:
+            if (self.rows * self.T * H) % self.dropout.vec:
+                raise ValueError("the LoRA input is not whole vector accesses")
+            threads, advance = self.dropout.launch(self.rows * self.T * H)
+            seed, ctr = _as_int64(self.dropout.gen.initial_seed()), self.drawn // 4
+            self.drawn += advance
+        else:
+            seed, ctr, threads = self.dropout.draw(self.rows * self.T * H)
         if self.drop_seed is None:
             self.drop_seed, self.drop_threads = seed, threads
         elif (seed, threads) != (self.drop_seed, self.drop_threads):
@@ -584,7 +636,13 @@ class _Head(torch.autograd.Function):
                              for _ in range(2))
         correct = torch.empty((n,), device=dev, dtype=torch.int32)
         grad_rows = torch.zeros_like(rows)
-        scale = 1.0 / float(denom) if float(denom) else float("nan")  # 0/0 as the base
+        # a device denominator (a captured step) divides in the loss and in the backward's
+        # incoming gradient; a host one scales the norm backward's output directly
+        ctx.denom = denom if isinstance(denom, torch.Tensor) else None
+        if ctx.denom is not None:
+            scale = 1.0
+        else:
+            scale = 1.0 / float(denom) if float(denom) else float("nan")  # 0/0 as the base
         for lo in range(0, n, chunk):
             hi = min(n, lo + chunk)
             logits = L.linear(hn[lo:hi], lm_w)
@@ -600,12 +658,15 @@ class _Head(torch.autograd.Function):
         ctx.save_for_backward(dh)
         stats.order, stats.tok_loss, stats.entropy, stats.correct = \
             order, tok_loss, entropy, correct
+        if ctx.denom is not None:
+            return tok_loss.sum() / ctx.denom
         return tok_loss.sum() * scale
 
     @staticmethod
     def backward(ctx, grad):
         (dh,) = ctx.saved_tensors
-        return dh * grad, None, None, None, None, None, None, None
+        g = grad if ctx.denom is None else grad / ctx.denom
+        return dh * g, None, None, None, None, None, None, None
 
 # ---------------------------------------------------------------------------------------------
 # The model
@@ -731,12 +792,16 @@ class FusedQwen2:
         sup = sorted({max(1, (c * f) // 4) for c in counts for f in (2, 3)})
         return t + G.tune(shapes[-1:], sup, self.device, log=log)
 
-    def step(self, input_ids, attention_mask, labels, denom, lengths=None, n_supervised=None):
+    def step(self, input_ids, attention_mask, labels, denom, lengths=None, n_supervised=None,
+             padded=False, ctr_base=None):
         """The step's forward: (loss, packed, stats); autograd runs the backward. `lengths`
         and `n_supervised`: the batch's row lengths and supervised-token count when the caller
-        has them on the host (then the step reads nothing back from the device)."""
+        has them on the host (then the step reads nothing back from the device). `padded`:
+        device-only packing (Packed); `denom` may then be a device scalar and `ctr_base` the
+        device int64 of the step's first dropout counter (StepGraph passes both)."""
         packed = Packed(input_ids, attention_mask, labels, self.rope, self.dropout,
-                        self.dropout_p, lengths=lengths, n_supervised=n_supervised)
+                        self.dropout_p, lengths=lengths, n_supervised=n_supervised,
+                        padded=padded, ctr_base=ctr_base)
         if self.autotune:
             shapes = self.gemm_shapes()
             G.tune(shapes, [packed.n], self.device)
@@ -763,3 +828,85 @@ class FusedQwen2:
         loss = _Head.apply(h, self.norm_w, self.eps, self.lm_w, packed, denom, stats,
                            self.HEAD_CHUNK)
         return loss, packed, stats
+
+
+class StepGraph:
+    """One training step of a FusedQwen2 (forward and backward, device-only packing) captured
+    as a HIP graph for batches of one [rows, T] shape, and replayed with each new batch copied
+    into the graph's input buffers: one launch of the graph instead of about a thousand kernel
+    launches from Python (the reference's packing, engine.py:705-751, reads the lengths back
+    from the device, which no graph can hold).
+
+    What changes between steps reaches the graph through device memory: the batch (ids, mask,
+    labels), the loss denominator and the loss scale (GradScaler's) as device scalars, and the
+    step's first dropout counter (the generator's offset when the step runs, as an eager step
+    would draw it; after a replay the generator moves on by the step's draws). The LoRA
+    parameters' .grad are the graph's own tensors, overwritten by every replay with the step's
+    gradient of loss * scale. Which layers keep their intermediates is decided at capture
+    (model.keep_all; None follows the memory plan as it stands then). The LoRA weights are read
+    from the fp32 parameters at every replay (the step's fp16 refresh is captured)."""
+
+    def __init__(self, model, rows, T, warmup=2):
+        dev = model.device
+        self.model, self.rows, self.T = model, rows, T
+        self.ids = torch.zeros((rows, T), device=dev, dtype=torch.int64)
+        self.mask = torch.ones((rows, T), device=dev, dtype=torch.int64)
+        self.labels = torch.zeros((rows, T), device=dev, dtype=torch.int64)
+        self.denom = torch.ones((), device=dev, dtype=torch.float32)
+        self.scale = torch.ones((), device=dev, dtype=torch.float32)
+        self.ctr = torch.zeros((1,), device=dev, dtype=torch.int64)
+        drop = model.dropout
+        self.seed = _as_int64(drop.gen.initial_seed()) if drop is not None else None
+        params = model.parameters()
+        for p in params:
+            p.grad = None
+        # eager runs first, on a side stream: the GEMM choices for rows * T tokens, the dropout
+        # self-check, the libraries' workspaces, the attention's second stream and the caching
+        # allocator's blocks are then in place, and the capture only records launches
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            for _ in range(warmup):
+                self._run()
+                for p in params:
+                    p.grad = None
+        torch.cuda.current_stream(dev).wait_stream(side)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.loss, self.packed, self.stats = self._run()
+        self.grads = [p.grad for p in params]
+        self.advance = self.packed.drawn
+
+    def _run(self):
+        base = self.ctr if self.model.dropout is not None else None
+        loss, packed, stats = self.model.step(self.ids, self.mask, self.labels, self.denom,
+                                              padded=True, ctr_base=base)
+        (loss * self.scale).backward()
+        return loss, packed, stats
+
+    def replay(self, input_ids, attention_mask, labels, denom, scale=1.0):
+        """Runs the captured step on this batch ([rows, T] as captured; denom and scale host
+        numbers or device scalars) and returns the loss, a device scalar the next replay
+        overwrites; the parameters' .grad then hold this step's gradient of loss * scale, and
+        self.stats / self.packed its per-token statistics and packing."""
+        if tuple(input_ids.shape) != (self.rows, self.T):
+            raise ValueError(f"the graph takes [{self.rows}, {self.T}] batches")
+        self.ids.copy_(input_ids)
+        self.mask.copy_(attention_mask)
+        self.labels.copy_(labels)
+        for dst, v in ((self.denom, denom), (self.scale, scale)):
+            if isinstance(v, torch.Tensor):
+                dst.copy_(v.reshape(()))
+            else:
+                dst.fill_(float(v))
+        drop = self.model.dropout
+        if drop is not None:
+            if _as_int64(drop.gen.initial_seed()) != self.seed:
+                raise RuntimeError("the dropout generator was reseeded after the capture")
+            offset = drop.gen.get_offset()
+            self.ctr.fill_(offset // 4)
+            drop.gen.set_offset(offset + self.advance)
+        self.graph.replay()
+        for p, g in zip(self.model.parameters(), self.grads):
+            p.grad = g
+        return self.loss

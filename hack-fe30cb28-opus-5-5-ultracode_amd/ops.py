@@ -449,6 +449,18 @@ def _keep_arg(keep, n, H, dev):
     return _ptr(keep)
 
 
+def _ctr_base(packed, dev):
+    """Device pointer of the step's first dropout counter when the batch keeps it on the device
+    (its masks' counters are then relative to it), else None."""
+    base = getattr(packed, "ctr_base", None)
+    if base is None:
+        return None
+    _need(base, "packed.ctr_base", torch.int64, dev)
+    if base.numel() != 1:
+        raise ValueError("packed.ctr_base must hold one int64")
+    return _ptr(base)
+
+
 def _rms_fwd(spec, x, weight, packed, *, delta=None, write_y=True, seeds=(0, 0),
              drop_q=False, drop_v=False, keep=None):
     """[x += delta] + RMSNorm -> (xsum, y fp16, yq, yv, rstd) (engine.py:947-966). With keep
@@ -480,7 +492,7 @@ def _rms_fwd(spec, x, weight, packed, *, delta=None, write_y=True, seeds=(0, 0),
                   _ptr(rstd), _ptr(tok) if (drop_q or drop_v) else None, n, H,
                   float(spec.eps), p_keep, keep_scale, int(seed), int(ctr_q), int(ctr_v),
                   int(threads), int(delta is not None), int(write_y), int(drop_q), int(drop_v),
-                  int(vec), keep_p, _stream(dev))
+                  int(vec), keep_p, _ctr_base(packed, dev), _stream(dev))
     return xsum, y, yq, yv, rstd
 
 
@@ -522,7 +534,7 @@ def _rms_bwd(spec, dy, x, rstd, weight, packed, *, dres=None, tq=None, tv=None, 
                   _ptr(tok) if (tq is not None or tv is not None) else None, n, H, dy_stride,
                   p_keep, keep_scale, int(seed), int(ctr_q), int(ctr_v), int(threads),
                   float(grad_scale), int(tq is not None), int(tv is not None),
-                  int(dres is not None), int(vec), keep_p, _stream(dev))
+                  int(dres is not None), int(vec), keep_p, _ctr_base(packed, dev), _stream(dev))
     return dx
 
 

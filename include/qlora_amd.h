@@ -96,12 +96,16 @@ int qlora_dropout_keep(int8_t* out, int64_t nelem, int64_t seed, int64_t ctr, in
  *   keep (may be null) u8 [n][2][ceil(H/4)]: with dropout, the masks stored as bits (bit k of
  *   byte j of mask m = element 4j+k kept; m = 0 for yq, 1 for yv) for qlora_rms_bwd to read
  *   instead of drawing them again (no reference counterpart: the reference draws them twice).
+ *   ctr_base (may be null) i64 [1] on the device: added to ctr_q and ctr_v (a step captured in
+ *   a HIP graph passes its counters relative to the step's first, kept there; no reference
+ *   counterpart).
  */
 int qlora_rms_fwd(const float* x, const void* delta, const void* w, int32_t w_half, float* xsum,
                   void* y, void* yq, void* yv, float* rstd, const int64_t* tok, int64_t n,
                   int64_t H, float eps, float p_keep, float keep_scale, int64_t seed,
                   int64_t ctr_q, int64_t ctr_v, int64_t G, int32_t has_delta, int32_t write_y,
-                  int32_t drop_q, int32_t drop_v, int32_t vec, uint8_t* keep, void* stream);
+                  int32_t drop_q, int32_t drop_v, int32_t vec, uint8_t* keep,
+                  const int64_t* ctr_base, void* stream);
 
 /*
  * RMSNorm backward: g = w * (dy + keep_q * tq * keep_scale + keep_v * tv * keep_scale),
@@ -112,13 +116,14 @@ int qlora_rms_fwd(const float* x, const void* delta, const void* w, int32_t w_ha
  *   (engine.py:1238 and 1301 round the gradient to fp16 before it).
  *   keep (may be null) u8 [n][2][ceil(H/4)]: the masks qlora_rms_fwd stored for these rows
  *   (same tok, seed, counters and drop_q/drop_v); null: drawn again from (seed, ctr_q, ctr_v).
+ *   ctr_base (may be null): as qlora_rms_fwd's.
  */
 int qlora_rms_bwd(const void* dy, const void* tq, const void* tv, const float* x,
                   const float* rstd, const void* w, int32_t w_half, const float* dres, float* dx,
-                  void* dx16, const int64_t* tok, int64_t n, int64_t H, int64_t dy_stride, float p_keep,
-                  float keep_scale, int64_t seed, int64_t ctr_q, int64_t ctr_v, int64_t G,
-                  float grad_scale, int32_t drop_q, int32_t drop_v, int32_t has_res,
-                  int32_t vec, const uint8_t* keep, void* stream);
+                  void* dx16, const int64_t* tok, int64_t n, int64_t H, int64_t dy_stride,
+                  float p_keep, float keep_scale, int64_t seed, int64_t ctr_q, int64_t ctr_v,
+                  int64_t G, float grad_scale, int32_t drop_q, int32_t drop_v, int32_t has_res,
+                  int32_t vec, const uint8_t* keep, const int64_t* ctr_base, void* stream);
 
 /*
  * qkv split + LoRA deltas + rotate-half RoPE. q = f16(rope(qkv_q + s*lq)),

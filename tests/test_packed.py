@@ -99,3 +99,45 @@ def test_scaled_rotary_embedding_is_refused(scaling):
     causal = NS(model=NS(layers=[layer]), config=cfg)
     with pytest.raises(E.UnsupportedModel, match="rotary"):
         E.from_peft(NS(get_base_model=lambda: causal))
+
+
+@pytest.mark.parametrize("lengths,T", [([5, 9, 1, 9], 9), ([3, 0, 7], 8), ([16], 16)])
+def test_padded_packing_keeps_the_real_tokens(lengths, T):
+    """Device-only packing (padded=True): every row is a sequence of T tokens; at each real
+    token the ids, position and next-token target equal the unpadded packing's, the padding
+    tokens take no target, the supervised rows come first in the same order, and nothing in it
+    depends on a read of the device (n, max_len and cu_seqlens follow from [B, T])."""
+    ids, mask, labels = _batch(lengths, T, 7 + sum(lengths))
+    a = _packed(ids, mask, labels)
+    p = _packed(ids, mask, labels, padded=True)
+    B = len(lengths)
+    assert p.n == B * T and p.max_len == T and p.lengths == [T] * B
+    assert p.cu_seqlens.tolist() == p.cu_seqlens_host == [T * r for r in range(B + 1)]
+    assert torch.equal(p.tok, torch.arange(B * T)) and torch.equal(p.ids, ids.reshape(-1))
+    assert torch.equal(p.pos.long(), torch.arange(B * T) % T)
+    # the real tokens: same target as the unpadded packing; padding: none
+    assert torch.equal(p.targets.index_select(0, a.tok), a.targets)
+    real = mask.reshape(-1).bool()
+    assert bool((p.targets[~real] == -100).all())
+    # supervised first, in packed order: the same rows as the unpadded head order
+    n_sup = a.n_supervised
+    assert torch.equal(p.tok[p.head_order[:n_sup]], a.tok[a.head_order[:n_sup]])
+    assert bool((p.targets[p.head_order[n_sup:]] < 0).all())
+    assert p.n_supervised == B * T and bool(p.metadata_ok)
+    assert p.ctr_base is None and p.drawn == 0
+
+
+def test_padded_packing_flags_left_padding_without_a_read():
+    ids, mask, labels = _batch([4, 6], 6, 1)
+    p = _packed(ids, mask.flip(1), labels, padded=True)  # no exception: nothing is read
+    assert not bool(p.metadata_ok)
+
+
+def test_device_counter_base_needs_padding():
+    ids, mask, labels = _batch([4, 6], 6, 2)
+    with pytest.raises(ValueError):
+        _packed(ids, mask, labels, ctr_base=torch.zeros(1, dtype=torch.int64))
+    p = _packed(ids, mask, labels, padded=True, ctr_base=torch.zeros(1, dtype=torch.int64))
+    assert p.ctr_base is not None
+    with pytest.raises(ValueError):
+        _packed(ids, mask, labels, padded=True, ctr_base=torch.zeros(2, dtype=torch.int64))
