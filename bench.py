@@ -177,7 +177,8 @@ def measure_step_kernels(pkg, trainer, batch, cfg):
     the attention forward / backward TFLOP/s on the batch's causal pairs (fwd: QK^T and PV, 4 D
     flops per pair and head; bwd: S, dP, dQ, dK, dV, 10 D flops per pair and head), and the
     library GEMMs' TFLOP/s (2 M N K a product): all of the step's projection and lm_head
-    products, and the gate|up forward alone (the largest MFMA kernel of the step)."""
+    products, and the gate|up forward alone (the largest MFMA kernel of the step), and the
+    package's own MFMA GEMM (the forward's gate|up with the SwiGLU epilogue)."""
     P = pkg.profiling
     pairs = causal_pairs(batch[5]["lengths"])
     heads, D = cfg.num_attention_heads, cfg.head_dim
@@ -187,8 +188,12 @@ def measure_step_kernels(pkg, trainer, batch, cfg):
     flops = lambda a: 2.0 * a[1] * a[2] * a[3]  # noqa: E731  (op, M, N, K, ...)
     gemms = [P.LaunchTimer(e, work=flops, bound="mfma")
              for e in ("qlora_gemm", "qlora_gemm_splitk", "qlora_gemmlt")]
+    # qlora_hgemm (a, lda, b, ldb, M, N, K, mode, ..., epi, swiglu_I, ...): N is the output's
+    # columns, I with the SwiGLU epilogue, whose product is [M, 2 I]
+    own = P.LaunchTimer("qlora_hgemm", bound="mfma",
+                        work=lambda a: 2.0 * a[4] * a[5] * a[6] * (2 if a[13] == 3 else 1))
     with contextlib.ExitStack() as stack:
-        for t in (dq, fwd, bwd, *gemms):
+        for t in (dq, fwd, bwd, *gemms, own):
             stack.enter_context(t)
         trainer.step(batch)
     torch.cuda.synchronize()
@@ -202,7 +207,12 @@ def measure_step_kernels(pkg, trainer, batch, cfg):
         out.append(dict(every, kernel="every library GEMM of the step (projections, lm_head)"))
     gu = gemms[0].summary(also=gemms[1:], select=lambda a: a[0] == 0 and a[2] == gate_up)
     if gu is not None:
-        out.append(dict(gu, kernel="gate|up forward GEMM (y = x W^T, N = 2 I)"))
+        out.append(dict(gu, kernel="gate|up forward GEMM of the library (the backward's recompute, "
+                                   "y = x W^T, N = 2 I)"))
+    mine = own.summary()
+    if mine is not None:
+        out.append(dict(mine, kernel="gate|up forward with the SwiGLU epilogue on this package's "
+                                     "MFMA GEMM (qlora_hgemm gemm_kernel, the forward pass)"))
     return dq.summary(), out
 
 
