@@ -5,6 +5,8 @@ Compiled in-tree, next to this file, so the library travels with the source tree
   -ffp-contract=off          no implicit FMA: the NF4 dequant must round the product
                              code2 * absmax2 before adding the offset, as bitsandbytes does
   -target-feature -packed-fp32-ops   no packed fp32 VALU instructions
+  -target-feature -fma-mix-insts      no v_fma_mix*: the NF4 decode's fp16(fp32(level * scale))
+                             rounds twice, as bitsandbytes; the mix form rounds once
 Linked against rocBLAS and hipBLASLt (the plain projection GEMMs, csrc/blas.hip, csrc/blaslt.hip).
 Usage: python -m <package>.build  (or build() from __graft_entry__)
 """
@@ -21,6 +23,7 @@ ARCH = "gfx950"
 FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-fPIC", "-shared", "-std=c++17", "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Xclang", "-target-feature", "-Xclang", "-fma-mix-insts",
     "-fvisibility=hidden", "-Wno-unused-command-line-argument",
 ]
 

@@ -50,6 +50,8 @@
 // reads and the A tiles are shared through the MALL.
 #include "nf4.h"
 
+#include <type_traits>
+
 namespace qlora {
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
@@ -173,9 +175,11 @@ __device__ __forceinline__ NF4Planes nf4_planes(float scale, const float* lv) {
   uint32_t d[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    float p0 = lv[2 * i] * scale, p1 = lv[2 * i + 1] * scale;
-    fp32_barrier(p0);  // the fp32 product, then one RNE rounding to fp16 (never an FMA-mix)
-    fp32_barrier(p1);
+    // the fp32 product, then one RNE rounding to fp16: the library is built without the
+    // v_fma_mix instructions, which would round the product to fp16 once (and an empty asm
+    // pinning the product would also keep the scheduler from spreading the decode over the
+    // MFMAs)
+    const float p0 = lv[2 * i] * scale, p1 = lv[2 * i + 1] * scale;
     typedef float f2 __attribute__((ext_vector_type(2)));
     typedef _Float16 h2 __attribute__((ext_vector_type(2)));
     d[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){p0, p1}, h2));
@@ -290,14 +294,15 @@ __device__ __forceinline__ void sched_step() {
 }
 
 // Half `part` (0, 1) of the decode of one half-block (32 values, codes `v`) with scale `sc` into
-// the B stage: part 0 forms the byte planes and words 0-1, part 1 words 2-3. NT: LDS row `row`,
-// chunks 0-3; NN: row `row`, chunks chunk0 .. chunk0+3.
-template <bool NN>
+// the B stage: part 0 forms the byte planes (unless the planes of the block's other half are
+// still in `t`: FRESH false) and words 0-1, part 1 words 2-3. NT: LDS row `row`, chunks 0-3;
+// NN: row `row`, chunks chunk0 .. chunk0+3.
+template <bool NN, bool FRESH = true>
 __device__ __forceinline__ void nf4_decode_part(const uint4& v, float sc, NF4Planes& t,
                                                 uint16_t* sb, int row, int chunk0,
                                                 const float* lv, int part) {
   const uint32_t wds[4] = {v.x, v.y, v.z, v.w};
-  if (part == 0) t = nf4_planes(sc, lv);
+  if (part == 0 && FRESH) t = nf4_planes(sc, lv);
 #pragma unroll
   for (int c = 2 * part; c < 2 * part + 2; ++c) {
     const int off = NN ? nmaj_off(row, chunk0 + c) : kmaj_off(row, c);
@@ -456,14 +461,19 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
   constexpr bool kT = EPI == kEpiStore || EPI == kEpiBias || EPI == kEpiSwiglu;
   Frags f0, f1;
   read_frags<NN>(f0, sA0, sB0, 0, wm, wn, lane);
+  // NT: a 64-value block spans k-tiles 2j and 2j + 1 of one W row (the rows start on a block:
+  // Kr % 128 == 0), so the odd k-tile's decode reuses the even one's byte planes (`fresh`
+  // false); the k-tile decoded is t + 2, even for the first and third of a trip's four
   auto k_tile = [&](int64_t t, uint16_t* sa, uint16_t* sb, uint16_t* sa_next, uint16_t* sb_next,
                     uint16_t* sa_pre, uint16_t* sb_pre, uint16_t* sb_dec, uint8_t* c_load,
                     float* s_load, const uint8_t* c_read, const float* s_read,
-                    const uint4& c_dec, const float& s_dec, uint4& c_next, float& s_next) {
+                    const uint4& c_dec, const float& s_dec, uint4& c_next, float& s_next,
+                    auto fresh) {
     __builtin_amdgcn_sched_barrier(0);
     read_frags<NN>(f1, sa, sb, 1, wm, wn, lane);
     if constexpr (BSRC == kBNF4)
-      nf4_decode_part<NN>(c_dec, s_dec, planes, sb_dec, b_row, b_chunk0, lv, 0);
+      nf4_decode_part<NN, NN || decltype(fresh)::value>(c_dec, s_dec, planes, sb_dec, b_row,
+                                                        b_chunk0, lv, 0);
     mfma_step<kT>(acc, f0);
     sched_step<NN, kValu, 0>();
     __builtin_amdgcn_sched_barrier(0);
@@ -483,10 +493,12 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
     __builtin_amdgcn_sched_barrier(0);
   };
   for (int64_t t = kt0; t < kt1; t += 4) {
-    k_tile(t, sA0, sB0, sA1, sB1, sA3, sB3, sB2, sC1, sS1, sC3, sS3, cx, sx, cy, sy);
-    k_tile(t + 1, sA1, sB1, sA2, sB2, sA0, sB0, sB3, sC2, sS2, sC0, sS0, cy, sy, cx, sx);
-    k_tile(t + 2, sA2, sB2, sA3, sB3, sA1, sB1, sB0, sC3, sS3, sC1, sS1, cx, sx, cy, sy);
-    k_tile(t + 3, sA3, sB3, sA0, sB0, sA2, sB2, sB1, sC0, sS0, sC2, sS2, cy, sy, cx, sx);
+    const std::true_type even;
+    const std::false_type odd;
+    k_tile(t, sA0, sB0, sA1, sB1, sA3, sB3, sB2, sC1, sS1, sC3, sS3, cx, sx, cy, sy, even);
+    k_tile(t + 1, sA1, sB1, sA2, sB2, sA0, sB0, sB3, sC2, sS2, sC0, sS0, cy, sy, cx, sx, odd);
+    k_tile(t + 2, sA2, sB2, sA3, sB3, sA1, sB1, sB0, sC3, sS3, sC1, sS1, cx, sx, cy, sy, even);
+    k_tile(t + 3, sA3, sB3, sA0, sB0, sA2, sB2, sB1, sC0, sS0, sC2, sS2, cy, sy, cx, sx, odd);
   }
   __builtin_amdgcn_s_waitcnt(0);  // the prefetches past the end: nothing left in flight
 
