@@ -35,8 +35,8 @@ SIGNATURES = {
     "qlora_ce_finish": [P, P, P, P, P, P, P, P, P, P, I64, I64, I64, P],
     "qlora_ce_grad": [P, I64, P, P, I64, I64, I64, P],
     "qlora_nf4_block_scales": [P, P, P, P, I32, I32, I64, I64, I64, P, P],
-    "qlora_nf4_gemm": [P, I64, P, P, P, I32, I64, I64, P, I64, P, P, I64, I64, I32, I32, I64,
-                       I32, P, I64, P],
+    "qlora_nf4_gemm": [P, I64, P, P, P, I32, I32, I64, I64, P, I64, P, P, I64, I64, I32, I32,
+                       I64, I32, P, I64, P],
     "qlora_hgemm": [P, I64, P, I64, I64, I64, I64, I32, P, I64, P, P, I64, I32, I64, I32, P, I64,
                     P],
     "qlora_resid_add": [P, P, P, I64, P],

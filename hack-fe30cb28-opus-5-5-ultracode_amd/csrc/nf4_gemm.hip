@@ -75,6 +75,7 @@ struct GemmArgs {
   const uint8_t* w_packed;  // codes, two per byte (element 2j in the high nibble of byte j)
   const float* w_scales;    // fp32 scale of each block
   const float* w_code;      // the 16 levels, or null for the NF4 table
+  int w_tiled;              // NT: codes and scales in the tile-major order (qlora_nf4_gemm)
   int64_t Kw;
   void* c;               // fp16 [M, ldc]; fp32 for kEpiResid; fp32 [splits, M, N] partials
   int64_t ldc;
@@ -155,14 +156,14 @@ struct DmaN {
 // ---- NF4 block decode -------------------------------------------------------------------------
 // NF4 B by DMA: the codes of a thread's half-block of a k-tile (16 bytes, 32 values) and its
 // block's fp32 scale go into slot `tid` of a codes stage and a scales stage (wavefront w's lanes
-// fill slots 64 w .. 64 w + 63, the same wavefront's threads read them). `e`: the half-block's
-// first element in W.
-__device__ __forceinline__ void nf4_issue(const GemmArgs& g, int64_t e, uint8_t* codes,
-                                          float* scales, int wave) {
-  __builtin_amdgcn_global_load_lds(g.w_packed + (e >> 1), (lds_void_t*)(codes + 1024 * wave), 16,
+// fill slots 64 w .. 64 w + 63, the same wavefront's threads read them). `code_off`: the
+// half-block's first byte in the codes, `scale_idx`: its block's scale.
+__device__ __forceinline__ void nf4_issue(const GemmArgs& g, int64_t code_off, int64_t scale_idx,
+                                          uint8_t* codes, float* scales, int wave) {
+  __builtin_amdgcn_global_load_lds(g.w_packed + code_off, (lds_void_t*)(codes + 1024 * wave), 16,
                                    0, 0);
-  __builtin_amdgcn_global_load_lds(g.w_scales + (e >> 6), (lds_void_t*)(scales + 64 * wave), 4, 0,
-                                   0);
+  __builtin_amdgcn_global_load_lds(g.w_scales + scale_idx, (lds_void_t*)(scales + 64 * wave), 4,
+                                   0, 0);
 }
 
 // The block's 16 values fp16(fp32(level[c] * scale)) as byte planes: lo[p] holds the low bytes
@@ -375,24 +376,44 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
     }
   }
 
-  // NF4: levels in registers; this thread's half-block at k-tile kt is element e_base + kt *
-  // e_step, decoded into row b_row from chunk b_chunk0 (NT: row tid; NN: row tid / 8, chunks
-  // 4 (tid % 8) ..)
+  // NF4: levels in registers; this thread's half-block of k-tile kt (decoded into row b_row
+  // from chunk b_chunk0; NT: row tid; NN: row tid / 8, chunks 4 (tid % 8) ..) has its codes at
+  // byte c_base + kt c_step and its scale at s_base + (kt >> s_shift) s_step. Row-major codes
+  // (bitsandbytes' order): NT one W row, 16 bytes a k-tile, a scale per two k-tiles; NN a
+  // quarter of a W row, 32 rows down a k-tile. Tile-major codes (NT): each k-tile's 256 rows
+  // of a tile are 4 KB in a row and their scales 1 KB, so one DMA instruction reads 1 KB in a
+  // row instead of 16 bytes from each of 64 W rows.
   float lv[16];
-  int64_t e_base = 0, e_step = 0;
+  int64_t c_base = 0, c_step = 0, s_base = 0, s_step = 0;
+  int s_shift = 0;
   int b_row = 0, b_chunk0 = 0;
   if constexpr (BSRC == kBNF4) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) lv[i] = g.w_code ? g.w_code[i] : kNF4Levels[i];
     if constexpr (!NN) {
       b_row = tid;
-      e_base = nt_wrow<EPI>(g, tile_n, tid) * g.Kw;
-      e_step = kBK;
+      s_shift = 1;
+      if (g.w_tiled) {
+        const int64_t kt_all = g.Kr / kBK;
+        c_base = (tile_n * kt_all * kThreads + tid) * 16;
+        c_step = kThreads * 16;
+        s_base = tile_n * (kt_all / 2) * kThreads + tid;
+        s_step = kThreads;
+      } else {
+        const int64_t e_base = nt_wrow<EPI>(g, tile_n, tid) * g.Kw;
+        c_base = e_base >> 1;
+        c_step = kBK / 2;
+        s_base = e_base >> 6;
+        s_step = 1;
+      }
     } else {
       b_row = tid >> 3;
       b_chunk0 = 4 * (tid & 7);
-      e_base = (int64_t)b_row * g.Kw + tile_n * kBN + 32 * (tid & 7);
-      e_step = (int64_t)kBK * g.Kw;
+      const int64_t e_base = (int64_t)b_row * g.Kw + tile_n * kBN + 32 * (tid & 7);
+      c_base = e_base >> 1;
+      c_step = (int64_t)kBK * g.Kw / 2;
+      s_base = e_base >> 6;
+      s_step = (int64_t)kBK * g.Kw / 64;
     }
   }
   // vector-memory instructions one k-tile issues (its DMA; NF4: the A DMA, codes and scales)
@@ -423,12 +444,15 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
   NF4Planes planes;
   uint4 cx{}, cy{};  // codes of the half-block decoded at the even / odd k-tiles of a trip
   float sx = 0.0f, sy = 0.0f;
-  auto nf4_at = [&](int64_t kt) { return e_base + clamp_kt(kt) * e_step; };
+  auto nf4_at = [&](int64_t kt, uint8_t* codes, float* scales) {
+    kt = clamp_kt(kt);
+    nf4_issue(g, c_base + kt * c_step, s_base + (kt >> s_shift) * s_step, codes, scales, wave);
+  };
   if constexpr (BSRC == kBNF4) {
-    nf4_issue(g, nf4_at(kt0), sC0, sS0, wave);
-    nf4_issue(g, nf4_at(kt0 + 1), sC1, sS1, wave);
-    nf4_issue(g, nf4_at(kt0 + 2), sC2, sS2, wave);
-    nf4_issue(g, nf4_at(kt0 + 3), sC3, sS3, wave);
+    nf4_at(kt0, sC0, sS0);
+    nf4_at(kt0 + 1, sC1, sS1);
+    nf4_at(kt0 + 2, sC2, sS2);
+    nf4_at(kt0 + 3, sC3, sS3);
     __builtin_amdgcn_s_waitcnt(0);  // (each thread reads the slots its own wavefront filled)
     const uint4 c0 = *reinterpret_cast<const uint4*>(sC0 + 16 * tid);
     const uint4 c1 = *reinterpret_cast<const uint4*>(sC1 + 16 * tid);
@@ -440,7 +464,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
     nf4_decode_part<NN>(c1, s1, planes, sB1, b_row, b_chunk0, lv, 0);
     nf4_decode_part<NN>(c1, s1, planes, sB1, b_row, b_chunk0, lv, 1);
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): stage 0 read before its next DMA
-    nf4_issue(g, nf4_at(kt0 + 4), sC0, sS0, wave);
+    nf4_at(kt0 + 4, sC0, sS0);
   }
   sync_tile<0>();
 
@@ -481,7 +505,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
     // the DMA of t + 3 into the stage t - 1 used (every wavefront's reads of it ended before
     // the barrier), spread over this k-step's MFMAs
     issue_tile(t + 3, sa_pre, sb_pre);
-    if constexpr (BSRC == kBNF4) nf4_issue(g, nf4_at(t + 5), c_load, s_load, wave);
+    if constexpr (BSRC == kBNF4) nf4_at(t + 5, c_load, s_load);
     read_frags<NN>(f0, sa_next, sb_next, 0, wm, wn, lane);
     if constexpr (BSRC == kBNF4) {
       nf4_decode_part<NN>(c_dec, s_dec, planes, sb_dec, b_row, b_chunk0, lv, 1);
@@ -725,20 +749,24 @@ QLORA_API int qlora_nf4_block_scales(const void* absmax, const float* code2,
 }
 
 // NF4-decode GEMM. W [w_rows, w_cols]: `packed` codes, `scales` the fp32 scale of each 64-value
-// block (qlora_nf4_block_scales), `code` the 16 levels or null for the NF4 table. mode: 0 = NT
-// (C = A W^T), 1 = NN (C = A W). epi: 0 store fp16, 1 + bias, 2 fp32 residual, 3 SwiGLU (NT
-// only). splits > 1: split-K through `ws` (fp32, splits M N).
+// block (qlora_nf4_block_scales), `code` the 16 levels or null for the NF4 table; tiled = 1
+// (NT only): both in the tile-major order (each 32-column k-tile of each 256-row tile, its rows
+// in the order the kernel's tile holds them, contiguous). mode: 0 = NT (C = A W^T), 1 = NN
+// (C = A W). epi: 0 store fp16, 1 + bias, 2 fp32 residual, 3 SwiGLU (NT only). splits > 1:
+// split-K through `ws` (fp32, splits M N).
 QLORA_API int qlora_nf4_gemm(const void* a, int64_t lda, const void* packed, const float* scales,
-                             const float* code, int32_t bs1, int64_t w_rows, int64_t w_cols,
-                             void* c, int64_t ldc, const void* bias, const float* resid,
-                             int64_t ldr, int64_t M, int32_t mode, int32_t epi, int64_t swiglu_I,
-                             int32_t splits, float* ws, int64_t ws_elems, void* stream) {
+                             const float* code, int32_t bs1, int32_t tiled, int64_t w_rows,
+                             int64_t w_cols, void* c, int64_t ldc, const void* bias,
+                             const float* resid, int64_t ldr, int64_t M, int32_t mode,
+                             int32_t epi, int64_t swiglu_I, int32_t splits, float* ws,
+                             int64_t ws_elems, void* stream) {
   QLORA_CHECK_ARG(M >= 0 && w_rows > 0 && w_cols > 0);
   if (M == 0) return 0;
   QLORA_CHECK_ARG(a && packed && scales && c && (mode == 0 || mode == 1));
   QLORA_CHECK_ARG(epi >= 0 && epi <= 3 && !(epi == 3 && mode != 0));
   QLORA_CHECK_ARG(splits >= 1 && splits <= 16 && !(splits > 1 && epi == 3));
   QLORA_CHECK_ARG(bs1 == 64);  // a thread's 32 values of a k-tile lie in one block
+  QLORA_CHECK_ARG(tiled == 0 || (tiled == 1 && mode == 0));
   QLORA_CHECK_ARG(epi != 1 || bias);
   QLORA_CHECK_ARG(epi != 2 || (resid && ldr >= 0));
   int64_t N, Kr;
@@ -753,6 +781,7 @@ QLORA_API int qlora_nf4_gemm(const void* a, int64_t lda, const void* packed, con
   g.w_packed = static_cast<const uint8_t*>(packed);
   g.w_scales = scales;
   g.w_code = code;
+  g.w_tiled = tiled;
   g.Kw = w_cols;
   g.c = c;
   g.ldc = ldc;

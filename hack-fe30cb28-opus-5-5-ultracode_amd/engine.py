@@ -73,6 +73,7 @@ class LayerSpec:
         self.qkv = NF4Group.of([self.w["q_proj"], self.w["k_proj"], self.w["v_proj"]])
         self.gu = NF4Group.of([self.w["gate_proj"], self.w["up_proj"]])
         self.nf4_all = [self.qkv, self.w["o_proj"], self.gu, self.w["down_proj"]]
+        self.nf4_nogu = [self.qkv, self.w["o_proj"], self.w["down_proj"]]
         self.bias_qkv = bias_qkv
         self.lora = lora  # {"q": (A, B, scaling), "v": (A, B, scaling)}
 
@@ -518,8 +519,10 @@ class _Layer(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, h, spec, packed, keep_all, aq_w, bq_w, av_w, bv_w):
-        with L.reuse_dequant() as weights:  # the layer's four weights in one dequant launch
-            L.dequant_layer(spec.nf4_all)
+        with L.reuse_dequant() as weights:  # the layer's weights in one dequant launch
+            # (a recomputing layer's gate|up product decodes its NF4 weight itself)
+            fused_gu = not keep_all and L.swiglu_fused_nf4()
+            L.dequant_layer(spec.nf4_nogu if fused_gu else spec.nf4_all)
             h3 = _Layer._forward(ctx, h, spec, packed, keep_all, aq_w, bq_w, av_w, bv_w)
         # a layer that keeps its intermediates may keep its dequantized weights as well, so
         # that its backward does not dequantize the same NF4 weights a second time

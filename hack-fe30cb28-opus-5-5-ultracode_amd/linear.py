@@ -15,7 +15,7 @@ GEMM with the fp16 weight (SWIGLU_EPILOGUE).
 import torch
 
 from . import _lib, gemm
-from .ops import NF4Group, _need, _ptr, _resid_add, _stream, dequant, dequant_many
+from .ops import NF4Group, _need, _ptr, _resid_add, _stream, dequant, dequant_many, gemm_tiles
 
 BACKEND = "dequant"
 
@@ -75,10 +75,14 @@ def _shape(w):
     return sum(x.shape[0] for x in ws), ws[0].shape[1]
 
 
-def _nf4_args(w):
-    """(packed, scales, code, bs1) of an NF4Weight or NF4Group, as qlora_nf4_gemm takes them
-    (code null for the NF4 table)."""
-    return (_ptr(w.packed), _ptr(w.block_scales()), None if w.standard else _ptr(w.code), w.bs1)
+def _nf4_args(w, tiled=False, swiglu_I=0):
+    """(packed, scales, code, bs1, tiled) of an NF4Weight or NF4Group, as qlora_nf4_gemm takes
+    them (code null for the NF4 table); tiled: the tile-major copy of codes and scales."""
+    if tiled:
+        codes, scales = gemm_tiles(w, swiglu_I)
+    else:
+        codes, scales = w.packed, w.block_scales()
+    return (_ptr(codes), _ptr(scales), None if w.standard else _ptr(w.code), w.bs1, int(tiled))
 
 
 TILE = 256  # output tile of the MFMA GEMM kernels (256 x 256; SwiGLU: 256 x 128 outputs)
@@ -128,10 +132,12 @@ def _a16(a):
     return a
 
 
-def nf4_gemm(a, w, mode, epi=0, bias=None, resid=None, out=None, swiglu_I=0, splits=None):
+def nf4_gemm(a, w, mode, epi=0, bias=None, resid=None, out=None, swiglu_I=0, splits=None,
+             tiled=True):
     """The fused NF4-decode GEMM (qlora_nf4_gemm). mode 0: A [M, K] x W^T; mode 1:
     A [M, N_w] x W. epi 0 fp16, 1 + bias, 2 fp32 residual (out = resid + fp16(acc)), 3 SwiGLU
-    of [gate | up] (mode 0)."""
+    of [gate | up] (mode 0). tiled (mode 0): read the weight's tile-major copy (formed on first
+    use) instead of the bitsandbytes order; the same results."""
     dev = a.device
     a = _a16(a)
     M = a.shape[0]
@@ -152,7 +158,9 @@ def nf4_gemm(a, w, mode, epi=0, bias=None, resid=None, out=None, swiglu_I=0, spl
     splits = split_k(M, n_out, kr, epi) if splits is None else splits
     ws = torch.empty((splits * M * n_out,), device=dev, dtype=torch.float32) if splits > 1 \
         else None
-    _lib.call("qlora_nf4_gemm", _ptr(a), a.stride(0), *_nf4_args(w), w_rows, w_cols, _ptr(out),
+    tiled = tiled and mode == 0
+    _lib.call("qlora_nf4_gemm", _ptr(a), a.stride(0),
+              *_nf4_args(w, tiled, swiglu_I if epi == 3 else 0), w_rows, w_cols, _ptr(out),
               out.stride(0), _ptr(bias), _ptr(resid), ldr, M, mode, epi, swiglu_I, splits,
               _ptr(ws), 0 if ws is None else ws.numel(), _stream(dev))
     return out
@@ -202,11 +210,21 @@ def nf4_linear(x, w, bias=None):
 # instead of the library GEMM and the SwiGLU kernel. Measured on MI355X, config 5, alternating
 # runs on one box: 34.38 / 34.52 ms per step against 34.49 / 34.41 ms for the library pair.
 SWIGLU_EPILOGUE = True
+# ... and with the NF4 weight decoded inside that GEMM (qlora_nf4_gemm over the weight's
+# tile-major copy): the forward then dequantizes the layer's other three weights only. Off: the
+# same alternating runs on one box gave 36.16 / 36.28 ms per step against 35.98 / 35.98 ms with
+# the fp16 weight (the in-kernel decode costs about as much as the dequant it saves).
+SWIGLU_NF4 = False
+
+
+def swiglu_fused_nf4():
+    """Whether the forward's gate|up product reads the NF4 weight itself (no fp16 copy)."""
+    return BACKEND == "fused" or (SWIGLU_EPILOGUE and SWIGLU_NF4)
 
 
 def nf4_linear_swiglu(x, w, I):
     """m = fp16(silu(g) * u) of [g | u] = X W^T for the stacked gate|up weight, fp16 [M, I]."""
-    if BACKEND == "fused":
+    if swiglu_fused_nf4():
         return nf4_gemm(x, w, 0, epi=3, swiglu_I=I)
     if SWIGLU_EPILOGUE:
         return hgemm(x, dequantize(w), 0, epi=3, swiglu_I=I)

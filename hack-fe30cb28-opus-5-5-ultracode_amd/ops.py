@@ -260,6 +260,45 @@ def _block_scales(w, offsets, seg1, seg2):
     return out
 
 
+GEMM_TILE = 256  # W rows per tile of the fused GEMM (qlora_nf4_gemm)
+
+
+def _gemm_tile_rows(w_rows, swiglu_I):
+    """The W row each position of the tile-major order holds (qlora_nf4_gemm, tiled): tile t's
+    row r is W row 256 t + r, or with the SwiGLU epilogue row j = 128 t + 64 (r // 128) + r % 64
+    of the gate (r % 128 < 64) or the up projection (I + j)."""
+    n = torch.arange(w_rows, dtype=torch.int64)
+    if not swiglu_I:
+        return n
+    t, r = n // GEMM_TILE, n % GEMM_TILE
+    j = t * 128 + (r // 128) * 64 + r % 64
+    return torch.where(r % 128 >= 64, swiglu_I + j, j)
+
+
+def gemm_tiles(w, swiglu_I=0):
+    """The codes and fp32 block scales of an NF4Weight / NF4Group in the fused GEMM's tile-major
+    order for y = x W^T (qlora_nf4_gemm, tiled = 1): formed once per weight and layout (the
+    weights are frozen) and kept on it; the same bytes as the bitsandbytes order, rearranged so
+    that each k-tile of a 256-row tile is 4 KB of codes and 1 KB of scales in a row."""
+    cache = w.__dict__.setdefault("_gemm_tiles", {})
+    if swiglu_I in cache:
+        return cache[swiglu_I]
+    rows, cols = w.shape
+    if rows % GEMM_TILE or cols % 64 or w.bs1 != 64:
+        raise ValueError("the tile-major order takes 256-row tiles of 64-value blocks")
+    if swiglu_I and 2 * swiglu_I != rows:
+        raise ValueError("the SwiGLU order takes [gate; up] with I rows each")
+    dev = w.packed.device
+    order = _gemm_tile_rows(rows, swiglu_I).to(dev)
+    tiles, kt = rows // GEMM_TILE, cols // 32
+    codes = w.packed.reshape(rows, cols // 2).index_select(0, order)
+    codes = codes.view(tiles, GEMM_TILE, kt, 16).permute(0, 2, 1, 3).contiguous().view(-1)
+    scales = w.block_scales().reshape(rows, cols // 64).index_select(0, order)
+    scales = scales.view(tiles, GEMM_TILE, cols // 64).permute(0, 2, 1).contiguous().view(-1)
+    cache[swiglu_I] = (codes, scales)
+    return cache[swiglu_I]
+
+
 def _dq_segs(w):
     return (w.seg1, w.seg2) if isinstance(w, NF4Group) else (_NO_SEG, _NO_SEG)
 

@@ -247,7 +247,11 @@ int qlora_nf4_block_scales(const void* absmax, const float* code2, const float* 
  * NF4 dequantisation fused into an fp16 MFMA GEMM (fp32 accumulation) with a frozen NF4 weight
  * W [w_rows, w_cols]: `packed` codes as qlora_nf4_dequant's, `scales` fp32 [w_rows*w_cols/64]
  * (qlora_nf4_block_scales), `code` the 16 levels (null: the NF4 table); 256 x 256 output tiles,
- * the NF4 blocks decoded into LDS inside the kernel:
+ * the NF4 blocks decoded into LDS inside the kernel. tiled = 1 (mode 0 only): codes and scales
+ * rearranged once into the tile-major order, element (tile t, row r, k) at codes byte
+ * ((t * w_cols/32 + k/32) * 256 + r) * 16 + (k%32)/2 and scale ((t * w_cols/64 + k/64) * 256 + r),
+ * where tile row r is W row 256 t + r (epi 3: W row j or I + j, j = 128 t + 64 (r/128) +
+ * r%64, the up row when r%128 >= 64); a DMA instruction then reads 1 KB in a row:
  *   mode 0 (NT): C[M, w_rows] = A[M, w_cols] W^T      mode 1 (NN): C[M, w_cols] = A[M, w_rows] W
  *   A f16 [M, lda].
  *   epi 0: C f16 = f16(acc);  epi 1: C f16 = f16(acc + bias[n]) (bias f16);
@@ -265,10 +269,10 @@ int qlora_nf4_block_scales(const void* absmax, const float* code2, const float* 
  * 16-byte aligned, scales 4-byte aligned; splits <= 16.
  */
 int qlora_nf4_gemm(const void* a, int64_t lda, const void* packed, const float* scales,
-                   const float* code, int32_t bs1, int64_t w_rows, int64_t w_cols, void* c,
-                   int64_t ldc, const void* bias, const float* resid, int64_t ldr, int64_t M,
-                   int32_t mode, int32_t epi, int64_t swiglu_I, int32_t splits, float* ws,
-                   int64_t ws_elems, void* stream);
+                   const float* code, int32_t bs1, int32_t tiled, int64_t w_rows, int64_t w_cols,
+                   void* c, int64_t ldc, const void* bias, const float* resid, int64_t ldr,
+                   int64_t M, int32_t mode, int32_t epi, int64_t swiglu_I, int32_t splits,
+                   float* ws, int64_t ws_elems, void* stream);
 
 /*
  * The same GEMM with an fp16 B operand in memory (the dequantized projections; the lm_head):

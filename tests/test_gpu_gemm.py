@@ -195,3 +195,34 @@ def test_lm_head_shapes(pkg):
     G = (torch.randn(300, 151936, generator=g, device=DEV) * 1e-3).half()
     dh = L.hgemm(G, E, 1)
     assert rel_err(dh, G.double() @ E.double()) < 1e-3
+
+
+@pytest.mark.parametrize("epi", [0, 1, 2, 3])
+def test_tile_major_order_equals_bnb_order(pkg, epi):
+    """The fused GEMM over the weight's tile-major copy of codes and scales (the order its DMA
+    reads in 1 KB runs) gives the results of the bitsandbytes order bit for bit: every NT
+    epilogue, split-K, a ragged M; and the copy holds the same bytes."""
+    L = pkg.linear
+    M = 700
+    if epi == 3:
+        w = _group(pkg, [(8960, 1536), (8960, 1536)], 21)
+        N = 8960
+    else:
+        w = _weight(pkg, (2048, 1536), 21)
+        N = 2048
+    g = torch.Generator(device=DEV).manual_seed(5)
+    x = (torch.randn(M, 1536, generator=g, device=DEV) * 0.5).half()
+    kw = {}
+    if epi == 1:
+        kw["bias"] = (torch.randn(N, generator=g, device=DEV) * 0.1).half()
+    if epi == 2:
+        kw["resid"] = torch.randn(M, N, generator=g, device=DEV)
+    if epi == 3:
+        kw["swiglu_I"] = 8960
+    for splits in ([1] if epi == 3 else [1, 2]):
+        a = L.nf4_gemm(x, w, 0, epi=epi, tiled=True, splits=splits, **kw)
+        b = L.nf4_gemm(x, w, 0, epi=epi, tiled=False, splits=splits, **kw)
+        assert torch.equal(a, b)
+    codes, scales = pkg.ops.gemm_tiles(w, kw.get("swiglu_I", 0))
+    assert torch.equal(torch.sort(codes).values, torch.sort(w.packed.reshape(-1)).values)
+    assert torch.equal(torch.sort(scales).values, torch.sort(w.block_scales()).values)
