@@ -142,7 +142,9 @@ def graph_leg(pkg, trainer, batches, count=8):
         tokens, rows = 0, 0
         for ids, mask, labels, denom, ntok in padded:
             if replay:
-                graphs[tuple(ids.shape)].replay(ids, mask, labels, denom, scaler._scale)
+                # GradScaler's scale as its device tensor (get_scale() would read it back)
+                scale = scaler._scale if scaler._scale is not None else scaler.get_scale()
+                graphs[tuple(ids.shape)].replay(ids, mask, labels, denom, scale)
             else:
                 loss, _, _ = model.step(ids, mask, labels, denom, padded=True)
                 scaler.scale(loss).backward()

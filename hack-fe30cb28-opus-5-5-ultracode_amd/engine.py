@@ -521,7 +521,7 @@ class _Layer(torch.autograd.Function):
     def forward(ctx, h, spec, packed, keep_all, aq_w, bq_w, av_w, bv_w):
         with L.reuse_dequant() as weights:  # the layer's weights in one dequant launch
             # (a recomputing layer's gate|up product decodes its NF4 weight itself)
-            fused_gu = not keep_all and L.swiglu_fused_nf4()
+            fused_gu = not keep_all and L.swiglu_fused_nf4() and L._gemm_fits(spec.I, spec.H)
             L.dequant_layer(spec.nf4_nogu if fused_gu else spec.nf4_all)
             h3 = _Layer._forward(ctx, h, spec, packed, keep_all, aq_w, bq_w, av_w, bv_w)
         # a layer that keeps its intermediates may keep its dequantized weights as well, so

@@ -222,11 +222,18 @@ def swiglu_fused_nf4():
     return BACKEND == "fused" or (SWIGLU_EPILOGUE and SWIGLU_NF4)
 
 
+def _gemm_fits(I, K):
+    """The package's GEMM takes the SwiGLU output in 128-column tiles and the reduction in
+    blocks of 128 (every Qwen2.5 size does: I = 4864 ... 29568, H = 896 ... 8192)."""
+    return I % 128 == 0 and K % 128 == 0
+
+
 def nf4_linear_swiglu(x, w, I):
     """m = fp16(silu(g) * u) of [g | u] = X W^T for the stacked gate|up weight, fp16 [M, I]."""
-    if swiglu_fused_nf4():
+    fits = _gemm_fits(I, x.shape[1])
+    if swiglu_fused_nf4() and fits:
         return nf4_gemm(x, w, 0, epi=3, swiglu_I=I)
-    if SWIGLU_EPILOGUE:
+    if SWIGLU_EPILOGUE and fits:
         return hgemm(x, dequantize(w), 0, epi=3, swiglu_I=I)
     from .ops import _glu_fwd
     return _glu_fwd(nf4_linear(x, w), I)
