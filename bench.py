@@ -178,9 +178,10 @@ def measure_step_kernels(pkg, trainer, batch, cfg):
     attention and the GEMM entry points: the dequant's achieved GB/s (dispatch-recorded events),
     the attention forward / backward TFLOP/s on the batch's causal pairs (fwd: QK^T and PV, 4 D
     flops per pair and head; bwd: S, dP, dQ, dK, dV, 10 D flops per pair and head), and the
-    library GEMMs' TFLOP/s (2 M N K a product): all of the step's projection and lm_head
-    products, and the gate|up forward alone (the largest MFMA kernel of the step), and the
-    package's own MFMA GEMM (the forward's gate|up with the SwiGLU epilogue)."""
+    library GEMMs' TFLOP/s (2 M N K a product): all of the step's library projection and lm_head
+    products, the library's gate|up forward if any, and the package's own MFMA GEMM (the
+    gate|up forward products: with the SwiGLU epilogue in the forward pass, [g | u] kept in the
+    recompute; the largest MFMA kernel of the step)."""
     P = pkg.profiling
     pairs = causal_pairs(batch[5]["lengths"])
     heads, D = cfg.num_attention_heads, cfg.head_dim
@@ -213,8 +214,9 @@ def measure_step_kernels(pkg, trainer, batch, cfg):
                                    "y = x W^T, N = 2 I)"))
     mine = own.summary()
     if mine is not None:
-        out.append(dict(mine, kernel="gate|up forward with the SwiGLU epilogue on this package's "
-                                     "MFMA GEMM (qlora_hgemm gemm_kernel, the forward pass)"))
+        out.append(dict(mine, kernel="gate|up forward products on this package's MFMA GEMM "
+                                     "(qlora_hgemm hgemm_kernel: the forward pass's with the "
+                                     "SwiGLU epilogue, the recompute's [g | u])"))
     return dq.summary(), out
 
 

@@ -6,20 +6,24 @@
 //   NT (forward):  C[m, n] = sum_k A[m, k] B[n, k]      B = W [N, K], K = reduction
 //   NN (backward): C[m, n] = sum_k A[m, k] B[k, n]      B = W [K, N], N = W's columns
 //
-// One workgroup = 4 wavefronts on a 256 x 256 output tile, k-tiles of 32; each wavefront owns a
-// 128 x 128 block as 4 x 4 v_mfma_f32_32x32x16_f16 accumulators (256 accumulation registers, one
-// wavefront per SIMD). On gfx950 a 128 x 128 wavefront block is what keeps the operand reads
+// One workgroup = 4 wavefronts on a 256 x 256 output tile; each wavefront owns a 128 x 128
+// block as 4 x 4 v_mfma_f32_32x32x16_f16 accumulators (256 accumulation registers, one
+// wavefront per SIMD). Two main loops share the tile, the MFMA order and the epilogues: the NF4
+// one (nf4_gemm_kernel, k-tiles of 32, four LDS stages, described below) and the fp16-B one
+// (hgemm_kernel, k-tiles of 64, two stages: every DMA lane group then fetches whole 128-byte
+// lines, which the L1 serves at twice the rate of 64-byte halves; described at the kernel). On gfx950 a 128 x 128 wavefront block is what keeps the operand reads
 // below the MFMA time: per 16-wide k-step a wavefront reads 2 x 128 x 16 fp16 from LDS for 16
 // MFMAs; smaller blocks make the kernel LDS-bound.
 //
-// Operand staging. The A tile (and an fp16 B tile) goes from global memory straight into LDS
+// Operand staging (NF4 kernel). The A tile goes from global memory straight into LDS
 // (global_load_lds_dwordx4: a wavefront instruction writes 1 KB of consecutive LDS, lane l at
 // 16 l), four stages, the loads of k-tile t + 3 issued in the middle of k-tile t and spread
 // over its MFMAs. The LDS layout is swizzled through the choice of which global 16-byte chunk a
 // lane fetches: in a K-contiguous tile [rows][32] (A; B in NT) chunk c of row r sits in slot
 // c ^ ((r >> 2) & 3), so a fragment read covers all banks; in an N-contiguous tile [32][256] (B
-// in NN) chunk c of row k sits in slot c ^ ((k & 3) << 2), the pattern under which
-// ds_read_b64_tr_b16 (4 rows x 16 columns per 16 lanes) is conflict-free. Every stage is its own
+// in NN; the decoded NF4 B is written the same way) chunk c of row k sits in slot
+// c ^ ((k & 3) << 2), the pattern under which ds_read_b64_tr_b16 (4 rows x 16 columns per 16
+// lanes) is conflict-free. Every stage is its own
 // __shared__ array and the loop is unrolled by four, so the compiler can tell which buffer a
 // read touches (an LDS read is otherwise held behind every outstanding LDS DMA); the waits are
 // explicit: one vmcnt + lgkmcnt(0) and one s_barrier per k-tile.
@@ -320,223 +324,22 @@ __device__ __forceinline__ void sync_tile() {
   __builtin_amdgcn_s_barrier();
 }
 
-template <bool NN, int BSRC, int EPI>
-__global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
-  __shared__ __attribute__((aligned(1024))) uint16_t sA0[kTile];
-  __shared__ __attribute__((aligned(1024))) uint16_t sA1[kTile];
-  __shared__ __attribute__((aligned(1024))) uint16_t sA2[kTile];
-  __shared__ __attribute__((aligned(1024))) uint16_t sA3[kTile];
-  __shared__ __attribute__((aligned(1024))) uint16_t sB0[kTile];
-  __shared__ __attribute__((aligned(1024))) uint16_t sB1[kTile];
-  __shared__ __attribute__((aligned(1024))) uint16_t sB2[kTile];
-  __shared__ __attribute__((aligned(1024))) uint16_t sB3[kTile];
-  // NF4 codes and scales, stage u % 4 for k-tile u (unused with an fp16 B)
-  __shared__ __attribute__((aligned(1024))) uint8_t sC0[kThreads * 16];
-  __shared__ __attribute__((aligned(1024))) uint8_t sC1[kThreads * 16];
-  __shared__ __attribute__((aligned(1024))) uint8_t sC2[kThreads * 16];
-  __shared__ __attribute__((aligned(1024))) uint8_t sC3[kThreads * 16];
-  __shared__ __attribute__((aligned(1024))) float sS0[kThreads];
-  __shared__ __attribute__((aligned(1024))) float sS1[kThreads];
-  __shared__ __attribute__((aligned(1024))) float sS2[kThreads];
-  __shared__ __attribute__((aligned(1024))) float sS3[kThreads];
-
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
-
-  const int64_t t_lin = tile_order(blockIdx.x, gridDim.x);
-  const int64_t tile_m = t_lin % g.m_tiles, tile_n = t_lin / g.m_tiles;
-  const int64_t m0 = tile_m * kBM;
-  const int64_t kt0 = (int64_t)blockIdx.z * g.kt_per_split;
-  int64_t kt1 = kt0 + g.kt_per_split;
-  if (kt1 > g.Kr / kBK) kt1 = g.Kr / kBK;  // k-tile counts are multiples of 4 (host check)
-  const int64_t kt_last = kt1 - 1;
-
-  DmaK dma_a;
-  const int64_t a_rows = g.M - m0;  // rows past M re-read the last row
-  dma_a.init(g.lda, [&](int r) -> int64_t { return r < a_rows ? r : a_rows - 1; }, wave, lane);
-  const uint16_t* a_base = g.a + m0 * g.lda;  // + k0 per k-tile
-  DmaK dma_bk;
-  DmaN dma_bn;
-  const uint16_t* b_base = nullptr;
-  int64_t b_step = 0;
-  if constexpr (BSRC == kBHalf) {
-    if constexpr (NN) {
-      dma_bn.init(g.ldb, wave, lane);
-      b_base = g.b + tile_n * kBN;
-      b_step = (int64_t)kBK * g.ldb;
-    } else {
-      // rows past N (a last, partial tile: the lm_head's 151,936) re-read row N - 1
-      dma_bk.init(g.ldb, [&](int r) -> int64_t {
-        const int64_t row = nt_wrow<EPI>(g, tile_n, r);
-        return (EPI == kEpiSwiglu || row < g.N) ? row : g.N - 1;
-      }, wave, lane);
-      b_base = g.b;
-      b_step = kBK;
-    }
-  }
-
-  // NF4: levels in registers; this thread's half-block of k-tile kt (decoded into row b_row
-  // from chunk b_chunk0; NT: row tid; NN: row tid / 8, chunks 4 (tid % 8) ..) has its codes at
-  // byte c_base + kt c_step and its scale at s_base + (kt >> s_shift) s_step. Row-major codes
-  // (bitsandbytes' order): NT one W row, 16 bytes a k-tile, a scale per two k-tiles; NN a
-  // quarter of a W row, 32 rows down a k-tile. Tile-major codes (NT): each k-tile's 256 rows
-  // of a tile are 4 KB in a row and their scales 1 KB, so one DMA instruction reads 1 KB in a
-  // row instead of 16 bytes from each of 64 W rows.
-  float lv[16];
-  int64_t c_base = 0, c_step = 0, s_base = 0, s_step = 0;
-  int s_shift = 0;
-  int b_row = 0, b_chunk0 = 0;
-  if constexpr (BSRC == kBNF4) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) lv[i] = g.w_code ? g.w_code[i] : kNF4Levels[i];
-    if constexpr (!NN) {
-      b_row = tid;
-      s_shift = 1;
-      if (g.w_tiled) {
-        const int64_t kt_all = g.Kr / kBK;
-        c_base = (tile_n * kt_all * kThreads + tid) * 16;
-        c_step = kThreads * 16;
-        s_base = tile_n * (kt_all / 2) * kThreads + tid;
-        s_step = kThreads;
-      } else {
-        const int64_t e_base = nt_wrow<EPI>(g, tile_n, tid) * g.Kw;
-        c_base = e_base >> 1;
-        c_step = kBK / 2;
-        s_base = e_base >> 6;
-        s_step = 1;
-      }
-    } else {
-      b_row = tid >> 3;
-      b_chunk0 = 4 * (tid & 7);
-      const int64_t e_base = (int64_t)b_row * g.Kw + tile_n * kBN + 32 * (tid & 7);
-      c_base = e_base >> 1;
-      c_step = (int64_t)kBK * g.Kw / 2;
-      s_base = e_base >> 6;
-      s_step = (int64_t)kBK * g.Kw / 64;
-    }
-  }
-  // vector-memory instructions one k-tile issues (its DMA; NF4: the A DMA, codes and scales)
-  constexpr int kVmPerTile = 4 + (BSRC == kBHalf ? 4 : 2);
-
-  f32x16 acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
-
-  auto clamp_kt = [&](int64_t kt) { return kt < kt1 ? kt : kt_last; };
-  auto issue_tile = [&](int64_t kt, uint16_t* sa, uint16_t* sb) {
-    kt = clamp_kt(kt);
-    dma_a.issue(a_base + kt * kBK, sa, wave);
-    if constexpr (BSRC == kBHalf) {
-      if constexpr (NN) dma_bn.issue(b_base + kt * b_step, sb, wave);
-      else dma_bk.issue(b_base + kt * b_step, sb, wave);
-    }
-  };
-
-  // prologue: k-tiles kt0 .. kt0+2 into stages 0-2. NF4: the codes and scales of kt0 .. kt0+3
-  // into their stages; kt0 and kt0+1 decoded into B stages 0 and 1, kt0+2's read into
-  // registers (decoded during kt0), then kt0+4's DMA into stage 0.
-  issue_tile(kt0, sA0, sB0);
-  issue_tile(kt0 + 1, sA1, sB1);
-  issue_tile(kt0 + 2, sA2, sB2);
-  NF4Planes planes;
-  uint4 cx{}, cy{};  // codes of the half-block decoded at the even / odd k-tiles of a trip
-  float sx = 0.0f, sy = 0.0f;
-  auto nf4_at = [&](int64_t kt, uint8_t* codes, float* scales) {
-    kt = clamp_kt(kt);
-    nf4_issue(g, c_base + kt * c_step, s_base + (kt >> s_shift) * s_step, codes, scales, wave);
-  };
-  if constexpr (BSRC == kBNF4) {
-    nf4_at(kt0, sC0, sS0);
-    nf4_at(kt0 + 1, sC1, sS1);
-    nf4_at(kt0 + 2, sC2, sS2);
-    nf4_at(kt0 + 3, sC3, sS3);
-    __builtin_amdgcn_s_waitcnt(0);  // (each thread reads the slots its own wavefront filled)
-    const uint4 c0 = *reinterpret_cast<const uint4*>(sC0 + 16 * tid);
-    const uint4 c1 = *reinterpret_cast<const uint4*>(sC1 + 16 * tid);
-    const float s0 = sS0[tid], s1 = sS1[tid];
-    cx = *reinterpret_cast<const uint4*>(sC2 + 16 * tid);
-    sx = sS2[tid];
-    nf4_decode_part<NN>(c0, s0, planes, sB0, b_row, b_chunk0, lv, 0);
-    nf4_decode_part<NN>(c0, s0, planes, sB0, b_row, b_chunk0, lv, 1);
-    nf4_decode_part<NN>(c1, s1, planes, sB1, b_row, b_chunk0, lv, 0);
-    nf4_decode_part<NN>(c1, s1, planes, sB1, b_row, b_chunk0, lv, 1);
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): stage 0 read before its next DMA
-    nf4_at(kt0 + 4, sC0, sS0);
-  }
-  sync_tile<0>();
-
-  // Software pipeline over four LDS stages, unrolled by four so every buffer is static (k-tile
-  // t on stage t % 4). After the barrier in the middle of k-tile t the DMA of t + 3 goes into
-  // the stage k-tile t - 1 used. NF4: k-tile t decodes t + 2 into its B stage across both
-  // k-steps (done by the barrier that ends t + 1) from codes read into registers during t - 1;
-  // after its barrier it issues the DMA of t + 5's codes and scales (stage (t + 1) % 4, read
-  // during t - 2) and reads t + 3's, which that barrier made complete: everything a k-tile
-  // issues has landed by the barrier of the k-tile after next. Every memory operand reaches the
-  // kernel through LDS, so the compiler's waits on loaded registers never drain the queue. Each
-  // k-step's 16 MFMAs run while the next k-step's fragments are read; the second k-step reads
-  // the first fragments of t + 1 after the barrier that makes t + 1 visible (the wait leaves
-  // the loads of t + 2 in flight). Past the last k-tile the prefetches re-read it into stages
-  // no longer read: a trip has no branch.
-  constexpr int kValu = BSRC == kBNF4 ? 5 : 0;
-  // fp16 outputs leave through LDS from transposed accumulators (mfma_step)
+// The epilogue of a 256 x 256 tile from the accumulators of mfma_step (4 wavefronts, 128 x 128
+// each; register layouts as mfma_step): fp16 outputs are staged through LDS (`lo`: the
+// wavefront's rows 0-63, `hi`: 64-127, [64][columns] each, free for this wavefront's use) and
+// leave as whole 16-byte row pieces; fp32 ones (split-K partials, the residual output) are
+// stored from the registers.
+template <int EPI>
+__device__ __forceinline__ void store_tile(const GemmArgs& g, f32x16 (&acc)[4][4], uint16_t* lo,
+                                           uint16_t* hi, int64_t m0, int64_t tile_n, int lane,
+                                           int wave) {
   constexpr bool kT = EPI == kEpiStore || EPI == kEpiBias || EPI == kEpiSwiglu;
-  Frags f0, f1;
-  read_frags<NN>(f0, sA0, sB0, 0, wm, wn, lane);
-  // NT: a 64-value block spans k-tiles 2j and 2j + 1 of one W row (the rows start on a block:
-  // Kr % 128 == 0), so the odd k-tile's decode reuses the even one's byte planes (`fresh`
-  // false); the k-tile decoded is t + 2, even for the first and third of a trip's four
-  auto k_tile = [&](int64_t t, uint16_t* sa, uint16_t* sb, uint16_t* sa_next, uint16_t* sb_next,
-                    uint16_t* sa_pre, uint16_t* sb_pre, uint16_t* sb_dec, uint8_t* c_load,
-                    float* s_load, const uint8_t* c_read, const float* s_read,
-                    const uint4& c_dec, const float& s_dec, uint4& c_next, float& s_next,
-                    auto fresh) {
-    __builtin_amdgcn_sched_barrier(0);
-    read_frags<NN>(f1, sa, sb, 1, wm, wn, lane);
-    if constexpr (BSRC == kBNF4)
-      nf4_decode_part<NN, NN || decltype(fresh)::value>(c_dec, s_dec, planes, sb_dec, b_row,
-                                                        b_chunk0, lv, 0);
-    mfma_step<kT>(acc, f0);
-    sched_step<NN, kValu, 0>();
-    __builtin_amdgcn_sched_barrier(0);
-    sync_tile<kVmPerTile>();  // k-tile t + 1 landed; t + 2 may still be in flight
-    // the DMA of t + 3 into the stage t - 1 used (every wavefront's reads of it ended before
-    // the barrier), spread over this k-step's MFMAs
-    issue_tile(t + 3, sa_pre, sb_pre);
-    if constexpr (BSRC == kBNF4) nf4_at(t + 5, c_load, s_load);
-    read_frags<NN>(f0, sa_next, sb_next, 0, wm, wn, lane);
-    if constexpr (BSRC == kBNF4) {
-      nf4_decode_part<NN>(c_dec, s_dec, planes, sb_dec, b_row, b_chunk0, lv, 1);
-      c_next = *reinterpret_cast<const uint4*>(c_read + 16 * tid);
-      s_next = s_read[tid];
-    }
-    mfma_step<kT>(acc, f1);
-    sched_step<NN, kValu, kVmPerTile>();
-    __builtin_amdgcn_sched_barrier(0);
-  };
-  for (int64_t t = kt0; t < kt1; t += 4) {
-    const std::true_type even;
-    const std::false_type odd;
-    k_tile(t, sA0, sB0, sA1, sB1, sA3, sB3, sB2, sC1, sS1, sC3, sS3, cx, sx, cy, sy, even);
-    k_tile(t + 1, sA1, sB1, sA2, sB2, sA0, sB0, sB3, sC2, sS2, sC0, sS0, cy, sy, cx, sx, odd);
-    k_tile(t + 2, sA2, sB2, sA3, sB3, sA1, sB1, sB0, sC3, sS3, sC1, sS1, cx, sx, cy, sy, even);
-    k_tile(t + 3, sA3, sB3, sA0, sB0, sA2, sB2, sB1, sC0, sS0, sC2, sS2, cy, sy, cx, sx, odd);
-  }
-  __builtin_amdgcn_s_waitcnt(0);  // the prefetches past the end: nothing left in flight
-
-  // epilogue (register layouts: mfma_step)
+  const int wm = wave >> 1, wn = wave & 1;
   const int col_in = lane & 31;
   if constexpr (kT) {
-    // fp16 outputs go through LDS: each wavefront writes its block there as fp16 (8-byte LDS
-    // stores of four columns, 16-byte chunks XOR-swizzled by row so the 32 rows of a store
-    // spread over the banks), then stores whole rows to memory with 16-byte stores. Stages are
-    // free once every wavefront is done.
-    __builtin_amdgcn_s_waitcnt(0);
-    __builtin_amdgcn_s_barrier();
-    uint16_t* lo = wave == 0 ? sA0 : wave == 1 ? sA2 : wave == 2 ? sB0 : sB2;
-    uint16_t* hi = wave == 0 ? sA1 : wave == 1 ? sA3 : wave == 2 ? sB1 : sB3;
+    // each wavefront writes its block to LDS as fp16 (8-byte LDS stores of four columns,
+    // 16-byte chunks XOR-swizzled by row so the 32 rows of a store spread over the banks), then
+    // stores whole rows to memory with 16-byte stores
     constexpr int kCols = EPI == kEpiSwiglu ? 64 : 128;   // output columns of a wavefront
     constexpr int kChunks = kCols / 8;
     // [128 rows][kCols] fp16: rows 0-63 in `lo`, 64-127 in `hi`
@@ -618,6 +421,383 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
   }
 }
 
+template <bool NN, int EPI>
+__global__ __launch_bounds__(kThreads, 1) void nf4_gemm_kernel(GemmArgs g) {
+  __shared__ __attribute__((aligned(1024))) uint16_t sA0[kTile];
+  __shared__ __attribute__((aligned(1024))) uint16_t sA1[kTile];
+  __shared__ __attribute__((aligned(1024))) uint16_t sA2[kTile];
+  __shared__ __attribute__((aligned(1024))) uint16_t sA3[kTile];
+  __shared__ __attribute__((aligned(1024))) uint16_t sB0[kTile];
+  __shared__ __attribute__((aligned(1024))) uint16_t sB1[kTile];
+  __shared__ __attribute__((aligned(1024))) uint16_t sB2[kTile];
+  __shared__ __attribute__((aligned(1024))) uint16_t sB3[kTile];
+  // NF4 codes and scales, stage u % 4 for k-tile u (unused with an fp16 B)
+  __shared__ __attribute__((aligned(1024))) uint8_t sC0[kThreads * 16];
+  __shared__ __attribute__((aligned(1024))) uint8_t sC1[kThreads * 16];
+  __shared__ __attribute__((aligned(1024))) uint8_t sC2[kThreads * 16];
+  __shared__ __attribute__((aligned(1024))) uint8_t sC3[kThreads * 16];
+  __shared__ __attribute__((aligned(1024))) float sS0[kThreads];
+  __shared__ __attribute__((aligned(1024))) float sS1[kThreads];
+  __shared__ __attribute__((aligned(1024))) float sS2[kThreads];
+  __shared__ __attribute__((aligned(1024))) float sS3[kThreads];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+
+  const int64_t t_lin = tile_order(blockIdx.x, gridDim.x);
+  const int64_t tile_m = t_lin % g.m_tiles, tile_n = t_lin / g.m_tiles;
+  const int64_t m0 = tile_m * kBM;
+  const int64_t kt0 = (int64_t)blockIdx.z * g.kt_per_split;
+  int64_t kt1 = kt0 + g.kt_per_split;
+  if (kt1 > g.Kr / kBK) kt1 = g.Kr / kBK;  // k-tile counts are multiples of 4 (host check)
+  const int64_t kt_last = kt1 - 1;
+
+  DmaK dma_a;
+  const int64_t a_rows = g.M - m0;  // rows past M re-read the last row
+  dma_a.init(g.lda, [&](int r) -> int64_t { return r < a_rows ? r : a_rows - 1; }, wave, lane);
+  const uint16_t* a_base = g.a + m0 * g.lda;  // + k0 per k-tile
+  // NF4: levels in registers; this thread's half-block of k-tile kt (decoded into row b_row
+  // from chunk b_chunk0; NT: row tid; NN: row tid / 8, chunks 4 (tid % 8) ..) has its codes at
+  // byte c_base + kt c_step and its scale at s_base + (kt >> s_shift) s_step. Row-major codes
+  // (bitsandbytes' order): NT one W row, 16 bytes a k-tile, a scale per two k-tiles; NN a
+  // quarter of a W row, 32 rows down a k-tile. Tile-major codes (NT): each k-tile's 256 rows
+  // of a tile are 4 KB in a row and their scales 1 KB, so one DMA instruction reads 1 KB in a
+  // row instead of 16 bytes from each of 64 W rows.
+  float lv[16];
+  int64_t c_base = 0, c_step = 0, s_base = 0, s_step = 0;
+  int s_shift = 0;
+  int b_row = 0, b_chunk0 = 0;
+  {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) lv[i] = g.w_code ? g.w_code[i] : kNF4Levels[i];
+    if constexpr (!NN) {
+      b_row = tid;
+      s_shift = 1;
+      if (g.w_tiled) {
+        const int64_t kt_all = g.Kr / kBK;
+        c_base = (tile_n * kt_all * kThreads + tid) * 16;
+        c_step = kThreads * 16;
+        s_base = tile_n * (kt_all / 2) * kThreads + tid;
+        s_step = kThreads;
+      } else {
+        const int64_t e_base = nt_wrow<EPI>(g, tile_n, tid) * g.Kw;
+        c_base = e_base >> 1;
+        c_step = kBK / 2;
+        s_base = e_base >> 6;
+        s_step = 1;
+      }
+    } else {
+      b_row = tid >> 3;
+      b_chunk0 = 4 * (tid & 7);
+      const int64_t e_base = (int64_t)b_row * g.Kw + tile_n * kBN + 32 * (tid & 7);
+      c_base = e_base >> 1;
+      c_step = (int64_t)kBK * g.Kw / 2;
+      s_base = e_base >> 6;
+      s_step = (int64_t)kBK * g.Kw / 64;
+    }
+  }
+  // vector-memory instructions one k-tile issues (the A DMA, codes and scales)
+  constexpr int kVmPerTile = 4 + 2;
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+
+  auto clamp_kt = [&](int64_t kt) { return kt < kt1 ? kt : kt_last; };
+  auto issue_tile = [&](int64_t kt, uint16_t* sa, uint16_t* sb) {
+    kt = clamp_kt(kt);
+    dma_a.issue(a_base + kt * kBK, sa, wave);
+  };
+
+  // prologue: k-tiles kt0 .. kt0+2 into stages 0-2. NF4: the codes and scales of kt0 .. kt0+3
+  // into their stages; kt0 and kt0+1 decoded into B stages 0 and 1, kt0+2's read into
+  // registers (decoded during kt0), then kt0+4's DMA into stage 0.
+  issue_tile(kt0, sA0, sB0);
+  issue_tile(kt0 + 1, sA1, sB1);
+  issue_tile(kt0 + 2, sA2, sB2);
+  NF4Planes planes;
+  uint4 cx{}, cy{};  // codes of the half-block decoded at the even / odd k-tiles of a trip
+  float sx = 0.0f, sy = 0.0f;
+  auto nf4_at = [&](int64_t kt, uint8_t* codes, float* scales) {
+    kt = clamp_kt(kt);
+    nf4_issue(g, c_base + kt * c_step, s_base + (kt >> s_shift) * s_step, codes, scales, wave);
+  };
+  {
+    nf4_at(kt0, sC0, sS0);
+    nf4_at(kt0 + 1, sC1, sS1);
+    nf4_at(kt0 + 2, sC2, sS2);
+    nf4_at(kt0 + 3, sC3, sS3);
+    __builtin_amdgcn_s_waitcnt(0);  // (each thread reads the slots its own wavefront filled)
+    const uint4 c0 = *reinterpret_cast<const uint4*>(sC0 + 16 * tid);
+    const uint4 c1 = *reinterpret_cast<const uint4*>(sC1 + 16 * tid);
+    const float s0 = sS0[tid], s1 = sS1[tid];
+    cx = *reinterpret_cast<const uint4*>(sC2 + 16 * tid);
+    sx = sS2[tid];
+    nf4_decode_part<NN>(c0, s0, planes, sB0, b_row, b_chunk0, lv, 0);
+    nf4_decode_part<NN>(c0, s0, planes, sB0, b_row, b_chunk0, lv, 1);
+    nf4_decode_part<NN>(c1, s1, planes, sB1, b_row, b_chunk0, lv, 0);
+    nf4_decode_part<NN>(c1, s1, planes, sB1, b_row, b_chunk0, lv, 1);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): stage 0 read before its next DMA
+    nf4_at(kt0 + 4, sC0, sS0);
+  }
+  sync_tile<0>();
+
+  // Software pipeline over four LDS stages, unrolled by four so every buffer is static (k-tile
+  // t on stage t % 4). After the barrier in the middle of k-tile t the DMA of t + 3 goes into
+  // the stage k-tile t - 1 used. NF4: k-tile t decodes t + 2 into its B stage across both
+  // k-steps (done by the barrier that ends t + 1) from codes read into registers during t - 1;
+  // after its barrier it issues the DMA of t + 5's codes and scales (stage (t + 1) % 4, read
+  // during t - 2) and reads t + 3's, which that barrier made complete: everything a k-tile
+  // issues has landed by the barrier of the k-tile after next. Every memory operand reaches the
+  // kernel through LDS, so the compiler's waits on loaded registers never drain the queue. Each
+  // k-step's 16 MFMAs run while the next k-step's fragments are read; the second k-step reads
+  // the first fragments of t + 1 after the barrier that makes t + 1 visible (the wait leaves
+  // the loads of t + 2 in flight). Past the last k-tile the prefetches re-read it into stages
+  // no longer read: a trip has no branch.
+  constexpr int kValu = 5;
+  // fp16 outputs leave through LDS from transposed accumulators (mfma_step)
+  constexpr bool kT = EPI == kEpiStore || EPI == kEpiBias || EPI == kEpiSwiglu;
+  Frags f0, f1;
+  read_frags<NN>(f0, sA0, sB0, 0, wm, wn, lane);
+  // NT: a 64-value block spans k-tiles 2j and 2j + 1 of one W row (the rows start on a block:
+  // Kr % 128 == 0), so the odd k-tile's decode reuses the even one's byte planes (`fresh`
+  // false); the k-tile decoded is t + 2, even for the first and third of a trip's four
+  auto k_tile = [&](int64_t t, uint16_t* sa, uint16_t* sb, uint16_t* sa_next, uint16_t* sb_next,
+                    uint16_t* sa_pre, uint16_t* sb_pre, uint16_t* sb_dec, uint8_t* c_load,
+                    float* s_load, const uint8_t* c_read, const float* s_read,
+                    const uint4& c_dec, const float& s_dec, uint4& c_next, float& s_next,
+                    auto fresh) {
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags<NN>(f1, sa, sb, 1, wm, wn, lane);
+    nf4_decode_part<NN, NN || decltype(fresh)::value>(c_dec, s_dec, planes, sb_dec, b_row,
+                                                      b_chunk0, lv, 0);
+    mfma_step<kT>(acc, f0);
+    sched_step<NN, kValu, 0>();
+    __builtin_amdgcn_sched_barrier(0);
+    sync_tile<kVmPerTile>();  // k-tile t + 1 landed; t + 2 may still be in flight
+    // the DMA of t + 3 into the stage t - 1 used (every wavefront's reads of it ended before
+    // the barrier), spread over this k-step's MFMAs
+    issue_tile(t + 3, sa_pre, sb_pre);
+    nf4_at(t + 5, c_load, s_load);
+    read_frags<NN>(f0, sa_next, sb_next, 0, wm, wn, lane);
+    nf4_decode_part<NN>(c_dec, s_dec, planes, sb_dec, b_row, b_chunk0, lv, 1);
+    c_next = *reinterpret_cast<const uint4*>(c_read + 16 * tid);
+    s_next = s_read[tid];
+    mfma_step<kT>(acc, f1);
+    sched_step<NN, kValu, kVmPerTile>();
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  for (int64_t t = kt0; t < kt1; t += 4) {
+    const std::true_type even;
+    const std::false_type odd;
+    k_tile(t, sA0, sB0, sA1, sB1, sA3, sB3, sB2, sC1, sS1, sC3, sS3, cx, sx, cy, sy, even);
+    k_tile(t + 1, sA1, sB1, sA2, sB2, sA0, sB0, sB3, sC2, sS2, sC0, sS0, cy, sy, cx, sx, odd);
+    k_tile(t + 2, sA2, sB2, sA3, sB3, sA1, sB1, sB0, sC3, sS3, sC1, sS1, cx, sx, cy, sy, even);
+    k_tile(t + 3, sA3, sB3, sA0, sB0, sA2, sB2, sB1, sC0, sS0, sC2, sS2, cy, sy, cx, sx, odd);
+  }
+  // the prefetches past the end: nothing left in flight; fp16 outputs go through the LDS
+  // stages, free once every wavefront is done with them
+  __builtin_amdgcn_s_waitcnt(0);
+  if constexpr (kT) __builtin_amdgcn_s_barrier();
+  store_tile<EPI>(g, acc, wave == 0 ? sA0 : wave == 1 ? sA2 : wave == 2 ? sB0 : sB2,
+                  wave == 0 ? sA1 : wave == 1 ? sA3 : wave == 2 ? sB1 : sB3, m0, tile_n, lane,
+                  wave);
+}
+
+
+// ---- fp16 B: 64-wide k-tiles ------------------------------------------------------------------
+// The vector L1 serves whole 128-byte lines at about twice the rate of 64-byte halves (measured
+// on MI355X: ~56 against ~29 bytes per clock per CU for global_load_lds_dwordx4 from L2): with
+// 64-wide k-tiles every K-contiguous row piece a DMA lane group fetches is a whole line. Two
+// 64 KB stages (A and B 32 KB each) fill 128 KB of LDS, so the loop runs one k-tile ahead; each
+// k-tile's 16 DMA instructions per wavefront are spread over three k-steps of the one before.
+constexpr int kBK64 = 64;
+constexpr int kTile64 = 256 * kBK64;  // halves per operand stage (32 KB)
+// of a k-tile's 16 DMA instructions: kSplitA issued during k-step 3 of the k-tile two before,
+// kSplitB during k-step 0 of the k-tile before and the rest during its k-step 1
+constexpr int kSplitA = 6, kSplitB = 5;
+
+// [rows][64]: chunk c of row r in slot c ^ ((r >> 1) & 7). A 16-lane group of a fragment read
+// takes 16 consecutive rows of one chunk: two rows per 256-byte bank cycle, eight slots.
+__device__ __forceinline__ int kmaj64_off(int row, int chunk) {
+  return row * 64 + ((chunk ^ ((row >> 1) & 7)) << 3);
+}
+
+// K-contiguous tile (256 rows x 64 halves): wavefront w loads rows 64w .. 64w+63, eight whole
+// 128-byte rows per instruction.
+struct DmaK64 {
+  uint32_t off[8];
+  template <typename RowOf>
+  __device__ __forceinline__ void init(int64_t ld, RowOf row_of, int wave, int lane) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int r = 64 * wave + 8 * j + (lane >> 3);
+      const int c = (lane & 7) ^ ((r >> 1) & 7);
+      off[j] = (uint32_t)((row_of(r) * ld + 8 * c) * 2);
+    }
+  }
+  __device__ __forceinline__ void issue(const uint16_t* base, uint16_t* dst, int wave,
+                                        int j) const {
+    __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(base) + off[j],
+                                     (lds_void_t*)(dst + (64 * wave + 8 * j) * 64), 16, 0, 0);
+  }
+};
+
+// N-contiguous tile (64 rows x 256 halves, nmaj_off): wavefront w loads rows 16w .. 16w+15,
+// two rows per instruction.
+struct DmaN64 {
+  uint32_t off[8];
+  __device__ __forceinline__ void init(int64_t ld, int wave, int lane) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int r = 16 * wave + 2 * j + (lane >> 5);
+      const int c = (lane & 31) ^ ((r & 3) << 2);
+      off[j] = (uint32_t)((r * ld + 8 * c) * 2);
+    }
+  }
+  __device__ __forceinline__ void issue(const uint16_t* base, uint16_t* dst, int wave,
+                                        int j) const {
+    __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(base) + off[j],
+                                     (lds_void_t*)(dst + (16 * wave + 2 * j) * 256), 16, 0, 0);
+  }
+};
+
+// read_frags for 64-wide stages: k-step s = 0..3
+template <bool NN>
+__device__ __forceinline__ void read_frags64(Frags& f, const uint16_t* sa, const uint16_t* sb,
+                                             int s, int wm, int wn, int lane) {
+  const int frow = lane & 31, fhalf = lane >> 5;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    f.a[i] = *reinterpret_cast<const half8_t*>(
+        sa + kmaj64_off(wm * 128 + 32 * i + frow, 2 * s + fhalf));
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if constexpr (!NN) {
+      f.b[j] = *reinterpret_cast<const half8_t*>(
+          sb + kmaj64_off(wn * 128 + 32 * j + frow, 2 * s + fhalf));
+    } else {
+      const int p = lane & 15;
+      const int col = wn * 128 + 32 * j + 16 * ((lane >> 4) & 1) + 4 * (p & 3);
+      const int k = 16 * s + 8 * fhalf + (p >> 2);
+      const int o0 = nmaj_off(k, col >> 3) + (col & 7);
+      const int o1 = nmaj_off(k + 4, col >> 3) + (col & 7);
+      const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)(sb + o0));
+      const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)(sb + o1));
+      f.b[j] = __builtin_bit_cast(half8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+    }
+  }
+}
+
+// The GEMM with an fp16 B in memory (qlora_hgemm): the same tile, wavefront blocks, MFMA order
+// and epilogues as nf4_gemm_kernel, so the results are the same bits as that kernel's for the
+// same B values (the k-steps of 16 are accumulated in the same order).
+template <bool NN, int EPI>
+__global__ __launch_bounds__(kThreads, 1) void hgemm_kernel(GemmArgs g) {
+  __shared__ __attribute__((aligned(1024))) uint16_t sA0[kTile64];
+  __shared__ __attribute__((aligned(1024))) uint16_t sA1[kTile64];
+  __shared__ __attribute__((aligned(1024))) uint16_t sB0[kTile64];
+  __shared__ __attribute__((aligned(1024))) uint16_t sB1[kTile64];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+
+  const int64_t t_lin = tile_order(blockIdx.x, gridDim.x);
+  const int64_t tile_m = t_lin % g.m_tiles, tile_n = t_lin / g.m_tiles;
+  const int64_t m0 = tile_m * kBM;
+  const int64_t kt0 = (int64_t)blockIdx.z * g.kt_per_split;
+  int64_t kt1 = kt0 + g.kt_per_split;
+  if (kt1 > g.Kr / kBK64) kt1 = g.Kr / kBK64;  // k-tile counts are even (host check)
+  const int64_t kt_last = kt1 - 1;
+
+  DmaK64 dma_a;
+  const int64_t a_rows = g.M - m0;  // rows past M re-read the last row
+  dma_a.init(g.lda, [&](int r) -> int64_t { return r < a_rows ? r : a_rows - 1; }, wave, lane);
+  const uint16_t* a_base = g.a + m0 * g.lda;  // + k0 per k-tile
+  DmaK64 dma_bk;
+  DmaN64 dma_bn;
+  const uint16_t* b_base;
+  int64_t b_step;
+  if constexpr (NN) {
+    dma_bn.init(g.ldb, wave, lane);
+    b_base = g.b + tile_n * kBN;
+    b_step = (int64_t)kBK64 * g.ldb;
+  } else {
+    // rows past N (a last, partial tile: the lm_head's 151,936) re-read row N - 1
+    dma_bk.init(g.ldb, [&](int r) -> int64_t {
+      const int64_t row = nt_wrow<EPI>(g, tile_n, r);
+      return (EPI == kEpiSwiglu || row < g.N) ? row : g.N - 1;
+    }, wave, lane);
+    b_base = g.b;
+    b_step = kBK64;
+  }
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+
+  // DMA instructions q0 .. q1 - 1 of k-tile kt (q even: A row group q / 2, odd: B's); past the
+  // last k-tile the last one is re-read into a stage no longer read
+  auto issue_part = [&](int64_t kt, uint16_t* sa, uint16_t* sb, int q0, int q1) {
+    kt = kt < kt1 ? kt : kt_last;
+#pragma unroll
+    for (int q = q0; q < q1; ++q) {
+      if ((q & 1) == 0) dma_a.issue(a_base + kt * kBK64, sa, wave, q >> 1);
+      else if constexpr (NN) dma_bn.issue(b_base + kt * b_step, sb, wave, q >> 1);
+      else dma_bk.issue(b_base + kt * b_step, sb, wave, q >> 1);
+    }
+  };
+
+  issue_part(kt0, sA0, sB0, 0, 16);
+  issue_part(kt0 + 1, sA1, sB1, 0, kSplitA);
+  sync_tile<kSplitA>();  // k-tile kt0 landed
+
+  constexpr bool kT = EPI == kEpiStore || EPI == kEpiBias || EPI == kEpiSwiglu;
+  Frags f0, f1;
+  read_frags64<NN>(f0, sA0, sB0, 0, wm, wn, lane);
+  // k-tile t on stage t % 2, its four k-steps each reading the next one's fragments while its
+  // 16 MFMAs run. k-steps 0 and 1 finish the DMA of t + 1 into the other stage. After k-step 2
+  // every wavefront has read this stage and t + 1 has landed (the barrier): k-step 3 reads
+  // t + 1's first fragments and starts the DMA of t + 2 into this stage.
+  auto k_tile = [&](int64_t t, uint16_t* sa, uint16_t* sb, uint16_t* sa_n, uint16_t* sb_n) {
+    __builtin_amdgcn_sched_barrier(0);
+    issue_part(t + 1, sa_n, sb_n, kSplitA, kSplitA + kSplitB);
+    read_frags64<NN>(f1, sa, sb, 1, wm, wn, lane);
+    mfma_step<kT>(acc, f0);
+    sched_step<NN, 0, kSplitB>();
+    __builtin_amdgcn_sched_barrier(0);
+    issue_part(t + 1, sa_n, sb_n, kSplitA + kSplitB, 16);
+    read_frags64<NN>(f0, sa, sb, 2, wm, wn, lane);
+    mfma_step<kT>(acc, f1);
+    sched_step<NN, 0, 16 - kSplitA - kSplitB>();
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags64<NN>(f1, sa, sb, 3, wm, wn, lane);
+    mfma_step<kT>(acc, f0);
+    sched_step<NN, 0, 0>();
+    __builtin_amdgcn_sched_barrier(0);
+    sync_tile<0>();
+    issue_part(t + 2, sa, sb, 0, kSplitA);
+    read_frags64<NN>(f0, sa_n, sb_n, 0, wm, wn, lane);
+    mfma_step<kT>(acc, f1);
+    sched_step<NN, 0, kSplitA>();
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  for (int64_t t = kt0; t < kt1; t += 2) {
+    k_tile(t, sA0, sB0, sA1, sB1);
+    k_tile(t + 1, sA1, sB1, sA0, sB0);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  if constexpr (kT) __builtin_amdgcn_s_barrier();
+  uint16_t* st = wave == 0 ? sA0 : wave == 1 ? sA1 : wave == 2 ? sB0 : sB1;
+  store_tile<EPI>(g, acc, st, st + 64 * 128, m0, tile_n, lane, wave);
+}
+
 // Sum of the split-K partials [splits, M, N] and the epilogue (store / bias / residual).
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* ws, int splits,
                                                             int64_t M, int64_t N, int epi,
@@ -654,16 +834,24 @@ using namespace qlora;
 
 namespace {
 
+// kernel selector: BSRC kBNF4 -> nf4_gemm_kernel, kBHalf -> hgemm_kernel
+template <int BSRC, bool NN, int EPI>
+void launch_one(const GemmArgs& g, dim3 grid, hipStream_t s) {
+  if constexpr (BSRC == kBNF4)
+    hipLaunchKernelGGL((nf4_gemm_kernel<NN, EPI>), grid, dim3(kThreads), 0, s, g);
+  else
+    hipLaunchKernelGGL((hgemm_kernel<NN, EPI>), grid, dim3(kThreads), 0, s, g);
+}
+
 template <bool NN, int BSRC>
 void launch_epi(const GemmArgs& g, dim3 grid, hipStream_t s, int epi) {
-  const dim3 block(kThreads);
   switch (epi) {
-    case kEpiStore: hipLaunchKernelGGL((gemm_kernel<NN, BSRC, kEpiStore>), grid, block, 0, s, g); break;
-    case kEpiBias: hipLaunchKernelGGL((gemm_kernel<NN, BSRC, kEpiBias>), grid, block, 0, s, g); break;
-    case kEpiResid: hipLaunchKernelGGL((gemm_kernel<NN, BSRC, kEpiResid>), grid, block, 0, s, g); break;
-    case kEpiPartial: hipLaunchKernelGGL((gemm_kernel<NN, BSRC, kEpiPartial>), grid, block, 0, s, g); break;
+    case kEpiStore: launch_one<BSRC, NN, kEpiStore>(g, grid, s); break;
+    case kEpiBias: launch_one<BSRC, NN, kEpiBias>(g, grid, s); break;
+    case kEpiResid: launch_one<BSRC, NN, kEpiResid>(g, grid, s); break;
+    case kEpiPartial: launch_one<BSRC, NN, kEpiPartial>(g, grid, s); break;
     default:
-      if constexpr (!NN) hipLaunchKernelGGL((gemm_kernel<NN, BSRC, kEpiSwiglu>), grid, block, 0, s, g);
+      if constexpr (!NN) launch_one<BSRC, NN, kEpiSwiglu>(g, grid, s);
       break;
   }
 }
@@ -680,9 +868,12 @@ int run_gemm(GemmArgs& g, int bsrc, int mode, int epi, int splits, float* ws, in
   // fp16 outputs leave in 16-byte row pieces
   QLORA_CHECK_ARG(epi == kEpiResid || splits > 1 || (g.ldc % 8 == 0 && al(g.c, 16)));
   QLORA_CHECK_ARG(splits == 1 || (ws && ws_elems >= (int64_t)splits * g.M * g.N && al(ws, 16)));
-  const int64_t ktiles = g.Kr / kBK;
-  QLORA_CHECK_ARG(ktiles % kStages == 0);  // the main loop takes four k-tiles per trip
-  g.kt_per_split = (int)(qlora_cdiv(qlora_cdiv(ktiles, splits), kStages) * kStages);
+  // NF4 B: k-tiles of 32, four per loop trip; fp16 B: k-tiles of 64, two per trip (the split
+  // boundaries fall on the same multiples of 128 either way)
+  const int bk = bsrc == kBNF4 ? kBK : kBK64, per_trip = bsrc == kBNF4 ? kStages : 2;
+  const int64_t ktiles = g.Kr / bk;
+  QLORA_CHECK_ARG(ktiles % per_trip == 0);
+  g.kt_per_split = (int)(qlora_cdiv(qlora_cdiv(ktiles, splits), per_trip) * per_trip);
   QLORA_CHECK_ARG((int64_t)g.kt_per_split * (splits - 1) < ktiles);  // no empty slice
   const int kepi = splits > 1 ? (int)kEpiPartial : epi;
   void* out = g.c;

@@ -501,7 +501,7 @@ def _layer_forward(spec, h, packed, lora16, seeds, keep):
     h2, b, _, _, rstd2 = _rms_fwd(spec, h, spec.ln2, packed, delta=o)
     del o
     if keep:
-        gu = L.nf4_linear(b, spec.gu)
+        gu = L.nf4_linear_gu(b, spec.gu)
         f.update(q=q, k=k, v=v, out=out, lse=lse, aseed=aseed, aoffset=aoffset, h2=h2,
                  rstd2=rstd2, gu=gu)
         return None, f

@@ -217,6 +217,14 @@ SWIGLU_EPILOGUE = True
 SWIGLU_NF4 = False
 
 
+# The stacked [gate | up] product of a layer that keeps its intermediates (its output is stored
+# for the SwiGLU backward) on the same package GEMM, fp16 weight. Off: alone at M = 2560 it ran
+# 139 against 155 us for the library's choice (hipBLASLt, 256 x 256 tiles), but in the step
+# (the recompute's product, right after the layer's dequant) alternating blocks of 20 steps in
+# one process gave 36.40 ms per step against 35.61 ms with the library.
+WIDE_ON_PACKAGE = False
+
+
 def swiglu_fused_nf4():
     """Whether the forward's gate|up product reads the NF4 weight itself (no fp16 copy)."""
     return BACKEND == "fused" or (SWIGLU_EPILOGUE and SWIGLU_NF4)
@@ -237,6 +245,13 @@ def nf4_linear_swiglu(x, w, I):
         return hgemm(x, dequantize(w), 0, epi=3, swiglu_I=I)
     from .ops import _glu_fwd
     return _glu_fwd(nf4_linear(x, w), I)
+
+
+def nf4_linear_gu(x, w):
+    """[g | u] = X W^T for the stacked gate|up weight, fp16 [M, 2 I] (kept for the backward)."""
+    if BACKEND == "dequant" and WIDE_ON_PACKAGE and _gemm_fits(w.shape[0], x.shape[1]):
+        return hgemm(x, dequantize(w), 0)
+    return nf4_linear(x, w)
 
 
 def nf4_linear_resid(x, w, resid, out=None):
