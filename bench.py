@@ -10,9 +10,12 @@ fp16 embedding. `value` = tokens/s over the K timed steps, inputs resident in HB
 Beside it, on the same JSON line:
   loss_curve     the loss of steps 1..64 from the random init (warmup and timed steps included)
   keep_all       the same step with every layer keeping its intermediates (no recompute)
-  roofline       the step's NF4 dequant launches (the north star's dequant GB/s); roofline_mfma:
-                 the attention kernels against the fp16 MFMA peak (algorithmic flops of the
-                 batch's causal pairs)
+  roofline       the step's largest hand-written kernel by time, the package's MFMA GEMM
+                 (hgemm_kernel: the gate|up forward with the SwiGLU epilogue), 2 M N K flops
+                 over the dispatch-recorded duration, against the fp16 MFMA peak
+  roofline_dequant  the step's NF4 dequant launches (the north star's dequant GB/s)
+  roofline_mfma  the attention kernels against the fp16 MFMA peak (algorithmic flops of the
+                 batch's causal pairs) and the step's library GEMMs
   config1..4     BASELINE configs 1-4 on the GPU (dequant GB/s; MLP, attention-input block and
                  LM-head TFLOP/s on their algorithmic work), each with its CPU oracle time
   cpu_baseline   one full 28-layer step of the CPU oracle (oracle.step, torch fp32 autograd) on
@@ -187,14 +190,11 @@ def measure_step_kernels(pkg, trainer, batch, cfg):
     heads, D = cfg.num_attention_heads, cfg.head_dim
     fwd = P.LaunchTimer("qlora_attn_fwd_split", bound="mfma")
     bwd = P.LaunchTimer("qlora_attn_bwd_split", bound="mfma")
-    dq = P.LaunchTimer(P.DOMINANT)
+    dq = P.LaunchTimer(P.DEQUANT)
     flops = lambda a: 2.0 * a[1] * a[2] * a[3]  # noqa: E731  (op, M, N, K, ...)
     gemms = [P.LaunchTimer(e, work=flops, bound="mfma")
              for e in ("qlora_gemm", "qlora_gemm_splitk", "qlora_gemmlt")]
-    # qlora_hgemm (a, lda, b, ldb, M, N, K, mode, ..., epi, swiglu_I, ...): N is the output's
-    # columns, I with the SwiGLU epilogue, whose product is [M, 2 I]
-    own = P.LaunchTimer("qlora_hgemm", bound="mfma",
-                        work=lambda a: 2.0 * a[4] * a[5] * a[6] * (2 if a[13] == 3 else 1))
+    own = P.LaunchTimer(P.DOMINANT, bound="mfma", work=P.hgemm_flops, nbytes=P.hgemm_bytes)
     with contextlib.ExitStack() as stack:
         for t in (dq, fwd, bwd, *gemms, own):
             stack.enter_context(t)
@@ -214,10 +214,9 @@ def measure_step_kernels(pkg, trainer, batch, cfg):
                                    "y = x W^T, N = 2 I)"))
     mine = own.summary()
     if mine is not None:
-        out.append(dict(mine, kernel="gate|up forward products on this package's MFMA GEMM "
-                                     "(qlora_hgemm hgemm_kernel: the forward pass's with the "
-                                     "SwiGLU epilogue, the recompute's [g | u])"))
-    return dq.summary(), out
+        mine = dict(mine, kernel="hgemm_kernel (qlora_hgemm): the gate|up forward with the "
+                                 "SwiGLU epilogue, this package's MFMA GEMM")
+    return mine, dq.summary(), out
 
 
 def _median_time(fn, reps, sync=True):
@@ -604,7 +603,8 @@ def main():
                                    "every layer keeps its intermediates (no recompute)"),
                    "gemm_backend": pkg.linear.BACKEND},
         "roofline": kernels[0],
-        "roofline_mfma": kernels[1],
+        "roofline_dequant": kernels[1],
+        "roofline_mfma": kernels[2],
         "loss_curve": curve,
         "keep_all": keep,
         "graph": graph,

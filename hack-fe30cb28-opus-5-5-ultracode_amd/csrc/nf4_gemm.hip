@@ -54,6 +54,8 @@
 // reads and the A tiles are shared through the MALL.
 #include "nf4.h"
 
+#include <hip/hip_ext.h>
+
 #include <type_traits>
 
 namespace qlora {
@@ -834,24 +836,27 @@ using namespace qlora;
 
 namespace {
 
-// kernel selector: BSRC kBNF4 -> nf4_gemm_kernel, kBHalf -> hgemm_kernel
+// kernel selector: BSRC kBNF4 -> nf4_gemm_kernel, kBHalf -> hgemm_kernel. start/stop (may be
+// null): events the dispatch records at the kernel's own start and end (hipExtLaunchKernelGGL)
 template <int BSRC, bool NN, int EPI>
-void launch_one(const GemmArgs& g, dim3 grid, hipStream_t s) {
-  if constexpr (BSRC == kBNF4)
-    hipLaunchKernelGGL((nf4_gemm_kernel<NN, EPI>), grid, dim3(kThreads), 0, s, g);
+void launch_one(const GemmArgs& g, dim3 grid, hipStream_t s, hipEvent_t start, hipEvent_t stop) {
+  auto kernel = BSRC == kBNF4 ? nf4_gemm_kernel<NN, EPI> : hgemm_kernel<NN, EPI>;
+  if (start != nullptr || stop != nullptr)
+    hipExtLaunchKernelGGL(kernel, grid, dim3(kThreads), 0, s, start, stop, 0, g);
   else
-    hipLaunchKernelGGL((hgemm_kernel<NN, EPI>), grid, dim3(kThreads), 0, s, g);
+    hipLaunchKernelGGL(kernel, grid, dim3(kThreads), 0, s, g);
 }
 
 template <bool NN, int BSRC>
-void launch_epi(const GemmArgs& g, dim3 grid, hipStream_t s, int epi) {
+void launch_epi(const GemmArgs& g, dim3 grid, hipStream_t s, int epi, hipEvent_t start,
+                hipEvent_t stop) {
   switch (epi) {
-    case kEpiStore: launch_one<BSRC, NN, kEpiStore>(g, grid, s); break;
-    case kEpiBias: launch_one<BSRC, NN, kEpiBias>(g, grid, s); break;
-    case kEpiResid: launch_one<BSRC, NN, kEpiResid>(g, grid, s); break;
-    case kEpiPartial: launch_one<BSRC, NN, kEpiPartial>(g, grid, s); break;
+    case kEpiStore: launch_one<BSRC, NN, kEpiStore>(g, grid, s, start, stop); break;
+    case kEpiBias: launch_one<BSRC, NN, kEpiBias>(g, grid, s, start, stop); break;
+    case kEpiResid: launch_one<BSRC, NN, kEpiResid>(g, grid, s, start, stop); break;
+    case kEpiPartial: launch_one<BSRC, NN, kEpiPartial>(g, grid, s, start, stop); break;
     default:
-      if constexpr (!NN) launch_one<BSRC, NN, kEpiSwiglu>(g, grid, s);
+      if constexpr (!NN) launch_one<BSRC, NN, kEpiSwiglu>(g, grid, s, start, stop);
       break;
   }
 }
@@ -859,8 +864,10 @@ void launch_epi(const GemmArgs& g, dim3 grid, hipStream_t s, int epi) {
 bool al(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 
 // Shared launch path: shapes and workspace checked, then the tile grid (and the split-K reduce).
+// start/stop (may be null): recorded at the start of the tile grid and the end of the last
+// kernel.
 int run_gemm(GemmArgs& g, int bsrc, int mode, int epi, int splits, float* ws, int64_t ws_elems,
-             hipStream_t s) {
+             hipStream_t s, hipEvent_t start = nullptr, hipEvent_t stop = nullptr) {
   const int64_t n_tiles = epi == kEpiSwiglu ? g.N / 128 : qlora_cdiv(g.N, kBN);
   g.m_tiles = (int)qlora_cdiv(g.M, kBM);
   const int64_t grid = (int64_t)g.m_tiles * n_tiles;
@@ -879,19 +886,25 @@ int run_gemm(GemmArgs& g, int bsrc, int mode, int epi, int splits, float* ws, in
   void* out = g.c;
   if (splits > 1) g.c = ws;
   const dim3 gdim((unsigned)grid, 1, (unsigned)splits);
+  hipEvent_t gemm_stop = splits > 1 ? nullptr : stop;
   if (mode == 0) {
-    if (bsrc == kBNF4) launch_epi<false, kBNF4>(g, gdim, s, kepi);
-    else launch_epi<false, kBHalf>(g, gdim, s, kepi);
+    if (bsrc == kBNF4) launch_epi<false, kBNF4>(g, gdim, s, kepi, start, gemm_stop);
+    else launch_epi<false, kBHalf>(g, gdim, s, kepi, start, gemm_stop);
   } else {
-    if (bsrc == kBNF4) launch_epi<true, kBNF4>(g, gdim, s, kepi);
-    else launch_epi<true, kBHalf>(g, gdim, s, kepi);
+    if (bsrc == kBNF4) launch_epi<true, kBNF4>(g, gdim, s, kepi, start, gemm_stop);
+    else launch_epi<true, kBHalf>(g, gdim, s, kepi, start, gemm_stop);
   }
   int rc = qlora_launch_status();
   if (rc != 0 || splits == 1) return rc;
   QLORA_CHECK_ARG(g.N % 4 == 0 && g.ldc % 4 == 0 && (epi != kEpiResid || g.ldr % 4 == 0));
   const int64_t quads = g.M * g.N / 4;
-  hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)qlora_cdiv(quads, 256)), dim3(256), 0,
-                     s, ws, splits, g.M, g.N, epi, out, g.ldc, g.bias, g.resid, g.ldr);
+  const dim3 rgrid((unsigned)qlora_cdiv(quads, 256));
+  if (stop != nullptr)
+    hipExtLaunchKernelGGL(splitk_reduce_kernel, rgrid, dim3(256), 0, s, nullptr, stop, 0, ws,
+                          splits, g.M, g.N, epi, out, g.ldc, g.bias, g.resid, g.ldr);
+  else
+    hipLaunchKernelGGL(splitk_reduce_kernel, rgrid, dim3(256), 0, s, ws, splits, g.M, g.N, epi,
+                       out, g.ldc, g.bias, g.resid, g.ldr);
   return qlora_launch_status();
 }
 
@@ -986,12 +999,14 @@ QLORA_API int qlora_nf4_gemm(const void* a, int64_t lda, const void* packed, con
   return run_gemm(g, kBNF4, mode, epi, splits, ws, ws_elems, (hipStream_t)stream);
 }
 
-// The same GEMM with an fp16 B in memory: NT B [N, K] (ldb), NN B [K, N] (ldb).
-QLORA_API int qlora_hgemm(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t M,
-                          int64_t N, int64_t K, int32_t mode, void* c, int64_t ldc,
-                          const void* bias, const float* resid, int64_t ldr, int32_t epi,
-                          int64_t swiglu_I, int32_t splits, float* ws, int64_t ws_elems,
-                          void* stream) {
+// The same GEMM with an fp16 B in memory: NT B [N, K] (ldb), NN B [K, N] (ldb). The timed form
+// also records start/stop (hipEvent_t with timing, or null) at the start of the tile grid and
+// the end of the last kernel.
+QLORA_API int qlora_hgemm_timed(const void* a, int64_t lda, const void* b, int64_t ldb,
+                                int64_t M, int64_t N, int64_t K, int32_t mode, void* c,
+                                int64_t ldc, const void* bias, const float* resid, int64_t ldr,
+                                int32_t epi, int64_t swiglu_I, int32_t splits, float* ws,
+                                int64_t ws_elems, void* stream, void* start, void* stop) {
   QLORA_CHECK_ARG(M >= 0 && N > 0 && K > 0);
   if (M == 0) return 0;
   QLORA_CHECK_ARG(a && b && c && (mode == 0 || mode == 1));
@@ -1022,5 +1037,15 @@ QLORA_API int qlora_hgemm(const void* a, int64_t lda, const void* b, int64_t ldb
   g.N = N;
   g.Kr = K;
   g.I = swiglu_I;
-  return run_gemm(g, kBHalf, mode, epi, splits, ws, ws_elems, (hipStream_t)stream);
+  return run_gemm(g, kBHalf, mode, epi, splits, ws, ws_elems, (hipStream_t)stream,
+                  static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop));
+}
+
+QLORA_API int qlora_hgemm(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t M,
+                          int64_t N, int64_t K, int32_t mode, void* c, int64_t ldc,
+                          const void* bias, const float* resid, int64_t ldr, int32_t epi,
+                          int64_t swiglu_I, int32_t splits, float* ws, int64_t ws_elems,
+                          void* stream) {
+  return qlora_hgemm_timed(a, lda, b, ldb, M, N, K, mode, c, ldc, bias, resid, ldr, epi,
+                           swiglu_I, splits, ws, ws_elems, stream, nullptr, nullptr);
 }

@@ -15,15 +15,23 @@ from . import _lib
 HBM_PEAK_GBS = 8000.0
 FP16_PEAK_TFLOPS = 2500.0
 
-# the kernel reported as the step's roofline entry
-DOMINANT = "qlora_nf4_dequant_many"
+# the kernel reported as the step's roofline entry: the largest hand-written kernel of the step by
+# time (the package's MFMA GEMM: the gate|up forward with the SwiGLU epilogue); the dequant, the
+# north star's "NF4 dequant HBM GB/s", is reported beside it
+DOMINANT = "qlora_hgemm"
+DEQUANT = "qlora_nf4_dequant_many"
 
 # Measured HBM bytes per launch over algorithmic bytes per launch: rocprofv3 FETCH_SIZE and
 # WRITE_SIZE of the layer-wide dequant launch (the same kernel and byte count as each of the
 # step's launches), each divided by what the counter reads for a plain device copy of 1 GiB
 # (512 MiB each way; FETCH 0.50004, WRITE 1.000 of the bytes moved):
 # (11,892.4 / 0.50004 + 91,392) KiB per launch = 1.0018 x the algorithmic 117,728,444 B.
-TRAFFIC_RATIO = {"qlora_nf4_dequant_many": 1.0018}
+# The package GEMM's SwiGLU launch (hgemm_kernel<NT, SwiGLU>) at the M = 1,875 batch the bench
+# measures: (95,837 / 0.50004 + 32,812) KiB per launch = 2.435 x the algorithmic bytes (A, the
+# [gate; up] weight and the output once each); 2.78 at M = 2,325, 2.86 at M = 2,614. The
+# excess is the A tile re-read by each XCD and B tiles re-read past the 4 MB L2 (FETCH_SIZE
+# counts what leaves the L2, Infinity Cache hits included).
+TRAFFIC_RATIO = {"qlora_nf4_dequant_many": 1.0018, "qlora_hgemm": 2.435}
 
 
 def _dequant_bytes(args):
@@ -53,7 +61,21 @@ def _dequant_many_bytes(args):
 
 
 # entries with a form that records the events from the kernel dispatch itself
-TIMED = {"qlora_nf4_dequant_many": "qlora_nf4_dequant_many_timed"}
+TIMED = {"qlora_nf4_dequant_many": "qlora_nf4_dequant_many_timed",
+         "qlora_hgemm": "qlora_hgemm_timed"}
+
+
+def hgemm_flops(args):
+    """2 M N K of one qlora_hgemm launch (a, lda, b, ldb, M, N, K, mode, ..., epi at 13): N is
+    the output's columns, I with the SwiGLU epilogue, whose product is [M, 2 I]."""
+    return 2.0 * args[4] * args[5] * args[6] * (2 if args[13] == 3 else 1)
+
+
+def hgemm_bytes(args):
+    """Algorithmic HBM bytes of one qlora_hgemm launch: A [M, K], the weight ([N, K], [2 I, K]
+    with the SwiGLU epilogue, [K, N] in NN) and the fp16 output [M, N] once each."""
+    M, N, K, epi = args[4], args[5], args[6], args[13]
+    return 2.0 * (M * K + (2 * N if epi == 3 else N) * K + M * N)
 
 WORK = {
     "qlora_nf4_dequant": ("hbm", _dequant_bytes),
@@ -64,9 +86,10 @@ WORK = {
 class LaunchTimer:
     """Times every launch of `entry` while active. The work of a launch comes from WORK, or
     from `work` (a function of the call's arguments) with its `bound` ("hbm": bytes, "mfma":
-    flops), or is given afterwards per launch to summary() (`work_total`)."""
+    flops), or is given afterwards per launch to summary() (`work_total`). `nbytes`: the
+    algorithmic HBM bytes of a launch of an MFMA-bound entry (the base of its measured traffic)."""
 
-    def __init__(self, entry, work=None, bound=None):
+    def __init__(self, entry, work=None, bound=None, nbytes=None):
         if work is None and bound is None and entry not in WORK:
             raise ValueError(f"no work model for {entry}")
         self.entry = entry
@@ -75,6 +98,7 @@ class LaunchTimer:
             self.bound, self.work = bound, work
         if self.work is None:
             self.work = lambda args: 0.0
+        self.nbytes = nbytes
         self.records = []
 
     def __enter__(self):
@@ -118,7 +142,11 @@ class LaunchTimer:
             achieved = work / total_s / 1e12
             peak, unit = FP16_PEAK_TFLOPS, "TFLOP/s"
         ratio = TRAFFIC_RATIO.get(self.entry)
-        traffic = work / len(ms) * ratio if ratio is not None else None
+        traffic = None
+        if ratio is not None and self.bound == "hbm":
+            traffic = work / len(ms) * ratio
+        elif ratio is not None and self.nbytes is not None:
+            traffic = sum(self.nbytes(r[3]) for r in recs) / len(recs) * ratio
         return {"bound": self.bound, "achieved": achieved, "peak": peak, "unit": unit,
                 "frac": achieved / peak, "traffic": traffic, "kernel": self.entry,
                 "launches": len(ms), "avg_us": avg_us,

@@ -289,6 +289,18 @@ int qlora_hgemm(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t 
                 float* ws, int64_t ws_elems, void* stream);
 
 /*
+ * qlora_hgemm that also records start/stop (hipEvent_t created with timing, or null) at the start
+ * of its tile grid and the end of its last kernel (the split-K reduce when splits > 1), the
+ * dispatches' own timestamps. No reference counterpart: the bench's per-launch timing of the
+ * step's own MFMA GEMM.
+ */
+int qlora_hgemm_timed(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t M,
+                      int64_t N, int64_t K, int32_t mode, void* c, int64_t ldc, const void* bias,
+                      const float* resid, int64_t ldr, int32_t epi, int64_t swiglu_I,
+                      int32_t splits, float* ws, int64_t ws_elems, void* stream, void* start,
+                      void* stop);
+
+/*
  * out = a + fp32(d) over numel elements (a, out f32; d f16; numel % 4 == 0; out may alias a):
  * the residual add after the down projection, h3 = h2 + d (engine.py:1048-1051, 1179).
  */

@@ -226,3 +226,27 @@ def test_tile_major_order_equals_bnb_order(pkg, epi):
     codes, scales = pkg.ops.gemm_tiles(w, kw.get("swiglu_I", 0))
     assert torch.equal(torch.sort(codes).values, torch.sort(w.packed.reshape(-1)).values)
     assert torch.equal(torch.sort(scales).values, torch.sort(w.block_scales()).values)
+
+
+@pytest.mark.parametrize("splits", [1, 2])
+def test_hgemm_timed_form(pkg, splits):
+    """qlora_hgemm_timed gives qlora_hgemm's output bit for bit and records its two events
+    around the kernels (the bench's per-launch timing of the package GEMM)."""
+    L, lib = pkg.linear, pkg._lib
+    g = torch.Generator(device=DEV).manual_seed(3 + splits)
+    a = torch.randn(700, 1536, generator=g, device=DEV).half()
+    b = (torch.randn(2048, 1536, generator=g, device=DEV) * 0.02).half()
+    want = L.hgemm(a, b, 0, splits=splits)
+    got = torch.empty_like(want)
+    ws = torch.empty(splits * 700 * 2048, device=DEV) if splits > 1 else None
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()  # creates the events on the device
+    stop.record()
+    stream = torch.cuda.current_stream().cuda_stream
+    lib.call("qlora_hgemm_timed", a.data_ptr(), 1536, b.data_ptr(), 1536, 700, 2048, 1536, 0,
+             got.data_ptr(), 2048, None, None, 0, 0, 0, splits,
+             None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(), stream,
+             start.cuda_event, stop.cuda_event)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    assert start.elapsed_time(stop) > 0
