@@ -52,6 +52,8 @@ SIGNATURES = {
     "qlora_gemm": [I32, I64, I64, I64, P, I64, P, I64, P, I64, F32, F32, I32, P],
     "qlora_gemm_solutions": [I32, I64, I64, I64, P, I64, P, I64, P, I64, P, I32, P],
     "qlora_gemm_splitk": [I32, I64, I64, I64, P, I64, P, I64, P, I64, P, I32, P, I64, I32, P],
+    "qlora_gemm_splitk_resid": [I32, I64, I64, I64, P, I64, P, I64, P, I64, P, I64, I32, P, I64,
+                                I32, P],
     "qlora_gemm_splitk_solutions": [I32, I64, I64, I64, P, I64, P, I64, P, I32, P, I32, P],
     "qlora_gemmlt": [I32, I64, I64, I64, P, I64, P, I64, P, I64, P, F32, F32, I32, P, I64, P],
     "qlora_gemmlt_solutions": [I32, I64, I64, I64, I64, I64, I64, I32, I64, P, I32, P],

@@ -165,6 +165,32 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   *reinterpret_cast<uint2*>(out + m * ldc + n) = r;
 }
 
+// out_f32[m][n] = resid[m][n] + f32(fp16(sum_j work[j][m][n])): the split-K sum rounded to fp16
+// (the product's own rounding) and added to the fp32 residual stream, as resid_add_kernel adds
+// an fp16 product.
+__global__ __launch_bounds__(256) void splitk_reduce_resid_kernel(const float* __restrict__ work,
+                                                                  int splits, int64_t M,
+                                                                  int64_t N,
+                                                                  const float* __restrict__ resid,
+                                                                  int64_t ldr, float* out,
+                                                                  int64_t ldo) {
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i >= M * N) return;
+  const int64_t m = i / N, n = i % N;
+  float4 acc = *reinterpret_cast<const float4*>(work + i);
+  for (int j = 1; j < splits; ++j) {
+    const float4 w = *reinterpret_cast<const float4*>(work + (int64_t)j * M * N + i);
+    acc.x += w.x;
+    acc.y += w.y;
+    acc.z += w.z;
+    acc.w += w.w;
+  }
+  const float4 r = *reinterpret_cast<const float4*>(resid + m * ldr + n);
+  *reinterpret_cast<float4*>(out + m * ldo + n) =
+      make_float4(r.x + h2f(f2h(acc.x)), r.y + h2f(f2h(acc.y)), r.z + h2f(f2h(acc.z)),
+                  r.w + h2f(f2h(acc.w)));
+}
+
 struct Split {
   Problem p;
   rocblas_int kc;                 // K per slice
@@ -193,6 +219,33 @@ int make_split(int32_t op, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t
 // fp32 partial products into work [splits][M][N] (one strided-batched rocBLAS call, solution as
 // in qlora_gemm but of the batched fp32-output problem), then one fixed-order sum and rounding.
 // Requires K % (8 splits) == 0, N % 4 == 0, work_elems >= splits M N.
+namespace {
+
+// The strided-batched fp32-output GEMM of a split: work[j] = A[:, slice j] op(B)[slice j, :].
+int splitk_partials(const qlora::blas::Split& sp, int64_t N, const void* A, const void* B,
+                    float* work, int32_t splits, int32_t solution, hipStream_t st) {
+  using namespace qlora::blas;
+  rocblas_handle h;
+  int rc;
+  if ((rc = handle_for(&h)) != 0) return rc;
+  if ((rc = status(rocblas_set_stream(h, st))) != 0) return rc;
+  const float alpha = 1.f, beta = 0.f;
+  const Problem& p = sp.p;
+  return status(rocblas_gemm_strided_batched_ex(
+      h, p.ta, rocblas_operation_none, p.m, p.n, p.k, &alpha, B, rocblas_datatype_f16_r, p.lda,
+      sp.sa, A, rocblas_datatype_f16_r, p.ldb, sp.sb, &beta, work, rocblas_datatype_f32_r,
+      (rocblas_int)N, sp.sc, work, rocblas_datatype_f32_r, (rocblas_int)N, sp.sc, splits,
+      rocblas_datatype_f32_r,
+      solution > 0 ? rocblas_gemm_algo_solution_index : rocblas_gemm_algo_standard, solution,
+      rocblas_gemm_flags_none));
+}
+
+}  // namespace
+
+// fp16 C[M, N] (ld ldc) = fp16(A op(B) (+ bias)) with the reduction cut into `splits` slices:
+// fp32 partial products into work [splits][M][N] (one strided-batched rocBLAS call, solution as
+// in qlora_gemm but of the batched fp32-output problem), then one fixed-order sum and rounding.
+// Requires K % (8 splits) == 0, N % 4 == 0, work_elems >= splits M N.
 QLORA_API int qlora_gemm_splitk(int32_t op, int64_t M, int64_t N, int64_t K, const void* A,
                                 int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc,
                                 const void* bias, int32_t splits, float* work,
@@ -203,24 +256,35 @@ QLORA_API int qlora_gemm_splitk(int32_t op, int64_t M, int64_t N, int64_t K, con
   QLORA_CHECK_ARG(A && B && C && work && solution >= 0 && ldc >= N);
   QLORA_CHECK_ARG(work_elems >= M * N * (int64_t)splits);
   QLORA_CHECK_ARG(((uintptr_t)C & 7) == 0 && ldc % 4 == 0 && ((uintptr_t)work & 15) == 0);
-  rocblas_handle h;
-  if ((rc = handle_for(&h)) != 0) return rc;
   hipStream_t st = (hipStream_t)stream;
-  if ((rc = status(rocblas_set_stream(h, st))) != 0) return rc;
-  const float alpha = 1.f, beta = 0.f;
-  const Problem& p = sp.p;
-  rc = status(rocblas_gemm_strided_batched_ex(
-      h, p.ta, rocblas_operation_none, p.m, p.n, p.k, &alpha, B, rocblas_datatype_f16_r, p.lda,
-      sp.sa, A, rocblas_datatype_f16_r, p.ldb, sp.sb, &beta, work, rocblas_datatype_f32_r,
-      (rocblas_int)N, sp.sc, work, rocblas_datatype_f32_r, (rocblas_int)N, sp.sc, splits,
-      rocblas_datatype_f32_r,
-      solution > 0 ? rocblas_gemm_algo_solution_index : rocblas_gemm_algo_standard, solution,
-      rocblas_gemm_flags_none));
-  if (rc != 0) return rc;
+  if ((rc = splitk_partials(sp, N, A, B, work, splits, solution, st)) != 0) return rc;
   const int64_t quads = M * N / 4;
   hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)qlora_cdiv(quads, 256)), dim3(256), 0,
                      st, work, splits, M, N, static_cast<uint16_t*>(C), ldc,
                      static_cast<const uint16_t*>(bias));
+  return qlora_launch_status();
+}
+
+// The same product added to an fp32 residual: out[M, N] (fp32, ld ldo) = resid (fp32, ld ldr) +
+// f32(fp16(A op(B))), the sum of the slices rounded once to fp16 and added (out may be resid).
+// Requires as qlora_gemm_splitk, and ldr, ldo % 4 == 0, resid and out 16-byte aligned.
+QLORA_API int qlora_gemm_splitk_resid(int32_t op, int64_t M, int64_t N, int64_t K, const void* A,
+                                      int64_t lda, const void* B, int64_t ldb,
+                                      const float* resid, int64_t ldr, float* out, int64_t ldo,
+                                      int32_t splits, float* work, int64_t work_elems,
+                                      int32_t solution, void* stream) {
+  Split sp;
+  int rc = make_split(op, M, N, K, lda, ldb, splits, &sp);
+  if (rc != 0) return rc;
+  QLORA_CHECK_ARG(A && B && resid && out && work && solution >= 0 && ldr >= N && ldo >= N);
+  QLORA_CHECK_ARG(work_elems >= M * N * (int64_t)splits);
+  QLORA_CHECK_ARG(ldr % 4 == 0 && ldo % 4 == 0 && ((uintptr_t)resid & 15) == 0 &&
+                  ((uintptr_t)out & 15) == 0 && ((uintptr_t)work & 15) == 0);
+  hipStream_t st = (hipStream_t)stream;
+  if ((rc = splitk_partials(sp, N, A, B, work, splits, solution, st)) != 0) return rc;
+  const int64_t quads = M * N / 4;
+  hipLaunchKernelGGL(splitk_reduce_resid_kernel, dim3((unsigned)qlora_cdiv(quads, 256)),
+                     dim3(256), 0, st, work, splits, M, N, resid, ldr, out, ldo);
   return qlora_launch_status();
 }
 

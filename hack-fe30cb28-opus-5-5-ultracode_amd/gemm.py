@@ -31,7 +31,7 @@ import time
 import torch
 
 from . import _lib
-from .ops import _need, _ptr, _stream
+from .ops import _need, _ptr, _resid_add, _stream
 
 BUCKET = 256
 TORCH = (-1, 1)   # torch's matmul
@@ -148,6 +148,40 @@ def mm(a, b, op, out=None, bias=None):
         _CHOICE[(dev.index or 0, op, N, K, bias is not None, _bucket(M))] = DEFAULT
         _run(DEFAULT, op, a, b, out, bias, M, N, K, lda, ldb, ldc, dev)
     return out
+
+
+def mm_resid(a, b, op, resid, out=None):
+    """fp32 [M, N] = resid + fp32(fp16(a op(b))): the product rounded to fp16 as mm() rounds it,
+    added to the fp32 residual stream (out may be resid). When the variant tuned for the product
+    is a split of K, the split's reduce kernel adds the residual itself (no fp16 [M, N] output,
+    no second pass); otherwise mm() and the residual-add kernel."""
+    dev = a.device
+    lda = _check(a, "a", dev)
+    ldb = _check(b, "b", dev)
+    M, N, K = _dims(a, b, op)
+    _need(resid, "resid", torch.float32, dev, contiguous=False)
+    if resid.shape != (M, N) or resid.stride(1) != 1:
+        raise ValueError(f"resid must be [{M}, {N}] with unit column stride")
+    if out is None:
+        out = torch.empty((M, N), device=dev, dtype=torch.float32)
+    _need(out, "out", torch.float32, dev, contiguous=False)
+    if out.shape != (M, N) or out.stride(1) != 1:
+        raise ValueError(f"out must be [{M}, {N}] with unit column stride")
+    if M == 0:
+        return out
+    sol, splits = choice(dev.index or 0, op, N, K, M, False)
+    ldr, ldo = resid.stride(0), out.stride(0)
+    if sol >= 0 and splits > 1 and ldr % 4 == 0 and ldo % 4 == 0 and \
+            resid.data_ptr() % 16 == 0 and out.data_ptr() % 16 == 0:
+        work = torch.empty((splits * M * N,), device=dev, dtype=torch.float32)
+        try:
+            _lib.call("qlora_gemm_splitk_resid", op, M, N, K, _ptr(a), lda, _ptr(b), ldb,
+                      _ptr(resid), ldr, _ptr(out), ldo, splits, _ptr(work), work.numel(),
+                      int(sol), _stream(dev))
+            return out
+        except RuntimeError:
+            pass  # the variant rejects this exact size: the two-pass form below
+    return _resid_add(resid, mm(a, b, op), out=out)
 
 
 def _listed(fn, *args):

@@ -15,7 +15,7 @@ GEMM with the fp16 weight (SWIGLU_EPILOGUE).
 import torch
 
 from . import _lib, gemm
-from .ops import NF4Group, _need, _ptr, _resid_add, _stream, dequant, dequant_many, gemm_tiles
+from .ops import NF4Group, _need, _ptr, _stream, dequant, dequant_many, gemm_tiles
 
 BACKEND = "dequant"
 
@@ -255,10 +255,11 @@ def nf4_linear_gu(x, w):
 
 
 def nf4_linear_resid(x, w, resid, out=None):
-    """fp32 resid + fp16(X W^T) (the layer output h2 + d)."""
+    """fp32 resid + fp16(X W^T) (the layer output h2 + d); with a split-K library GEMM the
+    residual is added by the split's reduce (one pass, no fp16 product in memory)."""
     if BACKEND == "fused":
         return nf4_gemm(x, w, 0, epi=2, resid=resid, out=out)
-    return _resid_add(resid, nf4_linear(x, w), out=out)
+    return gemm.mm_resid(_a16(x), dequantize(w), gemm.NT, resid, out=out)
 
 
 def nf4_linear_t(dy, w):

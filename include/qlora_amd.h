@@ -339,6 +339,17 @@ int qlora_gemm_splitk(int32_t op, int64_t M, int64_t N, int64_t K, const void* A
                       const void* B, int64_t ldb, void* C, int64_t ldc, const void* bias,
                       int32_t splits, float* work, int64_t work_elems, int32_t solution,
                       void* stream);
+/*
+ * qlora_gemm_splitk added to the fp32 residual stream: out[M, N] (fp32, ld ldo) = resid (fp32, ld
+ * ldr) + f32(fp16(A op(B))), the slices' fixed-order sum rounded once to fp16, then added (the
+ * down projection and the residual add of the layer output, engine.py:1179 and its h2 + d). out
+ * may alias resid. Requires as qlora_gemm_splitk, ldr and ldo % 4 == 0, resid and out 16-byte
+ * aligned.
+ */
+int qlora_gemm_splitk_resid(int32_t op, int64_t M, int64_t N, int64_t K, const void* A,
+                            int64_t lda, const void* B, int64_t ldb, const float* resid,
+                            int64_t ldr, float* out, int64_t ldo, int32_t splits, float* work,
+                            int64_t work_elems, int32_t solution, void* stream);
 int qlora_gemm_splitk_solutions(int32_t op, int64_t M, int64_t N, int64_t K, const void* A,
                                 int64_t lda, const void* B, int64_t ldb, float* work,
                                 int32_t splits, int32_t* list, int32_t cap, int32_t* count);

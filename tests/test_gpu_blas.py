@@ -133,6 +133,32 @@ def test_mm_uses_a_tuned_split_variant(pkg):
         G.reset()
 
 
+@pytest.mark.parametrize("variant", [(0, 4), (0, 2), (0, 1)])
+@pytest.mark.parametrize("M", [2537, 37])
+def test_mm_resid_equals_mm_then_resid_add(pkg, variant, M):
+    """The down projection with the residual add (gemm.mm_resid): with a split-K variant the
+    split's reduce adds the fp32 residual itself; the result equals mm() followed by the
+    residual-add kernel bit for bit (the same fp16 rounding of the product, the same fp32 add),
+    also in place (out = resid); without a split it is that two-pass form."""
+    G = pkg.gemm
+    G.reset()
+    try:
+        N, K = 1536, 8960
+        G._CHOICE[(0, G.NT, N, K, False, G._bucket(M))] = variant
+        g = torch.Generator(device=DEV).manual_seed(M + variant[1])
+        x = torch.randn((M, K), device=DEV, generator=g).half()
+        w = (torch.randn((N, K), device=DEV, generator=g) * 0.02).half()
+        res = torch.randn((M, N), device=DEV, generator=g)
+        want = pkg.ops._resid_add(res, G.mm(x, w, G.NT))
+        assert torch.equal(G.mm_resid(x, w, G.NT, res), want)
+        inplace = res.clone()
+        G.mm_resid(x, w, G.NT, inplace, out=inplace)
+        assert torch.equal(inplace, want)
+        check((want - res).half(), ref(x, w, 0))
+    finally:
+        G.reset()
+
+
 def _lt_listed(pkg, op, M, N, K, lda, ldb, ldc, bias, ws_bytes):
     cnt = ctypes.c_int32(0)
     arr = (ctypes.c_int32 * 512)()
