@@ -104,9 +104,17 @@ __device__ __forceinline__ int nmaj_off(int row, int chunk) {  // [32][256]
 
 // Workgroup b of `total` -> tile index: XCD x (= b % 8) takes the contiguous range
 // [x total/8, (x+1) total/8) of tiles.
-__device__ __forceinline__ int64_t tile_order(int64_t b, int64_t total) {
-  const int64_t full = total / 8 * 8;
+__device__ __forceinline__ int tile_order(int b, int total) {
+  const int full = total / 8 * 8;
   return b < full ? (b % 8) * (full / 8) + b / 8 : b;
+}
+
+// The workgroup's (M tile, N tile), in scalar registers: the values are the same for every
+// lane, and held in VGPRs across the main loop they cost registers the loop needs
+__device__ __forceinline__ void tile_of(int m_tiles, int64_t& tile_m, int64_t& tile_n) {
+  const int t = tile_order(blockIdx.x, gridDim.x);  // the grid is below 2^31 (host check)
+  tile_m = __builtin_amdgcn_readfirstlane(t % m_tiles);
+  tile_n = __builtin_amdgcn_readfirstlane(t / m_tiles);
 }
 
 // ---- global -> LDS (DMA) ----------------------------------------------------------------------
@@ -447,8 +455,8 @@ __global__ __launch_bounds__(kThreads, 1) void nf4_gemm_kernel(GemmArgs g) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
 
-  const int64_t t_lin = tile_order(blockIdx.x, gridDim.x);
-  const int64_t tile_m = t_lin % g.m_tiles, tile_n = t_lin / g.m_tiles;
+  int64_t tile_m, tile_n;
+  tile_of(g.m_tiles, tile_m, tile_n);
   const int64_t m0 = tile_m * kBM;
   const int64_t kt0 = (int64_t)blockIdx.z * g.kt_per_split;
   int64_t kt1 = kt0 + g.kt_per_split;
@@ -708,8 +716,8 @@ __global__ __launch_bounds__(kThreads, 1) void hgemm_kernel(GemmArgs g) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
 
-  const int64_t t_lin = tile_order(blockIdx.x, gridDim.x);
-  const int64_t tile_m = t_lin % g.m_tiles, tile_n = t_lin / g.m_tiles;
+  int64_t tile_m, tile_n;
+  tile_of(g.m_tiles, tile_m, tile_n);
   const int64_t m0 = tile_m * kBM;
   const int64_t kt0 = (int64_t)blockIdx.z * g.kt_per_split;
   int64_t kt1 = kt0 + g.kt_per_split;
