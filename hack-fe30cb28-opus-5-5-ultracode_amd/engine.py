@@ -793,7 +793,10 @@ class FusedQwen2:
         shapes = self.gemm_shapes()
         t = G.tune(shapes, counts, self.device, log=log)
         sup = sorted({max(1, (c * f) // 4) for c in counts for f in (2, 3)})
-        return t + G.tune(shapes[-1:], sup, self.device, log=log)
+        t += G.tune(shapes[-1:], sup, self.device, log=log)
+        for I, H in sorted({(spec.I, spec.H) for spec in self.layers}):
+            t += L.tune_swiglu(I, H, counts, self.device, log=log)
+        return t
 
     def step(self, input_ids, attention_mask, labels, denom, lengths=None, n_supervised=None,
              padded=False, ctr_base=None):
@@ -809,6 +812,8 @@ class FusedQwen2:
             shapes = self.gemm_shapes()
             G.tune(shapes, [packed.n], self.device)
             G.tune(shapes[-1:], [max(1, packed.n_supervised)], self.device)
+            for I, H in sorted({(spec.I, spec.H) for spec in self.layers}):
+                L.tune_swiglu(I, H, [packed.n], self.device)
         if self.dropout is not None and self.dropout.ok is None:
             self.dropout.ok = self.dropout.check(packed.rows,
                                                  min(packed.T, TorchDropout.CHECK_TOKENS),

@@ -19,6 +19,12 @@ candidates, and then, per bucket of BUCKET tokens, the fastest candidate, with t
 shape has one. Every variant computes fp16(sum of fp16 products in fp32 (+ bias)); only the
 summation order differs.
 
+The package's own MFMA GEMM (qlora_hgemm: 256 x 256 tiles, bias or fp32-residual epilogue) is
+one more candidate for the x W^T products whose reduction length it tiles (K % 128 == 0): it
+wins where its one tile shape divides the work well (the [gate | up] product at 2,560 tokens:
+139 against 155 us) and loses where its last round of tiles is nearly empty (2,561-2,816
+tokens: 770 tiles on 256 CUs), which the per-bucket timing sorts out.
+
 hipBLASLt's listed solutions are not candidates: they are mostly rocBLAS's own (rocBLAS runs
 the same Tensile library on this GPU), none was faster than rocBLAS's best by more than 4 % at
 the step's shapes with cold caches, and listing them costs ~30 ms of host time per new token
@@ -39,6 +45,7 @@ DEFAULT = (0, 1)  # rocBLAS's own choice
 NT, NN = 0, 1     # op: C = A B^T (B [N, K]) or C = A B (B [K, N])
 LT = 0           # splits value of the hipBLASLt variant
 LT_DEFAULT = (0, LT)
+PKG = (-2, 1)     # qlora_hgemm, the package's MFMA GEMM (op NT)
 LT_WORKSPACE = 32 * 2**20  # bytes of workspace offered to hipBLASLt
 SPLITS = (2, 4, 8)
 MIN_SLICE = 1024  # no split leaves less than this much K per slice
@@ -91,8 +98,18 @@ def choice(dev_index, op, N, K, M, bias=False):
     return _CHOICE[shape + (nb,)]
 
 
+def pkg_fits(op, N, K):
+    """Whether qlora_hgemm takes this product shape as a tuner candidate."""
+    return op == NT and K % 128 == 0 and N % 8 == 0
+
+
 def _run(variant, op, a, b, out, bias, M, N, K, lda, ldb, ldc, dev, work=None):
     sol, splits = variant
+    if variant == PKG:
+        _lib.call("qlora_hgemm", _ptr(a), lda, _ptr(b), ldb, M, N, K, op, _ptr(out), ldc,
+                  _ptr(bias), None, 0, 1 if bias is not None else 0, 0, 1, None, 0,
+                  _stream(dev))
+        return
     if splits == LT:
         if work is None or work.numel() * work.element_size() < LT_WORKSPACE:
             work = torch.empty((LT_WORKSPACE,), device=dev, dtype=torch.uint8)
@@ -144,8 +161,10 @@ def mm(a, b, op, out=None, bias=None):
     except RuntimeError:
         if v == DEFAULT:
             raise
-        # the bucket's variant rejects this exact size (the libraries check before launching)
-        _CHOICE[(dev.index or 0, op, N, K, bias is not None, _bucket(M))] = DEFAULT
+        # the bucket's variant rejects this exact size (the libraries check before launching);
+        # the package's GEMM rejects operands by their alignment, so its choice stays
+        if v != PKG:
+            _CHOICE[(dev.index or 0, op, N, K, bias is not None, _bucket(M))] = DEFAULT
         _run(DEFAULT, op, a, b, out, bias, M, N, K, lda, ldb, ldc, dev)
     return out
 
@@ -169,8 +188,16 @@ def mm_resid(a, b, op, resid, out=None):
         raise ValueError(f"out must be [{M}, {N}] with unit column stride")
     if M == 0:
         return out
-    sol, splits = choice(dev.index or 0, op, N, K, M, False)
+    v = choice(dev.index or 0, op, N, K, M, False)
+    sol, splits = v
     ldr, ldo = resid.stride(0), out.stride(0)
+    if v == PKG:  # the residual added in the GEMM's epilogue
+        try:
+            _lib.call("qlora_hgemm", _ptr(a), lda, _ptr(b), ldb, M, N, K, op, _ptr(out), ldo,
+                      None, _ptr(resid), ldr, 2, 0, 1, None, 0, _stream(dev))
+            return out
+        except RuntimeError:
+            pass  # this exact problem is not tiled (alignment): the two-pass form below
     if sol >= 0 and splits > 1 and ldr % 4 == 0 and ldo % 4 == 0 and \
             resid.data_ptr() % 16 == 0 and out.data_ptr() % 16 == 0:
         work = torch.empty((splits * M * N,), device=dev, dtype=torch.float32)
@@ -234,10 +261,10 @@ def _time(fn, reps):
 
 def tune(shapes, Ms, device, top=6, top_split=2, reps=3, log=None):
     """Measure, for each (op, N, K[, bias]) in shapes and each token count in Ms, the fastest of:
-    torch's matmul, rocBLAS's default, hipBLASLt's first choice, the `top` rocBLAS solutions that
-    were fastest at the median token count and, per split count, rocBLAS's default and the
-    `top_split` fastest; with a bias added when the shape has one. Buckets already tuned are
-    skipped. Returns the seconds spent."""
+    torch's matmul, rocBLAS's default, hipBLASLt's first choice, the package's GEMM (NT shapes
+    it tiles), the `top` rocBLAS solutions that were fastest at the median token count and, per
+    split count, rocBLAS's default and the `top_split` fastest; with a bias added when the shape
+    has one. Buckets already tuned are skipped. Returns the seconds spent."""
     t0 = time.perf_counter()
     dev = torch.device(device)
     di = dev.index or 0
@@ -282,7 +309,7 @@ def tune(shapes, Ms, device, top=6, top_split=2, reps=3, log=None):
         key = (di, op, N, K, has_bias)
         if key not in _CANDIDATES:
             m_mid = todo[len(todo) // 2] * BUCKET
-            cands = [TORCH, DEFAULT, LT_DEFAULT]
+            cands = [TORCH, DEFAULT, LT_DEFAULT] + ([PKG] if pkg_fits(op, N, K) else [])
             for splits, keep in [(1, top)] + [(s, top_split) for s in splits_ok]:
                 timed = []
                 for sol in listed(m_mid, splits):
@@ -297,7 +324,7 @@ def tune(shapes, Ms, device, top=6, top_split=2, reps=3, log=None):
             _CANDIDATES[key] = cands
         for bk in todo:
             M = bk * BUCKET
-            valid = {TORCH, DEFAULT, LT_DEFAULT}
+            valid = {TORCH, DEFAULT, LT_DEFAULT, PKG}
             for splits in [1] + splits_ok:
                 valid |= {(s, splits) for s in [0] + listed(M, splits)}
             timed = []

@@ -8,9 +8,13 @@ after down_proj, fp32 gradients rounded to fp16 on load).
 Backend "dequant" (default while it is the faster one): the standalone dequant kernel into an
 fp16 buffer, then a plain GEMM (gemm.mm: rocBLAS with a measured solution per shape and token
 bucket, or torch's matmul where that is the faster) - the reference's own structure (dequant,
-then cuBLAS) - except the gate|up forward with its SwiGLU, which runs on this package's MFMA
-GEMM with the fp16 weight (SWIGLU_EPILOGUE).
+then cuBLAS), with this package's MFMA GEMM (qlora_hgemm) among the tuner's candidates - and
+the gate|up forward with its SwiGLU on that GEMM with the SwiGLU in its epilogue, for the token
+counts where it was timed faster than the library GEMM and the SwiGLU kernel (SWIGLU_EPILOGUE,
+tune_swiglu).
 """
+
+import time
 
 import torch
 
@@ -207,22 +211,17 @@ def nf4_linear(x, w, bias=None):
 
 # With the layer-wide dequant: the gate|up product of a recomputing layer's forward on the MFMA
 # GEMM of this package (qlora_hgemm), the SwiGLU in its epilogue ([gate | up] never stored),
-# instead of the library GEMM and the SwiGLU kernel. Measured on MI355X, config 5, alternating
-# runs on one box: 34.38 / 34.52 ms per step against 34.49 / 34.41 ms for the library pair.
+# instead of the library GEMM and the SwiGLU kernel, for the token-count buckets where the tuner
+# (tune_swiglu) timed it faster than that pair; untimed buckets take the package's form.
+# Measured on MI355X, config 5, alternating runs on one box, package form at every count:
+# 34.38 / 34.52 ms per step against 34.49 / 34.41 ms for the library pair.
 SWIGLU_EPILOGUE = True
+_SWIGLU_ON_PKG = {}  # (device index, I, K, bucket) -> the package's form was the faster
 # ... and with the NF4 weight decoded inside that GEMM (qlora_nf4_gemm over the weight's
 # tile-major copy): the forward then dequantizes the layer's other three weights only. Off: the
 # same alternating runs on one box gave 36.16 / 36.28 ms per step against 35.98 / 35.98 ms with
 # the fp16 weight (the in-kernel decode costs about as much as the dequant it saves).
 SWIGLU_NF4 = False
-
-
-# The stacked [gate | up] product of a layer that keeps its intermediates (its output is stored
-# for the SwiGLU backward) on the same package GEMM, fp16 weight. Off: alone at M = 2560 it ran
-# 139 against 155 us for the library's choice (hipBLASLt, 256 x 256 tiles), but in the step
-# (the recompute's product, right after the layer's dequant) alternating blocks of 20 steps in
-# one process gave 36.40 ms per step against 35.61 ms with the library.
-WIDE_ON_PACKAGE = False
 
 
 def swiglu_fused_nf4():
@@ -236,21 +235,60 @@ def _gemm_fits(I, K):
     return I % 128 == 0 and K % 128 == 0
 
 
+def swiglu_on_package(dev_index, I, K, M):
+    """Whether the fp16-weight SwiGLU product of M tokens runs on the package's GEMM with the
+    SwiGLU epilogue (else the library GEMM and the SwiGLU kernel)."""
+    if not (SWIGLU_EPILOGUE and _gemm_fits(I, K)):
+        return False
+    return _SWIGLU_ON_PKG.get((dev_index, I, K, gemm._bucket(M)), True)
+
+
+def tune_swiglu(I, K, Ms, device, reps=3, log=None):
+    """Times, per bucket of the token counts Ms, the SwiGLU product on the package's GEMM
+    against the library pair (the tuned library GEMM, then qlora_glu_fwd), with cold caches as
+    gemm.tune; run after gemm.tune has measured the (NT, 2 I, K) product. Returns seconds."""
+    from .ops import _glu_fwd
+    t0 = time.perf_counter()
+    dev = torch.device(device)
+    di = dev.index or 0
+    todo = sorted({gemm._bucket(M) for M in Ms if M > 0} -
+                  {k[3] for k in _SWIGLU_ON_PKG if k[:3] == (di, I, K)})
+    if not todo or not (SWIGLU_EPILOGUE and _gemm_fits(I, K)):
+        return 0.0
+    g = torch.Generator(device=dev).manual_seed(0)
+    m_max = todo[-1] * gemm.BUCKET
+    a_full = torch.randn((m_max, K), device=dev, generator=g).to(torch.float16)
+    w = (torch.randn((2 * I, K), device=dev, generator=g) * 0.02).to(torch.float16)
+    gu = torch.empty((m_max, 2 * I), device=dev, dtype=torch.float16)
+    m = torch.empty((m_max, I), device=dev, dtype=torch.float16)
+    for bk in todo:
+        M = bk * gemm.BUCKET
+        a = a_full[:M]
+        pkg = gemm._time(lambda: hgemm(a, w, 0, epi=3, swiglu_I=I, out=m[:M]), reps)
+        lib = gemm._time(lambda: _glu_fwd(gemm.mm(a, w, gemm.NT, out=gu[:M]), I, out=m[:M]),
+                         reps)
+        _SWIGLU_ON_PKG[(di, I, K, bk)] = pkg <= lib
+        if log is not None:
+            log(f"swiglu tune I={I} K={K} M={M}: package {pkg * 1e3:.1f} us, "
+                f"library pair {lib * 1e3:.1f} us")
+    del a_full, w, gu, m
+    return time.perf_counter() - t0
+
+
 def nf4_linear_swiglu(x, w, I):
     """m = fp16(silu(g) * u) of [g | u] = X W^T for the stacked gate|up weight, fp16 [M, I]."""
     fits = _gemm_fits(I, x.shape[1])
     if swiglu_fused_nf4() and fits:
         return nf4_gemm(x, w, 0, epi=3, swiglu_I=I)
-    if SWIGLU_EPILOGUE and fits:
+    if swiglu_on_package(x.device.index or 0, I, x.shape[1], x.shape[0]):
         return hgemm(x, dequantize(w), 0, epi=3, swiglu_I=I)
     from .ops import _glu_fwd
     return _glu_fwd(nf4_linear(x, w), I)
 
 
 def nf4_linear_gu(x, w):
-    """[g | u] = X W^T for the stacked gate|up weight, fp16 [M, 2 I] (kept for the backward)."""
-    if BACKEND == "dequant" and WIDE_ON_PACKAGE and _gemm_fits(w.shape[0], x.shape[1]):
-        return hgemm(x, dequantize(w), 0)
+    """[g | u] = X W^T for the stacked gate|up weight, fp16 [M, 2 I] (kept for the backward;
+    gemm.mm's tuned variant, the package's GEMM among the candidates)."""
     return nf4_linear(x, w)
 
 

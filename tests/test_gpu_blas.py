@@ -133,13 +133,76 @@ def test_mm_uses_a_tuned_split_variant(pkg):
         G.reset()
 
 
-@pytest.mark.parametrize("variant", [(0, 4), (0, 2), (0, 1)])
+def test_package_gemm_variant(pkg):
+    """The package's MFMA GEMM as a tuned variant of gemm.mm (PKG): a candidate of the tuner for
+    the NT shapes it tiles, with and without the bias, at sizes of neighbouring buckets; an
+    output it does not take (unaligned row stride) runs rocBLAS's default instead and the
+    bucket keeps its choice."""
+    G = pkg.gemm
+    G.reset()
+    try:
+        N, K = 2048, 1536
+        G.tune([(G.NT, N, K)], [700], DEV)
+        assert G.PKG in G._CANDIDATES[(0, G.NT, N, K, False)]
+        assert G.pkg_fits(G.NT, N, K) and not G.pkg_fits(G.NN, N, K)
+        assert not G.pkg_fits(G.NT, N, 200)
+        g = torch.Generator(device=DEV).manual_seed(12)
+        w = (torch.randn((N, K), device=DEV, generator=g) * 0.02).half()
+        bias = (torch.randn((N,), device=DEV, generator=g) * 0.1).half()
+        for M in (700, 1, 300, 2600):
+            for b in (None, bias):
+                G._CHOICE[(0, G.NT, N, K, b is not None, G._bucket(M))] = G.PKG
+            x = torch.randn((M, K), device=DEV, generator=g).half()
+            y = G.mm(x, w, G.NT)
+            check(y, ref(x, w, 0))
+            assert torch.equal(y, pkg.linear.hgemm(x, w, 0, splits=1))
+            check(G.mm(x, w, G.NT, bias=bias), ref(x, w, 0, bias))
+        cbuf = torch.empty((M, N + 4), device=DEV, dtype=torch.float16)
+        out = G.mm(x, w, G.NT, out=cbuf[:, :N])  # row stride N + 4: not 16-byte rows
+        check(out, ref(x, w, 0))
+        assert G._CHOICE[(0, G.NT, N, K, False, G._bucket(M))] == G.PKG
+    finally:
+        G.reset()
+
+
+def test_swiglu_tuned_choice(pkg):
+    """The forward's SwiGLU product per token bucket: tune_swiglu times the package's GEMM with
+    the SwiGLU epilogue against the library GEMM + SwiGLU kernel; either form, forced, matches
+    fp64 silu(g) u of the fp16-rounded [g | u]."""
+    G, L = pkg.gemm, pkg.linear
+    G.reset()
+    L._SWIGLU_ON_PKG.clear()
+    try:
+        I, K, M = 1024, 1536, 700
+        g = torch.Generator(device=DEV).manual_seed(13)
+        w16 = (torch.randn((2 * I, K), device=DEV, generator=g) * 0.02).half()
+        w = pkg.ops.NF4Weight(pkg.quant.quantize_nf4(w16))
+        G.tune([(G.NT, 2 * I, K)], [M], DEV)
+        L.tune_swiglu(I, K, [M], DEV)
+        assert (0, I, K, G._bucket(M)) in L._SWIGLU_ON_PKG
+        x = torch.randn((M, K), device=DEV, generator=g).half()
+        gu = (x.double() @ L.dequantize(w).double().t()).half().double()
+        gt, up = gu[:, :I], gu[:, I:]
+        want = gt * torch.sigmoid(gt) * up
+        for on_pkg in (True, False):
+            L._SWIGLU_ON_PKG[(0, I, K, G._bucket(M))] = on_pkg
+            assert L.swiglu_on_package(0, I, K, M) == on_pkg
+            m = L.nf4_linear_swiglu(x, w, I)
+            err = (m.double() - want).abs()
+            assert bool((err <= want.abs() * 2.0**-9 + 2e-3 * want.abs().max()).all())
+    finally:
+        G.reset()
+        L._SWIGLU_ON_PKG.clear()
+
+
+@pytest.mark.parametrize("variant", [(0, 4), (0, 2), (0, 1), (-2, 1)])
 @pytest.mark.parametrize("M", [2537, 37])
 def test_mm_resid_equals_mm_then_resid_add(pkg, variant, M):
     """The down projection with the residual add (gemm.mm_resid): with a split-K variant the
-    split's reduce adds the fp32 residual itself; the result equals mm() followed by the
-    residual-add kernel bit for bit (the same fp16 rounding of the product, the same fp32 add),
-    also in place (out = resid); without a split it is that two-pass form."""
+    split's reduce adds the fp32 residual itself, with the package's GEMM (-2, 1) its epilogue;
+    the result equals mm() followed by the residual-add kernel bit for bit (the same fp16
+    rounding of the product, the same fp32 add), also in place (out = resid); without a split
+    it is that two-pass form."""
     G = pkg.gemm
     G.reset()
     try:
