@@ -92,6 +92,12 @@ struct GemmArgs {
   int64_t I;             // SwiGLU: first W row of the up projection
   int kt_per_split;      // k-tiles per z-slice
   int m_tiles;
+  // fp16 B, one slice: the last round's few tiles split along K (0: none). Workgroups
+  // main_tiles .. main_tiles + tail tiles x tail_splits - 1 each form one K slice of one of the
+  // last tiles (kt_per_tail k-tiles) into tail_ws ([tile][slice][256][256] fp32), summed in
+  // slice order by tail_reduce_kernel with the epilogue.
+  int main_tiles, tail_splits, kt_per_tail;
+  float* tail_ws;
 };
 
 // ---- swizzled LDS offsets (in halves) ---------------------------------------------------------
@@ -111,8 +117,9 @@ __device__ __forceinline__ int tile_order(int b, int total) {
 
 // The workgroup's (M tile, N tile), in scalar registers: the values are the same for every
 // lane, and held in VGPRs across the main loop they cost registers the loop needs
-__device__ __forceinline__ void tile_of(int m_tiles, int64_t& tile_m, int64_t& tile_n) {
-  const int t = tile_order(blockIdx.x, gridDim.x);  // the grid is below 2^31 (host check)
+__device__ __forceinline__ void tile_of(int m_tiles, int total, int64_t& tile_m,
+                                        int64_t& tile_n) {
+  const int t = tile_order(blockIdx.x, total);  // the grid is below 2^31 (host check)
   tile_m = __builtin_amdgcn_readfirstlane(t % m_tiles);
   tile_n = __builtin_amdgcn_readfirstlane(t / m_tiles);
 }
@@ -456,7 +463,7 @@ __global__ __launch_bounds__(kThreads, 1) void nf4_gemm_kernel(GemmArgs g) {
   const int wm = wave >> 1, wn = wave & 1;
 
   int64_t tile_m, tile_n;
-  tile_of(g.m_tiles, tile_m, tile_n);
+  tile_of(g.m_tiles, gridDim.x, tile_m, tile_n);
   const int64_t m0 = tile_m * kBM;
   const int64_t kt0 = (int64_t)blockIdx.z * g.kt_per_split;
   int64_t kt1 = kt0 + g.kt_per_split;
@@ -702,26 +709,50 @@ __device__ __forceinline__ void read_frags64(Frags& f, const uint16_t* sa, const
   }
 }
 
+// Tail split, slice partials: the tile's accumulators as fp32 [256 rows][256 B columns] (B
+// column: the tile's n (SwiGLU: its gate and up rows) as the wavefront blocks hold them:
+// wn 128 + 32 j + column within the MFMA block). T: transposed accumulators (mfma_step).
+template <bool T>
+__device__ __forceinline__ void store_tail_part(float* p, const f32x16 (&acc)[4][4], int lane,
+                                                int wave) {
+  const int wm = wave >> 1, wn = wave & 1;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if constexpr (T) {  // register 4 q + e: row i 32 + l % 32, column 8 q + 4 (l / 32) + e
+        float* row = p + (wm * 128 + i * 32 + (lane & 31)) * kBN + wn * 128 + j * 32 +
+                     4 * (lane >> 5);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          *reinterpret_cast<float4*>(row + 8 * q) =
+              make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                          acc[i][j][4 * q + 3]);
+      } else {  // register r: row i 32 + 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          p[(wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * kBN + wn * 128 +
+            j * 32 + (lane & 31)] = acc[i][j][r];
+      }
+    }
+}
+
 // The GEMM with an fp16 B in memory (qlora_hgemm): the same tile, wavefront blocks, MFMA order
 // and epilogues as nf4_gemm_kernel, so the results are the same bits as that kernel's for the
 // same B values (the k-steps of 16 are accumulated in the same order).
-template <bool NN, int EPI>
-__global__ __launch_bounds__(kThreads, 1) void hgemm_kernel(GemmArgs g) {
-  __shared__ __attribute__((aligned(1024))) uint16_t sA0[kTile64];
-  __shared__ __attribute__((aligned(1024))) uint16_t sA1[kTile64];
-  __shared__ __attribute__((aligned(1024))) uint16_t sB0[kTile64];
-  __shared__ __attribute__((aligned(1024))) uint16_t sB1[kTile64];
-
+// One tile (TAIL: one K slice of a tail tile, its partial sums to g.tail_ws + tail_u tiles)
+// over k-tiles kt0 .. kt1 - 1 through the LDS stages sA0/sA1/sB0/sB1. The tail form is a
+// separate instantiation so that the main tiles' register allocation stays that of the plain
+// epilogue.
+template <bool NN, int EPI, bool TAIL>
+__device__ __forceinline__ void hgemm_tile(const GemmArgs& g, int64_t tile_m, int64_t tile_n,
+                                           int64_t kt0, int64_t kt1, int tail_u, uint16_t* sA0,
+                                           uint16_t* sA1, uint16_t* sB0, uint16_t* sB1) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
-
-  int64_t tile_m, tile_n;
-  tile_of(g.m_tiles, tile_m, tile_n);
-  const int64_t m0 = tile_m * kBM;
-  const int64_t kt0 = (int64_t)blockIdx.z * g.kt_per_split;
-  int64_t kt1 = kt0 + g.kt_per_split;
   if (kt1 > g.Kr / kBK64) kt1 = g.Kr / kBK64;  // k-tile counts are even (host check)
+  const int64_t m0 = tile_m * kBM;
   const int64_t kt_last = kt1 - 1;
 
   DmaK64 dma_a;
@@ -803,9 +834,99 @@ __global__ __launch_bounds__(kThreads, 1) void hgemm_kernel(GemmArgs g) {
     k_tile(t + 1, sA1, sB1, sA0, sB0);
   }
   __builtin_amdgcn_s_waitcnt(0);
-  if constexpr (kT) __builtin_amdgcn_s_barrier();
-  uint16_t* st = wave == 0 ? sA0 : wave == 1 ? sA1 : wave == 2 ? sB0 : sB1;
-  store_tile<EPI>(g, acc, st, st + 64 * 128, m0, tile_n, lane, wave);
+  if constexpr (TAIL) {
+    store_tail_part<kT>(g.tail_ws + (int64_t)tail_u * kBM * kBN, acc, lane, wave);
+  } else {
+    if constexpr (kT) __builtin_amdgcn_s_barrier();
+    uint16_t* st = wave == 0 ? sA0 : wave == 1 ? sA1 : wave == 2 ? sB0 : sB1;
+    store_tile<EPI>(g, acc, st, st + 64 * 128, m0, tile_n, lane, wave);
+  }
+}
+
+template <bool NN, int EPI>
+__global__ __launch_bounds__(kThreads, 1) void hgemm_kernel(GemmArgs g) {
+  __shared__ __attribute__((aligned(1024))) uint16_t sA0[kTile64];
+  __shared__ __attribute__((aligned(1024))) uint16_t sA1[kTile64];
+  __shared__ __attribute__((aligned(1024))) uint16_t sB0[kTile64];
+  __shared__ __attribute__((aligned(1024))) uint16_t sB1[kTile64];
+  // past the main tiles: one K slice of one of the last round's tiles (tail split)
+  const int tail_u = g.tail_splits > 0 ? (int)blockIdx.x - g.main_tiles : -1;
+  if (tail_u >= 0) {
+    const int t = g.main_tiles + tail_u / g.tail_splits;
+    const int64_t kt0 =
+        (int64_t)__builtin_amdgcn_readfirstlane(tail_u % g.tail_splits) * g.kt_per_tail;
+    hgemm_tile<NN, EPI, true>(g, __builtin_amdgcn_readfirstlane(t % g.m_tiles),
+                              __builtin_amdgcn_readfirstlane(t / g.m_tiles), kt0,
+                              kt0 + g.kt_per_tail, tail_u, sA0, sA1, sB0, sB1);
+    return;
+  }
+  int64_t tile_m, tile_n;
+  tile_of(g.m_tiles, g.tail_splits > 0 ? g.main_tiles : (int)gridDim.x, tile_m, tile_n);
+  const int64_t kt0 = (int64_t)blockIdx.z * g.kt_per_split;
+  hgemm_tile<NN, EPI, false>(g, tile_m, tile_n, kt0, kt0 + g.kt_per_split, -1, sA0, sA1, sB0,
+                             sB1);
+}
+
+// Tail split: the slices of each tail tile summed in slice order, then the epilogue (fp16 store,
+// bias, fp32 residual, SwiGLU), four outputs per thread.
+__global__ __launch_bounds__(256) void tail_reduce_kernel(GemmArgs g, int epi, int tiles) {
+  const bool sw = epi == kEpiSwiglu;
+  const int per_tile = sw ? kBM * 32 : kBM * 64;  // threads per tile
+  const int64_t id = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (id >= (int64_t)tiles * per_tile) return;
+  const int u = (int)(id / per_tile), w = (int)(id - (int64_t)u * per_tile);
+  const int t = g.main_tiles + u;
+  const int64_t tile_m = t % g.m_tiles, tile_n = t / g.m_tiles;
+  const float* part = g.tail_ws + (int64_t)u * g.tail_splits * kBM * kBN;
+  const int S = g.tail_splits;
+  if (sw) {
+    const int row = w >> 5, oc = (w & 31) * 4;  // four of the tile's 128 output columns
+    const int lc = (oc >> 6) * 128 + (((oc & 63) >> 5) * 32) + (oc & 31);  // gate; up: + 64
+    float4 gs = *reinterpret_cast<const float4*>(part + row * kBN + lc);
+    float4 us = *reinterpret_cast<const float4*>(part + row * kBN + lc + 64);
+    for (int k = 1; k < S; ++k) {
+      const float4 a = *reinterpret_cast<const float4*>(part + (int64_t)k * kBM * kBN +
+                                                        row * kBN + lc);
+      const float4 b = *reinterpret_cast<const float4*>(part + (int64_t)k * kBM * kBN +
+                                                        row * kBN + lc + 64);
+      gs.x += a.x; gs.y += a.y; gs.z += a.z; gs.w += a.w;
+      us.x += b.x; us.y += b.y; us.z += b.z; us.w += b.w;
+    }
+    const int64_t m = tile_m * kBM + row, n = tile_n * 128 + oc;
+    if (m >= g.M) return;
+    const float gv[4] = {gs.x, gs.y, gs.z, gs.w}, uv[4] = {us.x, us.y, us.z, us.w};
+    float mv[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float gt = h2f(f2h(gv[e])), up = h2f(f2h(uv[e]));
+      mv[e] = gt * sigmoid_fast(gt) * up;  // as store_tile
+    }
+    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(g.c) + m * g.ldc + n) =
+        make_uint2(pack2h(mv[0], mv[1]), pack2h(mv[2], mv[3]));
+    return;
+  }
+  const int row = w >> 6, lc = (w & 63) * 4;
+  float4 v4 = *reinterpret_cast<const float4*>(part + row * kBN + lc);
+  for (int k = 1; k < S; ++k) {
+    const float4 a =
+        *reinterpret_cast<const float4*>(part + (int64_t)k * kBM * kBN + row * kBN + lc);
+    v4.x += a.x; v4.y += a.y; v4.z += a.z; v4.w += a.w;
+  }
+  const int64_t m = tile_m * kBM + row, n = tile_n * kBN + lc;
+  if (m >= g.M || n >= g.N) return;  // N % 8 == 0: the four columns lie on one side
+  float v[4] = {v4.x, v4.y, v4.z, v4.w};
+  if (epi == kEpiResid) {
+    float* out = static_cast<float*>(g.c) + m * g.ldc + n;
+    const float* r = g.resid + m * g.ldr + n;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) out[e] = r[e] + h2f(f2h(v[e]));
+    return;
+  }
+  if (epi == kEpiBias)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] += h2f_bits(g.bias[n + e]);
+  *reinterpret_cast<uint2*>(static_cast<uint16_t*>(g.c) + m * g.ldc + n) =
+      make_uint2(pack2h(v[0], v[1]), pack2h(v[2], v[3]));
 }
 
 // Sum of the split-K partials [splits, M, N] and the epilogue (store / bias / residual).
@@ -874,9 +995,33 @@ bool al(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 // Shared launch path: shapes and workspace checked, then the tile grid (and the split-K reduce).
 // start/stop (may be null): recorded at the start of the tile grid and the end of the last
 // kernel.
+constexpr int kCUs = 256;  // compute units of an MI355X
+
+// Tail split of an fp16-B product in one slice: when the tiles past the GPU's last full round
+// of tiles are few (at most a quarter of a round) they would take a whole round; as K slices
+// (tail_splits of them per tile, kt_per_tail k-tiles each, an even count, no empty slice) they
+// fill about one round of short workgroups instead. Returns the fp32 workspace elements it
+// needs, 0 when it does not apply.
+int64_t tail_plan(int64_t m_tiles, int64_t n_tiles, int64_t ktiles, int* main_tiles, int* splits,
+                  int* kt_per) {
+  const int64_t tiles = m_tiles * n_tiles, full = tiles / kCUs * kCUs, r = tiles - full;
+  if (full == 0 || r == 0 || r > kCUs / 4) return 0;
+  for (int sp = 16; sp >= 2; --sp) {
+    const int64_t per = qlora_cdiv(qlora_cdiv(ktiles, sp), 2) * 2;
+    if (r * sp > kCUs || per * (sp - 1) >= ktiles) continue;
+    *main_tiles = (int)full;
+    *splits = sp;
+    *kt_per = (int)per;
+    return r * sp * kBM * kBN;
+  }
+  return 0;
+}
+
+int64_t n_tiles_of(int64_t N, int epi) { return epi == kEpiSwiglu ? N / 128 : qlora_cdiv(N, kBN); }
+
 int run_gemm(GemmArgs& g, int bsrc, int mode, int epi, int splits, float* ws, int64_t ws_elems,
              hipStream_t s, hipEvent_t start = nullptr, hipEvent_t stop = nullptr) {
-  const int64_t n_tiles = epi == kEpiSwiglu ? g.N / 128 : qlora_cdiv(g.N, kBN);
+  const int64_t n_tiles = n_tiles_of(g.N, epi);
   g.m_tiles = (int)qlora_cdiv(g.M, kBM);
   const int64_t grid = (int64_t)g.m_tiles * n_tiles;
   QLORA_CHECK_ARG(grid < (1ll << 31));
@@ -890,6 +1035,29 @@ int run_gemm(GemmArgs& g, int bsrc, int mode, int epi, int splits, float* ws, in
   QLORA_CHECK_ARG(ktiles % per_trip == 0);
   g.kt_per_split = (int)(qlora_cdiv(qlora_cdiv(ktiles, splits), per_trip) * per_trip);
   QLORA_CHECK_ARG((int64_t)g.kt_per_split * (splits - 1) < ktiles);  // no empty slice
+  int main_t = 0, tail_s = 0, kt_tail = 0;
+  const int64_t tail_need = bsrc == kBHalf && splits == 1 && ws != nullptr
+                                ? tail_plan(g.m_tiles, n_tiles, ktiles, &main_t, &tail_s, &kt_tail)
+                                : 0;
+  if (tail_need > 0 && ws_elems >= tail_need && al(ws, 16)) {
+    g.main_tiles = main_t;
+    g.tail_splits = tail_s;
+    g.kt_per_tail = kt_tail;
+    g.tail_ws = ws;
+    const int64_t r = grid - main_t;
+    const dim3 tg((unsigned)(main_t + r * tail_s));
+    if (mode == 0) launch_epi<false, kBHalf>(g, tg, s, epi, start, nullptr);
+    else launch_epi<true, kBHalf>(g, tg, s, epi, start, nullptr);
+    if (int rc = qlora_launch_status()) return rc;
+    const int64_t threads = r * (epi == kEpiSwiglu ? kBM * 32 : kBM * 64);
+    const dim3 rg((unsigned)qlora_cdiv(threads, 256));
+    if (stop != nullptr)
+      hipExtLaunchKernelGGL(tail_reduce_kernel, rg, dim3(256), 0, s, nullptr, stop, 0, g, epi,
+                            (int)r);
+    else
+      hipLaunchKernelGGL(tail_reduce_kernel, rg, dim3(256), 0, s, g, epi, (int)r);
+    return qlora_launch_status();
+  }
   const int kepi = splits > 1 ? (int)kEpiPartial : epi;
   void* out = g.c;
   if (splits > 1) g.c = ws;
@@ -1056,4 +1224,19 @@ QLORA_API int qlora_hgemm(const void* a, int64_t lda, const void* b, int64_t ldb
                           void* stream) {
   return qlora_hgemm_timed(a, lda, b, ldb, M, N, K, mode, c, ldc, bias, resid, ldr, epi,
                            swiglu_I, splits, ws, ws_elems, stream, nullptr, nullptr);
+}
+
+QLORA_API int qlora_hgemm_workspace(int64_t M, int64_t N, int64_t K, int32_t epi, int32_t splits,
+                                    int64_t* elems) {
+  QLORA_CHECK_ARG(elems && M >= 0 && N > 0 && K > 0 && splits >= 1 && epi >= 0 && epi <= 3);
+  *elems = 0;
+  if (splits > 1) {
+    *elems = (int64_t)splits * M * N;
+    return 0;
+  }
+  if (M == 0 || K % (kStages * kBK) != 0) return 0;
+  int main_t, tail_s, kt_tail;
+  *elems = tail_plan(qlora_cdiv(M, kBM), n_tiles_of(N, epi), K / kBK64, &main_t, &tail_s,
+                     &kt_tail);
+  return 0;
 }

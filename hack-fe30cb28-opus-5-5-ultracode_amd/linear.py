@@ -14,6 +14,7 @@ counts where it was timed faster than the library GEMM and the SwiGLU kernel (SW
 tune_swiglu).
 """
 
+import ctypes
 import time
 
 import torch
@@ -170,9 +171,28 @@ def nf4_gemm(a, w, mode, epi=0, bias=None, resid=None, out=None, swiglu_I=0, spl
     return out
 
 
-def hgemm(a, b, mode, epi=0, bias=None, resid=None, out=None, swiglu_I=0, splits=None):
+_HGEMM_WS = {}  # (M, N, K, epi, splits) -> fp32 workspace elements qlora_hgemm uses
+# qlora_hgemm in one slice runs a last, nearly empty round of tiles as K slices (default of
+# hgemm's `tail`)
+HGEMM_TAIL = True
+
+
+def hgemm_workspace(M, N, K, epi, splits):
+    """fp32 elements of qlora_hgemm's workspace for this problem (qlora_hgemm_workspace)."""
+    key = (M, N, K, epi, splits)
+    n = _HGEMM_WS.get(key)
+    if n is None:
+        c = ctypes.c_int64(0)
+        _lib.call("qlora_hgemm_workspace", M, N, K, epi, splits, ctypes.byref(c))
+        n = _HGEMM_WS[key] = c.value
+    return n
+
+
+def hgemm(a, b, mode, epi=0, bias=None, resid=None, out=None, swiglu_I=0, splits=None,
+          tail=None):
     """The MFMA GEMM with an fp16 B (qlora_hgemm): mode 0 C = A B^T (B [N, K]), mode 1 C = A B
-    (B [K, N]); epilogues as nf4_gemm."""
+    (B [K, N]); epilogues as nf4_gemm. tail: with one slice, the tiles of a last, nearly empty
+    round of the GPU run as K slices through a workspace (False: whole; None: HGEMM_TAIL)."""
     dev = a.device
     a = _a16(a)
     _need(b, "b", torch.float16, dev, contiguous=False)
@@ -194,8 +214,9 @@ def hgemm(a, b, mode, epi=0, bias=None, resid=None, out=None, swiglu_I=0, splits
     if M == 0:
         return out
     splits = split_k(M, n_out, K, epi) if splits is None else splits
-    ws = torch.empty((splits * M * n_out,), device=dev, dtype=torch.float32) if splits > 1 \
-        else None
+    tail = HGEMM_TAIL if tail is None else tail
+    n_ws = hgemm_workspace(M, n_out, K, epi, splits) if splits > 1 or tail else 0
+    ws = torch.empty((n_ws,), device=dev, dtype=torch.float32) if n_ws else None
     _lib.call("qlora_hgemm", _ptr(a), a.stride(0), _ptr(b), b.stride(0), M, n_out, K, mode,
               _ptr(out), out.stride(0), _ptr(bias), _ptr(resid), ldr, epi, swiglu_I, splits,
               _ptr(ws), 0 if ws is None else ws.numel(), _stream(dev))

@@ -277,7 +277,11 @@ int qlora_nf4_gemm(const void* a, int64_t lda, const void* packed, const float* 
 /*
  * The same GEMM with an fp16 B operand in memory (the dequantized projections; the lm_head):
  *   mode 0 (NT): C[M, N] = A[M, K] B^T, B [N, K] (ldb);  mode 1 (NN): C = A B, B [K, N] (ldb).
- * epi, splits, ws as qlora_nf4_gemm (epi 3: B = [gate; up] rows, N = I).
+ * epi, splits, ws as qlora_nf4_gemm (epi 3: B = [gate; up] rows, N = I). With splits == 1 a
+ * 16-byte aligned ws of at least qlora_hgemm_workspace's elements lets the few tiles of a last,
+ * nearly empty round of the GPU run as K slices (partials in ws, summed in a fixed order, then
+ * the epilogue); a null or smaller ws runs them whole (results then differ in the fp32
+ * summation order of those tiles only).
  * Replaces the cuBLAS products of the frozen projections after dequant (engine.py:1082, 1112,
  * 1163, 1179, 1239, 1293, 1301, 1316) and of the lm_head (engine.py:1376-1381).
  * Requires: K % 128 == 0; mode 1: N % 256 == 0; mode 0: N % 8 == 0 (epi 3: N % 128 == 0);
@@ -289,8 +293,16 @@ int qlora_hgemm(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t 
                 float* ws, int64_t ws_elems, void* stream);
 
 /*
+ * fp32 workspace elements (*elems) qlora_hgemm uses for this problem: splits * M * N with
+ * splits > 1; with one slice the K-sliced last round's partials, 0 when that does not apply.
+ * N as qlora_hgemm's (epi 3: I). No reference counterpart (sizes the caller's workspace).
+ */
+int qlora_hgemm_workspace(int64_t M, int64_t N, int64_t K, int32_t epi, int32_t splits,
+                          int64_t* elems);
+
+/*
  * qlora_hgemm that also records start/stop (hipEvent_t created with timing, or null) at the start
- * of its tile grid and the end of its last kernel (the split-K reduce when splits > 1), the
+ * of its tile grid and the end of its last kernel (the split-K or K-sliced-tail reduce), the
  * dispatches' own timestamps. No reference counterpart: the bench's per-launch timing of the
  * step's own MFMA GEMM.
  */

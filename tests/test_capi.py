@@ -120,3 +120,31 @@ def test_gemm_splitk_rejects_bad_problems(pkg):
                                   (4, 8, 64, 1, 1 << 20), (4, 8, 64, 2, 10)):
         assert lib.qlora_gemm_splitk(1, M, N, K, 16, K, 16, N, 16, N, None, splits, 16, work, 0,
                                      None) == 1
+
+
+def test_hgemm_workspace_sizes(pkg):
+    """qlora_hgemm_workspace (host only): splits x M x N with split-K; with one slice the
+    K-sliced last round's partials when at most 64 tiles are left past the last full round of
+    256 (the largest slice count that fits that round with no empty slice), else 0."""
+    import ctypes
+    lib = pkg._lib.load()
+
+    def ws(M, N, K, epi, splits):
+        n = ctypes.c_int64(-1)
+        assert lib.qlora_hgemm_workspace(M, N, K, epi, splits, ctypes.byref(n)) == 0
+        return n.value
+
+    tile = 256 * 256
+    assert ws(700, 2048, 1536, 0, 4) == 4 * 700 * 2048
+    # SwiGLU, I = 8960 (70 tiles per 256 rows): 2,600 rows -> 770 tiles, 2 past 768; 24 k-tiles
+    # of 64: 12 slices of 2 (16 slices would leave some empty)
+    assert ws(2600, 8960, 1536, 3, 1) == 2 * 12 * tile
+    assert ws(2560, 8960, 1536, 3, 1) == 0  # 700 tiles: 188 past 512, more than a quarter
+    assert ws(300, 8960, 1536, 3, 1) == 0   # 140 tiles: no full round
+    # 2,048 columns (8 tiles per 256 rows), 33 row tiles -> 264 tiles, 8 past 256: 16 slices
+    # would leave empty ones with 24 k-tiles, 12 of 2 fit (8 x 12 <= 256)
+    assert ws(8348, 2048, 1536, 0, 1) == 8 * 12 * tile
+    assert ws(8348, 2048, 16384, 0, 1) == 8 * 16 * tile  # 256 k-tiles: 16 slices of 16
+    assert ws(0, 2048, 1536, 0, 1) == 0
+    assert lib.qlora_hgemm_workspace(4, 8, 128, 0, 0, ctypes.byref(ctypes.c_int64())) == 1
+    assert lib.qlora_hgemm_workspace(4, 8, 128, 0, 1, None) == 1

@@ -228,6 +228,51 @@ def test_tile_major_order_equals_bnb_order(pkg, epi):
     assert torch.equal(torch.sort(scales).values, torch.sort(w.block_scales()).values)
 
 
+@pytest.mark.parametrize("mode,epi", [(0, 0), (0, 1), (0, 2), (0, 3), (1, 0), (1, 2)])
+def test_fp16_b_gemm_tail_slices(pkg, mode, epi):
+    """One slice with a last round of at most 64 tiles: qlora_hgemm given its workspace runs those
+    tiles as K slices (partials summed in slice order, then the epilogue). The tail tiles agree
+    with fp64 to fp16 rounding, every other output is the same bits as without the workspace
+    (all tiles whole), for every epilogue and both orientations."""
+    L = pkg.linear
+    g = torch.Generator(device=DEV).manual_seed(40 + 10 * mode + epi)
+    if epi == 3:  # SwiGLU, I = 8960: 2,600 rows -> 770 tiles, tiles 768-769 sliced
+        M, N, K, I = 2600, 8960, 1536, 8960
+        w = (torch.randn(2 * I, K, generator=g, device=DEV) * 0.02).half()
+        tail_rows, tail_cols = slice(2304, M), slice(69 * 128, N)
+    else:  # 2,048 columns, 8,348 rows -> 264 tiles, tiles 256-263 (column tile 7) sliced
+        M, N, K = 8348, 2048, 1536
+        w = (torch.randn(*((N, K) if mode == 0 else (K, N)), generator=g, device=DEV) *
+             0.02).half()
+        tail_rows, tail_cols = slice(25 * 256, M), slice(7 * 256, N)
+    assert L.hgemm_workspace(M, N, K, epi, 1) > 0
+    a = torch.randn(M, K, generator=g, device=DEV).half()
+    kw = {"splits": 1}
+    if epi == 1:
+        kw["bias"] = (torch.randn(N, generator=g, device=DEV) * 0.1).half()
+    if epi == 2:
+        kw["resid"] = torch.randn(M, N, generator=g, device=DEV)
+    if epi == 3:
+        kw["swiglu_I"] = I
+    sliced = L.hgemm(a, w, mode, epi=epi, tail=True, **kw)
+    whole = L.hgemm(a, w, mode, epi=epi, tail=False, **kw)
+    outside = torch.ones(M, N, dtype=torch.bool, device=DEV)
+    outside[tail_rows, tail_cols] = False
+    assert torch.equal(sliced[outside], whole[outside])
+    assert not torch.equal(sliced, whole)  # the sliced tiles sum in another order
+    prod = a.double() @ (w.double().t() if mode == 0 else w.double())
+    if epi == 3:
+        gt, up = prod[:, :I].half().double(), prod[:, I:].half().double()
+        want = gt * torch.sigmoid(gt) * up
+    else:
+        want = prod + (kw["bias"].double() if epi == 1 else 0)
+        if epi == 2:
+            want = kw["resid"].double() + prod.half().double()
+    got, want = sliced[tail_rows, tail_cols].double(), want[tail_rows, tail_cols]
+    err = (got - want).abs()
+    assert bool((err <= want.abs() * 2.0**-9 + 2e-3 * want.abs().max()).all())
+
+
 @pytest.mark.parametrize("splits", [1, 2])
 def test_hgemm_timed_form(pkg, splits):
     """qlora_hgemm_timed gives qlora_hgemm's output bit for bit and records its two events
