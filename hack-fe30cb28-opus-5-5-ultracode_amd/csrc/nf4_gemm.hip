@@ -51,7 +51,10 @@
 //
 // Work order: workgroup ids are dealt to the 8 XCDs in turn; tile_order gives each XCD a
 // contiguous range of tiles (the M tiles of a few N tiles), so an XCD's L2 holds the B tiles it
-// reads and the A tiles are shared through the MALL.
+// reads and the A tiles are shared through the MALL. fp16 B in one slice: when at most 64 tiles
+// are left past the last full round of the 256 CUs, the same launch runs them as K slices
+// (tail_plan; fp32 partials in the caller's workspace, tail_reduce_kernel sums them in slice
+// order with the epilogue), so the last round is short instead of a whole tile long.
 #include "nf4.h"
 
 #include <hip/hip_ext.h>
