@@ -13,7 +13,9 @@
  *     csrc/blaslt.hip);
  *   - one second stream and two events per device (csrc/attn.hip), on which the attention
  *     backward runs dK/dV beside dQ; it is forked from and joined back into the caller's stream
- *     inside the call, so the call is ordered on the caller's stream as any other.
+ *     inside the call, so the call is ordered on the caller's stream as any other;
+ *   - the 16 MiB static device array of qlora_lora_grad_noalloc (csrc/lora.hip), one per device
+ *     for the life of the process, and its address per device.
  * Entry points are callable from any thread; the state above is created under a lock.
  * n == 0 (rows, tokens, blocks) is a no-op that returns 0, as the reference skips such launches.
  *
