@@ -12,7 +12,8 @@ Beside it, on the same JSON line:
   keep_all       the same step with every layer keeping its intermediates (no recompute)
   roofline       the step's largest hand-written kernel by time, the package's MFMA GEMM
                  (hgemm_kernel: the gate|up forward with the SwiGLU epilogue), 2 M N K flops
-                 over the dispatch-recorded duration, against the fp16 MFMA peak
+                 over the dispatch-recorded duration, against the fp16 MFMA peak, over the
+                 launches of four extra untimed steps (four batches' token counts)
   roofline_dequant  the step's NF4 dequant launches (the north star's dequant GB/s)
   roofline_mfma  the attention kernels against the fp16 MFMA peak (algorithmic flops of the
                  batch's causal pairs) and the step's library GEMMs
@@ -176,17 +177,17 @@ def causal_pairs(lengths):
     return sum(L * (L + 1) // 2 for L in lengths)
 
 
-def measure_step_kernels(pkg, trainer, batch, cfg):
-    """One extra (untimed) step with HIP events around every launch of the dequant, the
-    attention and the GEMM entry points: the dequant's achieved GB/s (dispatch-recorded events),
-    the attention forward / backward TFLOP/s on the batch's causal pairs (fwd: QK^T and PV, 4 D
-    flops per pair and head; bwd: S, dP, dQ, dK, dV, 10 D flops per pair and head), and the
-    library GEMMs' TFLOP/s (2 M N K a product): all of the step's library projection and lm_head
-    products, the library's gate|up forward if any, and the package's own MFMA GEMM (the
-    gate|up forward products: with the SwiGLU epilogue in the forward pass, [g | u] kept in the
-    recompute; the largest MFMA kernel of the step)."""
+def measure_step_kernels(pkg, trainer, batches, cfg):
+    """Extra (untimed) steps, one per batch given (token counts spread as the timed steps'),
+    with HIP events around every launch of the dequant, the attention and the GEMM entry points:
+    the dequant's achieved GB/s (dispatch-recorded events), the attention forward / backward
+    TFLOP/s on each batch's causal pairs (fwd: QK^T and PV, 4 D flops per pair and head; bwd: S,
+    dP, dQ, dK, dV, 10 D flops per pair and head), and the library GEMMs' TFLOP/s (2 M N K a
+    product): all of the step's library projection and lm_head products, the library's gate|up
+    forward if any, and the package's own MFMA GEMM (the gate|up forward products with the
+    SwiGLU epilogue; the largest MFMA kernel of the step). Rates are total work over total
+    launch time across the steps."""
     P = pkg.profiling
-    pairs = causal_pairs(batch[5]["lengths"])
     heads, D = cfg.num_attention_heads, cfg.head_dim
     fwd = P.LaunchTimer("qlora_attn_fwd_split", bound="mfma")
     bwd = P.LaunchTimer("qlora_attn_bwd_split", bound="mfma")
@@ -195,15 +196,20 @@ def measure_step_kernels(pkg, trainer, batch, cfg):
     gemms = [P.LaunchTimer(e, work=flops, bound="mfma")
              for e in ("qlora_gemm", "qlora_gemm_splitk", "qlora_gemmlt")]
     own = P.LaunchTimer(P.DOMINANT, bound="mfma", work=P.hgemm_flops, nbytes=P.hgemm_bytes)
+    work_f = work_b = 0.0
     with contextlib.ExitStack() as stack:
         for t in (dq, fwd, bwd, *gemms, own):
             stack.enter_context(t)
-        trainer.step(batch)
+        for batch in batches:
+            pairs = causal_pairs(batch[5]["lengths"])
+            n_f, n_b = len(fwd.records), len(bwd.records)
+            trainer.step(batch)
+            work_f += 4.0 * D * heads * pairs * (len(fwd.records) - n_f)
+            work_b += 10.0 * D * heads * pairs * (len(bwd.records) - n_b)
     torch.cuda.synchronize()
-    n_f, n_b = len(fwd.records), len(bwd.records)
     gate_up = 2 * cfg.intermediate_size
-    out = [dict(fwd.summary(work_total=4.0 * D * heads * pairs * n_f), kernel="attn_fwd_kernel"),
-           dict(bwd.summary(work_total=10.0 * D * heads * pairs * n_b),
+    out = [dict(fwd.summary(work_total=work_f), kernel="attn_fwd_kernel"),
+           dict(bwd.summary(work_total=work_b),
                 kernel="attn_delta + attn_dq + attn_dkdv kernels")]
     every = gemms[0].summary(also=gemms[1:])
     if every is not None:
@@ -552,7 +558,7 @@ def main():
     sizes = range(4 * 256, 4 * 1024 + pkg.gemm.BUCKET, pkg.gemm.BUCKET)
     if args.profile:
         sizes = sorted({int(b[4]) for b in batches[:args.warmup + args.steps]} |
-                       {int(batches[-1][4])})
+                       {int(b[4]) for b in batches[-4:]})
         args.no_cpu, args.no_configs, args.keep_steps = True, True, 0
     tune_s = model.tune_gemms(sizes, log=log)
     cpu_model = None
@@ -571,7 +577,7 @@ def main():
     if not args.profile:
         _, _, rest = time_steps(trainer, batches, done, max(0, CURVE_STEPS - done))
     curve = (warm_losses + timed_losses + rest)[:CURVE_STEPS]
-    kernels = measure_step_kernels(pkg, trainer, batches[-1], cfg)
+    kernels = measure_step_kernels(pkg, trainer, batches[-4:], cfg)
     keep = None
     if args.keep_steps > 0 and args.policy != "keep":
         model.keep_all = True

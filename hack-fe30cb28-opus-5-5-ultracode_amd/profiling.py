@@ -26,12 +26,13 @@ DEQUANT = "qlora_nf4_dequant_many"
 # step's launches), each divided by what the counter reads for a plain device copy of 1 GiB
 # (512 MiB each way; FETCH 0.50004, WRITE 1.000 of the bytes moved):
 # (11,892.4 / 0.50004 + 91,392) KiB per launch = 1.0018 x the algorithmic 117,728,444 B.
-# The package GEMM's SwiGLU launch (hgemm_kernel<NT, SwiGLU>) at the M = 1,875 batch the bench
-# measures: (95,837 / 0.50004 + 32,812) KiB per launch = 2.435 x the algorithmic bytes (A, the
-# [gate; up] weight and the output once each); 2.78 at M = 2,325, 2.86 at M = 2,614. The
-# excess is the A tile re-read by each XCD and B tiles re-read past the 4 MB L2 (FETCH_SIZE
-# counts what leaves the L2, Infinity Cache hits included).
-TRAFFIC_RATIO = {"qlora_nf4_dequant_many": 1.0018, "qlora_hgemm": 2.435}
+# The package GEMM's SwiGLU launches (hgemm_kernel<NT, SwiGLU>, with the reduce of a K-sliced
+# last round where there is one) over the step dispatches of the bench's four measuring
+# batches: 2.92 x the algorithmic bytes (A, the [gate; up] weight and the output once each),
+# weighted by launch; 2.74 at 9 row tiles, 2.78 at 10, 2.97 at 11 (sliced tail), 3.44 at 12.
+# The excess is the A tile re-read by each XCD and B tiles re-read past the 4 MB L2
+# (FETCH_SIZE counts what leaves the L2, Infinity Cache hits included).
+TRAFFIC_RATIO = {"qlora_nf4_dequant_many": 1.0018, "qlora_hgemm": 2.92}
 
 
 def _dequant_bytes(args):
