@@ -223,11 +223,19 @@ int launch(Args& a, int r, hipStream_t stream) {
   for (int i = 0; i < 2; ++i)
     if (a.job[i].Y != nullptr)
       chunks = (int)std::max<int64_t>(chunks, qlora_cdiv(a.job[i].M2, kChunkCols));
-  // the chunks of a row go to separate workgroups while the launch stays within one workgroup
-  // per CU (256 on MI355X); a fuller launch keeps them together
+  // the chunks of a row go to separate workgroups while the workgroups that have work stay
+  // within one per CU (256 on MI355X: a job with fewer chunks leaves its later groups empty,
+  // and those return at once); a fuller launch keeps them together
   const int64_t rows = qlora_cdiv(a.n, kTok);
+  auto working = [&](int g) {
+    const int64_t per = qlora_cdiv(chunks, g);  // chunks per workgroup
+    int64_t w = 0;
+    for (int i = 0; i < 2; ++i)
+      w += rows * qlora_cdiv(a.job[i].Y ? qlora_cdiv(a.job[i].M2, kChunkCols) : 1, per);
+    return w;
+  };
   int groups = chunks;
-  while (groups > 1 && rows * 2 * groups > kCUs) --groups;
+  while (groups > 1 && working(groups) > kCUs) --groups;
   a.cpw = (int)qlora_cdiv(chunks, groups);
   groups = (int)qlora_cdiv(chunks, a.cpw);
   const dim3 grid((unsigned)rows, 2, (unsigned)groups), block(64 * kWaves);

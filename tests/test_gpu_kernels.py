@@ -575,7 +575,7 @@ def test_lora_bwd_rows(pkg, n, H, Nq, Nv, r=16):
 
 @pytest.mark.parametrize("n,H,Nq,Nv", [(300, 1536, 1536, 256), (1, 1536, 1536, 256),
                                        (77, 256, 256, 128), (4100, 896, 896, 128),
-                                       (33, 3584, 3584, 512)])
+                                       (33, 3584, 3584, 512), (2540, 1536, 1536, 256)])
 def test_lora_fwd_rows(pkg, n, H, Nq, Nv, r=16):
     """x = fp16(a A^T), l = fp16(x B^T) for both adapters (engine.py:1088-1093) against fp64 of
     the same roundings."""
