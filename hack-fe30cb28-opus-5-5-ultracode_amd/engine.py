@@ -353,6 +353,7 @@ class Packed:
         self.targets = torch.where(real, nxt, torch.full_like(nxt, -100)).reshape(-1)
         self.head_order = torch.argsort((self.targets < 0).to(torch.int8), stable=True)
         self.n_supervised = n
+        self.sup_upper_bound = True  # n_supervised counts ignored tokens too
         right = torch.arange(T, device=dev)[None, :] < real.sum(dim=1, keepdim=True)
         self.metadata_ok = (real == right).all()
         if ctr_base is not None:
@@ -386,6 +387,7 @@ class Packed:
         self.head_order = torch.argsort(unsupervised.to(torch.int8), stable=True)
         counted = (n - unsupervised.sum()) if n_supervised is None or given else None
         self.n_supervised = int(counted) if n_supervised is None else int(n_supervised)
+        self.sup_upper_bound = False
         self.metadata_ok = None
         if given:
             cu = index[3 * n:]
@@ -622,9 +624,10 @@ class _Head(torch.autograd.Function):
     The loss is linear in the per-token losses, so its gradient w.r.t. h is formed during the
     forward and the backward only scales it. Tokens are taken in packed.head_order (supervised
     first). Per slab of at most `chunk` tokens: one GEMM forms the logits, the CE kernel
-    reduces each row and overwrites it with softmax - onehot (zeros for unsupervised tokens),
-    and the slab's supervised rows alone go through G E and the norm's backward (scaled by
-    1/denom); the other rows' gradient is zero."""
+    reduces each row and overwrites it with softmax - onehot (the rows of ignored tokens with
+    zeros, or left as they are when n_supervised is exact), and the slab's first n_supervised
+    rows alone go through G E and the norm's backward (scaled by 1/denom); the other rows'
+    gradient is zero."""
 
     @staticmethod
     def forward(ctx, h, norm_w, eps, lm_w, packed, denom, stats, chunk):
@@ -649,8 +652,12 @@ class _Head(torch.autograd.Function):
         for lo in range(0, n, chunk):
             hi = min(n, lo + chunk)
             logits = L.linear(hn[lo:hi], lm_w)
+            # with an exact supervised count the rows of ignored tokens are never read again
+            # (G E takes the first n_sup rows, the supervised ones): the CE kernel leaves them
+            # instead of writing zeros; with an upper bound (device-only packing) they are
+            # zeroed, as G E then reads some of them
             _ce(logits, targets[lo:hi], tok_loss[lo:hi], entropy[lo:hi], correct[lo:hi],
-                zero_unsupervised=lo < n_sup)
+                zero_unsupervised=packed.sup_upper_bound)
             top = min(hi, n_sup)
             if top > lo:
                 g_hn = L.linear_t(logits[:top - lo], lm_w)

@@ -524,6 +524,32 @@ def test_piece_kernels_match_ce_kernel(pkg, n, n_prompt):
         assert err_b < 1e-3 and err_b <= 1.5 * err_a + 1e-6, (err_a.item(), err_b.item())
 
 
+@pytest.mark.parametrize("V", [151936, 5000])
+def test_ce_leaves_unsupervised_rows(pkg, V):
+    """zero_unsupervised=False (the step's head, whose dh product reads the supervised rows
+    only): the statistics and the supervised rows' gradient are those of the zeroing form bit
+    for bit, and the rows of ignored tokens keep their logits."""
+    n = 300
+    g = torch.Generator().manual_seed(V)
+    targets = torch.randint(0, V, (n,), generator=g)
+    targets[::3] = -100
+    targets = targets.to(DEV)
+    logits = (torch.randn(n, V, generator=g) * 3).half().to(DEV)
+    out = {}
+    for zero in (True, False):
+        work = logits.clone()
+        st = (torch.empty(n, device=DEV), torch.empty(n, device=DEV),
+              torch.empty(n, device=DEV, dtype=torch.int32))
+        pkg.ops._ce(work, targets, *st, zero_unsupervised=zero)
+        out[zero] = (work, *st)
+    sup = targets >= 0
+    for a, b in zip(out[True][1:], out[False][1:]):
+        assert torch.equal(a, b)
+    assert torch.equal(out[True][0][sup], out[False][0][sup])
+    assert torch.equal(out[False][0][~sup], logits[~sup])
+    assert not out[True][0][~sup].any()
+
+
 def test_ce_kernels_take_the_target_logit_before_the_row_is_overwritten(pkg):
     """Over many launches every token's loss is logsumexp - its target's logit
     (test_host_head.py:91-125: the in-place gradient write must not race the target read)."""
