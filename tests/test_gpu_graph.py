@@ -14,8 +14,8 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
-def _tiny(pkg, layers=2, dropout=0.05, H=256, HQ=4, HKV=2, D=64, r=16):
-    cfg = pkg.engine.Qwen2Config(hidden_size=H, intermediate_size=640, num_hidden_layers=layers,
+def _tiny(pkg, layers=2, dropout=0.05, H=256, HQ=4, HKV=2, D=64, r=16, I=640):
+    cfg = pkg.engine.Qwen2Config(hidden_size=H, intermediate_size=I, num_hidden_layers=layers,
                                  num_attention_heads=HQ, num_key_value_heads=HKV, head_dim=D,
                                  vocab_size=3000, lora_dropout=dropout, lora_r=r,
                                  lora_alpha=2 * r)
@@ -115,3 +115,35 @@ def test_graph_replay_equals_eager_padded_step(pkg, keep_all):
             assert torch.equal(a, b)
     with pytest.raises(ValueError):
         graph.replay(ids[:, :32], mask[:, :32], labels[:, :32], 1.0)
+
+
+def test_graph_replay_with_k_sliced_gemm_tail(pkg):
+    """The forward's SwiGLU product on the package GEMM with a K-sliced last round (I = 8960:
+    70 column tiles; 4 x 256 tokens: 280 tiles, the 24 past the first round of 256 CUs in K
+    slices through a workspace) captured and replayed equals the eager padded step bit for
+    bit."""
+    model = _tiny(pkg, I=8960)
+    B, T = 4, 256
+    M, I, H = B * T, 8960, 256
+    assert pkg.linear.hgemm_workspace(M, I, H, 3, 1) > 0
+    torch.cuda.manual_seed(7)
+    graph = pkg.engine.StepGraph(model, B, T)
+    gen = model.dropout.gen
+    params = model.parameters()
+    lengths = [256, 200, 100, 256]
+    ids, mask, labels = (t.to(DEV) for t in _batch(lengths, T, model.cfg.vocab_size, 21))
+    denom = float((labels[:, 1:] != -100).sum())
+    offset = gen.get_offset()
+    _clear(model)
+    loss_e, _, _ = model.step(ids, mask, labels, torch.tensor(denom, device=DEV), padded=True)
+    (loss_e * torch.tensor(8.0, device=DEV)).backward()
+    g_e = _grads(model)
+    loss_e = loss_e.detach().clone()
+    torch.cuda.synchronize()
+    gen.set_offset(offset)
+    _clear(model)
+    loss_g = graph.replay(ids, mask, labels, denom, 8.0)
+    torch.cuda.synchronize()
+    assert torch.equal(loss_g, loss_e), (loss_g.item(), loss_e.item())
+    for a, b in zip([p.grad for p in params], g_e):
+        assert torch.equal(a, b)
