@@ -131,6 +131,9 @@ __global__ __launch_bounds__(64 * kWaves) void lora_rows_kernel(Args a) {
 #pragma unroll
       for (int t = 0; t < NT1; ++t) wb[i][t] = ld8(wrow[t] + 16 * ks);
     }
+    // keep every load of the chunk ahead of its MFMAs: left alone, the scheduler sinks each
+    // load next to its MFMA and the wavefront waits out one memory round trip per k-step
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < CH1; ++i)
 #pragma unroll
