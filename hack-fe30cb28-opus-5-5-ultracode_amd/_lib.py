@@ -22,6 +22,7 @@ SIGNATURES = {
     "qlora_nf4_dequant_many": [I32, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P],
     "qlora_nf4_dequant_many_timed": [I32, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P],
     "qlora_dropout_keep": [P, I64, I64, I64, I64, F32, I32, P],
+    "qlora_dropout_keep_below": [F32, P],
     "qlora_rms_fwd": [P, P, P, I32, P, P, P, P, P, P, I64, I64, F32, F32, F32, I64, I64, I64,
                       I64, I32, I32, I32, I32, I32, P, P, P],
     "qlora_rms_bwd": [P, P, P, P, P, P, I32, P, P, P, P, I64, I64, I64, F32, F32, I64, I64,

@@ -311,11 +311,22 @@ __global__ __launch_bounds__(kWave* kRowsPerBlock) void rms_fwd4_kernel(RmsFwdAr
     DropParams dq = a.drop, dv = a.drop;
     dq.ctr = mask_ctr(a.ctr_q, a.ctr_base);
     dv.ctr = mask_ctr(a.ctr_v, a.ctr_base);
+    // element groups of the lane's NV quads, g0 + step i: one division for both masks and
+    // every quad (a launch over at least one row has G >= 256 NV > step (NV - 1) threads, so
+    // the thread index wraps at most once; the loop also takes any smaller G)
+    const uint32_t e_first = tok_e + 4u * (uint32_t)lane;
+    const uint32_t g0 = e_first >> vs, step = 64u >> (vs - 2);
+    const uint32_t sub = (e_first & ((1u << vs) - 1)) >> 2;
+    uint32_t it = g0 / G32, th = g0 - it * G32;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
-      const uint32_t e0 = tok_e + 4u * (uint32_t)(lane + 64 * i);
-      kq[i] = !a.yq ? 0u : all ? 0xFu : drop_keep4_u32(dq, e0, G32, vs);
-      kv[i] = !a.yv ? 0u : all ? 0xFu : drop_keep4_u32(dv, e0, G32, vs);
+      kq[i] = !a.yq ? 0u : all ? 0xFu : drop_keep4_at(dq, it, th, vs, sub);
+      kv[i] = !a.yv ? 0u : all ? 0xFu : drop_keep4_at(dv, it, th, vs, sub);
+      th += step;
+      while (th >= G32) {
+        th -= G32;
+        ++it;
+      }
     }
     if (a.keep) {
       const int64_t kb = a.H / 4;
@@ -565,6 +576,24 @@ void launch_nv(int nv, dim3 g, hipStream_t s, const Args& a) {
 
 bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 
+// The smallest Philox word r whose uniform 2^-32 + r 2^-32 (fp32, as the kernels and rocRAND's
+// uniform map form it) is not below p_keep: the words below it are kept. The map is
+// non-decreasing in r (the conversion rounds to nearest, the product is exact), so a binary
+// search over [0, 2^32) finds it. 0 keeps nothing (p_keep <= 2^-32, or NaN); p_keep >= 1 keeps
+// every word through the kernels' own test.
+uint32_t keep_below(float p_keep) {
+  const float inv = 0x1p-32f;
+  auto u = [inv](uint64_t r) { return inv + (float)(uint32_t)r * inv; };
+  if (!(p_keep > u(0))) return 0u;
+  if (p_keep >= 1.0f) return 0xFFFFFFFFu;
+  uint64_t lo = 0, hi = 0xFFFFFFFFull;  // u(lo) < p_keep <= u(hi) = 1
+  while (hi - lo > 1) {
+    const uint64_t mid = (lo + hi) / 2;
+    (u(mid) < p_keep ? lo : hi) = mid;
+  }
+  return (uint32_t)hi;
+}
+
 DropParams make_drop(int64_t seed, int64_t G, float p_keep, int32_t vec) {
   DropParams d;
   d.seed = (uint64_t)seed;
@@ -572,10 +601,17 @@ DropParams make_drop(int64_t seed, int64_t G, float p_keep, int32_t vec) {
   d.G = (uint64_t)(G > 0 ? G : 1);
   d.p_keep = p_keep;
   d.vec = vec;
+  d.keep_below = keep_below(p_keep);
   return d;
 }
 
 }  // namespace
+
+QLORA_API int qlora_dropout_keep_below(float p_keep, uint32_t* out) {
+  QLORA_CHECK_ARG(out);
+  *out = keep_below(p_keep);
+  return 0;
+}
 
 QLORA_API int qlora_rms_fwd(const float* x, const void* delta, const void* w, int32_t w_half,
                             float* xsum, void* y, void* yq, void* yv, float* rstd,

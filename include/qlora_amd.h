@@ -88,6 +88,13 @@ int qlora_dropout_keep(int8_t* out, int64_t nelem, int64_t seed, int64_t ctr, in
                        float p_keep, int32_t vec, void* stream);
 
 /*
+ * Host only (no GPU call): the keep threshold every dropout kernel of the library uses, the
+ * smallest Philox word whose uniform 2^-32 + r 2^-32 (fp32) is not below p_keep; words below
+ * it are kept (the compare of _torch_dropout_keep, kernels.py:108-126, made an integer one).
+ */
+int qlora_dropout_keep_below(float p_keep, uint32_t* out);
+
+/*
  * RMSNorm forward over n rows of H: [x += f32(delta); xsum = x], rstd = 1/sqrt(mean(x^2)+eps),
  * y = w * (x * rstd) -> f16, and the LoRA inputs yq / yv = f16(keep ? y * keep_scale : 0) with
  * the keep masks of two dropout calls (counters ctr_q, ctr_v) at padded-batch elements

@@ -1,9 +1,11 @@
 """The C-ABI library: loads, exports every entry point include/qlora_amd.h declares, and the
 Python binding covers the same set with the same arity. No device call is made here."""
 
+import ctypes
 import os
 import re
 
+import numpy as np
 import pytest
 import torch
 
@@ -148,3 +150,31 @@ def test_hgemm_workspace_sizes(pkg):
     assert ws(0, 2048, 1536, 0, 1) == 0
     assert lib.qlora_hgemm_workspace(4, 8, 128, 0, 0, ctypes.byref(ctypes.c_int64())) == 1
     assert lib.qlora_hgemm_workspace(4, 8, 128, 0, 1, None) == 1
+
+
+def _uniform32(r):
+    """rocRAND's fp32 uniform of Philox words r (uint32 array): 2^-32 + r 2^-32, in numpy fp32."""
+    inv = np.float32(2.0**-32)
+    return inv + r.astype(np.float32) * inv
+
+
+@pytest.mark.parametrize("p_keep", [0.95, 0.9, 0.75, 0.5, 0.25, 0.05, 1e-3, 0.999999,
+                                    np.nextafter(np.float32(1), np.float32(0)), 2.0**-32,
+                                    3.0 * 2.0**-32, 0.0, 1.0])
+def test_dropout_keep_below_is_the_fp32_compare(pkg, p_keep):
+    """The integer keep test r < keep_below of every dropout kernel equals the fp32 compare
+    2^-32 + r 2^-32 < p_keep: the words just below and at the threshold, the whole word range's
+    ends, and a spread of words, evaluated in numpy fp32 (not through the library)."""
+    lib = pkg._lib.load()
+    out = ctypes.c_uint32()
+    assert lib.qlora_dropout_keep_below(ctypes.c_float(p_keep), ctypes.byref(out)) == 0
+    T = int(out.value)
+    p = np.float32(p_keep)
+    if p >= 1:
+        return  # every word is kept by the kernels' own p_keep >= 1 test
+    words = np.unique(np.concatenate([
+        np.arange(max(T - 300, 0), min(T + 300, 2**32), dtype=np.int64),
+        np.array([0, 1, 2**32 - 1], dtype=np.int64),
+        np.linspace(0, 2**32 - 1, 4097).astype(np.int64)])).astype(np.uint32)
+    want = _uniform32(words) < p
+    assert np.array_equal(words.astype(np.int64) < T, want), (p_keep, T)
