@@ -492,14 +492,33 @@ def cpu_step(pkg, model, cpu_model, batch, first):
 
 
 def _cpu_model():
+    """The host CPU as the CPU-baseline record states it: model name (/proc/cpuinfo, and lscpu's
+    vendor, family/model/stepping and socket/core/thread counts where lscpu runs), os.cpu_count(),
+    the cores this process may run on, and torch's intra-op threads (the threads the oracle
+    used)."""
+    info = {"model": "unknown", "os_cpu_count": os.cpu_count(),
+            "affinity_cores": len(os.sched_getaffinity(0)),
+            "torch_threads": torch.get_num_threads()}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
                 if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                    info["model"] = line.split(":", 1)[1].strip()
+                    break
     except OSError:
         pass
-    return "unknown"
+    try:
+        import subprocess
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        keep = {"Vendor ID", "Model name", "CPU family", "Model", "Stepping", "Socket(s)",
+                "Core(s) per socket", "Thread(s) per core", "CPU max MHz", "L3"}
+        for line in out.splitlines():
+            k, _, v = line.partition(":")
+            if k.strip() in keep:
+                info["lscpu " + k.strip()] = v.strip()
+    except Exception:
+        pass
+    return info
 
 
 def time_steps(trainer, batches, start, count):

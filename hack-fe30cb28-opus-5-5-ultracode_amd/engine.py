@@ -152,7 +152,7 @@ def _lora_targets(layer):
 
 
 @torch.no_grad()
-def from_peft(peft_model, keep_all=None):
+def from_peft(peft_model, keep_all=False):
     """The step over a PEFT-wrapped, bitsandbytes-4bit Qwen2ForCausalLM (engine.py:1571-1600,
     875-921): the NF4 weights and norms are borrowed (Params4bit `.data` / `.quant_state`), the
     LoRA A/B parameters are the PEFT modules' own (the optimizer's), the embedding is the tied
@@ -306,7 +306,11 @@ class Packed:
     step's first launches are queued. The caller's metadata is then checked on the device
     without waiting: `metadata_ok` is a device bool, False when the mask is not right-padded to
     the given lengths or the supervised count differs (read it when the step is synchronised
-    anyway).
+    anyway). A caller's count that overstates the supervised tokens costs work only (the head
+    zeroes the ignored rows it then takes in); one that understates them drops supervised rows
+    from the head's gradient, which metadata_ok reports. Without lengths the count is read with
+    them, and a caller's n_supervised that differs raises ValueError. `sup_exact`: n_supervised
+    is the device's own count.
 
     `padded=True` keeps the padding in place instead (device-only packing): every row is one
     sequence of T tokens, its padding after its real tokens, so causal attention keeps the
@@ -353,7 +357,7 @@ class Packed:
         self.targets = torch.where(real, nxt, torch.full_like(nxt, -100)).reshape(-1)
         self.head_order = torch.argsort((self.targets < 0).to(torch.int8), stable=True)
         self.n_supervised = n
-        self.sup_upper_bound = True  # n_supervised counts ignored tokens too
+        self.sup_exact = False  # n_supervised counts ignored tokens too
         right = torch.arange(T, device=dev)[None, :] < real.sum(dim=1, keepdim=True)
         self.metadata_ok = (real == right).all()
         if ctr_base is not None:
@@ -366,9 +370,15 @@ class Packed:
         B, T = input_ids.shape
         dev = input_ids.device
         given = lengths is not None
+        # whether n_supervised is the device's own count (else the caller's, checked on the
+        # device without a read: metadata_ok)
+        exact = not given or n_supervised is None
         if not given:
             lengths, counted = _read_lengths(attention_mask, labels)
-            n_supervised = counted if n_supervised is None else n_supervised
+            if n_supervised is not None and int(n_supervised) != counted:
+                raise ValueError(f"n_supervised {int(n_supervised)} differs from the batch's "
+                                 f"{counted} supervised tokens")
+            n_supervised = counted
         lengths = [int(x) for x in lengths]
         if len(lengths) != B or any(not 0 <= x <= T for x in lengths):
             raise UnsupportedBatch("lengths do not fit the batch")
@@ -387,7 +397,7 @@ class Packed:
         self.head_order = torch.argsort(unsupervised.to(torch.int8), stable=True)
         counted = (n - unsupervised.sum()) if n_supervised is None or given else None
         self.n_supervised = int(counted) if n_supervised is None else int(n_supervised)
-        self.sup_upper_bound = False
+        self.sup_exact = exact
         self.metadata_ok = None
         if given:
             cu = index[3 * n:]
@@ -624,10 +634,9 @@ class _Head(torch.autograd.Function):
     The loss is linear in the per-token losses, so its gradient w.r.t. h is formed during the
     forward and the backward only scales it. Tokens are taken in packed.head_order (supervised
     first). Per slab of at most `chunk` tokens: one GEMM forms the logits, the CE kernel
-    reduces each row and overwrites it with softmax - onehot (the rows of ignored tokens with
-    zeros, or left as they are when n_supervised is exact), and the slab's first n_supervised
-    rows alone go through G E and the norm's backward (scaled by 1/denom); the other rows'
-    gradient is zero."""
+    reduces each row and overwrites it with softmax - onehot (with zeros for an ignored token's
+    row below n_supervised), and the slab's first n_supervised rows alone go through G E and the
+    norm's backward (scaled by 1/denom); the other rows' gradient is zero."""
 
     @staticmethod
     def forward(ctx, h, norm_w, eps, lm_w, packed, denom, stats, chunk):
@@ -648,17 +657,20 @@ class _Head(torch.autograd.Function):
         if ctx.denom is not None:
             scale = 1.0
         else:
-            scale = 1.0 / float(denom) if float(denom) else float("nan")  # 0/0 as the base
+            # a batch without supervised tokens: NaN, what sum / 0 of an empty sum gives
+            scale = 1.0 / float(denom) if float(denom) else float("nan")
         for lo in range(0, n, chunk):
             hi = min(n, lo + chunk)
             logits = L.linear(hn[lo:hi], lm_w)
-            # with an exact supervised count the rows of ignored tokens are never read again
-            # (G E takes the first n_sup rows, the supervised ones): the CE kernel leaves them
-            # instead of writing zeros; with an upper bound (device-only packing) they are
-            # zeroed, as G E then reads some of them
-            _ce(logits, targets[lo:hi], tok_loss[lo:hi], entropy[lo:hi], correct[lo:hi],
-                zero_unsupervised=packed.sup_upper_bound)
+            # G E reads the rows below n_sup: an ignored token's row among them (n_sup an
+            # upper bound: device-only packing, or a caller's count that overstates) is zeroed
+            # by the CE kernel; the rows from n_sup on are never read again and keep what the
+            # kernel leaves (no zero writes)
             top = min(hi, n_sup)
+            for a, b, zero in ((lo, top, True), (max(lo, top), hi, False)):
+                if b > a:
+                    _ce(logits[a - lo:b - lo], targets[a:b], tok_loss[a:b], entropy[a:b],
+                        correct[a:b], zero_unsupervised=zero)
             if top > lo:
                 g_hn = L.linear_t(logits[:top - lo], lm_w)
                 _rms_bwd(norm, g_hn, rows[lo:top], rstd[lo:top], norm_w, packed,
@@ -684,16 +696,16 @@ class _Head(torch.autograd.Function):
 class FusedQwen2:
     """The step of a Qwen2 NF4 + LoRA model (engine.py:1568-1922 without the host offload).
 
-    Which layers keep their intermediates for the backward instead of recomputing their forward
-    follows the reference's memory-cap plan (keep_plan, engine.py:1626-1640): the last layers
-    keep everything as long as the step's predicted peak stays under the cap. The default cap is
-    the GPU's memory (less a margin), under which every layer of a 1.5B step keeps its
-    intermediates; `keep_all` True/False forces one policy for every layer."""
+    By default every layer recomputes its forward in the backward from its fp32 input
+    (`keep_all=False`, the per-layer recompute of the reference's step). `keep_all=True` keeps
+    every layer's intermediates instead; `keep_all=None` follows the reference's memory-cap plan
+    (keep_plan, engine.py:1626-1640): the last layers keep everything as long as the step's
+    predicted peak stays under the cap (the GPU's memory less a margin by default)."""
 
     HEAD_CHUNK = 4096  # rows of logits alive at a time (4096 x 151936 fp16 = 1.2 GB)
     CAP_MARGIN = 8 * 2**30  # bytes of device memory the default cap leaves free
 
-    def __init__(self, cfg, layers, embed, norm_w, device, keep_all=None):
+    def __init__(self, cfg, layers, embed, norm_w, device, keep_all=False):
         self.cfg = cfg
         self.layers = layers
         self.embed = embed
@@ -888,7 +900,11 @@ class StepGraph:
         torch.cuda.current_stream(dev).wait_stream(side)
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):
-            self.loss, self.packed, self.stats = self._run()
+            loss, self.packed, self.stats = self._run()
+        # the loss without its autograd graph: holding the graph would keep its nodes (the
+        # AccumulateGrad nodes of the captured stream among them) alive across later steps
+        self.loss = loss.detach()
+        del loss
         self.grads = [p.grad for p in params]
         self.advance = self.packed.drawn
 

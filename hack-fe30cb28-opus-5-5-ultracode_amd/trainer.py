@@ -1,126 +1,184 @@
-"""The trainer drop-in: Hugging Face Trainer / TRL SFTTrainer `compute_loss` replaced by the fused
-step (the reference's patch.py:268-398 `fused_compute_loss`, `_flush_metrics`, `install`
-452-503, without its host offload and Soup-specific patches).
+"""Hugging Face Trainer / TRL SFTTrainer drop-in: `trainer.compute_loss` served by the fused step.
+
+Reference interface: solution/patch.py:268-347 (`fused_compute_loss`), 349-378 (its metric
+flush) and 452-503 (`install`); the host offload and the Soup-specific patches there have no
+counterpart (everything stays resident on one GPU).
 
 `install(trainer)` builds the step over the trainer's PEFT 4-bit Qwen2 (`engine.from_peft`) and
-swaps `trainer.compute_loss` for `fused_compute_loss`, which
+puts a `FusedLoss` in place of `trainer.compute_loss`. A call goes to the fused step when the
+batch is exactly the causal-LM triple (input_ids, attention_mask, labels), the model is in
+training mode and the trainer uses its built-in loss (no `compute_loss_func`, no label
+smoother); otherwise, and when the engine raises `UnsupportedBatch` (before it changed
+anything), the trainer's own `compute_loss` gets the call with the inputs untouched.
+`FusedLoss.last_refusal` names the reason of the last hand-back.
 
-- runs the fused step when the batch is a plain causal-LM batch (input_ids, attention_mask,
-  labels) of a model in training mode and the trainer uses its default loss; otherwise, and on
-  `UnsupportedBatch` (raised before anything changed), the original `compute_loss` runs;
-- normalises the loss as HF does: the sum over the batch divided by `num_items_in_batch` when
-  the model accepts loss kwargs, else the mean over supervised tokens; scaled by the number of
-  processes under `average_tokens_across_devices`;
-- records TRL's metrics (entropy, mean_token_accuracy, num_tokens) without stalling the GPU
-  between forward and backward: the token count is a host number, entropy and accuracy are read
-  once backward is queued (callback `on_pre_optimizer_step`), still before the optimizer step
-  and the log, in TRL's key order.
-"""
+Loss normalisation is Hugging Face's (an interface, kept): the summed token loss divided by
+`num_items_in_batch` when the model accepts loss kwargs and the trainer passed it, else by the
+batch's supervised shifted labels; under `average_tokens_across_devices` the loss is multiplied
+by the data-parallel degree, as Trainer.compute_loss does.
 
-import types
+TRL's metrics (an interface, kept: `entropy` averaged over the packed tokens,
+`mean_token_accuracy` over the supervised ones, the running `num_tokens`) are gathered without
+stalling the GPU: each step's three sums are reduced on the device and copied into pinned host
+memory behind an event, right after the forward is queued; `MetricsQueue.drain` waits for that
+event only (not for the device) once backward is queued (callback `on_pre_optimizer_step`, or
+`on_step_end` when no optimizer step ran), which is still before the optimizer step and the
+log."""
 
 import torch
 
 from . import engine as E
 
-_ENGINE_ATTR = "_qlora_engine"
-_ORIGINAL_ATTR = "_qlora_original_compute_loss"
-_PENDING_ATTR = "_qlora_pending_metrics"
 BATCH_KEYS = ("input_ids", "attention_mask", "labels")
-
-
-def _usable(trainer, model, inputs):
-    return (getattr(trainer, _ENGINE_ATTR, None) is not None
-            and getattr(model, "training", False)
-            and isinstance(inputs, dict)
-            and set(inputs) <= set(BATCH_KEYS) | {"_prediction_loss_only"}
-            and all(k in inputs for k in BATCH_KEYS)
-            and getattr(trainer, "compute_loss_func", None) is None
-            and getattr(trainer, "label_smoother", None) is None)
+# keys Trainer may add to a training batch that the fused step does not read
+PASSIVE_KEYS = frozenset({"_prediction_loss_only"})
+_ATTR = "_qlora_fused_loss"  # the installed FusedLoss, on the trainer
 
 
 def loss_denominator(trainer, labels, num_items_in_batch):
-    """HF Trainer's normaliser: num_items_in_batch when the model takes loss kwargs, else the
-    number of supervised (shifted) labels of the batch (patch.py:292-297)."""
-    if getattr(trainer, "model_accepts_loss_kwargs", False) and num_items_in_batch is not None:
-        denom = num_items_in_batch
+    """The divisor of the summed token loss, as Hugging Face's Trainer picks it: the count the
+    trainer passes when the model takes loss kwargs, else the supervised shifted labels."""
+    if num_items_in_batch is not None and getattr(trainer, "model_accepts_loss_kwargs", False):
+        n = num_items_in_batch
     else:
-        denom = (labels[:, 1:] != -100).sum()
-    return float(denom.item() if torch.is_tensor(denom) else denom)
+        n = labels[..., 1:].ne(-100).sum()
+    return float(n)
 
 
-def fused_compute_loss(self, model, inputs, return_outputs=False, num_items_in_batch=None):
-    """Trainer.compute_loss with the fused step (patch.py:268-347)."""
-    engine = getattr(self, _ENGINE_ATTR, None)
-    original = getattr(self, _ORIGINAL_ATTR)
-    if not _usable(self, model, inputs):
-        return original(model, inputs, return_outputs=return_outputs,
-                        num_items_in_batch=num_items_in_batch)
-    popped = {k: inputs.pop(k) for k in ("_prediction_loss_only",) if k in inputs}
-    input_ids, attention_mask, labels = (inputs[k] for k in BATCH_KEYS)
-    denom = loss_denominator(self, labels, num_items_in_batch)
-    try:
-        loss, packed, stats = engine.step(input_ids, attention_mask, labels, denom)
-    except E.UnsupportedBatch:  # e.g. left padding: raised before the step changed anything
-        inputs.update(popped)
-        return original(model, inputs, return_outputs=return_outputs,
-                        num_items_in_batch=num_items_in_batch)
-    args = getattr(self, "args", None)
-    if getattr(args, "average_tokens_across_devices", False) \
-            and getattr(self, "model_accepts_loss_kwargs", False) \
-            and num_items_in_batch is not None:
-        accel = getattr(self, "accelerator", None)
-        scale = getattr(accel, "num_processes", 1)
-        pc = getattr(accel, "parallelism_config", None)
-        if pc is not None:
-            scale //= getattr(pc, "tp_size", 1)
-        n_gpu = getattr(args, "n_gpu", 1)
-        loss = loss * (scale if n_gpu <= 1 else n_gpu)
-    metrics = getattr(self, "_metrics", None)
-    if metrics is not None:
-        flush_metrics(self)  # a previous micro-batch's, under gradient accumulation
+def device_average_factor(trainer, num_items_in_batch):
+    """What Trainer multiplies the loss by under `average_tokens_across_devices` (the
+    num_items_in_batch it divided by counts every data-parallel rank's tokens): the GPU count
+    of a DataParallel run, else the processes over the tensor-parallel degree; 1 otherwise."""
+    args = getattr(trainer, "args", None)
+    if not (getattr(args, "average_tokens_across_devices", False)
+            and getattr(trainer, "model_accepts_loss_kwargs", False)
+            and num_items_in_batch is not None):
+        return 1
+    n_gpu = getattr(args, "n_gpu", 1)
+    if n_gpu > 1:
+        return n_gpu
+    accel = getattr(trainer, "accelerator", None)
+    procs = getattr(accel, "num_processes", 1)
+    tp = getattr(getattr(accel, "parallelism_config", None), "tp_size", 1)
+    return procs // tp
+
+
+class MetricsQueue:
+    """Per-step metric sums on their way from the device to the trainer's `_metrics`."""
+
+    def __init__(self):
+        self.pending = []  # (host or device tensor [3], event or None, packed token count)
+
+    def push(self, packed, stats):
+        """Queue the sums of one step: entropy over every packed token, correct predictions and
+        supervised tokens (targets >= 0)."""
+        with torch.no_grad():
+            supervised = packed.targets.ge(0)
+            sums = torch.stack([stats.entropy.float().sum(),
+                                stats.correct.float().sum(),
+                                supervised.float().sum()])
+            event = None
+            if sums.is_cuda:
+                host = torch.empty((3,), dtype=torch.float32, pin_memory=True)
+                host.copy_(sums, non_blocking=True)
+                event = torch.cuda.Event()
+                event.record()
+                sums = host
+        self.pending.append((sums, event, int(packed.n)))
+
+    def drain(self, metrics):
+        """Append every queued step's entropy and accuracy to `metrics` (TRL's train dict)."""
+        while self.pending:
+            sums, event, n_tok = self.pending.pop(0)
+            if event is not None:
+                event.synchronize()
+            ent, right, sup = (float(x) for x in sums.tolist())
+            metrics["entropy"].append(ent / n_tok if n_tok else 0.0)
+            metrics["mean_token_accuracy"].append(right / sup if sup else 0.0)
+
+
+class FusedLoss:
+    """The callable installed as `trainer.compute_loss`."""
+
+    def __init__(self, trainer, engine, original):
+        self.trainer, self.engine, self.original = trainer, engine, original
+        self.queue = MetricsQueue()
+        self.last_refusal = None
+
+    def refusal(self, model, inputs):
+        """Why the fused step does not take this call (None: it does)."""
+        t = self.trainer
+        if not getattr(model, "training", False):
+            return "the model is not in training mode"
+        if not isinstance(inputs, dict):
+            return "the inputs are not a dict"
+        keys = set(inputs) - PASSIVE_KEYS
+        if keys != set(BATCH_KEYS):
+            return f"batch keys {sorted(keys)} are not {list(BATCH_KEYS)}"
+        if getattr(t, "compute_loss_func", None) is not None:
+            return "the trainer has a custom loss function"
+        if getattr(t, "label_smoother", None) is not None:
+            return "the trainer smooths labels"
+        return None
+
+    def _hand_back(self, reason, model, inputs, return_outputs, num_items_in_batch):
+        self.last_refusal = reason
+        return self.original(model, inputs, return_outputs=return_outputs,
+                             num_items_in_batch=num_items_in_batch)
+
+    def __call__(self, model, inputs, return_outputs=False, num_items_in_batch=None):
+        reason = self.refusal(model, inputs)
+        if reason is not None:
+            return self._hand_back(reason, model, inputs, return_outputs, num_items_in_batch)
+        ids, mask, labels = (inputs[k] for k in BATCH_KEYS)
+        denom = loss_denominator(self.trainer, labels, num_items_in_batch)
+        try:
+            loss, packed, stats = self.engine.step(ids, mask, labels, denom)
+        except E.UnsupportedBatch as exc:  # raised before the step changed anything
+            return self._hand_back(str(exc), model, inputs, return_outputs, num_items_in_batch)
+        self.last_refusal = None
+        factor = device_average_factor(self.trainer, num_items_in_batch)
+        if factor != 1:
+            loss = loss * factor
+        self._record(packed, stats)
+        if return_outputs:
+            from transformers.modeling_outputs import CausalLMOutputWithPast
+            return loss, CausalLMOutputWithPast(loss=loss, logits=None)
+        return loss
+
+    def _record(self, packed, stats):
+        metrics = getattr(self.trainer, "_metrics", None)
+        if metrics is None:
+            return
         train = metrics["train"]
-        train["entropy"], train["mean_token_accuracy"]  # noqa: B018 - TRL's key order
-        self._total_train_tokens = getattr(self, "_total_train_tokens", 0) + int(packed.n)
-        train["num_tokens"] = [self._total_train_tokens]
-        setattr(self, _PENDING_ATTR, (packed, stats))
-    if return_outputs:
-        from transformers.modeling_outputs import CausalLMOutputWithPast
-        return loss, CausalLMOutputWithPast(loss=loss, logits=None)
-    return loss
+        self.flush()  # an earlier micro-batch of this optimizer step (gradient accumulation)
+        for key in ("entropy", "mean_token_accuracy"):  # TRL's key order in the log
+            train.setdefault(key, [])
+        # TRL's running count of trained tokens lives on the trainer (its own compute_loss adds
+        # to it too, on the calls handed back)
+        total = getattr(self.trainer, "_total_train_tokens", 0) + int(packed.n)
+        self.trainer._total_train_tokens = total
+        train["num_tokens"] = [total]
+        self.queue.push(packed, stats)
+
+    def flush(self):
+        """Record the queued steps' entropy and accuracy in the trainer's metrics."""
+        metrics = getattr(self.trainer, "_metrics", None)
+        if metrics is not None:
+            self.queue.drain(metrics["train"])
 
 
-def step_metrics(packed, stats):
-    """(entropy averaged over the packed tokens, accuracy over the supervised ones) of a step,
-    as TRL's SFTTrainer computes them from the logits (one device read)."""
+def row_losses(packed, stats):
+    """Each batch row's mean token loss over its supervised tokens, and those tokens' counts
+    (what the reference's rewind recorder takes, patch.py:372-378), from the packed targets:
+    the head's per-token losses (in its supervised-first order `stats.order`) summed by row."""
     with torch.no_grad():
-        valid = packed.targets >= 0
-        ent, cor, cnt = torch.stack([stats.entropy.sum(), stats.correct.sum().float(),
-                                     valid.sum().float()]).tolist()
-    return ent / max(packed.n, 1), (cor / cnt if cnt > 0 else 0.0)
-
-
-def row_losses(packed, stats, labels):
-    """Per-row mean cross-entropy over the row's supervised tokens (the reference's rewind
-    rows, patch.py:372-378) and the rows' supervised-token counts."""
-    with torch.no_grad():
-        totals = torch.zeros(packed.rows, device=stats.tok_loss.device, dtype=torch.float32)
-        # tok_loss is in the head's row order (supervised first): stats.order maps it back
-        totals.index_add_(0, packed.row_of_token.index_select(0, stats.order), stats.tok_loss)
-        counts = (labels[:, 1:] != -100).sum(dim=1)
-        means = totals / counts.clamp(min=1).to(totals.dtype)
+        rows = packed.row_of_token.index_select(0, stats.order)
+        sums = torch.bincount(rows, weights=stats.tok_loss.double(), minlength=packed.rows)
+        sup = packed.targets.index_select(0, stats.order).ge(0)
+        counts = torch.bincount(rows[sup], minlength=packed.rows)
+        means = sums / counts.clamp(min=1).double()
     return [float(x) for x in means.tolist()], [int(x) for x in counts.tolist()]
-
-
-def flush_metrics(trainer):
-    """Record the queued micro-batch's entropy and accuracy (patch.py:350-370)."""
-    pending = getattr(trainer, _PENDING_ATTR, None)
-    if pending is None:
-        return
-    setattr(trainer, _PENDING_ATTR, None)
-    entropy, accuracy = step_metrics(*pending)
-    trainer._metrics["train"]["entropy"].append(entropy)
-    trainer._metrics["train"]["mean_token_accuracy"].append(accuracy)
 
 
 def _callback_base():
@@ -132,31 +190,41 @@ def _callback_base():
 
 
 class FlushMetrics(_callback_base()):
-    """Records the pending metrics once backward is queued, before the optimizer step."""
+    """Moves the queued metrics into the trainer's log once backward is queued."""
 
-    def __init__(self, trainer):
-        self.trainer = trainer
+    def __init__(self, fused):
+        self.fused = fused
 
     def on_pre_optimizer_step(self, args, state, control, **kwargs):
-        flush_metrics(self.trainer)
+        self.fused.flush()
 
-    def on_step_end(self, args, state, control, **kwargs):  # in case no optimizer step ran
-        flush_metrics(self.trainer)
+    def on_step_end(self, args, state, control, **kwargs):  # a step without an optimizer step
+        self.fused.flush()
 
 
 def install(trainer, engine=None):
-    """Swap `trainer.compute_loss` for the fused step (patch.py:452-503); returns True when
-    installed (or already), False when the model is not one the step supports."""
-    if getattr(trainer, _ENGINE_ATTR, None) is not None:
+    """Put the fused step in place of `trainer.compute_loss`. True when installed (now or
+    before), False when the model is not one the step supports (the trainer is left as it
+    was)."""
+    if getattr(trainer, _ATTR, None) is not None:
         return True
     if engine is None:
         try:
             engine = E.from_peft(trainer.model)
         except E.UnsupportedModel:
             return False
-    setattr(trainer, _ORIGINAL_ATTR, trainer.compute_loss)
-    setattr(trainer, _ENGINE_ATTR, engine)
-    trainer.compute_loss = types.MethodType(fused_compute_loss, trainer)
+    fused = FusedLoss(trainer, engine, trainer.compute_loss)
+    setattr(trainer, _ATTR, fused)
+    trainer.compute_loss = fused
     if hasattr(trainer, "add_callback"):
-        trainer.add_callback(FlushMetrics(trainer))
+        trainer.add_callback(FlushMetrics(fused))
     return True
+
+
+def installed(trainer):
+    """The trainer's FusedLoss, or None."""
+    return getattr(trainer, _ATTR, None)
+
+
+__all__ = ["BATCH_KEYS", "FusedLoss", "FlushMetrics", "MetricsQueue", "device_average_factor",
+           "install", "installed", "loss_denominator", "row_losses"]

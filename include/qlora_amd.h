@@ -466,7 +466,7 @@ int qlora_lora_grad_noalloc(const void* g_q, const void* g_v, int64_t ldg, const
  *   length <= max_len), scale = softmax scale (D^-1/2).
  * Replaces _attn_fwd engine.py:857-862 (aten._efficient_attention_forward with cu_seqlens,
  * causal) and the k/v repeat of _expand_kv engine.py:655-660.
- * Requires D in {64, 128}, HQ % KH == 0, HQ / KH <= 6, 16-byte aligned tensors.
+ * Requires D in {64, 128}, HQ % KH == 0, HQ / KH <= 8, 16-byte aligned tensors.
  */
 int qlora_attn_fwd(const void* q, const void* k, const void* v, void* out, float* lse,
                    const int32_t* cu_seqlens, int32_t nseq, int32_t max_len, int64_t n,

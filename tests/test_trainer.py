@@ -35,13 +35,17 @@ class _Engine:
         self.calls.append(denom)
         B, T = ids.shape
         n = int(mask.sum())
-        targets = torch.tensor([1, -100, 2, 3][:n] + [5] * max(0, n - 4))
+        # each real token's next-token label (-100 past the row's end), as the packing forms it
+        nxt = torch.cat([labels[:, 1:], torch.full((B, 1), -100)], dim=1)
+        targets = nxt[mask.bool()]
         packed = _Packed(n, targets, B, T)
         stats = _Stats()
         stats.entropy = torch.full((n,), 2.0)
-        stats.correct = torch.tensor([1, 0, 1, 0][:n] + [1] * max(0, n - 4), dtype=torch.int32)
-        stats.tok_loss = torch.ones(n)
-        stats.order = torch.arange(n)
+        # the head's supervised-first order, its per-token losses 1, 2, ... in that order
+        stats.order = torch.argsort(targets.lt(0).to(torch.int8), stable=True)
+        stats.correct = torch.tensor([1, 0, 1, 1, 0, 0][:n], dtype=torch.int32)
+        stats.tok_loss = torch.arange(1, n + 1, dtype=torch.float32) * \
+            targets.index_select(0, stats.order).ge(0)
         loss = torch.tensor(3.0, requires_grad=True) * 1.0
         return loss, packed, stats
 
@@ -120,10 +124,11 @@ def test_metrics_recorded_after_backward_is_queued(pkg):
     tr.compute_loss(model, _batch())
     m = tr._metrics["train"]
     assert m["num_tokens"] == [6] and m["entropy"] == []  # deferred
+    assert list(m) == ["entropy", "mean_token_accuracy", "num_tokens"]  # TRL's key order
     tr.callbacks[0].on_pre_optimizer_step(None, None, None)
     assert m["entropy"] == [2.0]
-    # correct 1,0,1,0,1,1 over the supervised 1,-,2,3,5,5: 4 right out of 5 supervised
-    assert m["mean_token_accuracy"] == [pytest.approx(4 / 5)]
+    # targets 6, 7, 8, -, 10, -: 4 supervised tokens, 3 of them right
+    assert m["mean_token_accuracy"] == [pytest.approx(3 / 4)]
     tr.compute_loss(model, _batch())  # the next micro-batch flushes nothing new by itself
     assert m["num_tokens"] == [12] and len(m["entropy"]) == 1
     tr.callbacks[0].on_step_end(None, None, None)
@@ -145,9 +150,28 @@ def test_row_losses(pkg):
     eng = _Engine(pkg)
     b = _batch()
     loss, packed, stats = eng.step(b["input_ids"], b["attention_mask"], b["labels"], 1.0)
-    means, counts = pkg.trainer.row_losses(packed, stats, b["labels"])
-    assert counts == [3, 1]
-    assert means == pytest.approx([4 / 3, 2.0])  # row 0 holds tokens 0-3, row 1 4-5 (T = 4)
+    means, counts = pkg.trainer.row_losses(packed, stats)
+    assert counts == [3, 1]  # supervised tokens of each row (its shifted labels)
+    # head order: tokens 0, 1, 2, 4 (supervised), then 3, 5; losses 1, 2, 3, 4 then 0, 0
+    assert means == pytest.approx([(1 + 2 + 3) / 3, 4.0])
+
+
+def test_refusal_reasons_and_untouched_inputs(pkg):
+    eng = _Engine(pkg)
+    tr = _install(pkg, eng)
+    fused = pkg.trainer.installed(tr)
+    b = _batch()
+    b["pixel_values"] = torch.zeros(1)
+    tr.compute_loss(types.SimpleNamespace(training=True), b)
+    assert "pixel_values" in fused.last_refusal and "pixel_values" in b
+    b = _batch()
+    b["_prediction_loss_only"] = False
+    tr.compute_loss(types.SimpleNamespace(training=True), b)  # a passive key: fused step
+    assert fused.last_refusal is None and b["_prediction_loss_only"] is False
+    tr.label_smoother = object()
+    tr.compute_loss(types.SimpleNamespace(training=True), _batch())
+    assert fused.last_refusal == "the trainer smooths labels"
+    assert len(eng.calls) == 1
 
 
 def _fake_peft(r=16, HQ=12, HKV=2, D=128, H=1536):
