@@ -6,9 +6,9 @@ heads of 128, RoPE theta 1e6 with per-sequence positions, LoRA r 16 / alpha 32 o
 dropout 0.05 and the masks of the CUDA generator, forward and backward.
 
 Config 5: the full-width Qwen2.5-1.5B step (hidden 1536, intermediate 8960, 12/2 heads, vocab
-151,936, tied fp16 embedding) with 2 of its 28 decoder layers, on one batch of 4 sequences with
-lengths ~ U[256, 1024], against oracle.step at the reference's whole-step tolerance
-(test_kernels.py:314-400: loss relative 2e-3, LoRA gradients relative norm 2e-2).
+151,936, tied fp16 embedding) with 2 and with all 28 of its decoder layers, on one batch of 4
+sequences with lengths ~ U[256, 1024], against oracle.step at the reference's whole-step
+tolerance (test_kernels.py:314-400: loss relative 2e-3, LoRA gradients relative norm 2e-2).
 """
 
 import numpy as np
@@ -97,12 +97,16 @@ def test_config3_attention_input_block(pkg):
     assert T == max(lengths)
 
 
-def test_config5_full_width_step(pkg):
-    """Loss and every LoRA gradient of the full-width 1.5B step (2 layers) against the oracle."""
+def _config5_step(pkg, layers, overstate=0):
+    """Loss and every LoRA gradient of the full-width 1.5B step (`layers` decoder layers, per-layer
+    recompute) against the oracle. overstate: the caller's supervised-token count exceeds the
+    batch's by this much (the step must still give the oracle's gradients; metadata_ok
+    reports the mismatch)."""
     E = pkg.engine
     lengths = _lengths(256, 1024, 4, seed=5)
-    print(f"config 5 step, 2 layers, lengths {lengths}", flush=True)
-    cfg = E.Qwen2Config(num_hidden_layers=2)
+    print(f"config 5 step, {layers} layers, lengths {lengths}, n_supervised +{overstate}",
+          flush=True)
+    cfg = E.Qwen2Config(num_hidden_layers=layers)
     model = E.random_qwen2(cfg, DEV, seed=5)
     model.keep_all = False  # per-layer recompute, as config 5 states
     ids, mask, labels = _batch(lengths, cfg.vocab_size, seed=5)
@@ -111,14 +115,14 @@ def test_config5_full_width_step(pkg):
     gen = model.dropout.gen
     seed, offset = gen.initial_seed(), gen.get_offset()
     loss, packed, _ = model.step(ids.to(DEV), mask.to(DEV), labels.to(DEV), denom,
-                                 lengths=lengths, n_supervised=int(denom))
+                                 lengths=lengths, n_supervised=int(denom) + overstate)
     # fp16 training scales the loss (GradScaler's 2^16, as the trainer): unscaled, the
     # per-token gradients of a 151,936-way softmax over ~2,000 tokens sit in fp16's subnormal
     # range inside the layers' fp16 products
     scale = 2.0**16
     (loss * scale).backward()
     torch.cuda.synchronize()
-    assert bool(packed.metadata_ok)
+    assert bool(packed.metadata_ok) == (overstate == 0)
     print(f"gpu loss {loss.item():.6f}; oracle...", flush=True)
     cpu = OS.CpuQwen2(model)
     ref, _ = OS.forward_loss(cpu, ids, mask, labels, denom, drop_seed=seed, drop_offset=offset,
@@ -129,3 +133,14 @@ def test_config5_full_width_step(pkg):
     for i, (g_gpu, leaf) in enumerate(zip(model.parameters(), cpu.lora_leaves())):
         r = rel(g_gpu.grad / scale, leaf.grad)
         assert r < 2e-2, (i, r)
+
+
+@pytest.mark.parametrize("overstate", [0, 41])
+def test_config5_full_width_step(pkg, overstate):
+    _config5_step(pkg, 2, overstate)
+
+
+def test_config5_28_layer_step(pkg):
+    """The whole config-5 model: 28 layers of the full-width step against oracle.step (about half
+    a minute of the host's cores for the oracle)."""
+    _config5_step(pkg, 28)
