@@ -45,9 +45,10 @@
 // Epilogues: fp16 store; + fp16 bias (qkv); fp32 residual out = res + f32(fp16(acc)) (down);
 // SwiGLU m = fp16(silu(fp16 g) * fp16 u) (gate|up: each wavefront's first two 32-column blocks
 // are gate rows, the last two the up rows of the same output columns); fp32 partial sums for
-// split-K ([splits, M, N], summed in a fixed order by splitk_reduce_kernel). The fp16 ones are
-// staged through LDS from transposed accumulators (four consecutive columns per lane) and leave
-// as whole 16-byte row pieces.
+// split-K ([splits, M, N], summed in a fixed order by splitk_reduce_kernel). All but the
+// partials stage the fp16 product through LDS from transposed accumulators (four consecutive
+// columns per lane) and leave as whole 16-byte row pieces (the residual form: 32-byte fp32
+// pieces, the residual's loaded in batches ahead of the stores).
 //
 // Work order: workgroup ids are dealt to the 8 XCDs in turn; tile_order gives each XCD a
 // contiguous range of tiles (the M tiles of a few N tiles), so an XCD's L2 holds the B tiles it
@@ -75,6 +76,11 @@ constexpr int kTile = 256 * kBK;  // halves per operand stage (16 KB)
 enum { kEpiStore = 0, kEpiBias = 1, kEpiResid = 2, kEpiSwiglu = 3, kEpiPartial = 4 };
 enum { kBHalf = 0, kBNF4 = 1 };
 
+// Epilogues that leave through LDS from transposed accumulators (every one but the split-K
+// partials): the fp16 product staged, then whole 16-byte row pieces (the residual form reads
+// and writes fp32 row pieces of the same columns).
+constexpr bool staged_epi(int epi) { return epi != kEpiPartial; }
+
 struct GemmArgs {
   const uint16_t* a;     // A [M, Kr] fp16
   int64_t lda;
@@ -95,12 +101,14 @@ struct GemmArgs {
   int64_t I;             // SwiGLU: first W row of the up projection
   int kt_per_split;      // k-tiles per z-slice
   int m_tiles;
+  int tiles;             // tiles of one K slice (m_tiles x the N tiles)
   // fp16 B, one slice: the last round's few tiles split along K (0: none). Workgroups
   // main_tiles .. main_tiles + tail tiles x tail_splits - 1 each form one K slice of one of the
   // last tiles (kt_per_tail k-tiles) into tail_ws ([tile][slice][256][256] fp32), summed in
   // slice order by tail_reduce_kernel with the epilogue.
   int main_tiles, tail_splits, kt_per_tail;
   float* tail_ws;
+  int bm, bn;            // output tile (fp16 B: 256 x 256 or 128 x 128)
 };
 
 // ---- swizzled LDS offsets (in halves) ---------------------------------------------------------
@@ -118,11 +126,16 @@ __device__ __forceinline__ int tile_order(int b, int total) {
   return b < full ? (b % 8) * (full / 8) + b / 8 : b;
 }
 
-// The workgroup's (M tile, N tile), in scalar registers: the values are the same for every
-// lane, and held in VGPRs across the main loop they cost registers the loop needs
-__device__ __forceinline__ void tile_of(int m_tiles, int total, int64_t& tile_m,
-                                        int64_t& tile_n) {
-  const int t = tile_order(blockIdx.x, total);  // the grid is below 2^31 (host check)
+// The workgroup's (M tile, N tile, K slice), in scalar registers: the values are the same for
+// every lane, and held in VGPRs across the main loop they cost registers the loop needs. The
+// grid is one-dimensional, the K slices included (slice-major, then N tile, then M tile), so
+// the XCD order above gives each XCD a run of tiles of one K slice: its L2 then holds the few
+// A and B blocks of that K range which its workgroups share.
+__device__ __forceinline__ void tile_of(int m_tiles, int tiles, int total, int64_t& tile_m,
+                                        int64_t& tile_n, int& slice) {
+  int t = tile_order(blockIdx.x, total);  // the grid is below 2^31 (host check)
+  slice = __builtin_amdgcn_readfirstlane(t / tiles);
+  t -= slice * tiles;
   tile_m = __builtin_amdgcn_readfirstlane(t % m_tiles);
   tile_n = __builtin_amdgcn_readfirstlane(t / m_tiles);
 }
@@ -239,24 +252,27 @@ __device__ __forceinline__ uint4 nf4_decode8(const NF4Planes& t, uint32_t wd) {
   return make_uint4(a.x, a.y, b.x, b.y);
 }
 
-// W row of LDS B row `n` (NT). SwiGLU: within each wavefront's 128 rows the first 64 are gate
-// rows and the last 64 the up rows of the same 64 output columns.
-template <int EPI>
+// W row of LDS B row `n` (NT) of a tile BN rows wide. SwiGLU: within each wavefront's BN/2 rows
+// the first BN/4 are gate rows and the last BN/4 the up rows of the same BN/4 output columns.
+template <int EPI, int BN = kBN>
 __device__ __forceinline__ int64_t nt_wrow(const GemmArgs& g, int64_t tile_n, int n) {
   if constexpr (EPI == kEpiSwiglu) {
-    const int64_t j = tile_n * 128 + (n >> 7) * 64 + (n & 63);
-    return (n & 64) ? g.I + j : j;
+    constexpr int WC = BN / 2, HC = BN / 4;
+    const int64_t j = tile_n * (BN / 2) + (n / WC) * HC + (n % HC);
+    return (n % WC) >= HC ? g.I + j : j;
   } else {
-    return tile_n * kBN + n;
+    return tile_n * BN + n;
   }
 }
 
 // ---- the kernel -------------------------------------------------------------------------------
 // The operand fragments of one 16-wide k-step: 4 A blocks (rows) and 4 B blocks (columns) of
 // 32, 8 halves a lane.
-struct Frags {
-  half8_t a[4], b[4];
+template <int FM, int FN>
+struct FragsT {
+  half8_t a[FM], b[FN];
 };
+typedef FragsT<4, 4> Frags;
 
 template <bool NN>
 __device__ __forceinline__ void read_frags(Frags& f, const uint16_t* sa, const uint16_t* sb,
@@ -290,12 +306,12 @@ __device__ __forceinline__ void read_frags(Frags& f, const uint16_t* sa, const u
 // register r of lane l in block (i, j) is row 32 i + l % 32, column 32 j + 8 (r / 4) + 4 (l / 32)
 // + r % 4: four consecutive output columns per lane, stored as one 8-byte LDS write. Otherwise
 // register r is row 32 i + 8 (r / 4) + 4 (l / 32) + r % 4, column 32 j + l % 32.
-template <bool T>
-__device__ __forceinline__ void mfma_step(f32x16 (&acc)[4][4], const Frags& f) {
+template <bool T, int FM, int FN>
+__device__ __forceinline__ void mfma_step(f32x16 (&acc)[FM][FN], const FragsT<FM, FN>& f) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < FN; ++j)
       acc[i][j] = T ? __builtin_amdgcn_mfma_f32_32x32x16_f16(f.b[j], f.a[i], acc[i][j], 0, 0, 0)
                     : __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
 }
@@ -306,14 +322,20 @@ __device__ __forceinline__ void mfma_step(f32x16 (&acc)[4][4], const Frags& f) {
 // Spreading the DMA over the MFMAs keeps the four wavefronts, which leave the k-tile's barrier
 // together, from queueing all their loads at the texture unit at once (measured: 6 % of the
 // gate|up GEMM's time).
-template <bool NN, int VALU, int VMEM>
+// FM x FN MFMA blocks a k-step: MF = FM FN MFMAs, FM + FN fragment reads (NN: B's take two
+// transposed reads each); reads and loads dealt over the MFMAs as evenly as they go.
+template <bool NN, int VALU, int VMEM, int FM = 4, int FN = 4>
 __device__ __forceinline__ void sched_step() {
-  constexpr int reads = NN ? 12 : 8;
+  constexpr int MF = FM * FN, reads = FM + (NN ? 2 : 1) * FN;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
+  for (int i = 0; i < MF; ++i) {
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-    if (i < reads) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-    if (i < VMEM) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
+    constexpr int rq = reads / MF, rr = reads % MF;
+    if (i < rr) __builtin_amdgcn_sched_group_barrier(0x100, rq + 1, 0);  // DS read
+    else if (rq > 0) __builtin_amdgcn_sched_group_barrier(0x100, rq, 0);
+    constexpr int vq = VMEM / MF, vr = VMEM % MF;
+    if (i < vr) __builtin_amdgcn_sched_group_barrier(0x020, vq + 1, 0);  // VMEM read
+    else if (vq > 0) __builtin_amdgcn_sched_group_barrier(0x020, vq, 0);
     if constexpr (VALU > 0) __builtin_amdgcn_sched_group_barrier(0x002, VALU, 0);  // VALU
   }
 }
@@ -344,44 +366,45 @@ __device__ __forceinline__ void sync_tile() {
   __builtin_amdgcn_s_barrier();
 }
 
-// The epilogue of a 256 x 256 tile from the accumulators of mfma_step (4 wavefronts, 128 x 128
-// each; register layouts as mfma_step): fp16 outputs are staged through LDS (`lo`: the
-// wavefront's rows 0-63, `hi`: 64-127, [64][columns] each, free for this wavefront's use) and
-// leave as whole 16-byte row pieces; fp32 ones (split-K partials, the residual output) are
-// stored from the registers.
-template <int EPI>
-__device__ __forceinline__ void store_tile(const GemmArgs& g, f32x16 (&acc)[4][4], uint16_t* lo,
-                                           uint16_t* hi, int64_t m0, int64_t tile_n, int lane,
-                                           int wave) {
-  constexpr bool kT = EPI == kEpiStore || EPI == kEpiBias || EPI == kEpiSwiglu;
+// The epilogue of a BM x BN tile from the accumulators of mfma_step (4 wavefronts, each on a
+// WR x WC block, WR = BM / 2, WC = BN / 2; register layouts as mfma_step): fp16 outputs are
+// staged through LDS (`lo`: the wavefront's rows 0 .. WR/2 - 1, `hi`: the rest, [WR/2][columns]
+// each, free for this wavefront's use) and leave as whole 16-byte row pieces (the fp32 residual
+// output as 32-byte pieces); split-K partials are stored from the registers.
+template <int EPI, int BM = kBM, int BN = kBN>
+__device__ __forceinline__ void store_tile(const GemmArgs& g, f32x16 (&acc)[BM / 64][BN / 64],
+                                           uint16_t* lo, uint16_t* hi, int64_t m0,
+                                           int64_t tile_n, int lane, int wave, int slice = 0) {
+  constexpr int FM = BM / 64, FN = BN / 64, WR = BM / 2, WC = BN / 2;
+  constexpr bool kT = staged_epi(EPI);
   const int wm = wave >> 1, wn = wave & 1;
   const int col_in = lane & 31;
   if constexpr (kT) {
     // each wavefront writes its block to LDS as fp16 (8-byte LDS stores of four columns,
     // 16-byte chunks XOR-swizzled by row so the 32 rows of a store spread over the banks), then
     // stores whole rows to memory with 16-byte stores
-    constexpr int kCols = EPI == kEpiSwiglu ? 64 : 128;   // output columns of a wavefront
+    constexpr int kCols = EPI == kEpiSwiglu ? WC / 2 : WC;  // output columns of a wavefront
     constexpr int kChunks = kCols / 8;
-    // [128 rows][kCols] fp16: rows 0-63 in `lo`, 64-127 in `hi`
+    constexpr int kHalf = WR / 2;  // rows staged in `lo`
     auto stage_off = [&](int row, int chunk) {
-      return (row & 63) * kCols + ((chunk ^ (row & (kChunks - 1))) << 3);
+      return (row % kHalf) * kCols + ((chunk ^ (row & (kChunks - 1))) << 3);
     };
     const int c4 = 4 * (lane >> 5);  // first of the lane's four columns in an 8-column group
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < FM; ++i) {
       const int row = i * 32 + col_in;
-      uint16_t* base = i < 2 ? lo : hi;
+      uint16_t* base = i < FM / 2 ? lo : hi;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {  // 8-column group q of each 32-column block
         if constexpr (EPI == kEpiSwiglu) {
 #pragma unroll
-          for (int j = 0; j < 2; ++j) {
+          for (int j = 0; j < FN / 2; ++j) {
             const int col = j * 32 + 8 * q + c4;
             float m[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               const float gt = h2f(f2h(acc[i][j][4 * q + e]));
-              const float up = h2f(f2h(acc[i][j + 2][4 * q + e]));
+              const float up = h2f(f2h(acc[i][j + FN / 2][4 * q + e]));
               m[e] = gt * sigmoid_fast(gt) * up;  // as glu_fwd_kernel
             }
             *reinterpret_cast<uint2*>(base + stage_off(row, col >> 3) + c4) =
@@ -389,14 +412,14 @@ __device__ __forceinline__ void store_tile(const GemmArgs& g, f32x16 (&acc)[4][4
           }
         } else {
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
+          for (int j = 0; j < FN; ++j) {
             const int col = j * 32 + 8 * q + c4;
             float v[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               v[e] = acc[i][j][4 * q + e];
               if constexpr (EPI == kEpiBias) {
-                const int64_t n = tile_n * kBN + wn * 128 + col + e;
+                const int64_t n = tile_n * BN + wn * WC + col + e;
                 v[e] += h2f_bits(g.bias[n < g.N ? n : g.N - 1]);
               }
             }
@@ -408,33 +431,64 @@ __device__ __forceinline__ void store_tile(const GemmArgs& g, f32x16 (&acc)[4][4
     }
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the wavefront's own LDS stores
     constexpr int kRowsPer = 64 / kChunks;  // rows per 16-byte store instruction
-    const int64_t n_base = EPI == kEpiSwiglu ? tile_n * 128 + wn * 64 : tile_n * kBN + wn * 128;
+    const int64_t n_base = EPI == kEpiSwiglu ? tile_n * (BN / 2) + wn * (WC / 2)
+                                             : tile_n * BN + wn * WC;
+    if constexpr (EPI == kEpiResid) {
+      // out = resid + f32(fp16 product), eight columns a lane: the residual row pieces of a
+      // batch of rows are loaded before any output is stored (out may be resid itself; each
+      // element is read before it is written), so their latencies overlap
+      constexpr int kIters = WR / kRowsPer, kBatch = kIters < 4 ? kIters : 4;
 #pragma unroll
-    for (int k = 0; k < 128 / kRowsPer; ++k) {
+      for (int k0 = 0; k0 < kIters; k0 += kBatch) {
+        uint4 v[kBatch];
+        float4 r0[kBatch], r1[kBatch];
+        int64_t mo[kBatch];
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+          const int row = (k0 + b) * kRowsPer + lane / kChunks, chunk = lane % kChunks;
+          v[b] = *reinterpret_cast<const uint4*>((row < kHalf ? lo : hi) + stage_off(row, chunk));
+          const int64_t m = m0 + wm * WR + row, n = n_base + chunk * 8;
+          mo[b] = (m < g.M && n < g.N) ? m : -1;
+          if (mo[b] >= 0) {
+            const float4* rp = reinterpret_cast<const float4*>(g.resid + m * g.ldr + n);
+            r0[b] = rp[0];
+            r1[b] = rp[1];
+          }
+        }
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+          if (mo[b] < 0) continue;
+          const int64_t n = n_base + (lane % kChunks) * 8;
+          float4* op = reinterpret_cast<float4*>(static_cast<float*>(g.c) + mo[b] * g.ldc + n);
+          op[0] = make_float4(r0[b].x + lo_h(v[b].x), r0[b].y + hi_h(v[b].x),
+                              r0[b].z + lo_h(v[b].y), r0[b].w + hi_h(v[b].y));
+          op[1] = make_float4(r1[b].x + lo_h(v[b].z), r1[b].y + hi_h(v[b].z),
+                              r1[b].z + lo_h(v[b].w), r1[b].w + hi_h(v[b].w));
+        }
+      }
+      return;
+    }
+#pragma unroll
+    for (int k = 0; k < WR / kRowsPer; ++k) {
       const int row = k * kRowsPer + lane / kChunks, chunk = lane % kChunks;
-      const uint4 v = *reinterpret_cast<const uint4*>((row < 64 ? lo : hi) +
+      const uint4 v = *reinterpret_cast<const uint4*>((row < kHalf ? lo : hi) +
                                                        stage_off(row, chunk));
-      const int64_t m = m0 + wm * 128 + row, n = n_base + chunk * 8;
+      const int64_t m = m0 + wm * WR + row, n = n_base + chunk * 8;
       if (m < g.M && n < g.N)
         *reinterpret_cast<uint4*>(static_cast<uint16_t*>(g.c) + m * g.ldc + n) = v;
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < FM; ++i) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int64_t m = m0 + wm * 128 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+        const int64_t m = m0 + wm * WR + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
         if (m >= g.M) continue;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int64_t n = tile_n * kBN + wn * 128 + j * 32 + col_in;
+        for (int j = 0; j < FN; ++j) {
+          const int64_t n = tile_n * BN + wn * WC + j * 32 + col_in;
           if (n >= g.N) continue;
-          const float v = acc[i][j][r];
-          if constexpr (EPI == kEpiPartial) {
-            static_cast<float*>(g.c)[((int64_t)blockIdx.z * g.M + m) * g.N + n] = v;
-          } else {
-            static_cast<float*>(g.c)[m * g.ldc + n] = g.resid[m * g.ldr + n] + h2f(f2h(v));
-          }
+          static_cast<float*>(g.c)[((int64_t)slice * g.M + m) * g.N + n] = acc[i][j][r];
         }
       }
     }
@@ -466,9 +520,10 @@ __global__ __launch_bounds__(kThreads, 1) void nf4_gemm_kernel(GemmArgs g) {
   const int wm = wave >> 1, wn = wave & 1;
 
   int64_t tile_m, tile_n;
-  tile_of(g.m_tiles, gridDim.x, tile_m, tile_n);
+  int slice;
+  tile_of(g.m_tiles, g.tiles, gridDim.x, tile_m, tile_n, slice);
   const int64_t m0 = tile_m * kBM;
-  const int64_t kt0 = (int64_t)blockIdx.z * g.kt_per_split;
+  const int64_t kt0 = (int64_t)slice * g.kt_per_split;
   int64_t kt1 = kt0 + g.kt_per_split;
   if (kt1 > g.Kr / kBK) kt1 = g.Kr / kBK;  // k-tile counts are multiples of 4 (host check)
   const int64_t kt_last = kt1 - 1;
@@ -579,7 +634,7 @@ __global__ __launch_bounds__(kThreads, 1) void nf4_gemm_kernel(GemmArgs g) {
   // no longer read: a trip has no branch.
   constexpr int kValu = 5;
   // fp16 outputs leave through LDS from transposed accumulators (mfma_step)
-  constexpr bool kT = EPI == kEpiStore || EPI == kEpiBias || EPI == kEpiSwiglu;
+  constexpr bool kT = staged_epi(EPI);
   Frags f0, f1;
   read_frags<NN>(f0, sA0, sB0, 0, wm, wn, lane);
   // NT: a 64-value block spans k-tiles 2j and 2j + 1 of one W row (the rows start on a block:
@@ -624,7 +679,7 @@ __global__ __launch_bounds__(kThreads, 1) void nf4_gemm_kernel(GemmArgs g) {
   if constexpr (kT) __builtin_amdgcn_s_barrier();
   store_tile<EPI>(g, acc, wave == 0 ? sA0 : wave == 1 ? sA2 : wave == 2 ? sB0 : sB2,
                   wave == 0 ? sA1 : wave == 1 ? sA3 : wave == 2 ? sB1 : sB3, m0, tile_n, lane,
-                  wave);
+                  wave, slice);
 }
 
 
@@ -632,13 +687,16 @@ __global__ __launch_bounds__(kThreads, 1) void nf4_gemm_kernel(GemmArgs g) {
 // The vector L1 serves whole 128-byte lines at about twice the rate of 64-byte halves (measured
 // on MI355X: ~56 against ~29 bytes per clock per CU for global_load_lds_dwordx4 from L2): with
 // 64-wide k-tiles every K-contiguous row piece a DMA lane group fetches is a whole line. Two
-// 64 KB stages (A and B 32 KB each) fill 128 KB of LDS, so the loop runs one k-tile ahead; each
-// k-tile's 16 DMA instructions per wavefront are spread over three k-steps of the one before.
+// stages per operand; the loop runs one k-tile ahead, each k-tile's DMA instructions spread over
+// three k-steps of the one before.
+//
+// Two tile shapes share the code: 256 x 256 (4 wavefronts of 128 x 128, one workgroup per CU,
+// 128 KB of LDS) for the wide products, and 128 x 128 (4 wavefronts of 64 x 64, 64 KB of LDS, so
+// two workgroups share a CU and cover each other's waits) for the narrow ones (N = 1536 - 2048
+// at a few thousand tokens: 60 tiles of 256 x 256 for 256 CUs, 240 of 128 x 128). A 64 x 64
+// wavefront block reads twice the LDS bytes per MFMA of a 128 x 128 one.
 constexpr int kBK64 = 64;
-constexpr int kTile64 = 256 * kBK64;  // halves per operand stage (32 KB)
-// of a k-tile's 16 DMA instructions: kSplitA issued during k-step 3 of the k-tile two before,
-// kSplitB during k-step 0 of the k-tile before and the rest during its k-step 1
-constexpr int kSplitA = 6, kSplitB = 5;
+constexpr int kTile64 = 256 * kBK64;  // halves per operand stage of a 256 x 256 tile (32 KB)
 
 // [rows][64]: chunk c of row r in slot c ^ ((r >> 1) & 7). A 16-lane group of a fragment read
 // takes 16 consecutive rows of one chunk: two rows per 256-byte bank cycle, eight slots.
@@ -646,15 +704,24 @@ __device__ __forceinline__ int kmaj64_off(int row, int chunk) {
   return row * 64 + ((chunk ^ ((row >> 1) & 7)) << 3);
 }
 
-// K-contiguous tile (256 rows x 64 halves): wavefront w loads rows 64w .. 64w+63, eight whole
-// 128-byte rows per instruction.
-struct DmaK64 {
-  uint32_t off[8];
+// [64][BN] (N-contiguous): chunk c of row k in slot c ^ ((k & 3) << 2), the pattern under which
+// ds_read_b64_tr_b16 (4 rows x 16 columns per 16 lanes) is conflict-free for either width.
+template <int BN>
+__device__ __forceinline__ int nmaj_off_w(int row, int chunk) {
+  return row * BN + ((chunk ^ ((row & 3) << 2)) << 3);
+}
+
+// K-contiguous tile (ROWS rows x 64 halves): wavefront w loads rows w ROWS/4 .. (w+1) ROWS/4 - 1,
+// eight whole 128-byte rows per instruction (ROWS / 32 instructions a wavefront).
+template <int ROWS>
+struct DmaKT {
+  static constexpr int N = ROWS / 32;
+  uint32_t off[N];
   template <typename RowOf>
   __device__ __forceinline__ void init(int64_t ld, RowOf row_of, int wave, int lane) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int r = 64 * wave + 8 * j + (lane >> 3);
+    for (int j = 0; j < N; ++j) {
+      const int r = (ROWS / 4) * wave + 8 * j + (lane >> 3);
       const int c = (lane & 7) ^ ((r >> 1) & 7);
       off[j] = (uint32_t)((row_of(r) * ld + 8 * c) * 2);
     }
@@ -662,49 +729,57 @@ struct DmaK64 {
   __device__ __forceinline__ void issue(const uint16_t* base, uint16_t* dst, int wave,
                                         int j) const {
     __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(base) + off[j],
-                                     (lds_void_t*)(dst + (64 * wave + 8 * j) * 64), 16, 0, 0);
+                                     (lds_void_t*)(dst + ((ROWS / 4) * wave + 8 * j) * 64), 16,
+                                     0, 0);
   }
 };
 
-// N-contiguous tile (64 rows x 256 halves, nmaj_off): wavefront w loads rows 16w .. 16w+15,
-// two rows per instruction.
-struct DmaN64 {
-  uint32_t off[8];
+// N-contiguous tile (64 rows x BN halves, nmaj_off_w): wavefront w loads rows 16w .. 16w+15,
+// 1 KB (2048 / BN rows) per instruction (BN / 32 instructions a wavefront).
+template <int BN>
+struct DmaNT {
+  static constexpr int RPI = 512 / BN, N = 16 / RPI, LPR = BN / 8;
+  uint32_t off[N];
   __device__ __forceinline__ void init(int64_t ld, int wave, int lane) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int r = 16 * wave + 2 * j + (lane >> 5);
-      const int c = (lane & 31) ^ ((r & 3) << 2);
+    for (int j = 0; j < N; ++j) {
+      const int r = 16 * wave + RPI * j + lane / LPR;
+      const int c = (lane % LPR) ^ ((r & 3) << 2);
       off[j] = (uint32_t)((r * ld + 8 * c) * 2);
     }
   }
   __device__ __forceinline__ void issue(const uint16_t* base, uint16_t* dst, int wave,
                                         int j) const {
     __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(base) + off[j],
-                                     (lds_void_t*)(dst + (16 * wave + 2 * j) * 256), 16, 0, 0);
+                                     (lds_void_t*)(dst + (16 * wave + RPI * j) * BN), 16, 0, 0);
   }
 };
 
-// read_frags for 64-wide stages: k-step s = 0..3
-template <bool NN>
-__device__ __forceinline__ void read_frags64(Frags& f, const uint16_t* sa, const uint16_t* sb,
-                                             int s, int wm, int wn, int lane) {
+// The fragments of k-step s = 0..3 of a 64-wide stage: FM A blocks of 32 rows, FN B blocks of 32
+// columns (the wavefront's block: rows wm BM/2 .., columns wn BN/2 ..).
+template <bool NN, int BM, int BN>
+__device__ __forceinline__ void read_frags64(FragsT<BM / 64, BN / 64>& f, const uint16_t* sa,
+                                             const uint16_t* sb, int s, int wm, int wn,
+                                             int lane) {
+  constexpr int FM = BM / 64, FN = BN / 64;
   const int frow = lane & 31, fhalf = lane >> 5;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < FM; ++i)
     f.a[i] = *reinterpret_cast<const half8_t*>(
-        sa + kmaj64_off(wm * 128 + 32 * i + frow, 2 * s + fhalf));
+        sa + kmaj64_off(wm * (BM / 2) + 32 * i + frow, 2 * s + fhalf));
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < FN; ++j) {
     if constexpr (!NN) {
       f.b[j] = *reinterpret_cast<const half8_t*>(
-          sb + kmaj64_off(wn * 128 + 32 * j + frow, 2 * s + fhalf));
+          sb + kmaj64_off(wn * (BN / 2) + 32 * j + frow, 2 * s + fhalf));
     } else {
+      // ds_read_b64_tr_b16: lane p of a 16-lane group reads row k + p / 4, columns
+      // c0 + 4 (p % 4) .. + 3; lane i of the group receives column c0 + i of rows k .. k+3
       const int p = lane & 15;
-      const int col = wn * 128 + 32 * j + 16 * ((lane >> 4) & 1) + 4 * (p & 3);
+      const int col = wn * (BN / 2) + 32 * j + 16 * ((lane >> 4) & 1) + 4 * (p & 3);
       const int k = 16 * s + 8 * fhalf + (p >> 2);
-      const int o0 = nmaj_off(k, col >> 3) + (col & 7);
-      const int o1 = nmaj_off(k + 4, col >> 3) + (col & 7);
+      const int o0 = nmaj_off_w<BN>(k, col >> 3) + (col & 7);
+      const int o1 = nmaj_off_w<BN>(k + 4, col >> 3) + (col & 7);
       const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)(sb + o0));
       const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)(sb + o1));
       f.b[j] = __builtin_bit_cast(half8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
@@ -712,19 +787,20 @@ __device__ __forceinline__ void read_frags64(Frags& f, const uint16_t* sa, const
   }
 }
 
-// Tail split, slice partials: the tile's accumulators as fp32 [256 rows][256 B columns] (B
-// column: the tile's n (SwiGLU: its gate and up rows) as the wavefront blocks hold them:
-// wn 128 + 32 j + column within the MFMA block). T: transposed accumulators (mfma_step).
-template <bool T>
-__device__ __forceinline__ void store_tail_part(float* p, const f32x16 (&acc)[4][4], int lane,
-                                                int wave) {
+// Tail split, slice partials: the tile's accumulators as fp32 [BM rows][BN B columns] (B column:
+// the tile's n (SwiGLU: its gate and up rows) as the wavefront blocks hold them:
+// wn BN/2 + 32 j + column within the MFMA block). T: transposed accumulators (mfma_step).
+template <bool T, int BM, int BN>
+__device__ __forceinline__ void store_tail_part(float* p, const f32x16 (&acc)[BM / 64][BN / 64],
+                                                int lane, int wave) {
+  constexpr int FM = BM / 64, FN = BN / 64;
   const int wm = wave >> 1, wn = wave & 1;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < FN; ++j) {
       if constexpr (T) {  // register 4 q + e: row i 32 + l % 32, column 8 q + 4 (l / 32) + e
-        float* row = p + (wm * 128 + i * 32 + (lane & 31)) * kBN + wn * 128 + j * 32 +
+        float* row = p + (wm * (BM / 2) + i * 32 + (lane & 31)) * BN + wn * (BN / 2) + j * 32 +
                      4 * (lane >> 5);
 #pragma unroll
         for (int q = 0; q < 4; ++q)
@@ -734,57 +810,69 @@ __device__ __forceinline__ void store_tail_part(float* p, const f32x16 (&acc)[4]
       } else {  // register r: row i 32 + 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32
 #pragma unroll
         for (int r = 0; r < 16; ++r)
-          p[(wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * kBN + wn * 128 +
-            j * 32 + (lane & 31)] = acc[i][j][r];
+          p[(wm * (BM / 2) + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * BN +
+            wn * (BN / 2) + j * 32 + (lane & 31)] = acc[i][j][r];
       }
     }
 }
 
-// The GEMM with an fp16 B in memory (qlora_hgemm): the same tile, wavefront blocks, MFMA order
-// and epilogues as nf4_gemm_kernel, so the results are the same bits as that kernel's for the
-// same B values (the k-steps of 16 are accumulated in the same order).
-// One tile (TAIL: one K slice of a tail tile, its partial sums to g.tail_ws + tail_u tiles)
-// over k-tiles kt0 .. kt1 - 1 through the LDS stages sA0/sA1/sB0/sB1. The tail form is a
+// The GEMM with an fp16 B in memory (qlora_hgemm): for 256 x 256 tiles the same wavefront blocks,
+// MFMA order and epilogues as nf4_gemm_kernel, so the results are the same bits as that
+// kernel's for the same B values; every tile shape accumulates each output's k-steps of 16 in
+// order, so either shape gives the same bits in one slice.
+// One tile (TAIL: one K slice of a tail tile, its partial sums to g.tail_ws + tail_u tiles;
+// otherwise tail_u is the tile's K slice, for split-K partials) over k-tiles kt0 .. kt1 - 1
+// through the LDS stages sA0/sA1/sB0/sB1. The tail form is a
 // separate instantiation so that the main tiles' register allocation stays that of the plain
 // epilogue.
-template <bool NN, int EPI, bool TAIL>
+template <bool NN, int EPI, bool TAIL, int BM, int BN, int STAGES>
 __device__ __forceinline__ void hgemm_tile(const GemmArgs& g, int64_t tile_m, int64_t tile_n,
                                            int64_t kt0, int64_t kt1, int tail_u, uint16_t* sA0,
-                                           uint16_t* sA1, uint16_t* sB0, uint16_t* sB1) {
+                                           uint16_t* sA1, uint16_t* sB0, uint16_t* sB1,
+                                           uint16_t* sA2, uint16_t* sA3, uint16_t* sB2,
+                                           uint16_t* sB3) {
+  static_assert(BM == BN && (BM == 256 || BM == 128), "square 256 or 128 tiles");
+  static_assert(STAGES == 2 || (STAGES == 4 && BM == 128), "four stages fit 128 x 128 tiles");
+  constexpr int FM = BM / 64, FN = BN / 64;
+  // DMA instructions a wavefront issues per k-tile (A and B alternate), and how they are dealt:
+  // kSA during k-step 3 of the k-tile two before, kSB during k-step 0 of the one before, the rest
+  // during its k-step 1
+  constexpr int kQ = BM / 32 + BN / 32, kSA = kQ * 6 / 16, kSB = kQ * 5 / 16;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
-  if (kt1 > g.Kr / kBK64) kt1 = g.Kr / kBK64;  // k-tile counts are even (host check)
-  const int64_t m0 = tile_m * kBM;
+  // k-tile counts are multiples of STAGES (host check)
+  if (kt1 > g.Kr / kBK64) kt1 = g.Kr / kBK64;
+  const int64_t m0 = tile_m * BM;
   const int64_t kt_last = kt1 - 1;
 
-  DmaK64 dma_a;
+  DmaKT<BM> dma_a;
   const int64_t a_rows = g.M - m0;  // rows past M re-read the last row
   dma_a.init(g.lda, [&](int r) -> int64_t { return r < a_rows ? r : a_rows - 1; }, wave, lane);
   const uint16_t* a_base = g.a + m0 * g.lda;  // + k0 per k-tile
-  DmaK64 dma_bk;
-  DmaN64 dma_bn;
+  DmaKT<BN> dma_bk;
+  DmaNT<BN> dma_bn;
   const uint16_t* b_base;
   int64_t b_step;
   if constexpr (NN) {
     dma_bn.init(g.ldb, wave, lane);
-    b_base = g.b + tile_n * kBN;
+    b_base = g.b + tile_n * BN;
     b_step = (int64_t)kBK64 * g.ldb;
   } else {
     // rows past N (a last, partial tile: the lm_head's 151,936) re-read row N - 1
     dma_bk.init(g.ldb, [&](int r) -> int64_t {
-      const int64_t row = nt_wrow<EPI>(g, tile_n, r);
+      const int64_t row = nt_wrow<EPI, BN>(g, tile_n, r);
       return (EPI == kEpiSwiglu || row < g.N) ? row : g.N - 1;
     }, wave, lane);
     b_base = g.b;
     b_step = kBK64;
   }
 
-  f32x16 acc[4][4];
+  f32x16 acc[FM][FN];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+    for (int j = 0; j < FN; ++j) acc[i][j] = f32x16{};
 
   // DMA instructions q0 .. q1 - 1 of k-tile kt (q even: A row group q / 2, odd: B's); past the
   // last k-tile the last one is re-read into a stage no longer read
@@ -798,104 +886,162 @@ __device__ __forceinline__ void hgemm_tile(const GemmArgs& g, int64_t tile_m, in
     }
   };
 
-  issue_part(kt0, sA0, sB0, 0, 16);
-  issue_part(kt0 + 1, sA1, sB1, 0, kSplitA);
-  sync_tile<kSplitA>();  // k-tile kt0 landed
-
-  constexpr bool kT = EPI == kEpiStore || EPI == kEpiBias || EPI == kEpiSwiglu;
-  Frags f0, f1;
-  read_frags64<NN>(f0, sA0, sB0, 0, wm, wn, lane);
-  // k-tile t on stage t % 2, its four k-steps each reading the next one's fragments while its
-  // 16 MFMAs run. k-steps 0 and 1 finish the DMA of t + 1 into the other stage. After k-step 2
-  // every wavefront has read this stage and t + 1 has landed (the barrier): k-step 3 reads
-  // t + 1's first fragments and starts the DMA of t + 2 into this stage.
-  auto k_tile = [&](int64_t t, uint16_t* sa, uint16_t* sb, uint16_t* sa_n, uint16_t* sb_n) {
-    __builtin_amdgcn_sched_barrier(0);
-    issue_part(t + 1, sa_n, sb_n, kSplitA, kSplitA + kSplitB);
-    read_frags64<NN>(f1, sa, sb, 1, wm, wn, lane);
-    mfma_step<kT>(acc, f0);
-    sched_step<NN, 0, kSplitB>();
-    __builtin_amdgcn_sched_barrier(0);
-    issue_part(t + 1, sa_n, sb_n, kSplitA + kSplitB, 16);
-    read_frags64<NN>(f0, sa, sb, 2, wm, wn, lane);
-    mfma_step<kT>(acc, f1);
-    sched_step<NN, 0, 16 - kSplitA - kSplitB>();
-    __builtin_amdgcn_sched_barrier(0);
-    read_frags64<NN>(f1, sa, sb, 3, wm, wn, lane);
-    mfma_step<kT>(acc, f0);
-    sched_step<NN, 0, 0>();
-    __builtin_amdgcn_sched_barrier(0);
-    sync_tile<0>();
-    issue_part(t + 2, sa, sb, 0, kSplitA);
-    read_frags64<NN>(f0, sa_n, sb_n, 0, wm, wn, lane);
-    mfma_step<kT>(acc, f1);
-    sched_step<NN, 0, kSplitA>();
-    __builtin_amdgcn_sched_barrier(0);
-  };
-  for (int64_t t = kt0; t < kt1; t += 2) {
-    k_tile(t, sA0, sB0, sA1, sB1);
-    k_tile(t + 1, sA1, sB1, sA0, sB0);
+  constexpr bool kT = staged_epi(EPI);
+  FragsT<FM, FN> f0, f1;
+  if constexpr (STAGES == 2) {
+    issue_part(kt0, sA0, sB0, 0, kQ);
+    issue_part(kt0 + 1, sA1, sB1, 0, kSA);
+    sync_tile<kSA>();  // k-tile kt0 landed
+    read_frags64<NN, BM, BN>(f0, sA0, sB0, 0, wm, wn, lane);
+    // k-tile t on stage t % 2, its four k-steps each reading the next one's fragments while its
+    // MFMAs run. k-steps 0 and 1 finish the DMA of t + 1 into the other stage. After k-step 2
+    // every wavefront has read this stage and t + 1 has landed (the barrier): k-step 3 reads
+    // t + 1's first fragments and starts the DMA of t + 2 into this stage.
+    auto k_tile = [&](int64_t t, uint16_t* sa, uint16_t* sb, uint16_t* sa_n, uint16_t* sb_n) {
+      __builtin_amdgcn_sched_barrier(0);
+      issue_part(t + 1, sa_n, sb_n, kSA, kSA + kSB);
+      read_frags64<NN, BM, BN>(f1, sa, sb, 1, wm, wn, lane);
+      mfma_step<kT>(acc, f0);
+      sched_step<NN, 0, kSB, FM, FN>();
+      __builtin_amdgcn_sched_barrier(0);
+      issue_part(t + 1, sa_n, sb_n, kSA + kSB, kQ);
+      read_frags64<NN, BM, BN>(f0, sa, sb, 2, wm, wn, lane);
+      mfma_step<kT>(acc, f1);
+      sched_step<NN, 0, kQ - kSA - kSB, FM, FN>();
+      __builtin_amdgcn_sched_barrier(0);
+      read_frags64<NN, BM, BN>(f1, sa, sb, 3, wm, wn, lane);
+      mfma_step<kT>(acc, f0);
+      sched_step<NN, 0, 0, FM, FN>();
+      __builtin_amdgcn_sched_barrier(0);
+      sync_tile<0>();
+      issue_part(t + 2, sa, sb, 0, kSA);
+      read_frags64<NN, BM, BN>(f0, sa_n, sb_n, 0, wm, wn, lane);
+      mfma_step<kT>(acc, f1);
+      sched_step<NN, 0, kSA, FM, FN>();
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    for (int64_t t = kt0; t < kt1; t += 2) {
+      k_tile(t, sA0, sB0, sA1, sB1);
+      k_tile(t + 1, sA1, sB1, sA0, sB0);
+    }
+  } else {
+    // Four stages, k-tile t on stage t % 4: the DMA of t + 3 goes into the stage t - 1 used
+    // (free since the barrier that ended t - 1's reads), spread over k-steps 0-2 of t, so a
+    // k-tile's loads have about eleven k-steps to land; the barrier after k-step 2 waits for
+    // t + 1 only (t + 2 and t + 3 stay in flight).
+    constexpr int q1 = (kQ + 2) / 3, q2 = 2 * q1;
+    issue_part(kt0, sA0, sB0, 0, kQ);
+    issue_part(kt0 + 1, sA1, sB1, 0, kQ);
+    issue_part(kt0 + 2, sA2, sB2, 0, kQ);
+    sync_tile<2 * kQ>();  // k-tile kt0 landed
+    read_frags64<NN, BM, BN>(f0, sA0, sB0, 0, wm, wn, lane);
+    auto k_tile = [&](int64_t t, uint16_t* sa, uint16_t* sb, uint16_t* sa_n, uint16_t* sb_n,
+                      uint16_t* sa_p, uint16_t* sb_p) {
+      __builtin_amdgcn_sched_barrier(0);
+      issue_part(t + 3, sa_p, sb_p, 0, q1);
+      read_frags64<NN, BM, BN>(f1, sa, sb, 1, wm, wn, lane);
+      mfma_step<kT>(acc, f0);
+      sched_step<NN, 0, q1, FM, FN>();
+      __builtin_amdgcn_sched_barrier(0);
+      issue_part(t + 3, sa_p, sb_p, q1, q2);
+      read_frags64<NN, BM, BN>(f0, sa, sb, 2, wm, wn, lane);
+      mfma_step<kT>(acc, f1);
+      sched_step<NN, 0, q2 - q1, FM, FN>();
+      __builtin_amdgcn_sched_barrier(0);
+      issue_part(t + 3, sa_p, sb_p, q2, kQ);
+      read_frags64<NN, BM, BN>(f1, sa, sb, 3, wm, wn, lane);
+      mfma_step<kT>(acc, f0);
+      sched_step<NN, 0, kQ - q2, FM, FN>();
+      __builtin_amdgcn_sched_barrier(0);
+      sync_tile<2 * kQ>();  // t + 1 landed; t + 2, t + 3 may be in flight
+      read_frags64<NN, BM, BN>(f0, sa_n, sb_n, 0, wm, wn, lane);
+      mfma_step<kT>(acc, f1);
+      sched_step<NN, 0, 0, FM, FN>();
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    for (int64_t t = kt0; t < kt1; t += 4) {
+      k_tile(t, sA0, sB0, sA1, sB1, sA3, sB3);
+      k_tile(t + 1, sA1, sB1, sA2, sB2, sA0, sB0);
+      k_tile(t + 2, sA2, sB2, sA3, sB3, sA1, sB1);
+      k_tile(t + 3, sA3, sB3, sA0, sB0, sA2, sB2);
+    }
   }
   __builtin_amdgcn_s_waitcnt(0);
   if constexpr (TAIL) {
-    store_tail_part<kT>(g.tail_ws + (int64_t)tail_u * kBM * kBN, acc, lane, wave);
+    store_tail_part<kT, BM, BN>(g.tail_ws + (int64_t)tail_u * BM * BN, acc, lane, wave);
   } else {
     if constexpr (kT) __builtin_amdgcn_s_barrier();
+    // each wavefront stages its fp16 block in one of the four operand stages
     uint16_t* st = wave == 0 ? sA0 : wave == 1 ? sA1 : wave == 2 ? sB0 : sB1;
-    store_tile<EPI>(g, acc, st, st + 64 * 128, m0, tile_n, lane, wave);
+    store_tile<EPI, BM, BN>(g, acc, st, st + (BM / 4) * (BN / 2), m0, tile_n, lane, wave,
+                            tail_u);
   }
 }
 
-template <bool NN, int EPI>
-__global__ __launch_bounds__(kThreads, 1) void hgemm_kernel(GemmArgs g) {
-  __shared__ __attribute__((aligned(1024))) uint16_t sA0[kTile64];
-  __shared__ __attribute__((aligned(1024))) uint16_t sA1[kTile64];
-  __shared__ __attribute__((aligned(1024))) uint16_t sB0[kTile64];
-  __shared__ __attribute__((aligned(1024))) uint16_t sB1[kTile64];
+// STAGES: 2 (either tile; 128 x 128 tiles then leave room for a second workgroup per CU) or 4
+// (128 x 128 only, 128 KB: one workgroup per CU, loads issued three k-tiles ahead).
+template <bool NN, int EPI, int BM, int STAGES>
+__global__ __launch_bounds__(kThreads, (BM == 128 && STAGES == 2) ? 2 : 1) void hgemm_kernel(
+    GemmArgs g) {
+  constexpr int kX = STAGES == 4 ? BM * kBK64 : 8;  // stages 2-3 (unused with two stages)
+  __shared__ __attribute__((aligned(1024))) uint16_t sA0[BM * kBK64];
+  __shared__ __attribute__((aligned(1024))) uint16_t sA1[BM * kBK64];
+  __shared__ __attribute__((aligned(1024))) uint16_t sB0[BM * kBK64];
+  __shared__ __attribute__((aligned(1024))) uint16_t sB1[BM * kBK64];
+  __shared__ __attribute__((aligned(1024))) uint16_t sA2[kX];
+  __shared__ __attribute__((aligned(1024))) uint16_t sA3[kX];
+  __shared__ __attribute__((aligned(1024))) uint16_t sB2[kX];
+  __shared__ __attribute__((aligned(1024))) uint16_t sB3[kX];
   // past the main tiles: one K slice of one of the last round's tiles (tail split)
   const int tail_u = g.tail_splits > 0 ? (int)blockIdx.x - g.main_tiles : -1;
   if (tail_u >= 0) {
     const int t = g.main_tiles + tail_u / g.tail_splits;
     const int64_t kt0 =
         (int64_t)__builtin_amdgcn_readfirstlane(tail_u % g.tail_splits) * g.kt_per_tail;
-    hgemm_tile<NN, EPI, true>(g, __builtin_amdgcn_readfirstlane(t % g.m_tiles),
-                              __builtin_amdgcn_readfirstlane(t / g.m_tiles), kt0,
-                              kt0 + g.kt_per_tail, tail_u, sA0, sA1, sB0, sB1);
+    hgemm_tile<NN, EPI, true, BM, BM, STAGES>(
+        g, __builtin_amdgcn_readfirstlane(t % g.m_tiles),
+        __builtin_amdgcn_readfirstlane(t / g.m_tiles), kt0, kt0 + g.kt_per_tail, tail_u, sA0,
+        sA1, sB0, sB1, sA2, sA3, sB2, sB3);
     return;
   }
   int64_t tile_m, tile_n;
-  tile_of(g.m_tiles, g.tail_splits > 0 ? g.main_tiles : (int)gridDim.x, tile_m, tile_n);
-  const int64_t kt0 = (int64_t)blockIdx.z * g.kt_per_split;
-  hgemm_tile<NN, EPI, false>(g, tile_m, tile_n, kt0, kt0 + g.kt_per_split, -1, sA0, sA1, sB0,
-                             sB1);
+  int slice;
+  tile_of(g.m_tiles, g.tiles, g.tail_splits > 0 ? g.main_tiles : (int)gridDim.x, tile_m, tile_n,
+          slice);
+  const int64_t kt0 = (int64_t)slice * g.kt_per_split;
+  hgemm_tile<NN, EPI, false, BM, BM, STAGES>(g, tile_m, tile_n, kt0, kt0 + g.kt_per_split, slice,
+                                             sA0, sA1, sB0, sB1, sA2, sA3, sB2, sB3);
 }
 
 // Tail split: the slices of each tail tile summed in slice order, then the epilogue (fp16 store,
-// bias, fp32 residual, SwiGLU), four outputs per thread.
+// bias, fp32 residual, SwiGLU), four outputs per thread. Tile g.bm x g.bn.
 __global__ __launch_bounds__(256) void tail_reduce_kernel(GemmArgs g, int epi, int tiles) {
   const bool sw = epi == kEpiSwiglu;
-  const int per_tile = sw ? kBM * 32 : kBM * 64;  // threads per tile
+  const int BM = g.bm, BN = g.bn, WC = BN / 2;
+  const int per_tile = sw ? BM * (BN / 8) : BM * (BN / 4);  // threads per tile
   const int64_t id = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (id >= (int64_t)tiles * per_tile) return;
   const int u = (int)(id / per_tile), w = (int)(id - (int64_t)u * per_tile);
   const int t = g.main_tiles + u;
   const int64_t tile_m = t % g.m_tiles, tile_n = t / g.m_tiles;
-  const float* part = g.tail_ws + (int64_t)u * g.tail_splits * kBM * kBN;
+  const int64_t slice = (int64_t)BM * BN;
+  const float* part = g.tail_ws + (int64_t)u * g.tail_splits * slice;
   const int S = g.tail_splits;
   if (sw) {
-    const int row = w >> 5, oc = (w & 31) * 4;  // four of the tile's 128 output columns
-    const int lc = (oc >> 6) * 128 + (((oc & 63) >> 5) * 32) + (oc & 31);  // gate; up: + 64
-    float4 gs = *reinterpret_cast<const float4*>(part + row * kBN + lc);
-    float4 us = *reinterpret_cast<const float4*>(part + row * kBN + lc + 64);
+    // four of the tile's BN / 2 output columns; a wavefront block's first WC / 2 B columns are
+    // gate rows, its last WC / 2 the matching up rows
+    const int row = w / (BN / 8), oc = (w % (BN / 8)) * 4;
+    const int lc = (oc / (WC / 2)) * WC + oc % (WC / 2);  // gate; up: + WC / 2
+    float4 gs = *reinterpret_cast<const float4*>(part + row * BN + lc);
+    float4 us = *reinterpret_cast<const float4*>(part + row * BN + lc + WC / 2);
     for (int k = 1; k < S; ++k) {
-      const float4 a = *reinterpret_cast<const float4*>(part + (int64_t)k * kBM * kBN +
-                                                        row * kBN + lc);
-      const float4 b = *reinterpret_cast<const float4*>(part + (int64_t)k * kBM * kBN +
-                                                        row * kBN + lc + 64);
+      const float4 a = *reinterpret_cast<const float4*>(part + k * slice + row * BN + lc);
+      const float4 b = *reinterpret_cast<const float4*>(part + k * slice + row * BN + lc +
+                                                        WC / 2);
       gs.x += a.x; gs.y += a.y; gs.z += a.z; gs.w += a.w;
       us.x += b.x; us.y += b.y; us.z += b.z; us.w += b.w;
     }
-    const int64_t m = tile_m * kBM + row, n = tile_n * 128 + oc;
+    const int64_t m = tile_m * BM + row, n = tile_n * (BN / 2) + oc;
     if (m >= g.M) return;
     const float gv[4] = {gs.x, gs.y, gs.z, gs.w}, uv[4] = {us.x, us.y, us.z, us.w};
     float mv[4];
@@ -908,14 +1054,13 @@ __global__ __launch_bounds__(256) void tail_reduce_kernel(GemmArgs g, int epi, i
         make_uint2(pack2h(mv[0], mv[1]), pack2h(mv[2], mv[3]));
     return;
   }
-  const int row = w >> 6, lc = (w & 63) * 4;
-  float4 v4 = *reinterpret_cast<const float4*>(part + row * kBN + lc);
+  const int row = w / (BN / 4), lc = (w % (BN / 4)) * 4;
+  float4 v4 = *reinterpret_cast<const float4*>(part + row * BN + lc);
   for (int k = 1; k < S; ++k) {
-    const float4 a =
-        *reinterpret_cast<const float4*>(part + (int64_t)k * kBM * kBN + row * kBN + lc);
+    const float4 a = *reinterpret_cast<const float4*>(part + k * slice + row * BN + lc);
     v4.x += a.x; v4.y += a.y; v4.z += a.z; v4.w += a.w;
   }
-  const int64_t m = tile_m * kBM + row, n = tile_n * kBN + lc;
+  const int64_t m = tile_m * BM + row, n = tile_n * BN + lc;
   if (m >= g.M || n >= g.N) return;  // N % 8 == 0: the four columns lie on one side
   float v[4] = {v4.x, v4.y, v4.z, v4.w};
   if (epi == kEpiResid) {
@@ -970,78 +1115,150 @@ namespace {
 
 // kernel selector: BSRC kBNF4 -> nf4_gemm_kernel, kBHalf -> hgemm_kernel. start/stop (may be
 // null): events the dispatch records at the kernel's own start and end (hipExtLaunchKernelGGL)
-template <int BSRC, bool NN, int EPI>
+template <int BSRC, bool NN, int EPI, int BM, int ST>
 void launch_one(const GemmArgs& g, dim3 grid, hipStream_t s, hipEvent_t start, hipEvent_t stop) {
-  auto kernel = BSRC == kBNF4 ? nf4_gemm_kernel<NN, EPI> : hgemm_kernel<NN, EPI>;
+  auto kernel = [] {
+    if constexpr (BSRC == kBNF4) return nf4_gemm_kernel<NN, EPI>;
+    else return hgemm_kernel<NN, EPI, BM, ST>;
+  }();
   if (start != nullptr || stop != nullptr)
     hipExtLaunchKernelGGL(kernel, grid, dim3(kThreads), 0, s, start, stop, 0, g);
   else
     hipLaunchKernelGGL(kernel, grid, dim3(kThreads), 0, s, g);
 }
 
-template <bool NN, int BSRC>
+template <bool NN, int BSRC, int BM, int ST>
 void launch_epi(const GemmArgs& g, dim3 grid, hipStream_t s, int epi, hipEvent_t start,
                 hipEvent_t stop) {
   switch (epi) {
-    case kEpiStore: launch_one<BSRC, NN, kEpiStore>(g, grid, s, start, stop); break;
-    case kEpiBias: launch_one<BSRC, NN, kEpiBias>(g, grid, s, start, stop); break;
-    case kEpiResid: launch_one<BSRC, NN, kEpiResid>(g, grid, s, start, stop); break;
-    case kEpiPartial: launch_one<BSRC, NN, kEpiPartial>(g, grid, s, start, stop); break;
+    case kEpiStore: launch_one<BSRC, NN, kEpiStore, BM, ST>(g, grid, s, start, stop); break;
+    case kEpiBias: launch_one<BSRC, NN, kEpiBias, BM, ST>(g, grid, s, start, stop); break;
+    case kEpiResid: launch_one<BSRC, NN, kEpiResid, BM, ST>(g, grid, s, start, stop); break;
+    case kEpiPartial: launch_one<BSRC, NN, kEpiPartial, BM, ST>(g, grid, s, start, stop); break;
     default:
-      if constexpr (!NN) launch_one<BSRC, NN, kEpiSwiglu>(g, grid, s, start, stop);
+      if constexpr (!NN) launch_one<BSRC, NN, kEpiSwiglu, BM, ST>(g, grid, s, start, stop);
       break;
+  }
+}
+
+// The kernel for (B source, mode, tile, stages) with the epilogue epi.
+void launch_any(const GemmArgs& g, int bsrc, int mode, int tile, int stages, dim3 grid,
+                hipStream_t s, int epi, hipEvent_t start, hipEvent_t stop) {
+  if (bsrc == kBNF4) {
+    if (mode == 0) launch_epi<false, kBNF4, 256, 2>(g, grid, s, epi, start, stop);
+    else launch_epi<true, kBNF4, 256, 2>(g, grid, s, epi, start, stop);
+  } else if (tile == 128 && stages == 4) {
+    if (mode == 0) launch_epi<false, kBHalf, 128, 4>(g, grid, s, epi, start, stop);
+    else launch_epi<true, kBHalf, 128, 4>(g, grid, s, epi, start, stop);
+  } else if (tile == 128) {
+    if (mode == 0) launch_epi<false, kBHalf, 128, 2>(g, grid, s, epi, start, stop);
+    else launch_epi<true, kBHalf, 128, 2>(g, grid, s, epi, start, stop);
+  } else {
+    if (mode == 0) launch_epi<false, kBHalf, 256, 2>(g, grid, s, epi, start, stop);
+    else launch_epi<true, kBHalf, 256, 2>(g, grid, s, epi, start, stop);
   }
 }
 
 bool al(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 
-// Shared launch path: shapes and workspace checked, then the tile grid (and the split-K reduce).
-// start/stop (may be null): recorded at the start of the tile grid and the end of the last
-// kernel.
 constexpr int kCUs = 256;  // compute units of an MI355X
 
+// Workgroups resident at once for a tile shape: 256 x 256 tiles take a CU each (128 KB of
+// LDS), 128 x 128 tiles two per CU with two stages (64 KB each), one with four (128 KB).
+int64_t slots_of(int tile, int stages) { return tile == 128 && stages == 2 ? 2 * kCUs : kCUs; }
+
 // Tail split of an fp16-B product in one slice: when the tiles past the GPU's last full round
-// of tiles are few (at most a quarter of a round) they would take a whole round; as K slices
-// (tail_splits of them per tile, kt_per_tail k-tiles each, an even count, no empty slice) they
-// fill about one round of short workgroups instead. Returns the fp32 workspace elements it
-// needs, 0 when it does not apply.
-int64_t tail_plan(int64_t m_tiles, int64_t n_tiles, int64_t ktiles, int* main_tiles, int* splits,
-                  int* kt_per) {
-  const int64_t tiles = m_tiles * n_tiles, full = tiles / kCUs * kCUs, r = tiles - full;
-  if (full == 0 || r == 0 || r > kCUs / 4) return 0;
+// of tiles fill at most half a round they would take a whole round; as K slices (tail_splits
+// of them per tile, kt_per_tail k-tiles each, an even count, no empty slice) they fill about
+// one round of short workgroups instead. Returns the fp32 workspace elements it needs, 0 when
+// it does not apply.
+int64_t tail_plan(int64_t m_tiles, int64_t n_tiles, int64_t ktiles, int tile, int stages,
+                  int* main_tiles, int* splits, int* kt_per) {
+  const int64_t slots = slots_of(tile, stages);
+  const int64_t tiles = m_tiles * n_tiles, full = tiles / slots * slots, r = tiles - full;
+  if (full == 0 || r == 0 || r > slots / 2) return 0;
   for (int sp = 16; sp >= 2; --sp) {
-    const int64_t per = qlora_cdiv(qlora_cdiv(ktiles, sp), 2) * 2;
-    if (r * sp > kCUs || per * (sp - 1) >= ktiles) continue;
+    const int64_t per = qlora_cdiv(qlora_cdiv(ktiles, sp), stages) * stages;
+    if (r * sp > slots || per * (sp - 1) >= ktiles) continue;
     *main_tiles = (int)full;
     *splits = sp;
     *kt_per = (int)per;
-    return r * sp * kBM * kBN;
+    return r * sp * tile * tile;
   }
   return 0;
 }
 
-int64_t n_tiles_of(int64_t N, int epi) { return epi == kEpiSwiglu ? N / 128 : qlora_cdiv(N, kBN); }
+int64_t n_tiles_of(int64_t N, int epi, int tile) {
+  return epi == kEpiSwiglu ? N / (tile / 2) : qlora_cdiv(N, tile);
+}
 
+// The tile shape, stage count and K split of qlora_gemm16 with tile 0 / splits 0: a fixed rule
+// from the step's measured shapes (M = 1,875 - 2,949 tokens, MI355X; every choice below was the
+// fastest of the package's variants there), so a problem always runs the same kernels and gives
+// the same bits:
+//   - the SwiGLU form and wide products (N > 4096: gate|up, the down projection's dX, the
+//     lm_head): 256 x 256 tiles, one slice (the last round's few tiles K-sliced);
+//   - narrow products (N <= 4096) with K <= 4096 (qkv, o and their dX): 128 x 128 tiles, four
+//     stages while the tiles fit one round of the 256 CUs (each CU one workgroup), else two
+//     stages (two workgroups share a CU);
+//   - narrow products with a long K (the down projection, gate|up's dX, the head's G E):
+//     256 x 256 tiles split along K while the slices fit one round and keep >= 32 k-tiles each.
+void auto_plan(int64_t M, int64_t N, int64_t K, int mode, int epi, int* tile, int* stages,
+               int* splits) {
+  const int64_t kt = K / kBK64;
+  *tile = 256;
+  *stages = 2;
+  *splits = 1;
+  if (epi == kEpiSwiglu || N > 4096) return;
+  if (K <= 4096 && (mode == 0 || N % 128 == 0)) {
+    const int64_t tiles = qlora_cdiv(M, 128) * qlora_cdiv(N, 128);
+    *tile = 128;
+    *stages = (tiles <= kCUs && kt % 4 == 0) ? 4 : 2;
+    return;
+  }
+  if (mode == 1 && N % 256 != 0) {  // NN on 128 x 128 tiles only
+    *tile = 128;
+    return;
+  }
+  const int64_t tiles = qlora_cdiv(M, 256) * qlora_cdiv(N, 256);
+  int p = 1;
+  while (p < 16 && tiles * (p + 1) <= kCUs && kt / (p + 1) >= 32) ++p;
+  while (p > 1 && qlora_cdiv(qlora_cdiv(kt, p), 2) * 2 * (p - 1) >= kt) --p;  // no empty slice
+  *splits = p;
+}
+
+// Shared launch path: shapes and workspace checked, then the tile grid (and the split-K reduce).
+// tile: 256 or 128 (fp16 B; the NF4 kernel's is 256). start/stop (may be null): recorded at the
+// start of the tile grid and the end of the last kernel.
 int run_gemm(GemmArgs& g, int bsrc, int mode, int epi, int splits, float* ws, int64_t ws_elems,
-             hipStream_t s, hipEvent_t start = nullptr, hipEvent_t stop = nullptr) {
-  const int64_t n_tiles = n_tiles_of(g.N, epi);
-  g.m_tiles = (int)qlora_cdiv(g.M, kBM);
+             hipStream_t s, hipEvent_t start = nullptr, hipEvent_t stop = nullptr,
+             int tile = 256, int stages = 2) {
+  QLORA_CHECK_ARG((tile == 256 && stages == 2) ||
+                  (tile == 128 && bsrc == kBHalf && (stages == 2 || stages == 4)));
+  g.bm = g.bn = tile;
+  const int64_t n_tiles = n_tiles_of(g.N, epi, tile);
+  g.m_tiles = (int)qlora_cdiv(g.M, tile);
   const int64_t grid = (int64_t)g.m_tiles * n_tiles;
   QLORA_CHECK_ARG(grid < (1ll << 31));
+  g.tiles = (int)grid;
   // fp16 outputs leave in 16-byte row pieces
   QLORA_CHECK_ARG(epi == kEpiResid || splits > 1 || (g.ldc % 8 == 0 && al(g.c, 16)));
+  // the fp32 residual form reads and writes 32-byte row pieces
+  QLORA_CHECK_ARG(epi != kEpiResid || splits > 1 ||
+                  (g.ldc % 4 == 0 && g.ldr % 4 == 0 && al(g.c, 16) && al(g.resid, 16)));
   QLORA_CHECK_ARG(splits == 1 || (ws && ws_elems >= (int64_t)splits * g.M * g.N && al(ws, 16)));
   // NF4 B: k-tiles of 32, four per loop trip; fp16 B: k-tiles of 64, two per trip (the split
   // boundaries fall on the same multiples of 128 either way)
-  const int bk = bsrc == kBNF4 ? kBK : kBK64, per_trip = bsrc == kBNF4 ? kStages : 2;
+  const int bk = bsrc == kBNF4 ? kBK : kBK64, per_trip = bsrc == kBNF4 ? kStages : stages;
   const int64_t ktiles = g.Kr / bk;
   QLORA_CHECK_ARG(ktiles % per_trip == 0);
   g.kt_per_split = (int)(qlora_cdiv(qlora_cdiv(ktiles, splits), per_trip) * per_trip);
   QLORA_CHECK_ARG((int64_t)g.kt_per_split * (splits - 1) < ktiles);  // no empty slice
   int main_t = 0, tail_s = 0, kt_tail = 0;
-  const int64_t tail_need = bsrc == kBHalf && splits == 1 && ws != nullptr
-                                ? tail_plan(g.m_tiles, n_tiles, ktiles, &main_t, &tail_s, &kt_tail)
-                                : 0;
+  const int64_t tail_need =
+      bsrc == kBHalf && splits == 1 && ws != nullptr
+          ? tail_plan(g.m_tiles, n_tiles, ktiles, tile, stages, &main_t, &tail_s, &kt_tail)
+          : 0;
   if (tail_need > 0 && ws_elems >= tail_need && al(ws, 16)) {
     g.main_tiles = main_t;
     g.tail_splits = tail_s;
@@ -1049,10 +1266,9 @@ int run_gemm(GemmArgs& g, int bsrc, int mode, int epi, int splits, float* ws, in
     g.tail_ws = ws;
     const int64_t r = grid - main_t;
     const dim3 tg((unsigned)(main_t + r * tail_s));
-    if (mode == 0) launch_epi<false, kBHalf>(g, tg, s, epi, start, nullptr);
-    else launch_epi<true, kBHalf>(g, tg, s, epi, start, nullptr);
+    launch_any(g, bsrc, mode, tile, stages, tg, s, epi, start, nullptr);
     if (int rc = qlora_launch_status()) return rc;
-    const int64_t threads = r * (epi == kEpiSwiglu ? kBM * 32 : kBM * 64);
+    const int64_t threads = r * (epi == kEpiSwiglu ? tile * (tile / 8) : tile * (tile / 4));
     const dim3 rg((unsigned)qlora_cdiv(threads, 256));
     if (stop != nullptr)
       hipExtLaunchKernelGGL(tail_reduce_kernel, rg, dim3(256), 0, s, nullptr, stop, 0, g, epi,
@@ -1064,15 +1280,9 @@ int run_gemm(GemmArgs& g, int bsrc, int mode, int epi, int splits, float* ws, in
   const int kepi = splits > 1 ? (int)kEpiPartial : epi;
   void* out = g.c;
   if (splits > 1) g.c = ws;
-  const dim3 gdim((unsigned)grid, 1, (unsigned)splits);
-  hipEvent_t gemm_stop = splits > 1 ? nullptr : stop;
-  if (mode == 0) {
-    if (bsrc == kBNF4) launch_epi<false, kBNF4>(g, gdim, s, kepi, start, gemm_stop);
-    else launch_epi<false, kBHalf>(g, gdim, s, kepi, start, gemm_stop);
-  } else {
-    if (bsrc == kBNF4) launch_epi<true, kBNF4>(g, gdim, s, kepi, start, gemm_stop);
-    else launch_epi<true, kBHalf>(g, gdim, s, kepi, start, gemm_stop);
-  }
+  QLORA_CHECK_ARG(grid * splits < (1ll << 31));
+  const dim3 gdim((unsigned)(grid * splits));
+  launch_any(g, bsrc, mode, tile, stages, gdim, s, kepi, start, splits > 1 ? nullptr : stop);
   int rc = qlora_launch_status();
   if (rc != 0 || splits == 1) return rc;
   QLORA_CHECK_ARG(g.N % 4 == 0 && g.ldc % 4 == 0 && (epi != kEpiResid || g.ldr % 4 == 0));
@@ -1178,30 +1388,34 @@ QLORA_API int qlora_nf4_gemm(const void* a, int64_t lda, const void* packed, con
   return run_gemm(g, kBNF4, mode, epi, splits, ws, ws_elems, (hipStream_t)stream);
 }
 
-// The same GEMM with an fp16 B in memory: NT B [N, K] (ldb), NN B [K, N] (ldb). The timed form
-// also records start/stop (hipEvent_t with timing, or null) at the start of the tile grid and
-// the end of the last kernel.
-QLORA_API int qlora_hgemm_timed(const void* a, int64_t lda, const void* b, int64_t ldb,
-                                int64_t M, int64_t N, int64_t K, int32_t mode, void* c,
-                                int64_t ldc, const void* bias, const float* resid, int64_t ldr,
-                                int32_t epi, int64_t swiglu_I, int32_t splits, float* ws,
-                                int64_t ws_elems, void* stream, void* start, void* stop) {
+// The GEMM with an fp16 B in memory: NT B [N, K] (ldb), NN B [K, N] (ldb), on tile x tile
+// output tiles (256 or 128). The timed form also records start/stop (hipEvent_t with timing,
+// or null) at the start of the tile grid and the end of the last kernel.
+QLORA_API int qlora_gemm16_timed(const void* a, int64_t lda, const void* b, int64_t ldb,
+                                 int64_t M, int64_t N, int64_t K, int32_t mode, void* c,
+                                 int64_t ldc, const void* bias, const float* resid, int64_t ldr,
+                                 int32_t epi, int64_t swiglu_I, int32_t tile, int32_t stages,
+                                 int32_t splits, float* ws, int64_t ws_elems, void* stream,
+                                 void* start, void* stop) {
   QLORA_CHECK_ARG(M >= 0 && N > 0 && K > 0);
   if (M == 0) return 0;
   QLORA_CHECK_ARG(a && b && c && (mode == 0 || mode == 1));
+  QLORA_CHECK_ARG((tile == 0) == (splits == 0));
+  if (tile == 0) auto_plan(M, N, K, mode, epi, &tile, &stages, &splits);
+  QLORA_CHECK_ARG((tile == 256 && stages == 2) || (tile == 128 && (stages == 2 || stages == 4)));
   QLORA_CHECK_ARG(epi >= 0 && epi <= 3 && !(epi == 3 && mode != 0));
   QLORA_CHECK_ARG(splits >= 1 && splits <= 16 && !(splits > 1 && epi == 3));
   QLORA_CHECK_ARG(epi != 1 || bias);
   QLORA_CHECK_ARG(epi != 2 || (resid && ldr >= N));
-  QLORA_CHECK_ARG(K % (kStages * kBK) == 0);
-  if (epi == kEpiSwiglu) QLORA_CHECK_ARG(N % 128 == 0);  // N = I (output columns)
-  else QLORA_CHECK_ARG(mode == 0 ? N % 8 == 0 : N % kBN == 0);  // NT: a partial last tile
+  QLORA_CHECK_ARG(K % (kStages * kBK) == 0 && (K / kBK64) % stages == 0);
+  if (epi == kEpiSwiglu) QLORA_CHECK_ARG(N % (tile / 2) == 0);  // N = I (output columns)
+  else QLORA_CHECK_ARG(mode == 0 ? N % 8 == 0 : N % tile == 0);  // NT: a partial last tile
   QLORA_CHECK_ARG(lda >= K && lda % 8 == 0 && al(a, 16) && al(b, 16) && ldb % 8 == 0);
   QLORA_CHECK_ARG(mode == 0 ? ldb >= K : ldb >= N);
   QLORA_CHECK_ARG(ldc >= N);
   // the DMA addresses rows by 32-bit byte offsets: from B's start (NT), from a tile (A, NN B)
   if (mode == 0) QLORA_CHECK_ARG((epi == kEpiSwiglu ? 2 * N : N) * ldb * 2 < (1ll << 32));
-  QLORA_CHECK_ARG(256 * lda * 2 < (1ll << 32) && 64 * ldb * 2 < (1ll << 32));
+  QLORA_CHECK_ARG((int64_t)tile * lda * 2 < (1ll << 32) && 64 * ldb * 2 < (1ll << 32));
   GemmArgs g{};
   g.a = static_cast<const uint16_t*>(a);
   g.lda = lda;
@@ -1217,7 +1431,62 @@ QLORA_API int qlora_hgemm_timed(const void* a, int64_t lda, const void* b, int64
   g.Kr = K;
   g.I = swiglu_I;
   return run_gemm(g, kBHalf, mode, epi, splits, ws, ws_elems, (hipStream_t)stream,
-                  static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop));
+                  static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop), tile, stages);
+}
+
+QLORA_API int qlora_gemm16(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t M,
+                           int64_t N, int64_t K, int32_t mode, void* c, int64_t ldc,
+                           const void* bias, const float* resid, int64_t ldr, int32_t epi,
+                           int64_t swiglu_I, int32_t tile, int32_t stages, int32_t splits,
+                           float* ws, int64_t ws_elems, void* stream) {
+  return qlora_gemm16_timed(a, lda, b, ldb, M, N, K, mode, c, ldc, bias, resid, ldr, epi,
+                            swiglu_I, tile, stages, splits, ws, ws_elems, stream, nullptr,
+                            nullptr);
+}
+
+// fp32 workspace elements of a qlora_gemm16 problem: the split-K partials, or with one slice the
+// tail split's (0 when the last round needs none).
+QLORA_API int qlora_gemm16_workspace(int64_t M, int64_t N, int64_t K, int32_t mode, int32_t epi,
+                                     int32_t tile, int32_t stages, int32_t splits,
+                                     int64_t* elems) {
+  QLORA_CHECK_ARG(elems && M >= 0 && N > 0 && K > 0 && splits >= 0 && epi >= 0 && epi <= 3);
+  QLORA_CHECK_ARG((tile == 0) == (splits == 0) && (mode == 0 || mode == 1));
+  *elems = 0;
+  if (M == 0) return 0;
+  if (tile == 0) auto_plan(M, N, K, mode, epi, &tile, &stages, &splits);
+  QLORA_CHECK_ARG((tile == 256 && stages == 2) || (tile == 128 && (stages == 2 || stages == 4)));
+  if (splits > 1) {
+    *elems = (int64_t)splits * M * N;
+    return 0;
+  }
+  if (M == 0 || K % (kStages * kBK) != 0) return 0;
+  int main_t, tail_s, kt_tail;
+  *elems = tail_plan(qlora_cdiv(M, tile), n_tiles_of(N, epi, tile), K / kBK64, tile, stages,
+                     &main_t, &tail_s, &kt_tail);
+  return 0;
+}
+
+// The (tile, stages, splits) qlora_gemm16 runs with tile 0 and splits 0.
+QLORA_API int qlora_gemm16_plan(int64_t M, int64_t N, int64_t K, int32_t mode, int32_t epi,
+                                int32_t* tile, int32_t* stages, int32_t* splits) {
+  QLORA_CHECK_ARG(tile && stages && splits && M >= 0 && N > 0 && K > 0);
+  QLORA_CHECK_ARG((mode == 0 || mode == 1) && epi >= 0 && epi <= 3);
+  int t, st, sp;
+  auto_plan(M, N, K, mode, epi, &t, &st, &sp);
+  *tile = t;
+  *stages = st;
+  *splits = sp;
+  return 0;
+}
+
+// The 256 x 256 form (qlora_gemm16 with tile 256).
+QLORA_API int qlora_hgemm_timed(const void* a, int64_t lda, const void* b, int64_t ldb,
+                                int64_t M, int64_t N, int64_t K, int32_t mode, void* c,
+                                int64_t ldc, const void* bias, const float* resid, int64_t ldr,
+                                int32_t epi, int64_t swiglu_I, int32_t splits, float* ws,
+                                int64_t ws_elems, void* stream, void* start, void* stop) {
+  return qlora_gemm16_timed(a, lda, b, ldb, M, N, K, mode, c, ldc, bias, resid, ldr, epi,
+                            swiglu_I, 256, 2, splits, ws, ws_elems, stream, start, stop);
 }
 
 QLORA_API int qlora_hgemm(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t M,
@@ -1225,21 +1494,11 @@ QLORA_API int qlora_hgemm(const void* a, int64_t lda, const void* b, int64_t ldb
                           const void* bias, const float* resid, int64_t ldr, int32_t epi,
                           int64_t swiglu_I, int32_t splits, float* ws, int64_t ws_elems,
                           void* stream) {
-  return qlora_hgemm_timed(a, lda, b, ldb, M, N, K, mode, c, ldc, bias, resid, ldr, epi,
-                           swiglu_I, splits, ws, ws_elems, stream, nullptr, nullptr);
+  return qlora_gemm16_timed(a, lda, b, ldb, M, N, K, mode, c, ldc, bias, resid, ldr, epi,
+                            swiglu_I, 256, 2, splits, ws, ws_elems, stream, nullptr, nullptr);
 }
 
 QLORA_API int qlora_hgemm_workspace(int64_t M, int64_t N, int64_t K, int32_t epi, int32_t splits,
                                     int64_t* elems) {
-  QLORA_CHECK_ARG(elems && M >= 0 && N > 0 && K > 0 && splits >= 1 && epi >= 0 && epi <= 3);
-  *elems = 0;
-  if (splits > 1) {
-    *elems = (int64_t)splits * M * N;
-    return 0;
-  }
-  if (M == 0 || K % (kStages * kBK) != 0) return 0;
-  int main_t, tail_s, kt_tail;
-  *elems = tail_plan(qlora_cdiv(M, kBM), n_tiles_of(N, epi), K / kBK64, &main_t, &tail_s,
-                     &kt_tail);
-  return 0;
+  return qlora_gemm16_workspace(M, N, K, 0, epi, 256, 2, splits, elems);
 }

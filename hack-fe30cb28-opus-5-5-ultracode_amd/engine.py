@@ -715,7 +715,9 @@ class FusedQwen2:
         self.device = torch.device(device)
         self.keep_all = keep_all
         self.memory_cap = None
-        self.autotune = True  # time the projections' GEMM solutions for each new token bucket
+        # with the library GEMMs (linear.GEMM == "library"): time their solutions for each new
+        # token bucket; the package's GEMM has a fixed plan and nothing to time
+        self.autotune = True
         # layers that keep their intermediates also keep their dequantized weights for the
         # backward (one dequant per layer and step instead of two; 94 MB per 1.5B layer)
         self.keep_weights = True
@@ -808,6 +810,8 @@ class FusedQwen2:
         """Measure the GEMM solutions for the buckets of these step sizes (tokens); the head's
         dX product runs over the supervised rows only, so it is also measured at 3/4 and 1/2 of
         each size. Returns the seconds spent."""
+        if L.GEMM != "library":
+            return 0.0  # the package's GEMM plan is fixed: nothing to measure
         counts = list(token_counts)
         shapes = self.gemm_shapes()
         t = G.tune(shapes, counts, self.device, log=log)
@@ -827,7 +831,7 @@ class FusedQwen2:
         packed = Packed(input_ids, attention_mask, labels, self.rope, self.dropout,
                         self.dropout_p, lengths=lengths, n_supervised=n_supervised,
                         padded=padded, ctr_base=ctr_base)
-        if self.autotune:
+        if self.autotune and L.GEMM == "library":
             shapes = self.gemm_shapes()
             G.tune(shapes, [packed.n], self.device)
             G.tune(shapes[-1:], [max(1, packed.n_supervised)], self.device)

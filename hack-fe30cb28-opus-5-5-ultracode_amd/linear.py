@@ -171,28 +171,40 @@ def nf4_gemm(a, w, mode, epi=0, bias=None, resid=None, out=None, swiglu_I=0, spl
     return out
 
 
-_HGEMM_WS = {}  # (M, N, K, epi, splits) -> fp32 workspace elements qlora_hgemm uses
-# qlora_hgemm in one slice runs a last, nearly empty round of tiles as K slices (default of
+_HGEMM_WS = {}  # (M, N, K, epi, tile, splits) -> fp32 workspace elements qlora_gemm16 uses
+# qlora_gemm16 in one slice runs a last, nearly empty round of tiles as K slices (default of
 # hgemm's `tail`)
 HGEMM_TAIL = True
 
 
-def hgemm_workspace(M, N, K, epi, splits):
-    """fp32 elements of qlora_hgemm's workspace for this problem (qlora_hgemm_workspace)."""
-    key = (M, N, K, epi, splits)
+def hgemm_workspace(M, N, K, epi, splits, tile=256, stages=2, mode=0):
+    """fp32 elements of qlora_gemm16's workspace for this problem (qlora_gemm16_workspace;
+    tile 0 / splits 0: the automatic plan's)."""
+    key = (M, N, K, mode, epi, tile, stages, splits)
     n = _HGEMM_WS.get(key)
     if n is None:
         c = ctypes.c_int64(0)
-        _lib.call("qlora_hgemm_workspace", M, N, K, epi, splits, ctypes.byref(c))
+        _lib.call("qlora_gemm16_workspace", M, N, K, mode, epi, tile, stages, splits,
+                  ctypes.byref(c))
         n = _HGEMM_WS[key] = c.value
     return n
 
 
+def gemm_plan(M, N, K, mode, epi=0):
+    """(tile, stages, splits) of qlora_gemm16's automatic plan for this problem."""
+    t, st, sp = ctypes.c_int32(0), ctypes.c_int32(0), ctypes.c_int32(0)
+    _lib.call("qlora_gemm16_plan", M, N, K, mode, epi, ctypes.byref(t), ctypes.byref(st),
+              ctypes.byref(sp))
+    return t.value, st.value, sp.value
+
+
 def hgemm(a, b, mode, epi=0, bias=None, resid=None, out=None, swiglu_I=0, splits=None,
-          tail=None):
-    """The MFMA GEMM with an fp16 B (qlora_hgemm): mode 0 C = A B^T (B [N, K]), mode 1 C = A B
-    (B [K, N]); epilogues as nf4_gemm. tail: with one slice, the tiles of a last, nearly empty
-    round of the GPU run as K slices through a workspace (False: whole; None: HGEMM_TAIL)."""
+          tail=None, tile=256, stages=2):
+    """The MFMA GEMM with an fp16 B (qlora_gemm16): mode 0 C = A B^T (B [N, K]), mode 1 C = A B
+    (B [K, N]); epilogues as nf4_gemm; tile: 256 or 128 (output tile edge), stages: 2, or 4 for
+    128 x 128 tiles (one workgroup per CU, loads three k-tiles ahead). tail: with one slice, the
+    tiles of a last, nearly empty round of the GPU run as K slices through a workspace (False:
+    whole; None: HGEMM_TAIL)."""
     dev = a.device
     a = _a16(a)
     _need(b, "b", torch.float16, dev, contiguous=False)
@@ -213,13 +225,17 @@ def hgemm(a, b, mode, epi=0, bias=None, resid=None, out=None, swiglu_I=0, splits
     out, ldr = _gemm_out(a, M, n_out, epi, resid, out, dev)
     if M == 0:
         return out
-    splits = split_k(M, n_out, K, epi) if splits is None else splits
+    if tile == 0:  # the library's plan
+        splits = 0
+    elif splits is None:
+        splits = split_k(M, n_out, K, epi)
     tail = HGEMM_TAIL if tail is None else tail
-    n_ws = hgemm_workspace(M, n_out, K, epi, splits) if splits > 1 or tail else 0
+    n_ws = hgemm_workspace(M, n_out, K, epi, splits, tile, stages, mode) \
+        if splits != 1 or tail or tile == 0 else 0
     ws = torch.empty((n_ws,), device=dev, dtype=torch.float32) if n_ws else None
-    _lib.call("qlora_hgemm", _ptr(a), a.stride(0), _ptr(b), b.stride(0), M, n_out, K, mode,
-              _ptr(out), out.stride(0), _ptr(bias), _ptr(resid), ldr, epi, swiglu_I, splits,
-              _ptr(ws), 0 if ws is None else ws.numel(), _stream(dev))
+    _lib.call("qlora_gemm16", _ptr(a), a.stride(0), _ptr(b), b.stride(0), M, n_out, K, mode,
+              _ptr(out), out.stride(0), _ptr(bias), _ptr(resid), ldr, epi, swiglu_I, tile,
+              stages, splits, _ptr(ws), 0 if ws is None else ws.numel(), _stream(dev))
     return out
 
 
@@ -227,7 +243,22 @@ def nf4_linear(x, w, bias=None):
     """Y = X W^T [+ bias], fp16 [M, N]."""
     if BACKEND == "fused":
         return nf4_gemm(x, w, 0, epi=1 if bias is not None else 0, bias=bias)
+    if GEMM == "package" and tiles(x.shape[1], _shape(w)[0], 0):
+        return hgemm(x, dequantize(w), 0, epi=1 if bias is not None else 0, bias=bias, tile=0)
     return gemm.mm(x, dequantize(w), gemm.NT, bias=bias)
+
+
+# Which GEMMs run the dequantized products and the lm_head's: "package" - this library's MFMA
+# GEMM (qlora_gemm16) with its fixed tile/split plan; "library" - rocBLAS/hipBLASLt with a
+# variant measured per shape and token bucket (gemm.py), kept for comparison.
+GEMM = "package"
+
+
+def tiles(K, N, mode):
+    """Whether qlora_gemm16 takes this product: the reduction in blocks of 128, N a multiple of
+    8 (NT) or of 128 (NN). Every Qwen2 size does (H, I, the vocabulary 151,936); a shape that
+    does not (test models' odd vocabularies) runs torch's matmul."""
+    return K % 128 == 0 and (N % 8 == 0 if mode == 0 else N % 128 == 0)
 
 
 # With the layer-wide dequant: the gate|up product of a recomputing layer's forward on the MFMA
@@ -301,23 +332,26 @@ def nf4_linear_swiglu(x, w, I):
     fits = _gemm_fits(I, x.shape[1])
     if swiglu_fused_nf4() and fits:
         return nf4_gemm(x, w, 0, epi=3, swiglu_I=I)
-    if swiglu_on_package(x.device.index or 0, I, x.shape[1], x.shape[0]):
+    if GEMM == "package" and fits:
+        return hgemm(x, dequantize(w), 0, epi=3, swiglu_I=I, tile=0)
+    if GEMM != "package" and swiglu_on_package(x.device.index or 0, I, x.shape[1], x.shape[0]):
         return hgemm(x, dequantize(w), 0, epi=3, swiglu_I=I)
     from .ops import _glu_fwd
     return _glu_fwd(nf4_linear(x, w), I)
 
 
 def nf4_linear_gu(x, w):
-    """[g | u] = X W^T for the stacked gate|up weight, fp16 [M, 2 I] (kept for the backward;
-    gemm.mm's tuned variant, the package's GEMM among the candidates)."""
+    """[g | u] = X W^T for the stacked gate|up weight, fp16 [M, 2 I] (kept for the backward)."""
     return nf4_linear(x, w)
 
 
 def nf4_linear_resid(x, w, resid, out=None):
-    """fp32 resid + fp16(X W^T) (the layer output h2 + d); with a split-K library GEMM the
-    residual is added by the split's reduce (one pass, no fp16 product in memory)."""
+    """fp32 resid + fp16(X W^T) (the layer output h2 + d): the residual added in the GEMM's
+    epilogue (or the split-K reduce's), no fp16 product in memory."""
     if BACKEND == "fused":
         return nf4_gemm(x, w, 0, epi=2, resid=resid, out=out)
+    if GEMM == "package" and tiles(x.shape[1], _shape(w)[0], 0):
+        return hgemm(x, dequantize(w), 0, epi=2, resid=resid, out=out, tile=0)
     return gemm.mm_resid(_a16(x), dequantize(w), gemm.NT, resid, out=out)
 
 
@@ -328,14 +362,24 @@ def nf4_linear_t(dy, w):
         return nf4_gemm(dy, w, 1)
     if dy.dtype != torch.float16:
         dy = dy.to(torch.float16)
+    if GEMM == "package" and tiles(dy.shape[1], _shape(w)[1], 1):
+        return hgemm(dy, dequantize(w), 1, tile=0)
     return gemm.mm(dy, dequantize(w), gemm.NN)
 
 
 def linear(x, w):
     """x W^T for an fp16 weight [V, H] (the lm_head)."""
+    if GEMM == "package":
+        if tiles(x.shape[1], w.shape[0], 0):
+            return hgemm(x, w, 0, tile=0)
+        return torch.mm(x, w.t())
     return gemm.mm(x, w, gemm.NT)
 
 
 def linear_t(g, w):
     """g W for an fp16 weight [V, H]."""
+    if GEMM == "package":
+        if tiles(g.shape[1], w.shape[1], 1):
+            return hgemm(g, w, 1, tile=0)
+        return torch.mm(g, w)
     return gemm.mm(g, w, gemm.NN)

@@ -322,6 +322,48 @@ int qlora_hgemm_timed(const void* a, int64_t lda, const void* b, int64_t ldb, in
                       void* stop);
 
 /*
+ * qlora_hgemm on tile x tile output tiles: tile 256 (qlora_hgemm itself: one workgroup of four
+ * 128 x 128 wavefront blocks per CU) or 128 (four 64 x 64 wavefront blocks, two workgroups per
+ * CU: four times the tiles, for the narrow products - N = 1536 or 2048 at a few thousand
+ * tokens). In one slice both tile shapes give the same bits (each output sums its k-steps of
+ * 16 in order); split-K and the K-sliced last round (whose size follows the tile count and the
+ * GPU's workgroup slots: 256 tiles of 256, 512 of 128) sum fp32 partials in a fixed order.
+ * stages: 2 (either tile; two 128 x 128 workgroups then share a CU) or 4 (128 x 128 tiles
+ * only: 128 KB of LDS, one workgroup per CU, each k-tile's loads issued three k-tiles ahead).
+ * tile 0 with splits 0 (and any stages): the plan of qlora_gemm16_plan.
+ * Replaces the same cuBLAS products as qlora_hgemm (engine.py:1082, 1112, 1163, 1179, 1239,
+ * 1293, 1301, 1316, 1376-1381). Requires qlora_hgemm's conditions with mode 1: N % tile == 0;
+ * epi 3: N % (tile / 2) == 0; K % (64 stages) == 0.
+ */
+int qlora_gemm16(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t M, int64_t N,
+                 int64_t K, int32_t mode, void* c, int64_t ldc, const void* bias,
+                 const float* resid, int64_t ldr, int32_t epi, int64_t swiglu_I, int32_t tile,
+                 int32_t stages, int32_t splits, float* ws, int64_t ws_elems, void* stream);
+
+/* qlora_gemm16 with the start/stop events of qlora_hgemm_timed (no reference counterpart). */
+int qlora_gemm16_timed(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t M,
+                       int64_t N, int64_t K, int32_t mode, void* c, int64_t ldc,
+                       const void* bias, const float* resid, int64_t ldr, int32_t epi,
+                       int64_t swiglu_I, int32_t tile, int32_t stages, int32_t splits,
+                       float* ws, int64_t ws_elems, void* stream, void* start, void* stop);
+
+/*
+ * fp32 workspace elements (*elems) qlora_gemm16 uses for this problem, mode, tile and stage count
+ * (as qlora_hgemm_workspace; tile 0 / splits 0: the automatic plan's). No reference counterpart
+ * (sizes the caller's workspace).
+ */
+int qlora_gemm16_workspace(int64_t M, int64_t N, int64_t K, int32_t mode, int32_t epi,
+                           int32_t tile, int32_t stages, int32_t splits, int64_t* elems);
+
+/*
+ * The tile, stage count and K split qlora_gemm16 runs when given tile 0 and splits 0: a fixed
+ * rule on (M, N, K, mode, epi), so a problem always runs the same kernels and gives the same
+ * bits (no timing). No reference counterpart.
+ */
+int qlora_gemm16_plan(int64_t M, int64_t N, int64_t K, int32_t mode, int32_t epi, int32_t* tile,
+                      int32_t* stages, int32_t* splits);
+
+/*
  * out = a + fp32(d) over numel elements (a, out f32; d f16; numel % 4 == 0; out may alias a):
  * the residual add after the down projection, h3 = h2 + d (engine.py:1048-1051, 1179).
  */

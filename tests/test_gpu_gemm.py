@@ -295,3 +295,86 @@ def test_hgemm_timed_form(pkg, splits):
     torch.cuda.synchronize()
     assert torch.equal(got, want)
     assert start.elapsed_time(stop) > 0
+
+
+@pytest.mark.parametrize("mode,epi,M,N", [(0, 0, 700, 2048), (0, 1, 2600, 2048),
+                                          (0, 2, 2549, 1536), (0, 3, 1875, 8960),
+                                          (1, 0, 2560, 1536), (1, 2, 301, 8960),
+                                          (0, 0, 1, 1536), (1, 0, 129, 1536)])
+def test_tile128_equals_tile256(pkg, mode, epi, M, N):
+    """qlora_gemm16 on 128 x 128 tiles gives the 256 x 256 tiles' results bit for bit in one
+    slice (each output sums its k-steps of 16 in order), for every epilogue, both orientations,
+    ragged M; and matches fp64."""
+    L = pkg.linear
+    g = torch.Generator(device=DEV).manual_seed(M + 10 * epi + mode)
+    K = 1536
+    kw = {}
+    if epi == 3:
+        w = (torch.randn(2 * N, K, generator=g, device=DEV) * 0.02).half()
+        kw["swiglu_I"] = N
+    else:
+        w = (torch.randn(*((N, K) if mode == 0 else (K, N)), generator=g, device=DEV) *
+             0.02).half()
+    a = torch.randn(M, K, generator=g, device=DEV).half()
+    if epi == 1:
+        kw["bias"] = (torch.randn(N, generator=g, device=DEV) * 0.1).half()
+    if epi == 2:
+        kw["resid"] = torch.randn(M, N, generator=g, device=DEV)
+    big = L.hgemm(a, w, mode, epi=epi, splits=1, tail=False, tile=256, **kw)
+    small = L.hgemm(a, w, mode, epi=epi, splits=1, tail=False, tile=128, **kw)
+    assert torch.equal(big, small)
+    deep = L.hgemm(a, w, mode, epi=epi, splits=1, tail=False, tile=128, stages=4, **kw)
+    assert torch.equal(big, deep)
+    prod = a.double() @ (w.double().t() if mode == 0 else w.double())
+    if epi == 3:
+        gt, up = prod[:, :N].half().double(), prod[:, N:].half().double()
+        want = gt * torch.sigmoid(gt) * up
+    elif epi == 2:
+        want = kw["resid"].double() + prod.half().double()
+    else:
+        want = prod + (kw["bias"].double() if epi == 1 else 0)
+    assert rel_err(small, want) < 1e-3
+
+
+@pytest.mark.parametrize("mode,epi,M,N,K", [(0, 2, 2560, 1536, 8960), (1, 0, 2560, 1536, 17920),
+                                            (0, 1, 2949, 2048, 1536), (0, 3, 2949, 8960, 1536),
+                                            (1, 0, 2949, 8960, 1536), (0, 0, 1875, 1536, 1536)])
+def test_tile128_splits_and_tail_against_fp64(pkg, mode, epi, M, N, K):
+    """128 x 128 tiles with split-K (2 and 4 slices) and with the K-sliced last round (the
+    step's token counts: 2,949 tokens -> 24 row tiles, 288 or 1,680 tiles over 512 slots)
+    against fp64 of the same operands."""
+    L = pkg.linear
+    g = torch.Generator(device=DEV).manual_seed(M + N + K + epi)
+    kw = {}
+    if epi == 3:
+        w = (torch.randn(2 * N, K, generator=g, device=DEV) * 0.02).half()
+        kw["swiglu_I"] = N
+    else:
+        w = (torch.randn(*((N, K) if mode == 0 else (K, N)), generator=g, device=DEV) *
+             0.02).half()
+    a = torch.randn(M, K, generator=g, device=DEV).half()
+    if epi == 1:
+        kw["bias"] = (torch.randn(N, generator=g, device=DEV) * 0.1).half()
+    if epi == 2:
+        kw["resid"] = torch.randn(M, N, generator=g, device=DEV)
+    prod = a.double() @ (w.double().t() if mode == 0 else w.double())
+    if epi == 3:
+        gt, up = prod[:, :N].half().double(), prod[:, N:].half().double()
+        want = gt * torch.sigmoid(gt) * up
+    elif epi == 2:
+        want = kw["resid"].double() + prod.half().double()
+    else:
+        want = prod + (kw["bias"].double() if epi == 1 else 0)
+    variants = [(1, True)] + ([] if epi == 3 else [(2, False), (4, False)])
+    for stages in (2, 4):
+        for splits, tail in variants:
+            kt = K // 64
+            per = -(-(-(-kt // splits)) // stages) * stages  # k-tiles a slice, whole loop trips
+            if per * (splits - 1) >= kt:
+                continue  # the split would leave a slice empty (refused by the library)
+            got = L.hgemm(a, w, mode, epi=epi, splits=splits, tail=tail, tile=128, stages=stages,
+                          **kw)
+            err = rel_err(got, want)
+            print(f"tile 128 stages {stages} splits {splits} tail {tail}: rel {err:.2e}",
+                  flush=True)
+            assert err < 1e-3
