@@ -214,13 +214,25 @@ def measure_step_kernels(pkg, trainer, batches, cfg):
     every = gemms[0].summary(also=gemms[1:])
     if every is not None:
         out.append(dict(every, kernel="every library GEMM of the step (projections, lm_head)"))
-    gu = gemms[0].summary(also=gemms[1:], select=lambda a: a[0] == 0 and a[2] == gate_up)
-    if gu is not None:
-        out.append(dict(gu, kernel="gate|up forward GEMM of the library (the backward's recompute, "
-                                   "y = x W^T, N = 2 I)"))
-    mine = own.summary()
+    # the package's GEMM (qlora_gemm16, args: a, lda, b, ldb, M, N, K, mode, ..., epi at 13)
+    H = cfg.hidden_size
+    classes = (
+        ("every package GEMM launch of the step (projections, lm_head, its dX products)", None),
+        ("narrow products, K <= 2048 (qkv, o and their dX; 128 x 128 tiles)",
+         lambda a: a[5] <= 2048 and a[6] <= 2048),
+        ("long reductions (down forward, gate|up dX, the head's G E; 256 x 256 split-K)",
+         lambda a: a[5] <= 2048 and a[6] > 2048),
+        ("gate|up recompute forward ([g|u] kept for the backward, N = 2 I)",
+         lambda a: a[7] == 0 and a[5] == gate_up and a[13] == 0),
+        ("down dX (N = I)", lambda a: a[7] == 1 and a[5] == cfg.intermediate_size),
+        ("lm_head logits (N = V)", lambda a: a[7] == 0 and a[5] == cfg.vocab_size))
+    for name, sel in classes:
+        r = own.summary(select=sel)
+        if r is not None:  # (HBM traffic was measured on the SwiGLU launches only)
+            out.append(dict(r, kernel=name, traffic=None))
+    mine = own.summary(select=lambda a: a[13] == 3)
     if mine is not None:
-        mine = dict(mine, kernel="hgemm_kernel (qlora_hgemm): the gate|up forward with the "
+        mine = dict(mine, kernel="hgemm_kernel (qlora_gemm16): the gate|up forward with the "
                                  "SwiGLU epilogue, this package's MFMA GEMM")
     return mine, dq.summary(), out
 
@@ -626,7 +638,7 @@ def main():
                                    "recomputes its forward (NF4 dequant included) in backward"
                                    if args.policy == "recompute" else
                                    "every layer keeps its intermediates (no recompute)"),
-                   "gemm_backend": pkg.linear.BACKEND},
+                   "gemm_backend": pkg.linear.BACKEND, "gemm": pkg.linear.GEMM},
         "roofline": kernels[0],
         "roofline_dequant": kernels[1],
         "roofline_mfma": kernels[2],

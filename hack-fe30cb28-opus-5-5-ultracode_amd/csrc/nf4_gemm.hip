@@ -1192,39 +1192,78 @@ int64_t n_tiles_of(int64_t N, int epi, int tile) {
   return epi == kEpiSwiglu ? N / (tile / 2) : qlora_cdiv(N, tile);
 }
 
-// The tile shape, stage count and K split of qlora_gemm16 with tile 0 / splits 0: a fixed rule
-// from the step's measured shapes (M = 1,875 - 2,949 tokens, MI355X; every choice below was the
-// fastest of the package's variants there), so a problem always runs the same kernels and gives
-// the same bits:
-//   - the SwiGLU form and wide products (N > 4096: gate|up, the down projection's dX, the
-//     lm_head): 256 x 256 tiles, one slice (the last round's few tiles K-sliced);
-//   - narrow products (N <= 4096) with K <= 4096 (qkv, o and their dX): 128 x 128 tiles, four
-//     stages while the tiles fit one round of the 256 CUs (each CU one workgroup), else two
-//     stages (two workgroups share a CU);
-//   - narrow products with a long K (the down projection, gate|up's dX, the head's G E):
-//     256 x 256 tiles split along K while the slices fit one round and keep >= 32 k-tiles each.
+// The tile shape, stage count and K split of qlora_gemm16 with tile 0 / splits 0: the cheapest
+// variant under a fixed cost model, so a problem always runs the same kernels and gives the same
+// bits (no timing at run time). A launch runs in rounds (as many workgroups as the GPU holds at
+// once: 256 tiles of 256 x 256, 512 of 128 x 128 with two stages, 256 with four); its cost is
+//   a rounds + b (the k elements its rounds walk) + c (MB of fp32 partials) + d (a reduce),
+// the constants (us) least-squares fits of every variant over the step's nine products and the
+// lm_head's at 1,024 - 4,096 tokens on MI355X (HIP graphs, warm caches; median error 5-8 %).
+// Candidates: 256 x 256 tiles in 1-6 K slices, 128 x 128 tiles in 1, 2 or 4 (up to K = 12,288:
+// beyond that the measurements favoured 256 x 256 tiles, whose loads per flop are half).
+struct PlanCoef {
+  int tile, stages;
+  double a, b, c, d;
+};
+constexpr PlanCoef kPlanCoef[] = {{256, 2, 9.74, 0.01998, 0.1219, 7.50},
+                                  {128, 4, 4.62, 0.00788, 0.1462, 5.29},
+                                  {128, 2, 6.31, 0.01262, 0.1125, 6.45}};
+
+// The model's cost (us) of one variant, or a negative value when it cannot run the problem.
+double plan_cost(int64_t M, int64_t N, int64_t K, int mode, int epi, const PlanCoef& v,
+                 int splits) {
+  const int tile = v.tile, stages = v.stages;
+  const int64_t kt = K / kBK64;
+  if (kt % stages != 0 || (mode == 1 && N % tile != 0)) return -1.0;
+  if (epi == kEpiSwiglu && (splits > 1 || N % (tile / 2) != 0)) return -1.0;
+  const int64_t per = qlora_cdiv(qlora_cdiv(kt, splits), stages) * stages;
+  if (per * (splits - 1) >= kt) return -1.0;  // an empty slice
+  const int64_t m_tiles = qlora_cdiv(M, tile), tiles = m_tiles * n_tiles_of(N, epi, tile);
+  const int64_t slots = slots_of(tile, stages);
+  if (splits > 1) {
+    const double rounds = (double)qlora_cdiv(tiles * splits, slots);
+    return v.a * rounds + v.b * rounds * (double)(per * kBK64) +
+           v.c * 8.0 * splits * (double)M * (double)N / 1e6 + v.d;
+  }
+  const int64_t full = tiles / slots, r = tiles - full * slots;
+  double rounds = (double)full, kwalk = (double)full * (double)K, part = 0.0, red = 0.0;
+  if (r > 0) {
+    int main_t, ts, ktp;
+    rounds += 1.0;
+    if (tail_plan(m_tiles, tiles / m_tiles, kt, tile, stages, &main_t, &ts, &ktp) > 0) {
+      kwalk += (double)ktp * kBK64;
+      part = 8.0 * (double)(r * ts) * tile * tile / 1e6;
+      red = 1.0;
+    } else {
+      kwalk += (double)K;
+    }
+  }
+  return v.a * rounds + v.b * kwalk + v.c * part + v.d * red;
+}
+
 void auto_plan(int64_t M, int64_t N, int64_t K, int mode, int epi, int* tile, int* stages,
                int* splits) {
-  const int64_t kt = K / kBK64;
+  double best = -1.0;
   *tile = 256;
   *stages = 2;
   *splits = 1;
-  if (epi == kEpiSwiglu || N > 4096) return;
-  if (K <= 4096 && (mode == 0 || N % 128 == 0)) {
-    const int64_t tiles = qlora_cdiv(M, 128) * qlora_cdiv(N, 128);
-    *tile = 128;
-    *stages = (tiles <= kCUs && kt % 4 == 0) ? 4 : 2;
-    return;
+  // first pass: 128 x 128 tiles up to K = 12,288 only; second (when none of the first's can run
+  // the problem: an NN product whose N is not a multiple of 256), every variant
+  for (int pass = 0; pass < 2 && best < 0.0; ++pass) {
+    for (const PlanCoef& v : kPlanCoef) {
+      if (pass == 0 && v.tile == 128 && K > 12288) continue;
+      for (int sp = 1; sp <= (v.tile == 256 ? 6 : 4); ++sp) {
+        if (v.tile == 128 && sp == 3) continue;
+        const double c = plan_cost(M, N, K, mode, epi, v, sp);
+        if (c >= 0.0 && (best < 0.0 || c < best)) {
+          best = c;
+          *tile = v.tile;
+          *stages = v.stages;
+          *splits = sp;
+        }
+      }
+    }
   }
-  if (mode == 1 && N % 256 != 0) {  // NN on 128 x 128 tiles only
-    *tile = 128;
-    return;
-  }
-  const int64_t tiles = qlora_cdiv(M, 256) * qlora_cdiv(N, 256);
-  int p = 1;
-  while (p < 16 && tiles * (p + 1) <= kCUs && kt / (p + 1) >= 32) ++p;
-  while (p > 1 && qlora_cdiv(qlora_cdiv(kt, p), 2) * 2 * (p - 1) >= kt) --p;  // no empty slice
-  *splits = p;
 }
 
 // Shared launch path: shapes and workspace checked, then the tile grid (and the split-K reduce).

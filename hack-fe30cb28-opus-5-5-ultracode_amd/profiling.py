@@ -15,10 +15,10 @@ from . import _lib
 HBM_PEAK_GBS = 8000.0
 FP16_PEAK_TFLOPS = 2500.0
 
-# the kernel reported as the step's roofline entry: the largest hand-written kernel of the step by
-# time (the package's MFMA GEMM: the gate|up forward with the SwiGLU epilogue); the dequant, the
-# north star's "NF4 dequant HBM GB/s", is reported beside it
-DOMINANT = "qlora_hgemm"
+# the entry point of the step's largest hand-written kernel by time, the package's MFMA GEMM
+# (every projection and lm_head product; the roofline entry is its gate|up forward with the
+# SwiGLU epilogue); the dequant, the north star's "NF4 dequant HBM GB/s", is reported beside it
+DOMINANT = "qlora_gemm16"
 DEQUANT = "qlora_nf4_dequant_many"
 
 # Measured HBM bytes per launch over algorithmic bytes per launch: rocprofv3 FETCH_SIZE and
@@ -32,7 +32,7 @@ DEQUANT = "qlora_nf4_dequant_many"
 # weighted by launch; 2.74 at 9 row tiles, 2.78 at 10, 2.97 at 11 (sliced tail), 3.44 at 12.
 # The excess is the A tile re-read by each XCD and B tiles re-read past the 4 MB L2
 # (FETCH_SIZE counts what leaves the L2, Infinity Cache hits included).
-TRAFFIC_RATIO = {"qlora_nf4_dequant_many": 1.0018, "qlora_hgemm": 2.92}
+TRAFFIC_RATIO = {"qlora_nf4_dequant_many": 1.0018, "qlora_hgemm": 2.92, "qlora_gemm16": 2.92}
 
 
 def _dequant_bytes(args):
@@ -63,18 +63,20 @@ def _dequant_many_bytes(args):
 
 # entries with a form that records the events from the kernel dispatch itself
 TIMED = {"qlora_nf4_dequant_many": "qlora_nf4_dequant_many_timed",
-         "qlora_hgemm": "qlora_hgemm_timed"}
+         "qlora_hgemm": "qlora_hgemm_timed", "qlora_gemm16": "qlora_gemm16_timed"}
 
 
 def hgemm_flops(args):
-    """2 M N K of one qlora_hgemm launch (a, lda, b, ldb, M, N, K, mode, ..., epi at 13): N is
-    the output's columns, I with the SwiGLU epilogue, whose product is [M, 2 I]."""
+    """2 M N K of one qlora_hgemm / qlora_gemm16 launch (a, lda, b, ldb, M, N, K, mode, ..., epi
+    at 13): N is the output's columns, I with the SwiGLU epilogue, whose product is
+    [M, 2 I]."""
     return 2.0 * args[4] * args[5] * args[6] * (2 if args[13] == 3 else 1)
 
 
 def hgemm_bytes(args):
-    """Algorithmic HBM bytes of one qlora_hgemm launch: A [M, K], the weight ([N, K], [2 I, K]
-    with the SwiGLU epilogue, [K, N] in NN) and the fp16 output [M, N] once each."""
+    """Algorithmic HBM bytes of one qlora_hgemm / qlora_gemm16 launch: A [M, K], the weight
+    ([N, K], [2 I, K] with the SwiGLU epilogue, [K, N] in NN) and the fp16 output [M, N] once
+    each."""
     M, N, K, epi = args[4], args[5], args[6], args[13]
     return 2.0 * (M * K + (2 * N if epi == 3 else N) * K + M * N)
 

@@ -178,3 +178,45 @@ def test_dropout_keep_below_is_the_fp32_compare(pkg, p_keep):
         np.linspace(0, 2**32 - 1, 4097).astype(np.int64)])).astype(np.uint32)
     want = _uniform32(words) < p
     assert np.array_equal(words.astype(np.int64) < T, want), (p_keep, T)
+
+
+def test_gemm16_plan_is_fixed_and_valid(pkg):
+    """qlora_gemm16's automatic plan (host only, no device call): the same answer every time
+    for a problem, and always a variant the library accepts (its workspace query succeeds with
+    that explicit variant, and asks the same workspace as the automatic form) - over the step's
+    products at token counts from 1 to 8,192 and other Qwen2 widths."""
+    L = pkg.linear
+    shapes = [(0, 2048, 1536, 1), (0, 1536, 1536, 2), (0, 17920, 1536, 0), (0, 8960, 1536, 3),
+              (0, 1536, 8960, 2), (1, 1536, 2048, 0), (1, 1536, 1536, 0), (1, 1536, 17920, 0),
+              (1, 8960, 1536, 0), (0, 151936, 1536, 0), (1, 1536, 151936, 0),
+              (0, 1152, 896, 1), (1, 896, 4864, 0), (0, 4864, 896, 3), (1, 3584, 18944, 0)]
+    for M in (1, 37, 300, 1875, 2325, 2560, 2949, 4096, 8192):
+        for mode, N, K, epi in shapes:
+            plan = L.gemm_plan(M, N, K, mode, epi)
+            assert plan == L.gemm_plan(M, N, K, mode, epi)
+            tile, stages, splits = plan
+            assert (tile, stages) in ((256, 2), (128, 2), (128, 4)) and 1 <= splits <= 8
+            assert (K // 64) % stages == 0 and (mode == 0 or N % tile == 0)
+            assert epi != 3 or splits == 1
+            auto = L.hgemm_workspace(M, N, K, epi, 0, 0, 0, mode)
+            assert auto == L.hgemm_workspace(M, N, K, epi, splits, tile, stages, mode)
+            if splits > 1:
+                assert auto == splits * M * N
+
+
+def test_gemm16_plan_at_the_step_shapes(pkg):
+    """The plan's choices at config-5 token counts, each the variant measured fastest there on
+    MI355X (HIP graphs, warm caches): 128 x 128 tiles for the narrow products (four stages while
+    one round of 256 CUs holds them, else two workgroups per CU), 256 x 256 tiles split along K
+    for the longest reductions, and 256 x 256 tiles in one slice for gate|up and the lm_head."""
+    L = pkg.linear
+    assert L.gemm_plan(2560, 1536, 1536, 1, 0) == (128, 4, 1)  # o dX: 240 tiles
+    assert L.gemm_plan(2560, 1536, 2048, 1, 0) == (128, 4, 1)  # qkv dX
+    assert L.gemm_plan(2949, 1536, 1536, 1, 0) == (128, 2, 1)  # 288 tiles: two per CU
+    assert L.gemm_plan(2560, 2048, 1536, 0, 1) == (128, 2, 1)  # qkv + bias: 320 tiles
+    assert L.gemm_plan(2560, 8960, 1536, 0, 3) == (256, 2, 1)  # gate|up with SwiGLU
+    assert L.gemm_plan(2560, 151936, 1536, 0, 0) == (256, 2, 1)  # lm_head
+    assert L.gemm_plan(2560, 1536, 8960, 0, 2) == (128, 4, 1)  # down + residual: 84 us
+    assert L.gemm_plan(2949, 1536, 8960, 0, 2) == (256, 2, 3)  # (288 tiles of 128)
+    assert L.gemm_plan(2560, 1536, 17920, 1, 0) == (256, 2, 4)  # gate|up dX
+    assert L.gemm_plan(2560, 8960, 1536, 1, 0) == (128, 2, 1)  # down dX: 1,400 tiles

@@ -172,6 +172,7 @@ def test_swiglu_tuned_choice(pkg):
     G, L = pkg.gemm, pkg.linear
     G.reset()
     L._SWIGLU_ON_PKG.clear()
+    gemm_was, L.GEMM = L.GEMM, "library"  # the step's library path (the per-bucket choice)
     try:
         I, K, M = 1024, 1536, 700
         g = torch.Generator(device=DEV).manual_seed(13)
@@ -191,6 +192,7 @@ def test_swiglu_tuned_choice(pkg):
             err = (m.double() - want).abs()
             assert bool((err <= want.abs() * 2.0**-9 + 2e-3 * want.abs().max()).all())
     finally:
+        L.GEMM = gemm_was
         G.reset()
         L._SWIGLU_ON_PKG.clear()
 

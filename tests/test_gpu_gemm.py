@@ -378,3 +378,42 @@ def test_tile128_splits_and_tail_against_fp64(pkg, mode, epi, M, N, K):
             print(f"tile 128 stages {stages} splits {splits} tail {tail}: rel {err:.2e}",
                   flush=True)
             assert err < 1e-3
+
+
+@pytest.mark.parametrize("M", [1, 300, 1875, 2949])
+def test_auto_plan_against_fp64(pkg, M):
+    """qlora_gemm16 with its automatic plan (tile 0) at the step's nine products, every epilogue
+    they use, against fp64 of the same operands; and the same bits on a second call."""
+    L = pkg.linear
+    g = torch.Generator(device=DEV).manual_seed(M)
+    cases = [(0, 2048, 1536, 1), (0, 1536, 1536, 2), (0, 17920, 1536, 0), (0, 8960, 1536, 3),
+             (0, 1536, 8960, 2), (1, 1536, 2048, 0), (1, 1536, 1536, 0), (1, 1536, 17920, 0),
+             (1, 8960, 1536, 0)]
+    for mode, N, K, epi in cases:
+        kw = {}
+        if epi == 3:
+            w = (torch.randn(2 * N, K, generator=g, device=DEV) * 0.02).half()
+            kw["swiglu_I"] = N
+        else:
+            w = (torch.randn(*((N, K) if mode == 0 else (K, N)), generator=g, device=DEV) *
+                 0.02).half()
+        a = torch.randn(M, K, generator=g, device=DEV).half()
+        if epi == 1:
+            kw["bias"] = (torch.randn(N, generator=g, device=DEV) * 0.1).half()
+        if epi == 2:
+            kw["resid"] = torch.randn(M, N, generator=g, device=DEV)
+        got = L.hgemm(a, w, mode, epi=epi, tile=0, **kw)
+        again = L.hgemm(a, w, mode, epi=epi, tile=0, **kw)
+        assert torch.equal(got, again)
+        prod = a.double() @ (w.double().t() if mode == 0 else w.double())
+        if epi == 3:
+            gt, up = prod[:, :N].half().double(), prod[:, N:].half().double()
+            want = gt * torch.sigmoid(gt) * up
+        elif epi == 2:
+            want = kw["resid"].double() + prod.half().double()
+        else:
+            want = prod + (kw["bias"].double() if epi == 1 else 0)
+        err = rel_err(got, want)
+        print(f"M={M} mode={mode} N={N} K={K} epi={epi} plan={L.gemm_plan(M, N, K, mode, epi)}"
+              f" rel {err:.2e}", flush=True)
+        assert err < 1e-3
