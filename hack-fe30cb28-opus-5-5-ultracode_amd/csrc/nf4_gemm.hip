@@ -73,7 +73,12 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 constexpr int kBM = 256, kBN = 256, kBK = 32, kStages = 4, kThreads = 256;
 constexpr int kTile = 256 * kBK;  // halves per operand stage (16 KB)
 
-enum { kEpiStore = 0, kEpiBias = 1, kEpiResid = 2, kEpiSwiglu = 3, kEpiPartial = 4 };
+enum { kEpiStore = 0, kEpiBias = 1, kEpiResid = 2, kEpiSwiglu = 3, kEpiPartial = 4,
+       kEpiSwigluKeep = 5 };
+
+// The SwiGLU forms: 3 writes m = fp16(silu(g) u) only, 5 also the fp16 [g | u] product (a
+// recomputing layer keeps it for its backward instead of multiplying again).
+constexpr bool swiglu_epi(int epi) { return epi == kEpiSwiglu || epi == kEpiSwigluKeep; }
 enum { kBHalf = 0, kBNF4 = 1 };
 
 // Epilogues that leave through LDS from transposed accumulators (every one but the split-K
@@ -109,6 +114,8 @@ struct GemmArgs {
   int main_tiles, tail_splits, kt_per_tail;
   float* tail_ws;
   int bm, bn;            // output tile (fp16 B: 256 x 256 or 128 x 128)
+  uint16_t* gu;          // kEpiSwigluKeep: fp16 [M, 2 I] product [g | u] (ld ldgu)
+  int64_t ldgu;
 };
 
 // ---- swizzled LDS offsets (in halves) ---------------------------------------------------------
@@ -256,7 +263,7 @@ __device__ __forceinline__ uint4 nf4_decode8(const NF4Planes& t, uint32_t wd) {
 // the first BN/4 are gate rows and the last BN/4 the up rows of the same BN/4 output columns.
 template <int EPI, int BN = kBN>
 __device__ __forceinline__ int64_t nt_wrow(const GemmArgs& g, int64_t tile_n, int n) {
-  if constexpr (EPI == kEpiSwiglu) {
+  if constexpr (swiglu_epi(EPI)) {
     constexpr int WC = BN / 2, HC = BN / 4;
     const int64_t j = tile_n * (BN / 2) + (n / WC) * HC + (n % HC);
     return (n % WC) >= HC ? g.I + j : j;
@@ -383,7 +390,7 @@ __device__ __forceinline__ void store_tile(const GemmArgs& g, f32x16 (&acc)[BM /
     // each wavefront writes its block to LDS as fp16 (8-byte LDS stores of four columns,
     // 16-byte chunks XOR-swizzled by row so the 32 rows of a store spread over the banks), then
     // stores whole rows to memory with 16-byte stores
-    constexpr int kCols = EPI == kEpiSwiglu ? WC / 2 : WC;  // output columns of a wavefront
+    constexpr int kCols = swiglu_epi(EPI) ? WC / 2 : WC;  // output columns of a wavefront
     constexpr int kChunks = kCols / 8;
     constexpr int kHalf = WR / 2;  // rows staged in `lo`
     auto stage_off = [&](int row, int chunk) {
@@ -396,7 +403,7 @@ __device__ __forceinline__ void store_tile(const GemmArgs& g, f32x16 (&acc)[BM /
       uint16_t* base = i < FM / 2 ? lo : hi;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {  // 8-column group q of each 32-column block
-        if constexpr (EPI == kEpiSwiglu) {
+        if constexpr (swiglu_epi(EPI)) {
 #pragma unroll
           for (int j = 0; j < FN / 2; ++j) {
             const int col = j * 32 + 8 * q + c4;
@@ -431,8 +438,8 @@ __device__ __forceinline__ void store_tile(const GemmArgs& g, f32x16 (&acc)[BM /
     }
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the wavefront's own LDS stores
     constexpr int kRowsPer = 64 / kChunks;  // rows per 16-byte store instruction
-    const int64_t n_base = EPI == kEpiSwiglu ? tile_n * (BN / 2) + wn * (WC / 2)
-                                             : tile_n * BN + wn * WC;
+    const int64_t n_base = swiglu_epi(EPI) ? tile_n * (BN / 2) + wn * (WC / 2)
+                                           : tile_n * BN + wn * WC;
     if constexpr (EPI == kEpiResid) {
       // out = resid + f32(fp16 product), eight columns a lane: the residual row pieces of a
       // batch of rows are loaded before any output is stored (out may be resid itself; each
@@ -476,6 +483,42 @@ __device__ __forceinline__ void store_tile(const GemmArgs& g, f32x16 (&acc)[BM /
       const int64_t m = m0 + wm * WR + row, n = n_base + chunk * 8;
       if (m < g.M && n < g.N)
         *reinterpret_cast<uint4*>(static_cast<uint16_t*>(g.c) + m * g.ldc + n) = v;
+    }
+    if constexpr (EPI == kEpiSwigluKeep) {
+      // the product itself, fp16 [g | u]: the wavefront's WC B columns (its WC / 2 gate
+      // columns, then the matching up columns) staged as a plain store would, then written to
+      // gate column n and up column I + n of g.gu
+      constexpr int kCh2 = WC / 8, kRows2 = 64 / kCh2;
+      auto stage2 = [&](int row, int chunk) {
+        return (row % kHalf) * WC + ((chunk ^ (row & (kCh2 - 1))) << 3);
+      };
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // the m pass's LDS reads, before the area is reused
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const int row = i * 32 + col_in;
+        uint16_t* base = i < FM / 2 ? lo : hi;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int j = 0; j < FN; ++j) {
+            const int col = j * 32 + 8 * q + c4;
+            *reinterpret_cast<uint2*>(base + stage2(row, col >> 3) + c4) =
+                make_uint2(pack2h(acc[i][j][4 * q], acc[i][j][4 * q + 1]),
+                           pack2h(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]));
+          }
+      }
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+      const int64_t g_base = tile_n * (BN / 2) + wn * (WC / 2);
+#pragma unroll
+      for (int k = 0; k < WR / kRows2; ++k) {
+        const int row = k * kRows2 + lane / kCh2, chunk = lane % kCh2;
+        const uint4 v = *reinterpret_cast<const uint4*>((row < kHalf ? lo : hi) +
+                                                         stage2(row, chunk));
+        const int64_t m = m0 + wm * WR + row;
+        const int col = chunk * 8;
+        const int64_t n = g_base + (col % (WC / 2)) + (col >= WC / 2 ? g.I : 0);
+        if (m < g.M) *reinterpret_cast<uint4*>(g.gu + m * g.ldgu + n) = v;
+      }
     }
   } else {
 #pragma unroll
@@ -862,7 +905,7 @@ __device__ __forceinline__ void hgemm_tile(const GemmArgs& g, int64_t tile_m, in
     // rows past N (a last, partial tile: the lm_head's 151,936) re-read row N - 1
     dma_bk.init(g.ldb, [&](int r) -> int64_t {
       const int64_t row = nt_wrow<EPI, BN>(g, tile_n, r);
-      return (EPI == kEpiSwiglu || row < g.N) ? row : g.N - 1;
+      return (swiglu_epi(EPI) || row < g.N) ? row : g.N - 1;
     }, wave, lane);
     b_base = g.b;
     b_step = kBK64;
@@ -1016,7 +1059,7 @@ __global__ __launch_bounds__(kThreads, (BM == 128 && STAGES == 2) ? 2 : 1) void 
 // Tail split: the slices of each tail tile summed in slice order, then the epilogue (fp16 store,
 // bias, fp32 residual, SwiGLU), four outputs per thread. Tile g.bm x g.bn.
 __global__ __launch_bounds__(256) void tail_reduce_kernel(GemmArgs g, int epi, int tiles) {
-  const bool sw = epi == kEpiSwiglu;
+  const bool sw = swiglu_epi(epi);
   const int BM = g.bm, BN = g.bn, WC = BN / 2;
   const int per_tile = sw ? BM * (BN / 8) : BM * (BN / 4);  // threads per tile
   const int64_t id = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -1044,6 +1087,12 @@ __global__ __launch_bounds__(256) void tail_reduce_kernel(GemmArgs g, int epi, i
     const int64_t m = tile_m * BM + row, n = tile_n * (BN / 2) + oc;
     if (m >= g.M) return;
     const float gv[4] = {gs.x, gs.y, gs.z, gs.w}, uv[4] = {us.x, us.y, us.z, us.w};
+    if (epi == kEpiSwigluKeep) {  // the product [g | u] itself
+      *reinterpret_cast<uint2*>(g.gu + m * g.ldgu + n) =
+          make_uint2(pack2h(gv[0], gv[1]), pack2h(gv[2], gv[3]));
+      *reinterpret_cast<uint2*>(g.gu + m * g.ldgu + g.I + n) =
+          make_uint2(pack2h(uv[0], uv[1]), pack2h(uv[2], uv[3]));
+    }
     float mv[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -1136,7 +1185,10 @@ void launch_epi(const GemmArgs& g, dim3 grid, hipStream_t s, int epi, hipEvent_t
     case kEpiResid: launch_one<BSRC, NN, kEpiResid, BM, ST>(g, grid, s, start, stop); break;
     case kEpiPartial: launch_one<BSRC, NN, kEpiPartial, BM, ST>(g, grid, s, start, stop); break;
     default:
-      if constexpr (!NN) launch_one<BSRC, NN, kEpiSwiglu, BM, ST>(g, grid, s, start, stop);
+      if constexpr (!NN) {
+        if (epi == kEpiSwigluKeep) launch_one<BSRC, NN, kEpiSwigluKeep, BM, ST>(g, grid, s, start, stop);
+        else launch_one<BSRC, NN, kEpiSwiglu, BM, ST>(g, grid, s, start, stop);
+      }
       break;
   }
 }
@@ -1189,7 +1241,7 @@ int64_t tail_plan(int64_t m_tiles, int64_t n_tiles, int64_t ktiles, int tile, in
 }
 
 int64_t n_tiles_of(int64_t N, int epi, int tile) {
-  return epi == kEpiSwiglu ? N / (tile / 2) : qlora_cdiv(N, tile);
+  return swiglu_epi(epi) ? N / (tile / 2) : qlora_cdiv(N, tile);
 }
 
 // The tile shape, stage count and K split of qlora_gemm16 with tile 0 / splits 0: the cheapest
@@ -1215,7 +1267,7 @@ double plan_cost(int64_t M, int64_t N, int64_t K, int mode, int epi, const PlanC
   const int tile = v.tile, stages = v.stages;
   const int64_t kt = K / kBK64;
   if (kt % stages != 0 || (mode == 1 && N % tile != 0)) return -1.0;
-  if (epi == kEpiSwiglu && (splits > 1 || N % (tile / 2) != 0)) return -1.0;
+  if (swiglu_epi(epi) && (splits > 1 || N % (tile / 2) != 0)) return -1.0;
   const int64_t per = qlora_cdiv(qlora_cdiv(kt, splits), stages) * stages;
   if (per * (splits - 1) >= kt) return -1.0;  // an empty slice
   const int64_t m_tiles = qlora_cdiv(M, tile), tiles = m_tiles * n_tiles_of(N, epi, tile);
@@ -1307,7 +1359,7 @@ int run_gemm(GemmArgs& g, int bsrc, int mode, int epi, int splits, float* ws, in
     const dim3 tg((unsigned)(main_t + r * tail_s));
     launch_any(g, bsrc, mode, tile, stages, tg, s, epi, start, nullptr);
     if (int rc = qlora_launch_status()) return rc;
-    const int64_t threads = r * (epi == kEpiSwiglu ? tile * (tile / 8) : tile * (tile / 4));
+    const int64_t threads = r * (swiglu_epi(epi) ? tile * (tile / 8) : tile * (tile / 4));
     const dim3 rg((unsigned)qlora_cdiv(threads, 256));
     if (stop != nullptr)
       hipExtLaunchKernelGGL(tail_reduce_kernel, rg, dim3(256), 0, s, nullptr, stop, 0, g, epi,
@@ -1433,27 +1485,29 @@ QLORA_API int qlora_nf4_gemm(const void* a, int64_t lda, const void* packed, con
 QLORA_API int qlora_gemm16_timed(const void* a, int64_t lda, const void* b, int64_t ldb,
                                  int64_t M, int64_t N, int64_t K, int32_t mode, void* c,
                                  int64_t ldc, const void* bias, const float* resid, int64_t ldr,
-                                 int32_t epi, int64_t swiglu_I, int32_t tile, int32_t stages,
-                                 int32_t splits, float* ws, int64_t ws_elems, void* stream,
-                                 void* start, void* stop) {
+                                 int32_t epi, int64_t swiglu_I, void* gu, int64_t ldgu,
+                                 int32_t tile, int32_t stages, int32_t splits, float* ws,
+                                 int64_t ws_elems, void* stream, void* start, void* stop) {
   QLORA_CHECK_ARG(M >= 0 && N > 0 && K > 0);
   if (M == 0) return 0;
   QLORA_CHECK_ARG(a && b && c && (mode == 0 || mode == 1));
   QLORA_CHECK_ARG((tile == 0) == (splits == 0));
+  QLORA_CHECK_ARG(epi >= 0 && epi <= 5 && epi != kEpiPartial && !(swiglu_epi(epi) && mode != 0));
   if (tile == 0) auto_plan(M, N, K, mode, epi, &tile, &stages, &splits);
   QLORA_CHECK_ARG((tile == 256 && stages == 2) || (tile == 128 && (stages == 2 || stages == 4)));
-  QLORA_CHECK_ARG(epi >= 0 && epi <= 3 && !(epi == 3 && mode != 0));
-  QLORA_CHECK_ARG(splits >= 1 && splits <= 16 && !(splits > 1 && epi == 3));
+  QLORA_CHECK_ARG(splits >= 1 && splits <= 16 && !(splits > 1 && swiglu_epi(epi)));
   QLORA_CHECK_ARG(epi != 1 || bias);
   QLORA_CHECK_ARG(epi != 2 || (resid && ldr >= N));
+  // the kept product [g | u]: [M, 2 N] fp16, 16-byte rows
+  QLORA_CHECK_ARG(epi != kEpiSwigluKeep || (gu && ldgu >= 2 * N && ldgu % 8 == 0 && al(gu, 16)));
   QLORA_CHECK_ARG(K % (kStages * kBK) == 0 && (K / kBK64) % stages == 0);
-  if (epi == kEpiSwiglu) QLORA_CHECK_ARG(N % (tile / 2) == 0);  // N = I (output columns)
+  if (swiglu_epi(epi)) QLORA_CHECK_ARG(N % (tile / 2) == 0);  // N = I (output columns)
   else QLORA_CHECK_ARG(mode == 0 ? N % 8 == 0 : N % tile == 0);  // NT: a partial last tile
   QLORA_CHECK_ARG(lda >= K && lda % 8 == 0 && al(a, 16) && al(b, 16) && ldb % 8 == 0);
   QLORA_CHECK_ARG(mode == 0 ? ldb >= K : ldb >= N);
   QLORA_CHECK_ARG(ldc >= N);
   // the DMA addresses rows by 32-bit byte offsets: from B's start (NT), from a tile (A, NN B)
-  if (mode == 0) QLORA_CHECK_ARG((epi == kEpiSwiglu ? 2 * N : N) * ldb * 2 < (1ll << 32));
+  if (mode == 0) QLORA_CHECK_ARG((swiglu_epi(epi) ? 2 * N : N) * ldb * 2 < (1ll << 32));
   QLORA_CHECK_ARG((int64_t)tile * lda * 2 < (1ll << 32) && 64 * ldb * 2 < (1ll << 32));
   GemmArgs g{};
   g.a = static_cast<const uint16_t*>(a);
@@ -1469,6 +1523,8 @@ QLORA_API int qlora_gemm16_timed(const void* a, int64_t lda, const void* b, int6
   g.N = N;
   g.Kr = K;
   g.I = swiglu_I;
+  g.gu = static_cast<uint16_t*>(gu);
+  g.ldgu = ldgu;
   return run_gemm(g, kBHalf, mode, epi, splits, ws, ws_elems, (hipStream_t)stream,
                   static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop), tile, stages);
 }
@@ -1476,11 +1532,12 @@ QLORA_API int qlora_gemm16_timed(const void* a, int64_t lda, const void* b, int6
 QLORA_API int qlora_gemm16(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t M,
                            int64_t N, int64_t K, int32_t mode, void* c, int64_t ldc,
                            const void* bias, const float* resid, int64_t ldr, int32_t epi,
-                           int64_t swiglu_I, int32_t tile, int32_t stages, int32_t splits,
-                           float* ws, int64_t ws_elems, void* stream) {
+                           int64_t swiglu_I, void* gu, int64_t ldgu, int32_t tile,
+                           int32_t stages, int32_t splits, float* ws, int64_t ws_elems,
+                           void* stream) {
   return qlora_gemm16_timed(a, lda, b, ldb, M, N, K, mode, c, ldc, bias, resid, ldr, epi,
-                            swiglu_I, tile, stages, splits, ws, ws_elems, stream, nullptr,
-                            nullptr);
+                            swiglu_I, gu, ldgu, tile, stages, splits, ws, ws_elems, stream,
+                            nullptr, nullptr);
 }
 
 // fp32 workspace elements of a qlora_gemm16 problem: the split-K partials, or with one slice the
@@ -1488,7 +1545,8 @@ QLORA_API int qlora_gemm16(const void* a, int64_t lda, const void* b, int64_t ld
 QLORA_API int qlora_gemm16_workspace(int64_t M, int64_t N, int64_t K, int32_t mode, int32_t epi,
                                      int32_t tile, int32_t stages, int32_t splits,
                                      int64_t* elems) {
-  QLORA_CHECK_ARG(elems && M >= 0 && N > 0 && K > 0 && splits >= 0 && epi >= 0 && epi <= 3);
+  QLORA_CHECK_ARG(elems && M >= 0 && N > 0 && K > 0 && splits >= 0 && epi >= 0 && epi <= 5 &&
+                  epi != kEpiPartial);
   QLORA_CHECK_ARG((tile == 0) == (splits == 0) && (mode == 0 || mode == 1));
   *elems = 0;
   if (M == 0) return 0;
@@ -1509,7 +1567,7 @@ QLORA_API int qlora_gemm16_workspace(int64_t M, int64_t N, int64_t K, int32_t mo
 QLORA_API int qlora_gemm16_plan(int64_t M, int64_t N, int64_t K, int32_t mode, int32_t epi,
                                 int32_t* tile, int32_t* stages, int32_t* splits) {
   QLORA_CHECK_ARG(tile && stages && splits && M >= 0 && N > 0 && K > 0);
-  QLORA_CHECK_ARG((mode == 0 || mode == 1) && epi >= 0 && epi <= 3);
+  QLORA_CHECK_ARG((mode == 0 || mode == 1) && epi >= 0 && epi <= 5 && epi != kEpiPartial);
   int t, st, sp;
   auto_plan(M, N, K, mode, epi, &t, &st, &sp);
   *tile = t;
@@ -1524,8 +1582,10 @@ QLORA_API int qlora_hgemm_timed(const void* a, int64_t lda, const void* b, int64
                                 int64_t ldc, const void* bias, const float* resid, int64_t ldr,
                                 int32_t epi, int64_t swiglu_I, int32_t splits, float* ws,
                                 int64_t ws_elems, void* stream, void* start, void* stop) {
+  QLORA_CHECK_ARG(epi <= 3);
   return qlora_gemm16_timed(a, lda, b, ldb, M, N, K, mode, c, ldc, bias, resid, ldr, epi,
-                            swiglu_I, 256, 2, splits, ws, ws_elems, stream, start, stop);
+                            swiglu_I, nullptr, 0, 256, 2, splits, ws, ws_elems, stream, start,
+                            stop);
 }
 
 QLORA_API int qlora_hgemm(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t M,
@@ -1533,8 +1593,10 @@ QLORA_API int qlora_hgemm(const void* a, int64_t lda, const void* b, int64_t ldb
                           const void* bias, const float* resid, int64_t ldr, int32_t epi,
                           int64_t swiglu_I, int32_t splits, float* ws, int64_t ws_elems,
                           void* stream) {
+  QLORA_CHECK_ARG(epi <= 3);
   return qlora_gemm16_timed(a, lda, b, ldb, M, N, K, mode, c, ldc, bias, resid, ldr, epi,
-                            swiglu_I, 256, 2, splits, ws, ws_elems, stream, nullptr, nullptr);
+                            swiglu_I, nullptr, 0, 256, 2, splits, ws, ws_elems, stream, nullptr,
+                            nullptr);
 }
 
 QLORA_API int qlora_hgemm_workspace(int64_t M, int64_t N, int64_t K, int32_t epi, int32_t splits,

@@ -503,25 +503,33 @@ def attn_input_bwd(spec, dq, dk, dv, h, saved, packed, lora16t, seeds, dres=None
     return dh, dh16, grads
 
 
-def _layer_forward(spec, h, packed, lora16, seeds, keep):
-    """The layer's forward; with keep=True returns (None, everything the backward reads)."""
+def _layer_forward(spec, h, packed, lora16, seeds, keep, gu=None, keep_gu=False):
+    """The layer's forward. keep=True: returns (None, everything the backward reads), with the
+    [gate|up] product `gu` when the caller has it (a recomputing layer's backward: the forward
+    kept it) instead of multiplying again. keep=False: (h3, None), or (h3, [gate|up]) with
+    keep_gu (the product written beside the SwiGLU by the same GEMM, for the backward)."""
     n, H = h.shape
     D, HQ = spec.D, spec.HQ
     q, k, v, f = attn_input_fwd(spec, h, packed, lora16, seeds, keep_bits=keep)
     out, lse, aseed, aoffset = _attn_fwd(q, k, v, packed, spec.scale)
     o = L.nf4_linear(out.reshape(n, HQ * D), spec.w["o_proj"])
-    h2, b, _, _, rstd2 = _rms_fwd(spec, h, spec.ln2, packed, delta=o)
+    h2, b, _, _, rstd2 = _rms_fwd(spec, h, spec.ln2, packed, delta=o, write_y=gu is None)
     del o
     if keep:
-        gu = L.nf4_linear_gu(b, spec.gu)
+        if gu is None:
+            gu = L.nf4_linear_gu(b, spec.gu)
         f.update(q=q, k=k, v=v, out=out, lse=lse, aseed=aseed, aoffset=aoffset, h2=h2,
                  rstd2=rstd2, gu=gu)
         return None, f
-    # gate|up GEMM with the SwiGLU in its epilogue ([gate|up] never stored), then down_proj
-    # with the residual add in its epilogue: h3 = h2 + fp16(m W_d^T)
-    m = L.nf4_linear_swiglu(b, spec.gu, spec.I)
+    # gate|up GEMM with the SwiGLU in its epilogue ([gate|up] not stored unless kept for the
+    # backward), then down_proj with the residual add in its epilogue: h3 = h2 + fp16(m W_d^T)
+    both = L.nf4_linear_swiglu_keep(b, spec.gu, spec.I) if keep_gu else None
+    if both is not None:
+        m, gu = both
+    else:
+        m = L.nf4_linear_swiglu(b, spec.gu, spec.I)
     del b
-    return L.nf4_linear_resid(m, spec.w["down_proj"], h2), None
+    return L.nf4_linear_resid(m, spec.w["down_proj"], h2), gu
 
 
 class _Layer(torch.autograd.Function):
@@ -553,7 +561,11 @@ class _Layer(torch.autograd.Function):
             del m
             ctx.kept = f
         else:
-            h3, _ = _layer_forward(spec, h, packed, lora16, seeds, keep=False)
+            # a recomputing layer keeps its [gate|up] product for the backward (the reference's
+            # plan keeps it first, on the GPU or in host memory, engine.py:1204-1213, 430-445):
+            # the backward then recomputes the forward up to the MLP input only
+            h3, ctx.gu = _layer_forward(spec, h, packed, lora16, seeds, keep=False,
+                                        keep_gu=getattr(packed, "keep_gu", False))
             ctx.kept = None
         ctx.save_for_backward(h, aq_w, bq_w, av_w, bv_w)
         ctx.spec, ctx.packed, ctx.seeds = spec, packed, seeds
@@ -585,8 +597,10 @@ class _Layer(torch.autograd.Function):
         if ctx.kept is not None:
             f, ctx.kept = ctx.kept, None
         else:
+            gu_kept, ctx.gu = getattr(ctx, "gu", None), None
             with torch.no_grad():
-                _, f = _layer_forward(spec, h, packed, lora16, seeds, keep=True)
+                _, f = _layer_forward(spec, h, packed, lora16, seeds, keep=True, gu=gu_kept)
+            del gu_kept
         gu = f.pop("gu")
         _glu_bwd(dm, gu, spec.I)
         del dm
@@ -697,10 +711,12 @@ class FusedQwen2:
     """The step of a Qwen2 NF4 + LoRA model (engine.py:1568-1922 without the host offload).
 
     By default every layer recomputes its forward in the backward from its fp32 input
-    (`keep_all=False`, the per-layer recompute of the reference's step). `keep_all=True` keeps
-    every layer's intermediates instead; `keep_all=None` follows the reference's memory-cap plan
-    (keep_plan, engine.py:1626-1640): the last layers keep everything as long as the step's
-    predicted peak stays under the cap (the GPU's memory less a margin by default)."""
+    (`keep_all=False`, the per-layer recompute of the reference's step), up to the MLP input:
+    its [gate|up] product is kept from the forward (`keep_gu`), as the reference's step keeps
+    it. `keep_all=True` keeps every layer's intermediates instead; `keep_all=None` follows the
+    reference's memory-cap plan (keep_plan, engine.py:1626-1640): the last layers keep
+    everything as long as the step's predicted peak stays under the cap (the GPU's memory less
+    a margin by default)."""
 
     HEAD_CHUNK = 4096  # rows of logits alive at a time (4096 x 151936 fp16 = 1.2 GB)
     CAP_MARGIN = 8 * 2**30  # bytes of device memory the default cap leaves free
@@ -721,6 +737,11 @@ class FusedQwen2:
         # layers that keep their intermediates also keep their dequantized weights for the
         # backward (one dequant per layer and step instead of two; 94 MB per 1.5B layer)
         self.keep_weights = True
+        # recomputing layers keep their [gate|up] product (2 I fp16 per token: 2.6 GB over a
+        # 1.5B step of 2,560 tokens) and recompute their forward up to the MLP input only, the
+        # reference's plan (its [gate|up] is kept first, on the GPU or in pinned host memory,
+        # engine.py:1204-1213, 430-445); False: they multiply again
+        self.keep_gu = True
         self.dropout_p = cfg.lora_dropout
         self.rope = RopeTable(cfg.rope_theta, cfg.head_dim, self.device)
         self.dropout = TorchDropout(self.device, torch.float32) if self.dropout_p > 0 else None
@@ -853,6 +874,7 @@ class FusedQwen2:
         keep_from = len(self.layers) - self.keep_plan(packed.n)
         packed.keep_all_from = keep_from
         packed.keep_weights = self.keep_weights
+        packed.keep_gu = self.keep_gu
         for i, spec in enumerate(self.layers):
             h = _Layer.apply(h, spec, packed, i >= keep_from, *spec.lora_params())
         stats = HeadStats()

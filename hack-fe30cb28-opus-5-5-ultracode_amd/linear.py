@@ -98,7 +98,7 @@ def split_k(M, N, Kr, epi):
     """Slices of the reduction for the MFMA GEMMs: doubled while the tiles alone leave CUs idle
     and every slice keeps at least 8 k-tiles of 64 (the partial sums cost an fp32 round trip
     of M N per slice)."""
-    if epi == 3:
+    if epi in (3, 5):
         return 1
     tiles = -(-M // TILE) * (N // TILE)
     ktiles = Kr // 64
@@ -199,12 +199,13 @@ def gemm_plan(M, N, K, mode, epi=0):
 
 
 def hgemm(a, b, mode, epi=0, bias=None, resid=None, out=None, swiglu_I=0, splits=None,
-          tail=None, tile=256, stages=2):
+          tail=None, tile=256, stages=2, gu=None):
     """The MFMA GEMM with an fp16 B (qlora_gemm16): mode 0 C = A B^T (B [N, K]), mode 1 C = A B
     (B [K, N]); epilogues as nf4_gemm; tile: 256 or 128 (output tile edge), stages: 2, or 4 for
     128 x 128 tiles (one workgroup per CU, loads three k-tiles ahead). tail: with one slice, the
     tiles of a last, nearly empty round of the GPU run as K slices through a workspace (False:
-    whole; None: HGEMM_TAIL)."""
+    whole; None: HGEMM_TAIL). epi 5: SwiGLU as epi 3 and the product [g | u] itself written
+    to `gu` (fp16 [M, 2 I])."""
     dev = a.device
     a = _a16(a)
     _need(b, "b", torch.float16, dev, contiguous=False)
@@ -213,7 +214,7 @@ def hgemm(a, b, mode, epi=0, bias=None, resid=None, out=None, swiglu_I=0, splits
     M, K = a.shape
     if mode == 0:
         rows, kb = b.shape
-        n_out = swiglu_I if epi == 3 else rows
+        n_out = swiglu_I if epi in (3, 5) else rows
     else:
         kb, n_out = b.shape
     if kb != K:
@@ -222,6 +223,10 @@ def hgemm(a, b, mode, epi=0, bias=None, resid=None, out=None, swiglu_I=0, splits
         _need(bias, "bias", torch.float16, dev)
         if bias.numel() != n_out:
             raise ValueError("bias must have one entry per output column")
+    if epi == 5:
+        _need(gu, "gu", torch.float16, dev, contiguous=False)
+        if gu.shape != (M, 2 * n_out) or gu.stride(1) != 1:
+            raise ValueError("gu must be [M, 2 I] with unit column stride")
     out, ldr = _gemm_out(a, M, n_out, epi, resid, out, dev)
     if M == 0:
         return out
@@ -234,8 +239,9 @@ def hgemm(a, b, mode, epi=0, bias=None, resid=None, out=None, swiglu_I=0, splits
         if splits != 1 or tail or tile == 0 else 0
     ws = torch.empty((n_ws,), device=dev, dtype=torch.float32) if n_ws else None
     _lib.call("qlora_gemm16", _ptr(a), a.stride(0), _ptr(b), b.stride(0), M, n_out, K, mode,
-              _ptr(out), out.stride(0), _ptr(bias), _ptr(resid), ldr, epi, swiglu_I, tile,
-              stages, splits, _ptr(ws), 0 if ws is None else ws.numel(), _stream(dev))
+              _ptr(out), out.stride(0), _ptr(bias), _ptr(resid), ldr, epi, swiglu_I, _ptr(gu),
+              0 if gu is None else gu.stride(0), tile, stages, splits, _ptr(ws),
+              0 if ws is None else ws.numel(), _stream(dev))
     return out
 
 
@@ -338,6 +344,19 @@ def nf4_linear_swiglu(x, w, I):
         return hgemm(x, dequantize(w), 0, epi=3, swiglu_I=I)
     from .ops import _glu_fwd
     return _glu_fwd(nf4_linear(x, w), I)
+
+
+def nf4_linear_swiglu_keep(x, w, I):
+    """(m, [g | u]): the SwiGLU of the stacked gate|up product and the product itself, fp16
+    [M, I] and [M, 2 I], from one GEMM (a recomputing layer keeps [g | u] for its backward, as
+    the reference's step keeps it rather than multiplying again, engine.py:1204-1213); None
+    when the package's GEMM does not take the shape."""
+    if GEMM != "package" or BACKEND == "fused" or not _gemm_fits(I, x.shape[1]):
+        return None
+    M = x.shape[0]
+    gu = torch.empty((M, 2 * I), device=x.device, dtype=torch.float16)
+    m = hgemm(x, dequantize(w), 0, epi=5, swiglu_I=I, tile=0, gu=gu)
+    return m, gu
 
 
 def nf4_linear_gu(x, w):

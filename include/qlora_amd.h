@@ -331,21 +331,28 @@ int qlora_hgemm_timed(const void* a, int64_t lda, const void* b, int64_t ldb, in
  * stages: 2 (either tile; two 128 x 128 workgroups then share a CU) or 4 (128 x 128 tiles
  * only: 128 KB of LDS, one workgroup per CU, each k-tile's loads issued three k-tiles ahead).
  * tile 0 with splits 0 (and any stages): the plan of qlora_gemm16_plan.
+ * epi 5 (NT, one slice): the SwiGLU of epi 3 and the product [g | u] itself, fp16 [M, 2 N]
+ * into gu (ldgu, 16-byte rows; gate column n and up column N + n), the same values a plain
+ * store of the product gives: a recomputing layer keeps it for its backward (the reference's
+ * step keeps [gate | up] rather than multiplying again: engine.py:1204-1213, 430-445).
+ * gu is read for epi 5 only (else null).
  * Replaces the same cuBLAS products as qlora_hgemm (engine.py:1082, 1112, 1163, 1179, 1239,
  * 1293, 1301, 1316, 1376-1381). Requires qlora_hgemm's conditions with mode 1: N % tile == 0;
  * epi 3: N % (tile / 2) == 0; K % (64 stages) == 0.
  */
 int qlora_gemm16(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t M, int64_t N,
                  int64_t K, int32_t mode, void* c, int64_t ldc, const void* bias,
-                 const float* resid, int64_t ldr, int32_t epi, int64_t swiglu_I, int32_t tile,
-                 int32_t stages, int32_t splits, float* ws, int64_t ws_elems, void* stream);
+                 const float* resid, int64_t ldr, int32_t epi, int64_t swiglu_I, void* gu,
+                 int64_t ldgu, int32_t tile, int32_t stages, int32_t splits, float* ws,
+                 int64_t ws_elems, void* stream);
 
 /* qlora_gemm16 with the start/stop events of qlora_hgemm_timed (no reference counterpart). */
 int qlora_gemm16_timed(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t M,
                        int64_t N, int64_t K, int32_t mode, void* c, int64_t ldc,
                        const void* bias, const float* resid, int64_t ldr, int32_t epi,
-                       int64_t swiglu_I, int32_t tile, int32_t stages, int32_t splits,
-                       float* ws, int64_t ws_elems, void* stream, void* start, void* stop);
+                       int64_t swiglu_I, void* gu, int64_t ldgu, int32_t tile, int32_t stages,
+                       int32_t splits, float* ws, int64_t ws_elems, void* stream, void* start,
+                       void* stop);
 
 /*
  * fp32 workspace elements (*elems) qlora_gemm16 uses for this problem, mode, tile and stage count

@@ -417,3 +417,32 @@ def test_auto_plan_against_fp64(pkg, M):
         print(f"M={M} mode={mode} N={N} K={K} epi={epi} plan={L.gemm_plan(M, N, K, mode, epi)}"
               f" rel {err:.2e}", flush=True)
         assert err < 1e-3
+
+
+@pytest.mark.parametrize("M,tile,stages,tail", [(2560, 256, 2, False), (2600, 256, 2, True),
+                                                (1875, 128, 2, True), (1875, 128, 2, False),
+                                                (700, 128, 4, False), (1, 0, 0, True)])
+def test_swiglu_keep_epilogue(pkg, M, tile, stages, tail):
+    """Epilogue 5: the SwiGLU output equals epilogue 3's bit for bit and the kept product
+    [g | u] equals the plain GEMM's store of it bit for bit (each output sums the same k-steps
+    in the same order), for both tile shapes, with the K-sliced last round (2,600 rows: 770
+    tiles, the last two sliced) and through the automatic plan (tile 0)."""
+    L = pkg.linear
+    I, K = 8960, 1536
+    g = torch.Generator(device=DEV).manual_seed(M + tile)
+    w = (torch.randn(2 * I, K, generator=g, device=DEV) * 0.02).half()
+    a = torch.randn(M, K, generator=g, device=DEV).half()
+    kw = dict(tile=tile, stages=stages) if tile else dict(tile=0)
+    if tile:
+        kw.update(splits=1, tail=tail)
+    gu = torch.full((M, 2 * I), float("nan"), device=DEV, dtype=torch.float16)
+    m5 = L.hgemm(a, w, 0, epi=5, swiglu_I=I, gu=gu, **kw)
+    m3 = L.hgemm(a, w, 0, epi=3, swiglu_I=I, **kw)
+    plain = L.hgemm(a, w, 0, tile=tile or 0, **({"splits": 1, "tail": False, "stages": stages}
+                                                 if tile else {}))
+    assert torch.equal(m5, m3)
+    if tile and not tail:  # whole tiles: the same bits as the plain product's
+        assert torch.equal(gu, plain)
+    ref = (a.double() @ w.double().t())
+    assert rel_err(gu, ref) < 1e-3
+    assert not torch.isnan(gu).any()

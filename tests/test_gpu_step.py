@@ -99,6 +99,27 @@ def test_step_other_model_shapes(pkg, H, HQ, HKV, D, r):
         assert rel < 2e-2, rel.item()
 
 
+def test_kept_gate_up_equals_multiplying_again(pkg):
+    """A recomputing layer keeps its [gate|up] product from the forward (keep_gu) instead of
+    multiplying again in its backward: the same loss and LoRA gradients bit for bit (the kept
+    product is the same bits as the recompute's)."""
+    out = []
+    for keep_gu in (True, False):
+        model = _tiny(pkg, H=512, HQ=8, HKV=2, D=64)
+        model.keep_all, model.keep_gu = False, keep_gu
+        lengths = [17, 60, 33, 5]
+        ids, mask, labels = _batch(lengths, model.cfg.vocab_size)
+        denom = float((labels[:, 1:] != -100).sum())
+        torch.cuda.manual_seed(7)
+        loss, _, _ = model.step(ids.to(DEV), mask.to(DEV), labels.to(DEV), denom)
+        loss.backward()
+        torch.cuda.synchronize()
+        out.append((loss.item(), [p.grad.clone() for p in model.parameters()]))
+    assert out[0][0] == out[1][0]
+    for a, b in zip(out[0][1], out[1][1]):
+        assert torch.equal(a, b)
+
+
 @pytest.mark.parametrize("lengths,keep_all", [([17, 60, 33, 5], False), ([4], False),
                                               ([40, 40], True), ([17, 60, 33, 5], None),
                                               ([17, 60, 33, 5], "mixed"),
