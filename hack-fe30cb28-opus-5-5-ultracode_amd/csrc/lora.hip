@@ -524,7 +524,7 @@ QLORA_API int qlora_lora_fwd_rows(const void* a_q, const void* a_v, const void* 
                                   int32_t N_v, int32_t H, int32_t r, void* stream) {
   QLORA_CHECK_ARG(n >= 0 && N_q > 0 && N_v > 0 && H > 0);
   if (n == 0) return 0;
-  QLORA_CHECK_ARG(rank_ok(r) && l_q && l_v);
+  QLORA_CHECK_ARG(rank_ok(r) && (l_q == nullptr) == (l_v == nullptr));
   Args a{};
   a.job[0] = Job{static_cast<const uint16_t*>(a_q), static_cast<const uint16_t*>(A_q),
                  static_cast<uint16_t*>(x_q), static_cast<const uint16_t*>(B_q),

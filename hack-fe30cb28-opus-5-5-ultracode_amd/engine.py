@@ -450,11 +450,13 @@ class Packed:
 # ---------------------------------------------------------------------------------------------
 # One decoder layer (engine.py:1054-1340)
 # ---------------------------------------------------------------------------------------------
-def attn_input_fwd(spec, h, packed, lora16, seeds, keep_bits=False):
+def attn_input_fwd(spec, h, packed, lora16, seeds, keep_bits=False, qkv=None):
     """The attention-input block (engine.py:1073-1109): input RMSNorm with the two LoRA-dropout
     copies, the qkv projection (+ bias), the q/v LoRA products and RoPE. Returns q [n, HQ, D],
     k and v in grouped layout [n, HKV, D], and what attn_input_bwd reads. keep_bits: store the
-    dropout masks as bits for the backward (else it draws them again)."""
+    dropout masks as bits for the backward (else it draws them again). qkv: (q, k, v) kept from
+    the forward (a backward's recompute): then only the norm and the LoRA inputs' products
+    the gradients read are formed again (no projection, no RoPE)."""
     n, H = h.shape
     aq_w, bq_w, av_w, bv_w = lora16
     s = _lora_scale(spec)
@@ -465,13 +467,18 @@ def attn_input_fwd(spec, h, packed, lora16, seeds, keep_bits=False):
     kbits = (torch.empty(keep_bits_shape(n, H), device=h.device, dtype=torch.uint8)
              if keep_bits and (drop_q or drop_v) else None)
     _, a, aq, av, rstd1 = _rms_fwd(spec, h, spec.ln1, packed, seeds=seeds, drop_q=drop_q,
-                                   drop_v=drop_v, keep=kbits)
+                                   drop_v=drop_v, keep=kbits, write_y=qkv is None or not drop)
     if not drop:
         aq, av = (a if aq_w is not None else None), (a if av_w is not None else None)
-    qkv = L.nf4_linear(a, spec.qkv, bias=spec.bias_qkv)
+    if qkv is not None:
+        del a
+        xq, xv, _, _ = _lora_fwd_rows(aq, av, aq_w, bq_w, av_w, bv_w, need_l=False)
+        q, k, v = qkv
+        return q, k, v, dict(rstd1=rstd1, aq=aq, av=av, xq=xq, xv=xv, keep=kbits)
+    proj = L.nf4_linear(a, spec.qkv, bias=spec.bias_qkv)
     del a
     xq, xv, lq, lv = _lora_fwd_rows(aq, av, aq_w, bq_w, av_w, bv_w)
-    q, k, v = _rope_fwd(spec, qkv, lq, lv, packed, s, kv_heads=spec.HKV)
+    q, k, v = _rope_fwd(spec, proj, lq, lv, packed, s, kv_heads=spec.HKV)
     return q, k, v, dict(rstd1=rstd1, aq=aq, av=av, xq=xq, xv=xv, keep=kbits)
 
 
@@ -503,17 +510,34 @@ def attn_input_bwd(spec, dq, dk, dv, h, saved, packed, lora16t, seeds, dres=None
     return dh, dh16, grads
 
 
-def _layer_forward(spec, h, packed, lora16, seeds, keep, gu=None, keep_gu=False):
-    """The layer's forward. keep=True: returns (None, everything the backward reads), with the
-    [gate|up] product `gu` when the caller has it (a recomputing layer's backward: the forward
-    kept it) instead of multiplying again. keep=False: (h3, None), or (h3, [gate|up]) with
-    keep_gu (the product written beside the SwiGLU by the same GEMM, for the backward)."""
+ATTN_KEPT = ("q", "k", "v", "out", "lse", "aseed", "aoffset", "o")
+
+
+def _layer_forward(spec, h, packed, lora16, seeds, keep, kept=None, save=()):
+    """The layer's forward.
+    keep=True: returns (None, everything the backward reads). `kept`: what the forward kept
+    (a recomputing layer's backward), used instead of computing it again: the [gate|up] product
+    ("gu") and the attention's q, k, v, output, log-sum-exp and o_proj output (ATTN_KEPT); with
+    both, only the two RMSNorms and the LoRA inputs' products are formed again.
+    keep=False: (h3, kept) with the tensors `save` names ("gu": the product, written beside the
+    SwiGLU by the same GEMM; "attn": ATTN_KEPT) for the backward."""
     n, H = h.shape
     D, HQ = spec.D, spec.HQ
-    q, k, v, f = attn_input_fwd(spec, h, packed, lora16, seeds, keep_bits=keep)
-    out, lse, aseed, aoffset = _attn_fwd(q, k, v, packed, spec.scale)
-    o = L.nf4_linear(out.reshape(n, HQ * D), spec.w["o_proj"])
-    h2, b, _, _, rstd2 = _rms_fwd(spec, h, spec.ln2, packed, delta=o, write_y=gu is None)
+    kept = kept or {}
+    has_attn = "o" in kept
+    q, k, v, f = attn_input_fwd(spec, h, packed, lora16, seeds, keep_bits=keep,
+                                qkv=(kept["q"], kept["k"], kept["v"]) if has_attn else None)
+    if has_attn:
+        out, lse, aseed, aoffset, o = (kept[x] for x in ATTN_KEPT[3:])
+    else:
+        out, lse, aseed, aoffset = _attn_fwd(q, k, v, packed, spec.scale)
+        o = L.nf4_linear(out.reshape(n, HQ * D), spec.w["o_proj"])
+    gu = kept.get("gu")
+    h2, b, _, _, rstd2 = _rms_fwd(spec, h, spec.ln2, packed, delta=o,
+                                  write_y=not (keep and gu is not None))
+    saved = {}
+    if not keep and "attn" in save:
+        saved.update(q=q, k=k, v=v, out=out, lse=lse, aseed=aseed, aoffset=aoffset, o=o)
     del o
     if keep:
         if gu is None:
@@ -523,13 +547,13 @@ def _layer_forward(spec, h, packed, lora16, seeds, keep, gu=None, keep_gu=False)
         return None, f
     # gate|up GEMM with the SwiGLU in its epilogue ([gate|up] not stored unless kept for the
     # backward), then down_proj with the residual add in its epilogue: h3 = h2 + fp16(m W_d^T)
-    both = L.nf4_linear_swiglu_keep(b, spec.gu, spec.I) if keep_gu else None
+    both = L.nf4_linear_swiglu_keep(b, spec.gu, spec.I) if "gu" in save else None
     if both is not None:
-        m, gu = both
+        m, saved["gu"] = both
     else:
         m = L.nf4_linear_swiglu(b, spec.gu, spec.I)
     del b
-    return L.nf4_linear_resid(m, spec.w["down_proj"], h2), gu
+    return L.nf4_linear_resid(m, spec.w["down_proj"], h2), saved
 
 
 class _Layer(torch.autograd.Function):
@@ -564,8 +588,10 @@ class _Layer(torch.autograd.Function):
             # a recomputing layer keeps its [gate|up] product for the backward (the reference's
             # plan keeps it first, on the GPU or in host memory, engine.py:1204-1213, 430-445):
             # the backward then recomputes the forward up to the MLP input only
-            h3, ctx.gu = _layer_forward(spec, h, packed, lora16, seeds, keep=False,
-                                        keep_gu=getattr(packed, "keep_gu", False))
+            save = (("gu",) if getattr(packed, "keep_gu", False) else ()) + \
+                (("attn",) if getattr(packed, "keep_attn", False) else ())
+            h3, ctx.saved_fwd = _layer_forward(spec, h, packed, lora16, seeds, keep=False,
+                                               save=save)
             ctx.kept = None
         ctx.save_for_backward(h, aq_w, bq_w, av_w, bv_w)
         ctx.spec, ctx.packed, ctx.seeds = spec, packed, seeds
@@ -597,10 +623,10 @@ class _Layer(torch.autograd.Function):
         if ctx.kept is not None:
             f, ctx.kept = ctx.kept, None
         else:
-            gu_kept, ctx.gu = getattr(ctx, "gu", None), None
+            saved, ctx.saved_fwd = getattr(ctx, "saved_fwd", None), None
             with torch.no_grad():
-                _, f = _layer_forward(spec, h, packed, lora16, seeds, keep=True, gu=gu_kept)
-            del gu_kept
+                _, f = _layer_forward(spec, h, packed, lora16, seeds, keep=True, kept=saved)
+            del saved
         gu = f.pop("gu")
         _glu_bwd(dm, gu, spec.I)
         del dm
@@ -711,9 +737,11 @@ class FusedQwen2:
     """The step of a Qwen2 NF4 + LoRA model (engine.py:1568-1922 without the host offload).
 
     By default every layer recomputes its forward in the backward from its fp32 input
-    (`keep_all=False`, the per-layer recompute of the reference's step), up to the MLP input:
-    its [gate|up] product is kept from the forward (`keep_gu`), as the reference's step keeps
-    it. `keep_all=True` keeps every layer's intermediates instead; `keep_all=None` follows the
+    (`keep_all=False`, the per-layer recompute of the reference's step) as far as the reference's
+    step does: its [gate|up] product (`keep_gu`) and its attention's q, k, v, output and o_proj
+    output (`keep_attn`) are kept from the forward, as the reference keeps them (GuStream,
+    AttnStream: in host memory on its GPU, in HBM here), and the backward forms the two
+    RMSNorms and the LoRA inputs' products again. `keep_all=True` keeps every layer's intermediates instead; `keep_all=None` follows the
     reference's memory-cap plan (keep_plan, engine.py:1626-1640): the last layers keep
     everything as long as the step's predicted peak stays under the cap (the GPU's memory less
     a margin by default)."""
@@ -742,6 +770,11 @@ class FusedQwen2:
         # reference's plan (its [gate|up] is kept first, on the GPU or in pinned host memory,
         # engine.py:1204-1213, 430-445); False: they multiply again
         self.keep_gu = True
+        # ... and the attention's q, k, v, output, log-sum-exp and o_proj output (about 10 KB a
+        # token), so their backward recomputes only the two RMSNorms and the LoRA inputs'
+        # products: the reference's AttnStream (engine.py:560-571), on by default there
+        # (OFFLOAD_ATTN, patch.py:45-51) where host copies are fast enough; False: recompute
+        self.keep_attn = True
         self.dropout_p = cfg.lora_dropout
         self.rope = RopeTable(cfg.rope_theta, cfg.head_dim, self.device)
         self.dropout = TorchDropout(self.device, torch.float32) if self.dropout_p > 0 else None
@@ -875,6 +908,7 @@ class FusedQwen2:
         packed.keep_all_from = keep_from
         packed.keep_weights = self.keep_weights
         packed.keep_gu = self.keep_gu
+        packed.keep_attn = self.keep_attn
         for i, spec in enumerate(self.layers):
             h = _Layer.apply(h, spec, packed, i >= keep_from, *spec.lora_params())
         stats = HeadStats()

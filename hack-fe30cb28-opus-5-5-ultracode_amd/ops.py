@@ -655,9 +655,10 @@ def _resid_add(a, d, out=None):
 # ---------------------------------------------------------------------------------------------
 # LoRA per-token products (engine.py:1088-1093, 1319-1331)
 # ---------------------------------------------------------------------------------------------
-def _lora_fwd_rows(a_q, a_v, A_q, B_q, A_v, B_v):
+def _lora_fwd_rows(a_q, a_v, A_q, B_q, A_v, B_v, need_l=True):
     """(x_q, x_v, l_q, l_v): x = fp16(a A^T) [n, r], l = fp16(x B^T) [n, N] for the q and v
-    adapters (engine.py:1088-1093); a [n, H], A [r, H], B [N, r] fp16."""
+    adapters (engine.py:1088-1093); a [n, H], A [r, H], B [N, r] fp16. need_l False: x only
+    (l_q, l_v None)."""
     _need(a_q, "a_q", torch.float16)
     n, H = a_q.shape
     dev = a_q.device
@@ -671,8 +672,8 @@ def _lora_fwd_rows(a_q, a_v, A_q, B_q, A_v, B_v):
     Nq, Nv = B_q.shape[0], B_v.shape[0]
     x_q = torch.empty((n, r), device=dev, dtype=torch.float16)
     x_v = torch.empty((n, r), device=dev, dtype=torch.float16)
-    l_q = torch.empty((n, Nq), device=dev, dtype=torch.float16)
-    l_v = torch.empty((n, Nv), device=dev, dtype=torch.float16)
+    l_q = torch.empty((n, Nq), device=dev, dtype=torch.float16) if need_l else None
+    l_v = torch.empty((n, Nv), device=dev, dtype=torch.float16) if need_l else None
     if n:
         _lib.call("qlora_lora_fwd_rows", _ptr(a_q), _ptr(a_v), _ptr(A_q), _ptr(A_v), _ptr(B_q),
                   _ptr(B_v), _ptr(x_q), _ptr(x_v), _ptr(l_q), _ptr(l_v), n, Nq, Nv, H, r,

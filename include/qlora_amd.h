@@ -448,6 +448,8 @@ int qlora_gemmlt_solutions(int32_t op, int64_t M, int64_t N, int64_t K, int64_t 
  *   x_a = f16(a_a A_a^T)   f16 [n, r] (kept for the backward)
  *   l_a = f16(x_a B_a^T)   f16 [n, N_a] (added to the projection output by qlora_rope_fwd)
  * a_a f16 [n, H] (the dropped LoRA inputs of qlora_rms_fwd); A_a f16 [r, H]; B_a f16 [N_a, r].
+ * l_q and l_v both null: x only (a backward that recomputes the LoRA inputs for its gradients,
+ * its q and v kept from the forward).
  * Requires r in {8, 16, 32, 64}, H % 16 == 0, N_a % 32 == 0; a_a, A_a, B_a, l_a 16-byte
  * aligned.
  * No reference counterpart as one launch: the reference makes four fp16 products.

@@ -99,14 +99,15 @@ def test_step_other_model_shapes(pkg, H, HQ, HKV, D, r):
         assert rel < 2e-2, rel.item()
 
 
-def test_kept_gate_up_equals_multiplying_again(pkg):
-    """A recomputing layer keeps its [gate|up] product from the forward (keep_gu) instead of
-    multiplying again in its backward: the same loss and LoRA gradients bit for bit (the kept
-    product is the same bits as the recompute's)."""
+def test_kept_tensors_equal_recomputing_them(pkg):
+    """A recomputing layer keeps its [gate|up] product (keep_gu) and its attention tensors
+    (keep_attn: q, k, v, output, log-sum-exp, o_proj output) from the forward instead of
+    forming them again in its backward: the same loss and LoRA gradients bit for bit in all
+    four combinations (what is kept is the same bits as what the recompute forms)."""
     out = []
-    for keep_gu in (True, False):
+    for keep_gu, keep_attn in ((True, True), (False, False), (True, False), (False, True)):
         model = _tiny(pkg, H=512, HQ=8, HKV=2, D=64)
-        model.keep_all, model.keep_gu = False, keep_gu
+        model.keep_all, model.keep_gu, model.keep_attn = False, keep_gu, keep_attn
         lengths = [17, 60, 33, 5]
         ids, mask, labels = _batch(lengths, model.cfg.vocab_size)
         denom = float((labels[:, 1:] != -100).sum())
@@ -115,9 +116,10 @@ def test_kept_gate_up_equals_multiplying_again(pkg):
         loss.backward()
         torch.cuda.synchronize()
         out.append((loss.item(), [p.grad.clone() for p in model.parameters()]))
-    assert out[0][0] == out[1][0]
-    for a, b in zip(out[0][1], out[1][1]):
-        assert torch.equal(a, b)
+    for other in out[1:]:
+        assert out[0][0] == other[0]
+        for a, b in zip(out[0][1], other[1]):
+            assert torch.equal(a, b)
 
 
 @pytest.mark.parametrize("lengths,keep_all", [([17, 60, 33, 5], False), ([4], False),
