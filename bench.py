@@ -1,14 +1,19 @@
 """Benchmark: full Qwen2.5-1.5B NF4 + LoRA training steps on one MI355X.
 
-A step = forward + backward with per-layer recompute (each decoder layer keeps only its input
-and recomputes its forward in backward, as config 5 states) + fp16 loss scaling (GradScaler) +
-fused AdamW on the LoRA parameters, over one synthetic batch of 4 packed sequences with lengths
-~ U[256, 1024] and random token ids (first 25 % of each sequence unsupervised). Random-init
-weights of the Qwen2.5-1.5B architecture, all linears NF4 double-quant (blocksize 64), tied
-fp16 embedding. `value` = tokens/s over the K timed steps, inputs resident in HBM.
+A step = forward + backward with per-layer recompute as the reference's step does it (each
+decoder layer keeps its input, its [gate|up] product and its attention's q, k, v, output and
+o_proj output - the reference's GuStream and AttnStream, in host memory on its GPU, in HBM here -
+and recomputes its two RMSNorms with the LoRA inputs' dropout and products in backward) + fp16
+loss scaling (GradScaler) + fused AdamW on the LoRA parameters, over one synthetic batch of 4
+packed sequences with lengths ~ U[256, 1024] and random token ids (first 25 % of each sequence
+unsupervised). Random-init weights of the Qwen2.5-1.5B architecture, all linears NF4
+double-quant (blocksize 64), tied fp16 embedding. `value` = tokens/s over the K timed steps,
+inputs resident in HBM.
 
 Beside it, on the same JSON line:
   loss_curve     the loss of steps 1..64 from the random init (warmup and timed steps included)
+  full_recompute the same step with every layer recomputing its whole forward from its input
+                 in backward (nothing but the input kept)
   keep_all       the same step with every layer keeping its intermediates (no recompute)
   roofline       the step's largest hand-written kernel by time, the package's MFMA GEMM
                  (hgemm_kernel: the gate|up forward with the SwiGLU epilogue), 2 M N K flops
@@ -207,7 +212,6 @@ def measure_step_kernels(pkg, trainer, batches, cfg):
             work_f += 4.0 * D * heads * pairs * (len(fwd.records) - n_f)
             work_b += 10.0 * D * heads * pairs * (len(bwd.records) - n_b)
     torch.cuda.synchronize()
-    gate_up = 2 * cfg.intermediate_size
     out = [dict(fwd.summary(work_total=work_f), kernel="attn_fwd_kernel"),
            dict(bwd.summary(work_total=work_b),
                 kernel="attn_delta + attn_dq + attn_dkdv kernels")]
@@ -222,18 +226,17 @@ def measure_step_kernels(pkg, trainer, batches, cfg):
          lambda a: a[5] <= 2048 and a[6] <= 2048),
         ("long reductions (down forward, gate|up dX, the head's G E; 256 x 256 split-K)",
          lambda a: a[5] <= 2048 and a[6] > 2048),
-        ("gate|up recompute forward ([g|u] kept for the backward, N = 2 I)",
-         lambda a: a[7] == 0 and a[5] == gate_up and a[13] == 0),
         ("down dX (N = I)", lambda a: a[7] == 1 and a[5] == cfg.intermediate_size),
         ("lm_head logits (N = V)", lambda a: a[7] == 0 and a[5] == cfg.vocab_size))
     for name, sel in classes:
         r = own.summary(select=sel)
         if r is not None:  # (HBM traffic was measured on the SwiGLU launches only)
             out.append(dict(r, kernel=name, traffic=None))
-    mine = own.summary(select=lambda a: a[13] == 3)
+    mine = own.summary(select=lambda a: a[13] in P.SWIGLU_EPIS)
     if mine is not None:
         mine = dict(mine, kernel="hgemm_kernel (qlora_gemm16): the gate|up forward with the "
-                                 "SwiGLU epilogue, this package's MFMA GEMM")
+                                 "SwiGLU epilogue (and the [g|u] product kept for the backward), "
+                                 "this package's MFMA GEMM")
     return mine, dq.summary(), out
 
 
@@ -609,6 +612,17 @@ def main():
         _, _, rest = time_steps(trainer, batches, done, max(0, CURVE_STEPS - done))
     curve = (warm_losses + timed_losses + rest)[:CURVE_STEPS]
     kernels = measure_step_kernels(pkg, trainer, batches[-4:], cfg)
+    full = None
+    if args.keep_steps > 0 and args.policy != "keep":
+        model.keep_gu = model.keep_attn = False
+        time_steps(trainer, batches, 0, 2)
+        ftok, fel, _ = time_steps(trainer, batches, args.warmup, args.keep_steps)
+        full = {"value": ftok / fel, "ms_per_step": 1000.0 * fel / args.keep_steps,
+                "steps": args.keep_steps,
+                "what": "every layer recomputes its whole forward from its input in backward "
+                        "(the [gate|up] product and the attention tensors formed again)"}
+        model.keep_gu = model.keep_attn = True
+        log(f"full recompute: {full['value']:.0f} tokens/s")
     keep = None
     if args.keep_steps > 0 and args.policy != "keep":
         model.keep_all = True
@@ -634,8 +648,12 @@ def main():
         "config": {"workload": "config 5: full Qwen2.5-1.5B NF4+LoRA training step",
                    "batch": "4 packed sequences, lengths U[256,1024]",
                    "tokens": tokens, "layers": args.layers, "parallelism": "single GPU",
-                   "activations": ("per-layer recompute: each layer keeps its input and "
-                                   "recomputes its forward (NF4 dequant included) in backward"
+                   "activations": ("per-layer recompute as the reference's step does it: each "
+                                   "layer keeps its input, its [gate|up] product and its "
+                                   "attention's q, k, v, output and o_proj output (the "
+                                   "reference's GuStream/AttnStream, in HBM here) and "
+                                   "recomputes the two RMSNorms and the LoRA inputs' products "
+                                   "in backward"
                                    if args.policy == "recompute" else
                                    "every layer keeps its intermediates (no recompute)"),
                    "gemm_backend": pkg.linear.BACKEND, "gemm": pkg.linear.GEMM},
@@ -643,6 +661,7 @@ def main():
         "roofline_dequant": kernels[1],
         "roofline_mfma": kernels[2],
         "loss_curve": curve,
+        "full_recompute": full,
         "keep_all": keep,
         "graph": graph,
         "gemm_tuning_s": tune_s,

@@ -66,19 +66,22 @@ TIMED = {"qlora_nf4_dequant_many": "qlora_nf4_dequant_many_timed",
          "qlora_hgemm": "qlora_hgemm_timed", "qlora_gemm16": "qlora_gemm16_timed"}
 
 
+SWIGLU_EPIS = (3, 5)  # the SwiGLU epilogues (5: the product [g | u] written beside it)
+
+
 def hgemm_flops(args):
     """2 M N K of one qlora_hgemm / qlora_gemm16 launch (a, lda, b, ldb, M, N, K, mode, ..., epi
-    at 13): N is the output's columns, I with the SwiGLU epilogue, whose product is
-    [M, 2 I]."""
-    return 2.0 * args[4] * args[5] * args[6] * (2 if args[13] == 3 else 1)
+    at 13): N is the output's columns, I with a SwiGLU epilogue, whose product is [M, 2 I]."""
+    return 2.0 * args[4] * args[5] * args[6] * (2 if args[13] in SWIGLU_EPIS else 1)
 
 
 def hgemm_bytes(args):
     """Algorithmic HBM bytes of one qlora_hgemm / qlora_gemm16 launch: A [M, K], the weight
-    ([N, K], [2 I, K] with the SwiGLU epilogue, [K, N] in NN) and the fp16 output [M, N] once
-    each."""
+    ([N, K], [2 I, K] with a SwiGLU epilogue, [K, N] in NN) and the fp16 output [M, N] once
+    each, and with epilogue 5 the product [g | u] [M, 2 I] written beside it."""
     M, N, K, epi = args[4], args[5], args[6], args[13]
-    return 2.0 * (M * K + (2 * N if epi == 3 else N) * K + M * N)
+    b = 2.0 * (M * K + (2 * N if epi in SWIGLU_EPIS else N) * K + M * N)
+    return b + (2.0 * M * 2 * N if epi == 5 else 0.0)
 
 WORK = {
     "qlora_nf4_dequant": ("hbm", _dequant_bytes),
