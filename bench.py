@@ -21,7 +21,7 @@ Beside it, on the same JSON line:
                  launches of four extra untimed steps (four batches' token counts)
   roofline_dequant  the step's NF4 dequant launches (the north star's dequant GB/s)
   roofline_mfma  the attention kernels against the fp16 MFMA peak (algorithmic flops of the
-                 batch's causal pairs) and the step's library GEMMs
+                 batch's causal pairs) and the package GEMM's launches by product class
   config1..4     BASELINE configs 1-4 on the GPU (dequant GB/s; MLP, attention-input block and
                  LM-head TFLOP/s on their algorithmic work), each with its CPU oracle time
   cpu_baseline   one full 28-layer step of the CPU oracle (oracle.step, torch fp32 autograd) on
@@ -187,23 +187,19 @@ def measure_step_kernels(pkg, trainer, batches, cfg):
     with HIP events around every launch of the dequant, the attention and the GEMM entry points:
     the dequant's achieved GB/s (dispatch-recorded events), the attention forward / backward
     TFLOP/s on each batch's causal pairs (fwd: QK^T and PV, 4 D flops per pair and head; bwd: S,
-    dP, dQ, dK, dV, 10 D flops per pair and head), and the library GEMMs' TFLOP/s (2 M N K a
-    product): all of the step's library projection and lm_head products, the library's gate|up
-    forward if any, and the package's own MFMA GEMM (the gate|up forward products with the
-    SwiGLU epilogue; the largest MFMA kernel of the step). Rates are total work over total
-    launch time across the steps."""
+    dP, dQ, dK, dV, 10 D flops per pair and head), and the package GEMM's TFLOP/s (2 M N K a
+    product) over every launch and by product class, with the gate|up forward products with
+    the SwiGLU epilogue (the largest MFMA kernel of the step) on their own. Rates are total
+    work over total launch time across the steps."""
     P = pkg.profiling
     heads, D = cfg.num_attention_heads, cfg.head_dim
     fwd = P.LaunchTimer("qlora_attn_fwd_split", bound="mfma")
     bwd = P.LaunchTimer("qlora_attn_bwd_split", bound="mfma")
     dq = P.LaunchTimer(P.DEQUANT)
-    flops = lambda a: 2.0 * a[1] * a[2] * a[3]  # noqa: E731  (op, M, N, K, ...)
-    gemms = [P.LaunchTimer(e, work=flops, bound="mfma")
-             for e in ("qlora_gemm", "qlora_gemm_splitk", "qlora_gemmlt")]
     own = P.LaunchTimer(P.DOMINANT, bound="mfma", work=P.hgemm_flops, nbytes=P.hgemm_bytes)
     work_f = work_b = 0.0
     with contextlib.ExitStack() as stack:
-        for t in (dq, fwd, bwd, *gemms, own):
+        for t in (dq, fwd, bwd, own):
             stack.enter_context(t)
         for batch in batches:
             pairs = causal_pairs(batch[5]["lengths"])
@@ -215,9 +211,6 @@ def measure_step_kernels(pkg, trainer, batches, cfg):
     out = [dict(fwd.summary(work_total=work_f), kernel="attn_fwd_kernel"),
            dict(bwd.summary(work_total=work_b),
                 kernel="attn_delta + attn_dq + attn_dkdv kernels")]
-    every = gemms[0].summary(also=gemms[1:])
-    if every is not None:
-        out.append(dict(every, kernel="every library GEMM of the step (projections, lm_head)"))
     # the package's GEMM (qlora_gemm16, args: a, lda, b, ldb, M, N, K, mode, ..., epi at 13)
     H = cfg.hidden_size
     classes = (
@@ -587,20 +580,15 @@ def main():
     trainer = Trainer(model)
     n_batches = max(CURVE_STEPS, args.warmup + args.steps) + 1
     batches = make_batches(n_batches, cfg.vocab_size, device=dev)
-    log("model built; timing the projection GEMM solutions")
-    # every step size config 5 can produce (4 rows of 256..1024 tokens), before any timing
-    sizes = range(4 * 256, 4 * 1024 + pkg.gemm.BUCKET, pkg.gemm.BUCKET)
+    log("model built")
     if args.profile:
-        sizes = sorted({int(b[4]) for b in batches[:args.warmup + args.steps]} |
-                       {int(b[4]) for b in batches[-4:]})
         args.no_cpu, args.no_configs, args.keep_steps = True, True, 0
-    tune_s = model.tune_gemms(sizes, log=log)
     cpu_model = None
     if not args.no_cpu:
         from oracle import step as OS
         cpu_model = OS.CpuQwen2(model)  # the init's weights, before any optimizer step
     first = first_step(model, batches[0])
-    log(f"GEMM tuning {tune_s:.1f} s; first step loss {first['loss']:.5f}; warmup {args.warmup}")
+    log(f"first step loss {first['loss']:.5f}; warmup {args.warmup}")
     _, _, warm_losses = time_steps(trainer, batches, 0, args.warmup)
     log("timing")
     tokens, elapsed, timed_losses = time_steps(trainer, batches, args.warmup, args.steps)
@@ -656,7 +644,9 @@ def main():
                                    "in backward"
                                    if args.policy == "recompute" else
                                    "every layer keeps its intermediates (no recompute)"),
-                   "gemm_backend": pkg.linear.BACKEND, "gemm": pkg.linear.GEMM},
+                   "gemm": ("the package's MFMA GEMM (qlora_gemm16, fixed tile/split plan) "
+                            "after the layer-wide NF4 dequant" if pkg.linear.BACKEND == "dequant"
+                            else "the package's NF4-decoding MFMA GEMM (qlora_nf4_gemm)")},
         "roofline": kernels[0],
         "roofline_dequant": kernels[1],
         "roofline_mfma": kernels[2],
@@ -664,7 +654,6 @@ def main():
         "full_recompute": full,
         "keep_all": keep,
         "graph": graph,
-        "gemm_tuning_s": tune_s,
     }
     if not args.no_configs:
         for name, fn in (("config1", config1), ("config2", config2), ("config3", config3),

@@ -38,11 +38,6 @@ SIGNATURES = {
     "qlora_nf4_block_scales": [P, P, P, P, I32, I32, I64, I64, I64, P, P],
     "qlora_nf4_gemm": [P, I64, P, P, P, I32, I32, I64, I64, P, I64, P, P, I64, I64, I32, I32,
                        I64, I32, P, I64, P],
-    "qlora_hgemm": [P, I64, P, I64, I64, I64, I64, I32, P, I64, P, P, I64, I32, I64, I32, P, I64,
-                    P],
-    "qlora_hgemm_workspace": [I64, I64, I64, I32, I32, P],
-    "qlora_hgemm_timed": [P, I64, P, I64, I64, I64, I64, I32, P, I64, P, P, I64, I32, I64, I32,
-                          P, I64, P, P, P],
     "qlora_gemm16": [P, I64, P, I64, I64, I64, I64, I32, P, I64, P, P, I64, I32, I64, P, I64,
                      I32, I32, I32, P, I64, P],
     "qlora_gemm16_timed": [P, I64, P, I64, I64, I64, I64, I32, P, I64, P, P, I64, I32, I64, P,
@@ -57,14 +52,6 @@ SIGNATURES = {
                         I64, P],
     "qlora_lora_grad_noalloc": [P, P, I64, P, P, P, P, P, P, P, P, P, P, I64, I32, I32, I32, I32,
                                 F32, P],
-    "qlora_gemm": [I32, I64, I64, I64, P, I64, P, I64, P, I64, F32, F32, I32, P],
-    "qlora_gemm_solutions": [I32, I64, I64, I64, P, I64, P, I64, P, I64, P, I32, P],
-    "qlora_gemm_splitk": [I32, I64, I64, I64, P, I64, P, I64, P, I64, P, I32, P, I64, I32, P],
-    "qlora_gemm_splitk_resid": [I32, I64, I64, I64, P, I64, P, I64, P, I64, P, I64, I32, P, I64,
-                                I32, P],
-    "qlora_gemm_splitk_solutions": [I32, I64, I64, I64, P, I64, P, I64, P, I32, P, I32, P],
-    "qlora_gemmlt": [I32, I64, I64, I64, P, I64, P, I64, P, I64, P, F32, F32, I32, P, I64, P],
-    "qlora_gemmlt_solutions": [I32, I64, I64, I64, I64, I64, I64, I32, I64, P, I32, P],
     "qlora_nf4_quantize": [P, I32, I64, P, P, P],
     "qlora_nf4_quantize_stats_workspace": [I64, P],
     "qlora_nf4_quantize_stats": [P, I64, P, P, I64, P, P, P, P],

@@ -7,7 +7,7 @@ Compiled in-tree, next to this file, so the library travels with the source tree
   -target-feature -packed-fp32-ops   no packed fp32 VALU instructions
   -target-feature -fma-mix-insts      no v_fma_mix*: the NF4 decode's fp16(fp32(level * scale))
                              rounds twice, as bitsandbytes; the mix form rounds once
-Linked against rocBLAS and hipBLASLt (the plain projection GEMMs, csrc/blas.hip, csrc/blaslt.hip).
+No vendor GEMM library is linked: every product runs on the package's own kernels.
 Usage: python -m <package>.build  (or build() from __graft_entry__)
 """
 
@@ -58,8 +58,7 @@ def build(verbose=False, jobs=None):
         msg = "\n".join(f"--- {s}\n{o}" for s, o in failed)
         raise RuntimeError(f"hipcc failed:\n{msg}")
     tmp = LIB + ".tmp"
-    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp,
-           "-L/opt/rocm/lib", "-lrocblas", "-lhipblaslt"]
+    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
     subprocess.run(cmd, check=True)
     os.replace(tmp, LIB)
     return LIB

@@ -859,7 +859,7 @@ __device__ __forceinline__ void store_tail_part(float* p, const f32x16 (&acc)[BM
     }
 }
 
-// The GEMM with an fp16 B in memory (qlora_hgemm): for 256 x 256 tiles the same wavefront blocks,
+// The GEMM with an fp16 B in memory (qlora_gemm16): for 256 x 256 tiles the same wavefront blocks,
 // MFMA order and epilogues as nf4_gemm_kernel, so the results are the same bits as that
 // kernel's for the same B values; every tile shape accumulates each output's k-steps of 16 in
 // order, so either shape gives the same bits in one slice.
@@ -1574,32 +1574,4 @@ QLORA_API int qlora_gemm16_plan(int64_t M, int64_t N, int64_t K, int32_t mode, i
   *stages = st;
   *splits = sp;
   return 0;
-}
-
-// The 256 x 256 form (qlora_gemm16 with tile 256).
-QLORA_API int qlora_hgemm_timed(const void* a, int64_t lda, const void* b, int64_t ldb,
-                                int64_t M, int64_t N, int64_t K, int32_t mode, void* c,
-                                int64_t ldc, const void* bias, const float* resid, int64_t ldr,
-                                int32_t epi, int64_t swiglu_I, int32_t splits, float* ws,
-                                int64_t ws_elems, void* stream, void* start, void* stop) {
-  QLORA_CHECK_ARG(epi <= 3);
-  return qlora_gemm16_timed(a, lda, b, ldb, M, N, K, mode, c, ldc, bias, resid, ldr, epi,
-                            swiglu_I, nullptr, 0, 256, 2, splits, ws, ws_elems, stream, start,
-                            stop);
-}
-
-QLORA_API int qlora_hgemm(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t M,
-                          int64_t N, int64_t K, int32_t mode, void* c, int64_t ldc,
-                          const void* bias, const float* resid, int64_t ldr, int32_t epi,
-                          int64_t swiglu_I, int32_t splits, float* ws, int64_t ws_elems,
-                          void* stream) {
-  QLORA_CHECK_ARG(epi <= 3);
-  return qlora_gemm16_timed(a, lda, b, ldb, M, N, K, mode, c, ldc, bias, resid, ldr, epi,
-                            swiglu_I, nullptr, 0, 256, 2, splits, ws, ws_elems, stream, nullptr,
-                            nullptr);
-}
-
-QLORA_API int qlora_hgemm_workspace(int64_t M, int64_t N, int64_t K, int32_t epi, int32_t splits,
-                                    int64_t* elems) {
-  return qlora_gemm16_workspace(M, N, K, 0, epi, 256, 2, splits, elems);
 }

@@ -20,7 +20,6 @@ import math
 
 import torch
 
-from . import gemm as G
 from . import linear as L
 from .ops import (NF4Group, NF4Weight, TorchDropout, _attn_bwd, _attn_fwd, _ce, _glu_bwd,
                   _glu_fwd, _lora_bwd_rows, _lora_fwd_rows, _lora_grad, _rms_bwd, _rms_fwd,
@@ -733,6 +732,21 @@ class _Head(torch.autograd.Function):
 # ---------------------------------------------------------------------------------------------
 # The model
 # ---------------------------------------------------------------------------------------------
+def check_gemm_shapes(cfg):
+    """Raise UnsupportedModel unless the package's GEMM takes every product of the step: each
+    projection and the lm_head forward (NT) and their input gradients (NN), the reduction in
+    blocks of 128 (every Qwen2 size: H, I, the q/k/v widths and the vocabulary are)."""
+    H, I, V = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size
+    qkv = (cfg.num_attention_heads + 2 * cfg.num_key_value_heads) * cfg.head_dim
+    o = cfg.num_attention_heads * cfg.head_dim
+    fwd = [(H, qkv), (o, H), (H, 2 * I), (I, H), (H, V)]  # (K, N) of y = x W^T
+    ok = all(L.tiles(k, n, 0) and L.tiles(n, k, 1) for k, n in fwd) and I % 128 == 0
+    if not ok:
+        raise UnsupportedModel(
+            f"hidden {H}, intermediate {I}, q/k/v width {qkv}, o width {o}, vocabulary {V}: "
+            "the step's GEMM takes sizes that are multiples of 128")
+
+
 class FusedQwen2:
     """The step of a Qwen2 NF4 + LoRA model (engine.py:1568-1922 without the host offload).
 
@@ -750,6 +764,7 @@ class FusedQwen2:
     CAP_MARGIN = 8 * 2**30  # bytes of device memory the default cap leaves free
 
     def __init__(self, cfg, layers, embed, norm_w, device, keep_all=False):
+        check_gemm_shapes(cfg)
         self.cfg = cfg
         self.layers = layers
         self.embed = embed
@@ -759,9 +774,6 @@ class FusedQwen2:
         self.device = torch.device(device)
         self.keep_all = keep_all
         self.memory_cap = None
-        # with the library GEMMs (linear.GEMM == "library"): time their solutions for each new
-        # token bucket; the package's GEMM has a fixed plan and nothing to time
-        self.autotune = True
         # layers that keep their intermediates also keep their dequantized weights for the
         # backward (one dequant per layer and step instead of two; 94 MB per 1.5B layer)
         self.keep_weights = True
@@ -851,30 +863,6 @@ class FusedQwen2:
         per_layer = max(1, self.kept_bytes_per_layer(n) + (weights if self.keep_weights else 0))
         return int(max(0, min(len(self.layers), free // per_layer)))
 
-    def gemm_shapes(self):
-        """(op, N, K, bias) of the step's GEMMs: y = x W^T (+ b for qkv) for qkv, o, gate|up,
-        down and the lm_head, and dX = dY W for the same five weights (the lm_head last)."""
-        spec = self.layers[0]
-        H, I, qkv, o = spec.H, spec.I, (spec.HQ + 2 * spec.HKV) * spec.D, spec.HQ * spec.D
-        fwd = [(qkv, H), (H, o), (2 * I, H), (H, I), (self.cfg.vocab_size, H)]
-        return ([(G.NT, n, k, i == 0) for i, (n, k) in enumerate(fwd)] +
-                [(G.NN, k, n, False) for n, k in fwd])
-
-    def tune_gemms(self, token_counts, log=None):
-        """Measure the GEMM solutions for the buckets of these step sizes (tokens); the head's
-        dX product runs over the supervised rows only, so it is also measured at 3/4 and 1/2 of
-        each size. Returns the seconds spent."""
-        if L.GEMM != "library":
-            return 0.0  # the package's GEMM plan is fixed: nothing to measure
-        counts = list(token_counts)
-        shapes = self.gemm_shapes()
-        t = G.tune(shapes, counts, self.device, log=log)
-        sup = sorted({max(1, (c * f) // 4) for c in counts for f in (2, 3)})
-        t += G.tune(shapes[-1:], sup, self.device, log=log)
-        for I, H in sorted({(spec.I, spec.H) for spec in self.layers}):
-            t += L.tune_swiglu(I, H, counts, self.device, log=log)
-        return t
-
     def step(self, input_ids, attention_mask, labels, denom, lengths=None, n_supervised=None,
              padded=False, ctr_base=None):
         """The step's forward: (loss, packed, stats); autograd runs the backward. `lengths`
@@ -885,12 +873,6 @@ class FusedQwen2:
         packed = Packed(input_ids, attention_mask, labels, self.rope, self.dropout,
                         self.dropout_p, lengths=lengths, n_supervised=n_supervised,
                         padded=padded, ctr_base=ctr_base)
-        if self.autotune and L.GEMM == "library":
-            shapes = self.gemm_shapes()
-            G.tune(shapes, [packed.n], self.device)
-            G.tune(shapes[-1:], [max(1, packed.n_supervised)], self.device)
-            for I, H in sorted({(spec.I, spec.H) for spec in self.layers}):
-                L.tune_swiglu(I, H, [packed.n], self.device)
         if self.dropout is not None and self.dropout.ok is None:
             self.dropout.ok = self.dropout.check(packed.rows,
                                                  min(packed.T, TorchDropout.CHECK_TOKENS),

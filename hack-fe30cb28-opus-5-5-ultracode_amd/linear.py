@@ -1,25 +1,20 @@
 """The step's GEMMs: frozen NF4 projections forward (Y = X W^T [+ bias]) and backward
 (dX = dY W), and the plain fp16 lm_head products (engine.py:1082, 1112, 1163, 1179, 1239, 1293,
-1301, 1316, 1376, 1381).
+1301, 1316, 1376, 1381). Every product runs on this package's MFMA GEMM.
 
-Backend "fused": qlora_nf4_gemm, the NF4 decode inside the MFMA GEMM's B-operand
-loader, with the epilogues the step needs (qkv bias, the SwiGLU of gate|up, the residual add
-after down_proj, fp32 gradients rounded to fp16 on load).
-Backend "dequant" (default while it is the faster one): the standalone dequant kernel into an
-fp16 buffer, then a plain GEMM (gemm.mm: rocBLAS with a measured solution per shape and token
-bucket, or torch's matmul where that is the faster) - the reference's own structure (dequant,
-then cuBLAS), with this package's MFMA GEMM (qlora_hgemm) among the tuner's candidates - and
-the gate|up forward with its SwiGLU on that GEMM with the SwiGLU in its epilogue, for the token
-counts where it was timed faster than the library GEMM and the SwiGLU kernel (SWIGLU_EPILOGUE,
-tune_swiglu).
+Backend "dequant" (default, the faster one): the layer-wide dequant kernel into fp16 buffers,
+then the package's fp16-B GEMM (qlora_gemm16) with its fixed tile/split plan - the reference's
+own structure (dequant, then cuBLAS) - with the epilogues the step needs (qkv bias, the SwiGLU of
+gate|up with or without the product kept, the residual add after down_proj).
+Backend "fused": qlora_nf4_gemm, the NF4 decode inside the MFMA GEMM's B-operand loader, with
+the same epilogues.
 """
 
 import ctypes
-import time
 
 import torch
 
-from . import _lib, gemm
+from . import _lib
 from .ops import NF4Group, _need, _ptr, _stream, dequant, dequant_many, gemm_tiles
 
 BACKEND = "dequant"
@@ -245,46 +240,37 @@ def hgemm(a, b, mode, epi=0, bias=None, resid=None, out=None, swiglu_I=0, splits
     return out
 
 
+def tiles(K, N, mode):
+    """Whether qlora_gemm16 takes a product with reduction K and N output columns: K in blocks
+    of 128, N a multiple of 8 (NT) or of 128 (NN). Every Qwen2 size does (H, I, the q/k/v
+    widths, the vocabularies 151,936 and 152,064)."""
+    return K % 128 == 0 and (N % 8 == 0 if mode == 0 else N % 128 == 0)
+
+
+def _check(K, N, mode, what):
+    if not tiles(K, N, mode):
+        raise ValueError(f"{what}: the package GEMM needs the reduction in blocks of 128 and "
+                         f"{'N % 8' if mode == 0 else 'N % 128'} == 0 (got K = {K}, N = {N})")
+
+
 def nf4_linear(x, w, bias=None):
     """Y = X W^T [+ bias], fp16 [M, N]."""
     if BACKEND == "fused":
         return nf4_gemm(x, w, 0, epi=1 if bias is not None else 0, bias=bias)
-    if GEMM == "package" and tiles(x.shape[1], _shape(w)[0], 0):
-        return hgemm(x, dequantize(w), 0, epi=1 if bias is not None else 0, bias=bias, tile=0)
-    return gemm.mm(x, dequantize(w), gemm.NT, bias=bias)
+    _check(x.shape[1], _shape(w)[0], 0, "X W^T")
+    return hgemm(x, dequantize(w), 0, epi=1 if bias is not None else 0, bias=bias, tile=0)
 
 
-# Which GEMMs run the dequantized products and the lm_head's: "package" - this library's MFMA
-# GEMM (qlora_gemm16) with its fixed tile/split plan; "library" - rocBLAS/hipBLASLt with a
-# variant measured per shape and token bucket (gemm.py), kept for comparison.
-GEMM = "package"
-
-
-def tiles(K, N, mode):
-    """Whether qlora_gemm16 takes this product: the reduction in blocks of 128, N a multiple of
-    8 (NT) or of 128 (NN). Every Qwen2 size does (H, I, the vocabulary 151,936); a shape that
-    does not (test models' odd vocabularies) runs torch's matmul."""
-    return K % 128 == 0 and (N % 8 == 0 if mode == 0 else N % 128 == 0)
-
-
-# With the layer-wide dequant: the gate|up product of a recomputing layer's forward on the MFMA
-# GEMM of this package (qlora_hgemm), the SwiGLU in its epilogue ([gate | up] never stored),
-# instead of the library GEMM and the SwiGLU kernel, for the token-count buckets where the tuner
-# (tune_swiglu) timed it faster than that pair; untimed buckets take the package's form.
-# Measured on MI355X, config 5, alternating runs on one box, package form at every count:
-# 34.38 / 34.52 ms per step against 34.49 / 34.41 ms for the library pair.
-SWIGLU_EPILOGUE = True
-_SWIGLU_ON_PKG = {}  # (device index, I, K, bucket) -> the package's form was the faster
-# ... and with the NF4 weight decoded inside that GEMM (qlora_nf4_gemm over the weight's
-# tile-major copy): the forward then dequantizes the layer's other three weights only. Off: the
-# same alternating runs on one box gave 36.16 / 36.28 ms per step against 35.98 / 35.98 ms with
+# The gate|up product with the NF4 weight decoded inside the GEMM (qlora_nf4_gemm over the
+# weight's tile-major copy): the forward then dequantizes the layer's other three weights only.
+# Off: alternating runs on one box gave 36.16 / 36.28 ms per step against 35.98 / 35.98 ms with
 # the fp16 weight (the in-kernel decode costs about as much as the dequant it saves).
 SWIGLU_NF4 = False
 
 
 def swiglu_fused_nf4():
     """Whether the forward's gate|up product reads the NF4 weight itself (no fp16 copy)."""
-    return BACKEND == "fused" or (SWIGLU_EPILOGUE and SWIGLU_NF4)
+    return BACKEND == "fused" or SWIGLU_NF4
 
 
 def _gemm_fits(I, K):
@@ -293,66 +279,25 @@ def _gemm_fits(I, K):
     return I % 128 == 0 and K % 128 == 0
 
 
-def swiglu_on_package(dev_index, I, K, M):
-    """Whether the fp16-weight SwiGLU product of M tokens runs on the package's GEMM with the
-    SwiGLU epilogue (else the library GEMM and the SwiGLU kernel)."""
-    if not (SWIGLU_EPILOGUE and _gemm_fits(I, K)):
-        return False
-    return _SWIGLU_ON_PKG.get((dev_index, I, K, gemm._bucket(M)), True)
-
-
-def tune_swiglu(I, K, Ms, device, reps=3, log=None):
-    """Times, per bucket of the token counts Ms, the SwiGLU product on the package's GEMM
-    against the library pair (the tuned library GEMM, then qlora_glu_fwd), with cold caches as
-    gemm.tune; run after gemm.tune has measured the (NT, 2 I, K) product. Returns seconds."""
-    from .ops import _glu_fwd
-    t0 = time.perf_counter()
-    dev = torch.device(device)
-    di = dev.index or 0
-    todo = sorted({gemm._bucket(M) for M in Ms if M > 0} -
-                  {k[3] for k in _SWIGLU_ON_PKG if k[:3] == (di, I, K)})
-    if not todo or not (SWIGLU_EPILOGUE and _gemm_fits(I, K)):
-        return 0.0
-    g = torch.Generator(device=dev).manual_seed(0)
-    m_max = todo[-1] * gemm.BUCKET
-    a_full = torch.randn((m_max, K), device=dev, generator=g).to(torch.float16)
-    w = (torch.randn((2 * I, K), device=dev, generator=g) * 0.02).to(torch.float16)
-    gu = torch.empty((m_max, 2 * I), device=dev, dtype=torch.float16)
-    m = torch.empty((m_max, I), device=dev, dtype=torch.float16)
-    for bk in todo:
-        M = bk * gemm.BUCKET
-        a = a_full[:M]
-        pkg = gemm._time(lambda: hgemm(a, w, 0, epi=3, swiglu_I=I, out=m[:M]), reps)
-        lib = gemm._time(lambda: _glu_fwd(gemm.mm(a, w, gemm.NT, out=gu[:M]), I, out=m[:M]),
-                         reps)
-        _SWIGLU_ON_PKG[(di, I, K, bk)] = pkg <= lib
-        if log is not None:
-            log(f"swiglu tune I={I} K={K} M={M}: package {pkg * 1e3:.1f} us, "
-                f"library pair {lib * 1e3:.1f} us")
-    del a_full, w, gu, m
-    return time.perf_counter() - t0
-
-
 def nf4_linear_swiglu(x, w, I):
-    """m = fp16(silu(g) * u) of [g | u] = X W^T for the stacked gate|up weight, fp16 [M, I]."""
-    fits = _gemm_fits(I, x.shape[1])
-    if swiglu_fused_nf4() and fits:
+    """m = fp16(silu(g) * u) of [g | u] = X W^T for the stacked gate|up weight, fp16 [M, I]:
+    the SwiGLU in the GEMM's epilogue ([gate | up] never stored)."""
+    if not _gemm_fits(I, x.shape[1]):
+        raise ValueError(f"SwiGLU product: I = {I} and K = {x.shape[1]} must be multiples of 128")
+    if swiglu_fused_nf4():
         return nf4_gemm(x, w, 0, epi=3, swiglu_I=I)
-    if GEMM == "package" and fits:
-        return hgemm(x, dequantize(w), 0, epi=3, swiglu_I=I, tile=0)
-    if GEMM != "package" and swiglu_on_package(x.device.index or 0, I, x.shape[1], x.shape[0]):
-        return hgemm(x, dequantize(w), 0, epi=3, swiglu_I=I)
-    from .ops import _glu_fwd
-    return _glu_fwd(nf4_linear(x, w), I)
+    return hgemm(x, dequantize(w), 0, epi=3, swiglu_I=I, tile=0)
 
 
 def nf4_linear_swiglu_keep(x, w, I):
     """(m, [g | u]): the SwiGLU of the stacked gate|up product and the product itself, fp16
     [M, I] and [M, 2 I], from one GEMM (a recomputing layer keeps [g | u] for its backward, as
     the reference's step keeps it rather than multiplying again, engine.py:1204-1213); None
-    when the package's GEMM does not take the shape."""
-    if GEMM != "package" or BACKEND == "fused" or not _gemm_fits(I, x.shape[1]):
+    with the NF4-decoding backend (which has no such epilogue)."""
+    if BACKEND == "fused":
         return None
+    if not _gemm_fits(I, x.shape[1]):
+        raise ValueError(f"SwiGLU product: I = {I} and K = {x.shape[1]} must be multiples of 128")
     M = x.shape[0]
     gu = torch.empty((M, 2 * I), device=x.device, dtype=torch.float16)
     m = hgemm(x, dequantize(w), 0, epi=5, swiglu_I=I, tile=0, gu=gu)
@@ -369,9 +314,8 @@ def nf4_linear_resid(x, w, resid, out=None):
     epilogue (or the split-K reduce's), no fp16 product in memory."""
     if BACKEND == "fused":
         return nf4_gemm(x, w, 0, epi=2, resid=resid, out=out)
-    if GEMM == "package" and tiles(x.shape[1], _shape(w)[0], 0):
-        return hgemm(x, dequantize(w), 0, epi=2, resid=resid, out=out, tile=0)
-    return gemm.mm_resid(_a16(x), dequantize(w), gemm.NT, resid, out=out)
+    _check(x.shape[1], _shape(w)[0], 0, "X W^T + resid")
+    return hgemm(x, dequantize(w), 0, epi=2, resid=resid, out=out, tile=0)
 
 
 def nf4_linear_t(dy, w):
@@ -381,24 +325,17 @@ def nf4_linear_t(dy, w):
         return nf4_gemm(dy, w, 1)
     if dy.dtype != torch.float16:
         dy = dy.to(torch.float16)
-    if GEMM == "package" and tiles(dy.shape[1], _shape(w)[1], 1):
-        return hgemm(dy, dequantize(w), 1, tile=0)
-    return gemm.mm(dy, dequantize(w), gemm.NN)
+    _check(dy.shape[1], _shape(w)[1], 1, "dY W")
+    return hgemm(dy, dequantize(w), 1, tile=0)
 
 
 def linear(x, w):
     """x W^T for an fp16 weight [V, H] (the lm_head)."""
-    if GEMM == "package":
-        if tiles(x.shape[1], w.shape[0], 0):
-            return hgemm(x, w, 0, tile=0)
-        return torch.mm(x, w.t())
-    return gemm.mm(x, w, gemm.NT)
+    _check(x.shape[1], w.shape[0], 0, "lm_head x E^T")
+    return hgemm(x, w, 0, tile=0)
 
 
 def linear_t(g, w):
-    """g W for an fp16 weight [V, H]."""
-    if GEMM == "package":
-        if tiles(g.shape[1], w.shape[1], 1):
-            return hgemm(g, w, 1, tile=0)
-        return torch.mm(g, w)
-    return gemm.mm(g, w, gemm.NN)
+    """g W for an fp16 weight [V, H] (the lm_head's input gradient)."""
+    _check(g.shape[1], w.shape[1], 1, "lm_head G E")
+    return hgemm(g, w, 1, tile=0)

@@ -32,7 +32,7 @@ DEQUANT = "qlora_nf4_dequant_many"
 # weighted by launch; 2.74 at 9 row tiles, 2.78 at 10, 2.97 at 11 (sliced tail), 3.44 at 12.
 # The excess is the A tile re-read by each XCD and B tiles re-read past the 4 MB L2
 # (FETCH_SIZE counts what leaves the L2, Infinity Cache hits included).
-TRAFFIC_RATIO = {"qlora_nf4_dequant_many": 1.0018, "qlora_hgemm": 2.92, "qlora_gemm16": 2.92}
+TRAFFIC_RATIO = {"qlora_nf4_dequant_many": 1.0018, "qlora_gemm16": 2.92}
 
 
 def _dequant_bytes(args):
@@ -63,20 +63,20 @@ def _dequant_many_bytes(args):
 
 # entries with a form that records the events from the kernel dispatch itself
 TIMED = {"qlora_nf4_dequant_many": "qlora_nf4_dequant_many_timed",
-         "qlora_hgemm": "qlora_hgemm_timed", "qlora_gemm16": "qlora_gemm16_timed"}
+         "qlora_gemm16": "qlora_gemm16_timed"}
 
 
 SWIGLU_EPIS = (3, 5)  # the SwiGLU epilogues (5: the product [g | u] written beside it)
 
 
 def hgemm_flops(args):
-    """2 M N K of one qlora_hgemm / qlora_gemm16 launch (a, lda, b, ldb, M, N, K, mode, ..., epi
+    """2 M N K of one qlora_gemm16 launch (a, lda, b, ldb, M, N, K, mode, ..., epi
     at 13): N is the output's columns, I with a SwiGLU epilogue, whose product is [M, 2 I]."""
     return 2.0 * args[4] * args[5] * args[6] * (2 if args[13] in SWIGLU_EPIS else 1)
 
 
 def hgemm_bytes(args):
-    """Algorithmic HBM bytes of one qlora_hgemm / qlora_gemm16 launch: A [M, K], the weight
+    """Algorithmic HBM bytes of one qlora_gemm16 launch: A [M, K], the weight
     ([N, K], [2 I, K] with a SwiGLU epilogue, [K, N] in NN) and the fp16 output [M, N] once
     each, and with epilogue 5 the product [g | u] [M, 2 I] written beside it."""
     M, N, K, epi = args[4], args[5], args[6], args[13]

@@ -6,11 +6,6 @@
  * hipError_t (hipErrorInvalidValue = 1 for arguments a kernel cannot take; checked before any
  * launch). Kernels allocate nothing: callers pass every output and workspace. The library keeps
  * this process-wide state, each created on first use per device and kept until the process ends:
- *   - one rocBLAS handle per device (qlora_gemm*, csrc/blas.hip; rocBLAS keeps its own small
- *     workspace in it);
- *   - one hipBLASLt handle per device and a cache of its plans (matmul descriptors and the
- *     heuristic's choice) per exact problem, in a map behind a mutex (qlora_gemmlt*,
- *     csrc/blaslt.hip);
  *   - one second stream and two events per device (csrc/attn.hip), on which the attention
  *     backward runs dK/dV beside dQ; it is forked from and joined back into the caller's stream
  *     inside the call, so the call is ordered on the caller's stream as any other;
@@ -286,59 +281,30 @@ int qlora_nf4_gemm(const void* a, int64_t lda, const void* packed, const float* 
 /*
  * The same GEMM with an fp16 B operand in memory (the dequantized projections; the lm_head):
  *   mode 0 (NT): C[M, N] = A[M, K] B^T, B [N, K] (ldb);  mode 1 (NN): C = A B, B [K, N] (ldb).
- * epi, splits, ws as qlora_nf4_gemm (epi 3: B = [gate; up] rows, N = I). With splits == 1 a
- * 16-byte aligned ws of at least qlora_hgemm_workspace's elements lets the few tiles of a last,
- * nearly empty round of the GPU run as K slices (partials in ws, summed in a fixed order, then
- * the epilogue); a null or smaller ws runs them whole (results then differ in the fp32
- * summation order of those tiles only).
+ * Output tiles of tile x tile: tile 256 (one workgroup of four 128 x 128 wavefront blocks per
+ * CU) or 128 (four 64 x 64 wavefront blocks, two workgroups per CU: four times the tiles, for
+ * the narrow products - N = 1536 or 2048 at a few thousand tokens). In one slice both tile
+ * shapes give the same bits (each output sums its k-steps of 16 in order). stages: 2 (either
+ * tile) or 4 (128 x 128 tiles only: 128 KB of LDS, one workgroup per CU, each k-tile's loads
+ * issued three k-tiles ahead).
+ * epi as qlora_nf4_gemm (epi 3: B = [gate; up] rows, N = I), and
+ *   5 (NT, one slice): the SwiGLU of epi 3 and the product [g | u] itself, fp16 [M, 2 N] into
+ *     gu (ldgu, 16-byte rows; gate column n and up column N + n), the same values a plain
+ *     store of the product gives: a recomputing layer keeps it for its backward (the
+ *     reference's step keeps [gate | up] rather than multiplying again: engine.py:1204-1213,
+ *     430-445). gu is read for epi 5 only (else null).
+ * splits > 1: split-K, fp32 partials in ws (>= splits*M*N elements), summed in a fixed order by
+ * a reduce kernel that applies the epilogue (not with the SwiGLU forms). With splits == 1 a
+ * 16-byte aligned ws of at least qlora_gemm16_workspace's elements lets the few tiles of a
+ * last, nearly empty round of the GPU run as K slices (partials in ws, summed in slice order,
+ * then the epilogue; the slice count follows the tile count and the GPU's workgroup slots: 256
+ * tiles of 256, 512 of 128); a null or smaller ws runs them whole (results then differ in the
+ * fp32 summation order of those tiles only).
+ * tile 0 with splits 0 (and any stages): the plan of qlora_gemm16_plan.
  * Replaces the cuBLAS products of the frozen projections after dequant (engine.py:1082, 1112,
  * 1163, 1179, 1239, 1293, 1301, 1316) and of the lm_head (engine.py:1376-1381).
- * Requires: K % 128 == 0; mode 1: N % 256 == 0; mode 0: N % 8 == 0 (epi 3: N % 128 == 0);
- * lda, ldb % 8 == 0; A, B 16-byte aligned.
- */
-int qlora_hgemm(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t M, int64_t N,
-                int64_t K, int32_t mode, void* c, int64_t ldc, const void* bias,
-                const float* resid, int64_t ldr, int32_t epi, int64_t swiglu_I, int32_t splits,
-                float* ws, int64_t ws_elems, void* stream);
-
-/*
- * fp32 workspace elements (*elems) qlora_hgemm uses for this problem: splits * M * N with
- * splits > 1; with one slice the K-sliced last round's partials, 0 when that does not apply.
- * N as qlora_hgemm's (epi 3: I). No reference counterpart (sizes the caller's workspace).
- */
-int qlora_hgemm_workspace(int64_t M, int64_t N, int64_t K, int32_t epi, int32_t splits,
-                          int64_t* elems);
-
-/*
- * qlora_hgemm that also records start/stop (hipEvent_t created with timing, or null) at the start
- * of its tile grid and the end of its last kernel (the split-K or K-sliced-tail reduce), the
- * dispatches' own timestamps. No reference counterpart: the bench's per-launch timing of the
- * step's own MFMA GEMM.
- */
-int qlora_hgemm_timed(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t M,
-                      int64_t N, int64_t K, int32_t mode, void* c, int64_t ldc, const void* bias,
-                      const float* resid, int64_t ldr, int32_t epi, int64_t swiglu_I,
-                      int32_t splits, float* ws, int64_t ws_elems, void* stream, void* start,
-                      void* stop);
-
-/*
- * qlora_hgemm on tile x tile output tiles: tile 256 (qlora_hgemm itself: one workgroup of four
- * 128 x 128 wavefront blocks per CU) or 128 (four 64 x 64 wavefront blocks, two workgroups per
- * CU: four times the tiles, for the narrow products - N = 1536 or 2048 at a few thousand
- * tokens). In one slice both tile shapes give the same bits (each output sums its k-steps of
- * 16 in order); split-K and the K-sliced last round (whose size follows the tile count and the
- * GPU's workgroup slots: 256 tiles of 256, 512 of 128) sum fp32 partials in a fixed order.
- * stages: 2 (either tile; two 128 x 128 workgroups then share a CU) or 4 (128 x 128 tiles
- * only: 128 KB of LDS, one workgroup per CU, each k-tile's loads issued three k-tiles ahead).
- * tile 0 with splits 0 (and any stages): the plan of qlora_gemm16_plan.
- * epi 5 (NT, one slice): the SwiGLU of epi 3 and the product [g | u] itself, fp16 [M, 2 N]
- * into gu (ldgu, 16-byte rows; gate column n and up column N + n), the same values a plain
- * store of the product gives: a recomputing layer keeps it for its backward (the reference's
- * step keeps [gate | up] rather than multiplying again: engine.py:1204-1213, 430-445).
- * gu is read for epi 5 only (else null).
- * Replaces the same cuBLAS products as qlora_hgemm (engine.py:1082, 1112, 1163, 1179, 1239,
- * 1293, 1301, 1316, 1376-1381). Requires qlora_hgemm's conditions with mode 1: N % tile == 0;
- * epi 3: N % (tile / 2) == 0; K % (64 stages) == 0.
+ * Requires: K % (64 stages) == 0 and K % 128 == 0; mode 1: N % tile == 0; mode 0: N % 8 == 0
+ * (epi 3, 5: N % (tile / 2) == 0); lda, ldb % 8 == 0; A, B 16-byte aligned.
  */
 int qlora_gemm16(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t M, int64_t N,
                  int64_t K, int32_t mode, void* c, int64_t ldc, const void* bias,
@@ -346,7 +312,12 @@ int qlora_gemm16(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t
                  int64_t ldgu, int32_t tile, int32_t stages, int32_t splits, float* ws,
                  int64_t ws_elems, void* stream);
 
-/* qlora_gemm16 with the start/stop events of qlora_hgemm_timed (no reference counterpart). */
+/*
+ * qlora_gemm16 that also records start/stop (hipEvent_t created with timing, or null) at the
+ * start of its tile grid and the end of its last kernel (the split-K or K-sliced-tail reduce),
+ * the dispatches' own timestamps. No reference counterpart: the bench's per-launch timing of
+ * the step's own MFMA GEMM.
+ */
 int qlora_gemm16_timed(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t M,
                        int64_t N, int64_t K, int32_t mode, void* c, int64_t ldc,
                        const void* bias, const float* resid, int64_t ldr, int32_t epi,
@@ -355,9 +326,10 @@ int qlora_gemm16_timed(const void* a, int64_t lda, const void* b, int64_t ldb, i
                        void* stop);
 
 /*
- * fp32 workspace elements (*elems) qlora_gemm16 uses for this problem, mode, tile and stage count
- * (as qlora_hgemm_workspace; tile 0 / splits 0: the automatic plan's). No reference counterpart
- * (sizes the caller's workspace).
+ * fp32 workspace elements (*elems) qlora_gemm16 uses for this problem, mode, tile and stage
+ * count: splits * M * N with splits > 1; with one slice the K-sliced last round's partials, 0
+ * when that does not apply (tile 0 / splits 0: the automatic plan's). N as qlora_gemm16's
+ * (epi 3, 5: I). No reference counterpart (sizes the caller's workspace).
  */
 int qlora_gemm16_workspace(int64_t M, int64_t N, int64_t K, int32_t mode, int32_t epi,
                            int32_t tile, int32_t stages, int32_t splits, int64_t* elems);
@@ -375,73 +347,6 @@ int qlora_gemm16_plan(int64_t M, int64_t N, int64_t K, int32_t mode, int32_t epi
  * the residual add after the down projection, h3 = h2 + d (engine.py:1048-1051, 1179).
  */
 int qlora_resid_add(const float* a, const void* d, float* out, int64_t numel, void* stream);
-
-/*
- * Row-major fp16 GEMM, fp32 accumulation, through rocBLAS with an explicit Tensile solution:
- *   C[M, N] = alpha * A[M, K] op(B) + beta * C,  op = 0: B [N, K] (C = A B^T), op = 1: B [K, N].
- * Leading dimensions in elements; solution 0 = rocBLAS's own choice, > 0 an index returned by
- * qlora_gemm_solutions for the same problem. Replaces the frozen projections' torch matmuls:
- * y = x W^T (engine.py:1082, 1112, 1135, 1156) and dX = dY W (engine.py:1239, 1293, 1301, 1316).
- * Returns 100000 + rocblas_status on a rocBLAS error.
- */
-int qlora_gemm(int32_t op, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
-               const void* B, int64_t ldb, void* C, int64_t ldc, float alpha, float beta,
-               int32_t solution, void* stream);
-
-/*
- * The rocBLAS solution indices that can run the qlora_gemm problem with these sizes: up to cap of
- * them into list, their total number into *count (no kernel is launched; the pointers are the
- * problem's buffers). No reference counterpart: the tuning step of the projections above.
- */
-int qlora_gemm_solutions(int32_t op, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
-                         const void* B, int64_t ldb, void* C, int64_t ldc, int32_t* list,
-                         int32_t cap, int32_t* count);
-
-/*
- * qlora_gemm with the reduction cut into `splits` equal slices: one strided-batched rocBLAS call
- * writes fp32 partial products into work [splits][M][N], a kernel sums them in a fixed order and
- * rounds once: C = fp16(sum + bias) (bias f16 [N] or null). For long-K, narrow-N products whose
- * output alone has too few tiles for the GPU (dX of gate|up, engine.py:1293; dX of the lm_head,
- * engine.py:1381). Requires K % (8 splits) == 0, N % 4 == 0, ldc % 4 == 0, C 8-byte aligned,
- * work_elems >= splits M N; solution: 0 or an index from qlora_gemm_splitk_solutions.
- */
-int qlora_gemm_splitk(int32_t op, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
-                      const void* B, int64_t ldb, void* C, int64_t ldc, const void* bias,
-                      int32_t splits, float* work, int64_t work_elems, int32_t solution,
-                      void* stream);
-/*
- * qlora_gemm_splitk added to the fp32 residual stream: out[M, N] (fp32, ld ldo) = resid (fp32, ld
- * ldr) + f32(fp16(A op(B))), the slices' fixed-order sum rounded once to fp16, then added (the
- * down projection and the residual add of the layer output, engine.py:1179 and its h2 + d). out
- * may alias resid. Requires as qlora_gemm_splitk, ldr and ldo % 4 == 0, resid and out 16-byte
- * aligned.
- */
-int qlora_gemm_splitk_resid(int32_t op, int64_t M, int64_t N, int64_t K, const void* A,
-                            int64_t lda, const void* B, int64_t ldb, const float* resid,
-                            int64_t ldr, float* out, int64_t ldo, int32_t splits, float* work,
-                            int64_t work_elems, int32_t solution, void* stream);
-int qlora_gemm_splitk_solutions(int32_t op, int64_t M, int64_t N, int64_t K, const void* A,
-                                int64_t lda, const void* B, int64_t ldb, float* work,
-                                int32_t splits, int32_t* list, int32_t cap, int32_t* count);
-
-/*
- * The qlora_gemm problem through hipBLASLt: C = alpha A op(B) (+ bias[N], f16, in the epilogue
- * before the one rounding) + beta C. solution: an index that qlora_gemmlt_solutions lists for the
- * same (op, sizes, leading dimensions, bias or not, ws_bytes); any other is rejected
- * (hipErrorInvalidValue, nothing launched). workspace: device memory of ws_bytes (may be 0).
- * Same reference call sites as qlora_gemm (engine.py:1082-1316); returns 200000 +
- * hipblasStatus_t on a hipBLASLt error.
- */
-int qlora_gemmlt(int32_t op, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
-                 const void* B, int64_t ldb, void* C, int64_t ldc, const void* bias, float alpha,
-                 float beta, int32_t solution, void* workspace, int64_t ws_bytes, void* stream);
-/*
- * The solution indices hipBLASLt's heuristic returns for that problem (bias != 0: with the bias
- * epilogue), in its order: up to cap into list, the number into *count. No kernel is launched.
- */
-int qlora_gemmlt_solutions(int32_t op, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
-                           int64_t ldc, int32_t bias, int64_t ws_bytes, int32_t* list,
-                           int32_t cap, int32_t* count);
 
 /*
  * The LoRA forward of a layer's q and v adapters in one launch (engine.py:1088-1093):

@@ -93,47 +93,48 @@ def test_invalid_arguments_rejected_before_launch(pkg):
                                  0, 0, None) == 1
 
 
-def test_gemm_rejects_bad_problems_before_any_device_call(pkg):
-    """qlora_gemm / qlora_gemm_solutions check op, sizes and leading dimensions on the host."""
-    import ctypes
+def test_gemm16_rejects_bad_problems_before_any_device_call(pkg):
+    """qlora_gemm16 checks mode, sizes, leading dimensions, tile/stage pairs and the epilogue's
+    operands on the host (hipErrorInvalidValue, nothing launched): null pointers stand in for
+    the buffers, which the checks never read."""
     lib = pkg._lib.load()
-    cnt = ctypes.c_int32(0)
-    for op, M, N, K, lda in ((2, 4, 4, 4, 4), (0, 0, 4, 4, 4), (0, 4, 4, -1, 4), (0, 4, 4, 8, 4)):
-        assert lib.qlora_gemm_solutions(op, M, N, K, 8, lda, 8, max(K, N), 8, N, None, 0,
-                                        ctypes.byref(cnt)) == 1
-        assert lib.qlora_gemm(op, M, N, K, 8, lda, 8, max(K, N), 8, N, 1.0, 0.0, 0, None) == 1
-        assert lib.qlora_gemmlt_solutions(op, M, N, K, lda, max(K, N), N, 0, 0, None, 0,
-                                          ctypes.byref(cnt)) == 1
-        assert lib.qlora_gemmlt(op, M, N, K, 8, lda, 8, max(K, N), 8, N, None, 1.0, 0.0, 0,
-                                None, 0, None) == 1
-    # a workspace size without a workspace, a negative workspace size
-    assert lib.qlora_gemmlt(0, 4, 4, 4, 8, 4, 8, 4, 8, 4, None, 1.0, 0.0, 0, None, 64, None) == 1
-    assert lib.qlora_gemmlt_solutions(0, 4, 4, 4, 4, 4, 4, 0, -1, None, 0,
-                                      ctypes.byref(cnt)) == 1
-    assert lib.qlora_error_string(100000 + 3) != lib.qlora_error_string(3)
-    assert lib.qlora_error_string(200000 + 3) != lib.qlora_error_string(100000 + 3)
+    P = 16  # a non-null, 16-byte aligned stand-in address: the checks fail before any access
+
+    def gemm(M=256, N=256, K=256, mode=0, ldc=256, epi=0, tile=256, stages=2, splits=1,
+             lda=256, ldb=256, bias=None, resid=None, ldr=0, gu=None, ldgu=0, swiglu_I=0):
+        return lib.qlora_gemm16(P, lda, P, ldb, M, N, K, mode, P, ldc, bias, resid, ldr, epi,
+                                swiglu_I, gu, ldgu, tile, stages, splits, None, 0, None)
+
+    assert gemm(mode=2) == 1                       # no such mode
+    assert gemm(K=192) == 1                        # reduction not in blocks of 128
+    assert gemm(mode=1, N=200, ldb=256) == 1       # NN: N not a multiple of the tile
+    assert gemm(N=12, ldb=256, ldc=16) == 1        # NT: N % 8
+    assert gemm(tile=256, stages=4) == 1           # four stages need 128 x 128 tiles
+    assert gemm(tile=64) == 1                      # no such tile
+    assert gemm(tile=0, splits=1) == 1             # the automatic plan takes tile 0 and splits 0
+    assert gemm(lda=200) == 1                      # lda < K
+    assert gemm(epi=1) == 1                        # bias epilogue without a bias
+    assert gemm(epi=2) == 1                        # residual epilogue without a residual
+    assert gemm(epi=5, N=128, swiglu_I=128) == 1   # SwiGLU keep without gu
+    assert gemm(epi=3, mode=1) == 1                # SwiGLU is NT only
+    assert gemm(epi=3, splits=2) == 1              # SwiGLU takes no split-K
+    assert gemm(splits=2) == 1                     # split-K without a workspace
+    assert gemm(epi=4) == 1                        # the partials form is internal
+    assert gemm(M=-1) == 1
+    assert gemm(M=0) == 0                          # no rows: nothing to do
 
 
-def test_gemm_splitk_rejects_bad_problems(pkg):
-    """qlora_gemm_splitk needs K divisible into 8-aligned slices, N % 4 == 0, a workspace."""
-    lib = pkg._lib.load()
-    # K % (8 splits) != 0; N % 4 != 0; splits < 2; workspace too small
-    for M, N, K, splits, work in ((4, 8, 100, 2, 1 << 20), (4, 6, 64, 2, 1 << 20),
-                                  (4, 8, 64, 1, 1 << 20), (4, 8, 64, 2, 10)):
-        assert lib.qlora_gemm_splitk(1, M, N, K, 16, K, 16, N, 16, N, None, splits, 16, work, 0,
-                                     None) == 1
-
-
-def test_hgemm_workspace_sizes(pkg):
-    """qlora_hgemm_workspace (host only): splits x M x N with split-K; with one slice the
-    K-sliced last round's partials when at most 64 tiles are left past the last full round of
-    256 (the largest slice count that fits that round with no empty slice), else 0."""
+def test_gemm16_workspace_sizes(pkg):
+    """qlora_gemm16_workspace (host only) at 256 x 256 tiles: splits x M x N with split-K; with
+    one slice the K-sliced last round's partials when at most 64 tiles are left past the last
+    full round of 256 (the largest slice count that fits that round with no empty slice), else
+    0."""
     import ctypes
     lib = pkg._lib.load()
 
     def ws(M, N, K, epi, splits):
         n = ctypes.c_int64(-1)
-        assert lib.qlora_hgemm_workspace(M, N, K, epi, splits, ctypes.byref(n)) == 0
+        assert lib.qlora_gemm16_workspace(M, N, K, 0, epi, 256, 2, splits, ctypes.byref(n)) == 0
         return n.value
 
     tile = 256 * 256
@@ -141,6 +142,7 @@ def test_hgemm_workspace_sizes(pkg):
     # SwiGLU, I = 8960 (70 tiles per 256 rows): 2,600 rows -> 770 tiles, 2 past 768; 24 k-tiles
     # of 64: 12 slices of 2 (16 slices would leave some empty)
     assert ws(2600, 8960, 1536, 3, 1) == 2 * 12 * tile
+    assert ws(2600, 8960, 1536, 5, 1) == 2 * 12 * tile  # the keep form: the same tail
     assert ws(2560, 8960, 1536, 3, 1) == 0  # 700 tiles: 188 past 512, more than a quarter
     assert ws(300, 8960, 1536, 3, 1) == 0   # 140 tiles: no full round
     # 2,048 columns (8 tiles per 256 rows), 33 row tiles -> 264 tiles, 8 past 256: 16 slices
@@ -148,8 +150,10 @@ def test_hgemm_workspace_sizes(pkg):
     assert ws(8348, 2048, 1536, 0, 1) == 8 * 12 * tile
     assert ws(8348, 2048, 16384, 0, 1) == 8 * 16 * tile  # 256 k-tiles: 16 slices of 16
     assert ws(0, 2048, 1536, 0, 1) == 0
-    assert lib.qlora_hgemm_workspace(4, 8, 128, 0, 0, ctypes.byref(ctypes.c_int64())) == 1
-    assert lib.qlora_hgemm_workspace(4, 8, 128, 0, 1, None) == 1
+    n = ctypes.c_int64()
+    assert lib.qlora_gemm16_workspace(4, 8, 128, 0, 0, 256, 2, 0, ctypes.byref(n)) == 1
+    assert lib.qlora_gemm16_workspace(4, 8, 128, 0, 0, 256, 2, 1, None) == 1
+    assert lib.qlora_gemm16_workspace(4, 8, 128, 0, 4, 256, 2, 1, ctypes.byref(n)) == 1
 
 
 def _uniform32(r):

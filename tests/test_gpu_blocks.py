@@ -49,7 +49,7 @@ def test_config3_attention_input_block(pkg):
     E = pkg.engine
     lengths = _lengths(128, 1024, 4, seed=3)
     print(f"config 3 block, lengths {lengths}", flush=True)
-    cfg = E.Qwen2Config(num_hidden_layers=1, vocab_size=1000)
+    cfg = E.Qwen2Config(num_hidden_layers=1, vocab_size=1024)
     model = E.random_qwen2(cfg, DEV, seed=3)
     spec = model.layers[0]
     H, HQ, HKV, D = cfg.hidden_size, cfg.num_attention_heads, cfg.num_key_value_heads, \

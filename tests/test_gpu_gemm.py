@@ -169,7 +169,7 @@ def test_every_split(pkg, splits, mode):
 @pytest.mark.parametrize("M", [2560, 1, 300])
 @pytest.mark.parametrize("mode", [0, 1])
 def test_fp16_b_gemm_equals_fused(pkg, M, mode):
-    """qlora_hgemm on the dequantized weight equals qlora_nf4_gemm on the NF4 weight bit for bit
+    """qlora_gemm16 on the dequantized weight equals qlora_nf4_gemm on the NF4 weight bit for bit
     (same B values, same summation order) at the step's widest shapes, and both match fp64."""
     L = pkg.linear
     gu_w = _group(pkg, [(8960, 1536), (8960, 1536)], 40)
@@ -230,7 +230,7 @@ def test_tile_major_order_equals_bnb_order(pkg, epi):
 
 @pytest.mark.parametrize("mode,epi", [(0, 0), (0, 1), (0, 2), (0, 3), (1, 0), (1, 2)])
 def test_fp16_b_gemm_tail_slices(pkg, mode, epi):
-    """One slice with a last round of at most 64 tiles: qlora_hgemm given its workspace runs those
+    """One slice with a last round of at most 64 tiles: qlora_gemm16 given its workspace runs those
     tiles as K slices (partials summed in slice order, then the epilogue). The tail tiles agree
     with fp64 to fp16 rounding, every other output is the same bits as without the workspace
     (all tiles whole), for every epilogue and both orientations."""
@@ -274,8 +274,8 @@ def test_fp16_b_gemm_tail_slices(pkg, mode, epi):
 
 
 @pytest.mark.parametrize("splits", [1, 2])
-def test_hgemm_timed_form(pkg, splits):
-    """qlora_hgemm_timed gives qlora_hgemm's output bit for bit and records its two events
+def test_gemm16_timed_form(pkg, splits):
+    """qlora_gemm16_timed gives qlora_gemm16's output bit for bit and records its two events
     around the kernels (the bench's per-launch timing of the package GEMM)."""
     L, lib = pkg.linear, pkg._lib
     g = torch.Generator(device=DEV).manual_seed(3 + splits)
@@ -288,8 +288,8 @@ def test_hgemm_timed_form(pkg, splits):
     start.record()  # creates the events on the device
     stop.record()
     stream = torch.cuda.current_stream().cuda_stream
-    lib.call("qlora_hgemm_timed", a.data_ptr(), 1536, b.data_ptr(), 1536, 700, 2048, 1536, 0,
-             got.data_ptr(), 2048, None, None, 0, 0, 0, splits,
+    lib.call("qlora_gemm16_timed", a.data_ptr(), 1536, b.data_ptr(), 1536, 700, 2048, 1536, 0,
+             got.data_ptr(), 2048, None, None, 0, 0, 0, None, 0, 256, 2, splits,
              None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(), stream,
              start.cuda_event, stop.cuda_event)
     torch.cuda.synchronize()

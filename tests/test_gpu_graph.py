@@ -17,7 +17,7 @@ DEV = "cuda"
 def _tiny(pkg, layers=2, dropout=0.05, H=256, HQ=4, HKV=2, D=64, r=16, I=640):
     cfg = pkg.engine.Qwen2Config(hidden_size=H, intermediate_size=I, num_hidden_layers=layers,
                                  num_attention_heads=HQ, num_key_value_heads=HKV, head_dim=D,
-                                 vocab_size=3000, lora_dropout=dropout, lora_r=r,
+                                 vocab_size=3072, lora_dropout=dropout, lora_r=r,
                                  lora_alpha=2 * r)
     return pkg.engine.random_qwen2(cfg, DEV, seed=3)
 

@@ -141,3 +141,17 @@ def test_device_counter_base_needs_padding():
     assert p.ctr_base is not None
     with pytest.raises(ValueError):
         _packed(ids, mask, labels, padded=True, ctr_base=torch.zeros(2, dtype=torch.int64))
+
+
+def test_gemm_shape_check():
+    """The step refuses a model whose products the package GEMM cannot tile (a reduction or
+    width off the multiples of 128) before any weight is built; every Qwen2 size passes."""
+    for kw in ({}, dict(hidden_size=896, intermediate_size=4864, num_attention_heads=14,
+                        num_key_value_heads=2, head_dim=64),
+               dict(hidden_size=3584, intermediate_size=18944, num_attention_heads=28,
+                    num_key_value_heads=4, vocab_size=152064)):
+        E.check_gemm_shapes(E.Qwen2Config(**kw))
+    for kw in (dict(vocab_size=151937), dict(vocab_size=3000), dict(intermediate_size=8900),
+               dict(hidden_size=1500)):
+        with pytest.raises(E.UnsupportedModel, match="multiples of 128"):
+            E.check_gemm_shapes(E.Qwen2Config(**kw))

@@ -194,7 +194,7 @@ def _fake_peft(r=16, HQ=12, HKV=2, D=128, H=1536):
                input_layernorm=NS(weight=None, variance_epsilon=1e-6),
                post_attention_layernorm=NS(weight=None, variance_epsilon=1e-6))
     config = NS(hidden_size=H, intermediate_size=4 * H, num_attention_heads=HQ,
-                num_key_value_heads=HKV, head_dim=D, vocab_size=1000, rope_theta=1e6)
+                num_key_value_heads=HKV, head_dim=D, vocab_size=1024, rope_theta=1e6)
     causal = NS(model=NS(layers=[layer]), config=config)
     return NS(get_base_model=lambda: causal)
 
