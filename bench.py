@@ -557,10 +557,11 @@ def main():
     ap.add_argument("--no-configs", action="store_true", help="skip the config 1-4 legs")
     ap.add_argument("--config1", action="store_true",
                     help="only the config-1 dequant measurement (and its copy calibration)")
+    ap.add_argument("--only", choices=("config1", "config2", "config3", "config4"),
+                    help="only this config leg (one JSON object; no step)")
     ap.add_argument("--profile", action="store_true",
-                    help="a run to profile: GEMM solutions timed only for the token counts of "
-                         "the batches it runs; no loss curve past the timed steps, no keep-all "
-                         "extra, no config legs, no CPU baseline")
+                    help="a run to profile: no loss curve past the timed steps, no keep-all or "
+                         "full-recompute extra, no config legs, no CPU baseline")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus}: this build measures one GPU only (the path is "
@@ -570,7 +571,11 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     if args.config1:
-        print(json.dumps({"config1": config1(pkg)}), flush=True)
+        args.only = "config1"
+    if args.only:
+        fn = {"config1": config1, "config2": config2, "config3": config3,
+              "config4": config4}[args.only]
+        print(json.dumps({args.only: fn(pkg)}), flush=True)
         return
     torch.manual_seed(0)
     torch.cuda.manual_seed(0)

@@ -42,6 +42,8 @@ SIGNATURES = {
                      I32, I32, I32, P, I64, P],
     "qlora_gemm16_timed": [P, I64, P, I64, I64, I64, I64, I32, P, I64, P, P, I64, I32, I64, P,
                            I64, I32, I32, I32, P, I64, P, P, P],
+    "qlora_gemm16_f32": [P, I64, P, I64, I64, I64, I64, I32, P, I64, F32, P, P, I64, I32, I32,
+                         I32, P, I64, P],
     "qlora_gemm16_workspace": [I64, I64, I64, I32, I32, I32, I32, I32, P],
     "qlora_gemm16_plan": [I64, I64, I64, I32, I32, P, P, P],
     "qlora_resid_add": [P, P, P, I64, P],

@@ -74,20 +74,25 @@ constexpr int kBM = 256, kBN = 256, kBK = 32, kStages = 4, kThreads = 256;
 constexpr int kTile = 256 * kBK;  // halves per operand stage (16 KB)
 
 enum { kEpiStore = 0, kEpiBias = 1, kEpiResid = 2, kEpiSwiglu = 3, kEpiPartial = 4,
-       kEpiSwigluKeep = 5 };
+       kEpiSwigluKeep = 5, kEpiF32 = 6 };
 
 // The SwiGLU forms: 3 writes m = fp16(silu(g) u) only, 5 also the fp16 [g | u] product (a
 // recomputing layer keeps it for its backward instead of multiplying again).
 constexpr bool swiglu_epi(int epi) { return epi == kEpiSwiglu || epi == kEpiSwigluKeep; }
 enum { kBHalf = 0, kBNF4 = 1 };
 
-// Epilogues that leave through LDS from transposed accumulators (every one but the split-K
-// partials): the fp16 product staged, then whole 16-byte row pieces (the residual form reads
-// and writes fp32 row pieces of the same columns).
-constexpr bool staged_epi(int epi) { return epi != kEpiPartial; }
+// Epilogues that leave through LDS from transposed accumulators (every one but the fp32 forms:
+// the split-K partials and kEpiF32): the fp16 product staged, then whole 16-byte row pieces (the
+// residual form reads and writes fp32 row pieces of the same columns).
+constexpr bool staged_epi(int epi) { return epi != kEpiPartial && epi != kEpiF32; }
+
+// kEpiF32: out fp32 = alpha acc + (resid ? (row_scale ? row_scale[m] : 1) resid[m, n] : 0),
+// unrounded (the accumulations of the LM head over vocabulary pieces). The K-sliced last round
+// is not used with it (its reduce applies the fp16 epilogues).
+constexpr bool tail_epi(int epi) { return epi != kEpiF32; }
 
 struct GemmArgs {
-  const uint16_t* a;     // A [M, Kr] fp16
+  const uint16_t* a;     // A [M, Kr] fp16 (transposed-A mode: stored [Kr, M], lda >= M)
   int64_t lda;
   const uint16_t* b;     // fp16 B: NT [N rows, Kr], NN [Kr rows, N]
   int64_t ldb;
@@ -116,6 +121,8 @@ struct GemmArgs {
   int bm, bn;            // output tile (fp16 B: 256 x 256 or 128 x 128)
   uint16_t* gu;          // kEpiSwigluKeep: fp16 [M, 2 I] product [g | u] (ld ldgu)
   int64_t ldgu;
+  float alpha;              // kEpiF32: scale of the product
+  const float* row_scale;   // kEpiF32: fp32 [M] scale of each resid row, or null (1)
 };
 
 // ---- swizzled LDS offsets (in halves) ---------------------------------------------------------
@@ -331,9 +338,9 @@ __device__ __forceinline__ void mfma_step(f32x16 (&acc)[FM][FN], const FragsT<FM
 // gate|up GEMM's time).
 // FM x FN MFMA blocks a k-step: MF = FM FN MFMAs, FM + FN fragment reads (NN: B's take two
 // transposed reads each); reads and loads dealt over the MFMAs as evenly as they go.
-template <bool NN, int VALU, int VMEM, int FM = 4, int FN = 4>
+template <bool NN, int VALU, int VMEM, int FM = 4, int FN = 4, bool TA = false>
 __device__ __forceinline__ void sched_step() {
-  constexpr int MF = FM * FN, reads = FM + (NN ? 2 : 1) * FN;
+  constexpr int MF = FM * FN, reads = (TA ? 2 : 1) * FM + (NN ? 2 : 1) * FN;
 #pragma unroll
   for (int i = 0; i < MF; ++i) {
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
@@ -518,6 +525,28 @@ __device__ __forceinline__ void store_tile(const GemmArgs& g, f32x16 (&acc)[BM /
         const int col = chunk * 8;
         const int64_t n = g_base + (col % (WC / 2)) + (col >= WC / 2 ? g.I : 0);
         if (m < g.M) *reinterpret_cast<uint4*>(g.gu + m * g.ldgu + n) = v;
+      }
+    }
+  } else if constexpr (EPI == kEpiF32) {
+    // fp32 out = alpha acc (+ row-scaled resid), from the registers: each store instruction
+    // writes 32 consecutive columns of two rows; each element's resid is read by the thread
+    // that writes it (out may be resid itself)
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t m = m0 + wm * WR + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+        if (m >= g.M) continue;
+        const float rs = g.resid == nullptr ? 0.0f : g.row_scale == nullptr ? 1.0f
+                                                                              : g.row_scale[m];
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          const int64_t n = tile_n * BN + wn * WC + j * 32 + col_in;
+          if (n >= g.N) continue;
+          float v = g.alpha * acc[i][j][r];
+          if (g.resid != nullptr) v += rs * g.resid[m * g.ldr + n];
+          static_cast<float*>(g.c)[m * g.ldc + n] = v;
+        }
       }
     }
   } else {
@@ -798,35 +827,46 @@ struct DmaNT {
   }
 };
 
+// One MFMA operand fragment (32 rows or columns x 16 k, lane l: index l % 32, k 8 (l / 32) ..
+// + 7) of k-step s from an N-contiguous stage [64][W] (nmaj_off_w): ds_read_b64_tr_b16, where lane
+// p of a 16-lane group reads row k + p / 4, columns c0 + 4 (p % 4) .. + 3, and lane i of the
+// group receives column c0 + i of rows k .. k+3; c: the fragment's first column in the stage.
+template <int W>
+__device__ __forceinline__ half8_t read_frag_tr(const uint16_t* st, int c, int s, int lane) {
+  const int p = lane & 15, fhalf = lane >> 5;
+  const int col = c + 16 * ((lane >> 4) & 1) + 4 * (p & 3);
+  const int k = 16 * s + 8 * fhalf + (p >> 2);
+  const int o0 = nmaj_off_w<W>(k, col >> 3) + (col & 7);
+  const int o1 = nmaj_off_w<W>(k + 4, col >> 3) + (col & 7);
+  const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)(st + o0));
+  const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)(st + o1));
+  return __builtin_bit_cast(half8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
 // The fragments of k-step s = 0..3 of a 64-wide stage: FM A blocks of 32 rows, FN B blocks of 32
-// columns (the wavefront's block: rows wm BM/2 .., columns wn BN/2 ..).
-template <bool NN, int BM, int BN>
+// columns (the wavefront's block: rows wm BM/2 .., columns wn BN/2 ..). TA: the A stage is
+// M-contiguous [64][BM] (A stored transposed), read as B is in NN.
+template <bool NN, int BM, int BN, bool TA = false>
 __device__ __forceinline__ void read_frags64(FragsT<BM / 64, BN / 64>& f, const uint16_t* sa,
                                              const uint16_t* sb, int s, int wm, int wn,
                                              int lane) {
   constexpr int FM = BM / 64, FN = BN / 64;
   const int frow = lane & 31, fhalf = lane >> 5;
 #pragma unroll
-  for (int i = 0; i < FM; ++i)
-    f.a[i] = *reinterpret_cast<const half8_t*>(
-        sa + kmaj64_off(wm * (BM / 2) + 32 * i + frow, 2 * s + fhalf));
+  for (int i = 0; i < FM; ++i) {
+    if constexpr (TA)
+      f.a[i] = read_frag_tr<BM>(sa, wm * (BM / 2) + 32 * i, s, lane);
+    else
+      f.a[i] = *reinterpret_cast<const half8_t*>(
+          sa + kmaj64_off(wm * (BM / 2) + 32 * i + frow, 2 * s + fhalf));
+  }
 #pragma unroll
   for (int j = 0; j < FN; ++j) {
-    if constexpr (!NN) {
+    if constexpr (!NN)
       f.b[j] = *reinterpret_cast<const half8_t*>(
           sb + kmaj64_off(wn * (BN / 2) + 32 * j + frow, 2 * s + fhalf));
-    } else {
-      // ds_read_b64_tr_b16: lane p of a 16-lane group reads row k + p / 4, columns
-      // c0 + 4 (p % 4) .. + 3; lane i of the group receives column c0 + i of rows k .. k+3
-      const int p = lane & 15;
-      const int col = wn * (BN / 2) + 32 * j + 16 * ((lane >> 4) & 1) + 4 * (p & 3);
-      const int k = 16 * s + 8 * fhalf + (p >> 2);
-      const int o0 = nmaj_off_w<BN>(k, col >> 3) + (col & 7);
-      const int o1 = nmaj_off_w<BN>(k + 4, col >> 3) + (col & 7);
-      const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)(sb + o0));
-      const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)(sb + o1));
-      f.b[j] = __builtin_bit_cast(half8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-    }
+    else
+      f.b[j] = read_frag_tr<BN>(sb, wn * (BN / 2) + 32 * j, s, lane);
   }
 }
 
@@ -868,7 +908,7 @@ __device__ __forceinline__ void store_tail_part(float* p, const f32x16 (&acc)[BM
 // through the LDS stages sA0/sA1/sB0/sB1. The tail form is a
 // separate instantiation so that the main tiles' register allocation stays that of the plain
 // epilogue.
-template <bool NN, int EPI, bool TAIL, int BM, int BN, int STAGES>
+template <bool NN, bool TA, int EPI, bool TAIL, int BM, int BN, int STAGES>
 __device__ __forceinline__ void hgemm_tile(const GemmArgs& g, int64_t tile_m, int64_t tile_n,
                                            int64_t kt0, int64_t kt1, int tail_u, uint16_t* sA0,
                                            uint16_t* sA1, uint16_t* sB0, uint16_t* sB1,
@@ -890,9 +930,19 @@ __device__ __forceinline__ void hgemm_tile(const GemmArgs& g, int64_t tile_m, in
   const int64_t kt_last = kt1 - 1;
 
   DmaKT<BM> dma_a;
-  const int64_t a_rows = g.M - m0;  // rows past M re-read the last row
-  dma_a.init(g.lda, [&](int r) -> int64_t { return r < a_rows ? r : a_rows - 1; }, wave, lane);
-  const uint16_t* a_base = g.a + m0 * g.lda;  // + k0 per k-tile
+  DmaNT<BM> dma_at;  // TA: A stored [K, M], the tile's BM columns of 64 rows a k-tile
+  const uint16_t* a_base;
+  int64_t a_step;
+  if constexpr (TA) {
+    dma_at.init(g.lda, wave, lane);  // M % BM == 0 (host check): whole tiles only
+    a_base = g.a + m0;
+    a_step = (int64_t)kBK64 * g.lda;
+  } else {
+    const int64_t a_rows = g.M - m0;  // rows past M re-read the last row
+    dma_a.init(g.lda, [&](int r) -> int64_t { return r < a_rows ? r : a_rows - 1; }, wave, lane);
+    a_base = g.a + m0 * g.lda;
+    a_step = kBK64;
+  }
   DmaKT<BN> dma_bk;
   DmaNT<BN> dma_bn;
   const uint16_t* b_base;
@@ -923,8 +973,10 @@ __device__ __forceinline__ void hgemm_tile(const GemmArgs& g, int64_t tile_m, in
     kt = kt < kt1 ? kt : kt_last;
 #pragma unroll
     for (int q = q0; q < q1; ++q) {
-      if ((q & 1) == 0) dma_a.issue(a_base + kt * kBK64, sa, wave, q >> 1);
-      else if constexpr (NN) dma_bn.issue(b_base + kt * b_step, sb, wave, q >> 1);
+      if ((q & 1) == 0) {
+        if constexpr (TA) dma_at.issue(a_base + kt * a_step, sa, wave, q >> 1);
+        else dma_a.issue(a_base + kt * a_step, sa, wave, q >> 1);
+      } else if constexpr (NN) dma_bn.issue(b_base + kt * b_step, sb, wave, q >> 1);
       else dma_bk.issue(b_base + kt * b_step, sb, wave, q >> 1);
     }
   };
@@ -935,7 +987,7 @@ __device__ __forceinline__ void hgemm_tile(const GemmArgs& g, int64_t tile_m, in
     issue_part(kt0, sA0, sB0, 0, kQ);
     issue_part(kt0 + 1, sA1, sB1, 0, kSA);
     sync_tile<kSA>();  // k-tile kt0 landed
-    read_frags64<NN, BM, BN>(f0, sA0, sB0, 0, wm, wn, lane);
+    read_frags64<NN, BM, BN, TA>(f0, sA0, sB0, 0, wm, wn, lane);
     // k-tile t on stage t % 2, its four k-steps each reading the next one's fragments while its
     // MFMAs run. k-steps 0 and 1 finish the DMA of t + 1 into the other stage. After k-step 2
     // every wavefront has read this stage and t + 1 has landed (the barrier): k-step 3 reads
@@ -943,24 +995,24 @@ __device__ __forceinline__ void hgemm_tile(const GemmArgs& g, int64_t tile_m, in
     auto k_tile = [&](int64_t t, uint16_t* sa, uint16_t* sb, uint16_t* sa_n, uint16_t* sb_n) {
       __builtin_amdgcn_sched_barrier(0);
       issue_part(t + 1, sa_n, sb_n, kSA, kSA + kSB);
-      read_frags64<NN, BM, BN>(f1, sa, sb, 1, wm, wn, lane);
+      read_frags64<NN, BM, BN, TA>(f1, sa, sb, 1, wm, wn, lane);
       mfma_step<kT>(acc, f0);
-      sched_step<NN, 0, kSB, FM, FN>();
+      sched_step<NN, 0, kSB, FM, FN, TA>();
       __builtin_amdgcn_sched_barrier(0);
       issue_part(t + 1, sa_n, sb_n, kSA + kSB, kQ);
-      read_frags64<NN, BM, BN>(f0, sa, sb, 2, wm, wn, lane);
+      read_frags64<NN, BM, BN, TA>(f0, sa, sb, 2, wm, wn, lane);
       mfma_step<kT>(acc, f1);
-      sched_step<NN, 0, kQ - kSA - kSB, FM, FN>();
+      sched_step<NN, 0, kQ - kSA - kSB, FM, FN, TA>();
       __builtin_amdgcn_sched_barrier(0);
-      read_frags64<NN, BM, BN>(f1, sa, sb, 3, wm, wn, lane);
+      read_frags64<NN, BM, BN, TA>(f1, sa, sb, 3, wm, wn, lane);
       mfma_step<kT>(acc, f0);
-      sched_step<NN, 0, 0, FM, FN>();
+      sched_step<NN, 0, 0, FM, FN, TA>();
       __builtin_amdgcn_sched_barrier(0);
       sync_tile<0>();
       issue_part(t + 2, sa, sb, 0, kSA);
-      read_frags64<NN, BM, BN>(f0, sa_n, sb_n, 0, wm, wn, lane);
+      read_frags64<NN, BM, BN, TA>(f0, sa_n, sb_n, 0, wm, wn, lane);
       mfma_step<kT>(acc, f1);
-      sched_step<NN, 0, kSA, FM, FN>();
+      sched_step<NN, 0, kSA, FM, FN, TA>();
       __builtin_amdgcn_sched_barrier(0);
     };
     for (int64_t t = kt0; t < kt1; t += 2) {
@@ -977,29 +1029,29 @@ __device__ __forceinline__ void hgemm_tile(const GemmArgs& g, int64_t tile_m, in
     issue_part(kt0 + 1, sA1, sB1, 0, kQ);
     issue_part(kt0 + 2, sA2, sB2, 0, kQ);
     sync_tile<2 * kQ>();  // k-tile kt0 landed
-    read_frags64<NN, BM, BN>(f0, sA0, sB0, 0, wm, wn, lane);
+    read_frags64<NN, BM, BN, TA>(f0, sA0, sB0, 0, wm, wn, lane);
     auto k_tile = [&](int64_t t, uint16_t* sa, uint16_t* sb, uint16_t* sa_n, uint16_t* sb_n,
                       uint16_t* sa_p, uint16_t* sb_p) {
       __builtin_amdgcn_sched_barrier(0);
       issue_part(t + 3, sa_p, sb_p, 0, q1);
-      read_frags64<NN, BM, BN>(f1, sa, sb, 1, wm, wn, lane);
+      read_frags64<NN, BM, BN, TA>(f1, sa, sb, 1, wm, wn, lane);
       mfma_step<kT>(acc, f0);
-      sched_step<NN, 0, q1, FM, FN>();
+      sched_step<NN, 0, q1, FM, FN, TA>();
       __builtin_amdgcn_sched_barrier(0);
       issue_part(t + 3, sa_p, sb_p, q1, q2);
-      read_frags64<NN, BM, BN>(f0, sa, sb, 2, wm, wn, lane);
+      read_frags64<NN, BM, BN, TA>(f0, sa, sb, 2, wm, wn, lane);
       mfma_step<kT>(acc, f1);
-      sched_step<NN, 0, q2 - q1, FM, FN>();
+      sched_step<NN, 0, q2 - q1, FM, FN, TA>();
       __builtin_amdgcn_sched_barrier(0);
       issue_part(t + 3, sa_p, sb_p, q2, kQ);
-      read_frags64<NN, BM, BN>(f1, sa, sb, 3, wm, wn, lane);
+      read_frags64<NN, BM, BN, TA>(f1, sa, sb, 3, wm, wn, lane);
       mfma_step<kT>(acc, f0);
-      sched_step<NN, 0, kQ - q2, FM, FN>();
+      sched_step<NN, 0, kQ - q2, FM, FN, TA>();
       __builtin_amdgcn_sched_barrier(0);
       sync_tile<2 * kQ>();  // t + 1 landed; t + 2, t + 3 may be in flight
-      read_frags64<NN, BM, BN>(f0, sa_n, sb_n, 0, wm, wn, lane);
+      read_frags64<NN, BM, BN, TA>(f0, sa_n, sb_n, 0, wm, wn, lane);
       mfma_step<kT>(acc, f1);
-      sched_step<NN, 0, 0, FM, FN>();
+      sched_step<NN, 0, 0, FM, FN, TA>();
       __builtin_amdgcn_sched_barrier(0);
     };
     for (int64_t t = kt0; t < kt1; t += 4) {
@@ -1023,7 +1075,7 @@ __device__ __forceinline__ void hgemm_tile(const GemmArgs& g, int64_t tile_m, in
 
 // STAGES: 2 (either tile; 128 x 128 tiles then leave room for a second workgroup per CU) or 4
 // (128 x 128 only, 128 KB: one workgroup per CU, loads issued three k-tiles ahead).
-template <bool NN, int EPI, int BM, int STAGES>
+template <bool NN, int EPI, int BM, int STAGES, bool TA = false>
 __global__ __launch_bounds__(kThreads, (BM == 128 && STAGES == 2) ? 2 : 1) void hgemm_kernel(
     GemmArgs g) {
   constexpr int kX = STAGES == 4 ? BM * kBK64 : 8;  // stages 2-3 (unused with two stages)
@@ -1041,7 +1093,7 @@ __global__ __launch_bounds__(kThreads, (BM == 128 && STAGES == 2) ? 2 : 1) void 
     const int t = g.main_tiles + tail_u / g.tail_splits;
     const int64_t kt0 =
         (int64_t)__builtin_amdgcn_readfirstlane(tail_u % g.tail_splits) * g.kt_per_tail;
-    hgemm_tile<NN, EPI, true, BM, BM, STAGES>(
+    hgemm_tile<NN, TA, EPI, true, BM, BM, STAGES>(
         g, __builtin_amdgcn_readfirstlane(t % g.m_tiles),
         __builtin_amdgcn_readfirstlane(t / g.m_tiles), kt0, kt0 + g.kt_per_tail, tail_u, sA0,
         sA1, sB0, sB1, sA2, sA3, sB2, sB3);
@@ -1052,8 +1104,8 @@ __global__ __launch_bounds__(kThreads, (BM == 128 && STAGES == 2) ? 2 : 1) void 
   tile_of(g.m_tiles, g.tiles, g.tail_splits > 0 ? g.main_tiles : (int)gridDim.x, tile_m, tile_n,
           slice);
   const int64_t kt0 = (int64_t)slice * g.kt_per_split;
-  hgemm_tile<NN, EPI, false, BM, BM, STAGES>(g, tile_m, tile_n, kt0, kt0 + g.kt_per_split, slice,
-                                             sA0, sA1, sB0, sB1, sA2, sA3, sB2, sB3);
+  hgemm_tile<NN, TA, EPI, false, BM, BM, STAGES>(g, tile_m, tile_n, kt0, kt0 + g.kt_per_split,
+                                                 slice, sA0, sA1, sB0, sB1, sA2, sA3, sB2, sB3);
 }
 
 // Tail split: the slices of each tail tile summed in slice order, then the epilogue (fp16 store,
@@ -1126,12 +1178,15 @@ __global__ __launch_bounds__(256) void tail_reduce_kernel(GemmArgs g, int epi, i
       make_uint2(pack2h(v[0], v[1]), pack2h(v[2], v[3]));
 }
 
-// Sum of the split-K partials [splits, M, N] and the epilogue (store / bias / residual).
+// Sum of the split-K partials [splits, M, N] and the epilogue (store / bias / residual / fp32
+// with alpha and a row-scaled residual).
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* ws, int splits,
                                                             int64_t M, int64_t N, int epi,
                                                             void* c, int64_t ldc,
                                                             const uint16_t* bias,
-                                                            const float* resid, int64_t ldr) {
+                                                            const float* resid, int64_t ldr,
+                                                            float alpha,
+                                                            const float* row_scale) {
   const int64_t idx = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
   if (idx >= M * N) return;
   const int64_t m = idx / N, n = idx - m * N;  // N % 4 == 0: four columns of one row
@@ -1141,7 +1196,16 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* ws, int
     s.x += t.x; s.y += t.y; s.z += t.z; s.w += t.w;
   }
   float v[4] = {s.x, s.y, s.z, s.w};
-  if (epi == kEpiResid) {
+  if (epi == kEpiF32) {  // as store_tile's kEpiF32 (out may be resid)
+    float* out = static_cast<float*>(c) + m * ldc + n;
+    const float rs = resid == nullptr ? 0.0f : row_scale == nullptr ? 1.0f : row_scale[m];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float o = alpha * v[i];
+      if (resid != nullptr) o += rs * resid[m * ldr + n + i];
+      out[i] = o;
+    }
+  } else if (epi == kEpiResid) {
     float* out = static_cast<float*>(c) + m * ldc + n;
     const float* r = resid + m * ldr + n;
 #pragma unroll
@@ -1164,11 +1228,11 @@ namespace {
 
 // kernel selector: BSRC kBNF4 -> nf4_gemm_kernel, kBHalf -> hgemm_kernel. start/stop (may be
 // null): events the dispatch records at the kernel's own start and end (hipExtLaunchKernelGGL)
-template <int BSRC, bool NN, int EPI, int BM, int ST>
+template <int BSRC, bool NN, int EPI, int BM, int ST, bool TA = false>
 void launch_one(const GemmArgs& g, dim3 grid, hipStream_t s, hipEvent_t start, hipEvent_t stop) {
   auto kernel = [] {
     if constexpr (BSRC == kBNF4) return nf4_gemm_kernel<NN, EPI>;
-    else return hgemm_kernel<NN, EPI, BM, ST>;
+    else return hgemm_kernel<NN, EPI, BM, ST, TA>;
   }();
   if (start != nullptr || stop != nullptr)
     hipExtLaunchKernelGGL(kernel, grid, dim3(kThreads), 0, s, start, stop, 0, g);
@@ -1184,6 +1248,9 @@ void launch_epi(const GemmArgs& g, dim3 grid, hipStream_t s, int epi, hipEvent_t
     case kEpiBias: launch_one<BSRC, NN, kEpiBias, BM, ST>(g, grid, s, start, stop); break;
     case kEpiResid: launch_one<BSRC, NN, kEpiResid, BM, ST>(g, grid, s, start, stop); break;
     case kEpiPartial: launch_one<BSRC, NN, kEpiPartial, BM, ST>(g, grid, s, start, stop); break;
+    case kEpiF32:
+      if constexpr (NN && BSRC == kBHalf) launch_one<BSRC, NN, kEpiF32, BM, ST>(g, grid, s, start, stop);
+      break;
     default:
       if constexpr (!NN) {
         if (epi == kEpiSwigluKeep) launch_one<BSRC, NN, kEpiSwigluKeep, BM, ST>(g, grid, s, start, stop);
@@ -1193,9 +1260,23 @@ void launch_epi(const GemmArgs& g, dim3 grid, hipStream_t s, int epi, hipEvent_t
   }
 }
 
-// The kernel for (B source, mode, tile, stages) with the epilogue epi.
+// Transposed A (B as in NN): the fp32 epilogue and its split-K partials only.
+template <int BM, int ST>
+void launch_ta(const GemmArgs& g, dim3 grid, hipStream_t s, int epi, hipEvent_t start,
+               hipEvent_t stop) {
+  if (epi == kEpiF32) launch_one<kBHalf, true, kEpiF32, BM, ST, true>(g, grid, s, start, stop);
+  else launch_one<kBHalf, true, kEpiPartial, BM, ST, true>(g, grid, s, start, stop);
+}
+
+// The kernel for (B source, mode, tile, stages) with the epilogue epi (mode 2: transposed A).
 void launch_any(const GemmArgs& g, int bsrc, int mode, int tile, int stages, dim3 grid,
                 hipStream_t s, int epi, hipEvent_t start, hipEvent_t stop) {
+  if (mode == 2) {
+    if (tile == 128 && stages == 4) launch_ta<128, 4>(g, grid, s, epi, start, stop);
+    else if (tile == 128) launch_ta<128, 2>(g, grid, s, epi, start, stop);
+    else launch_ta<256, 2>(g, grid, s, epi, start, stop);
+    return;
+  }
   if (bsrc == kBNF4) {
     if (mode == 0) launch_epi<false, kBNF4, 256, 2>(g, grid, s, epi, start, stop);
     else launch_epi<true, kBNF4, 256, 2>(g, grid, s, epi, start, stop);
@@ -1266,7 +1347,8 @@ double plan_cost(int64_t M, int64_t N, int64_t K, int mode, int epi, const PlanC
                  int splits) {
   const int tile = v.tile, stages = v.stages;
   const int64_t kt = K / kBK64;
-  if (kt % stages != 0 || (mode == 1 && N % tile != 0)) return -1.0;
+  if (kt % stages != 0 || (mode != 0 && N % tile != 0) || (mode == 2 && M % tile != 0))
+    return -1.0;
   if (swiglu_epi(epi) && (splits > 1 || N % (tile / 2) != 0)) return -1.0;
   const int64_t per = qlora_cdiv(qlora_cdiv(kt, splits), stages) * stages;
   if (per * (splits - 1) >= kt) return -1.0;  // an empty slice
@@ -1282,7 +1364,8 @@ double plan_cost(int64_t M, int64_t N, int64_t K, int mode, int epi, const PlanC
   if (r > 0) {
     int main_t, ts, ktp;
     rounds += 1.0;
-    if (tail_plan(m_tiles, tiles / m_tiles, kt, tile, stages, &main_t, &ts, &ktp) > 0) {
+    if (tail_epi(epi) &&
+        tail_plan(m_tiles, tiles / m_tiles, kt, tile, stages, &main_t, &ts, &ktp) > 0) {
       kwalk += (double)ktp * kBK64;
       part = 8.0 * (double)(r * ts) * tile * tile / 1e6;
       red = 1.0;
@@ -1333,7 +1416,8 @@ int run_gemm(GemmArgs& g, int bsrc, int mode, int epi, int splits, float* ws, in
   QLORA_CHECK_ARG(grid < (1ll << 31));
   g.tiles = (int)grid;
   // fp16 outputs leave in 16-byte row pieces
-  QLORA_CHECK_ARG(epi == kEpiResid || splits > 1 || (g.ldc % 8 == 0 && al(g.c, 16)));
+  QLORA_CHECK_ARG(epi == kEpiResid || epi == kEpiF32 || splits > 1 ||
+                  (g.ldc % 8 == 0 && al(g.c, 16)));
   // the fp32 residual form reads and writes 32-byte row pieces
   QLORA_CHECK_ARG(epi != kEpiResid || splits > 1 ||
                   (g.ldc % 4 == 0 && g.ldr % 4 == 0 && al(g.c, 16) && al(g.resid, 16)));
@@ -1347,7 +1431,7 @@ int run_gemm(GemmArgs& g, int bsrc, int mode, int epi, int splits, float* ws, in
   QLORA_CHECK_ARG((int64_t)g.kt_per_split * (splits - 1) < ktiles);  // no empty slice
   int main_t = 0, tail_s = 0, kt_tail = 0;
   const int64_t tail_need =
-      bsrc == kBHalf && splits == 1 && ws != nullptr
+      bsrc == kBHalf && splits == 1 && ws != nullptr && tail_epi(epi)
           ? tail_plan(g.m_tiles, n_tiles, ktiles, tile, stages, &main_t, &tail_s, &kt_tail)
           : 0;
   if (tail_need > 0 && ws_elems >= tail_need && al(ws, 16)) {
@@ -1381,10 +1465,11 @@ int run_gemm(GemmArgs& g, int bsrc, int mode, int epi, int splits, float* ws, in
   const dim3 rgrid((unsigned)qlora_cdiv(quads, 256));
   if (stop != nullptr)
     hipExtLaunchKernelGGL(splitk_reduce_kernel, rgrid, dim3(256), 0, s, nullptr, stop, 0, ws,
-                          splits, g.M, g.N, epi, out, g.ldc, g.bias, g.resid, g.ldr);
+                          splits, g.M, g.N, epi, out, g.ldc, g.bias, g.resid, g.ldr, g.alpha,
+                          g.row_scale);
   else
     hipLaunchKernelGGL(splitk_reduce_kernel, rgrid, dim3(256), 0, s, ws, splits, g.M, g.N, epi,
-                       out, g.ldc, g.bias, g.resid, g.ldr);
+                       out, g.ldc, g.bias, g.resid, g.ldr, g.alpha, g.row_scale);
   return qlora_launch_status();
 }
 
@@ -1496,6 +1581,8 @@ QLORA_API int qlora_gemm16_timed(const void* a, int64_t lda, const void* b, int6
   if (tile == 0) auto_plan(M, N, K, mode, epi, &tile, &stages, &splits);
   QLORA_CHECK_ARG((tile == 256 && stages == 2) || (tile == 128 && (stages == 2 || stages == 4)));
   QLORA_CHECK_ARG(splits >= 1 && splits <= 16 && !(splits > 1 && swiglu_epi(epi)));
+  // the split-K reduce writes four columns a thread
+  QLORA_CHECK_ARG(splits == 1 || (N % 4 == 0 && ldc % 4 == 0 && (epi != 2 || ldr % 4 == 0)));
   QLORA_CHECK_ARG(epi != 1 || bias);
   QLORA_CHECK_ARG(epi != 2 || (resid && ldr >= N));
   // the kept product [g | u]: [M, 2 N] fp16, 16-byte rows
@@ -1540,14 +1627,55 @@ QLORA_API int qlora_gemm16(const void* a, int64_t lda, const void* b, int64_t ld
                             nullptr, nullptr);
 }
 
-// fp32 workspace elements of a qlora_gemm16 problem: the split-K partials, or with one slice the
-// tail split's (0 when the last round needs none).
+// The fp32-output GEMM: c = alpha A op(B) (+ row-scaled resid), mode 1 A [M, K] x B [K, N],
+// mode 2 A^T: A stored [K, M] (lda >= M), B [K, N].
+QLORA_API int qlora_gemm16_f32(const void* a, int64_t lda, const void* b, int64_t ldb,
+                               int64_t M, int64_t N, int64_t K, int32_t mode, float* c,
+                               int64_t ldc, float alpha, const float* row_scale,
+                               const float* resid, int64_t ldr, int32_t tile, int32_t stages,
+                               int32_t splits, float* ws, int64_t ws_elems, void* stream) {
+  QLORA_CHECK_ARG(M >= 0 && N > 0 && K > 0);
+  if (M == 0) return 0;
+  QLORA_CHECK_ARG(a && b && c && (mode == 1 || mode == 2) && (tile == 0) == (splits == 0));
+  QLORA_CHECK_ARG(row_scale == nullptr || resid != nullptr);
+  if (tile == 0) auto_plan(M, N, K, mode, kEpiF32, &tile, &stages, &splits);
+  QLORA_CHECK_ARG((tile == 256 && stages == 2) || (tile == 128 && (stages == 2 || stages == 4)));
+  QLORA_CHECK_ARG(splits >= 1 && splits <= 16);
+  QLORA_CHECK_ARG(K % (kStages * kBK) == 0 && (K / kBK64) % stages == 0 && N % tile == 0);
+  QLORA_CHECK_ARG(mode == 1 ? lda >= K : (lda >= M && M % tile == 0));
+  QLORA_CHECK_ARG(lda % 8 == 0 && al(a, 16) && al(b, 16) && ldb % 8 == 0 && ldb >= N);
+  QLORA_CHECK_ARG(ldc >= N && (resid == nullptr || ldr >= N));
+  QLORA_CHECK_ARG(splits == 1 || ldc % 4 == 0);
+  // 32-bit DMA byte offsets within a tile: A's rows (mode 1) or 64 k-rows (mode 2), B's k-rows
+  QLORA_CHECK_ARG((int64_t)(mode == 1 ? tile : 64) * lda * 2 < (1ll << 32) &&
+                  64 * ldb * 2 < (1ll << 32));
+  GemmArgs g{};
+  g.a = static_cast<const uint16_t*>(a);
+  g.lda = lda;
+  g.b = static_cast<const uint16_t*>(b);
+  g.ldb = ldb;
+  g.c = c;
+  g.ldc = ldc;
+  g.resid = resid;
+  g.ldr = ldr;
+  g.M = M;
+  g.N = N;
+  g.Kr = K;
+  g.alpha = alpha;
+  g.row_scale = row_scale;
+  return run_gemm(g, kBHalf, mode, kEpiF32, splits, ws, ws_elems, (hipStream_t)stream, nullptr,
+                  nullptr, tile, stages);
+}
+
+// fp32 workspace elements of a qlora_gemm16 / qlora_gemm16_f32 (epi 6) problem: the split-K
+// partials, or with one slice the tail split's (0 when the last round needs none).
 QLORA_API int qlora_gemm16_workspace(int64_t M, int64_t N, int64_t K, int32_t mode, int32_t epi,
                                      int32_t tile, int32_t stages, int32_t splits,
                                      int64_t* elems) {
-  QLORA_CHECK_ARG(elems && M >= 0 && N > 0 && K > 0 && splits >= 0 && epi >= 0 && epi <= 5 &&
+  QLORA_CHECK_ARG(elems && M >= 0 && N > 0 && K > 0 && splits >= 0 && epi >= 0 && epi <= 6 &&
                   epi != kEpiPartial);
-  QLORA_CHECK_ARG((tile == 0) == (splits == 0) && (mode == 0 || mode == 1));
+  QLORA_CHECK_ARG((tile == 0) == (splits == 0) && mode >= 0 && mode <= 2);
+  QLORA_CHECK_ARG((mode == 2) <= (epi == kEpiF32) && (epi == kEpiF32) <= (mode != 0));
   *elems = 0;
   if (M == 0) return 0;
   if (tile == 0) auto_plan(M, N, K, mode, epi, &tile, &stages, &splits);
@@ -1556,7 +1684,7 @@ QLORA_API int qlora_gemm16_workspace(int64_t M, int64_t N, int64_t K, int32_t mo
     *elems = (int64_t)splits * M * N;
     return 0;
   }
-  if (M == 0 || K % (kStages * kBK) != 0) return 0;
+  if (M == 0 || K % (kStages * kBK) != 0 || !tail_epi(epi)) return 0;
   int main_t, tail_s, kt_tail;
   *elems = tail_plan(qlora_cdiv(M, tile), n_tiles_of(N, epi, tile), K / kBK64, tile, stages,
                      &main_t, &tail_s, &kt_tail);
@@ -1567,7 +1695,8 @@ QLORA_API int qlora_gemm16_workspace(int64_t M, int64_t N, int64_t K, int32_t mo
 QLORA_API int qlora_gemm16_plan(int64_t M, int64_t N, int64_t K, int32_t mode, int32_t epi,
                                 int32_t* tile, int32_t* stages, int32_t* splits) {
   QLORA_CHECK_ARG(tile && stages && splits && M >= 0 && N > 0 && K > 0);
-  QLORA_CHECK_ARG((mode == 0 || mode == 1) && epi >= 0 && epi <= 5 && epi != kEpiPartial);
+  QLORA_CHECK_ARG(mode >= 0 && mode <= 2 && epi >= 0 && epi <= 6 && epi != kEpiPartial);
+  QLORA_CHECK_ARG((mode == 2) <= (epi == kEpiF32) && (epi == kEpiF32) <= (mode != 0));
   int t, st, sp;
   auto_plan(M, N, K, mode, epi, &t, &st, &sp);
   *tile = t;

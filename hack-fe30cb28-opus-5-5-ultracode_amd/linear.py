@@ -240,6 +240,55 @@ def hgemm(a, b, mode, epi=0, bias=None, resid=None, out=None, swiglu_I=0, splits
     return out
 
 
+def gemm_f32(a, b, mode, alpha=1.0, row_scale=None, resid=None, out=None, tile=0, stages=2,
+             splits=None):
+    """The MFMA GEMM with an unrounded fp32 output (qlora_gemm16_f32): out = alpha A op(B)
+    (+ row_scale[:, None] * resid). mode 1: A [M, K] x B [K, N]; mode 2: A^T B with A given as
+    [K, M] (its columns are the output rows). resid may be out itself (then updated in place).
+    tile 0: the automatic plan; else tile 256 or 128 with `stages` and `splits` (default 1)."""
+    dev = a.device
+    _need(a, "a", torch.float16, dev, contiguous=False)
+    _need(b, "b", torch.float16, dev, contiguous=False)
+    if a.dim() != 2 or b.dim() != 2 or a.stride(1) != 1 or b.stride(1) != 1:
+        raise ValueError("a and b must be 2-D with unit column stride")
+    if mode == 1:
+        M, K = a.shape
+    elif mode == 2:
+        K, M = a.shape
+    else:
+        raise ValueError("mode must be 1 (A B) or 2 (A^T B)")
+    kb, N = b.shape
+    if kb != K:
+        raise ValueError(f"inner dimensions differ: {K} vs {kb}")
+    if out is None:
+        out = torch.empty((M, N), device=dev, dtype=torch.float32)
+    _need(out, "out", torch.float32, dev, contiguous=False)
+    if out.shape != (M, N) or out.stride(1) != 1:
+        raise ValueError("out must be [M, N] fp32 with unit column stride")
+    ldr = 0
+    if resid is not None:
+        _need(resid, "resid", torch.float32, dev, contiguous=False)
+        if resid.shape != (M, N) or resid.stride(1) != 1:
+            raise ValueError("resid must match the output")
+        ldr = resid.stride(0)
+    if row_scale is not None:
+        _need(row_scale, "row_scale", torch.float32, dev)
+        if resid is None or row_scale.numel() != M:
+            raise ValueError("row_scale needs resid and one entry per output row")
+    if M == 0:
+        return out
+    if tile == 0:
+        splits = 0
+    elif splits is None:
+        splits = 1
+    n_ws = hgemm_workspace(M, N, K, 6, splits, tile, stages, mode) if splits != 1 else 0
+    ws = torch.empty((n_ws,), device=dev, dtype=torch.float32) if n_ws else None
+    _lib.call("qlora_gemm16_f32", _ptr(a), a.stride(0), _ptr(b), b.stride(0), M, N, K, mode,
+              _ptr(out), out.stride(0), float(alpha), _ptr(row_scale), _ptr(resid), ldr, tile,
+              stages, splits, _ptr(ws), 0 if ws is None else ws.numel(), _stream(dev))
+    return out
+
+
 def tiles(K, N, mode):
     """Whether qlora_gemm16 takes a product with reduction K and N output columns: K in blocks
     of 128, N a multiple of 8 (NT) or of 128 (NN). Every Qwen2 size does (H, I, the q/k/v

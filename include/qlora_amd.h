@@ -326,18 +326,37 @@ int qlora_gemm16_timed(const void* a, int64_t lda, const void* b, int64_t ldb, i
                        void* stop);
 
 /*
- * fp32 workspace elements (*elems) qlora_gemm16 uses for this problem, mode, tile and stage
- * count: splits * M * N with splits > 1; with one slice the K-sliced last round's partials, 0
- * when that does not apply (tile 0 / splits 0: the automatic plan's). N as qlora_gemm16's
- * (epi 3, 5: I). No reference counterpart (sizes the caller's workspace).
+ * The package GEMM with an unrounded fp32 output (the LM head over vocabulary pieces):
+ *   c[M, N] (f32, ldc) = alpha A op(B) + (resid ? rs[m] resid[m, n] : 0),
+ *   rs = row_scale (f32 [M]) or 1 when null; resid (f32, ldr) may be c itself;
+ *   mode 1: A [M, K] (lda >= K), B [K, N];  mode 2: A^T, A stored [K, M] (lda >= M), B [K, N].
+ * tile, stages, splits, ws as qlora_gemm16 (no K-sliced last round: ws is for split-K only;
+ * tile 0 / splits 0: the plan of qlora_gemm16_plan with epi 6).
+ * Replaces the fp32 products of the reference's streamed head, acc = acc * alpha + P E_piece
+ * (engine.py:1498-1547), the whole-row head's dh = G E, and the embedding gradient dE = G^T h
+ * (the BASELINE config-4 extra: the reference freezes the embedding).
+ * Requires: K % (64 stages) == 0 and K % 128 == 0; N % tile == 0; mode 2: M % tile == 0;
+ * lda, ldb % 8 == 0; A, B 16-byte aligned; row_scale only with resid.
+ */
+int qlora_gemm16_f32(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t M,
+                     int64_t N, int64_t K, int32_t mode, float* c, int64_t ldc, float alpha,
+                     const float* row_scale, const float* resid, int64_t ldr, int32_t tile,
+                     int32_t stages, int32_t splits, float* ws, int64_t ws_elems, void* stream);
+
+/*
+ * fp32 workspace elements (*elems) qlora_gemm16 (epi 0-5, modes 0-1) or qlora_gemm16_f32
+ * (epi 6, modes 1-2) uses for this problem, mode, tile and stage count: splits * M * N with
+ * splits > 1; with one slice the K-sliced last round's partials (fp16 epilogues only), 0 when
+ * that does not apply (tile 0 / splits 0: the automatic plan's). N as qlora_gemm16's (epi 3,
+ * 5: I). No reference counterpart (sizes the caller's workspace).
  */
 int qlora_gemm16_workspace(int64_t M, int64_t N, int64_t K, int32_t mode, int32_t epi,
                            int32_t tile, int32_t stages, int32_t splits, int64_t* elems);
 
 /*
- * The tile, stage count and K split qlora_gemm16 runs when given tile 0 and splits 0: a fixed
- * rule on (M, N, K, mode, epi), so a problem always runs the same kernels and gives the same
- * bits (no timing). No reference counterpart.
+ * The tile, stage count and K split qlora_gemm16 (or, with epi 6, qlora_gemm16_f32) runs when
+ * given tile 0 and splits 0: a fixed rule on (M, N, K, mode, epi), so a problem always runs the
+ * same kernels and gives the same bits (no timing). No reference counterpart.
  */
 int qlora_gemm16_plan(int64_t M, int64_t N, int64_t K, int32_t mode, int32_t epi, int32_t* tile,
                       int32_t* stages, int32_t* splits);

@@ -124,6 +124,30 @@ def test_gemm16_rejects_bad_problems_before_any_device_call(pkg):
     assert gemm(M=0) == 0                          # no rows: nothing to do
 
 
+def test_gemm16_f32_rejects_bad_problems_before_any_device_call(pkg):
+    """qlora_gemm16_f32 checks its mode, the transposed-A shape (whole tiles of M), the
+    reduction blocks, leading dimensions and the row scale's residual on the host."""
+    lib = pkg._lib.load()
+    P = 16  # non-null, 16-byte aligned stand-in: the checks fail before any access
+
+    def f32(M=256, N=256, K=256, mode=1, lda=256, ldb=256, ldc=256, tile=256, stages=2,
+            splits=1, row_scale=None, resid=None, ldr=0):
+        return lib.qlora_gemm16_f32(P, lda, P, ldb, M, N, K, mode, P, ldc, 1.0, row_scale,
+                                    resid, ldr, tile, stages, splits, None, 0, None)
+
+    assert f32(mode=0) == 1                    # the fp32 form is NN or transposed-A
+    assert f32(mode=3) == 1
+    assert f32(mode=2, M=200, lda=256) == 1    # transposed A: whole tiles of M
+    assert f32(mode=2, M=256, lda=200) == 1    # lda >= M
+    assert f32(K=192) == 1                     # reduction in blocks of 128
+    assert f32(N=200) == 1                     # N % tile
+    assert f32(row_scale=P) == 1               # a row scale without a residual
+    assert f32(resid=P, ldr=100) == 1          # ldr >= N
+    assert f32(splits=2) == 1                  # split-K without a workspace
+    assert f32(tile=256, stages=4) == 1
+    assert f32(M=0) == 0
+
+
 def test_gemm16_workspace_sizes(pkg):
     """qlora_gemm16_workspace (host only) at 256 x 256 tiles: splits x M x N with split-K; with
     one slice the K-sliced last round's partials when at most 64 tiles are left past the last

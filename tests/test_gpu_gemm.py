@@ -446,3 +446,51 @@ def test_swiglu_keep_epilogue(pkg, M, tile, stages, tail):
     ref = (a.double() @ w.double().t())
     assert rel_err(gu, ref) < 1e-3
     assert not torch.isnan(gu).any()
+
+
+def _f32_ref(a, b, mode, alpha, row_scale=None, resid=None):
+    A = a.double() if mode == 1 else a.double().t()
+    want = alpha * (A @ b.double())
+    if resid is not None:
+        rs = row_scale.double()[:, None] if row_scale is not None else 1.0
+        want = want + rs * resid.double()
+    return want
+
+
+@pytest.mark.parametrize("mode,M,K", [(1, 300, 8192), (1, 2048, 4480), (1, 1, 128),
+                                      (2, 8192, 384), (2, 3712, 1664), (2, 128, 128)])
+def test_gemm_f32_against_fp64(pkg, mode, M, K):
+    """qlora_gemm16_f32 (the LM head's fp32 products): out = alpha A op(B) + row_scale * resid,
+    A B (mode 1) or A^T B with A stored [K, M] (mode 2), updated in place (out is resid), at
+    every tile / stage / split variant that takes the shape and the automatic plan, against
+    fp64. In one slice every tile shape gives the same bits."""
+    L = pkg.linear
+    N = 1536
+    g = torch.Generator(device=DEV).manual_seed(M + K + mode)
+    a = (torch.randn(*((M, K) if mode == 1 else (K, M)), generator=g, device=DEV) * 0.5).half()
+    b = (torch.randn(K, N, generator=g, device=DEV) * 0.02).half()
+    resid = torch.randn(M, N, generator=g, device=DEV)
+    rs = torch.rand(M, generator=g, device=DEV) + 0.5
+    want = _f32_ref(a, b, mode, 0.25, rs, resid)
+    plain = _f32_ref(a, b, mode, 1.0)
+    one_slice = []
+    variants = [(256, 2), (128, 2), (128, 4)]
+    for tile, stages in variants:
+        if (K // 64) % stages or N % tile or (mode == 2 and M % tile):
+            continue
+        for splits in (1, 2, 4):
+            if (K // 64) < splits * stages:
+                continue
+            out = resid.clone()
+            L.gemm_f32(a, b, mode, alpha=0.25, row_scale=rs, resid=out, out=out, tile=tile,
+                       stages=stages, splits=splits)
+            err = (out.double() - want).abs().max().item()
+            assert err <= 1e-5 * want.abs().max().item() + 1e-6, (tile, stages, splits, err)
+            if splits == 1:
+                one_slice.append(out)
+            p = L.gemm_f32(a, b, mode, tile=tile, stages=stages, splits=splits)
+            assert rel_err(p, plain) < 1e-6
+    assert one_slice and all(torch.equal(o, one_slice[0]) for o in one_slice[1:])
+    auto = L.gemm_f32(a, b, mode, alpha=0.25, row_scale=rs, resid=resid)
+    assert (auto.double() - want).abs().max().item() <= 1e-5 * want.abs().max().item() + 1e-6
+    assert torch.equal(auto, L.gemm_f32(a, b, mode, alpha=0.25, row_scale=rs, resid=resid))

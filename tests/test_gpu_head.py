@@ -27,13 +27,21 @@ def _inputs(T, V, H, seed, ignore=0.25):
     return hn, E, targets
 
 
-@pytest.mark.parametrize("T,V,piece", [(37, 20000, 8192), (16, 151936, 8192), (9, 12288, 4096)])
-def test_chunked_head_against_fp64(pkg, T, V, piece):
+@pytest.mark.parametrize("T,V,piece", [(37, 20096, 8192), (16, 151936, 8192), (9, 12288, 4096),
+                                        (300, 8320, 4096)])
+@pytest.mark.parametrize("path", ["chunked", "full"])
+def test_head_against_fp64(pkg, T, V, piece, path):
+    """Loss, per-token loss, dh and dE of either head (pieces, whole rows) against fp64
+    autograd: row counts off the 128-row blocks of the dE product, a last piece narrower than
+    the others (and than 256 columns: the GEMM's 128 x 128 tiles)."""
     H = 1536
     hn, E, targets = _inputs(T, V, H, T)
     targets[1] = -100  # at least one ignored row
     denom = float((targets >= 0).sum())
-    r = pkg.head.chunked_head(hn, E, targets, denom, piece=piece)
+    if path == "chunked":
+        r = pkg.head.chunked_head(hn, E, targets, denom, piece=piece)
+    else:
+        r = pkg.head.full_head(hn, E, targets, denom)
     x = hn.double().cpu().requires_grad_(True)
     w = E.double().cpu().requires_grad_(True)
     tg = targets.cpu()
@@ -67,7 +75,7 @@ def test_config4_chunked_equals_whole_row(pkg):
 @pytest.mark.parametrize("path", ["chunked", "full"])
 def test_config4_full_size_against_fp64(pkg, path):
     """Config 4 at its stated size (T = 2048, V = 151,936, ~25 % ignored): loss, every token's
-    loss, dh and dE against fp64 autograd of the same fp16 operands (rocBLAS double-precision
+    loss, dh and dE against fp64 autograd of the same fp16 operands (torch's double-precision
     products on the GPU, independent of this package's kernels), at the reference's head
     tolerances (test_host_head.py:157-178: loss 1e-5 relative, per-token loss rtol 1e-4 /
     atol 1e-3, gradients 1e-3 relative)."""
