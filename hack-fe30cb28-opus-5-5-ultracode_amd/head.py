@@ -76,7 +76,8 @@ def chunked_head(hn, E, targets, denom, piece=PIECE, want_dE=True):
     inv = 1.0 / float(denom) if float(denom) else float("nan")
     dE = None
     if want_dE:
-        dE = torch.zeros((V, H), device=dev, dtype=torch.float32)
+        # every row of dE is written by its piece's product (zeros without supervised rows)
+        dE = (torch.empty if n_sup else torch.zeros)((V, H), device=dev, dtype=torch.float32)
         if n_sup:
             kp = -(-n_sup // 128) * 128  # rows of the dE reduction (n_sup <= kp <= Tp)
             for v0 in range(0, V, piece):

@@ -277,6 +277,14 @@ def gemm_f32(a, b, mode, alpha=1.0, row_scale=None, resid=None, out=None, tile=0
             raise ValueError("row_scale needs resid and one entry per output row")
     if M == 0:
         return out
+    if tile == 0 and mode == 2 and M > 256 and M % 256:
+        # transposed A takes whole tiles of M only: the columns up to the last multiple of 256
+        # on 256 x 256 tiles, the rest (128 of them for every Qwen2 vocabulary) on their own
+        m1 = M // 256 * 256
+        for lo, hi in ((0, m1), (m1, M)):
+            gemm_f32(a[:, lo:hi], b, 2, alpha, None if row_scale is None else row_scale[lo:hi],
+                     None if resid is None else resid[lo:hi], out[lo:hi])
+        return out
     if tile == 0:
         splits = 0
     elif splits is None:
