@@ -607,14 +607,15 @@ def main():
     kernels = measure_step_kernels(pkg, trainer, batches[-4:], cfg)
     full = None
     if args.keep_steps > 0 and args.policy != "keep":
-        model.keep_gu = model.keep_attn = False
+        model.keep_gu = model.keep_attn = model.keep_weights_recompute = False
         time_steps(trainer, batches, 0, 2)
         ftok, fel, _ = time_steps(trainer, batches, args.warmup, args.keep_steps)
         full = {"value": ftok / fel, "ms_per_step": 1000.0 * fel / args.keep_steps,
                 "steps": args.keep_steps,
                 "what": "every layer recomputes its whole forward from its input in backward "
-                        "(the [gate|up] product and the attention tensors formed again)"}
-        model.keep_gu = model.keep_attn = True
+                        "(the [gate|up] product, the attention tensors and the dequantized "
+                        "weights formed again)"}
+        model.keep_gu = model.keep_attn = model.keep_weights_recompute = True
         log(f"full recompute: {full['value']:.0f} tokens/s")
     keep = None
     if args.keep_steps > 0 and args.policy != "keep":
@@ -646,7 +647,9 @@ def main():
                                    "attention's q, k, v, output and o_proj output (the "
                                    "reference's GuStream/AttnStream, in HBM here) and "
                                    "recomputes the two RMSNorms and the LoRA inputs' products "
-                                   "in backward"
+                                   "in backward; its dequantized fp16 weights stay resident "
+                                   "from the forward to the backward (2.6 GB in all) instead "
+                                   "of a second dequant"
                                    if args.policy == "recompute" else
                                    "every layer keeps its intermediates (no recompute)"),
                    "gemm": ("the package's MFMA GEMM (qlora_gemm16, fixed tile/split plan) "

@@ -569,7 +569,9 @@ class _Layer(torch.autograd.Function):
             h3 = _Layer._forward(ctx, h, spec, packed, keep_all, aq_w, bq_w, av_w, bv_w)
         # a layer that keeps its intermediates may keep its dequantized weights as well, so
         # that its backward does not dequantize the same NF4 weights a second time
-        ctx.weights = weights.copies if keep_all and getattr(packed, "keep_weights", False) else None
+        keep_w = getattr(packed, "keep_weights", False) if keep_all else \
+            getattr(packed, "keep_weights_recompute", False)
+        ctx.weights = weights.copies if keep_w else None
         return h3
 
     @staticmethod
@@ -755,8 +757,11 @@ class FusedQwen2:
     step does: its [gate|up] product (`keep_gu`) and its attention's q, k, v, output and o_proj
     output (`keep_attn`) are kept from the forward, as the reference keeps them (GuStream,
     AttnStream: in host memory on its GPU, in HBM here), and the backward forms the two
-    RMSNorms and the LoRA inputs' products again. `keep_all=True` keeps every layer's intermediates instead; `keep_all=None` follows the
-    reference's memory-cap plan (keep_plan, engine.py:1626-1640): the last layers keep
+    RMSNorms and the LoRA inputs' products again; the layer's dequantized weights are kept too
+    (`keep_weights_recompute`: the frozen weights stay resident in fp16 between the forward and
+    the backward, 2.6 GB for the 1.5B model, instead of a second dequant). `keep_all=True`
+    keeps every layer's intermediates instead; `keep_all=None` follows the reference's
+    memory-cap plan (keep_plan, engine.py:1626-1640): the last layers keep
     everything as long as the step's predicted peak stays under the cap (the GPU's memory less
     a margin by default)."""
 
@@ -777,6 +782,11 @@ class FusedQwen2:
         # layers that keep their intermediates also keep their dequantized weights for the
         # backward (one dequant per layer and step instead of two; 94 MB per 1.5B layer)
         self.keep_weights = True
+        # ... and so does a recomputing layer (94 MB per 1.5B layer, 2.6 GB for the 28: the
+        # frozen weights stay resident in fp16 from the forward to the backward, which then
+        # skips the layer's second dequant; the activations are still recomputed). Config-5 step
+        # on one box: 29.51 -> 28.80 ms
+        self.keep_weights_recompute = True
         # recomputing layers keep their [gate|up] product (2 I fp16 per token: 2.6 GB over a
         # 1.5B step of 2,560 tokens) and recompute their forward up to the MLP input only, the
         # reference's plan (its [gate|up] is kept first, on the GPU or in pinned host memory,
@@ -837,6 +847,18 @@ class FusedQwen2:
                      + 2 * spec.I * 2 + spec.HQ * 4 + 2 * 4 + 2 * 16 * 2 + 2 * ((spec.H + 3) // 4))
         return n * per_token
 
+    def recompute_bytes_per_layer(self, n):
+        """Device bytes a recomputing layer holds from its forward to its backward beyond its
+        fp32 input: its [gate | up] product (keep_gu: 2 I fp16 per token), its attention
+        tensors (keep_attn: q, k, v, the output, the log-sum-exp and the o_proj output) and its
+        dequantized weights (keep_weights_recompute)."""
+        spec = self.layers[0]
+        per_token = (2 * spec.I * 2 if self.keep_gu else 0)
+        if self.keep_attn:
+            per_token += (2 * spec.HQ + 2 * spec.HKV) * spec.D * 2 + spec.HQ * 4 + spec.H * 2
+        return n * per_token + (self.weight_bytes_per_layer() if self.keep_weights_recompute
+                                else 0)
+
     def weight_bytes_per_layer(self):
         """Device bytes of one layer's dequantized fp16 weights (qkv, o, gate|up, down)."""
         spec = self.layers[0]
@@ -848,10 +870,11 @@ class FusedQwen2:
 
     def keep_plan(self, n):
         """The number of last layers that keep every intermediate for a step of n tokens: as
-        many as fit under the memory cap above what is allocated now plus one recomputing
-        layer's working set (its dequantized weights and per-token buffers). With keep_weights
-        a keeping layer also holds its dequantized weights from the forward to its backward
-        (weight_bytes_per_layer more per layer)."""
+        many as fit under the memory cap above what is allocated now, one recomputing layer's
+        working set (its dequantized weights and per-token buffers) and what every layer holds
+        as a recomputing one (recompute_bytes_per_layer). With keep_weights a keeping layer also
+        holds its dequantized weights from the forward to its backward (weight_bytes_per_layer
+        more per layer)."""
         if self.keep_all is not None:
             return len(self.layers) if self.keep_all else 0
         cap = self.memory_cap
@@ -859,8 +882,10 @@ class FusedQwen2:
             cap = torch.cuda.get_device_properties(self.device).total_memory - self.CAP_MARGIN
         weights = self.weight_bytes_per_layer()
         work = weights + 64 * 2**20 + n * 96 * 1024 + n * self.cfg.vocab_size * 2
-        free = cap - self.allocated_bytes() - work
-        per_layer = max(1, self.kept_bytes_per_layer(n) + (weights if self.keep_weights else 0))
+        rec = self.recompute_bytes_per_layer(n)
+        free = cap - self.allocated_bytes() - work - len(self.layers) * rec
+        per_layer = max(1, self.kept_bytes_per_layer(n) + (weights if self.keep_weights else 0)
+                        - rec)
         return int(max(0, min(len(self.layers), free // per_layer)))
 
     def step(self, input_ids, attention_mask, labels, denom, lengths=None, n_supervised=None,
@@ -889,6 +914,7 @@ class FusedQwen2:
         keep_from = len(self.layers) - self.keep_plan(packed.n)
         packed.keep_all_from = keep_from
         packed.keep_weights = self.keep_weights
+        packed.keep_weights_recompute = self.keep_weights_recompute
         packed.keep_gu = self.keep_gu
         packed.keep_attn = self.keep_attn
         for i, spec in enumerate(self.layers):

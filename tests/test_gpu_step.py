@@ -100,14 +100,18 @@ def test_step_other_model_shapes(pkg, H, HQ, HKV, D, r):
 
 
 def test_kept_tensors_equal_recomputing_them(pkg):
-    """A recomputing layer keeps its [gate|up] product (keep_gu) and its attention tensors
-    (keep_attn: q, k, v, output, log-sum-exp, o_proj output) from the forward instead of
-    forming them again in its backward: the same loss and LoRA gradients bit for bit in all
-    four combinations (what is kept is the same bits as what the recompute forms)."""
+    """A recomputing layer keeps its [gate|up] product (keep_gu), its attention tensors
+    (keep_attn: q, k, v, output, log-sum-exp, o_proj output) and its dequantized weights
+    (keep_weights_recompute) from the forward instead of forming them again in its backward:
+    the same loss and LoRA gradients bit for bit in every combination (what is kept is the same
+    bits as what the recompute forms)."""
     out = []
-    for keep_gu, keep_attn in ((True, True), (False, False), (True, False), (False, True)):
+    for keep_gu, keep_attn, keep_w in ((True, True, True), (False, False, False),
+                                       (True, False, True), (False, True, False),
+                                       (True, True, False)):
         model = _tiny(pkg, H=512, HQ=8, HKV=2, D=64)
         model.keep_all, model.keep_gu, model.keep_attn = False, keep_gu, keep_attn
+        model.keep_weights_recompute = keep_w
         lengths = [17, 60, 33, 5]
         ids, mask, labels = _batch(lengths, model.cfg.vocab_size)
         denom = float((labels[:, 1:] != -100).sum())
@@ -144,7 +148,9 @@ def test_step_matches_oracle(pkg, lengths, keep_all):
         # tests' tensors, which would shift the cap between here and the step
         base = torch.cuda.memory_allocated()
         model.allocated_bytes = lambda: base
-        model.set_memory_cap(base + work + int(1.5 * (model.kept_bytes_per_layer(n) + weights)))
+        rec = model.recompute_bytes_per_layer(n)
+        model.set_memory_cap(base + work + 2 * rec +
+                             int(1.5 * (model.kept_bytes_per_layer(n) + weights - rec)))
         assert model.keep_plan(n) == 1
     elif keep_all == "no_weights":
         model.keep_all = True
