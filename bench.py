@@ -367,7 +367,8 @@ def config3(pkg, reps=10):
     from oracle import step as OS
     E, P = pkg.engine, pkg.profiling
     dev = torch.device("cuda:0")
-    cfg = E.Qwen2Config(num_hidden_layers=1, vocab_size=1000)
+    # one layer; the block does not use the vocabulary (any multiple of 128 the GEMM takes)
+    cfg = E.Qwen2Config(num_hidden_layers=1, vocab_size=1024)
     model = E.random_qwen2(cfg, dev, seed=3)
     spec = model.layers[0]
     H, HQ, HKV, D = cfg.hidden_size, cfg.num_attention_heads, cfg.num_key_value_heads, \

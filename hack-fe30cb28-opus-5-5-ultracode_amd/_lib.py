@@ -46,6 +46,7 @@ SIGNATURES = {
                          I32, P, I64, P],
     "qlora_gemm16_workspace": [I64, I64, I64, I32, I32, I32, I32, I32, P],
     "qlora_gemm16_plan": [I64, I64, I64, I32, I32, P, P, P],
+    "qlora_gemm16_plan_split": [I64, I64, I64, I32, I32, P, P, P, P, P],
     "qlora_resid_add": [P, P, P, I64, P],
     "qlora_lora_fwd_rows": [P, P, P, P, P, P, P, P, P, P, I64, I32, I32, I32, I32, P],
     "qlora_lora_bwd_rows": [P, P, I64, P, P, P, P, P, P, P, P, I64, I32, I32, I32, I32, F32, P],

@@ -380,6 +380,100 @@ __device__ __forceinline__ void sync_tile() {
   __builtin_amdgcn_s_barrier();
 }
 
+// Epilogue 5 of a BM x BN tile (registers and LDS areas as store_tile): the product [g | u]
+// first, staged as a plain store would and written to gate column n and up column I + n of g.gu;
+// while those stores issue (they stall when every CU of a round writes at once), the SwiGLU of
+// the same accumulators is formed, one group of four values a lane per 16-byte store, and kept
+// packed in registers; then m is staged in the same LDS area and stored. The values are those of
+// epilogue 3 and of a plain store of the product, bit for bit.
+template <int BM, int BN>
+__device__ __forceinline__ void store_swiglu_keep(const GemmArgs& g,
+                                                  f32x16 (&acc)[BM / 64][BN / 64], uint16_t* lo,
+                                                  uint16_t* hi, int64_t m0, int64_t tile_n,
+                                                  int lane, int wave) {
+  constexpr int FM = BM / 64, FN = BN / 64, WR = BM / 2, WC = BN / 2, kHalf = WR / 2;
+  constexpr int kCh2 = WC / 8, kRows2 = 64 / kCh2, kIt = WR / kRows2;
+  constexpr int kGroups = FM * 4 * (FN / 2), kPer = kGroups / kIt;
+  static_assert(kGroups % kIt == 0, "whole groups of SwiGLU values per store");
+  const int wm = wave >> 1, wn = wave & 1, col_in = lane & 31, c4 = 4 * (lane >> 5);
+  auto stage2 = [&](int row, int chunk) {
+    return (row % kHalf) * WC + ((chunk ^ (row & (kCh2 - 1))) << 3);
+  };
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    const int row = i * 32 + col_in;
+    uint16_t* base = i < FM / 2 ? lo : hi;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int col = j * 32 + 8 * q + c4;
+        *reinterpret_cast<uint2*>(base + stage2(row, col >> 3) + c4) =
+            make_uint2(pack2h(acc[i][j][4 * q], acc[i][j][4 * q + 1]),
+                       pack2h(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]));
+      }
+  }
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the wavefront's own LDS stores
+  const int64_t g_base = tile_n * (BN / 2) + wn * (WC / 2);
+  auto gu_piece = [&](int k) {
+    const int row = k * kRows2 + lane / kCh2, chunk = lane % kCh2;
+    return *reinterpret_cast<const uint4*>((row < kHalf ? lo : hi) + stage2(row, chunk));
+  };
+  uint2 mv[kGroups];  // group (i, q, j): four m values of row 32 i + l % 32, packed
+  uint4 v = gu_piece(0);
+#pragma unroll
+  for (int k = 0; k < kIt; ++k) {
+    uint4 vn;
+    if (k + 1 < kIt) vn = gu_piece(k + 1);
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int gi = k * kPer + u, i = gi / (4 * (FN / 2)), q = (gi / (FN / 2)) % 4,
+                j = gi % (FN / 2);
+      float m[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float gt = h2f(f2h(acc[i][j][4 * q + e]));
+        const float up = h2f(f2h(acc[i][j + FN / 2][4 * q + e]));
+        m[e] = gt * sigmoid_fast(gt) * up;  // as glu_fwd_kernel
+      }
+      mv[gi] = make_uint2(pack2h(m[0], m[1]), pack2h(m[2], m[3]));
+      // formed here, between this store and the next (else the compiler sinks the arithmetic
+      // below the loop, where nothing overlaps it)
+      asm volatile("" : "+v"(mv[gi].x), "+v"(mv[gi].y));
+    }
+    const int row = k * kRows2 + lane / kCh2, col = (lane % kCh2) * 8;
+    const int64_t mm = m0 + wm * WR + row;
+    const int64_t n = g_base + (col % (WC / 2)) + (col >= WC / 2 ? g.I : 0);
+    if (mm < g.M) *reinterpret_cast<uint4*>(g.gu + mm * g.ldgu + n) = v;
+    v = vn;
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // m, fp16 [rows][WC / 2] per wavefront, through the same LDS area (its reads are complete:
+  // their values have been stored)
+  constexpr int kCols = WC / 2, kChunks = kCols / 8, kRowsPer = 64 / kChunks;
+  auto stage_off = [&](int row, int chunk) {
+    return (row % kHalf) * kCols + ((chunk ^ (row & (kChunks - 1))) << 3);
+  };
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+#pragma unroll
+  for (int gi = 0; gi < kGroups; ++gi) {
+    const int i = gi / (4 * (FN / 2)), q = (gi / (FN / 2)) % 4, j = gi % (FN / 2);
+    const int row = i * 32 + col_in, col = j * 32 + 8 * q + c4;
+    *reinterpret_cast<uint2*>((i < FM / 2 ? lo : hi) + stage_off(row, col >> 3) + c4) = mv[gi];
+  }
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  const int64_t n_base = tile_n * (BN / 2) + wn * (WC / 2);
+#pragma unroll
+  for (int k = 0; k < WR / kRowsPer; ++k) {
+    const int row = k * kRowsPer + lane / kChunks, chunk = lane % kChunks;
+    const uint4 w = *reinterpret_cast<const uint4*>((row < kHalf ? lo : hi) +
+                                                     stage_off(row, chunk));
+    const int64_t mm = m0 + wm * WR + row, n = n_base + chunk * 8;
+    if (mm < g.M && n < g.N)
+      *reinterpret_cast<uint4*>(static_cast<uint16_t*>(g.c) + mm * g.ldc + n) = w;
+  }
+}
+
 // The epilogue of a BM x BN tile from the accumulators of mfma_step (4 wavefronts, each on a
 // WR x WC block, WR = BM / 2, WC = BN / 2; register layouts as mfma_step): fp16 outputs are
 // staged through LDS (`lo`: the wavefront's rows 0 .. WR/2 - 1, `hi`: the rest, [WR/2][columns]
@@ -393,7 +487,9 @@ __device__ __forceinline__ void store_tile(const GemmArgs& g, f32x16 (&acc)[BM /
   constexpr bool kT = staged_epi(EPI);
   const int wm = wave >> 1, wn = wave & 1;
   const int col_in = lane & 31;
-  if constexpr (kT) {
+  if constexpr (EPI == kEpiSwigluKeep) {
+    store_swiglu_keep<BM, BN>(g, acc, lo, hi, m0, tile_n, lane, wave);
+  } else if constexpr (kT) {
     // each wavefront writes its block to LDS as fp16 (8-byte LDS stores of four columns,
     // 16-byte chunks XOR-swizzled by row so the 32 rows of a store spread over the banks), then
     // stores whole rows to memory with 16-byte stores
@@ -490,42 +586,6 @@ __device__ __forceinline__ void store_tile(const GemmArgs& g, f32x16 (&acc)[BM /
       const int64_t m = m0 + wm * WR + row, n = n_base + chunk * 8;
       if (m < g.M && n < g.N)
         *reinterpret_cast<uint4*>(static_cast<uint16_t*>(g.c) + m * g.ldc + n) = v;
-    }
-    if constexpr (EPI == kEpiSwigluKeep) {
-      // the product itself, fp16 [g | u]: the wavefront's WC B columns (its WC / 2 gate
-      // columns, then the matching up columns) staged as a plain store would, then written to
-      // gate column n and up column I + n of g.gu
-      constexpr int kCh2 = WC / 8, kRows2 = 64 / kCh2;
-      auto stage2 = [&](int row, int chunk) {
-        return (row % kHalf) * WC + ((chunk ^ (row & (kCh2 - 1))) << 3);
-      };
-      __builtin_amdgcn_s_waitcnt(0xC07F);  // the m pass's LDS reads, before the area is reused
-#pragma unroll
-      for (int i = 0; i < FM; ++i) {
-        const int row = i * 32 + col_in;
-        uint16_t* base = i < FM / 2 ? lo : hi;
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-#pragma unroll
-          for (int j = 0; j < FN; ++j) {
-            const int col = j * 32 + 8 * q + c4;
-            *reinterpret_cast<uint2*>(base + stage2(row, col >> 3) + c4) =
-                make_uint2(pack2h(acc[i][j][4 * q], acc[i][j][4 * q + 1]),
-                           pack2h(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]));
-          }
-      }
-      __builtin_amdgcn_s_waitcnt(0xC07F);
-      const int64_t g_base = tile_n * (BN / 2) + wn * (WC / 2);
-#pragma unroll
-      for (int k = 0; k < WR / kRows2; ++k) {
-        const int row = k * kRows2 + lane / kCh2, chunk = lane % kCh2;
-        const uint4 v = *reinterpret_cast<const uint4*>((row < kHalf ? lo : hi) +
-                                                         stage2(row, chunk));
-        const int64_t m = m0 + wm * WR + row;
-        const int col = chunk * 8;
-        const int64_t n = g_base + (col % (WC / 2)) + (col >= WC / 2 ? g.I : 0);
-        if (m < g.M) *reinterpret_cast<uint4*>(g.gu + m * g.ldgu + n) = v;
-      }
     }
   } else if constexpr (EPI == kEpiF32) {
     // fp32 out = alpha acc (+ row-scaled resid), from the registers: each store instruction
@@ -1376,12 +1436,42 @@ double plan_cost(int64_t M, int64_t N, int64_t K, int mode, int epi, const PlanC
   return v.a * rounds + v.b * kwalk + v.c * part + v.d * red;
 }
 
+// A product in one slice on 256 x 256 tiles whose last round of tiles would run part-full can
+// instead run its whole rounds on 256 x 256 tiles, over the leading output columns that fill
+// them (whole N tiles), and the remaining columns as a second launch on 128 x 128 tiles (which
+// fill a round four times as finely and need no partials or reduce, where the K-sliced last
+// round writes and sums fp32 slices). Returns the columns of the first launch (0 when the split
+// does not apply) and, through cost, the model's cost of both launches (the same constants,
+// plus kGap us for the second launch's start).
+constexpr double kGap = 1.5;
+int64_t rest_split(int64_t M, int64_t N, int64_t K, int mode, int epi, const PlanCoef& v128,
+                   double* cost) {
+  const PlanCoef& v256 = kPlanCoef[0];
+  const int64_t kt = K / kBK64;
+  if (epi == kEpiF32 || mode == 2 || kt % 2 != 0 || kt % v128.stages != 0 || K > 12288)
+    return 0;
+  const int cols = swiglu_epi(epi) ? 128 : 256;  // output columns of a 256 x 256 tile
+  if (swiglu_epi(epi) ? N % 128 != 0 : (mode != 0 && N % 256 != 0)) return 0;
+  const int64_t m_tiles = qlora_cdiv(M, 256), n_tiles = n_tiles_of(N, epi, 256);
+  const int64_t rounds = m_tiles * n_tiles / kCUs;
+  const int64_t n_main = rounds * kCUs / m_tiles;  // whole N tiles in the full rounds
+  if (rounds == 0 || n_main == 0 || n_main >= n_tiles) return 0;
+  const int64_t n_rest = N - n_main * cols;
+  const int64_t t128 = qlora_cdiv(M, 128) * n_tiles_of(n_rest, epi, 128);
+  const double r128 = (double)qlora_cdiv(t128, slots_of(128, v128.stages));
+  *cost = v256.a * rounds + v256.b * rounds * (double)K + v128.a * r128 +
+          v128.b * r128 * (double)K + kGap;
+  return n_main * cols;
+}
+
 void auto_plan(int64_t M, int64_t N, int64_t K, int mode, int epi, int* tile, int* stages,
-               int* splits) {
+               int* splits, int* rest = nullptr, int64_t* n_first = nullptr) {
   double best = -1.0;
   *tile = 256;
   *stages = 2;
   *splits = 1;
+  if (rest != nullptr) *rest = 0;
+  if (n_first != nullptr) *n_first = 0;
   // first pass: 128 x 128 tiles up to K = 12,288 only; second (when none of the first's can run
   // the problem: an NN product whose N is not a multiple of 256), every variant
   for (int pass = 0; pass < 2 && best < 0.0; ++pass) {
@@ -1397,6 +1487,19 @@ void auto_plan(int64_t M, int64_t N, int64_t K, int mode, int epi, int* tile, in
           *splits = sp;
         }
       }
+    }
+  }
+  if (rest == nullptr || best < 0.0) return;
+  for (int vi = 1; vi <= 2; ++vi) {
+    double c = -1.0;
+    const int64_t nf = rest_split(M, N, K, mode, epi, kPlanCoef[vi], &c);
+    if (nf > 0 && c < best) {
+      best = c;
+      *tile = 256;
+      *stages = 2;
+      *splits = 1;
+      *rest = kPlanCoef[vi].stages;
+      *n_first = nf;
     }
   }
 }
@@ -1578,7 +1681,9 @@ QLORA_API int qlora_gemm16_timed(const void* a, int64_t lda, const void* b, int6
   QLORA_CHECK_ARG(a && b && c && (mode == 0 || mode == 1));
   QLORA_CHECK_ARG((tile == 0) == (splits == 0));
   QLORA_CHECK_ARG(epi >= 0 && epi <= 5 && epi != kEpiPartial && !(swiglu_epi(epi) && mode != 0));
-  if (tile == 0) auto_plan(M, N, K, mode, epi, &tile, &stages, &splits);
+  int rest = 0;
+  int64_t n_first = 0;
+  if (tile == 0) auto_plan(M, N, K, mode, epi, &tile, &stages, &splits, &rest, &n_first);
   QLORA_CHECK_ARG((tile == 256 && stages == 2) || (tile == 128 && (stages == 2 || stages == 4)));
   QLORA_CHECK_ARG(splits >= 1 && splits <= 16 && !(splits > 1 && swiglu_epi(epi)));
   // the split-K reduce writes four columns a thread
@@ -1612,6 +1717,23 @@ QLORA_API int qlora_gemm16_timed(const void* a, int64_t lda, const void* b, int6
   g.I = swiglu_I;
   g.gu = static_cast<uint16_t*>(gu);
   g.ldgu = ldgu;
+  if (rest > 0) {
+    // the leading n_first output columns on 256 x 256 tiles in whole rounds, the rest on
+    // 128 x 128 tiles (NT: W rows n_first.., SwiGLU's up rows I + n_first..; NN: B's columns)
+    GemmArgs g2 = g;
+    g.N = n_first;
+    if (int rc = run_gemm(g, kBHalf, mode, epi, 1, nullptr, 0, (hipStream_t)stream,
+                          static_cast<hipEvent_t>(start), nullptr, 256, 2))
+      return rc;
+    g2.N = N - n_first;
+    g2.b += mode == 0 ? n_first * ldb : n_first;
+    g2.c = static_cast<char*>(c) + n_first * (epi == kEpiResid ? 4 : 2);
+    if (g2.bias) g2.bias += n_first;
+    if (g2.resid) g2.resid += n_first;
+    if (g2.gu) g2.gu += n_first;
+    return run_gemm(g2, kBHalf, mode, epi, 1, nullptr, 0, (hipStream_t)stream, nullptr,
+                    static_cast<hipEvent_t>(stop), 128, rest);
+  }
   return run_gemm(g, kBHalf, mode, epi, splits, ws, ws_elems, (hipStream_t)stream,
                   static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop), tile, stages);
 }
@@ -1678,7 +1800,10 @@ QLORA_API int qlora_gemm16_workspace(int64_t M, int64_t N, int64_t K, int32_t mo
   QLORA_CHECK_ARG((mode == 2) <= (epi == kEpiF32) && (epi == kEpiF32) <= (mode != 0));
   *elems = 0;
   if (M == 0) return 0;
-  if (tile == 0) auto_plan(M, N, K, mode, epi, &tile, &stages, &splits);
+  int rest = 0;
+  int64_t n_first = 0;
+  if (tile == 0) auto_plan(M, N, K, mode, epi, &tile, &stages, &splits, &rest, &n_first);
+  if (rest > 0) return 0;
   QLORA_CHECK_ARG((tile == 256 && stages == 2) || (tile == 128 && (stages == 2 || stages == 4)));
   if (splits > 1) {
     *elems = (int64_t)splits * M * N;
@@ -1691,14 +1816,34 @@ QLORA_API int qlora_gemm16_workspace(int64_t M, int64_t N, int64_t K, int32_t mo
   return 0;
 }
 
-// The (tile, stages, splits) qlora_gemm16 runs with tile 0 and splits 0.
+// The plan of qlora_gemm16 with tile 0 and splits 0 in full: the first launch's (tile, stages,
+// splits) and, when the remaining output columns run as a second launch on 128 x 128 tiles, that
+// launch's stage count (rest, else 0) and the first launch's output columns (n_first).
+QLORA_API int qlora_gemm16_plan_split(int64_t M, int64_t N, int64_t K, int32_t mode, int32_t epi,
+                                      int32_t* tile, int32_t* stages, int32_t* splits,
+                                      int32_t* rest, int64_t* n_first) {
+  QLORA_CHECK_ARG(tile && stages && splits && rest && n_first && M >= 0 && N > 0 && K > 0);
+  QLORA_CHECK_ARG(mode >= 0 && mode <= 1 && epi >= 0 && epi <= 5 && epi != kEpiPartial);
+  int t, st, sp, r;
+  int64_t nf;
+  auto_plan(M, N, K, mode, epi, &t, &st, &sp, &r, &nf);
+  *tile = t;
+  *stages = st;
+  *splits = sp;
+  *rest = r;
+  *n_first = nf;
+  return 0;
+}
+
+// The (tile, stages, splits) qlora_gemm16 runs with tile 0 and splits 0 (its first launch's).
 QLORA_API int qlora_gemm16_plan(int64_t M, int64_t N, int64_t K, int32_t mode, int32_t epi,
                                 int32_t* tile, int32_t* stages, int32_t* splits) {
   QLORA_CHECK_ARG(tile && stages && splits && M >= 0 && N > 0 && K > 0);
   QLORA_CHECK_ARG(mode >= 0 && mode <= 2 && epi >= 0 && epi <= 6 && epi != kEpiPartial);
   QLORA_CHECK_ARG((mode == 2) <= (epi == kEpiF32) && (epi == kEpiF32) <= (mode != 0));
-  int t, st, sp;
-  auto_plan(M, N, K, mode, epi, &t, &st, &sp);
+  int t, st, sp, r;
+  int64_t nf;
+  auto_plan(M, N, K, mode, epi, &t, &st, &sp, epi == kEpiF32 ? nullptr : &r, &nf);
   *tile = t;
   *stages = st;
   *splits = sp;

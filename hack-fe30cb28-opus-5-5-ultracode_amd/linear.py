@@ -193,6 +193,17 @@ def gemm_plan(M, N, K, mode, epi=0):
     return t.value, st.value, sp.value
 
 
+def gemm_plan_split(M, N, K, mode, epi=0):
+    """qlora_gemm16's automatic plan in full: (tile, stages, splits, rest, n_first); rest > 0:
+    the output columns past n_first run as a second launch on 128 x 128 tiles with `rest`
+    stages."""
+    t, st, sp, r = (ctypes.c_int32(0) for _ in range(4))
+    nf = ctypes.c_int64(0)
+    _lib.call("qlora_gemm16_plan_split", M, N, K, mode, epi, ctypes.byref(t), ctypes.byref(st),
+              ctypes.byref(sp), ctypes.byref(r), ctypes.byref(nf))
+    return t.value, st.value, sp.value, r.value, nf.value
+
+
 def hgemm(a, b, mode, epi=0, bias=None, resid=None, out=None, swiglu_I=0, splits=None,
           tail=None, tile=256, stages=2, gu=None):
     """The MFMA GEMM with an fp16 B (qlora_gemm16): mode 0 C = A B^T (B [N, K]), mode 1 C = A B

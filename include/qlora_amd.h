@@ -300,7 +300,10 @@ int qlora_nf4_gemm(const void* a, int64_t lda, const void* packed, const float* 
  * then the epilogue; the slice count follows the tile count and the GPU's workgroup slots: 256
  * tiles of 256, 512 of 128); a null or smaller ws runs them whole (results then differ in the
  * fp32 summation order of those tiles only).
- * tile 0 with splits 0 (and any stages): the plan of qlora_gemm16_plan.
+ * tile 0 with splits 0 (and any stages): the plan of qlora_gemm16_plan_split; when it splits the
+ * output columns, the first n_first run as whole rounds of 256 x 256 tiles and the rest as a
+ * second launch on 128 x 128 tiles, on the same stream (the same bits as one launch of whole
+ * 256 x 256 tiles without the K-sliced last round).
  * Replaces the cuBLAS products of the frozen projections after dequant (engine.py:1082, 1112,
  * 1163, 1179, 1239, 1293, 1301, 1316) and of the lm_head (engine.py:1376-1381).
  * Requires: K % (64 stages) == 0 and K % 128 == 0; mode 1: N % tile == 0; mode 0: N % 8 == 0
@@ -360,6 +363,19 @@ int qlora_gemm16_workspace(int64_t M, int64_t N, int64_t K, int32_t mode, int32_
  */
 int qlora_gemm16_plan(int64_t M, int64_t N, int64_t K, int32_t mode, int32_t epi, int32_t* tile,
                       int32_t* stages, int32_t* splits);
+
+/*
+ * The plan of qlora_gemm16 (epi 0-5, modes 0-1) with tile 0 and splits 0 in full: the first
+ * launch's tile, stages and splits, and rest > 0 when the output columns past n_first run as a
+ * second launch on 128 x 128 tiles with rest stages (else rest = n_first = 0). The split applies
+ * to a product in one slice whose last round of 256 x 256 tiles would run part-full: its whole
+ * rounds take the leading whole N tiles, and the remaining columns fill a round four times as
+ * finely, without the K-sliced last round's fp32 partials and reduce; chosen by the same fixed
+ * cost model. No reference counterpart.
+ */
+int qlora_gemm16_plan_split(int64_t M, int64_t N, int64_t K, int32_t mode, int32_t epi,
+                            int32_t* tile, int32_t* stages, int32_t* splits, int32_t* rest,
+                            int64_t* n_first);
 
 /*
  * out = a + fp32(d) over numel elements (a, out f32; d f16; numel % 4 == 0; out may alias a):

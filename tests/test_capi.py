@@ -227,6 +227,15 @@ def test_gemm16_plan_is_fixed_and_valid(pkg):
             assert (K // 64) % stages == 0 and (mode == 0 or N % tile == 0)
             assert epi != 3 or splits == 1
             auto = L.hgemm_workspace(M, N, K, epi, 0, 0, 0, mode)
+            full = L.gemm_plan_split(M, N, K, mode, epi)
+            assert full[:3] == plan
+            rest, n_first = full[3:]
+            if rest:  # leading columns on whole rounds of 256 x 256 tiles, the rest on 128 x 128
+                assert tile == 256 and splits == 1 and rest in (2, 4) and auto == 0
+                assert 0 < n_first < N and n_first % (128 if epi in (3, 5) else 256) == 0
+                assert (K // 64) % rest == 0 and (mode == 0 or (N - n_first) % 128 == 0)
+                continue
+            assert n_first == 0
             assert auto == L.hgemm_workspace(M, N, K, epi, splits, tile, stages, mode)
             if splits > 1:
                 assert auto == splits * M * N
@@ -247,4 +256,9 @@ def test_gemm16_plan_at_the_step_shapes(pkg):
     assert L.gemm_plan(2560, 1536, 8960, 0, 2) == (128, 4, 1)  # down + residual: 84 us
     assert L.gemm_plan(2949, 1536, 8960, 0, 2) == (256, 2, 3)  # (288 tiles of 128)
     assert L.gemm_plan(2560, 1536, 17920, 1, 0) == (256, 2, 4)  # gate|up dX
-    assert L.gemm_plan(2560, 8960, 1536, 1, 0) == (128, 2, 1)  # down dX: 1,400 tiles
+    # down dX: two whole rounds of 256 x 256 tiles over the first 6,400 columns, the other
+    # 2,560 on 128 x 128 tiles (two workgroups per CU), instead of 1,400 tiles of 128 x 128
+    assert L.gemm_plan_split(2560, 8960, 1536, 1, 0) == (256, 2, 1, 2, 6400)
+    # gate|up with SwiGLU at 2,113 tokens: 9 x 70 tiles; 56 whole N tiles in two rounds
+    assert L.gemm_plan_split(2113, 8960, 1536, 0, 5) == (256, 2, 1, 2, 7168)
+    assert L.gemm_plan_split(2560, 8960, 1536, 0, 5) == (256, 2, 1, 0, 0)

@@ -380,7 +380,7 @@ def test_tile128_splits_and_tail_against_fp64(pkg, mode, epi, M, N, K):
             assert err < 1e-3
 
 
-@pytest.mark.parametrize("M", [1, 300, 1875, 2949])
+@pytest.mark.parametrize("M", [1, 300, 1875, 2113, 2949])
 def test_auto_plan_against_fp64(pkg, M):
     """qlora_gemm16 with its automatic plan (tile 0) at the step's nine products, every epilogue
     they use, against fp64 of the same operands; and the same bits on a second call."""
@@ -419,9 +419,56 @@ def test_auto_plan_against_fp64(pkg, M):
         assert err < 1e-3
 
 
+@pytest.mark.parametrize("mode,N,K,epi,M", [(0, 4096, 1536, 0, 4160), (0, 4096, 1536, 1, 4160),
+                                            (0, 4096, 1536, 2, 4160), (1, 4096, 1536, 0, 4160),
+                                            (1, 4096, 1536, 2, 4160), (0, 2048, 1536, 5, 4160),
+                                            (0, 8960, 1536, 5, 2113), (1, 8960, 1536, 0, 2113),
+                                            (0, 8960, 1536, 5, 1875), (0, 151936, 1536, 0, 2325)])
+def test_split_plan_equals_whole_tiles(pkg, mode, N, K, epi, M):
+    """The automatic plan's split (the leading columns in whole rounds of 256 x 256 tiles, the
+    rest as a second launch on 128 x 128 tiles) gives the same bits as one launch of whole
+    256 x 256 tiles without the K-sliced last round (both tile shapes sum each output's k-steps
+    in the same order), for every epilogue: store, bias, fp32 residual, SwiGLU with [g | u]."""
+    L = pkg.linear
+    plan = L.gemm_plan_split(M, N, K, mode, epi)
+    print(f"split plan M={M} N={N} K={K} mode={mode} epi={epi}: {plan}", flush=True)
+    assert plan[3] in (2, 4) and 0 < plan[4] < N
+    g = torch.Generator(device=DEV).manual_seed(M + N + epi)
+    wshape = (2 * N, K) if epi == 5 else ((N, K) if mode == 0 else (K, N))
+    w = (torch.randn(*wshape, generator=g, device=DEV) * 0.02).half()
+    a = torch.randn(M, K, generator=g, device=DEV).half()
+    kw = {}
+    if epi == 1:
+        kw["bias"] = (torch.randn(N, generator=g, device=DEV) * 0.1).half()
+    if epi == 2:
+        kw["resid"] = torch.randn(M, N, generator=g, device=DEV)
+    if epi == 5:
+        kw["swiglu_I"] = N
+    outs = []
+    for whole in (False, True):
+        if epi == 5:
+            kw["gu"] = torch.full((M, 2 * N), float("nan"), device=DEV, dtype=torch.float16)
+        plan_kw = dict(tile=256, stages=2, splits=1, tail=False) if whole else dict(tile=0)
+        out = L.hgemm(a, w, mode, epi=epi, **kw, **plan_kw)
+        outs.append((out, kw.get("gu")))
+    assert torch.equal(outs[0][0], outs[1][0])
+    if epi == 5:
+        assert torch.equal(outs[0][1], outs[1][1]) and not torch.isnan(outs[0][1]).any()
+    prod = a.double() @ (w.double().t() if mode == 0 else w.double())
+    if epi == 5:
+        gt, up = prod[:, :N].half().double(), prod[:, N:].half().double()
+        want = gt * torch.sigmoid(gt) * up
+    elif epi == 2:
+        want = kw["resid"].double() + prod.half().double()
+    else:
+        want = prod + (kw["bias"].double() if epi == 1 else 0)
+    assert rel_err(outs[0][0], want) < 1e-3
+
+
 @pytest.mark.parametrize("M,tile,stages,tail", [(2560, 256, 2, False), (2600, 256, 2, True),
                                                 (1875, 128, 2, True), (1875, 128, 2, False),
-                                                (700, 128, 4, False), (1, 0, 0, True)])
+                                                (700, 128, 4, False), (1, 0, 0, True),
+                                                (2113, 0, 0, True)])
 def test_swiglu_keep_epilogue(pkg, M, tile, stages, tail):
     """Epilogue 5: the SwiGLU output equals epilogue 3's bit for bit and the kept product
     [g | u] equals the plain GEMM's store of it bit for bit (each output sums the same k-steps
