@@ -24,7 +24,7 @@ SIGNATURES = {
     "qlora_dropout_keep": [P, I64, I64, I64, I64, F32, I32, P],
     "qlora_dropout_keep_below": [F32, P],
     "qlora_rms_fwd": [P, P, P, I32, P, P, P, P, P, P, I64, I64, F32, F32, F32, I64, I64, I64,
-                      I64, I32, I32, I32, I32, I32, P, P, P],
+                      I64, I32, I32, I32, I32, I32, P, P, P, P],
     "qlora_rms_bwd": [P, P, P, P, P, P, I32, P, P, P, P, I64, I64, I64, F32, F32, I64, I64,
                       I64, I64, F32, I32, I32, I32, I32, P, P, P],
     "qlora_rope_fwd": [P, P, P, P, P, I64, P, P, P, P, I64, I32, I32, I32, I32, F32, P],

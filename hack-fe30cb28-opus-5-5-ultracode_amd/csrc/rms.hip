@@ -35,6 +35,7 @@ struct RmsFwdArgs {
   int w_half;
   uint8_t* keep;          // u8 [n][2][ceil(H / 4)] keep bits (written when dropping) or null
   const int64_t* ctr_base = nullptr;  // device int64 added to ctr_q / ctr_v, or null
+  const uint8_t* keep_in = nullptr;   // keep bits an earlier pass stored: read, not drawn
 };
 
 struct RmsBwdArgs {
@@ -156,10 +157,15 @@ __global__ __launch_bounds__(kWave* kRowsPerBlock) void rms_fwd_kernel(RmsFwdArg
     if (a.y) store_h<W>(a.y + base + c * W, y);
     const uint64_t e0 = tok_e + (uint64_t)(c * W);
     uint8_t* kr = W == 4 && a.keep ? a.keep + row * 2 * keep_row_bytes(a.H) + c : nullptr;
+    // mask m's bits of these W elements from the stored bits (bit k of byte j: element 4 j + k)
+    auto stored = [&](int m) -> uint32_t {
+      const uint8_t* b = a.keep_in + (row * 2 + m) * keep_row_bytes(a.H);
+      return W == 4 ? (uint32_t)b[c] : ((uint32_t)b[(c * W) >> 2] >> ((c * W) & 3)) & 1u;
+    };
     if (a.yq) {
       DropParams d = a.drop;
       d.ctr = mask_ctr(a.ctr_q, a.ctr_base);
-      const uint32_t keep = keep_bits<W>(d, e0);
+      const uint32_t keep = a.keep_in ? stored(0) : keep_bits<W>(d, e0);
       float o[W];
 #pragma unroll
       for (int k = 0; k < W; ++k) o[k] = (keep >> k) & 1 ? y[k] * a.keep_scale : 0.f;
@@ -169,7 +175,7 @@ __global__ __launch_bounds__(kWave* kRowsPerBlock) void rms_fwd_kernel(RmsFwdArg
     if (a.yv) {
       DropParams d = a.drop;
       d.ctr = mask_ctr(a.ctr_v, a.ctr_base);
-      const uint32_t keep = keep_bits<W>(d, e0);
+      const uint32_t keep = a.keep_in ? stored(1) : keep_bits<W>(d, e0);
       float o[W];
 #pragma unroll
       for (int k = 0; k < W; ++k) o[k] = (keep >> k) & 1 ? y[k] * a.keep_scale : 0.f;
@@ -304,7 +310,15 @@ __global__ __launch_bounds__(kWave* kRowsPerBlock) void rms_fwd4_kernel(RmsFwdAr
   float4 wv[NV];
   load_w4<NV>(a.w, a.w_half, lane, wv);
   uint32_t kq[NV], kv[NV];
-  if constexpr (DROP) {  // the masks, while the loads are in flight (p = 0: all kept)
+  if (DROP && a.keep_in) {  // the masks an earlier pass stored as bits (a recompute)
+    const int64_t kb = a.H / 4;
+    const uint8_t* kr = a.keep_in + row * 2 * kb;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      kq[i] = a.yq ? (uint32_t)kr[lane + 64 * i] : 0u;
+      kv[i] = a.yv ? (uint32_t)kr[kb + lane + 64 * i] : 0u;
+    }
+  } else if constexpr (DROP) {  // the masks, while the loads are in flight (p = 0: all kept)
     const uint32_t G32 = (uint32_t)a.drop.G;
     const int vs = a.drop.vec == 8 ? 3 : 2;
     const bool all = a.drop.p_keep >= 1.0f;
@@ -619,10 +633,11 @@ QLORA_API int qlora_rms_fwd(const float* x, const void* delta, const void* w, in
                             float keep_scale, int64_t seed, int64_t ctr_q, int64_t ctr_v,
                             int64_t G, int32_t has_delta, int32_t write_y, int32_t drop_q,
                             int32_t drop_v, int32_t vec, uint8_t* keep,
-                            const int64_t* ctr_base, void* stream) {
+                            const uint8_t* keep_in, const int64_t* ctr_base, void* stream) {
   QLORA_CHECK_ARG(n >= 0 && H > 0);
   if (n == 0) return 0;
   QLORA_CHECK_ARG(x && w && rstd);
+  QLORA_CHECK_ARG(!(keep && keep_in) && (!keep_in || drop_q || drop_v));
   QLORA_CHECK_ARG(!has_delta || (delta && xsum));
   QLORA_CHECK_ARG(!write_y || y);
   QLORA_CHECK_ARG(!drop_q || yq);
@@ -635,6 +650,7 @@ QLORA_API int qlora_rms_fwd(const float* x, const void* delta, const void* w, in
                (drop_q || drop_v) ? tok : nullptr, n, H, eps, keep_scale, (uint64_t)ctr_q,
                (uint64_t)ctr_v, make_drop(seed, G, p_keep, vec), w_half};
   a.keep = drop_q || drop_v ? keep : nullptr;
+  a.keep_in = keep_in;
   a.ctr_base = ctr_base;
   const bool v4 = H % 4 == 0 && aligned(x, 16) && aligned(w, w_half ? 8 : 16) &&
                   (!a.delta || aligned(delta, 8)) && (!a.xsum || aligned(xsum, 16)) &&

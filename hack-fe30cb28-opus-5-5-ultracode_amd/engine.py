@@ -449,13 +449,14 @@ class Packed:
 # ---------------------------------------------------------------------------------------------
 # One decoder layer (engine.py:1054-1340)
 # ---------------------------------------------------------------------------------------------
-def attn_input_fwd(spec, h, packed, lora16, seeds, keep_bits=False, qkv=None):
+def attn_input_fwd(spec, h, packed, lora16, seeds, keep_bits=False, qkv=None, bits=None):
     """The attention-input block (engine.py:1073-1109): input RMSNorm with the two LoRA-dropout
     copies, the qkv projection (+ bias), the q/v LoRA products and RoPE. Returns q [n, HQ, D],
     k and v in grouped layout [n, HKV, D], and what attn_input_bwd reads. keep_bits: store the
     dropout masks as bits for the backward (else it draws them again). qkv: (q, k, v) kept from
     the forward (a backward's recompute): then only the norm and the LoRA inputs' products
-    the gradients read are formed again (no projection, no RoPE)."""
+    the gradients read are formed again (no projection, no RoPE). bits: the masks the forward
+    stored, which a recompute reads instead of drawing them again (and hands to the backward)."""
     n, H = h.shape
     aq_w, bq_w, av_w, bv_w = lora16
     s = _lora_scale(spec)
@@ -463,10 +464,14 @@ def attn_input_fwd(spec, h, packed, lora16, seeds, keep_bits=False, qkv=None):
     # adapters read the normed rows themselves
     drop = packed.dropout is not None
     drop_q, drop_v = drop and aq_w is not None, drop and av_w is not None
+    bits = bits if drop_q or drop_v else None
     kbits = (torch.empty(keep_bits_shape(n, H), device=h.device, dtype=torch.uint8)
-             if keep_bits and (drop_q or drop_v) else None)
+             if keep_bits and (drop_q or drop_v) and bits is None else None)
     _, a, aq, av, rstd1 = _rms_fwd(spec, h, spec.ln1, packed, seeds=seeds, drop_q=drop_q,
-                                   drop_v=drop_v, keep=kbits, write_y=qkv is None or not drop)
+                                   drop_v=drop_v, keep=kbits, keep_in=bits,
+                                   write_y=qkv is None or not drop)
+    if bits is not None:
+        kbits = bits
     if not drop:
         aq, av = (a if aq_w is not None else None), (a if av_w is not None else None)
     if qkv is not None:
@@ -524,8 +529,12 @@ def _layer_forward(spec, h, packed, lora16, seeds, keep, kept=None, save=()):
     D, HQ = spec.D, spec.HQ
     kept = kept or {}
     has_attn = "o" in kept
-    q, k, v, f = attn_input_fwd(spec, h, packed, lora16, seeds, keep_bits=keep,
-                                qkv=(kept["q"], kept["k"], kept["v"]) if has_attn else None)
+    # the dropout masks as bits: a keeping layer's backward reads them; a recomputing layer's
+    # forward stores them for its recompute, which reads them instead of drawing them again
+    q, k, v, f = attn_input_fwd(spec, h, packed, lora16, seeds,
+                                keep_bits=keep or "bits" in save,
+                                qkv=(kept["q"], kept["k"], kept["v"]) if has_attn else None,
+                                bits=kept.get("bits"))
     if has_attn:
         out, lse, aseed, aoffset, o = (kept[x] for x in ATTN_KEPT[3:])
     else:
@@ -537,6 +546,8 @@ def _layer_forward(spec, h, packed, lora16, seeds, keep, kept=None, save=()):
     saved = {}
     if not keep and "attn" in save:
         saved.update(q=q, k=k, v=v, out=out, lse=lse, aseed=aseed, aoffset=aoffset, o=o)
+    if not keep and f["keep"] is not None:
+        saved["bits"] = f["keep"]
     del o
     if keep:
         if gu is None:
@@ -590,7 +601,8 @@ class _Layer(torch.autograd.Function):
             # plan keeps it first, on the GPU or in host memory, engine.py:1204-1213, 430-445):
             # the backward then recomputes the forward up to the MLP input only
             save = (("gu",) if getattr(packed, "keep_gu", False) else ()) + \
-                (("attn",) if getattr(packed, "keep_attn", False) else ())
+                (("attn",) if getattr(packed, "keep_attn", False) else ()) + \
+                (("bits",) if getattr(packed, "keep_bits", False) else ())
             h3, ctx.saved_fwd = _layer_forward(spec, h, packed, lora16, seeds, keep=False,
                                                save=save)
             ctx.kept = None
@@ -797,6 +809,9 @@ class FusedQwen2:
         # products: the reference's AttnStream (engine.py:560-571), on by default there
         # (OFFLOAD_ATTN, patch.py:45-51) where host copies are fast enough; False: recompute
         self.keep_attn = True
+        # ... and the input norm's two LoRA-dropout masks as bits (H / 4 bytes a token), which
+        # the recompute reads instead of drawing them again with Philox (the same bits)
+        self.keep_bits = True
         self.dropout_p = cfg.lora_dropout
         self.rope = RopeTable(cfg.rope_theta, cfg.head_dim, self.device)
         self.dropout = TorchDropout(self.device, torch.float32) if self.dropout_p > 0 else None
@@ -917,6 +932,7 @@ class FusedQwen2:
         packed.keep_weights_recompute = self.keep_weights_recompute
         packed.keep_gu = self.keep_gu
         packed.keep_attn = self.keep_attn
+        packed.keep_bits = self.keep_bits
         for i, spec in enumerate(self.layers):
             h = _Layer.apply(h, spec, packed, i >= keep_from, *spec.lora_params())
         stats = HeadStats()

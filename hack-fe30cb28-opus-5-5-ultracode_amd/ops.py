@@ -501,10 +501,11 @@ def _ctr_base(packed, dev):
 
 
 def _rms_fwd(spec, x, weight, packed, *, delta=None, write_y=True, seeds=(0, 0),
-             drop_q=False, drop_v=False, keep=None):
+             drop_q=False, drop_v=False, keep=None, keep_in=None):
     """[x += delta] + RMSNorm -> (xsum, y fp16, yq, yv, rstd) (engine.py:947-966). With keep
     (uint8 keep_bits_shape(n, H)) the dropout masks are also stored there as bits, for
-    _rms_bwd to read instead of drawing them again."""
+    _rms_bwd to read instead of drawing them again; with keep_in the masks are read from bits
+    an earlier pass over the same rows stored (a recompute), not drawn."""
     _need(x, "x", torch.float32)
     n, H = x.shape
     dev = x.device
@@ -519,6 +520,9 @@ def _rms_fwd(spec, x, weight, packed, *, delta=None, write_y=True, seeds=(0, 0),
     yv = torch.empty((n, H), device=dev, dtype=torch.float16) if drop_v else None
     rstd = torch.empty((n,), device=dev, dtype=torch.float32)
     keep_p = _keep_arg(keep, n, H, dev)
+    keep_in_p = _keep_arg(keep_in, n, H, dev)
+    if keep_in_p is not None and (keep_p is not None or not (drop_q or drop_v)):
+        raise ValueError("keep_in reads the masks of a dropping pass that stores none itself")
     if n:
         tok, p_keep, keep_scale, seed, ctr_q, ctr_v, threads = _dropout_args(packed, x, seeds)
         vec = getattr(packed, "drop_vec", 4)
@@ -531,7 +535,7 @@ def _rms_fwd(spec, x, weight, packed, *, delta=None, write_y=True, seeds=(0, 0),
                   _ptr(rstd), _ptr(tok) if (drop_q or drop_v) else None, n, H,
                   float(spec.eps), p_keep, keep_scale, int(seed), int(ctr_q), int(ctr_v),
                   int(threads), int(delta is not None), int(write_y), int(drop_q), int(drop_v),
-                  int(vec), keep_p, _ctr_base(packed, dev), _stream(dev))
+                  int(vec), keep_p, keep_in_p, _ctr_base(packed, dev), _stream(dev))
     return xsum, y, yq, yv, rstd
 
 

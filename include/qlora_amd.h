@@ -100,6 +100,9 @@ int qlora_dropout_keep_below(float p_keep, uint32_t* out);
  *   keep (may be null) u8 [n][2][ceil(H/4)]: with dropout, the masks stored as bits (bit k of
  *   byte j of mask m = element 4j+k kept; m = 0 for yq, 1 for yv) for qlora_rms_bwd to read
  *   instead of drawing them again (no reference counterpart: the reference draws them twice).
+ *   keep_in (may be null; not with keep) u8 [n][2][ceil(H/4)]: with dropout, the masks read
+ *   from bits an earlier call over the same rows stored (a recompute), not drawn (no reference
+ *   counterpart).
  *   ctr_base (may be null) i64 [1] on the device: added to ctr_q and ctr_v (a step captured in
  *   a HIP graph passes its counters relative to the step's first, kept there; no reference
  *   counterpart).
@@ -109,7 +112,7 @@ int qlora_rms_fwd(const float* x, const void* delta, const void* w, int32_t w_ha
                   int64_t H, float eps, float p_keep, float keep_scale, int64_t seed,
                   int64_t ctr_q, int64_t ctr_v, int64_t G, int32_t has_delta, int32_t write_y,
                   int32_t drop_q, int32_t drop_v, int32_t vec, uint8_t* keep,
-                  const int64_t* ctr_base, void* stream);
+                  const uint8_t* keep_in, const int64_t* ctr_base, void* stream);
 
 /*
  * RMSNorm backward: g = w * (dy + keep_q * tq * keep_scale + keep_v * tv * keep_scale),

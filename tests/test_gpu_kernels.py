@@ -326,6 +326,16 @@ def test_rms_forward_backward(pkg, n, H, wdtype):
     dx5 = pkg.ops._rms_bwd(_Spec, dy.to(DEV), xsum, rstd, w.to(DEV), packed, dres=dres.to(DEV),
                            tq=tq.to(DEV), tv=tv.to(DEV), seeds=ctrs, grad_scale=0.5, keep=kb)
     assert torch.equal(dx5, dx)
+    # a recompute reads the stored bits instead of drawing the masks: the same outputs; bits
+    # that differ from the draw show through (all zero: every dropped copy zero)
+    _, y6, yq6, yv6, _ = pkg.ops._rms_fwd(_Spec, x.to(DEV), w.to(DEV), packed,
+                                          delta=delta.to(DEV), seeds=ctrs, drop_q=True,
+                                          drop_v=True, keep_in=kb)
+    assert torch.equal(y6, y) and torch.equal(yq6, yq) and torch.equal(yv6, yv)
+    _, _, yq7, yv7, _ = pkg.ops._rms_fwd(_Spec, x.to(DEV), w.to(DEV), packed,
+                                         delta=delta.to(DEV), seeds=ctrs, drop_q=True,
+                                         drop_v=True, keep_in=torch.zeros_like(kb))
+    assert not yq7.any() and not yv7.any()
 
 
 def _pack_keep(masks, n, H):

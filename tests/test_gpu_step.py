@@ -101,17 +101,20 @@ def test_step_other_model_shapes(pkg, H, HQ, HKV, D, r):
 
 def test_kept_tensors_equal_recomputing_them(pkg):
     """A recomputing layer keeps its [gate|up] product (keep_gu), its attention tensors
-    (keep_attn: q, k, v, output, log-sum-exp, o_proj output) and its dequantized weights
-    (keep_weights_recompute) from the forward instead of forming them again in its backward:
-    the same loss and LoRA gradients bit for bit in every combination (what is kept is the same
-    bits as what the recompute forms)."""
+    (keep_attn: q, k, v, output, log-sum-exp, o_proj output), its dequantized weights
+    (keep_weights_recompute) and its input norm's dropout masks as bits (keep_bits) from the
+    forward instead of forming them again in its backward: the same loss and LoRA gradients
+    bit for bit in every combination (what is kept is the same bits as what the recompute
+    forms)."""
     out = []
-    for keep_gu, keep_attn, keep_w in ((True, True, True), (False, False, False),
-                                       (True, False, True), (False, True, False),
-                                       (True, True, False)):
+    for keep_gu, keep_attn, keep_w, keep_b in ((True, True, True, True),
+                                               (False, False, False, False),
+                                               (True, False, True, False),
+                                               (False, True, False, True),
+                                               (True, True, False, True)):
         model = _tiny(pkg, H=512, HQ=8, HKV=2, D=64)
         model.keep_all, model.keep_gu, model.keep_attn = False, keep_gu, keep_attn
-        model.keep_weights_recompute = keep_w
+        model.keep_weights_recompute, model.keep_bits = keep_w, keep_b
         lengths = [17, 60, 33, 5]
         ids, mask, labels = _batch(lengths, model.cfg.vocab_size)
         denom = float((labels[:, 1:] != -100).sum())
