@@ -26,7 +26,7 @@ SIGNATURES = {
     "qlora_rms_fwd": [P, P, P, I32, P, P, P, P, P, P, I64, I64, F32, F32, F32, I64, I64, I64,
                       I64, I32, I32, I32, I32, I32, P, P, P, P],
     "qlora_rms_bwd": [P, P, P, P, P, P, I32, P, P, P, P, I64, I64, I64, F32, F32, I64, I64,
-                      I64, I64, F32, I32, I32, I32, I32, P, P, P],
+                      I64, I64, F32, I32, I32, I32, I32, P, P, P, F32, P],
     "qlora_rope_fwd": [P, P, P, P, P, I64, P, P, P, P, I64, I32, I32, I32, I32, F32, P],
     "qlora_rope_bwd": [P, P, P, P, P, I64, P, P, I64, I32, I32, I32, I32, P],
     "qlora_glu_fwd": [P, P, I64, I64, P],

@@ -56,6 +56,10 @@ struct RmsBwdArgs {
   int w_half;
   const uint8_t* keep;  // keep bits stored by the forward, or null: draw them again
   const int64_t* ctr_base = nullptr;  // device int64 added to ctr_q / ctr_v, or null
+  // fp16 [n, H] or null: the forward's input was x + f32(xdelta) and its rstd is formed here
+  // again (the forward's order of operations, the same bits), rstd then not read
+  const uint16_t* xdelta = nullptr;
+  float eps = 0.f;
 };
 
 // The counter of a mask: the launch's argument plus, when the caller keeps the step's first
@@ -192,7 +196,30 @@ __global__ __launch_bounds__(kWave* kRowsPerBlock) void rms_bwd_kernel(RmsBwdArg
   if (row >= a.n) return;
   const int64_t base = row * a.H;
   const int64_t chunks = a.H / W;
-  const float rstd = a.rstd[row];
+  float xs[NV][W];  // with xdelta: the forward's input x + delta, and rstd formed from it
+  float rstd;
+  if (a.xdelta) {
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int64_t c = lane + (int64_t)i * kWave;
+#pragma unroll
+      for (int k = 0; k < W; ++k) xs[i][k] = 0.f;
+      if (c < chunks) {
+        float d[W];
+        load_f32<W>(a.x + base + c * W, xs[i]);
+        load_h<W>(a.xdelta + base + c * W, d);
+#pragma unroll
+        for (int k = 0; k < W; ++k) xs[i][k] += d[k];
+#pragma unroll
+        for (int k = 0; k < W; ++k) ss += xs[i][k] * xs[i][k];
+      }
+    }
+    ss = wave_sum(ss);
+    rstd = 1.0f / sqrtf(ss / (float)a.H + a.eps);
+  } else {
+    rstd = a.rstd[row];
+  }
   const uint64_t tok_e = a.tok ? (uint64_t)a.tok[row] * (uint64_t)a.H : 0;
   float g[NV][W], xh[NV][W];
   float dot = 0.f;
@@ -226,7 +253,12 @@ __global__ __launch_bounds__(kWave* kRowsPerBlock) void rms_bwd_kernel(RmsBwdArg
     }
     float wv[W], xv[W];
     load_w<W>(a.w, a.w_half, c * W, wv);
-    load_f32<W>(a.x + base + c * W, xv);
+    if (a.xdelta) {
+#pragma unroll
+      for (int k = 0; k < W; ++k) xv[k] = xs[i][k];
+    } else {
+      load_f32<W>(a.x + base + c * W, xv);
+    }
 #pragma unroll
     for (int k = 0; k < W; ++k) {
       g[i][k] = dy[k] * wv[k];
@@ -393,7 +425,7 @@ __global__ __launch_bounds__(kWave* kRowsPerBlock) void rms_fwd4_kernel(RmsFwdAr
   }
 }
 
-template <int NV, bool DROP, bool RES>
+template <int NV, bool DROP, bool RES, bool XD = false>
 __global__ __launch_bounds__(kWave* kRowsPerBlock) void rms_bwd4_kernel(RmsBwdArgs a) {
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t row =  // wave-uniform, as the forward
@@ -401,13 +433,14 @@ __global__ __launch_bounds__(kWave* kRowsPerBlock) void rms_bwd4_kernel(RmsBwdAr
   if (row >= a.n) return;
   const int64_t base = row * a.H;
   const uint32_t tok_e = DROP && !a.keep ? (uint32_t)a.tok[row] * (uint32_t)a.H : 0u;
-  uint2 dyr[NV], tqr[NV], tvr[NV];
+  uint2 dyr[NV], tqr[NV], tvr[NV], xdr[NV];
   float4 x[NV], r[NV];
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int64_t col = 4 * (lane + 64 * i);
     dyr[i] = *reinterpret_cast<const uint2*>(a.dy + row * a.dy_stride + col);
     x[i] = *reinterpret_cast<const float4*>(a.x + base + col);
+    if constexpr (XD) xdr[i] = *reinterpret_cast<const uint2*>(a.xdelta + base + col);
     if constexpr (DROP) {
       tqr[i] = *reinterpret_cast<const uint2*>(a.tq + base + col);
       tvr[i] = *reinterpret_cast<const uint2*>(a.tv + base + col);
@@ -416,7 +449,26 @@ __global__ __launch_bounds__(kWave* kRowsPerBlock) void rms_bwd4_kernel(RmsBwdAr
   }
   float4 wv[NV];
   load_w4<NV>(a.w, a.w_half, lane, wv);
-  const float rstd = a.rstd[row];
+  float rstd;
+  if constexpr (XD) {  // the forward's x += delta and rstd, in its order of operations
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const float4 d = h4(xdr[i]);
+      x[i].x += d.x;
+      x[i].y += d.y;
+      x[i].z += d.z;
+      x[i].w += d.w;
+      ss += x[i].x * x[i].x;
+      ss += x[i].y * x[i].y;
+      ss += x[i].z * x[i].z;
+      ss += x[i].w * x[i].w;
+    }
+    ss = wave_sum(ss);
+    rstd = 1.0f / sqrtf(ss / (float)a.H + a.eps);
+  } else {
+    rstd = a.rstd[row];
+  }
   uint32_t kq[NV], kv[NV];
   if (DROP && a.keep) {  // the forward's masks
     const int64_t kb = a.H / 4;
@@ -549,7 +601,16 @@ void fwd4_launch(dim3 g, hipStream_t s, const RmsFwdArgs& a, bool delta, bool dr
 template <int NV>
 void bwd4_launch(dim3 g, hipStream_t s, const RmsBwdArgs& a, bool drop, bool res) {
   const dim3 b(kWave * kRowsPerBlock);
-  if (drop && res) hipLaunchKernelGGL((rms_bwd4_kernel<NV, true, true>), g, b, 0, s, a);
+  // the input x + xdelta (the post-attention norm's backward after a recompute)
+  if (a.xdelta && !drop && res)
+    hipLaunchKernelGGL((rms_bwd4_kernel<NV, false, true, true>), g, b, 0, s, a);
+  else if (a.xdelta && !drop)
+    hipLaunchKernelGGL((rms_bwd4_kernel<NV, false, false, true>), g, b, 0, s, a);
+  else if (a.xdelta && res)
+    hipLaunchKernelGGL((rms_bwd4_kernel<NV, true, true, true>), g, b, 0, s, a);
+  else if (a.xdelta)
+    hipLaunchKernelGGL((rms_bwd4_kernel<NV, true, false, true>), g, b, 0, s, a);
+  else if (drop && res) hipLaunchKernelGGL((rms_bwd4_kernel<NV, true, true>), g, b, 0, s, a);
   else if (drop) hipLaunchKernelGGL((rms_bwd4_kernel<NV, true, false>), g, b, 0, s, a);
   else if (res) hipLaunchKernelGGL((rms_bwd4_kernel<NV, false, true>), g, b, 0, s, a);
   else hipLaunchKernelGGL((rms_bwd4_kernel<NV, false, false>), g, b, 0, s, a);
@@ -687,10 +748,11 @@ QLORA_API int qlora_rms_bwd(const void* dy, const void* tq, const void* tv, cons
                             int64_t dy_stride, float p_keep, float keep_scale, int64_t seed,
                             int64_t ctr_q, int64_t ctr_v, int64_t G, float grad_scale,
                             int32_t drop_q, int32_t drop_v, int32_t has_res, int32_t vec,
-                            const uint8_t* keep, const int64_t* ctr_base, void* stream) {
+                            const uint8_t* keep, const int64_t* ctr_base, const void* xdelta,
+                            float eps, void* stream) {
   QLORA_CHECK_ARG(n >= 0 && H > 0);
   if (n == 0) return 0;
-  QLORA_CHECK_ARG(dy && x && rstd && w && dx && dy_stride >= H);
+  QLORA_CHECK_ARG(dy && x && (rstd || xdelta) && w && dx && dy_stride >= H);
   QLORA_CHECK_ARG(!drop_q || tq);
   QLORA_CHECK_ARG(!drop_v || tv);
   QLORA_CHECK_ARG(!has_res || dres);
@@ -704,7 +766,10 @@ QLORA_API int qlora_rms_bwd(const void* dy, const void* tq, const void* tv, cons
                make_drop(seed, G, p_keep, vec), w_half};
   a.keep = drop_q || drop_v ? keep : nullptr;  // the one-column kernel draws the masks again
   a.ctr_base = ctr_base;
+  a.xdelta = static_cast<const uint16_t*>(xdelta);
+  a.eps = eps;
   const bool v4 = H % 4 == 0 && dy_stride % 4 == 0 && aligned(dy, 8) && aligned(x, 16) &&
+                  (!xdelta || aligned(xdelta, 8)) &&
                   aligned(w, w_half ? 8 : 16) && aligned(dx, 16) &&
                   (!a.tq || aligned(tq, 8)) && (!a.tv || aligned(tv, 8)) &&
                   (!a.dres || aligned(dres, 16));

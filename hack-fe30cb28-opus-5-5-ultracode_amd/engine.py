@@ -541,6 +541,12 @@ def _layer_forward(spec, h, packed, lora16, seeds, keep, kept=None, save=()):
         out, lse, aseed, aoffset = _attn_fwd(q, k, v, packed, spec.scale)
         o = L.nf4_linear(out.reshape(n, HQ * D), spec.w["o_proj"])
     gu = kept.get("gu")
+    if keep and gu is not None and getattr(packed, "norm_in_bwd", False):
+        # a recompute with the [gate|up] product kept needs the post-attention norm only for
+        # its backward, which forms h2 = h + o and its rstd itself (the same bits)
+        f.update(q=q, k=k, v=v, out=out, lse=lse, aseed=aseed, aoffset=aoffset, h2=None,
+                 rstd2=None, o2=o, gu=gu)
+        return None, f
     h2, b, _, _, rstd2 = _rms_fwd(spec, h, spec.ln2, packed, delta=o,
                                   write_y=not (keep and gu is not None))
     saved = {}
@@ -646,8 +652,10 @@ class _Layer(torch.autograd.Function):
         db = L.nf4_linear_t(gu, spec.gu)
         del gu
         dh2_16 = torch.empty((n, H), device=h.device, dtype=torch.float16)
-        dh2 = _rms_bwd(spec, db, f.pop("h2"), f.pop("rstd2"), spec.ln2, packed, dres=dh3,
-                       out16=dh2_16)
+        h2, o2 = f.pop("h2"), f.pop("o2", None)
+        dh2 = _rms_bwd(spec, db, h if h2 is None else h2, f.pop("rstd2"), spec.ln2, packed,
+                       dres=dh3, out16=dh2_16, xdelta=o2 if h2 is None else None)
+        del h2, o2
         del db, dh3
         dout = L.nf4_linear_t(dh2_16, spec.w["o_proj"]).view(n, HQ, D)
         del dh2_16
@@ -812,6 +820,10 @@ class FusedQwen2:
         # ... and the input norm's two LoRA-dropout masks as bits (H / 4 bytes a token), which
         # the recompute reads instead of drawing them again with Philox (the same bits)
         self.keep_bits = True
+        # the recompute's post-attention norm (h2 = h + o and its rstd: the [gate|up] product
+        # kept, nothing else reads them) formed inside that norm's backward kernel rather than
+        # by a forward launch of its own (the same bits)
+        self.norm_in_bwd = True
         self.dropout_p = cfg.lora_dropout
         self.rope = RopeTable(cfg.rope_theta, cfg.head_dim, self.device)
         self.dropout = TorchDropout(self.device, torch.float32) if self.dropout_p > 0 else None
@@ -933,6 +945,7 @@ class FusedQwen2:
         packed.keep_gu = self.keep_gu
         packed.keep_attn = self.keep_attn
         packed.keep_bits = self.keep_bits
+        packed.norm_in_bwd = self.norm_in_bwd
         for i, spec in enumerate(self.layers):
             h = _Layer.apply(h, spec, packed, i >= keep_from, *spec.lora_params())
         stats = HeadStats()

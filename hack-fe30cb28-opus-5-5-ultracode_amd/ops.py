@@ -540,17 +540,24 @@ def _rms_fwd(spec, x, weight, packed, *, delta=None, write_y=True, seeds=(0, 0),
 
 
 def _rms_bwd(spec, dy, x, rstd, weight, packed, *, dres=None, tq=None, tv=None, seeds=(0, 0),
-             grad_scale=1.0, out=None, out16=None, keep=None):
+             grad_scale=1.0, out=None, out16=None, keep=None, xdelta=None):
     """RMSNorm backward with the LoRA-dropout gradients merged (engine.py:969-981). With out16
     (fp16 [n, H]) the kernel also writes fp16(dx) there, the operand the next backward product
     rounds the gradient to. keep: the masks _rms_fwd stored for these rows (same packed and
-    seeds), or None to draw them again."""
+    seeds), or None to draw them again. xdelta (fp16 [n, H]): the forward normed x + xdelta
+    (_rms_fwd with delta); the kernel forms that sum and its rstd again, in the forward's order
+    of operations (the same bits), and rstd is not read (may be None)."""
     _need(x, "x", torch.float32)
     n, H = x.shape
     dev = x.device
     w_half = _weight_arg(weight, H, dev)
     dy_stride = _rows_view(dy, "dy", torch.float16, n, H, dev) if n else H
-    _need(rstd, "rstd", torch.float32, dev)
+    if xdelta is not None:
+        _need(xdelta, "xdelta", torch.float16, dev)
+        if xdelta.shape != x.shape:
+            raise ValueError("xdelta must match x")
+    else:
+        _need(rstd, "rstd", torch.float32, dev)
     for t, name in ((tq, "tq"), (tv, "tv")):
         if t is not None:
             _need(t, name, torch.float16, dev)
@@ -577,7 +584,8 @@ def _rms_bwd(spec, dy, x, rstd, weight, packed, *, dres=None, tq=None, tv=None, 
                   _ptr(tok) if (tq is not None or tv is not None) else None, n, H, dy_stride,
                   p_keep, keep_scale, int(seed), int(ctr_q), int(ctr_v), int(threads),
                   float(grad_scale), int(tq is not None), int(tv is not None),
-                  int(dres is not None), int(vec), keep_p, _ctr_base(packed, dev), _stream(dev))
+                  int(dres is not None), int(vec), keep_p, _ctr_base(packed, dev),
+                  _ptr(xdelta), float(spec.eps), _stream(dev))
     return dx
 
 

@@ -124,13 +124,18 @@ int qlora_rms_fwd(const float* x, const void* delta, const void* w, int32_t w_ha
  *   keep (may be null) u8 [n][2][ceil(H/4)]: the masks qlora_rms_fwd stored for these rows
  *   (same tok, seed, counters and drop_q/drop_v); null: drawn again from (seed, ctr_q, ctr_v).
  *   ctr_base (may be null): as qlora_rms_fwd's.
+ *   xdelta (may be null) f16 [n,H]: the forward normed x + f32(xdelta) (qlora_rms_fwd with
+ *   delta); the kernel forms that sum and rstd = 1/sqrt(mean(x^2)+eps) again in the forward's
+ *   order of operations (the same bits) and does not read rstd (may then be null). No reference
+ *   counterpart: a recompute's post-attention norm folded into its backward.
  */
 int qlora_rms_bwd(const void* dy, const void* tq, const void* tv, const float* x,
                   const float* rstd, const void* w, int32_t w_half, const float* dres, float* dx,
                   void* dx16, const int64_t* tok, int64_t n, int64_t H, int64_t dy_stride,
                   float p_keep, float keep_scale, int64_t seed, int64_t ctr_q, int64_t ctr_v,
                   int64_t G, float grad_scale, int32_t drop_q, int32_t drop_v, int32_t has_res,
-                  int32_t vec, const uint8_t* keep, const int64_t* ctr_base, void* stream);
+                  int32_t vec, const uint8_t* keep, const int64_t* ctr_base, const void* xdelta,
+                  float eps, void* stream);
 
 /*
  * qkv split + LoRA deltas + rotate-half RoPE. q = f16(rope(qkv_q + s*lq)),

@@ -314,6 +314,16 @@ def test_rms_forward_backward(pkg, n, H, wdtype):
                            tq=tq.to(DEV), tv=tv.to(DEV), seeds=ctrs, grad_scale=0.5, out16=dx16)
     assert torch.equal(dx3, dx)
     assert torch.equal(dx16.view(torch.int16), dx.half().view(torch.int16))
+    # the input given as x + delta (the forward's sum and rstd formed in the backward kernel):
+    # the same bits as from the forward's xsum and rstd
+    dx8 = pkg.ops._rms_bwd(_Spec, dy.to(DEV), x.to(DEV), None, w.to(DEV), packed,
+                           dres=dres.to(DEV), tq=tq.to(DEV), tv=tv.to(DEV), seeds=ctrs,
+                           grad_scale=0.5, xdelta=delta.to(DEV))
+    assert torch.equal(dx8, dx)
+    dxn = pkg.ops._rms_bwd(_Spec, dy.to(DEV), xsum, rstd, w.to(DEV), packed, dres=dres.to(DEV))
+    dxn2 = pkg.ops._rms_bwd(_Spec, dy.to(DEV), x.to(DEV), None, w.to(DEV), packed,
+                            dres=dres.to(DEV), xdelta=delta.to(DEV))
+    assert torch.equal(dxn, dxn2)
     # the masks stored as bits by the forward: the oracle's masks, the same outputs, and a
     # backward that reads them equals the one that draws them again, bit for bit
     kb = torch.full(pkg.ops.keep_bits_shape(n, H), 0xAA, dtype=torch.uint8, device=DEV)
