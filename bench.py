@@ -608,7 +608,8 @@ def main():
     kernels = measure_step_kernels(pkg, trainer, batches[-4:], cfg)
     full = None
     if args.keep_steps > 0 and args.policy != "keep":
-        model.keep_gu = model.keep_attn = model.keep_weights_recompute = model.keep_bits = False
+        model.keep_gu = model.keep_attn = model.keep_weights_recompute = False
+        model.keep_bits = model.keep_lora_x = False
         time_steps(trainer, batches, 0, 2)
         ftok, fel, _ = time_steps(trainer, batches, args.warmup, args.keep_steps)
         full = {"value": ftok / fel, "ms_per_step": 1000.0 * fel / args.keep_steps,
@@ -616,7 +617,8 @@ def main():
                 "what": "every layer recomputes its whole forward from its input in backward "
                         "(the [gate|up] product, the attention tensors and the dequantized "
                         "weights formed again)"}
-        model.keep_gu = model.keep_attn = model.keep_weights_recompute = model.keep_bits = True
+        model.keep_gu = model.keep_attn = model.keep_weights_recompute = True
+        model.keep_bits = model.keep_lora_x = True
         log(f"full recompute: {full['value']:.0f} tokens/s")
     keep = None
     if args.keep_steps > 0 and args.policy != "keep":

@@ -449,14 +449,16 @@ class Packed:
 # ---------------------------------------------------------------------------------------------
 # One decoder layer (engine.py:1054-1340)
 # ---------------------------------------------------------------------------------------------
-def attn_input_fwd(spec, h, packed, lora16, seeds, keep_bits=False, qkv=None, bits=None):
+def attn_input_fwd(spec, h, packed, lora16, seeds, keep_bits=False, qkv=None, bits=None,
+                   lora_x=None):
     """The attention-input block (engine.py:1073-1109): input RMSNorm with the two LoRA-dropout
     copies, the qkv projection (+ bias), the q/v LoRA products and RoPE. Returns q [n, HQ, D],
     k and v in grouped layout [n, HKV, D], and what attn_input_bwd reads. keep_bits: store the
     dropout masks as bits for the backward (else it draws them again). qkv: (q, k, v) kept from
     the forward (a backward's recompute): then only the norm and the LoRA inputs' products
     the gradients read are formed again (no projection, no RoPE). bits: the masks the forward
-    stored, which a recompute reads instead of drawing them again (and hands to the backward)."""
+    stored, which a recompute reads instead of drawing them again (and hands to the backward).
+    lora_x: the forward's rank-r products (xq, xv) with qkv (not formed again)."""
     n, H = h.shape
     aq_w, bq_w, av_w, bv_w = lora16
     s = _lora_scale(spec)
@@ -476,7 +478,10 @@ def attn_input_fwd(spec, h, packed, lora16, seeds, keep_bits=False, qkv=None, bi
         aq, av = (a if aq_w is not None else None), (a if av_w is not None else None)
     if qkv is not None:
         del a
-        xq, xv, _, _ = _lora_fwd_rows(aq, av, aq_w, bq_w, av_w, bv_w, need_l=False)
+        if lora_x is not None:
+            xq, xv = lora_x
+        else:
+            xq, xv, _, _ = _lora_fwd_rows(aq, av, aq_w, bq_w, av_w, bv_w, need_l=False)
         q, k, v = qkv
         return q, k, v, dict(rstd1=rstd1, aq=aq, av=av, xq=xq, xv=xv, keep=kbits)
     proj = L.nf4_linear(a, spec.qkv, bias=spec.bias_qkv)
@@ -534,7 +539,7 @@ def _layer_forward(spec, h, packed, lora16, seeds, keep, kept=None, save=()):
     q, k, v, f = attn_input_fwd(spec, h, packed, lora16, seeds,
                                 keep_bits=keep or "bits" in save,
                                 qkv=(kept["q"], kept["k"], kept["v"]) if has_attn else None,
-                                bits=kept.get("bits"))
+                                bits=kept.get("bits"), lora_x=kept.get("lora_x"))
     if has_attn:
         out, lse, aseed, aoffset, o = (kept[x] for x in ATTN_KEPT[3:])
     else:
@@ -554,6 +559,8 @@ def _layer_forward(spec, h, packed, lora16, seeds, keep, kept=None, save=()):
         saved.update(q=q, k=k, v=v, out=out, lse=lse, aseed=aseed, aoffset=aoffset, o=o)
     if not keep and f["keep"] is not None:
         saved["bits"] = f["keep"]
+    if not keep and "lora_x" in save and "attn" in save:
+        saved["lora_x"] = (f["xq"], f["xv"])
     del o
     if keep:
         if gu is None:
@@ -608,7 +615,8 @@ class _Layer(torch.autograd.Function):
             # the backward then recomputes the forward up to the MLP input only
             save = (("gu",) if getattr(packed, "keep_gu", False) else ()) + \
                 (("attn",) if getattr(packed, "keep_attn", False) else ()) + \
-                (("bits",) if getattr(packed, "keep_bits", False) else ())
+                (("bits",) if getattr(packed, "keep_bits", False) else ()) + \
+                (("lora_x",) if getattr(packed, "keep_lora_x", False) else ())
             h3, ctx.saved_fwd = _layer_forward(spec, h, packed, lora16, seeds, keep=False,
                                                save=save)
             ctx.kept = None
@@ -824,6 +832,9 @@ class FusedQwen2:
         # kept, nothing else reads them) formed inside that norm's backward kernel rather than
         # by a forward launch of its own (the same bits)
         self.norm_in_bwd = True
+        # ... and its LoRA inputs' rank-r products x = drop(a) A^T (2 r fp16 a token), so a
+        # recompute with the attention tensors kept forms only the input norm again
+        self.keep_lora_x = True
         self.dropout_p = cfg.lora_dropout
         self.rope = RopeTable(cfg.rope_theta, cfg.head_dim, self.device)
         self.dropout = TorchDropout(self.device, torch.float32) if self.dropout_p > 0 else None
@@ -946,6 +957,7 @@ class FusedQwen2:
         packed.keep_attn = self.keep_attn
         packed.keep_bits = self.keep_bits
         packed.norm_in_bwd = self.norm_in_bwd
+        packed.keep_lora_x = self.keep_lora_x
         for i, spec in enumerate(self.layers):
             h = _Layer.apply(h, spec, packed, i >= keep_from, *spec.lora_params())
         stats = HeadStats()

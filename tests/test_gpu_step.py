@@ -104,17 +104,20 @@ def test_kept_tensors_equal_recomputing_them(pkg):
     (keep_attn: q, k, v, output, log-sum-exp, o_proj output), its dequantized weights
     (keep_weights_recompute) and its input norm's dropout masks as bits (keep_bits) from the
     forward instead of forming them again in its backward, whose post-attention norm may be
-    formed inside that norm's backward (norm_in_bwd): the same loss and LoRA gradients bit for
-    bit in every combination (what is kept is the same bits as what the recompute forms)."""
+    formed inside that norm's backward (norm_in_bwd), and its LoRA inputs' rank-r products
+    (keep_lora_x): the same loss and LoRA gradients bit for bit in every combination (what is
+    kept is the same bits as what the recompute forms)."""
     out = []
-    for keep_gu, keep_attn, keep_w, keep_b, nib in ((True, True, True, True, True),
-                                                    (False, False, False, False, False),
-                                                    (True, False, True, False, True),
-                                                    (False, True, False, True, True),
-                                                    (True, True, False, True, False)):
+    for keep_gu, keep_attn, keep_w, keep_b, nib, kx in ((True, True, True, True, True, True),
+                                                        (False, False, False, False, False,
+                                                         False),
+                                                        (True, False, True, False, True, True),
+                                                        (False, True, False, True, True, True),
+                                                        (True, True, False, True, False, False)):
         model = _tiny(pkg, H=512, HQ=8, HKV=2, D=64)
         model.keep_all, model.keep_gu, model.keep_attn = False, keep_gu, keep_attn
         model.keep_weights_recompute, model.keep_bits, model.norm_in_bwd = keep_w, keep_b, nib
+        model.keep_lora_x = kx
         lengths = [17, 60, 33, 5]
         ids, mask, labels = _batch(lengths, model.cfg.vocab_size)
         denom = float((labels[:, 1:] != -100).sum())
