@@ -26,7 +26,7 @@ SIGNATURES = {
     "qlora_rms_fwd": [P, P, P, I32, P, P, P, P, P, P, I64, I64, F32, F32, F32, I64, I64, I64,
                       I64, I32, I32, I32, I32, I32, P, P, P, P],
     "qlora_rms_bwd": [P, P, P, P, P, P, I32, P, P, P, P, I64, I64, I64, F32, F32, I64, I64,
-                      I64, I64, F32, I32, I32, I32, I32, P, P, P, F32, P],
+                      I64, I64, F32, I32, I32, I32, I32, P, P, P, F32, P, I32, P],
     "qlora_rope_fwd": [P, P, P, P, P, I64, P, P, P, P, I64, I32, I32, I32, I32, F32, P],
     "qlora_rope_bwd": [P, P, P, P, P, I64, P, P, I64, I32, I32, I32, I32, P],
     "qlora_glu_fwd": [P, P, I64, I64, P],
@@ -46,6 +46,7 @@ SIGNATURES = {
                          I32, P, I64, P],
     "qlora_gemm16_workspace": [I64, I64, I64, I32, I32, I32, I32, I32, P],
     "qlora_gemm16_plan": [I64, I64, I64, I32, I32, P, P, P],
+    "qlora_gemm16_parts": [P, I64, P, I64, I64, I64, I64, I32, I32, I32, I32, P, I64, P],
     "qlora_gemm16_plan_split": [I64, I64, I64, I32, I32, P, P, P, P, P],
     "qlora_resid_add": [P, P, P, I64, P],
     "qlora_lora_fwd_rows": [P, P, P, P, P, P, P, P, P, P, I64, I32, I32, I32, I32, P],

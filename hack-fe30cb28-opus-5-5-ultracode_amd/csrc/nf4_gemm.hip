@@ -1392,8 +1392,9 @@ int64_t n_tiles_of(int64_t N, int epi, int tile) {
 //   a rounds + b (the k elements its rounds walk) + c (MB of fp32 partials) + d (a reduce),
 // the constants (us) least-squares fits of every variant over the step's nine products and the
 // lm_head's at 1,024 - 4,096 tokens on MI355X (HIP graphs, warm caches; median error 5-8 %).
-// Candidates: 256 x 256 tiles in 1-6 K slices, 128 x 128 tiles in 1, 2 or 4 (up to K = 12,288:
-// beyond that the measurements favoured 256 x 256 tiles, whose loads per flop are half).
+// Candidates: 256 x 256 tiles in 1-8 K slices (7 or 8 fill the GPU when a long reduction has
+// 32-36 output tiles), 128 x 128 tiles in 1, 2 or 4 (up to K = 12,288: beyond that the
+// measurements favoured 256 x 256 tiles, whose loads per flop are half).
 struct PlanCoef {
   int tile, stages;
   double a, b, c, d;
@@ -1477,7 +1478,7 @@ void auto_plan(int64_t M, int64_t N, int64_t K, int mode, int epi, int* tile, in
   for (int pass = 0; pass < 2 && best < 0.0; ++pass) {
     for (const PlanCoef& v : kPlanCoef) {
       if (pass == 0 && v.tile == 128 && K > 12288) continue;
-      for (int sp = 1; sp <= (v.tile == 256 ? 6 : 4); ++sp) {
+      for (int sp = 1; sp <= (v.tile == 256 ? 8 : 4); ++sp) {
         if (v.tile == 128 && sp == 3) continue;
         const double c = plan_cost(M, N, K, mode, epi, v, sp);
         if (c >= 0.0 && (best < 0.0 || c < best)) {
@@ -1509,7 +1510,7 @@ void auto_plan(int64_t M, int64_t N, int64_t K, int mode, int epi, int* tile, in
 // start of the tile grid and the end of the last kernel.
 int run_gemm(GemmArgs& g, int bsrc, int mode, int epi, int splits, float* ws, int64_t ws_elems,
              hipStream_t s, hipEvent_t start = nullptr, hipEvent_t stop = nullptr,
-             int tile = 256, int stages = 2) {
+             int tile = 256, int stages = 2, bool parts_only = false) {
   QLORA_CHECK_ARG((tile == 256 && stages == 2) ||
                   (tile == 128 && bsrc == kBHalf && (stages == 2 || stages == 4)));
   g.bm = g.bn = tile;
@@ -1562,7 +1563,7 @@ int run_gemm(GemmArgs& g, int bsrc, int mode, int epi, int splits, float* ws, in
   const dim3 gdim((unsigned)(grid * splits));
   launch_any(g, bsrc, mode, tile, stages, gdim, s, kepi, start, splits > 1 ? nullptr : stop);
   int rc = qlora_launch_status();
-  if (rc != 0 || splits == 1) return rc;
+  if (rc != 0 || splits == 1 || parts_only) return rc;
   QLORA_CHECK_ARG(g.N % 4 == 0 && g.ldc % 4 == 0 && (epi != kEpiResid || g.ldr % 4 == 0));
   const int64_t quads = g.M * g.N / 4;
   const dim3 rgrid((unsigned)qlora_cdiv(quads, 256));
@@ -1747,6 +1748,35 @@ QLORA_API int qlora_gemm16(const void* a, int64_t lda, const void* b, int64_t ld
   return qlora_gemm16_timed(a, lda, b, ldb, M, N, K, mode, c, ldc, bias, resid, ldr, epi,
                             swiglu_I, gu, ldgu, tile, stages, splits, ws, ws_elems, stream,
                             nullptr, nullptr);
+}
+
+// The K slices of a split-K product left unsummed: ws [splits, M, N] fp32, slice k the sum over
+// its k-tiles, for a consumer that sums them itself in slice order (qlora_rms_bwd dy_parts).
+QLORA_API int qlora_gemm16_parts(const void* a, int64_t lda, const void* b, int64_t ldb,
+                                 int64_t M, int64_t N, int64_t K, int32_t mode, int32_t tile,
+                                 int32_t stages, int32_t splits, float* ws, int64_t ws_elems,
+                                 void* stream) {
+  QLORA_CHECK_ARG(M > 0 && N > 0 && K > 0 && a && b && ws && (mode == 0 || mode == 1));
+  QLORA_CHECK_ARG((tile == 256 && stages == 2) || (tile == 128 && (stages == 2 || stages == 4)));
+  QLORA_CHECK_ARG(splits >= 2 && splits <= 16);
+  QLORA_CHECK_ARG(K % (kStages * kBK) == 0 && (K / kBK64) % stages == 0);
+  QLORA_CHECK_ARG(mode == 0 ? N % 8 == 0 : N % tile == 0);
+  QLORA_CHECK_ARG(lda >= K && lda % 8 == 0 && al(a, 16) && al(b, 16) && ldb % 8 == 0);
+  QLORA_CHECK_ARG(mode == 0 ? ldb >= K : ldb >= N);
+  if (mode == 0) QLORA_CHECK_ARG(N * ldb * 2 < (1ll << 32));
+  QLORA_CHECK_ARG((int64_t)tile * lda * 2 < (1ll << 32) && 64 * ldb * 2 < (1ll << 32));
+  GemmArgs g{};
+  g.a = static_cast<const uint16_t*>(a);
+  g.lda = lda;
+  g.b = static_cast<const uint16_t*>(b);
+  g.ldb = ldb;
+  g.c = ws;
+  g.ldc = N;
+  g.M = M;
+  g.N = N;
+  g.Kr = K;
+  return run_gemm(g, kBHalf, mode, kEpiStore, splits, ws, ws_elems, (hipStream_t)stream,
+                  nullptr, nullptr, tile, stages, true);
 }
 
 // The fp32-output GEMM: c = alpha A op(B) (+ row-scaled resid), mode 1 A [M, K] x B [K, N],

@@ -60,6 +60,10 @@ struct RmsBwdArgs {
   // again (the forward's order of operations, the same bits), rstd then not read
   const uint16_t* xdelta = nullptr;
   float eps = 0.f;
+  // fp32 [nparts, n, H] or null: dy = fp16(the parts summed in order), the split-K product's
+  // slices (its reduce folded in here); dy is then not read
+  const float* dy_parts = nullptr;
+  int nparts = 0;
 };
 
 // The counter of a mask: the launch's argument plus, when the caller keeps the step's first
@@ -230,7 +234,19 @@ __global__ __launch_bounds__(kWave* kRowsPerBlock) void rms_bwd_kernel(RmsBwdArg
     for (int k = 0; k < W; ++k) g[i][k] = xh[i][k] = 0.f;
     if (c >= chunks) continue;
     float dy[W];
-    load_h<W>(a.dy + row * a.dy_stride + c * W, dy);
+    if (a.dy_parts) {  // fp16 of the K slices summed in slice order (the reduce's)
+      load_f32<W>(a.dy_parts + base + c * W, dy);
+      for (int kp = 1; kp < a.nparts; ++kp) {
+        float t[W];
+        load_f32<W>(a.dy_parts + (int64_t)kp * a.n * a.H + base + c * W, t);
+#pragma unroll
+        for (int k = 0; k < W; ++k) dy[k] += t[k];
+      }
+#pragma unroll
+      for (int k = 0; k < W; ++k) dy[k] = h2f_bits(f2h_bits(dy[k]));
+    } else {
+      load_h<W>(a.dy + row * a.dy_stride + c * W, dy);
+    }
     const uint64_t e0 = tok_e + (uint64_t)(c * W);
     const uint8_t* kr = W == 4 && a.keep ? a.keep + row * 2 * keep_row_bytes(a.H) + c : nullptr;
     if (a.tq) {
@@ -425,7 +441,7 @@ __global__ __launch_bounds__(kWave* kRowsPerBlock) void rms_fwd4_kernel(RmsFwdAr
   }
 }
 
-template <int NV, bool DROP, bool RES, bool XD = false>
+template <int NV, bool DROP, bool RES, bool XD = false, bool PARTS = false>
 __global__ __launch_bounds__(kWave* kRowsPerBlock) void rms_bwd4_kernel(RmsBwdArgs a) {
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t row =  // wave-uniform, as the forward
@@ -438,7 +454,7 @@ __global__ __launch_bounds__(kWave* kRowsPerBlock) void rms_bwd4_kernel(RmsBwdAr
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int64_t col = 4 * (lane + 64 * i);
-    dyr[i] = *reinterpret_cast<const uint2*>(a.dy + row * a.dy_stride + col);
+    if constexpr (!PARTS) dyr[i] = *reinterpret_cast<const uint2*>(a.dy + row * a.dy_stride + col);
     x[i] = *reinterpret_cast<const float4*>(a.x + base + col);
     if constexpr (XD) xdr[i] = *reinterpret_cast<const uint2*>(a.xdelta + base + col);
     if constexpr (DROP) {
@@ -446,6 +462,22 @@ __global__ __launch_bounds__(kWave* kRowsPerBlock) void rms_bwd4_kernel(RmsBwdAr
       tvr[i] = *reinterpret_cast<const uint2*>(a.tv + base + col);
     }
     if constexpr (RES) r[i] = *reinterpret_cast<const float4*>(a.dres + base + col);
+  }
+  if constexpr (PARTS) {  // dy = fp16 of the K slices summed in slice order (the reduce's)
+    float4 ps[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+      ps[i] = *reinterpret_cast<const float4*>(a.dy_parts + base + 4 * (lane + 64 * i));
+    for (int k = 1; k < a.nparts; ++k) {
+      const float* pk = a.dy_parts + (int64_t)k * a.n * a.H + base;
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const float4 t = *reinterpret_cast<const float4*>(pk + 4 * (lane + 64 * i));
+        ps[i].x += t.x; ps[i].y += t.y; ps[i].z += t.z; ps[i].w += t.w;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < NV; ++i) dyr[i] = pack4(ps[i].x, ps[i].y, ps[i].z, ps[i].w);
   }
   float4 wv[NV];
   load_w4<NV>(a.w, a.w_half, lane, wv);
@@ -601,6 +633,18 @@ void fwd4_launch(dim3 g, hipStream_t s, const RmsFwdArgs& a, bool delta, bool dr
 template <int NV>
 void bwd4_launch(dim3 g, hipStream_t s, const RmsBwdArgs& a, bool drop, bool res) {
   const dim3 b(kWave * kRowsPerBlock);
+  // dy from split-K slices (the post-attention norm's backward: no dropout)
+  if (a.dy_parts && !drop) {
+    if (a.xdelta && res)
+      hipLaunchKernelGGL((rms_bwd4_kernel<NV, false, true, true, true>), g, b, 0, s, a);
+    else if (a.xdelta)
+      hipLaunchKernelGGL((rms_bwd4_kernel<NV, false, false, true, true>), g, b, 0, s, a);
+    else if (res)
+      hipLaunchKernelGGL((rms_bwd4_kernel<NV, false, true, false, true>), g, b, 0, s, a);
+    else
+      hipLaunchKernelGGL((rms_bwd4_kernel<NV, false, false, false, true>), g, b, 0, s, a);
+    return;
+  }
   // the input x + xdelta (the post-attention norm's backward after a recompute)
   if (a.xdelta && !drop && res)
     hipLaunchKernelGGL((rms_bwd4_kernel<NV, false, true, true>), g, b, 0, s, a);
@@ -749,10 +793,11 @@ QLORA_API int qlora_rms_bwd(const void* dy, const void* tq, const void* tv, cons
                             int64_t ctr_q, int64_t ctr_v, int64_t G, float grad_scale,
                             int32_t drop_q, int32_t drop_v, int32_t has_res, int32_t vec,
                             const uint8_t* keep, const int64_t* ctr_base, const void* xdelta,
-                            float eps, void* stream) {
+                            float eps, const float* dy_parts, int32_t nparts, void* stream) {
   QLORA_CHECK_ARG(n >= 0 && H > 0);
   if (n == 0) return 0;
-  QLORA_CHECK_ARG(dy && x && (rstd || xdelta) && w && dx && dy_stride >= H);
+  QLORA_CHECK_ARG((dy || dy_parts) && x && (rstd || xdelta) && w && dx && dy_stride >= H);
+  QLORA_CHECK_ARG(!dy_parts || (nparts >= 1 && nparts <= 16 && !drop_q && !drop_v));
   QLORA_CHECK_ARG(!drop_q || tq);
   QLORA_CHECK_ARG(!drop_v || tv);
   QLORA_CHECK_ARG(!has_res || dres);
@@ -768,7 +813,11 @@ QLORA_API int qlora_rms_bwd(const void* dy, const void* tq, const void* tv, cons
   a.ctr_base = ctr_base;
   a.xdelta = static_cast<const uint16_t*>(xdelta);
   a.eps = eps;
-  const bool v4 = H % 4 == 0 && dy_stride % 4 == 0 && aligned(dy, 8) && aligned(x, 16) &&
+  a.dy_parts = dy_parts;
+  a.nparts = dy_parts ? nparts : 0;
+  const bool v4 = H % 4 == 0 && dy_stride % 4 == 0 && (dy_parts ? aligned(dy_parts, 16)
+                                                                 : aligned(dy, 8)) &&
+                  aligned(x, 16) &&
                   (!xdelta || aligned(xdelta, 8)) &&
                   aligned(w, w_half ? 8 : 16) && aligned(dx, 16) &&
                   (!a.tq || aligned(tq, 8)) && (!a.tv || aligned(tv, 8)) &&

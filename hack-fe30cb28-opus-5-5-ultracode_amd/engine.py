@@ -657,13 +657,17 @@ class _Layer(torch.autograd.Function):
         gu = f.pop("gu")
         _glu_bwd(dm, gu, spec.I)
         del dm
-        db = L.nf4_linear_t(gu, spec.gu)
+        # a split-K plan's slices go to the norm backward unsummed (it sums them in the
+        # reduce's order): no reduce launch, no fp16 round trip of db
+        db, db_parts = L.nf4_linear_t_parts(gu, spec.gu) if getattr(
+            packed, "parts_to_norm", False) else (L.nf4_linear_t(gu, spec.gu), None)
         del gu
         dh2_16 = torch.empty((n, H), device=h.device, dtype=torch.float16)
         h2, o2 = f.pop("h2"), f.pop("o2", None)
         dh2 = _rms_bwd(spec, db, h if h2 is None else h2, f.pop("rstd2"), spec.ln2, packed,
-                       dres=dh3, out16=dh2_16, xdelta=o2 if h2 is None else None)
-        del h2, o2
+                       dres=dh3, out16=dh2_16, xdelta=o2 if h2 is None else None,
+                       dy_parts=db_parts)
+        del h2, o2, db_parts
         del db, dh3
         dout = L.nf4_linear_t(dh2_16, spec.w["o_proj"]).view(n, HQ, D)
         del dh2_16
@@ -835,6 +839,9 @@ class FusedQwen2:
         # ... and its LoRA inputs' rank-r products x = drop(a) A^T (2 r fp16 a token), so a
         # recompute with the attention tensors kept forms only the input norm again
         self.keep_lora_x = True
+        # the gate|up input gradient's split-K slices summed by the post-attention norm's
+        # backward (the reduce's order: the same bits) instead of a reduce launch
+        self.parts_to_norm = True
         self.dropout_p = cfg.lora_dropout
         self.rope = RopeTable(cfg.rope_theta, cfg.head_dim, self.device)
         self.dropout = TorchDropout(self.device, torch.float32) if self.dropout_p > 0 else None
@@ -958,6 +965,7 @@ class FusedQwen2:
         packed.keep_bits = self.keep_bits
         packed.norm_in_bwd = self.norm_in_bwd
         packed.keep_lora_x = self.keep_lora_x
+        packed.parts_to_norm = self.parts_to_norm
         for i, spec in enumerate(self.layers):
             h = _Layer.apply(h, spec, packed, i >= keep_from, *spec.lora_params())
         stats = HeadStats()

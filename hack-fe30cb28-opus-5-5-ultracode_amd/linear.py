@@ -397,6 +397,31 @@ def nf4_linear_t(dy, w):
     return hgemm(dy, dequantize(w), 1, tile=0)
 
 
+def hgemm_parts(a, b, mode):
+    """qlora_gemm16 under its automatic plan, but a split-K plan's K slices are returned unsummed
+    (fp32 [S, M, N], for a consumer that sums them in slice order: _rms_bwd dy_parts); a plan in
+    one slice returns the fp16 product itself. Returns (product or None, slices or None)."""
+    M, K = a.shape
+    N = b.shape[0] if mode == 0 else b.shape[1]
+    tile, stages, splits, rest, _ = gemm_plan_split(M, N, K, mode, 0)
+    if splits == 1 or M == 0:
+        return hgemm(a, b, mode, tile=0), None
+    a = _a16(a)
+    _need(b, "b", torch.float16, a.device, contiguous=False)
+    ws = torch.empty((splits, M, N), device=a.device, dtype=torch.float32)
+    _lib.call("qlora_gemm16_parts", _ptr(a), a.stride(0), _ptr(b), b.stride(0), M, N, K, mode,
+              tile, stages, splits, _ptr(ws), ws.numel(), _stream(a.device))
+    return None, ws
+
+
+def nf4_linear_t_parts(dy, w):
+    """nf4_linear_t, but a split-K plan's slices returned unsummed (hgemm_parts)."""
+    if BACKEND == "fused" or dy.dtype != torch.float16:
+        return nf4_linear_t(dy, w), None
+    _check(dy.shape[1], _shape(w)[1], 1, "dY W")
+    return hgemm_parts(dy, dequantize(w), 1)
+
+
 def linear(x, w):
     """x W^T for an fp16 weight [V, H] (the lm_head)."""
     _check(x.shape[1], w.shape[0], 0, "lm_head x E^T")

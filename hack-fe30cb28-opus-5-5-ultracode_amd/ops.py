@@ -540,18 +540,27 @@ def _rms_fwd(spec, x, weight, packed, *, delta=None, write_y=True, seeds=(0, 0),
 
 
 def _rms_bwd(spec, dy, x, rstd, weight, packed, *, dres=None, tq=None, tv=None, seeds=(0, 0),
-             grad_scale=1.0, out=None, out16=None, keep=None, xdelta=None):
+             grad_scale=1.0, out=None, out16=None, keep=None, xdelta=None, dy_parts=None):
     """RMSNorm backward with the LoRA-dropout gradients merged (engine.py:969-981). With out16
     (fp16 [n, H]) the kernel also writes fp16(dx) there, the operand the next backward product
     rounds the gradient to. keep: the masks _rms_fwd stored for these rows (same packed and
     seeds), or None to draw them again. xdelta (fp16 [n, H]): the forward normed x + xdelta
     (_rms_fwd with delta); the kernel forms that sum and its rstd again, in the forward's order
-    of operations (the same bits), and rstd is not read (may be None)."""
+    of operations (the same bits), and rstd is not read (may be None). dy_parts (fp32
+    [S, n, H], no dropout): dy is fp16 of these split-K slices summed in order (a product's
+    qlora_gemm16_parts output, its reduce done here); dy is then None."""
     _need(x, "x", torch.float32)
     n, H = x.shape
     dev = x.device
     w_half = _weight_arg(weight, H, dev)
-    dy_stride = _rows_view(dy, "dy", torch.float16, n, H, dev) if n else H
+    if dy_parts is not None:
+        _need(dy_parts, "dy_parts", torch.float32, dev)
+        if dy_parts.dim() != 3 or tuple(dy_parts.shape[1:]) != (n, H) or \
+                not 1 <= dy_parts.shape[0] <= 16 or tq is not None or tv is not None:
+            raise ValueError("dy_parts must be fp32 [S <= 16, n, H], without dropout inputs")
+        dy_stride = H
+    else:
+        dy_stride = _rows_view(dy, "dy", torch.float16, n, H, dev) if n else H
     if xdelta is not None:
         _need(xdelta, "xdelta", torch.float16, dev)
         if xdelta.shape != x.shape:
@@ -585,7 +594,8 @@ def _rms_bwd(spec, dy, x, rstd, weight, packed, *, dres=None, tq=None, tv=None, 
                   p_keep, keep_scale, int(seed), int(ctr_q), int(ctr_v), int(threads),
                   float(grad_scale), int(tq is not None), int(tv is not None),
                   int(dres is not None), int(vec), keep_p, _ctr_base(packed, dev),
-                  _ptr(xdelta), float(spec.eps), _stream(dev))
+                  _ptr(xdelta), float(spec.eps), _ptr(dy_parts),
+                  0 if dy_parts is None else dy_parts.shape[0], _stream(dev))
     return dx
 
 

@@ -128,6 +128,9 @@ int qlora_rms_fwd(const float* x, const void* delta, const void* w, int32_t w_ha
  *   delta); the kernel forms that sum and rstd = 1/sqrt(mean(x^2)+eps) again in the forward's
  *   order of operations (the same bits) and does not read rstd (may then be null). No reference
  *   counterpart: a recompute's post-attention norm folded into its backward.
+ *   dy_parts (may be null; not with dropout) f32 [nparts, n, H]: dy = fp16 of the parts summed
+ *   in order (the K slices of qlora_gemm16_parts: the split-K reduce folded in, the same bits);
+ *   dy is then not read (may be null). No reference counterpart.
  */
 int qlora_rms_bwd(const void* dy, const void* tq, const void* tv, const float* x,
                   const float* rstd, const void* w, int32_t w_half, const float* dres, float* dx,
@@ -135,7 +138,7 @@ int qlora_rms_bwd(const void* dy, const void* tq, const void* tv, const float* x
                   float p_keep, float keep_scale, int64_t seed, int64_t ctr_q, int64_t ctr_v,
                   int64_t G, float grad_scale, int32_t drop_q, int32_t drop_v, int32_t has_res,
                   int32_t vec, const uint8_t* keep, const int64_t* ctr_base, const void* xdelta,
-                  float eps, void* stream);
+                  float eps, const float* dy_parts, int32_t nparts, void* stream);
 
 /*
  * qkv split + LoRA deltas + rotate-half RoPE. q = f16(rope(qkv_q + s*lq)),
@@ -322,6 +325,18 @@ int qlora_gemm16(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t
                  const float* resid, int64_t ldr, int32_t epi, int64_t swiglu_I, void* gu,
                  int64_t ldgu, int32_t tile, int32_t stages, int32_t splits, float* ws,
                  int64_t ws_elems, void* stream);
+
+/*
+ * The split-K form of qlora_gemm16 (epilogue 0) without its reduce: ws (16-byte aligned, at
+ * least splits*M*N elements) receives the fp32 K slices [splits, M, N], slice k the sum over its
+ * k-tiles, for a consumer that sums them in slice order itself (qlora_rms_bwd's dy_parts: the
+ * gate|up input gradient, engine.py:1293, feeding the post-attention norm's backward). tile,
+ * stages as qlora_gemm16 (splits >= 2). No reference counterpart (the reduce moved into the
+ * consumer).
+ */
+int qlora_gemm16_parts(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t M,
+                       int64_t N, int64_t K, int32_t mode, int32_t tile, int32_t stages,
+                       int32_t splits, float* ws, int64_t ws_elems, void* stream);
 
 /*
  * qlora_gemm16 that also records start/stop (hipEvent_t created with timing, or null) at the

@@ -465,6 +465,31 @@ def test_split_plan_equals_whole_tiles(pkg, mode, N, K, epi, M):
     assert rel_err(outs[0][0], want) < 1e-3
 
 
+@pytest.mark.parametrize("mode,M,N,K,tile,stages,splits", [(1, 2560, 1536, 17920, 256, 2, 4),
+                                                          (1, 1406, 1536, 17920, 256, 2, 7),
+                                                          (0, 700, 2048, 1536, 128, 4, 2)])
+def test_gemm16_parts_sum_to_the_split_product(pkg, mode, M, N, K, tile, stages, splits):
+    """qlora_gemm16_parts leaves the K slices of the split-K product unsummed: summed in slice
+    order and rounded to fp16 they are the split-K product bit for bit, and the slice sums add
+    up to the fp64 product."""
+    L = pkg.linear
+    g = torch.Generator(device=DEV).manual_seed(M + splits)
+    a = torch.randn(M, K, generator=g, device=DEV).half()
+    w = (torch.randn(*((N, K) if mode == 0 else (K, N)), generator=g, device=DEV) *
+         0.02).half()
+    ws = torch.full((splits, M, N), float("nan"), device=DEV)
+    pkg._lib.call("qlora_gemm16_parts", a.data_ptr(), a.stride(0), w.data_ptr(), w.stride(0),
+                  M, N, K, mode, tile, stages, splits, ws.data_ptr(), ws.numel(),
+                  L._stream(a.device))
+    whole = L.hgemm(a, w, mode, tile=tile, stages=stages, splits=splits)
+    s = ws[0].clone()
+    for k in range(1, splits):
+        s += ws[k]
+    assert torch.equal(s.half(), whole)
+    prod = a.double() @ (w.double().t() if mode == 0 else w.double())
+    assert rel_err(s, prod) < 1e-3
+
+
 @pytest.mark.parametrize("M,tile,stages,tail", [(2560, 256, 2, False), (2600, 256, 2, True),
                                                 (1875, 128, 2, True), (1875, 128, 2, False),
                                                 (700, 128, 4, False), (1, 0, 0, True),

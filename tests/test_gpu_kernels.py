@@ -324,6 +324,13 @@ def test_rms_forward_backward(pkg, n, H, wdtype):
     dxn2 = pkg.ops._rms_bwd(_Spec, dy.to(DEV), x.to(DEV), None, w.to(DEV), packed,
                             dres=dres.to(DEV), xdelta=delta.to(DEV))
     assert torch.equal(dxn, dxn2)
+    # dy given as split-K slices: fp16 of their sum in slice order, the same bits as dy itself
+    parts = torch.randn(3, n, H, generator=g).to(DEV)
+    dy16 = ((parts[0] + parts[1]) + parts[2]).half()
+    dxp = pkg.ops._rms_bwd(_Spec, dy16, xsum, rstd, w.to(DEV), packed, dres=dres.to(DEV))
+    dxp2 = pkg.ops._rms_bwd(_Spec, None, x.to(DEV), None, w.to(DEV), packed, dres=dres.to(DEV),
+                            xdelta=delta.to(DEV), dy_parts=parts)
+    assert torch.equal(dxp, dxp2)
     # the masks stored as bits by the forward: the oracle's masks, the same outputs, and a
     # backward that reads them equals the one that draws them again, bit for bit
     kb = torch.full(pkg.ops.keep_bits_shape(n, H), 0xAA, dtype=torch.uint8, device=DEV)

@@ -117,7 +117,7 @@ def test_kept_tensors_equal_recomputing_them(pkg):
         model = _tiny(pkg, H=512, HQ=8, HKV=2, D=64)
         model.keep_all, model.keep_gu, model.keep_attn = False, keep_gu, keep_attn
         model.keep_weights_recompute, model.keep_bits, model.norm_in_bwd = keep_w, keep_b, nib
-        model.keep_lora_x = kx
+        model.keep_lora_x = model.parts_to_norm = kx
         lengths = [17, 60, 33, 5]
         ids, mask, labels = _batch(lengths, model.cfg.vocab_size)
         denom = float((labels[:, 1:] != -100).sum())
