@@ -745,9 +745,13 @@ class _Head(torch.autograd.Function):
                     _ce(logits[a - lo:b - lo], targets[a:b], tok_loss[a:b], entropy[a:b],
                         correct[a:b], zero_unsupervised=zero)
             if top > lo:
-                g_hn = L.linear_t(logits[:top - lo], lm_w)
+                # a split-K plan's slices summed by the norm backward (the reduce's order)
+                g_hn, g_parts = L.hgemm_parts(logits[:top - lo], lm_w, 1) if getattr(
+                    packed, "parts_to_norm", False) else (L.linear_t(logits[:top - lo], lm_w),
+                                                          None)
                 _rms_bwd(norm, g_hn, rows[lo:top], rstd[lo:top], norm_w, packed,
-                         grad_scale=scale, out=grad_rows[lo:top])
+                         grad_scale=scale, out=grad_rows[lo:top], dy_parts=g_parts)
+                del g_hn, g_parts
             del logits
         dh = torch.empty_like(h).index_copy_(0, order, grad_rows)
         ctx.save_for_backward(dh)
@@ -839,8 +843,8 @@ class FusedQwen2:
         # ... and its LoRA inputs' rank-r products x = drop(a) A^T (2 r fp16 a token), so a
         # recompute with the attention tensors kept forms only the input norm again
         self.keep_lora_x = True
-        # the gate|up input gradient's split-K slices summed by the post-attention norm's
-        # backward (the reduce's order: the same bits) instead of a reduce launch
+        # the gate|up input gradient's (and the head's dh = G E) split-K slices summed by the
+        # following norm backward (the reduce's order: the same bits) instead of a reduce launch
         self.parts_to_norm = True
         self.dropout_p = cfg.lora_dropout
         self.rope = RopeTable(cfg.rope_theta, cfg.head_dim, self.device)
