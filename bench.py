@@ -197,9 +197,14 @@ def measure_step_kernels(pkg, trainer, batches, cfg):
     bwd = P.LaunchTimer("qlora_attn_bwd_split", bound="mfma")
     dq = P.LaunchTimer(P.DEQUANT)
     own = P.LaunchTimer(P.DOMINANT, bound="mfma", work=P.hgemm_flops, nbytes=P.hgemm_bytes)
+    # the package GEMM's other entry in the step (args a, lda, b, ldb, M, N, K, mode first):
+    # the split-K slices summed by the next norm backward (gate|up dX, the head's G E); events
+    # around the call (the launch gap in)
+    parts = P.LaunchTimer("qlora_gemm16_parts", bound="mfma",
+                          work=lambda a: 2.0 * a[4] * a[5] * a[6])
     work_f = work_b = 0.0
     with contextlib.ExitStack() as stack:
-        for t in (dq, fwd, bwd, own):
+        for t in (dq, fwd, bwd, own, parts):
             stack.enter_context(t)
         for batch in batches:
             pairs = causal_pairs(batch[5]["lengths"])
@@ -222,7 +227,7 @@ def measure_step_kernels(pkg, trainer, batches, cfg):
         ("down dX (N = I)", lambda a: a[7] == 1 and a[5] == cfg.intermediate_size),
         ("lm_head logits (N = V)", lambda a: a[7] == 0 and a[5] == cfg.vocab_size))
     for name, sel in classes:
-        r = own.summary(select=sel)
+        r = own.summary(select=sel, also=(parts,))
         if r is not None:  # (HBM traffic was measured on the SwiGLU launches only)
             out.append(dict(r, kernel=name, traffic=None))
     mine = own.summary(select=lambda a: a[13] in P.SWIGLU_EPIS)
@@ -296,6 +301,13 @@ def config1(pkg, copies=64, reps=20):
         [None] * 7 + [w.blocks, 1, None, 64, 256, getattr(w, "seg1", 2**63 - 1),
                       getattr(w, "seg2", 2**63 - 1)]) for w in layers[0])
     t_l = _event_time(lambda: [pkg.ops.dequant_many(layers[i], dev) for i in range(8)], reps) / 8
+    # the same 32 weights in one launch (the C-ABI's capacity): the kernel's rate once the launch
+    # is large enough, beside the step's one-layer launches (which keep the weights the GEMMs
+    # read next in the Infinity Cache)
+    all_w = [w for lay in layers for w in lay]
+    all_o = [torch.empty(w.shape, device=dev, dtype=torch.float16) for w in all_w]
+    t_8 = _event_time(lambda: pkg.ops.dequant_many(all_w, dev, outs=all_o), reps)
+    del all_o
     src = torch.empty(256 * 2**20, device=dev, dtype=torch.float16).normal_()
     dst = torch.empty_like(src)
     t_c = _event_time(lambda: dst.copy_(src), reps)
@@ -310,6 +322,8 @@ def config1(pkg, copies=64, reps=20):
     return {"q_proj_dequant_GBs": per_q / t_q / 1e9, "q_proj_bytes": per_q,
             "q_proj_us": t_q * 1e6, "layer_dequant_GBs": per_layer / t_l / 1e9,
             "layer_bytes": per_layer, "layer_us": t_l * 1e6,
+            "eight_layers_dequant_GBs": 8 * per_layer / t_8 / 1e9, "eight_layers_us": t_8 * 1e6,
+            "eight_layers_frac": 8 * per_layer / t_8 / 8e12,
             "copy_GBs": 2 * src.numel() * 2 / t_c / 1e9, "copy_bytes": 2 * src.numel() * 2,
             "copies": copies,
             "cpu": {"q_proj_ms": t_cpu * 1e3, "GBs": per_q / t_cpu / 1e9, "threads": 1,
