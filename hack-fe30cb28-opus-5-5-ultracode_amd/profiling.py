@@ -26,14 +26,14 @@ DEQUANT = "qlora_nf4_dequant_many"
 # step's launches), each divided by what the counter reads for a plain device copy of 1 GiB
 # (512 MiB each way; FETCH 0.50004, WRITE 1.000 of the bytes moved):
 # (11,892.4 / 0.50004 + 91,392) KiB per launch = 1.0018 x the algorithmic 117,728,444 B.
-# The package GEMM's SwiGLU launches that keep [g | u] (hgemm_kernel<NT, epilogue 5> with the
-# automatic tile plan, and the reduce of a K-sliced last round where there is one) over the step
-# dispatches of the bench's four measuring batches: 2.574 x the algorithmic bytes (x, the
-# [gate; up] weight, m and [g | u] once each), weighted by launch; 2.23-2.83 per token count.
-# WRITE is 1.22 x the outputs (the sliced tiles' partials); the excess is in FETCH, the A rows
-# and B tiles fetched by each XCD that uses them (FETCH_SIZE counts what leaves the 4 MB L2,
+# The package GEMM's SwiGLU products that keep [g | u] (hgemm_kernel<NT, epilogue 5> with the
+# automatic plan: one launch, or whole 256 x 256 rounds and the remaining columns on 128 x 128
+# tiles) over the step's products of the bench's four measuring batches: 2.030 x the
+# algorithmic bytes (x, the [gate; up] weight, m and [g | u] once each), weighted by product;
+# 1.85-2.34 per token count. WRITE equals the outputs; the excess is in FETCH, the A rows and
+# B tiles fetched by each XCD that uses them (FETCH_SIZE counts what leaves the 4 MB L2,
 # Infinity Cache hits included).
-TRAFFIC_RATIO = {"qlora_nf4_dequant_many": 1.0018, "qlora_gemm16": 2.574}
+TRAFFIC_RATIO = {"qlora_nf4_dequant_many": 1.0018, "qlora_gemm16": 2.030}
 
 
 def _dequant_bytes(args):
