@@ -114,7 +114,7 @@ def first_step(model, batch, scale=2.0**16):
     if gen is not None:
         gen.set_offset(offset)
     torch.cuda.synchronize()
-    return {"loss": float(loss), "grads": grads, "seed": seed, "offset": offset,
+    return {"loss": float(loss.detach()), "grads": grads, "seed": seed, "offset": offset,
             "metadata_ok": None if ok is None else bool(ok)}
 
 
