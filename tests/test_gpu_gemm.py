@@ -467,7 +467,11 @@ def test_split_plan_equals_whole_tiles(pkg, mode, N, K, epi, M):
 
 @pytest.mark.parametrize("mode,M,N,K,tile,stages,splits", [(1, 2560, 1536, 17920, 256, 2, 4),
                                                           (1, 1406, 1536, 17920, 256, 2, 7),
-                                                          (0, 700, 2048, 1536, 128, 4, 2)])
+                                                          (0, 700, 2048, 1536, 128, 4, 2),
+                                                          (1, 2949, 1536, 17920, 256, 2, 3),
+                                                          (1, 1875, 1536, 17920, 256, 2, 5),
+                                                          (1, 1, 1536, 17920, 256, 2, 16),
+                                                          (1, 300, 1536, 2048, 128, 2, 8)])
 def test_gemm16_parts_sum_to_the_split_product(pkg, mode, M, N, K, tile, stages, splits):
     """qlora_gemm16_parts leaves the K slices of the split-K product unsummed: summed in slice
     order and rounded to fp16 they are the split-K product bit for bit, and the slice sums add

@@ -262,6 +262,32 @@ class _Packed:
         self.dropout_p = p
 
 
+@pytest.mark.parametrize("nparts,n,H", [(1, 37, 1536), (2, 5, 100), (5, 2304, 1536),
+                                         (16, 9, 896), (4, 0, 1536)])
+def test_rms_bwd_sums_split_slices(pkg, nparts, n, H):
+    """dy given as S split-K slices (fp32 [S, n, H]): the backward equals the one given fp16 of
+    their sum in slice order, bit for bit, for every slice count the GEMM plan uses (and 1, 16
+    and no rows), with and without the forward's sum formed in the kernel."""
+    g = torch.Generator().manual_seed(nparts + n)
+    x = torch.randn(n, H, generator=g) * 3
+    delta = torch.randn(n, H, generator=g).half()
+    w = (torch.rand(H, generator=g) + 0.5).half()
+    packed = _Packed(0.0)
+    xsum, _, _, _, rstd = pkg.ops._rms_fwd(_Spec, x.to(DEV), w.to(DEV), packed,
+                                           delta=delta.to(DEV))
+    parts = torch.randn(nparts, n, H, generator=g).to(DEV)
+    s = parts[0].clone()
+    for k in range(1, nparts):
+        s = s + parts[k]
+    dres = torch.randn(n, H, generator=g).to(DEV)
+    want = pkg.ops._rms_bwd(_Spec, s.half(), xsum, rstd, w.to(DEV), packed, dres=dres)
+    got = pkg.ops._rms_bwd(_Spec, None, xsum, rstd, w.to(DEV), packed, dres=dres,
+                           dy_parts=parts)
+    got2 = pkg.ops._rms_bwd(_Spec, None, x.to(DEV), None, w.to(DEV), packed, dres=dres,
+                            xdelta=delta.to(DEV), dy_parts=parts)
+    assert torch.equal(got, want) and torch.equal(got2, want)
+
+
 @pytest.mark.parametrize("n,H,wdtype", [(37, 1536, torch.float32), (5, 100, torch.float32),
                                         (2304, 1536, torch.float16), (3, 50, torch.float16),
                                         (7, 3584, torch.float32), (9, 896, torch.float32),
