@@ -252,9 +252,17 @@ def _median_time(fn, reps, sync=True):
 
 
 def _event_time(fn, reps):
+    """GPU seconds per call of fn over `reps` back-to-back calls, bracketed by two events behind
+    a spin kernel that keeps the GPU busy while the host enqueues them (the host's Python and
+    ctypes time per launch is then not in the figure; the GPU's gaps between launches are)."""
+    torch.cuda.synchronize()
+    h0 = time.perf_counter()
     fn()
+    host_s = time.perf_counter() - h0  # the host's time to enqueue one call
     torch.cuda.synchronize()
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # shader-clock cycles for twice the host's enqueue time of the whole loop (2.4 GHz at most)
+    torch.cuda._sleep(int(max(2e5, 2.0 * reps * host_s * 2.4e9)))
     s.record()
     for _ in range(reps):
         fn()

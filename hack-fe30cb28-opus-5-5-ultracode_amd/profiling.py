@@ -2,10 +2,12 @@
 
 `LaunchTimer(entry)` times each launch of `entry` while active with a pair of HIP events on
 torch's current stream (the stream every entry point is launched on): recorded by the kernel
-dispatch itself at the kernel's start and end where the entry has a timed form (the dequant), else
-around the call (then the launch gap is included). It reports the average launch duration and
-the achieved bandwidth or FLOP rate against the MI355X peak (HBM 8 TB/s, dense fp16 MFMA
-2.5 PFLOP/s).
+dispatch itself at the kernel's start and end where the entry has a timed form (the dequant, the
+package GEMM), else around the call, behind a short spin kernel that keeps the GPU busy while
+the host enqueues the events and the launch (so the events bracket the launch's own GPU time,
+not the host's Python and ctypes overhead; the dispatch gap between the kernels of a multi-kernel
+entry stays in). It reports the average launch duration and the achieved bandwidth or FLOP rate
+against the MI355X peak (HBM 8 TB/s, dense fp16 MFMA 2.5 PFLOP/s).
 """
 
 import torch
@@ -14,6 +16,9 @@ from . import _lib
 
 HBM_PEAK_GBS = 8000.0
 FP16_PEAK_TFLOPS = 2500.0
+# GPU clock cycles of the spin kernel ahead of an event-bracketed launch (about 100 us, well
+# above the host's time to record an event and enqueue one entry point's kernels)
+COVER_CYCLES = 200_000
 
 # the entry point of the step's largest hand-written kernel by time, the package's MFMA GEMM
 # (every projection and lm_head product; the roofline entry is its gate|up forward with the
@@ -119,13 +124,18 @@ class LaunchTimer:
     def call(self, fn, args):
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
-        start.record()  # creates the events (and, for entries without a timed form, brackets it)
         timed = TIMED.get(self.entry)
         if timed is not None:
-            # the dispatch records both events at the kernel's own start and end
+            # the dispatch records both events at the kernel's own start and end (the records
+            # here only create the events)
+            start.record()
             end.record()
             rc = getattr(_lib.load(), timed)(*args, start.cuda_event, end.cuda_event)
         else:
+            # the GPU spins while the host records the start event and enqueues the launch, so
+            # the launch follows the start event at once
+            torch.cuda._sleep(COVER_CYCLES)
+            start.record()
             rc = fn(*args)
             end.record()
         self.records.append((start, end, self.work(args), args))

@@ -733,3 +733,25 @@ def test_dequant_timed_form(pkg):
     assert torch.equal(bits16(got), bits16(want))
     s = timer.summary()
     assert s["launches"] == 1 and 0 < s["avg_us"] <= outer0.elapsed_time(outer1) * 1e3
+
+
+def test_event_bracketed_timer_excludes_the_spin(pkg):
+    """An entry without a timed form (the RMSNorm forward) is bracketed by events behind a spin
+    kernel: the launch still computes what an untimed launch computes, and its recorded
+    duration is positive and shorter than the spin plus the launch measured around both."""
+    g = torch.Generator().manual_seed(5)
+    x = (torch.randn(2048, 1536, generator=g) * 2).to(DEV)
+    w = (torch.rand(1536, generator=g) + 0.5).to(DEV)
+    packed = _Packed(0.0)
+    _, want, _, _, _ = pkg.ops._rms_fwd(_Spec, x, w, packed)
+    timer = pkg.profiling.LaunchTimer("qlora_rms_fwd", work=lambda a: 1.0, bound="hbm")
+    outer0, outer1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with timer:
+        outer0.record()
+        _, got, _, _, _ = pkg.ops._rms_fwd(_Spec, x, w, packed)
+        outer1.record()
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    s = timer.summary()
+    outer_us = outer0.elapsed_time(outer1) * 1e3
+    assert s["launches"] == 1 and 0 < s["avg_us"] < outer_us
