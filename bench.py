@@ -32,6 +32,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--policy 
 """
 
 import argparse
+import concurrent.futures
 import contextlib
 import importlib
 import json
@@ -40,6 +41,7 @@ import statistics
 import sys
 import time
 
+import numpy as np
 import torch
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
@@ -327,6 +329,15 @@ def config1(pkg, copies=64, reps=20):
                                              256))
     packed = w0.packed.cpu().numpy().reshape(-1)
     t_cpu = _median_time(lambda: ON.dequantize_nf4(packed, st), 5, sync=False)
+    # the same dequant over the host's cores: the weight's blocks cut at double-quant group
+    # boundaries, one numpy call per part on a thread pool (numpy releases the GIL in them)
+    workers = len(os.sched_getaffinity(0))
+    one = ON.dequantize_nf4(packed, st)
+    with concurrent.futures.ThreadPoolExecutor(workers) as ex:
+        assert np.array_equal(_dequant_parts(ON, packed, st, workers, ex).view(np.uint16),
+                              one.view(np.uint16))
+        t_cpu_n = _median_time(lambda: _dequant_parts(ON, packed, st, workers, ex), 5,
+                               sync=False)
     return {"q_proj_dequant_GBs": per_q / t_q / 1e9, "q_proj_bytes": per_q,
             "q_proj_us": t_q * 1e6, "layer_dequant_GBs": per_layer / t_l / 1e9,
             "layer_bytes": per_layer, "layer_us": t_l * 1e6,
@@ -335,7 +346,26 @@ def config1(pkg, copies=64, reps=20):
             "copy_GBs": 2 * src.numel() * 2 / t_c / 1e9, "copy_bytes": 2 * src.numel() * 2,
             "copies": copies,
             "cpu": {"q_proj_ms": t_cpu * 1e3, "GBs": per_q / t_cpu / 1e9, "threads": 1,
-                    "kind": "port (oracle.nf4, numpy)"}}
+                    "q_proj_ms_threads": t_cpu_n * 1e3, "GBs_threads": per_q / t_cpu_n / 1e9,
+                    "threads_used": workers, "kind": "port (oracle.nf4, numpy)"}}
+
+
+def _dequant_parts(ON, packed, st, parts, ex):
+    """oracle.nf4.dequantize_nf4 of a nested-quant weight in `parts` pieces on the executor `ex`,
+    each a run of whole 256-block double-quant groups; the same values as one call."""
+    bs, g2 = st.blocksize, st.state2.blocksize
+    nb = st.absmax.size
+    groups = -(-nb // g2)
+    bounds = [min(nb, g2 * (groups * i // parts)) for i in range(parts + 1)]
+
+    def part(b0, b1):
+        sub = ON.QuantState(st.absmax[b0:b1], ((b1 - b0) * bs,), st.code, bs, offset=st.offset,
+                            state2=ON.QuantState2(st.state2.absmax[b0 // g2:-(-b1 // g2)],
+                                                  st.state2.code, g2))
+        return ON.dequantize_nf4(packed[b0 * bs // 2:b1 * bs // 2], sub)
+
+    futs = [ex.submit(part, b0, b1) for b0, b1 in zip(bounds[:-1], bounds[1:]) if b1 > b0]
+    return np.concatenate([f.result() for f in futs]).reshape(st.shape)
 
 
 def config2(pkg, reps=10):
